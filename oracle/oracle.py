@@ -1,0 +1,438 @@
+"""TEST INFRASTRUCTURE ONLY: numpy/ctypes access to the C oracle (oracle/kt_oracle.c).
+
+The oracle is the CPU restatement of tritify's exact-integer path that the GPU backend is checked against, and the
+timed CPU baseline. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module;
+the product package (tritify_amd) never does.
+
+Each wrapper names the reference function it restates (paths relative to the tritify repository root).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkt_oracle.so")
+
+WLEVELS = 265_720  # crates/01-engine/kt-core/src/layers.rs:16
+ACT_LEVELS = 1 << 28  # layers.rs:18
+K_MAX = (2**63 - 1) // (WLEVELS * WLEVELS)  # kt-cuda/src/digits.rs:23
+KT_FLUSH = (2**31 - 1) // (16 * 40 * 40)  # kt-cuda/src/digits.rs:20
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle with its committed Makefile."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class Scale(C.Structure):
+    """kt_int::Scale (crates/00-kernels/kt-int/src/lib.rs:175-178)."""
+
+    _fields_ = [("mant", C.c_int64), ("shift", C.c_int32)]
+
+    def __repr__(self) -> str:
+        return f"Scale(mant={self.mant}, shift={self.shift})"
+
+    def __eq__(self, o) -> bool:
+        return (self.mant, self.shift) == (o.mant, o.shift)
+
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+
+
+def _declare(L: C.CDLL) -> None:
+    sig = {
+        "kt_lcg_next": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+        "kt_sha256": (None, [_P, _SZ, _P]),
+        "kt_dot_portable": (C.c_int64, [_P, _P, _SZ]),
+        "kt_cpu_variant_available": (C.c_int, [C.c_int]),
+        "kt_cpu_auto_variant": (C.c_int, []),
+        "kt_set_max_threads": (None, [_SZ]),
+        "kt_max_threads": (_SZ, []),
+        "kt_resolve_threads": (_SZ, [_SZ]),
+        "kt_plan_threads": (_SZ, [_SZ, _SZ]),
+        "kt_linear_cpu": (None, [_P, _P, _SZ, _SZ, _SZ, C.c_int, _P]),
+        "kt_linear_cpu_threads": (None, [_P, _P, _SZ, _SZ, _SZ, C.c_int, _SZ, _P]),
+        "kt_linear_planted_partition": (None, [_P, _P, _SZ, _SZ, _SZ, C.c_int, _SZ, _P]),
+        "kt_linear_planted_dot": (None, [_P, _P, _SZ, _SZ, _SZ, C.c_int, _P]),
+        "kt_gen_demo": (None, [_SZ, _SZ, _SZ, C.c_uint64, _P, _P]),
+        "kt_gen_wlevels": (None, [C.POINTER(C.c_uint64), _SZ, _P]),
+        "kt_gen_w12": (None, [C.c_uint64, _SZ, _P]),
+        "kt_gen_act_gauss": (None, [C.c_uint64, C.c_int64, _SZ, _P]),
+        "kt_gen_act_uniform": (None, [C.c_uint64, _SZ, _P]),
+        "kt_split81": (C.c_int, [C.c_int32, _P]),
+        "kt_join81": (C.c_int64, [_P]),
+        "kt_split256": (C.c_int, [C.c_int64, C.c_int, C.c_int, _P]),
+        "kt_join256": (C.c_int64, [_P, C.c_int]),
+        "kt_planes_for": (C.c_int, [_P, _SZ]),
+        "kt_pack_planes": (None, [_P, _SZ, _SZ, C.c_int, C.c_int, _P]),
+        "kt_flush_k": (C.c_int64, [C.c_int, C.c_int]),
+        "kt_emu_linear": (None, [_P, _P, _SZ, _SZ, _SZ, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, _P]),
+        "kt_frexp": (C.c_double, [C.c_double, C.POINTER(C.c_int32)]),
+        "kt_frexp_scale": (None, [C.c_double, C.c_uint32, C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
+        "kt_requant": (C.c_int64, [C.c_int64, C.c_int64, C.c_int32]),
+        "kt_scale_from_ratio": (Scale, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64]),
+        "kt_scale_from_f64": (Scale, [C.c_double]),
+        "kt_scale_ge": (C.c_int, [Scale, Scale]),
+        "kt_scale_mul": (Scale, [Scale, Scale]),
+        "kt_scale_apply": (C.c_int64, [Scale, C.c_int64]),
+        "kt_scale_recip": (Scale, [Scale]),
+        "kt_scale_add": (Scale, [Scale, Scale]),
+        "kt_scale_rsqrt": (Scale, [Scale]),
+        "kt_scale_to_i32": (Scale, [Scale]),
+        "kt_isqrt_u128": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "kt_quant_to": (None, [_P, _SZ, C.c_int64, _P]),
+        "kt_requant_dyn": (C.c_int32, [C.c_int64, C.c_int64, C.c_int64]),
+        "kt_w12_pack": (None, [_P, _SZ, _SZ, _P, _P]),
+        "kt_w12_get": (C.c_int32, [_P, _P, _SZ, _SZ, _SZ]),
+        "kt_w12_linear": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _P]),
+        "kt_requant_channels": (None, [_P, _SZ, _SZ, _P, _P, C.c_int64, C.c_int64, _P]),
+        "kt_channel_scales": (None, [_P, _SZ, _SZ, C.c_int64, _P, _P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# hashing
+
+
+def sha256_hex(a: np.ndarray) -> str:
+    """SHA-256 over the array's little-endian words (apps/kt-demo/src/main.rs:57-63; kt-core/src/verify.rs:35-41)."""
+    a = np.ascontiguousarray(a)
+    out = (C.c_uint8 * 32)()
+    lib().kt_sha256(_ptr(a), a.nbytes, out)
+    return bytes(out).hex()
+
+
+def sha256_py(a: np.ndarray) -> str:
+    """hashlib's SHA-256 of the same bytes (an independent implementation, used to pin kt_sha256)."""
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the linear accumulate
+
+
+def linear_cpu(x, w, rows: int, out: int, k: int, variant: int | None = None) -> np.ndarray:
+    """linear_cpu on a dot variant (crates/01-engine/kt-core/src/backend.rs:133-140; kt-runtime/src/cpu.rs).
+
+    variant: 0 portable, 1 avx2, 2 avx512; None = the auto rank (kt-runtime/src/lib.rs:93-96)."""
+    x, w = _i32(x), _i32(w)
+    assert x.size == rows * k and w.size == out * k
+    v = lib().kt_cpu_auto_variant() if variant is None else variant
+    y = np.empty(rows * out, dtype=np.int64)
+    lib().kt_linear_cpu(_ptr(x), _ptr(w), rows, out, k, v, _ptr(y))
+    return y
+
+
+def portable(x, w, rows: int, out: int, k: int) -> np.ndarray:
+    """Portable.linear (backend.rs:143-152)."""
+    return linear_cpu(x, w, rows, out, k, variant=0)
+
+
+def linear_threads(x, w, rows, out, k, threads, variant=0) -> np.ndarray:
+    x, w = _i32(x), _i32(w)
+    y = np.full(rows * out, -1, dtype=np.int64)
+    lib().kt_linear_cpu_threads(_ptr(x), _ptr(w), rows, out, k, variant, threads, _ptr(y))
+    return y
+
+
+def planted_partition(x, w, rows, out, k, bad: int, threads: int = 0) -> np.ndarray:
+    """kt-runtime/src/planted.rs:28-59. bad: 1 FloorOffsets, 2 DropLastRun, 3 SwappedIndex."""
+    x, w = _i32(x), _i32(w)
+    y = np.zeros(rows * out, dtype=np.int64)
+    lib().kt_linear_planted_partition(_ptr(x), _ptr(w), rows, out, k, bad, threads, _ptr(y))
+    return y
+
+
+def planted_dot(x, w, rows, out, k, which: int) -> np.ndarray:
+    """kt-runtime/src/tests.rs:9-17. which: 10 wrapping i32 accumulator, 11 f32 accumulator."""
+    x, w = _i32(x), _i32(w)
+    y = np.zeros(rows * out, dtype=np.int64)
+    lib().kt_linear_planted_dot(_ptr(x), _ptr(w), rows, out, k, which, _ptr(y))
+    return y
+
+
+def set_max_threads(n: int) -> None:
+    lib().kt_set_max_threads(n)
+
+
+def plan_threads(elems: int, work: int) -> int:
+    return lib().kt_plan_threads(elems, min(work, 2**64 - 1))
+
+
+def resolve_threads(nblocks: int) -> int:
+    return lib().kt_resolve_threads(nblocks)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# generators
+
+
+def gen_demo(m: int, n: int, k: int, seed: int = 42):
+    """apps/kt-demo/src/main.rs:23-28."""
+    qx = np.empty(m * k, dtype=np.int32)
+    qw = np.empty(n * k, dtype=np.int32)
+    lib().kt_gen_demo(m, n, k, seed, _ptr(qx), _ptr(qw))
+    return qx, qw
+
+
+class Stream:
+    """One LCG stream (main.rs:19-22) drawing codes uniform in +-WLEVELS (gate.rs:29-36)."""
+
+    def __init__(self, seed: int):
+        self.s = C.c_uint64(seed)
+
+    def wlevels(self, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.int32)
+        lib().kt_gen_wlevels(C.byref(self.s), n, _ptr(out))
+        return out
+
+
+def codes(n: int, seed: int) -> np.ndarray:
+    """kt-cuda/src/tests.rs:9-15: codes uniform in +-WLEVELS from a seeded LCG."""
+    return Stream(seed).wlevels(n)
+
+
+class Case:
+    def __init__(self, label, rows, out, k, x, w):
+        self.label, self.rows, self.out, self.k, self.x, self.w = label, rows, out, k, x, w
+
+
+def corpus() -> list[Case]:
+    """The fixed gate corpus, crates/02-runtime/kt-runtime/src/gate.rs:26-56."""
+    lv = WLEVELS
+    st = Stream(0x5032_0B00)
+    cases = []
+    for label, rows, out, k in [
+        ("k=1", 1, 1, 1),
+        ("odd tail", 3, 5, 7),
+        ("k=33", 2, 17, 33),
+        ("k=1023", 4, 64, 1023),
+        ("k=4099 (long)", 1, 9, 4099),
+        ("threaded 8×512×2048", 8, 512, 2048),
+    ]:
+        x = st.wlevels(rows * k)
+        w = st.wlevels(out * k)
+        cases.append(Case(label, rows, out, k, x, w))
+    k = 1027
+    x = np.array([-lv if i % 3 == 0 else lv for i in range(2 * k)], dtype=np.int32)
+    w = np.array([lv if i % 2 == 0 else -lv for i in range(3 * k)], dtype=np.int32)
+    cases.append(Case("extremes ±WLEVELS", 2, 3, k, x, w))
+    x = np.full(4 * 2048, lv, dtype=np.int32)
+    cases.append(Case("all +WLEVELS", 4, 4, 2048, x, x.copy()))
+    return cases
+
+
+def flush_case() -> Case:
+    """gate.rs:61-66: the smallest k beyond one int32 flush of the reference's digit backend."""
+    k = (KT_FLUSH + 1) * 16
+    lv = WLEVELS
+    w = np.concatenate([np.full(k, lv, dtype=np.int32), np.full(k, -lv, dtype=np.int32)])
+    return Case("k beyond one int32 flush", 1, 2, k, np.full(k, lv, dtype=np.int32), w)
+
+
+def gen_w12(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_gen_w12(seed, n, _ptr(out))
+    return out
+
+
+def gen_act_gauss(seed: int, sigma: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_gen_act_gauss(seed, sigma, n, _ptr(out))
+    return out
+
+
+def gen_act_uniform(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_gen_act_uniform(seed, n, _ptr(out))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# digits and the plane emulator
+
+
+def split81(v: int):
+    d = (C.c_int8 * 3)()
+    ok = lib().kt_split81(v, d)
+    return list(d) if ok else None
+
+
+def join81(d) -> int:
+    a = (C.c_int8 * 3)(*d)
+    return lib().kt_join81(a)
+
+
+def split256(v: int, p: int, wrong_carry: bool = False):
+    d = (C.c_int8 * 5)()
+    ok = lib().kt_split256(v, p, int(wrong_carry), d)
+    return list(d)[:p] if ok else None
+
+
+def planes_for(v) -> int:
+    v = _i32(v)
+    return lib().kt_planes_for(_ptr(v), v.size)
+
+
+def pack_planes(codes_, rows, k, p, wrong_carry=False) -> np.ndarray:
+    codes_ = _i32(codes_)
+    kp = (k + 63) // 64 * 64
+    out = np.empty(p * rows * kp, dtype=np.int8)
+    lib().kt_pack_planes(_ptr(codes_), rows, k, p, int(wrong_carry), _ptr(out))
+    return out.reshape(p, rows, kp)
+
+
+def flush_k(px: int, pw: int) -> int:
+    return lib().kt_flush_k(px, pw)
+
+
+def emu_linear(x, w, rows, out, k, px=None, pw=None, flush=None, drop_top=False, wrong_carry=False) -> np.ndarray:
+    """The plane product step for step on the CPU (analogue of kt-cuda/src/host.rs:53-84)."""
+    x, w = _i32(x), _i32(w)
+    px = planes_for(x) if px is None else px
+    pw = planes_for(w) if pw is None else pw
+    fk = flush_k(px, pw) if flush is None else flush
+    y = np.zeros(rows * out, dtype=np.int64)
+    lib().kt_emu_linear(_ptr(x), _ptr(w), rows, out, k, px, pw, fk, int(drop_top), int(wrong_carry), _ptr(y))
+    return y
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# kt-int
+
+
+def requant(accum: int, mant: int, shift: int) -> int:
+    return lib().kt_requant(accum, mant, shift)
+
+
+def frexp(x: float):
+    e = C.c_int32()
+    m = lib().kt_frexp(x, C.byref(e))
+    return m, e.value
+
+
+def frexp_scale(x: float, mant_bits: int):
+    m, s = C.c_int64(), C.c_int32()
+    lib().kt_frexp_scale(x, mant_bits, C.byref(m), C.byref(s))
+    return m.value, s.value
+
+
+def from_ratio(num: int, den: int) -> Scale:
+    return lib().kt_scale_from_ratio(num >> 64, num & (2**64 - 1), den >> 64, den & (2**64 - 1))
+
+
+def from_f64(x: float) -> Scale:
+    return lib().kt_scale_from_f64(x)
+
+
+def scale_mul(a: Scale, b: Scale) -> Scale:
+    return lib().kt_scale_mul(a, b)
+
+
+def scale_apply(a: Scale, v: int) -> int:
+    return lib().kt_scale_apply(a, v)
+
+
+def scale_recip(a: Scale) -> Scale:
+    return lib().kt_scale_recip(a)
+
+
+def scale_add(a: Scale, b: Scale) -> Scale:
+    return lib().kt_scale_add(a, b)
+
+
+def scale_rsqrt(a: Scale) -> Scale:
+    return lib().kt_scale_rsqrt(a)
+
+
+def scale_ge(a: Scale, b: Scale) -> bool:
+    return bool(lib().kt_scale_ge(a, b))
+
+
+def scale_to_i32(a: Scale) -> Scale:
+    return lib().kt_scale_to_i32(a)
+
+
+def isqrt_u128(n: int) -> int:
+    return lib().kt_isqrt_u128(n >> 64, n & (2**64 - 1))
+
+
+def quant_to(data, xmax: int) -> np.ndarray:
+    data = _i32(data)
+    out = np.empty_like(data)
+    lib().kt_quant_to(_ptr(data), data.size, xmax, _ptr(out))
+    return out
+
+
+def requant_dyn(v: int, num_level: int, den: int) -> int:
+    return lib().kt_requant_dyn(v, num_level, den)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the 12-bit weight path
+
+
+def w12_pack(codes_, n: int, k: int):
+    codes_ = _i32(codes_)
+    kp = (k + 63) // 64 * 64
+    lo = np.empty(n * kp, dtype=np.int8)
+    nib = np.empty(n * kp // 2, dtype=np.uint8)
+    lib().kt_w12_pack(_ptr(codes_), n, k, _ptr(lo), _ptr(nib))
+    return lo, nib
+
+
+def w12_get(lo, nib, k, r, c) -> int:
+    return lib().kt_w12_get(_ptr(lo), _ptr(nib), k, r, c)
+
+
+def w12_linear(x, lo, nib, m, n, k) -> np.ndarray:
+    x = _i32(x)
+    y = np.empty(m * n, dtype=np.int64)
+    lib().kt_w12_linear(_ptr(x), _ptr(lo), _ptr(nib), m, n, k, _ptr(y))
+    return y
+
+
+def requant_channels(acc, m, n, mant, shift, lo=-127, hi=127) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, dtype=np.int64)
+    mant, shift = _i32(mant), _i32(shift)
+    out = np.empty(m * n, dtype=np.int32)
+    lib().kt_requant_channels(_ptr(acc), m, n, _ptr(mant), _ptr(shift), lo, hi, _ptr(out))
+    return out
+
+
+def channel_scales(w, n, k, sigma=40):
+    w = _i32(w)
+    mant = np.empty(n, dtype=np.int32)
+    shift = np.empty(n, dtype=np.int32)
+    lib().kt_channel_scales(_ptr(w), n, k, sigma, _ptr(mant), _ptr(shift))
+    return mant, shift

@@ -1,0 +1,65 @@
+"""Writes tests/golden/goldens.json: input and output hashes of the BASELINE workloads, computed by the CPU oracle
+(oracle/kt_oracle.c, the restated reference CPU path). The GPU tests compare the device results with these fixtures
+at full size, where recomputing the CPU answer inside a test would take too long.
+
+Run from the repository root:  python tests/golden/make_goldens.py
+"""
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+from oracle import oracle as O  # noqa: E402
+
+OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "goldens.json")
+
+# BASELINE config 2 (this build's definitions; see oracle/kt_oracle.c kt_gen_w12 / kt_gen_act_gauss /
+# kt_channel_scales): N = K = 4096, M in {1, 16, 128, 2048} taking the first M rows of one 2048-row activation draw.
+C2 = {"w_seed": 2, "x_seed": 3, "sigma": 40, "N": 4096, "K": 4096, "Ms": [1, 16, 128, 2048]}
+
+
+def main() -> None:
+    t0 = time.time()
+    g = {}
+    qx, qw = O.gen_demo(64, 1024, 1024, 42)
+    y = O.linear_cpu(qx, qw, 64, 1024, 1024)
+    g["config1"] = {
+        "M": 64, "N": 1024, "K": 1024, "seed": 42,
+        "x_sha256": O.sha256_hex(qx), "w_sha256": O.sha256_hex(qw),
+        "y_i64_sha256": O.sha256_hex(y), "y_i32_sha256": O.sha256_hex(y.astype(np.int32)),
+    }
+    cs = O.corpus()
+    g["corpus_sha256"] = O.sha256_hex(np.concatenate([O.linear_cpu(c.x, c.w, c.rows, c.out, c.k) for c in cs]))
+
+    N, K = C2["N"], C2["K"]
+    w = O.gen_w12(C2["w_seed"], N * K)
+    x = O.gen_act_gauss(C2["x_seed"], C2["sigma"], max(C2["Ms"]) * K)
+    mant, shift = O.channel_scales(w, N, K, C2["sigma"])
+    c2 = dict(C2)
+    c2.update({
+        "w_sha256": O.sha256_hex(w), "x_sha256": O.sha256_hex(x),
+        "mant_sha256": O.sha256_hex(mant), "shift_sha256": O.sha256_hex(shift), "outputs": {},
+    })
+    for m in C2["Ms"]:
+        t = time.time()
+        acc = O.linear_cpu(x[: m * K], w, m, N, K)
+        q = O.requant_channels(acc, m, N, mant, shift, -127, 127).astype(np.int8)
+        c2["outputs"][str(m)] = {
+            "x_sha256": O.sha256_hex(x[: m * K]),
+            "acc_i64_sha256": O.sha256_hex(acc),
+            "out_i8_sha256": O.sha256_hex(q),
+            "acc_absmax": int(np.abs(acc).max()),
+            "out_i8_saturated": int((np.abs(q.astype(np.int32)) == 127).sum()),
+        }
+        print(f"config2 M={m}: {time.time() - t:.1f}s", flush=True)
+    g["config2"] = c2
+    json.dump(g, open(OUT, "w"), indent=1, sort_keys=True)
+    print(f"wrote {OUT} in {time.time() - t0:.1f}s")
+
+
+if __name__ == "__main__":
+    main()

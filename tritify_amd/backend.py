@@ -1,0 +1,272 @@
+"""Python binding of the MI355X backend's C ABI (include/kt_hip.h).
+
+`HipBackend` mirrors tritify's `LinearBackend` trait (crates/01-engine/kt-core/src/backend.rs:46-58) as the CUDA
+digit backend exposes it (`kt_cuda::open`, `TcLinear`, crates/02-runtime/kt-cuda/src/lib.rs:252-279 and
+backend.rs:77-192): `name`, `linear`, `linear_weights`, `resident_bytes`, and the process-wide `fallbacks` counter.
+Errors raise `HipError` -- the reference panics there, because "a wrong answer is worse than a stop"
+(crates/02-runtime/kt-cuda/src/device.rs:40-48).
+
+The 12-bit-weight functions (`w12_*`) work on device-resident operands. torch tensors are accepted as plain device
+buffers (their data_ptr is passed through the C ABI); torch never computes anything here.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(PKG, "libkt_hip.so")
+LIB_PLANTED = os.path.join(PKG, "libkt_hip_planted.so")
+
+OUT_I64, OUT_I32, OUT_I8 = 0, 1, 2
+
+# kt_cuda::Plant (crates/02-runtime/kt-cuda/src/backend.rs:31-40)
+PLANT_DROP_TOP, PLANT_WRONG_CARRY, PLANT_NO_FLUSH, PLANT_CACHE_BY_SHAPE = 1, 2, 3, 4
+
+_libs: dict[str, C.CDLL] = {}
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def _load(path: str) -> C.CDLL:
+    if path not in _libs:
+        if not os.path.exists(path):
+            raise ImportError(f"the HIP backend is not built ({path} is missing): run __graft_entry__.build()")
+        lib = C.CDLL(path)
+        _declare(lib)
+        _libs[path] = lib
+    return _libs[path]
+
+
+def lib(planted: bool = False) -> C.CDLL:
+    return _load(LIB_PLANTED if planted else LIB)
+
+
+_P, _SZ, _I, _I64, _U64 = C.c_void_p, C.c_size_t, C.c_int, C.c_int64, C.c_uint64
+
+
+def _declare(L: C.CDLL) -> None:
+    sig = {
+        "kt_hip_device_count": (_I, [C.POINTER(_I)]),
+        "kt_hip_device_info": (_I, [_I, C.c_char_p, _I, C.POINTER(_I), C.POINTER(_I), C.POINTER(_SZ)]),
+        "kt_hip_alloc": (_I, [_I, _SZ, C.POINTER(_P)]),
+        "kt_hip_free": (_I, [_I, _P]),
+        "kt_hip_upload": (_I, [_I, _P, _P, _SZ]),
+        "kt_hip_download": (_I, [_I, _P, _P, _SZ]),
+        "kt_hip_error_string": (C.c_char_p, [_I]),
+        "kt_hip_kp": (_I64, [_I64]),
+        "kt_hip_planes_for": (_I, [_P, _SZ]),
+        "kt_hip_pack_planes": (_I, [_I, _P, _I64, _I64, _I, _P, _P]),
+        "kt_hip_flush_k": (_I64, [_I, _I]),
+        "kt_hip_digit_gemm": (_I, [_I, _P, _I, _P, _I, _P, _I64, _I64, _I64, _I64, _I, _P]),
+        "kt_hip_open": (_I, [_I, _U64, C.POINTER(_P)]),
+        "kt_hip_open_planted": (_I, [_I, _I, C.POINTER(_P)]),
+        "kt_hip_close": (None, [_P]),
+        "kt_hip_name": (_I, [_P, C.c_char_p, _I]),
+        "kt_hip_linear": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _P]),
+        "kt_hip_linear_weights": (_I, [_P, _P, _U64, _P, _SZ, _SZ, _SZ, _P]),
+        "kt_hip_weight_id_fresh": (_U64, []),
+        "kt_hip_resident_bytes": (_U64, [_P]),
+        "kt_hip_fallbacks": (_U64, []),
+        "kt_hip_w12_pack": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
+        "kt_hip_w12_upload": (_I, [_I, _P, _I64, _I64, _P, _P]),
+        "kt_hip_w12_linear": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
+        "kt_hip_probe_mfma": (_I, [_I, _P, _P, _P, _P, _P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def check(e: int, what: str) -> None:
+    if e != 0:
+        msg = lib().kt_hip_error_string(e).decode()
+        raise HipError(f"kt-hip: {what}: {msg} (hipError {e})")
+
+
+def _i32(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.int32:
+        if a.size and (a.min() < -(2**31) or a.max() > 2**31 - 1):
+            raise ValueError("codes must fit i32")
+        a = a.astype(np.int32)
+    return a
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# device layer
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    e = lib().kt_hip_device_count(C.byref(n))
+    return n.value if e == 0 else 0
+
+
+def device_info(dev: int = 0) -> dict:
+    name = C.create_string_buffer(256)
+    major, minor, free = C.c_int(), C.c_int(), C.c_size_t()
+    check(lib().kt_hip_device_info(dev, name, 256, C.byref(major), C.byref(minor), C.byref(free)), "device info")
+    return {"name": name.value.decode(), "major": major.value, "minor": minor.value, "free": free.value}
+
+
+def kp(k: int) -> int:
+    """k padded to the 64-value tile of the device layouts."""
+    return (k + 63) // 64 * 64
+
+
+def planes_for(codes) -> int:
+    c = _i32(codes)
+    return lib().kt_hip_planes_for(c.ctypes.data, c.size)
+
+
+def flush_k(px: int, pw: int) -> int:
+    return lib().kt_hip_flush_k(px, pw)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# backend layer
+
+
+@dataclass(frozen=True)
+class Weights:
+    """kt_core::backend::Weights (backend.rs:37-42): codes behind an id never change."""
+
+    id: int
+    codes: np.ndarray
+
+
+def weight_id_fresh() -> int:
+    """WeightId::fresh (backend.rs:29-35)."""
+    return lib().kt_hip_weight_id_fresh()
+
+
+def fallbacks() -> int:
+    """kt_cuda::fallbacks (backend.rs:42-48); this backend never falls back, so it stays 0."""
+    return lib().kt_hip_fallbacks()
+
+
+class HipBackend:
+    """One LinearBackend on one MI355X (TcLinear<DeviceExec>)."""
+
+    def __init__(self, dev: int = 0, budget: int | None = None, plant: int | None = None):
+        self._planted = plant is not None
+        self._lib = lib(self._planted)
+        h = C.c_void_p()
+        if plant is None:
+            check(self._lib.kt_hip_open(dev, budget or 0, C.byref(h)), "open")
+        else:
+            if budget is not None:
+                raise ValueError("a planted backend takes the default budget")
+            check(self._lib.kt_hip_open_planted(dev, plant, C.byref(h)), "open planted")
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.kt_hip_close(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def name(self) -> str:
+        buf = C.create_string_buffer(512)
+        check(self._lib.kt_hip_name(self._h, buf, 512), "name")
+        return buf.value.decode()
+
+    def _args(self, x, w, rows, out, k):
+        x, w = _i32(x), _i32(w)
+        if x.size != rows * k:
+            raise ValueError("linear: x is not rows·k")
+        if w.size != out * k:
+            raise ValueError("linear: w is not out·k")
+        return x, w, np.empty(rows * out, dtype=np.int64)
+
+    def linear(self, x, w, rows: int, out: int, k: int) -> np.ndarray:
+        x, w, y = self._args(x, w, rows, out, k)
+        check(self._lib.kt_hip_linear(self._h, x.ctypes.data, w.ctypes.data, rows, out, k, y.ctypes.data), "linear")
+        return y
+
+    def linear_weights(self, x, weights: Weights, rows: int, out: int, k: int) -> np.ndarray:
+        x, w, y = self._args(x, weights.codes, rows, out, k)
+        check(
+            self._lib.kt_hip_linear_weights(self._h, x.ctypes.data, weights.id, w.ctypes.data, rows, out, k,
+                                            y.ctypes.data),
+            "linear_weights",
+        )
+        return y
+
+    def resident_bytes(self) -> int:
+        return self._lib.kt_hip_resident_bytes(self._h)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# 12-bit-weight path (device-resident operands; torch tensors or raw device pointers)
+
+
+def _ptr(t) -> int:
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(s) -> int:
+    if s is None:
+        return 0
+    if isinstance(s, int):
+        return s
+    return s.cuda_stream
+
+
+def w12_pack(codes_dev, n: int, k: int, lo_dev, nib_dev, stream=None, dev: int = 0) -> None:
+    """Pack n x k codes in [-2048, 2047] (i32, device) into the W12 planes lo (n x kp) and nib (n x kp/2)."""
+    check(lib().kt_hip_w12_pack(dev, _ptr(codes_dev), n, k, _ptr(lo_dev), _ptr(nib_dev), _stream(stream)), "w12 pack")
+
+
+def w12_upload(codes, n: int, k: int, lo_dev, nib_dev, dev: int = 0) -> None:
+    """Check host codes against [-2048, 2047], upload and pack them (synchronous)."""
+    c = _i32(codes)
+    if c.size != n * k:
+        raise ValueError("codes are not n·k")
+    check(lib().kt_hip_w12_upload(dev, c.ctypes.data, n, k, _ptr(lo_dev), _ptr(nib_dev)), "w12 upload")
+
+
+def w12_linear(x_dev, lo_dev, nib_dev, m: int, n: int, k: int, y_dev, out_kind: int = OUT_I64, mant_dev=None,
+               shift_dev=None, stream=None, dev: int = 0) -> None:
+    """y = requant_or_identity(x · Wᵀ) with x int8 (m x kp, zero padded) and W12 weights (n x k). Asynchronous."""
+    check(
+        lib().kt_hip_w12_linear(dev, _ptr(x_dev), _ptr(lo_dev), _ptr(nib_dev), m, n, k, _ptr(mant_dev),
+                                _ptr(shift_dev), out_kind, _ptr(y_dev), _stream(stream)),
+        "w12 linear",
+    )
+
+
+def digit_gemm(xa_dev, px: int, wb_dev, pw: int, y_dev, rows: int, out: int, k: int, flush: int = 0,
+               drop_top: bool = False, stream=None, dev: int = 0) -> None:
+    """The digit-plane product on device planes (kt_cuda_digit_gemm without the host copies)."""
+    check(
+        lib().kt_hip_digit_gemm(dev, _ptr(xa_dev), px, _ptr(wb_dev), pw, _ptr(y_dev), rows, out, k, flush,
+                                int(drop_top), _stream(stream)),
+        "digit gemm",
+    )
+
+
+def pack_planes(codes_dev, rows: int, k: int, planes: int, planes_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_pack_planes(dev, _ptr(codes_dev), rows, k, planes, _ptr(planes_dev), _stream(stream)),
+          "pack planes")
+
+
+def probe_mfma(a_dev, b_dev, c32_dev, c16_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_probe_mfma(dev, _ptr(a_dev), _ptr(b_dev), _ptr(c32_dev), _ptr(c16_dev), _stream(stream)),
+          "mfma probe")

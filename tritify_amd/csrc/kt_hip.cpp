@@ -1,0 +1,458 @@
+// Host side of the MI355X exact-integer linear backend: the C ABI declared in include/kt_hip.h.
+//
+// The backend layer is this build's counterpart of TcLinear<DeviceExec> (crates/02-runtime/kt-cuda/src/backend.rs:77-192
+// with device.rs:119-197): it chooses the digit planes from the operand ranges, keeps packed weights resident by
+// WeightId under an LRU byte budget, packs the activations on the device, runs the digit-plane MFMA product in
+// k-chunks short enough that no int32 accumulator can wrap, and copies the i64 result back. One mutex per backend
+// orders the calls and guards the scratch buffers and the cache (the reference's scratch and cache Mutexes).
+//
+// Compiled twice: libkt_hip.so (the product) and, with KT_HIP_PLANTS, libkt_hip_planted.so (the firing controls of
+// backend.rs:31-40, for tests only).
+
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <string.h>
+
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+#include "kt_kernels.h"
+
+namespace {
+
+std::atomic<uint64_t> g_fallbacks{0};
+std::atomic<uint64_t> g_next_id{1};
+
+int64_t kp_of(int64_t k) { return (k + 63) / 64 * 64; }
+
+// A device allocation that only grows (DevBuf::grow, kt-cuda/src/device.rs:101-106).
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t cap = 0;
+    hipError_t grow(size_t bytes) {
+        if (bytes <= cap) return hipSuccess;
+        if (ptr) {
+            hipError_t e = hipFree(ptr);
+            ptr = nullptr;
+            cap = 0;
+            if (e != hipSuccess) return e;
+        }
+        hipError_t e = hipMalloc(&ptr, bytes);
+        if (e != hipSuccess) {
+            ptr = nullptr;
+            return e;
+        }
+        cap = bytes;
+        return hipSuccess;
+    }
+    void release() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        cap = 0;
+    }
+};
+
+// The plane counts with a kernel instantiation: a code needing p balanced base-256 digits runs as 1, 3 or 5 planes.
+int plane_class(int p) { return p <= 1 ? 1 : (p <= 3 ? 3 : 5); }
+
+// The fewest balanced base-256 digits holding every code: 1 digit covers [-128, 127], each further digit maps a
+// range [lo, hi] to [256 lo - 128, 256 hi + 127].
+int digits_for(const int32_t* v, size_t n) {
+    int32_t lo = 0, hi = 0;
+    for (size_t i = 0; i < n; i++) {
+        lo = v[i] < lo ? v[i] : lo;
+        hi = v[i] > hi ? v[i] : hi;
+    }
+    int64_t mn = -128, mx = 127;
+    for (int p = 1; p < 5; p++) {
+        if (lo >= mn && hi <= mx) return p;
+        mn = mn * 256 - 128;
+        mx = mx * 256 + 127;
+    }
+    return 5;
+}
+
+// k-chunk of the int32 accumulators: a group sums at most min(px, pw) plane pairs per k, each at most 128^2 in
+// magnitude, so floor((2^31 - 1) / (min(px,pw) * 16384)) terms cannot wrap; rounded down to 256.
+int64_t flush_of(int px, int pw) {
+    int64_t n = px < pw ? px : pw;
+    return (2147483647LL / (n * 16384)) / 256 * 256;
+}
+
+struct Key {
+    bool has_id;
+    uint64_t id;
+    size_t out, k;
+    bool operator<(const Key& o) const {
+        return std::tie(has_id, id, out, k) < std::tie(o.has_id, o.id, o.out, o.k);
+    }
+};
+
+struct Entry {
+    int8_t* planes;
+    int pw;
+    uint64_t bytes;
+    uint64_t last_use;
+};
+
+const char* plant_name(int p) {
+    switch (p) {
+        case KT_PLANT_DROP_TOP: return "DropTopPlane";
+        case KT_PLANT_WRONG_CARRY: return "WrongCarry";
+        case KT_PLANT_NO_FLUSH: return "NoFlush";
+        case KT_PLANT_CACHE_BY_SHAPE: return "CacheByShape";
+        default: return "None";
+    }
+}
+
+}  // namespace
+
+struct kt_hip_backend {
+    int dev = 0;
+    std::string devname;
+    uint64_t budget = 0;
+    bool budget_given = false;
+    int plant = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    std::map<Key, Entry> cache;
+    uint64_t bytes = 0, tick = 0;
+    DevBuf xcodes, xplanes, ydev, wcodes;
+};
+
+#define KT_TRY(expr)                          \
+    do {                                      \
+        hipError_t e_ = (expr);               \
+        if (e_ != hipSuccess) return (int)e_; \
+    } while (0)
+
+extern "C" {
+
+// ----------------------------------------------------------------------------------------------------------------
+// Device layer (kt_cuda_* of crates/02-runtime/kt-cuda/src/digit_gemm.cu:86-147)
+// ----------------------------------------------------------------------------------------------------------------
+
+int kt_hip_device_count(int* n) {
+    *n = 0;
+    return (int)hipGetDeviceCount(n);
+}
+
+int kt_hip_device_info(int dev, char* name, int len, int* major, int* minor, size_t* free_bytes) {
+    hipDeviceProp_t p;
+    KT_TRY(hipGetDeviceProperties(&p, dev));
+    if (len > 0) {
+        strncpy(name, p.name, (size_t)len - 1);
+        name[len - 1] = 0;
+    }
+    *major = p.major;
+    *minor = p.minor;
+    KT_TRY(hipSetDevice(dev));
+    size_t total = 0;
+    return (int)hipMemGetInfo(free_bytes, &total);
+}
+
+int kt_hip_alloc(int dev, size_t bytes, void** p) {
+    KT_TRY(hipSetDevice(dev));
+    return (int)hipMalloc(p, bytes);
+}
+
+int kt_hip_free(int dev, void* p) {
+    KT_TRY(hipSetDevice(dev));
+    return (int)hipFree(p);
+}
+
+int kt_hip_upload(int dev, void* dst, const void* src, size_t bytes) {
+    KT_TRY(hipSetDevice(dev));
+    return (int)hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+}
+
+int kt_hip_download(int dev, void* dst, const void* src, size_t bytes) {
+    KT_TRY(hipSetDevice(dev));
+    return (int)hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+}
+
+const char* kt_hip_error_string(int e) { return hipGetErrorString((hipError_t)e); }
+
+int64_t kt_hip_kp(int64_t k) { return kp_of(k); }
+
+int kt_hip_planes_for(const int32_t* codes, size_t n) { return plane_class(digits_for(codes, n)); }
+
+int kt_hip_pack_planes(int dev, const int32_t* codes_dev, int64_t rows, int64_t k, int planes, int8_t* planes_dev,
+                       void* stream) {
+    if (planes != 1 && planes != 3 && planes != 5) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_pack_planes(codes_dev, rows, k, planes, 0, planes_dev, (hipStream_t)stream);
+}
+
+int64_t kt_hip_flush_k(int px, int pw) { return flush_of(px, pw); }
+
+int kt_hip_digit_gemm(int dev, const int8_t* xa_dev, int px, const int8_t* wb_dev, int pw, int64_t* y_dev,
+                      int64_t rows, int64_t out, int64_t k, int64_t flush_k, int drop_top, void* stream) {
+    if (rows <= 0 || out <= 0) return 0;
+    const int64_t kp = kp_of(k);
+    if (rows > INT_MAX || out > INT_MAX || kp > INT_MAX) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    hipStream_t s = (hipStream_t)stream;
+    if (k == 0) return (int)hipMemsetAsync(y_dev, 0, (size_t)rows * (size_t)out * 8, s);
+    int64_t fk = flush_k <= 0 ? flush_of(px, pw) : flush_k;
+    if (fk % 256) return (int)hipErrorInvalidValue;
+    for (int64_t k0 = 0; k0 < kp; k0 += fk) {
+        const int64_t k1 = kp - k0 < fk ? kp : k0 + fk;
+        KT_TRY(kt::launch_plane_gemm(px, pw, xa_dev, wb_dev, y_dev, (int)rows, (int)out, (int)kp, (int)k0, (int)k1,
+                                     k0 > 0, drop_top, s));
+    }
+    return 0;
+}
+
+// ----------------------------------------------------------------------------------------------------------------
+// Backend layer (TcLinear, crates/02-runtime/kt-cuda/src/backend.rs:77-192)
+// ----------------------------------------------------------------------------------------------------------------
+
+static int open_impl(int dev, uint64_t budget, int plant, kt_hip_backend** out) {
+    *out = nullptr;
+    int n = 0;
+    KT_TRY(hipGetDeviceCount(&n));
+    if (dev < 0 || dev >= n) return (int)hipErrorInvalidDevice;
+    hipDeviceProp_t p;
+    KT_TRY(hipGetDeviceProperties(&p, dev));
+    KT_TRY(hipSetDevice(dev));
+    size_t free_b = 0, total = 0;
+    KT_TRY(hipMemGetInfo(&free_b, &total));
+    kt_hip_backend* b = new kt_hip_backend();
+    b->dev = dev;
+    b->devname = p.name;
+    b->budget_given = budget != 0;
+    b->budget = budget != 0 ? budget : (uint64_t)free_b / 5 * 4;  // kt-cuda/src/device.rs:147-149
+    b->plant = plant;
+    hipError_t e = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete b;
+        return (int)e;
+    }
+    *out = b;
+    return 0;
+}
+
+int kt_hip_open(int dev, uint64_t budget_bytes, kt_hip_backend** out) { return open_impl(dev, budget_bytes, 0, out); }
+
+int kt_hip_open_planted(int dev, int plant, kt_hip_backend** out) {
+#ifdef KT_HIP_PLANTS
+    if (plant < KT_PLANT_DROP_TOP || plant > KT_PLANT_CACHE_BY_SHAPE) return (int)hipErrorInvalidValue;
+    return open_impl(dev, 0, plant, out);
+#else
+    (void)dev;
+    (void)plant;
+    *out = nullptr;
+    return (int)hipErrorNotSupported;  // plants exist only in the test build
+#endif
+}
+
+void kt_hip_close(kt_hip_backend* b) {
+    if (!b) return;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        (void)hipSetDevice(b->dev);
+        (void)hipStreamSynchronize(b->stream);
+        for (auto& kv : b->cache) (void)hipFree(kv.second.planes);
+        b->cache.clear();
+        b->xcodes.release();
+        b->xplanes.release();
+        b->ydev.release();
+        b->wcodes.release();
+        (void)hipStreamDestroy(b->stream);
+    }
+    delete b;
+}
+
+int kt_hip_name(const kt_hip_backend* b, char* buf, int len) {
+    std::string s;
+    if (b->plant) s = std::string("planted-hip-") + plant_name(b->plant);
+    else if (b->budget_given) s = "hip:" + b->devname + " [budget " + std::to_string(b->budget) + " B]";
+    else s = "hip:" + b->devname;
+    if (len <= 0) return (int)hipErrorInvalidValue;
+    strncpy(buf, s.c_str(), (size_t)len - 1);
+    buf[len - 1] = 0;
+    return 0;
+}
+
+uint64_t kt_hip_weight_id_fresh(void) { return g_next_id.fetch_add(1); }
+
+uint64_t kt_hip_resident_bytes(const kt_hip_backend* b) {
+    std::lock_guard<std::mutex> g(const_cast<kt_hip_backend*>(b)->mu);
+    return b->bytes;
+}
+
+uint64_t kt_hip_fallbacks(void) { return g_fallbacks.load(); }
+
+// Packed weights for this call (TcLinear::weights, backend.rs:125-154): resident if the key was seen, else uploaded,
+// packed on the device and cached under the budget, evicting the least recently used. A weight larger than the
+// budget is used for its call and dropped (*temp = true).
+static hipError_t weights_for(kt_hip_backend* b, const int32_t* w, const uint64_t* id, size_t out, size_t k,
+                              int8_t** planes, int* pw, bool* temp) {
+    const bool keyed = id != nullptr;
+    Key key{keyed && b->plant != KT_PLANT_CACHE_BY_SHAPE, keyed ? *id : 0, out, k};
+    b->tick++;
+    if (keyed) {
+        auto it = b->cache.find(key);
+        if (it != b->cache.end()) {
+            it->second.last_use = b->tick;
+            *planes = it->second.planes;
+            *pw = it->second.pw;
+            *temp = false;
+            return hipSuccess;
+        }
+    }
+    const int p = plane_class(digits_for(w, out * k));
+    const int64_t kp = kp_of((int64_t)k);
+    const uint64_t bytes = (uint64_t)p * out * (uint64_t)kp;
+    hipError_t e = b->wcodes.grow(out * k * sizeof(int32_t));
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(b->wcodes.ptr, w, out * k * sizeof(int32_t), hipMemcpyHostToDevice, b->stream);
+    if (e != hipSuccess) return e;
+    if (keyed) {
+        while (b->bytes + bytes > b->budget && !b->cache.empty()) {
+            auto lru = b->cache.begin();
+            for (auto it = b->cache.begin(); it != b->cache.end(); ++it)
+                if (it->second.last_use < lru->second.last_use) lru = it;
+            e = hipStreamSynchronize(b->stream);  // nothing queued may still read the evicted planes
+            if (e != hipSuccess) return e;
+            e = hipFree(lru->second.planes);
+            b->bytes -= lru->second.bytes;
+            b->cache.erase(lru);
+            if (e != hipSuccess) return e;
+        }
+    }
+    int8_t* dst = nullptr;
+    e = hipMalloc((void**)&dst, bytes);
+    if (e != hipSuccess) return e;
+    e = kt::launch_pack_planes((const int32_t*)b->wcodes.ptr, (int64_t)out, (int64_t)k, p, 0, dst, b->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(dst);
+        return e;
+    }
+    *planes = dst;
+    *pw = p;
+    *temp = !(keyed && bytes <= b->budget);
+    if (!*temp) {
+        b->cache[key] = Entry{dst, p, bytes, b->tick};
+        b->bytes += bytes;
+    }
+    return hipSuccess;
+}
+
+// TcLinear::run (backend.rs:156-172) on the device.
+static int run(kt_hip_backend* b, const int32_t* x, const int32_t* w, const uint64_t* id, size_t rows, size_t out,
+               size_t k, int64_t* y) {
+    if (rows == 0 || out == 0) return 0;
+    if (k == 0) {
+        memset(y, 0, rows * out * sizeof(int64_t));
+        return 0;
+    }
+    const int64_t kp = kp_of((int64_t)k);
+    if (rows > INT_MAX || out > INT_MAX || kp > INT_MAX) return (int)hipErrorInvalidValue;
+    std::lock_guard<std::mutex> g(b->mu);
+    KT_TRY(hipSetDevice(b->dev));
+    const int px = plane_class(digits_for(x, rows * k));
+    int8_t* wplanes = nullptr;
+    int pw = 0;
+    bool temp = false;
+    KT_TRY(weights_for(b, w, id, out, k, &wplanes, &pw, &temp));
+    hipError_t e = hipSuccess;
+    auto fail = [&](hipError_t err) {
+        if (temp) {
+            (void)hipStreamSynchronize(b->stream);
+            (void)hipFree(wplanes);
+        }
+        return (int)err;
+    };
+    if ((e = b->xcodes.grow(rows * k * sizeof(int32_t))) != hipSuccess) return fail(e);
+    if ((e = b->xplanes.grow((size_t)px * rows * (size_t)kp)) != hipSuccess) return fail(e);
+    if ((e = b->ydev.grow(rows * out * sizeof(int64_t))) != hipSuccess) return fail(e);
+    if ((e = hipMemcpyAsync(b->xcodes.ptr, x, rows * k * sizeof(int32_t), hipMemcpyHostToDevice, b->stream)) !=
+        hipSuccess)
+        return fail(e);
+    const int wrong_carry = b->plant == KT_PLANT_WRONG_CARRY;
+    if ((e = kt::launch_pack_planes((const int32_t*)b->xcodes.ptr, (int64_t)rows, (int64_t)k, px, wrong_carry,
+                                    (int8_t*)b->xplanes.ptr, b->stream)) != hipSuccess)
+        return fail(e);
+    const int64_t fk = b->plant == KT_PLANT_NO_FLUSH ? kp : flush_of(px, pw);
+    for (int64_t k0 = 0; k0 < kp; k0 += fk) {
+        const int64_t k1 = kp - k0 < fk ? kp : k0 + fk;
+        if ((e = kt::launch_plane_gemm(px, pw, (const int8_t*)b->xplanes.ptr, wplanes, (int64_t*)b->ydev.ptr,
+                                       (int)rows, (int)out, (int)kp, (int)k0, (int)k1, k0 > 0,
+                                       b->plant == KT_PLANT_DROP_TOP, b->stream)) != hipSuccess)
+            return fail(e);
+    }
+    if ((e = hipMemcpyAsync(y, b->ydev.ptr, rows * out * sizeof(int64_t), hipMemcpyDeviceToHost, b->stream)) !=
+        hipSuccess)
+        return fail(e);
+    if ((e = hipStreamSynchronize(b->stream)) != hipSuccess) return fail(e);
+    if (temp) KT_TRY(hipFree(wplanes));
+    return 0;
+}
+
+int kt_hip_linear(kt_hip_backend* b, const int32_t* x, const int32_t* w, size_t rows, size_t out, size_t k,
+                  int64_t* y) {
+    return run(b, x, w, nullptr, rows, out, k, y);
+}
+
+int kt_hip_linear_weights(kt_hip_backend* b, const int32_t* x, uint64_t weight_id, const int32_t* w, size_t rows,
+                          size_t out, size_t k, int64_t* y) {
+    return run(b, x, w, &weight_id, rows, out, k, y);
+}
+
+// ----------------------------------------------------------------------------------------------------------------
+// 12-bit-weight path
+// ----------------------------------------------------------------------------------------------------------------
+
+int kt_hip_w12_pack(int dev, const int32_t* codes_dev, int64_t n, int64_t k, int8_t* lo_dev, uint8_t* nib_dev,
+                    void* stream) {
+    if (n < 0 || k < 0) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_pack(codes_dev, n, k, lo_dev, nib_dev, (hipStream_t)stream);
+}
+
+int kt_hip_w12_upload(int dev, const int32_t* codes, int64_t n, int64_t k, int8_t* lo_dev, uint8_t* nib_dev) {
+    if (n < 0 || k < 0) return (int)hipErrorInvalidValue;
+    const size_t cnt = (size_t)n * (size_t)k;
+    for (size_t i = 0; i < cnt; i++)
+        if (codes[i] < -2048 || codes[i] > 2047) return (int)hipErrorInvalidValue;
+    if (cnt == 0) return 0;
+    KT_TRY(hipSetDevice(dev));
+    void* tmp = nullptr;
+    KT_TRY(hipMalloc(&tmp, cnt * sizeof(int32_t)));
+    hipError_t e = hipMemcpy(tmp, codes, cnt * sizeof(int32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = kt::launch_w12_pack((const int32_t*)tmp, n, k, lo_dev, nib_dev, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    hipError_t f = hipFree(tmp);
+    return (int)(e != hipSuccess ? e : f);
+}
+
+int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                      int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
+                      void* y_dev, void* stream) {
+    if (m < 0 || n < 0 || k < 0) return (int)hipErrorInvalidValue;
+    if (m == 0 || n == 0) return 0;
+    const int64_t kp = kp_of(k);
+    if (m > INT_MAX || n > INT_MAX || kp > INT_MAX) return (int)hipErrorInvalidValue;
+    if (out_kind != KT_OUT_I64 && (mant_dev == nullptr || shift_dev == nullptr)) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    if (kp == 0) {
+        // an empty dot is 0; its requant is 0 as well
+        const size_t w = out_kind == KT_OUT_I64 ? 8 : (out_kind == KT_OUT_I32 ? 4 : 1);
+        return (int)hipMemsetAsync(y_dev, 0, (size_t)m * (size_t)n * w, (hipStream_t)stream);
+    }
+    return (int)kt::launch_w12_linear(x_dev, lo_dev, nib_dev, (int)m, (int)n, (int)kp, mant_dev, shift_dev, out_kind,
+                                      y_dev, (hipStream_t)stream);
+}
+
+int kt_hip_probe_mfma(int dev, const int8_t* a_dev, const int8_t* b_dev, int32_t* c32_dev, int32_t* c16_dev,
+                      void* stream) {
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_mfma_probe(a_dev, b_dev, c32_dev, c16_dev, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,20 @@
+// Internal launch interface between the host library (kt_hip.cpp) and the gfx950 kernels (kt_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kt_hip.h"
+
+namespace kt {
+
+hipError_t launch_pack_planes(const int32_t* codes, int64_t rows, int64_t k, int p, int wrong_carry, int8_t* out,
+                              hipStream_t s);
+hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int8_t* lo, uint8_t* nib, hipStream_t s);
+hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
+                             int k0, int k1, int accumulate, int drop_top, hipStream_t s);
+hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
+                             const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s);
+hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
+
+}  // namespace kt

@@ -1,0 +1,143 @@
+"""Synthetic inputs of the benchmark workloads, integer-only and identical on every machine.
+
+The stream is the reference's LCG, s <- s*6364136223846793005 + 1442695040888963407 mod 2^64
+(apps/kt-demo/src/main.rs:19-22), drawn as (s >> 33). It is evaluated here in numpy: a first block step by step,
+then the sequence doubles, each new half the affine map s -> A*s + C (mod 2^64) of the half before it.
+
+- gen_demo: the kt-demo generator (main.rs:23-28), BASELINE config 1.
+- gen_w12 / gen_act_gauss / channel_scales: BASELINE config 2 (this build's definitions): 12-bit weight codes
+  uniform in [-2048, 2047]; activations round(N(0, sigma)) clipped to +-127, N(0,1) drawn as an Irwin-Hall sum of
+  12 16-bit uniforms; per-channel int32 requant scales mapping 4 standard deviations of a channel's accumulator to
+  127 (crates/00-kernels/kt-int/src/lib.rs:191-212 for the fixed-point ratio).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+LCG_A = 6364136223846793005
+LCG_C = 1442695040888963407
+M64 = (1 << 64) - 1
+_BLOCK = 1 << 10
+
+
+def lcg_states(seed: int, n: int) -> np.ndarray:
+    """The n states after `seed` (the value lcg() returns on each of n calls). The first block is stepped; then,
+    holding `have` states and the affine map (A, C) of `have` steps, the next `have` states are A*out[i] + C."""
+    out = np.empty(n, dtype=np.uint64)
+    if n == 0:
+        return out
+    first = min(n, _BLOCK)
+    s, a, c = seed & M64, 1, 0
+    head = []
+    for _ in range(first):
+        s = (s * LCG_A + LCG_C) & M64
+        a, c = (a * LCG_A) & M64, (c * LCG_A + LCG_C) & M64
+        head.append(s)
+    out[:first] = np.array(head, dtype=np.uint64)
+    have = first
+    with np.errstate(over="ignore"):
+        while have < n:
+            take = min(have, n - have)
+            dst = out[have:have + take]
+            np.multiply(out[:take], np.uint64(a), out=dst)
+            np.add(dst, np.uint64(c), out=dst)
+            a, c = (a * a) & M64, (a * c + c) & M64
+            have += take
+    return out
+
+
+def _draws(seed: int, n: int) -> np.ndarray:
+    st = lcg_states(seed, n)
+    np.right_shift(st, np.uint64(33), out=st)
+    return st.view(np.int64)
+
+
+def gen_demo(m: int, n: int, k: int, seed: int = 42):
+    """kt-demo: qx (m*k in [-127,127]) then qw (n*k in {-1,0,1}) from one stream (main.rs:23-28)."""
+    d = _draws(seed ^ 0x9E3779B97F4A7C15, m * k + n * k)
+    qx = (d[: m * k] % 255 - 127).astype(np.int32)
+    qw = (d[m * k:] % 3 - 1).astype(np.int32)
+    return qx, qw
+
+
+def gen_w12(seed: int, n: int) -> np.ndarray:
+    """n codes uniform in [-2048, 2047] on the stream seed ^ 0x9E3779B97F4A7C15."""
+    d = _draws(seed ^ 0x9E3779B97F4A7C15, n)
+    np.bitwise_and(d, 4095, out=d)  # % 4096 of a non-negative draw
+    np.subtract(d, 2048, out=d)
+    return d.astype(np.int32)
+
+
+def gen_act_gauss(seed: int, sigma: int, n: int) -> np.ndarray:
+    """n activations round_half_away(N(0, sigma)) clipped to +-127 on the stream seed ^ 0xD1B54A32D192ED03:
+    t = 2 * (sum of 12 draws & 0xFFFF) - 12 * 65535, x = sign(t) * ((|t| * sigma + 2^16) >> 17)."""
+    out = np.empty(n, dtype=np.int32)
+    chunk = 1 << 20
+    s = (seed ^ 0xD1B54A32D192ED03) & M64
+    done = 0
+    while done < n:
+        cnt = min(chunk, n - done)
+        st = lcg_states(s, 12 * cnt)
+        s = int(st[-1])
+        np.right_shift(st, np.uint64(33), out=st)
+        u = st.view(np.int64)
+        np.bitwise_and(u, 0xFFFF, out=u)
+        t = 2 * u.reshape(cnt, 12).sum(axis=1) - 12 * 65535
+        mag = (np.abs(t) * sigma + 65536) >> 17
+        v = np.where(t < 0, -mag, mag)
+        out[done:done + cnt] = np.clip(v, -127, 127)
+        done += cnt
+    return out
+
+
+def _bits(x: int) -> int:
+    return x.bit_length()
+
+
+def scale_from_ratio(num: int, den: int) -> tuple[int, int]:
+    """kt_int::Scale::from_ratio (crates/00-kernels/kt-int/src/lib.rs:191-212): (mant, shift), mant ~31 bits."""
+    if num == 0:
+        return 0, 0
+    while _bits(num) > 64 or _bits(den) > 64:
+        num >>= 1
+        den >>= 1
+    den = max(den, 1)
+    s = 31 - (_bits(num) - _bits(den))
+    if s >= 0:
+        mant = ((num << s) + den // 2) // den
+    else:
+        dd = den << (-s)
+        mant = (num + dd // 2) // dd
+    return mant, s
+
+
+def scale_to_i32(mant: int, shift: int) -> tuple[int, int]:
+    """An int32 multiplier: halve the mantissa with rounding (lowering the shift) until it is below 2^31."""
+    while mant >= 1 << 31:
+        mant = (mant + 1) >> 1
+        shift -= 1
+    return mant, shift
+
+
+def channel_scales(w: np.ndarray, n: int, k: int, sigma: int = 40):
+    """Per output channel: scale = to_i32(from_ratio(127, 4 * sigma * isqrt(sum_k w^2)))."""
+    ss = (w.reshape(n, k).astype(np.int64) ** 2).sum(axis=1)
+    mant = np.zeros(n, dtype=np.int32)
+    shift = np.zeros(n, dtype=np.int32)
+    for o in range(n):
+        root = math.isqrt(int(ss[o]))
+        if root == 0:
+            continue
+        m, s = scale_to_i32(*scale_from_ratio(127, 4 * sigma * root))
+        mant[o], shift[o] = m, s
+    return mant, shift
+
+
+def pad_k(x: np.ndarray, m: int, k: int) -> np.ndarray:
+    """int8 activations m x k -> m x kp (kp = k rounded up to 64), zero padded: the device operand layout."""
+    kp = (k + 63) // 64 * 64
+    out = np.zeros((m, kp), dtype=np.int8)
+    out[:, :k] = x.reshape(m, k)
+    return out
