@@ -293,7 +293,8 @@ uint64_t kt_hip_fallbacks(void) { return g_fallbacks.load(); }
 static hipError_t weights_for(kt_hip_backend* b, const int32_t* w, const uint64_t* id, size_t out, size_t k,
                               int8_t** planes, int* pw, bool* temp) {
     const bool keyed = id != nullptr;
-    Key key{keyed && b->plant != KT_PLANT_CACHE_BY_SHAPE, keyed ? *id : 0, out, k};
+    const bool by_id = keyed && b->plant != KT_PLANT_CACHE_BY_SHAPE;  // the planted cache drops the id
+    Key key{by_id, by_id ? *id : 0, out, k};
     b->tick++;
     if (keyed) {
         auto it = b->cache.find(key);
