@@ -105,9 +105,12 @@ uint64_t kt_hip_fallbacks(void);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * 12-bit-weight path (BASELINE workloads), device-resident operands. No counterpart in the reference: there the
- * weights are 12-trit codes on the digit path above. Layout (W12): lo [n][kp] int8 = (v & 255) - 128 and
- * nib [n][kp/2] with hi = (v + 2048) >> 8; kp = kt_hip_kp(k).
+ * weights are 12-trit codes on the digit path above. W12 digits: lo = (v & 255) - 128 (int8), hi = (v + 2048) >> 8
+ * (4 bits), v = lo + 256 hi - 1920, stored fragment-tiled in blocks of 32 rows x 32 k (64 lanes x 16 lo bytes and
+ * 64 lanes x 8 nib bytes per block, in MFMA operand order). Activations are int8, m x kp, zero padded in k.
  * ------------------------------------------------------------------------------------------------------------- */
+/* Bytes of the W12 planes of an n x k matrix: lo = round_up(n, 32) * kp, nib = lo / 2. */
+void kt_hip_w12_bytes(int64_t n, int64_t k, size_t* lo_bytes, size_t* nib_bytes);
 /* Pack n x k codes in [-2048, 2047] (device) into W12 planes (device). Codes outside the range give wrong planes:
  * use kt_hip_w12_upload to have them checked. */
 int kt_hip_w12_pack(int dev, const int32_t* codes_dev, int64_t n, int64_t k, int8_t* lo_dev, uint8_t* nib_dev,
@@ -117,8 +120,9 @@ int kt_hip_w12_upload(int dev, const int32_t* codes, int64_t n, int64_t k, int8_
 /* Y = X W^T for int8 activations x_dev (m x kp, zero padded in k) against W12 weights (n x k), recombined exactly
  * in i64, then written per out_kind: KT_OUT_I64 the accumulators; KT_OUT_I32 / KT_OUT_I8
  * requant(acc, mant[o], shift[o]) (crates/00-kernels/kt-int/src/lib.rs:78-86) per output channel o, saturated /
- * clamped. mant_dev and shift_dev (n x i32, device) may be NULL for KT_OUT_I64. m <= 8 runs the streaming GEMV,
- * larger m the MFMA GEMM. Asynchronous on `stream`. */
+ * clamped. mant_dev and shift_dev (n x i32, device) may be NULL for KT_OUT_I64. Any int32 mant and shift are exact
+ * for |acc| < 2^31 (k <= 8192); larger k take a 128-bit product path. m <= 8 runs the streaming GEMV, larger m the
+ * MFMA GEMM. Asynchronous on `stream`. */
 int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                       int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
                       void* y_dev, void* stream);

@@ -705,54 +705,69 @@ int32_t kt_requant_dyn(int64_t v, int64_t num_level, int64_t den) {
 /* The 12-bit weight path (this build's own format, restated here as the checker)          */
 /* ------------------------------------------------------------------------------------------------------------ */
 
-/* W12 layout for an n x k matrix of codes v in [-2048, 2047], kp = k rounded up to 64:
- *   lo plane [n][kp] int8: (v & 255) ^ 0x80, i.e. lo = (v & 255) - 128 in [-128, 127];
- *   nib plane [n][kp/2] bytes: hi = (v + 2048) >> 8 in [0, 15], two per byte. In each 16-byte group (32 k-values
- *   of one row), byte 4q + b (q = 0..3, b = 0..3) holds k = 8q + b in its low nibble and k = 8q + 4 + b in its
- *   high nibble, so (dword_q & 0x0F0F0F0F) gives k = 8q..8q+3 and ((dword_q >> 4) & 0x0F0F0F0F) k = 8q+4..8q+7.
- * Padding (k >= K) is lo = 0, hi = 0 (the value there is irrelevant: the matching activation padding is 0).
- * The value is v = lo + 256 * hi - 1920, so sum_k x*v = S_lo + 256 * S_hi - 1920 * sum_k x. */
+/* W12 layout (this build's 12-bit weight format) for an n x k matrix of codes v in [-2048, 2047]. Digits:
+ *   lo = (v & 255) - 128 in [-128, 127] (an int8 plane), hi = (v + 2048) >> 8 in [0, 15], so v = lo + 256 hi - 1920
+ *   and sum_k x v = S_lo + 256 S_hi - 1920 sum_k x.
+ * Fragment tiling: np = n rounded up to 32, kp = k rounded up to 64. The matrix is cut into blocks of 32 rows x 32 k;
+ * block (nb, kb) (kb fastest, kp/32 per row block) holds 64 "lanes" of 16 lo bytes and 8 nib bytes each. Lane
+ * l = (n % 32) + 32 h, h = (k % 32) / 16, covers t = k % 16 = 0..15 of its row:
+ *   lo byte  ((nb * KB + kb) * 64 + l) * 16 + t;
+ *   nib byte ((nb * KB + kb) * 64 + l) * 8 + 4 (t / 8) + (t % 4), low nibble for t % 8 < 4, high nibble otherwise,
+ * so a lane's 8 nib bytes as dwords D0, D1 unpack to hi in t order as D0 & 0x0F0F0F0F, (D0 >> 4) & 0x0F0F0F0F,
+ * D1 & 0x0F0F0F0F, (D1 >> 4) & 0x0F0F0F0F. Padding rows and k are lo = 0, hi = 0. */
+static size_t w12_lo_index(size_t kp, size_t r, size_t c) {
+    size_t KB = kp / 32, nb = r / 32, kb = c / 32, lane = (r % 32) + 32 * ((c % 32) / 16);
+    return ((nb * KB + kb) * 64 + lane) * 16 + (c % 16);
+}
+
+static size_t w12_nib_index(size_t kp, size_t r, size_t c, int* high) {
+    size_t KB = kp / 32, nb = r / 32, kb = c / 32, lane = (r % 32) + 32 * ((c % 32) / 16), t = c % 16;
+    *high = (t % 8) >= 4;
+    return ((nb * KB + kb) * 64 + lane) * 8 + 4 * (t / 8) + (t % 4);
+}
+
+size_t kt_w12_lo_bytes(size_t n, size_t k) { return (n + 31) / 32 * 32 * ((k + 63) / 64 * 64); }
+
 void kt_w12_pack(const int32_t* codes, size_t n, size_t k, int8_t* lo, uint8_t* nib) {
-    size_t kp = (k + 63) / 64 * 64;
-    memset(lo, 0, n * kp);
-    memset(nib, 0, n * kp / 2);
+    size_t kp = (k + 63) / 64 * 64, np = (n + 31) / 32 * 32;
+    memset(lo, 0, np * kp);
+    memset(nib, 0, np * kp / 2);
     for (size_t r = 0; r < n; r++)
         for (size_t c = 0; c < k; c++) {
             int32_t v = codes[r * k + c];
-            lo[r * kp + c] = (int8_t)((v & 255) - 128);
+            lo[w12_lo_index(kp, r, c)] = (int8_t)((v & 255) - 128);
+            int high;
+            size_t b = w12_nib_index(kp, r, c, &high);
             uint32_t hi = (uint32_t)(v + 2048) >> 8;
-            size_t g = c / 32, kk = c % 32, q = kk / 8, within = kk % 8;
-            size_t byte = r * (kp / 2) + g * 16 + q * 4 + (within & 3);
-            nib[byte] |= (uint8_t)(within < 4 ? hi : hi << 4);
+            nib[b] |= (uint8_t)(high ? hi << 4 : hi);
         }
 }
 
 /* Decode one code back from the W12 layout (for the exhaustive round-trip test). */
 int32_t kt_w12_get(const int8_t* lo, const uint8_t* nib, size_t k, size_t r, size_t c) {
     size_t kp = (k + 63) / 64 * 64;
-    size_t g = c / 32, kk = c % 32, q = kk / 8, within = kk % 8;
-    uint8_t b = nib[r * (kp / 2) + g * 16 + q * 4 + (within & 3)];
-    int32_t hi = within < 4 ? (b & 15) : (b >> 4);
-    return (int32_t)lo[r * kp + c] + 256 * hi - 1920;
+    int high;
+    uint8_t b = nib[w12_nib_index(kp, r, c, &high)];
+    int32_t hi = high ? (b >> 4) : (b & 15);
+    return (int32_t)lo[w12_lo_index(kp, r, c)] + 256 * hi - 1920;
 }
 
-/* The exact accumulators of int8 activations x (m x k, values in [-128,127] as i32) against 12-bit weights
- * (n x k codes), computed from the W12 planes the way the device does -- two int32 plane sums and the row-sum
- * correction, recombined in i64 -- so a layout or recombination mistake shows up against kt_linear_cpu. */
+/* The exact accumulators of int8 activations x (m x k, values in [-128,127] as i32) against 12-bit weights in the
+ * W12 layout, computed the way the device does -- two int32 plane sums and the row-sum correction, recombined in
+ * i64 -- so a layout or recombination mistake shows up against kt_linear_cpu. */
 void kt_w12_linear(const int32_t* x, const int8_t* lo, const uint8_t* nib, size_t m, size_t n, size_t k,
                    int64_t* y) {
+    size_t kp = (k + 63) / 64 * 64;
     for (size_t r = 0; r < m; r++) {
         int64_t rs = 0;
         for (size_t c = 0; c < k; c++) rs += x[r * k + c];
         for (size_t o = 0; o < n; o++) {
             int32_t s_lo = 0, s_hi = 0;
-            size_t kp = (k + 63) / 64 * 64;
             for (size_t c = 0; c < k; c++) {
-                int32_t l = lo[o * kp + c];
-                size_t g = c / 32, kk = c % 32, q = kk / 8, within = kk % 8;
-                uint8_t b = nib[o * (kp / 2) + g * 16 + q * 4 + (within & 3)];
-                int32_t h = within < 4 ? (b & 15) : (b >> 4);
-                s_lo += x[r * k + c] * l;
+                int high;
+                uint8_t b = nib[w12_nib_index(kp, o, c, &high)];
+                int32_t h = high ? (b >> 4) : (b & 15);
+                s_lo += x[r * k + c] * (int32_t)lo[w12_lo_index(kp, o, c)];
                 s_hi += x[r * k + c] * h;
             }
             y[r * n + o] = (int64_t)s_lo + 256 * (int64_t)s_hi - 1920 * rs;

@@ -402,11 +402,17 @@ def requant_dyn(v: int, num_level: int, den: int) -> int:
 # the 12-bit weight path
 
 
+def w12_sizes(n: int, k: int):
+    """Bytes of the W12 lo and nib planes: rows rounded up to 32, k to 64."""
+    lo = (n + 31) // 32 * 32 * ((k + 63) // 64 * 64)
+    return lo, lo // 2
+
+
 def w12_pack(codes_, n: int, k: int):
     codes_ = _i32(codes_)
-    kp = (k + 63) // 64 * 64
-    lo = np.empty(n * kp, dtype=np.int8)
-    nib = np.empty(n * kp // 2, dtype=np.uint8)
+    nlo, nnib = w12_sizes(n, k)
+    lo = np.empty(nlo, dtype=np.int8)
+    nib = np.empty(nnib, dtype=np.uint8)
     lib().kt_w12_pack(_ptr(codes_), n, k, _ptr(lo), _ptr(nib))
     return lo, nib
 

@@ -229,9 +229,9 @@ def test_device_level_digit_gemm(torch_dev):
 
 def _w12_device(torch, w, n, k):
     T = tb()
-    kp = T.kp(k)
-    lo = torch.empty(n * kp, dtype=torch.int8, device="cuda")
-    nib = torch.empty(n * kp // 2, dtype=torch.uint8, device="cuda")
+    nlo, nnib = T.w12_bytes(n, k)
+    lo = torch.empty(nlo, dtype=torch.int8, device="cuda")
+    nib = torch.empty(nnib, dtype=torch.uint8, device="cuda")
     T.w12_upload(w, n, k, lo, nib)
     return lo, nib
 

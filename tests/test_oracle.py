@@ -378,26 +378,33 @@ def test_quant_to_and_requant_dyn_against_rationals():
 
 
 def test_w12_layout_round_trips_every_code():
-    """Exhaustive: all 4096 codes, placed so each (row, k) position class is hit, decode back exactly."""
+    """Exhaustive: all 4096 codes, placed so each (row, k) position class is hit, decode back exactly; and the
+    fragment rule the kernels use holds on the packed bytes: lane l = (n % 32) + 32 h of block (n // 32, k // 32)
+    carries k = 32 kb + 16 h + t, t = 0..15, as 16 lo bytes in t order and 8 nib bytes whose dwords D0, D1 give
+    hi(t) for t = 0..15 as D0 & 0x0F0F0F0F, (D0 >> 4) & .., D1 & .., (D1 >> 4) & .. ."""
     n, k = 64, 64
     codes = np.arange(-2048, 2048, dtype=np.int32).reshape(n, k)
     lo, nib = O.w12_pack(codes, n, k)
     for r in range(n):
         for c in range(k):
             assert O.w12_get(lo, nib, k, r, c) == codes[r, c]
-    # the unpack rule the kernels use: dword q of a 16-byte group, AND 0x0F0F0F0F -> k = 8q..8q+3,
-    # (>> 4) AND 0x0F0F0F0F -> k = 8q+4..8q+7
-    words = nib.view(np.uint32).reshape(n, k // 8)
-    his = ((codes + 2048) >> 8).astype(np.uint32)
-    for r in range(n):
-        for g in range(k // 32):
-            for q in range(4):
-                d = int(words[r, g * 4 + q])
-                lo4 = [(d >> (8 * b)) & 15 for b in range(4)]
-                hi4 = [(d >> (8 * b + 4)) & 15 for b in range(4)]
-                base = 32 * g + 8 * q
-                assert lo4 == list(his[r, base:base + 4]) and hi4 == list(his[r, base + 4:base + 8])
-    assert np.array_equal(lo.reshape(n, k).astype(np.int32), (codes & 255) - 128)
+    KB = k // 32
+    his = ((codes + 2048) >> 8).astype(np.int64)
+    los = (codes & 255) - 128
+    for nb in range(n // 32):
+        for kb in range(KB):
+            for l in range(64):
+                frag = (nb * KB + kb) * 64 + l
+                row, ks = nb * 32 + l % 32, kb * 32 + 16 * (l // 32)
+                assert list(lo[frag * 16:frag * 16 + 16]) == list(los[row, ks:ks + 16])
+                d0, d1 = (int(v) for v in nib[frag * 8:frag * 8 + 8].view(np.uint32))
+                got = []
+                for d in (d0 & 0x0F0F0F0F, (d0 >> 4) & 0x0F0F0F0F, d1 & 0x0F0F0F0F, (d1 >> 4) & 0x0F0F0F0F):
+                    got += [(d >> (8 * b)) & 255 for b in range(4)]
+                assert got == list(his[row, ks:ks + 16])
+    # padding rows / k are zero digits
+    lo2, nib2 = O.w12_pack(np.full(3 * 5, 7, np.int32), 3, 5)
+    assert lo2.size == 32 * 64 and (lo2 != 0).sum() == 15 and (nib2 != 0).sum() > 0
 
 
 def test_w12_recombination_equals_the_direct_sum():

@@ -25,6 +25,7 @@ from .backend import (  # noqa: F401
     pack_planes,
     planes_for,
     probe_mfma,
+    w12_bytes,
     w12_linear,
     w12_pack,
     w12_upload,

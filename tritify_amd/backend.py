@@ -73,6 +73,7 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_weight_id_fresh": (_U64, []),
         "kt_hip_resident_bytes": (_U64, [_P]),
         "kt_hip_fallbacks": (_U64, []),
+        "kt_hip_w12_bytes": (None, [_I64, _I64, C.POINTER(_SZ), C.POINTER(_SZ)]),
         "kt_hip_w12_pack": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
         "kt_hip_w12_upload": (_I, [_I, _P, _I64, _I64, _P, _P]),
         "kt_hip_w12_linear": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
@@ -227,6 +228,13 @@ def _stream(s) -> int:
     if isinstance(s, int):
         return s
     return s.cuda_stream
+
+
+def w12_bytes(n: int, k: int) -> tuple[int, int]:
+    """Bytes of the W12 lo and nib planes of an n x k weight matrix (rows padded to 32, k to 64)."""
+    lo, nib = C.c_size_t(), C.c_size_t()
+    lib().kt_hip_w12_bytes(n, k, C.byref(lo), C.byref(nib))
+    return lo.value, nib.value
 
 
 def w12_pack(codes_dev, n: int, k: int, lo_dev, nib_dev, stream=None, dev: int = 0) -> None:

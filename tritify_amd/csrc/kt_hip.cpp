@@ -409,6 +409,12 @@ int kt_hip_linear_weights(kt_hip_backend* b, const int32_t* x, uint64_t weight_i
 // 12-bit-weight path
 // ----------------------------------------------------------------------------------------------------------------
 
+void kt_hip_w12_bytes(int64_t n, int64_t k, size_t* lo_bytes, size_t* nib_bytes) {
+    const size_t lo = (size_t)((n + 31) / 32 * 32) * (size_t)kp_of(k);
+    *lo_bytes = lo;
+    *nib_bytes = lo / 2;
+}
+
 int kt_hip_w12_pack(int dev, const int32_t* codes_dev, int64_t n, int64_t k, int8_t* lo_dev, uint8_t* nib_dev,
                     void* stream) {
     if (n < 0 || k < 0) return (int)hipErrorInvalidValue;

@@ -11,11 +11,12 @@
 //    wrap and launches one kernel per chunk, each adding its i64 result into y.
 //    Layout of a planed operand: [plane][row][kp] int8, kp = k rounded up to 64, zero padded.
 //
-// 2. W12 (int8 activations x 12-bit weight codes in [-2048, 2047]):
-//    lo plane [n][kp] int8 = (v & 255) - 128, nib plane [n][kp/2] holding hi = (v + 2048) >> 8 in [0, 15], so that
-//    v = lo + 256*hi - 1920 and sum_k x*v = S_lo + 256*S_hi - 1920*sum_k x. In each 16-byte nib group (32 k-values
-//    of one row) dword q has k = 8q..8q+3 in its low nibbles and k = 8q+4..8q+7 in its high nibbles, so one AND and
-//    one shift+AND unpack eight codes into two int8 dwords in natural k order.
+// 2. W12 (int8 activations x 12-bit weight codes in [-2048, 2047]): lo = (v & 255) - 128 (int8)
+//    and hi = (v + 2048) >> 8 (4 bits), v = lo + 256*hi - 1920, so sum_k x*v = S_lo + 256*S_hi - 1920*sum_k x.
+//    The weights are stored fragment-tiled: blocks of 32 rows x 32 k, each 64 lanes x (16 lo bytes + 8 nib bytes)
+//    in exactly the order one MFMA B operand takes them (lane l: row l%32, k = 16*(l/32) .. +16), so a wave fetches
+//    a B fragment with one fully coalesced 1 KB load and one 512-byte load, no LDS round trip. A lane's 8 nib bytes
+//    as dwords D0, D1 unpack in k order as D0 & 0x0F0F0F0F, (D0 >> 4) & .., D1 & .., (D1 >> 4) & .. .
 //
 // MFMA: v_mfma_i32_32x32x32_i8 (GEMM) and, for skinny M, v_mfma_i32_16x16x64_i8. A lane's 16 operand bytes are
 // 16 consecutive k of one row (A) / one column (B); the hardware pairs A and B bytes with the same k-slot, so any
@@ -25,6 +26,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "kt_kernels.h"
 
@@ -63,6 +66,15 @@ __device__ __forceinline__ void lds_write16(int8_t* base, int off, v4i v) {
 
 __device__ __forceinline__ v4i gload16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 __device__ __forceinline__ v2i gload8(const uint8_t* p) { return *reinterpret_cast<const v2i*>(p); }
+
+// A raw buffer over `bytes` bytes at `base`: loads at offsets past the end return zeros, so tile rows beyond the
+// matrix need no branch. The descriptor lives in SGPRs; each load takes a 32-bit VGPR offset plus a scalar offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
 
 // 16 nibble bytes (32 codes of one nib group) -> two 16-byte chunks of the hi plane in natural k order.
 __device__ __forceinline__ void unpack_nib(v4i d, v4i& h0, v4i& h1) {
@@ -124,30 +136,29 @@ __global__ void pack_planes_kernel(const int32_t* __restrict__ codes, int64_t ro
     }
 }
 
-// i32 codes [n][k] in [-2048, 2047] -> W12 planes (lo [n][kp], nib [n][kp/2]). One thread per nib byte.
+// i32 codes [n][k] in [-2048, 2047] -> fragment-tiled W12 planes (lo np*kp bytes, nib np*kp/2 bytes, np = n rounded
+// up to 32). One thread per fragment lane: 16 lo bytes and 8 nib bytes; padding rows and k get lo = 0, hi = 0.
 __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, int64_t k, int64_t kp,
                                 int8_t* __restrict__ lo, uint8_t* __restrict__ nib) {
-    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t per_row = kp / 2;
-    if (idx >= n * per_row) return;
-    int64_t r = idx / per_row, b = idx - r * per_row;
-    int64_t g = b >> 4, bi = b & 15;
-    int64_t c0 = g * 32 + (bi >> 2) * 8 + (bi & 3), c1 = c0 + 4;
-    int8_t l0 = 0, l1 = 0;  // padding (k..kp) is lo = 0, hi = 0
-    uint32_t h0 = 0, h1 = 0;
-    if (c0 < k) {
-        int32_t v = codes[r * k + c0];
-        l0 = (int8_t)((v & 255) - 128);
-        h0 = ((uint32_t)(v + 2048) >> 8) & 15;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // fragment-lane index
+    const int64_t KB = kp / 32, total = (n + 31) / 32 * KB * 64;
+    if (idx >= total) return;
+    const int64_t frag = idx >> 6, l = idx & 63, nb = frag / KB, kb = frag - nb * KB;
+    const int64_t r = nb * 32 + (l & 31), c0 = kb * 32 + 16 * (l >> 5);
+    uint32_t lw[4] = {0, 0, 0, 0}, nw[2] = {0, 0};
+    for (int t = 0; t < 16; t++) {
+        const int64_t c = c0 + t;
+        uint32_t lb = 0, hb = 0;
+        if (r < n && c < k) {
+            const int32_t v = codes[r * k + c];
+            lb = (uint32_t)((v & 255) - 128) & 255;
+            hb = ((uint32_t)(v + 2048) >> 8) & 15;
+        }
+        lw[t >> 2] |= lb << (8 * (t & 3));
+        nw[t >> 3] |= hb << (8 * (t & 3) + 4 * ((t >> 2) & 1));
     }
-    if (c1 < k) {
-        int32_t v = codes[r * k + c1];
-        l1 = (int8_t)((v & 255) - 128);
-        h1 = ((uint32_t)(v + 2048) >> 8) & 15;
-    }
-    lo[r * kp + c0] = l0;
-    lo[r * kp + c1] = l1;
-    nib[idx] = (uint8_t)(h0 | (h1 << 4));
+    *reinterpret_cast<v4i*>(lo + idx * 16) = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+    *reinterpret_cast<v2i*>(nib + idx * 8) = v2i{(int)nw[0], (int)nw[1]};
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -278,239 +289,404 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// W12 GEMM (BASELINE path, M >= 16). x int8 [M][lda] (lda = kp, zero padded), W12 lo [N][kp], nib [N][kp/2].
-// CTA = 4 waves in 2x2, each WTM x WTN tiles of 32x32; the hi plane is unpacked once per CTA on its way into LDS.
-// The row sums of x (for the -1920*sum_k x term) come from the A staging registers.
+// W12 GEMM (BASELINE path, M > 8). x int8 [M][kp] (zero padded); W12 fragment-tiled lo / nib.
+// CTA = 4 waves side by side along N; each wave owns WTM x WTN tiles of 32x32 (all BM = 32*WTM rows of the CTA,
+// its own 32*WTN columns), BK = 64. A goes global -> registers -> a 3-slot LDS ring; each wave's B fragments go
+// straight from global memory into registers. Both are issued two tiles ahead of the tile being multiplied, and
+// the loop is unrolled by three so every register set has a compile-time slot. Loads past the last tile read
+// other rows of the same buffer or zeros (never outside it); issuing them unconditionally lets the compiler wait
+// only for the set it is about to use. Row sums of x (for -1920 * sum_k x) come from the A staging registers.
+// Tiles are numbered so that the CTAs the hardware places on one XCD (block b -> XCD b % 8) form a compact group
+// of GM tile-rows, sharing A rows and B columns in that XCD's L2.
 // ------------------------------------------------------------------------------------------------------------------
-template <int WTM, int WTN, int BK, int OUT>
-__global__ __launch_bounds__(256) void w12_gemm_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ wlo,
-                                                       const uint8_t* __restrict__ wnib, void* __restrict__ y,
-                                                       int M, int N, int kp, const int32_t* __restrict__ mant,
-                                                       const int32_t* __restrict__ shift) {
-    constexpr int CPR = BK / 16;
-    constexpr int BM = 64 * WTM, BN = 64 * WTN;
-    constexpr int AL = BM * CPR / 256, BL = BN * CPR / 256;
-    constexpr int NC = BN * (BK / 32), NL = (NC + 255) / 256;  // 16-byte nib chunks of a tile
-    static_assert(AL >= 1 && BL >= 1, "tile too small for 256 threads");
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * BK];
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][2][BN * BK];
+
+// One W12 output from its two plane sums and the row-sum term: v = s_lo + 256 s_hi + corr (corr = -1920 sum x).
+// SMALL: every partial sum and v fit int32 (kp <= 8192: |v| <= 8192 * 2048 * 128 = 2^31), so v is formed in 32 bits
+// and the requant product |v| * mant (< 2^62) in 64 -- a handful of instructions per output.
+template <int OUT, bool SMALL>
+__device__ __forceinline__ void store_w12(void* y, size_t idx, int s_lo, int s_hi, int corr, int32_t mant, int32_t sh) {
+    if constexpr (SMALL) {
+        const int v = s_lo + (s_hi << 8) + corr;
+        if constexpr (OUT == KT_OUT_I64) {
+            reinterpret_cast<int64_t*>(y)[idx] = (int64_t)v;
+        } else {
+            const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+            const uint64_t prod = (uint64_t)a * (uint32_t)mant;
+            int64_t q;
+            if (sh <= 0) q = (int64_t)(prod << (-sh));
+            else q = (int64_t)((prod + ((uint64_t)1 << (sh - 1))) >> sh);  // sh <= 63: prod < 2^62
+            if (v < 0) q = -q;
+            if constexpr (OUT == KT_OUT_I32) {
+                q = q > INT32_MAX ? INT32_MAX : (q < INT32_MIN ? INT32_MIN : q);
+                reinterpret_cast<int32_t*>(y)[idx] = (int32_t)q;
+            } else {
+                q = q > 127 ? 127 : (q < -127 ? -127 : q);
+                reinterpret_cast<int8_t*>(y)[idx] = (int8_t)q;
+            }
+        }
+    } else {
+        const int64_t v = (int64_t)s_lo + 256 * (int64_t)s_hi + (int64_t)corr;
+        store_out<OUT>(y, idx, v, &mant, &sh, 0);
+    }
+}
+
+// The per-channel requant of a value |v| < 2^32 as one multiply-add and shift: for int32 mant and any shift,
+// requant(v, mant, shift) = sign * ((|v| * mt + bias) >> shr) with mt <= 2^32 - 1 (kt-int/src/lib.rs:78-86):
+//   shift > 0: mt = |mant|, shr = shift, bias = 2^(shift-1) (shift >= 63 gives 0: |v| * mt < 2^63 - 2^62);
+//   shift <= 0: mt = |mant| << -shift, saturated at 2^32 - 1 -- a saturated mt only arises when any nonzero |v|
+//   already exceeds every clamp bound, and zero stays zero.
+struct ColQ {
+    uint32_t mt, shr;
+    uint64_t bias;
+    bool neg;
+};
+
+__device__ __forceinline__ ColQ col_q(int32_t mant, int32_t sh) {
+    ColQ q;
+    q.neg = mant < 0;
+    const uint64_t am = mant < 0 ? (uint64_t)(-(int64_t)mant) : (uint64_t)mant;
+    if (sh >= 63) {
+        q.mt = 0, q.shr = 0, q.bias = 0;
+    } else if (sh > 0) {
+        q.mt = (uint32_t)am, q.shr = (uint32_t)sh, q.bias = (uint64_t)1 << (sh - 1);
+    } else {
+        const int up = -sh;
+        const uint64_t t = up >= 32 ? (am ? 0xFFFFFFFFull : 0) : am << up;
+        q.mt = (uint32_t)(t > 0xFFFFFFFFull ? 0xFFFFFFFFull : t), q.shr = 0, q.bias = 0;
+    }
+    return q;
+}
+
+// requant(v) clamped to [-lim, lim] for the int8 / int32 outputs.
+__device__ __forceinline__ int32_t col_requant(int v, const ColQ& q, uint32_t lim) {
+    const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+    uint64_t m = ((uint64_t)a * q.mt + q.bias) >> q.shr;
+    m = m > lim ? lim : m;
+    return ((v < 0) != q.neg) ? -(int32_t)m : (int32_t)m;
+}
+
+__device__ __forceinline__ void tile_coords(int M, int N, int BM, int BN, int& m0, int& n0) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, nt = tiles_m * tiles_n;
+    int bid = blockIdx.x;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);  // consecutive ids on one XCD
+    constexpr int GM = 4;
+    const int group = bid / (GM * tiles_n), first_m = group * GM;
+    const int gsize = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+    const int in_group = bid - group * GM * tiles_n;
+    m0 = (first_m + in_group % gsize) * BM;
+    n0 = (in_group / gsize) * BN;
+}
+
+__device__ __forceinline__ v2i bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
+
+__device__ __forceinline__ v4i unpack_hi(v2i d) {
+    const int m4 = 0x0F0F0F0F;
+    return v4i{d.x & m4, (d.x >> 4) & m4, d.y & m4, (d.y >> 4) & m4};
+}
+
+template <int I>
+using slot_t = std::integral_constant<int, I>;
+
+// Tile shape of the large-M W12 GEMM: waves per SIMD the register allocation targets, 32x32 tiles per wave.
+#ifndef KT_W12_WTM
+#define KT_W12_WTM 4
+#endif
+#ifndef KT_W12_WTN
+#define KT_W12_WTN 1
+#endif
+#ifndef KT_W12_WAVES
+#define KT_W12_WAVES 2
+#endif
+
+template <int WTM, int WTN, int WAVES, int OUT, bool SMALL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
+    const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
+    void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift) {
+    constexpr int BK = 64, CPR = 4;
+    constexpr int BM = 32 * WTM, BN = 128 * WTN;
+    constexpr int AC = BM * CPR, AL = (AC + 255) / 256;  // 16-byte A chunks per tile / per thread
+    constexpr int SA = 3 * BM * BK, SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // A ring; the int8 output tile after it
+    __shared__ __attribute__((aligned(16))) int8_t smem[SA > SO ? SA : SO];
+    int8_t(*sA)[BM * BK] = reinterpret_cast<int8_t(*)[BM * BK]>(smem);
     __shared__ int sRow[BM];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int tiles_n = (N + BN - 1) / BN;
-    const int m0 = (blockIdx.x / tiles_n) * BM, n0 = (blockIdx.x % tiles_n) * BN;
-    const size_t ldn = (size_t)kp / 2;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    int m0, n0;
+    tile_coords(M, N, BM, BN, m0, n0);
+    const int KB = kp / 32;
+
+    // A: the CTA's rows; rows past the matrix read as zero
+    const uint32_t rows_a = (uint32_t)(M - m0 < BM ? M - m0 : BM);
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(x + (size_t)m0 * kp, rows_a * (uint32_t)kp);
+    uint32_t oa[AL];
+#pragma unroll
+    for (int i = 0; i < AL; i++) {
+        const int idx = tid + 256 * i;
+        oa[i] = idx < AC ? (uint32_t)(idx >> 2) * (uint32_t)kp + 16 * (idx & 3) : 0xFFFFFFF0u;
+    }
+    // B: the CTA's column blocks (fragment-tiled); blocks past the matrix read as zero
+    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    uint32_t ob[WTN], on[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; j++) {
+        ob[j] = (uint32_t)((wave * WTN + j) * KB) * 1024 + 16 * lane;
+        on[j] = (uint32_t)((wave * WTN + j) * KB) * 512 + 8 * lane;
+    }
 
     v16i acc0[WTM][WTN], acc1[WTM][WTN];
 #pragma unroll
     for (int i = 0; i < WTM; i++)
 #pragma unroll
         for (int j = 0; j < WTN; j++) acc0[i][j] = acc1[i][j] = v16i{};
-
     int rsum[AL];
 #pragma unroll
     for (int i = 0; i < AL; i++) rsum[i] = 0;
 
-    v4i ra[AL], rl[BL], rn[NL];
-    auto gload_tile = [&](int k) {
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            int idx = tid + 256 * i, r = idx / CPR, c = idx % CPR;
-            int gr = m0 + r;
-            ra[i] = gr < M ? gload16(x + (size_t)gr * kp + k + 16 * c) : v4i{};
-        }
-#pragma unroll
-        for (int i = 0; i < BL; i++) {
-            int idx = tid + 256 * i, r = idx / CPR, c = idx % CPR;
-            int gr = n0 + r;
-            rl[i] = gr < N ? gload16(wlo + (size_t)gr * kp + k + 16 * c) : v4i{};
-        }
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            int idx = tid + 256 * i, r = idx / (BK / 32), g = idx % (BK / 32);
-            int gr = n0 + r;
-            rn[i] = (idx < NC && gr < N) ? gload16(reinterpret_cast<const int8_t*>(wnib) + (size_t)gr * ldn + k / 2 + 16 * g)
-                           : v4i{};
-        }
-    };
-    auto lstore_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            int idx = tid + 256 * i, r = idx / CPR, c = idx % CPR;
-            lds_write16(sA[buf], lds_off<CPR>(r, c), ra[i]);
-            rsum[i] += sum4(ra[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < BL; i++) {
-            int idx = tid + 256 * i, r = idx / CPR, c = idx % CPR;
-            lds_write16(sB[buf][0], lds_off<CPR>(r, c), rl[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            int idx = tid + 256 * i, r = idx / (BK / 32), g = idx % (BK / 32);
-            if (NC % 256 != 0 && idx >= NC) continue;
-            v4i h0, h1;
-            unpack_nib(rn[i], h0, h1);
-            lds_write16(sB[buf][1], lds_off<CPR>(r, 2 * g), h0);
-            lds_write16(sB[buf][1], lds_off<CPR>(r, 2 * g + 1), h1);
-        }
-    };
+    v4i ra[3][AL];
+    v4i bl[3][WTN][2];
+    v2i bn[3][WTN][2];
 
-    const int nk = kp / BK;
-    gload_tile(0);
-    lstore_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload_tile((kt + 1) * BK);
+    auto issue = [&](auto S, int kt) {  // global loads of tile kt into register slot S
+        constexpr int sl = decltype(S)::value;
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
-            const int chunk = 2 * ks + (lane >> 5);
-            v4i a[WTM], b0[WTN], b1[WTN];
+        for (int i = 0; i < AL; i++) ra[sl][i] = bload16(rA, oa[i], (uint32_t)(kt * BK));
+#pragma unroll
+        for (int j = 0; j < WTN; j++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                bl[sl][j][ks] = bload16(rL, ob[j], (uint32_t)(2 * kt + ks) * 1024u);
+                bn[sl][j][ks] = bload8(rN, on[j], (uint32_t)(2 * kt + ks) * 512u);
+            }
+    };
+    // `mask` is -1, or 0 for a tile past the end in the last round: its A fragments and row sums are zeroed
+    // instead of branched around, so no MFMA sits under control flow (which would cost accumulator copies).
+    auto stage = [&](auto S, int mask) {  // A of slot S into LDS buffer S
+        constexpr int sl = decltype(S)::value;
+#pragma unroll
+        for (int i = 0; i < AL; i++) {
+            const int idx = tid + 256 * i;
+            if (AC % 256 != 0 && idx >= AC) continue;
+            lds_write16(sA[sl], lds_off<CPR>(idx >> 2, idx & 3), ra[sl][i]);
+            rsum[i] += sum4(ra[sl][i]) & mask;
+        }
+    };
+    auto compute = [&](auto S, int mask) {
+        constexpr int sl = decltype(S)::value;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            v4i a[WTM];
 #pragma unroll
             for (int i = 0; i < WTM; i++) {
-                int r = wm * 32 * WTM + i * 32 + (lane & 31);
-                a[i] = lds_read16(sA[cur], lds_off<CPR>(r, chunk));
+                a[i] = lds_read16(sA[sl], lds_off<CPR>(i * 32 + (lane & 31), 2 * ks + half));
+                a[i] &= mask;
             }
 #pragma unroll
             for (int j = 0; j < WTN; j++) {
-                int r = wn * 32 * WTN + j * 32 + (lane & 31);
-                b0[j] = lds_read16(sB[cur][0], lds_off<CPR>(r, chunk));
-                b1[j] = lds_read16(sB[cur][1], lds_off<CPR>(r, chunk));
-            }
+                const v4i b0 = bl[sl][j][ks], b1 = unpack_hi(bn[sl][j][ks]);
 #pragma unroll
-            for (int i = 0; i < WTM; i++)
-#pragma unroll
-                for (int j = 0; j < WTN; j++) {
-                    acc0[i][j] = mfma32(a[i], b0[j], acc0[i][j]);
-                    acc1[i][j] = mfma32(a[i], b1[j], acc1[i][j]);
+                for (int i = 0; i < WTM; i++) {
+                    acc0[i][j] = mfma32(a[i], b0, acc0[i][j]);
+                    acc1[i][j] = mfma32(a[i], b1, acc1[i][j]);
                 }
+            }
         }
-        if (kt + 1 < nk) lstore_tile(cur ^ 1);
-        __syncthreads();
-    }
+    };
 
-    // row sums: the CPR threads of one row are consecutive lanes of one wave
+    // Rounds of three tiles kt, kt+1, kt+2 (slots 0, 1, 2); before a round, tile kt is in LDS slot 0 and tile
+    // kt+1 in register slot 1, and the round stages tile kt+3. Tiles past the end (only in the last round) are
+    // masked to zero. A do-while: the accumulators have one path into the epilogue.
+    const int nk = kp / BK;
+    issue(slot_t<0>{}, 0);
+    issue(slot_t<1>{}, 1);
+    stage(slot_t<0>{}, -1);
+    __syncthreads();
+    int kt = 0;
+    do {
+        const int m1 = kt + 1 < nk ? -1 : 0, m2 = kt + 2 < nk ? -1 : 0, m3 = kt + 3 < nk ? -1 : 0;
+        issue(slot_t<2>{}, kt + 2);
+        compute(slot_t<0>{}, -1);
+        stage(slot_t<1>{}, m1);
+        __syncthreads();
+        issue(slot_t<0>{}, kt + 3);
+        compute(slot_t<1>{}, m1);
+        stage(slot_t<2>{}, m2);
+        __syncthreads();
+        issue(slot_t<1>{}, kt + 4);
+        compute(slot_t<2>{}, m2);
+        stage(slot_t<0>{}, m3);
+        __syncthreads();
+        kt += 3;
+    } while (kt < nk);
+
+    // row sums: the 4 threads of a row are consecutive lanes
 #pragma unroll
     for (int i = 0; i < AL; i++) {
-        int s = rsum[i];
-#pragma unroll
-        for (int o = 1; o < CPR; o <<= 1) s += __shfl_xor(s, o);
-        int idx = tid + 256 * i;
-        if ((idx % CPR) == 0) sRow[idx / CPR] = s;
+        const int idx = tid + 256 * i;
+        int v = rsum[i];
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        if (idx < AC && (idx & 3) == 0) sRow[idx >> 2] = v;
     }
     __syncthreads();
 
-#pragma unroll
-    for (int i = 0; i < WTM; i++)
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+    if constexpr (OUT == KT_OUT_I8 && SMALL) {
+        // requantize into an int8 tile in LDS (the A ring is no longer read), then store it with 16-byte writes
 #pragma unroll
         for (int j = 0; j < WTN; j++) {
-            const int n = n0 + wn * 32 * WTN + j * 32 + (lane & 31);
+            const int c = wave * 32 * WTN + j * 32 + (lane & 31), n = n0 + c;
+            const ColQ q = col_q(n < N ? mant[n] : 0, n < N ? shift[n] : 1);
+#pragma unroll
+            for (int i = 0; i < WTM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int rt = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const int v = acc0[i][j][r] + (acc1[i][j][r] << 8) - 1920 * sRow[rt];
+                    smem[rt * BN + c] = (int8_t)col_requant(v, q, 127);
+                }
+        }
+        __syncthreads();
+        constexpr int CH = BM * BN / 16;  // 16-byte chunks of the tile
+#pragma unroll
+        for (int i = 0; i < (CH + 255) / 256; i++) {
+            const int idx = tid + 256 * i;
+            if (CH % 256 != 0 && idx >= CH) break;
+            const int rt = idx / (BN / 16), c = (idx % (BN / 16)) * 16, m = m0 + rt, n = n0 + c;
+            const v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
+            int8_t* dst = reinterpret_cast<int8_t*>(y) + (size_t)m * N + n;
+            if (full && (N & 15) == 0) {
+                *reinterpret_cast<v4i*>(dst) = v;
+            } else if (m < M) {
+                const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+                for (int t = 0; t < 16 && n + t < N; t++) dst[t] = b[t];
+            }
+        }
+    } else if constexpr (OUT == KT_OUT_I32 && SMALL) {
+#pragma unroll
+        for (int j = 0; j < WTN; j++) {
+            const int n = n0 + wave * 32 * WTN + j * 32 + (lane & 31);
+            const ColQ q = col_q(n < N ? mant[n] : 0, n < N ? shift[n] : 1);
+#pragma unroll
+            for (int i = 0; i < WTM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int rt = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3), m = m0 + rt;
+                    const int v = acc0[i][j][r] + (acc1[i][j][r] << 8) - 1920 * sRow[rt];
+                    // [-(2^31 - 1), 2^31 - 1]; -2^31 is unreachable: |v| < 2^31 except v = -2^31 with mt = 1
+                    int32_t o = col_requant(v, q, 0x7FFFFFFF);
+                    if (v == INT32_MIN && q.mt == 1 && q.shr == 0 && !q.neg) o = INT32_MIN;
+                    if (full || (m < M && n < N)) reinterpret_cast<int32_t*>(y)[(size_t)m * N + n] = o;
+                }
+        }
+    } else {
+        int32_t cm[WTN], cs[WTN];
+#pragma unroll
+        for (int j = 0; j < WTN; j++) {
+            const int n = n0 + wave * 32 * WTN + j * 32 + (lane & 31);
+            cm[j] = (OUT != KT_OUT_I64 && n < N) ? mant[n] : 0;
+            cs[j] = (OUT != KT_OUT_I64 && n < N) ? shift[n] : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < WTM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int rl_ = wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int m = m0 + rl_;
-                int64_t v = (int64_t)acc0[i][j][r] + 256 * (int64_t)acc1[i][j][r] - 1920 * (int64_t)sRow[rl_];
-                if (m < M && n < N) store_out<OUT>(y, (size_t)m * N + n, v, mant, shift, n);
-            }
-        }
-}
-
-// ------------------------------------------------------------------------------------------------------------------
-// W12 GEMV (batch decode, M <= 8). Bandwidth-bound: each wave owns NR output channels and streams their packed
-// codes with coalesced 16-byte (lo) and 8-byte (nib) loads -- lane j of chunk i reads k = 1024 i + 16 j .. +16 --
-// dots them against x with v_dot4_i32_i8, and reduces the lanes with DPP and ds_swizzle.
-// ------------------------------------------------------------------------------------------------------------------
-
-// Sum over the 64 lanes of a wave; every lane gets the total.
-__device__ __forceinline__ int wave_sum(int v) {
-    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]: lane ^ 1
-    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]: lane ^ 2
-    v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true); // row_half_mirror: the other quad of 8
-    v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true); // row_mirror: the other half of the row of 16
-    v += __builtin_amdgcn_ds_swizzle(v, 0x401F);             // xor 16 within 32 lanes
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
-}
-
-template <int MR, int NR, int OUT>
-__global__ __launch_bounds__(256) void w12_gemv_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ wlo,
-                                                       const uint8_t* __restrict__ wnib, void* __restrict__ y,
-                                                       int M, int N, int kp, const int32_t* __restrict__ mant,
-                                                       const int32_t* __restrict__ shift) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nbase = (blockIdx.x * 4 + wave) * NR;
-    if (nbase >= N) return;  // whole wave leaves; no barrier follows
-    const size_t ldn = (size_t)kp / 2;
-    const int mask = 0x0F0F0F0F, ones = 0x01010101;
-
-    int slo[MR][NR], shi[MR][NR], sx[MR];
+                const int rt = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);  // row within the CTA tile
+                const int corr = -1920 * sRow[rt];
+                const int m = m0 + rt;
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-        sx[m] = 0;
-#pragma unroll
-        for (int r = 0; r < NR; r++) slo[m][r] = shi[m][r] = 0;
-    }
-
-    constexpr int U = 4;  // chunks in flight per row
-    for (int c0 = 0; c0 * 1024 < kp; c0 += U) {
-        v4i L[U][NR];
-        v2i D[U][NR];
-        v4i X[U][MR];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int kk = (c0 + u) * 1024 + 16 * lane;
-            const bool ok = kk < kp;
-#pragma unroll
-            for (int r = 0; r < NR; r++) {
-                const int n = nbase + r;
-                const bool v = ok && n < N;
-                L[u][r] = v ? gload16(wlo + (size_t)n * kp + kk) : v4i{};
-                D[u][r] = v ? gload8(wnib + (size_t)n * ldn + kk / 2) : v2i{};
-            }
-#pragma unroll
-            for (int m = 0; m < MR; m++) X[u][m] = (ok && m < M) ? gload16(x + (size_t)m * kp + kk) : v4i{};
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                sx[m] = __builtin_amdgcn_sdot4(X[u][m].x, ones, sx[m], false);
-                sx[m] = __builtin_amdgcn_sdot4(X[u][m].y, ones, sx[m], false);
-                sx[m] = __builtin_amdgcn_sdot4(X[u][m].z, ones, sx[m], false);
-                sx[m] = __builtin_amdgcn_sdot4(X[u][m].w, ones, sx[m], false);
-            }
-#pragma unroll
-            for (int r = 0; r < NR; r++) {
-                const int h0 = D[u][r].x & mask, h1 = (D[u][r].x >> 4) & mask;
-                const int h2 = D[u][r].y & mask, h3 = (D[u][r].y >> 4) & mask;
-#pragma unroll
-                for (int m = 0; m < MR; m++) {
-                    int s = slo[m][r], t = shi[m][r];
-                    s = __builtin_amdgcn_sdot4(X[u][m].x, L[u][r].x, s, false);
-                    s = __builtin_amdgcn_sdot4(X[u][m].y, L[u][r].y, s, false);
-                    s = __builtin_amdgcn_sdot4(X[u][m].z, L[u][r].z, s, false);
-                    s = __builtin_amdgcn_sdot4(X[u][m].w, L[u][r].w, s, false);
-                    t = __builtin_amdgcn_sdot4(X[u][m].x, h0, t, false);
-                    t = __builtin_amdgcn_sdot4(X[u][m].y, h1, t, false);
-                    t = __builtin_amdgcn_sdot4(X[u][m].z, h2, t, false);
-                    t = __builtin_amdgcn_sdot4(X[u][m].w, h3, t, false);
-                    slo[m][r] = s;
-                    shi[m][r] = t;
+                for (int j = 0; j < WTN; j++) {
+                    const int n = n0 + wave * 32 * WTN + j * 32 + (lane & 31);
+                    if (full || (m < M && n < N))
+                        store_w12<OUT, SMALL>(y, (size_t)m * N + n, acc0[i][j][r], acc1[i][j][r], corr, cm[j], cs[j]);
                 }
             }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// W12 GEMV (batch decode, M <= 8). Bandwidth-bound: one CTA per 32-column block; its WPB waves take the block's
+// k32 fragments round-robin, so together they sweep the block's contiguous bytes with coalesced 1 KB (lo) and
+// 512-byte (nib) loads, U fragments in flight per wave. Each lane dots its 16 k of one column against x with
+// v_dot4_i32_i8; lanes l and l^32 hold the two k-halves, waves are summed through LDS.
+// ------------------------------------------------------------------------------------------------------------------
+template <int MR, int WPB, int U, int OUT>
+__global__ __launch_bounds__(64 * WPB) void w12_gemv_kernel(const int8_t* __restrict__ x,
+                                                            const int8_t* __restrict__ wlo,
+                                                            const uint8_t* __restrict__ wnib, void* __restrict__ y,
+                                                            int M, int N, int kp, const int32_t* __restrict__ mant,
+                                                            const int32_t* __restrict__ shift) {
+    __shared__ int64_t sPart[WPB][MR][32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
+    const int cb = blockIdx.x, KB = kp / 32;
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb * KB * 512, (uint32_t)KB * 512);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)(M * kp));
+    const int ones = 0x01010101;
+
+    int slo[MR], shi[MR], sx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) slo[m] = shi[m] = sx[m] = 0;
+
+    for (int base = wave; base < KB; base += WPB * U) {
+        v4i L[U], X[U][MR];
+        v2i D[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int kb = base + u * WPB;  // past the block: zeros from the weight buffers
+            L[u] = bload16(rL, 16 * lane, (uint32_t)kb * 1024u);
+            D[u] = bload8(rN, 8 * lane, (uint32_t)kb * 512u);
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                X[u][m] = m < M ? bload16(rX, (uint32_t)(m * kp + 16 * half), (uint32_t)kb * 32u) : v4i{};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (base + u * WPB >= KB) break;  // uniform: x past kp would be the next row
+            const v4i H = unpack_hi(D[u]);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const v4i xv = X[u][m];
+                int s = slo[m], t = shi[m], q = sx[m];
+                s = __builtin_amdgcn_sdot4(xv.x, L[u].x, s, false);
+                s = __builtin_amdgcn_sdot4(xv.y, L[u].y, s, false);
+                s = __builtin_amdgcn_sdot4(xv.z, L[u].z, s, false);
+                s = __builtin_amdgcn_sdot4(xv.w, L[u].w, s, false);
+                t = __builtin_amdgcn_sdot4(xv.x, H.x, t, false);
+                t = __builtin_amdgcn_sdot4(xv.y, H.y, t, false);
+                t = __builtin_amdgcn_sdot4(xv.z, H.z, t, false);
+                t = __builtin_amdgcn_sdot4(xv.w, H.w, t, false);
+                q = __builtin_amdgcn_sdot4(xv.x, ones, q, false);
+                q = __builtin_amdgcn_sdot4(xv.y, ones, q, false);
+                q = __builtin_amdgcn_sdot4(xv.z, ones, q, false);
+                q = __builtin_amdgcn_sdot4(xv.w, ones, q, false);
+                slo[m] = s;
+                shi[m] = t;
+                sx[m] = q;
+            }
         }
     }
 
+    // lane l and l^32 hold the two k-halves of column l%32 (DPP row broadcasts cannot cross the 32-lane halves,
+    // so this one exchange goes through ds_swizzle-free bpermute), then the waves meet in LDS
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-        if (m >= M) break;
-        const int64_t xs = wave_sum(sx[m]);
+        int64_t v = (int64_t)slo[m] + 256 * (int64_t)shi[m] - 1920 * (int64_t)sx[m];
+        v += __shfl_xor(v, 32);
+        if (half == 0) sPart[wave][m][lane] = v;
+    }
+    __syncthreads();
+    if (wave == 0 && half == 0) {
+        const int n = cb * 32 + lane;
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const int n = nbase + r;
-            const int64_t v = (int64_t)wave_sum(slo[m][r]) + 256 * (int64_t)wave_sum(shi[m][r]) - 1920 * xs;
-            if (lane == 0 && n < N) store_out<OUT>(y, (size_t)m * N + n, v, mant, shift, n);
+        for (int m = 0; m < MR; m++) {
+            int64_t v = 0;
+#pragma unroll
+            for (int w = 0; w < WPB; w++) v += sPart[w][m][lane];
+            if (m < M && n < N) store_out<OUT>(y, (size_t)m * N + n, v, mant, shift, n);
         }
     }
 }
@@ -546,7 +722,7 @@ hipError_t launch_pack_planes(const int32_t* codes, int64_t rows, int64_t k, int
 }
 
 hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int8_t* lo, uint8_t* nib, hipStream_t s) {
-    const int64_t kp = ceil_div(k, 64) * 64, total = n * (kp / 2);
+    const int64_t kp = ceil_div(k, 64) * 64, total = ceil_div(n, 32) * (kp / 32) * 64;
     if (total == 0) return hipSuccess;
     w12_pack_kernel<<<dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s>>>(codes, n, k, kp, lo, nib);
     return hipGetLastError();
@@ -581,23 +757,26 @@ template <int OUT>
 static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
                                  const int32_t* mant, const int32_t* shift, void* y, hipStream_t s) {
     if (M <= 8) {
-        constexpr int NR = 4;
-        dim3 grid((unsigned)ceil_div(N, 4 * NR));
-#define KT_GEMV(mr) \
-    if (M <= mr) { \
-        w12_gemv_kernel<mr, NR, OUT><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift); \
-        return hipGetLastError(); \
+        dim3 grid((unsigned)ceil_div(N, 32));
+#define KT_GEMV(mr, u)                                                                                      \
+    if (M <= mr) {                                                                                          \
+        w12_gemv_kernel<mr, 8, u, OUT><<<grid, dim3(512), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift); \
+        return hipGetLastError();                                                                           \
     }
-        KT_GEMV(1) KT_GEMV(2) KT_GEMV(4) KT_GEMV(8)
+        KT_GEMV(1, 8) KT_GEMV(2, 8) KT_GEMV(4, 4) KT_GEMV(8, 2)
 #undef KT_GEMV
     }
+    const bool small = kp <= 8192;
     if (M <= 64) {
-        dim3 grid((unsigned)(ceil_div(N, 64) * ceil_div(M, 64)));
-        w12_gemm_kernel<1, 1, 64, OUT><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+        dim3 grid((unsigned)(ceil_div(N, 128) * ceil_div(M, 32)));
+        if (small) w12_gemm_kernel<1, 1, 2, OUT, true><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+        else w12_gemm_kernel<1, 1, 2, OUT, false><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
         return hipGetLastError();
     }
-    dim3 grid((unsigned)(ceil_div(N, 128) * ceil_div(M, 128)));
-    w12_gemm_kernel<2, 2, 64, OUT><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+    constexpr int WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES;
+    dim3 grid((unsigned)(ceil_div(N, 128 * WTN) * ceil_div(M, 32 * WTM)));
+    if (small) w12_gemm_kernel<WTM, WTN, WV, OUT, true><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+    else w12_gemm_kernel<WTM, WTN, WV, OUT, false><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
     return hipGetLastError();
 }
 
