@@ -45,10 +45,12 @@ __device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
 }
 
 // LDS tiles are rows of BK bytes in 16-byte chunks; chunk c of row r sits at chunk position c ^ swz(r) so that the
-// MFMA operand reads (consecutive lanes = consecutive rows, same chunk) fall in distinct banks.
+// MFMA operand reads (consecutive lanes = consecutive rows, same chunk) fall in distinct banks. For 64-byte rows
+// swz = (r >> 2) & 3 measured conflict-free on gfx950 (about 195 B/clk per CU for ds_read_b128, against about
+// 120 for (r >> 1) & 3 and 62 without a swizzle).
 template <int CPR>
 __device__ __forceinline__ int swz(int r) {
-    if constexpr (CPR == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+    if constexpr (CPR == 4) return (r >> 2) & 3;
     else return (r ^ (r >> 3)) & 7;
 }
 
@@ -399,20 +401,38 @@ using slot_t = std::integral_constant<int, I>;
 #ifndef KT_W12_WAVES
 #define KT_W12_WAVES 2
 #endif
+#ifndef KT_W12_WM
+#define KT_W12_WM 1
+#endif
+#ifndef KT_W12_NSLOT
+#define KT_W12_NSLOT 4
+#endif
 
-template <int WTM, int WTN, int WAVES, int OUT, bool SMALL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
+// Compile-time loop: f(integral_constant<int, I>) for I = B..E-1.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+template <int WM, int WTM, int WTN, int WAVES, int NSLOT, int OUT, bool SMALL>
+__global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift) {
+    constexpr int NT = 256 * WM;  // WM waves along M x 4 waves along N
     constexpr int BK = 64, CPR = 4;
-    constexpr int BM = 32 * WTM, BN = 128 * WTN;
-    constexpr int AC = BM * CPR, AL = (AC + 255) / 256;  // 16-byte A chunks per tile / per thread
-    constexpr int SA = 3 * BM * BK, SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // A ring; the int8 output tile after it
-    __shared__ __attribute__((aligned(16))) int8_t smem[SA > SO ? SA : SO];
+    constexpr int BM = 32 * WTM * WM, BN = 128 * WTN;
+    constexpr int AC = BM * CPR, AL = (AC + NT - 1) / NT;  // 16-byte A chunks per tile / per thread
+    constexpr int SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // the int8 output tile reuses the A ring after the loop
+    __shared__ __attribute__((aligned(16))) int8_t smem[(NSLOT * BM * BK) > SO ? NSLOT * BM * BK : SO];
     int8_t(*sA)[BM * BK] = reinterpret_cast<int8_t(*)[BM * BK]>(smem);
     __shared__ int sRow[BM];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int wave = (tid >> 6) & 3, wr = (tid >> 6) >> 2 ;  // wave column (N) and wave row (M)
+    const int rw0 = wr * 32 * WTM;                           // the wave's first row in the tile
     int m0, n0;
     tile_coords(M, N, BM, BN, m0, n0);
     const int KB = kp / 32;
@@ -423,7 +443,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
     uint32_t oa[AL];
 #pragma unroll
     for (int i = 0; i < AL; i++) {
-        const int idx = tid + 256 * i;
+        const int idx = tid + NT * i;
         oa[i] = idx < AC ? (uint32_t)(idx >> 2) * (uint32_t)kp + 16 * (idx & 3) : 0xFFFFFFF0u;
     }
     // B: the CTA's column blocks (fragment-tiled); blocks past the matrix read as zero
@@ -446,14 +466,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
 #pragma unroll
     for (int i = 0; i < AL; i++) rsum[i] = 0;
 
-    v4i ra[3][AL];
-    v4i bl[3][WTN][2];
-    v2i bn[3][WTN][2];
+    v4i ra[NSLOT][AL];
+    v4i bl[NSLOT][WTN][2];
+    v2i bn[NSLOT][WTN][2];
 
     auto issue = [&](auto S, int kt) {  // global loads of tile kt into register slot S
         constexpr int sl = decltype(S)::value;
-#pragma unroll
-        for (int i = 0; i < AL; i++) ra[sl][i] = bload16(rA, oa[i], (uint32_t)(kt * BK));
 #pragma unroll
         for (int j = 0; j < WTN; j++)
 #pragma unroll
@@ -461,28 +479,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
                 bl[sl][j][ks] = bload16(rL, ob[j], (uint32_t)(2 * kt + ks) * 1024u);
                 bn[sl][j][ks] = bload8(rN, on[j], (uint32_t)(2 * kt + ks) * 512u);
             }
+#pragma unroll
+        for (int i = 0; i < AL; i++) ra[sl][i] = bload16(rA, oa[i], (uint32_t)(kt * BK));
+        // keep the loads at the head of the step: the scheduler would otherwise sink them behind the MFMAs and
+        // shorten the distance they have to land
+        __builtin_amdgcn_sched_barrier(0);
     };
-    // `mask` is -1, or 0 for a tile past the end in the last round: its A fragments and row sums are zeroed
-    // instead of branched around, so no MFMA sits under control flow (which would cost accumulator copies).
+    // `mask` is -1, or 0 for a tile past the end in the last round: such a tile is staged as zeros (and adds
+    // nothing to the row sums), so its MFMAs add zero instead of being branched around -- no MFMA sits under
+    // control flow, which would cost accumulator copies.
     auto stage = [&](auto S, int mask) {  // A of slot S into LDS buffer S
         constexpr int sl = decltype(S)::value;
 #pragma unroll
         for (int i = 0; i < AL; i++) {
-            const int idx = tid + 256 * i;
-            if (AC % 256 != 0 && idx >= AC) continue;
-            lds_write16(sA[sl], lds_off<CPR>(idx >> 2, idx & 3), ra[sl][i]);
-            rsum[i] += sum4(ra[sl][i]) & mask;
+            const int idx = tid + NT * i;
+            if (AC % NT != 0 && idx >= AC) continue;
+            const v4i v = ra[sl][i] & mask;
+            lds_write16(sA[sl], lds_off<CPR>(idx >> 2, idx & 3), v);
+            rsum[i] += sum4(v);
         }
     };
-    auto compute = [&](auto S, int mask) {
+    auto compute = [&](auto S) {
         constexpr int sl = decltype(S)::value;
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             v4i a[WTM];
 #pragma unroll
             for (int i = 0; i < WTM; i++) {
-                a[i] = lds_read16(sA[sl], lds_off<CPR>(i * 32 + (lane & 31), 2 * ks + half));
-                a[i] &= mask;
+                a[i] = lds_read16(sA[sl], lds_off<CPR>(rw0 + i * 32 + (lane & 31), 2 * ks + half));
             }
 #pragma unroll
             for (int j = 0; j < WTN; j++) {
@@ -496,36 +520,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
         }
     };
 
-    // Rounds of three tiles kt, kt+1, kt+2 (slots 0, 1, 2); before a round, tile kt is in LDS slot 0 and tile
-    // kt+1 in register slot 1, and the round stages tile kt+3. Tiles past the end (only in the last round) are
+    // Rounds of NSLOT tiles kt .. kt+NSLOT-1 in slots 0 .. NSLOT-1. Before a round, tile kt is in LDS slot 0 and
+    // tiles kt+1 .. kt+NSLOT-2 are in flight in register slots 1 .. NSLOT-2; step s issues tile kt+s+NSLOT-1 (NSLOT-1
+    // tiles ahead), multiplies tile kt+s and stages tile kt+s+1. Tiles past the end (only in the last round) are
     // masked to zero. A do-while: the accumulators have one path into the epilogue.
     const int nk = kp / BK;
-    issue(slot_t<0>{}, 0);
-    issue(slot_t<1>{}, 1);
+    static_for<0, NSLOT - 1>([&](auto S) { issue(S, decltype(S)::value); });
     stage(slot_t<0>{}, -1);
     __syncthreads();
     int kt = 0;
     do {
-        const int m1 = kt + 1 < nk ? -1 : 0, m2 = kt + 2 < nk ? -1 : 0, m3 = kt + 3 < nk ? -1 : 0;
-        issue(slot_t<2>{}, kt + 2);
-        compute(slot_t<0>{}, -1);
-        stage(slot_t<1>{}, m1);
-        __syncthreads();
-        issue(slot_t<0>{}, kt + 3);
-        compute(slot_t<1>{}, m1);
-        stage(slot_t<2>{}, m2);
-        __syncthreads();
-        issue(slot_t<1>{}, kt + 4);
-        compute(slot_t<2>{}, m2);
-        stage(slot_t<0>{}, m3);
-        __syncthreads();
-        kt += 3;
+        static_for<0, NSLOT>([&](auto S) {
+            constexpr int st = decltype(S)::value;
+            issue(slot_t<(st + NSLOT - 1) % NSLOT>{}, kt + st + NSLOT - 1);
+            compute(S);
+            stage(slot_t<(st + 1) % NSLOT>{}, kt + st + 1 < nk ? -1 : 0);
+            __syncthreads();
+        });
+        kt += NSLOT;
     } while (kt < nk);
 
     // row sums: the 4 threads of a row are consecutive lanes
 #pragma unroll
     for (int i = 0; i < AL; i++) {
-        const int idx = tid + 256 * i;
+        const int idx = tid + NT * i;
         int v = rsum[i];
         v += __shfl_xor(v, 1);
         v += __shfl_xor(v, 2);
@@ -544,7 +562,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
             for (int i = 0; i < WTM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int rt = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                     const int v = acc0[i][j][r] + (acc1[i][j][r] << 8) - 1920 * sRow[rt];
                     smem[rt * BN + c] = (int8_t)col_requant(v, q, 127);
                 }
@@ -552,9 +570,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
         __syncthreads();
         constexpr int CH = BM * BN / 16;  // 16-byte chunks of the tile
 #pragma unroll
-        for (int i = 0; i < (CH + 255) / 256; i++) {
-            const int idx = tid + 256 * i;
-            if (CH % 256 != 0 && idx >= CH) break;
+        for (int i = 0; i < (CH + NT - 1) / NT; i++) {
+            const int idx = tid + NT * i;
+            if (CH % NT != 0 && idx >= CH) break;
             const int rt = idx / (BN / 16), c = (idx % (BN / 16)) * 16, m = m0 + rt, n = n0 + c;
             const v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
             int8_t* dst = reinterpret_cast<int8_t*>(y) + (size_t)m * N + n;
@@ -574,7 +592,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
             for (int i = 0; i < WTM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int rt = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3), m = m0 + rt;
+                    const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3), m = m0 + rt;
                     const int v = acc0[i][j][r] + (acc1[i][j][r] << 8) - 1920 * sRow[rt];
                     // [-(2^31 - 1), 2^31 - 1]; -2^31 is unreachable: |v| < 2^31 except v = -2^31 with mt = 1
                     int32_t o = col_requant(v, q, 0x7FFFFFFF);
@@ -594,7 +612,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVE
         for (int i = 0; i < WTM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int rt = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);  // row within the CTA tile
+                const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);  // row within the CTA tile
                 const int corr = -1920 * sRow[rt];
                 const int m = m0 + rt;
 #pragma unroll
@@ -769,14 +787,14 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     const bool small = kp <= 8192;
     if (M <= 64) {
         dim3 grid((unsigned)(ceil_div(N, 128) * ceil_div(M, 32)));
-        if (small) w12_gemm_kernel<1, 1, 2, OUT, true><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
-        else w12_gemm_kernel<1, 1, 2, OUT, false><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+        if (small) w12_gemm_kernel<1, 1, 1, 2, 3, OUT, true><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+        else w12_gemm_kernel<1, 1, 1, 2, 3, OUT, false><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
         return hipGetLastError();
     }
-    constexpr int WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES;
-    dim3 grid((unsigned)(ceil_div(N, 128 * WTN) * ceil_div(M, 32 * WTM)));
-    if (small) w12_gemm_kernel<WTM, WTN, WV, OUT, true><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
-    else w12_gemm_kernel<WTM, WTN, WV, OUT, false><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+    constexpr int WM = KT_W12_WM, WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES, NS = KT_W12_NSLOT;
+    dim3 grid((unsigned)(ceil_div(N, 128 * WTN) * ceil_div(M, 32 * WTM * WM))), block(256 * WM);
+    if (small) w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+    else w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, false><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
     return hipGetLastError();
 }
 
