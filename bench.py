@@ -45,20 +45,21 @@ def sha(a: np.ndarray) -> str:
 
 
 def time_launches(torch, launch, n: int, warmup: int):
-    """Per-launch durations (ms) from HIP events on the launching stream, plus the wall time of the n launches."""
+    """Time n back-to-back launches between two HIP events recorded on the launching stream (the stream the kernel
+    runs on). Returns the mean launch duration (ms) and the host wall time of the n launches (s)."""
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(n):
-        ev[i][0].record(stream)
         launch(i)
-        ev[i][1].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return [s.elapsed_time(e) for s, e in ev], wall
+    return start.elapsed_time(end) / n, wall
 
 
 def cpu_baseline(x32: np.ndarray, w32: np.ndarray, m: int, n: int, k: int) -> dict:
@@ -94,6 +95,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--ms", type=str, default="", help="comma-separated subset of M to run (profiling runs)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the 12-bit GEMM on one MI355X); "
@@ -101,6 +104,15 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_calib:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": 256 << 20, "copies": 10}), flush=True)
+        return 0
 
     import tritify_amd as T
     from tritify_amd import workloads as W
@@ -153,31 +165,29 @@ def main() -> int:
         n_launch = args.steps if m == MH else max(args.steps, 200)
         warm = args.warmup if m == MH else max(args.warmup, 20)
         log(f"bench: M={m}: bit-exact vs the CPU fixture; timing {n_launch} launches")
-        durs, wall = time_launches(torch, launch, n_launch, warm)
-        us = float(np.mean(durs)) * 1e3
+        ms, wall = time_launches(torch, launch, n_launch, warm)
+        us = ms * 1e3
         ops = 2.0 * m * N * K
         bytes_alg = 1.5 * N * K + m * K + m * N * 1  # packed weights + int8 activations + int8 outputs
         tops = ops / (us * 1e-6) / 1e12
         gbs = bytes_alg / (us * 1e-6) / 1e9
         sweep[str(m)] = {
             "us_per_launch": round(us, 3),
-            "us_median": round(float(np.median(durs)) * 1e3, 3),
             "effective_tops": round(tops, 2),
             "executed_int8_tops": round(2 * tops, 2),
             "mfma_frac_logical": round(tops / INT8_PEAK_TOPS, 4),
             "alg_gbs": round(gbs, 1),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "bit_exact": True,
-            "kernel": "w12_gemv" if m <= 8 else "w12_gemm",
+            "kernel": "w12_skinny" if m <= 64 else "w12_gemm",
         }
         if m == MH:
-            headline = (durs, wall, n_launch, warm, us, tops)
+            headline = (ms, wall, n_launch, warm, us, tops)
 
     if headline is None:
         print(json.dumps({"sweep": sweep}), flush=True)
         return 0
-    durs, wall, n_launch, warm, us, tops = headline
-    ms_per_step = float(np.mean(durs))
+    ms_per_step, wall, n_launch, warm, us, tops = headline
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "w12_gemm_m2048_traffic.json")
     if os.path.exists(tpath):

@@ -775,13 +775,34 @@ void kt_w12_linear(const int32_t* x, const int8_t* lo, const uint8_t* nib, size_
     }
 }
 
+/* requant's value without the wrap: round(accum * mant / 2^shift) half away from zero, saturated to i64, for any
+ * int32 shift. Equals kt_requant (lib.rs:78-86) wherever that value fits i64; kt_requant casts a larger one to i64
+ * with wrap-around (and shifts of 128 or more are outside its i128 arithmetic). */
+int64_t kt_requant_sat(int64_t accum, int64_t mant, int32_t shift) {
+    i128 prod = (i128)accum * (i128)mant; /* |prod| <= 2^126 */
+    if (prod == 0) return 0;
+    int neg = prod < 0;
+    u128 mag = neg ? (u128)(-prod) : (u128)prod, limit = (u128)1 << 63, q;
+    if (shift <= 0) {
+        int64_t up = -(int64_t)shift;
+        if (up >= 64) q = limit;
+        else q = (mag >= ((u128)1 << (63 - up))) ? limit : mag << up;
+    } else if (shift >= 127) {
+        q = 0;
+    } else {
+        q = (mag + ((u128)1 << (shift - 1))) >> shift;
+    }
+    if (q >= limit) return neg ? INT64_MIN : INT64_MAX;
+    return neg ? -(int64_t)q : (int64_t)q;
+}
+
 /* The per-channel epilogue: out = clamp(requant(acc, mant[n], shift[n]), lo, hi) (kt-int/src/lib.rs:78-86 per
- * output channel; the clamp is this build's int8 output). */
+ * output channel, without the i64 wrap; the clamp is this build's int8 / int32 output). */
 void kt_requant_channels(const int64_t* acc, size_t m, size_t n, const int32_t* mant, const int32_t* shift,
                          int64_t lo, int64_t hi, int32_t* out) {
     for (size_t r = 0; r < m; r++)
         for (size_t o = 0; o < n; o++) {
-            int64_t v = kt_requant(acc[r * n + o], mant[o], shift[o]);
+            int64_t v = kt_requant_sat(acc[r * n + o], mant[o], shift[o]);
             if (v < lo) v = lo;
             if (v > hi) v = hi;
             out[r * n + o] = (int32_t)v;

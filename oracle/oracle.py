@@ -88,6 +88,7 @@ def _declare(L: C.CDLL) -> None:
         "kt_frexp": (C.c_double, [C.c_double, C.POINTER(C.c_int32)]),
         "kt_frexp_scale": (None, [C.c_double, C.c_uint32, C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
         "kt_requant": (C.c_int64, [C.c_int64, C.c_int64, C.c_int32]),
+        "kt_requant_sat": (C.c_int64, [C.c_int64, C.c_int64, C.c_int32]),
         "kt_scale_from_ratio": (Scale, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64]),
         "kt_scale_from_f64": (Scale, [C.c_double]),
         "kt_scale_ge": (C.c_int, [Scale, Scale]),
@@ -333,6 +334,10 @@ def emu_linear(x, w, rows, out, k, px=None, pw=None, flush=None, drop_top=False,
 
 def requant(accum: int, mant: int, shift: int) -> int:
     return lib().kt_requant(accum, mant, shift)
+
+
+def requant_sat(accum: int, mant: int, shift: int) -> int:
+    return lib().kt_requant_sat(accum, mant, shift)
 
 
 def frexp(x: float):

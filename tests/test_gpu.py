@@ -286,11 +286,12 @@ def test_w12_linear_against_the_oracle(torch_dev, out_kind):
 
 
 def test_w12_extremes(torch_dev):
-    """Every product at its largest magnitude, k = 4096, on the GEMV and on the GEMM."""
+    """Every product at its largest magnitude on the skinny kernel and on the GEMM, at k = 4096 and at k = 20000
+    (where the row-sum term -1920 * sum(x) no longer fits int32)."""
     torch = torch_dev
     T = tb()
-    k, n = 4096, 64
-    for m in (1, 64):
+    n = 64
+    for m, k in [(1, 4096), (64, 4096), (65, 4096), (3, 20000), (65, 20000)]:
         for xv, wv in [(-128, -2048), (127, 2047), (-128, 2047), (127, -2048)]:
             x = np.full(m * k, xv, np.int32)
             w = np.full(n * k, wv, np.int32)
@@ -300,6 +301,116 @@ def test_w12_extremes(torch_dev):
             T.w12_linear(_x_device(torch, x, m, k), lo, nib, m, n, k, y)
             torch.cuda.synchronize()
             assert (y.cpu().numpy() == k * xv * wv).all()
+
+
+def test_w12_int32_bound_at_k_8192(torch_dev):
+    """x = -128 against w = -2048 over k = 8192 sums to exactly 2^31, one past int32: the skinny kernel (m <= 64) and
+    the GEMM (m > 64) must both carry it into i64 and requantize it exactly."""
+    torch = torch_dev
+    T = tb()
+    k, n = 8192, 40
+    w = np.full(n * k, -2048, np.int32)
+    lo, nib = _w12_device(torch, w, n, k)
+    mant = np.full(n, 1, np.int32)
+    shift = np.full(n, 24, np.int32)  # 2^31 / 2^24 = 128 -> clamps to 127 for int8, 128 for int32
+    md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
+    for m in (1, 33, 65, 130):
+        x = np.full(m * k, -128, np.int32)
+        xd = _x_device(torch, x, m, k)
+        say(f"case: w12 2^31 bound m={m}")
+        y = torch.empty(m * n, dtype=torch.int64, device="cuda")
+        q32 = torch.empty(m * n, dtype=torch.int32, device="cuda")
+        T.w12_linear(xd, lo, nib, m, n, k, y)
+        T.w12_linear(xd, lo, nib, m, n, k, q32, T.OUT_I32, md, sd)
+        torch.cuda.synchronize()
+        assert (y.cpu().numpy() == 2**31).all() and (q32.cpu().numpy() == 128).all(), m
+
+
+def test_w12_few_columns_and_long_k(torch_dev):
+    """Few 16-column blocks against long k (past the int32 range of one dot, up to 70000) on the skinny kernel,
+    every output kind, against the oracle; every launch twice, so nothing depends on state a launch leaves."""
+    torch = torch_dev
+    T = tb()
+    rng = np.random.default_rng(21)
+    cases = [(1, 32, 8192), (2, 64, 20000), (8, 40, 12345), (32, 100, 9000), (33, 96, 16384), (64, 33, 70000),
+             (17, 1000, 4096), (5, 4096, 896)]
+    data = []
+    for m, n, k in cases:
+        x = rng.integers(-128, 128, size=m * k).astype(np.int32)
+        w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
+        mant, shift = O.channel_scales(w, n, k, 40)
+        acc = O.portable(x, w, m, n, k)
+        data.append((m, n, k, x, w, mant, shift, acc))
+    for rep in range(2):
+        for m, n, k, x, w, mant, shift, acc in data:
+            lo, nib = _w12_device(torch, w, n, k)
+            xd = _x_device(torch, x, m, k)
+            md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
+            say(f"case: w12 long k {m}x{n}x{k} rep {rep}")
+            y = torch.empty(m * n, dtype=torch.int64, device="cuda")
+            q32 = torch.empty(m * n, dtype=torch.int32, device="cuda")
+            q8 = torch.empty(m * n, dtype=torch.int8, device="cuda")
+            T.w12_linear(xd, lo, nib, m, n, k, y)
+            T.w12_linear(xd, lo, nib, m, n, k, q32, T.OUT_I32, md, sd)
+            T.w12_linear(xd, lo, nib, m, n, k, q8, T.OUT_I8, md, sd)
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), acc), (m, n, k)
+            assert np.array_equal(q32.cpu().numpy(), O.requant_channels(acc, m, n, mant, shift, -(2**31),
+                                                                         2**31 - 1)), (m, n, k)
+            assert np.array_equal(q8.cpu().numpy(), O.requant_channels(acc, m, n, mant, shift, -127, 127)), (m, n, k)
+
+
+def test_w12_requant_edges(torch_dev):
+    """Every pairing of edge multipliers and shifts (one output channel each; shifts from -2^31 to 2^31 - 1) on the
+    skinny kernel, the int32-fast GEMM (k <= 8128) and the i64 GEMM (longer k), against the oracle's exact clamp."""
+    from test_oracle import EDGE_MANT, EDGE_SHIFT
+
+    torch = torch_dev
+    T = tb()
+    pairs = [(mm, ss) for mm in EDGE_MANT for ss in EDGE_SHIFT]
+    n = len(pairs)
+    mant = np.array([p[0] for p in pairs], np.int32)
+    shift = np.array([p[1] for p in pairs], np.int32)
+    md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
+    rng = np.random.default_rng(22)
+    for m, k in [(3, 4096), (65, 4096), (70, 9000)]:
+        x = rng.integers(-128, 128, size=m * k).astype(np.int32)
+        w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
+        w[: 2 * k] = -2048  # two channels at the largest magnitude
+        x[:k] = -128
+        lo, nib = _w12_device(torch, w, n, k)
+        xd = _x_device(torch, x, m, k)
+        acc = O.portable(x, w, m, n, k)
+        say(f"case: w12 requant edges {m}x{n}x{k}")
+        q32 = torch.empty(m * n, dtype=torch.int32, device="cuda")
+        q8 = torch.empty(m * n, dtype=torch.int8, device="cuda")
+        T.w12_linear(xd, lo, nib, m, n, k, q32, T.OUT_I32, md, sd)
+        T.w12_linear(xd, lo, nib, m, n, k, q8, T.OUT_I8, md, sd)
+        torch.cuda.synchronize()
+        assert np.array_equal(q32.cpu().numpy(), O.requant_channels(acc, m, n, mant, shift, -(2**31), 2**31 - 1))
+        assert np.array_equal(q8.cpu().numpy(), O.requant_channels(acc, m, n, mant, shift, -127, 127))
+
+
+def test_w12_two_streams(torch_dev):
+    """Launches interleaved on two streams give the oracle's result on each."""
+    torch = torch_dev
+    T = tb()
+    rng = np.random.default_rng(23)
+    m, n, k = 4, 256, 8192
+    ws = [rng.integers(-2048, 2048, size=n * k).astype(np.int32) for _ in range(2)]
+    x = rng.integers(-128, 128, size=m * k).astype(np.int32)
+    xd = _x_device(torch, x, m, k)
+    devs = [_w12_device(torch, w, n, k) for w in ws]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ys = [torch.empty(m * n, dtype=torch.int64, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+    say("case: w12 two streams")
+    for rep in range(4):
+        for i in range(2):
+            T.w12_linear(xd, devs[i][0], devs[i][1], m, n, k, ys[i], stream=streams[i])
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert np.array_equal(ys[i].cpu().numpy(), O.portable(x, ws[i], m, n, k)), i
 
 
 def test_config2_full_size_against_fixtures(torch_dev):

@@ -283,6 +283,49 @@ def test_requant_against_exact_rationals():
         assert O.requant(a, m, s) == want
 
 
+EDGE_ACC = [0, 1, -1, 2**31 - 1, -(2**31), 2**31, 12345, -98765, 2**40 + 3, 2**62, -(2**63), 2**63 - 1]
+EDGE_MANT = [0, 1, -1, 3, 2**31 - 1, -(2**31), 1 << 30, -12345]
+EDGE_SHIFT = [-(2**31), -200, -128, -64, -63, -62, -40, -33, -1, 0, 1, 2, 30, 31, 32, 33, 62, 63, 64, 65, 94, 95,
+              96, 126, 127, 128, 200, 2**31 - 1]
+
+
+def _exact_requant(a: int, m: int, s: int) -> int:
+    """round(a * m / 2^s) half away from zero, saturated to i64, with exact rationals. |a * m| <= 2^126, so for
+    s > 300 the value is below 2^-174 and rounds to 0; for s < -300 any nonzero product saturates."""
+    p = a * m
+    if p == 0:
+        return 0
+    if s > 300:
+        return 0
+    if s < -300:
+        return 2**63 - 1 if p > 0 else -(2**63)
+    q = Fraction(p) / Fraction(2) ** s
+    r = (abs(q.numerator) * 2 + q.denominator) // (2 * q.denominator)  # floor(|q| + 1/2)
+    r = r if q > 0 else -r
+    return max(-(2**63), min(2**63 - 1, r))
+
+
+def test_requant_sat_against_exact_rationals_on_every_edge():
+    """The per-channel epilogue's requant (no i64 wrap) over the edges of i64 accumulators, int32 multipliers and
+    every class of int32 shift, including shifts outside the 128-bit product's range."""
+    for a in EDGE_ACC:
+        for m in EDGE_MANT:
+            for s in EDGE_SHIFT:
+                assert O.requant_sat(a, m, s) == _exact_requant(a, m, s), (a, m, s)
+
+
+def test_requant_sat_equals_requant_where_the_value_fits():
+    """Where round(a * m / 2^s) fits i64, the saturating form and the reference's wrapping form agree."""
+    rng = np.random.default_rng(12)
+    for _ in range(4000):
+        a = int(rng.integers(-(2**62), 2**62)) >> int(rng.integers(0, 62))
+        m = int(rng.integers(-(2**31), 2**31))
+        s = int(rng.integers(-40, 127))
+        want = _exact_requant(a, m, s)
+        if -(2**63) < want < 2**63 - 1:
+            assert O.requant(a, m, s) == want == O.requant_sat(a, m, s), (a, m, s)
+
+
 def _lcg(s):
     s = (s * 6364136223846793005 + 1442695040888963407) % 2**64
     return s

@@ -93,13 +93,26 @@ __device__ __forceinline__ int sum4(v4i v) {
     return __builtin_amdgcn_sdot4(v.w, ones, s, false);
 }
 
-// round(acc * mant / 2^shift), half away from zero, widening product (crates/00-kernels/kt-int/src/lib.rs:78-86).
+// round(acc * mant / 2^shift), half away from zero, from the exact 128-bit product, saturated to i64 -- for every
+// int32 shift. kt-int's requant (crates/00-kernels/kt-int/src/lib.rs:78-86) computes the same value and casts it to
+// i64 with wrap-around; the two agree wherever the value fits i64 (always for shift > 0 and |acc| < 2^32).
 __device__ __forceinline__ int64_t requant_dev(int64_t acc, int64_t mant, int shift) {
-    __int128 prod = (__int128)acc * (__int128)mant;
-    if (shift <= 0) return (int64_t)(prod << (-shift));
-    __int128 half = (__int128)1 << (shift - 1);
-    __int128 r = prod >= 0 ? (prod + half) >> shift : -(((-prod) + half) >> shift);
-    return (int64_t)r;
+    typedef unsigned __int128 u128;
+    const __int128 prod = (__int128)acc * (__int128)mant;  // |prod| <= 2^126
+    if (prod == 0) return 0;
+    const bool neg = prod < 0;
+    const u128 a = neg ? (u128)(-prod) : (u128)prod, top = (u128)1 << 63;
+    u128 q;
+    if (shift <= 0) {
+        const int s = shift < -64 ? 64 : -shift;
+        q = (s >= 64 || (a >> (63 - s)) != 0) ? top : a << s;
+    } else if (shift >= 127) {
+        q = 0;  // |prod| < 2^126 <= 2^(shift - 1)
+    } else {
+        q = (a + ((u128)1 << (shift - 1))) >> shift;
+    }
+    if (q >= top) return neg ? INT64_MIN : INT64_MAX;
+    return neg ? -(int64_t)q : (int64_t)q;
 }
 
 template <int OUT>
@@ -302,13 +315,19 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
 // of GM tile-rows, sharing A rows and B columns in that XCD's L2.
 // ------------------------------------------------------------------------------------------------------------------
 
+// s_lo + 256 s_hi + corr for a dot known to fit int32: formed modulo 2^32 (256 s_hi alone may not fit).
+__device__ __forceinline__ int w12_value(int s_lo, int s_hi, int corr) {
+    return (int)((uint32_t)s_lo + ((uint32_t)s_hi << 8) + (uint32_t)corr);
+}
+
 // One W12 output from its two plane sums and the row-sum term: v = s_lo + 256 s_hi + corr (corr = -1920 sum x).
-// SMALL: every partial sum and v fit int32 (kp <= 8192: |v| <= 8192 * 2048 * 128 = 2^31), so v is formed in 32 bits
+// SMALL: every partial sum and v fit int32 (kp <= 8128: |v| <= 8128 * 2048 * 128 < 2^31), so v is formed in 32 bits
 // and the requant product |v| * mant (< 2^62) in 64 -- a handful of instructions per output.
 template <int OUT, bool SMALL>
-__device__ __forceinline__ void store_w12(void* y, size_t idx, int s_lo, int s_hi, int corr, int32_t mant, int32_t sh) {
+__device__ __forceinline__ void store_w12(void* y, size_t idx, int s_lo, int s_hi, int64_t corr, int32_t mant,
+                                          int32_t sh) {
     if constexpr (SMALL) {
-        const int v = s_lo + (s_hi << 8) + corr;
+        const int v = w12_value(s_lo, s_hi, (int)corr);
         if constexpr (OUT == KT_OUT_I64) {
             reinterpret_cast<int64_t*>(y)[idx] = (int64_t)v;
         } else {
@@ -327,7 +346,7 @@ __device__ __forceinline__ void store_w12(void* y, size_t idx, int s_lo, int s_h
             }
         }
     } else {
-        const int64_t v = (int64_t)s_lo + 256 * (int64_t)s_hi + (int64_t)corr;
+        const int64_t v = (int64_t)s_lo + 256 * (int64_t)s_hi + corr;
         store_out<OUT>(y, idx, v, &mant, &sh, 0);
     }
 }
@@ -359,12 +378,15 @@ __device__ __forceinline__ ColQ col_q(int32_t mant, int32_t sh) {
     return q;
 }
 
-// requant(v) clamped to [-lim, lim] for the int8 / int32 outputs.
-__device__ __forceinline__ int32_t col_requant(int v, const ColQ& q, uint32_t lim) {
+// requant(v) clamped to the output: [-127, 127] for int8, [-2^31, 2^31 - 1] for int32.
+template <bool I32>
+__device__ __forceinline__ int32_t col_requant(int v, const ColQ& q) {
     const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
     uint64_t m = ((uint64_t)a * q.mt + q.bias) >> q.shr;
+    const bool neg = (v < 0) != q.neg;
+    const uint64_t lim = I32 ? (neg ? 0x80000000ull : 0x7FFFFFFFull) : 127;
     m = m > lim ? lim : m;
-    return ((v < 0) != q.neg) ? -(int32_t)m : (int32_t)m;
+    return neg ? (int32_t)(0u - (uint32_t)m) : (int32_t)m;
 }
 
 __device__ __forceinline__ void tile_coords(int M, int N, int BM, int BN, int& m0, int& n0) {
@@ -387,6 +409,9 @@ __device__ __forceinline__ v4i unpack_hi(v2i d) {
     const int m4 = 0x0F0F0F0F;
     return v4i{d.x & m4, (d.x >> 4) & m4, d.y & m4, (d.y >> 4) & m4};
 }
+
+// The longest k for which every W12 dot fits int32: 8128 * 128 * 2048 < 2^31 <= 8192 * 128 * 2048.
+#define KT_SMALL_KP 8128
 
 template <int I>
 using slot_t = std::integral_constant<int, I>;
@@ -563,8 +588,8 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    const int v = acc0[i][j][r] + (acc1[i][j][r] << 8) - 1920 * sRow[rt];
-                    smem[rt * BN + c] = (int8_t)col_requant(v, q, 127);
+                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
+                    smem[rt * BN + c] = (int8_t)col_requant<false>(v, q);
                 }
         }
         __syncthreads();
@@ -593,10 +618,8 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3), m = m0 + rt;
-                    const int v = acc0[i][j][r] + (acc1[i][j][r] << 8) - 1920 * sRow[rt];
-                    // [-(2^31 - 1), 2^31 - 1]; -2^31 is unreachable: |v| < 2^31 except v = -2^31 with mt = 1
-                    int32_t o = col_requant(v, q, 0x7FFFFFFF);
-                    if (v == INT32_MIN && q.mt == 1 && q.shr == 0 && !q.neg) o = INT32_MIN;
+                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
+                    const int32_t o = col_requant<true>(v, q);
                     if (full || (m < M && n < N)) reinterpret_cast<int32_t*>(y)[(size_t)m * N + n] = o;
                 }
         }
@@ -613,7 +636,7 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);  // row within the CTA tile
-                const int corr = -1920 * sRow[rt];
+                const int64_t corr = -1920 * (int64_t)sRow[rt];  // past int32 for k > 8738
                 const int m = m0 + rt;
 #pragma unroll
                 for (int j = 0; j < WTN; j++) {
@@ -626,85 +649,117 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// W12 GEMV (batch decode, M <= 8). Bandwidth-bound: one CTA per 32-column block; its WPB waves take the block's
-// k32 fragments round-robin, so together they sweep the block's contiguous bytes with coalesced 1 KB (lo) and
-// 512-byte (nib) loads, U fragments in flight per wave. Each lane dots its 16 k of one column against x with
-// v_dot4_i32_i8; lanes l and l^32 hold the two k-halves, waves are summed through LDS.
+// W12 skinny GEMM (M <= 16 * MT, batch decode and short prefill chunks). Bandwidth-bound: the weights are read once,
+// so the grid must reach every CU with enough loads in flight and end without a cross-CTA reduction. A CTA owns half
+// a column block (16 columns: fragment lanes 16 hb + c + 32 h, i.e. two 256-byte runs of each 1 KB lo fragment and
+// two 128-byte runs of each 512-byte nib fragment; the two halves of a block read disjoint bytes) over all of k, so
+// N = 4096 gives 256 CTAs. Its NW waves take pairs of k32 blocks round-robin, U pairs in flight per wave. On the
+// 16x16x64 MFMA, lane l = c + 16 g supplies column c (B) / row c (A) for k-group g = (k32 block 2p + g / 2,
+// k-half g % 2): exactly the lanes the half block's bytes arrive in, so no operand moves between lanes. Rows past
+// M read as zero through the x buffer descriptor. The waves meet in LDS in i64; the per-channel scales are fetched
+// at the start, so the epilogue waits on no memory.
 // ------------------------------------------------------------------------------------------------------------------
-template <int MR, int WPB, int U, int OUT>
-__global__ __launch_bounds__(64 * WPB) void w12_gemv_kernel(const int8_t* __restrict__ x,
-                                                            const int8_t* __restrict__ wlo,
-                                                            const uint8_t* __restrict__ wnib, void* __restrict__ y,
-                                                            int M, int N, int kp, const int32_t* __restrict__ mant,
-                                                            const int32_t* __restrict__ shift) {
-    __shared__ int64_t sPart[WPB][MR][32];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
-    const int cb = blockIdx.x, KB = kp / 32;
+template <int MT, int NW, int U, int OUT, bool SMALL>
+__global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __restrict__ x,
+                                                             const int8_t* __restrict__ wlo,
+                                                             const uint8_t* __restrict__ wnib, void* __restrict__ y,
+                                                             int M, int N, int kp, const int32_t* __restrict__ mant,
+                                                             const int32_t* __restrict__ shift) {
+    constexpr int NT = 64 * NW, OUTS = MT * 256;  // threads; outputs of the CTA (MT row tiles x 16 columns)
+    static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
+    typedef typename std::conditional<SMALL, int32_t, int64_t>::type part_t;  // SMALL: every dot fits int32
+    __shared__ part_t sP[NW][OUTS];
+    __shared__ int32_t sX[NW][MT * 16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar load offsets
+    const int cb = blockIdx.x >> 1, hb = blockIdx.x & 1, n0 = cb * 32 + 16 * hb;
+    const int KB = kp / 32;
+
+    // the epilogue's channel scales, fetched now
+    const int oc = tid & 15, on = n0 + oc;  // every output of this thread is in column on (NT is a multiple of 16)
+    const int32_t om = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? mant[on] : 0;
+    const int32_t os = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? shift[on] : 0;
+
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
     const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb * KB * 512, (uint32_t)KB * 512);
-    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)(M * kp));
-    const int ones = 0x01010101;
-
-    int slo[MR], shi[MR], sx[MR];
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)M * (uint32_t)kp);
+    const int c = lane & 15, g = lane >> 4, kbq = g >> 1, h = g & 1;
+    const int slot = 16 * hb + c + 32 * h;
+    const uint32_t oL = 16 * slot + 1024 * kbq, oN = 8 * slot + 512 * kbq;
+    uint32_t oX[MT];
 #pragma unroll
-    for (int m = 0; m < MR; m++) slo[m] = shi[m] = sx[m] = 0;
+    for (int t = 0; t < MT; t++) oX[t] = (uint32_t)(c + 16 * t) * (uint32_t)kp + 32 * kbq + 16 * h;
 
-    for (int base = wave; base < KB; base += WPB * U) {
-        v4i L[U], X[U][MR];
-        v2i D[U];
+    v4i acc0[MT], acc1[MT];
+    int sx[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc0[t] = acc1[t] = v4i{}, sx[t] = 0;
+
+    v4i L[U], X[U][MT];
+    v2i D[U];
+    const int np = (KB + 1) / 2, nb = (np + NW * U - 1) / (NW * U);
+    int b = 0;
+    do {  // batch b: U pairs of k32 blocks per wave, all loads in flight before the first MFMA
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int kb = base + u * WPB;  // past the block: zeros from the weight buffers
-            L[u] = bload16(rL, 16 * lane, (uint32_t)kb * 1024u);
-            D[u] = bload8(rN, 8 * lane, (uint32_t)kb * 512u);
+            const uint32_t p = (uint32_t)(w + NW * (U * b + u));  // past the end: zeros from the weight buffers
+            L[u] = bload16(rL, oL, p * 2048u);
+            D[u] = bload8(rN, oN, p * 1024u);
 #pragma unroll
-            for (int m = 0; m < MR; m++)
-                X[u][m] = m < M ? bload16(rX, (uint32_t)(m * kp + 16 * half), (uint32_t)kb * 32u) : v4i{};
+            for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], p * 64u);
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (base + u * WPB >= KB) break;  // uniform: x past kp would be the next row
-            const v4i H = unpack_hi(D[u]);
+            const int mask = 2 * (w + NW * (U * b + u)) + kbq < KB ? -1 : 0;  // x past k is not in the row sums
+            const v4i hi = unpack_hi(D[u]);
 #pragma unroll
-            for (int m = 0; m < MR; m++) {
-                const v4i xv = X[u][m];
-                int s = slo[m], t = shi[m], q = sx[m];
-                s = __builtin_amdgcn_sdot4(xv.x, L[u].x, s, false);
-                s = __builtin_amdgcn_sdot4(xv.y, L[u].y, s, false);
-                s = __builtin_amdgcn_sdot4(xv.z, L[u].z, s, false);
-                s = __builtin_amdgcn_sdot4(xv.w, L[u].w, s, false);
-                t = __builtin_amdgcn_sdot4(xv.x, H.x, t, false);
-                t = __builtin_amdgcn_sdot4(xv.y, H.y, t, false);
-                t = __builtin_amdgcn_sdot4(xv.z, H.z, t, false);
-                t = __builtin_amdgcn_sdot4(xv.w, H.w, t, false);
-                q = __builtin_amdgcn_sdot4(xv.x, ones, q, false);
-                q = __builtin_amdgcn_sdot4(xv.y, ones, q, false);
-                q = __builtin_amdgcn_sdot4(xv.z, ones, q, false);
-                q = __builtin_amdgcn_sdot4(xv.w, ones, q, false);
-                slo[m] = s;
-                shi[m] = t;
-                sx[m] = q;
+            for (int t = 0; t < MT; t++) {
+                const v4i a = X[u][t] & mask;
+                sx[t] += sum4(a);
+                acc0[t] = mfma16(a, L[u], acc0[t]);
+                acc1[t] = mfma16(a, hi, acc1[t]);
             }
         }
-    }
+    } while (++b < nb);
 
-    // lane l and l^32 hold the two k-halves of column l%32 (DPP row broadcasts cannot cross the 32-lane halves,
-    // so this one exchange goes through ds_swizzle-free bpermute), then the waves meet in LDS
+    // the wave's partials (lane l, register r: row 4 g + r of the tile, column c) and row sums into LDS
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-        int64_t v = (int64_t)slo[m] + 256 * (int64_t)shi[m] - 1920 * (int64_t)sx[m];
-        v += __shfl_xor(v, 32);
-        if (half == 0) sPart[wave][m][lane] = v;
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            if constexpr (SMALL)  // modulo 2^32: the CTA's total is exact
+                sP[w][(t * 16 + 4 * g + r) * 16 + c] = (int32_t)((uint32_t)acc0[t][r] + ((uint32_t)acc1[t][r] << 8));
+            else
+                sP[w][(t * 16 + 4 * g + r) * 16 + c] = (int64_t)acc0[t][r] + 256 * (int64_t)acc1[t][r];
+        }
+        int s = sx[t];
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        if (lane < 16) sX[w][t * 16 + lane] = s;
     }
     __syncthreads();
-    if (wave == 0 && half == 0) {
-        const int n = cb * 32 + lane;
+    const ColQ cq = col_q(om, os);
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            int64_t v = 0;
+    for (int o = tid; o < OUTS; o += NT) {
+        const int m = o >> 4;  // output (m, oc)
+        if constexpr (SMALL) {
+            uint32_t v = 0, rs = 0;
 #pragma unroll
-            for (int w = 0; w < WPB; w++) v += sPart[w][m][lane];
-            if (m < M && n < N) store_out<OUT>(y, (size_t)m * N + n, v, mant, shift, n);
+            for (int q = 0; q < NW; q++) v += (uint32_t)sP[q][o], rs += (uint32_t)sX[q][m];
+            const int vi = (int)(v - 1920u * rs);
+            if (m < M && on < N) {
+                const size_t idx = (size_t)m * N + on;
+                if constexpr (OUT == KT_OUT_I64) reinterpret_cast<int64_t*>(y)[idx] = vi;
+                else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
+                else reinterpret_cast<int8_t*>(y)[idx] = (int8_t)col_requant<false>(vi, cq);
+            }
+        } else {
+            int64_t v = 0, rs = 0;
+#pragma unroll
+            for (int q = 0; q < NW; q++) v += sP[q][o], rs += sX[q][m];
+            v -= 1920 * rs;
+            if (m < M && on < N) store_out<OUT>(y, (size_t)m * N + on, v, &om, &os, 0);
         }
     }
 }
@@ -774,23 +829,25 @@ hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb,
 template <int OUT>
 static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
                                  const int32_t* mant, const int32_t* shift, void* y, hipStream_t s) {
-    if (M <= 8) {
-        dim3 grid((unsigned)ceil_div(N, 32));
-#define KT_GEMV(mr, u)                                                                                      \
-    if (M <= mr) {                                                                                          \
-        w12_gemv_kernel<mr, 8, u, OUT><<<grid, dim3(512), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift); \
-        return hipGetLastError();                                                                           \
-    }
-        KT_GEMV(1, 8) KT_GEMV(2, 8) KT_GEMV(4, 4) KT_GEMV(8, 2)
-#undef KT_GEMV
-    }
-    const bool small = kp <= 8192;
     if (M <= 64) {
-        dim3 grid((unsigned)(ceil_div(N, 128) * ceil_div(M, 32)));
-        if (small) w12_gemm_kernel<1, 1, 1, 2, 3, OUT, true><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
-        else w12_gemm_kernel<1, 1, 1, 2, 3, OUT, false><<<grid, dim3(256), 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
-        return hipGetLastError();
+        const int64_t ctas = 2 * ceil_div(N, 32);
+        if (ctas > INT32_MAX || (int64_t)M * kp > (int64_t)UINT32_MAX || kp > KT_W12_SKINNY_MAX_K)
+            return hipErrorInvalidValue;
+        dim3 grid((unsigned)ctas);
+#define KT_SKINNY(mt, nw, u)                                                                                        \
+    if (M <= 16 * mt) {                                                                                             \
+        if (kp <= KT_SMALL_KP)                                                                                      \
+            w12_skinny_kernel<mt, nw, u, OUT, true><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, M, N, kp, mant,   \
+                                                                                   shift);                          \
+        else                                                                                                        \
+            w12_skinny_kernel<mt, nw, u, OUT, false><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, M, N, kp, mant,  \
+                                                                                    shift);                         \
+        return hipGetLastError();                                                                                   \
     }
+        KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2)
+#undef KT_SKINNY
+    }
+    const bool small = kp <= KT_SMALL_KP;
     constexpr int WM = KT_W12_WM, WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES, NS = KT_W12_NSLOT;
     dim3 grid((unsigned)(ceil_div(N, 128 * WTN) * ceil_div(M, 32 * WTM * WM))), block(256 * WM);
     if (small) w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
