@@ -179,7 +179,7 @@ def main() -> int:
             "alg_gbs": round(gbs, 1),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "bit_exact": True,
-            "kernel": "w12_skinny" if m <= 64 else "w12_gemm",
+            "kernel": "w12_skinny" if m <= 128 else "w12_gemm",
         }
         if m == MH:
             headline = (ms, wall, n_launch, warm, us, tops)

@@ -122,11 +122,12 @@ int kt_hip_w12_upload(int dev, const int32_t* codes, int64_t n, int64_t k, int8_
  * requant of crates/00-kernels/kt-int/src/lib.rs:78-86, round(acc * mant[o] / 2^shift[o]) half away from zero,
  * clamped to [-2^31, 2^31 - 1] / [-127, 127]. That value is exact for every int32 mant and shift (kt-int
  * wraps a product beyond i64 where this clamps; they agree wherever the value fits i64). mant_dev and shift_dev
- * (n x i32, device) may be NULL for KT_OUT_I64. m <= 64 runs the skinny kernel (one CTA per 16 output columns,
- * k <= KT_W12_SKINNY_MAX_K), larger m the MFMA GEMM (k <= KT_W12_GEMM_MAX_K); longer k is hipErrorInvalidValue.
- * Asynchronous on `stream`. */
+ * (n x i32, device) may be NULL for KT_OUT_I64. m <= KT_W12_SKINNY_MAX_M runs the skinny kernel (one CTA per 16
+ * output columns, k <= KT_W12_SKINNY_MAX_K), larger m the MFMA GEMM (k <= KT_W12_GEMM_MAX_K); longer k is
+ * hipErrorInvalidValue. Asynchronous on `stream`. */
+#define KT_W12_SKINNY_MAX_M 128
 #define KT_W12_GEMM_MAX_K 131008 /* 131008 * 128 * 128 < 2^31: the GEMM's int32 plane accumulators cannot wrap */
-#define KT_W12_SKINNY_MAX_K 1048576 /* each of the skinny kernel's waves sums at most k / 16 per accumulator */
+#define KT_W12_SKINNY_MAX_K 262144 /* >= 4 waves each sum <= k / 4 per int32 accumulator: 65536 * 128 * 128 = 2^30 */
 int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                       int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
                       void* y_dev, void* stream);

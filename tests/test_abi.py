@@ -70,13 +70,13 @@ def test_the_product_never_imports_the_oracle():
 
 def test_w12_linear_rejects_bad_arguments_before_any_device_call():
     """Argument checks of kt_hip_w12_linear that need no GPU: an unknown output kind, a requant output without its
-    scales, and k past the limit of the GEMM's (m > 64) or the skinny kernel's int32 accumulators."""
+    scales, and k past the limit of the GEMM's (m > 128) or the skinny kernel's int32 accumulators."""
     from tritify_amd import backend as B
 
     L = B.lib()
     inval = 1  # hipErrorInvalidValue
     assert L.kt_hip_w12_linear(0, None, None, None, 4, 32, 64, None, None, 7, None, None) == inval
     assert L.kt_hip_w12_linear(0, None, None, None, 4, 32, 64, None, None, B.OUT_I8, None, None) == inval
-    assert L.kt_hip_w12_linear(0, None, None, None, 65, 32, 131009, None, None, B.OUT_I64, None, None) == inval
-    assert L.kt_hip_w12_linear(0, None, None, None, 64, 32, 1048577, None, None, B.OUT_I64, None, None) == inval
+    assert L.kt_hip_w12_linear(0, None, None, None, 129, 32, 131009, None, None, B.OUT_I64, None, None) == inval
+    assert L.kt_hip_w12_linear(0, None, None, None, 128, 32, 262145, None, None, B.OUT_I64, None, None) == inval
     assert L.kt_hip_w12_linear(0, None, None, None, -1, 32, 64, None, None, B.OUT_I64, None, None) == inval

@@ -263,7 +263,7 @@ def test_w12_linear_against_the_oracle(torch_dev, out_kind):
     rng = np.random.default_rng(10 + out_kind)
     for m, n, k in [(1, 1, 1), (1, 5, 7), (2, 33, 100), (3, 64, 64), (4, 130, 1000), (5, 17, 4096), (8, 256, 2048),
                     (9, 70, 129), (16, 4096, 512), (17, 65, 64), (33, 200, 300), (64, 64, 4096), (65, 129, 640),
-                    (128, 512, 1024), (130, 300, 96), (300, 257, 448)]:
+                    (100, 96, 2000), (128, 512, 1024), (129, 100, 256), (130, 300, 96), (300, 257, 448)]:
         x = rng.integers(-128, 128, size=m * k).astype(np.int32)
         w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
         mant, shift = O.channel_scales(w, n, k, 40)
@@ -291,7 +291,7 @@ def test_w12_extremes(torch_dev):
     torch = torch_dev
     T = tb()
     n = 64
-    for m, k in [(1, 4096), (64, 4096), (65, 4096), (3, 20000), (65, 20000)]:
+    for m, k in [(1, 4096), (64, 4096), (128, 4096), (129, 4096), (3, 20000), (100, 20000), (129, 20000)]:
         for xv, wv in [(-128, -2048), (127, 2047), (-128, 2047), (127, -2048)]:
             x = np.full(m * k, xv, np.int32)
             w = np.full(n * k, wv, np.int32)
@@ -304,8 +304,8 @@ def test_w12_extremes(torch_dev):
 
 
 def test_w12_int32_bound_at_k_8192(torch_dev):
-    """x = -128 against w = -2048 over k = 8192 sums to exactly 2^31, one past int32: the skinny kernel (m <= 64) and
-    the GEMM (m > 64) must both carry it into i64 and requantize it exactly."""
+    """x = -128 against w = -2048 over k = 8192 sums to exactly 2^31, one past int32: the skinny kernel (m <= 128) and
+    the GEMM (m > 128) must both carry it into i64 and requantize it exactly."""
     torch = torch_dev
     T = tb()
     k, n = 8192, 40
@@ -314,7 +314,7 @@ def test_w12_int32_bound_at_k_8192(torch_dev):
     mant = np.full(n, 1, np.int32)
     shift = np.full(n, 24, np.int32)  # 2^31 / 2^24 = 128 -> clamps to 127 for int8, 128 for int32
     md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
-    for m in (1, 33, 65, 130):
+    for m in (1, 33, 65, 130, 200):
         x = np.full(m * k, -128, np.int32)
         xd = _x_device(torch, x, m, k)
         say(f"case: w12 2^31 bound m={m}")
@@ -373,7 +373,7 @@ def test_w12_requant_edges(torch_dev):
     shift = np.array([p[1] for p in pairs], np.int32)
     md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
     rng = np.random.default_rng(22)
-    for m, k in [(3, 4096), (65, 4096), (70, 9000)]:
+    for m, k in [(3, 4096), (70, 9000), (130, 4096), (140, 9000)]:
         x = rng.integers(-128, 128, size=m * k).astype(np.int32)
         w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
         w[: 2 * k] = -2048  # two channels at the largest magnitude

@@ -447,7 +447,7 @@ int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
     if (m > INT_MAX || n > INT_MAX || kp > INT_MAX) return (int)hipErrorInvalidValue;
     if (out_kind != KT_OUT_I64 && (mant_dev == nullptr || shift_dev == nullptr)) return (int)hipErrorInvalidValue;
     if (out_kind != KT_OUT_I64 && out_kind != KT_OUT_I32 && out_kind != KT_OUT_I8) return (int)hipErrorInvalidValue;
-    if (kp > (m > 64 ? KT_W12_GEMM_MAX_K : KT_W12_SKINNY_MAX_K)) return (int)hipErrorInvalidValue;
+    if (kp > (m > KT_W12_SKINNY_MAX_M ? KT_W12_GEMM_MAX_K : KT_W12_SKINNY_MAX_K)) return (int)hipErrorInvalidValue;
     KT_TRY(hipSetDevice(dev));
     if (kp == 0) {
         // an empty dot is 0; its requant is 0 as well

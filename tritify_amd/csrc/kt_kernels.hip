@@ -649,7 +649,7 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// W12 skinny GEMM (M <= 16 * MT, batch decode and short prefill chunks). Bandwidth-bound: the weights are read once,
+// W12 skinny GEMM (M <= 16 * MT <= 128, batch decode and short prefill chunks). Bandwidth-bound: the weights are read once,
 // so the grid must reach every CU with enough loads in flight and end without a cross-CTA reduction. A CTA owns half
 // a column block (16 columns: fragment lanes 16 hb + c + 32 h, i.e. two 256-byte runs of each 1 KB lo fragment and
 // two 128-byte runs of each 512-byte nib fragment; the two halves of a block read disjoint bytes) over all of k, so
@@ -829,7 +829,7 @@ hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb,
 template <int OUT>
 static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
                                  const int32_t* mant, const int32_t* shift, void* y, hipStream_t s) {
-    if (M <= 64) {
+    if (M <= KT_W12_SKINNY_MAX_M) {
         const int64_t ctas = 2 * ceil_div(N, 32);
         if (ctas > INT32_MAX || (int64_t)M * kp > (int64_t)UINT32_MAX || kp > KT_W12_SKINNY_MAX_K)
             return hipErrorInvalidValue;
@@ -844,7 +844,7 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
                                                                                     shift);                         \
         return hipGetLastError();                                                                                   \
     }
-        KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2)
+        KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2) KT_SKINNY(8, 4, 4)
 #undef KT_SKINNY
     }
     const bool small = kp <= KT_SMALL_KP;
