@@ -132,6 +132,106 @@ int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
                       int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
                       void* y_dev, void* stream);
 
+/* As kt_hip_w12_linear with out_kind KT_OUT_I8, then each int8 output q replaced by lut_dev[q + 127] (255 int8
+ * entries, device): an activation-code table applied in the epilogue (the GELU of config 5's FeedForward,
+ * crates/03-models/kt-model-vision/src/hiera.rs:336-340 with nonlin.rs:30-47, as an int8 code table).
+ * 1 <= k <= 8128. */
+int kt_hip_w12_linear_lut(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                          int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
+                          const int8_t* lut_dev, int8_t* y_dev, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * MoE layer of config 4 (GLM-4.5-Air shape), device-resident operands. Replaces the reference's per-token MoE path:
+ * MoeMlp::route / topk (crates/01-engine/kt-core/src/layers.rs:800-851), the expert calls of
+ * forward_int_with_experts (layers.rs:954-986) and MoeMlp::combine (layers.rs:893-923), with the shared expert of
+ * layers.rs:757-780. Integer semantics (this build's int8 definition of that layer):
+ *   route:   the top_k experts of token t by router code r[t, e] (descending, ties to the lower index), weight
+ *            cw = sig[clamp(round_half_away(r / 16), -127, 127) + 127] (sig: 255 int16 sigmoid codes);
+ *   expert:  gq, uq = int8 per-channel requant of the gate and up rows of x . WGU^T; h = clamp(requant(
+ *            silu[gq + 127] * uq, 1, h_shift), +-127) (silu: 255 int16 codes); d = int8 per-channel requant of
+ *            h . WD^T;
+ *   combine: out = clamp(requant(sum_i cw_i d_i + 4096 d_shared, 1, out_shift), +-127).
+ * Experts are groups 0..E-1, the shared expert is group E. Expert g's gate/up weights are the W12 planes of its
+ * 2F x H matrix (rows 0..F-1 gate, F..2F-1 up) packed by kt_hip_w12_pack_gate_up, at gu_lo + g * gu_lo_bytes
+ * (kt_hip_w12_bytes(2F, H)) and gu_nib + g * gu_lo_bytes / 2, scales (2F per group, natural order) at
+ * gu_mant/gu_shift + g * 2F; its down weights are H x F planes at d_lo + g * d_lo_bytes (kt_hip_w12_bytes(H, F)),
+ * scales at d_mant/d_shift + g * H. H and F are multiples of 64, at most 8128; 1 <= top_k <= min(E, 32); E + 1 <=
+ * KT_MAX_GROUPS.
+ * ------------------------------------------------------------------------------------------------------------- */
+#define KT_MAX_GROUPS 1024
+#define KT_EPI_I8 0     /* grouped GEMM epilogue: per-channel int8 requant */
+#define KT_EPI_SWIGLU 1 /* grouped GEMM epilogue: SwiGLU over an interleaved gate/up matrix */
+
+/* Pack a SwiGLU gate/up matrix (2*ffn x k i32 codes in [-2048, 2047], device: gate rows then up rows) into W12
+ * planes with 32-row gate/up interleave (packed row block 2j = gate rows 32j.., 2j+1 = up rows 32j..), the layout
+ * the SwiGLU epilogue reads. ffn is a multiple of 32. */
+int kt_hip_w12_pack_gate_up(int dev, const int32_t* codes_dev, int64_t ffn, int64_t k, int8_t* lo_dev,
+                            uint8_t* nib_dev, void* stream);
+
+/* MoeMlp::route (layers.rs:826-851, sigmoid score as GLM-4.5's router.rs:29-79): logits T x E int32 (device) ->
+ * sel (T x top_k expert ids) and cw (T x top_k weights). E <= 1024. */
+int kt_hip_moe_route(int dev, const int32_t* logits_dev, int64_t tokens, int64_t experts, int top_k,
+                     const int16_t* sig_dev, int32_t* sel_dev, int32_t* cw_dev, void* stream);
+
+/* Bucket the routed tokens by expert: list ((E + 1) x T) holds group g's tokens in increasing order at
+ * g * T .. g * T + count[g] - 1 (group E: every token), pos (T x top_k) each choice's row within its group. */
+int kt_hip_moe_bucket(int dev, const int32_t* sel_dev, int64_t tokens, int64_t experts, int top_k,
+                      int32_t* list_dev, int32_t* pos_dev, int32_t* count_dev, void* stream);
+
+/* The ragged grouped W12 GEMM (the experts of forward_int_with_experts, layers.rs:954-986, run as one launch).
+ * groups <= KT_MAX_GROUPS; group g has count[g] rows (sum <= max_rows); its row j is x row list[g * list_stride + j]
+ * (list_dev non-null) or x row off[g] + j (off = exclusive prefix of count); x is x_rows x kp(k) int8. Group g's
+ * weights: n x k W12 planes at lo_dev + g * lo_bytes(n, k) and nib_dev + g * lo_bytes / 2, scales mant/shift +
+ * g * n. Output row j of group g is y row off[g] + j (row stride y_stride bytes). epilogue KT_EPI_I8: the n columns'
+ * per-channel int8 requant; KT_EPI_SWIGLU: weights packed by kt_hip_w12_pack_gate_up (n = 2F), output F columns of
+ * clamp(requant(silu[gq + 127] * uq, 1, h_shift)). off_dev (optional, groups + 1 int32) receives off. k <= 8128. */
+int kt_hip_w12_grouped_linear(int dev, const int8_t* x_dev, int64_t x_rows, const int32_t* list_dev,
+                              int64_t list_stride, const int32_t* count_dev, int64_t groups, int64_t max_rows,
+                              const int8_t* lo_dev, const uint8_t* nib_dev, int64_t n, int64_t k,
+                              const int32_t* mant_dev, const int32_t* shift_dev, int epilogue,
+                              const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride,
+                              int32_t* off_dev, void* stream);
+
+/* MoeMlp::combine (layers.rs:893-923) plus the shared expert: out (T x H int8) from d (rows in bucket order, H
+ * columns), off (groups + 1, from the grouped GEMM), sel, cw, pos. */
+int kt_hip_moe_combine(int dev, const int8_t* d_dev, const int32_t* off_dev, const int32_t* sel_dev,
+                       const int32_t* cw_dev, const int32_t* pos_dev, int64_t tokens, int64_t hidden,
+                       int64_t experts, int top_k, int out_shift, int8_t* out_dev, void* stream);
+
+/* The workspace of kt_hip_moe_forward: total bytes and the byte offsets of its parts, in this order: sel, cw, pos
+ * (T x top_k int32 each), list ((E + 1) x T int32), count (E + 1 int32), off (E + 2 int32), h (P x F int8) and
+ * d (P x H int8), P = T * (top_k + 1). Every part is 256-byte aligned. */
+#define KT_MOE_WS_PARTS 8
+int kt_hip_moe_workspace(int64_t tokens, int64_t hidden, int64_t ffn, int64_t experts, int top_k, size_t* total,
+                         size_t* offsets);
+
+/* The whole layer (MoeMlp::forward_int_with_experts with the local experts, layers.rs:954-986): route, bucket,
+ * gate/up grouped GEMM with the SwiGLU epilogue, down grouped GEMM, combine -- five launches on `stream`, no host
+ * synchronization. x is T x H int8 (H a multiple of 64), logits T x E int32, out T x H int8; workspace as
+ * kt_hip_moe_workspace describes (its intermediates stay readable after the call). */
+int kt_hip_moe_forward(int dev, const int8_t* x_dev, const int32_t* logits_dev, int64_t tokens, int64_t hidden,
+                       int64_t ffn, int64_t experts, int top_k, const int8_t* gu_lo_dev, const uint8_t* gu_nib_dev,
+                       const int32_t* gu_mant_dev, const int32_t* gu_shift_dev, const int8_t* d_lo_dev,
+                       const uint8_t* d_nib_dev, const int32_t* d_mant_dev, const int32_t* d_shift_dev,
+                       const int16_t* silu_dev, const int16_t* sig_dev, int h_shift, int out_shift,
+                       void* workspace_dev, int8_t* out_dev, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Synthetic workload generators (host only, no GPU): the BASELINE configs' integer samplers on the reference LCG
+ * (apps/kt-demo/src/main.rs:19-22), multithreaded over the host cores. No counterpart in the reference.
+ * ------------------------------------------------------------------------------------------------------------- */
+/* n codes uniform in [-2048, 2047]: ((s >> 33) % 4096) - 2048 on the stream seeded seed ^ 0x9E3779B97F4A7C15. */
+void kt_hip_gen_w12(uint64_t seed, size_t n, int32_t* out);
+/* n values round_half_away(N(0, sigma)), clipped to +-clip when clip > 0: an Irwin-Hall sum of 12 draws
+ * u = (s >> 33) & 0xFFFF on the stream seed ^ 0xD1B54A32D192ED03, t = 2 sum - 12 * 65535,
+ * v = sign(t) * ((|t| sigma + 2^16) >> 17). */
+void kt_hip_gen_gauss(uint64_t seed, int64_t sigma, int64_t clip, size_t n, int32_t* out);
+/* n values uniform in [lo, hi]: ((s >> 33) % (hi - lo + 1)) + lo on the stream seed ^ 0x9E3779B97F4A7C15. */
+void kt_hip_gen_uniform(uint64_t seed, int64_t lo, int64_t hi, size_t n, int32_t* out);
+/* Per output channel of an n x k code matrix: to_i32(Scale::from_ratio(127, 4 * sigma * isqrt(sum_k w^2)))
+ * (crates/00-kernels/kt-int/src/lib.rs:191-212), mapping 4 standard deviations of the accumulator to 127. */
+void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, int32_t* mant, int32_t* shift);
+
 /* Test hook: one 32x32x32 and one 16x16x64 int8 MFMA on 64 lanes x 16 bytes of a_dev / b_dev; the raw accumulator
  * registers go to c32_dev (64 x 16 i32) and c16_dev (64 x 4 i32). */
 int kt_hip_probe_mfma(int dev, const int8_t* a_dev, const int8_t* b_dev, int32_t* c32_dev, int32_t* c16_dev,

@@ -106,6 +106,17 @@ def _declare(L: C.CDLL) -> None:
         "kt_w12_linear": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _P]),
         "kt_requant_channels": (None, [_P, _SZ, _SZ, _P, _P, C.c_int64, C.c_int64, _P]),
         "kt_channel_scales": (None, [_P, _SZ, _SZ, C.c_int64, _P, _P]),
+        "kt_gen_w12_i16": (None, [C.c_uint64, _SZ, _P]),
+        "kt_gen_gauss_i32": (None, [C.c_uint64, C.c_int64, _SZ, _P]),
+        "kt_channel_scales_i16": (None, [_P, _SZ, _SZ, C.c_int64, _P, _P]),
+        "kt_gemm_i8w16": (C.c_int, [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _SZ]),
+        "kt_moe_route": (None, [_P, _SZ, _SZ, _SZ, _P, _P, _P]),
+        "kt_moe_bucket": (None, [_P, _SZ, _SZ, _SZ, _P, _P, _P]),
+        "kt_moe_experts": (C.c_int, [_P, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, _P, _P,
+                                     _SZ]),
+        "kt_moe_combine": (None, [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, C.c_int, _P]),
+        "kt_moe_forward_token": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int,
+                                        C.c_int, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -447,3 +458,109 @@ def channel_scales(w, n, k, sigma=40):
     shift = np.empty(n, dtype=np.int32)
     lib().kt_channel_scales(_ptr(w), n, k, sigma, _ptr(mant), _ptr(shift))
     return mant, shift
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the layers of configs 3-5 (kt_oracle_layers.c)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def gen_w12_i16(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int16)
+    lib().kt_gen_w12_i16(seed & (2**64 - 1), n, _ptr(out))
+    return out
+
+
+def gen_gauss_i32(seed: int, sigma: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_gen_gauss_i32(seed & (2**64 - 1), sigma, n, _ptr(out))
+    return out
+
+
+def channel_scales_i16(w, n: int, k: int, sigma: int):
+    w = _c(w, np.int16)
+    mant = np.empty(n, dtype=np.int32)
+    shift = np.empty(n, dtype=np.int32)
+    lib().kt_channel_scales_i16(_ptr(w), n, k, sigma, _ptr(mant), _ptr(shift))
+    return mant, shift
+
+
+def gemm_i8w16(x, w, m: int, n: int, k: int, mant=None, shift=None, threads: int = 0):
+    """(acc i64 m x n, y8 int8 m x n or None): x int8 m x k against int16 codes n x k, the int8 epilogue when
+    scales are given."""
+    x, w = _c(x, np.int8), _c(w, np.int16)
+    acc = np.empty(m * n, dtype=np.int64)
+    y8 = np.empty(m * n, dtype=np.int8) if mant is not None else None
+    mant_ = _c(mant, np.int32) if mant is not None else None
+    shift_ = _c(shift, np.int32) if shift is not None else None
+    r = lib().kt_gemm_i8w16(_ptr(x), _ptr(w), m, n, k, _ptr(mant_) if mant_ is not None else None,
+                            _ptr(shift_) if shift_ is not None else None, _ptr(acc),
+                            _ptr(y8) if y8 is not None else None, threads)
+    if r != 0:
+        raise ValueError("gemm_i8w16: k beyond the int32-exact bound")
+    return acc, y8
+
+
+def moe_route(logits, T: int, E: int, top_k: int, sig):
+    logits, sig = _c(logits, np.int32), _c(sig, np.int16)
+    sel = np.empty(T * top_k, dtype=np.int32)
+    cw = np.empty(T * top_k, dtype=np.int32)
+    lib().kt_moe_route(_ptr(logits), T, E, top_k, _ptr(sig), _ptr(sel), _ptr(cw))
+    return sel, cw
+
+
+def moe_bucket(sel, T: int, E: int, top_k: int):
+    sel = _c(sel, np.int32)
+    lst = np.full((E + 1) * T, -1, dtype=np.int32)
+    pos = np.empty(T * top_k, dtype=np.int32)
+    count = np.empty(E + 1, dtype=np.int32)
+    lib().kt_moe_bucket(_ptr(sel), T, E, top_k, _ptr(lst), _ptr(pos), _ptr(count))
+    return lst, pos, count
+
+
+def moe_experts(x, T, H, F, G, lst, count, wgu, wd, gm, gs, dm, ds, silu, h_shift, threads: int = 0):
+    """h (P x F) and d (P x H) int8 in bucket order, P = sum(count)."""
+    x = _c(x, np.int8)
+    lst, count = _c(lst, np.int32), _c(count, np.int32)
+    wgu, wd, silu = _c(wgu, np.int16), _c(wd, np.int16), _c(silu, np.int16)
+    gm, gs, dm, ds = (_c(a, np.int32) for a in (gm, gs, dm, ds))
+    P = int(count.astype(np.int64).sum())
+    h = np.empty(P * F, dtype=np.int8)
+    d = np.empty(P * H, dtype=np.int8)
+    r = lib().kt_moe_experts(_ptr(x), T, H, F, G, _ptr(lst), _ptr(count), _ptr(wgu), _ptr(wd), _ptr(gm), _ptr(gs),
+                             _ptr(dm), _ptr(ds), _ptr(silu), h_shift, _ptr(h), _ptr(d), threads)
+    if r != 0:
+        raise ValueError("moe_experts: a dimension beyond the int32-exact bound")
+    return h, d
+
+
+def moe_combine(d, sel, cw, pos, count, T: int, H: int, E: int, top_k: int, out_shift: int) -> np.ndarray:
+    d = _c(d, np.int8)
+    sel, cw, pos, count = (_c(a, np.int32) for a in (sel, cw, pos, count))
+    out = np.empty(T * H, dtype=np.int8)
+    lib().kt_moe_combine(_ptr(d), _ptr(sel), _ptr(cw), _ptr(pos), _ptr(count), T, H, E, top_k, out_shift, _ptr(out))
+    return out
+
+
+def moe_forward_token(x, logits, T, H, F, E, top_k, wgu, wd, gm, gs, dm, ds, silu, sig, h_shift, out_shift):
+    """The reference's loop order: token by token, each chosen expert on one row (slow; small shapes only)."""
+    x, logits = _c(x, np.int8), _c(logits, np.int32)
+    wgu, wd, silu, sig = _c(wgu, np.int16), _c(wd, np.int16), _c(silu, np.int16), _c(sig, np.int16)
+    gm, gs, dm, ds = (_c(a, np.int32) for a in (gm, gs, dm, ds))
+    out = np.empty(T * H, dtype=np.int8)
+    lib().kt_moe_forward_token(_ptr(x), _ptr(logits), T, H, F, E, top_k, _ptr(wgu), _ptr(wd), _ptr(gm), _ptr(gs),
+                               _ptr(dm), _ptr(ds), _ptr(silu), _ptr(sig), h_shift, out_shift, _ptr(out))
+    return out
+
+
+def moe_layer(x, logits, T, H, F, E, top_k, wgu, wd, gm, gs, dm, ds, silu, sig, h_shift, out_shift, threads=0):
+    """The expert-major evaluation the GPU performs: route, bucket, experts, combine. Returns a dict of every
+    intermediate (sel, cw, list, pos, count, h, d) and out."""
+    sel, cw = moe_route(logits, T, E, top_k, sig)
+    lst, pos, count = moe_bucket(sel, T, E, top_k)
+    h, d = moe_experts(x, T, H, F, E + 1, lst, count, wgu, wd, gm, gs, dm, ds, silu, h_shift, threads)
+    out = moe_combine(d, sel, cw, pos, count, T, H, E, top_k, out_shift)
+    return dict(sel=sel, cw=cw, list=lst, pos=pos, count=count, h=h, d=d, out=out)

@@ -21,6 +21,47 @@ OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "goldens.json")
 # kt_channel_scales): N = K = 4096, M in {1, 16, 128, 2048} taking the first M rows of one 2048-row activation draw.
 C2 = {"w_seed": 2, "x_seed": 3, "sigma": 40, "N": 4096, "K": 4096, "Ms": [1, 16, 128, 2048]}
 
+# BASELINE config 4 (this build's integer MoE layer, include/kt_hip.h): GLM-4.5-Air shape.
+C4 = {"T": 4096, "H": 4096, "F": 1408, "E": 128, "top_k": 8, "x_seed": 41, "r_seed": 42, "w_seed": 4000,
+      "sigma_x": 40, "sigma_r": 1024, "sigma_h": 16, "h_shift": 8, "out_shift": 13}
+
+
+def config4() -> dict:
+    """The expert-major oracle (kt_moe_layer) on the full config-4 layer: weights from the oracle's own generator
+    (kt_gen_w12_i16, the kt_gen_w12 stream), tables from the workload definitions."""
+    from tritify_amd import workloads as W
+
+    c = dict(C4)
+    T, H, F, E, K = c["T"], c["H"], c["F"], c["E"], c["top_k"]
+    x = O.gen_act_gauss(c["x_seed"], c["sigma_x"], T * H)
+    r = O.gen_gauss_i32(c["r_seed"], c["sigma_r"], T * E)
+    silu, sig = W.silu_table(), W.sigmoid_table()
+    G = E + 1
+    wgu = np.empty((G, 2 * F * H), np.int16)
+    wd = np.empty((G, H * F), np.int16)
+    gm = np.empty((G, 2 * F), np.int32)
+    gs = np.empty((G, 2 * F), np.int32)
+    dm = np.empty((G, H), np.int32)
+    ds = np.empty((G, H), np.int32)
+    for g in range(G):
+        wgu[g] = O.gen_w12_i16(c["w_seed"] + 2 * g, 2 * F * H)
+        wd[g] = O.gen_w12_i16(c["w_seed"] + 2 * g + 1, H * F)
+        gm[g], gs[g] = O.channel_scales_i16(wgu[g], 2 * F, H, c["sigma_x"])
+        dm[g], ds[g] = O.channel_scales_i16(wd[g], H, F, c["sigma_h"])
+    t = time.time()
+    res = O.moe_layer(x, r, T, H, F, E, K, wgu, wd, gm, gs, dm, ds, silu, sig, c["h_shift"], c["out_shift"])
+    print(f"config4 layer: {time.time() - t:.1f}s", flush=True)
+    c.update({
+        "x_sha256": O.sha256_hex(x), "logits_sha256": O.sha256_hex(r),
+        "silu_sha256": O.sha256_hex(silu), "sig_sha256": O.sha256_hex(sig),
+        "sel_sha256": O.sha256_hex(res["sel"]), "cw_sha256": O.sha256_hex(res["cw"]),
+        "count": [int(v) for v in res["count"]],
+        "h_sha256": O.sha256_hex(res["h"]), "d_sha256": O.sha256_hex(res["d"]), "out_sha256": O.sha256_hex(res["out"]),
+        "out_absmean": float(np.abs(res["out"].astype(np.int32)).mean()),
+        "out_saturated": int((np.abs(res["out"].astype(np.int32)) == 127).sum()),
+    })
+    return c
+
 
 def main() -> None:
     t0 = time.time()
@@ -57,6 +98,7 @@ def main() -> None:
         }
         print(f"config2 M={m}: {time.time() - t:.1f}s", flush=True)
     g["config2"] = c2
+    g["config4"] = config4()
     json.dump(g, open(OUT, "w"), indent=1, sort_keys=True)
     print(f"wrote {OUT} in {time.time() - t0:.1f}s")
 

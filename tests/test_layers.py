@@ -1,0 +1,185 @@
+"""CPU tests: the oracle of the layers around the 12-bit GEMM (oracle/kt_oracle_layers.c) pinned against brute
+force and closed forms, and the product's host-side workload generators against the oracle's. No GPU needed.
+
+What pins what:
+  - gemm_i8w16 (the blocked dot of every dense W12 check) equals kt_linear_cpu, the restated reference linear_cpu;
+  - moe_route equals a Python sort with the reference's tie rule (MoeMlp::topk, layers.rs:800-805);
+  - moe_bucket equals a Python loop;
+  - the expert-major MoE layer equals the per-token loop order of the reference (layers.rs:928-936, 988-1020), and
+    on a tiny case both equal a pure-Python restatement with Python integers (requant of kt-int lib.rs:78-86);
+  - the SiLU / sigmoid code tables satisfy the identities of the closed forms they come from.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def py_requant(acc: int, mant: int, shift: int) -> int:
+    """kt-int requant (crates/00-kernels/kt-int/src/lib.rs:78-86) in Python integers: round(acc * mant / 2^shift)
+    half away from zero."""
+    p = acc * mant
+    if shift <= 0:
+        return p << (-shift)
+    q = (abs(p) + (1 << (shift - 1))) >> shift
+    return q if p >= 0 else -q
+
+
+def clamp(v, lo=-127, hi=127):
+    return max(lo, min(hi, v))
+
+
+def test_gemm_i8w16_equals_linear_cpu():
+    rng = np.random.default_rng(1)
+    for m, n, k in [(1, 1, 1), (3, 70, 129), (33, 64, 512), (65, 5, 4096)]:
+        x = rng.integers(-128, 128, size=m * k).astype(np.int8)
+        w = rng.integers(-2048, 2048, size=n * k).astype(np.int16)
+        acc, _ = O.gemm_i8w16(x, w, m, n, k)
+        assert np.array_equal(acc, O.linear_cpu(x.astype(np.int32), w.astype(np.int32), m, n, k))
+        mant = rng.integers(-(2**31), 2**31, size=n).astype(np.int32)
+        shift = rng.integers(-3, 64, size=n).astype(np.int32)
+        _, y8 = O.gemm_i8w16(x, w, m, n, k, mant, shift)
+        want = O.requant_channels(acc, m, n, mant, shift, -127, 127)
+        assert np.array_equal(y8.astype(np.int32), want)
+
+
+def test_gemm_i8w16_extremes_fit_int32():
+    """|x| = 128, |w| = 2048 at k = 8128: every partial sum of the int32 dot stays exact."""
+    k = 8128
+    x = np.full(k, -128, np.int8)
+    w = np.full(2 * k, -2048, np.int16)
+    acc, _ = O.gemm_i8w16(x, w, 1, 2, k)
+    assert acc.tolist() == [k * 128 * 2048] * 2
+    with pytest.raises(ValueError):
+        O.gemm_i8w16(np.zeros(8192, np.int8), np.zeros(8192, np.int16), 1, 1, 8192)
+
+
+def route_py(r, E, K, sig):
+    out = []
+    for t in range(len(r) // E):
+        row = [int(v) for v in r[t * E:(t + 1) * E]]
+        top = sorted(range(E), key=lambda e: (-row[e], e))[:K]
+        cws = []
+        for e in top:
+            a = abs(row[e])
+            q = min((a + 8) >> 4, 127)
+            idx = q if row[e] >= 0 else -q
+            cws.append(int(sig[idx + 127]))
+        out.append((top, cws))
+    return out
+
+
+def test_moe_route_equals_python_sort():
+    from tritify_amd import workloads as W
+
+    sig = W.sigmoid_table()
+    rng = np.random.default_rng(2)
+    for T, E, K in [(50, 16, 4), (20, 128, 8), (5, 3, 3)]:
+        r = O.gen_gauss_i32(T + E, 1024, T * E)
+        r[: E] = 5  # one token of ties
+        r[E: E + 3] = 10**7  # far outside the table
+        r[E + 3: E + 6] = -(10**7)
+        sel, cw = O.moe_route(r, T, E, K, sig)
+        want = route_py(r, E, K, sig)
+        assert sel.reshape(T, K).tolist() == [w[0] for w in want]
+        assert cw.reshape(T, K).tolist() == [w[1] for w in want]
+
+
+def test_moe_bucket_equals_python():
+    rng = np.random.default_rng(3)
+    T, E, K = 97, 10, 3
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32).reshape(-1)
+    lst, pos, count = O.moe_bucket(sel, T, E, K)
+    groups = {g: [] for g in range(E + 1)}
+    for t in range(T):
+        for i in range(K):
+            g = int(sel[t * K + i])
+            assert pos[t * K + i] == len(groups[g])
+            groups[g].append(t)
+        groups[E].append(t)
+    assert count.tolist() == [len(groups[g]) for g in range(E + 1)]
+    for g in range(E + 1):
+        assert lst[g * T: g * T + count[g]].tolist() == groups[g]
+
+
+def moe_case(T, H, F, E, K, seed, logits=None):
+    from tritify_amd import workloads as W
+
+    x = O.gen_act_gauss(seed, 40, T * H)
+    r = O.gen_gauss_i32(seed + 1, 1024, T * E) if logits is None else logits
+    G = E + 1
+    wgu = np.stack([O.gen_w12_i16(seed + 10 + 2 * g, 2 * F * H) for g in range(G)])
+    wd = np.stack([O.gen_w12_i16(seed + 11 + 2 * g, H * F) for g in range(G)])
+    gm, gs = zip(*[O.channel_scales_i16(wgu[g], 2 * F, H, 40) for g in range(G)])
+    dm, ds = zip(*[O.channel_scales_i16(wd[g], H, F, 16) for g in range(G)])
+    return dict(x=x, r=r, wgu=wgu, wd=wd, gm=np.stack(gm), gs=np.stack(gs), dm=np.stack(dm), ds=np.stack(ds),
+                silu=W.silu_table(), sig=W.sigmoid_table())
+
+
+@pytest.mark.parametrize("T,H,F,E,K", [(64, 64, 32, 8, 2), (130, 128, 64, 6, 6), (1, 64, 32, 4, 1)])
+def test_moe_expert_major_equals_token_order(T, H, F, E, K):
+    c = moe_case(T, H, F, E, K, 17 * T + E)
+    res = O.moe_layer(c["x"], c["r"], T, H, F, E, K, c["wgu"], c["wd"], c["gm"], c["gs"], c["dm"], c["ds"],
+                      c["silu"], c["sig"], 8, 13)
+    tok = O.moe_forward_token(c["x"], c["r"], T, H, F, E, K, c["wgu"], c["wd"], c["gm"], c["gs"], c["dm"], c["ds"],
+                              c["silu"], c["sig"], 8, 13)
+    assert np.array_equal(res["out"], tok)
+    assert int(res["count"].sum()) == T * (K + 1)
+
+
+def test_moe_layer_equals_python_restatement():
+    """A tiny layer evaluated with Python integers only (route, SwiGLU, down, combine) equals the C oracle."""
+    T, H, F, E, K = 3, 64, 32, 4, 2
+    c = moe_case(T, H, F, E, K, 5)
+    res = O.moe_layer(c["x"], c["r"], T, H, F, E, K, c["wgu"], c["wd"], c["gm"], c["gs"], c["dm"], c["ds"],
+                      c["silu"], c["sig"], 8, 13)
+    routes = route_py(c["r"], E, K, c["sig"])
+    x = c["x"].reshape(T, H).astype(object)
+    for t in range(T):
+        y = [0] * H
+        top, cws = routes[t]
+        for g, wgt in list(zip(top, cws)) + [(E, 4096)]:
+            wgu = c["wgu"][g].reshape(2 * F, H).astype(object)
+            wd = c["wd"][g].reshape(H, F).astype(object)
+            h = []
+            for ch in range(F):
+                gq = clamp(py_requant(int(np.dot(x[t], wgu[ch])), int(c["gm"][g][ch]), int(c["gs"][g][ch])))
+                uq = clamp(py_requant(int(np.dot(x[t], wgu[F + ch])), int(c["gm"][g][F + ch]),
+                                      int(c["gs"][g][F + ch])))
+                h.append(clamp(py_requant(int(c["silu"][gq + 127]) * uq, 1, 8)))
+            d = [clamp(py_requant(int(np.dot(np.array(h, dtype=object), wd[o])), int(c["dm"][g][o]),
+                                  int(c["ds"][g][o]))) for o in range(H)]
+            y = [a + wgt * b for a, b in zip(y, d)]
+        want = [clamp(py_requant(v, 1, 13)) for v in y]
+        assert res["out"].reshape(T, H)[t].tolist() == want
+
+
+def test_code_tables_closed_forms():
+    """sigmoid(v) + sigmoid(-v) = 1 and silu(v) - silu(-v) = v, at the tables' scales and resolution."""
+    from tritify_amd import workloads as W
+
+    sig, silu = W.sigmoid_table().astype(int), W.silu_table().astype(int)
+    assert sig[127] == 2048 and silu[127] == 0
+    for i in range(1, 128):
+        assert sig[127 + i] + sig[127 - i] == 4096
+        assert abs((silu[127 + i] - silu[127 - i]) - 8 * i) <= 1  # 256 * (i / 32)
+    assert (np.diff(sig) >= 0).all()
+    assert silu.min() >= -72 and silu.max() <= 1000
+
+
+def test_product_generators_equal_the_oracle():
+    """The product's multithreaded host generators (libkt_hip.so) draw the same streams as the oracle's."""
+    import tritify_amd as TA
+
+    for seed in (0, 3, 2**63 + 5):
+        n = 3_000_001
+        assert np.array_equal(TA.gen_w12_fast(seed, n), O.gen_w12(seed, n))
+        assert np.array_equal(TA.gen_gauss_fast(seed, 40, n, clip=127), O.gen_act_gauss(seed, 40, n))
+        assert np.array_equal(TA.gen_gauss_fast(seed, 1024, n // 7), O.gen_gauss_i32(seed, 1024, n // 7))
+        assert np.array_equal(TA.gen_uniform_fast(seed, -127, 127, n), O.gen_act_uniform(seed, n))
+    w = O.gen_w12(9, 300 * 517)
+    m1, s1 = TA.channel_scales_fast(w, 300, 517, 40)
+    m2, s2 = O.channel_scales(w, 300, 517, 40)
+    assert np.array_equal(m1, m2) and np.array_equal(s1, s2)
+    m3, s3 = O.channel_scales_i16(w.astype(np.int16), 300, 517, 40)
+    assert np.array_equal(m1, m3) and np.array_equal(s1, s3)

@@ -78,6 +78,20 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_w12_upload": (_I, [_I, _P, _I64, _I64, _P, _P]),
         "kt_hip_w12_linear": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
         "kt_hip_probe_mfma": (_I, [_I, _P, _P, _P, _P, _P]),
+        "kt_hip_w12_linear_lut": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_w12_pack_gate_up": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
+        "kt_hip_moe_route": (_I, [_I, _P, _I64, _I64, _I, _P, _P, _P, _P]),
+        "kt_hip_moe_bucket": (_I, [_I, _P, _I64, _I64, _I, _P, _P, _P, _P]),
+        "kt_hip_w12_grouped_linear": (_I, [_I, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I,
+                                           _P, _I, _P, _I64, _P, _P]),
+        "kt_hip_moe_combine": (_I, [_I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P]),
+        "kt_hip_moe_workspace": (_I, [_I64, _I64, _I64, _I64, _I, C.POINTER(_SZ), C.POINTER(_SZ)]),
+        "kt_hip_moe_forward": (_I, [_I, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _I, _I, _P, _P, _P]),
+        "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
+        "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
+        "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
+        "kt_hip_channel_scales": (None, [_P, _SZ, _SZ, _I64, _P, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -278,3 +292,112 @@ def pack_planes(codes_dev, rows: int, k: int, planes: int, planes_dev, stream=No
 def probe_mfma(a_dev, b_dev, c32_dev, c16_dev, stream=None, dev: int = 0) -> None:
     check(lib().kt_hip_probe_mfma(dev, _ptr(a_dev), _ptr(b_dev), _ptr(c32_dev), _ptr(c16_dev), _stream(stream)),
           "mfma probe")
+
+
+def w12_linear_lut(x_dev, lo_dev, nib_dev, m: int, n: int, k: int, y_dev, mant_dev, shift_dev, lut_dev, stream=None,
+                   dev: int = 0) -> None:
+    """y = lut[int8 requant(x · Wᵀ) + 127]: the dense W12 product with an activation-code table in the epilogue."""
+    check(
+        lib().kt_hip_w12_linear_lut(dev, _ptr(x_dev), _ptr(lo_dev), _ptr(nib_dev), m, n, k, _ptr(mant_dev),
+                                    _ptr(shift_dev), _ptr(lut_dev), _ptr(y_dev), _stream(stream)),
+        "w12 linear lut",
+    )
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# MoE layer (config 4): MoeMlp::route / experts / combine (crates/01-engine/kt-core/src/layers.rs:800-1020)
+
+EPI_I8, EPI_SWIGLU = 0, 1
+MAX_GROUPS = 1024
+
+
+def w12_pack_gate_up(codes_dev, ffn: int, k: int, lo_dev, nib_dev, stream=None, dev: int = 0) -> None:
+    """Pack a 2·ffn x k gate/up code matrix (gate rows first, device i32) with the 32-row gate/up interleave."""
+    check(lib().kt_hip_w12_pack_gate_up(dev, _ptr(codes_dev), ffn, k, _ptr(lo_dev), _ptr(nib_dev), _stream(stream)),
+          "w12 pack gate/up")
+
+
+def moe_route(logits_dev, tokens: int, experts: int, top_k: int, sig_dev, sel_dev, cw_dev, stream=None,
+              dev: int = 0) -> None:
+    check(lib().kt_hip_moe_route(dev, _ptr(logits_dev), tokens, experts, top_k, _ptr(sig_dev), _ptr(sel_dev),
+                                 _ptr(cw_dev), _stream(stream)), "moe route")
+
+
+def moe_bucket(sel_dev, tokens: int, experts: int, top_k: int, list_dev, pos_dev, count_dev, stream=None,
+               dev: int = 0) -> None:
+    check(lib().kt_hip_moe_bucket(dev, _ptr(sel_dev), tokens, experts, top_k, _ptr(list_dev), _ptr(pos_dev),
+                                  _ptr(count_dev), _stream(stream)), "moe bucket")
+
+
+def w12_grouped_linear(x_dev, x_rows: int, list_dev, list_stride: int, count_dev, groups: int, max_rows: int, lo_dev,
+                       nib_dev, n: int, k: int, mant_dev, shift_dev, epilogue: int, y_dev, y_stride: int,
+                       silu_dev=None, h_shift: int = 0, off_dev=None, stream=None, dev: int = 0) -> None:
+    """The ragged grouped W12 GEMM (one launch over every group; see include/kt_hip.h)."""
+    check(
+        lib().kt_hip_w12_grouped_linear(dev, _ptr(x_dev), x_rows, _ptr(list_dev), list_stride, _ptr(count_dev), groups,
+                                        max_rows, _ptr(lo_dev), _ptr(nib_dev), n, k, _ptr(mant_dev), _ptr(shift_dev),
+                                        epilogue, _ptr(silu_dev), h_shift, _ptr(y_dev), y_stride, _ptr(off_dev),
+                                        _stream(stream)),
+        "w12 grouped linear",
+    )
+
+
+def moe_combine(d_dev, off_dev, sel_dev, cw_dev, pos_dev, tokens: int, hidden: int, experts: int, top_k: int,
+                out_shift: int, out_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_moe_combine(dev, _ptr(d_dev), _ptr(off_dev), _ptr(sel_dev), _ptr(cw_dev), _ptr(pos_dev),
+                                   tokens, hidden, experts, top_k, out_shift, _ptr(out_dev), _stream(stream)),
+          "moe combine")
+
+
+MOE_WS_PARTS = ("sel", "cw", "pos", "list", "count", "off", "h", "d")
+
+
+def moe_workspace(tokens: int, hidden: int, ffn: int, experts: int, top_k: int) -> tuple[int, dict]:
+    """Bytes of kt_hip_moe_forward's workspace and the byte offset of each part."""
+    total = C.c_size_t()
+    offs = (C.c_size_t * len(MOE_WS_PARTS))()
+    check(lib().kt_hip_moe_workspace(tokens, hidden, ffn, experts, top_k, C.byref(total), offs), "moe workspace")
+    return total.value, dict(zip(MOE_WS_PARTS, [o for o in offs]))
+
+
+def moe_forward(x_dev, logits_dev, tokens: int, hidden: int, ffn: int, experts: int, top_k: int, gu_lo, gu_nib,
+                gu_mant, gu_shift, d_lo, d_nib, d_mant, d_shift, silu_dev, sig_dev, h_shift: int, out_shift: int,
+                workspace_dev, out_dev, stream=None, dev: int = 0) -> None:
+    """The config-4 MoE layer: route, bucket, gate/up + SwiGLU, down, combine (five launches, asynchronous)."""
+    check(
+        lib().kt_hip_moe_forward(dev, _ptr(x_dev), _ptr(logits_dev), tokens, hidden, ffn, experts, top_k, _ptr(gu_lo),
+                                 _ptr(gu_nib), _ptr(gu_mant), _ptr(gu_shift), _ptr(d_lo), _ptr(d_nib), _ptr(d_mant),
+                                 _ptr(d_shift), _ptr(silu_dev), _ptr(sig_dev), h_shift, out_shift,
+                                 _ptr(workspace_dev), _ptr(out_dev), _stream(stream)),
+        "moe forward",
+    )
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# host-side synthetic workload generators (no GPU)
+
+
+def gen_w12_fast(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_hip_gen_w12(seed & (2**64 - 1), n, out.ctypes.data)
+    return out
+
+
+def gen_gauss_fast(seed: int, sigma: int, n: int, clip: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_hip_gen_gauss(seed & (2**64 - 1), sigma, clip, n, out.ctypes.data)
+    return out
+
+
+def gen_uniform_fast(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_hip_gen_uniform(seed & (2**64 - 1), lo, hi, n, out.ctypes.data)
+    return out
+
+
+def channel_scales_fast(w: np.ndarray, n: int, k: int, sigma: int) -> tuple[np.ndarray, np.ndarray]:
+    w = _i32(w)
+    mant = np.empty(n, dtype=np.int32)
+    shift = np.empty(n, dtype=np.int32)
+    lib().kt_hip_channel_scales(w.ctypes.data, n, k, sigma, mant.ctypes.data, shift.ctypes.data)
+    return mant, shift

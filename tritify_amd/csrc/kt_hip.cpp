@@ -419,7 +419,7 @@ int kt_hip_w12_pack(int dev, const int32_t* codes_dev, int64_t n, int64_t k, int
                     void* stream) {
     if (n < 0 || k < 0) return (int)hipErrorInvalidValue;
     KT_TRY(hipSetDevice(dev));
-    return (int)kt::launch_w12_pack(codes_dev, n, k, lo_dev, nib_dev, (hipStream_t)stream);
+    return (int)kt::launch_w12_pack(codes_dev, n, k, 0, lo_dev, nib_dev, (hipStream_t)stream);
 }
 
 int kt_hip_w12_upload(int dev, const int32_t* codes, int64_t n, int64_t k, int8_t* lo_dev, uint8_t* nib_dev) {
@@ -432,7 +432,7 @@ int kt_hip_w12_upload(int dev, const int32_t* codes, int64_t n, int64_t k, int8_
     void* tmp = nullptr;
     KT_TRY(hipMalloc(&tmp, cnt * sizeof(int32_t)));
     hipError_t e = hipMemcpy(tmp, codes, cnt * sizeof(int32_t), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = kt::launch_w12_pack((const int32_t*)tmp, n, k, lo_dev, nib_dev, nullptr);
+    if (e == hipSuccess) e = kt::launch_w12_pack((const int32_t*)tmp, n, k, 0, lo_dev, nib_dev, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     hipError_t f = hipFree(tmp);
     return (int)(e != hipSuccess ? e : f);
@@ -454,8 +454,136 @@ int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
         const size_t w = out_kind == KT_OUT_I64 ? 8 : (out_kind == KT_OUT_I32 ? 4 : 1);
         return (int)hipMemsetAsync(y_dev, 0, (size_t)m * (size_t)n * w, (hipStream_t)stream);
     }
-    return (int)kt::launch_w12_linear(x_dev, lo_dev, nib_dev, (int)m, (int)n, (int)kp, mant_dev, shift_dev, out_kind,
+    return (int)kt::launch_w12_linear(x_dev, lo_dev, nib_dev, (int)m, (int)n, (int)kp, mant_dev, shift_dev, nullptr, out_kind,
                                       y_dev, (hipStream_t)stream);
+}
+
+int kt_hip_w12_linear_lut(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                          int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
+                          const int8_t* lut_dev, int8_t* y_dev, void* stream) {
+    if (m < 0 || n < 0 || k < 1 || lut_dev == nullptr || mant_dev == nullptr || shift_dev == nullptr)
+        return (int)hipErrorInvalidValue;
+    if (m == 0 || n == 0) return 0;
+    const int64_t kp = kp_of(k);
+    if (m > INT_MAX || n > INT_MAX || kp > 8128) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_linear(x_dev, lo_dev, nib_dev, (int)m, (int)n, (int)kp, mant_dev, shift_dev, lut_dev,
+                                      KT_OUT_I8, y_dev, (hipStream_t)stream);
+}
+
+// ----------------------------------------------------------------------------------------------------------------
+// MoE layer (config 4)
+// ----------------------------------------------------------------------------------------------------------------
+
+int kt_hip_w12_pack_gate_up(int dev, const int32_t* codes_dev, int64_t ffn, int64_t k, int8_t* lo_dev,
+                            uint8_t* nib_dev, void* stream) {
+    if (ffn <= 0 || k < 0 || ffn % 32) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_pack(codes_dev, 2 * ffn, k, ffn, lo_dev, nib_dev, (hipStream_t)stream);
+}
+
+int kt_hip_moe_route(int dev, const int32_t* logits_dev, int64_t tokens, int64_t experts, int top_k,
+                     const int16_t* sig_dev, int32_t* sel_dev, int32_t* cw_dev, void* stream) {
+    if (tokens < 0 || tokens > INT_MAX / 64 || experts < 1 || experts > 1024) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_moe_route(logits_dev, (int)tokens, (int)experts, top_k, sig_dev, sel_dev, cw_dev,
+                                     (hipStream_t)stream);
+}
+
+int kt_hip_moe_bucket(int dev, const int32_t* sel_dev, int64_t tokens, int64_t experts, int top_k,
+                      int32_t* list_dev, int32_t* pos_dev, int32_t* count_dev, void* stream) {
+    if (tokens < 0 || experts < 1 || (experts + 1) * tokens > INT_MAX || tokens * top_k > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_moe_bucket(sel_dev, (int)tokens, (int)experts, top_k, list_dev, pos_dev, count_dev,
+                                      (hipStream_t)stream);
+}
+
+int kt_hip_w12_grouped_linear(int dev, const int8_t* x_dev, int64_t x_rows, const int32_t* list_dev,
+                              int64_t list_stride, const int32_t* count_dev, int64_t groups, int64_t max_rows,
+                              const int8_t* lo_dev, const uint8_t* nib_dev, int64_t n, int64_t k,
+                              const int32_t* mant_dev, const int32_t* shift_dev, int epilogue,
+                              const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride,
+                              int32_t* off_dev, void* stream) {
+    if (x_rows < 0 || groups < 0 || max_rows < 0 || n < 0 || k < 1 || y_stride < 0 || list_stride < 0)
+        return (int)hipErrorInvalidValue;
+    if (groups == 0 || n == 0) return 0;
+    const int64_t kp = kp_of(k);
+    if (groups > KT_MAX_GROUPS || kp > 8128 || n > INT_MAX || y_stride > INT_MAX || list_stride > INT_MAX ||
+        mant_dev == nullptr || shift_dev == nullptr)
+        return (int)hipErrorInvalidValue;
+    const int64_t ycols = epilogue == KT_EPI_SWIGLU ? n / 2 : n;
+    if (y_stride < ycols) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    size_t lo_bytes = 0, nib_bytes = 0;
+    kt_hip_w12_bytes(n, k, &lo_bytes, &nib_bytes);
+    return (int)kt::launch_w12_grouped(x_dev, (size_t)x_rows * (size_t)kp, list_dev, (int)list_stride, count_dev,
+                                       (int)groups, max_rows, lo_dev, nib_dev, lo_bytes, (int)n, (int)kp, mant_dev,
+                                       shift_dev, epilogue, silu_dev, h_shift, y_dev, (int)y_stride, off_dev,
+                                       (hipStream_t)stream);
+}
+
+int kt_hip_moe_combine(int dev, const int8_t* d_dev, const int32_t* off_dev, const int32_t* sel_dev,
+                       const int32_t* cw_dev, const int32_t* pos_dev, int64_t tokens, int64_t hidden,
+                       int64_t experts, int top_k, int out_shift, int8_t* out_dev, void* stream) {
+    if (tokens < 0 || tokens > INT_MAX || hidden < 0 || hidden > INT_MAX || experts < 1) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_moe_combine(d_dev, off_dev, sel_dev, cw_dev, pos_dev, (int)tokens, (int)hidden,
+                                       (int)experts, top_k, out_shift, out_dev, (hipStream_t)stream);
+}
+
+static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+int kt_hip_moe_workspace(int64_t tokens, int64_t hidden, int64_t ffn, int64_t experts, int top_k, size_t* total,
+                         size_t* offsets) {
+    if (tokens < 0 || hidden < 0 || ffn < 0 || experts < 1 || top_k < 1) return (int)hipErrorInvalidValue;
+    const size_t T = (size_t)tokens, E = (size_t)experts, K = (size_t)top_k, P = T * (K + 1);
+    const size_t sizes[KT_MOE_WS_PARTS] = {T * K * 4, T * K * 4, T * K * 4, (E + 1) * T * 4,
+                                           (E + 1) * 4, (E + 2) * 4, P * (size_t)ffn, P * (size_t)hidden};
+    size_t at = 0;
+    for (int i = 0; i < KT_MOE_WS_PARTS; i++) {
+        if (offsets) offsets[i] = at;
+        at += align256(sizes[i]);
+    }
+    *total = at;
+    return 0;
+}
+
+int kt_hip_moe_forward(int dev, const int8_t* x_dev, const int32_t* logits_dev, int64_t tokens, int64_t hidden,
+                       int64_t ffn, int64_t experts, int top_k, const int8_t* gu_lo_dev, const uint8_t* gu_nib_dev,
+                       const int32_t* gu_mant_dev, const int32_t* gu_shift_dev, const int8_t* d_lo_dev,
+                       const uint8_t* d_nib_dev, const int32_t* d_mant_dev, const int32_t* d_shift_dev,
+                       const int16_t* silu_dev, const int16_t* sig_dev, int h_shift, int out_shift,
+                       void* workspace_dev, int8_t* out_dev, void* stream) {
+    if (tokens < 0 || hidden <= 0 || ffn <= 0 || hidden % 64 || ffn % 64 || hidden > 8128 || ffn > 8128 ||
+        experts < 1 || experts + 1 > KT_MAX_GROUPS || top_k < 1 || top_k > experts || top_k > 32 ||
+        workspace_dev == nullptr)
+        return (int)hipErrorInvalidValue;
+    if (tokens == 0) return 0;
+    const int64_t P = tokens * (top_k + 1);
+    if (P * hidden > (int64_t)0xFFFFFF00 || tokens * hidden > (int64_t)0xFFFFFF00 || (experts + 1) * tokens > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    size_t total = 0, off[KT_MOE_WS_PARTS];
+    KT_TRY((hipError_t)kt_hip_moe_workspace(tokens, hidden, ffn, experts, top_k, &total, off));
+    char* ws = (char*)workspace_dev;
+    int32_t *sel = (int32_t*)(ws + off[0]), *cw = (int32_t*)(ws + off[1]), *pos = (int32_t*)(ws + off[2]);
+    int32_t *list = (int32_t*)(ws + off[3]), *count = (int32_t*)(ws + off[4]), *goff = (int32_t*)(ws + off[5]);
+    int8_t *h = (int8_t*)(ws + off[6]), *d = (int8_t*)(ws + off[7]);
+    hipStream_t s = (hipStream_t)stream;
+    KT_TRY(hipSetDevice(dev));
+    const int T = (int)tokens, E = (int)experts;
+    KT_TRY(kt::launch_moe_route(logits_dev, T, E, top_k, sig_dev, sel, cw, s));
+    KT_TRY(kt::launch_moe_bucket(sel, T, E, top_k, list, pos, count, s));
+    size_t gu_lo = 0, gu_nib = 0, dn_lo = 0, dn_nib = 0;
+    kt_hip_w12_bytes(2 * ffn, hidden, &gu_lo, &gu_nib);
+    kt_hip_w12_bytes(hidden, ffn, &dn_lo, &dn_nib);
+    KT_TRY(kt::launch_w12_grouped(x_dev, (size_t)tokens * (size_t)hidden, list, T, count, E + 1, P, gu_lo_dev,
+                                  gu_nib_dev, gu_lo, (int)(2 * ffn), (int)hidden, gu_mant_dev, gu_shift_dev,
+                                  KT_EPI_SWIGLU, silu_dev, h_shift, h, (int)ffn, goff, s));
+    KT_TRY(kt::launch_w12_grouped(h, (size_t)P * (size_t)ffn, nullptr, 0, count, E + 1, P, d_lo_dev, d_nib_dev, dn_lo,
+                                  (int)hidden, (int)ffn, d_mant_dev, d_shift_dev, KT_EPI_I8, nullptr, 0, d,
+                                  (int)hidden, nullptr, s));
+    return (int)kt::launch_moe_combine(d, goff, sel, cw, pos, T, (int)hidden, E, top_k, out_shift, out_dev, s);
 }
 
 int kt_hip_probe_mfma(int dev, const int8_t* a_dev, const int8_t* b_dev, int32_t* c32_dev, int32_t* c16_dev,

@@ -10,11 +10,25 @@ namespace kt {
 
 hipError_t launch_pack_planes(const int32_t* codes, int64_t rows, int64_t k, int p, int wrong_carry, int8_t* out,
                               hipStream_t s);
-hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int8_t* lo, uint8_t* nib, hipStream_t s);
+hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t ilv, int8_t* lo, uint8_t* nib,
+                           hipStream_t s);
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
                              int k0, int k1, int accumulate, int drop_top, hipStream_t s);
 hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
-                             const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s);
+                             const int32_t* mant, const int32_t* shift, const int8_t* lut, int out_kind, void* y,
+                             hipStream_t s);
+hipError_t launch_moe_route(const int32_t* logits, int T, int E, int top_k, const int16_t* sig, int32_t* sel,
+                            int32_t* cw, hipStream_t s);
+hipError_t launch_moe_bucket(const int32_t* sel, int T, int E, int top_k, int32_t* list, int32_t* pos,
+                             int32_t* count, hipStream_t s);
+hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* list, int list_stride,
+                              const int32_t* count, int groups, int64_t max_rows, const int8_t* wlo,
+                              const uint8_t* wnib, size_t glo, int N, int kp, const int32_t* mant,
+                              const int32_t* shift, int epi, const int16_t* silu, int h_shift, int8_t* y,
+                              int ystride, int32_t* off_out, hipStream_t s);
+hipError_t launch_moe_combine(const int8_t* d, const int32_t* off, const int32_t* sel, const int32_t* cw,
+                              const int32_t* pos, int T, int H, int E, int top_k, int out_shift, int8_t* out,
+                              hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

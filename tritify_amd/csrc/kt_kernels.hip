@@ -11,126 +11,19 @@
 //    wrap and launches one kernel per chunk, each adding its i64 result into y.
 //    Layout of a planed operand: [plane][row][kp] int8, kp = k rounded up to 64, zero padded.
 //
-// 2. W12 (int8 activations x 12-bit weight codes in [-2048, 2047]): lo = (v & 255) - 128 (int8)
-//    and hi = (v + 2048) >> 8 (4 bits), v = lo + 256*hi - 1920, so sum_k x*v = S_lo + 256*S_hi - 1920*sum_k x.
-//    The weights are stored fragment-tiled: blocks of 32 rows x 32 k, each 64 lanes x (16 lo bytes + 8 nib bytes)
-//    in exactly the order one MFMA B operand takes them (lane l: row l%32, k = 16*(l/32) .. +16), so a wave fetches
-//    a B fragment with one fully coalesced 1 KB load and one 512-byte load, no LDS round trip. A lane's 8 nib bytes
-//    as dwords D0, D1 unpack in k order as D0 & 0x0F0F0F0F, (D0 >> 4) & .., D1 & .., (D1 >> 4) & .. .
+// 2. W12 (int8 activations x 12-bit weight codes in [-2048, 2047]), the format and the mainloop
+//    of kt_w12_core.h: the dense GEMM for large M and the skinny GEMM for batch decode live here, the grouped (MoE)
+//    and im2col GEMMs in their own files.
 //
-// MFMA: v_mfma_i32_32x32x32_i8 (GEMM) and, for skinny M, v_mfma_i32_16x16x64_i8. A lane's 16 operand bytes are
-// 16 consecutive k of one row (A) / one column (B); the hardware pairs A and B bytes with the same k-slot, so any
-// lane->k assignment that is the same for A and B gives the exact dot product. The C layout of the 32x32 MFMA is
-// lane l, register r -> row 8*(r/4) + 4*(l/32) + (r%4), column l%32; of the 16x16 MFMA: row 4*(l/16) + r, col l%16
-// (checked by the layout test in tests/test_gpu.py).
-
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <type_traits>
 
 #include "kt_kernels.h"
+#include "kt_w12_core.h"
 
 namespace kt {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v2i __attribute__((ext_vector_type(2)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
-// LDS tiles are rows of BK bytes in 16-byte chunks; chunk c of row r sits at chunk position c ^ swz(r) so that the
-// MFMA operand reads (consecutive lanes = consecutive rows, same chunk) fall in distinct banks. For 64-byte rows
-// swz = (r >> 2) & 3 measured conflict-free on gfx950 (about 195 B/clk per CU for ds_read_b128, against about
-// 120 for (r >> 1) & 3 and 62 without a swizzle).
-template <int CPR>
-__device__ __forceinline__ int swz(int r) {
-    if constexpr (CPR == 4) return (r >> 2) & 3;
-    else return (r ^ (r >> 3)) & 7;
-}
-
-template <int CPR>
-__device__ __forceinline__ int lds_off(int r, int c) {
-    return r * (CPR * 16) + ((c ^ swz<CPR>(r)) << 4);
-}
-
-__device__ __forceinline__ v4i lds_read16(const int8_t* base, int off) {
-    return *reinterpret_cast<const v4i*>(base + off);
-}
-__device__ __forceinline__ void lds_write16(int8_t* base, int off, v4i v) {
-    *reinterpret_cast<v4i*>(base + off) = v;
-}
-
-__device__ __forceinline__ v4i gload16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
-__device__ __forceinline__ v2i gload8(const uint8_t* p) { return *reinterpret_cast<const v2i*>(p); }
-
-// A raw buffer over `bytes` bytes at `base`: loads at offsets past the end return zeros, so tile rows beyond the
-// matrix need no branch. The descriptor lives in SGPRs; each load takes a 32-bit VGPR offset plus a scalar offset.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-}
-
-// 16 nibble bytes (32 codes of one nib group) -> two 16-byte chunks of the hi plane in natural k order.
-__device__ __forceinline__ void unpack_nib(v4i d, v4i& h0, v4i& h1) {
-    const int m = 0x0F0F0F0F;
-    h0 = v4i{d.x & m, (d.x >> 4) & m, d.y & m, (d.y >> 4) & m};
-    h1 = v4i{d.z & m, (d.z >> 4) & m, d.w & m, (d.w >> 4) & m};
-}
-
-__device__ __forceinline__ int sum4(v4i v) {
-    const int ones = 0x01010101;
-    int s = __builtin_amdgcn_sdot4(v.x, ones, 0, false);
-    s = __builtin_amdgcn_sdot4(v.y, ones, s, false);
-    s = __builtin_amdgcn_sdot4(v.z, ones, s, false);
-    return __builtin_amdgcn_sdot4(v.w, ones, s, false);
-}
-
-// round(acc * mant / 2^shift), half away from zero, from the exact 128-bit product, saturated to i64 -- for every
-// int32 shift. kt-int's requant (crates/00-kernels/kt-int/src/lib.rs:78-86) computes the same value and casts it to
-// i64 with wrap-around; the two agree wherever the value fits i64 (always for shift > 0 and |acc| < 2^32).
-__device__ __forceinline__ int64_t requant_dev(int64_t acc, int64_t mant, int shift) {
-    typedef unsigned __int128 u128;
-    const __int128 prod = (__int128)acc * (__int128)mant;  // |prod| <= 2^126
-    if (prod == 0) return 0;
-    const bool neg = prod < 0;
-    const u128 a = neg ? (u128)(-prod) : (u128)prod, top = (u128)1 << 63;
-    u128 q;
-    if (shift <= 0) {
-        const int s = shift < -64 ? 64 : -shift;
-        q = (s >= 64 || (a >> (63 - s)) != 0) ? top : a << s;
-    } else if (shift >= 127) {
-        q = 0;  // |prod| < 2^126 <= 2^(shift - 1)
-    } else {
-        q = (a + ((u128)1 << (shift - 1))) >> shift;
-    }
-    if (q >= top) return neg ? INT64_MIN : INT64_MAX;
-    return neg ? -(int64_t)q : (int64_t)q;
-}
-
-template <int OUT>
-__device__ __forceinline__ void store_out(void* y, size_t idx, int64_t v, const int32_t* mant, const int32_t* shift,
-                                          int n) {
-    if constexpr (OUT == KT_OUT_I64) {
-        reinterpret_cast<int64_t*>(y)[idx] = v;
-    } else {
-        int64_t q = requant_dev(v, mant[n], shift[n]);
-        if constexpr (OUT == KT_OUT_I32) {
-            q = q > INT32_MAX ? INT32_MAX : (q < INT32_MIN ? INT32_MIN : q);
-            reinterpret_cast<int32_t*>(y)[idx] = (int32_t)q;
-        } else {
-            q = q > 127 ? 127 : (q < -127 ? -127 : q);
-            reinterpret_cast<int8_t*>(y)[idx] = (int8_t)q;
-        }
-    }
-}
 
 // ------------------------------------------------------------------------------------------------------------------
 // Packing kernels
@@ -153,19 +46,22 @@ __global__ void pack_planes_kernel(const int32_t* __restrict__ codes, int64_t ro
 
 // i32 codes [n][k] in [-2048, 2047] -> fragment-tiled W12 planes (lo np*kp bytes, nib np*kp/2 bytes, np = n rounded
 // up to 32). One thread per fragment lane: 16 lo bytes and 8 nib bytes; padding rows and k get lo = 0, hi = 0.
-__global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, int64_t k, int64_t kp,
+// ilv > 0 interleaves two halves of ilv rows each (a SwiGLU gate/up matrix, n = 2 ilv, ilv a multiple of 32):
+// packed row block 2j holds source rows 32j.. (gate), block 2j+1 source rows ilv + 32j.. (up).
+__global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, int64_t k, int64_t kp, int64_t ilv,
                                 int8_t* __restrict__ lo, uint8_t* __restrict__ nib) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // fragment-lane index
     const int64_t KB = kp / 32, total = (n + 31) / 32 * KB * 64;
     if (idx >= total) return;
     const int64_t frag = idx >> 6, l = idx & 63, nb = frag / KB, kb = frag - nb * KB;
     const int64_t r = nb * 32 + (l & 31), c0 = kb * 32 + 16 * (l >> 5);
+    const int64_t src = ilv > 0 ? (nb & 1) * ilv + (nb >> 1) * 32 + (l & 31) : r;
     uint32_t lw[4] = {0, 0, 0, 0}, nw[2] = {0, 0};
     for (int t = 0; t < 16; t++) {
         const int64_t c = c0 + t;
         uint32_t lb = 0, hb = 0;
         if (r < n && c < k) {
-            const int32_t v = codes[r * k + c];
+            const int32_t v = codes[src * k + c];
             lb = (uint32_t)((v & 255) - 128) & 255;
             hb = ((uint32_t)(v + 2048) >> 8) & 15;
         }
@@ -304,21 +200,10 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// W12 GEMM (BASELINE path, M > 8). x int8 [M][kp] (zero padded); W12 fragment-tiled lo / nib.
-// CTA = 4 waves side by side along N; each wave owns WTM x WTN tiles of 32x32 (all BM = 32*WTM rows of the CTA,
-// its own 32*WTN columns), BK = 64. A goes global -> registers -> a 3-slot LDS ring; each wave's B fragments go
-// straight from global memory into registers. Both are issued two tiles ahead of the tile being multiplied, and
-// the loop is unrolled by three so every register set has a compile-time slot. Loads past the last tile read
-// other rows of the same buffer or zeros (never outside it); issuing them unconditionally lets the compiler wait
-// only for the set it is about to use. Row sums of x (for -1920 * sum_k x) come from the A staging registers.
+// W12 GEMM (M > 128). x int8 [M][kp] (zero padded); W12 fragment-tiled lo / nib; the mainloop of kt_w12_core.h.
 // Tiles are numbered so that the CTAs the hardware places on one XCD (block b -> XCD b % 8) form a compact group
 // of GM tile-rows, sharing A rows and B columns in that XCD's L2.
 // ------------------------------------------------------------------------------------------------------------------
-
-// s_lo + 256 s_hi + corr for a dot known to fit int32: formed modulo 2^32 (256 s_hi alone may not fit).
-__device__ __forceinline__ int w12_value(int s_lo, int s_hi, int corr) {
-    return (int)((uint32_t)s_lo + ((uint32_t)s_hi << 8) + (uint32_t)corr);
-}
 
 // One W12 output from its two plane sums and the row-sum term: v = s_lo + 256 s_hi + corr (corr = -1920 sum x).
 // SMALL: every partial sum and v fit int32 (kp <= 8128: |v| <= 8128 * 2048 * 128 < 2^31), so v is formed in 32 bits
@@ -351,44 +236,6 @@ __device__ __forceinline__ void store_w12(void* y, size_t idx, int s_lo, int s_h
     }
 }
 
-// The per-channel requant of a value |v| < 2^32 as one multiply-add and shift: for int32 mant and any shift,
-// requant(v, mant, shift) = sign * ((|v| * mt + bias) >> shr) with mt <= 2^32 - 1 (kt-int/src/lib.rs:78-86):
-//   shift > 0: mt = |mant|, shr = shift, bias = 2^(shift-1) (shift >= 63 gives 0: |v| * mt < 2^63 - 2^62);
-//   shift <= 0: mt = |mant| << -shift, saturated at 2^32 - 1 -- a saturated mt only arises when any nonzero |v|
-//   already exceeds every clamp bound, and zero stays zero.
-struct ColQ {
-    uint32_t mt, shr;
-    uint64_t bias;
-    bool neg;
-};
-
-__device__ __forceinline__ ColQ col_q(int32_t mant, int32_t sh) {
-    ColQ q;
-    q.neg = mant < 0;
-    const uint64_t am = mant < 0 ? (uint64_t)(-(int64_t)mant) : (uint64_t)mant;
-    if (sh >= 63) {
-        q.mt = 0, q.shr = 0, q.bias = 0;
-    } else if (sh > 0) {
-        q.mt = (uint32_t)am, q.shr = (uint32_t)sh, q.bias = (uint64_t)1 << (sh - 1);
-    } else {
-        const int up = -sh;
-        const uint64_t t = up >= 32 ? (am ? 0xFFFFFFFFull : 0) : am << up;
-        q.mt = (uint32_t)(t > 0xFFFFFFFFull ? 0xFFFFFFFFull : t), q.shr = 0, q.bias = 0;
-    }
-    return q;
-}
-
-// requant(v) clamped to the output: [-127, 127] for int8, [-2^31, 2^31 - 1] for int32.
-template <bool I32>
-__device__ __forceinline__ int32_t col_requant(int v, const ColQ& q) {
-    const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
-    uint64_t m = ((uint64_t)a * q.mt + q.bias) >> q.shr;
-    const bool neg = (v < 0) != q.neg;
-    const uint64_t lim = I32 ? (neg ? 0x80000000ull : 0x7FFFFFFFull) : 127;
-    m = m > lim ? lim : m;
-    return neg ? (int32_t)(0u - (uint32_t)m) : (int32_t)m;
-}
-
 __device__ __forceinline__ void tile_coords(int M, int N, int BM, int BN, int& m0, int& n0) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, nt = tiles_m * tiles_n;
     int bid = blockIdx.x;
@@ -400,21 +247,6 @@ __device__ __forceinline__ void tile_coords(int M, int N, int BM, int BN, int& m
     m0 = (first_m + in_group % gsize) * BM;
     n0 = (in_group / gsize) * BN;
 }
-
-__device__ __forceinline__ v2i bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
-}
-
-__device__ __forceinline__ v4i unpack_hi(v2i d) {
-    const int m4 = 0x0F0F0F0F;
-    return v4i{d.x & m4, (d.x >> 4) & m4, d.y & m4, (d.y >> 4) & m4};
-}
-
-// The longest k for which every W12 dot fits int32: 8128 * 128 * 2048 < 2^31 <= 8192 * 128 * 2048.
-#define KT_SMALL_KP 8128
-
-template <int I>
-using slot_t = std::integral_constant<int, I>;
 
 // Tile shape of the large-M W12 GEMM: waves per SIMD the register allocation targets, 32x32 tiles per wave.
 #ifndef KT_W12_WTM
@@ -433,43 +265,35 @@ using slot_t = std::integral_constant<int, I>;
 #define KT_W12_NSLOT 4
 #endif
 
-// Compile-time loop: f(integral_constant<int, I>) for I = B..E-1.
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
+// An optional int8 -> int8 table (`lut`, 255 entries indexed by q + 127) is applied after the int8 requant: the
+// activation-code epilogue (GELU of config 5). lut is read only for OUT == KT_OUT_I8 and may be null.
 template <int WM, int WTM, int WTN, int WAVES, int NSLOT, int OUT, bool SMALL>
 __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
-    void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift) {
-    constexpr int NT = 256 * WM;  // WM waves along M x 4 waves along N
-    constexpr int BK = 64, CPR = 4;
-    constexpr int BM = 32 * WTM * WM, BN = 128 * WTN;
-    constexpr int AC = BM * CPR, AL = (AC + NT - 1) / NT;  // 16-byte A chunks per tile / per thread
+    void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+    const int8_t* __restrict__ lut) {
+    typedef W12Tile<WM, WTM, WTN, NSLOT> C;
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
     constexpr int SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // the int8 output tile reuses the A ring after the loop
-    __shared__ __attribute__((aligned(16))) int8_t smem[(NSLOT * BM * BK) > SO ? NSLOT * BM * BK : SO];
-    int8_t(*sA)[BM * BK] = reinterpret_cast<int8_t(*)[BM * BK]>(smem);
+    __shared__ __attribute__((aligned(16))) int8_t smem[C::RING > SO ? C::RING : SO];
     __shared__ int sRow[BM];
+    __shared__ int8_t sLut[256];
 
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
-    const int wave = (tid >> 6) & 3, wr = (tid >> 6) >> 2 ;  // wave column (N) and wave row (M)
-    const int rw0 = wr * 32 * WTM;                           // the wave's first row in the tile
+    const int wave = (tid >> 6) & 3, rw0 = ((tid >> 6) >> 2) * 32 * WTM;
     int m0, n0;
     tile_coords(M, N, BM, BN, m0, n0);
     const int KB = kp / 32;
+    if (OUT == KT_OUT_I8 && SMALL && tid < 256) sLut[tid] = lut ? lut[tid < 255 ? tid : 254] : 0;
 
-    // A: the CTA's rows; rows past the matrix read as zero
+    // A: the CTA's rows; rows past the matrix read as zero (their offsets are past the descriptor)
     const uint32_t rows_a = (uint32_t)(M - m0 < BM ? M - m0 : BM);
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(x + (size_t)m0 * kp, rows_a * (uint32_t)kp);
     uint32_t oa[AL];
 #pragma unroll
     for (int i = 0; i < AL; i++) {
         const int idx = tid + NT * i;
-        oa[i] = idx < AC ? (uint32_t)(idx >> 2) * (uint32_t)kp + 16 * (idx & 3) : 0xFFFFFFF0u;
+        oa[i] = idx < AC ? (uint32_t)(idx >> 2) * (uint32_t)kp + 16 * (idx & 3) : KT_OOB;
     }
     // B: the CTA's column blocks (fragment-tiled); blocks past the matrix read as zero
     const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
@@ -483,115 +307,14 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
     }
 
     v16i acc0[WTM][WTN], acc1[WTM][WTN];
-#pragma unroll
-    for (int i = 0; i < WTM; i++)
-#pragma unroll
-        for (int j = 0; j < WTN; j++) acc0[i][j] = acc1[i][j] = v16i{};
     int rsum[AL];
-#pragma unroll
-    for (int i = 0; i < AL; i++) rsum[i] = 0;
-
-    v4i ra[NSLOT][AL];
-    v4i bl[NSLOT][WTN][2];
-    v2i bn[NSLOT][WTN][2];
-
-    auto issue = [&](auto S, int kt) {  // global loads of tile kt into register slot S
-        constexpr int sl = decltype(S)::value;
-#pragma unroll
-        for (int j = 0; j < WTN; j++)
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                bl[sl][j][ks] = bload16(rL, ob[j], (uint32_t)(2 * kt + ks) * 1024u);
-                bn[sl][j][ks] = bload8(rN, on[j], (uint32_t)(2 * kt + ks) * 512u);
-            }
-#pragma unroll
-        for (int i = 0; i < AL; i++) ra[sl][i] = bload16(rA, oa[i], (uint32_t)(kt * BK));
-        // keep the loads at the head of the step: the scheduler would otherwise sink them behind the MFMAs and
-        // shorten the distance they have to land
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // `mask` is -1, or 0 for a tile past the end in the last round: such a tile is staged as zeros (and adds
-    // nothing to the row sums), so its MFMAs add zero instead of being branched around -- no MFMA sits under
-    // control flow, which would cost accumulator copies.
-    auto stage = [&](auto S, int mask) {  // A of slot S into LDS buffer S
-        constexpr int sl = decltype(S)::value;
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            const int idx = tid + NT * i;
-            if (AC % NT != 0 && idx >= AC) continue;
-            const v4i v = ra[sl][i] & mask;
-            lds_write16(sA[sl], lds_off<CPR>(idx >> 2, idx & 3), v);
-            rsum[i] += sum4(v);
-        }
-    };
-    auto compute = [&](auto S) {
-        constexpr int sl = decltype(S)::value;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            v4i a[WTM];
-#pragma unroll
-            for (int i = 0; i < WTM; i++) {
-                a[i] = lds_read16(sA[sl], lds_off<CPR>(rw0 + i * 32 + (lane & 31), 2 * ks + half));
-            }
-#pragma unroll
-            for (int j = 0; j < WTN; j++) {
-                const v4i b0 = bl[sl][j][ks], b1 = unpack_hi(bn[sl][j][ks]);
-#pragma unroll
-                for (int i = 0; i < WTM; i++) {
-                    acc0[i][j] = mfma32(a[i], b0, acc0[i][j]);
-                    acc1[i][j] = mfma32(a[i], b1, acc1[i][j]);
-                }
-            }
-        }
-    };
-
-    // Rounds of NSLOT tiles kt .. kt+NSLOT-1 in slots 0 .. NSLOT-1. Before a round, tile kt is in LDS slot 0 and
-    // tiles kt+1 .. kt+NSLOT-2 are in flight in register slots 1 .. NSLOT-2; step s issues tile kt+s+NSLOT-1 (NSLOT-1
-    // tiles ahead), multiplies tile kt+s and stages tile kt+s+1. Tiles past the end (only in the last round) are
-    // masked to zero. A do-while: the accumulators have one path into the epilogue.
-    const int nk = kp / BK;
-    static_for<0, NSLOT - 1>([&](auto S) { issue(S, decltype(S)::value); });
-    stage(slot_t<0>{}, -1);
-    __syncthreads();
-    int kt = 0;
-    do {
-        static_for<0, NSLOT>([&](auto S) {
-            constexpr int st = decltype(S)::value;
-            issue(slot_t<(st + NSLOT - 1) % NSLOT>{}, kt + st + NSLOT - 1);
-            compute(S);
-            stage(slot_t<(st + 1) % NSLOT>{}, kt + st + 1 < nk ? -1 : 0);
-            __syncthreads();
-        });
-        kt += NSLOT;
-    } while (kt < nk);
-
-    // row sums: the 4 threads of a row are consecutive lanes
-#pragma unroll
-    for (int i = 0; i < AL; i++) {
-        const int idx = tid + NT * i;
-        int v = rsum[i];
-        v += __shfl_xor(v, 1);
-        v += __shfl_xor(v, 2);
-        if (idx < AC && (idx & 3) == 0) sRow[idx >> 2] = v;
-    }
-    __syncthreads();
+    w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
+    w12_row_sums<C>(rsum, sRow);
 
     const bool full = m0 + BM <= M && n0 + BN <= N;
     if constexpr (OUT == KT_OUT_I8 && SMALL) {
         // requantize into an int8 tile in LDS (the A ring is no longer read), then store it with 16-byte writes
-#pragma unroll
-        for (int j = 0; j < WTN; j++) {
-            const int c = wave * 32 * WTN + j * 32 + (lane & 31), n = n0 + c;
-            const ColQ q = col_q(n < N ? mant[n] : 0, n < N ? shift[n] : 1);
-#pragma unroll
-            for (int i = 0; i < WTM; i++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
-                    smem[rt * BN + c] = (int8_t)col_requant<false>(v, q);
-                }
-        }
+        w12_requant_tile8<C>(acc0, acc1, sRow, mant, shift, n0, N, [](int n) { return n; }, smem);
         __syncthreads();
         constexpr int CH = BM * BN / 16;  // 16-byte chunks of the tile
 #pragma unroll
@@ -599,7 +322,12 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
             const int idx = tid + NT * i;
             if (CH % NT != 0 && idx >= CH) break;
             const int rt = idx / (BN / 16), c = (idx % (BN / 16)) * 16, m = m0 + rt, n = n0 + c;
-            const v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
+            v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
+            if (lut) {
+                int8_t* b = reinterpret_cast<int8_t*>(&v);
+#pragma unroll
+                for (int t = 0; t < 16; t++) b[t] = sLut[b[t] + 127];
+            }
             int8_t* dst = reinterpret_cast<int8_t*>(y) + (size_t)m * N + n;
             if (full && (N & 15) == 0) {
                 *reinterpret_cast<v4i*>(dst) = v;
@@ -656,7 +384,8 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
 // N = 4096 gives 256 CTAs. Its NW waves take pairs of k32 blocks round-robin, U pairs in flight per wave. On the
 // 16x16x64 MFMA, lane l = c + 16 g supplies column c (B) / row c (A) for k-group g = (k32 block 2p + g / 2,
 // k-half g % 2): exactly the lanes the half block's bytes arrive in, so no operand moves between lanes. Rows past
-// M read as zero through the x buffer descriptor. The waves meet in LDS in i64; the per-channel scales are fetched
+// M read as zero through the x buffer descriptor (kp is a multiple of 64, so a column block has an even number of
+// k32 blocks and np whole pairs). The waves meet in LDS in i64; the per-channel scales are fetched
 // at the start, so the epilogue waits on no memory.
 // ------------------------------------------------------------------------------------------------------------------
 template <int MT, int NW, int U, int OUT, bool SMALL>
@@ -664,7 +393,8 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
                                                              const int8_t* __restrict__ wlo,
                                                              const uint8_t* __restrict__ wnib, void* __restrict__ y,
                                                              int M, int N, int kp, const int32_t* __restrict__ mant,
-                                                             const int32_t* __restrict__ shift) {
+                                                             const int32_t* __restrict__ shift,
+                                                             const int8_t* __restrict__ lut) {
     constexpr int NT = 64 * NW, OUTS = MT * 256;  // threads; outputs of the CTA (MT row tiles x 16 columns)
     static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
     typedef typename std::conditional<SMALL, int32_t, int64_t>::type part_t;  // SMALL: every dot fits int32
@@ -702,11 +432,13 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
     do {  // batch b: U pairs of k32 blocks per wave, all loads in flight before the first MFMA
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const uint32_t p = (uint32_t)(w + NW * (U * b + u));  // past the end: zeros from the weight buffers
-            L[u] = bload16(rL, oL, p * 2048u);
-            D[u] = bload8(rN, oN, p * 1024u);
+            // a pair past the end re-reads the last pair (its x is masked below): every load stays in the buffers
+            const int p = w + NW * (U * b + u);
+            const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
+            L[u] = bload16(rL, oL, pl * 2048u);
+            D[u] = bload8(rN, oN, pl * 1024u);
 #pragma unroll
-            for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], p * 64u);
+            for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -752,7 +484,10 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
                 const size_t idx = (size_t)m * N + on;
                 if constexpr (OUT == KT_OUT_I64) reinterpret_cast<int64_t*>(y)[idx] = vi;
                 else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
-                else reinterpret_cast<int8_t*>(y)[idx] = (int8_t)col_requant<false>(vi, cq);
+                else {
+                    const int q = col_requant<false>(vi, cq);
+                    reinterpret_cast<int8_t*>(y)[idx] = lut ? lut[q + 127] : (int8_t)q;
+                }
             }
         } else {
             int64_t v = 0, rs = 0;
@@ -794,10 +529,12 @@ hipError_t launch_pack_planes(const int32_t* codes, int64_t rows, int64_t k, int
     return hipGetLastError();
 }
 
-hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int8_t* lo, uint8_t* nib, hipStream_t s) {
+hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t ilv, int8_t* lo, uint8_t* nib,
+                           hipStream_t s) {
     const int64_t kp = ceil_div(k, 64) * 64, total = ceil_div(n, 32) * (kp / 32) * 64;
     if (total == 0) return hipSuccess;
-    w12_pack_kernel<<<dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s>>>(codes, n, k, kp, lo, nib);
+    if (ilv > 0 && (ilv % 32 || n != 2 * ilv)) return hipErrorInvalidValue;
+    w12_pack_kernel<<<dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s>>>(codes, n, k, kp, ilv, lo, nib);
     return hipGetLastError();
 }
 
@@ -828,7 +565,8 @@ hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb,
 
 template <int OUT>
 static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
-                                 const int32_t* mant, const int32_t* shift, void* y, hipStream_t s) {
+                                 const int32_t* mant, const int32_t* shift, const int8_t* lut, void* y, hipStream_t s) {
+    if (lut && (OUT != KT_OUT_I8 || kp > KT_SMALL_KP)) return hipErrorInvalidValue;
     if (M <= KT_W12_SKINNY_MAX_M) {
         const int64_t ctas = 2 * ceil_div(N, 32);
         if (ctas > INT32_MAX || (int64_t)M * kp > (int64_t)UINT32_MAX || kp > KT_W12_SKINNY_MAX_K)
@@ -838,10 +576,10 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     if (M <= 16 * mt) {                                                                                             \
         if (kp <= KT_SMALL_KP)                                                                                      \
             w12_skinny_kernel<mt, nw, u, OUT, true><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, M, N, kp, mant,   \
-                                                                                   shift);                          \
+                                                                                   shift, lut);                     \
         else                                                                                                        \
             w12_skinny_kernel<mt, nw, u, OUT, false><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, M, N, kp, mant,  \
-                                                                                    shift);                         \
+                                                                                    shift, nullptr);                \
         return hipGetLastError();                                                                                   \
     }
         KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2) KT_SKINNY(8, 4, 4)
@@ -850,19 +588,23 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     const bool small = kp <= KT_SMALL_KP;
     constexpr int WM = KT_W12_WM, WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES, NS = KT_W12_NSLOT;
     dim3 grid((unsigned)(ceil_div(N, 128 * WTN) * ceil_div(M, 32 * WTM * WM))), block(256 * WM);
-    if (small) w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
-    else w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, false><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift);
+    if (small)
+        w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift, lut);
+    else
+        w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, false><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift,
+                                                                                 nullptr);
     return hipGetLastError();
 }
 
 hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
-                             const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s) {
+                             const int32_t* mant, const int32_t* shift, const int8_t* lut, int out_kind, void* y,
+                             hipStream_t s) {
     if (M <= 0 || N <= 0) return hipSuccess;
     if (kp <= 0 || (kp % 64) || ceil_div(M, 64) * ceil_div(N, 64) > INT32_MAX) return hipErrorInvalidValue;
     switch (out_kind) {
-        case KT_OUT_I64: return w12_linear_out<KT_OUT_I64>(x, lo, nib, M, N, kp, mant, shift, y, s);
-        case KT_OUT_I32: return w12_linear_out<KT_OUT_I32>(x, lo, nib, M, N, kp, mant, shift, y, s);
-        case KT_OUT_I8: return w12_linear_out<KT_OUT_I8>(x, lo, nib, M, N, kp, mant, shift, y, s);
+        case KT_OUT_I64: return w12_linear_out<KT_OUT_I64>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
+        case KT_OUT_I32: return w12_linear_out<KT_OUT_I32>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
+        case KT_OUT_I8: return w12_linear_out<KT_OUT_I8>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         default: return hipErrorInvalidValue;
     }
 }

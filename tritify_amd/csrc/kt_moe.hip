@@ -1,0 +1,320 @@
+// The MoE layer of BASELINE config 4 on gfx950: routing, bucketing, the ragged grouped W12 GEMM and the weighted
+// combine. The reference runs a MoE layer token by token (MoeMlp::forward_routed / forward_one_int,
+// crates/01-engine/kt-core/src/layers.rs:928-936, 988-1020), each selected expert called with one row; here the
+// tokens are bucketed by expert and every expert's rows run as one ragged group of a single grouped GEMM launch.
+// Integer sums do not depend on the order, so the bytes equal the per-token evaluation.
+//
+//   route   one wave per token: top-k router codes (descending, ties to the lower index, layers.rs:800-805) and
+//           their sigmoid-table weights;
+//   bucket  one CTA per expert: the tokens that chose it, in increasing token order (a block prefix sum, so the
+//           order is deterministic), and each (token, choice)'s row within the group; group E (the shared expert)
+//           lists every token;
+//   grouped GEMM  persistent CTAs walk the (group row tile, column tile) space, A rows gathered through the token
+//           lists (or contiguous per group), each group's own W12 weights and scales, the mainloop of kt_w12_core.h;
+//           epilogues: per-channel int8 requant, or SwiGLU on an interleaved gate/up matrix;
+//   combine one CTA per token: sum_i cw_i d_i + 4096 d_shared, requantized to int8.
+
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <stdint.h>
+
+#include "kt_kernels.h"
+#include "kt_w12_core.h"
+
+namespace kt {
+
+// round_half_away(r / 16) clamped to [-127, 127]: the sigmoid table index of a router code.
+__device__ __forceinline__ int sig_index(int r) {
+    const uint32_t a = r < 0 ? 0u - (uint32_t)r : (uint32_t)r;
+    uint32_t q = (a + 8) >> 4;
+    q = q > 127 ? 127 : q;
+    return r < 0 ? -(int)q : (int)q;
+}
+
+// One wave per token: top_k rounds of a wave-wide max over (code, -index) keys. Up to 16 codes per lane (E <= 1024).
+__global__ __launch_bounds__(256) void moe_route_kernel(const int32_t* __restrict__ logits, int T, int E, int top_k,
+                                                        const int16_t* __restrict__ sig, int32_t* __restrict__ sel,
+                                                        int32_t* __restrict__ cw) {
+    constexpr int MAXV = 16;
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // the whole wave
+    const int32_t* r = logits + (size_t)t * E;
+    uint64_t key[MAXV];
+#pragma unroll
+    for (int q = 0; q < MAXV; q++) {
+        const int e = lane + 64 * q;
+        // the code with its sign bit flipped orders as unsigned; the low word orders lower indices first
+        key[q] = e < E ? ((uint64_t)((uint32_t)r[e] ^ 0x80000000u) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e) : 0;
+    }
+    for (int it = 0; it < top_k; it++) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int q = 0; q < MAXV; q++) best = key[q] > best ? key[q] : best;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            const uint64_t o = __shfl_xor(best, d);
+            best = o > best ? o : best;
+        }
+        const int e = (int)(0xFFFFFFFFu - (uint32_t)best);
+        const int code = (int)((uint32_t)(best >> 32) ^ 0x80000000u);
+        if (lane == (e & 63)) {
+#pragma unroll
+            for (int q = 0; q < MAXV; q++)
+                if (q == (e >> 6)) key[q] = 0;  // taken
+        }
+        if (lane == 0) {
+            sel[(size_t)t * top_k + it] = e;
+            cw[(size_t)t * top_k + it] = sig[sig_index(code) + 127];
+        }
+    }
+}
+
+// One CTA per group g <= E: list[g * T + j] = the j-th token (increasing) that chose g, pos[t * top_k + i] = j for
+// (t, its choice i == g), count[g] = the group size. Group E (the shared expert) is every token.
+__global__ __launch_bounds__(256) void moe_bucket_kernel(const int32_t* __restrict__ sel, int T, int E, int top_k,
+                                                         int32_t* __restrict__ list, int32_t* __restrict__ pos,
+                                                         int32_t* __restrict__ count) {
+    __shared__ int scr[8];
+    const int g = blockIdx.x, tid = threadIdx.x;
+    int32_t* lg = list + (size_t)g * T;
+    if (g == E) {
+        for (int t = tid; t < T; t += 256) lg[t] = t;
+        if (tid == 0) count[E] = T;
+        return;
+    }
+    int base = 0;
+    for (int t0 = 0; t0 < T; t0 += 256) {
+        const int t = t0 + tid;
+        int hit = -1;
+        if (t < T)
+            for (int i = 0; i < top_k; i++)
+                if (sel[(size_t)t * top_k + i] == g) hit = i;
+        int ex, ez, tot, tz;
+        block_scan2<256>(hit >= 0 ? 1 : 0, 0, ex, ez, tot, tz, scr);
+        if (hit >= 0) {
+            lg[base + ex] = t;
+            pos[(size_t)t * top_k + hit] = base + ex;
+        }
+        base += tot;
+    }
+    if (tid == 0) count[g] = base;
+}
+
+// The grouped GEMM's CTA tile: the dense GEMM's 128 x 128 (4 waves along N, 4 x 1 tiles of 32x32 each).
+typedef W12Tile<1, 4, 1, 4> GTile;
+
+// Ragged grouped W12 GEMM. Group g has count[g] rows; its row j is x row list[g * list_stride + j] (list != null) or
+// x row off[g] + j (off = the exclusive prefix of count); its weights are the W12 planes at wlo + g * glo (lo) and
+// wnib + g * glo / 2 (nib), n x k with per-channel scales mant/shift + g * n; its output row j is y row off[g] + j
+// (row stride ystride). EPI_I8: y = the int8 requant of the n columns. EPI_SWIGLU: the weights are a gate/up
+// matrix packed with the 32-row interleave (n = 2F), the scales in natural order (gate 0..F-1, up F..2F-1), and
+// y = clamp(requant(silu[gq + 127] * uq, 1, h_shift)) over F columns. off_out (optional) receives off[0..groups].
+// Persistent: CTA b (XCD b % 8) takes the tiles of its XCD's contiguous share of the tile space, so an XCD's L2
+// serves consecutive column tiles of the same rows and consecutive groups' weights.
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_grouped_kernel(
+    const int8_t* __restrict__ x, uint32_t x_bytes, const int32_t* __restrict__ list, int list_stride,
+    const int32_t* __restrict__ count, int groups, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
+    size_t glo, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+    const int16_t* __restrict__ silu, int h_shift, int8_t* __restrict__ y, int ystride,
+    int32_t* __restrict__ off_out) {
+    typedef GTile C;
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
+    static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
+    __shared__ __attribute__((aligned(16))) int8_t smem[C::RING];
+    __shared__ int sRow[BM];
+    __shared__ int sRpre[KT_MAX_GROUPS + 1], sOff[KT_MAX_GROUPS + 1];
+    __shared__ int scr[8];
+    __shared__ int16_t sSilu[256];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int carry_r = 0, carry_o = 0;
+    for (int g0 = 0; g0 < groups; g0 += NT) {
+        const int g = g0 + tid, c = g < groups ? count[g] : 0;
+        int er, eo, tr, to;
+        block_scan2<NT>((c + BM - 1) / BM, c, er, eo, tr, to, scr);
+        if (g < groups) sRpre[g] = carry_r + er, sOff[g] = carry_o + eo;
+        carry_r += tr, carry_o += to;
+    }
+    if (tid == 0) sRpre[groups] = carry_r, sOff[groups] = carry_o;
+    if (EPI == KT_EPI_SWIGLU) sSilu[tid] = silu[tid < 255 ? tid : 254];
+    __syncthreads();
+    if (off_out && blockIdx.x == 0)
+        for (int g = tid; g <= groups; g += NT) off_out[g] = sOff[g];
+
+    const int KB = kp / 32, tiles_n = (N + BN - 1) / BN, total = sRpre[groups] * tiles_n;
+    const int nx = gridDim.x >> 3, xcd = blockIdx.x & 7, per = (total + 7) >> 3;
+    const int t_end = min(total, (xcd + 1) * per);
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(x, x_bytes);
+    for (int t = xcd * per + (blockIdx.x >> 3); t < t_end; t += nx) {
+        const int rt = t / tiles_n, n0 = (t - rt * tiles_n) * BN;
+        int lo = 0, hi = groups - 1;  // the last group whose first row tile is <= rt (it is not empty)
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (sRpre[mid] <= rt) lo = mid;
+            else hi = mid - 1;
+        }
+        const int g = lo, row0 = (rt - sRpre[g]) * BM, cnt = sOff[g + 1] - sOff[g];
+        const int rows = cnt - row0 < BM ? cnt - row0 : BM;
+
+        uint32_t oa[AL];
+#pragma unroll
+        for (int i = 0; i < AL; i++) {
+            const int idx = tid + NT * i, r = idx >> 2;
+            if (idx < AC && r < rows) {
+                const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
+                oa[i] = (uint32_t)xr * (uint32_t)kp + 16 * (idx & 3);
+            } else {
+                oa[i] = x_bytes;  // out of range whatever the k offset: reads zero
+            }
+        }
+        const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
+        const int8_t* gl = wlo + (size_t)g * glo;
+        const uint8_t* gn = wnib + (size_t)g * (glo / 2);
+        const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+        const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+        uint32_t ob[1] = {(uint32_t)(wave * KB) * 1024 + 16 * lane}, on[1] = {(uint32_t)(wave * KB) * 512 + 8 * lane};
+
+        v16i acc0[4][1], acc1[4][1];
+        int rsum[AL];
+        w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
+        w12_row_sums<C>(rsum, sRow);
+
+        const int32_t* gm = mant + (size_t)g * N;
+        const int32_t* gs = shift + (size_t)g * N;
+        int8_t* yg = y + (size_t)(sOff[g] + row0) * ystride;
+        if constexpr (EPI == KT_EPI_I8) {
+            w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, [](int n) { return n; }, smem);
+            __syncthreads();
+            constexpr int CH = BM * BN / 16;
+            const bool vec = n0 + BN <= N && (ystride & 15) == 0;
+#pragma unroll
+            for (int i = 0; i < CH / NT; i++) {
+                const int idx = tid + NT * i, r = idx / (BN / 16), c = (idx % (BN / 16)) * 16;
+                if (r >= rows) continue;
+                const v4i v = *reinterpret_cast<const v4i*>(smem + r * BN + c);
+                int8_t* dst = yg + (size_t)r * ystride + n0 + c;
+                if (vec) {
+                    *reinterpret_cast<v4i*>(dst) = v;
+                } else {
+                    const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+                    for (int q = 0; q < 16 && n0 + c + q < N; q++) dst[q] = b[q];
+                }
+            }
+        } else {
+            const int F = N / 2;
+            auto chan = [F](int n) {
+                const int blk = n >> 5;
+                return (blk & 1) * F + (blk >> 1) * 32 + (n & 31);
+            };
+            w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, chan, smem);
+            __syncthreads();
+            // the tile's columns are gate/up block pairs: hidden units n0/2 .. n0/2 + units - 1
+            const int units = (N - n0 < BN ? N - n0 : BN) / 2;
+            for (int task = tid; task < BM * (BN / 32); task += NT) {
+                const int r = task / (BN / 32), q = task % (BN / 32);  // row, 16-unit chunk
+                if (r >= rows || 16 * q >= units) continue;
+                v4i out;
+                int8_t* ob8 = reinterpret_cast<int8_t*>(&out);
+#pragma unroll
+                for (int t2 = 0; t2 < 16; t2++) {
+                    const int u = 16 * q + t2, gc = (u >> 5) * 64 + (u & 31);
+                    const int gq = smem[r * BN + gc], uq = smem[r * BN + gc + 32];
+                    ob8[t2] = (int8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
+                }
+                *reinterpret_cast<v4i*>(yg + (size_t)r * ystride + n0 / 2 + 16 * q) = out;
+            }
+        }
+        __syncthreads();  // the next tile's prologue rewrites the ring
+    }
+}
+
+// One CTA per token: y = 4096 d[off[E] + t] + sum_i cw_i d[off[e_i] + pos_i] (int32 is exact: |cw| < 2^15,
+// top_k <= 32), out = clamp(requant(y, 1, out_shift)), 16 columns per thread.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const int8_t* __restrict__ d, const int32_t* __restrict__ off,
+                                                          const int32_t* __restrict__ sel,
+                                                          const int32_t* __restrict__ cw,
+                                                          const int32_t* __restrict__ pos, int H, int E, int top_k,
+                                                          int out_shift, int8_t* __restrict__ out) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int8_t* ds = d + (size_t)(off[E] + t) * H;
+    for (int c = tid; c < H / 16; c += 256) {
+        int y[16];
+        const v4i vs = *reinterpret_cast<const v4i*>(ds + 16 * c);
+        const int8_t* bs = reinterpret_cast<const int8_t*>(&vs);
+#pragma unroll
+        for (int q = 0; q < 16; q++) y[q] = 4096 * bs[q];
+        for (int i = 0; i < top_k; i++) {
+            const int e = sel[(size_t)t * top_k + i], w = cw[(size_t)t * top_k + i];
+            const int8_t* dr = d + (size_t)(off[e] + pos[(size_t)t * top_k + i]) * H;
+            const v4i v = *reinterpret_cast<const v4i*>(dr + 16 * c);
+            const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+#pragma unroll
+            for (int q = 0; q < 16; q++) y[q] += w * b[q];
+        }
+        v4i o;
+        int8_t* ob = reinterpret_cast<int8_t*>(&o);
+#pragma unroll
+        for (int q = 0; q < 16; q++) ob[q] = (int8_t)shift_rq8(y[q], out_shift);
+        *reinterpret_cast<v4i*>(out + (size_t)t * H + 16 * c) = o;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Launchers
+// ------------------------------------------------------------------------------------------------------------------
+
+hipError_t launch_moe_route(const int32_t* logits, int T, int E, int top_k, const int16_t* sig, int32_t* sel,
+                            int32_t* cw, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    if (E < 1 || E > 1024 || top_k < 1 || top_k > E || top_k > 32) return hipErrorInvalidValue;
+    moe_route_kernel<<<dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s>>>(logits, T, E, top_k, sig, sel, cw);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_bucket(const int32_t* sel, int T, int E, int top_k, int32_t* list, int32_t* pos,
+                             int32_t* count, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    if (E < 1 || E + 1 > KT_MAX_GROUPS || top_k < 1 || top_k > E) return hipErrorInvalidValue;
+    moe_bucket_kernel<<<dim3((unsigned)(E + 1)), dim3(256), 0, s>>>(sel, T, E, top_k, list, pos, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* list, int list_stride,
+                              const int32_t* count, int groups, int64_t max_rows, const int8_t* wlo,
+                              const uint8_t* wnib, size_t glo, int N, int kp, const int32_t* mant,
+                              const int32_t* shift, int epi, const int16_t* silu, int h_shift, int8_t* y,
+                              int ystride, int32_t* off_out, hipStream_t s) {
+    if (groups <= 0 || N <= 0) return hipSuccess;
+    if (groups > KT_MAX_GROUPS || kp <= 0 || kp % 64 || kp > KT_SMALL_KP || x_bytes + kp >= 0xFFFFFFF0ull ||
+        max_rows < 0)
+        return hipErrorInvalidValue;
+    if (epi == KT_EPI_SWIGLU && (N % 64 || !silu || h_shift < 1 || h_shift > 30 || ystride % 16))
+        return hipErrorInvalidValue;
+    const int64_t tiles_n = (N + GTile::BN - 1) / GTile::BN;
+    const int64_t ub = ((max_rows + GTile::BM - 1) / GTile::BM + groups) * tiles_n;  // row tiles <= rows/BM + groups
+    if (ub * GTile::BN > INT32_MAX) return hipErrorInvalidValue;
+    const int64_t grid = ub < 512 ? (ub + 7) / 8 * 8 : 512;  // two CTAs per CU, a multiple of 8 (XCDs)
+    if (epi == KT_EPI_I8)
+        w12_grouped_kernel<KT_EPI_I8><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
+            x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu, h_shift,
+            y, ystride, off_out);
+    else if (epi == KT_EPI_SWIGLU)
+        w12_grouped_kernel<KT_EPI_SWIGLU><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
+            x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu, h_shift,
+            y, ystride, off_out);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const int8_t* d, const int32_t* off, const int32_t* sel, const int32_t* cw,
+                              const int32_t* pos, int T, int H, int E, int top_k, int out_shift, int8_t* out,
+                              hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    if (H % 16 || top_k < 1 || top_k > 32 || out_shift < 1 || out_shift > 30) return hipErrorInvalidValue;
+    moe_combine_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(d, off, sel, cw, pos, H, E, top_k, out_shift, out);
+    return hipGetLastError();
+}
+
+}  // namespace kt

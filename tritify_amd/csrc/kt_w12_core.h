@@ -1,0 +1,377 @@
+// Device building blocks shared by the gfx950 kernels: MFMA wrappers, LDS swizzle, raw buffer loads, the exact
+// requant epilogue arithmetic, and the W12 tile mainloop that the dense, grouped (MoE) and im2col GEMMs all run.
+//
+// W12 (int8 activations x 12-bit weight codes in [-2048, 2047]): lo = (v & 255) - 128 (int8) and
+// hi = (v + 2048) >> 8 (4 bits), v = lo + 256*hi - 1920, so sum_k x*v = S_lo + 256*S_hi - 1920*sum_k x.
+// The weights are stored fragment-tiled: blocks of 32 rows x 32 k, each 64 lanes x (16 lo bytes + 8 nib bytes) in
+// exactly the order one MFMA B operand takes them (lane l: row l%32, k = 16*(l/32) .. +16), so a wave fetches a B
+// fragment with one fully coalesced 1 KB load and one 512-byte load, no LDS round trip. A lane's 8 nib bytes as
+// dwords D0, D1 unpack in k order as D0 & 0x0F0F0F0F, (D0 >> 4) & .., D1 & .., (D1 >> 4) & .. . One 32-row column
+// block is kp*32 lo bytes + kp*16 nib bytes, contiguous along k.
+//
+// MFMA: v_mfma_i32_32x32x32_i8 and v_mfma_i32_16x16x64_i8. A lane's 16 operand bytes are 16 consecutive k of one
+// row (A) / one column (B); the hardware pairs A and B bytes with the same k-slot, so any lane->k assignment that is
+// the same for A and B gives the exact dot product. The C layout of the 32x32 MFMA is lane l, register r -> row
+// 8*(r/4) + 4*(l/32) + (r%4), column l%32; of the 16x16 MFMA: row 4*(l/16) + r, col l%16 (the layout test in
+// tests/test_gpu.py checks both).
+//
+// Buffer loads: the hardware range-checks a raw buffer access by its VGPR offset (plus the instruction offset);
+// the SGPR offset is added to the address unchecked. Every load here keeps voffset + soffset inside the buffer, and
+// uses an out-of-range voffset (never soffset) where a row must read as zero.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "kt_hip.h"
+
+namespace kt {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// LDS tiles are rows of BK bytes in 16-byte chunks; chunk c of row r sits at chunk position c ^ swz(r) so that the
+// MFMA operand reads (consecutive lanes = consecutive rows, same chunk) fall in distinct banks. For 64-byte rows
+// swz = (r >> 2) & 3 measured conflict-free on gfx950 (about 195 B/clk per CU for ds_read_b128, against about
+// 120 for (r >> 1) & 3 and 62 without a swizzle).
+template <int CPR>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (CPR == 4) return (r >> 2) & 3;
+    else return (r ^ (r >> 3)) & 7;
+}
+
+template <int CPR>
+__device__ __forceinline__ int lds_off(int r, int c) {
+    return r * (CPR * 16) + ((c ^ swz<CPR>(r)) << 4);
+}
+
+__device__ __forceinline__ v4i lds_read16(const int8_t* base, int off) {
+    return *reinterpret_cast<const v4i*>(base + off);
+}
+__device__ __forceinline__ void lds_write16(int8_t* base, int off, v4i v) {
+    *reinterpret_cast<v4i*>(base + off) = v;
+}
+
+__device__ __forceinline__ v4i gload16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
+
+// A raw buffer over `bytes` bytes at `base`: a load whose VGPR offset is past the end returns zeros, so tile rows
+// beyond the matrix need no branch. The descriptor lives in SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ v2i bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
+// An offset that is out of range for every buffer here (buffers are below 4 GB - 16 B).
+#define KT_OOB 0xFFFFFFF0u
+
+// 8 nib bytes of a lane -> 16 hi digits in natural k order.
+__device__ __forceinline__ v4i unpack_hi(v2i d) {
+    const int m4 = 0x0F0F0F0F;
+    return v4i{d.x & m4, (d.x >> 4) & m4, d.y & m4, (d.y >> 4) & m4};
+}
+
+__device__ __forceinline__ int sum4(v4i v) {
+    const int ones = 0x01010101;
+    int s = __builtin_amdgcn_sdot4(v.x, ones, 0, false);
+    s = __builtin_amdgcn_sdot4(v.y, ones, s, false);
+    s = __builtin_amdgcn_sdot4(v.z, ones, s, false);
+    return __builtin_amdgcn_sdot4(v.w, ones, s, false);
+}
+
+// round(acc * mant / 2^shift), half away from zero, from the exact 128-bit product, saturated to i64 -- for every
+// int32 shift. kt-int's requant (crates/00-kernels/kt-int/src/lib.rs:78-86) computes the same value and casts it to
+// i64 with wrap-around; the two agree wherever the value fits i64 (always for shift > 0 and |acc| < 2^32).
+__device__ __forceinline__ int64_t requant_dev(int64_t acc, int64_t mant, int shift) {
+    typedef unsigned __int128 u128;
+    const __int128 prod = (__int128)acc * (__int128)mant;  // |prod| <= 2^126
+    if (prod == 0) return 0;
+    const bool neg = prod < 0;
+    const u128 a = neg ? (u128)(-prod) : (u128)prod, top = (u128)1 << 63;
+    u128 q;
+    if (shift <= 0) {
+        const int s = shift < -64 ? 64 : -shift;
+        q = (s >= 64 || (a >> (63 - s)) != 0) ? top : a << s;
+    } else if (shift >= 127) {
+        q = 0;  // |prod| < 2^126 <= 2^(shift - 1)
+    } else {
+        q = (a + ((u128)1 << (shift - 1))) >> shift;
+    }
+    if (q >= top) return neg ? INT64_MIN : INT64_MAX;
+    return neg ? -(int64_t)q : (int64_t)q;
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void* y, size_t idx, int64_t v, const int32_t* mant, const int32_t* shift,
+                                          int n) {
+    if constexpr (OUT == KT_OUT_I64) {
+        reinterpret_cast<int64_t*>(y)[idx] = v;
+    } else {
+        int64_t q = requant_dev(v, mant[n], shift[n]);
+        if constexpr (OUT == KT_OUT_I32) {
+            q = q > INT32_MAX ? INT32_MAX : (q < INT32_MIN ? INT32_MIN : q);
+            reinterpret_cast<int32_t*>(y)[idx] = (int32_t)q;
+        } else {
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            reinterpret_cast<int8_t*>(y)[idx] = (int8_t)q;
+        }
+    }
+}
+
+// s_lo + 256 s_hi + corr for a dot known to fit int32: formed modulo 2^32 (256 s_hi alone may not fit).
+__device__ __forceinline__ int w12_value(int s_lo, int s_hi, int corr) {
+    return (int)((uint32_t)s_lo + ((uint32_t)s_hi << 8) + (uint32_t)corr);
+}
+
+// The per-channel requant of a value |v| < 2^32 as one multiply-add and shift: for int32 mant and any shift,
+// requant(v, mant, shift) = sign * ((|v| * mt + bias) >> shr) with mt <= 2^32 - 1 (kt-int/src/lib.rs:78-86):
+//   shift > 0: mt = |mant|, shr = shift, bias = 2^(shift-1) (shift >= 63 gives 0: |v| * mt < 2^63 - 2^62);
+//   shift <= 0: mt = |mant| << -shift, saturated at 2^32 - 1 -- a saturated mt only arises when any nonzero |v|
+//   already exceeds every clamp bound, and zero stays zero.
+struct ColQ {
+    uint32_t mt, shr;
+    uint64_t bias;
+    bool neg;
+};
+
+__device__ __forceinline__ ColQ col_q(int32_t mant, int32_t sh) {
+    ColQ q;
+    q.neg = mant < 0;
+    const uint64_t am = mant < 0 ? (uint64_t)(-(int64_t)mant) : (uint64_t)mant;
+    if (sh >= 63) {
+        q.mt = 0, q.shr = 0, q.bias = 0;
+    } else if (sh > 0) {
+        q.mt = (uint32_t)am, q.shr = (uint32_t)sh, q.bias = (uint64_t)1 << (sh - 1);
+    } else {
+        const int up = -sh;
+        const uint64_t t = up >= 32 ? (am ? 0xFFFFFFFFull : 0) : am << up;
+        q.mt = (uint32_t)(t > 0xFFFFFFFFull ? 0xFFFFFFFFull : t), q.shr = 0, q.bias = 0;
+    }
+    return q;
+}
+
+// requant(v) clamped to the output: [-127, 127] for int8, [-2^31, 2^31 - 1] for int32.
+template <bool I32>
+__device__ __forceinline__ int32_t col_requant(int v, const ColQ& q) {
+    const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+    uint64_t m = ((uint64_t)a * q.mt + q.bias) >> q.shr;
+    const bool neg = (v < 0) != q.neg;
+    const uint64_t lim = I32 ? (neg ? 0x80000000ull : 0x7FFFFFFFull) : 127;
+    m = m > lim ? lim : m;
+    return neg ? (int32_t)(0u - (uint32_t)m) : (int32_t)m;
+}
+
+// clamp(requant(v, 1, sh), -127, 127) for 1 <= sh <= 30 and |v| < 2^31: round half away from zero.
+__device__ __forceinline__ int32_t shift_rq8(int v, int sh) {
+    const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+    uint32_t m = (uint32_t)(((uint64_t)a + (1u << (sh - 1))) >> sh);
+    m = m > 127 ? 127 : m;
+    return v < 0 ? -(int32_t)m : (int32_t)m;
+}
+
+// The longest k for which every W12 dot fits int32: 8128 * 128 * 2048 < 2^31 <= 8192 * 128 * 2048.
+#define KT_SMALL_KP 8128
+
+template <int I>
+using slot_t = std::integral_constant<int, I>;
+
+// Compile-time loop: f(integral_constant<int, I>) for I = B..E-1.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// The W12 tile mainloop. CTA = WM x 4 waves (WM along M, 4 along N); each wave owns WTM x WTN tiles of 32x32 (its
+// wave row's 32*WTM rows, its own 32*WTN columns), BK = 64. A goes global -> registers -> an NSLOT-slot LDS ring;
+// each wave's B fragments go straight from global memory into registers. Both are issued NSLOT-1 tiles ahead of the
+// tile being multiplied, and the loop is unrolled by NSLOT so every register set has a compile-time slot. Loads of
+// tiles past the end re-read the last tile (staying inside the buffers) and are masked to zero when staged, so their
+// MFMAs add zero instead of being branched around -- no MFMA sits under control flow, which would cost accumulator
+// copies. Row sums of x (for -1920 * sum_k x) come from the A staging registers.
+// ------------------------------------------------------------------------------------------------------------------
+template <int WM_, int WTM_, int WTN_, int NSLOT_>
+struct W12Tile {
+    static constexpr int WM = WM_, WTM = WTM_, WTN = WTN_, NSLOT = NSLOT_;
+    static constexpr int NT = 256 * WM;  // threads
+    static constexpr int BK = 64, CPR = 4;
+    static constexpr int BM = 32 * WTM * WM, BN = 128 * WTN;
+    static constexpr int AC = BM * CPR, AL = (AC + NT - 1) / NT;  // 16-byte A chunks per k-tile / per thread
+    static constexpr int RING = NSLOT * BM * BK;                   // bytes of the A ring
+};
+
+// A chunk idx = tid + NT * i of a k-tile is tile row idx >> 2, 16-byte column idx & 3; oa[i] is its byte offset in
+// rA at k = 0 (KT_OOB for a row that must read as zero or a chunk index past the tile). B column block j of the
+// wave starts at ob[j] in rL (1 KB per k32 block) and on[j] in rN (512 B per k32 block). nk = kp / 64 >= 1.
+template <class C>
+__device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, const uint32_t (&oa)[C::AL],
+                                             const __amdgpu_buffer_rsrc_t rL, const __amdgpu_buffer_rsrc_t rN,
+                                             const uint32_t (&ob)[C::WTN], const uint32_t (&on)[C::WTN], int nk,
+                                             int8_t* smem, v16i (&acc0)[C::WTM][C::WTN],
+                                             v16i (&acc1)[C::WTM][C::WTN], int (&rsum)[C::AL]) {
+    constexpr int NT = C::NT, NSLOT = C::NSLOT, AL = C::AL, AC = C::AC, WTM = C::WTM, WTN = C::WTN;
+    constexpr int CPR = C::CPR, BM = C::BM, BK = C::BK;
+    int8_t(*sA)[BM * BK] = reinterpret_cast<int8_t(*)[BM * BK]>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int rw0 = ((tid >> 6) >> 2) * 32 * WTM;  // the wave's first row in the tile
+
+#pragma unroll
+    for (int i = 0; i < WTM; i++)
+#pragma unroll
+        for (int j = 0; j < WTN; j++) acc0[i][j] = acc1[i][j] = v16i{};
+#pragma unroll
+    for (int i = 0; i < AL; i++) rsum[i] = 0;
+
+    v4i ra[NSLOT][AL];
+    v4i bl[NSLOT][WTN][2];
+    v2i bn[NSLOT][WTN][2];
+
+    auto issue = [&](auto S, int kt) {  // global loads of tile kt (clamped to the last tile) into register slot S
+        constexpr int sl = decltype(S)::value;
+        const uint32_t kl = (uint32_t)(kt < nk ? kt : nk - 1);
+#pragma unroll
+        for (int j = 0; j < WTN; j++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                bl[sl][j][ks] = bload16(rL, ob[j], (2 * kl + ks) * 1024u);
+                bn[sl][j][ks] = bload8(rN, on[j], (2 * kl + ks) * 512u);
+            }
+#pragma unroll
+        for (int i = 0; i < AL; i++) ra[sl][i] = bload16(rA, oa[i], kl * BK);
+        // keep the loads at the head of the step: the scheduler would otherwise sink them behind the MFMAs and
+        // shorten the distance they have to land
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // `mask` is -1, or 0 for a tile past the end in the last round: such a tile is staged as zeros (and adds
+    // nothing to the row sums)
+    auto stage = [&](auto S, int mask) {  // A of slot S into LDS buffer S
+        constexpr int sl = decltype(S)::value;
+#pragma unroll
+        for (int i = 0; i < AL; i++) {
+            const int idx = tid + NT * i;
+            if (AC % NT != 0 && idx >= AC) continue;
+            const v4i v = ra[sl][i] & mask;
+            lds_write16(sA[sl], lds_off<CPR>(idx >> 2, idx & 3), v);
+            rsum[i] += sum4(v);
+        }
+    };
+    auto compute = [&](auto S) {
+        constexpr int sl = decltype(S)::value;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            v4i a[WTM];
+#pragma unroll
+            for (int i = 0; i < WTM; i++) a[i] = lds_read16(sA[sl], lds_off<CPR>(rw0 + i * 32 + (lane & 31), 2 * ks + half));
+#pragma unroll
+            for (int j = 0; j < WTN; j++) {
+                const v4i b0 = bl[sl][j][ks], b1 = unpack_hi(bn[sl][j][ks]);
+#pragma unroll
+                for (int i = 0; i < WTM; i++) {
+                    acc0[i][j] = mfma32(a[i], b0, acc0[i][j]);
+                    acc1[i][j] = mfma32(a[i], b1, acc1[i][j]);
+                }
+            }
+        }
+    };
+
+    // Rounds of NSLOT tiles kt .. kt+NSLOT-1 in slots 0 .. NSLOT-1. Before a round, tile kt is in LDS slot 0 and
+    // tiles kt+1 .. kt+NSLOT-2 are in flight in register slots 1 .. NSLOT-2; step s issues tile kt+s+NSLOT-1 (NSLOT-1
+    // tiles ahead), multiplies tile kt+s and stages tile kt+s+1. A do-while: the accumulators have one path out.
+    static_for<0, NSLOT - 1>([&](auto S) { issue(S, decltype(S)::value); });
+    stage(slot_t<0>{}, -1);
+    __syncthreads();
+    int kt = 0;
+    do {
+        static_for<0, NSLOT>([&](auto S) {
+            constexpr int st = decltype(S)::value;
+            issue(slot_t<(st + NSLOT - 1) % NSLOT>{}, kt + st + NSLOT - 1);
+            compute(S);
+            stage(slot_t<(st + 1) % NSLOT>{}, kt + st + 1 < nk ? -1 : 0);
+            __syncthreads();
+        });
+        kt += NSLOT;
+    } while (kt < nk);
+}
+
+// The CTA's row sums of x into sRow[BM] (the 4 threads of a row are consecutive lanes). Ends with a barrier.
+template <class C>
+__device__ __forceinline__ void w12_row_sums(const int (&rsum)[C::AL], int* sRow) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < C::AL; i++) {
+        const int idx = tid + C::NT * i;
+        int v = rsum[i];
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        if (idx < C::AC && (idx & 3) == 0) sRow[idx >> 2] = v;
+    }
+    __syncthreads();
+}
+
+// Requantize the CTA tile (SMALL domain: every dot fits int32) per output channel into an int8 tile sO[BM][BN] in
+// LDS. Channel n of the tile's column c is n0 + c; chan(n) maps it to the index of its (mant, shift) pair, and
+// columns at or past N get a zero scale.
+template <class C, class ChanFn>
+__device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::WTN],
+                                                  const v16i (&acc1)[C::WTM][C::WTN], const int* sRow,
+                                                  const int32_t* mant, const int32_t* shift, int n0, int N,
+                                                  ChanFn chan, int8_t* sO) {
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int wave = (tid >> 6) & 3, rw0 = ((tid >> 6) >> 2) * 32 * C::WTM;
+#pragma unroll
+    for (int j = 0; j < C::WTN; j++) {
+        const int c = wave * 32 * C::WTN + j * 32 + (lane & 31), n = n0 + c;
+        const int ch = n < N ? chan(n) : 0;
+        const ColQ q = col_q(n < N ? mant[ch] : 0, n < N ? shift[ch] : 1);
+#pragma unroll
+        for (int i = 0; i < C::WTM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
+                sO[rt * C::BN + c] = (int8_t)col_requant<false>(v, q);
+            }
+    }
+}
+
+// Block-wide exclusive prefix sums of two ints per thread (blockDim.x = NT, a multiple of 64); `tot` receives the
+// totals. Uses 2 * (NT / 64) ints of LDS at `scr` and ends with a barrier.
+template <int NT>
+__device__ __forceinline__ void block_scan2(int a, int b, int& ea, int& eb, int& ta, int& tb, int* scr) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int ia = a, ib = b;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int xa = __shfl_up(ia, d), xb = __shfl_up(ib, d);
+        if (lane >= d) ia += xa, ib += xb;
+    }
+    if (lane == 63) scr[2 * w] = ia, scr[2 * w + 1] = ib;
+    __syncthreads();
+    int pa = 0, pb = 0;
+    ta = 0, tb = 0;
+#pragma unroll
+    for (int q = 0; q < NT / 64; q++) {
+        if (q < w) pa += scr[2 * q], pb += scr[2 * q + 1];
+        ta += scr[2 * q], tb += scr[2 * q + 1];
+    }
+    ea = pa + ia - a, eb = pb + ib - b;
+    __syncthreads();
+}
+
+}  // namespace kt

@@ -141,3 +141,50 @@ def pad_k(x: np.ndarray, m: int, k: int) -> np.ndarray:
     out = np.zeros((m, kp), dtype=np.int8)
     out[:, :k] = x.reshape(m, k)
     return out
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Config 4: one MoE layer, GLM-4.5-Air shape (this build's integer definition; include/kt_hip.h states the rule)
+
+MOE_FULL = dict(T=4096, H=4096, F=1408, E=128, top_k=8)
+MOE_SEEDS = dict(x_seed=41, r_seed=42, w_seed=4000)
+MOE_CONST = dict(sigma_x=40, sigma_r=1024, sigma_h=16, h_shift=8, out_shift=13)
+
+
+def _round_half_away(v: float) -> int:
+    return int(math.floor(abs(v) + 0.5)) * (1 if v >= 0 else -1)
+
+
+def silu_table() -> np.ndarray:
+    """255 int16 SiLU codes: t[i] = round(256 * v * sigmoid(v)), v = (i - 127) / 32 (int8 code q <-> q / 32), the
+    integer-code SiLU of SwiGluMlp (crates/01-engine/kt-core/src/layers.rs:599) on this build's int8 grid."""
+    return np.array([_round_half_away(256.0 * ((i - 127) / 32.0) / (1.0 + math.exp(-(i - 127) / 32.0)))
+                     for i in range(255)], dtype=np.int16)
+
+
+def sigmoid_table() -> np.ndarray:
+    """255 int16 router weight codes: t[i] = round(4096 * sigmoid((i - 127) / 64)); a router code r (N(0,1) in units
+    of 1/1024) reads entry clamp(round(r / 16), -127, 127) + 127 (GLM-4.5's sigmoid score, router.rs:29-79)."""
+    return np.array([_round_half_away(4096.0 / (1.0 + math.exp(-(i - 127) / 64.0))) for i in range(255)],
+                    dtype=np.int16)
+
+
+def moe_inputs(T: int, H: int, E: int, x_seed: int, r_seed: int, sigma_x: int = 40, sigma_r: int = 1024):
+    """x (T x H int8 as int32, round(N(0, sigma_x)) clipped to +-127) and router codes (T x E int32, round(N(0,
+    sigma_r)) unclipped)."""
+    from . import backend as B
+
+    return B.gen_gauss_fast(x_seed, sigma_x, T * H, clip=127), B.gen_gauss_fast(r_seed, sigma_r, T * E)
+
+
+def moe_expert(g: int, H: int, F: int, w_seed: int, sigma_x: int = 40, sigma_h: int = 16):
+    """Expert g's codes and scales: gate/up (2F x H, gate rows first) from seed w_seed + 2g, down (H x F) from
+    w_seed + 2g + 1; per-channel scales map 4 standard deviations of the accumulator to 127 (sigma_x for gate/up,
+    sigma_h for down)."""
+    from . import backend as B
+
+    gu = B.gen_w12_fast(w_seed + 2 * g, 2 * F * H)
+    dn = B.gen_w12_fast(w_seed + 2 * g + 1, H * F)
+    gm, gs = B.channel_scales_fast(gu, 2 * F, H, sigma_x)
+    dm, ds = B.channel_scales_fast(dn, H, F, sigma_h)
+    return gu, dn, gm, gs, dm, ds
