@@ -1,21 +1,27 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X exact-integer GEMM on BASELINE config 2 (the 12-bit GEMM sweep).
+"""Benchmark of the MI355X exact-integer GEMM backend on the BASELINE workloads, one GPU.
 
-A step is one exact 12-bit GEMM at the headline shape M = 2048, N = K = 4096: int8 activations (round(N(0,40))
+Headline (`value`): config 2, the exact 12-bit GEMM at M = 2048, N = K = 4096 -- int8 activations (round(N(0,40))
 clipped to +-127) against 12-bit weight codes (packed W12, 1.5 bytes per weight), int32 accumulation per digit plane,
-exact recombination in i64, then the per-channel integer requant (int32 multiplier + shift) to int8 outputs. Inputs
-are resident in HBM before the timed region; the weights rotate over 12 copies (> 256 MB) so no launch finds them in
-the Infinity Cache. The result of every configuration is checked byte for byte against the fixture hashes the CPU
-oracle produced (tests/golden/goldens.json) before anything is timed.
+exact recombination, then the per-channel integer requant (int32 multiplier + shift) to int8 outputs. A step is one
+launch. Inputs are resident in HBM before the timed region; the weights rotate over 12 copies (> 256 MB) so no
+launch finds them in the Infinity Cache. Every configuration's result is checked byte for byte against the fixture
+hashes the CPU oracle produced (tests/golden/goldens.json) before anything is timed.
+
+Also measured, each under "configs" (skip with --configs):
+  4  one MoE layer, GLM-4.5-Air shape (4096 tokens, H 4096, 128 experts top-8 + 1 shared, F 1408): route, bucket,
+     the ragged grouped W12 GEMMs (gate/up with the SwiGLU epilogue, down), combine; per-stage times.
+  5  SAM 2.1 Hiera-B+ encoder GEMMs: the 1024 x 1024 x 3 patch embed as an im2col-fused W12 GEMM (M 65,536, K 147,
+     N 112) and the stage-3 MLP (4096 tokens, 448 -> 1792 with the GELU table -> 448).
 
 Prints one JSON line on stdout (progress goes to stderr):
   value      logical effective TOPS = 2*M*N*K / time per step (one launch per step)
   roofline   the dominant kernel (w12_gemm at M = 2048) against the dense int8 MFMA peak (5.0 POPS)
-  sweep      M in {1, 16, 128, 2048}: per-launch time, effective TOPS, algorithmic GB/s and both roofline fractions
+  sweep      config 2, M in {1, 16, 128, 2048}: per-launch time, effective TOPS, algorithmic GB/s, roofline fractions
   cpu_baseline  the reference's multithreaded CPU integer path (the oracle's restatement of linear_cpu, AVX-512
              variant when the host has it) on the same M = 2048 workload, timed on this host's cores
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,4]
 """
 from __future__ import annotations
 
@@ -44,6 +50,10 @@ def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
 
+def gold() -> dict:
+    return json.load(open(os.path.join(ROOT, "tests", "golden", "goldens.json")))
+
+
 def time_launches(torch, launch, n: int, warmup: int):
     """Time n back-to-back launches between two HIP events recorded on the launching stream (the stream the kernel
     runs on). Returns the mean launch duration (ms) and the host wall time of the n launches (s)."""
@@ -62,13 +72,17 @@ def time_launches(torch, launch, n: int, warmup: int):
     return start.elapsed_time(end) / n, wall
 
 
+def cpu_threads() -> int:
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    return max(1, min(cores, os.cpu_count() or 1))
+
+
 def cpu_baseline(x32: np.ndarray, w32: np.ndarray, m: int, n: int, k: int) -> dict:
     """The reference's CPU path (crates/01-engine/kt-core/src/backend.rs:133-140 on the auto dot variant,
     kt-runtime/src/lib.rs:93-96), timed as cuda_bench does (one untimed call, then >= 2 calls and >= 5 s)."""
     from oracle import oracle as O
 
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    cores = max(1, min(cores, os.cpu_count() or 1))
+    cores = cpu_threads()
     O.set_max_threads(cores)
     variant = O.lib().kt_cpu_auto_variant()
     O.linear_cpu(x32, w32, m, n, k, variant)
@@ -88,13 +102,282 @@ def cpu_baseline(x32: np.ndarray, w32: np.ndarray, m: int, n: int, k: int) -> di
     }
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# config 2: the 12-bit GEMM sweep
+
+
+def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
+    import tritify_amd as T
+    from tritify_amd import workloads as W
+
+    g2 = gold()["config2"]
+    N, K, sigma = g2["N"], g2["K"], g2["sigma"]
+    Ms = g2["Ms"]
+    MH = max(Ms)
+    if args.ms:
+        Ms = [int(v) for v in args.ms.split(",")]
+        assert all(str(m) in g2["outputs"] for m in Ms), "--ms takes values of the config-2 sweep"
+    dev = torch.device("cuda:0")
+
+    log("bench: generating config-2 inputs")
+    w = W.gen_w12(g2["w_seed"], N * K)
+    x = W.gen_act_gauss(g2["x_seed"], sigma, MH * K)
+    mant, shift = W.channel_scales(w, N, K, sigma)
+    assert sha(w) == g2["w_sha256"] and sha(x) == g2["x_sha256"], "synthetic inputs differ from the fixtures"
+    assert sha(mant) == g2["mant_sha256"] and sha(shift) == g2["shift_sha256"]
+
+    nlo, nnib = T.w12_bytes(N, K)
+    lo0 = torch.empty(nlo, dtype=torch.int8, device=dev)
+    nib0 = torch.empty(nnib, dtype=torch.uint8, device=dev)
+    T.w12_upload(w, N, K, lo0, nib0)
+    los = [lo0] + [lo0.clone() for _ in range(ROTATE - 1)]
+    nibs = [nib0] + [nib0.clone() for _ in range(ROTATE - 1)]
+    xd = torch.from_numpy(W.pad_k(x, MH, K)).to(dev)
+    md, sd = torch.from_numpy(mant).to(dev), torch.from_numpy(shift).to(dev)
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+
+    sweep = {}
+    headline = None
+    for m in Ms:
+        want = g2["outputs"][str(m)]
+        y8 = torch.empty(m * N, dtype=torch.int8, device=dev)
+        acc = torch.empty(m * N, dtype=torch.int64, device=dev)
+        T.w12_linear(xd, lo0, nib0, m, N, K, acc, T.OUT_I64, stream=stream)
+        T.w12_linear(xd, lo0, nib0, m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+        torch.cuda.synchronize()
+        exact = sha(acc.cpu().numpy()) == want["acc_i64_sha256"] and sha(y8.cpu().numpy()) == want["out_i8_sha256"]
+        if not exact:
+            raise SystemExit(f"bench: config 2 M={m}: the GPU result differs from the CPU fixture")
+
+        def launch(i, m=m, y8=y8):
+            j = i % ROTATE
+            T.w12_linear(xd, los[j], nibs[j], m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+
+        n_launch = args.steps if m == MH else max(args.steps, 200)
+        warm = args.warmup if m == MH else max(args.warmup, 20)
+        log(f"bench: config 2 M={m}: bit-exact vs the CPU fixture; timing {n_launch} launches")
+        ms, wall = time_launches(torch, launch, n_launch, warm)
+        us = ms * 1e3
+        ops = 2.0 * m * N * K
+        bytes_alg = 1.5 * N * K + m * K + m * N * 1  # packed weights + int8 activations + int8 outputs
+        tops = ops / (us * 1e-6) / 1e12
+        gbs = bytes_alg / (us * 1e-6) / 1e9
+        sweep[str(m)] = {
+            "us_per_launch": round(us, 3),
+            "effective_tops": round(tops, 2),
+            "executed_int8_tops": round(2 * tops, 2),
+            "mfma_frac_logical": round(tops / INT8_PEAK_TOPS, 4),
+            "alg_gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bit_exact": True,
+            "kernel": "w12_skinny" if m <= 128 else "w12_gemm",
+        }
+        if m == MH:
+            headline = (ms, wall, n_launch, warm, us, tops)
+    del los, nibs
+    return sweep, headline, x, w
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# config 4: one MoE layer
+
+
+def bench_config4(torch, args) -> dict:
+    import tritify_amd as T
+    from tritify_amd import workloads as W
+    from tritify_amd.moe import MoeLayer
+
+    g4 = gold()["config4"]
+    Tk, H, F, E, K = g4["T"], g4["H"], g4["F"], g4["E"], g4["top_k"]
+    log(f"bench: config 4: generating and packing {E} + 1 experts (H={H}, F={F})")
+    t0 = time.perf_counter()
+    x, r = W.moe_inputs(Tk, H, E, g4["x_seed"], g4["r_seed"], g4["sigma_x"], g4["sigma_r"])
+    assert sha(x) == g4["x_sha256"] and sha(r) == g4["logits_sha256"]
+    layer = MoeLayer(H, F, E, K, W.silu_table(), W.sigmoid_table(), g4["h_shift"], g4["out_shift"])
+    for g in range(E + 1):
+        layer.set_expert(g, *W.moe_expert(g, H, F, g4["w_seed"], g4["sigma_x"], g4["sigma_h"]))
+    log(f"bench: config 4: weights resident in {time.perf_counter() - t0:.1f}s")
+    xd = torch.from_numpy(x.astype(np.int8)).cuda()
+    rd = torch.from_numpy(r).cuda()
+    out = torch.empty(Tk * H, dtype=torch.int8, device="cuda")
+    v = layer.forward(xd, rd, Tk, out)
+    torch.cuda.synchronize()
+    if sha(out.cpu().numpy()) != g4["out_sha256"] or sha(v["d"].cpu().numpy()[: Tk * (K + 1) * H]) != g4["d_sha256"]:
+        raise SystemExit("bench: config 4: the GPU result differs from the CPU fixture")
+    log("bench: config 4: bit-exact vs the CPU fixture; timing")
+
+    stream = torch.cuda.current_stream()
+    steps = max(5, args.steps // 10)
+    ms_layer, _ = time_launches(torch, lambda i: layer.forward(xd, rd, Tk, out, stream=stream), steps, 2)
+    # per stage: events between the stage launches of one pass
+    P = Tk * (K + 1)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    stage_ms = np.zeros(4)
+    for _ in range(steps):
+        ev[0].record(stream)
+        layer.route(rd, Tk, v["sel"], v["cw"], stream=stream)
+        layer.bucket(v["sel"], Tk, v["list"], v["pos"], v["count"], stream=stream)
+        ev[1].record(stream)
+        T.w12_grouped_linear(xd, Tk, v["list"], Tk, v["count"], E + 1, P, layer.gu_lo, layer.gu_nib, 2 * F, H,
+                             layer.gu_mant, layer.gu_shift, T.EPI_SWIGLU, v["h"], F, silu_dev=layer.silu,
+                             h_shift=layer.h_shift, off_dev=v["off"], stream=stream)
+        ev[2].record(stream)
+        T.w12_grouped_linear(v["h"], P, None, 0, v["count"], E + 1, P, layer.d_lo, layer.d_nib, H, F, layer.d_mant,
+                             layer.d_shift, T.EPI_I8, v["d"], H, stream=stream)
+        ev[3].record(stream)
+        layer.combine(v["d"], v["off"], v["sel"], v["cw"], v["pos"], Tk, out, stream=stream)
+        ev[4].record(stream)
+        torch.cuda.synchronize()
+        stage_ms += [ev[i].elapsed_time(ev[i + 1]) for i in range(4)]
+    stage_ms /= steps
+    if sha(out.cpu().numpy()) != g4["out_sha256"]:
+        raise SystemExit("bench: config 4: the staged run differs from the CPU fixture")
+    ops_gu, ops_dn = 2.0 * P * 2 * F * H, 2.0 * P * H * F
+    w_gu, w_dn = 1.5 * (E + 1) * 2 * F * H, 1.5 * (E + 1) * H * F
+
+    def kern(ms, ops, wbytes, xbytes, ybytes):
+        s = ms * 1e-3
+        return {"us": round(ms * 1e3, 1), "effective_tops": round(ops / s / 1e12, 1),
+                "mfma_frac_logical": round(ops / s / 1e12 / INT8_PEAK_TOPS, 4),
+                "alg_gbs": round((wbytes + xbytes + ybytes) / s / 1e9, 1),
+                "hbm_frac": round((wbytes + xbytes + ybytes) / s / 1e9 / HBM_PEAK_GBS, 4)}
+
+    res = {
+        "workload": f"config 4: MoE layer, {Tk} tokens, H={H}, {E} experts top-{K} + 1 shared, F={F}, int8 "
+                    f"activations, W12 weights ({(w_gu + w_dn) / 1e9:.2f} GB)",
+        "bit_exact": True,
+        "layer_us": round(ms_layer * 1e3, 1),
+        "layer_effective_tops": round((ops_gu + ops_dn) / (ms_layer * 1e-3) / 1e12, 1),
+        "tokens_per_s": round(Tk / (ms_layer * 1e-3), 0),
+        "stages_us": {"route+bucket": round(stage_ms[0] * 1e3, 1), "gate_up_swiglu": round(stage_ms[1] * 1e3, 1),
+                      "down": round(stage_ms[2] * 1e3, 1), "combine": round(stage_ms[3] * 1e3, 1)},
+        "w12_grouped_gate_up": kern(stage_ms[1], ops_gu, w_gu, P * H, P * F),
+        "w12_grouped_down": kern(stage_ms[2], ops_dn, w_dn, P * F, P * H),
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_moe(g4, x, r)
+    return res
+
+
+def bench_config5(torch, args) -> dict:
+    import tritify_amd as T
+    from tritify_amd import workloads as W
+
+    g5 = gold()["config5"]
+    C, H, Wd, CO, KH, KW, S, P = (g5[k] for k in ("C", "H", "W", "CO", "KH", "KW", "S", "P"))
+    log("bench: config 5: generating the image, patch-embed and stage-3 MLP weights")
+    img, w, b, mant, shift = W.sam_patch_inputs(C, H, Wd, CO, KH, KW, g5["img_seed"], g5["pe_seed"],
+                                                g5["bias_seed"], g5["sigma_q"], g5["bias_sigma"])
+    lut = W.sam_entry_table(g5["entry_scale"])
+    assert sha(img) == g5["img_sha256"] and sha(lut) == g5["entry_sha256"]
+    k = C * KH * KW
+    lo_b, nib_b = T.w12_bytes(CO, k)
+    lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
+    nib = torch.empty(nib_b, dtype=torch.uint8, device="cuda")
+    T.w12_upload(w, CO, k, lo, nib)
+    OH, OW = (H + 2 * P - KH) // S + 1, (Wd + 2 * P - KW) // S + 1
+    out = torch.empty(CO * OH * OW, dtype=torch.int8, device="cuda")
+    imgd, lutd = torch.from_numpy(img).cuda(), torch.from_numpy(lut).cuda()
+    bd, md, sd = (torch.from_numpy(a).cuda() for a in (b, mant, shift))
+    stream = torch.cuda.current_stream()
+
+    def patch(i):
+        T.sam_patch_embed(imgd, lutd, C, H, Wd, lo, nib, CO, KH, KW, S, P, bd, md, sd, out, stream=stream)
+
+    patch(0)
+    torch.cuda.synchronize()
+    if sha(out.cpu().numpy()) != g5["patch_sha256"]:
+        raise SystemExit("bench: config 5: the patch embed differs from the CPU fixture")
+
+    Tk, D, Dh = g5["tokens"], g5["dim"], g5["hidden"]
+    x, wi, wo, im, is_, om, os_ = W.sam_mlp_inputs(Tk, D, Dh, g5["x_seed"], g5["wi_seed"], g5["wo_seed"],
+                                                   g5["sigma_x"], g5["sigma_h"])
+    li = [torch.empty(n, dtype=dt, device="cuda") for n, dt in zip(T.w12_bytes(Dh, D), (torch.int8, torch.uint8))]
+    lo_ = [torch.empty(n, dtype=dt, device="cuda") for n, dt in zip(T.w12_bytes(D, Dh), (torch.int8, torch.uint8))]
+    T.w12_upload(wi, Dh, D, *li)
+    T.w12_upload(wo, D, Dh, *lo_)
+    xd = torch.from_numpy(W.pad_k(x, Tk, D)).cuda()
+    hd = torch.zeros(Tk * Dh, dtype=torch.int8, device="cuda")
+    yd = torch.empty(Tk * D, dtype=torch.int8, device="cuda")
+    gelu = torch.from_numpy(W.gelu_table()).cuda()
+    imd, isd, omd, osd = (torch.from_numpy(a).cuda() for a in (im, is_, om, os_))
+
+    def mlp_in(i):
+        T.w12_linear_lut(xd, *li, Tk, Dh, D, hd, imd, isd, gelu, stream=stream)
+
+    def mlp_out(i):
+        T.w12_linear(hd, *lo_, Tk, D, Dh, yd, T.OUT_I8, omd, osd, stream=stream)
+
+    mlp_in(0)
+    mlp_out(0)
+    torch.cuda.synchronize()
+    if sha(hd.cpu().numpy()) != g5["mlp_h_sha256"] or sha(yd.cpu().numpy()) != g5["mlp_y_sha256"]:
+        raise SystemExit("bench: config 5: the stage-3 MLP differs from the CPU fixture")
+    log("bench: config 5: bit-exact vs the CPU fixtures; timing")
+    n = max(50, args.steps)
+    ms_p, _ = time_launches(torch, patch, n, 5)
+    ms_i, _ = time_launches(torch, mlp_in, n, 5)
+    ms_o, _ = time_launches(torch, mlp_out, n, 5)
+    M = OH * OW
+
+    def kern(ms, ops, bytes_):
+        s = ms * 1e-3
+        return {"us": round(ms * 1e3, 2), "effective_tops": round(ops / s / 1e12, 1),
+                "mfma_frac_logical": round(ops / s / 1e12 / INT8_PEAK_TOPS, 4),
+                "alg_gbs": round(bytes_ / s / 1e9, 1), "hbm_frac": round(bytes_ / s / 1e9 / HBM_PEAK_GBS, 4)}
+
+    return {
+        "workload": f"config 5: SAM 2.1 Hiera-B+ encoder GEMMs: {H}x{Wd}x{C} image -> patch embed (im2col GEMM "
+                    f"M={M}, K={k}, N={CO}); stage-3 MLP {Tk} tokens {D} -> {Dh} (GELU) -> {D}",
+        "bit_exact": True,
+        "patch_embed": kern(ms_p, 2.0 * M * k * CO, C * H * Wd + 1.5 * CO * k + CO * M),
+        "mlp_in_gelu": kern(ms_i, 2.0 * Tk * D * Dh, Tk * D + 1.5 * D * Dh + Tk * Dh),
+        "mlp_out": kern(ms_o, 2.0 * Tk * D * Dh, Tk * Dh + 1.5 * D * Dh + Tk * D),
+        "total_us": round((ms_p + ms_i + ms_o) * 1e3, 2),
+    }
+
+
+def cpu_baseline_moe(g4: dict, x: np.ndarray, r: np.ndarray) -> dict:
+    """The reference's MoE loop (MoeMlp::forward_routed, layers.rs:988-1020: token by token, each chosen expert and
+    the shared expert on one row) restated by the oracle, on a bounded sample of tokens; single-threaded."""
+    from oracle import oracle as O
+    from tritify_amd import workloads as W
+
+    H, F, E, K = g4["H"], g4["F"], g4["E"], g4["top_k"]
+    n_tok = 4
+    sel, _ = O.moe_route(r[: n_tok * E], n_tok, E, K, W.sigmoid_table())
+    need = sorted(set(sel.tolist()) | {E})
+    G = E + 1
+    wgu = np.zeros((G, 2 * F * H), np.int16)
+    wd = np.zeros((G, H * F), np.int16)
+    gm, gs = np.zeros((G, 2 * F), np.int32), np.zeros((G, 2 * F), np.int32)
+    dm, ds = np.zeros((G, H), np.int32), np.zeros((G, H), np.int32)
+    for g in need:  # only the experts the sample uses are generated
+        gu, dn, a, b, c, d = W.moe_expert(g, H, F, g4["w_seed"], g4["sigma_x"], g4["sigma_h"])
+        wgu[g], wd[g], gm[g], gs[g], dm[g], ds[g] = gu, dn, a, b, c, d
+    t0 = time.perf_counter()
+    O.moe_forward_token(x[: n_tok * H], r[: n_tok * E], n_tok, H, F, E, K, wgu, wd, gm, gs, dm, ds, W.silu_table(),
+                        W.sigmoid_table(), g4["h_shift"], g4["out_shift"])
+    dt = time.perf_counter() - t0
+    ops = 2.0 * n_tok * (K + 1) * 3 * F * H
+    return {"value": round(n_tok / dt, 2), "unit": "tokens/s", "effective_tops": round(ops / dt / 1e12, 5),
+            "cores": 1, "kind": "port",
+            "sample": f"{n_tok} tokens of config 4 through the oracle's restatement of the reference's per-token MoE "
+                      f"loop (each of {K} chosen experts + the shared expert on one row, i64 dots), {dt:.2f} s"}
+
+
+# ---------------------------------------------------------------------------------------------------------------
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--ms", type=str, default="", help="comma-separated subset of M to run (profiling runs)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--configs", type=str, default="2,4,5", help="comma-separated configs to run (2 is the headline)")
+    ap.add_argument("--ms", type=str, default="", help="comma-separated subset of config-2 M to run (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -114,80 +397,25 @@ def main() -> int:
         print(json.dumps({"copy_calib_bytes": 256 << 20, "copies": 10}), flush=True)
         return 0
 
-    import tritify_amd as T
-    from tritify_amd import workloads as W
-
-    gold = json.load(open(os.path.join(ROOT, "tests", "golden", "goldens.json")))["config2"]
-    N, K, sigma = gold["N"], gold["K"], gold["sigma"]
-    Ms = gold["Ms"]
-    MH = max(Ms)
-    if args.ms:
-        Ms = [int(v) for v in args.ms.split(",")]
-        assert all(str(m) in gold["outputs"] for m in Ms), "--ms takes values of the config-2 sweep"
-    dev = torch.device("cuda:0")
-
-    log("bench: generating config-2 inputs")
-    w = W.gen_w12(gold["w_seed"], N * K)
-    x = W.gen_act_gauss(gold["x_seed"], sigma, MH * K)
-    mant, shift = W.channel_scales(w, N, K, sigma)
-    assert sha(w) == gold["w_sha256"] and sha(x) == gold["x_sha256"], "synthetic inputs differ from the fixtures"
-    assert sha(mant) == gold["mant_sha256"] and sha(shift) == gold["shift_sha256"]
-
-    nlo, nnib = T.w12_bytes(N, K)
-    lo0 = torch.empty(nlo, dtype=torch.int8, device=dev)
-    nib0 = torch.empty(nnib, dtype=torch.uint8, device=dev)
-    T.w12_upload(w, N, K, lo0, nib0)
-    los = [lo0] + [lo0.clone() for _ in range(ROTATE - 1)]
-    nibs = [nib0] + [nib0.clone() for _ in range(ROTATE - 1)]
-    xd = torch.from_numpy(W.pad_k(x, MH, K)).to(dev)
-    md, sd = torch.from_numpy(mant).to(dev), torch.from_numpy(shift).to(dev)
-    stream = torch.cuda.current_stream()
-    torch.cuda.synchronize()
-
-    sweep = {}
+    configs = [c.strip() for c in args.configs.split(",") if c.strip()]
+    extra = {}
     headline = None
-    for m in Ms:
-        want = gold["outputs"][str(m)]
-        y8 = torch.empty(m * N, dtype=torch.int8, device=dev)
-        acc = torch.empty(m * N, dtype=torch.int64, device=dev)
-        T.w12_linear(xd, lo0, nib0, m, N, K, acc, T.OUT_I64, stream=stream)
-        T.w12_linear(xd, lo0, nib0, m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
-        torch.cuda.synchronize()
-        exact = sha(acc.cpu().numpy()) == want["acc_i64_sha256"] and sha(y8.cpu().numpy()) == want["out_i8_sha256"]
-        if not exact:
-            log(f"bench: M={m}: the GPU result differs from the CPU fixture")
-            return 1
-
-        def launch(i, m=m, y8=y8):
-            j = i % ROTATE
-            T.w12_linear(xd, los[j], nibs[j], m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
-
-        n_launch = args.steps if m == MH else max(args.steps, 200)
-        warm = args.warmup if m == MH else max(args.warmup, 20)
-        log(f"bench: M={m}: bit-exact vs the CPU fixture; timing {n_launch} launches")
-        ms, wall = time_launches(torch, launch, n_launch, warm)
-        us = ms * 1e3
-        ops = 2.0 * m * N * K
-        bytes_alg = 1.5 * N * K + m * K + m * N * 1  # packed weights + int8 activations + int8 outputs
-        tops = ops / (us * 1e-6) / 1e12
-        gbs = bytes_alg / (us * 1e-6) / 1e9
-        sweep[str(m)] = {
-            "us_per_launch": round(us, 3),
-            "effective_tops": round(tops, 2),
-            "executed_int8_tops": round(2 * tops, 2),
-            "mfma_frac_logical": round(tops / INT8_PEAK_TOPS, 4),
-            "alg_gbs": round(gbs, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "bit_exact": True,
-            "kernel": "w12_skinny" if m <= 128 else "w12_gemm",
-        }
-        if m == MH:
-            headline = (ms, wall, n_launch, warm, us, tops)
+    if "2" in configs:
+        sweep, headline, x, w = bench_config2(torch, args)
+    for c in configs:
+        if c == "4":
+            extra["4"] = bench_config4(torch, args)
+            torch.cuda.empty_cache()
+        if c == "5":
+            extra["5"] = bench_config5(torch, args)
+            torch.cuda.empty_cache()
 
     if headline is None:
-        print(json.dumps({"sweep": sweep}), flush=True)
+        print(json.dumps({"sweep": sweep if "2" in configs else None, "configs": extra}), flush=True)
         return 0
     ms_per_step, wall, n_launch, warm, us, tops = headline
+    g2 = gold()["config2"]
+    N, K, MH = g2["N"], g2["K"], max(g2["Ms"])
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "w12_gemm_m2048_traffic.json")
     if os.path.exists(tpath):
@@ -222,6 +450,7 @@ def main() -> int:
             "kernel": "w12_gemm_kernel (logical ops 2*M*N*K per launch; the 2 digit planes execute twice that)",
         },
         "sweep": sweep,
+        "configs": extra,
         "cpu_baseline": None,
     }
     if not args.no_cpu:

@@ -217,6 +217,23 @@ int kt_hip_moe_forward(int dev, const int8_t* x_dev, const int32_t* logits_dev, 
                        void* workspace_dev, int8_t* out_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * SAM 2.1 image path of config 5, device-resident operands.
+ * ------------------------------------------------------------------------------------------------------------- */
+/* The patch-embed convolution (Conv2d::forward_int, crates/01-engine/kt-core/src/conv.rs:68-130, as PatchEmbed
+ * uses it, crates/03-models/kt-model-vision/src/hiera.rs:165-190) as an im2col-fused W12 GEMM. img_dev holds the
+ * u8 pixels [ci][h][w]; each pixel p of channel c enters as the int8 code lut_dev[c * 256 + p] (the entry
+ * quantization of the normalized image, plugin.rs:38); taps outside the image contribute nothing. The weights are
+ * the W12 planes (kt_hip_w12_upload / kt_hip_w12_pack) of the co x (ci * kh * kw) code matrix, k ordered
+ * (ic, ky, kx) as the reference's accumulation. out_dev [co][oh][ow] int8 receives
+ * clamp(requant(acc + bias[c], mant[c], shift[c]), +-127) (bias_dev may be NULL; |bias| < 2^30).
+ * oh = (h + 2 pad - kh) / stride + 1, likewise ow. Limits: ci <= 4, ci * kh * kw <= 256,
+ * ci * kh * (127 stride + kw) <= 16384. Asynchronous on `stream`. */
+int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_dev, int64_t ci, int64_t h, int64_t w,
+                           const int8_t* lo_dev, const uint8_t* nib_dev, int64_t co, int64_t kh, int64_t kw,
+                           int64_t stride, int64_t pad, const int32_t* bias_dev, const int32_t* mant_dev,
+                           const int32_t* shift_dev, int8_t* out_dev, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Synthetic workload generators (host only, no GPU): the BASELINE configs' integer samplers on the reference LCG
  * (apps/kt-demo/src/main.rs:19-22), multithreaded over the host cores. No counterpart in the reference.
  * ------------------------------------------------------------------------------------------------------------- */

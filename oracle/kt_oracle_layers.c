@@ -379,3 +379,81 @@ void kt_moe_forward_token(const int8_t* x, const int32_t* logits, size_t T, size
     free(dd);
     free(y);
 }
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Config 5: SAM 2.1 Hiera-B+ image-encoder GEMMs (this build's int8 definition)                                   */
+/* ------------------------------------------------------------------------------------------------------------ */
+/*
+ * Entry (IntTensor::from_reals of the normalized image, crates/03-models/kt-model-vision/src/plugin.rs:38, with
+ * preprocess.rs's ImageNet normalization): pixel p of channel c -> q = lut[c * 256 + p], an int8 code table built
+ * once from the closed form round(48 * (p / 255 - mean_c) / std_c).
+ * Patch embed (Conv2d::forward_int, crates/01-engine/kt-core/src/conv.rs:68-130): per output channel oc and
+ * position (oy, ox), acc = sum over (ic, ky, kx) of q[ic][iy][ix] * w[oc][ic][ky][kx] with iy = oy*stride + ky - pad,
+ * ix = ox*stride + kx - pad, taps outside the image skipped; out[oc][oy][ox] = rq8(acc + bias[oc], mant[oc],
+ * shift[oc]) (the reference adds the bias in accumulator units, then requantizes).
+ */
+void kt_sam_entry(const uint8_t* img, size_t C, size_t HW, const int8_t* lut, int8_t* q) {
+    for (size_t c = 0; c < C; c++)
+        for (size_t i = 0; i < HW; i++) q[c * HW + i] = lut[c * 256 + img[c * HW + i]];
+}
+
+typedef struct {
+    const int8_t* q;
+    size_t ci, h, w, co, kh, kw, stride, pad, oh, ow;
+    const int16_t* wt;
+    const int32_t *bias, *mant, *shift;
+    int8_t* out;
+    int64_t* acc_out;
+} conv_ctx;
+
+static void conv_task(void* p, size_t oc) {
+    conv_ctx* c = (conv_ctx*)p;
+    const int16_t* wb = c->wt + oc * c->ci * c->kh * c->kw;
+    for (size_t oy = 0; oy < c->oh; oy++)
+        for (size_t ox = 0; ox < c->ow; ox++) {
+            int64_t acc = 0;
+            for (size_t ic = 0; ic < c->ci; ic++)
+                for (size_t ky = 0; ky < c->kh; ky++) {
+                    size_t iy = oy * c->stride + ky;
+                    if (iy < c->pad || iy - c->pad >= c->h) continue;
+                    iy -= c->pad;
+                    for (size_t kx = 0; kx < c->kw; kx++) {
+                        size_t ix = ox * c->stride + kx;
+                        if (ix < c->pad || ix - c->pad >= c->w) continue;
+                        ix -= c->pad;
+                        acc += (int64_t)c->q[(ic * c->h + iy) * c->w + ix] * wb[(ic * c->kh + ky) * c->kw + kx];
+                    }
+                }
+            acc += c->bias ? c->bias[oc] : 0;
+            size_t o = (oc * c->oh + oy) * c->ow + ox;
+            if (c->acc_out) c->acc_out[o] = acc;
+            c->out[o] = rq8(acc, c->mant[oc], c->shift[oc]);
+        }
+}
+
+/* The patch-embed conv on the int8 entry codes q ([ci][h][w]); out is [co][oh][ow] int8, acc_out (optional) the
+ * i64 sums including the bias. Output channels run in parallel (each a disjoint plane, as par_blocks does). */
+void kt_conv2d_i8w16(const int8_t* q, size_t ci, size_t h, size_t w, const int16_t* wt, size_t co, size_t kh,
+                     size_t kw, size_t stride, size_t pad, const int32_t* bias, const int32_t* mant,
+                     const int32_t* shift, int8_t* out, int64_t* acc_out, size_t threads) {
+    size_t oh = (h + 2 * pad - kh) / stride + 1, ow = (w + 2 * pad - kw) / stride + 1;
+    conv_ctx c = {q, ci, h, w, co, kh, kw, stride, pad, oh, ow, wt, bias, mant, shift, out, acc_out};
+    pool_run(conv_task, &c, co, threads);
+}
+
+/* Hiera's stage MLP (FeedForward::forward_int, crates/03-models/kt-model-vision/src/hiera.rs:336-340, with the
+ * GELU of nonlin.rs:30-47 as an int8 code table): h = gelu[rq8(x . Wi^T) + 127], y = rq8(h . Wo^T). */
+int kt_mlp_gelu(const int8_t* x, size_t m, size_t d, size_t dh, const int16_t* wi, const int32_t* im,
+                const int32_t* is, const int8_t* gelu, const int16_t* wo, const int32_t* om, const int32_t* os,
+                int8_t* h, int8_t* y, size_t threads) {
+    if (kt_gemm_i8w16(x, wi, m, dh, d, im, is, NULL, h, threads)) return -1;
+    for (size_t i = 0; i < m * dh; i++) h[i] = gelu[h[i] + 127];
+    return kt_gemm_i8w16(h, wo, m, d, dh, om, os, NULL, y, threads);
+}
+
+/* n values uniform in [lo, hi]: ((s >> 33) % (hi - lo + 1)) + lo on the stream seed ^ 0x9E3779B97F4A7C15 (the image
+ * pixels of config 5 with lo = 0, hi = 255). */
+void kt_gen_uniform_i32(uint64_t seed, int64_t lo, int64_t hi, size_t n, int32_t* out) {
+    uint64_t s = seed ^ 0x9E3779B97F4A7C15ULL, range = (uint64_t)(hi - lo + 1);
+    for (size_t i = 0; i < n; i++) out[i] = (int32_t)((int64_t)((kt_lcg_next(&s) >> 33) % range) + lo);
+}

@@ -115,6 +115,10 @@ def _declare(L: C.CDLL) -> None:
         "kt_moe_experts": (C.c_int, [_P, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int, _P, _P,
                                      _SZ]),
         "kt_moe_combine": (None, [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, C.c_int, _P]),
+        "kt_sam_entry": (None, [_P, _SZ, _SZ, _P, _P]),
+        "kt_gen_uniform_i32": (None, [C.c_uint64, C.c_int64, C.c_int64, _SZ, _P]),
+        "kt_conv2d_i8w16": (None, [_P, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _SZ]),
+        "kt_mlp_gelu": (C.c_int, [_P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ]),
         "kt_moe_forward_token": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int,
                                         C.c_int, _P]),
     }
@@ -564,3 +568,42 @@ def moe_layer(x, logits, T, H, F, E, top_k, wgu, wd, gm, gs, dm, ds, silu, sig, 
     h, d = moe_experts(x, T, H, F, E + 1, lst, count, wgu, wd, gm, gs, dm, ds, silu, h_shift, threads)
     out = moe_combine(d, sel, cw, pos, count, T, H, E, top_k, out_shift)
     return dict(sel=sel, cw=cw, list=lst, pos=pos, count=count, h=h, d=d, out=out)
+
+
+def sam_entry(img, C: int, HW: int, lut) -> np.ndarray:
+    img, lut = _c(img, np.uint8), _c(lut, np.int8)
+    q = np.empty(C * HW, dtype=np.int8)
+    lib().kt_sam_entry(_ptr(img), C, HW, _ptr(lut), _ptr(q))
+    return q
+
+
+def conv2d(q, ci, h, w, wt, co, kh, kw, stride, pad, bias, mant, shift, threads: int = 0, want_acc=False):
+    """Conv2d::forward_int's direct loop (conv.rs:68-130) on int8 codes: (out int8 [co][oh][ow], acc i64 or None)."""
+    q, wt = _c(q, np.int8), _c(wt, np.int16)
+    bias = _c(bias, np.int32) if bias is not None else None
+    mant, shift = _c(mant, np.int32), _c(shift, np.int32)
+    oh, ow = (h + 2 * pad - kh) // stride + 1, (w + 2 * pad - kw) // stride + 1
+    out = np.empty(co * oh * ow, dtype=np.int8)
+    acc = np.empty(co * oh * ow, dtype=np.int64) if want_acc else None
+    lib().kt_conv2d_i8w16(_ptr(q), ci, h, w, _ptr(wt), co, kh, kw, stride, pad,
+                          _ptr(bias) if bias is not None else None, _ptr(mant), _ptr(shift), _ptr(out),
+                          _ptr(acc) if acc is not None else None, threads)
+    return out, acc
+
+
+def mlp_gelu(x, m, d, dh, wi, im, is_, gelu, wo, om, os_, threads: int = 0):
+    x, wi, wo, gelu = _c(x, np.int8), _c(wi, np.int16), _c(wo, np.int16), _c(gelu, np.int8)
+    im, is_, om, os_ = (_c(a, np.int32) for a in (im, is_, om, os_))
+    h = np.empty(m * dh, dtype=np.int8)
+    y = np.empty(m * d, dtype=np.int8)
+    r = lib().kt_mlp_gelu(_ptr(x), m, d, dh, _ptr(wi), _ptr(im), _ptr(is_), _ptr(gelu), _ptr(wo), _ptr(om), _ptr(os_),
+                          _ptr(h), _ptr(y), threads)
+    if r:
+        raise ValueError("mlp_gelu: a dimension beyond the int32-exact bound")
+    return h, y
+
+
+def gen_uniform(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().kt_gen_uniform_i32(seed & (2**64 - 1), lo, hi, n, _ptr(out))
+    return out

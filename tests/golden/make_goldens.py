@@ -2,7 +2,7 @@
 (oracle/kt_oracle.c, the restated reference CPU path). The GPU tests compare the device results with these fixtures
 at full size, where recomputing the CPU answer inside a test would take too long.
 
-Run from the repository root:  python tests/golden/make_goldens.py
+Run from the repository root:  python tests/golden/make_goldens.py [config1 config2 config4 config5]
 """
 import json
 import os
@@ -24,6 +24,44 @@ C2 = {"w_seed": 2, "x_seed": 3, "sigma": 40, "N": 4096, "K": 4096, "Ms": [1, 16,
 # BASELINE config 4 (this build's integer MoE layer, include/kt_hip.h): GLM-4.5-Air shape.
 C4 = {"T": 4096, "H": 4096, "F": 1408, "E": 128, "top_k": 8, "x_seed": 41, "r_seed": 42, "w_seed": 4000,
       "sigma_x": 40, "sigma_r": 1024, "sigma_h": 16, "h_shift": 8, "out_shift": 13}
+
+# BASELINE config 5 (this build's integer definition of the SAM 2.1 Hiera-B+ encoder GEMMs, include/kt_hip.h).
+C5 = {"C": 3, "H": 1024, "W": 1024, "CO": 112, "KH": 7, "KW": 7, "S": 4, "P": 3, "tokens": 4096, "dim": 448,
+      "hidden": 1792, "img_seed": 51, "pe_seed": 52, "bias_seed": 53, "x_seed": 54, "wi_seed": 55, "wo_seed": 56,
+      "entry_scale": 48, "sigma_q": 61, "bias_sigma": 131072, "sigma_x": 40, "sigma_h": 24}
+
+
+def config5() -> dict:
+    """The oracle's direct conv (the reference's loop order) on the entry codes of the full image, and the stage-3
+    MLP; inputs from the oracle's generators, tables from the workload definitions."""
+    from tritify_amd import workloads as W
+
+    c = dict(C5)
+    C, H, Wd, CO, KH, KW = c["C"], c["H"], c["W"], c["CO"], c["KH"], c["KW"]
+    img = O.gen_uniform(c["img_seed"], 0, 255, C * H * Wd).astype(np.uint8)
+    lut = W.sam_entry_table(c["entry_scale"])
+    k = C * KH * KW
+    w = O.gen_w12_i16(c["pe_seed"], CO * k)
+    b = O.gen_gauss_i32(c["bias_seed"], c["bias_sigma"], CO)
+    mant, shift = O.channel_scales_i16(w, CO, k, c["sigma_q"])
+    t = time.time()
+    q = O.sam_entry(img, C, H * Wd, lut)
+    out, _ = O.conv2d(q, C, H, Wd, w, CO, KH, KW, c["S"], c["P"], b, mant, shift)
+    print(f"config5 patch embed: {time.time() - t:.1f}s", flush=True)
+    T, D, Dh = c["tokens"], c["dim"], c["hidden"]
+    x = O.gen_act_gauss(c["x_seed"], c["sigma_x"], T * D)
+    wi = O.gen_w12_i16(c["wi_seed"], Dh * D)
+    wo = O.gen_w12_i16(c["wo_seed"], D * Dh)
+    im, is_ = O.channel_scales_i16(wi, Dh, D, c["sigma_x"])
+    om, os_ = O.channel_scales_i16(wo, D, Dh, c["sigma_h"])
+    h, y = O.mlp_gelu(x, T, D, Dh, wi, im, is_, W.gelu_table(), wo, om, os_)
+    c.update({
+        "img_sha256": O.sha256_hex(img), "entry_sha256": O.sha256_hex(lut), "gelu_sha256": O.sha256_hex(W.gelu_table()),
+        "patch_sha256": O.sha256_hex(out), "mlp_h_sha256": O.sha256_hex(h), "mlp_y_sha256": O.sha256_hex(y),
+        "patch_absmean": float(np.abs(out.astype(np.int32)).mean()),
+        "mlp_y_absmean": float(np.abs(y.astype(np.int32)).mean()),
+    })
+    return c
 
 
 def config4() -> dict:
@@ -64,18 +102,32 @@ def config4() -> dict:
 
 
 def main() -> None:
+    """Recompute the configs named on the command line (config1 config2 config4 config5; none = all) and keep the
+    other entries of the existing file."""
     t0 = time.time()
-    g = {}
-    qx, qw = O.gen_demo(64, 1024, 1024, 42)
-    y = O.linear_cpu(qx, qw, 64, 1024, 1024)
-    g["config1"] = {
-        "M": 64, "N": 1024, "K": 1024, "seed": 42,
-        "x_sha256": O.sha256_hex(qx), "w_sha256": O.sha256_hex(qw),
-        "y_i64_sha256": O.sha256_hex(y), "y_i32_sha256": O.sha256_hex(y.astype(np.int32)),
-    }
-    cs = O.corpus()
-    g["corpus_sha256"] = O.sha256_hex(np.concatenate([O.linear_cpu(c.x, c.w, c.rows, c.out, c.k) for c in cs]))
+    want = set(sys.argv[1:]) or {"config1", "config2", "config4", "config5"}
+    g = json.load(open(OUT)) if os.path.exists(OUT) else {}
+    if "config1" in want:
+        qx, qw = O.gen_demo(64, 1024, 1024, 42)
+        y = O.linear_cpu(qx, qw, 64, 1024, 1024)
+        g["config1"] = {
+            "M": 64, "N": 1024, "K": 1024, "seed": 42,
+            "x_sha256": O.sha256_hex(qx), "w_sha256": O.sha256_hex(qw),
+            "y_i64_sha256": O.sha256_hex(y), "y_i32_sha256": O.sha256_hex(y.astype(np.int32)),
+        }
+        cs = O.corpus()
+        g["corpus_sha256"] = O.sha256_hex(np.concatenate([O.linear_cpu(c.x, c.w, c.rows, c.out, c.k) for c in cs]))
+    if "config2" in want:
+        g["config2"] = config2()
+    if "config4" in want:
+        g["config4"] = config4()
+    if "config5" in want:
+        g["config5"] = config5()
+    json.dump(g, open(OUT, "w"), indent=1, sort_keys=True)
+    print(f"wrote {OUT} in {time.time() - t0:.1f}s")
 
+
+def config2() -> dict:
     N, K = C2["N"], C2["K"]
     w = O.gen_w12(C2["w_seed"], N * K)
     x = O.gen_act_gauss(C2["x_seed"], C2["sigma"], max(C2["Ms"]) * K)
@@ -97,10 +149,7 @@ def main() -> None:
             "out_i8_saturated": int((np.abs(q.astype(np.int32)) == 127).sum()),
         }
         print(f"config2 M={m}: {time.time() - t:.1f}s", flush=True)
-    g["config2"] = c2
-    g["config4"] = config4()
-    json.dump(g, open(OUT, "w"), indent=1, sort_keys=True)
-    print(f"wrote {OUT} in {time.time() - t0:.1f}s")
+    return c2
 
 
 if __name__ == "__main__":

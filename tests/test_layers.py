@@ -183,3 +183,61 @@ def test_product_generators_equal_the_oracle():
     assert np.array_equal(m1, m2) and np.array_equal(s1, s2)
     m3, s3 = O.channel_scales_i16(w.astype(np.int16), 300, 517, 40)
     assert np.array_equal(m1, m3) and np.array_equal(s1, s3)
+
+
+def conv_numpy(q, ci, h, w, wt, co, kh, kw, s, p, bias):
+    """The reference's direct loop (conv.rs:68-130) as a zero-padded numpy convolution: skipping a tap outside the
+    image equals multiplying a zero."""
+    x = np.zeros((ci, h + 2 * p, w + 2 * p), np.int64)
+    x[:, p:p + h, p:p + w] = q.reshape(ci, h, w)
+    oh, ow = (h + 2 * p - kh) // s + 1, (w + 2 * p - kw) // s + 1
+    wt = wt.reshape(co, ci, kh, kw).astype(np.int64)
+    acc = np.zeros((co, oh, ow), np.int64)
+    for ky in range(kh):
+        for kx in range(kw):
+            patch = x[:, ky:ky + s * (oh - 1) + 1:s, kx:kx + s * (ow - 1) + 1:s]  # ci x oh x ow
+            acc += np.einsum("cij,oc->oij", patch, wt[:, :, ky, kx])
+    if bias is not None:
+        acc += bias.astype(np.int64)[:, None, None]
+    return acc.reshape(-1)
+
+
+@pytest.mark.parametrize("ci,h,w,co,kh,kw,s,p", [(3, 30, 41, 7, 7, 7, 4, 3), (2, 9, 9, 3, 3, 3, 1, 1),
+                                                 (1, 5, 12, 2, 5, 2, 2, 0)])
+def test_conv_oracle_equals_padded_convolution(ci, h, w, co, kh, kw, s, p):
+    rng = np.random.default_rng(ci * h + w)
+    q = rng.integers(-127, 128, size=ci * h * w).astype(np.int8)
+    wt = rng.integers(-2048, 2048, size=co * ci * kh * kw).astype(np.int16)
+    bias = rng.integers(-(2**20), 2**20, size=co).astype(np.int32)
+    mant = rng.integers(1, 2**31, size=co).astype(np.int32)
+    shift = rng.integers(10, 40, size=co).astype(np.int32)
+    out, acc = O.conv2d(q, ci, h, w, wt, co, kh, kw, s, p, bias, mant, shift, want_acc=True)
+    want = conv_numpy(q, ci, h, w, wt, co, kh, kw, s, p, bias)
+    assert np.array_equal(acc, want)
+    oh, ow = (h + 2 * p - kh) // s + 1, (w + 2 * p - kw) // s + 1
+    chan = np.repeat(np.arange(co), oh * ow)
+    rq = [max(-127, min(127, py_requant(int(a), int(mant[c]), int(shift[c])))) for a, c in zip(want, chan)]
+    assert out.tolist() == rq
+
+
+def test_entry_and_gelu_tables_closed_forms():
+    """The entry table is the ImageNet normalization at scale 48 (monotone, within int8, zero crossing at the mean);
+    the GELU table is gelu on the int8 grid (gelu(v) - gelu(-v) = v, gelu(0) = 0)."""
+    from tritify_amd import workloads as W
+
+    t = W.sam_entry_table().astype(int)
+    for c, (mu, sd) in enumerate(zip(W.IMAGENET_MEAN, W.IMAGENET_STD)):
+        assert (np.diff(t[c]) >= 0).all() and abs(t[c]).max() <= 127
+        p0 = int(round(mu * 255))
+        assert abs(t[c][p0]) <= 1
+        assert abs(t[c][255] - 48 * (1 - mu) / sd) <= 0.5 + 1e-9
+    g = W.gelu_table().astype(int)
+    assert g[127] == 0
+    for i in range(1, 128):
+        assert abs((g[127 + i] - g[127 - i]) - i) <= 1
+
+
+def test_uniform_pixels_generator():
+    import tritify_amd as TA
+
+    assert np.array_equal(TA.gen_uniform_fast(51, 0, 255, 1_000_003), O.gen_uniform(51, 0, 255, 1_000_003))

@@ -88,6 +88,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_moe_workspace": (_I, [_I64, _I64, _I64, _I64, _I, C.POINTER(_SZ), C.POINTER(_SZ)]),
         "kt_hip_moe_forward": (_I, [_I, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _I, _I, _P, _P, _P]),
+        "kt_hip_sam_patch_embed": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P,
+                                        _P, _P, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
@@ -370,6 +372,21 @@ def moe_forward(x_dev, logits_dev, tokens: int, hidden: int, ffn: int, experts: 
                                  _ptr(d_shift), _ptr(silu_dev), _ptr(sig_dev), h_shift, out_shift,
                                  _ptr(workspace_dev), _ptr(out_dev), _stream(stream)),
         "moe forward",
+    )
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# SAM image path (config 5)
+
+
+def sam_patch_embed(img_dev, lut_dev, ci: int, h: int, w: int, lo_dev, nib_dev, co: int, kh: int, kw: int,
+                    stride: int, pad: int, bias_dev, mant_dev, shift_dev, out_dev, stream=None, dev: int = 0) -> None:
+    """The im2col-fused patch-embed conv: u8 pixels -> entry codes -> W12 GEMM -> +bias -> int8 [co][oh][ow]."""
+    check(
+        lib().kt_hip_sam_patch_embed(dev, _ptr(img_dev), _ptr(lut_dev), ci, h, w, _ptr(lo_dev), _ptr(nib_dev), co, kh,
+                                     kw, stride, pad, _ptr(bias_dev), _ptr(mant_dev), _ptr(shift_dev), _ptr(out_dev),
+                                     _stream(stream)),
+        "sam patch embed",
     )
 
 

@@ -586,6 +586,24 @@ int kt_hip_moe_forward(int dev, const int8_t* x_dev, const int32_t* logits_dev, 
     return (int)kt::launch_moe_combine(d, goff, sel, cw, pos, T, (int)hidden, E, top_k, out_shift, out_dev, s);
 }
 
+// ----------------------------------------------------------------------------------------------------------------
+// SAM image path (config 5)
+// ----------------------------------------------------------------------------------------------------------------
+
+int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_dev, int64_t ci, int64_t h, int64_t w,
+                           const int8_t* lo_dev, const uint8_t* nib_dev, int64_t co, int64_t kh, int64_t kw,
+                           int64_t stride, int64_t pad, const int32_t* bias_dev, const int32_t* mant_dev,
+                           const int32_t* shift_dev, int8_t* out_dev, void* stream) {
+    if (ci < 1 || ci > 4 || h < 1 || w < 1 || h > INT_MAX || w > INT_MAX || co < 1 || co > INT_MAX || kh < 1 ||
+        kw < 1 || kh > 256 || kw > 256 || stride < 1 || stride > 256 || pad < 0 || pad > 256 || mant_dev == nullptr ||
+        shift_dev == nullptr || lut_dev == nullptr)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_conv_patch(img_dev, lut_dev, (int)ci, (int)h, (int)w, (int)kh, (int)kw, (int)stride,
+                                      (int)pad, lo_dev, nib_dev, (int)co, bias_dev, mant_dev, shift_dev, out_dev,
+                                      (hipStream_t)stream);
+}
+
 int kt_hip_probe_mfma(int dev, const int8_t* a_dev, const int8_t* b_dev, int32_t* c32_dev, int32_t* c16_dev,
                       void* stream) {
     KT_TRY(hipSetDevice(dev));

@@ -29,6 +29,9 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
 hipError_t launch_moe_combine(const int8_t* d, const int32_t* off, const int32_t* sel, const int32_t* cw,
                               const int32_t* pos, int T, int H, int E, int top_k, int out_shift, int8_t* out,
                               hipStream_t s);
+hipError_t launch_conv_patch(const uint8_t* img, const int8_t* lut, int CI, int H, int W, int KH, int KW, int S, int P,
+                             const int8_t* wlo, const uint8_t* wnib, int CO, const int32_t* bias, const int32_t* mant,
+                             const int32_t* shift, int8_t* out, hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

@@ -188,3 +188,62 @@ def moe_expert(g: int, H: int, F: int, w_seed: int, sigma_x: int = 40, sigma_h: 
     gm, gs = B.channel_scales_fast(gu, 2 * F, H, sigma_x)
     dm, ds = B.channel_scales_fast(dn, H, F, sigma_h)
     return gu, dn, gm, gs, dm, ds
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Config 5: SAM 2.1 Hiera-B+ image-encoder GEMMs (this build's integer definition; include/kt_hip.h states the rule)
+
+SAM_FULL = dict(C=3, H=1024, W=1024, CO=112, KH=7, KW=7, S=4, P=3, tokens=4096, dim=448, hidden=1792)
+SAM_SEEDS = dict(img_seed=51, pe_seed=52, bias_seed=53, x_seed=54, wi_seed=55, wo_seed=56)
+SAM_CONST = dict(entry_scale=48, sigma_q=61, bias_sigma=131072, sigma_x=40, sigma_h=24)
+IMAGENET_MEAN = (0.485, 0.456, 0.406)  # crates/03-models/kt-model-vision/src/preprocess.rs:6-7
+IMAGENET_STD = (0.229, 0.224, 0.225)
+
+
+def sam_entry_table(scale: int = 48) -> np.ndarray:
+    """3 x 256 int8 entry codes: t[c][p] = clamp(round(scale * (p / 255 - mean_c) / std_c), -127, 127), the ImageNet
+    normalization of preprocess.rs and the entry quantization of plugin.rs:38 as one table per channel."""
+    t = np.empty((3, 256), dtype=np.int8)
+    for c in range(3):
+        for p in range(256):
+            v = _round_half_away(scale * (p / 255.0 - IMAGENET_MEAN[c]) / IMAGENET_STD[c])
+            t[c, p] = max(-127, min(127, v))
+    return t
+
+
+def gelu_table() -> np.ndarray:
+    """255 int8 GELU codes: t[i] = clamp(round(32 * gelu(v)), -127, 127), v = (i - 127) / 32, gelu(v) =
+    v (1 + erf(v / sqrt 2)) / 2 (apply_gelu of crates/03-models/kt-model-vision/src/nonlin.rs:30-47 on the int8 grid)."""
+    out = np.empty(255, dtype=np.int8)
+    for i in range(255):
+        v = (i - 127) / 32.0
+        out[i] = max(-127, min(127, _round_half_away(32.0 * 0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))))))
+    return out
+
+
+def sam_patch_inputs(C: int, H: int, W: int, CO: int, KH: int, KW: int, img_seed: int, pe_seed: int, bias_seed: int,
+                     sigma_q: int = 61, bias_sigma: int = 131072):
+    """The image (C x H x W u8, uniform), the patch-embed codes (CO x C*KH*KW, k ordered (ic, ky, kx)), its bias
+    (CO int32, round(N(0, bias_sigma))) and per-channel scales (4 sigma of the accumulator at entry-code sigma_q)."""
+    from . import backend as B
+
+    img = B.gen_uniform_fast(img_seed, 0, 255, C * H * W).astype(np.uint8)
+    k = C * KH * KW
+    w = B.gen_w12_fast(pe_seed, CO * k)
+    bias = B.gen_gauss_fast(bias_seed, bias_sigma, CO)
+    mant, shift = B.channel_scales_fast(w, CO, k, sigma_q)
+    return img, w, bias, mant, shift
+
+
+def sam_mlp_inputs(tokens: int, dim: int, hidden: int, x_seed: int, wi_seed: int, wo_seed: int, sigma_x: int = 40,
+                   sigma_h: int = 24):
+    """Stage-3 MLP: tokens (tokens x dim int8, round(N(0, sigma_x)) clipped), proj_in (hidden x dim codes) and
+    proj_out (dim x hidden codes) with their per-channel scales."""
+    from . import backend as B
+
+    x = B.gen_gauss_fast(x_seed, sigma_x, tokens * dim, clip=127)
+    wi = B.gen_w12_fast(wi_seed, hidden * dim)
+    wo = B.gen_w12_fast(wo_seed, dim * hidden)
+    im, is_ = B.channel_scales_fast(wi, hidden, dim, sigma_x)
+    om, os_ = B.channel_scales_fast(wo, dim, hidden, sigma_h)
+    return x, wi, wo, im, is_, om, os_
