@@ -33,6 +33,7 @@ extern "C" {
 #define KT_OUT_I64 0 /* the exact accumulators */
 #define KT_OUT_I32 1 /* per-channel requant, saturated to i32 */
 #define KT_OUT_I8 2  /* per-channel requant, clamped to [-127, 127] */
+#define KT_OUT_I32_ADD 3 /* per-channel requant saturated to i32, added (saturating) to the i32 already in y */
 
 /* Planted defects (firing controls). Only the test build, libkt_hip_planted.so, accepts them; the product library
  * returns hipErrorNotSupported from kt_hip_open_planted. Mirrors kt_cuda::Plant
@@ -234,6 +235,41 @@ int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_de
                            const int32_t* shift_dev, int8_t* out_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * Decoder of config 3 (Qwen2.5-0.5B shape): the operations between the W12 GEMMs, device-resident operands. They
+ * replace the reference decoder's host-side steps (DecoderModel::embed_int / blocks_int / head_int / decode_step,
+ * crates/01-engine/kt-core/src/model.rs:168-188, 290-353; RmsNorm and Attention, attention.rs:347-480;
+ * generate_greedy_by, generate.rs:82-111) with this build's int8 rules. Positions are read from pos_dev (the
+ * position of row 0 of the call) so a captured decode step replays at every position; kt_hip_dec_advance moves it.
+ * The q/k/v projection output is one row of nqkv = (nh + 2 nkv) hd int8 values per token: q heads, k heads, v heads.
+ * ------------------------------------------------------------------------------------------------------------- */
+/* r[t] = emb[tokens[t]] (int16 codes, the tied embedding) into the int32 residual rows (t < T, d wide). */
+int kt_hip_dec_embed(int dev, const int32_t* tokens_dev, int64_t tokens, const int16_t* emb_dev, int64_t d,
+                     int32_t* r_dev, void* stream);
+/* RmsNorm to int8: rms = isqrt(floor(sum_i r_i^2 / d)), q_i = clamp(round_half_away(32 r_i / rms), +-127), 0 when
+ * rms is 0. q rows have stride q_stride (>= d). */
+int kt_hip_dec_rmsnorm(int dev, const int32_t* r_dev, int64_t tokens, int64_t d, int8_t* q_dev, int64_t q_stride,
+                       void* stream);
+/* Rotate-half RoPE of the q and k heads of each row in place at position p = pos + t (pairs i, i + hd/2:
+ * a' = clamp(sr(a C - b S, 14)), b' = clamp(sr(b C + a S, 14)), sr = round-half-away shift, C/S = cos/sin tables
+ * [max_pos][hd/2] int16 at 2^14), then the rotated k and the v heads into the layer's caches [max_pos][nkv][hd]. */
+int kt_hip_dec_rope_kv(int dev, int8_t* qkv_dev, int64_t tokens, int64_t nqkv, const int32_t* pos_dev, int64_t nh,
+                       int64_t nkv, int64_t hd, const int16_t* cos_dev, const int16_t* sin_dev, int8_t* kcache_dev,
+                       int8_t* vcache_dev, void* stream);
+/* Causal GQA attention with an integer softmax: head h of row t (kv head g = h / (nh / nkv)) attends positions
+ * j <= p: s_j = q . k_j, m = max s_j, e_j = exp_tab[(m - s_j + 64) >> 7] (0 past its 1024 entries),
+ * o = clamp(round_half_away(sum_j e_j v_j / sum_j e_j)). o is tokens x nh hd int8. hd = 64, max_pos <= 16384. */
+int kt_hip_dec_attention(int dev, const int8_t* qkv_dev, int64_t tokens, int64_t nqkv, const int32_t* pos_dev,
+                         const int8_t* kcache_dev, const int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd,
+                         const int32_t* exp_tab_dev, int8_t* o_dev, int64_t max_pos, void* stream);
+/* argmax_codes (generate.rs:48-56): token_dev[0] = the first index of the maximum of n int32 logits. With
+ * record_dev non-null the logits are also copied to record_dev + step_dev[0] * n and step_dev[0] advances by one
+ * (the per-step logits the generation hash covers). */
+int kt_hip_dec_argmax(int dev, const int32_t* logits_dev, int64_t n, int32_t* token_dev, int32_t* record_dev,
+                      int32_t* step_dev, void* stream);
+/* pos_dev[0] += by. */
+int kt_hip_dec_advance(int dev, int32_t* pos_dev, int64_t by, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Synthetic workload generators (host only, no GPU): the BASELINE configs' integer samplers on the reference LCG
  * (apps/kt-demo/src/main.rs:19-22), multithreaded over the host cores. No counterpart in the reference.
  * ------------------------------------------------------------------------------------------------------------- */
@@ -245,9 +281,14 @@ void kt_hip_gen_w12(uint64_t seed, size_t n, int32_t* out);
 void kt_hip_gen_gauss(uint64_t seed, int64_t sigma, int64_t clip, size_t n, int32_t* out);
 /* n values uniform in [lo, hi]: ((s >> 33) % (hi - lo + 1)) + lo on the stream seed ^ 0x9E3779B97F4A7C15. */
 void kt_hip_gen_uniform(uint64_t seed, int64_t lo, int64_t hi, size_t n, int32_t* out);
-/* Per output channel of an n x k code matrix: to_i32(Scale::from_ratio(127, 4 * sigma * isqrt(sum_k w^2)))
- * (crates/00-kernels/kt-int/src/lib.rs:191-212), mapping 4 standard deviations of the accumulator to 127. */
-void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, int32_t* mant, int32_t* shift);
+/* Per output channel of an n x k code matrix: to_i32(Scale::from_ratio(target, 4 * sigma * isqrt(sum_k w^2)))
+ * (crates/00-kernels/kt-int/src/lib.rs:191-212), mapping 4 standard deviations of the accumulator (inputs of
+ * standard deviation sigma) to target (127 for int8 outputs). */
+void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, int64_t target, int32_t* mant,
+                           int32_t* shift);
+/* rows x cols 12-bit codes of a Gaussian matrix quantized per row: v = round(N(0, 2^20)) on kt_hip_gen_gauss's
+ * stream, code = round_half_away(2047 v / max_row |v|). */
+void kt_hip_gen_quant_rows(uint64_t seed, size_t rows, size_t cols, int32_t* out);
 
 /* Test hook: one 32x32x32 and one 16x16x64 int8 MFMA on 64 lanes x 16 bytes of a_dev / b_dev; the raw accumulator
  * registers go to c32_dev (64 x 16 i32) and c16_dev (64 x 4 i32). */

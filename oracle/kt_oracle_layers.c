@@ -142,34 +142,52 @@ typedef struct {
     const int32_t *mant, *shift;
     int64_t* acc;
     int8_t* y8;
+    int32_t* y32;
+    int add32;
     dot16_fn dot;
+    size_t ncb; /* column blocks per row block */
 } gemm_ctx;
 
 #define GEMM_ROWS 32
+#define GEMM_COLS 256
+
+static inline int32_t sat32(int64_t v) { return (int32_t)clamp64(v, INT32_MIN, INT32_MAX); }
 
 static void gemm_task(void* p, size_t task) {
     gemm_ctx* c = (gemm_ctx*)p;
-    size_t r0 = task * GEMM_ROWS, r1 = r0 + GEMM_ROWS < c->m ? r0 + GEMM_ROWS : c->m;
+    size_t rb = task / c->ncb, cb = task % c->ncb;
+    size_t r0 = rb * GEMM_ROWS, r1 = r0 + GEMM_ROWS < c->m ? r0 + GEMM_ROWS : c->m;
+    size_t o0 = cb * GEMM_COLS, o1 = o0 + GEMM_COLS < c->n ? o0 + GEMM_COLS : c->n;
     int16_t* a = (int16_t*)malloc((r1 - r0) * c->k * sizeof(int16_t) + 1);
     for (size_t r = r0; r < r1; r++)
         for (size_t i = 0; i < c->k; i++) a[(r - r0) * c->k + i] = c->x[r * c->k + i];
-    for (size_t o = 0; o < c->n; o++)
+    for (size_t o = o0; o < o1; o++)
         for (size_t r = r0; r < r1; r++) {
             int64_t v = c->dot(a + (r - r0) * c->k, c->w + o * c->k, c->k);
             if (c->acc) c->acc[r * c->n + o] = v;
             if (c->y8) c->y8[r * c->n + o] = rq8(v, c->mant[o], c->shift[o]);
+            if (c->y32) {
+                int64_t q = kt_requant_sat(v, c->mant[o], c->shift[o]);
+                c->y32[r * c->n + o] = c->add32 ? sat32((int64_t)c->y32[r * c->n + o] + sat32(q)) : sat32(q);
+            }
         }
     free(a);
+}
+
+static int gemm_run(const int8_t* x, const int16_t* w, size_t m, size_t n, size_t k, const int32_t* mant,
+                    const int32_t* shift, int64_t* acc, int8_t* y8, int32_t* y32, int add32, size_t threads) {
+    if (k > KT_DOT16_MAX_K) return -1;
+    size_t ncb = (n + GEMM_COLS - 1) / GEMM_COLS;
+    gemm_ctx c = {x, w, m, n, k, mant, shift, acc, y8, y32, add32, dot16_pick(), ncb};
+    pool_run(gemm_task, &c, (m + GEMM_ROWS - 1) / GEMM_ROWS * ncb, threads);
+    return 0;
 }
 
 /* acc (m x n i64, optional) = x (m x k int8) . w^T (n x k int16 codes), and y8 (optional) = rq8(acc, mant[o],
  * shift[o]). Returns -1 when k exceeds the int32-exact bound. */
 int kt_gemm_i8w16(const int8_t* x, const int16_t* w, size_t m, size_t n, size_t k, const int32_t* mant,
                   const int32_t* shift, int64_t* acc, int8_t* y8, size_t threads) {
-    if (k > KT_DOT16_MAX_K) return -1;
-    gemm_ctx c = {x, w, m, n, k, mant, shift, acc, y8, dot16_pick()};
-    pool_run(gemm_task, &c, (m + GEMM_ROWS - 1) / GEMM_ROWS, threads);
-    return 0;
+    return gemm_run(x, w, m, n, k, mant, shift, acc, y8, NULL, 0, threads);
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
@@ -456,4 +474,227 @@ int kt_mlp_gelu(const int8_t* x, size_t m, size_t d, size_t dh, const int16_t* w
 void kt_gen_uniform_i32(uint64_t seed, int64_t lo, int64_t hi, size_t n, int32_t* out) {
     uint64_t s = seed ^ 0x9E3779B97F4A7C15ULL, range = (uint64_t)(hi - lo + 1);
     for (size_t i = 0; i < n; i++) out[i] = (int32_t)((int64_t)((kt_lcg_next(&s) >> 33) % range) + lo);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Config 3: a Qwen2.5-0.5B-shape decoder (this build's int8 definition of the reference's DecoderModel)           */
+/* ------------------------------------------------------------------------------------------------------------ */
+/*
+ * The reference's decoder (DecoderModel::embed_int / blocks_int / head_int / decode_step,
+ * crates/01-engine/kt-core/src/model.rs:168-188, 290-353; Attention, attention.rs; SwiGluMlp, layers.rs:609-640;
+ * generate_greedy_by, generate.rs:82-111) with int8 activations, W12 weights and per-channel requant:
+ *   residual r: int32 per hidden unit; embed: r = emb[token] (the 12-bit codes of the tied embedding row);
+ *   rmsnorm(r) -> int8: rms = isqrt(floor(sum r^2 / d)), q = clamp(div_round(32 r, rms), +-127) (0 when rms = 0),
+ *     div_round = round half away from zero;
+ *   attention block: qkv = rq8(rmsnorm(r) . Wqkv^T) (q: nh heads, then k, v: nkv heads, each hd wide);
+ *     rope at position p (rotate-half pairs i, i + hd/2): a' = sr(a C - b S, 14), b' = sr(b C + a S, 14) with the
+ *     int16 tables C = cos[p][i], S = sin[p][i] (2^14 scale), sr = round-half-away shift, clamped to +-127;
+ *     the rotated k and v are appended to the caches at p; head h (kv head g = h / (nh / nkv)) attends positions
+ *     j <= p: s_j = q . k_j, m = max s_j, e_j = EXP[(m - s_j + 64) >> 7] (0 past the 1024-entry table),
+ *     o = div_round(sum_j e_j v_j, sum_j e_j); r = sat32(r + sat32(requant(o . Wo^T, o scales)));
+ *   mlp block: g, u = rq8(rmsnorm(r) . Wgu^T) (gate rows 0..ffn-1, up ffn..2ffn-1); h = clamp(sr(SILU[g + 127] u,
+ *     h_shift)); r = sat32(r + sat32(requant(h . Wd^T, down scales)));
+ *   head: logits = sat32(requant(rmsnorm(r) . emb^T, lm scales)) (int32); greedy: the first maximum
+ *     (argmax_codes, generate.rs:48-56).
+ * Every operation is per row except attention, whose row t sees only positions <= its own: feeding a prompt as one
+ * batch or position by position (the reference's generate_greedy_by) gives the same integers.
+ */
+typedef struct {
+    int64_t d, ffn, nh, nkv, hd, layers, vocab, max_pos, h_shift;
+    const int16_t* emb;                    /* vocab x d codes; the lm_head is tied */
+    const int32_t *lm_mant, *lm_shift;     /* vocab */
+    const int16_t* wqkv;                   /* layers x (nh + 2 nkv) hd x d */
+    const int32_t *qkv_mant, *qkv_shift;   /* layers x (nh + 2 nkv) hd */
+    const int16_t* wo;                     /* layers x d x nh hd */
+    const int32_t *o_mant, *o_shift;       /* layers x d */
+    const int16_t* wgu;                    /* layers x 2 ffn x d */
+    const int32_t *gu_mant, *gu_shift;     /* layers x 2 ffn */
+    const int16_t* wd;                     /* layers x d x ffn */
+    const int32_t *d_mant, *d_shift;       /* layers x d */
+    const int16_t *rope_cos, *rope_sin;    /* max_pos x hd / 2 */
+    const int32_t* exp_tab;                /* 1024 */
+    const int16_t* silu;                   /* 255 */
+} kt_dec_model;
+
+static inline int64_t div_round(int64_t a, int64_t b) { /* b > 0, round half away from zero */
+    int64_t q = (2 * (a < 0 ? -a : a) + b) / (2 * b);
+    return a < 0 ? -q : q;
+}
+static inline int64_t shift_round(int64_t v, int s) {
+    int64_t q = ((v < 0 ? -v : v) + ((int64_t)1 << (s - 1))) >> s;
+    return v < 0 ? -q : q;
+}
+
+static void rmsnorm_rows(const int32_t* r, size_t rows, size_t d, int8_t* q) {
+    for (size_t t = 0; t < rows; t++) {
+        const int32_t* x = r + t * d;
+        uint64_t ss = 0;
+        for (size_t i = 0; i < d; i++) ss += (uint64_t)((int64_t)x[i] * x[i]);
+        int64_t rms = (int64_t)kt_isqrt_u128(0, ss / d);
+        for (size_t i = 0; i < d; i++) q[t * d + i] = rms == 0 ? 0 : (int8_t)clamp64(div_round(32 * (int64_t)x[i], rms), -127, 127);
+    }
+}
+
+/* kt_dec_forward: rows tokens[0 .. T) at positions pos0 .. pos0 + T - 1 through every layer, appending k and v to the
+ * caches (layers x max_pos x nkv x hd int8 each); logits (vocab int32, optional) of the last row. r is scratch of
+ * T x d int32. */
+void kt_dec_forward(const kt_dec_model* M, const int32_t* tokens, size_t T, size_t pos0, int8_t* kc, int8_t* vc,
+                    int32_t* logits, size_t threads) {
+    const size_t d = (size_t)M->d, ffn = (size_t)M->ffn, nh = (size_t)M->nh, nkv = (size_t)M->nkv, hd = (size_t)M->hd;
+    const size_t nq = (nh + 2 * nkv) * hd, hh = hd / 2, maxp = (size_t)M->max_pos, rep = nh / nkv;
+    int32_t* r = (int32_t*)malloc(T * d * sizeof(int32_t));
+    int8_t* xn = (int8_t*)malloc(T * (d > ffn ? ffn : d) * 2 + T * ffn);
+    int8_t* qkv = (int8_t*)malloc(T * nq);
+    int8_t* o = (int8_t*)malloc(T * nh * hd);
+    int8_t* gu = (int8_t*)malloc(T * 2 * ffn);
+    int8_t* h = (int8_t*)malloc(T * ffn);
+    int64_t* sc = (int64_t*)malloc(maxp * sizeof(int64_t));
+    for (size_t t = 0; t < T; t++)
+        for (size_t i = 0; i < d; i++) r[t * d + i] = M->emb[(size_t)tokens[t] * d + i];
+    for (size_t l = 0; l < (size_t)M->layers; l++) {
+        int8_t* kl = kc + l * maxp * nkv * hd;
+        int8_t* vl = vc + l * maxp * nkv * hd;
+        rmsnorm_rows(r, T, d, xn);
+        gemm_run(xn, M->wqkv + l * nq * d, T, nq, d, M->qkv_mant + l * nq, M->qkv_shift + l * nq, NULL, qkv, NULL, 0,
+                 threads);
+        for (size_t t = 0; t < T; t++) {
+            size_t p = pos0 + t;
+            int8_t* row = qkv + t * nq;
+            for (size_t hv = 0; hv < nh + nkv; hv++) { /* q heads then k heads */
+                int8_t* x = row + hv * hd;
+                for (size_t i = 0; i < hh; i++) {
+                    int64_t a = x[i], b = x[i + hh], C = M->rope_cos[p * hh + i], S = M->rope_sin[p * hh + i];
+                    x[i] = (int8_t)clamp64(shift_round(a * C - b * S, 14), -127, 127);
+                    x[i + hh] = (int8_t)clamp64(shift_round(b * C + a * S, 14), -127, 127);
+                }
+            }
+            memcpy(kl + p * nkv * hd, row + nh * hd, nkv * hd);
+            memcpy(vl + p * nkv * hd, row + (nh + nkv) * hd, nkv * hd);
+        }
+        for (size_t t = 0; t < T; t++) {
+            size_t p = pos0 + t;
+            for (size_t hq = 0; hq < nh; hq++) {
+                const int8_t* q = qkv + t * nq + hq * hd;
+                size_t g = hq / rep;
+                int64_t m = INT64_MIN;
+                for (size_t j = 0; j <= p; j++) {
+                    const int8_t* k = kl + (j * nkv + g) * hd;
+                    int64_t s = 0;
+                    for (size_t i = 0; i < hd; i++) s += (int64_t)q[i] * k[i];
+                    sc[j] = s;
+                    if (s > m) m = s;
+                }
+                int64_t den = 0;
+                for (size_t j = 0; j <= p; j++) {
+                    int64_t idx = (m - sc[j] + 64) >> 7;
+                    sc[j] = idx < 1024 ? M->exp_tab[idx] : 0;
+                    den += sc[j];
+                }
+                for (size_t i = 0; i < hd; i++) {
+                    int64_t acc = 0;
+                    for (size_t j = 0; j <= p; j++) acc += sc[j] * vl[(j * nkv + g) * hd + i];
+                    o[t * nh * hd + hq * hd + i] = (int8_t)clamp64(div_round(acc, den), -127, 127);
+                }
+            }
+        }
+        gemm_run(o, M->wo + l * d * nh * hd, T, d, nh * hd, M->o_mant + l * d, M->o_shift + l * d, NULL, NULL, r, 1,
+                 threads);
+        rmsnorm_rows(r, T, d, xn);
+        gemm_run(xn, M->wgu + l * 2 * ffn * d, T, 2 * ffn, d, M->gu_mant + l * 2 * ffn, M->gu_shift + l * 2 * ffn,
+                 NULL, gu, NULL, 0, threads);
+        for (size_t t = 0; t < T; t++)
+            for (size_t c = 0; c < ffn; c++) {
+                int64_t g = gu[t * 2 * ffn + c], u = gu[t * 2 * ffn + ffn + c];
+                h[t * ffn + c] = (int8_t)clamp64(shift_round(M->silu[g + 127] * u, (int)M->h_shift), -127, 127);
+            }
+        gemm_run(h, M->wd + l * d * ffn, T, d, ffn, M->d_mant + l * d, M->d_shift + l * d, NULL, NULL, r, 1, threads);
+    }
+    if (logits) {
+        rmsnorm_rows(r + (T - 1) * d, 1, d, xn);
+        gemm_run(xn, M->emb, 1, (size_t)M->vocab, d, M->lm_mant, M->lm_shift, NULL, NULL, logits, 0, threads);
+    }
+    free(r);
+    free(xn);
+    free(qkv);
+    free(o);
+    free(gu);
+    free(h);
+    free(sc);
+}
+
+/* argmax_codes (generate.rs:48-56): the first index of the maximum. */
+int64_t kt_argmax_i32(const int32_t* v, size_t n) {
+    size_t best = 0;
+    for (size_t i = 1; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return (int64_t)best;
+}
+
+/* generate_greedy_by (generate.rs:82-111) with no stop tokens: the prompt (P tokens) as one batch when `batched`,
+ * else position by position as the reference feeds it; then max_new tokens, hashing (here: returning) the logits of
+ * every step before its argmax. tokens_out: max_new ids; logits_out: max_new x vocab int32. The caches must hold
+ * P + max_new - 1 positions (max_pos). */
+int kt_dec_generate(const kt_dec_model* M, const int32_t* prompt, size_t P, size_t max_new, int batched,
+                    int32_t* tokens_out, int32_t* logits_out, size_t threads) {
+    if (P == 0 || P + max_new - 1 > (size_t)M->max_pos || M->d > KT_DOT16_MAX_K || M->ffn > KT_DOT16_MAX_K) return -1;
+    size_t cache = (size_t)M->layers * (size_t)M->max_pos * (size_t)M->nkv * (size_t)M->hd;
+    int8_t* kc = (int8_t*)calloc(cache, 1);
+    int8_t* vc = (int8_t*)calloc(cache, 1);
+    size_t V = (size_t)M->vocab;
+    if (batched) {
+        kt_dec_forward(M, prompt, P, 0, kc, vc, logits_out, threads);
+    } else {
+        for (size_t p = 0; p < P; p++) kt_dec_forward(M, prompt + p, 1, p, kc, vc, p + 1 == P ? logits_out : NULL, threads);
+    }
+    size_t pos = P;
+    for (size_t n = 0; n < max_new; n++) {
+        int32_t next = (int32_t)kt_argmax_i32(logits_out + n * V, V);
+        tokens_out[n] = next;
+        if (n + 1 < max_new) {
+            kt_dec_forward(M, &next, 1, pos, kc, vc, logits_out + (n + 1) * V, threads);
+            pos++;
+        }
+    }
+    free(kc);
+    free(vc);
+    return 0;
+}
+
+/* Per-output-channel 12-bit codes of a Gaussian matrix (config 3's "N(0, 0.02) quantized to 12-bit codes per output
+ * channel", in integers): v = round(N(0, 2^20)) on kt_gen_gauss_i32's stream, then per row
+ * code = div_round(2047 v, max_row |v|) (a zero row stays zero). */
+void kt_gen_quant_rows(uint64_t seed, size_t rows, size_t cols, int16_t* out) {
+    int32_t* v = (int32_t*)malloc(cols * sizeof(int32_t));
+    uint64_t s = seed ^ 0xD1B54A32D192ED03ULL;
+    for (size_t r = 0; r < rows; r++) {
+        int64_t mx = 0;
+        for (size_t c = 0; c < cols; c++) {
+            int64_t sum = 0;
+            for (int j = 0; j < 12; j++) sum += (int64_t)((kt_lcg_next(&s) >> 33) & 0xFFFF);
+            int64_t t = 2 * sum - 12 * 65535;
+            int64_t mag = ((t < 0 ? -t : t) * (1 << 20) + 65536) >> 17;
+            v[c] = (int32_t)(t < 0 ? -mag : mag);
+            if (mag > mx) mx = mag;
+        }
+        for (size_t c = 0; c < cols; c++) out[r * cols + c] = mx == 0 ? 0 : (int16_t)div_round(2047 * (int64_t)v[c], mx);
+    }
+    free(v);
+}
+
+/* kt_channel_scales_i16 with the accumulator's 4 sigma mapped to `target` instead of 127. */
+void kt_channel_scales_target_i16(const int16_t* w, size_t n, size_t k, int64_t sigma, int64_t target, int32_t* mant,
+                                  int32_t* shift) {
+    for (size_t o = 0; o < n; o++) {
+        uint64_t ss = 0;
+        for (size_t c = 0; c < k; c++) ss += (uint64_t)((int64_t)w[o * k + c] * w[o * k + c]);
+        uint64_t root = kt_isqrt_u128(0, ss);
+        if (root == 0) {
+            mant[o] = 0;
+            shift[o] = 0;
+            continue;
+        }
+        kt_scale s = kt_scale_to_i32(kt_scale_from_ratio(0, (uint64_t)target, 0, 4 * (uint64_t)sigma * root));
+        mant[o] = (int32_t)s.mant;
+        shift[o] = s.shift;
+    }
 }

@@ -117,6 +117,10 @@ def _declare(L: C.CDLL) -> None:
         "kt_moe_combine": (None, [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, C.c_int, _P]),
         "kt_sam_entry": (None, [_P, _SZ, _SZ, _P, _P]),
         "kt_gen_uniform_i32": (None, [C.c_uint64, C.c_int64, C.c_int64, _SZ, _P]),
+        "kt_gen_quant_rows": (None, [C.c_uint64, _SZ, _SZ, _P]),
+        "kt_channel_scales_target_i16": (None, [_P, _SZ, _SZ, C.c_int64, C.c_int64, _P, _P]),
+        "kt_argmax_i32": (C.c_int64, [_P, _SZ]),
+        "kt_dec_generate": (C.c_int, [_P, _P, _SZ, _SZ, C.c_int, _P, _P, _SZ]),
         "kt_conv2d_i8w16": (None, [_P, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _SZ]),
         "kt_mlp_gelu": (C.c_int, [_P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ]),
         "kt_moe_forward_token": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int,
@@ -607,3 +611,54 @@ def gen_uniform(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.int32)
     lib().kt_gen_uniform_i32(seed & (2**64 - 1), lo, hi, n, _ptr(out))
     return out
+
+
+def gen_quant_rows(seed: int, rows: int, cols: int) -> np.ndarray:
+    out = np.empty(rows * cols, dtype=np.int16)
+    lib().kt_gen_quant_rows(seed & (2**64 - 1), rows, cols, _ptr(out))
+    return out
+
+
+def channel_scales_target(w, n: int, k: int, sigma: int, target: int):
+    w = _c(w, np.int16)
+    mant = np.empty(n, dtype=np.int32)
+    shift = np.empty(n, dtype=np.int32)
+    lib().kt_channel_scales_target_i16(_ptr(w), n, k, sigma, target, _ptr(mant), _ptr(shift))
+    return mant, shift
+
+
+class DecModel(C.Structure):
+    """kt_dec_model of kt_oracle_layers.c."""
+
+    _fields_ = [(n, C.c_int64) for n in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab", "max_pos", "h_shift")] + [
+        (n, C.c_void_p) for n in ("emb", "lm_mant", "lm_shift", "wqkv", "qkv_mant", "qkv_shift", "wo", "o_mant",
+                                  "o_shift", "wgu", "gu_mant", "gu_shift", "wd", "d_mant", "d_shift", "rope_cos",
+                                  "rope_sin", "exp_tab", "silu")]
+
+
+def dec_model(shape: dict, arrays: dict):
+    """A DecModel over numpy arrays (kept alive in the returned pair)."""
+    keep = {}
+    m = DecModel()
+    for k in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab", "max_pos", "h_shift"):
+        setattr(m, k, int(shape[k]))
+    types = {"emb": np.int16, "wqkv": np.int16, "wo": np.int16, "wgu": np.int16, "wd": np.int16,
+             "rope_cos": np.int16, "rope_sin": np.int16, "silu": np.int16}
+    for k, _ in DecModel._fields_[9:]:
+        a = _c(arrays[k], types.get(k, np.int32))
+        keep[k] = a
+        setattr(m, k, a.ctypes.data)
+    return m, keep
+
+
+def dec_generate(shape: dict, arrays: dict, prompt, max_new: int, batched: bool = True, threads: int = 0):
+    """generate_greedy_by on the oracle decoder: (tokens max_new int32, logits max_new x vocab int32)."""
+    m, keep = dec_model(shape, arrays)
+    prompt = _c(prompt, np.int32)
+    toks = np.empty(max_new, dtype=np.int32)
+    logits = np.empty(max_new * int(shape["vocab"]), dtype=np.int32)
+    r = lib().kt_dec_generate(C.byref(m), _ptr(prompt), prompt.size, max_new, int(batched), _ptr(toks), _ptr(logits),
+                              threads)
+    if r:
+        raise ValueError("dec_generate: shape beyond the oracle's bounds")
+    return toks, logits

@@ -2,7 +2,7 @@
 (oracle/kt_oracle.c, the restated reference CPU path). The GPU tests compare the device results with these fixtures
 at full size, where recomputing the CPU answer inside a test would take too long.
 
-Run from the repository root:  python tests/golden/make_goldens.py [config1 config2 config4 config5]
+Run from the repository root:  python tests/golden/make_goldens.py [config1 config2 config3 config4 config5]
 """
 import json
 import os
@@ -64,6 +64,49 @@ def config5() -> dict:
     return c
 
 
+# BASELINE config 3 (this build's integer decoder, include/kt_hip.h): Qwen2.5-0.5B shape.
+C3 = {"d": 896, "ffn": 4864, "nh": 14, "nkv": 2, "hd": 64, "layers": 24, "vocab": 151936, "prompt": 512,
+      "max_new": 129, "w_seed": 3000, "prompt_seed": 3001, "h_shift": 8}
+
+
+def config3() -> dict:
+    """The oracle decoder (the reference's generate_greedy_by loop with a batched prefill) on the full shape: weights
+    from the oracle's generators, tables from the workload definitions; the logits of all 129 steps hashed."""
+    from tritify_amd import workloads as W
+
+    c = dict(C3)
+    d, ffn, nh, nkv, hd, L, V = (c[k] for k in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab"))
+    nq, nhd, max_pos = (nh + 2 * nkv) * hd, nh * hd, c["prompt"] + c["max_new"]
+    t = time.time()
+    a = {k: [] for k in ("wqkv", "qkv_mant", "qkv_shift", "wo", "o_mant", "o_shift", "wgu", "gu_mant", "gu_shift",
+                         "wd", "d_mant", "d_shift")}
+    for l in range(L):
+        for j, (name, n, k, key) in enumerate((("qkv", nq, d, "qkv"), ("o", d, nhd, "o"), ("gu", 2 * ffn, d, "gu"),
+                                               ("dn", d, ffn, "d"))):
+            w = O.gen_quant_rows(c["w_seed"] + 8 * l + j, n, k)
+            sig, tgt = W.DEC_SCALES[name]
+            ms = O.channel_scales_target(w, n, k, sig, tgt)
+            a[{"qkv": "wqkv", "o": "wo", "gu": "wgu", "d": "wd"}[key]].append(w)
+            a[key + "_mant"].append(ms[0])
+            a[key + "_shift"].append(ms[1])
+    arrays = {k: np.concatenate(v) for k, v in a.items()}
+    emb = O.gen_quant_rows(c["w_seed"] - 1, V, d)
+    sig, tgt = W.DEC_SCALES["lm"]
+    arrays["emb"] = emb
+    arrays["lm_mant"], arrays["lm_shift"] = O.channel_scales_target(emb, V, d, sig, tgt)
+    arrays["rope_cos"], arrays["rope_sin"] = W.rope_tables(max_pos, hd)
+    arrays["exp_tab"], arrays["silu"] = W.exp_table(), W.silu_table()
+    print(f"config3 weights: {time.time() - t:.1f}s", flush=True)
+    prompt = O.gen_uniform(c["prompt_seed"], 0, V - 1, c["prompt"])
+    t = time.time()
+    toks, logits = O.dec_generate(dict(c, max_pos=max_pos), arrays, prompt, c["max_new"])
+    print(f"config3 generate: {time.time() - t:.1f}s", flush=True)
+    c.update({"prompt_sha256": O.sha256_hex(prompt), "tokens": [int(v) for v in toks],
+              "logits_sha256": O.sha256_hex(logits), "rope_sha256": O.sha256_hex(arrays["rope_cos"]),
+              "exp_sha256": O.sha256_hex(arrays["exp_tab"])})
+    return c
+
+
 def config4() -> dict:
     """The expert-major oracle (kt_moe_layer) on the full config-4 layer: weights from the oracle's own generator
     (kt_gen_w12_i16, the kt_gen_w12 stream), tables from the workload definitions."""
@@ -105,7 +148,7 @@ def main() -> None:
     """Recompute the configs named on the command line (config1 config2 config4 config5; none = all) and keep the
     other entries of the existing file."""
     t0 = time.time()
-    want = set(sys.argv[1:]) or {"config1", "config2", "config4", "config5"}
+    want = set(sys.argv[1:]) or {"config1", "config2", "config3", "config4", "config5"}
     g = json.load(open(OUT)) if os.path.exists(OUT) else {}
     if "config1" in want:
         qx, qw = O.gen_demo(64, 1024, 1024, 42)
@@ -119,6 +162,8 @@ def main() -> None:
         g["corpus_sha256"] = O.sha256_hex(np.concatenate([O.linear_cpu(c.x, c.w, c.rows, c.out, c.k) for c in cs]))
     if "config2" in want:
         g["config2"] = config2()
+    if "config3" in want:
+        g["config3"] = config3()
     if "config4" in want:
         g["config4"] = config4()
     if "config5" in want:

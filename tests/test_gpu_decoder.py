@@ -1,0 +1,116 @@
+"""Parity of the config-3 decoder (Qwen2.5-0.5B shape) on the MI355X with the CPU oracle, through the C ABI. Run on
+a GPU box with -m gpu.
+
+The GPU path (tritify_amd.decoder: embed, RmsNorm, q/k/v W12 GEMM, RoPE + KV cache, integer attention, o GEMM into
+the residual, SwiGLU gate/up GEMM, down GEMM into the residual, lm_head, greedy argmax on the device) is compared
+with the oracle's decoder (kt_dec_generate, the reference's DecoderModel / generate_greedy_by loop,
+crates/01-engine/kt-core/src/model.rs:290-353, generate.rs:82-111): every step's logits and token byte for byte on
+a small model, eager and as a replayed HIP graph, and at the full BASELINE shape (512-token prefill, 128 greedy
+decode steps) against the fixture's logits hash.
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "goldens.json")))
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def build(cfg, w_seed, max_pos, max_rows, h_shift=8):
+    """The GPU model from the product's generators, and the same arrays for the oracle."""
+    from tritify_amd import workloads as W
+    from tritify_amd.decoder import DecoderModel
+
+    m = DecoderModel(cfg, max_pos, max_rows, h_shift)
+    a = {k: [] for k in ("wqkv", "qkv_mant", "qkv_shift", "wo", "o_mant", "o_shift", "wgu", "gu_mant", "gu_shift",
+                         "wd", "d_mant", "d_shift")}
+    for l in range(cfg["layers"]):
+        wqkv, qms, wo, oms, wgu, gms, wd, dms = W.decoder_layer_codes(l, cfg, w_seed)
+        m.set_layer(l, wqkv, qms, wo, oms, wgu, gms, wd, dms)
+        for key, w, ms in (("qkv", wqkv, qms), ("o", wo, oms), ("gu", wgu, gms), ("d", wd, dms)):
+            a[{"qkv": "wqkv", "o": "wo", "gu": "wgu", "d": "wd"}[key]].append(w.astype(np.int16))
+            a[key + "_mant"].append(ms[0])
+            a[key + "_shift"].append(ms[1])
+    arrays = {k: np.concatenate(v) for k, v in a.items()}
+    emb, lms = W.decoder_embedding_codes(cfg, w_seed)
+    m.set_embedding(emb, lms)
+    cos, sin = W.rope_tables(max_pos, cfg["hd"])
+    m.set_tables(cos, sin, W.exp_table(), W.silu_table())
+    arrays.update(emb=emb.astype(np.int16), lm_mant=lms[0], lm_shift=lms[1], rope_cos=cos, rope_sin=sin,
+                  exp_tab=W.exp_table(), silu=W.silu_table())
+    return m, arrays
+
+
+SMALL = dict(d=128, ffn=256, nh=4, nkv=2, hd=64, layers=2, vocab=1000)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_decoder_small_against_oracle(torch_dev, graph):
+    from tritify_amd import workloads as W
+
+    say(f"case: decoder small {SMALL} prompt 37, 9 tokens, graph={graph}")
+    m, arrays = build(SMALL, 500, 64, 64)
+    prompt = W.decoder_prompt(501, 37, SMALL["vocab"])
+    toks, logits = m.generate(prompt, 9, graph=graph)
+    shape = dict(SMALL, max_pos=64, h_shift=8)
+    wt, wl = O.dec_generate(shape, arrays, prompt, 9)
+    assert np.array_equal(logits.reshape(-1), wl), "logits differ from the oracle"
+    assert np.array_equal(toks, wt)
+
+
+def test_decoder_prompt_of_one_and_ragged_heads(torch_dev):
+    """A one-token prompt (prefill is a decode step) and 6 query heads over 3 kv heads."""
+    from tritify_amd import workloads as W
+
+    cfg = dict(d=192, ffn=128, nh=6, nkv=3, hd=64, layers=1, vocab=300)
+    say(f"case: decoder {cfg} prompt 1, 5 tokens")
+    m, arrays = build(cfg, 600, 16, 8)
+    prompt = W.decoder_prompt(601, 1, cfg["vocab"])
+    toks, logits = m.generate(prompt, 5)
+    wt, wl = O.dec_generate(dict(cfg, max_pos=16, h_shift=8), arrays, prompt, 5)
+    assert np.array_equal(logits.reshape(-1), wl) and np.array_equal(toks, wt)
+
+
+def test_decoder_full_config3(torch_dev):
+    """Qwen2.5-0.5B shape, 512-token prefill, 128 greedy decode steps (129 hashed logit rows),
+    decode steps replayed from one captured HIP graph."""
+    from tritify_amd import workloads as W
+
+    g3 = GOLD["config3"]
+    cfg = {k: g3[k] for k in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab")}
+    say(f"case: decoder full config 3 {cfg}")
+    m, _ = build_full(cfg, g3)
+    prompt = W.decoder_prompt(g3["prompt_seed"], g3["prompt"], cfg["vocab"])
+    assert sha(prompt) == g3["prompt_sha256"]
+    toks, logits = m.generate(prompt, g3["max_new"], graph=True)
+    assert toks.tolist() == g3["tokens"], "generated tokens differ from the CPU fixture"
+    assert sha(logits) == g3["logits_sha256"], "the logits hash differs from the CPU fixture"
+
+
+def build_full(cfg, g3):
+    from tritify_amd import workloads as W
+    from tritify_amd.decoder import DecoderModel
+
+    max_pos = g3["prompt"] + g3["max_new"]
+    m = DecoderModel(cfg, max_pos, g3["prompt"], g3["h_shift"])
+    for l in range(cfg["layers"]):
+        m.set_layer(l, *W.decoder_layer_codes(l, cfg, g3["w_seed"]))
+    m.set_embedding(*W.decoder_embedding_codes(cfg, g3["w_seed"]))
+    cos, sin = W.rope_tables(max_pos, cfg["hd"])
+    m.set_tables(cos, sin, W.exp_table(), W.silu_table())
+    return m, None

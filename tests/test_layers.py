@@ -241,3 +241,158 @@ def test_uniform_pixels_generator():
     import tritify_amd as TA
 
     assert np.array_equal(TA.gen_uniform_fast(51, 0, 255, 1_000_003), O.gen_uniform(51, 0, 255, 1_000_003))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# config 3: the decoder oracle
+
+
+def dec_arrays(cfg, w_seed, max_pos):
+    """Oracle-side model arrays (the oracle's own generators)."""
+    from tritify_amd import workloads as W
+
+    d, ffn, nh, nkv, hd, L, V = (cfg[k] for k in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab"))
+    nq, nhd = (nh + 2 * nkv) * hd, nh * hd
+    a = {k: [] for k in ("wqkv", "qkv_mant", "qkv_shift", "wo", "o_mant", "o_shift", "wgu", "gu_mant", "gu_shift",
+                         "wd", "d_mant", "d_shift")}
+    for l in range(L):
+        for j, (name, n, k, key) in enumerate((("qkv", nq, d, "qkv"), ("o", d, nhd, "o"), ("gu", 2 * ffn, d, "gu"),
+                                               ("dn", d, ffn, "d"))):
+            w = O.gen_quant_rows(w_seed + 8 * l + j, n, k)
+            sig, tgt = W.DEC_SCALES[name]
+            m, s = O.channel_scales_target(w, n, k, sig, tgt)
+            a[{"qkv": "wqkv", "o": "wo", "gu": "wgu", "d": "wd"}[key]].append(w)
+            a[key + "_mant"].append(m)
+            a[key + "_shift"].append(s)
+    arrays = {k: np.concatenate(v) for k, v in a.items()}
+    emb = O.gen_quant_rows(w_seed - 1, V, d)
+    sig, tgt = W.DEC_SCALES["lm"]
+    arrays["emb"] = emb
+    arrays["lm_mant"], arrays["lm_shift"] = O.channel_scales_target(emb, V, d, sig, tgt)
+    arrays["rope_cos"], arrays["rope_sin"] = W.rope_tables(max_pos, hd)
+    arrays["exp_tab"] = W.exp_table()
+    arrays["silu"] = W.silu_table()
+    return arrays
+
+
+TINY = dict(d=64, ffn=128, nh=2, nkv=1, hd=64, layers=2, vocab=53)
+
+
+def test_decoder_batched_prefill_equals_position_by_position():
+    """The prompt as one batch equals the reference's position-by-position feed (generate_greedy_by,
+    generate.rs:82-111): every op is per row except attention, which is causal."""
+    cfg = dict(TINY, max_pos=40, h_shift=8)
+    arrays = dec_arrays(cfg, 700, 40)
+    prompt = O.gen_uniform(701, 0, cfg["vocab"] - 1, 23)
+    t1, l1 = O.dec_generate(cfg, arrays, prompt, 9, batched=True)
+    t2, l2 = O.dec_generate(cfg, arrays, prompt, 9, batched=False)
+    assert np.array_equal(l1, l2) and np.array_equal(t1, t2)
+    assert np.array_equal(t1, l1.reshape(9, -1).argmax(axis=1))  # np.argmax is the first maximum too
+    assert len(set(l1.tolist())) > 100
+
+
+def py_decoder(cfg, a, prompt, max_new):
+    """The decoder rules in Python integers, position by position (a second statement of the oracle's definition)."""
+    d, ffn, nh, nkv, hd, L, V = (cfg[k] for k in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab"))
+    nq, hh, rep = (nh + 2 * nkv) * hd, hd // 2, nh // nkv
+
+    def dr(x, y):
+        q = (2 * abs(x) + y) // (2 * y)
+        return q if x >= 0 else -q
+
+    def sr(v, s):
+        q = (abs(v) + (1 << (s - 1))) >> s
+        return q if v >= 0 else -q
+
+    def c127(v):
+        return max(-127, min(127, v))
+
+    def s32(v):
+        return max(-(2**31), min(2**31 - 1, v))
+
+    def norm(r):
+        ss = sum(v * v for v in r)
+        import math as m_
+        rms = m_.isqrt(ss // d)
+        return [0 if rms == 0 else c127(dr(32 * v, rms)) for v in r]
+
+    def mat(name, l, n, k):
+        w = a[name].reshape(L if name != "emb" else 1, n, k)[l] if name != "emb" else a["emb"].reshape(n, k)
+        return w.astype(np.int64)
+
+    def lin(x, w, mant, shift):
+        acc = w @ np.array(x, dtype=np.int64)
+        return [py_requant(int(v), int(m), int(s)) for v, m, s in zip(acc, mant, shift)]
+
+    kc = [[None] * (len(prompt) + max_new) for _ in range(L)]
+    vc = [[None] * (len(prompt) + max_new) for _ in range(L)]
+
+    def step(tok, p):
+        r = [int(v) for v in a["emb"].reshape(V, d)[tok]]
+        for l in range(L):
+            x = norm(r)
+            qkv = [c127(v) for v in lin(x, mat("wqkv", l, nq, d), a["qkv_mant"][l * nq:(l + 1) * nq],
+                                        a["qkv_shift"][l * nq:(l + 1) * nq])]
+            for hv in range(nh + nkv):
+                seg = qkv[hv * hd:(hv + 1) * hd]
+                for i in range(hh):
+                    A, Bv = seg[i], seg[i + hh]
+                    C, S = int(a["rope_cos"][p][i]), int(a["rope_sin"][p][i])
+                    seg[i], seg[i + hh] = c127(sr(A * C - Bv * S, 14)), c127(sr(Bv * C + A * S, 14))
+                qkv[hv * hd:(hv + 1) * hd] = seg
+            kc[l][p] = qkv[nh * hd:(nh + nkv) * hd]
+            vc[l][p] = qkv[(nh + nkv) * hd:]
+            o = []
+            for h in range(nh):
+                g = h // rep
+                q = qkv[h * hd:(h + 1) * hd]
+                s = [sum(qi * ki for qi, ki in zip(q, kc[l][j][g * hd:(g + 1) * hd])) for j in range(p + 1)]
+                m = max(s)
+                e = [int(a["exp_tab"][(m - sj + 64) >> 7]) if (m - sj + 64) >> 7 < 1024 else 0 for sj in s]
+                den = sum(e)
+                for i in range(hd):
+                    o.append(c127(dr(sum(e[j] * vc[l][j][g * hd + i] for j in range(p + 1)), den)))
+            add = lin(o, mat("wo", l, d, nh * hd), a["o_mant"][l * d:(l + 1) * d], a["o_shift"][l * d:(l + 1) * d])
+            r = [s32(x_ + s32(y_)) for x_, y_ in zip(r, add)]
+            x = norm(r)
+            gu = [c127(v) for v in lin(x, mat("wgu", l, 2 * ffn, d), a["gu_mant"][l * 2 * ffn:(l + 1) * 2 * ffn],
+                                       a["gu_shift"][l * 2 * ffn:(l + 1) * 2 * ffn])]
+            hv_ = [c127(sr(int(a["silu"][gu[c] + 127]) * gu[ffn + c], cfg["h_shift"])) for c in range(ffn)]
+            add = lin(hv_, mat("wd", l, d, ffn), a["d_mant"][l * d:(l + 1) * d], a["d_shift"][l * d:(l + 1) * d])
+            r = [s32(x_ + s32(y_)) for x_, y_ in zip(r, add)]
+        lg = lin(norm(r), a["emb"].reshape(V, d).astype(np.int64), a["lm_mant"], a["lm_shift"])
+        return [s32(v) for v in lg]
+
+    for p, t in enumerate(prompt):
+        lg = step(int(t), p)
+    toks, logs = [], []
+    pos = len(prompt)
+    for n in range(max_new):
+        logs.append(lg)
+        nxt = max(range(V), key=lambda i: (lg[i], -i))
+        toks.append(nxt)
+        if n + 1 < max_new:
+            lg = step(nxt, pos)
+            pos += 1
+    return toks, logs
+
+
+def test_decoder_oracle_equals_python_restatement():
+    cfg = dict(TINY, layers=1, vocab=37, max_pos=12, h_shift=8)
+    arrays = dec_arrays(cfg, 900, 12)
+    prompt = O.gen_uniform(901, 0, cfg["vocab"] - 1, 6)
+    toks, logits = O.dec_generate(cfg, arrays, prompt, 4)
+    pt, pl = py_decoder(cfg, arrays, prompt, 4)
+    assert toks.tolist() == pt
+    assert logits.reshape(4, -1).tolist() == pl
+
+
+def test_decoder_generators_equal_the_product():
+    import tritify_amd as TA
+
+    assert np.array_equal(TA.gen_quant_rows_fast(5, 37, 300), O.gen_quant_rows(5, 37, 300).astype(np.int32))
+    w = O.gen_quant_rows(6, 50, 200)
+    assert np.abs(w.reshape(50, 200)).max(axis=1).tolist() == [2047] * 50
+    m1, s1 = TA.channel_scales_fast(w.astype(np.int32), 50, 200, 16, 2048)
+    m2, s2 = O.channel_scales_target(w, 50, 200, 16, 2048)
+    assert np.array_equal(m1, m2) and np.array_equal(s1, s2)

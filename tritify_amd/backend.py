@@ -21,7 +21,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(PKG, "libkt_hip.so")
 LIB_PLANTED = os.path.join(PKG, "libkt_hip_planted.so")
 
-OUT_I64, OUT_I32, OUT_I8 = 0, 1, 2
+OUT_I64, OUT_I32, OUT_I8, OUT_I32_ADD = 0, 1, 2, 3
 
 # kt_cuda::Plant (crates/02-runtime/kt-cuda/src/backend.rs:31-40)
 PLANT_DROP_TOP, PLANT_WRONG_CARRY, PLANT_NO_FLUSH, PLANT_CACHE_BY_SHAPE = 1, 2, 3, 4
@@ -90,10 +90,17 @@ def _declare(L: C.CDLL) -> None:
                                     _I, _I, _P, _P, _P]),
         "kt_hip_sam_patch_embed": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P,
                                         _P, _P, _P]),
+        "kt_hip_dec_embed": (_I, [_I, _P, _I64, _P, _I64, _P, _P]),
+        "kt_hip_dec_rmsnorm": (_I, [_I, _P, _I64, _I64, _P, _I64, _P]),
+        "kt_hip_dec_rope_kv": (_I, [_I, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_dec_attention": (_I, [_I, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),
+        "kt_hip_dec_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P]),
+        "kt_hip_dec_advance": (_I, [_I, _P, _I64, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
-        "kt_hip_channel_scales": (None, [_P, _SZ, _SZ, _I64, _P, _P]),
+        "kt_hip_channel_scales": (None, [_P, _SZ, _SZ, _I64, _I64, _P, _P]),
+        "kt_hip_gen_quant_rows": (None, [_U64, _SZ, _SZ, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -412,9 +419,15 @@ def gen_uniform_fast(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
     return out
 
 
-def channel_scales_fast(w: np.ndarray, n: int, k: int, sigma: int) -> tuple[np.ndarray, np.ndarray]:
+def channel_scales_fast(w: np.ndarray, n: int, k: int, sigma: int, target: int = 127) -> tuple[np.ndarray, np.ndarray]:
     w = _i32(w)
     mant = np.empty(n, dtype=np.int32)
     shift = np.empty(n, dtype=np.int32)
-    lib().kt_hip_channel_scales(w.ctypes.data, n, k, sigma, mant.ctypes.data, shift.ctypes.data)
+    lib().kt_hip_channel_scales(w.ctypes.data, n, k, sigma, target, mant.ctypes.data, shift.ctypes.data)
     return mant, shift
+
+
+def gen_quant_rows_fast(seed: int, rows: int, cols: int) -> np.ndarray:
+    out = np.empty(rows * cols, dtype=np.int32)
+    lib().kt_hip_gen_quant_rows(seed & (2**64 - 1), rows, cols, out.ctypes.data)
+    return out

@@ -1,0 +1,243 @@
+// The non-GEMM kernels of the config-3 decoder on gfx950: embedding rows, integer RMSNorm, table RoPE with the KV
+// cache append, integer-softmax attention, greedy argmax with the logits record, and the position counter. The
+// GEMMs (q/k/v, o, gate/up, down, lm_head) are the W12 kernels; this file holds what sits between them in the
+// reference's decoder (DecoderModel::blocks_int / decode_step, crates/01-engine/kt-core/src/model.rs:168-188,
+// 290-353; Attention, attention.rs; generate_greedy_by, generate.rs:82-111).
+//
+// Positions live in device memory (`pos`: the position of row 0 of the call) and advance on the device, so one
+// captured decode step replays for every position with no host involvement. The integer rules are stated with
+// kt_hip_dec_* in include/kt_hip.h.
+
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <stdint.h>
+
+#include "kt_kernels.h"
+#include "kt_w12_core.h"
+
+namespace kt {
+
+// round(a / b) half away from zero, b > 0.
+__device__ __forceinline__ int64_t div_round(int64_t a, int64_t b) {
+    const int64_t q = (2 * (a < 0 ? -a : a) + b) / (2 * b);
+    return a < 0 ? -q : q;
+}
+
+__device__ __forceinline__ int shift_round(int v, int s) {  // |v| < 2^30
+    const int q = ((v < 0 ? -v : v) + (1 << (s - 1))) >> s;
+    return v < 0 ? -q : q;
+}
+
+__device__ __forceinline__ int clamp127(int64_t v) { return (int)(v > 127 ? 127 : (v < -127 ? -127 : v)); }
+
+// floor(sqrt(n)) exactly: a double estimate, then corrected by whole steps.
+__device__ __forceinline__ uint64_t isqrt_u64(uint64_t n) {
+    uint64_t x = (uint64_t)sqrt((double)n);
+    while (x > 0 && x * x > n) x--;
+    while ((x + 1) * (x + 1) <= n) x++;
+    return x;
+}
+
+// r[t][i] = emb[tokens[t]][i] (int16 codes -> the int32 residual).
+__global__ __launch_bounds__(256) void dec_embed_kernel(const int32_t* __restrict__ tokens,
+                                                        const int16_t* __restrict__ emb, int d,
+                                                        int32_t* __restrict__ r) {
+    const int t = blockIdx.x;
+    const int16_t* e = emb + (size_t)tokens[t] * d;
+    for (int i = threadIdx.x; i < d; i += 256) r[(size_t)t * d + i] = e[i];
+}
+
+// One CTA per row: rms = isqrt(floor(sum r^2 / d)), q = clamp(div_round(32 r, rms), +-127), 0 when rms = 0. q rows
+// have stride qs (columns d .. qs - 1 are left alone).
+__global__ __launch_bounds__(256) void dec_rmsnorm_kernel(const int32_t* __restrict__ r, int d, int8_t* __restrict__ q,
+                                                          int qs) {
+    __shared__ uint64_t sw[4];
+    __shared__ int64_t s_rms;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int32_t* x = r + (size_t)t * d;
+    uint64_t ss = 0;
+    for (int i = tid; i < d; i += 256) ss += (uint64_t)((int64_t)x[i] * x[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 63) == 0) sw[tid >> 6] = ss;
+    __syncthreads();
+    if (tid == 0) s_rms = (int64_t)isqrt_u64((sw[0] + sw[1] + sw[2] + sw[3]) / (uint64_t)d);
+    __syncthreads();
+    const int64_t rms = s_rms;
+    for (int i = tid; i < d; i += 256) q[(size_t)t * qs + i] = rms == 0 ? 0 : (int8_t)clamp127(div_round(32 * (int64_t)x[i], rms));
+}
+
+// One CTA per row t (position p = pos[0] + t): rotate-half RoPE of the nh q heads and nkv k heads in place
+// (a' = sr(a C - b S, 14), b' = sr(b C + a S, 14), C/S the int16 tables at p), then k and v to the caches at p.
+__global__ __launch_bounds__(256) void dec_rope_kv_kernel(int8_t* __restrict__ qkv, int nqkv,
+                                                          const int32_t* __restrict__ pos, int nh, int nkv, int hd,
+                                                          const int16_t* __restrict__ cosT,
+                                                          const int16_t* __restrict__ sinT, int8_t* __restrict__ kc,
+                                                          int8_t* __restrict__ vc) {
+    const int t = blockIdx.x, p = pos[0] + t, hh = hd / 2;
+    int8_t* row = qkv + (size_t)t * nqkv;
+    for (int idx = threadIdx.x; idx < (nh + nkv) * hh; idx += 256) {
+        const int hv = idx / hh, i = idx - hv * hh;
+        int8_t* x = row + hv * hd;
+        const int a = x[i], b = x[i + hh], C = cosT[(size_t)p * hh + i], S = sinT[(size_t)p * hh + i];
+        const int na = clamp127(shift_round(a * C - b * S, 14)), nb = clamp127(shift_round(b * C + a * S, 14));
+        x[i] = (int8_t)na;
+        x[i + hh] = (int8_t)nb;
+        if (hv >= nh) {
+            int8_t* kr = kc + ((size_t)p * nkv + (hv - nh)) * hd;
+            kr[i] = (int8_t)na;
+            kr[i + hh] = (int8_t)nb;
+        }
+    }
+    for (int i = threadIdx.x; i < nkv * hd; i += 256) vc[(size_t)p * nkv * hd + i] = row[(nh + nkv) * hd + i];
+}
+
+// One CTA (256 threads) per (row t, q head h), hd = 64: scores s_j = q . k_j over positions j <= p (kv head
+// g = h / (nh / nkv)) into LDS, m = max, e_j = EXP[(m - s_j + 64) >> 7] (0 past 1024), then each wave sums
+// e_j v_j over a quarter of the positions with lane = dimension, and o = div_round(sum, sum e).
+__global__ __launch_bounds__(256) void dec_attention_kernel(const int8_t* __restrict__ qkv, int nqkv,
+                                                            const int32_t* __restrict__ pos,
+                                                            const int8_t* __restrict__ kc,
+                                                            const int8_t* __restrict__ vc, int nh, int nkv,
+                                                            const int32_t* __restrict__ exp_tab,
+                                                            int8_t* __restrict__ o, int max_pos) {
+    constexpr int HD = 64;
+    extern __shared__ int s_sc[];  // max_pos scores, then weights
+    __shared__ int s_red[8];
+    __shared__ int64_t s_acc[4][HD];
+    const int t = blockIdx.x / nh, h = blockIdx.x - t * nh, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int p = pos[0] + t, g = h / (nh / nkv), L = p + 1;
+    const int8_t* qr = qkv + (size_t)t * nqkv + h * HD;
+    v4i q4[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) q4[c] = *reinterpret_cast<const v4i*>(qr + 16 * c);
+    int mx = INT_MIN;
+    for (int j = tid; j < L; j += 256) {
+        const int8_t* kr = kc + ((size_t)j * nkv + g) * HD;
+        int s = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const v4i k4 = *reinterpret_cast<const v4i*>(kr + 16 * c);
+            s = __builtin_amdgcn_sdot4(q4[c].x, k4.x, s, false);
+            s = __builtin_amdgcn_sdot4(q4[c].y, k4.y, s, false);
+            s = __builtin_amdgcn_sdot4(q4[c].z, k4.z, s, false);
+            s = __builtin_amdgcn_sdot4(q4[c].w, k4.w, s, false);
+        }
+        s_sc[j] = s;
+        mx = s > mx ? s : mx;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int v = __shfl_xor(mx, d);
+        mx = v > mx ? v : mx;
+    }
+    if (lane == 0) s_red[w] = mx;
+    __syncthreads();
+    mx = s_red[0];
+#pragma unroll
+    for (int q = 1; q < 4; q++) mx = s_red[q] > mx ? s_red[q] : mx;
+    int den = 0;
+    for (int j = tid; j < L; j += 256) {
+        const int idx = (int)(((int64_t)mx - s_sc[j] + 64) >> 7);
+        const int e = idx < 1024 ? exp_tab[idx] : 0;
+        s_sc[j] = e;
+        den += e;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) den += __shfl_xor(den, d);
+    __syncthreads();  // every wave has read s_red; every weight is in LDS
+    if (lane == 0) s_red[4 + w] = den;
+    // lane = dimension; wave w takes positions w, w + 4, ...
+    int64_t acc = 0;
+    const int8_t* vb = vc + (size_t)g * HD + lane;
+    for (int j = w; j < L; j += 4) acc += (int64_t)s_sc[j] * vb[(size_t)j * nkv * HD];
+    s_acc[w][lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        const int64_t sum = s_acc[0][lane] + s_acc[1][lane] + s_acc[2][lane] + s_acc[3][lane];
+        const int64_t dn = (int64_t)s_red[4] + s_red[5] + s_red[6] + s_red[7];
+        o[(size_t)t * nh * HD + h * HD + lane] = (int8_t)clamp127(div_round(sum, dn));
+    }
+}
+
+// Greedy argmax over n int32 logits (the first maximum, argmax_codes of generate.rs:48-56), one CTA of 1024 threads:
+// token[0] = the index; the logits row is also copied to record + step[0] * n and step[0] advances (the per-step
+// logits the hash covers). record may be null.
+__global__ __launch_bounds__(1024) void dec_argmax_kernel(const int32_t* __restrict__ logits, int n,
+                                                          int32_t* __restrict__ token, int32_t* __restrict__ record,
+                                                          int32_t* __restrict__ step) {
+    __shared__ int64_t s_key[16];
+    const int tid = threadIdx.x;
+    // key = (value, -index) ordered as one signed 64-bit integer: the max key is the first maximum
+    int64_t best = INT64_MIN;
+    int32_t* rec = record ? record + (size_t)step[0] * n : nullptr;
+    for (int i = tid; i < n; i += 1024) {
+        const int32_t v = logits[i];
+        if (rec) rec[i] = v;
+        const int64_t key = ((int64_t)v << 32) | (uint32_t)(0x7FFFFFFF - i);
+        best = key > best ? key : best;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int64_t o = __shfl_xor(best, d);
+        best = o > best ? o : best;
+    }
+    if ((tid & 63) == 0) s_key[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        int64_t b = s_key[0];
+        for (int q = 1; q < 16; q++) b = s_key[q] > b ? s_key[q] : b;
+        token[0] = 0x7FFFFFFF - (int32_t)(b & 0xFFFFFFFF);
+        if (record) step[0] += 1;
+    }
+}
+
+__global__ void dec_advance_kernel(int32_t* pos, int by) {
+    if (threadIdx.x == 0) pos[0] += by;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Launchers
+// ------------------------------------------------------------------------------------------------------------------
+
+hipError_t launch_dec_embed(const int32_t* tokens, int T, const int16_t* emb, int d, int32_t* r, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    dec_embed_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(tokens, emb, d, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_rmsnorm(const int32_t* r, int T, int d, int8_t* q, int qs, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    dec_rmsnorm_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(r, d, q, qs);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_rope_kv(int8_t* qkv, int T, int nqkv, const int32_t* pos, int nh, int nkv, int hd,
+                              const int16_t* cosT, const int16_t* sinT, int8_t* kc, int8_t* vc, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    dec_rope_kv_kernel<<<dim3((unsigned)T), dim3(256), 0, s>>>(qkv, nqkv, pos, nh, nkv, hd, cosT, sinT, kc, vc);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_attention(const int8_t* qkv, int T, int nqkv, const int32_t* pos, const int8_t* kc,
+                                const int8_t* vc, int nh, int nkv, const int32_t* exp_tab, int8_t* o, int max_pos,
+                                hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    const size_t lds = (size_t)max_pos * sizeof(int);
+    dec_attention_kernel<<<dim3((unsigned)(T * nh)), dim3(256), lds, s>>>(qkv, nqkv, pos, kc, vc, nh, nkv, exp_tab, o,
+                                                                          max_pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_argmax(const int32_t* logits, int n, int32_t* token, int32_t* record, int32_t* step,
+                             hipStream_t s) {
+    dec_argmax_kernel<<<dim3(1), dim3(1024), 0, s>>>(logits, n, token, record, step);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_advance(int32_t* pos, int by, hipStream_t s) {
+    dec_advance_kernel<<<dim3(1), dim3(64), 0, s>>>(pos, by);
+    return hipGetLastError();
+}
+
+}  // namespace kt

@@ -446,11 +446,13 @@ int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
     const int64_t kp = kp_of(k);
     if (m > INT_MAX || n > INT_MAX || kp > INT_MAX) return (int)hipErrorInvalidValue;
     if (out_kind != KT_OUT_I64 && (mant_dev == nullptr || shift_dev == nullptr)) return (int)hipErrorInvalidValue;
-    if (out_kind != KT_OUT_I64 && out_kind != KT_OUT_I32 && out_kind != KT_OUT_I8) return (int)hipErrorInvalidValue;
+    if (out_kind != KT_OUT_I64 && out_kind != KT_OUT_I32 && out_kind != KT_OUT_I8 && out_kind != KT_OUT_I32_ADD)
+        return (int)hipErrorInvalidValue;
     if (kp > (m > KT_W12_SKINNY_MAX_M ? KT_W12_GEMM_MAX_K : KT_W12_SKINNY_MAX_K)) return (int)hipErrorInvalidValue;
     KT_TRY(hipSetDevice(dev));
     if (kp == 0) {
-        // an empty dot is 0; its requant is 0 as well
+        // an empty dot is 0; its requant is 0 as well (and adds nothing)
+        if (out_kind == KT_OUT_I32_ADD) return 0;
         const size_t w = out_kind == KT_OUT_I64 ? 8 : (out_kind == KT_OUT_I32 ? 4 : 1);
         return (int)hipMemsetAsync(y_dev, 0, (size_t)m * (size_t)n * w, (hipStream_t)stream);
     }
@@ -602,6 +604,60 @@ int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_de
     return (int)kt::launch_conv_patch(img_dev, lut_dev, (int)ci, (int)h, (int)w, (int)kh, (int)kw, (int)stride,
                                       (int)pad, lo_dev, nib_dev, (int)co, bias_dev, mant_dev, shift_dev, out_dev,
                                       (hipStream_t)stream);
+}
+
+// ----------------------------------------------------------------------------------------------------------------
+// Decoder (config 3)
+// ----------------------------------------------------------------------------------------------------------------
+
+int kt_hip_dec_embed(int dev, const int32_t* tokens_dev, int64_t tokens, const int16_t* emb_dev, int64_t d,
+                     int32_t* r_dev, void* stream) {
+    if (tokens < 0 || tokens > INT_MAX || d < 1 || d > INT_MAX) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_embed(tokens_dev, (int)tokens, emb_dev, (int)d, r_dev, (hipStream_t)stream);
+}
+
+int kt_hip_dec_rmsnorm(int dev, const int32_t* r_dev, int64_t tokens, int64_t d, int8_t* q_dev, int64_t q_stride,
+                       void* stream) {
+    if (tokens < 0 || tokens > INT_MAX || d < 1 || d > (1 << 20) || q_stride < d || q_stride > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_rmsnorm(r_dev, (int)tokens, (int)d, q_dev, (int)q_stride, (hipStream_t)stream);
+}
+
+int kt_hip_dec_rope_kv(int dev, int8_t* qkv_dev, int64_t tokens, int64_t nqkv, const int32_t* pos_dev, int64_t nh,
+                       int64_t nkv, int64_t hd, const int16_t* cos_dev, const int16_t* sin_dev, int8_t* kcache_dev,
+                       int8_t* vcache_dev, void* stream) {
+    if (tokens < 0 || tokens > INT_MAX || nh < 1 || nkv < 1 || hd < 2 || hd % 2 || nh % nkv ||
+        nqkv != (nh + 2 * nkv) * hd || nqkv > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_rope_kv(qkv_dev, (int)tokens, (int)nqkv, pos_dev, (int)nh, (int)nkv, (int)hd, cos_dev,
+                                       sin_dev, kcache_dev, vcache_dev, (hipStream_t)stream);
+}
+
+int kt_hip_dec_attention(int dev, const int8_t* qkv_dev, int64_t tokens, int64_t nqkv, const int32_t* pos_dev,
+                         const int8_t* kcache_dev, const int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd,
+                         const int32_t* exp_tab_dev, int8_t* o_dev, int64_t max_pos, void* stream) {
+    if (tokens < 0 || hd != 64 || nh < 1 || nkv < 1 || nh % nkv || nqkv != (nh + 2 * nkv) * hd || max_pos < 1 ||
+        max_pos > 16384 || tokens * nh > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_attention(qkv_dev, (int)tokens, (int)nqkv, pos_dev, kcache_dev, vcache_dev, (int)nh,
+                                         (int)nkv, exp_tab_dev, o_dev, (int)max_pos, (hipStream_t)stream);
+}
+
+int kt_hip_dec_argmax(int dev, const int32_t* logits_dev, int64_t n, int32_t* token_dev, int32_t* record_dev,
+                      int32_t* step_dev, void* stream) {
+    if (n < 1 || n > INT_MAX || (record_dev != nullptr && step_dev == nullptr)) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_argmax(logits_dev, (int)n, token_dev, record_dev, step_dev, (hipStream_t)stream);
+}
+
+int kt_hip_dec_advance(int dev, int32_t* pos_dev, int64_t by, void* stream) {
+    if (by < 0 || by > INT_MAX) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_advance(pos_dev, (int)by, (hipStream_t)stream);
 }
 
 int kt_hip_probe_mfma(int dev, const int8_t* a_dev, const int8_t* b_dev, int32_t* c32_dev, int32_t* c16_dev,

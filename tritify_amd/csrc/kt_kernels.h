@@ -32,6 +32,16 @@ hipError_t launch_moe_combine(const int8_t* d, const int32_t* off, const int32_t
 hipError_t launch_conv_patch(const uint8_t* img, const int8_t* lut, int CI, int H, int W, int KH, int KW, int S, int P,
                              const int8_t* wlo, const uint8_t* wnib, int CO, const int32_t* bias, const int32_t* mant,
                              const int32_t* shift, int8_t* out, hipStream_t s);
+hipError_t launch_dec_embed(const int32_t* tokens, int T, const int16_t* emb, int d, int32_t* r, hipStream_t s);
+hipError_t launch_dec_rmsnorm(const int32_t* r, int T, int d, int8_t* q, int qs, hipStream_t s);
+hipError_t launch_dec_rope_kv(int8_t* qkv, int T, int nqkv, const int32_t* pos, int nh, int nkv, int hd,
+                              const int16_t* cosT, const int16_t* sinT, int8_t* kc, int8_t* vc, hipStream_t s);
+hipError_t launch_dec_attention(const int8_t* qkv, int T, int nqkv, const int32_t* pos, const int8_t* kc,
+                                const int8_t* vc, int nh, int nkv, const int32_t* exp_tab, int8_t* o, int max_pos,
+                                hipStream_t s);
+hipError_t launch_dec_argmax(const int32_t* logits, int n, int32_t* token, int32_t* record, int32_t* step,
+                             hipStream_t s);
+hipError_t launch_dec_advance(int32_t* pos, int by, hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

@@ -222,8 +222,9 @@ __device__ __forceinline__ void store_w12(void* y, size_t idx, int s_lo, int s_h
             if (sh <= 0) q = (int64_t)(prod << (-sh));
             else q = (int64_t)((prod + ((uint64_t)1 << (sh - 1))) >> sh);  // sh <= 63: prod < 2^62
             if (v < 0) q = -q;
-            if constexpr (OUT == KT_OUT_I32) {
+            if constexpr (OUT == KT_OUT_I32 || OUT == KT_OUT_I32_ADD) {
                 q = q > INT32_MAX ? INT32_MAX : (q < INT32_MIN ? INT32_MIN : q);
+                if constexpr (OUT == KT_OUT_I32_ADD) q = sat_add32(reinterpret_cast<int32_t*>(y)[idx], q);
                 reinterpret_cast<int32_t*>(y)[idx] = (int32_t)q;
             } else {
                 q = q > 127 ? 127 : (q < -127 ? -127 : q);
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
                 for (int t = 0; t < 16 && n + t < N; t++) dst[t] = b[t];
             }
         }
-    } else if constexpr (OUT == KT_OUT_I32 && SMALL) {
+    } else if constexpr ((OUT == KT_OUT_I32 || OUT == KT_OUT_I32_ADD) && SMALL) {
 #pragma unroll
         for (int j = 0; j < WTN; j++) {
             const int n = n0 + wave * 32 * WTN + j * 32 + (lane & 31);
@@ -348,7 +349,10 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3), m = m0 + rt;
                     const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
                     const int32_t o = col_requant<true>(v, q);
-                    if (full || (m < M && n < N)) reinterpret_cast<int32_t*>(y)[(size_t)m * N + n] = o;
+                    if (full || (m < M && n < N)) {
+                        int32_t* p = reinterpret_cast<int32_t*>(y) + (size_t)m * N + n;
+                        *p = OUT == KT_OUT_I32_ADD ? sat_add32(*p, o) : o;
+                    }
                 }
         }
     } else {
@@ -484,6 +488,10 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
                 const size_t idx = (size_t)m * N + on;
                 if constexpr (OUT == KT_OUT_I64) reinterpret_cast<int64_t*>(y)[idx] = vi;
                 else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
+                else if constexpr (OUT == KT_OUT_I32_ADD) {
+                    int32_t* p = reinterpret_cast<int32_t*>(y) + idx;
+                    *p = sat_add32(*p, col_requant<true>(vi, cq));
+                }
                 else {
                     const int q = col_requant<false>(vi, cq);
                     reinterpret_cast<int8_t*>(y)[idx] = lut ? lut[q + 127] : (int8_t)q;
@@ -604,6 +612,7 @@ hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* n
     switch (out_kind) {
         case KT_OUT_I64: return w12_linear_out<KT_OUT_I64>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         case KT_OUT_I32: return w12_linear_out<KT_OUT_I32>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
+        case KT_OUT_I32_ADD: return w12_linear_out<KT_OUT_I32_ADD>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         case KT_OUT_I8: return w12_linear_out<KT_OUT_I8>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         default: return hipErrorInvalidValue;
     }

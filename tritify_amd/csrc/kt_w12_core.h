@@ -114,6 +114,12 @@ __device__ __forceinline__ int64_t requant_dev(int64_t acc, int64_t mant, int sh
     return neg ? -(int64_t)q : (int64_t)q;
 }
 
+// a + b saturated to int32 (a residual add: the stored value plus a requantized output).
+__device__ __forceinline__ int32_t sat_add32(int32_t a, int64_t b) {
+    const int64_t v = (int64_t)a + b;
+    return (int32_t)(v > INT32_MAX ? INT32_MAX : (v < INT32_MIN ? INT32_MIN : v));
+}
+
 template <int OUT>
 __device__ __forceinline__ void store_out(void* y, size_t idx, int64_t v, const int32_t* mant, const int32_t* shift,
                                           int n) {
@@ -121,8 +127,9 @@ __device__ __forceinline__ void store_out(void* y, size_t idx, int64_t v, const 
         reinterpret_cast<int64_t*>(y)[idx] = v;
     } else {
         int64_t q = requant_dev(v, mant[n], shift[n]);
-        if constexpr (OUT == KT_OUT_I32) {
+        if constexpr (OUT == KT_OUT_I32 || OUT == KT_OUT_I32_ADD) {
             q = q > INT32_MAX ? INT32_MAX : (q < INT32_MIN ? INT32_MIN : q);
+            if constexpr (OUT == KT_OUT_I32_ADD) q = sat_add32(reinterpret_cast<int32_t*>(y)[idx], q);
             reinterpret_cast<int32_t*>(y)[idx] = (int32_t)q;
         } else {
             q = q > 127 ? 127 : (q < -127 ? -127 : q);

@@ -104,7 +104,8 @@ void kt_hip_gen_uniform(uint64_t seed, int64_t lo, int64_t hi, size_t n, int32_t
     });
 }
 
-void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, int32_t* mant, int32_t* shift) {
+void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, int64_t target, int32_t* mant,
+                           int32_t* shift) {
     parallel_for(n, 64, [&](size_t b, size_t e) {
         for (size_t o = b; o < e; o++) {
             uint64_t ss = 0;
@@ -114,8 +115,8 @@ void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, 
                 mant[o] = 0, shift[o] = 0;
                 continue;
             }
-            // Scale::from_ratio(127, 4 * sigma * root) (kt-int/src/lib.rs:191-212), then an int32 mantissa
-            unsigned __int128 num = 127, den = (unsigned __int128)(4 * (uint64_t)sigma) * root;
+            // Scale::from_ratio(target, 4 * sigma * root) (kt-int/src/lib.rs:191-212), then an int32 mantissa
+            unsigned __int128 num = (unsigned __int128)target, den = (unsigned __int128)(4 * (uint64_t)sigma) * root;
             while (bits128(num) > 64 || bits128(den) > 64) num >>= 1, den >>= 1;
             if (den == 0) den = 1;
             int s = 31 - (bits128(num) - bits128(den));
@@ -128,6 +129,33 @@ void kt_hip_channel_scales(const int32_t* w, size_t n, size_t k, int64_t sigma, 
             }
             while (m >= ((unsigned __int128)1 << 31)) m = (m + 1) >> 1, s -= 1;
             mant[o] = (int32_t)m, shift[o] = s;
+        }
+    });
+}
+
+void kt_hip_gen_quant_rows(uint64_t seed, size_t rows, size_t cols, int32_t* out) {
+    const uint64_t s0 = seed ^ 0xD1B54A32D192ED03ULL;
+    parallel_for(rows, 16, [&](size_t b, size_t e) {
+        uint64_t s = lcg_jump(s0, 12 * (uint64_t)b * cols);
+        for (size_t r = b; r < e; r++) {
+            int32_t* v = out + r * cols;
+            int64_t mx = 0;
+            for (size_t c = 0; c < cols; c++) {
+                int64_t sum = 0;
+                for (int j = 0; j < 12; j++) sum += (int64_t)((lcg(s) >> 33) & 0xFFFF);
+                const int64_t t = 2 * sum - 12 * 65535;
+                const int64_t mag = ((t < 0 ? -t : t) * (1 << 20) + 65536) >> 17;
+                v[c] = (int32_t)(t < 0 ? -mag : mag);
+                mx = mag > mx ? mag : mx;
+            }
+            for (size_t c = 0; c < cols; c++) {
+                if (mx == 0) {
+                    v[c] = 0;
+                    continue;
+                }
+                const int64_t a = 2047 * (int64_t)v[c], q = (2 * (a < 0 ? -a : a) + mx) / (2 * mx);
+                v[c] = (int32_t)(a < 0 ? -q : q);
+            }
         }
     });
 }

@@ -247,3 +247,62 @@ def sam_mlp_inputs(tokens: int, dim: int, hidden: int, x_seed: int, wi_seed: int
     im, is_ = B.channel_scales_fast(wi, hidden, dim, sigma_x)
     om, os_ = B.channel_scales_fast(wo, dim, hidden, sigma_h)
     return x, wi, wo, im, is_, om, os_
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Config 3: a Qwen2.5-0.5B-shape decoder (this build's integer definition; include/kt_hip.h states the rules)
+
+DEC_FULL = dict(d=896, ffn=4864, nh=14, nkv=2, hd=64, layers=24, vocab=151936)
+DEC_RUN = dict(prompt=512, max_new=129, w_seed=3000, prompt_seed=3001, h_shift=8)
+# per-channel scale rule of each projection: (sigma of its int8 input, the value 4 sigma of the accumulator maps to)
+DEC_SCALES = dict(qkv=(32, 127), o=(16, 16384), gu=(32, 127), dn=(16, 16384), lm=(32, 1 << 20))
+
+
+def rope_tables(max_pos: int, hd: int = 64, theta: float = 1.0e6):
+    """int16 cos / sin tables [max_pos][hd / 2] at 2^14: round(2^14 cos(p theta^(-2i / hd))) (Qwen2's rotary
+    embedding, rope_theta = 1e6)."""
+    hh = hd // 2
+    cos = np.empty((max_pos, hh), dtype=np.int16)
+    sin = np.empty((max_pos, hh), dtype=np.int16)
+    for i in range(hh):
+        f = theta ** (-2.0 * i / hd)
+        for p in range(max_pos):
+            a = p * f
+            cos[p, i] = _round_half_away(16384.0 * math.cos(a))
+            sin[p, i] = _round_half_away(16384.0 * math.sin(a))
+    return cos, sin
+
+
+def exp_table() -> np.ndarray:
+    """1024 int32 softmax weights: round(2^15 exp(-i / 64)); a score gap of m - s (q and k at 32 codes per unit, so
+    m - s = 8192 per unit of logit / sqrt(64)) reads entry (m - s + 64) >> 7."""
+    return np.array([_round_half_away(32768.0 * math.exp(-i / 64.0)) for i in range(1024)], dtype=np.int32)
+
+
+def decoder_layer_codes(l: int, cfg: dict, w_seed: int):
+    """Layer l's codes (per-row quantized Gaussians) and per-channel scales: qkv, o, gate/up (gate rows first), down."""
+    from . import backend as B
+
+    d, ffn, nq, nhd = cfg["d"], cfg["ffn"], (cfg["nh"] + 2 * cfg["nkv"]) * cfg["hd"], cfg["nh"] * cfg["hd"]
+    out = []
+    for j, (name, n, k) in enumerate((("qkv", nq, d), ("o", d, nhd), ("gu", 2 * ffn, d), ("dn", d, ffn))):
+        w = B.gen_quant_rows_fast(w_seed + 8 * l + j, n, k)
+        sig, tgt = DEC_SCALES[name]
+        out += [w, B.channel_scales_fast(w, n, k, sig, tgt)]
+    return out
+
+
+def decoder_embedding_codes(cfg: dict, w_seed: int):
+    """The tied embedding / lm_head codes (vocab x d) and the lm_head's per-row scales."""
+    from . import backend as B
+
+    w = B.gen_quant_rows_fast(w_seed - 1, cfg["vocab"], cfg["d"])
+    sig, tgt = DEC_SCALES["lm"]
+    return w, B.channel_scales_fast(w, cfg["vocab"], cfg["d"], sig, tgt)
+
+
+def decoder_prompt(seed: int, n: int, vocab: int) -> np.ndarray:
+    """n token ids uniform in [0, vocab)."""
+    from . import backend as B
+
+    return B.gen_uniform_fast(seed, 0, vocab - 1, n)
