@@ -9,6 +9,8 @@ launch finds them in the Infinity Cache. Every configuration's result is checked
 hashes the CPU oracle produced (tests/golden/goldens.json) before anything is timed.
 
 Also measured, each under "configs" (skip with --configs):
+  3  a Qwen2.5-0.5B-shape decoder: 512-token prefill, then 128 greedy decode steps replayed from one captured HIP
+     graph -- decode tokens/s (BASELINE's second metric), prefill tokens/s, the weight bandwidth of a decode step.
   4  one MoE layer, GLM-4.5-Air shape (4096 tokens, H 4096, 128 experts top-8 + 1 shared, F 1408): route, bucket,
      the ragged grouped W12 GEMMs (gate/up with the SwiGLU epilogue, down), combine; per-stage times.
   5  SAM 2.1 Hiera-B+ encoder GEMMs: the 1024 x 1024 x 3 patch embed as an im2col-fused W12 GEMM (M 65,536, K 147,
@@ -21,7 +23,7 @@ Prints one JSON line on stdout (progress goes to stderr):
   cpu_baseline  the reference's multithreaded CPU integer path (the oracle's restatement of linear_cpu, AVX-512
              variant when the host has it) on the same M = 2048 workload, timed on this host's cores
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,4]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,3,4,5]
 """
 from __future__ import annotations
 
@@ -338,6 +340,118 @@ def bench_config5(torch, args) -> dict:
     }
 
 
+def bench_config3(torch, args) -> dict:
+    from tritify_amd import workloads as W
+    from tritify_amd.decoder import DecoderModel
+
+    g3 = gold()["config3"]
+    cfg = {k: g3[k] for k in ("d", "ffn", "nh", "nkv", "hd", "layers", "vocab")}
+    P, max_new = g3["prompt"], g3["max_new"]
+    max_pos = P + max_new
+    log(f"bench: config 3: generating and packing the decoder ({cfg['layers']} layers, vocab {cfg['vocab']})")
+    t0 = time.perf_counter()
+    m = DecoderModel(cfg, max_pos, P, g3["h_shift"])
+    layers = []
+    for l in range(cfg["layers"]):
+        codes = W.decoder_layer_codes(l, cfg, g3["w_seed"])
+        m.set_layer(l, *codes)
+        layers.append(codes)
+    emb = W.decoder_embedding_codes(cfg, g3["w_seed"])
+    m.set_embedding(*emb)
+    cos, sin = W.rope_tables(max_pos, cfg["hd"])
+    m.set_tables(cos, sin, W.exp_table(), W.silu_table())
+    prompt = W.decoder_prompt(g3["prompt_seed"], P, cfg["vocab"])
+    log(f"bench: config 3: weights resident in {time.perf_counter() - t0:.1f}s")
+    toks, logits = m.generate(prompt, max_new, graph=True)
+    if toks.tolist() != g3["tokens"] or sha(logits) != g3["logits_sha256"]:
+        raise SystemExit("bench: config 3: the generation differs from the CPU fixture")
+    log("bench: config 3: bit-exact vs the CPU fixture (129 logit rows); timing")
+
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    graph = m.capture_decode_step()
+    reps = 3
+    pre_ms, dec_ms, eager_ms = [], [], []
+    for _ in range(reps):
+        m.pos.zero_()
+        m.step.zero_()
+        m.tok_in[:P] = torch.from_numpy(prompt).cuda()
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        m.forward(m.tok_in, P, stream)
+        m.argmax(stream)
+        ev[1].record(stream)
+        for _ in range(max_new - 1):
+            graph.replay()
+        ev[2].record(stream)
+        torch.cuda.synchronize()
+        pre_ms.append(ev[0].elapsed_time(ev[1]))
+        dec_ms.append(ev[1].elapsed_time(ev[2]))
+    # eager decode (one launch per kernel from the host) for comparison
+    m.pos.zero_()
+    m.step.zero_()
+    m.forward(m.tok_in, P, stream)
+    m.argmax(stream)
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for _ in range(max_new - 1):
+        m.decode_step(stream)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    eager_ms = ev[0].elapsed_time(ev[1])
+    steps = max_new - 1
+    dec = min(dec_ms)
+    wbytes = 1.5 * (cfg["layers"] * (((cfg["nh"] + 2 * cfg["nkv"]) * cfg["hd"] + cfg["nh"] * cfg["hd"]) * cfg["d"] +
+                                     3 * cfg["ffn"] * cfg["d"]) + cfg["vocab"] * cfg["d"])
+    res = {
+        "workload": f"config 3: Qwen2.5-0.5B-shape decoder (d {cfg['d']}, ffn {cfg['ffn']}, {cfg['nh']}/{cfg['nkv']} "
+                    f"heads, {cfg['layers']} layers, vocab {cfg['vocab']}), W12 weights ({wbytes / 1e6:.0f} MB), "
+                    f"{P}-token prefill then {steps} greedy decode steps",
+        "bit_exact": True,
+        "decode_tokens_per_s": round(steps / (dec * 1e-3), 1),
+        "decode_us_per_token": round(dec * 1e3 / steps, 1),
+        "decode_weight_gbs": round(wbytes / (dec * 1e-3 / steps) / 1e9, 1),
+        "decode_hbm_frac": round(wbytes / (dec * 1e-3 / steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_eager_tokens_per_s": round(steps / (eager_ms * 1e-3), 1),
+        "prefill_ms": round(min(pre_ms), 3),
+        "prefill_tokens_per_s": round(P / (min(pre_ms) * 1e-3), 0),
+        "decode": "one captured HIP graph per step, replayed; positions and tokens stay on the device",
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_decoder(cfg, layers, emb, cos, sin, prompt, g3["h_shift"])
+    return res
+
+
+def cpu_baseline_decoder(cfg, layers, emb, cos, sin, prompt, h_shift) -> dict:
+    """The oracle's restatement of the reference decoder loop (generate_greedy_by, generate.rs:82-111) on a bounded
+    sample: a 32-token prompt and 4 greedy decode steps, on this host's cores."""
+    from oracle import oracle as O
+    from tritify_amd import workloads as W
+
+    a = {k: [] for k in ("wqkv", "qkv_mant", "qkv_shift", "wo", "o_mant", "o_shift", "wgu", "gu_mant", "gu_shift",
+                         "wd", "d_mant", "d_shift")}
+    for wqkv, qms, wo, oms, wgu, gms, wd, dms in layers:
+        for key, w, ms in (("qkv", wqkv, qms), ("o", wo, oms), ("gu", wgu, gms), ("d", wd, dms)):
+            a[{"qkv": "wqkv", "o": "wo", "gu": "wgu", "d": "wd"}[key]].append(w.astype(np.int16))
+            a[key + "_mant"].append(ms[0])
+            a[key + "_shift"].append(ms[1])
+    arrays = {k: np.concatenate(v) for k, v in a.items()}
+    arrays.update(emb=emb[0].astype(np.int16), lm_mant=emb[1][0], lm_shift=emb[1][1], rope_cos=cos, rope_sin=sin,
+                  exp_tab=W.exp_table(), silu=W.silu_table())
+    cores = cpu_threads()
+    shape = dict(cfg, max_pos=cos.shape[0], h_shift=h_shift)
+    O.dec_generate(shape, arrays, prompt[:32], 1, threads=cores)  # prefill only
+    t0 = time.perf_counter()
+    O.dec_generate(shape, arrays, prompt[:32], 5, threads=cores)
+    t1 = time.perf_counter()
+    O.dec_generate(shape, arrays, prompt[:32], 1, threads=cores)
+    t2 = time.perf_counter()
+    dt = (t1 - t0) - (t2 - t1)  # the 4 decode steps alone
+    return {"value": round(4 / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"4 greedy decode steps after a 32-token prompt through the oracle's restatement of the "
+                      f"reference decoder loop (int16 weights, threaded GEMV), {dt * 1e3 / 4:.1f} ms/token"}
+
+
 def cpu_baseline_moe(g4: dict, x: np.ndarray, r: np.ndarray) -> dict:
     """The reference's MoE loop (MoeMlp::forward_routed, layers.rs:988-1020: token by token, each chosen expert and
     the shared expert on one row) restated by the oracle, on a bounded sample of tokens; single-threaded."""
@@ -376,7 +490,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--configs", type=str, default="2,4,5", help="comma-separated configs to run (2 is the headline)")
+    ap.add_argument("--configs", type=str, default="2,3,4,5", help="comma-separated configs to run (2 is the headline)")
     ap.add_argument("--ms", type=str, default="", help="comma-separated subset of config-2 M to run (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -408,6 +522,9 @@ def main() -> int:
             torch.cuda.empty_cache()
         if c == "5":
             extra["5"] = bench_config5(torch, args)
+            torch.cuda.empty_cache()
+        if c == "3":
+            extra["3"] = bench_config3(torch, args)
             torch.cuda.empty_cache()
 
     if headline is None:

@@ -93,8 +93,10 @@ __global__ __launch_bounds__(256) void dec_rope_kv_kernel(int8_t* __restrict__ q
 }
 
 // One CTA (256 threads) per (row t, q head h), hd = 64: scores s_j = q . k_j over positions j <= p (kv head
-// g = h / (nh / nkv)) into LDS, m = max, e_j = EXP[(m - s_j + 64) >> 7] (0 past 1024), then each wave sums
-// e_j v_j over a quarter of the positions with lane = dimension, and o = div_round(sum, sum e).
+// g = h / (nh / nkv)) into LDS, m = max, e_j = EXP[(m - s_j + 64) >> 7] (0 past 1024), then sum_j e_j v_j with four
+// threads per v row (16 dimensions each, 16-byte loads) and 64 rows in flight, the 64 row groups summed through
+// LDS, and o = div_round(sum, sum e). The partial sums fit int32: each thread adds at most max_pos / 64 <= 256
+// products of |e| <= 2^15 and |v| <= 127.
 __global__ __launch_bounds__(256) void dec_attention_kernel(const int8_t* __restrict__ qkv, int nqkv,
                                                             const int32_t* __restrict__ pos,
                                                             const int8_t* __restrict__ kc,
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(256) void dec_attention_kernel(const int8_t* __rest
     constexpr int HD = 64;
     extern __shared__ int s_sc[];  // max_pos scores, then weights
     __shared__ int s_red[8];
-    __shared__ int64_t s_acc[4][HD];
+    __shared__ int s_part[64][HD + 1];
     const int t = blockIdx.x / nh, h = blockIdx.x - t * nh, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int p = pos[0] + t, g = h / (nh / nkv), L = p + 1;
     const int8_t* qr = qkv + (size_t)t * nqkv + h * HD;
@@ -145,18 +147,29 @@ __global__ __launch_bounds__(256) void dec_attention_kernel(const int8_t* __rest
     }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) den += __shfl_xor(den, d);
-    __syncthreads();  // every wave has read s_red; every weight is in LDS
+    __syncthreads();  // every wave has read s_red[0..3]; every weight is in LDS
     if (lane == 0) s_red[4 + w] = den;
-    // lane = dimension; wave w takes positions w, w + 4, ...
-    int64_t acc = 0;
-    const int8_t* vb = vc + (size_t)g * HD + lane;
-    for (int j = w; j < L; j += 4) acc += (int64_t)s_sc[j] * vb[(size_t)j * nkv * HD];
-    s_acc[w][lane] = acc;
+    // thread (row group rg, 16-dimension chunk c): rows rg, rg + 64, ...
+    const int c = tid & 3, rg = tid >> 2;
+    int acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0;
+    const int8_t* vb = vc + (size_t)g * HD + 16 * c;
+    for (int j = rg; j < L; j += 64) {
+        const v4i v = *reinterpret_cast<const v4i*>(vb + (size_t)j * nkv * HD);
+        const int e = s_sc[j];
+        const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] += e * b[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) s_part[rg][16 * c + i] = acc[i];
     __syncthreads();
-    if (w == 0) {
-        const int64_t sum = s_acc[0][lane] + s_acc[1][lane] + s_acc[2][lane] + s_acc[3][lane];
+    if (tid < HD) {
+        int64_t sum = 0;
+        for (int q = 0; q < 64; q++) sum += s_part[q][tid];
         const int64_t dn = (int64_t)s_red[4] + s_red[5] + s_red[6] + s_red[7];
-        o[(size_t)t * nh * HD + h * HD + lane] = (int8_t)clamp127(div_round(sum, dn));
+        o[(size_t)t * nh * HD + h * HD + tid] = (int8_t)clamp127(div_round(sum, dn));
     }
 }
 
