@@ -193,6 +193,16 @@ int kt_hip_w12_grouped_linear(int dev, const int8_t* x_dev, int64_t x_rows, cons
                               const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride,
                               int32_t* off_dev, void* stream);
 
+/* The SwiGLU MLP's gate/up product for a dense batch (SwiGluMlp::forward_int, crates/01-engine/kt-core/src/
+ * layers.rs:609-640, with this build's int8 epilogue): x (m x kp(k) int8) against a gate/up matrix packed by
+ * kt_hip_w12_pack_gate_up (2 ffn x k), y (m rows of stride y_stride int8) = clamp(requant(silu[gq + 127] * uq, 1,
+ * h_shift)) with gq, uq the per-channel int8 requant of the gate and up rows (scales in natural order, 2 ffn).
+ * m <= KT_W12_SKINNY_MAX_M runs the bandwidth-bound skinny kernel, longer batches the MFMA tile kernel.
+ * ffn a multiple of 64, 1 <= k <= 8128. */
+int kt_hip_w12_swiglu(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                      int64_t ffn, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
+                      const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride, void* stream);
+
 /* MoeMlp::combine (layers.rs:893-923) plus the shared expert: out (T x H int8) from d (rows in bucket order, H
  * columns), off (groups + 1, from the grouped GEMM), sel, cw, pos. */
 int kt_hip_moe_combine(int dev, const int8_t* d_dev, const int32_t* off_dev, const int32_t* sel_dev,
@@ -268,6 +278,22 @@ int kt_hip_dec_argmax(int dev, const int32_t* logits_dev, int64_t n, int32_t* to
                       int32_t* step_dev, void* stream);
 /* pos_dev[0] += by. */
 int kt_hip_dec_advance(int dev, int32_t* pos_dev, int64_t by, void* stream);
+/* One decode step's attention (one row at p = pos) with its RoPE and KV append fused: the same integers as
+ * kt_hip_dec_rope_kv followed by kt_hip_dec_attention with tokens = 1 (qkv_dev is read, not rotated in place). */
+int kt_hip_dec_attention_step(int dev, const int8_t* qkv_dev, const int32_t* pos_dev, int8_t* kcache_dev,
+                              int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd, const int16_t* cos_dev,
+                              const int16_t* sin_dev, const int32_t* exp_tab_dev, int8_t* o_dev, int64_t max_pos,
+                              void* stream);
+/* The greedy argmax in two stages for a replayable decode step. Stage 1: nparts CTAs reduce the n logits to nparts
+ * keys (part_dev, uint64 each; the largest key is the first maximum), copy the logits to record_dev + step * n
+ * (record_dev optional) and advance pos_dev by `advance` (pos_dev optional). Stage 2, fused with the next step's
+ * embedding: token = the best key's index (written to token_dev when non-null), r_dev = emb[token], step += 1
+ * (step_dev optional). */
+int kt_hip_dec_argmax_part(int dev, const int32_t* logits_dev, int64_t n, uint64_t* part_dev, int64_t nparts,
+                           int32_t* record_dev, const int32_t* step_dev, int32_t* pos_dev, int64_t advance,
+                           void* stream);
+int kt_hip_dec_embed_argmax(int dev, const uint64_t* part_dev, int64_t nparts, const int16_t* emb_dev, int64_t d,
+                            int32_t* r_dev, int32_t* token_dev, int32_t* step_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Synthetic workload generators (host only, no GPU): the BASELINE configs' integer samplers on the reference LCG

@@ -114,3 +114,34 @@ def build_full(cfg, g3):
     cos, sin = W.rope_tables(max_pos, cfg["hd"])
     m.set_tables(cos, sin, W.exp_table(), W.silu_table())
     return m, None
+
+
+@pytest.mark.parametrize("m", [1, 20, 50, 100, 129, 300])
+def test_w12_swiglu_every_path(torch_dev, m):
+    """The dense SwiGLU gate/up product on each skinny tile count (m <= 16, 32, 64, 128) and on the MFMA tile path,
+    against the oracle's GEMM and the SwiGLU rule."""
+    import tritify_amd as TA
+    from tritify_amd import workloads as W
+
+    torch = torch_dev
+    ffn, k = 192, 320
+    say(f"case: w12 swiglu m={m} ffn={ffn} k={k}")
+    x = W.gen_act_gauss(1300 + m, 40, m * k)
+    w = W.gen_w12(1301, 2 * ffn * k)
+    mant, shift = W.channel_scales(w, 2 * ffn, k, 40)
+    silu = W.silu_table()
+    lo_b, nib_b = TA.w12_bytes(2 * ffn, k)
+    lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
+    nib = torch.empty(nib_b, dtype=torch.uint8, device="cuda")
+    TA.w12_pack_gate_up(torch.from_numpy(w).cuda(), ffn, k, lo, nib)
+    y = torch.full((m * (ffn + 16),), 55, dtype=torch.int8, device="cuda")
+    TA.w12_swiglu(torch.from_numpy(W.pad_k(x, m, k)).cuda(), lo, nib, m, ffn, k, torch.from_numpy(mant).cuda(),
+                  torch.from_numpy(shift).cuda(), torch.from_numpy(silu).cuda(), 8, y, ffn + 16)
+    torch.cuda.synchronize()
+    _, gu = O.gemm_i8w16(x.astype(np.int8), w.astype(np.int16), m, 2 * ffn, k, mant, shift)
+    gu = gu.reshape(m, 2 * ffn).astype(np.int64)
+    hv = silu.astype(np.int64)[gu[:, :ffn] + 127] * gu[:, ffn:]
+    want = np.clip(np.sign(hv) * ((np.abs(hv) + 128) >> 8), -127, 127).astype(np.int8)
+    got = y.cpu().numpy().reshape(m, ffn + 16)
+    assert np.array_equal(got[:, :ffn], want), "swiglu differs"
+    assert (got[:, ffn:] == 55).all(), "wrote past the row"

@@ -84,6 +84,7 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_moe_bucket": (_I, [_I, _P, _I64, _I64, _I, _P, _P, _P, _P]),
         "kt_hip_w12_grouped_linear": (_I, [_I, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I,
                                            _P, _I, _P, _I64, _P, _P]),
+        "kt_hip_w12_swiglu": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _P, _I64, _P]),
         "kt_hip_moe_combine": (_I, [_I, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P]),
         "kt_hip_moe_workspace": (_I, [_I64, _I64, _I64, _I64, _I, C.POINTER(_SZ), C.POINTER(_SZ)]),
         "kt_hip_moe_forward": (_I, [_I, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -96,6 +97,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_dec_attention": (_I, [_I, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),
         "kt_hip_dec_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P]),
         "kt_hip_dec_advance": (_I, [_I, _P, _I64, _P]),
+        "kt_hip_dec_attention_step": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+        "kt_hip_dec_argmax_part": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
+        "kt_hip_dec_embed_argmax": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
@@ -349,6 +353,14 @@ def w12_grouped_linear(x_dev, x_rows: int, list_dev, list_stride: int, count_dev
                                         _stream(stream)),
         "w12 grouped linear",
     )
+
+
+def w12_swiglu(x_dev, lo_dev, nib_dev, m: int, ffn: int, k: int, mant_dev, shift_dev, silu_dev, h_shift: int, y_dev,
+               y_stride: int, stream=None, dev: int = 0) -> None:
+    """The dense SwiGLU gate/up product: int8 h = clamp(requant(silu[gq + 127] * uq, 1, h_shift))."""
+    check(lib().kt_hip_w12_swiglu(dev, _ptr(x_dev), _ptr(lo_dev), _ptr(nib_dev), m, ffn, k, _ptr(mant_dev),
+                                  _ptr(shift_dev), _ptr(silu_dev), h_shift, _ptr(y_dev), y_stride, _stream(stream)),
+          "w12 swiglu")
 
 
 def moe_combine(d_dev, off_dev, sel_dev, cw_dev, pos_dev, tokens: int, hidden: int, experts: int, top_k: int,

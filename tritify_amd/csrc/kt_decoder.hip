@@ -205,6 +205,164 @@ __global__ __launch_bounds__(1024) void dec_argmax_kernel(const int32_t* __restr
     }
 }
 
+// A single-token decode step's attention with its RoPE and cache append fused (T = 1, position p = pos[0]). One CTA
+// per q head h: the head's q and its kv head's new k are rotated in registers; the first q head of each kv group
+// writes the rotated k and the v to the caches at p; positions j < p come from the caches, j = p from the rotated
+// values held in LDS (no CTA reads position p from the caches, so the writers race with no reader). The integer rules
+// are those of dec_rope_kv_kernel + dec_attention_kernel.
+__global__ __launch_bounds__(256) void dec_attention_step_kernel(const int8_t* __restrict__ qkv,
+                                                                 const int32_t* __restrict__ pos,
+                                                                 int8_t* __restrict__ kc, int8_t* __restrict__ vc,
+                                                                 int nh, int nkv, const int16_t* __restrict__ cosT,
+                                                                 const int16_t* __restrict__ sinT,
+                                                                 const int32_t* __restrict__ exp_tab,
+                                                                 int8_t* __restrict__ o) {
+    constexpr int HD = 64, HH = 32;
+    extern __shared__ int s_sc[];
+    __shared__ int s_red[8];
+    __shared__ int s_part[64][HD + 1];
+    __shared__ __attribute__((aligned(16))) int8_t s_q[HD], s_k[HD], s_v[HD];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int p = pos[0], rep = nh / nkv, g = h / rep, L = p + 1;
+    if (tid < 2 * HH) {  // rotate q (threads 0..31) and k (32..63) pairs i, i + 32
+        const int i = tid & (HH - 1), isk = tid >> 5;
+        const int8_t* src = qkv + (isk ? (nh + g) * HD : h * HD);
+        const int a = src[i], b = src[i + HH], C = cosT[(size_t)p * HH + i], S = sinT[(size_t)p * HH + i];
+        int8_t* dst = isk ? s_k : s_q;
+        dst[i] = (int8_t)clamp127(shift_round(a * C - b * S, 14));
+        dst[i + HH] = (int8_t)clamp127(shift_round(b * C + a * S, 14));
+    } else if (tid < 2 * HH + HD) {
+        s_v[tid - 2 * HH] = qkv[(nh + nkv + g) * HD + tid - 2 * HH];
+    }
+    __syncthreads();
+    if (h % rep == 0 && tid < HD) {
+        kc[((size_t)p * nkv + g) * HD + tid] = s_k[tid];
+        vc[((size_t)p * nkv + g) * HD + tid] = s_v[tid];
+    }
+    v4i q4[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) q4[c] = *reinterpret_cast<const v4i*>(s_q + 16 * c);
+    int mx = INT_MIN;
+    for (int j = tid; j < L; j += 256) {
+        const int8_t* kr = j < p ? kc + ((size_t)j * nkv + g) * HD : s_k;
+        int s = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const v4i k4 = *reinterpret_cast<const v4i*>(kr + 16 * c);
+            s = __builtin_amdgcn_sdot4(q4[c].x, k4.x, s, false);
+            s = __builtin_amdgcn_sdot4(q4[c].y, k4.y, s, false);
+            s = __builtin_amdgcn_sdot4(q4[c].z, k4.z, s, false);
+            s = __builtin_amdgcn_sdot4(q4[c].w, k4.w, s, false);
+        }
+        s_sc[j] = s;
+        mx = s > mx ? s : mx;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int v = __shfl_xor(mx, d);
+        mx = v > mx ? v : mx;
+    }
+    if (lane == 0) s_red[w] = mx;
+    __syncthreads();
+    mx = s_red[0];
+#pragma unroll
+    for (int q = 1; q < 4; q++) mx = s_red[q] > mx ? s_red[q] : mx;
+    int den = 0;
+    for (int j = tid; j < L; j += 256) {
+        const int idx = (int)(((int64_t)mx - s_sc[j] + 64) >> 7);
+        const int e = idx < 1024 ? exp_tab[idx] : 0;
+        s_sc[j] = e;
+        den += e;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) den += __shfl_xor(den, d);
+    __syncthreads();
+    if (lane == 0) s_red[4 + w] = den;
+    const int c = tid & 3, rg = tid >> 2;
+    int acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0;
+    for (int j = rg; j < L; j += 64) {
+        const v4i v = *reinterpret_cast<const v4i*>(j < p ? vc + ((size_t)j * nkv + g) * HD + 16 * c : s_v + 16 * c);
+        const int e = s_sc[j];
+        const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] += e * b[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) s_part[rg][16 * c + i] = acc[i];
+    __syncthreads();
+    if (tid < HD) {
+        int64_t sum = 0;
+        for (int q = 0; q < 64; q++) sum += s_part[q][tid];
+        const int64_t dn = (int64_t)s_red[4] + s_red[5] + s_red[6] + s_red[7];
+        o[h * HD + tid] = (int8_t)clamp127(div_round(sum, dn));
+    }
+}
+
+// First stage of the greedy argmax: CTA b reduces its share of the n logits to one key (logit, then the lower
+// index: ((v ^ 2^31) << 32) | (2^32 - 1 - i), the largest key is the first maximum), copies its share to
+// record + step[0] * n when record is set, and CTA 0 advances the position by `advance`.
+__global__ __launch_bounds__(256) void dec_argmax_part_kernel(const int32_t* __restrict__ logits, int n,
+                                                              uint64_t* __restrict__ part,
+                                                              int32_t* __restrict__ record,
+                                                              const int32_t* __restrict__ step,
+                                                              int32_t* __restrict__ pos, int advance) {
+    __shared__ uint64_t s_key[4];
+    const int tid = threadIdx.x, per = (n + gridDim.x - 1) / gridDim.x;
+    const int i0 = blockIdx.x * per, i1 = min(n, i0 + per);
+    int32_t* rec = record ? record + (size_t)step[0] * n : nullptr;
+    uint64_t best = 0;
+    for (int i = i0 + tid; i < i1; i += 256) {
+        const int32_t v = logits[i];
+        if (rec) rec[i] = v;
+        const uint64_t key = ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+        best = key > best ? key : best;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint64_t o = __shfl_xor(best, d);
+        best = o > best ? o : best;
+    }
+    if ((tid & 63) == 0) s_key[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t b = s_key[0];
+        for (int q = 1; q < 4; q++) b = s_key[q] > b ? s_key[q] : b;
+        part[blockIdx.x] = b;
+        if (blockIdx.x == 0 && pos) pos[0] += advance;
+    }
+}
+
+// Second stage, fused with the next step's embedding: token = the best of nparts keys, r = emb[token], step += 1.
+__global__ __launch_bounds__(256) void dec_embed_argmax_kernel(const uint64_t* __restrict__ part, int nparts,
+                                                               const int16_t* __restrict__ emb, int d,
+                                                               int32_t* __restrict__ r, int32_t* __restrict__ token,
+                                                               int32_t* __restrict__ step) {
+    __shared__ uint64_t s_key[4];
+    __shared__ int s_tok;
+    const int tid = threadIdx.x;
+    uint64_t best = 0;
+    for (int i = tid; i < nparts; i += 256) best = part[i] > best ? part[i] : best;
+#pragma unroll
+    for (int dd = 32; dd >= 1; dd >>= 1) {
+        const uint64_t o = __shfl_xor(best, dd);
+        best = o > best ? o : best;
+    }
+    if ((tid & 63) == 0) s_key[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t b = s_key[0];
+        for (int q = 1; q < 4; q++) b = s_key[q] > b ? s_key[q] : b;
+        s_tok = (int)(0xFFFFFFFFu - (uint32_t)b);
+        if (token) token[0] = s_tok;
+        if (step) step[0] += 1;
+    }
+    __syncthreads();
+    const int16_t* e = emb + (size_t)s_tok * d;
+    for (int i = tid; i < d; i += 256) r[i] = e[i];
+}
+
 __global__ void dec_advance_kernel(int32_t* pos, int by) {
     if (threadIdx.x == 0) pos[0] += by;
 }
@@ -245,6 +403,27 @@ hipError_t launch_dec_attention(const int8_t* qkv, int T, int nqkv, const int32_
 hipError_t launch_dec_argmax(const int32_t* logits, int n, int32_t* token, int32_t* record, int32_t* step,
                              hipStream_t s) {
     dec_argmax_kernel<<<dim3(1), dim3(1024), 0, s>>>(logits, n, token, record, step);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh, int nkv,
+                                     const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
+                                     int max_pos, hipStream_t s) {
+    const size_t lds = (size_t)max_pos * sizeof(int);
+    dec_attention_step_kernel<<<dim3((unsigned)nh), dim3(256), lds, s>>>(qkv, pos, kc, vc, nh, nkv, cosT, sinT,
+                                                                         exp_tab, o);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_argmax_part(const int32_t* logits, int n, uint64_t* part, int nparts, int32_t* record,
+                                  const int32_t* step, int32_t* pos, int advance, hipStream_t s) {
+    dec_argmax_part_kernel<<<dim3((unsigned)nparts), dim3(256), 0, s>>>(logits, n, part, record, step, pos, advance);
+    return hipGetLastError();
+}
+
+hipError_t launch_dec_embed_argmax(const uint64_t* part, int nparts, const int16_t* emb, int d, int32_t* r,
+                                   int32_t* token, int32_t* step, hipStream_t s) {
+    dec_embed_argmax_kernel<<<dim3(1), dim3(256), 0, s>>>(part, nparts, emb, d, r, token, step);
     return hipGetLastError();
 }
 

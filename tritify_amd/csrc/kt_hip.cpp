@@ -525,6 +525,26 @@ int kt_hip_w12_grouped_linear(int dev, const int8_t* x_dev, int64_t x_rows, cons
                                        (hipStream_t)stream);
 }
 
+int kt_hip_w12_swiglu(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                      int64_t ffn, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
+                      const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride, void* stream) {
+    if (m < 0 || ffn <= 0 || ffn % 64 || k < 1 || kp_of(k) > 8128 || y_stride < ffn || y_stride > INT_MAX ||
+        m > INT_MAX || mant_dev == nullptr || shift_dev == nullptr || silu_dev == nullptr || h_shift < 1 ||
+        h_shift > 30)
+        return (int)hipErrorInvalidValue;
+    if (m == 0) return 0;
+    const int64_t kp = kp_of(k);
+    KT_TRY(hipSetDevice(dev));
+    if (m <= KT_W12_SKINNY_MAX_M)
+        return (int)kt::launch_w12_swiglu(x_dev, lo_dev, nib_dev, (int)m, (int)ffn, (int)kp, mant_dev, shift_dev,
+                                          silu_dev, h_shift, y_dev, (int)y_stride, (hipStream_t)stream);
+    size_t lo_bytes = 0, nib_bytes = 0;
+    kt_hip_w12_bytes(2 * ffn, k, &lo_bytes, &nib_bytes);
+    return (int)kt::launch_w12_grouped(x_dev, (size_t)m * (size_t)kp, nullptr, 0, nullptr, 1, m, lo_dev, nib_dev,
+                                       lo_bytes, (int)(2 * ffn), (int)kp, mant_dev, shift_dev, KT_EPI_SWIGLU,
+                                       silu_dev, h_shift, y_dev, (int)y_stride, nullptr, (hipStream_t)stream);
+}
+
 int kt_hip_moe_combine(int dev, const int8_t* d_dev, const int32_t* off_dev, const int32_t* sel_dev,
                        const int32_t* cw_dev, const int32_t* pos_dev, int64_t tokens, int64_t hidden,
                        int64_t experts, int top_k, int out_shift, int8_t* out_dev, void* stream) {
@@ -658,6 +678,36 @@ int kt_hip_dec_advance(int dev, int32_t* pos_dev, int64_t by, void* stream) {
     if (by < 0 || by > INT_MAX) return (int)hipErrorInvalidValue;
     KT_TRY(hipSetDevice(dev));
     return (int)kt::launch_dec_advance(pos_dev, (int)by, (hipStream_t)stream);
+}
+
+int kt_hip_dec_attention_step(int dev, const int8_t* qkv_dev, const int32_t* pos_dev, int8_t* kcache_dev,
+                              int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd, const int16_t* cos_dev,
+                              const int16_t* sin_dev, const int32_t* exp_tab_dev, int8_t* o_dev, int64_t max_pos,
+                              void* stream) {
+    if (hd != 64 || nh < 1 || nkv < 1 || nh % nkv || nh > INT_MAX || max_pos < 1 || max_pos > 16384)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_attention_step(qkv_dev, pos_dev, kcache_dev, vcache_dev, (int)nh, (int)nkv, cos_dev,
+                                              sin_dev, exp_tab_dev, o_dev, (int)max_pos, (hipStream_t)stream);
+}
+
+int kt_hip_dec_argmax_part(int dev, const int32_t* logits_dev, int64_t n, uint64_t* part_dev, int64_t nparts,
+                           int32_t* record_dev, const int32_t* step_dev, int32_t* pos_dev, int64_t advance,
+                           void* stream) {
+    if (n < 1 || n > INT_MAX || nparts < 1 || nparts > 4096 || nparts > n || advance < 0 || advance > INT_MAX ||
+        (record_dev != nullptr && step_dev == nullptr))
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_argmax_part(logits_dev, (int)n, part_dev, (int)nparts, record_dev, step_dev, pos_dev,
+                                           (int)advance, (hipStream_t)stream);
+}
+
+int kt_hip_dec_embed_argmax(int dev, const uint64_t* part_dev, int64_t nparts, const int16_t* emb_dev, int64_t d,
+                            int32_t* r_dev, int32_t* token_dev, int32_t* step_dev, void* stream) {
+    if (nparts < 1 || nparts > 4096 || d < 1 || d > INT_MAX) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_embed_argmax(part_dev, (int)nparts, emb_dev, (int)d, r_dev, token_dev, step_dev,
+                                            (hipStream_t)stream);
 }
 
 int kt_hip_probe_mfma(int dev, const int8_t* a_dev, const int8_t* b_dev, int32_t* c32_dev, int32_t* c16_dev,

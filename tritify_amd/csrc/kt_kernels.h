@@ -42,6 +42,16 @@ hipError_t launch_dec_attention(const int8_t* qkv, int T, int nqkv, const int32_
 hipError_t launch_dec_argmax(const int32_t* logits, int n, int32_t* token, int32_t* record, int32_t* step,
                              hipStream_t s);
 hipError_t launch_dec_advance(int32_t* pos, int by, hipStream_t s);
+hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh, int nkv,
+                                     const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
+                                     int max_pos, hipStream_t s);
+hipError_t launch_dec_argmax_part(const int32_t* logits, int n, uint64_t* part, int nparts, int32_t* record,
+                                  const int32_t* step, int32_t* pos, int advance, hipStream_t s);
+hipError_t launch_dec_embed_argmax(const uint64_t* part, int nparts, const int16_t* emb, int d, int32_t* r,
+                                   int32_t* token, int32_t* step, hipStream_t s);
+hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int F, int kp,
+                             const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift, int8_t* y,
+                             int ystride, hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

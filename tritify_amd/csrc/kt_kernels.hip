@@ -508,6 +508,109 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// W12 skinny SwiGLU (M <= 16 * MT): the skinny kernel over a gate/up matrix packed with the 32-row interleave. A CTA
+// owns 16 hidden units u0 .. u0 + 15: half hb of gate block 2j and the same half of up block 2j + 1 (adjacent in
+// memory), both streamed in one pass over k. Epilogue: g, u = int8 requant per channel (gate channel u, up channel
+// F + u), h = clamp(requant(silu[g + 127] * u, 1, h_shift)). Every dot is SMALL (kp <= 8128).
+// ------------------------------------------------------------------------------------------------------------------
+template <int MT, int NW, int U>
+__global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
+    const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
+    int8_t* __restrict__ y, int ystride, int M, int F, int kp, const int32_t* __restrict__ mant,
+    const int32_t* __restrict__ shift, const int16_t* __restrict__ silu, int h_shift) {
+    constexpr int NT = 64 * NW, OUTS = MT * 256;
+    static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
+    __shared__ int32_t sPg[NW][OUTS], sPu[NW][OUTS];
+    __shared__ int32_t sX[NW][MT * 16];
+    __shared__ int16_t sSilu[256];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int u0 = 16 * blockIdx.x, cbg = 2 * (u0 >> 5), hb = (u0 >> 4) & 1;
+    const int KB = kp / 32;
+    for (int i = tid; i < 256; i += NT) sSilu[i] = silu[i < 255 ? i : 254];
+
+    const int oc = tid & 15, ou = u0 + oc;
+    const int32_t gm = tid < OUTS ? mant[ou] : 0, gs = tid < OUTS ? shift[ou] : 0;
+    const int32_t um = tid < OUTS ? mant[F + ou] : 0, us = tid < OUTS ? shift[F + ou] : 0;
+
+    // gate block cbg and up block cbg + 1 are adjacent: one descriptor over both
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cbg * KB * 1024, 2u * (uint32_t)KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cbg * KB * 512, 2u * (uint32_t)KB * 512);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)M * (uint32_t)kp);
+    const int c = lane & 15, g = lane >> 4, kbq = g >> 1, h = g & 1;
+    const int slot = 16 * hb + c + 32 * h;
+    const uint32_t oL = 16 * slot + 1024 * kbq, oN = 8 * slot + 512 * kbq;
+    const uint32_t uL = oL + (uint32_t)KB * 1024, uN = oN + (uint32_t)KB * 512;
+    uint32_t oX[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) oX[t] = (uint32_t)(c + 16 * t) * (uint32_t)kp + 32 * kbq + 16 * h;
+
+    v4i ag0[MT], ag1[MT], au0[MT], au1[MT];
+    int sx[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) ag0[t] = ag1[t] = au0[t] = au1[t] = v4i{}, sx[t] = 0;
+
+    v4i Lg[U], Lu[U], X[U][MT];
+    v2i Dg[U], Du[U];
+    const int np = KB / 2, nb = (np + NW * U - 1) / (NW * U);
+    int b = 0;
+    do {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int p = w + NW * (U * b + u);
+            const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
+            Lg[u] = bload16(rL, oL, pl * 2048u);
+            Dg[u] = bload8(rN, oN, pl * 1024u);
+            Lu[u] = bload16(rL, uL, pl * 2048u);
+            Du[u] = bload8(rN, uN, pl * 1024u);
+#pragma unroll
+            for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int mask = 2 * (w + NW * (U * b + u)) + kbq < KB ? -1 : 0;
+            const v4i hg = unpack_hi(Dg[u]), hu = unpack_hi(Du[u]);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const v4i a = X[u][t] & mask;
+                sx[t] += sum4(a);
+                ag0[t] = mfma16(a, Lg[u], ag0[t]);
+                ag1[t] = mfma16(a, hg, ag1[t]);
+                au0[t] = mfma16(a, Lu[u], au0[t]);
+                au1[t] = mfma16(a, hu, au1[t]);
+            }
+        }
+    } while (++b < nb);
+
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int o = (t * 16 + 4 * g + r) * 16 + c;
+            sPg[w][o] = (int32_t)((uint32_t)ag0[t][r] + ((uint32_t)ag1[t][r] << 8));
+            sPu[w][o] = (int32_t)((uint32_t)au0[t][r] + ((uint32_t)au1[t][r] << 8));
+        }
+        int s = sx[t];
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        if (lane < 16) sX[w][t * 16 + lane] = s;
+    }
+    __syncthreads();
+    const ColQ qg = col_q(gm, gs), qu = col_q(um, us);
+#pragma unroll
+    for (int o = tid; o < OUTS; o += NT) {
+        const int m = o >> 4;
+        uint32_t vg = 0, vu = 0, rs = 0;
+#pragma unroll
+        for (int q = 0; q < NW; q++) vg += (uint32_t)sPg[q][o], vu += (uint32_t)sPu[q][o], rs += (uint32_t)sX[q][m];
+        const int gq = col_requant<false>((int)(vg - 1920u * rs), qg);
+        const int uq = col_requant<false>((int)(vu - 1920u * rs), qu);
+        if (m < M) y[(size_t)m * ystride + ou] = (int8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // Lane-layout probe of the 32x32x32 and 16x16x64 int8 MFMAs (test hook): a and b are 64 lanes x 16 bytes each;
 // c32 gets the 64 x 16 raw accumulator registers of one 32x32x32 product, c16 the 64 x 4 of one 16x16x64 product.
 // ------------------------------------------------------------------------------------------------------------------
@@ -616,6 +719,27 @@ hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* n
         case KT_OUT_I8: return w12_linear_out<KT_OUT_I8>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int F, int kp,
+                             const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift, int8_t* y,
+                             int ystride, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    if (F <= 0 || F % 32 || kp <= 0 || kp % 64 || kp > KT_SMALL_KP || h_shift < 1 || h_shift > 30 || ystride < F ||
+        (int64_t)M * kp > (int64_t)UINT32_MAX)
+        return hipErrorInvalidValue;
+    if (M <= KT_W12_SKINNY_MAX_M) {
+        dim3 grid((unsigned)(F / 16));
+#define KT_SWIGLU(mt, nw, u)                                                                                         \
+    if (M <= 16 * mt) {                                                                                              \
+        w12_skinny_swiglu_kernel<mt, nw, u><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, ystride, M, F, kp, mant,  \
+                                                                           shift, silu, h_shift);                    \
+        return hipGetLastError();                                                                                    \
+    }
+        KT_SWIGLU(1, 8, 4) KT_SWIGLU(2, 8, 2) KT_SWIGLU(4, 8, 1) KT_SWIGLU(8, 4, 2)
+#undef KT_SWIGLU
+    }
+    return hipErrorInvalidValue;  // the caller takes the grouped kernel (one group) for longer batches
 }
 
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s) {

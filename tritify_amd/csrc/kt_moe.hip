@@ -103,8 +103,8 @@ __global__ __launch_bounds__(256) void moe_bucket_kernel(const int32_t* __restri
 // The grouped GEMM's CTA tile: the dense GEMM's 128 x 128 (4 waves along N, 4 x 1 tiles of 32x32 each).
 typedef W12Tile<1, 4, 1, 4> GTile;
 
-// Ragged grouped W12 GEMM. Group g has count[g] rows; its row j is x row list[g * list_stride + j] (list != null) or
-// x row off[g] + j (off = the exclusive prefix of count); its weights are the W12 planes at wlo + g * glo (lo) and
+// Ragged grouped W12 GEMM. Group g has count[g] rows (count null: one group of rows_one rows, a dense product); its
+// row j is x row list[g * list_stride + j] (list != null) or x row off[g] + j (off = the exclusive prefix of count); its weights are the W12 planes at wlo + g * glo (lo) and
 // wnib + g * glo / 2 (nib), n x k with per-channel scales mant/shift + g * n; its output row j is y row off[g] + j
 // (row stride ystride). EPI_I8: y = the int8 requant of the n columns. EPI_SWIGLU: the weights are a gate/up
 // matrix packed with the 32-row interleave (n = 2F), the scales in natural order (gate 0..F-1, up F..2F-1), and
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int32_t* __restrict__ count, int groups, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     size_t glo, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
     const int16_t* __restrict__ silu, int h_shift, int8_t* __restrict__ y, int ystride,
-    int32_t* __restrict__ off_out) {
+    int32_t* __restrict__ off_out, int rows_one) {
     typedef GTile C;
     constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
     static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int carry_r = 0, carry_o = 0;
     for (int g0 = 0; g0 < groups; g0 += NT) {
-        const int g = g0 + tid, c = g < groups ? count[g] : 0;
+        const int g = g0 + tid, c = g < groups ? (count ? count[g] : rows_one) : 0;
         int er, eo, tr, to;
         block_scan2<NT>((c + BM - 1) / BM, c, er, eo, tr, to, scr);
         if (g < groups) sRpre[g] = carry_r + er, sOff[g] = carry_o + eo;
@@ -287,7 +287,7 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
                               int ystride, int32_t* off_out, hipStream_t s) {
     if (groups <= 0 || N <= 0) return hipSuccess;
     if (groups > KT_MAX_GROUPS || kp <= 0 || kp % 64 || kp > KT_SMALL_KP || x_bytes + kp >= 0xFFFFFFF0ull ||
-        max_rows < 0)
+        max_rows < 0 || max_rows > INT32_MAX || (count == nullptr && groups != 1))
         return hipErrorInvalidValue;
     if (epi == KT_EPI_SWIGLU && (N % 64 || !silu || h_shift < 1 || h_shift > 30 || ystride % 16))
         return hipErrorInvalidValue;
@@ -298,11 +298,11 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
     if (epi == KT_EPI_I8)
         w12_grouped_kernel<KT_EPI_I8><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
             x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu, h_shift,
-            y, ystride, off_out);
+            y, ystride, off_out, (int)max_rows);
     else if (epi == KT_EPI_SWIGLU)
         w12_grouped_kernel<KT_EPI_SWIGLU><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
             x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu, h_shift,
-            y, ystride, off_out);
+            y, ystride, off_out, (int)max_rows);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -64,7 +64,7 @@ class DecoderModel:
         self.token = zeros(1, torch.int32)
         self.pos = zeros(1, torch.int32)
         self.step = zeros(1, torch.int32)
-        self.count = {}
+        self.part = torch.zeros(self.NPARTS, dtype=torch.int64, device=dv)
         self.record = None
 
     # weights -------------------------------------------------------------------------------------------------------
@@ -109,43 +109,51 @@ class DecoderModel:
 
     # the forward ---------------------------------------------------------------------------------------------------
 
-    def _count(self, T: int):
-        if T not in self.count:
-            self.count[T] = self.torch.full((1,), T, dtype=self.torch.int32, device=self.device)
-        return self.count[T]
+    NPARTS = 128  # argmax first-stage CTAs
 
     def forward(self, tokens_dev, T: int, stream=None) -> None:
-        """Rows tokens_dev[0 .. T) at positions pos .. pos + T - 1 (pos on the device) through every layer, the
-        last row's logits into self.logits, then pos += T. Asynchronous on `stream`."""
-        if not 1 <= T <= self.max_rows:
-            raise ValueError("forward: 1 <= T <= max_rows")
+        """Rows at positions pos .. pos + T - 1 (pos on the device) through every layer; the last row's logits go to
+        self.logits and their argmax's first stage to self.part (with the logits recorded at self.record[step] when a
+        record is set), and pos advances by T. tokens_dev None: one row, the token the previous call's argmax chose
+        (a decode step; step advances by one). Asynchronous on `stream`."""
+        if not 1 <= T <= self.max_rows or (tokens_dev is None and T != 1):
+            raise ValueError("forward: 1 <= T <= max_rows, and T = 1 for a decode step")
         lib, dev, s = B.lib(), self.dev, B._stream(stream)
         P = B._ptr
         d, ffn, nh, nkv, hd, nq = self.d, self.ffn, self.nh, self.nkv, self.hd, self.nq
         cache = self.max_pos * nkv * hd
-        B.check(lib.kt_hip_dec_embed(dev, P(tokens_dev), T, P(self.emb16), d, P(self.r), s), "dec embed")
-        count = self._count(T)
+        if tokens_dev is None:
+            B.check(lib.kt_hip_dec_embed_argmax(dev, P(self.part), self.NPARTS, P(self.emb16), d, P(self.r),
+                                                P(self.token), P(self.step), s), "dec embed argmax")
+        else:
+            B.check(lib.kt_hip_dec_embed(dev, P(tokens_dev), T, P(self.emb16), d, P(self.r), s), "dec embed")
         for l in range(self.L):
             kc, vc = P(self.kc) + l * cache, P(self.vc) + l * cache
             B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
             self._gemm("qkv", l, self.xn, T, nq, d, self.qkv, B.OUT_I8, s)
-            B.check(lib.kt_hip_dec_rope_kv(dev, P(self.qkv), T, nq, P(self.pos), nh, nkv, hd, P(self.rope_cos),
-                                           P(self.rope_sin), kc, vc, s), "dec rope")
-            B.check(lib.kt_hip_dec_attention(dev, P(self.qkv), T, nq, P(self.pos), kc, vc, nh, nkv, hd,
-                                              P(self.exp_tab), P(self.o), self.max_pos, s), "dec attention")
+            if tokens_dev is None:
+                B.check(lib.kt_hip_dec_attention_step(dev, P(self.qkv), P(self.pos), kc, vc, nh, nkv, hd,
+                                                      P(self.rope_cos), P(self.rope_sin), P(self.exp_tab), P(self.o),
+                                                      self.max_pos, s), "dec attention step")
+            else:
+                B.check(lib.kt_hip_dec_rope_kv(dev, P(self.qkv), T, nq, P(self.pos), nh, nkv, hd, P(self.rope_cos),
+                                               P(self.rope_sin), kc, vc, s), "dec rope")
+                B.check(lib.kt_hip_dec_attention(dev, P(self.qkv), T, nq, P(self.pos), kc, vc, nh, nkv, hd,
+                                                  P(self.exp_tab), P(self.o), self.max_pos, s), "dec attention")
             self._gemm("o", l, self.o, T, d, nh * hd, self.r, B.OUT_I32_ADD, s)
             B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
             lo_b, nib_b = self.sizes["gu"]
             lo, nib = self.w["gu"]
             m, sh = self.scale["gu"]
-            B.check(lib.kt_hip_w12_grouped_linear(dev, P(self.xn), T, None, 0, P(count), 1, T, P(lo) + l * lo_b,
-                                                  P(nib) + l * nib_b, 2 * ffn, d, P(m) + l * 8 * ffn,
-                                                  P(sh) + l * 8 * ffn, B.EPI_SWIGLU, P(self.silu), self.h_shift,
-                                                  P(self.h), ffn, None, s), "dec gate/up")
+            B.check(lib.kt_hip_w12_swiglu(dev, P(self.xn), P(lo) + l * lo_b, P(nib) + l * nib_b, T, ffn, d,
+                                          P(m) + l * 8 * ffn, P(sh) + l * 8 * ffn, P(self.silu), self.h_shift,
+                                          P(self.h), ffn, s), "dec gate/up")
             self._gemm("dn", l, self.h, T, d, ffn, self.r, B.OUT_I32_ADD, s)
         B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r) + (T - 1) * d * 4, 1, d, P(self.xn), d, s), "dec rmsnorm")
         self._gemm("emb", 0, self.xn, 1, self.V, d, self.logits, B.OUT_I32, s)
-        B.check(lib.kt_hip_dec_advance(dev, P(self.pos), T, s), "dec advance")
+        rec = P(self.record) if self.record is not None else None
+        B.check(lib.kt_hip_dec_argmax_part(dev, P(self.logits), self.V, P(self.part), self.NPARTS, rec,
+                                           P(self.step), P(self.pos), T, s), "dec argmax")
 
     def _gemm(self, name, l, x, M, N, K, y, out_kind, s) -> None:
         lo_b, nib_b = self.sizes[name]
@@ -155,17 +163,9 @@ class DecoderModel:
         B.check(B.lib().kt_hip_w12_linear(self.dev, P(x), P(lo) + l * lo_b, P(nib) + l * nib_b, M, N, K,
                                           P(m) + l * N * 4, P(sh) + l * N * 4, out_kind, P(y), s), f"dec {name}")
 
-    def argmax(self, stream=None, record: bool = True) -> None:
-        """token = argmax(logits); with record, the logits row also goes to self.record[step] and step advances."""
-        P = B._ptr
-        rec = P(self.record) if record and self.record is not None else None
-        B.check(B.lib().kt_hip_dec_argmax(self.dev, P(self.logits), self.V, P(self.token), rec, P(self.step),
-                                          B._stream(stream)), "dec argmax")
-
     def decode_step(self, stream=None) -> None:
-        """DecoderModel::decode_step on the device: the last argmax token at the current position, then its argmax."""
-        self.forward(self.token, 1, stream)
-        self.argmax(stream)
+        """DecoderModel::decode_step on the device: the previous argmax's token at the current position."""
+        self.forward(None, 1, stream)
 
     def generate(self, prompt, max_new: int, graph: bool = False, stream=None):
         """generate_greedy_by with no stop tokens: prefill the prompt as one call, then max_new - 1 decode steps.
@@ -180,7 +180,6 @@ class DecoderModel:
         self.step.zero_()
         self.tok_in[:P] = torch.from_numpy(prompt).to(self.device)
         self.forward(self.tok_in, P, stream)
-        self.argmax(stream)
         steps = max_new - 1
         if graph and steps > 0:
             g = self.capture_decode_step()
@@ -196,7 +195,6 @@ class DecoderModel:
     def capture_decode_step(self):
         """One decode step captured as a HIP graph (every position and token is read from device memory)."""
         torch = self.torch
-        self._count(1)
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         g = torch.cuda.CUDAGraph()
