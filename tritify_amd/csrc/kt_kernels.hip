@@ -268,12 +268,12 @@ __device__ __forceinline__ void tile_coords(int M, int N, int BM, int BN, int& m
 
 // An optional int8 -> int8 table (`lut`, 255 entries indexed by q + 127) is applied after the int8 requant: the
 // activation-code epilogue (GELU of config 5). lut is read only for OUT == KT_OUT_I8 and may be null.
-template <int WM, int WTM, int WTN, int WAVES, int NSLOT, int OUT, bool SMALL>
-__global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
+template <int WM, int WTM, int WTN, int WAVES, int NSLOT, int OUT, bool SMALL, int WN = 4>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
     const int8_t* __restrict__ lut) {
-    typedef W12Tile<WM, WTM, WTN, NSLOT> C;
+    typedef W12Tile<WM, WTM, WTN, NSLOT, WN> C;
     constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
     constexpr int SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // the int8 output tile reuses the A ring after the loop
     __shared__ __attribute__((aligned(16))) int8_t smem[C::RING > SO ? C::RING : SO];
@@ -281,11 +281,11 @@ __global__ __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WAVES,
     __shared__ int8_t sLut[256];
 
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
-    const int wave = (tid >> 6) & 3, rw0 = ((tid >> 6) >> 2) * 32 * WTM;
+    const int wave = (tid >> 6) % WN, rw0 = ((tid >> 6) / WN) * 32 * WTM;
     int m0, n0;
     tile_coords(M, N, BM, BN, m0, n0);
     const int KB = kp / 32;
-    if (OUT == KT_OUT_I8 && SMALL && tid < 256) sLut[tid] = lut ? lut[tid < 255 ? tid : 254] : 0;
+    if (OUT == KT_OUT_I8 && SMALL && tid < 256) sLut[tid] = lut ? lut[tid < 255 ? tid : 254] : 0;  // NT >= 256
 
     // A: the CTA's rows; rows past the matrix read as zero (their offsets are past the descriptor)
     const uint32_t rows_a = (uint32_t)(M - m0 < BM ? M - m0 : BM);
@@ -698,7 +698,8 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     }
     const bool small = kp <= KT_SMALL_KP;
     constexpr int WM = KT_W12_WM, WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES, NS = KT_W12_NSLOT;
-    dim3 grid((unsigned)(ceil_div(N, 128 * WTN) * ceil_div(M, 32 * WTM * WM))), block(256 * WM);
+    const int64_t tiles4 = ceil_div(N, 32 * WTN * 4) * ceil_div(M, 32 * WTM * WM);
+    dim3 grid((unsigned)tiles4), block(256 * WM);
     if (small)
         w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift, lut);
     else

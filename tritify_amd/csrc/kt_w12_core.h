@@ -205,7 +205,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// The W12 tile mainloop. CTA = WM x 4 waves (WM along M, 4 along N); each wave owns WTM x WTN tiles of 32x32 (its
+// The W12 tile mainloop. CTA = WM x WN waves (WM along M, WN along N); each wave owns WTM x WTN tiles of 32x32 (its
 // wave row's 32*WTM rows, its own 32*WTN columns), BK = 64. A goes global -> registers -> an NSLOT-slot LDS ring;
 // each wave's B fragments go straight from global memory into registers. Both are issued NSLOT-1 tiles ahead of the
 // tile being multiplied, and the loop is unrolled by NSLOT so every register set has a compile-time slot. Loads of
@@ -213,12 +213,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 // MFMAs add zero instead of being branched around -- no MFMA sits under control flow, which would cost accumulator
 // copies. Row sums of x (for -1920 * sum_k x) come from the A staging registers.
 // ------------------------------------------------------------------------------------------------------------------
-template <int WM_, int WTM_, int WTN_, int NSLOT_>
+template <int WM_, int WTM_, int WTN_, int NSLOT_, int WN_ = 4>
 struct W12Tile {
-    static constexpr int WM = WM_, WTM = WTM_, WTN = WTN_, NSLOT = NSLOT_;
-    static constexpr int NT = 256 * WM;  // threads
+    static constexpr int WM = WM_, WTM = WTM_, WTN = WTN_, NSLOT = NSLOT_, WN = WN_;  // WN waves along N
+    static constexpr int NT = 64 * WM * WN;  // threads
     static constexpr int BK = 64, CPR = 4;
-    static constexpr int BM = 32 * WTM * WM, BN = 128 * WTN;
+    static constexpr int BM = 32 * WTM * WM, BN = 32 * WTN * WN;
     static constexpr int AC = BM * CPR, AL = (AC + NT - 1) / NT;  // 16-byte A chunks per k-tile / per thread
     static constexpr int RING = NSLOT * BM * BK;                   // bytes of the A ring
 };
@@ -236,7 +236,7 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
     constexpr int CPR = C::CPR, BM = C::BM, BK = C::BK;
     int8_t(*sA)[BM * BK] = reinterpret_cast<int8_t(*)[BM * BK]>(smem);
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
-    const int rw0 = ((tid >> 6) >> 2) * 32 * WTM;  // the wave's first row in the tile
+    const int rw0 = ((tid >> 6) / C::WN) * 32 * WTM;  // the wave's first row in the tile
 
 #pragma unroll
     for (int i = 0; i < WTM; i++)
@@ -278,6 +278,18 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
             rsum[i] += sum4(v);
         }
     };
+    auto mma = [&](auto S, const v4i (&a)[WTM], int ks) {
+        constexpr int sl = decltype(S)::value;
+#pragma unroll
+        for (int j = 0; j < WTN; j++) {
+            const v4i b0 = bl[sl][j][ks], b1 = unpack_hi(bn[sl][j][ks]);
+#pragma unroll
+            for (int i = 0; i < WTM; i++) {
+                acc0[i][j] = mfma32(a[i], b0, acc0[i][j]);
+                acc1[i][j] = mfma32(a[i], b1, acc1[i][j]);
+            }
+        }
+    };
     auto compute = [&](auto S) {
         constexpr int sl = decltype(S)::value;
 #pragma unroll
@@ -285,15 +297,7 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
             v4i a[WTM];
 #pragma unroll
             for (int i = 0; i < WTM; i++) a[i] = lds_read16(sA[sl], lds_off<CPR>(rw0 + i * 32 + (lane & 31), 2 * ks + half));
-#pragma unroll
-            for (int j = 0; j < WTN; j++) {
-                const v4i b0 = bl[sl][j][ks], b1 = unpack_hi(bn[sl][j][ks]);
-#pragma unroll
-                for (int i = 0; i < WTM; i++) {
-                    acc0[i][j] = mfma32(a[i], b0, acc0[i][j]);
-                    acc1[i][j] = mfma32(a[i], b1, acc1[i][j]);
-                }
-            }
+            mma(S, a, ks);
         }
     };
 
@@ -340,7 +344,7 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
                                                   const int32_t* mant, const int32_t* shift, int n0, int N,
                                                   ChanFn chan, int8_t* sO) {
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
-    const int wave = (tid >> 6) & 3, rw0 = ((tid >> 6) >> 2) * 32 * C::WTM;
+    const int wave = (tid >> 6) % C::WN, rw0 = ((tid >> 6) / C::WN) * 32 * C::WTM;
 #pragma unroll
     for (int j = 0; j < C::WTN; j++) {
         const int c = wave * 32 * C::WTN + j * 32 + (lane & 31), n = n0 + c;
