@@ -72,6 +72,40 @@ int kt_hip_digit_gemm(int dev, const int8_t* xa_dev, int px, const int8_t* wb_de
                       int64_t rows, int64_t out, int64_t k, int64_t flush_k, int drop_top, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * QuantLinear::forward_int on the device (crates/01-engine/kt-core/src/layers.rs:275-328, helpers 23-39): the
+ * reference's dynamic per-tensor quantization before and after the seam, with no host round trip.
+ * ------------------------------------------------------------------------------------------------------------- */
+/* A tensor's Scale (kt-int Scale { mant, shift }, real = code * mant / 2^shift) as a device record, plus the two
+ * maxima of the call that produced it (0 where not reached). The output record of one layer is the input record of
+ * the next. */
+typedef struct {
+    int64_t mant;
+    int32_t shift;
+    int32_t pad;
+    int64_t xmax;
+    int64_t ymax;
+} kt_hip_qscale;
+#define KT_QL_WS_PARTS 5 /* workspace parts: x planes, i64 accumulators, |x| maxima, |acc| maxima, per-call state */
+#define KT_QL_PARTS 1024 /* partial maxima per reduction */
+/* Workspace bytes of kt_hip_quant_linear for rows x in_f -> out_f (parts at *off, 256-byte aligned). */
+size_t kt_hip_quant_linear_workspace(int64_t rows, int64_t in_f, int64_t out_f, size_t off[KT_QL_WS_PARTS]);
+/* y_dev (rows x out_f i32 codes) and os_dev (their Scale) = QuantLinear::forward_int of x_dev (rows x in_f i32
+ * codes at the scale in xs_dev, device) against weights held as pw in {1, 3, 5} digit planes (kt_hip_pack_planes of
+ * the out_f x in_f codes) at scale (w_mant, w_shift), with optional bias codes bias_dev (out_f i64, device; NULL =
+ * none) at scale (b_mant, b_shift):
+ *   xmax = max |x|; xmax == 0 -> y = bias codes at the bias scale, or zeros at Scale::ZERO;
+ *   qx = quant_to(x, xmax) = round_half_away(x * WLEVELS / xmax); c = from_ratio(xmax, WLEVELS) * xs * ws;
+ *   c == 0 -> zeros; acc = qx . w^T (exact, i64) + (bs * c^-1).apply(bias); ymax = max |acc|; ymax == 0 -> zeros;
+ *   y = requant_dyn(acc, 2^28, ymax), os = from_ratio(ymax, 2^28) * c.
+ * Every pass runs on `stream` with no host synchronization (capturable in a HIP graph). ws_dev is the caller's
+ * workspace of kt_hip_quant_linear_workspace bytes; calls that share one workspace must not overlap. Requires
+ * rows, in_f, out_f >= 1, rows * kp and rows * out_f below 2^31, mantissas >= 0. */
+int kt_hip_quant_linear(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f, const kt_hip_qscale* xs_dev,
+                        const int8_t* w_planes_dev, int pw, int64_t out_f, int64_t w_mant, int32_t w_shift,
+                        const int64_t* bias_dev, int64_t b_mant, int32_t b_shift, void* ws_dev, size_t ws_bytes,
+                        int32_t* y_dev, kt_hip_qscale* os_dev, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Backend layer: one LinearBackend on one device (kt_cuda::open, lib.rs:252; TcLinear, backend.rs:77-192).
  * ------------------------------------------------------------------------------------------------------------- */
 typedef struct kt_hip_backend kt_hip_backend;

@@ -701,6 +701,67 @@ int32_t kt_requant_dyn(int64_t v, int64_t num_level, int64_t den) {
     return (int32_t)r;
 }
 
+/* |v| with the two's-complement wrap of i64::abs in a release build (i64::MIN stays negative). */
+static int64_t abs_wrap(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64_t)v) : v; }
+
+/*
+ * QuantLinear::forward_int (layers.rs:275-328) for rows x in i32 codes at scale xs against out x in weight codes at
+ * scale ws, with optional i64 bias codes at scale bs (NULL: no bias). Writes the rows x out i32 output codes and
+ * returns their scale in *os; *xmax_out and *ymax_out receive the two per-call maxima (0 when not reached).
+ *   1. xmax = max |x|; xmax == 0 -> the bias codes (as i32) at bs, or zeros at Scale::ZERO     (279-295)
+ *   2. qx = quant_to(x, xmax); c = from_ratio(xmax, WLEVELS) * xs * ws; c == 0 -> zeros        (297-302)
+ *   3. bias_in_c[o] = (bs * c^-1).apply(bias[o])                                                (304-307)
+ *   4. acc = linear(qx, w) + bias_in_c  (wrapping i64)                                          (312-320)
+ *   5. ymax = max |acc|; 0 -> zeros; y = requant_dyn(acc, ACT_LEVELS, ymax),
+ *      os = from_ratio(ymax, ACT_LEVELS) * c                                                    (321-327)
+ */
+void kt_quant_linear_forward(const int32_t* x, size_t rows, size_t in, kt_scale xs, const int32_t* w, size_t out,
+                             kt_scale ws, const int64_t* bias, kt_scale bs, size_t threads, int32_t* y, kt_scale* os,
+                             int64_t* xmax_out, int64_t* ymax_out) {
+    const size_t n = rows * out;
+    const kt_scale zero = {0, 0};
+    int64_t xmax = 0;
+    for (size_t i = 0; i < rows * in; i++) {
+        const int64_t a = abs_wrap((int64_t)x[i]);
+        if (a > xmax) xmax = a;
+    }
+    *xmax_out = xmax, *ymax_out = 0, *os = zero;
+    if (xmax == 0) {
+        for (size_t i = 0; i < n; i++) y[i] = bias ? (int32_t)bias[i % out] : 0;
+        if (bias) *os = bs;
+        return;
+    }
+    int32_t* qx = (int32_t*)malloc(rows * in * sizeof(int32_t) + 1);
+    int64_t* acc = (int64_t*)malloc(n * sizeof(int64_t) + 1);
+    if (!qx || !acc) abort();
+    kt_quant_to(x, rows * in, xmax, qx);
+    const kt_scale c = kt_scale_mul(kt_scale_mul(kt_scale_from_ratio(0, (uint64_t)xmax, 0, WLEVELS), xs), ws);
+    if (c.mant == 0) {
+        memset(y, 0, n * sizeof(int32_t));
+        free(qx), free(acc);
+        return;
+    }
+    fill_linear(qx, w, rows, out, in, variant_fn(kt_cpu_auto_variant()), acc,
+                threads ? threads : kt_plan_threads(n, sat_mul(n, in)), 0);
+    if (bias) {
+        const kt_scale f = kt_scale_mul(bs, kt_scale_recip(c));
+        for (size_t i = 0; i < n; i++) acc[i] = (int64_t)((uint64_t)acc[i] + (uint64_t)kt_scale_apply(f, bias[i % out]));
+    }
+    int64_t ymax = 0;
+    for (size_t i = 0; i < n; i++) {
+        const int64_t a = abs_wrap(acc[i]);
+        if (a > ymax) ymax = a;
+    }
+    *ymax_out = ymax;
+    if (ymax == 0) {
+        memset(y, 0, n * sizeof(int32_t));
+    } else {
+        for (size_t i = 0; i < n; i++) y[i] = kt_requant_dyn(acc[i], ACT_LEVELS, ymax);
+        *os = kt_scale_mul(kt_scale_from_ratio(0, (uint64_t)ymax, 0, ACT_LEVELS), c);
+    }
+    free(qx), free(acc);
+}
+
 /* ------------------------------------------------------------------------------------------------------------ */
 /* The 12-bit weight path (this build's own format, restated here as the checker)          */
 /* ------------------------------------------------------------------------------------------------------------ */

@@ -101,6 +101,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_isqrt_u128": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "kt_quant_to": (None, [_P, _SZ, C.c_int64, _P]),
         "kt_requant_dyn": (C.c_int32, [C.c_int64, C.c_int64, C.c_int64]),
+        "kt_quant_linear_forward": (None, [_P, _SZ, _SZ, Scale, _P, _SZ, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale),
+                                           C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
         "kt_w12_pack": (None, [_P, _SZ, _SZ, _P, _P]),
         "kt_w12_get": (C.c_int32, [_P, _P, _SZ, _SZ, _SZ]),
         "kt_w12_linear": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _P]),
@@ -420,6 +422,19 @@ def quant_to(data, xmax: int) -> np.ndarray:
 
 def requant_dyn(v: int, num_level: int, den: int) -> int:
     return lib().kt_requant_dyn(v, num_level, den)
+
+
+def quant_linear_forward(x, rows: int, in_f: int, xs, w, out_f: int, ws, bias=None, bs=(0, 0), threads: int = 0):
+    """QuantLinear::forward_int (layers.rs:275-328): (y codes rows x out_f, (mant, shift), xmax, ymax)."""
+    x, w = _i32(x), _i32(w)
+    assert x.size == rows * in_f and w.size == out_f * in_f
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.int64)
+    y = np.empty(rows * out_f, dtype=np.int32)
+    os_, xmax, ymax = Scale(), C.c_int64(), C.c_int64()
+    lib().kt_quant_linear_forward(_ptr(x), rows, in_f, Scale(*xs), _ptr(w), out_f, Scale(*ws),
+                                  0 if b is None else _ptr(b), Scale(*bs), threads, _ptr(y), C.byref(os_),
+                                  C.byref(xmax), C.byref(ymax))
+    return y.reshape(rows, out_f), (os_.mant, os_.shift), xmax.value, ymax.value
 
 
 # ---------------------------------------------------------------------------------------------------------------

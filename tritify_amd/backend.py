@@ -100,6 +100,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_dec_attention_step": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
         "kt_hip_dec_argmax_part": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
         "kt_hip_dec_embed_argmax": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _P]),
+        "kt_hip_quant_linear_workspace": (_SZ, [_I64, _I64, _I64, _P]),
+        "kt_hip_quant_linear": (_I, [_I, _P, _I64, _I64, _P, _P, _I, _I64, _I64, C.c_int32, _P, _I64, C.c_int32, _P,
+                                     _SZ, _P, _P, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
@@ -300,6 +303,31 @@ def digit_gemm(xa_dev, px: int, wb_dev, pw: int, y_dev, rows: int, out: int, k: 
 def pack_planes(codes_dev, rows: int, k: int, planes: int, planes_dev, stream=None, dev: int = 0) -> None:
     check(lib().kt_hip_pack_planes(dev, _ptr(codes_dev), rows, k, planes, _ptr(planes_dev), _stream(stream)),
           "pack planes")
+
+
+QL_WS_PARTS = 5
+
+
+def quant_linear_workspace(rows: int, in_f: int, out_f: int) -> tuple[int, list[int]]:
+    """Workspace bytes of quant_linear for rows x in_f -> out_f, and the byte offsets of its parts."""
+    off = (_SZ * QL_WS_PARTS)()
+    n = lib().kt_hip_quant_linear_workspace(rows, in_f, out_f, off)
+    if n == 0:
+        raise ValueError("quant_linear: rows, in_f and out_f must be >= 1")
+    return n, list(off)
+
+
+def quant_linear(x_dev, rows: int, in_f: int, xs_dev, w_planes_dev, pw: int, out_f: int, w_scale, bias_dev,
+                 b_scale, ws_dev, ws_bytes: int, y_dev, os_dev, stream=None, dev: int = 0) -> None:
+    """QuantLinear::forward_int on the device (layers.rs:275-328): y_dev (rows x out_f i32 codes) and os_dev (their
+    scale record) from x_dev at the scale record xs_dev. Scales are (mant, shift) pairs. Asynchronous."""
+    bm, bs = b_scale if b_scale is not None else (0, 0)
+    check(
+        lib().kt_hip_quant_linear(dev, _ptr(x_dev), rows, in_f, _ptr(xs_dev), _ptr(w_planes_dev), pw, out_f,
+                                  int(w_scale[0]), int(w_scale[1]), _ptr(bias_dev), int(bm), int(bs), _ptr(ws_dev),
+                                  ws_bytes, _ptr(y_dev), _ptr(os_dev), _stream(stream)),
+        "quant linear",
+    )
 
 
 def probe_mfma(a_dev, b_dev, c32_dev, c16_dev, stream=None, dev: int = 0) -> None:

@@ -208,6 +208,34 @@ int kt_hip_digit_gemm(int dev, const int8_t* xa_dev, int px, const int8_t* wb_de
 }
 
 // ----------------------------------------------------------------------------------------------------------------
+// QuantLinear::forward_int on the device (layers.rs:275-328)
+// ----------------------------------------------------------------------------------------------------------------
+
+size_t kt_hip_quant_linear_workspace(int64_t rows, int64_t in_f, int64_t out_f, size_t off[KT_QL_WS_PARTS]) {
+    size_t tmp[KT_QL_WS_PARTS];
+    if (rows < 1 || in_f < 1 || out_f < 1) return 0;
+    return kt::ql_workspace_bytes(rows, in_f, out_f, off ? off : tmp);
+}
+
+int kt_hip_quant_linear(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f, const kt_hip_qscale* xs_dev,
+                        const int8_t* w_planes_dev, int pw, int64_t out_f, int64_t w_mant, int32_t w_shift,
+                        const int64_t* bias_dev, int64_t b_mant, int32_t b_shift, void* ws_dev, size_t ws_bytes,
+                        int32_t* y_dev, kt_hip_qscale* os_dev, void* stream) {
+    if (rows < 1 || in_f < 1 || out_f < 1 || (pw != 1 && pw != 3 && pw != 5) || w_mant < 0 || b_mant < 0)
+        return (int)hipErrorInvalidValue;
+    const int64_t kp = kp_of(in_f);
+    if (rows * kp >= ((int64_t)1 << 31) || rows * out_f >= ((int64_t)1 << 31) || kp > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    if (!x_dev || !xs_dev || !w_planes_dev || !ws_dev || !y_dev || !os_dev ||
+        ws_bytes < kt_hip_quant_linear_workspace(rows, in_f, out_f, nullptr))
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_quant_linear(x_dev, rows, in_f, xs_dev, w_planes_dev, pw, out_f, w_mant, w_shift, bias_dev,
+                                        b_mant, b_shift, flush_of(3, pw), ws_dev, y_dev, os_dev,
+                                        (hipStream_t)stream);
+}
+
+// ----------------------------------------------------------------------------------------------------------------
 // Backend layer (TcLinear, crates/02-runtime/kt-cuda/src/backend.rs:77-192)
 // ----------------------------------------------------------------------------------------------------------------
 

@@ -52,6 +52,11 @@ hipError_t launch_dec_embed_argmax(const uint64_t* part, int nparts, const int16
 hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int F, int kp,
                              const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift, int8_t* y,
                              int ystride, hipStream_t s);
+size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]);
+hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
+                               const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
+                               const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
+                               int32_t* y, kt_hip_qscale* os, hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

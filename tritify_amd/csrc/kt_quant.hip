@@ -1,0 +1,337 @@
+// QuantLinear::forward_int (crates/01-engine/kt-core/src/layers.rs:275-328) with every pass on the device: the
+// reference's dynamic per-tensor quantization around the exact digit-plane GEMM, for i32 activation codes at any
+// scale and weight codes held as base-256 digit planes.
+//
+//   ql_absmax   partial maxima of |x|                                              (xmax, layers.rs:279)
+//   ql_scale    xmax, then the Scale products c = from_ratio(xmax, WLEVELS) * xs * ws and the bias factor
+//               f = bs * c^-1, in one thread (128-bit integer arithmetic, kt-int/src/lib.rs:191-280)
+//   ql_quant    qx = quant_to(x, xmax) (layers.rs:23-31) split straight into 3 balanced base-256 planes
+//   plane GEMM  acc = qx . w^T in i64 (kt_kernels.hip, plane_gemm_kernel)
+//   ql_bias     acc += f.apply(bias[o]) in place, and partial maxima of |acc|   (layers.rs:304-321)
+//   ql_requant  ymax, y = requant_dyn(acc, ACT_LEVELS, ymax) and the output scale (layers.rs:33-39, 321-327)
+//
+// No host synchronization: the maxima and the scales stay in the workspace, and the output scale is written to a
+// device record the next layer reads as its input scale. Integer arithmetic only, except a double-precision
+// quotient estimate in ql_requant and ql_quant that is corrected to the exact integer quotient before use.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kt_kernels.h"
+
+namespace kt {
+
+namespace {
+
+typedef unsigned __int128 u128;
+typedef __int128 i128;
+
+constexpr int64_t WLEVELS = 265720;       // (3^12 - 1) / 2, layers.rs:16
+constexpr int64_t ACT_LEVELS = 1LL << 28;  // layers.rs:18
+constexpr int QL_THREADS = 256;
+
+struct Sc {
+    int64_t mant;
+    int32_t shift;
+};
+
+__device__ inline int bits_u128(u128 v) {
+    const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
+    return hi ? 128 - __clzll((long long)hi) : (lo ? 64 - __clzll((long long)lo) : 0);
+}
+
+// n / d for d > 0: native when both fit 64 bits, else restoring long division (used by one thread per call).
+__device__ u128 udiv128(u128 n, u128 d) {
+    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
+    u128 q = 0, r = 0;
+    for (int i = bits_u128(n) - 1; i >= 0; i--) {
+        r = (r << 1) | ((n >> i) & 1);
+        if (r >= d) r -= d, q |= (u128)1 << i;
+    }
+    return q;
+}
+
+// Scale::from_ratio (kt-int/src/lib.rs:191-212): a 31-bit-normalized mantissa of num / den, rounded.
+__device__ Sc from_ratio(u128 num, u128 den) {
+    if (num == 0) return Sc{0, 0};
+    while (bits_u128(num) > 64 || bits_u128(den) > 64) num >>= 1, den >>= 1;
+    if (den == 0) den = 1;
+    const int s = 31 - (bits_u128(num) - bits_u128(den));
+    u128 m;
+    if (s >= 0) {
+        m = udiv128((num << s) + den / 2, den);
+    } else {
+        const u128 dd = den << (-s);
+        m = udiv128(num + dd / 2, dd);
+    }
+    return Sc{(int64_t)m, s};
+}
+
+// Scale::mul (lib.rs:252-258)
+__device__ Sc sc_mul(Sc a, Sc b) {
+    if (a.mant == 0 || b.mant == 0) return Sc{0, 0};
+    Sc q = from_ratio((u128)(uint64_t)a.mant * (u128)(uint64_t)b.mant, 1);
+    q.shift += a.shift + b.shift;
+    return q;
+}
+
+// Scale::recip (lib.rs:275-280); a.mant > 0.
+__device__ Sc sc_recip(Sc a) {
+    const Sc r = from_ratio((u128)1 << 40, (u128)(uint64_t)a.mant);
+    return Sc{r.mant, r.shift - a.shift + 40};
+}
+
+// requant / Scale::apply (lib.rs:78-86, 261-272): round(v * mant / 2^shift) half away from zero, i128 product,
+// result cast to i64. Shifts of 127 or more in either direction give 0 (the product has at most 126 bits).
+__device__ inline int64_t sc_apply(Sc a, int64_t v) {
+    if (a.mant == 0) return 0;
+    const i128 prod = (i128)v * (i128)a.mant;
+    if (a.shift <= 0) return a.shift <= -127 ? 0 : (int64_t)(prod << (-a.shift));
+    if (a.shift >= 127) return 0;
+    const i128 half = (i128)1 << (a.shift - 1);
+    return (int64_t)(prod >= 0 ? (prod + half) >> a.shift : -(((-prod) + half) >> a.shift));
+}
+
+// |v| with i64::abs's release-mode wrap (i64::MIN stays negative and never raises a maximum).
+__device__ inline int64_t abs_wrap(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64_t)v) : v; }
+
+// floor(n / d) for 0 <= n < 2^96, 0 < d < 2^63, with the quotient below 2^62: a double estimate (relative error
+// below 2^-50) corrected by the exact remainder.
+__device__ inline uint64_t udiv_est(u128 n, int64_t d) {
+    const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
+    double qd = dn / (double)d;
+    uint64_t q = qd <= 0.0 ? 0 : (qd >= 4.0e18 ? (uint64_t)4e18 : (uint64_t)qd);
+    i128 rem = (i128)n - (i128)q * (i128)d;
+#pragma unroll 1
+    for (int i = 0; i < 4 && rem < 0; i++) q--, rem += d;
+#pragma unroll 1
+    for (int i = 0; i < 4 && rem >= d; i++) q++, rem -= d;
+    return q;
+}
+
+template <typename T>
+__device__ inline T block_max(T v, T* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const T u = __shfl_xor(v, o, 64);
+        v = u > v ? u : v;
+    }
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) v = red[w] > v ? red[w] : v;
+        red[0] = v;
+    }
+    __syncthreads();
+    v = red[0];
+    __syncthreads();
+    return v;
+}
+
+}  // namespace
+
+// The per-call record in the workspace, written by ql_scale_kernel and read by every later pass.
+struct QlState {
+    int64_t xmax;
+    int64_t c_mant, f_mant;
+    int32_t c_shift, f_shift;
+    int32_t mode;  // 0: normal; 1: xmax == 0 (bias codes or zeros); 2: c == 0 (zeros)
+    int32_t pad;
+};
+
+__global__ __launch_bounds__(QL_THREADS) void ql_absmax_kernel(const int32_t* __restrict__ x, int64_t n,
+                                                               uint32_t* __restrict__ part) {
+    __shared__ uint32_t red[QL_THREADS / 64];
+    uint32_t m = 0;
+    for (int64_t i = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * QL_THREADS) {
+        const int32_t v = x[i];
+        const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+        m = a > m ? a : m;
+    }
+    m = block_max(m, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(QL_THREADS) void ql_scale_kernel(const uint32_t* __restrict__ part, int nparts,
+                                                              const kt_hip_qscale* __restrict__ xs, int64_t w_mant,
+                                                              int32_t w_shift, int has_bias, int64_t b_mant,
+                                                              int32_t b_shift, QlState* __restrict__ st) {
+    __shared__ uint32_t red[QL_THREADS / 64];
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
+    m = block_max(m, red);
+    if (threadIdx.x != 0) return;
+    QlState s{};
+    s.xmax = (int64_t)m;
+    if (m == 0) {
+        s.mode = 1;
+    } else {
+        const Sc c = sc_mul(sc_mul(from_ratio((u128)m, (u128)WLEVELS), Sc{xs->mant, xs->shift}), Sc{w_mant, w_shift});
+        s.c_mant = c.mant, s.c_shift = c.shift;
+        if (c.mant == 0) {
+            s.mode = 2;
+        } else if (has_bias) {
+            const Sc f = sc_mul(Sc{b_mant, b_shift}, sc_recip(c));
+            s.f_mant = f.mant, s.f_shift = f.shift;
+        }
+    }
+    *st = s;
+}
+
+// qx = quant_to(x, xmax) for 4 consecutive columns per thread, split into planes [3][rows][kp]; padding columns and
+// the xmax == 0 case give zero digits. |qx| <= WLEVELS < 127 * (1 + 256 + 65536), so 3 balanced digits hold it.
+__global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __restrict__ x, int64_t rows,
+                                                              int64_t in, int64_t kp,
+                                                              const QlState* __restrict__ st,
+                                                              int8_t* __restrict__ xa) {
+    const int64_t quads = rows * (kp / 4);
+    const int64_t xmax = st->xmax, half = xmax / 2;
+    const bool live = st->mode != 1;
+    const size_t plane = (size_t)rows * (size_t)kp;
+    const int64_t qpr = kp / 4, q0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x;
+    const int64_t step = (int64_t)gridDim.x * QL_THREADS, dr = step / qpr, dq = step - dr * qpr;
+    int64_t r = q0 / qpr, cq = q0 - r * qpr;  // (row, quad) of q, advanced incrementally
+    for (int64_t q = q0; q < quads; q += step, r += dr, cq += dq) {
+        if (cq >= qpr) cq -= qpr, r++;
+        const int64_t c0 = cq * 4;
+        uint32_t word[3] = {0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int64_t c = c0 + t;
+            int64_t v = 0;
+            if (live && c < in) {
+                const int64_t num = (int64_t)x[r * in + c] * WLEVELS;  // |num| < 2^49: exact in a double
+                const uint64_t a = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
+                const uint64_t qq = udiv_est((u128)a, xmax);
+                v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
+            }
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                const int64_t d = ((v + 128) & 255) - 128;
+                word[p] |= ((uint32_t)d & 255u) << (8 * t);
+                v = (v - d) >> 8;
+            }
+        }
+        const size_t at = (size_t)r * (size_t)kp + (size_t)c0;
+#pragma unroll
+        for (int p = 0; p < 3; p++) *reinterpret_cast<uint32_t*>(xa + p * plane + at) = word[p];
+    }
+}
+
+// acc[r][o] += f.apply(bias[o]) (wrapping, as the reference's i64 `+=`), then partial maxima of |acc|.
+__global__ __launch_bounds__(QL_THREADS) void ql_bias_kernel(int64_t* __restrict__ acc, int64_t n, int64_t out,
+                                                             const int64_t* __restrict__ bias,
+                                                             const QlState* __restrict__ st,
+                                                             int64_t* __restrict__ part) {
+    __shared__ int64_t red[QL_THREADS / 64];
+    const bool add = bias != nullptr && st->mode == 0;
+    const Sc f{st->f_mant, st->f_shift};
+    int64_t m = 0;
+    const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x, step = (int64_t)gridDim.x * QL_THREADS;
+    const int64_t dstep = step % out;
+    int64_t o = i0 % out;  // i % out, advanced incrementally
+    for (int64_t i = i0; i < n; i += step) {
+        int64_t v = acc[i];
+        if (add) {
+            v = (int64_t)((uint64_t)v + (uint64_t)sc_apply(f, bias[o]));
+            acc[i] = v;
+        }
+        o += dstep;
+        if (o >= out) o -= out;
+        const int64_t a = abs_wrap(v);
+        m = a > m ? a : m;
+    }
+    m = block_max(m, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* __restrict__ acc, int64_t n,
+                                                                int64_t out, const int64_t* __restrict__ bias,
+                                                                const QlState* __restrict__ st,
+                                                                const int64_t* __restrict__ part, int nparts,
+                                                                int64_t b_mant, int32_t b_shift,
+                                                                int32_t* __restrict__ y,
+                                                                kt_hip_qscale* __restrict__ os) {
+    __shared__ int64_t red[QL_THREADS / 64];
+    int64_t m = 0;
+    for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
+    const int64_t ymax = block_max(m, red);
+    const int mode = st->mode;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        kt_hip_qscale o{};
+        o.xmax = st->xmax;
+        if (mode == 1) {
+            if (bias) o.mant = b_mant, o.shift = b_shift;
+        } else if (mode == 0 && ymax > 0) {
+            const Sc s = sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{st->c_mant, st->c_shift});
+            o.mant = s.mant, o.shift = s.shift, o.ymax = ymax;
+        }
+        *os = o;
+    }
+    const u128 halfd = (u128)(uint64_t)(ymax / 2);
+    const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x, step = (int64_t)gridDim.x * QL_THREADS;
+    const int64_t dstep = step % out;
+    int64_t o = i0 % out;  // i % out, advanced incrementally
+    for (int64_t i = i0; i < n; i += step, o = o + dstep >= out ? o + dstep - out : o + dstep) {
+        int32_t r = 0;
+        if (mode == 1) {
+            r = bias ? (int32_t)bias[o] : 0;
+        } else if (mode == 0 && ymax > 0) {
+            const int64_t v = acc[i];
+            const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
+            const uint64_t q = udiv_est(((u128)a << 28) + halfd, ymax);  // requant_dyn(v, 2^28, ymax)
+            r = (int32_t)(v < 0 ? 0 - q : q);
+        }
+        y[i] = r;
+    }
+}
+
+size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]) {
+    const size_t kp = (size_t)((in + 63) / 64 * 64);
+    const size_t sizes[KT_QL_WS_PARTS] = {3 * (size_t)rows * kp, (size_t)rows * (size_t)out * 8, KT_QL_PARTS * 4,
+                                          KT_QL_PARTS * 8, sizeof(QlState)};
+    size_t at = 0;
+    for (int i = 0; i < KT_QL_WS_PARTS; i++) {
+        off[i] = at;
+        at += (sizes[i] + 255) / 256 * 256;
+    }
+    return at;
+}
+
+static int grid_for(int64_t n, int64_t per_thread) {
+    const int64_t g = (n + QL_THREADS * per_thread - 1) / (QL_THREADS * per_thread);
+    return (int)(g < 1 ? 1 : (g > KT_QL_PARTS ? KT_QL_PARTS : g));
+}
+
+hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
+                               const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
+                               const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
+                               int32_t* y, kt_hip_qscale* os, hipStream_t s) {
+    size_t off[KT_QL_WS_PARTS];
+    ql_workspace_bytes(rows, in, out, off);
+    char* base = (char*)ws;
+    int8_t* xa = (int8_t*)(base + off[0]);
+    int64_t* acc = (int64_t*)(base + off[1]);
+    uint32_t* part_x = (uint32_t*)(base + off[2]);
+    int64_t* part_y = (int64_t*)(base + off[3]);
+    QlState* st = (QlState*)(base + off[4]);
+    const int64_t kp = (in + 63) / 64 * 64, n = rows * out;
+
+    const int gx = grid_for(rows * in, 8);
+    ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
+    ql_scale_kernel<<<1, QL_THREADS, 0, s>>>(part_x, gx, xs, w_mant, w_shift, bias != nullptr, b_mant, b_shift, st);
+    ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(x, rows, in, kp, st, xa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    for (int64_t k0 = 0; k0 < kp; k0 += flush_k) {
+        const int64_t k1 = kp - k0 < flush_k ? kp : k0 + flush_k;
+        e = launch_plane_gemm(3, pw, xa, wb, acc, (int)rows, (int)out, (int)kp, (int)k0, (int)k1, k0 > 0, 0, s);
+        if (e != hipSuccess) return e;
+    }
+    const int gy = grid_for(n, 8);
+    ql_bias_kernel<<<gy, QL_THREADS, 0, s>>>(acc, n, out, bias, st, part_y);
+    ql_requant_kernel<<<grid_for(n, 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, part_y, gy, b_mant, b_shift, y, os);
+    return hipGetLastError();
+}
+
+}  // namespace kt
