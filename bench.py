@@ -15,6 +15,8 @@ Also measured, each under "configs" (skip with --configs):
      the ragged grouped W12 GEMMs (gate/up with the SwiGLU epilogue, down), combine; per-stage times.
   5  SAM 2.1 Hiera-B+ encoder GEMMs: the 1024 x 1024 x 3 patch embed as an im2col-fused W12 GEMM (M 65,536, K 147,
      N 112) and the stage-3 MLP (4096 tokens, 448 -> 1792 with the GELU table -> 448).
+  ql the reference's own QuantLinear::forward_int on the device (dynamic per-tensor quantization around the digit
+     GEMM) at the config-3 projection shapes, with the digit GEMM timed alone beside it.
 
 Prints one JSON line on stdout (progress goes to stderr):
   value      logical effective TOPS = 2*M*N*K / time per step (one launch per step)
@@ -23,7 +25,7 @@ Prints one JSON line on stdout (progress goes to stderr):
   cpu_baseline  the reference's multithreaded CPU integer path (the oracle's restatement of linear_cpu, AVX-512
              variant when the host has it) on the same M = 2048 workload, timed on this host's cores
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,3,4,5]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,3,4,5,ql]
 """
 from __future__ import annotations
 
@@ -179,6 +181,83 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
             headline = (ms, wall, n_launch, warm, us, tops)
     del los, nibs
     return sweep, headline, x, w
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# ql: the reference's own QuantLinear::forward_int (dynamic per-tensor quantization around the digit GEMM)
+
+QL_SHAPES = [("prefill gate/up", 512, 896, 4864, False), ("prefill q (bias)", 512, 896, 896, True),
+             ("prefill down", 512, 4864, 896, False), ("decode gate/up", 1, 896, 4864, False)]
+QL_ROTATE = 24  # weight copies cycled per step: 24 x 13 MB of digit planes > the 256 MB Infinity Cache
+
+
+def bench_quant_linear(torch, args) -> dict:
+    """The device QuantLinear::forward_int (layers.rs:275-328) on the config-3 projection shapes, 12-trit codes:
+    x at the 2^28 activation level, weights in +-WLEVELS (3 digit planes each), checked against the oracle's
+    restatement before timing; the digit GEMM alone is timed beside it, the rest is the pre/post passes."""
+    import tritify_amd as T
+    from oracle import oracle as O
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    xs, ws, bs = (1509949440, 58), (1657624235, 49), (1318646415, 57)
+    res = {"workload": "QuantLinear::forward_int (xmax, quant_to, 3x3-plane digit GEMM, bias, ymax, requant_dyn), "
+                       "config-3 projection shapes, 12-trit weights, 2^28-level activations", "shapes": {}}
+    for idx, (name, rows, inp, out, with_bias) in enumerate(QL_SHAPES):
+        x = T.gen_uniform_fast(700 + idx, -(1 << 28), 1 << 28, rows * inp)
+        w = T.gen_uniform_fast(800 + idx, -265720, 265720, out * inp)
+        b = T.gen_uniform_fast(900 + idx, -(1 << 28), 1 << 28, out).astype(np.int64) if with_bias else None
+        ql = T.QuantLinear(name, w, out, inp, ws, None if b is None else (b, bs))
+        y, sc = ql.forward_int_host(x, xs)
+        yo, so, _, ymax = O.quant_linear_forward(x, rows, inp, xs, w, out, ws, bias=b, bs=bs)
+        if not (np.array_equal(y, yo) and (sc["mant"], sc["shift"]) == so and sc["ymax"] == ymax):
+            raise SystemExit(f"bench: quant_linear {name}: the GPU result differs from the CPU oracle")
+        planes = [ql.w_planes] + [ql.w_planes.clone() for _ in range(QL_ROTATE - 1)]
+        xd = torch.from_numpy(x).to(dev)
+        xsd = T.qscale_record(*xs)
+        yd = torch.empty(rows * out, dtype=torch.int32, device=dev)
+        osd = torch.zeros(4, dtype=torch.int64, device=dev)
+        wsb, n = ql.workspace(rows)
+        _, off = T.quant_linear_workspace(rows, inp, out)
+        torch.cuda.synchronize()
+
+        def launch(i):
+            T.quant_linear(xd, rows, inp, xsd, planes[i % QL_ROTATE], ql.pw, out, ws, ql.bias, ql.b_scale, wsb, n,
+                           yd, osd, stream=stream)
+
+        def gemm(i):
+            T.digit_gemm(wsb[off[0]:], 3, planes[i % QL_ROTATE], ql.pw, wsb[off[1]:], rows, out, inp, stream=stream)
+
+        steps = max(args.steps // 2, 50)
+        log(f"bench: quant_linear {name}: bit-exact vs the CPU oracle; timing {steps} steps")
+        ms, _ = time_launches(torch, launch, steps, 10)
+        ms_g, _ = time_launches(torch, gemm, steps, 10)
+        ops = 2.0 * rows * inp * out
+        wbytes = 3 * out * T.kp(inp)
+        res["shapes"][name] = {
+            "rows": rows, "in": inp, "out": out, "bit_exact": True,
+            "us": round(ms * 1e3, 2), "gemm_us": round(ms_g * 1e3, 2),
+            "pre_post_us": round((ms - ms_g) * 1e3, 2),
+            "effective_tops": round(ops / (ms * 1e-3) / 1e12, 2),
+            "gemm_executed_int8_tops": round(9 * ops / (ms_g * 1e-3) / 1e12, 2),
+            "weight_plane_gbs": round(wbytes / (ms_g * 1e-3) / 1e9, 1),
+        }
+        del planes
+        if name == QL_SHAPES[0][0] and not args.no_cpu:
+            cores = cpu_threads()
+            O.set_max_threads(cores)
+            O.quant_linear_forward(x, rows, inp, xs, w, out, ws, threads=cores)
+            reps, t0 = 0, time.perf_counter()
+            while reps < 2 or time.perf_counter() - t0 < 3.0:
+                O.quant_linear_forward(x, rows, inp, xs, w, out, ws, threads=cores)
+                reps += 1
+            dt = (time.perf_counter() - t0) / reps
+            res["cpu_baseline"] = {
+                "value": round(dt * 1e6, 1), "unit": "us per forward_int", "cores": cores, "kind": "port",
+                "sample": f"the oracle's restatement of forward_int (host xmax, quant_to, threaded linear_cpu, "
+                          f"ymax, requant_dyn) on {name} {rows}x{inp}->{out}, {reps} calls",
+            }
+    return res
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -488,7 +567,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--configs", type=str, default="2,3,4,5", help="comma-separated configs to run (2 is the headline)")
+    ap.add_argument("--configs", type=str, default="2,3,4,5,ql",
+                    help="comma-separated configs to run (2 is the headline; ql = the reference's QuantLinear)")
     ap.add_argument("--ms", type=str, default="", help="comma-separated subset of config-2 M to run (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -523,6 +603,9 @@ def main() -> int:
             torch.cuda.empty_cache()
         if c == "3":
             extra["3"] = bench_config3(torch, args)
+            torch.cuda.empty_cache()
+        if c == "ql":
+            extra["ql"] = bench_quant_linear(torch, args)
             torch.cuda.empty_cache()
 
     if headline is None:
