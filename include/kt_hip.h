@@ -237,6 +237,22 @@ int kt_hip_w12_swiglu(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
                       int64_t ffn, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
                       const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride, void* stream);
 
+/* The decoder's one-token products with the RMSNorm before them fused in (RmsNorm then QuantLinear /
+ * SwiGluMlp::forward_int, crates/01-engine/kt-core/src/model.rs:290-353, layers.rs:609-640): r_dev holds m
+ * (1..KT_NORM_MAX_M) rows of the int32 residual, d values each; every CTA normalizes them into LDS with the rule of
+ * kt_hip_dec_rmsnorm (rms = isqrt(floor(sum r^2 / d)), q = clamp(round_half_away(32 r / rms), +-127), 0 when
+ * rms = 0) and then runs the product of kt_hip_w12_linear (out_kind KT_OUT_I64, KT_OUT_I32 or KT_OUT_I8) or of
+ * kt_hip_w12_swiglu on those rows: the same integers as kt_hip_dec_rmsnorm followed by that call, one launch
+ * instead of two. y_dev must not alias r_dev. d <= 8128 and m * kp(d) <= KT_NORM_LDS_BYTES. */
+#define KT_NORM_MAX_M 16
+#define KT_NORM_LDS_BYTES 65536
+int kt_hip_w12_linear_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                           int64_t n, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
+                           void* y_dev, void* stream);
+int kt_hip_w12_swiglu_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                           int64_t ffn, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev,
+                           const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride, void* stream);
+
 /* MoeMlp::combine (layers.rs:893-923) plus the shared expert: out (T x H int8) from d (rows in bucket order, H
  * columns), off (groups + 1, from the grouped GEMM), sel, cw, pos. */
 int kt_hip_moe_combine(int dev, const int8_t* d_dev, const int32_t* off_dev, const int32_t* sel_dev,

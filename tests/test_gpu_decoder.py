@@ -145,3 +145,94 @@ def test_w12_swiglu_every_path(torch_dev, m):
     got = y.cpu().numpy().reshape(m, ffn + 16)
     assert np.array_equal(got[:, :ffn], want), "swiglu differs"
     assert (got[:, ffn:] == 55).all(), "wrote past the row"
+
+
+def rmsnorm_rows_py(r: np.ndarray, d: int) -> np.ndarray:
+    """The decoder's RMSNorm in Python integers (the rule of kt_oracle_layers.c's rmsnorm_rows)."""
+    import math
+
+    out = np.zeros(r.shape, dtype=np.int8)
+    for t, row in enumerate(r.astype(np.int64)):
+        ss = int(sum(int(v) * int(v) for v in row)) % 2**64
+        rms = math.isqrt(ss // d)
+        for i, v in enumerate(row):
+            if rms:
+                a = 32 * int(v)
+                q = (2 * abs(a) + rms) // (2 * rms)
+                out[t, i] = max(-127, min(127, -q if a < 0 else q))
+    return out
+
+
+@pytest.mark.parametrize("m,d", [(1, 896), (1, 200), (5, 64), (16, 320)])
+def test_w12_norm_fused_products(torch_dev, m, d):
+    """kt_hip_w12_linear_norm (I64, I32, I8) and kt_hip_w12_swiglu_norm against the RMSNorm rule in Python integers
+    followed by the oracle's GEMM; residual rows with large, small and all-zero values."""
+    import tritify_amd as TA
+    from tritify_amd import workloads as W
+
+    torch = torch_dev
+    say(f"case: norm-fused products m={m} d={d}")
+    rng = np.random.default_rng(m * 1000 + d)
+    r = rng.integers(-(2**20), 2**20, size=(m, d)).astype(np.int32)
+    if m > 1:
+        r[1] = 0  # rms = 0: the row quantizes to zeros
+    if m > 2:
+        r[2] = rng.integers(-(2**31) + 1, 2**31 - 1, size=d).astype(np.int32)  # sum of squares wraps u64
+    q = rmsnorm_rows_py(r, d)
+    rd = torch.from_numpy(r.reshape(-1)).cuda()
+    n = 200
+    w = W.gen_w12(2000 + d, n * d)
+    mant, shift = W.channel_scales(w, n, d, 40)
+    lo_b, nib_b = TA.w12_bytes(n, d)
+    lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
+    nib = torch.empty(nib_b, dtype=torch.uint8, device="cuda")
+    TA.w12_upload(w, n, d, lo, nib)
+    md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
+    acc, y8 = O.gemm_i8w16(q.reshape(-1), w.astype(np.int16), m, n, d, mant, shift)
+    y64 = torch.empty(m * n, dtype=torch.int64, device="cuda")
+    y32 = torch.empty(m * n, dtype=torch.int32, device="cuda")
+    yi8 = torch.empty(m * n, dtype=torch.int8, device="cuda")
+    TA.w12_linear_norm(rd, lo, nib, m, n, d, y64, TA.OUT_I64)
+    TA.w12_linear_norm(rd, lo, nib, m, n, d, y32, TA.OUT_I32, md, sd)
+    TA.w12_linear_norm(rd, lo, nib, m, n, d, yi8, TA.OUT_I8, md, sd)
+    torch.cuda.synchronize()
+    assert np.array_equal(y64.cpu().numpy(), acc), "i64 accumulators differ"
+    assert np.array_equal(yi8.cpu().numpy(), y8), "int8 outputs differ"
+    want32 = np.array([O.requant_sat(int(a), int(mant[i % n]), int(shift[i % n])) for i, a in enumerate(acc)])
+    assert np.array_equal(y32.cpu().numpy().astype(np.int64), np.clip(want32, -(2**31), 2**31 - 1))
+
+    ffn = 128
+    wg = W.gen_w12(3000 + d, 2 * ffn * d)
+    gm, gs = W.channel_scales(wg, 2 * ffn, d, 40)
+    glo_b, gnib_b = TA.w12_bytes(2 * ffn, d)
+    glo = torch.empty(glo_b, dtype=torch.int8, device="cuda")
+    gnib = torch.empty(gnib_b, dtype=torch.uint8, device="cuda")
+    TA.w12_pack_gate_up(torch.from_numpy(wg).cuda(), ffn, d, glo, gnib)
+    silu = W.silu_table()
+    h = torch.full((m * (ffn + 8),), 55, dtype=torch.int8, device="cuda")
+    TA.w12_swiglu_norm(rd, glo, gnib, m, ffn, d, torch.from_numpy(gm).cuda(), torch.from_numpy(gs).cuda(),
+                       torch.from_numpy(silu).cuda(), 8, h, ffn + 8)
+    torch.cuda.synchronize()
+    _, gu = O.gemm_i8w16(q.reshape(-1), wg.astype(np.int16), m, 2 * ffn, d, gm, gs)
+    gu = gu.reshape(m, 2 * ffn).astype(np.int64)
+    hv = silu.astype(np.int64)[gu[:, :ffn] + 127] * gu[:, ffn:]
+    want = np.clip(np.sign(hv) * ((np.abs(hv) + 128) >> 8), -127, 127).astype(np.int8)
+    got = h.cpu().numpy().reshape(m, ffn + 8)
+    assert np.array_equal(got[:, :ffn], want), "swiglu (norm) differs"
+    assert (got[:, ffn:] == 55).all(), "wrote past the row"
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_decoder_long_context_step(torch_dev, fuse):
+    """Decode steps beyond the attention kernel's two prefetched chunks (positions past 1024, read in its loop) and
+    both RMSNorm placements, against the oracle."""
+    from tritify_amd import workloads as W
+
+    cfg = dict(d=64, ffn=64, nh=2, nkv=1, hd=64, layers=1, vocab=97)
+    say(f"case: decoder long context {cfg} prompt 1100, 4 tokens, fuse={fuse}")
+    m, arrays = build(cfg, 700, 1104, 1100)
+    m.fuse_norm = m.fuse_norm_head = fuse
+    prompt = W.decoder_prompt(701, 1100, cfg["vocab"])
+    toks, logits = m.generate(prompt, 4, graph=fuse)
+    wt, wl = O.dec_generate(dict(cfg, max_pos=1104, h_shift=8), arrays, prompt, 4)
+    assert np.array_equal(logits.reshape(-1), wl) and np.array_equal(toks, wt)

@@ -100,6 +100,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_dec_attention_step": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
         "kt_hip_dec_argmax_part": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
         "kt_hip_dec_embed_argmax": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _P]),
+        "kt_hip_w12_linear_norm": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
+        "kt_hip_w12_swiglu_norm": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I, _P, _I64, _P]),
         "kt_hip_quant_linear_workspace": (_SZ, [_I64, _I64, _I64, _P]),
         "kt_hip_quant_linear": (_I, [_I, _P, _I64, _I64, _P, _P, _I, _I64, _I64, C.c_int32, _P, _I64, C.c_int32, _P,
                                      _SZ, _P, _P, _P]),
@@ -303,6 +305,24 @@ def digit_gemm(xa_dev, px: int, wb_dev, pw: int, y_dev, rows: int, out: int, k: 
 def pack_planes(codes_dev, rows: int, k: int, planes: int, planes_dev, stream=None, dev: int = 0) -> None:
     check(lib().kt_hip_pack_planes(dev, _ptr(codes_dev), rows, k, planes, _ptr(planes_dev), _stream(stream)),
           "pack planes")
+
+
+NORM_MAX_M = 16
+
+
+def w12_linear_norm(r_dev, lo_dev, nib_dev, m: int, n: int, d: int, y_dev, out_kind: int, mant_dev=None,
+                    shift_dev=None, stream=None, dev: int = 0) -> None:
+    """The decoder's RMSNorm of m int32 residual rows (d values each) fused before w12_linear. Asynchronous."""
+    check(lib().kt_hip_w12_linear_norm(dev, _ptr(r_dev), _ptr(lo_dev), _ptr(nib_dev), m, n, d, _ptr(mant_dev),
+                                       _ptr(shift_dev), out_kind, _ptr(y_dev), _stream(stream)), "w12 linear norm")
+
+
+def w12_swiglu_norm(r_dev, lo_dev, nib_dev, m: int, ffn: int, d: int, mant_dev, shift_dev, silu_dev, h_shift: int,
+                    y_dev, y_stride: int, stream=None, dev: int = 0) -> None:
+    """The decoder's RMSNorm of m int32 residual rows fused before w12_swiglu. Asynchronous."""
+    check(lib().kt_hip_w12_swiglu_norm(dev, _ptr(r_dev), _ptr(lo_dev), _ptr(nib_dev), m, ffn, d, _ptr(mant_dev),
+                                       _ptr(shift_dev), _ptr(silu_dev), h_shift, _ptr(y_dev), y_stride,
+                                       _stream(stream)), "w12 swiglu norm")
 
 
 QL_WS_PARTS = 5

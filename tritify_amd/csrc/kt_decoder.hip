@@ -30,14 +30,6 @@ __device__ __forceinline__ int shift_round(int v, int s) {  // |v| < 2^30
 
 __device__ __forceinline__ int clamp127(int64_t v) { return (int)(v > 127 ? 127 : (v < -127 ? -127 : v)); }
 
-// floor(sqrt(n)) exactly: a double estimate, then corrected by whole steps.
-__device__ __forceinline__ uint64_t isqrt_u64(uint64_t n) {
-    uint64_t x = (uint64_t)sqrt((double)n);
-    while (x > 0 && x * x > n) x--;
-    while ((x + 1) * (x + 1) <= n) x++;
-    return x;
-}
-
 // r[t][i] = emb[tokens[t]][i] (int16 codes -> the int32 residual).
 __global__ __launch_bounds__(256) void dec_embed_kernel(const int32_t* __restrict__ tokens,
                                                         const int16_t* __restrict__ emb, int d,
@@ -64,7 +56,8 @@ __global__ __launch_bounds__(256) void dec_rmsnorm_kernel(const int32_t* __restr
     if (tid == 0) s_rms = (int64_t)isqrt_u64((sw[0] + sw[1] + sw[2] + sw[3]) / (uint64_t)d);
     __syncthreads();
     const int64_t rms = s_rms;
-    for (int i = tid; i < d; i += 256) q[(size_t)t * qs + i] = rms == 0 ? 0 : (int8_t)clamp127(div_round(32 * (int64_t)x[i], rms));
+    const uint64_t inv = rms_inv(rms);
+    for (int i = tid; i < d; i += 256) q[(size_t)t * qs + i] = (int8_t)rms_q8(x[i], rms, inv);
 }
 
 // One CTA per row t (position p = pos[0] + t): rotate-half RoPE of the nh q heads and nkv k heads in place
@@ -206,96 +199,187 @@ __global__ __launch_bounds__(1024) void dec_argmax_kernel(const int32_t* __restr
 }
 
 // A single-token decode step's attention with its RoPE and cache append fused (T = 1, position p = pos[0]). One CTA
-// per q head h: the head's q and its kv head's new k are rotated in registers; the first q head of each kv group
-// writes the rotated k and the v to the caches at p; positions j < p come from the caches, j = p from the rotated
-// values held in LDS (no CTA reads position p from the caches, so the writers race with no reader). The integer rules
-// are those of dec_rope_kv_kernel + dec_attention_kernel.
-__global__ __launch_bounds__(256) void dec_attention_step_kernel(const int8_t* __restrict__ qkv,
-                                                                 const int32_t* __restrict__ pos,
-                                                                 int8_t* __restrict__ kc, int8_t* __restrict__ vc,
-                                                                 int nh, int nkv, const int16_t* __restrict__ cosT,
-                                                                 const int16_t* __restrict__ sinT,
-                                                                 const int32_t* __restrict__ exp_tab,
-                                                                 int8_t* __restrict__ o) {
-    constexpr int HD = 64, HH = 32;
-    extern __shared__ int s_sc[];
-    __shared__ int s_red[8];
-    __shared__ int s_part[64][HD + 1];
+// of 512 threads per q head h; positions go in chunks of 512. Every load that does not depend on p is issued first:
+// the first two chunks' k and v (all rows below max_pos; rows at or past p are masked), the EXP table and the head's
+// q / k / v inputs. The head's q and its kv head's new k are rotated into LDS; the first q head of each kv group
+// writes the rotated k and the v to the caches at p; rows j < p come from the caches, j = p from LDS (no CTA uses
+// the cached row p, so the writers race with no reader). Layouts keep each load instruction on few cache lines:
+//   scores: 4 lanes per k row (16 bytes each, summed by two shuffles), 128 rows per pass, 4 passes per chunk;
+//   P.V:    lane group gq = lane / 16 of wave w takes rows 32 i + 4 w + gq (i < 16), lane c = lane % 16 dims
+//           4c .. 4c + 3: one dword of v per row, so a wave reads 4 rows x 64 bytes per instruction.
+// Partial sums of e v stay below 64 * 2^15 * 127 < 2^31 within a chunk and add in int64 across chunks and waves.
+// The integer rules are those of dec_rope_kv_kernel + dec_attention_kernel.
+constexpr int ATT_NT = 512, ATT_PRE = 2;  // threads; chunks of ATT_NT positions prefetched into registers
+
+__global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t* __restrict__ qkv,
+                                                                    const int32_t* __restrict__ pos,
+                                                                    int8_t* __restrict__ kc, int8_t* __restrict__ vc,
+                                                                    int nh, int nkv, const int16_t* __restrict__ cosT,
+                                                                    const int16_t* __restrict__ sinT,
+                                                                    const int32_t* __restrict__ exp_tab,
+                                                                    int8_t* __restrict__ o, int max_pos) {
+    constexpr int HD = 64, HH = 32, NWV = ATT_NT / 64, KP = ATT_NT / 128, VR = ATT_NT / 32;
+    extern __shared__ int s_sc[];  // max_pos: the scores, then the weights
+    __shared__ int s_exp[1024];
+    __shared__ int s_red[2][NWV];
+    __shared__ int64_t s_acc[NWV][HD];
     __shared__ __attribute__((aligned(16))) int8_t s_q[HD], s_k[HD], s_v[HD];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int p = pos[0], rep = nh / nkv, g = h / rep, L = p + 1;
-    if (tid < 2 * HH) {  // rotate q (threads 0..31) and k (32..63) pairs i, i + 32
-        const int i = tid & (HH - 1), isk = tid >> 5;
+    const int rep = nh / nkv, g = h / rep;
+    const size_t rstride = (size_t)nkv * HD;
+    const int8_t* kg = kc + (size_t)g * HD;
+    const int8_t* vg = vc + (size_t)g * HD;
+    const int kq = tid & 3, kr = tid >> 2;      // scores: 16-byte quarter kq of row kr + 128 i
+    const int gq = lane >> 4, c16 = lane & 15;  // P.V: rows 32 i + 4 w + gq, dims 4 c16 ..
+
+    v4i K[ATT_PRE][KP];
+    int V[ATT_PRE][VR];
+#pragma unroll
+    for (int c = 0; c < ATT_PRE; c++) {
+#pragma unroll
+        for (int i = 0; i < KP; i++) {
+            const int j = c * ATT_NT + 128 * i + kr;
+            K[c][i] = j < max_pos ? *reinterpret_cast<const v4i*>(kg + (size_t)j * rstride + 16 * kq) : v4i{};
+        }
+#pragma unroll
+        for (int i = 0; i < VR; i++) {
+            const int j = c * ATT_NT + 32 * i + 4 * w + gq;
+            V[c][i] = j < max_pos ? *reinterpret_cast<const int*>(vg + (size_t)j * rstride + 4 * c16) : 0;
+        }
+    }
+    int ex[1024 / ATT_NT];
+#pragma unroll
+    for (int i = 0; i < 1024 / ATT_NT; i++) ex[i] = exp_tab[tid + i * ATT_NT];
+    const int ri = tid & (HH - 1), isk = (tid >> 5) & 1;
+    int ra = 0, rb = 0;
+    if (tid < 2 * HH) {
         const int8_t* src = qkv + (isk ? (nh + g) * HD : h * HD);
-        const int a = src[i], b = src[i + HH], C = cosT[(size_t)p * HH + i], S = sinT[(size_t)p * HH + i];
-        int8_t* dst = isk ? s_k : s_q;
-        dst[i] = (int8_t)clamp127(shift_round(a * C - b * S, 14));
-        dst[i + HH] = (int8_t)clamp127(shift_round(b * C + a * S, 14));
+        ra = src[ri], rb = src[ri + HH];
     } else if (tid < 2 * HH + HD) {
-        s_v[tid - 2 * HH] = qkv[(nh + nkv + g) * HD + tid - 2 * HH];
+        ra = qkv[(nh + nkv + g) * HD + tid - 2 * HH];
+    }
+    const int p = pos[0], L = p + 1;
+    if (p < 0 || p >= max_pos) {  // a position outside the caches and tables: no access, a zero output
+        if (tid < HD) o[h * HD + tid] = 0;
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 1024 / ATT_NT; i++) s_exp[tid + i * ATT_NT] = ex[i];
+    if (tid < 2 * HH) {  // rotate q (threads 0..31) and k (32..63) pairs i, i + 32
+        const int C = cosT[(size_t)p * HH + ri], S = sinT[(size_t)p * HH + ri];
+        int8_t* dst = isk ? s_k : s_q;
+        dst[ri] = (int8_t)clamp127(shift_round(ra * C - rb * S, 14));
+        dst[ri + HH] = (int8_t)clamp127(shift_round(rb * C + ra * S, 14));
+    } else if (tid < 2 * HH + HD) {
+        s_v[tid - 2 * HH] = (int8_t)ra;
     }
     __syncthreads();
     if (h % rep == 0 && tid < HD) {
-        kc[((size_t)p * nkv + g) * HD + tid] = s_k[tid];
-        vc[((size_t)p * nkv + g) * HD + tid] = s_v[tid];
+        kc[(size_t)p * rstride + g * HD + tid] = s_k[tid];
+        vc[(size_t)p * rstride + g * HD + tid] = s_v[tid];
     }
-    v4i q4[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) q4[c] = *reinterpret_cast<const v4i*>(s_q + 16 * c);
+    const v4i q4 = *reinterpret_cast<const v4i*>(s_q + 16 * kq);
+    const v4i knew = *reinterpret_cast<const v4i*>(s_k + 16 * kq);
+    const int nch = (L + ATT_NT - 1) / ATT_NT;
+
+    // scores into LDS, and their maximum
     int mx = INT_MIN;
-    for (int j = tid; j < L; j += 256) {
-        const int8_t* kr = j < p ? kc + ((size_t)j * nkv + g) * HD : s_k;
-        int s = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const v4i k4 = *reinterpret_cast<const v4i*>(kr + 16 * c);
-            s = __builtin_amdgcn_sdot4(q4[c].x, k4.x, s, false);
-            s = __builtin_amdgcn_sdot4(q4[c].y, k4.y, s, false);
-            s = __builtin_amdgcn_sdot4(q4[c].z, k4.z, s, false);
-            s = __builtin_amdgcn_sdot4(q4[c].w, k4.w, s, false);
+    auto score = [&](int j, v4i k4) {
+        if (j == p) k4 = knew;
+        int sc = __builtin_amdgcn_sdot4(q4.x, k4.x, 0, false);
+        sc = __builtin_amdgcn_sdot4(q4.y, k4.y, sc, false);
+        sc = __builtin_amdgcn_sdot4(q4.z, k4.z, sc, false);
+        sc = __builtin_amdgcn_sdot4(q4.w, k4.w, sc, false);
+        sc += __shfl_xor(sc, 1);
+        sc += __shfl_xor(sc, 2);
+        if (j < L) {
+            if (kq == 0) s_sc[j] = sc;
+            mx = sc > mx ? sc : mx;
         }
-        s_sc[j] = s;
-        mx = s > mx ? s : mx;
+    };
+#pragma unroll
+    for (int c = 0; c < ATT_PRE; c++) {
+#pragma unroll
+        for (int i = 0; i < KP; i++) {
+            if (c * ATT_NT + 128 * i >= L) break;  // uniform: every later row is past p
+            score(c * ATT_NT + 128 * i + kr, K[c][i]);
+        }
+    }
+    for (int c = ATT_PRE; c < nch; c++) {
+#pragma unroll
+        for (int i = 0; i < KP; i++) {
+            const int j = c * ATT_NT + 128 * i + kr;
+            score(j, j < p ? *reinterpret_cast<const v4i*>(kg + (size_t)j * rstride + 16 * kq) : v4i{});
+        }
     }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
         const int v = __shfl_xor(mx, d);
         mx = v > mx ? v : mx;
     }
-    if (lane == 0) s_red[w] = mx;
+    if (lane == 0) s_red[0][w] = mx;
     __syncthreads();
-    mx = s_red[0];
+    mx = s_red[0][0];
 #pragma unroll
-    for (int q = 1; q < 4; q++) mx = s_red[q] > mx ? s_red[q] : mx;
+    for (int q = 1; q < NWV; q++) mx = s_red[0][q] > mx ? s_red[0][q] : mx;
+
+    // weights e_j = EXP[(m - s_j + 64) >> 7] in place of the scores, and their sum
     int den = 0;
-    for (int j = tid; j < L; j += 256) {
-        const int idx = (int)(((int64_t)mx - s_sc[j] + 64) >> 7);
-        const int e = idx < 1024 ? exp_tab[idx] : 0;
+    for (int j = tid; j < L; j += ATT_NT) {
+        const int64_t idx = ((int64_t)mx - s_sc[j] + 64) >> 7;
+        const int e = idx < 1024 ? s_exp[idx] : 0;
         s_sc[j] = e;
         den += e;
     }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) den += __shfl_xor(den, d);
+    if (lane == 0) s_red[1][w] = den;
     __syncthreads();
-    if (lane == 0) s_red[4 + w] = den;
-    const int c = tid & 3, rg = tid >> 2;
-    int acc[16];
+
+    // P.V
+    const int vnew = *reinterpret_cast<const int*>(s_v + 4 * c16);
+    int64_t accd[4] = {0, 0, 0, 0};
+    auto pv_chunk = [&](int c, const int (&v)[VR]) {
+        int a[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0;
-    for (int j = rg; j < L; j += 64) {
-        const v4i v = *reinterpret_cast<const v4i*>(j < p ? vc + ((size_t)j * nkv + g) * HD + 16 * c : s_v + 16 * c);
-        const int e = s_sc[j];
-        const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+        for (int i = 0; i < VR; i++) {
+            if (c * ATT_NT + 32 * i >= L) break;  // uniform: every later row is past p
+            const int j = c * ATT_NT + 32 * i + 4 * w + gq;
+            const int vv = j == p ? vnew : v[i];
+            const int ew = s_sc[j < L ? j : 0];  // branch-free: always an in-range read
+            const int e = j < L ? ew : 0;
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[i] += e * b[i];
+            for (int b = 0; b < 4; b++) a[b] += __mul24(e, (int)(int8_t)(vv >> (8 * b)));  // |e v| < 2^23
+        }
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            a[b] += __shfl_xor(a[b], 16);
+            a[b] += __shfl_xor(a[b], 32);
+            accd[b] += a[b];
+        }
+    };
+#pragma unroll
+    for (int c = 0; c < ATT_PRE; c++) {
+        if (c < nch) pv_chunk(c, V[c]);
     }
+    for (int c = ATT_PRE; c < nch; c++) {
+        int v[VR];
 #pragma unroll
-    for (int i = 0; i < 16; i++) s_part[rg][16 * c + i] = acc[i];
+        for (int i = 0; i < VR; i++) {
+            const int j = c * ATT_NT + 32 * i + 4 * w + gq;
+            v[i] = j < p ? *reinterpret_cast<const int*>(vg + (size_t)j * rstride + 4 * c16) : 0;
+        }
+        pv_chunk(c, v);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) s_acc[w][4 * c16 + b] = accd[b];
+    }
     __syncthreads();
     if (tid < HD) {
-        int64_t sum = 0;
-        for (int q = 0; q < 64; q++) sum += s_part[q][tid];
-        const int64_t dn = (int64_t)s_red[4] + s_red[5] + s_red[6] + s_red[7];
+        int64_t sum = 0, dn = 0;
+#pragma unroll
+        for (int q = 0; q < NWV; q++) sum += s_acc[q][tid], dn += s_red[1][q];
         o[h * HD + tid] = (int8_t)clamp127(div_round(sum, dn));
     }
 }
@@ -410,8 +494,19 @@ hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8
                                      const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
                                      int max_pos, hipStream_t s) {
     const size_t lds = (size_t)max_pos * sizeof(int);
-    dec_attention_step_kernel<<<dim3((unsigned)nh), dim3(256), lds, s>>>(qkv, pos, kc, vc, nh, nkv, cosT, sinT,
-                                                                         exp_tab, o);
+    static size_t lds_static = 0, lds_max = 0;  // queried once per process
+    if (lds_max == 0) {
+        hipFuncAttributes fa;
+        int dev = 0, mx = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+        if (e == hipSuccess) e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&dec_attention_step_kernel));
+        if (e != hipSuccess) return e;
+        lds_static = fa.sharedSizeBytes, lds_max = (size_t)mx;
+    }
+    if (lds_static + lds > lds_max) return hipErrorInvalidValue;  // max_pos too long for one CTA
+    dec_attention_step_kernel<<<dim3((unsigned)nh), dim3(ATT_NT), lds, s>>>(qkv, pos, kc, vc, nh, nkv, cosT, sinT,
+                                                                            exp_tab, o, max_pos);
     return hipGetLastError();
 }
 

@@ -573,6 +573,31 @@ int kt_hip_w12_swiglu(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
                                        silu_dev, h_shift, y_dev, (int)y_stride, nullptr, (hipStream_t)stream);
 }
 
+int kt_hip_w12_linear_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                           int64_t n, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
+                           void* y_dev, void* stream) {
+    if (m < 1 || m > KT_NORM_MAX_M || n < 1 || n > INT_MAX || d < 1 || kp_of(d) > 8128 ||
+        m * kp_of(d) > KT_NORM_LDS_BYTES || r_dev == nullptr || y_dev == nullptr || y_dev == (void*)r_dev ||
+        (out_kind != KT_OUT_I64 && out_kind != KT_OUT_I32 && out_kind != KT_OUT_I8) ||
+        (out_kind != KT_OUT_I64 && (mant_dev == nullptr || shift_dev == nullptr)))
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_linear_norm(r_dev, (int)m, (int)d, lo_dev, nib_dev, (int)n, mant_dev, shift_dev,
+                                           out_kind, y_dev, (hipStream_t)stream);
+}
+
+int kt_hip_w12_swiglu_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
+                           int64_t ffn, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev,
+                           const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride, void* stream) {
+    if (m < 1 || m > KT_NORM_MAX_M || ffn <= 0 || ffn % 64 || ffn > INT_MAX || d < 1 || kp_of(d) > 8128 ||
+        m * kp_of(d) > KT_NORM_LDS_BYTES || y_stride < ffn || y_stride > INT_MAX || r_dev == nullptr ||
+        mant_dev == nullptr || shift_dev == nullptr || silu_dev == nullptr || h_shift < 1 || h_shift > 30)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_swiglu_norm(r_dev, (int)m, (int)d, lo_dev, nib_dev, (int)ffn, mant_dev, shift_dev,
+                                           silu_dev, h_shift, y_dev, (int)y_stride, (hipStream_t)stream);
+}
+
 int kt_hip_moe_combine(int dev, const int8_t* d_dev, const int32_t* off_dev, const int32_t* sel_dev,
                        const int32_t* cw_dev, const int32_t* pos_dev, int64_t tokens, int64_t hidden,
                        int64_t experts, int top_k, int out_shift, int8_t* out_dev, void* stream) {

@@ -57,6 +57,11 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
                                const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
                                const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
                                int32_t* y, kt_hip_qscale* os, hipStream_t s);
+hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int N,
+                                  const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s);
+hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int F,
+                                  const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift,
+                                  int8_t* y, int ystride, hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

@@ -392,18 +392,23 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WA
 // k32 blocks and np whole pairs). The waves meet in LDS in i64; the per-channel scales are fetched
 // at the start, so the epilogue waits on no memory.
 // ------------------------------------------------------------------------------------------------------------------
-template <int MT, int NW, int U, int OUT, bool SMALL>
+template <int MT, int NW, int U, int OUT, bool SMALL, bool NORM = false>
 __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __restrict__ x,
                                                              const int8_t* __restrict__ wlo,
                                                              const uint8_t* __restrict__ wnib, void* __restrict__ y,
                                                              int M, int N, int kp, const int32_t* __restrict__ mant,
                                                              const int32_t* __restrict__ shift,
-                                                             const int8_t* __restrict__ lut) {
+                                                             const int8_t* __restrict__ lut, int d) {
     constexpr int NT = 64 * NW, OUTS = MT * 256;  // threads; outputs of the CTA (MT row tiles x 16 columns)
     static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
+    static_assert(!NORM || (MT == 1 && SMALL), "the RMSNorm prologue serves M <= 16 with int32 dots");
     typedef typename std::conditional<SMALL, int32_t, int64_t>::type part_t;  // SMALL: every dot fits int32
     __shared__ part_t sP[NW][OUTS];
     __shared__ int32_t sX[NW][MT * 16];
+    extern __shared__ __attribute__((aligned(16))) int8_t sQ[];  // NORM: the normalized rows, M x kp
+    __shared__ uint64_t sNss[NORM ? NW * 16 : 1], sNrq[NORM ? 32 : 1];
+    int32_t pre[2];  // NORM: row 0 of the residual, loaded first
+    if constexpr (NORM) norm_preload<64 * NW, 2>(reinterpret_cast<const int32_t*>(x), d, pre);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar load offsets
     const int cb = blockIdx.x >> 1, hb = blockIdx.x & 1, n0 = cb * 32 + 16 * hb;
@@ -441,8 +446,21 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
             const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
             L[u] = bload16(rL, oL, pl * 2048u);
             D[u] = bload8(rN, oN, pl * 1024u);
+            if constexpr (!NORM) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
+                for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
+            }
+        }
+        if constexpr (NORM) {  // x rows from LDS, normalized there while the first weight loads are in flight
+            __builtin_amdgcn_sched_barrier(0);
+            if (b == 0) norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int p = w + NW * (U * b + u);
+                const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
+                X[u][0] = c < M ? *reinterpret_cast<const v4i*>(sQ + (size_t)c * kp + pl * 64u + 32 * kbq + 16 * h)
+                                : v4i{};
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -513,16 +531,21 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
 // memory), both streamed in one pass over k. Epilogue: g, u = int8 requant per channel (gate channel u, up channel
 // F + u), h = clamp(requant(silu[g + 127] * u, 1, h_shift)). Every dot is SMALL (kp <= 8128).
 // ------------------------------------------------------------------------------------------------------------------
-template <int MT, int NW, int U>
+template <int MT, int NW, int U, bool NORM = false>
 __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     int8_t* __restrict__ y, int ystride, int M, int F, int kp, const int32_t* __restrict__ mant,
-    const int32_t* __restrict__ shift, const int16_t* __restrict__ silu, int h_shift) {
+    const int32_t* __restrict__ shift, const int16_t* __restrict__ silu, int h_shift, int d) {
     constexpr int NT = 64 * NW, OUTS = MT * 256;
     static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
+    static_assert(!NORM || MT == 1, "the RMSNorm prologue serves M <= 16");
     __shared__ int32_t sPg[NW][OUTS], sPu[NW][OUTS];
     __shared__ int32_t sX[NW][MT * 16];
     __shared__ int16_t sSilu[256];
+    extern __shared__ __attribute__((aligned(16))) int8_t sQ[];  // NORM: the normalized rows, M x kp
+    __shared__ uint64_t sNss[NORM ? NW * 16 : 1], sNrq[NORM ? 32 : 1];
+    int32_t pre[2];  // NORM: row 0 of the residual, loaded first
+    if constexpr (NORM) norm_preload<64 * NW, 2>(reinterpret_cast<const int32_t*>(x), d, pre);
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int u0 = 16 * blockIdx.x, cbg = 2 * (u0 >> 5), hb = (u0 >> 4) & 1;
@@ -563,8 +586,21 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
             Dg[u] = bload8(rN, oN, pl * 1024u);
             Lu[u] = bload16(rL, uL, pl * 2048u);
             Du[u] = bload8(rN, uN, pl * 1024u);
+            if constexpr (!NORM) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
+                for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
+            }
+        }
+        if constexpr (NORM) {  // x rows from LDS, normalized there while the first weight loads are in flight
+            __builtin_amdgcn_sched_barrier(0);
+            if (b == 0) norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int p = w + NW * (U * b + u);
+                const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
+                X[u][0] = c < M ? *reinterpret_cast<const v4i*>(sQ + (size_t)c * kp + pl * 64u + 32 * kbq + 16 * h)
+                                : v4i{};
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -687,10 +723,10 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     if (M <= 16 * mt) {                                                                                             \
         if (kp <= KT_SMALL_KP)                                                                                      \
             w12_skinny_kernel<mt, nw, u, OUT, true><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, M, N, kp, mant,   \
-                                                                                   shift, lut);                     \
+                                                                                   shift, lut, 0);                  \
         else                                                                                                        \
             w12_skinny_kernel<mt, nw, u, OUT, false><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, M, N, kp, mant,  \
-                                                                                    shift, nullptr);                \
+                                                                                    shift, nullptr, 0);             \
         return hipGetLastError();                                                                                   \
     }
         KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2) KT_SKINNY(8, 4, 4)
@@ -734,13 +770,55 @@ hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* n
 #define KT_SWIGLU(mt, nw, u)                                                                                         \
     if (M <= 16 * mt) {                                                                                              \
         w12_skinny_swiglu_kernel<mt, nw, u><<<grid, dim3(64 * nw), 0, s>>>(x, lo, nib, y, ystride, M, F, kp, mant,  \
-                                                                           shift, silu, h_shift);                    \
+                                                                           shift, silu, h_shift, 0);                 \
         return hipGetLastError();                                                                                    \
     }
         KT_SWIGLU(1, 8, 4) KT_SWIGLU(2, 8, 2) KT_SWIGLU(4, 8, 1) KT_SWIGLU(8, 4, 2)
 #undef KT_SWIGLU
     }
     return hipErrorInvalidValue;  // the caller takes the grouped kernel (one group) for longer batches
+}
+
+// The RMSNorm-fused skinny products (M <= 16): x is the int32 residual, M rows of d values; kp = d rounded up to 64.
+static bool norm_shape_ok(int M, int d, int kp) {
+    return M >= 1 && M <= 16 && d >= 1 && kp == (d + 63) / 64 * 64 && kp <= KT_SMALL_KP &&
+           (int64_t)M * kp <= KT_NORM_LDS_MAX;
+}
+
+hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int N,
+                                  const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s) {
+    const int kp = (d + 63) / 64 * 64;
+    if (N <= 0 || !norm_shape_ok(M, d, kp) || 2 * ceil_div(N, 32) > INT32_MAX) return hipErrorInvalidValue;
+    dim3 grid((unsigned)(2 * ceil_div(N, 32))), block(64 * 8);
+    const size_t lds = (size_t)M * kp;
+    const int8_t* x = reinterpret_cast<const int8_t*>(r);
+    switch (out_kind) {
+        case KT_OUT_I64:
+            w12_skinny_kernel<1, 8, 4, KT_OUT_I64, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
+                                                                                       shift, nullptr, d);
+            break;
+        case KT_OUT_I32:
+            w12_skinny_kernel<1, 8, 4, KT_OUT_I32, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
+                                                                                       shift, nullptr, d);
+            break;
+        case KT_OUT_I8:
+            w12_skinny_kernel<1, 8, 4, KT_OUT_I8, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
+                                                                                      shift, nullptr, d);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int F,
+                                  const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift,
+                                  int8_t* y, int ystride, hipStream_t s) {
+    const int kp = (d + 63) / 64 * 64;
+    if (F <= 0 || F % 32 || !norm_shape_ok(M, d, kp) || h_shift < 1 || h_shift > 30 || ystride < F)
+        return hipErrorInvalidValue;
+    w12_skinny_swiglu_kernel<1, 8, 4, true><<<dim3((unsigned)(F / 16)), dim3(64 * 8), (size_t)M * kp, s>>>(
+        reinterpret_cast<const int8_t*>(r), lo, nib, y, ystride, M, F, kp, mant, shift, silu, h_shift, d);
+    return hipGetLastError();
 }
 
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s) {

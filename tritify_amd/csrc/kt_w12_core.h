@@ -192,6 +192,90 @@ __device__ __forceinline__ int32_t shift_rq8(int v, int sh) {
 // The longest k for which every W12 dot fits int32: 8128 * 128 * 2048 < 2^31 <= 8192 * 128 * 2048.
 #define KT_SMALL_KP 8128
 
+// floor(sqrt(n)) exactly: a double estimate, then corrected by whole steps.
+__device__ __forceinline__ uint64_t isqrt_u64(uint64_t n) {
+    uint64_t x = (uint64_t)sqrt((double)n);
+    while (x > 0 && x * x > n) x--;
+    while ((x + 1) * (x + 1) <= n) x++;
+    return x;
+}
+
+// The decoder's RMSNorm code of one residual value: clamp(div_round(32 x, rms), +-127), 0 when rms = 0 (div_round =
+// round half away from zero). div_round(a, rms) = floor((2|a| + rms) / dd) with a's sign, dd = 2 rms. inv =
+// floor((2^64 - 1) / dd) (rms_inv) makes the quotient one high multiply: below the clamp n = 2|a| + rms < 2^38, so
+// mulhi(n, inv) is the exact quotient or one less, and the remainder test settles it.
+__device__ __forceinline__ uint64_t rms_inv(int64_t rms) { return rms > 0 ? ~0ULL / (uint64_t)(2 * rms) : 0; }
+__device__ __forceinline__ int rms_q8(int32_t x, int64_t rms, uint64_t inv) {
+    if (rms == 0) return 0;
+    const int64_t a = 32 * (int64_t)x, aa = a < 0 ? -a : a;
+    if (aa >= 128 * rms) return a < 0 ? -127 : 127;
+    const uint64_t n = (uint64_t)(2 * aa + rms), dd = (uint64_t)(2 * rms);
+    uint64_t q = __umul64hi(n, inv);
+    if ((q + 1) * dd <= n) q++;
+    q = q > 127 ? 127 : q;
+    return a < 0 ? -(int)q : (int)q;
+}
+
+// RMSNorm of rows 0 .. M-1 (M <= 16) of the int32 residual r (row stride d) into int8 rows q[m][0 .. kp) in LDS,
+// zero padded from d: rms = isqrt(floor(sum r^2 / d)) over the row (sum in wrapping u64), then rms_q8 per value. All
+// NT threads share every row; row 0's values tid + j NT (j < PRE) come preloaded in pre[] (norm_preload, issued
+// before anything else so their latency overlaps the caller's weight loads). s_ss (NT / 64 x 16) and s_rq (2 x 16)
+// are LDS scratch. Ends with a barrier.
+template <int NT, int PRE>
+__device__ __forceinline__ void norm_preload(const int32_t* __restrict__ r, int d, int32_t (&pre)[PRE]) {
+#pragma unroll
+    for (int j = 0; j < PRE; j++) {
+        const int i = (int)threadIdx.x + j * NT;
+        pre[j] = i < d ? r[i] : 0;
+    }
+}
+
+template <int NT, int PRE>
+__device__ __forceinline__ void norm_rows_to_lds(const int32_t* __restrict__ r, int M, int d, int kp, int8_t* q,
+                                                 uint64_t* s_ss, uint64_t* s_rq, const int32_t (&pre)[PRE]) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    for (int m = 0; m < M; m++) {
+        uint64_t ss = 0;
+        int i = tid;
+        if (m == 0) {
+#pragma unroll
+            for (int j = 0; j < PRE; j++, i += NT) ss += (uint64_t)((int64_t)pre[j] * pre[j]);  // zero past d
+        }
+        for (; i < d; i += NT) {
+            const int64_t v = r[(size_t)m * d + i];
+            ss += (uint64_t)(v * v);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) s_ss[w * 16 + m] = ss;
+    }
+    __syncthreads();
+    if (tid < M) {
+        uint64_t ss = 0;
+#pragma unroll
+        for (int q2 = 0; q2 < NT / 64; q2++) ss += s_ss[q2 * 16 + tid];
+        const int64_t rms = (int64_t)isqrt_u64(ss / (uint64_t)d);
+        s_rq[tid] = (uint64_t)rms;
+        s_rq[16 + tid] = rms_inv(rms);
+    }
+    __syncthreads();
+    for (int m = 0; m < M; m++) {
+        const int64_t rms = (int64_t)s_rq[m];
+        const uint64_t inv = s_rq[16 + m];
+        int i = tid;
+        if (m == 0) {
+#pragma unroll
+            for (int j = 0; j < PRE; j++, i += NT)
+                if (i < kp) q[i] = (int8_t)(i < d ? rms_q8(pre[j], rms, inv) : 0);
+        }
+        for (; i < kp; i += NT) q[(size_t)m * kp + i] = (int8_t)(i < d ? rms_q8(r[(size_t)m * d + i], rms, inv) : 0);
+    }
+    __syncthreads();
+}
+
+// Longest RMSNorm-fused skinny product: the normalized rows live in LDS (M * kp bytes).
+#define KT_NORM_LDS_MAX KT_NORM_LDS_BYTES
+
 template <int I>
 using slot_t = std::integral_constant<int, I>;
 

@@ -5,7 +5,7 @@ Every weight matrix is resident in HBM as W12 planes with per-channel scales (ga
 the SwiGLU epilogue reads; the embedding doubles as the lm_head, as Qwen2.5-0.5B ties them). A call runs T rows at the
 device-held position: embed -> per layer (RmsNorm, q/k/v GEMM, RoPE + KV append, attention, o GEMM added into the
 residual, RmsNorm, gate/up GEMM with SwiGLU, down GEMM added into the residual) -> final RmsNorm -> lm_head ->
-argmax. Prefill is one call of T = prompt rows; each decode step is one call of T = 1 fed by the previous argmax on
+argmax. For short calls (a decode step) each RmsNorm runs inside the prologue of the product that consumes it. Prefill is one call of T = prompt rows; each decode step is one call of T = 1 fed by the previous argmax on
 the device, so a decode step can be captured once as a HIP graph and replayed. torch allocates the device buffers; it
 computes nothing.
 """
@@ -30,6 +30,10 @@ class DecoderModel:
         self.d, self.ffn, self.nh, self.nkv, self.hd, self.L, self.V = d, ffn, nh, nkv, hd, L, V
         self.nq = (nh + 2 * nkv) * hd
         self.max_pos, self.max_rows, self.h_shift, self.dev = max_pos, max_rows, h_shift, dev
+        # calls of at most NORM_MAX_M rows run the RMSNorm inside the qkv / gate-up products' prologue (one launch
+        # instead of two); the lm_head's final norm likewise when fuse_norm_head is set (off: its 9,496 CTAs would
+        # each repeat the norm, which costs more than the separate launch)
+        self.fuse_norm, self.fuse_norm_head = True, False
         dv = torch.device("cuda", dev)
         self.device = dv
 
@@ -64,7 +68,8 @@ class DecoderModel:
         self.token = zeros(1, torch.int32)
         self.pos = zeros(1, torch.int32)
         self.step = zeros(1, torch.int32)
-        self.part = torch.zeros(self.NPARTS, dtype=torch.int64, device=dv)
+        self.nparts = min(self.NPARTS, V)  # argmax first-stage CTAs, each with at least one logit
+        self.part = torch.zeros(self.nparts, dtype=torch.int64, device=dv)
         self.record = None
 
     # weights -------------------------------------------------------------------------------------------------------
@@ -123,14 +128,18 @@ class DecoderModel:
         d, ffn, nh, nkv, hd, nq = self.d, self.ffn, self.nh, self.nkv, self.hd, self.nq
         cache = self.max_pos * nkv * hd
         if tokens_dev is None:
-            B.check(lib.kt_hip_dec_embed_argmax(dev, P(self.part), self.NPARTS, P(self.emb16), d, P(self.r),
+            B.check(lib.kt_hip_dec_embed_argmax(dev, P(self.part), self.nparts, P(self.emb16), d, P(self.r),
                                                 P(self.token), P(self.step), s), "dec embed argmax")
         else:
             B.check(lib.kt_hip_dec_embed(dev, P(tokens_dev), T, P(self.emb16), d, P(self.r), s), "dec embed")
+        fuse = self.fuse_norm and T <= B.NORM_MAX_M  # RMSNorm inside the skinny products' prologue
         for l in range(self.L):
             kc, vc = P(self.kc) + l * cache, P(self.vc) + l * cache
-            B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
-            self._gemm("qkv", l, self.xn, T, nq, d, self.qkv, B.OUT_I8, s)
+            if fuse:
+                self._gemm_norm("qkv", l, self.r, T, nq, d, self.qkv, B.OUT_I8, s)
+            else:
+                B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
+                self._gemm("qkv", l, self.xn, T, nq, d, self.qkv, B.OUT_I8, s)
             if tokens_dev is None:
                 B.check(lib.kt_hip_dec_attention_step(dev, P(self.qkv), P(self.pos), kc, vc, nh, nkv, hd,
                                                       P(self.rope_cos), P(self.rope_sin), P(self.exp_tab), P(self.o),
@@ -141,18 +150,27 @@ class DecoderModel:
                 B.check(lib.kt_hip_dec_attention(dev, P(self.qkv), T, nq, P(self.pos), kc, vc, nh, nkv, hd,
                                                   P(self.exp_tab), P(self.o), self.max_pos, s), "dec attention")
             self._gemm("o", l, self.o, T, d, nh * hd, self.r, B.OUT_I32_ADD, s)
-            B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
             lo_b, nib_b = self.sizes["gu"]
             lo, nib = self.w["gu"]
             m, sh = self.scale["gu"]
-            B.check(lib.kt_hip_w12_swiglu(dev, P(self.xn), P(lo) + l * lo_b, P(nib) + l * nib_b, T, ffn, d,
-                                          P(m) + l * 8 * ffn, P(sh) + l * 8 * ffn, P(self.silu), self.h_shift,
-                                          P(self.h), ffn, s), "dec gate/up")
+            if fuse:
+                B.check(lib.kt_hip_w12_swiglu_norm(dev, P(self.r), P(lo) + l * lo_b, P(nib) + l * nib_b, T, ffn, d,
+                                                   P(m) + l * 8 * ffn, P(sh) + l * 8 * ffn, P(self.silu),
+                                                   self.h_shift, P(self.h), ffn, s), "dec gate/up")
+            else:
+                B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
+                B.check(lib.kt_hip_w12_swiglu(dev, P(self.xn), P(lo) + l * lo_b, P(nib) + l * nib_b, T, ffn, d,
+                                              P(m) + l * 8 * ffn, P(sh) + l * 8 * ffn, P(self.silu), self.h_shift,
+                                              P(self.h), ffn, s), "dec gate/up")
             self._gemm("dn", l, self.h, T, d, ffn, self.r, B.OUT_I32_ADD, s)
-        B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r) + (T - 1) * d * 4, 1, d, P(self.xn), d, s), "dec rmsnorm")
-        self._gemm("emb", 0, self.xn, 1, self.V, d, self.logits, B.OUT_I32, s)
+        last = P(self.r) + (T - 1) * d * 4
+        if self.fuse_norm_head:
+            self._gemm_norm("emb", 0, last, 1, self.V, d, self.logits, B.OUT_I32, s)
+        else:
+            B.check(lib.kt_hip_dec_rmsnorm(dev, last, 1, d, P(self.xn), d, s), "dec rmsnorm")
+            self._gemm("emb", 0, self.xn, 1, self.V, d, self.logits, B.OUT_I32, s)
         rec = P(self.record) if self.record is not None else None
-        B.check(lib.kt_hip_dec_argmax_part(dev, P(self.logits), self.V, P(self.part), self.NPARTS, rec,
+        B.check(lib.kt_hip_dec_argmax_part(dev, P(self.logits), self.V, P(self.part), self.nparts, rec,
                                            P(self.step), P(self.pos), T, s), "dec argmax")
 
     def _gemm(self, name, l, x, M, N, K, y, out_kind, s) -> None:
@@ -162,6 +180,15 @@ class DecoderModel:
         P = B._ptr
         B.check(B.lib().kt_hip_w12_linear(self.dev, P(x), P(lo) + l * lo_b, P(nib) + l * nib_b, M, N, K,
                                           P(m) + l * N * 4, P(sh) + l * N * 4, out_kind, P(y), s), f"dec {name}")
+
+    def _gemm_norm(self, name, l, r, M, N, K, y, out_kind, s) -> None:
+        lo_b, nib_b = self.sizes[name]
+        lo, nib = self.w[name]
+        m, sh = self.scale[name]
+        P = B._ptr
+        B.check(B.lib().kt_hip_w12_linear_norm(self.dev, P(r), P(lo) + l * lo_b, P(nib) + l * nib_b, M, N, K,
+                                               P(m) + l * N * 4, P(sh) + l * N * 4, out_kind, P(y), s),
+                f"dec {name} (norm)")
 
     def decode_step(self, stream=None) -> None:
         """DecoderModel::decode_step on the device: the previous argmax's token at the current position."""
