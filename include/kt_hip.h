@@ -243,8 +243,9 @@ int kt_hip_w12_swiglu(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
  * kt_hip_dec_rmsnorm (rms = isqrt(floor(sum r^2 / d)), q = clamp(round_half_away(32 r / rms), +-127), 0 when
  * rms = 0) and then runs the product of kt_hip_w12_linear (out_kind KT_OUT_I64, KT_OUT_I32 or KT_OUT_I8) or of
  * kt_hip_w12_swiglu on those rows: the same integers as kt_hip_dec_rmsnorm followed by that call, one launch
- * instead of two. y_dev must not alias r_dev. d <= 8128 and m * kp(d) <= KT_NORM_LDS_BYTES. */
+ * instead of two. y_dev must not alias r_dev. d <= KT_NORM_MAX_D and m * kp(d) <= KT_NORM_LDS_BYTES. */
 #define KT_NORM_MAX_M 16
+#define KT_NORM_MAX_D 2048
 #define KT_NORM_LDS_BYTES 65536
 int kt_hip_w12_linear_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                            int64_t n, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,

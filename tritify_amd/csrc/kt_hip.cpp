@@ -576,7 +576,7 @@ int kt_hip_w12_swiglu(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
 int kt_hip_w12_linear_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                            int64_t n, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
                            void* y_dev, void* stream) {
-    if (m < 1 || m > KT_NORM_MAX_M || n < 1 || n > INT_MAX || d < 1 || kp_of(d) > 8128 ||
+    if (m < 1 || m > KT_NORM_MAX_M || n < 1 || n > INT_MAX || d < 1 || kp_of(d) > KT_NORM_MAX_D ||
         m * kp_of(d) > KT_NORM_LDS_BYTES || r_dev == nullptr || y_dev == nullptr || y_dev == (void*)r_dev ||
         (out_kind != KT_OUT_I64 && out_kind != KT_OUT_I32 && out_kind != KT_OUT_I8) ||
         (out_kind != KT_OUT_I64 && (mant_dev == nullptr || shift_dev == nullptr)))
@@ -589,7 +589,7 @@ int kt_hip_w12_linear_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, 
 int kt_hip_w12_swiglu_norm(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                            int64_t ffn, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev,
                            const int16_t* silu_dev, int h_shift, int8_t* y_dev, int64_t y_stride, void* stream) {
-    if (m < 1 || m > KT_NORM_MAX_M || ffn <= 0 || ffn % 64 || ffn > INT_MAX || d < 1 || kp_of(d) > 8128 ||
+    if (m < 1 || m > KT_NORM_MAX_M || ffn <= 0 || ffn % 64 || ffn > INT_MAX || d < 1 || kp_of(d) > KT_NORM_MAX_D ||
         m * kp_of(d) > KT_NORM_LDS_BYTES || y_stride < ffn || y_stride > INT_MAX || r_dev == nullptr ||
         mant_dev == nullptr || shift_dev == nullptr || silu_dev == nullptr || h_shift < 1 || h_shift > 30)
         return (int)hipErrorInvalidValue;

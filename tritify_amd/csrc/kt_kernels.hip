@@ -418,6 +418,13 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
     const int oc = tid & 15, on = n0 + oc;  // every output of this thread is in column on (NT is a multiple of 16)
     const int32_t om = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? mant[on] : 0;
     const int32_t os = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? shift[on] : 0;
+    // the residual an I32_ADD output adds to, loaded now (one output per thread when OUTS <= NT): the epilogue then
+    // has no dependent load; only this thread reads or writes that element
+    constexpr bool PRE_Y = OUT == KT_OUT_I32_ADD && SMALL && OUTS <= NT;
+    int32_t yres = 0;
+    if constexpr (PRE_Y) {
+        if (tid < OUTS && (tid >> 4) < M && on < N) yres = reinterpret_cast<const int32_t*>(y)[(size_t)(tid >> 4) * N + on];
+    }
 
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
     const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb * KB * 512, (uint32_t)KB * 512);
@@ -437,8 +444,10 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
     v4i L[U], X[U][MT];
     v2i D[U];
     const int np = (KB + 1) / 2, nb = (np + NW * U - 1) / (NW * U);
-    int b = 0;
-    do {  // batch b: U pairs of k32 blocks per wave, all loads in flight before the first MFMA
+    // batch b: U pairs of k32 blocks per wave, all loads in flight before the first MFMA. The RMSNorm variant runs
+    // exactly one batch (the host guarantees it), as straight-line code: no loop header to wait at, so the residual
+    // row's loads are the only ones its prologue waits for.
+    auto batch = [&](const int b) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             // a pair past the end re-reads the last pair (its x is masked below): every load stays in the buffers
@@ -453,7 +462,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
         }
         if constexpr (NORM) {  // x rows from LDS, normalized there while the first weight loads are in flight
             __builtin_amdgcn_sched_barrier(0);
-            if (b == 0) norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
+            norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int p = w + NW * (U * b + u);
@@ -475,7 +484,14 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
                 acc1[t] = mfma16(a, hi, acc1[t]);
             }
         }
-    } while (++b < nb);
+    };
+    if constexpr (NORM) {
+        batch(0);
+    } else {
+        int b = 0;
+        do batch(b);
+        while (++b < nb);
+    }
 
     // the wave's partials (lane l, register r: row 4 g + r of the tile, column c) and row sums into LDS
 #pragma unroll
@@ -508,7 +524,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
                 else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
                 else if constexpr (OUT == KT_OUT_I32_ADD) {
                     int32_t* p = reinterpret_cast<int32_t*>(y) + idx;
-                    *p = sat_add32(*p, col_requant<true>(vi, cq));
+                    *p = sat_add32(PRE_Y ? yres : *p, col_requant<true>(vi, cq));
                 }
                 else {
                     const int q = col_requant<false>(vi, cq);
@@ -550,7 +566,8 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int u0 = 16 * blockIdx.x, cbg = 2 * (u0 >> 5), hb = (u0 >> 4) & 1;
     const int KB = kp / 32;
-    for (int i = tid; i < 256; i += NT) sSilu[i] = silu[i < 255 ? i : 254];
+    static_assert(NT >= 256, "one SiLU table entry per thread");
+    const int16_t silu_v = tid < 256 ? silu[tid < 255 ? tid : 254] : 0;  // to LDS after the mainloop: no wait here
 
     const int oc = tid & 15, ou = u0 + oc;
     const int32_t gm = tid < OUTS ? mant[ou] : 0, gs = tid < OUTS ? shift[ou] : 0;
@@ -576,8 +593,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
     v4i Lg[U], Lu[U], X[U][MT];
     v2i Dg[U], Du[U];
     const int np = KB / 2, nb = (np + NW * U - 1) / (NW * U);
-    int b = 0;
-    do {
+    auto batch = [&](const int b) {  // as in w12_skinny_kernel; the RMSNorm variant runs one batch, loop-free
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int p = w + NW * (U * b + u);
@@ -593,7 +609,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
         }
         if constexpr (NORM) {  // x rows from LDS, normalized there while the first weight loads are in flight
             __builtin_amdgcn_sched_barrier(0);
-            if (b == 0) norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
+            norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int p = w + NW * (U * b + u);
@@ -617,7 +633,14 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
                 au1[t] = mfma16(a, hu, au1[t]);
             }
         }
-    } while (++b < nb);
+    };
+    if constexpr (NORM) {
+        batch(0);
+    } else {
+        int b = 0;
+        do batch(b);
+        while (++b < nb);
+    }
 
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -632,6 +655,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
         s += __shfl_xor(s, 32);
         if (lane < 16) sX[w][t * 16 + lane] = s;
     }
+    if (tid < 256) sSilu[tid] = silu_v;
     __syncthreads();
     const ColQ qg = col_q(gm, gs), qu = col_q(um, us);
 #pragma unroll
@@ -729,6 +753,9 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
                                                                                     shift, nullptr, 0);             \
         return hipGetLastError();                                                                                   \
     }
+        if (kp > 2048 && ctas < 256) {  // long k, few CTAs (M <= 16): 16 waves x 5 pairs, up to kp 5120 in one batch
+            KT_SKINNY(1, 16, 5)
+        }
         KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2) KT_SKINNY(8, 4, 4)
 #undef KT_SKINNY
     }
@@ -780,8 +807,8 @@ hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* n
 }
 
 // The RMSNorm-fused skinny products (M <= 16): x is the int32 residual, M rows of d values; kp = d rounded up to 64.
-static bool norm_shape_ok(int M, int d, int kp) {
-    return M >= 1 && M <= 16 && d >= 1 && kp == (d + 63) / 64 * 64 && kp <= KT_SMALL_KP &&
+static bool norm_shape_ok(int M, int d, int kp) {  // one batch of 8 waves x 4 pairs of k32 blocks: kp <= 2048
+    return M >= 1 && M <= 16 && d >= 1 && kp == (d + 63) / 64 * 64 && kp <= KT_NORM_MAX_D &&
            (int64_t)M * kp <= KT_NORM_LDS_MAX;
 }
 
