@@ -756,6 +756,9 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
         if (kp > 2048 && ctas < 256) {  // long k, few CTAs (M <= 16): 16 waves x 5 pairs, up to kp 5120 in one batch
             KT_SKINNY(1, 16, 5)
         }
+        if (kp <= 1024) {  // short k at M <= 16: 8 waves x 2 pairs cover kp in one batch with fewer clamped re-reads
+            KT_SKINNY(1, 8, 2)
+        }
         KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2) KT_SKINNY(8, 4, 4)
 #undef KT_SKINNY
     }
@@ -800,6 +803,9 @@ hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* n
                                                                            shift, silu, h_shift, 0);                 \
         return hipGetLastError();                                                                                    \
     }
+        if (kp <= 1024) {
+            KT_SWIGLU(1, 8, 2)
+        }
         KT_SWIGLU(1, 8, 4) KT_SWIGLU(2, 8, 2) KT_SWIGLU(4, 8, 1) KT_SWIGLU(8, 4, 2)
 #undef KT_SWIGLU
     }
@@ -812,29 +818,37 @@ static bool norm_shape_ok(int M, int d, int kp) {  // one batch of 8 waves x 4 p
            (int64_t)M * kp <= KT_NORM_LDS_MAX;
 }
 
-hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int N,
-                                  const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s) {
-    const int kp = (d + 63) / 64 * 64;
-    if (N <= 0 || !norm_shape_ok(M, d, kp) || 2 * ceil_div(N, 32) > INT32_MAX) return hipErrorInvalidValue;
+template <int U>
+static hipError_t linear_norm_u(const int8_t* x, int M, int d, int kp, const int8_t* lo, const uint8_t* nib, int N,
+                                const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s) {
     dim3 grid((unsigned)(2 * ceil_div(N, 32))), block(64 * 8);
     const size_t lds = (size_t)M * kp;
-    const int8_t* x = reinterpret_cast<const int8_t*>(r);
     switch (out_kind) {
         case KT_OUT_I64:
-            w12_skinny_kernel<1, 8, 4, KT_OUT_I64, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
+            w12_skinny_kernel<1, 8, U, KT_OUT_I64, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
                                                                                        shift, nullptr, d);
             break;
         case KT_OUT_I32:
-            w12_skinny_kernel<1, 8, 4, KT_OUT_I32, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
+            w12_skinny_kernel<1, 8, U, KT_OUT_I32, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
                                                                                        shift, nullptr, d);
             break;
         case KT_OUT_I8:
-            w12_skinny_kernel<1, 8, 4, KT_OUT_I8, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
+            w12_skinny_kernel<1, 8, U, KT_OUT_I8, true, true><<<grid, block, lds, s>>>(x, lo, nib, y, M, N, kp, mant,
                                                                                       shift, nullptr, d);
             break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+// U (pairs of k32 blocks per wave) is the smallest that covers kp in one batch of 8 waves: fewer clamped re-reads.
+hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int N,
+                                  const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s) {
+    const int kp = (d + 63) / 64 * 64;
+    if (N <= 0 || !norm_shape_ok(M, d, kp) || 2 * ceil_div(N, 32) > INT32_MAX) return hipErrorInvalidValue;
+    const int8_t* x = reinterpret_cast<const int8_t*>(r);
+    if (kp <= 1024) return linear_norm_u<2>(x, M, d, kp, lo, nib, N, mant, shift, out_kind, y, s);
+    return linear_norm_u<4>(x, M, d, kp, lo, nib, N, mant, shift, out_kind, y, s);
 }
 
 hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int F,
@@ -843,8 +857,14 @@ hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* 
     const int kp = (d + 63) / 64 * 64;
     if (F <= 0 || F % 32 || !norm_shape_ok(M, d, kp) || h_shift < 1 || h_shift > 30 || ystride < F)
         return hipErrorInvalidValue;
-    w12_skinny_swiglu_kernel<1, 8, 4, true><<<dim3((unsigned)(F / 16)), dim3(64 * 8), (size_t)M * kp, s>>>(
-        reinterpret_cast<const int8_t*>(r), lo, nib, y, ystride, M, F, kp, mant, shift, silu, h_shift, d);
+    dim3 grid((unsigned)(F / 16)), block(64 * 8);
+    const int8_t* x = reinterpret_cast<const int8_t*>(r);
+    if (kp <= 1024)
+        w12_skinny_swiglu_kernel<1, 8, 2, true><<<grid, block, (size_t)M * kp, s>>>(x, lo, nib, y, ystride, M, F, kp,
+                                                                                    mant, shift, silu, h_shift, d);
+    else
+        w12_skinny_swiglu_kernel<1, 8, 4, true><<<grid, block, (size_t)M * kp, s>>>(x, lo, nib, y, ystride, M, F, kp,
+                                                                                    mant, shift, silu, h_shift, d);
     return hipGetLastError();
 }
 
