@@ -15,6 +15,8 @@
 //   combine one CTA per token: sum_i cw_i d_i + 4096 d_shared, requantized to int8.
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <limits.h>
 #include <stdint.h>
 
@@ -100,34 +102,128 @@ __global__ __launch_bounds__(256) void moe_bucket_kernel(const int32_t* __restri
     if (tid == 0) count[g] = base;
 }
 
-// The grouped GEMM's CTA tile: the dense GEMM's 128 x 128 (4 waves along N, 4 x 1 tiles of 32x32 each).
+// The grouped GEMM's CTA tiles: the dense GEMM's 128 x 128 (4 waves along N, 4 x 1 tiles of 32x32 each), and a
+// 64 x 128 tile (2 x 1 tiles per wave) for a group's last row tile when it holds at most 64 rows, so ragged group
+// tails run half the MFMA work of a full tile.
 typedef W12Tile<1, 4, 1, 4> GTile;
+typedef W12Tile<1, 2, 1, 4> GTileH;
+
+// One output tile of the grouped GEMM: rows row0 .. row0 + rows - 1 of group g, columns n0 .. n0 + BN - 1.
+template <class C, int EPI>
+__device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, uint32_t x_bytes,
+                                             const int32_t* __restrict__ list, int list_stride, int g, int row0,
+                                             int rows, int n0, const int* sOff, const int8_t* __restrict__ wlo,
+                                             const uint8_t* __restrict__ wnib, size_t glo, int N, int kp,
+                                             const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+                                             const int16_t* sSilu, int h_shift, int8_t* __restrict__ y, int ystride,
+                                             int8_t* smem, int* sRow) {
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
+    static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int KB = kp / 32;
+    uint32_t oa[AL];
+#pragma unroll
+    for (int i = 0; i < AL; i++) {
+        const int idx = tid + NT * i, r = idx >> 2;
+        if (idx < AC && r < rows) {
+            const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
+            oa[i] = (uint32_t)xr * (uint32_t)kp + 16 * (idx & 3);
+        } else {
+            oa[i] = x_bytes;  // out of range whatever the k offset: reads zero
+        }
+    }
+    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
+    const int8_t* gl = wlo + (size_t)g * glo;
+    const uint8_t* gn = wnib + (size_t)g * (glo / 2);
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    const int wn = wave % C::WN;
+    uint32_t ob[1] = {(uint32_t)(wn * KB) * 1024 + 16 * lane}, on[1] = {(uint32_t)(wn * KB) * 512 + 8 * lane};
+
+    v16i acc0[C::WTM][1], acc1[C::WTM][1];
+    int rsum[AL];
+    w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
+    w12_row_sums<C>(rsum, sRow);
+
+    const int32_t* gm = mant + (size_t)g * N;
+    const int32_t* gs = shift + (size_t)g * N;
+    int8_t* yg = y + (size_t)(sOff[g] + row0) * ystride;
+    if constexpr (EPI == KT_EPI_I8) {
+        w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, [](int n) { return n; }, smem);
+        __syncthreads();
+        constexpr int CH = BM * BN / 16;
+        const bool vec = n0 + BN <= N && (ystride & 15) == 0;
+#pragma unroll
+        for (int i = 0; i < CH / NT; i++) {
+            const int idx = tid + NT * i, r = idx / (BN / 16), c = (idx % (BN / 16)) * 16;
+            if (r >= rows) continue;
+            const v4i v = *reinterpret_cast<const v4i*>(smem + r * BN + c);
+            int8_t* dst = yg + (size_t)r * ystride + n0 + c;
+            if (vec) {
+                *reinterpret_cast<v4i*>(dst) = v;
+            } else {
+                const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+                for (int q = 0; q < 16 && n0 + c + q < N; q++) dst[q] = b[q];
+            }
+        }
+    } else {
+        const int F = N / 2;
+        auto chan = [F](int n) {
+            const int blk = n >> 5;
+            return (blk & 1) * F + (blk >> 1) * 32 + (n & 31);
+        };
+        w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, chan, smem);
+        __syncthreads();
+        // the tile's columns are gate/up block pairs: hidden units n0/2 .. n0/2 + units - 1
+        const int units = (N - n0 < BN ? N - n0 : BN) / 2;
+        for (int task = tid; task < BM * (BN / 32); task += NT) {
+            const int r = task / (BN / 32), q = task % (BN / 32);  // row, 16-unit chunk
+            if (r >= rows || 16 * q >= units) continue;
+            v4i out;
+            int8_t* ob8 = reinterpret_cast<int8_t*>(&out);
+#pragma unroll
+            for (int t2 = 0; t2 < 16; t2++) {
+                const int u = 16 * q + t2, gc = (u >> 5) * 64 + (u & 31);
+                const int gq = smem[r * BN + gc], uq = smem[r * BN + gc + 32];
+                ob8[t2] = (int8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
+            }
+            *reinterpret_cast<v4i*>(yg + (size_t)r * ystride + n0 / 2 + 16 * q) = out;
+        }
+    }
+}
 
 // Ragged grouped W12 GEMM. Group g has count[g] rows (count null: one group of rows_one rows, a dense product); its
-// row j is x row list[g * list_stride + j] (list != null) or x row off[g] + j (off = the exclusive prefix of count); its weights are the W12 planes at wlo + g * glo (lo) and
-// wnib + g * glo / 2 (nib), n x k with per-channel scales mant/shift + g * n; its output row j is y row off[g] + j
-// (row stride ystride). EPI_I8: y = the int8 requant of the n columns. EPI_SWIGLU: the weights are a gate/up
-// matrix packed with the 32-row interleave (n = 2F), the scales in natural order (gate 0..F-1, up F..2F-1), and
-// y = clamp(requant(silu[gq + 127] * uq, 1, h_shift)) over F columns. off_out (optional) receives off[0..groups].
-// Persistent: CTA b (XCD b % 8) takes the tiles of its XCD's contiguous share of the tile space, so an XCD's L2
-// serves consecutive column tiles of the same rows and consecutive groups' weights.
-template <int EPI>
+// row j is x row list[g * list_stride + j] (list != null) or x row off[g] + j (off = the exclusive prefix of count);
+// its weights are the W12 planes at wlo + g * glo (lo) and wnib + g * glo / 2 (nib), n x k with per-channel scales
+// mant/shift + g * n; its output row j is y row off[g] + j (row stride ystride). EPI_I8: y = the int8 requant of the
+// n columns. EPI_SWIGLU: the weights are a gate/up matrix packed with the 32-row interleave (n = 2F), the scales in
+// natural order (gate 0..F-1, up F..2F-1), and y = clamp(requant(silu[gq + 127] * uq, 1, h_shift)) over F columns.
+// off_out (optional) receives off[0..groups]. The tile space is 128-row tiles x 128-column tiles; with TAILS =
+// GT_MIXED a tile of at most 64 rows (a ragged group tail) runs the 64-row tile, at half the MFMA work, in the same
+// pass (right after its group's other tiles, while their weights are in cache); GT_ALL runs every tile on the
+// 128-row tile (one group: a dense product, whose only short tile is its last). Persistent:
+// CTA b (XCD b % 8) takes the tiles of its XCD's contiguous share of the tile space, so an XCD's L2 serves
+// consecutive column tiles of the same rows and consecutive groups' weights.
+enum { GT_ALL = 0, GT_MIXED = 1 };
+
+template <int EPI, int TAILS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_grouped_kernel(
     const int8_t* __restrict__ x, uint32_t x_bytes, const int32_t* __restrict__ list, int list_stride,
     const int32_t* __restrict__ count, int groups, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     size_t glo, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
     const int16_t* __restrict__ silu, int h_shift, int8_t* __restrict__ y, int ystride,
     int32_t* __restrict__ off_out, int rows_one) {
-    typedef GTile C;
-    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
-    static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
-    __shared__ __attribute__((aligned(16))) int8_t smem[C::RING];
-    __shared__ int sRow[BM];
+    typedef GTile C;  // the tile space
+    typedef GTile CT;  // the computing tile (GT_MIXED: GTileH for a tail of at most 64 rows)
+    static_assert(GTileH::NT == C::NT && GTileH::BN == C::BN && GTileH::RING <= C::RING, "one tile space");
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN;
+    __shared__ __attribute__((aligned(16))) int8_t smem[CT::RING];
+    __shared__ int sRow[CT::BM];
     __shared__ int sRpre[KT_MAX_GROUPS + 1], sOff[KT_MAX_GROUPS + 1];
     __shared__ int scr[8];
     __shared__ int16_t sSilu[256];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     int carry_r = 0, carry_o = 0;
     for (int g0 = 0; g0 < groups; g0 += NT) {
         const int g = g0 + tid, c = g < groups ? (count ? count[g] : rows_one) : 0;
@@ -142,7 +238,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (off_out && blockIdx.x == 0)
         for (int g = tid; g <= groups; g += NT) off_out[g] = sOff[g];
 
-    const int KB = kp / 32, tiles_n = (N + BN - 1) / BN, total = sRpre[groups] * tiles_n;
+    const int tiles_n = (N + BN - 1) / BN, total = sRpre[groups] * tiles_n;
     const int nx = gridDim.x >> 3, xcd = blockIdx.x & 7, per = (total + 7) >> 3;
     const int t_end = min(total, (xcd + 1) * per);
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(x, x_bytes);
@@ -156,75 +252,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         const int g = lo, row0 = (rt - sRpre[g]) * BM, cnt = sOff[g + 1] - sOff[g];
         const int rows = cnt - row0 < BM ? cnt - row0 : BM;
-
-        uint32_t oa[AL];
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            const int idx = tid + NT * i, r = idx >> 2;
-            if (idx < AC && r < rows) {
-                const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
-                oa[i] = (uint32_t)xr * (uint32_t)kp + 16 * (idx & 3);
-            } else {
-                oa[i] = x_bytes;  // out of range whatever the k offset: reads zero
-            }
-        }
-        const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
-        const int8_t* gl = wlo + (size_t)g * glo;
-        const uint8_t* gn = wnib + (size_t)g * (glo / 2);
-        const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
-        const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
-        uint32_t ob[1] = {(uint32_t)(wave * KB) * 1024 + 16 * lane}, on[1] = {(uint32_t)(wave * KB) * 512 + 8 * lane};
-
-        v16i acc0[4][1], acc1[4][1];
-        int rsum[AL];
-        w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
-        w12_row_sums<C>(rsum, sRow);
-
-        const int32_t* gm = mant + (size_t)g * N;
-        const int32_t* gs = shift + (size_t)g * N;
-        int8_t* yg = y + (size_t)(sOff[g] + row0) * ystride;
-        if constexpr (EPI == KT_EPI_I8) {
-            w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, [](int n) { return n; }, smem);
-            __syncthreads();
-            constexpr int CH = BM * BN / 16;
-            const bool vec = n0 + BN <= N && (ystride & 15) == 0;
-#pragma unroll
-            for (int i = 0; i < CH / NT; i++) {
-                const int idx = tid + NT * i, r = idx / (BN / 16), c = (idx % (BN / 16)) * 16;
-                if (r >= rows) continue;
-                const v4i v = *reinterpret_cast<const v4i*>(smem + r * BN + c);
-                int8_t* dst = yg + (size_t)r * ystride + n0 + c;
-                if (vec) {
-                    *reinterpret_cast<v4i*>(dst) = v;
-                } else {
-                    const int8_t* b = reinterpret_cast<const int8_t*>(&v);
-                    for (int q = 0; q < 16 && n0 + c + q < N; q++) dst[q] = b[q];
-                }
-            }
-        } else {
-            const int F = N / 2;
-            auto chan = [F](int n) {
-                const int blk = n >> 5;
-                return (blk & 1) * F + (blk >> 1) * 32 + (n & 31);
-            };
-            w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, chan, smem);
-            __syncthreads();
-            // the tile's columns are gate/up block pairs: hidden units n0/2 .. n0/2 + units - 1
-            const int units = (N - n0 < BN ? N - n0 : BN) / 2;
-            for (int task = tid; task < BM * (BN / 32); task += NT) {
-                const int r = task / (BN / 32), q = task % (BN / 32);  // row, 16-unit chunk
-                if (r >= rows || 16 * q >= units) continue;
-                v4i out;
-                int8_t* ob8 = reinterpret_cast<int8_t*>(&out);
-#pragma unroll
-                for (int t2 = 0; t2 < 16; t2++) {
-                    const int u = 16 * q + t2, gc = (u >> 5) * 64 + (u & 31);
-                    const int gq = smem[r * BN + gc], uq = smem[r * BN + gc + 32];
-                    ob8[t2] = (int8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
-                }
-                *reinterpret_cast<v4i*>(yg + (size_t)r * ystride + n0 / 2 + 16 * q) = out;
-            }
-        }
+        if (TAILS == GT_MIXED && rows <= GTileH::BM)  // uniform: a ragged tail on the 64-row tile
+            grouped_tile<GTileH, EPI>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N, kp,
+                                      mant, shift, sSilu, h_shift, y, ystride, smem, sRow);
+        else
+            grouped_tile<CT, EPI>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N, kp,
+                                  mant, shift, sSilu, h_shift, y, ystride, smem, sRow);
         __syncthreads();  // the next tile's prologue rewrites the ring
     }
 }
@@ -295,16 +328,20 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
     const int64_t ub = ((max_rows + GTile::BM - 1) / GTile::BM + groups) * tiles_n;  // row tiles <= rows/BM + groups
     if (ub * GTile::BN > INT32_MAX) return hipErrorInvalidValue;
     const int64_t grid = ub < 512 ? (ub + 7) / 8 * 8 : 512;  // two CTAs per CU, a multiple of 8 (XCDs)
-    if (epi == KT_EPI_I8)
-        w12_grouped_kernel<KT_EPI_I8><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
-            x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu, h_shift,
-            y, ystride, off_out, (int)max_rows);
-    else if (epi == KT_EPI_SWIGLU)
-        w12_grouped_kernel<KT_EPI_SWIGLU><<<dim3((unsigned)grid), dim3(256), 0, s>>>(
-            x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu, h_shift,
-            y, ystride, off_out, (int)max_rows);
-    else
-        return hipErrorInvalidValue;
+    if (epi != KT_EPI_I8 && epi != KT_EPI_SWIGLU) return hipErrorInvalidValue;
+#define KT_GROUPED(E, T, off)                                                                                        \
+    w12_grouped_kernel<E, T><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, (uint32_t)x_bytes, list, list_stride,   \
+                                                                       count, groups, wlo, wnib, glo, N, kp, mant, \
+                                                                       shift, silu, h_shift, y, ystride, off,      \
+                                                                       (int)max_rows)
+    if (groups == 1) {
+        if (epi == KT_EPI_I8) KT_GROUPED(KT_EPI_I8, GT_ALL, off_out);
+        else KT_GROUPED(KT_EPI_SWIGLU, GT_ALL, off_out);
+    } else {
+        if (epi == KT_EPI_I8) KT_GROUPED(KT_EPI_I8, GT_MIXED, off_out);
+        else KT_GROUPED(KT_EPI_SWIGLU, GT_MIXED, off_out);
+    }
+#undef KT_GROUPED
     return hipGetLastError();
 }
 
