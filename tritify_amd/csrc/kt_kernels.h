@@ -12,8 +12,10 @@ hipError_t launch_pack_planes(const int32_t* codes, int64_t rows, int64_t k, int
                               hipStream_t s);
 hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t ilv, int8_t* lo, uint8_t* nib,
                            hipStream_t s);
+struct QlState;
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
-                             int k0, int k1, int accumulate, int drop_top, hipStream_t s);
+                             int k0, int k1, int accumulate, int drop_top, hipStream_t s,
+                             const int64_t* ql_bias = nullptr, QlState* ql = nullptr);
 hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
                              const int32_t* mant, const int32_t* shift, const int8_t* lut, int out_kind, void* y,
                              hipStream_t s);

@@ -76,10 +76,13 @@ __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, in
 // Digit-plane GEMM (LinearBackend path). CTA = 4 waves in 2x2; each wave WTM x WTN tiles of 32x32; BK = 64.
 // Processes k in [k0, k1) (multiples of 64) and writes y = result (first chunk) or y += result.
 // ------------------------------------------------------------------------------------------------------------------
+// With ql non-null (the last k-chunk of a device QuantLinear call) the epilogue also adds the bias in units of c,
+// (bs * c^-1).apply(bias[n]) when ql->mode == 0, and raises ql->ymax to the largest |result| (layers.rs:314-321).
 template <int PX, int PW, int WTM, int WTN>
 __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
                                                          int64_t* __restrict__ y, int M, int N, int kp, int k0,
-                                                         int k1, int accumulate, int drop_top) {
+                                                         int k1, int accumulate, int drop_top,
+                                                         const int64_t* __restrict__ ql_bias, QlState* ql) {
     constexpr int BK = 64, CPR = BK / 16;
     constexpr int BM = 64 * WTM, BN = 64 * WTN;
     constexpr int NG = PX + PW - 1;
@@ -176,11 +179,14 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
         __syncthreads();
     }
 
+    int64_t lmax = 0;
+    const bool badd = ql && ql_bias && ql->mode == 0;
 #pragma unroll
     for (int i = 0; i < WTM; i++)
 #pragma unroll
         for (int j = 0; j < WTN; j++) {
             const int n = n0 + wn * 32 * WTN + j * 32 + (lane & 31);
+            const uint64_t bc = badd && n < N ? (uint64_t)scale_apply(ql->f_mant, ql->f_shift, ql_bias[n]) : 0;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -193,10 +199,31 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
                 }
                 if (m < M && n < N) {
                     int64_t* p = y + (size_t)m * N + n;
-                    *p = accumulate ? (int64_t)((uint64_t)*p + v) : (int64_t)v;
+                    uint64_t f = accumulate ? (uint64_t)*p + v : v;
+                    if (ql) {
+                        f += bc;
+                        const int64_t a = (int64_t)f < 0 ? (int64_t)(0 - f) : (int64_t)f;  // i64::abs, wrapping
+                        lmax = a > lmax ? a : lmax;
+                    }
+                    *p = (int64_t)f;
                 }
             }
         }
+    if (ql) {  // the CTA's largest |result| into the call's maximum
+        __shared__ int64_t s_max[4];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const int64_t u = __shfl_xor(lmax, o);
+            lmax = u > lmax ? u : lmax;
+        }
+        if (lane == 0) s_max[wave] = lmax;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t b = s_max[0];
+            for (int q = 1; q < 4; q++) b = s_max[q] > b ? s_max[q] : b;
+            if (b > 0) atomicMax(&ql->ymax, (unsigned long long)b);
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -711,23 +738,27 @@ hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t i
 
 template <int PX, int PW>
 static hipError_t plane_gemm_px_pw(const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp, int k0,
-                                   int k1, int accumulate, int drop_top, hipStream_t s) {
+                                   int k1, int accumulate, int drop_top, const int64_t* ql_bias, QlState* ql,
+                                   hipStream_t s) {
     constexpr int NG = PX + PW - 1;
     // keep the accumulators within ~160 registers: 2x2 tiles for <= 2 groups, 1x2 for <= 5, 1x1 beyond
     constexpr int WTM = NG <= 2 ? 2 : 1;
     constexpr int WTN = NG <= 5 ? 2 : 1;
     constexpr int BM = 64 * WTM, BN = 64 * WTN;
     dim3 grid((unsigned)(ceil_div(N, BN) * ceil_div(M, BM)));
-    plane_gemm_kernel<PX, PW, WTM, WTN><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top);
+    plane_gemm_kernel<PX, PW, WTM, WTN><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top,
+                                                                   ql_bias, ql);
     return hipGetLastError();
 }
 
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
-                             int k0, int k1, int accumulate, int drop_top, hipStream_t s) {
+                             int k0, int k1, int accumulate, int drop_top, hipStream_t s, const int64_t* ql_bias,
+                             QlState* ql) {
     if (M <= 0 || N <= 0 || k1 <= k0) return hipSuccess;
     if ((k0 % 64) || (k1 % 64) || k1 > kp || ceil_div(M, 64) * ceil_div(N, 64) > INT32_MAX) return hipErrorInvalidValue;
 #define KT_CASE(a, b) \
-    if (px == a && pw == b) return plane_gemm_px_pw<a, b>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top, s);
+    if (px == a && pw == b)                                                                                  \
+        return plane_gemm_px_pw<a, b>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top, ql_bias, ql, s);
     KT_CASE(1, 1) KT_CASE(1, 3) KT_CASE(1, 5) KT_CASE(3, 1) KT_CASE(3, 3) KT_CASE(3, 5) KT_CASE(5, 1) KT_CASE(5, 3)
     KT_CASE(5, 5)
 #undef KT_CASE

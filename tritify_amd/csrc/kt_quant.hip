@@ -1,14 +1,14 @@
 // QuantLinear::forward_int (crates/01-engine/kt-core/src/layers.rs:275-328) with every pass on the device: the
 // reference's dynamic per-tensor quantization around the exact digit-plane GEMM, for i32 activation codes at any
-// scale and weight codes held as base-256 digit planes.
+// scale and weight codes held as base-256 digit planes. Four launches:
 //
-//   ql_absmax   partial maxima of |x|                                              (xmax, layers.rs:279)
-//   ql_scale    xmax, then the Scale products c = from_ratio(xmax, WLEVELS) * xs * ws and the bias factor
-//               f = bs * c^-1, in one thread (128-bit integer arithmetic, kt-int/src/lib.rs:191-280)
-//   ql_quant    qx = quant_to(x, xmax) (layers.rs:23-31) split straight into 3 balanced base-256 planes
-//   plane GEMM  acc = qx . w^T in i64 (kt_kernels.hip, plane_gemm_kernel)
-//   ql_bias     acc += f.apply(bias[o]) in place, and partial maxima of |acc|   (layers.rs:304-321)
-//   ql_requant  ymax, y = requant_dyn(acc, ACT_LEVELS, ymax) and the output scale (layers.rs:33-39, 321-327)
+//   ql_absmax   partial maxima of |x|                                                    (xmax, layers.rs:279)
+//   ql_quant    xmax from the partials, qx = quant_to(x, xmax) (layers.rs:23-31) split straight into 3 balanced
+//               base-256 planes; CTA 0 also forms the Scale products c = from_ratio(xmax, WLEVELS) * xs * ws and
+//               the bias factor f = bs * c^-1 in one thread (128-bit integer arithmetic, kt-int/src/lib.rs:191-280)
+//   plane GEMM  acc = qx . w^T in i64 (kt_kernels.hip, plane_gemm_kernel), whose epilogue adds f.apply(bias[o])
+//               and raises the call's max |acc| (layers.rs:304-321)
+//   ql_requant  y = requant_dyn(acc, ACT_LEVELS, ymax) and the output scale (layers.rs:33-39, 321-327)
 //
 // No host synchronization: the maxima and the scales stay in the workspace, and the output scale is written to a
 // device record the next layer reads as its input scale. Integer arithmetic only, except a double-precision
@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include "kt_kernels.h"
+#include "kt_w12_core.h"
 
 namespace kt {
 
@@ -80,17 +81,6 @@ __device__ Sc sc_recip(Sc a) {
     return Sc{r.mant, r.shift - a.shift + 40};
 }
 
-// requant / Scale::apply (lib.rs:78-86, 261-272): round(v * mant / 2^shift) half away from zero, i128 product,
-// result cast to i64. Shifts of 127 or more in either direction give 0 (the product has at most 126 bits).
-__device__ inline int64_t sc_apply(Sc a, int64_t v) {
-    if (a.mant == 0) return 0;
-    const i128 prod = (i128)v * (i128)a.mant;
-    if (a.shift <= 0) return a.shift <= -127 ? 0 : (int64_t)(prod << (-a.shift));
-    if (a.shift >= 127) return 0;
-    const i128 half = (i128)1 << (a.shift - 1);
-    return (int64_t)(prod >= 0 ? (prod + half) >> a.shift : -(((-prod) + half) >> a.shift));
-}
-
 // |v| with i64::abs's release-mode wrap (i64::MIN stays negative and never raises a maximum).
 __device__ inline int64_t abs_wrap(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64_t)v) : v; }
 
@@ -105,6 +95,14 @@ __device__ inline uint64_t udiv_est(u128 n, int64_t d) {
     for (int i = 0; i < 4 && rem < 0; i++) q--, rem += d;
 #pragma unroll 1
     for (int i = 0; i < 4 && rem >= d; i++) q++, rem -= d;
+    return q;
+}
+
+// floor(n / d) for 0 <= n < 2^53 and 0 < d < 2^53 (both exact in a double): the correctly rounded double quotient is
+// the exact one or one above it at an integer boundary, which the remainder test corrects.
+__device__ inline uint64_t udiv_est53(uint64_t n, int64_t d) {
+    uint64_t q = (uint64_t)((double)n / (double)d);
+    if (q * (uint64_t)d > n) q--;
     return q;
 }
 
@@ -130,15 +128,6 @@ __device__ inline T block_max(T v, T* red) {
 
 }  // namespace
 
-// The per-call record in the workspace, written by ql_scale_kernel and read by every later pass.
-struct QlState {
-    int64_t xmax;
-    int64_t c_mant, f_mant;
-    int32_t c_shift, f_shift;
-    int32_t mode;  // 0: normal; 1: xmax == 0 (bias codes or zeros); 2: c == 0 (zeros)
-    int32_t pad;
-};
-
 __global__ __launch_bounds__(QL_THREADS) void ql_absmax_kernel(const int32_t* __restrict__ x, int64_t n,
                                                                uint32_t* __restrict__ part) {
     __shared__ uint32_t red[QL_THREADS / 64];
@@ -152,41 +141,41 @@ __global__ __launch_bounds__(QL_THREADS) void ql_absmax_kernel(const int32_t* __
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-__global__ __launch_bounds__(QL_THREADS) void ql_scale_kernel(const uint32_t* __restrict__ part, int nparts,
-                                                              const kt_hip_qscale* __restrict__ xs, int64_t w_mant,
-                                                              int32_t w_shift, int has_bias, int64_t b_mant,
-                                                              int32_t b_shift, QlState* __restrict__ st) {
-    __shared__ uint32_t red[QL_THREADS / 64];
-    uint32_t m = 0;
-    for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
-    m = block_max(m, red);
-    if (threadIdx.x != 0) return;
-    QlState s{};
-    s.xmax = (int64_t)m;
-    if (m == 0) {
-        s.mode = 1;
-    } else {
-        const Sc c = sc_mul(sc_mul(from_ratio((u128)m, (u128)WLEVELS), Sc{xs->mant, xs->shift}), Sc{w_mant, w_shift});
-        s.c_mant = c.mant, s.c_shift = c.shift;
-        if (c.mant == 0) {
-            s.mode = 2;
-        } else if (has_bias) {
-            const Sc f = sc_mul(Sc{b_mant, b_shift}, sc_recip(c));
-            s.f_mant = f.mant, s.f_shift = f.shift;
-        }
-    }
-    *st = s;
-}
-
 // qx = quant_to(x, xmax) for 4 consecutive columns per thread, split into planes [3][rows][kp]; padding columns and
 // the xmax == 0 case give zero digits. |qx| <= WLEVELS < 127 * (1 + 256 + 65536), so 3 balanced digits hold it.
 __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __restrict__ x, int64_t rows,
                                                               int64_t in, int64_t kp,
-                                                              const QlState* __restrict__ st,
+                                                              const uint32_t* __restrict__ part, int nparts,
+                                                              const kt_hip_qscale* __restrict__ xs, int64_t w_mant,
+                                                              int32_t w_shift, int has_bias, int64_t b_mant,
+                                                              int32_t b_shift, QlState* __restrict__ st,
                                                               int8_t* __restrict__ xa) {
+    __shared__ uint32_t red[QL_THREADS / 64];
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
+    m = block_max(m, red);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {  // the call's record, for the GEMM epilogue and ql_requant
+        QlState s{};
+        s.xmax = (int64_t)m;
+        if (m == 0) {
+            s.mode = 1;
+        } else {
+            const Sc c = sc_mul(sc_mul(from_ratio((u128)m, (u128)WLEVELS), Sc{xs->mant, xs->shift}),
+                                Sc{w_mant, w_shift});
+            s.c_mant = c.mant, s.c_shift = c.shift;
+            if (c.mant == 0) {
+                s.mode = 2;
+            } else if (has_bias) {
+                const Sc f = sc_mul(Sc{b_mant, b_shift}, sc_recip(c));
+                s.f_mant = f.mant, s.f_shift = f.shift;
+            }
+        }
+        s.ymax = 0;
+        *st = s;
+    }
     const int64_t quads = rows * (kp / 4);
-    const int64_t xmax = st->xmax, half = xmax / 2;
-    const bool live = st->mode != 1;
+    const int64_t xmax = (int64_t)m, half = xmax / 2;
+    const bool live = m != 0;
     const size_t plane = (size_t)rows * (size_t)kp;
     const int64_t qpr = kp / 4, q0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x;
     const int64_t step = (int64_t)gridDim.x * QL_THREADS, dr = step / qpr, dq = step - dr * qpr;
@@ -202,7 +191,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
             if (live && c < in) {
                 const int64_t num = (int64_t)x[r * in + c] * WLEVELS;  // |num| < 2^49: exact in a double
                 const uint64_t a = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
-                const uint64_t qq = udiv_est((u128)a, xmax);
+                const uint64_t qq = udiv_est53(a, xmax);  // a < 2^31 * WLEVELS + 2^30 < 2^53
                 v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
             }
 #pragma unroll
@@ -218,44 +207,13 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
     }
 }
 
-// acc[r][o] += f.apply(bias[o]) (wrapping, as the reference's i64 `+=`), then partial maxima of |acc|.
-__global__ __launch_bounds__(QL_THREADS) void ql_bias_kernel(int64_t* __restrict__ acc, int64_t n, int64_t out,
-                                                             const int64_t* __restrict__ bias,
-                                                             const QlState* __restrict__ st,
-                                                             int64_t* __restrict__ part) {
-    __shared__ int64_t red[QL_THREADS / 64];
-    const bool add = bias != nullptr && st->mode == 0;
-    const Sc f{st->f_mant, st->f_shift};
-    int64_t m = 0;
-    const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x, step = (int64_t)gridDim.x * QL_THREADS;
-    const int64_t dstep = step % out;
-    int64_t o = i0 % out;  // i % out, advanced incrementally
-    for (int64_t i = i0; i < n; i += step) {
-        int64_t v = acc[i];
-        if (add) {
-            v = (int64_t)((uint64_t)v + (uint64_t)sc_apply(f, bias[o]));
-            acc[i] = v;
-        }
-        o += dstep;
-        if (o >= out) o -= out;
-        const int64_t a = abs_wrap(v);
-        m = a > m ? a : m;
-    }
-    m = block_max(m, red);
-    if (threadIdx.x == 0) part[blockIdx.x] = m;
-}
-
 __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* __restrict__ acc, int64_t n,
                                                                 int64_t out, const int64_t* __restrict__ bias,
                                                                 const QlState* __restrict__ st,
-                                                                const int64_t* __restrict__ part, int nparts,
                                                                 int64_t b_mant, int32_t b_shift,
                                                                 int32_t* __restrict__ y,
                                                                 kt_hip_qscale* __restrict__ os) {
-    __shared__ int64_t red[QL_THREADS / 64];
-    int64_t m = 0;
-    for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
-    const int64_t ymax = block_max(m, red);
+    const int64_t ymax = (int64_t)st->ymax;
     const int mode = st->mode;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         kt_hip_qscale o{};
@@ -313,24 +271,24 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
     int8_t* xa = (int8_t*)(base + off[0]);
     int64_t* acc = (int64_t*)(base + off[1]);
     uint32_t* part_x = (uint32_t*)(base + off[2]);
-    int64_t* part_y = (int64_t*)(base + off[3]);
+    (void)off[3];  // the workspace keeps its fifth part (formerly the |acc| partials) for a stable layout
     QlState* st = (QlState*)(base + off[4]);
     const int64_t kp = (in + 63) / 64 * 64, n = rows * out;
 
     const int gx = grid_for(rows * in, 8);
     ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
-    ql_scale_kernel<<<1, QL_THREADS, 0, s>>>(part_x, gx, xs, w_mant, w_shift, bias != nullptr, b_mant, b_shift, st);
-    ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(x, rows, in, kp, st, xa);
+    ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(x, rows, in, kp, part_x, gx, xs, w_mant, w_shift,
+                                                                      bias != nullptr, b_mant, b_shift, st, xa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     for (int64_t k0 = 0; k0 < kp; k0 += flush_k) {
         const int64_t k1 = kp - k0 < flush_k ? kp : k0 + flush_k;
-        e = launch_plane_gemm(3, pw, xa, wb, acc, (int)rows, (int)out, (int)kp, (int)k0, (int)k1, k0 > 0, 0, s);
+        const bool last = k1 == kp;
+        e = launch_plane_gemm(3, pw, xa, wb, acc, (int)rows, (int)out, (int)kp, (int)k0, (int)k1, k0 > 0, 0, s,
+                              last ? bias : nullptr, last ? st : nullptr);
         if (e != hipSuccess) return e;
     }
-    const int gy = grid_for(n, 8);
-    ql_bias_kernel<<<gy, QL_THREADS, 0, s>>>(acc, n, out, bias, st, part_y);
-    ql_requant_kernel<<<grid_for(n, 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, part_y, gy, b_mant, b_shift, y, os);
+    ql_requant_kernel<<<grid_for(n, 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift, y, os);
     return hipGetLastError();
 }
 

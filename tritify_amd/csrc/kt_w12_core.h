@@ -273,6 +273,28 @@ __device__ __forceinline__ void norm_rows_to_lds(const int32_t* __restrict__ r, 
     __syncthreads();
 }
 
+// The device QuantLinear's per-call record (kt_quant.hip writes it; the digit GEMM's epilogue reads it).
+struct QlState {
+    int64_t xmax;                // max |x|
+    int64_t c_mant, f_mant;      // c = from_ratio(xmax, WLEVELS) * xs * ws; f = bias scale * c^-1
+    int32_t c_shift, f_shift;
+    int32_t mode;                // 0: normal; 1: xmax == 0 (bias codes or zeros); 2: c == 0 (zeros)
+    int32_t pad;
+    unsigned long long ymax;     // max |acc + bias| over the output, raised by the GEMM epilogue's atomics
+};
+
+// Scale::apply / requant (crates/00-kernels/kt-int/src/lib.rs:78-86, 261-272): round(v * mant / 2^shift) half away
+// from zero from the i128 product, cast to i64. Shifts of 127 or more either way give 0 (the product has at most
+// 126 bits).
+__device__ __forceinline__ int64_t scale_apply(int64_t mant, int32_t shift, int64_t v) {
+    if (mant == 0) return 0;
+    const __int128 prod = (__int128)v * (__int128)mant;
+    if (shift <= 0) return shift <= -127 ? 0 : (int64_t)(prod << (-shift));
+    if (shift >= 127) return 0;
+    const __int128 half = (__int128)1 << (shift - 1);
+    return (int64_t)(prod >= 0 ? (prod + half) >> shift : -(((-prod) + half) >> shift));
+}
+
 // Longest RMSNorm-fused skinny product: the normalized rows live in LDS (M * kp bytes).
 #define KT_NORM_LDS_MAX KT_NORM_LDS_BYTES
 
