@@ -28,8 +28,9 @@ __global__ __launch_bounds__(256) void conv_patch_kernel(const uint8_t* __restri
                                                          const int32_t* __restrict__ mant,
                                                          const int32_t* __restrict__ shift, int8_t* __restrict__ out) {
     constexpr int BM = 128, BN = 128, KP = 64 * KTILES, KB = KP / 32, CPT = 2 * KTILES;  // chunks per thread
-    constexpr int NTILE = KTILES < 2 ? 2 : KTILES;
-    static_assert(NTILE * BM * 64 >= BM * BN, "the output tile reuses the A tiles");
+    constexpr int NTILE = KTILES < 3 ? 3 : KTILES;
+    constexpr int SOP = BM + 16;  // output tile row stride: rows 144 bytes apart spread the byte stores over banks
+    static_assert(NTILE * BM * 64 >= BN * SOP, "the output tile reuses the A tiles");
     __shared__ __attribute__((aligned(16))) int8_t sA[NTILE][BM * 64];
     __shared__ int8_t sPatch[CONV_PATCH_MAX];
     __shared__ int8_t sLut[4 * 256];
@@ -56,22 +57,77 @@ __global__ __launch_bounds__(256) void conv_patch_kernel(const uint8_t* __restri
         }
 
     for (int i = tid; i < CI * 256; i += 256) sLut[i] = lut[i];
+    // The staged rows cover image columns from a = ix0 rounded down to a multiple of 4 (dword loads when W % 4 == 0),
+    // so patch column j of the segment sits at byte o + j of its LDS row (row stride LP bytes).
+    const bool vec = (W & 3) == 0;
+    const int a = vec ? ix0 & ~3 : ix0, o = ix0 - a, ND = (L + o + 3) >> 2, LP = vec ? 4 * ND : L;
     for (int kk = tid; kk < KP; kk += 256) {
         if (kk < KK) {
             const int ic = kk / (KH * KW), r = kk - ic * KH * KW, ky = r / KW, kx = r - ky * KW;
-            sKoff[kk] = (ic * KH + ky) * L + kx;
+            sKoff[kk] = (ic * KH + ky) * LP + kx + o;
         } else {
             sKoff[kk] = -1;
         }
     }
-    __syncthreads();
-    // the image rows of this output row segment, as entry codes (zero outside the image)
-    for (int i = tid; i < CI * KH * L; i += 256) {
-        const int rowi = i / L, j = i - rowi * L, ic = rowi / KH, ky = rowi - ic * KH;
-        const int iy = oy * S - P + ky, ix = ix0 + j;
-        int8_t q = 0;
-        if (iy >= 0 && iy < H && ix >= 0 && ix < W) q = sLut[ic * 256 + img[((size_t)ic * H + iy) * W + ix]];
-        sPatch[i] = q;
+    // the image rows of this output row segment, as entry codes (zero outside the image), every load of a pass in
+    // flight before the first use
+    constexpr int RB = 24;
+    const int nrows = CI * KH;
+    if (vec) {  // thread d < ND: dword d of every row (4 pixels, inside or outside the image together)
+        const int col = a + 4 * tid;
+        const bool col_in = tid < ND && col >= 0 && col < W;
+        for (int r0 = 0; r0 < nrows; r0 += RB) {
+            int v[RB];
+            int ic = r0 / KH, ky = r0 - ic * KH;  // of row r0 + rr, advanced without divisions
+            int ics[RB];
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                const int iy = oy * S - P + ky;
+                const bool in = r0 + rr < nrows && col_in && iy >= 0 && iy < H;
+                v[rr] = in ? *reinterpret_cast<const int*>(img + ((size_t)ic * H + iy) * W + col) : 0;
+                ics[rr] = in ? ic : -1;
+                if (++ky == KH) ky = 0, ic++;
+            }
+            if (r0 == 0) __syncthreads();  // the entry table is in LDS
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                if (r0 + rr >= nrows || tid >= ND) continue;
+                int q = 0;
+                if (ics[rr] >= 0) {
+                    const int8_t* lt = sLut + ics[rr] * 256;
+#pragma unroll
+                    for (int b = 0; b < 4; b++) q |= ((int)(uint8_t)lt[(v[rr] >> (8 * b)) & 255]) << (8 * b);
+                }
+                *reinterpret_cast<int*>(sPatch + (r0 + rr) * LP + 4 * tid) = q;
+            }
+        }
+    } else {  // byte loads, one byte per thread and row per pass
+        bool first = true;
+        for (int j = tid; j - tid < L; j += 256) {
+            const int ix = ix0 + j;
+            const bool col_in = j < L && ix >= 0 && ix < W;
+            for (int r0 = 0; r0 < nrows; r0 += RB) {
+                int v[RB];
+                int ic = r0 / KH, ky = r0 - ic * KH;
+#pragma unroll
+                for (int rr = 0; rr < RB; rr++) {
+                    const int iy = oy * S - P + ky;
+                    // a pixel, plus 256 x its channel for the table lookup; -1 for a tap outside the image
+                    v[rr] = r0 + rr < nrows && col_in && iy >= 0 && iy < H
+                                ? (int)img[((size_t)ic * H + iy) * W + ix] + 256 * ic
+                                : -1;
+                    if (++ky == KH) ky = 0, ic++;
+                }
+                if (first) __syncthreads();  // the entry table is in LDS
+                first = false;
+#pragma unroll
+                for (int rr = 0; rr < RB; rr++) {
+                    const int row = r0 + rr;
+                    if (row < nrows && j < L) sPatch[row * LP + j] = v[rr] >= 0 ? sLut[v[rr]] : 0;
+                }
+            }
+        }
+        if (first) __syncthreads();
     }
     __syncthreads();
     // im2col: thread (row m = tid / 2) builds CPT 16-byte chunks of its row and their sum
@@ -124,7 +180,7 @@ __global__ __launch_bounds__(256) void conv_patch_kernel(const uint8_t* __restri
             for (int r = 0; r < 16; r++) {
                 const int m = i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                 const int v = w12_value(acc0[i][r], acc1[i][r], -1920 * sRow[m]) + b;
-                sO[c * BM + m] = (int8_t)col_requant<false>(v, q);
+                sO[c * SOP + m] = (int8_t)col_requant<false>(v, q);
             }
     }
     __syncthreads();
@@ -132,7 +188,7 @@ __global__ __launch_bounds__(256) void conv_patch_kernel(const uint8_t* __restri
     for (int idx = tid; idx < BN * BM / 16; idx += 256) {
         const int c = idx / (BM / 16), m = (idx - c * (BM / 16)) * 16, n = n0 + c;
         if (n >= CO) continue;
-        const v4i v = *reinterpret_cast<const v4i*>(sO + c * BM + m);
+        const v4i v = *reinterpret_cast<const v4i*>(sO + c * SOP + m);
         int8_t* dst = out + ((size_t)n * OH + oy) * OW + ox0 + m;
         if (full) {
             *reinterpret_cast<v4i*>(dst) = v;
@@ -149,7 +205,9 @@ hipError_t launch_conv_patch(const uint8_t* img, const int8_t* lut, int CI, int 
     if (CI < 1 || CI > 4 || KH < 1 || KW < 1 || S < 1 || P < 0 || H + 2 * P < KH || W + 2 * P < KW || CO < 1)
         return hipErrorInvalidValue;
     const int KK = CI * KH * KW;
-    if (KK > 256 || (int64_t)CI * KH * ((int64_t)S * 127 + KW) > CONV_PATCH_MAX) return hipErrorInvalidValue;
+    // staged rows: L = S * 127 + KW bytes, plus up to 6 of dword alignment, at most 1024 (one dword per thread)
+    const int64_t Lrow = (int64_t)S * 127 + KW + 6;
+    if (KK > 256 || Lrow > 1024 || (int64_t)CI * KH * Lrow > CONV_PATCH_MAX) return hipErrorInvalidValue;
     const int OH = (H + 2 * P - KH) / S + 1, OW = (W + 2 * P - KW) / S + 1;
     const int64_t segs = (OW + 127) / 128;
     if ((int64_t)OH * segs > INT32_MAX || (int64_t)CI * H * W > INT32_MAX) return hipErrorInvalidValue;
