@@ -312,7 +312,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WA
     int m0, n0;
     tile_coords(M, N, BM, BN, m0, n0);
     const int KB = kp / 32;
-    if (OUT == KT_OUT_I8 && SMALL && tid < 256) sLut[tid] = lut ? lut[tid < 255 ? tid : 254] : 0;  // NT >= 256
+    if (OUT == KT_OUT_I8 && SMALL)
+        for (int i = tid; i < 256; i += NT) sLut[i] = lut ? lut[i < 255 ? i : 254] : 0;
 
     // A: the CTA's rows; rows past the matrix read as zero (their offsets are past the descriptor)
     const uint32_t rows_a = (uint32_t)(M - m0 < BM ? M - m0 : BM);
@@ -796,6 +797,19 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     const bool small = kp <= KT_SMALL_KP;
     constexpr int WM = KT_W12_WM, WTM = KT_W12_WTM, WTN = KT_W12_WTN, WV = KT_W12_WAVES, NS = KT_W12_NSLOT;
     const int64_t tiles4 = ceil_div(N, 32 * WTN * 4) * ceil_div(M, 32 * WTM * WM);
+    // Fewer 128 x 128 tiles than CUs: 64 x 128 tiles, or 64 x 64 (128 threads) when even those leave CUs idle, so
+    // small products (prefill projections, the SAM MLP) spread over the chip
+    const int64_t tiles_h = ceil_div(N, 128) * ceil_div(M, 64), tiles_q = ceil_div(N, 64) * ceil_div(M, 64);
+    if (tiles4 < 256 && small) {
+        if (tiles_h >= 256 || tiles_q <= tiles_h) {
+            w12_gemm_kernel<1, 2, 1, WV, NS, OUT, true><<<dim3((unsigned)tiles_h), dim3(256), 0, s>>>(
+                x, lo, nib, y, M, N, kp, mant, shift, lut);
+        } else {
+            w12_gemm_kernel<1, 2, 1, WV, NS, OUT, true, 2><<<dim3((unsigned)tiles_q), dim3(128), 0, s>>>(
+                x, lo, nib, y, M, N, kp, mant, shift, lut);
+        }
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)tiles4), block(256 * WM);
     if (small)
         w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift, lut);
