@@ -352,17 +352,26 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WA
             if (CH % NT != 0 && idx >= CH) break;
             const int rt = idx / (BN / 16), c = (idx % (BN / 16)) * 16, m = m0 + rt, n = n0 + c;
             v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
+            // bytes are moved with shifts, never through the vector's address: an addressed vector becomes a
+            // per-thread LDS slot whose indexing reads the dispatch packet, a long stall before the stores
             if (lut) {
-                int8_t* b = reinterpret_cast<int8_t*>(&v);
 #pragma unroll
-                for (int t = 0; t < 16; t++) b[t] = sLut[b[t] + 127];
+                for (int w4 = 0; w4 < 4; w4++) {
+                    const uint32_t xw = (uint32_t)v[w4];
+                    uint32_t yw = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        yw |= (uint32_t)(uint8_t)sLut[(int)(int8_t)(xw >> (8 * t)) + 127] << (8 * t);
+                    v[w4] = (int)yw;
+                }
             }
             int8_t* dst = reinterpret_cast<int8_t*>(y) + (size_t)m * N + n;
             if (full && (N & 15) == 0) {
                 *reinterpret_cast<v4i*>(dst) = v;
             } else if (m < M) {
-                const int8_t* b = reinterpret_cast<const int8_t*>(&v);
-                for (int t = 0; t < 16 && n + t < N; t++) dst[t] = b[t];
+#pragma unroll
+                for (int t = 0; t < 16; t++)
+                    if (n + t < N) dst[t] = (int8_t)((uint32_t)v[t >> 2] >> (8 * (t & 3)));
             }
         }
     } else if constexpr ((OUT == KT_OUT_I32 || OUT == KT_OUT_I32_ADD) && SMALL) {
