@@ -161,9 +161,10 @@ __device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, ui
             int8_t* dst = yg + (size_t)r * ystride + n0 + c;
             if (vec) {
                 *reinterpret_cast<v4i*>(dst) = v;
-            } else {
-                const int8_t* b = reinterpret_cast<const int8_t*>(&v);
-                for (int q = 0; q < 16 && n0 + c + q < N; q++) dst[q] = b[q];
+            } else {  // bytes by shifts: an addressed vector would live in scratch memory
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    if (n0 + c + q < N) dst[q] = (int8_t)((uint32_t)v[q >> 2] >> (8 * (q & 3)));
             }
         }
     } else {
@@ -179,13 +180,13 @@ __device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, ui
         for (int task = tid; task < BM * (BN / 32); task += NT) {
             const int r = task / (BN / 32), q = task % (BN / 32);  // row, 16-unit chunk
             if (r >= rows || 16 * q >= units) continue;
-            v4i out;
-            int8_t* ob8 = reinterpret_cast<int8_t*>(&out);
+            v4i out = {0, 0, 0, 0};
 #pragma unroll
             for (int t2 = 0; t2 < 16; t2++) {
                 const int u = 16 * q + t2, gc = (u >> 5) * 64 + (u & 31);
                 const int gq = smem[r * BN + gc], uq = smem[r * BN + gc + 32];
-                ob8[t2] = (int8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
+                const uint32_t hb = (uint32_t)(uint8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
+                out[t2 >> 2] |= (int)(hb << (8 * (t2 & 3)));
             }
             *reinterpret_cast<v4i*>(yg + (size_t)r * ystride + n0 / 2 + 16 * q) = out;
         }
