@@ -564,8 +564,11 @@ def cpu_baseline_moe(g4: dict, x: np.ndarray, r: np.ndarray) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # 500 warmup launches (about 33 ms at M = 2048) let the GPU's clocks settle after the set-up's idle host work:
+    # the first tens of milliseconds of a burst run at lower clocks (measured 76.6 us per launch with 20 warmup
+    # launches and 200 timed against 65.6 us settled, on one box)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--configs", type=str, default="2,3,4,5,ql",
                     help="comma-separated configs to run (2 is the headline; ql = the reference's QuantLinear)")

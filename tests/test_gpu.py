@@ -413,6 +413,55 @@ def test_w12_two_streams(torch_dev):
         assert np.array_equal(ys[i].cpu().numpy(), O.portable(x, ws[i], m, n, k)), i
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 64), (2100, 3900, 100), (2305, 4000, 704), (4096, 2080, 1000)])
+def test_w12_dma_tile_kernel(torch_dev, m, n, k):
+    """Shapes whose 256 x 128 tiles cover every CU take the DMA-fed GEMM: ragged rows (a one-row last tile) and
+    columns (a last tile of one or a partial column block), k of one and two 64-deep k-tiles (fewer than the ring
+    keeps in flight) and longer; every output kind, the residual add included, against the oracle."""
+    torch = torch_dev
+    T = tb()
+    rng = np.random.default_rng(m + n + k)
+    x = rng.integers(-128, 128, size=m * k).astype(np.int32)
+    w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
+    mant, shift = O.channel_scales(w, n, k, 40)
+    lo, nib = _w12_device(torch, w, n, k)
+    xd = _x_device(torch, x, m, k)
+    md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
+    acc = O.linear_threads(x, w, m, n, k, 16, O.lib().kt_cpu_auto_variant())
+    q32 = O.requant_channels(acc, m, n, mant, shift, -(2**31), 2**31 - 1)
+    res = rng.integers(-(2**31), 2**31, size=m * n, dtype=np.int64).astype(np.int32)
+    res[:4] = [2**31 - 1, -(2**31), 5, -5]  # saturating adds at both ends
+    wants = {T.OUT_I64: acc, T.OUT_I32: q32,
+             T.OUT_I8: O.requant_channels(acc, m, n, mant, shift, -127, 127).astype(np.int8),
+             T.OUT_I32_ADD: np.clip(res.astype(np.int64) + q32, -(2**31), 2**31 - 1).astype(np.int32)}
+    for kind, want in wants.items():
+        say(f"case: w12 dma tile {m}x{n}x{k} out_kind={kind}")
+        y = torch.from_numpy(res.copy()).cuda() if kind == T.OUT_I32_ADD else \
+            torch.empty(m * n, dtype={T.OUT_I64: torch.int64, T.OUT_I32: torch.int32, T.OUT_I8: torch.int8}[kind],
+                        device="cuda")
+        T.w12_linear(xd, lo, nib, m, n, k, y, kind, md, sd)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.array_equal(got, want), (kind, np.argwhere(got != want)[:5].tolist())
+
+
+def test_w12_dma_tile_kernel_past_int32(torch_dev):
+    """The DMA-fed GEMM at k = 8200 (past the int32 recombination: the i64 epilogue) with every product at its
+    largest magnitude: each output is k * x * w exactly."""
+    torch = torch_dev
+    T = tb()
+    m, n, k = 2048, 4096, 8200
+    for xv, wv in [(-128, -2048), (127, -2048)]:
+        lo, nib = _w12_device(torch, np.full(n * k, wv, np.int32), n, k)
+        xd = torch.full((m, T.kp(k)), xv, dtype=torch.int8, device="cuda")
+        xd[:, k:] = 0
+        y = torch.empty(m * n, dtype=torch.int64, device="cuda")
+        say(f"case: w12 dma tile past int32 x={xv} w={wv}")
+        T.w12_linear(xd, lo, nib, m, n, k, y)
+        torch.cuda.synchronize()
+        assert bool((y == k * xv * wv).all().item())
+
+
 def test_config2_full_size_against_fixtures(torch_dev):
     """BASELINE config 2 at its full shape (N = K = 4096, M in {1, 16, 128, 2048}): the i64 accumulators and the
     requantized int8 outputs hash to the fixtures the CPU oracle produced (tests/golden/goldens.json)."""

@@ -293,53 +293,18 @@ __device__ __forceinline__ void tile_coords(int M, int N, int BM, int BN, int& m
 #define KT_W12_NSLOT 4
 #endif
 
-// An optional int8 -> int8 table (`lut`, 255 entries indexed by q + 127) is applied after the int8 requant: the
-// activation-code epilogue (GELU of config 5). lut is read only for OUT == KT_OUT_I8 and may be null.
-template <int WM, int WTM, int WTN, int WAVES, int NSLOT, int OUT, bool SMALL, int WN = 4>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
-    const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
-    void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
-    const int8_t* __restrict__ lut) {
-    typedef W12Tile<WM, WTM, WTN, NSLOT, WN> C;
-    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
-    constexpr int SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // the int8 output tile reuses the A ring after the loop
-    __shared__ __attribute__((aligned(16))) int8_t smem[C::RING > SO ? C::RING : SO];
-    __shared__ int sRow[BM];
-    __shared__ int8_t sLut[256];
-
+// The dense W12 GEMM's epilogue: recombine the two planes with the row-sum term (sRow), requantize per output channel
+// and store the CTA tile at (m0, n0). OUT_I8 stages the int8 tile in `smem` (BM x BN bytes, free once the mainloop
+// is done) and applies `sLut` when `lut` is non-null.
+template <class C, int OUT, bool SMALL>
+__device__ __forceinline__ void w12_gemm_epilogue(const v16i (&acc0)[C::WTM][C::WTN],
+                                                  const v16i (&acc1)[C::WTM][C::WTN], const int* sRow, int8_t* smem,
+                                                  const int8_t* sLut, void* __restrict__ y, int M, int N, int m0,
+                                                  int n0, const int32_t* __restrict__ mant,
+                                                  const int32_t* __restrict__ shift, const int8_t* __restrict__ lut) {
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, WTM = C::WTM, WTN = C::WTN, WN = C::WN;
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
     const int wave = (tid >> 6) % WN, rw0 = ((tid >> 6) / WN) * 32 * WTM;
-    int m0, n0;
-    tile_coords(M, N, BM, BN, m0, n0);
-    const int KB = kp / 32;
-    if (OUT == KT_OUT_I8 && SMALL)
-        for (int i = tid; i < 256; i += NT) sLut[i] = lut ? lut[i < 255 ? i : 254] : 0;
-
-    // A: the CTA's rows; rows past the matrix read as zero (their offsets are past the descriptor)
-    const uint32_t rows_a = (uint32_t)(M - m0 < BM ? M - m0 : BM);
-    const __amdgpu_buffer_rsrc_t rA = make_rsrc(x + (size_t)m0 * kp, rows_a * (uint32_t)kp);
-    uint32_t oa[AL];
-#pragma unroll
-    for (int i = 0; i < AL; i++) {
-        const int idx = tid + NT * i;
-        oa[i] = idx < AC ? (uint32_t)(idx >> 2) * (uint32_t)kp + 16 * (idx & 3) : KT_OOB;
-    }
-    // B: the CTA's column blocks (fragment-tiled); blocks past the matrix read as zero
-    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
-    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
-    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
-    uint32_t ob[WTN], on[WTN];
-#pragma unroll
-    for (int j = 0; j < WTN; j++) {
-        ob[j] = (uint32_t)((wave * WTN + j) * KB) * 1024 + 16 * lane;
-        on[j] = (uint32_t)((wave * WTN + j) * KB) * 512 + 8 * lane;
-    }
-
-    v16i acc0[WTM][WTN], acc1[WTM][WTN];
-    int rsum[AL];
-    w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
-    w12_row_sums<C>(rsum, sRow);
-
     const bool full = m0 + BM <= M && n0 + BN <= N;
     if constexpr (OUT == KT_OUT_I8 && SMALL) {
         // requantize into an int8 tile in LDS (the A ring is no longer read), then store it with 16-byte writes
@@ -415,6 +380,108 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WA
                 }
             }
     }
+}
+
+// An optional int8 -> int8 table (`lut`, 255 entries indexed by q + 127) is applied after the int8 requant: the
+// activation-code epilogue (GELU of config 5). lut is read only for OUT == KT_OUT_I8 and may be null.
+template <int WM, int WTM, int WTN, int WAVES, int NSLOT, int OUT, bool SMALL, int WN = 4>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void w12_gemm_kernel(
+    const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
+    void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+    const int8_t* __restrict__ lut) {
+    typedef W12Tile<WM, WTM, WTN, NSLOT, WN> C;
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
+    constexpr int SO = OUT == KT_OUT_I8 ? BM * BN : 0;  // the int8 output tile reuses the A ring after the loop
+    __shared__ __attribute__((aligned(16))) int8_t smem[C::RING > SO ? C::RING : SO];
+    __shared__ int sRow[BM];
+    __shared__ int8_t sLut[256];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = (tid >> 6) % WN;
+    int m0, n0;
+    tile_coords(M, N, BM, BN, m0, n0);
+    const int KB = kp / 32;
+    if (OUT == KT_OUT_I8 && SMALL)
+        for (int i = tid; i < 256; i += NT) sLut[i] = lut ? lut[i < 255 ? i : 254] : 0;
+
+    // A: the CTA's rows; rows past the matrix read as zero (their offsets are past the descriptor)
+    const uint32_t rows_a = (uint32_t)(M - m0 < BM ? M - m0 : BM);
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(x + (size_t)m0 * kp, rows_a * (uint32_t)kp);
+    uint32_t oa[AL];
+#pragma unroll
+    for (int i = 0; i < AL; i++) {
+        const int idx = tid + NT * i;
+        oa[i] = idx < AC ? (uint32_t)(idx >> 2) * (uint32_t)kp + 16 * (idx & 3) : KT_OOB;
+    }
+    // B: the CTA's column blocks (fragment-tiled); blocks past the matrix read as zero
+    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    uint32_t ob[WTN], on[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; j++) {
+        ob[j] = (uint32_t)((wave * WTN + j) * KB) * 1024 + 16 * lane;
+        on[j] = (uint32_t)((wave * WTN + j) * KB) * 512 + 8 * lane;
+    }
+
+    v16i acc0[WTM][WTN], acc1[WTM][WTN];
+    int rsum[AL];
+    w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
+    w12_row_sums<C>(rsum, sRow);
+
+    w12_gemm_epilogue<C, OUT, SMALL>(acc0, acc1, sRow, smem, sLut, y, M, N, m0, n0, mant, shift, lut);
+}
+
+// Dense W12 GEMM on 256 x 128 CTA tiles fed by LDS DMA (w12_mainloop_dma): one CTA of 8 waves per CU, every operand
+// byte moved once per CTA; the epilogue is the 128 x 128 kernel's. Dynamic LDS: KT_DMA_NS stages, which the int8
+// output tile reuses.
+#ifndef KT_W12_DMA
+#define KT_W12_DMA 1
+#endif
+#ifndef KT_DMA_NS
+#define KT_DMA_NS 4
+#endif
+template <int OUT, bool SMALL>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_gemm_dma_kernel(
+    const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
+    void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+    const int8_t* __restrict__ lut) {
+    typedef W12Tile<2, 4, 1, 2, 4> C;  // 256 x 128, 8 waves (the tile's NSLOT is not used by this mainloop)
+    static_assert(C::BM == 256 && C::BN == 128 && C::NT == 512, "the DMA mainloop's tile");
+    static_assert(KT_DMA_NS * KT_DMA_STAGE >= C::BM * C::BN, "the int8 output tile fits the ring");
+    extern __shared__ __attribute__((aligned(16))) int8_t ring[];
+    __shared__ int sRow[C::BM];
+    __shared__ int8_t sLut[256];
+    const int tid = threadIdx.x;
+    int m0, n0;
+    tile_coords(M, N, C::BM, C::BN, m0, n0);
+    const int KB = kp / 32;
+    if (OUT == KT_OUT_I8 && SMALL)
+        for (int i = tid; i < 256; i += C::NT) sLut[i] = lut ? lut[i < 255 ? i : 254] : 0;
+    // rows and column blocks past the matrix read as zero (their offsets are past the descriptors)
+    const uint32_t rows_a = (uint32_t)(M - m0 < C::BM ? M - m0 : C::BM);
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(x + (size_t)m0 * kp, rows_a * (uint32_t)kp);
+    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < 4 ? (N - n0 + 31) / 32 : 4;
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    v16i acc0[4][1], acc1[4][1];
+    w12_mainloop_dma<KT_DMA_NS>(rA, rL, rN, kp, ring, acc0, acc1, sRow);
+    w12_gemm_epilogue<C, OUT, SMALL>(acc0, acc1, sRow, ring, sLut, y, M, N, m0, n0, mant, shift, lut);
+}
+
+// Whether the device gives one CTA the DMA kernel's LDS (static arrays + the ring); queried once per process.
+static bool dma_lds_ok() {
+    static int ok = -1;
+    if (ok < 0) {
+        hipFuncAttributes fa;
+        int dev = 0, mx = 0;
+        ok = hipGetDevice(&dev) == hipSuccess &&
+             hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+             hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&w12_gemm_dma_kernel<KT_OUT_I8, true>)) ==
+                 hipSuccess &&
+             fa.sharedSizeBytes + (size_t)KT_DMA_NS * KT_DMA_STAGE <= (size_t)mx;
+    }
+    return ok == 1;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -819,6 +886,20 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
         }
         return hipGetLastError();
     }
+#if KT_W12_DMA
+    // enough 256 x 128 tiles to give every CU one: the DMA-fed kernel
+    const int64_t tiles_d = ceil_div(N, 128) * ceil_div(M, 256);
+    if (tiles_d >= 256 && dma_lds_ok()) {
+        const size_t lds = (size_t)KT_DMA_NS * KT_DMA_STAGE;
+        if (small)
+            w12_gemm_dma_kernel<OUT, true><<<dim3((unsigned)tiles_d), dim3(512), lds, s>>>(x, lo, nib, y, M, N, kp,
+                                                                                       mant, shift, lut);
+        else
+            w12_gemm_dma_kernel<OUT, false><<<dim3((unsigned)tiles_d), dim3(512), lds, s>>>(x, lo, nib, y, M, N, kp,
+                                                                                        mant, shift, nullptr);
+        return hipGetLastError();
+    }
+#endif
     dim3 grid((unsigned)tiles4), block(256 * WM);
     if (small)
         w12_gemm_kernel<WM, WTM, WTN, WV, NS, OUT, true><<<grid, block, 0, s>>>(x, lo, nib, y, M, N, kp, mant, shift, lut);

@@ -426,6 +426,118 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
     } while (kt < nk);
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// W12 mainloop for a 256 x 128 CTA tile whose operands all arrive by LDS DMA (buffer_load ... lds: each lane's bytes
+// land at M0 + size * lane without passing through VGPRs). 8 waves: wave w computes rows 128 (w / 4) .. + 127 against
+// column block w % 4 (4 x 1 tiles of 32x32, two planes). A stage holds one k-tile (BK = 64) of every operand:
+//   A    [0, 16384):     256 rows x 64 bytes, chunk c of row r at r * 64 + 16 (c ^ swz(r)) (the register path's layout)
+//   lo   [16384, 24576): the 4 column blocks' two 1 KB k32 fragments, block (cb, ks) at 1024 (2 cb + ks)
+//   nib  [24576, 28672): the matching 512-byte nib fragments at 512 (2 cb + ks)
+// Each wave moves 5 pieces per k-tile: A rows 32w .. 32w + 31 (two 1 KB DMAs whose lanes gather the swizzled
+// chunks), fragment (w / 2, w % 2) of lo (one 16-byte DMA) and of nib (two 4-byte DMAs). Operands are re-read by
+// every wave that uses them from LDS, so each byte crosses the L2 -> CU path once per CTA, against twice for A and
+// four times for B with two 128 x 128 CTAs. The ring has NS stages, NS - 1 k-tiles in flight beyond the one being
+// multiplied; a wave waits for its own DMAs of a tile (vmcnt, in order) and a barrier publishes everyone's. Tiles
+// past the end are re-reads of the last one into stages that are never consumed. The row sums of x come from the
+// A fragment of row tile w % 4, read once more by each wave. Ends with every DMA landed, sRow[256] written and a barrier: the ring is free.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int KT_DMA_STAGE = 28672, KT_DMA_LO = 16384, KT_DMA_NIB = 24576;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int8_t* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, int8_t* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 4, voff, soff, 0, 0);
+}
+
+template <int NS>
+__device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA, const __amdgpu_buffer_rsrc_t rL,
+                                                 const __amdgpu_buffer_rsrc_t rN, int kp, int8_t* ring,
+                                                 v16i (&acc0)[4][1], v16i (&acc1)[4][1], int* sRow) {
+    static_assert(NS >= 2 && 5 * (NS - 2) <= 63, "vmcnt holds the DMAs of NS - 2 later tiles");
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = w & 3, rw0 = 128 * (w >> 2);
+    const int nk = kp / 64, KB = kp / 32;
+
+    // DMA sources of this lane. A: instruction j covers LDS rows 16 j .. 16 j + 15, lane l lands at row
+    // 16 j + l / 4, chunk position l % 4, which holds chunk (l % 4) ^ swz(row) = (l % 4) ^ ((l / 16) % 4).
+    const uint32_t va = (uint32_t)(32 * w + (lane >> 2)) * (uint32_t)kp + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+    const int cbw = w >> 1, ksw = w & 1;  // the fragment this wave moves
+    const uint32_t vl = (uint32_t)(cbw * KB) * 1024u + 16 * lane, vn = (uint32_t)(cbw * KB) * 512u + 4 * lane;
+
+    // 5 DMAs per wave and k-tile on every wave, so one vmcnt target serves all (a wave-dependent count would put
+    // branches in the loop, which keep the scheduler from moving MFMAs across the barrier)
+    auto issue = [&](int st, int kt) {
+        const uint32_t kl = (uint32_t)(kt < nk ? kt : nk - 1);
+        int8_t* s = ring + st * KT_DMA_STAGE;
+        dma16(rA, s + 2048 * w, va, kl * 64);
+        dma16(rA, s + 2048 * w + 1024, va + 16u * (uint32_t)kp, kl * 64);
+        dma16(rL, s + KT_DMA_LO + 1024 * w, vl, (2 * kl + ksw) * 1024u);
+        dma4(rN, s + KT_DMA_NIB + 512 * w, vn, (2 * kl + ksw) * 512u);
+        dma4(rN, s + KT_DMA_NIB + 512 * w + 256, vn + 256, (2 * kl + ksw) * 512u);
+    };
+    // the wave's DMAs of a tile have landed once at most those of the NS - 2 later tiles are outstanding
+    auto wait_tile = [&]() {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(5 * (NS - 2)) : "memory");
+    };
+
+    struct Frag {  // one k32 half of a k-tile: the wave's 4 A fragments, its row-sum fragment and its B fragment
+        v4i a[4], ar, b0;
+        v2i bn;
+    };
+    auto load = [&](const int8_t* s, int ks, Frag& f) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) f.a[i] = lds_read16(s, lds_off<4>(rw0 + 32 * i + (lane & 31), 2 * ks + half));
+        // row tile wn once more: a wave-uniform select among f.a would compile to branches
+        f.ar = lds_read16(s, lds_off<4>(rw0 + 32 * wn + (lane & 31), 2 * ks + half));
+        f.b0 = lds_read16(s + KT_DMA_LO + 1024 * (2 * wn + ks), 16 * lane);
+        f.bn = *reinterpret_cast<const v2i*>(s + KT_DMA_NIB + 512 * (2 * wn + ks) + 8 * lane);
+    };
+    int rsum = 0;
+    auto mma = [&](const Frag& f) {
+        const v4i b1 = unpack_hi(f.bn);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc0[i][0] = mfma32(f.a[i], f.b0, acc0[i][0]);
+            acc1[i][0] = mfma32(f.a[i], b1, acc1[i][0]);
+        }
+        rsum += sum4(f.ar);
+    };
+
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc0[i][0] = acc1[i][0] = v16i{};
+#pragma unroll
+    for (int t = 0; t < NS - 1; t++) issue(t, t);
+    wait_tile();
+    issue(NS - 1, NS - 1);
+    Frag f0, f1;
+    load(ring, 0, f0);
+    load(ring, 1, f1);
+    // Ping-pong: the first half of tile kt's MFMAs covers the barrier that publishes tile kt + 1, the second half
+    // covers the LDS reads of tile kt + 1's first half, and those of its second half run under the next step's
+    // first MFMAs. Reads in the last step fetch a stage nobody consumes.
+    for (int kt = 0; kt < nk; kt++) {
+        mma(f0);
+        // tile kt + 1 has landed once at most the DMAs of tiles kt + 2 .. kt + NS - 1 are outstanding; every wave's
+        // reads of tile kt are done (lgkmcnt), so after the barrier its stage takes tile kt + NS
+        wait_tile();
+        issue(kt % NS, kt + NS);
+        const int8_t* sn = ring + ((kt + 1) % NS) * KT_DMA_STAGE;
+        load(sn, 0, f0);
+        __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs they hide under
+        mma(f1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(sn, 1, f1);
+    }
+    // the re-reads past the end still target the ring
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    rsum += __shfl_xor(rsum, 32);
+    if (lane < 32) sRow[rw0 + 32 * wn + lane] = rsum;
+    __syncthreads();
+}
+
 // The CTA's row sums of x into sRow[BM] (the 4 threads of a row are consecutive lanes). Ends with a barrier.
 template <class C>
 __device__ __forceinline__ void w12_row_sums(const int (&rsum)[C::AL], int* sRow) {
