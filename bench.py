@@ -648,7 +648,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(tops / INT8_PEAK_TOPS, 4),
             "traffic": traffic,
-            "kernel": "w12_gemm_kernel (logical ops 2*M*N*K per launch; the 2 digit planes execute twice that)",
+            "kernel": "w12_gemm_dma_kernel (logical ops 2*M*N*K per launch; the 2 digit planes execute twice that)",
         },
         "sweep": sweep,
         "configs": extra,
