@@ -179,6 +179,74 @@ def test_grouped_linear_ragged_gather(torch_dev):
         at += c
 
 
+@pytest.mark.parametrize("k,gathered", [(100, True), (320, False)])
+def test_grouped_dma_tiles(torch_dev, k, gathered):
+    """Enough rows for the DMA-fed grouped kernel (256-row tiles, one CTA per CU), int8 epilogue: groups of 0, 1, 64,
+    65, 128, 129, 256, 257, 300, 520 and 700 rows (every tail class: the 64- and 128-row register tiles and the DMA
+    tile), n = 4000 (a partial last column tile), k of two and five 64-deep k-tiles; rows gathered through a list with
+    repeats, or read in place from offset ranges."""
+    import tritify_amd as TA
+    from tritify_amd import workloads as W
+
+    torch = torch_dev
+    counts = np.array([0, 1, 64, 65, 128, 129, 256, 257, 300, 520, 700], dtype=np.int32)
+    G, n = len(counts), 4000
+    P = int(counts.sum())
+    kp = (k + 63) // 64 * 64
+    xrows = 900 if gathered else P
+    say(f"case: grouped dma tiles counts={counts.tolist()} n={n} k={k} gathered={gathered}")
+    rng = np.random.default_rng(k)
+    x = rng.integers(-127, 128, size=(xrows, k), dtype=np.int8)
+    xp = np.zeros((xrows, kp), np.int8)
+    xp[:, :k] = x
+    off_h = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    lst = np.full((G, 1024), -1, np.int32)
+    for g in range(G):
+        lst[g, : counts[g]] = rng.integers(0, xrows, size=counts[g]) if gathered else np.arange(off_h[g], off_h[g + 1])
+    lo_b, _ = TA.w12_bytes(n, k)
+    lo = torch.zeros(G * lo_b, dtype=torch.int8, device="cuda")
+    nib = torch.zeros(G * lo_b // 2, dtype=torch.uint8, device="cuda")
+    ws, ms, ss = [], [], []
+    for g in range(G):
+        w = W.gen_w12(1300 + g, n * k)
+        m_, s_ = W.channel_scales(w, n, k, 40)
+        TA.w12_upload(w, n, k, lo[g * lo_b:(g + 1) * lo_b], nib[g * lo_b // 2:(g + 1) * lo_b // 2])
+        ws.append(w), ms.append(m_), ss.append(s_)
+    y = torch.full((P * n,), 99, dtype=torch.int8, device="cuda")
+    off = torch.zeros(G + 1, dtype=torch.int32, device="cuda")
+    TA.w12_grouped_linear(torch.from_numpy(xp).cuda(), xrows, torch.from_numpy(lst).cuda() if gathered else None,
+                          1024, torch.from_numpy(counts).cuda(), G, P, lo, nib, n, k,
+                          torch.from_numpy(np.concatenate(ms)).cuda(), torch.from_numpy(np.concatenate(ss)).cuda(),
+                          TA.EPI_I8, y, n, off_dev=off)
+    torch.cuda.synchronize()
+    yh = y.cpu().numpy().reshape(P, n)
+    assert np.array_equal(off.cpu().numpy(), off_h)
+    for g in range(G):
+        c = int(counts[g])
+        if c == 0:
+            continue
+        rows = x[lst[g, :c]]
+        _, y8 = O.gemm_i8w16(rows, ws[g].astype(np.int16), c, n, k, ms[g], ss[g])
+        got = yh[off_h[g]:off_h[g + 1]]
+        assert np.array_equal(got, y8.reshape(c, n)), f"group {g} ({c} rows) differs"
+
+
+def test_moe_layer_on_dma_tiles(torch_dev):
+    """A layer whose gate/up product takes the DMA-fed grouped kernel (T = 1024 tokens x 4 rows, 2F = 2048) with the
+    SwiGLU epilogue, routed so the experts get 1024, 1024, 257, 256, 129, 128, 124, 65, 64, 1 and 0 rows (every
+    tail class); every intermediate against the oracle."""
+    T, H, F, E, K = 1024, 128, 1024, 16, 3
+    want = [1024, 1024, 257, 256, 129, 128, 65, 64, 1, 0, 124, 0, 0, 0, 0, 0]
+    assert sum(want) == T * K
+    seq = np.repeat(np.arange(E), want)  # expert ids by position; token t takes positions t, t + T, t + 2T
+    logits = np.full((T, E), 0, np.int64) - 1000 - np.arange(E)[None, :]
+    for t in range(T):
+        for r, e in enumerate(seq[[t, t + T, t + 2 * T]]):
+            logits[t, e] = 3000 - 1000 * r
+    ref = run_and_compare(torch_dev, T, H, F, E, K, logits=logits.astype(np.int32).ravel(), token_order=False)
+    assert ref["count"][:E].tolist() == want
+
+
 def test_moe_full_config4(torch_dev):
     """BASELINE config 4 at full size (4096 tokens, H 4096, 128 experts + shared, F 1408, top-8) against the
     fixture hashes of the oracle's expert-major evaluation."""

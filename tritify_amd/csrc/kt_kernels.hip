@@ -438,9 +438,6 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WA
 #ifndef KT_W12_DMA
 #define KT_W12_DMA 1
 #endif
-#ifndef KT_DMA_NS
-#define KT_DMA_NS 4
-#endif
 template <int OUT, bool SMALL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_gemm_dma_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
@@ -464,8 +461,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < 4 ? (N - n0 + 31) / 32 : 4;
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
     const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const uint32_t va0 = (uint32_t)dma_a_row(w, lane, 0) * (uint32_t)kp + dma_a_chunk(lane);
     v16i acc0[4][1], acc1[4][1];
-    w12_mainloop_dma<KT_DMA_NS>(rA, rL, rN, kp, ring, acc0, acc1, sRow);
+    w12_mainloop_dma<KT_DMA_NS>(rA, rL, rN, va0, va0 + 16u * (uint32_t)kp, kp, ring, acc0, acc1, sRow);
     w12_gemm_epilogue<C, OUT, SMALL>(acc0, acc1, sRow, ring, sLut, y, M, N, m0, n0, mant, shift, lut);
 }
 

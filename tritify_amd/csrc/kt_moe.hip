@@ -108,43 +108,17 @@ __global__ __launch_bounds__(256) void moe_bucket_kernel(const int32_t* __restri
 typedef W12Tile<1, 4, 1, 4> GTile;
 typedef W12Tile<1, 2, 1, 4> GTileH;
 
-// One output tile of the grouped GEMM: rows row0 .. row0 + rows - 1 of group g, columns n0 .. n0 + BN - 1.
+// The epilogue of one grouped output tile (rows row0 .. row0 + rows - 1 of group g, columns n0 .. n0 + BN - 1): the
+// int8 requant (EPI_I8) or the SwiGLU of the tile's gate/up block pairs (EPI_SWIGLU), staged through `smem`
+// (BM x BN bytes, free once the mainloop is done).
 template <class C, int EPI>
-__device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, uint32_t x_bytes,
-                                             const int32_t* __restrict__ list, int list_stride, int g, int row0,
-                                             int rows, int n0, const int* sOff, const int8_t* __restrict__ wlo,
-                                             const uint8_t* __restrict__ wnib, size_t glo, int N, int kp,
-                                             const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
-                                             const int16_t* sSilu, int h_shift, int8_t* __restrict__ y, int ystride,
-                                             int8_t* smem, int* sRow) {
-    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
-    static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int KB = kp / 32;
-    uint32_t oa[AL];
-#pragma unroll
-    for (int i = 0; i < AL; i++) {
-        const int idx = tid + NT * i, r = idx >> 2;
-        if (idx < AC && r < rows) {
-            const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
-            oa[i] = (uint32_t)xr * (uint32_t)kp + 16 * (idx & 3);
-        } else {
-            oa[i] = x_bytes;  // out of range whatever the k offset: reads zero
-        }
-    }
-    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
-    const int8_t* gl = wlo + (size_t)g * glo;
-    const uint8_t* gn = wnib + (size_t)g * (glo / 2);
-    const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
-    const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
-    const int wn = wave % C::WN;
-    uint32_t ob[1] = {(uint32_t)(wn * KB) * 1024 + 16 * lane}, on[1] = {(uint32_t)(wn * KB) * 512 + 8 * lane};
-
-    v16i acc0[C::WTM][1], acc1[C::WTM][1];
-    int rsum[AL];
-    w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
-    w12_row_sums<C>(rsum, sRow);
-
+__device__ __forceinline__ void grouped_epilogue(const v16i (&acc0)[C::WTM][1], const v16i (&acc1)[C::WTM][1],
+                                                 const int* sRow, int g, int row0, int rows, int n0, const int* sOff,
+                                                 int N, const int32_t* __restrict__ mant,
+                                                 const int32_t* __restrict__ shift, const int16_t* sSilu,
+                                                 int h_shift, int8_t* __restrict__ y, int ystride, int8_t* smem) {
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN;
+    const int tid = threadIdx.x;
     const int32_t* gm = mant + (size_t)g * N;
     const int32_t* gs = shift + (size_t)g * N;
     int8_t* yg = y + (size_t)(sOff[g] + row0) * ystride;
@@ -190,6 +164,147 @@ __device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, ui
             }
             *reinterpret_cast<v4i*>(yg + (size_t)r * ystride + n0 / 2 + 16 * q) = out;
         }
+    }
+}
+
+// One output tile of the grouped GEMM: rows row0 .. row0 + rows - 1 of group g, columns n0 .. n0 + BN - 1.
+template <class C, int EPI>
+__device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, uint32_t x_bytes,
+                                             const int32_t* __restrict__ list, int list_stride, int g, int row0,
+                                             int rows, int n0, const int* sOff, const int8_t* __restrict__ wlo,
+                                             const uint8_t* __restrict__ wnib, size_t glo, int N, int kp,
+                                             const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+                                             const int16_t* sSilu, int h_shift, int8_t* __restrict__ y, int ystride,
+                                             int8_t* smem, int* sRow) {
+    constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
+    static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int KB = kp / 32;
+    uint32_t oa[AL];
+#pragma unroll
+    for (int i = 0; i < AL; i++) {
+        const int idx = tid + NT * i, r = idx >> 2;
+        if (idx < AC && r < rows) {
+            const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
+            oa[i] = (uint32_t)xr * (uint32_t)kp + 16 * (idx & 3);
+        } else {
+            oa[i] = x_bytes;  // out of range whatever the k offset: reads zero
+        }
+    }
+    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
+    const int8_t* gl = wlo + (size_t)g * glo;
+    const uint8_t* gn = wnib + (size_t)g * (glo / 2);
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    const int wn = wave % C::WN;
+    uint32_t ob[1] = {(uint32_t)(wn * KB) * 1024 + 16 * lane}, on[1] = {(uint32_t)(wn * KB) * 512 + 8 * lane};
+
+    v16i acc0[C::WTM][1], acc1[C::WTM][1];
+    int rsum[AL];
+    w12_mainloop<C>(rA, oa, rL, rN, ob, on, kp / C::BK, smem, acc0, acc1, rsum);
+    w12_row_sums<C>(rsum, sRow);
+    grouped_epilogue<C, EPI>(acc0, acc1, sRow, g, row0, rows, n0, sOff, N, mant, shift, sSilu, h_shift, y, ystride,
+                             smem);
+}
+
+// The 256 x 128 tile of the DMA-fed grouped kernel (w12_mainloop_dma, 8 waves): the lanes' A pieces are gathered
+// rows of group g, rows at or past `rows` read zero.
+typedef W12Tile<2, 4, 1, 2, 4> GTileD;
+template <int EPI>
+__device__ __forceinline__ void grouped_tile_dma(const __amdgpu_buffer_rsrc_t rA, uint32_t x_bytes,
+                                                 const int32_t* __restrict__ list, int list_stride, int g, int row0,
+                                                 int rows, int n0, const int* sOff, const int8_t* __restrict__ wlo,
+                                                 const uint8_t* __restrict__ wnib, size_t glo, int N, int kp,
+                                                 const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+                                                 const int16_t* sSilu, int h_shift, int8_t* __restrict__ y,
+                                                 int ystride, int8_t* ring, int* sRow) {
+    constexpr int BN = GTileD::BN;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KB = kp / 32;
+    uint32_t va[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int r = dma_a_row(w, lane, j);
+        if (r < rows) {
+            const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
+            va[j] = (uint32_t)xr * (uint32_t)kp + dma_a_chunk(lane);
+        } else {
+            va[j] = x_bytes;  // out of range whatever the k offset: reads zero
+        }
+    }
+    const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
+    const int8_t* gl = wlo + (size_t)g * glo;
+    const uint8_t* gn = wnib + (size_t)g * (glo / 2);
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    v16i acc0[4][1], acc1[4][1];
+    w12_mainloop_dma<KT_DMA_NS>(rA, rL, rN, va[0], va[1], kp, ring, acc0, acc1, sRow);
+    grouped_epilogue<GTileD, EPI>(acc0, acc1, sRow, g, row0, rows, n0, sOff, N, mant, shift, sSilu, h_shift, y,
+                                  ystride, ring);
+}
+
+// The ragged grouped W12 GEMM on 256-row tiles fed by LDS DMA, for products with enough rows to give every CU a
+// tile: one CTA of 8 waves per CU, each group cut into 256-row tiles whose weights cross the L2 -> CU path once per
+// tile (against once per 128 rows for w12_grouped_kernel). A group's last row tile runs on the DMA tile when it
+// holds more than 128 rows, else on a 128- or 64-row tile of the register mainloop (8 waves, 2 along M) in the
+// same pass. Arguments, tile order and results are w12_grouped_kernel's (below).
+template <int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_grouped_dma_kernel(
+    const int8_t* __restrict__ x, uint32_t x_bytes, const int32_t* __restrict__ list, int list_stride,
+    const int32_t* __restrict__ count, int groups, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
+    size_t glo, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
+    const int16_t* __restrict__ silu, int h_shift, int8_t* __restrict__ y, int ystride,
+    int32_t* __restrict__ off_out, int rows_one) {
+    typedef W12Tile<2, 2, 1, 4, 4> GT128;
+    typedef W12Tile<2, 1, 1, 4, 4> GT64;
+    static_assert(GT128::NT == 512 && GT64::NT == 512 && GT128::BN == 128 && GT64::BN == 128, "one tile space");
+    static_assert(GT128::RING <= KT_DMA_NS * KT_DMA_STAGE, "the register tiles' A rings fit the DMA ring");
+    constexpr int NT = 512, BM = 256, BN = 128;
+    extern __shared__ __attribute__((aligned(16))) int8_t ring[];
+    __shared__ int sRow[BM];
+    __shared__ int sRpre[KT_MAX_GROUPS + 1], sOff[KT_MAX_GROUPS + 1];
+    __shared__ int scr[16];
+    __shared__ int16_t sSilu[256];
+
+    const int tid = threadIdx.x;
+    int carry_r = 0, carry_o = 0;
+    for (int g0 = 0; g0 < groups; g0 += NT) {
+        const int g = g0 + tid, c = g < groups ? (count ? count[g] : rows_one) : 0;
+        int er, eo, tr, to;
+        block_scan2<NT>((c + BM - 1) / BM, c, er, eo, tr, to, scr);
+        if (g < groups) sRpre[g] = carry_r + er, sOff[g] = carry_o + eo;
+        carry_r += tr, carry_o += to;
+    }
+    if (tid == 0) sRpre[groups] = carry_r, sOff[groups] = carry_o;
+    if (EPI == KT_EPI_SWIGLU && tid < 256) sSilu[tid] = silu[tid < 255 ? tid : 254];
+    __syncthreads();
+    if (off_out && blockIdx.x == 0)
+        for (int g = tid; g <= groups; g += NT) off_out[g] = sOff[g];
+
+    const int tiles_n = (N + BN - 1) / BN, total = sRpre[groups] * tiles_n;
+    const int nx = gridDim.x >> 3, xcd = blockIdx.x & 7, per = (total + 7) >> 3;
+    const int t_end = min(total, (xcd + 1) * per);
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(x, x_bytes);
+    for (int t = xcd * per + (blockIdx.x >> 3); t < t_end; t += nx) {
+        const int rt = t / tiles_n, n0 = (t - rt * tiles_n) * BN;
+        int lo = 0, hi = groups - 1;  // the last group whose first row tile is <= rt (it is not empty)
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (sRpre[mid] <= rt) lo = mid;
+            else hi = mid - 1;
+        }
+        const int g = lo, row0 = (rt - sRpre[g]) * BM, cnt = sOff[g + 1] - sOff[g];
+        const int rows = cnt - row0 < BM ? cnt - row0 : BM;
+        if (rows > GT128::BM)  // uniform
+            grouped_tile_dma<EPI>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N, kp, mant,
+                                  shift, sSilu, h_shift, y, ystride, ring, sRow);
+        else if (rows > GT64::BM)
+            grouped_tile<GT128, EPI>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N, kp,
+                                     mant, shift, sSilu, h_shift, y, ystride, ring, sRow);
+        else
+            grouped_tile<GT64, EPI>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N, kp,
+                                    mant, shift, sSilu, h_shift, y, ystride, ring, sRow);
+        __syncthreads();  // the next tile's prologue rewrites the ring
     }
 }
 
@@ -314,6 +429,21 @@ hipError_t launch_moe_bucket(const int32_t* sel, int T, int E, int top_k, int32_
     return hipGetLastError();
 }
 
+// Whether the device gives one CTA the DMA-fed grouped kernel's LDS; queried once per process.
+static bool grouped_dma_lds_ok() {
+    static int ok = -1;
+    if (ok < 0) {
+        hipFuncAttributes fa;
+        int dev = 0, mx = 0;
+        ok = hipGetDevice(&dev) == hipSuccess &&
+             hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+             hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&w12_grouped_dma_kernel<KT_EPI_SWIGLU>)) ==
+                 hipSuccess &&
+             fa.sharedSizeBytes + (size_t)KT_DMA_NS * KT_DMA_STAGE <= (size_t)mx;
+    }
+    return ok == 1;
+}
+
 hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* list, int list_stride,
                               const int32_t* count, int groups, int64_t max_rows, const int8_t* wlo,
                               const uint8_t* wnib, size_t glo, int N, int kp, const int32_t* mant,
@@ -330,6 +460,21 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
     if (ub * GTile::BN > INT32_MAX) return hipErrorInvalidValue;
     const int64_t grid = ub < 512 ? (ub + 7) / 8 * 8 : 512;  // two CTAs per CU, a multiple of 8 (XCDs)
     if (epi != KT_EPI_I8 && epi != KT_EPI_SWIGLU) return hipErrorInvalidValue;
+    // enough 256-row tiles (at full groups) to give every CU one: the DMA-fed kernel, one CTA per CU
+    if (max_rows / 256 * tiles_n >= 256 && grouped_dma_lds_ok()) {
+        const size_t lds = (size_t)KT_DMA_NS * KT_DMA_STAGE;
+        const int64_t ub2 = ((max_rows + 255) / 256 + groups) * tiles_n;
+        const unsigned grid2 = (unsigned)(ub2 < 256 ? (ub2 + 7) / 8 * 8 : 256);
+        if (epi == KT_EPI_I8)
+            w12_grouped_dma_kernel<KT_EPI_I8><<<dim3(grid2), dim3(512), lds, s>>>(
+                x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu,
+                h_shift, y, ystride, off_out, (int)max_rows);
+        else
+            w12_grouped_dma_kernel<KT_EPI_SWIGLU><<<dim3(grid2), dim3(512), lds, s>>>(
+                x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu,
+                h_shift, y, ystride, off_out, (int)max_rows);
+        return hipGetLastError();
+    }
 #define KT_GROUPED(E, T, off)                                                                                        \
     w12_grouped_kernel<E, T><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, (uint32_t)x_bytes, list, list_stride,   \
                                                                        count, groups, wlo, wnib, glo, N, kp, mant, \

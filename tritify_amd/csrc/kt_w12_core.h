@@ -442,6 +442,9 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
 // A fragment of row tile w % 4, read once more by each wave. Ends with every DMA landed, sRow[256] written and a barrier: the ring is free.
 // ------------------------------------------------------------------------------------------------------------------
 constexpr int KT_DMA_STAGE = 28672, KT_DMA_LO = 16384, KT_DMA_NIB = 24576;
+#ifndef KT_DMA_NS
+#define KT_DMA_NS 4  // ring stages of the DMA-fed kernels
+#endif
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int8_t* lds, uint32_t voff, uint32_t soff) {
@@ -451,19 +454,24 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, int8_t* lds, uint
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 4, voff, soff, 0, 0);
 }
 
+// The A rows a lane moves: tile rows 32w + l / 4 and 32w + 16 + l / 4 (DMA instructions 2w and 2w + 1 cover LDS rows
+// 16 j .. 16 j + 15; lane l lands at row 16 j + l / 4, chunk position l % 4). Returns the chunk of x it must fetch,
+// (l % 4) ^ swz(row) = (l % 4) ^ ((l / 16) % 4), as a byte offset within a k-tile row.
+__device__ __forceinline__ int dma_a_row(int w, int lane, int j) { return 32 * w + 16 * j + (lane >> 2); }
+__device__ __forceinline__ uint32_t dma_a_chunk(int lane) { return 16u * ((lane & 3) ^ ((lane >> 4) & 3)); }
+
+// va0 / va1: the byte offsets in rA of this lane's two A pieces at k = 0 (rows dma_a_row(w, lane, 0 / 1), chunk
+// dma_a_chunk(lane)); an offset past the descriptor reads zeros (rows past the tile's rows).
 template <int NS>
 __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA, const __amdgpu_buffer_rsrc_t rL,
-                                                 const __amdgpu_buffer_rsrc_t rN, int kp, int8_t* ring,
-                                                 v16i (&acc0)[4][1], v16i (&acc1)[4][1], int* sRow) {
+                                                 const __amdgpu_buffer_rsrc_t rN, uint32_t va0, uint32_t va1, int kp,
+                                                 int8_t* ring, v16i (&acc0)[4][1], v16i (&acc1)[4][1], int* sRow) {
     static_assert(NS >= 2 && 5 * (NS - 2) <= 63, "vmcnt holds the DMAs of NS - 2 later tiles");
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = w & 3, rw0 = 128 * (w >> 2);
     const int nk = kp / 64, KB = kp / 32;
 
-    // DMA sources of this lane. A: instruction j covers LDS rows 16 j .. 16 j + 15, lane l lands at row
-    // 16 j + l / 4, chunk position l % 4, which holds chunk (l % 4) ^ swz(row) = (l % 4) ^ ((l / 16) % 4).
-    const uint32_t va = (uint32_t)(32 * w + (lane >> 2)) * (uint32_t)kp + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
     const int cbw = w >> 1, ksw = w & 1;  // the fragment this wave moves
     const uint32_t vl = (uint32_t)(cbw * KB) * 1024u + 16 * lane, vn = (uint32_t)(cbw * KB) * 512u + 4 * lane;
 
@@ -472,8 +480,8 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
     auto issue = [&](int st, int kt) {
         const uint32_t kl = (uint32_t)(kt < nk ? kt : nk - 1);
         int8_t* s = ring + st * KT_DMA_STAGE;
-        dma16(rA, s + 2048 * w, va, kl * 64);
-        dma16(rA, s + 2048 * w + 1024, va + 16u * (uint32_t)kp, kl * 64);
+        dma16(rA, s + 2048 * w, va0, kl * 64);
+        dma16(rA, s + 2048 * w + 1024, va1, kl * 64);
         dma16(rL, s + KT_DMA_LO + 1024 * w, vl, (2 * kl + ksw) * 1024u);
         dma4(rN, s + KT_DMA_NIB + 512 * w, vn, (2 * kl + ksw) * 512u);
         dma4(rN, s + KT_DMA_NIB + 512 * w + 256, vn + 256, (2 * kl + ksw) * 512u);
