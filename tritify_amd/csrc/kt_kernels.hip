@@ -821,9 +821,15 @@ static hipError_t plane_gemm_px_pw(const int8_t* xa, const int8_t* wb, int64_t* 
     constexpr int WTM = NG <= 2 ? 2 : 1;
     constexpr int WTN = NG <= 5 ? 2 : 1;
     constexpr int BM = 64 * WTM, BN = 64 * WTN;
-    dim3 grid((unsigned)(ceil_div(N, BN) * ceil_div(M, BM)));
-    plane_gemm_kernel<PX, PW, WTM, WTN><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top,
-                                                                   ql_bias, ql);
+    const int64_t tiles = ceil_div(N, BN) * ceil_div(M, BM);
+    if (WTN == 2 && tiles < 256) {  // too few tiles for the CUs (N = 896 at M = 512): half-width tiles, twice the CTAs
+        dim3 grid((unsigned)(ceil_div(N, BN / 2) * ceil_div(M, BM)));
+        plane_gemm_kernel<PX, PW, WTM, 1><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
+                                                                     drop_top, ql_bias, ql);
+        return hipGetLastError();
+    }
+    plane_gemm_kernel<PX, PW, WTM, WTN><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1,
+                                                                                   accumulate, drop_top, ql_bias, ql);
     return hipGetLastError();
 }
 
