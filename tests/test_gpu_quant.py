@@ -3,8 +3,9 @@ crates/01-engine/kt-core/src/layers.rs:275-328, through the C ABI. Run on a GPU 
 
 Every case compares the output codes, the output Scale and both maxima bit for bit: the reference's own test case
 (kt-core/src/tests.rs:34-46), ragged shapes with and without a bias, extreme input codes (+-(2^31 - 1), -2^31),
-weights needing 1, 3 and 5 digit planes, the xmax == 0 and zero-scale paths, a config-3 projection shape, a chain of
-two layers that passes the scale record on the device, and replays of a captured HIP graph.
+weights needing 1, 3 and 5 digit planes, the xmax == 0 and zero-scale paths, a config-3 projection shape, shapes
+whose GEMM splits k across CTAs, a chain of two layers that passes the scale record on the device, and replays of a
+captured HIP graph.
 """
 import sys
 
@@ -83,6 +84,18 @@ def test_config3_projection_shape(torch_dev):
     x = rng.integers(-(2**28), 2**28, size=rows * inp).astype(np.int32)
     w = rng.integers(-WLEVELS, WLEVELS + 1, size=out * inp).astype(np.int32)
     run(torch_dev, x, rows, inp, (1509949440, 58), w, out, (1657624235, 49))
+
+
+@pytest.mark.parametrize("rows,inp,out,with_bias", [(512, 4864, 896, True), (64, 2048, 1000, False),
+                                                      (65, 1600, 300, True)])
+def test_split_k_shapes(torch_dev, rows, inp, out, with_bias):
+    """Shapes whose digit GEMM splits k across CTAs (few tiles: the config-3 down projection, one row tile, a ragged
+    second row tile), partial sums added with atomics and the bias and maximum taken by each tile's last CTA."""
+    rng = np.random.default_rng(rows + inp + out)
+    x = rng.integers(-(2**28), 2**28, size=rows * inp).astype(np.int32)
+    w = rng.integers(-WLEVELS, WLEVELS + 1, size=out * inp).astype(np.int32)
+    bias = rng.integers(-(2**28), 2**28, size=out).astype(np.int64) if with_bias else None
+    run(torch_dev, x, rows, inp, (1509949440, 58), w, out, (1657624235, 49), bias, (1318646415, 57))
 
 
 def _two_layers(rng, d0=96, d1=80, d2=48):

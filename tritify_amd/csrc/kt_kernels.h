@@ -15,7 +15,11 @@ hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t i
 struct QlState;
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
                              int k0, int k1, int accumulate, int drop_top, hipStream_t s,
-                             const int64_t* ql_bias = nullptr, QlState* ql = nullptr);
+                             const int64_t* ql_bias = nullptr, QlState* ql = nullptr, int splits = 1,
+                             unsigned* tile_cnt = nullptr);
+// How many runs of k the digit-plane GEMM of [k0, k1) splits into (1 unless its tiles leave CUs idle); a split
+// launch needs y zeroed, one zeroed counter per tile (the grid's tiles: at most 128) and accumulate = 0.
+int plane_gemm_splits(int px, int pw, int M, int N, int k0, int k1);
 hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
                              const int32_t* mant, const int32_t* shift, const int8_t* lut, int out_kind, void* y,
                              hipStream_t s);

@@ -78,11 +78,16 @@ __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, in
 // ------------------------------------------------------------------------------------------------------------------
 // With ql non-null (the last k-chunk of a device QuantLinear call) the epilogue also adds the bias in units of c,
 // (bs * c^-1).apply(bias[n]) when ql->mode == 0, and raises ql->ymax to the largest |result| (layers.rs:314-321).
+// Split k (gridDim.y = S > 1, a QuantLinear call whose tiles leave CUs idle): CTA (t, s) takes the s-th of S
+// contiguous runs of k-tiles and adds its partial result into y with 64-bit atomics (y starts at zero; wrapping
+// addition is exact in any order); the last of the S CTAs of tile t to arrive (tile_cnt[t], zero at the start)
+// reads the finished sums and does the bias and maximum part of the epilogue.
 template <int PX, int PW, int WTM, int WTN>
 __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
                                                          int64_t* __restrict__ y, int M, int N, int kp, int k0,
                                                          int k1, int accumulate, int drop_top,
-                                                         const int64_t* __restrict__ ql_bias, QlState* ql) {
+                                                         const int64_t* __restrict__ ql_bias, QlState* ql,
+                                                         unsigned* __restrict__ tile_cnt) {
     constexpr int BK = 64, CPR = BK / 16;
     constexpr int BM = 64 * WTM, BN = 64 * WTN;
     constexpr int NG = PX + PW - 1;
@@ -141,13 +146,16 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
             }
     };
 
-    const int nk = (k1 - k0) / BK;
-    gload_tile(k0);
+    // this CTA's run of k-tiles: [kb, kb + nk * BK), nk >= 1 by the launcher's choice of S
+    const int nk_all = (k1 - k0) / BK, per = (nk_all + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int kb = k0 + (int)blockIdx.y * per * BK;
+    const int nk = nk_all - (int)blockIdx.y * per < per ? nk_all - (int)blockIdx.y * per : per;
+    gload_tile(kb);
     lstore_tile(0);
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) gload_tile(k0 + (kt + 1) * BK);
+        if (kt + 1 < nk) gload_tile(kb + (kt + 1) * BK);
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ks++) {
             const int chunk = 2 * ks + (lane >> 5);
@@ -180,7 +188,38 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
     }
 
     int64_t lmax = 0;
-    const bool badd = ql && ql_bias && ql->mode == 0;
+    const bool badd = ql && ql_bias && ql->mode == 0, split = gridDim.y > 1;
+    if (split) {  // partial sums into y, then the tile's last CTA goes on with the finished sums
+#pragma unroll
+        for (int i = 0; i < WTM; i++)
+#pragma unroll
+            for (int j = 0; j < WTN; j++) {
+                const int n = n0 + wn * 32 * WTN + j * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    uint64_t v = 0;
+#pragma unroll
+                    for (int g = 0; g < NG; g++) {
+                        if (8 * g >= 64) continue;  // 256^g = 0 mod 2^64
+                        if (drop_top && g == NG - 1) continue;
+                        v += (uint64_t)(int64_t)acc[g][i][j][r] << (8 * g);
+                    }
+                    if (m < M && n < N)
+                        atomicAdd(reinterpret_cast<unsigned long long*>(y + (size_t)m * N + n), (unsigned long long)v);
+                }
+            }
+        // Every partial went to y as a device-scope atomic, performed where all CTAs' atomics are: once a wave's
+        // vector-memory count drains they are done, and the barrier then orders them before the tile's arrival
+        // (no cache write-back is needed, there are no plain stores to publish). The last CTA reads the sums
+        // with device-scope loads.
+        __shared__ int s_last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(&tile_cnt[blockIdx.x], 1u) == gridDim.y - 1;
+        __syncthreads();
+        if (!s_last) return;  // uniform
+    }
 #pragma unroll
     for (int i = 0; i < WTM; i++)
 #pragma unroll
@@ -190,22 +229,28 @@ __global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restric
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                uint64_t v = 0;
-#pragma unroll
-                for (int g = 0; g < NG; g++) {
-                    if (8 * g >= 64) continue;  // 256^g = 0 mod 2^64
-                    if (drop_top && g == NG - 1) continue;
-                    v += (uint64_t)(int64_t)acc[g][i][j][r] << (8 * g);
-                }
                 if (m < M && n < N) {
                     int64_t* p = y + (size_t)m * N + n;
-                    uint64_t f = accumulate ? (uint64_t)*p + v : v;
+                    uint64_t f;
+                    if (split) {  // the finished sum, read at the scope the other CTAs' atomics were performed
+                        f = __hip_atomic_load(reinterpret_cast<uint64_t*>(p), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        uint64_t v = 0;
+#pragma unroll
+                        for (int g = 0; g < NG; g++) {
+                            if (8 * g >= 64) continue;  // 256^g = 0 mod 2^64
+                            if (drop_top && g == NG - 1) continue;
+                            v += (uint64_t)(int64_t)acc[g][i][j][r] << (8 * g);
+                        }
+                        f = accumulate ? (uint64_t)*p + v : v;
+                    }
                     if (ql) {
                         f += bc;
                         const int64_t a = (int64_t)f < 0 ? (int64_t)(0 - f) : (int64_t)f;  // i64::abs, wrapping
                         lmax = a > lmax ? a : lmax;
                     }
-                    *p = (int64_t)f;
+                    if (!split || bc != 0) *p = (int64_t)f;
                 }
             }
         }
@@ -812,35 +857,58 @@ hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t i
     return hipGetLastError();
 }
 
+// The tile shape of the digit-plane GEMM for px x pw planes: accumulators within ~160 registers (2x2 tiles of 32x32
+// per wave for <= 2 plane-sum groups, 1x2 for <= 5, 1x1 beyond), and half-width tiles when 64 x 128 tiles would
+// leave CUs idle (N = 896 at M = 512). Returns the number of tiles.
+static int64_t plane_gemm_shape(int px, int pw, int M, int N, int& wtm, int& wtn) {
+    const int ng = px + pw - 1;
+    wtm = ng <= 2 ? 2 : 1, wtn = ng <= 5 ? 2 : 1;
+    if (wtn == 2 && ceil_div(N, 64 * wtn) * ceil_div(M, 64 * wtm) < 256) wtn = 1;
+    return ceil_div(N, 64 * wtn) * ceil_div(M, 64 * wtm);
+}
+
+int plane_gemm_splits(int px, int pw, int M, int N, int k0, int k1) {
+    int wtm, wtn;
+    const int64_t tiles = plane_gemm_shape(px, pw, M, N, wtm, wtn);
+    const int nk = (k1 - k0) / 64;
+    // the split costs atomic passes over the M x N outputs: worth it for long k (down: 76 k-tiles) or one row tile
+    // (decode), not for short k over many rows (N = 896 at M = 512, K = 896: measured slower)
+    if (tiles >= 128 || nk < 2 || (nk < 24 && M > 64)) return 1;
+    int want = (int)(256 / tiles);
+    want = want > 4 ? 4 : (want < 1 ? 1 : want);
+    want = want > nk ? nk : want;
+    const int per = (nk + want - 1) / want;
+    return (nk + per - 1) / per;  // every run of k-tiles is non-empty
+}
+
 template <int PX, int PW>
 static hipError_t plane_gemm_px_pw(const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp, int k0,
                                    int k1, int accumulate, int drop_top, const int64_t* ql_bias, QlState* ql,
-                                   hipStream_t s) {
-    constexpr int NG = PX + PW - 1;
-    // keep the accumulators within ~160 registers: 2x2 tiles for <= 2 groups, 1x2 for <= 5, 1x1 beyond
-    constexpr int WTM = NG <= 2 ? 2 : 1;
-    constexpr int WTN = NG <= 5 ? 2 : 1;
-    constexpr int BM = 64 * WTM, BN = 64 * WTN;
-    const int64_t tiles = ceil_div(N, BN) * ceil_div(M, BM);
-    if (WTN == 2 && tiles < 256) {  // too few tiles for the CUs (N = 896 at M = 512): half-width tiles, twice the CTAs
-        dim3 grid((unsigned)(ceil_div(N, BN / 2) * ceil_div(M, BM)));
+                                   int splits, unsigned* cnt, hipStream_t s) {
+    int wtm, wtn;
+    const int64_t tiles = plane_gemm_shape(PX, PW, M, N, wtm, wtn);
+    const dim3 grid((unsigned)tiles, (unsigned)splits);
+    constexpr int NG = PX + PW - 1, WTM = NG <= 2 ? 2 : 1;
+    if (wtn == 1)
         plane_gemm_kernel<PX, PW, WTM, 1><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
-                                                                     drop_top, ql_bias, ql);
-        return hipGetLastError();
-    }
-    plane_gemm_kernel<PX, PW, WTM, WTN><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1,
-                                                                                   accumulate, drop_top, ql_bias, ql);
+                                                                     drop_top, ql_bias, ql, cnt);
+    else if constexpr (NG <= 5)
+        plane_gemm_kernel<PX, PW, WTM, 2><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
+                                                                     drop_top, ql_bias, ql, cnt);
     return hipGetLastError();
 }
 
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
                              int k0, int k1, int accumulate, int drop_top, hipStream_t s, const int64_t* ql_bias,
-                             QlState* ql) {
+                             QlState* ql, int splits, unsigned* tile_cnt) {
     if (M <= 0 || N <= 0 || k1 <= k0) return hipSuccess;
     if ((k0 % 64) || (k1 % 64) || k1 > kp || ceil_div(M, 64) * ceil_div(N, 64) > INT32_MAX) return hipErrorInvalidValue;
+    if (splits != 1 && (splits != plane_gemm_splits(px, pw, M, N, k0, k1) || !tile_cnt || accumulate))
+        return hipErrorInvalidValue;
 #define KT_CASE(a, b) \
     if (px == a && pw == b)                                                                                  \
-        return plane_gemm_px_pw<a, b>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top, ql_bias, ql, s);
+        return plane_gemm_px_pw<a, b>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top, ql_bias, ql, splits, \
+                                      tile_cnt, s);
     KT_CASE(1, 1) KT_CASE(1, 3) KT_CASE(1, 5) KT_CASE(3, 1) KT_CASE(3, 3) KT_CASE(3, 5) KT_CASE(5, 1) KT_CASE(5, 3)
     KT_CASE(5, 5)
 #undef KT_CASE

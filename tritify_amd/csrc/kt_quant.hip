@@ -149,8 +149,15 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
                                                               const kt_hip_qscale* __restrict__ xs, int64_t w_mant,
                                                               int32_t w_shift, int has_bias, int64_t b_mant,
                                                               int32_t b_shift, QlState* __restrict__ st,
-                                                              int8_t* __restrict__ xa) {
+                                                              int8_t* __restrict__ xa, uint64_t* __restrict__ zacc,
+                                                              int64_t nzacc, uint32_t* __restrict__ zcnt,
+                                                              int nzcnt) {
     __shared__ uint32_t red[QL_THREADS / 64];
+    {  // a split-k GEMM follows: its accumulators and per-tile arrival counters start at zero
+        const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x, st_ = (int64_t)gridDim.x * QL_THREADS;
+        for (int64_t i = i0; i < nzacc; i += st_) zacc[i] = 0;
+        for (int64_t i = i0; i < nzcnt; i += st_) zcnt[i] = 0;
+    }
     uint32_t m = 0;
     for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
     m = block_max(m, red);
@@ -271,21 +278,26 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
     int8_t* xa = (int8_t*)(base + off[0]);
     int64_t* acc = (int64_t*)(base + off[1]);
     uint32_t* part_x = (uint32_t*)(base + off[2]);
-    (void)off[3];  // the workspace keeps its fifth part (formerly the |acc| partials) for a stable layout
+    uint32_t* tile_cnt = (uint32_t*)(base + off[3]);  // the split-k GEMM's per-tile arrival counters
     QlState* st = (QlState*)(base + off[4]);
     const int64_t kp = (in + 63) / 64 * 64, n = rows * out;
+    // one k-chunk whose tiles leave CUs idle (the decode row, N = 896 at M = 512): split k across CTAs
+    const int splits = kp <= flush_k ? plane_gemm_splits(3, pw, (int)rows, (int)out, 0, (int)kp) : 1;
+    const int ntiles = splits > 1 ? (int)(((out + 63) / 64) * ((rows + 63) / 64)) : 0;
+    if (ntiles * 4 > KT_QL_PARTS * 8) return hipErrorInvalidValue;  // cannot happen: a split grid has < 128 tiles
 
     const int gx = grid_for(rows * in, 8);
     ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
-    ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(x, rows, in, kp, part_x, gx, xs, w_mant, w_shift,
-                                                                      bias != nullptr, b_mant, b_shift, st, xa);
+    ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(
+        x, rows, in, kp, part_x, gx, xs, w_mant, w_shift, bias != nullptr, b_mant, b_shift, st, xa,
+        splits > 1 ? reinterpret_cast<uint64_t*>(acc) : nullptr, splits > 1 ? n : 0, tile_cnt, ntiles);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     for (int64_t k0 = 0; k0 < kp; k0 += flush_k) {
         const int64_t k1 = kp - k0 < flush_k ? kp : k0 + flush_k;
         const bool last = k1 == kp;
         e = launch_plane_gemm(3, pw, xa, wb, acc, (int)rows, (int)out, (int)kp, (int)k0, (int)k1, k0 > 0, 0, s,
-                              last ? bias : nullptr, last ? st : nullptr);
+                              last ? bias : nullptr, last ? st : nullptr, splits, tile_cnt);
         if (e != hipSuccess) return e;
     }
     ql_requant_kernel<<<grid_for(n, 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift, y, os);
