@@ -320,7 +320,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // 128-row tile (one group: a dense product, whose only short tile is its last). Persistent:
 // CTA b (XCD b % 8) takes the tiles of its XCD's contiguous share of the tile space, so an XCD's L2 serves
 // consecutive column tiles of the same rows and consecutive groups' weights.
-enum { GT_ALL = 0, GT_MIXED = 1 };
+enum { GT_ALL = 0, GT_MIXED = 1, GT_HALF = 2 };
 
 template <int EPI, int TAILS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_grouped_kernel(
@@ -329,8 +329,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     size_t glo, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
     const int16_t* __restrict__ silu, int h_shift, int8_t* __restrict__ y, int ystride,
     int32_t* __restrict__ off_out, int rows_one) {
-    typedef GTile C;  // the tile space
-    typedef GTile CT;  // the computing tile (GT_MIXED: GTileH for a tail of at most 64 rows)
+    // the tile space and the computing tile: 128-row tiles (GT_MIXED: GTileH for a tail of at most 64 rows), or
+    // 64-row tiles throughout (GT_HALF: one group whose 128-row tiles would leave CUs idle, a prefill batch)
+    typedef typename std::conditional<TAILS == GT_HALF, GTileH, GTile>::type C;
+    typedef C CT;
     static_assert(GTileH::NT == C::NT && GTileH::BN == C::BN && GTileH::RING <= C::RING, "one tile space");
     constexpr int NT = C::NT, BM = C::BM, BN = C::BN;
     __shared__ __attribute__((aligned(16))) int8_t smem[CT::RING];
@@ -480,6 +482,20 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
                                                                        count, groups, wlo, wnib, glo, N, kp, mant, \
                                                                        shift, silu, h_shift, y, ystride, off,      \
                                                                        (int)max_rows)
+    const int64_t tiles_h = (max_rows + GTileH::BM - 1) / GTileH::BM * tiles_n;
+    if (groups == 1 && (max_rows + GTile::BM - 1) / GTile::BM * tiles_n < 512) {
+        // a short dense batch, fewer 128-row tiles than CTA slots (two per CU): 64-row tiles, twice the tiles
+        const unsigned grid_h = (unsigned)(tiles_h < 512 ? (tiles_h + 7) / 8 * 8 : 512);
+        if (epi == KT_EPI_I8)
+            w12_grouped_kernel<KT_EPI_I8, GT_HALF><<<dim3(grid_h), dim3(256), 0, s>>>(
+                x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu,
+                h_shift, y, ystride, off_out, (int)max_rows);
+        else
+            w12_grouped_kernel<KT_EPI_SWIGLU, GT_HALF><<<dim3(grid_h), dim3(256), 0, s>>>(
+                x, (uint32_t)x_bytes, list, list_stride, count, groups, wlo, wnib, glo, N, kp, mant, shift, silu,
+                h_shift, y, ystride, off_out, (int)max_rows);
+        return hipGetLastError();
+    }
     if (groups == 1) {
         if (epi == KT_EPI_I8) KT_GROUPED(KT_EPI_I8, GT_ALL, off_out);
         else KT_GROUPED(KT_EPI_SWIGLU, GT_ALL, off_out);
