@@ -20,7 +20,7 @@ namespace kt {
 constexpr int CONV_PATCH_MAX = 16384;  // bytes of the staged image rows (ci * kh * (stride * 127 + kw))
 
 template <int KTILES>
-__global__ __launch_bounds__(256) void conv_patch_kernel(const uint8_t* __restrict__ img, const int8_t* __restrict__ lut,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_patch_kernel(const uint8_t* __restrict__ img, const int8_t* __restrict__ lut,
                                                          int CI, int H, int W, int KH, int KW, int S, int P, int OH,
                                                          int OW, const int8_t* __restrict__ wlo,
                                                          const uint8_t* __restrict__ wnib, int CO,
