@@ -83,7 +83,7 @@ __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, in
 // addition is exact in any order); the last of the S CTAs of tile t to arrive (tile_cnt[t], zero at the start)
 // reads the finished sums and does the bias and maximum part of the epilogue.
 template <int PX, int PW, int WTM, int WTN>
-__global__ __launch_bounds__(256) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
                                                          int64_t* __restrict__ y, int M, int N, int kp, int k0,
                                                          int k1, int accumulate, int drop_top,
                                                          const int64_t* __restrict__ ql_bias, QlState* ql,
