@@ -335,6 +335,32 @@ int kt_hip_dec_attention_step(int dev, const int8_t* qkv_dev, const int32_t* pos
                               int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd, const int16_t* cos_dev,
                               const int16_t* sin_dev, const int32_t* exp_tab_dev, int8_t* o_dev, int64_t max_pos,
                               void* stream);
+/* The decode step's attention output projection spread over the calls around it (no separate counterpart in the
+ * reference: its decode step runs attention and then the o QuantLinear, decoder.rs), three calls that together give
+ * the integers of kt_hip_dec_attention_step, kt_hip_w12_linear (KT_OUT_I32_ADD, the o projection into the
+ * residual r), kt_hip_w12_swiglu_norm (m = 1) and kt_hip_w12_linear (KT_OUT_I32_ADD, the down projection into r),
+ * with one launch fewer:
+ * 1. kt_hip_dec_attention_o_step: the attention step, then each head's CTA adds its 64 outputs' products with W_o
+ *    (wo_lo_dev / wo_nib_dev: the d x (nh * hd) W12 planes, kt_hip_w12_bytes layout) into oacc_dev (d int32, the
+ *    W12 dot sums before requantization), which must be zero on entry.
+ * 2. kt_hip_w12_swiglu_norm_o: kt_hip_w12_swiglu_norm of the one residual row r + requant_o(oacc) (saturating;
+ *    omant_dev / oshift_dev: the o projection's per-channel scales); r is not written.
+ * 3. kt_hip_w12_linear_add_o: r[n] = sat(sat(r[n] + requant_o(oacc[n])) + requant(x . W[n])) for the one row x
+ *    (the down projection), and oacc[n] = 0 again.
+ * The three calls share oacc_dev and must not overlap other calls that use it. d <= 1024, nh * hd <= 8128,
+ * k <= 8128. */
+int kt_hip_dec_attention_o_step(int dev, const int8_t* qkv_dev, const int32_t* pos_dev, int8_t* kcache_dev,
+                                int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd, const int16_t* cos_dev,
+                                const int16_t* sin_dev, const int32_t* exp_tab_dev, int64_t max_pos,
+                                const int8_t* wo_lo_dev, const uint8_t* wo_nib_dev, int64_t d, int32_t* oacc_dev,
+                                void* stream);
+int kt_hip_w12_swiglu_norm_o(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev,
+                             int64_t ffn, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev,
+                             const int16_t* silu_dev, int h_shift, int8_t* y_dev, const int32_t* oacc_dev,
+                             const int32_t* omant_dev, const int32_t* oshift_dev, void* stream);
+int kt_hip_w12_linear_add_o(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t n,
+                            int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int32_t* y_dev,
+                            int32_t* oacc_dev, const int32_t* omant_dev, const int32_t* oshift_dev, void* stream);
 /* The greedy argmax in two stages for a replayable decode step. Stage 1: nparts CTAs reduce the n logits to nparts
  * keys (part_dev, uint64 each; the largest key is the first maximum), copy the logits to record_dev + step * n
  * (record_dev optional) and advance pos_dev by `advance` (pos_dev optional). Stage 2, fused with the next step's

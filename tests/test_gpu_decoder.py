@@ -224,14 +224,14 @@ def test_w12_norm_fused_products(torch_dev, m, d):
 
 @pytest.mark.parametrize("fuse", [False, True])
 def test_decoder_long_context_step(torch_dev, fuse):
-    """Decode steps beyond the attention kernel's two prefetched chunks (positions past 1024, read in its loop) and
-    both RMSNorm placements, against the oracle."""
+    """Decode steps beyond the attention kernel's two prefetched chunks (positions past 1024, read in its loop),
+    both RMSNorm placements and the output projection inside or after the attention kernel, against the oracle."""
     from tritify_amd import workloads as W
 
     cfg = dict(d=64, ffn=64, nh=2, nkv=1, hd=64, layers=1, vocab=97)
     say(f"case: decoder long context {cfg} prompt 1100, 4 tokens, fuse={fuse}")
     m, arrays = build(cfg, 700, 1104, 1100)
-    m.fuse_norm = m.fuse_norm_head = fuse
+    m.fuse_norm = m.fuse_norm_head = m.fuse_o = fuse
     prompt = W.decoder_prompt(701, 1100, cfg["vocab"])
     toks, logits = m.generate(prompt, 4, graph=fuse)
     wt, wl = O.dec_generate(dict(cfg, max_pos=1104, h_shift=8), arrays, prompt, 4)

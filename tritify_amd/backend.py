@@ -98,6 +98,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_dec_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P]),
         "kt_hip_dec_advance": (_I, [_I, _P, _I64, _P]),
         "kt_hip_dec_attention_step": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+        "kt_hip_dec_attention_o_step": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P, _P]),
+        "kt_hip_w12_swiglu_norm_o": (_I, [_I, _P, _P, _P, _I64, _I64, _P, _P, _P, _I, _P, _P, _P, _P, _P]),
+        "kt_hip_w12_linear_add_o": (_I, [_I, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
         "kt_hip_dec_argmax_part": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
         "kt_hip_dec_embed_argmax": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _P, _P]),
         "kt_hip_w12_linear_norm": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),

@@ -8,6 +8,7 @@
 // captured decode step replays for every position with no host involvement. The integer rules are stated with
 // kt_hip_dec_* in include/kt_hip.h.
 
+#include <algorithm>
 #include <hip/hip_runtime.h>
 #include <limits.h>
 #include <stdint.h>
@@ -211,20 +212,41 @@ __global__ __launch_bounds__(1024) void dec_argmax_kernel(const int32_t* __restr
 // The integer rules are those of dec_rope_kv_kernel + dec_attention_kernel.
 constexpr int ATT_NT = 512, ATT_PRE = 2;  // threads; chunks of ATT_NT positions prefetched into registers
 
+// The o projection's dot products inside the attention step (FUSE_O): acc[n] += sum_h W_o[n, h] . o_h over d output
+// channels, W_o the d x (nh * 64) W12 planes. Each head runs on og CTAs that all compute its attention (the K / V
+// rows come from L2 after the first) and split the d channels into og ranges of cw: CTA (h, part) multiplies the
+// head's 64 outputs by W_o's 64 columns of head h for channels part * cw .. part * cw + cw - 1 (loaded while the
+// attention runs; og CTAs per head spread the d x 64 W12 bytes over og CUs) and adds the partial dots into acc
+// with atomics whose results nothing waits for. The requantization into the residual happens in the consumers: the next RMSNorm-fused
+// product folds requant(acc) into the residual it normalizes, and the residual-add product after it folds it into
+// the stored residual and clears acc (w12_skinny_swiglu_kernel / w12_skinny_kernel with FOLD_O).
+struct AttnO {
+    const int8_t* lo;
+    const uint8_t* nib;
+    int32_t* acc;
+    int d;
+    int og, cw;  // CTAs per head; channels per CTA (<= ATT_NT: one per thread)
+};
+#ifndef KT_ATT_OG
+#define KT_ATT_OG 8  // CTAs per head in the o-projection step
+#endif
+
+template <bool FUSE_O>
 __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t* __restrict__ qkv,
                                                                     const int32_t* __restrict__ pos,
                                                                     int8_t* __restrict__ kc, int8_t* __restrict__ vc,
                                                                     int nh, int nkv, const int16_t* __restrict__ cosT,
                                                                     const int16_t* __restrict__ sinT,
                                                                     const int32_t* __restrict__ exp_tab,
-                                                                    int8_t* __restrict__ o, int max_pos) {
+                                                                    int8_t* __restrict__ o, int max_pos, AttnO fo) {
     constexpr int HD = 64, HH = 32, NWV = ATT_NT / 64, KP = ATT_NT / 128, VR = ATT_NT / 32;
     extern __shared__ int s_sc[];  // max_pos: the scores, then the weights
     __shared__ int s_exp[1024];
     __shared__ int s_red[2][NWV];
     __shared__ int64_t s_acc[NWV][HD];
     __shared__ __attribute__((aligned(16))) int8_t s_q[HD], s_k[HD], s_v[HD];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int h = FUSE_O ? (int)blockIdx.x / fo.og : (int)blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int part = FUSE_O ? (int)blockIdx.x % fo.og : 0;
     const int rep = nh / nkv, g = h / rep;
     const size_t rstride = (size_t)nkv * HD;
     const int8_t* kg = kc + (size_t)g * HD;
@@ -260,7 +282,7 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
     }
     const int p = pos[0], L = p + 1;
     if (p < 0 || p >= max_pos) {  // a position outside the caches and tables: no access, a zero output
-        if (tid < HD) o[h * HD + tid] = 0;
+        if (!FUSE_O && tid < HD) o[h * HD + tid] = 0;  // (FUSE_O: the residual is left as a zero output leaves it)
         return;
     }
 #pragma unroll
@@ -274,9 +296,27 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
         s_v[tid - 2 * HH] = (int8_t)ra;
     }
     __syncthreads();
-    if (h % rep == 0 && tid < HD) {
+    if (h % rep == 0 && part == 0 && tid < HD) {
         kc[(size_t)p * rstride + g * HD + tid] = s_k[tid];
         vc[(size_t)p * rstride + g * HD + tid] = s_v[tid];
+    }
+    // FUSE_O: this head's W_o fragments for channel n = part * cw + tid: k32 blocks 2h, 2h + 1 of column block n / 32,
+    // lane slot n % 32 + 32 kh in each (kh: the 16-k half), 16 lo bytes and 8 nib bytes per (block, half). Issued
+    // after the q / k / v, position and rotation loads (vector loads complete in order, so a wait for those would
+    // wait for these too) and before the score pass, whose operands are already in registers.
+    v4i wl[4];
+    v2i wn[4];
+    const int on = part * fo.cw + tid;
+    const bool has_col = FUSE_O && tid < fo.cw && on < fo.d;
+    if constexpr (FUSE_O) {
+        const int KB = nh * 2;  // k32 blocks per column block (K = nh * 64)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const size_t blk = (size_t)(on / 32) * KB + 2 * h + (q >> 1);
+            const int slot = on % 32 + 32 * (q & 1);
+            wl[q] = has_col ? *reinterpret_cast<const v4i*>(fo.lo + blk * 1024 + 16 * slot) : v4i{};
+            wn[q] = has_col ? *reinterpret_cast<const v2i*>(fo.nib + blk * 512 + 8 * slot) : v2i{};
+        }
     }
     const v4i q4 = *reinterpret_cast<const v4i*>(s_q + 16 * kq);
     const v4i knew = *reinterpret_cast<const v4i*>(s_k + 16 * kq);
@@ -380,7 +420,31 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
         int64_t sum = 0, dn = 0;
 #pragma unroll
         for (int q = 0; q < NWV; q++) sum += s_acc[q][tid], dn += s_red[1][q];
-        o[h * HD + tid] = (int8_t)clamp127(div_round(sum, dn));
+        const int8_t ov = (int8_t)clamp127(div_round(sum, dn));
+        if constexpr (FUSE_O) s_q[tid] = ov;  // s_q is free again: the head's output, the A side of the o product
+        else o[h * HD + tid] = ov;
+    }
+    if constexpr (FUSE_O) {
+        __syncthreads();
+        const v4i* a4 = reinterpret_cast<const v4i*>(s_q);
+        int asum = 0;  // -1920 * sum(a): the W12 offset term, the same for every column
+#pragma unroll
+        for (int q = 0; q < 4; q++) asum += sum4(a4[q]);
+        if (has_col) {
+            uint32_t v = 0u - 1920u * (uint32_t)asum;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {  // k = 16 q .. 16 q + 15 of the head
+                const v4i a = a4[q], lw = wl[q], hw = unpack_hi(wn[q]);
+                int dl = 0, dh = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    dl = __builtin_amdgcn_sdot4(a[e], lw[e], dl, false);
+                    dh = __builtin_amdgcn_sdot4(a[e], hw[e], dh, false);
+                }
+                v += (uint32_t)dl + ((uint32_t)dh << 8);
+            }
+            atomicAdd(fo.acc + on, (int)v);
+        }
     }
 }
 
@@ -490,9 +554,10 @@ hipError_t launch_dec_argmax(const int32_t* logits, int n, int32_t* token, int32
     return hipGetLastError();
 }
 
-hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh, int nkv,
-                                     const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
-                                     int max_pos, hipStream_t s) {
+template <bool FUSE_O>
+static hipError_t attention_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh, int nkv,
+                                 const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
+                                 int max_pos, const AttnO& fo, hipStream_t s) {
     const size_t lds = (size_t)max_pos * sizeof(int);
     static size_t lds_static = 0, lds_max = 0;  // queried once per process
     if (lds_max == 0) {
@@ -500,14 +565,32 @@ hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8
         int dev = 0, mx = 0;
         hipError_t e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-        if (e == hipSuccess) e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&dec_attention_step_kernel));
+        if (e == hipSuccess)
+            e = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&dec_attention_step_kernel<FUSE_O>));
         if (e != hipSuccess) return e;
         lds_static = fa.sharedSizeBytes, lds_max = (size_t)mx;
     }
     if (lds_static + lds > lds_max) return hipErrorInvalidValue;  // max_pos too long for one CTA
-    dec_attention_step_kernel<<<dim3((unsigned)nh), dim3(ATT_NT), lds, s>>>(qkv, pos, kc, vc, nh, nkv, cosT, sinT,
-                                                                            exp_tab, o, max_pos);
+    const unsigned ctas = (unsigned)nh * (FUSE_O ? (unsigned)fo.og : 1u);
+    dec_attention_step_kernel<FUSE_O><<<dim3(ctas), dim3(ATT_NT), lds, s>>>(qkv, pos, kc, vc, nh, nkv, cosT, sinT,
+                                                                            exp_tab, o, max_pos, fo);
     return hipGetLastError();
+}
+
+hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh, int nkv,
+                                     const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
+                                     int max_pos, hipStream_t s) {
+    return attention_step<false>(qkv, pos, kc, vc, nh, nkv, cosT, sinT, exp_tab, o, max_pos, AttnO{}, s);
+}
+
+hipError_t launch_dec_attention_o_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh,
+                                       int nkv, const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab,
+                                       int max_pos, const int8_t* wo_lo, const uint8_t* wo_nib, int d, int32_t* acc,
+                                       hipStream_t s) {
+    if (d < 1 || d > 1024 || nh * 64 > KT_SMALL_KP) return hipErrorInvalidValue;
+    const int og = std::max(KT_ATT_OG, (d + ATT_NT - 1) / ATT_NT), cw = (d + og - 1) / og;
+    const AttnO fo{wo_lo, wo_nib, acc, d, og, cw};
+    return attention_step<true>(qkv, pos, kc, vc, nh, nkv, cosT, sinT, exp_tab, nullptr, max_pos, fo, s);
 }
 
 hipError_t launch_dec_argmax_part(const int32_t* logits, int n, uint64_t* part, int nparts, int32_t* record,

@@ -744,6 +744,44 @@ int kt_hip_dec_attention_step(int dev, const int8_t* qkv_dev, const int32_t* pos
                                               sin_dev, exp_tab_dev, o_dev, (int)max_pos, (hipStream_t)stream);
 }
 
+int kt_hip_dec_attention_o_step(int dev, const int8_t* qkv_dev, const int32_t* pos_dev, int8_t* kcache_dev,
+                                int8_t* vcache_dev, int64_t nh, int64_t nkv, int64_t hd, const int16_t* cos_dev,
+                                const int16_t* sin_dev, const int32_t* exp_tab_dev, int64_t max_pos,
+                                const int8_t* wo_lo_dev, const uint8_t* wo_nib_dev, int64_t d, int32_t* oacc_dev,
+                                void* stream) {
+    if (hd != 64 || nh < 1 || nkv < 1 || nh % nkv || nh * hd > 8128 || max_pos < 1 || max_pos > 16384 || d < 1 ||
+        d > 1024 || !wo_lo_dev || !wo_nib_dev || !oacc_dev)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_dec_attention_o_step(qkv_dev, pos_dev, kcache_dev, vcache_dev, (int)nh, (int)nkv, cos_dev,
+                                                sin_dev, exp_tab_dev, (int)max_pos, wo_lo_dev, wo_nib_dev, (int)d,
+                                                oacc_dev, (hipStream_t)stream);
+}
+
+int kt_hip_w12_swiglu_norm_o(int dev, const int32_t* r_dev, const int8_t* lo_dev, const uint8_t* nib_dev,
+                             int64_t ffn, int64_t d, const int32_t* mant_dev, const int32_t* shift_dev,
+                             const int16_t* silu_dev, int h_shift, int8_t* y_dev, const int32_t* oacc_dev,
+                             const int32_t* omant_dev, const int32_t* oshift_dev, void* stream) {
+    if (ffn <= 0 || ffn % 64 || ffn > INT_MAX || d < 1 || d > 1024 || r_dev == nullptr || mant_dev == nullptr ||
+        shift_dev == nullptr || silu_dev == nullptr || h_shift < 1 || h_shift > 30 || oacc_dev == nullptr ||
+        omant_dev == nullptr || oshift_dev == nullptr)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_swiglu_norm_o(r_dev, (int)d, lo_dev, nib_dev, (int)ffn, mant_dev, shift_dev, silu_dev,
+                                             h_shift, y_dev, oacc_dev, omant_dev, oshift_dev, (hipStream_t)stream);
+}
+
+int kt_hip_w12_linear_add_o(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t n,
+                            int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int32_t* y_dev,
+                            int32_t* oacc_dev, const int32_t* omant_dev, const int32_t* oshift_dev, void* stream) {
+    if (n < 1 || n > INT_MAX || k < 1 || kp_of(k) > 8128 || mant_dev == nullptr || shift_dev == nullptr ||
+        y_dev == nullptr || oacc_dev == nullptr || omant_dev == nullptr || oshift_dev == nullptr)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12_linear_add_o(x_dev, lo_dev, nib_dev, (int)n, (int)kp_of(k), mant_dev, shift_dev, y_dev,
+                                            oacc_dev, omant_dev, oshift_dev, (hipStream_t)stream);
+}
+
 int kt_hip_dec_argmax_part(int dev, const int32_t* logits_dev, int64_t n, uint64_t* part_dev, int64_t nparts,
                            int32_t* record_dev, const int32_t* step_dev, int32_t* pos_dev, int64_t advance,
                            void* stream) {

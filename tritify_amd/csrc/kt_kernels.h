@@ -51,6 +51,17 @@ hipError_t launch_dec_advance(int32_t* pos, int by, hipStream_t s);
 hipError_t launch_dec_attention_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh, int nkv,
                                      const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab, int8_t* o,
                                      int max_pos, hipStream_t s);
+hipError_t launch_dec_attention_o_step(const int8_t* qkv, const int32_t* pos, int8_t* kc, int8_t* vc, int nh,
+                                       int nkv, const int16_t* cosT, const int16_t* sinT, const int32_t* exp_tab,
+                                       int max_pos, const int8_t* wo_lo, const uint8_t* wo_nib, int d, int32_t* acc,
+                                       hipStream_t s);
+hipError_t launch_w12_swiglu_norm_o(const int32_t* r, int d, const int8_t* lo, const uint8_t* nib, int F,
+                                    const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift,
+                                    int8_t* y, const int32_t* oacc, const int32_t* omant, const int32_t* oshift,
+                                    hipStream_t s);
+hipError_t launch_w12_linear_add_o(const int8_t* x, const int8_t* lo, const uint8_t* nib, int N, int kp,
+                                   const int32_t* mant, const int32_t* shift, int32_t* y, int32_t* oacc,
+                                   const int32_t* omant, const int32_t* oshift, hipStream_t s);
 hipError_t launch_dec_argmax_part(const int32_t* logits, int n, uint64_t* part, int nparts, int32_t* record,
                                   const int32_t* step, int32_t* pos, int advance, hipStream_t s);
 hipError_t launch_dec_embed_argmax(const uint64_t* part, int nparts, const int16_t* emb, int d, int32_t* r,

@@ -539,17 +539,29 @@ static bool dma_lds_ok() {
 // M read as zero through the x buffer descriptor (kp is a multiple of 64, so a column block has an even number of
 // k32 blocks and np whole pairs). The waves meet in LDS in i64; the per-channel scales are fetched
 // at the start, so the epilogue waits on no memory.
+//
+// FOLD_O (one row, residual-add output): before this product's requantized dots are added, the residual takes the
+// requantized o-projection sums the decode attention step left in fo.acc (y[n] = sat(sat(y[n] + requant_o(acc[n]))
+// + requant(dot)), the two residual additions in the reference's order), and the thread that owns column n clears
+// acc[n] for the next step.
 // ------------------------------------------------------------------------------------------------------------------
-template <int MT, int NW, int U, int OUT, bool SMALL, bool NORM = false>
+struct FoldO {
+    int32_t* acc;          // d int32: the o projection's dot sums (W12 offset included)
+    const int32_t* mant;   // the o projection's per-channel scales
+    const int32_t* shift;
+};
+
+template <int MT, int NW, int U, int OUT, bool SMALL, bool NORM = false, bool FOLD_O = false>
 __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __restrict__ x,
                                                              const int8_t* __restrict__ wlo,
                                                              const uint8_t* __restrict__ wnib, void* __restrict__ y,
                                                              int M, int N, int kp, const int32_t* __restrict__ mant,
                                                              const int32_t* __restrict__ shift,
-                                                             const int8_t* __restrict__ lut, int d) {
+                                                             const int8_t* __restrict__ lut, int d, FoldO fo = {}) {
     constexpr int NT = 64 * NW, OUTS = MT * 256;  // threads; outputs of the CTA (MT row tiles x 16 columns)
     static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
     static_assert(!NORM || (MT == 1 && SMALL), "the RMSNorm prologue serves M <= 16 with int32 dots");
+    static_assert(!FOLD_O || (MT == 1 && SMALL && !NORM && OUT == KT_OUT_I32_ADD), "FOLD_O: one-row residual add");
     typedef typename std::conditional<SMALL, int32_t, int64_t>::type part_t;  // SMALL: every dot fits int32
     __shared__ part_t sP[NW][OUTS];
     __shared__ int32_t sX[NW][MT * 16];
@@ -572,6 +584,10 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
     int32_t yres = 0;
     if constexpr (PRE_Y) {
         if (tid < OUTS && (tid >> 4) < M && on < N) yres = reinterpret_cast<const int32_t*>(y)[(size_t)(tid >> 4) * N + on];
+    }
+    int32_t fa = 0, fm = 0, fs = 0;  // FOLD_O: row 0's o sum and its scale, loaded now as well
+    if constexpr (FOLD_O) {
+        if (tid < 16 && on < N) fa = fo.acc[on], fm = fo.mant[on], fs = fo.shift[on];
     }
 
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
@@ -672,7 +688,12 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
                 else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
                 else if constexpr (OUT == KT_OUT_I32_ADD) {
                     int32_t* p = reinterpret_cast<int32_t*>(y) + idx;
-                    *p = sat_add32(PRE_Y ? yres : *p, col_requant<true>(vi, cq));
+                    int32_t base = PRE_Y ? yres : *p;
+                    if constexpr (FOLD_O) {  // M == 1: this is row 0, column on
+                        base = sat_add32(base, col_requant<true>(fa, col_q(fm, fs)));
+                        fo.acc[on] = 0;
+                    }
+                    *p = sat_add32(base, col_requant<true>(vi, cq));
                 }
                 else {
                     const int q = col_requant<false>(vi, cq);
@@ -695,14 +716,20 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
 // memory), both streamed in one pass over k. Epilogue: g, u = int8 requant per channel (gate channel u, up channel
 // F + u), h = clamp(requant(silu[g + 127] * u, 1, h_shift)). Every dot is SMALL (kp <= 8128).
 // ------------------------------------------------------------------------------------------------------------------
-template <int MT, int NW, int U, bool NORM = false>
+//
+// FOLD_O (with NORM, one row, d <= 2 * 64 NW): the residual row is normalized with the o projection's requantized
+// sums in fo.acc added first (r + requant_o(acc), saturating): the residual the reference's o QuantLinear leaves.
+// The residual itself is not written here (other CTAs are reading it); the residual-add product after this one
+// folds the same sums into it.
+template <int MT, int NW, int U, bool NORM = false, bool FOLD_O = false>
 __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     int8_t* __restrict__ y, int ystride, int M, int F, int kp, const int32_t* __restrict__ mant,
-    const int32_t* __restrict__ shift, const int16_t* __restrict__ silu, int h_shift, int d) {
+    const int32_t* __restrict__ shift, const int16_t* __restrict__ silu, int h_shift, int d, FoldO fo = {}) {
     constexpr int NT = 64 * NW, OUTS = MT * 256;
     static_assert(OUTS % NT == 0 || NT % OUTS == 0, "the threads tile the outputs");
     static_assert(!NORM || MT == 1, "the RMSNorm prologue serves M <= 16");
+    static_assert(!FOLD_O || NORM, "FOLD_O folds into the RMSNorm prologue");
     __shared__ int32_t sPg[NW][OUTS], sPu[NW][OUTS];
     __shared__ int32_t sX[NW][MT * 16];
     __shared__ int16_t sSilu[256];
@@ -710,6 +737,14 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
     __shared__ uint64_t sNss[NORM ? NW * 16 : 1], sNrq[NORM ? 32 : 1];
     int32_t pre[2];  // NORM: row 0 of the residual, loaded first
     if constexpr (NORM) norm_preload<64 * NW, 2>(reinterpret_cast<const int32_t*>(x), d, pre);
+    int32_t fa[2] = {0, 0}, fm[2] = {0, 0}, fs[2] = {0, 0};  // FOLD_O: the o sums and scales of the same values
+    if constexpr (FOLD_O) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = (int)threadIdx.x + j * NT;
+            if (i < d) fa[j] = fo.acc[i], fm[j] = fo.mant[i], fs[j] = fo.shift[i];
+        }
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int u0 = 16 * blockIdx.x, cbg = 2 * (u0 >> 5), hb = (u0 >> 4) & 1;
@@ -757,6 +792,10 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
         }
         if constexpr (NORM) {  // x rows from LDS, normalized there while the first weight loads are in flight
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (FOLD_O) {  // values past d stay 0: requant of a zero sum is 0
+#pragma unroll
+                for (int j = 0; j < 2; j++) pre[j] = sat_add32(pre[j], col_requant<true>(fa[j], col_q(fm[j], fs[j])));
+            }
             norm_rows_to_lds<NT, 2>(reinterpret_cast<const int32_t*>(x), M, d, kp, sQ, sNss, sNrq, pre);
 #pragma unroll
             for (int u = 0; u < U; u++) {
@@ -1073,6 +1112,44 @@ hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* 
     else
         w12_skinny_swiglu_kernel<1, 8, 4, true><<<grid, block, (size_t)M * kp, s>>>(x, lo, nib, y, ystride, M, F, kp,
                                                                                     mant, shift, silu, h_shift, d);
+    return hipGetLastError();
+}
+
+// The decode step's gate/up product with the attention's o sums folded into the normalized residual: one row,
+// d <= 1024 (the two preloaded values per thread cover the row).
+hipError_t launch_w12_swiglu_norm_o(const int32_t* r, int d, const int8_t* lo, const uint8_t* nib, int F,
+                                    const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift,
+                                    int8_t* y, const int32_t* oacc, const int32_t* omant, const int32_t* oshift,
+                                    hipStream_t s) {
+    const int kp = (d + 63) / 64 * 64;
+    if (F <= 0 || F % 32 || !norm_shape_ok(1, d, kp) || kp > 1024 || h_shift < 1 || h_shift > 30 || !oacc ||
+        !omant || !oshift)
+        return hipErrorInvalidValue;
+    const FoldO fo{const_cast<int32_t*>(oacc), omant, oshift};  // read only here
+    w12_skinny_swiglu_kernel<1, 8, 2, true, true><<<dim3((unsigned)(F / 16)), dim3(512), (size_t)kp, s>>>(
+        reinterpret_cast<const int8_t*>(r), lo, nib, y, F, 1, F, kp, mant, shift, silu, h_shift, d, fo);
+    return hipGetLastError();
+}
+
+// The decode step's residual-add product (one row) that also folds the o sums into the residual and clears them;
+// the launch shapes of w12_linear_out for M = 1.
+hipError_t launch_w12_linear_add_o(const int8_t* x, const int8_t* lo, const uint8_t* nib, int N, int kp,
+                                   const int32_t* mant, const int32_t* shift, int32_t* y, int32_t* oacc,
+                                   const int32_t* omant, const int32_t* oshift, hipStream_t s) {
+    if (N <= 0 || kp <= 0 || kp % 64 || kp > KT_SMALL_KP || !oacc || !omant || !oshift) return hipErrorInvalidValue;
+    const int64_t ctas = 2 * ceil_div(N, 32);
+    if (ctas > INT32_MAX) return hipErrorInvalidValue;
+    const FoldO fo{oacc, omant, oshift};
+    const dim3 grid((unsigned)ctas);
+    if (kp > 2048 && ctas < 256)
+        w12_skinny_kernel<1, 16, 5, KT_OUT_I32_ADD, true, false, true><<<grid, dim3(1024), 0, s>>>(
+            x, lo, nib, y, 1, N, kp, mant, shift, nullptr, 0, fo);
+    else if (kp <= 1024)
+        w12_skinny_kernel<1, 8, 2, KT_OUT_I32_ADD, true, false, true><<<grid, dim3(512), 0, s>>>(
+            x, lo, nib, y, 1, N, kp, mant, shift, nullptr, 0, fo);
+    else
+        w12_skinny_kernel<1, 8, 4, KT_OUT_I32_ADD, true, false, true><<<grid, dim3(512), 0, s>>>(
+            x, lo, nib, y, 1, N, kp, mant, shift, nullptr, 0, fo);
     return hipGetLastError();
 }
 

@@ -34,6 +34,10 @@ class DecoderModel:
         # instead of two); the lm_head's final norm likewise when fuse_norm_head is set (off: its 9,496 CTAs would
         # each repeat the norm, which costs more than the separate launch)
         self.fuse_norm, self.fuse_norm_head = True, False
+        # decode steps fold the attention output projection into the calls around it (one launch fewer per layer):
+        # each head's attention CTA adds its W_o dot products into o_acc; the gate/up product normalizes the residual
+        # with their requantized sums added, and the down product adds them into the residual and clears o_acc
+        self.fuse_o = True
         dv = torch.device("cuda", dev)
         self.device = dv
 
@@ -60,6 +64,7 @@ class DecoderModel:
         self.xn = zeros(R * d, torch.int8)
         self.qkv = zeros(R * self.nq, torch.int8)
         self.o = zeros(R * nh * hd, torch.int8)
+        self.o_acc = zeros(d, torch.int32)  # fuse_o: zero between decode steps (the down product clears it)
         self.h = zeros(R * ffn, torch.int8)
         self.logits = zeros(V, torch.int32)
         self.kc = zeros(L * max_pos * nkv * hd, torch.int8)
@@ -133,6 +138,8 @@ class DecoderModel:
         else:
             B.check(lib.kt_hip_dec_embed(dev, P(tokens_dev), T, P(self.emb16), d, P(self.r), s), "dec embed")
         fuse = self.fuse_norm and T <= B.NORM_MAX_M  # RMSNorm inside the skinny products' prologue
+        # a decode step with the o projection spread over the attention, gate/up and down calls (o_acc between them)
+        fold_o = tokens_dev is None and self.fuse_o and fuse and d <= 1024 and ffn <= 8128 and nh * hd <= 8128
         for l in range(self.L):
             kc, vc = P(self.kc) + l * cache, P(self.vc) + l * cache
             if fuse:
@@ -140,29 +147,41 @@ class DecoderModel:
             else:
                 B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
                 self._gemm("qkv", l, self.xn, T, nq, d, self.qkv, B.OUT_I8, s)
-            if tokens_dev is None:
-                B.check(lib.kt_hip_dec_attention_step(dev, P(self.qkv), P(self.pos), kc, vc, nh, nkv, hd,
-                                                      P(self.rope_cos), P(self.rope_sin), P(self.exp_tab), P(self.o),
-                                                      self.max_pos, s), "dec attention step")
+            if fold_o:
+                o_lo, o_nib, o_m, o_sh = self._layer_ptrs("o", l, d)
+                B.check(lib.kt_hip_dec_attention_o_step(dev, P(self.qkv), P(self.pos), kc, vc, nh, nkv, hd,
+                                                        P(self.rope_cos), P(self.rope_sin), P(self.exp_tab),
+                                                        self.max_pos, o_lo, o_nib, d, P(self.o_acc), s),
+                        "dec attention + o")
             else:
-                B.check(lib.kt_hip_dec_rope_kv(dev, P(self.qkv), T, nq, P(self.pos), nh, nkv, hd, P(self.rope_cos),
-                                               P(self.rope_sin), kc, vc, s), "dec rope")
-                B.check(lib.kt_hip_dec_attention(dev, P(self.qkv), T, nq, P(self.pos), kc, vc, nh, nkv, hd,
-                                                  P(self.exp_tab), P(self.o), self.max_pos, s), "dec attention")
-            self._gemm("o", l, self.o, T, d, nh * hd, self.r, B.OUT_I32_ADD, s)
-            lo_b, nib_b = self.sizes["gu"]
-            lo, nib = self.w["gu"]
-            m, sh = self.scale["gu"]
-            if fuse:
-                B.check(lib.kt_hip_w12_swiglu_norm(dev, P(self.r), P(lo) + l * lo_b, P(nib) + l * nib_b, T, ffn, d,
-                                                   P(m) + l * 8 * ffn, P(sh) + l * 8 * ffn, P(self.silu),
-                                                   self.h_shift, P(self.h), ffn, s), "dec gate/up")
+                if tokens_dev is None:
+                    B.check(lib.kt_hip_dec_attention_step(dev, P(self.qkv), P(self.pos), kc, vc, nh, nkv, hd,
+                                                          P(self.rope_cos), P(self.rope_sin), P(self.exp_tab),
+                                                          P(self.o), self.max_pos, s), "dec attention step")
+                else:
+                    B.check(lib.kt_hip_dec_rope_kv(dev, P(self.qkv), T, nq, P(self.pos), nh, nkv, hd,
+                                                   P(self.rope_cos), P(self.rope_sin), kc, vc, s), "dec rope")
+                    B.check(lib.kt_hip_dec_attention(dev, P(self.qkv), T, nq, P(self.pos), kc, vc, nh, nkv, hd,
+                                                      P(self.exp_tab), P(self.o), self.max_pos, s), "dec attention")
+                self._gemm("o", l, self.o, T, d, nh * hd, self.r, B.OUT_I32_ADD, s)
+            gu_lo, gu_nib, gu_m, gu_sh = self._layer_ptrs("gu", l, 2 * ffn)
+            if fold_o:
+                B.check(lib.kt_hip_w12_swiglu_norm_o(dev, P(self.r), gu_lo, gu_nib, ffn, d, gu_m, gu_sh, P(self.silu),
+                                                     self.h_shift, P(self.h), P(self.o_acc), o_m, o_sh, s),
+                        "dec gate/up + o")
+            elif fuse:
+                B.check(lib.kt_hip_w12_swiglu_norm(dev, P(self.r), gu_lo, gu_nib, T, ffn, d, gu_m, gu_sh,
+                                                   P(self.silu), self.h_shift, P(self.h), ffn, s), "dec gate/up")
             else:
                 B.check(lib.kt_hip_dec_rmsnorm(dev, P(self.r), T, d, P(self.xn), d, s), "dec rmsnorm")
-                B.check(lib.kt_hip_w12_swiglu(dev, P(self.xn), P(lo) + l * lo_b, P(nib) + l * nib_b, T, ffn, d,
-                                              P(m) + l * 8 * ffn, P(sh) + l * 8 * ffn, P(self.silu), self.h_shift,
-                                              P(self.h), ffn, s), "dec gate/up")
-            self._gemm("dn", l, self.h, T, d, ffn, self.r, B.OUT_I32_ADD, s)
+                B.check(lib.kt_hip_w12_swiglu(dev, P(self.xn), gu_lo, gu_nib, T, ffn, d, gu_m, gu_sh, P(self.silu),
+                                              self.h_shift, P(self.h), ffn, s), "dec gate/up")
+            if fold_o:
+                dn_lo, dn_nib, dn_m, dn_sh = self._layer_ptrs("dn", l, d)
+                B.check(lib.kt_hip_w12_linear_add_o(dev, P(self.h), dn_lo, dn_nib, d, ffn, dn_m, dn_sh, P(self.r),
+                                                    P(self.o_acc), o_m, o_sh, s), "dec down + o")
+            else:
+                self._gemm("dn", l, self.h, T, d, ffn, self.r, B.OUT_I32_ADD, s)
         last = P(self.r) + (T - 1) * d * 4
         if self.fuse_norm_head:
             self._gemm_norm("emb", 0, last, 1, self.V, d, self.logits, B.OUT_I32, s)
@@ -172,6 +191,14 @@ class DecoderModel:
         rec = P(self.record) if self.record is not None else None
         B.check(lib.kt_hip_dec_argmax_part(dev, P(self.logits), self.V, P(self.part), self.nparts, rec,
                                            P(self.step), P(self.pos), T, s), "dec argmax")
+
+    def _layer_ptrs(self, name, l, N):
+        """Device addresses of layer l's lo plane, nib plane, and N per-channel multipliers and shifts."""
+        lo_b, nib_b = self.sizes[name]
+        lo, nib = self.w[name]
+        m, sh = self.scale[name]
+        P = B._ptr
+        return P(lo) + l * lo_b, P(nib) + l * nib_b, P(m) + l * N * 4, P(sh) + l * N * 4
 
     def _gemm(self, name, l, x, M, N, K, y, out_kind, s) -> None:
         lo_b, nib_b = self.sizes[name]
