@@ -81,9 +81,6 @@ __device__ Sc sc_recip(Sc a) {
     return Sc{r.mant, r.shift - a.shift + 40};
 }
 
-// |v| with i64::abs's release-mode wrap (i64::MIN stays negative and never raises a maximum).
-__device__ inline int64_t abs_wrap(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64_t)v) : v; }
-
 // floor(n / d) for 0 <= n < 2^96, 0 < d < 2^63, with the quotient below 2^62: a double estimate (relative error
 // below 2^-50) corrected by the exact remainder.
 __device__ inline uint64_t udiv_est(u128 n, int64_t d) {
