@@ -82,8 +82,13 @@ __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, in
 // contiguous runs of k-tiles and adds its partial result into y with 64-bit atomics (y starts at zero; wrapping
 // addition is exact in any order); the last of the S CTAs of tile t to arrive (tile_cnt[t], zero at the start)
 // reads the finished sums and does the bias and maximum part of the epilogue.
+// Two waves per SIMD (two CTAs per CU) wherever the accumulators and operands fit 256 VGPRs; the 5 x 5 planes and
+// the 1 x 5 planes on 1 x 2 wave tiles need more and run one wave per SIMD.
 template <int PX, int PW, int WTM, int WTN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
+constexpr int plane_gemm_waves() { return (PX == 5 && PW == 5) || (PX == 1 && PW == 5 && WTN == 2) ? 1 : 2; }
+
+template <int PX, int PW, int WTM, int WTN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_waves<PX, PW, WTM, WTN>(), 2))) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
                                                          int64_t* __restrict__ y, int M, int N, int kp, int k0,
                                                          int k1, int accumulate, int drop_top,
                                                          const int64_t* __restrict__ ql_bias, QlState* ql,
