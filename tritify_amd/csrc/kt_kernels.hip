@@ -77,7 +77,8 @@ __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, in
 // Processes k in [k0, k1) (multiples of 64) and writes y = result (first chunk) or y += result.
 // ------------------------------------------------------------------------------------------------------------------
 // With ql non-null (the last k-chunk of a device QuantLinear call) the epilogue also adds the bias in units of c,
-// (bs * c^-1).apply(bias[n]) when ql->mode == 0, and raises ql->ymax to the largest |result| (layers.rs:314-321).
+// (bs * c^-1).apply(bias[n]) when ql->mode == 0, and raises the call's output maximum (ql_raise_ymax) to the
+// largest |result| (layers.rs:314-321).
 // Split k (gridDim.y = S > 1, a QuantLinear call whose tiles leave CUs idle): CTA (t, s) takes the s-th of S
 // contiguous runs of k-tiles and adds its partial result into y with 64-bit atomics (y starts at zero; wrapping
 // addition is exact in any order); the last of the S CTAs of tile t to arrive (tile_cnt[t], zero at the start)
@@ -271,7 +272,112 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_
         if (tid == 0) {
             int64_t b = s_max[0];
             for (int q = 1; q < 4; q++) b = s_max[q] > b ? s_max[q] : b;
-            if (b > 0) atomicMax(&ql->ymax, (unsigned long long)b);
+            if (b > 0) ql_raise_ymax(ql, b);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// The digit-plane product for a few rows (M <= MM <= KT_PLANE_SKINNY_M: decode rows, where a 64-row MFMA tile would
+// do 64 rows of work for one): a wave per PS_CPW output columns, its lanes striding k[k0, k1) in 16-byte chunks of
+// every plane row (coalesced 1 KB per load instruction), int32 plane-group sums per lane with sdot4 (the host's
+// flush bound keeps every partial of a group within int32, as for the MFMA accumulators), a butterfly across the
+// wave, then plane_gemm_kernel's epilogue: groups recombined modulo 2^64, drop_top, accumulate, the QuantLinear
+// bias and maximum. No k split.
+// ------------------------------------------------------------------------------------------------------------------
+#define KT_PLANE_SKINNY_M 4
+constexpr int PS_CPW = 2;  // output columns per wave
+
+template <int PX, int PW, int MM>
+__global__ __launch_bounds__(256) void plane_skinny_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
+                                                           int64_t* __restrict__ y, int M, int N, int kp, int k0,
+                                                           int k1, int accumulate, int drop_top,
+                                                           const int64_t* __restrict__ ql_bias, QlState* ql) {
+    constexpr int NG = PX + PW - 1;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = ((int)blockIdx.x * 4 + wave) * PS_CPW;  // the wave's first column
+    const size_t xplane = (size_t)M * kp, wplane = (size_t)N * kp;
+    const int nch = (k1 - k0) / 16;
+    int acc[PS_CPW][MM][NG];
+#pragma unroll
+    for (int c = 0; c < PS_CPW; c++)
+#pragma unroll
+        for (int m = 0; m < MM; m++)
+#pragma unroll
+            for (int g = 0; g < NG; g++) acc[c][m][g] = 0;
+    for (int q = lane; q < nch; q += 64) {
+        const size_t ko = (size_t)k0 + 16 * (size_t)q;
+        v4i xv[PX][MM], wv[PS_CPW][PW];
+#pragma unroll
+        for (int i = 0; i < PX; i++)
+#pragma unroll
+            for (int m = 0; m < MM; m++)
+                xv[i][m] = m < M ? *reinterpret_cast<const v4i*>(xa + i * xplane + (size_t)m * kp + ko) : v4i{};
+#pragma unroll
+        for (int c = 0; c < PS_CPW; c++)
+#pragma unroll
+            for (int j = 0; j < PW; j++)
+                wv[c][j] = nb + c < N ? *reinterpret_cast<const v4i*>(wb + j * wplane + (size_t)(nb + c) * kp + ko)
+                                      : v4i{};
+#pragma unroll
+        for (int c = 0; c < PS_CPW; c++)
+#pragma unroll
+            for (int m = 0; m < MM; m++)
+#pragma unroll
+                for (int i = 0; i < PX; i++)
+#pragma unroll
+                    for (int j = 0; j < PW; j++) {
+                        int d = acc[c][m][i + j];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) d = __builtin_amdgcn_sdot4(xv[i][m][e], wv[c][j][e], d, false);
+                        acc[c][m][i + j] = d;
+                    }
+    }
+#pragma unroll
+    for (int c = 0; c < PS_CPW; c++)
+#pragma unroll
+        for (int m = 0; m < MM; m++)
+#pragma unroll
+            for (int g = 0; g < NG; g++)
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) acc[c][m][g] += __shfl_xor(acc[c][m][g], o);
+    const bool badd = ql && ql_bias && ql->mode == 0;
+    int64_t lmax = 0;
+    if (lane == 0) {
+#pragma unroll
+        for (int c = 0; c < PS_CPW; c++) {
+            const int n = nb + c;
+            if (n >= N) continue;
+            const uint64_t bc = badd ? (uint64_t)scale_apply(ql->f_mant, ql->f_shift, ql_bias[n]) : 0;
+#pragma unroll
+            for (int m = 0; m < MM; m++) {
+                if (m >= M) continue;
+                uint64_t v = 0;
+#pragma unroll
+                for (int g = 0; g < NG; g++) {
+                    if (8 * g >= 64) continue;  // 256^g = 0 mod 2^64
+                    if (drop_top && g == NG - 1) continue;
+                    v += (uint64_t)(int64_t)acc[c][m][g] << (8 * g);
+                }
+                int64_t* p = y + (size_t)m * N + n;
+                uint64_t f = accumulate ? (uint64_t)*p + v : v;
+                if (ql) {
+                    f += bc;
+                    const int64_t a = (int64_t)f < 0 ? (int64_t)(0 - f) : (int64_t)f;  // i64::abs, wrapping
+                    lmax = a > lmax ? a : lmax;
+                }
+                *p = (int64_t)f;
+            }
+        }
+    }
+    if (ql) {  // the CTA's largest |result| into the call's maximum
+        __shared__ int64_t s_max[4];
+        if (lane == 0) s_max[wave] = lmax;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t b = s_max[0];
+            for (int w2 = 1; w2 < 4; w2++) b = s_max[w2] > b ? s_max[w2] : b;
+            if (b > 0) ql_raise_ymax(ql, b);
         }
     }
 }
@@ -917,7 +1023,7 @@ int plane_gemm_splits(int px, int pw, int M, int N, int k0, int k1) {
     const int nk = (k1 - k0) / 64;
     // the split costs atomic passes over the M x N outputs: worth it for long k (down: 76 k-tiles) or one row tile
     // (decode), not for short k over many rows (N = 896 at M = 512, K = 896: measured slower)
-    if (tiles >= 128 || nk < 2 || (nk < 24 && M > 64)) return 1;
+    if (M <= KT_PLANE_SKINNY_M || tiles >= 128 || nk < 2 || (nk < 24 && M > 64)) return 1;  // a few rows: skinny
     int want = (int)(256 / tiles);
     want = want > 4 ? 4 : (want < 1 ? 1 : want);
     want = want > nk ? nk : want;
@@ -929,6 +1035,18 @@ template <int PX, int PW>
 static hipError_t plane_gemm_px_pw(const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp, int k0,
                                    int k1, int accumulate, int drop_top, const int64_t* ql_bias, QlState* ql,
                                    int splits, unsigned* cnt, hipStream_t s) {
+    if (M <= KT_PLANE_SKINNY_M) {
+        if (splits != 1) return hipErrorInvalidValue;
+        const dim3 grid((unsigned)ceil_div(N, 4 * PS_CPW));
+        if (M == 1)
+            plane_skinny_kernel<PX, PW, 1><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
+                                                                     drop_top, ql_bias, ql);
+        else
+            plane_skinny_kernel<PX, PW, KT_PLANE_SKINNY_M><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1,
+                                                                                     accumulate, drop_top, ql_bias,
+                                                                                     ql);
+        return hipGetLastError();
+    }
     int wtm, wtn;
     const int64_t tiles = plane_gemm_shape(PX, PW, M, N, wtm, wtn);
     const dim3 grid((unsigned)tiles, (unsigned)splits);

@@ -158,6 +158,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
     uint32_t m = 0;
     for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
     m = block_max(m, red);
+    if (blockIdx.x == 0 && threadIdx.x < KT_QL_YSLOTS) st->ymax[threadIdx.x].v = 0;
     if (blockIdx.x == 0 && threadIdx.x == 0) {  // the call's record, for the GEMM epilogue and ql_requant
         QlState s{};
         s.xmax = (int64_t)m;
@@ -174,8 +175,8 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
                 s.f_mant = f.mant, s.f_shift = f.shift;
             }
         }
-        s.ymax = 0;
-        *st = s;
+        st->xmax = s.xmax, st->c_mant = s.c_mant, st->f_mant = s.f_mant;
+        st->c_shift = s.c_shift, st->f_shift = s.f_shift, st->mode = s.mode;
     }
     const int64_t quads = rows * (kp / 4);
     const int64_t xmax = (int64_t)m, half = xmax / 2;
@@ -217,7 +218,9 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* _
                                                                 int64_t b_mant, int32_t b_shift,
                                                                 int32_t* __restrict__ y,
                                                                 kt_hip_qscale* __restrict__ os) {
-    const int64_t ymax = (int64_t)st->ymax;
+    int64_t ymax = 0;
+#pragma unroll
+    for (int i = 0; i < KT_QL_YSLOTS; i++) ymax = (int64_t)st->ymax[i].v > ymax ? (int64_t)st->ymax[i].v : ymax;
     const int mode = st->mode;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         kt_hip_qscale o{};

@@ -273,15 +273,28 @@ __device__ __forceinline__ void norm_rows_to_lds(const int32_t* __restrict__ r, 
     __syncthreads();
 }
 
-// The device QuantLinear's per-call record (kt_quant.hip writes it; the digit GEMM's epilogue reads it).
+// The device QuantLinear's per-call record (kt_quant.hip writes it; the digit GEMM's epilogue reads it). The output
+// maximum is kept in KT_QL_YSLOTS words on separate 128-byte lines: CTA b of the GEMM raises slot b % KT_QL_YSLOTS
+// with an atomic maximum (a few hundred CTAs on one word serialize), ql_requant takes the largest.
+#define KT_QL_YSLOTS 16
+struct QlYSlot {
+    unsigned long long v;
+    unsigned long long pad[15];
+};
 struct QlState {
     int64_t xmax;                // max |x|
     int64_t c_mant, f_mant;      // c = from_ratio(xmax, WLEVELS) * xs * ws; f = bias scale * c^-1
     int32_t c_shift, f_shift;
     int32_t mode;                // 0: normal; 1: xmax == 0 (bias codes or zeros); 2: c == 0 (zeros)
     int32_t pad;
-    unsigned long long ymax;     // max |acc + bias| over the output, raised by the GEMM epilogue's atomics
+    unsigned long long pad2[13];
+    QlYSlot ymax[KT_QL_YSLOTS];  // max |acc + bias| over the output, in slots (above)
 };
+
+// Raise the call's output maximum from CTA b (b > 0 only).
+__device__ __forceinline__ void ql_raise_ymax(QlState* ql, int64_t b) {
+    atomicMax(&ql->ymax[blockIdx.x % KT_QL_YSLOTS].v, (unsigned long long)b);
+}
 
 // Scale::apply / requant (crates/00-kernels/kt-int/src/lib.rs:78-86, 261-272): round(v * mant / 2^shift) half away
 // from zero from the i128 product, cast to i64. Shifts of 127 or more either way give 0 (the product has at most
