@@ -300,7 +300,9 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
                               last ? bias : nullptr, last ? st : nullptr, splits, tile_cnt);
         if (e != hipSuccess) return e;
     }
-    ql_requant_kernel<<<grid_for(n, 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift, y, os);
+    // one output per thread for short outputs (a decode row: its divisions then run side by side, not 8 in a row)
+    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift,
+                                                                           y, os);
     return hipGetLastError();
 }
 
