@@ -29,6 +29,7 @@ typedef __int128 i128;
 constexpr int64_t WLEVELS = 265720;       // (3^12 - 1) / 2, layers.rs:16
 constexpr int64_t ACT_LEVELS = 1LL << 28;  // layers.rs:18
 constexpr int QL_THREADS = 256;
+constexpr int64_t QL_FUSED_MAX = 8192;  // x of at most this many values: max |x| inside the quant pass
 
 struct Sc {
     int64_t mant;
@@ -156,7 +157,15 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
         for (int64_t i = i0; i < nzcnt; i += st_) zcnt[i] = 0;
     }
     uint32_t m = 0;
-    for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
+    if (nparts > 0) {
+        for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
+    } else {  // a short x (QL_FUSED_MAX values at most): every CTA takes max |x| itself, no ql_absmax pass
+        for (int64_t i = threadIdx.x; i < rows * in; i += QL_THREADS) {
+            const int32_t v = x[i];
+            const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+            m = a > m ? a : m;
+        }
+    }
     m = block_max(m, red);
     if (blockIdx.x == 0 && threadIdx.x < KT_QL_YSLOTS) st->ymax[threadIdx.x].v = 0;
     if (blockIdx.x == 0 && threadIdx.x == 0) {  // the call's record, for the GEMM epilogue and ql_requant
@@ -286,8 +295,9 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
     const int ntiles = splits > 1 ? (int)(((out + 63) / 64) * ((rows + 63) / 64)) : 0;
     if (ntiles * 4 > KT_QL_PARTS * 8) return hipErrorInvalidValue;  // cannot happen: a split grid has < 128 tiles
 
-    const int gx = grid_for(rows * in, 8);
-    ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
+    // max |x| by its own pass, or inside every quant CTA when x is short (one launch fewer for a decode row)
+    const int gx = rows * in <= QL_FUSED_MAX ? 0 : grid_for(rows * in, 8);
+    if (gx > 0) ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
     ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(
         x, rows, in, kp, part_x, gx, xs, w_mant, w_shift, bias != nullptr, b_mant, b_shift, st, xa,
         splits > 1 ? reinterpret_cast<uint64_t*>(acc) : nullptr, splits > 1 ? n : 0, tile_cnt, ntiles);
