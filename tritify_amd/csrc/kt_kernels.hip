@@ -1111,9 +1111,14 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
     // Fewer 128 x 128 tiles than CUs: 64 x 128 tiles, or 64 x 64 (128 threads) when even those leave CUs idle, so
     // small products (prefill projections, the SAM MLP) spread over the chip
     const int64_t tiles_h = ceil_div(N, 128) * ceil_div(M, 64), tiles_q = ceil_div(N, 64) * ceil_div(M, 64);
+    const int64_t tiles_e = ceil_div(N, 64) * ceil_div(M, 32);
     if (tiles4 < 256 && small) {
         if (tiles_h >= 256 || tiles_q <= tiles_h) {
             w12_gemm_kernel<1, 2, 1, WV, NS, OUT, true><<<dim3((unsigned)tiles_h), dim3(256), 0, s>>>(
+                x, lo, nib, y, M, N, kp, mant, shift, lut);
+        } else if (tiles_q < 256 && tiles_e <= 512) {
+            // even 64 x 64 tiles leave CUs idle: 32 x 64 tiles, twice the CTAs (config 3's prefill o and down)
+            w12_gemm_kernel<1, 1, 1, WV, NS, OUT, true, 2><<<dim3((unsigned)tiles_e), dim3(128), 0, s>>>(
                 x, lo, nib, y, M, N, kp, mant, shift, lut);
         } else {
             w12_gemm_kernel<1, 2, 1, WV, NS, OUT, true, 2><<<dim3((unsigned)tiles_q), dim3(128), 0, s>>>(
