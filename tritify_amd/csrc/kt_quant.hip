@@ -298,7 +298,7 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
     // max |x| by its own pass, or inside every quant CTA when x is short (one launch fewer for a decode row)
     const int gx = rows * in <= QL_FUSED_MAX ? 0 : grid_for(rows * in, 8);
     if (gx > 0) ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
-    ql_quant_kernel<<<grid_for(rows * kp / 4, 4), QL_THREADS, 0, s>>>(
+    ql_quant_kernel<<<grid_for(rows * kp / 4, 1), QL_THREADS, 0, s>>>(
         x, rows, in, kp, part_x, gx, xs, w_mant, w_shift, bias != nullptr, b_mant, b_shift, st, xa,
         splits > 1 ? reinterpret_cast<uint64_t*>(acc) : nullptr, splits > 1 ? n : 0, tile_cnt, ntiles);
     hipError_t e = hipGetLastError();
@@ -311,7 +311,7 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
         if (e != hipSuccess) return e;
     }
     // one output per thread for short outputs (a decode row: its divisions then run side by side, not 8 in a row)
-    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 8), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift,
+    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 2), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift,
                                                                            y, os);
     return hipGetLastError();
 }
