@@ -236,3 +236,49 @@ def test_decoder_long_context_step(torch_dev, fuse):
     toks, logits = m.generate(prompt, 4, graph=fuse)
     wt, wl = O.dec_generate(dict(cfg, max_pos=1104, h_shift=8), arrays, prompt, 4)
     assert np.array_equal(logits.reshape(-1), wl) and np.array_equal(toks, wt)
+
+
+def test_fold_o_entry_points_saturate(torch_dev):
+    """The decode step's o-projection fold through the C ABI against the unfused integers: kt_hip_w12_linear_add_o
+    adds the requantized o sums into the residual and then its own requantized product, each addition saturating
+    (residual entries at the int32 limits, o sums at both signs), and clears the accumulator; twice in a row on
+    one accumulator. (The gate/up side of the fold is covered by the decoder runs against the oracle.)"""
+    import tritify_amd as T
+
+    torch = torch_dev
+    lib, P = T.lib(), T.backend._ptr
+    s = torch.cuda.current_stream().cuda_stream
+    d, ffn = 128, 192
+    rng = np.random.default_rng(77)
+    w_dn = rng.integers(-2048, 2048, size=d * ffn).astype(np.int32)
+    dm, dsh = O.channel_scales(w_dn, d, ffn, 40)
+    om = rng.integers(1 << 29, 1 << 30, size=d).astype(np.int32)
+    osh = rng.integers(20, 30, size=d).astype(np.int32)
+    lo_dn, nib_dn = T.w12_bytes(d, ffn)
+    lo_d = torch.empty(lo_dn, dtype=torch.int8, device="cuda")
+    nib_d = torch.empty(nib_dn, dtype=torch.uint8, device="cuda")
+    T.w12_upload(w_dn, d, ffn, lo_d, nib_d)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    acc_d = torch.zeros(d, dtype=torch.int32, device="cuda")
+    for call in range(2):
+        r = rng.integers(-(2**31), 2**31, size=d, dtype=np.int64).astype(np.int32)
+        r[:4] = [2**31 - 1, -(2**31), 2**31 - 5, -(2**31) + 5]
+        acc = rng.integers(-(2**28), 2**28, size=d).astype(np.int32)
+        acc[:4] = [2**28, -(2**28), 2**28, -(2**28)]
+        h = rng.integers(-127, 128, size=ffn).astype(np.int8)
+        ro = np.clip(r.astype(np.int64) + O.requant_channels(acc, 1, d, om, osh, -(2**31), 2**31 - 1),
+                     -(2**31), 2**31 - 1)
+        dot = O.linear_threads(h.astype(np.int32), w_dn, 1, d, ffn, 1, O.lib().kt_cpu_auto_variant())
+        want = np.clip(ro + O.requant_channels(dot, 1, d, dm, dsh, -(2**31), 2**31 - 1), -(2**31), 2**31 - 1)
+        say(f"case: fold-o down d={d} ffn={ffn} call {call}")
+        acc_d.copy_(dev(acc))
+        r_d = dev(r)
+        h_d = torch.zeros(T.kp(ffn), dtype=torch.int8, device="cuda")
+        h_d[:ffn] = dev(h)
+        om_d, osh_d, dm_d, dsh_d = dev(om), dev(osh), dev(dm), dev(dsh)
+        T.backend.check(lib.kt_hip_w12_linear_add_o(0, P(h_d), P(lo_d), P(nib_d), d, ffn, P(dm_d), P(dsh_d),
+                                                    P(r_d),
+                                                    P(acc_d), P(om_d), P(osh_d), s), "w12 linear add o")
+        torch.cuda.synchronize()
+        assert np.array_equal(r_d.cpu().numpy(), want.astype(np.int32)), call
+        assert int(acc_d.count_nonzero().item()) == 0, "the accumulator is cleared"
