@@ -104,6 +104,18 @@ int kt_hip_quant_linear(int dev, const int32_t* x_dev, int64_t rows, int64_t in_
                         const int8_t* w_planes_dev, int pw, int64_t out_f, int64_t w_mant, int32_t w_shift,
                         const int64_t* bias_dev, int64_t b_mant, int32_t b_shift, void* ws_dev, size_t ws_bytes,
                         int32_t* y_dev, kt_hip_qscale* os_dev, void* stream);
+/* kt_hip_quant_linear with no workspace argument and no allocation of any kind: the workspace lives in a
+ * library-owned device array of KT_QL_SCRATCH_BYTES on each GPU (held until the process ends), so the call can run
+ * where hipMalloc cannot (code under HIP graph capture, tight serving loops, hosts that forbid allocation). No
+ * counterpart in the reference; it is for those callers that cannot allocate. Same integers, arguments and
+ * requirements as kt_hip_quant_linear, plus kt_hip_quant_linear_workspace(rows, in_f, out_f) <=
+ * KT_QL_SCRATCH_BYTES (else hipErrorInvalidValue before any device work). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, two threads) race and must be ordered by the caller. */
+#define KT_QL_SCRATCH_BYTES ((size_t)32 << 20)
+int kt_hip_quant_linear_noalloc(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f,
+                                const kt_hip_qscale* xs_dev, const int8_t* w_planes_dev, int pw, int64_t out_f,
+                                int64_t w_mant, int32_t w_shift, const int64_t* bias_dev, int64_t b_mant,
+                                int32_t b_shift, int32_t* y_dev, kt_hip_qscale* os_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Backend layer: one LinearBackend on one device (kt_cuda::open, lib.rs:252; TcLinear, backend.rs:77-192).

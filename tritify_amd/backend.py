@@ -108,6 +108,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_quant_linear_workspace": (_SZ, [_I64, _I64, _I64, _P]),
         "kt_hip_quant_linear": (_I, [_I, _P, _I64, _I64, _P, _P, _I, _I64, _I64, C.c_int32, _P, _I64, C.c_int32, _P,
                                      _SZ, _P, _P, _P]),
+        "kt_hip_quant_linear_noalloc": (_I, [_I, _P, _I64, _I64, _P, _P, _I, _I64, _I64, C.c_int32, _P, _I64,
+                                             C.c_int32, _P, _P, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
@@ -329,6 +331,7 @@ def w12_swiglu_norm(r_dev, lo_dev, nib_dev, m: int, ffn: int, d: int, mant_dev, 
 
 
 QL_WS_PARTS = 5
+QL_SCRATCH_BYTES = 32 << 20  # KT_QL_SCRATCH_BYTES: the no-allocation entry point's per-GPU scratch
 
 
 def quant_linear_workspace(rows: int, in_f: int, out_f: int) -> tuple[int, list[int]]:
@@ -350,6 +353,19 @@ def quant_linear(x_dev, rows: int, in_f: int, xs_dev, w_planes_dev, pw: int, out
                                   int(w_scale[0]), int(w_scale[1]), _ptr(bias_dev), int(bm), int(bs), _ptr(ws_dev),
                                   ws_bytes, _ptr(y_dev), _ptr(os_dev), _stream(stream)),
         "quant linear",
+    )
+
+
+def quant_linear_noalloc(x_dev, rows: int, in_f: int, xs_dev, w_planes_dev, pw: int, out_f: int, w_scale,
+                         bias_dev, b_scale, y_dev, os_dev, stream=None, dev: int = 0) -> None:
+    """quant_linear with its workspace in the library's per-GPU scratch array: allocates nothing. Calls that overlap
+    on one GPU race on that array."""
+    bm, bs = b_scale if b_scale is not None else (0, 0)
+    check(
+        lib().kt_hip_quant_linear_noalloc(dev, _ptr(x_dev), rows, in_f, _ptr(xs_dev), _ptr(w_planes_dev), pw, out_f,
+                                          int(w_scale[0]), int(w_scale[1]), _ptr(bias_dev), int(bm), int(bs),
+                                          _ptr(y_dev), _ptr(os_dev), _stream(stream)),
+        "quant linear (no allocation)",
     )
 
 

@@ -235,6 +235,25 @@ int kt_hip_quant_linear(int dev, const int32_t* x_dev, int64_t rows, int64_t in_
                                         (hipStream_t)stream);
 }
 
+int kt_hip_quant_linear_noalloc(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f,
+                                const kt_hip_qscale* xs_dev, const int8_t* w_planes_dev, int pw, int64_t out_f,
+                                int64_t w_mant, int32_t w_shift, const int64_t* bias_dev, int64_t b_mant,
+                                int32_t b_shift, int32_t* y_dev, kt_hip_qscale* os_dev, void* stream) {
+    if (rows < 1 || in_f < 1 || out_f < 1 || (pw != 1 && pw != 3 && pw != 5) || w_mant < 0 || b_mant < 0)
+        return (int)hipErrorInvalidValue;
+    const int64_t kp = kp_of(in_f);
+    if (rows * kp >= ((int64_t)1 << 31) || rows * out_f >= ((int64_t)1 << 31) || kp > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    if (!x_dev || !xs_dev || !w_planes_dev || !y_dev || !os_dev) return (int)hipErrorInvalidValue;
+    const size_t need = kt_hip_quant_linear_workspace(rows, in_f, out_f, nullptr);
+    if (need == 0 || need > KT_QL_SCRATCH_BYTES) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    void* ws = nullptr;
+    KT_TRY(kt::ql_scratch(dev, &ws));
+    return (int)kt::launch_quant_linear(x_dev, rows, in_f, xs_dev, w_planes_dev, pw, out_f, w_mant, w_shift, bias_dev,
+                                        b_mant, b_shift, flush_of(3, pw), ws, y_dev, os_dev, (hipStream_t)stream);
+}
+
 // ----------------------------------------------------------------------------------------------------------------
 // Backend layer (TcLinear, crates/02-runtime/kt-cuda/src/backend.rs:77-192)
 // ----------------------------------------------------------------------------------------------------------------

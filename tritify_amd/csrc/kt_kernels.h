@@ -74,6 +74,9 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
                                const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
                                const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
                                int32_t* y, kt_hip_qscale* os, hipStream_t s);
+// The device address of device `dev`'s QuantLinear scratch array (KT_QL_SCRATCH_BYTES), looked up once per device;
+// `dev` must be the current device.
+hipError_t ql_scratch(int dev, void** ptr);
 hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int N,
                                   const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s);
 hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int F,

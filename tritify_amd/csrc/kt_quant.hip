@@ -16,6 +16,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <vector>
+
 #include "kt_kernels.h"
 #include "kt_w12_core.h"
 
@@ -270,6 +273,29 @@ size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_Q
         at += (sizes[i] + 255) / 256 * 256;
     }
     return at;
+}
+
+// The workspace of kt_hip_quant_linear_noalloc: one copy per GPU, resident from the code object's load until the
+// process ends. Host code never passes this name to a kernel (on the host it is a stand-in, not a device address):
+// it uses the address ql_scratch looked up for the current device.
+static __device__ __align__(256) uint8_t scratch[KT_QL_SCRATCH_BYTES];
+
+hipError_t ql_scratch(int dev, void** ptr) {
+    static std::mutex mu;
+    static std::vector<void*> addr;  // per device, filled on the device's first call
+    *ptr = nullptr;
+    if (dev < 0) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(mu);
+    if ((size_t)dev >= addr.size()) addr.resize((size_t)dev + 1, nullptr);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 static int grid_for(int64_t n, int64_t per_thread) {
