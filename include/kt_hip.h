@@ -118,6 +118,85 @@ int kt_hip_quant_linear_noalloc(int dev, const int32_t* x_dev, int64_t rows, int
                                 int32_t b_shift, int32_t* y_dev, kt_hip_qscale* os_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * The reference decoder's layers at the reference's own integer semantics (crates/01-engine/kt-core/src/
+ * {layers,attention,model,generate}.rs), device-resident: activations are i32 codes at the 2^28 level with one
+ * kt-int Scale per tensor (a kt_hip_qscale record, the 32-byte device record of kt_hip_quant_linear), 12-trit
+ * weight codes, per-tensor dynamic requant after every op. With kt_hip_quant_linear for every projection they run
+ * DecoderModel::decode_step (model.rs:290-294, 338-353) with no host round trip. Each call is one launch on
+ * `stream`; output records may not alias input records of the same call except where noted.
+ * ------------------------------------------------------------------------------------------------------------- */
+/* A signed Scale: sign * mant * 2^-shift (sign +1 or -1). The RoPE tables' entries (attention.rs:58-60) and the KV
+ * cache's per-step scales (sign +1). */
+typedef struct {
+    int64_t mant;
+    int32_t shift;
+    int32_t sign;
+} kt_hip_sscale;
+/* A CodeLut's run-time constants (kt-int/src/lib.rs:346-396): the index factor inv_step as a Scale, lo_index,
+ * the entry count n, the code scale, the identity right tail. Its n codes (i64) live in device memory. */
+typedef struct {
+    int64_t inv_mant;
+    int32_t inv_shift;
+    int32_t n;
+    int64_t lo_index;
+    int64_t code_mant;
+    int32_t code_shift;
+    int32_t right_identity;
+} kt_hip_codelut;
+#define KT_LUT_EXP 0  /* exp(x): the softmax table of Attention::new and MoeMlp::new */
+#define KT_LUT_SILU 1 /* x / (1 + exp(-x)): SwiGluMlp::new's SiLU */
+#define KT_REF_MAX_HEADS 64
+#define KT_REF_ATTN_LDS 65536 /* the attention step's LDS: 40 B per cached position + 12 B per q value + 8 KB */
+
+/* Offline tables (host only, no GPU; f64 with the C library's exp/pow/cos/sin, as the reference's f64 methods use
+ * its platform's): Scale::from_f64 (lib.rs:215-222); CodeLut::build (lib.rs:359-379) of `kind` over [lo, hi] at
+ * 2^idx_bits entries and 2^code_bits code scale (codes may be NULL: constants only); the RoPE tables of
+ * Attention::new / rope_tables (attention.rs:64-90): entry p * rot_dim/2 + j is the signed Scale of
+ * cos / sin(p * theta^(-2j/rot_dim)). */
+void kt_hip_ref_scale_from_f64(double x, int64_t* mant, int32_t* shift);
+int kt_hip_ref_codelut(int kind, double lo, double hi, int idx_bits, int code_bits, int right_identity,
+                       int64_t* codes, kt_hip_codelut* lut);
+int kt_hip_ref_rope_tables(int64_t max_seq, int64_t rot_dim, double theta, kt_hip_sscale* cos_tab,
+                           kt_hip_sscale* sin_tab);
+
+/* Embedding::lookup (layers.rs:1127-1140): y (dim codes) and ys = the row of the token at token_dev[0] of the
+ * vocab x dim code table at Scale (e_mant, e_shift); a token outside [0, vocab) gives zeros at Scale::ZERO. */
+int kt_hip_ref_embed(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_shift, const int32_t* token_dev,
+                     int64_t vocab, int64_t dim, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+/* RmsNorm::forward_int (layers.rs:392-434) of rows (<= 64) x dim codes at xs: gamma codes g_dev at (g_mant,
+ * g_shift), eps as the Scale (eps_mant, eps_shift). */
+int kt_hip_ref_rmsnorm(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t rows, int64_t dim,
+                       const int32_t* g_dev, int64_t g_mant, int32_t g_shift, int64_t eps_mant, int32_t eps_shift,
+                       int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+/* add (layers.rs:121-136), the residual add of n codes: y_dev may alias a_dev or b_dev, ys_dev as_dev or bs_dev. */
+int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
+                   const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+/* SwiGluMlp::forward_int's activation (layers.rs:615-637): h = requant_dyn(silu_code(g) * u) of n values, the SiLU
+ * CodeLut (right_identity set) with its codes at silu_codes_dev. */
+int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
+                      const kt_hip_qscale* us_dev, int64_t n, const int64_t* silu_codes_dev,
+                      const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream);
+/* Attention::decode_step between its projections (attention.rs:358-458) at the position pos_dev[0]: RoPE of the q
+ * (nh x hd) and k (nkv x hd) codes by the tables cos_dev / sin_dev (max_seq x hd/2), the rotated k and the v codes
+ * appended at row pos of kc_dev / vc_dev (max_seq x nkv hd) with their scales at kscale_dev / vscale_dev[pos], the
+ * integer-code softmax over rows 0..pos at a common score scale (1/sqrt(hd) as (isq_mant, isq_shift); the exp
+ * CodeLut), and the heads brought to one scale: o_dev (nh hd codes) and os_dev, the o projection's input. Rows
+ * 0..pos-1 are those of earlier calls. A position outside [0, max_seq) gives zeros. nh <= KT_REF_MAX_HEADS, nh a
+ * multiple of nkv, hd even, LDS (KT_REF_ATTN_LDS) bounds max_seq. */
+int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev, const int32_t* k_dev,
+                              const kt_hip_qscale* ks_dev, const int32_t* v_dev, const kt_hip_qscale* vs_dev,
+                              const int32_t* pos_dev, int64_t nh, int64_t nkv, int64_t hd, int64_t max_seq,
+                              int32_t* kc_dev, int32_t* vc_dev, kt_hip_sscale* kscale_dev, kt_hip_sscale* vscale_dev,
+                              const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev, int64_t isq_mant,
+                              int32_t isq_shift, const int64_t* exp_codes_dev, const kt_hip_codelut* exp_lut,
+                              int32_t* o_dev, kt_hip_qscale* os_dev, void* stream);
+/* argmax_codes (generate.rs:48-56): token_dev[0] = the first index of the largest of n codes. With record_dev
+ * non-null the codes are copied to record_dev + step * n and (mant, shift) of ls_dev to rscale_dev[step], step =
+ * step_dev[0], which then advances (the per-step logits hash_step covers, generate.rs:58-64). */
+int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hip_qscale* ls_dev, int32_t* token_dev,
+                      int32_t* record_dev, kt_hip_sscale* rscale_dev, int32_t* step_dev, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Backend layer: one LinearBackend on one device (kt_cuda::open, lib.rs:252; TcLinear, backend.rs:77-192).
  * ------------------------------------------------------------------------------------------------------------- */
 typedef struct kt_hip_backend kt_hip_backend;

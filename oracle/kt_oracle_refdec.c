@@ -1,0 +1,645 @@
+/*
+ * kt_oracle_refdec.c -- TEST INFRASTRUCTURE ONLY (the CPU oracle; never part of the product). Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
+ *
+ * A C restatement of the reference's integer decoder engine, at the reference's own semantics: 12-trit weight codes
+ * (|w| <= WLEVELS) with per-tensor Scales, activations as i32 codes at the 2^28 level quantized dynamically per
+ * tensor, every op composed with kt-int's integer Scale arithmetic (restated in kt_oracle.c). Paths are relative to
+ * the tritify repository root.
+ *
+ *   model build (offline, f64): QuantLinear::from_weights, RmsNorm::new, Embedding::from_weights
+ *     (crates/01-engine/kt-core/src/layers.rs:212-232, 380-390, 1110-1125), Attention::new's RoPE tables, 1/sqrt(hd)
+ *     and exp CodeLut (attention.rs:64-140), SwiGluMlp::new's SiLU CodeLut (layers.rs:591-601),
+ *     CodeLut::build / index / code_at (crates/00-kernels/kt-int/src/lib.rs:346-396);
+ *   run time (integers only): RmsNorm::forward_int (layers.rs:392-434), add (layers.rs:121-136),
+ *     QuantLinear::forward_int (kt_oracle.c, layers.rs:275-328), Attention::rope_int (attention.rs:222-246),
+ *     Attention::decode_step (attention.rs:340-459), SwiGluMlp::forward_int (layers.rs:609-640),
+ *     DecoderModel::decode_step (model.rs:290-294, 338-353), generate_greedy_by / argmax_codes / hash_step
+ *     (generate.rs:48-111) and repro::run's per-position logits_hash (crates/04-ingest/kt-convert/src/repro.rs:
+ *     34-42, 60-84);
+ *   the seeded model of repro::synthetic_model (repro.rs:260-300).
+ *
+ * Pinning: verify_repro --synthetic (seed 7, prompt [3,14,15,9,26,5,35,8,9,7,9,3], 32 greedy tokens) prints
+ * logits_hash 8109ebad0a2883838a9d133351ce421f676e8d66dbcaffc5cde000272b748d03 (REPRODUCE.md:17); the same run here
+ * must give it (tests/test_refdec.py), which pins every function below through the whole decoder. The offline tables
+ * call the C library's exp / pow / cos / sin, as the reference's f64 methods call the platform libm.
+ *
+ * Built with -ffp-contract=off: no float expression is contracted into a fused multiply-add.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "kt_oracle.h"
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+#define WLEVELS 265720LL
+#define ACT_LEVELS (1LL << 28)
+
+/* kt-int restated in kt_oracle.c */
+kt_scale kt_scale_from_f64(double x);
+int kt_scale_ge(kt_scale a, kt_scale o);
+kt_scale kt_scale_mul(kt_scale a, kt_scale o);
+int64_t kt_scale_apply(kt_scale a, int64_t value);
+kt_scale kt_scale_recip(kt_scale a);
+kt_scale kt_scale_add(kt_scale a, kt_scale o);
+kt_scale kt_scale_rsqrt(kt_scale a);
+int32_t kt_requant_dyn(int64_t v, int64_t num_level, int64_t den);
+void kt_quant_linear_forward(const int32_t* x, size_t rows, size_t in, kt_scale xs, const int32_t* w, size_t out,
+                             kt_scale ws, const int64_t* bias, kt_scale bs, size_t threads, int32_t* y, kt_scale* os,
+                             int64_t* xmax_out, int64_t* ymax_out);
+size_t kt_sha256_ctx_size(void);
+void kt_sha256_init(void* c);
+void kt_sha256_update(void* c, const void* data, size_t n);
+void kt_sha256_final(void* c, uint8_t out[32]);
+
+static const kt_scale ZERO = {0, 0};
+
+static kt_scale ratio(u128 num, u128 den) {
+    return kt_scale_from_ratio((uint64_t)(num >> 64), (uint64_t)num, (uint64_t)(den >> 64), (uint64_t)den);
+}
+/* The engine's "largest scale" fold, |a, b| if b.ge(a) { b } else { a } from Scale::ZERO: of equal values the last
+ * one wins. */
+static kt_scale fold_max(kt_scale a, kt_scale b) { return kt_scale_ge(b, a) ? b : a; }
+static int64_t abs_w(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64_t)v) : v; } /* i64::abs, release build */
+static int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+static int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* CodeLut (kt-int/src/lib.rs:346-396)                                                                          */
+/* ------------------------------------------------------------------------------------------------------------ */
+typedef struct {
+    int64_t* codes;
+    size_t n;
+    kt_scale inv_step_scale;
+    int64_t lo_index;
+    kt_scale code_scale;
+    int right_identity;
+} rd_lut;
+
+enum { LUT_EXP = 0, LUT_SILU = 1 };
+
+static double lut_f(int kind, double x) { return kind == LUT_EXP ? exp(x) : x / (1.0 + exp(-x)); }
+
+static void lut_build(rd_lut* L, int kind, double lo, double hi, unsigned idx_bits, unsigned code_bits, int right_id) {
+    const size_t n = (size_t)1 << idx_bits;
+    const double k = (double)(1ULL << code_bits);
+    L->codes = (int64_t*)malloc(n * sizeof(int64_t));
+    for (size_t i = 0; i < n; i++) {
+        const double x = lo + (hi - lo) * ((double)i / (double)(n - 1));
+        L->codes[i] = (int64_t)round(lut_f(kind, x) * k);
+    }
+    const double inv_step = (double)(n - 1) / (hi - lo);
+    L->inv_step_scale = kt_scale_from_f64(inv_step);
+    L->lo_index = (int64_t)round(lo * inv_step);
+    L->n = n;
+    L->code_scale = kt_scale_from_f64(1.0 / k);
+    L->right_identity = right_id;
+}
+
+/* CodeLut::index: round((data * scale - lo) * inv_step) with the build-time constants. */
+static int64_t lut_index(const rd_lut* L, int64_t data, kt_scale scale) {
+    return kt_scale_apply(kt_scale_mul(scale, L->inv_step_scale), data) - L->lo_index;
+}
+static int64_t lut_code_at(const rd_lut* L, int64_t idx) {
+    if (idx < 0) idx = 0;
+    if (idx > (int64_t)L->n - 1) idx = (int64_t)L->n - 1;
+    return L->codes[idx];
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* The model                                                                                                    */
+/* ------------------------------------------------------------------------------------------------------------ */
+typedef struct {
+    int32_t* w;
+    kt_scale s;
+    size_t out, in;
+} rd_ql;
+typedef struct {
+    int32_t* w;
+    kt_scale s, eps;
+    size_t dim;
+} rd_norm;
+typedef struct {
+    rd_norm in_norm, post_norm;
+    rd_ql wq, wk, wv, wo, gate, up, down;
+} rd_layer;
+
+typedef struct {
+    size_t dim, layers, nh, nkv, hd, hidden, vocab, max_seq;
+    double eps, theta;
+    int32_t* emb;
+    kt_scale emb_scale;
+    rd_layer* L;
+    rd_norm final_norm;
+    rd_ql lm_head;
+    kt_scale *cos_mag, *sin_mag; /* max_seq x hd/2 */
+    int8_t *cos_sign, *sin_sign;
+    kt_scale inv_sqrt;
+    rd_lut exp_code, silu;
+} kt_refdec;
+
+/* One step's KV cache of one layer (LayerKv, attention.rs:251-265): post-RoPE k codes and v codes, each step with
+ * its own Scale. */
+typedef struct {
+    int32_t *k, *v;
+    kt_scale *ks, *vs;
+    size_t steps, kstride, cap;
+} rd_cache;
+
+/* An IntTensor: codes and one Scale. */
+typedef struct {
+    int32_t* d;
+    size_t n;
+    kt_scale s;
+} rd_t;
+
+static rd_t t_new(size_t n) {
+    rd_t t = {(int32_t*)calloc(n ? n : 1, sizeof(int32_t)), n, {0, 0}};
+    return t;
+}
+static void t_free(rd_t* t) {
+    free(t->d);
+    t->d = NULL;
+}
+
+/* QuantLinear::from_weights / RmsNorm::new / Embedding::from_weights: codes = clamp(round(w / step)), step =
+ * peak / WLEVELS, scale = Scale::from_f64(step) (layers.rs:212-232, 380-390, 1110-1125). */
+static kt_scale quant_weights(const float* w, size_t n, int32_t* codes) {
+    double peak = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        const double a = fabs((double)w[i]);
+        peak = a > peak ? a : peak;
+    }
+    if (peak == 0.0) {
+        memset(codes, 0, n * sizeof(int32_t));
+        return ZERO;
+    }
+    const double step = peak / (double)WLEVELS;
+    for (size_t i = 0; i < n; i++) {
+        int64_t c = (int64_t)round((double)w[i] / step);
+        codes[i] = (int32_t)(c < -WLEVELS ? -WLEVELS : c > WLEVELS ? WLEVELS : c);
+    }
+    return kt_scale_from_f64(step);
+}
+
+static void ql_build(rd_ql* q, const float* w, size_t out, size_t in) {
+    q->w = (int32_t*)malloc(out * in * sizeof(int32_t));
+    q->s = quant_weights(w, out * in, q->w);
+    q->out = out, q->in = in;
+}
+static void norm_build(rd_norm* nm, const float* w, size_t dim, double eps) {
+    nm->w = (int32_t*)malloc(dim * sizeof(int32_t));
+    nm->s = quant_weights(w, dim, nm->w);
+    nm->eps = kt_scale_from_f64(eps);
+    nm->dim = dim;
+}
+
+/* Attention::new's tables (attention.rs:64-90, 100-140): per (position p, pair j < hd/2) the angle
+ * p * theta^(-2j/hd) as signed Scales of its cosine and sine; 1/sqrt(hd); the exp CodeLut over [-30, 0]. SwiGLU's
+ * SiLU CodeLut over [-30, 30] with the identity right tail (layers.rs:599). */
+static void tables_build(kt_refdec* M) {
+    const size_t half = M->hd / 2, n = M->max_seq * half;
+    M->cos_mag = (kt_scale*)malloc(n * sizeof(kt_scale));
+    M->sin_mag = (kt_scale*)malloc(n * sizeof(kt_scale));
+    M->cos_sign = (int8_t*)malloc(n);
+    M->sin_sign = (int8_t*)malloc(n);
+    for (size_t p = 0; p < M->max_seq; p++)
+        for (size_t j = 0; j < half; j++) {
+            const double inv_freq = pow(M->theta, -(2.0 * (double)j) / (double)M->hd);
+            const double ang = (double)p * inv_freq;
+            const double c = cos(ang), s = sin(ang);
+            const size_t idx = p * half + j;
+            M->cos_mag[idx] = kt_scale_from_f64(fabs(c));
+            M->cos_sign[idx] = c < 0.0 ? -1 : 1;
+            M->sin_mag[idx] = kt_scale_from_f64(fabs(s));
+            M->sin_sign[idx] = s < 0.0 ? -1 : 1;
+        }
+    M->inv_sqrt = kt_scale_from_f64(1.0 / sqrt((double)M->hd));
+    lut_build(&M->exp_code, LUT_EXP, -30.0, 0.0, 16, 20, 0);
+    lut_build(&M->silu, LUT_SILU, -30.0, 30.0, 16, 20, 1);
+}
+
+/* repro::synthetic_model (repro.rs:260-300): weights uniform in [-1, 1) from the LCG, ((s >> 40) / 2^24) * 2 - 1 as
+ * f32, drawn per layer in the field order of LayerWeights, then the embedding, the final norm and the lm_head. */
+kt_refdec* kt_rd_synthetic(uint64_t seed, size_t dim, size_t layers, size_t nh, size_t nkv, size_t hd, size_t hidden,
+                           size_t vocab, double eps, double theta, size_t max_seq) {
+    kt_refdec* M = (kt_refdec*)calloc(1, sizeof(kt_refdec));
+    M->dim = dim, M->layers = layers, M->nh = nh, M->nkv = nkv, M->hd = hd, M->hidden = hidden, M->vocab = vocab;
+    M->eps = eps, M->theta = theta, M->max_seq = max_seq;
+    const size_t qd = nh * hd, kvd = nkv * hd;
+    size_t big = vocab * dim;
+    const size_t cand[4] = {qd * dim, hidden * dim, dim * hidden, kvd * dim};
+    for (int i = 0; i < 4; i++) big = cand[i] > big ? cand[i] : big;
+    float* buf = (float*)malloc(big * sizeof(float));
+    uint64_t s = seed;
+#define DRAW(n)                                                                                     \
+    for (size_t i_ = 0; i_ < (n); i_++) {                                                           \
+        s = s * 6364136223846793005ULL + 1442695040888963407ULL;                                    \
+        buf[i_] = (float)((double)(s >> 40) / (double)(1ULL << 24) * 2.0 - 1.0);                    \
+    }
+    M->L = (rd_layer*)calloc(layers, sizeof(rd_layer));
+    for (size_t l = 0; l < layers; l++) {
+        rd_layer* L = &M->L[l];
+        DRAW(dim);
+        norm_build(&L->in_norm, buf, dim, eps);
+        DRAW(qd * dim);
+        ql_build(&L->wq, buf, qd, dim);
+        DRAW(kvd * dim);
+        ql_build(&L->wk, buf, kvd, dim);
+        DRAW(kvd * dim);
+        ql_build(&L->wv, buf, kvd, dim);
+        DRAW(dim * qd);
+        ql_build(&L->wo, buf, dim, qd);
+        DRAW(dim);
+        norm_build(&L->post_norm, buf, dim, eps);
+        DRAW(hidden * dim);
+        ql_build(&L->gate, buf, hidden, dim);
+        DRAW(hidden * dim);
+        ql_build(&L->up, buf, hidden, dim);
+        DRAW(dim * hidden);
+        ql_build(&L->down, buf, dim, hidden);
+    }
+    DRAW(vocab * dim);
+    M->emb = (int32_t*)malloc(vocab * dim * sizeof(int32_t));
+    M->emb_scale = quant_weights(buf, vocab * dim, M->emb);
+    DRAW(dim);
+    norm_build(&M->final_norm, buf, dim, eps);
+    DRAW(vocab * dim);
+    ql_build(&M->lm_head, buf, vocab, dim);
+#undef DRAW
+    free(buf);
+    tables_build(M);
+    return M;
+}
+
+static void ql_free(rd_ql* q) { free(q->w); }
+void kt_rd_free(kt_refdec* M) {
+    if (!M) return;
+    for (size_t l = 0; l < M->layers; l++) {
+        rd_layer* L = &M->L[l];
+        free(L->in_norm.w), free(L->post_norm.w);
+        ql_free(&L->wq), ql_free(&L->wk), ql_free(&L->wv), ql_free(&L->wo);
+        ql_free(&L->gate), ql_free(&L->up), ql_free(&L->down);
+    }
+    free(M->L);
+    free(M->emb);
+    free(M->final_norm.w);
+    ql_free(&M->lm_head);
+    free(M->cos_mag), free(M->sin_mag), free(M->cos_sign), free(M->sin_sign);
+    free(M->exp_code.codes), free(M->silu.codes);
+    free(M);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* The run-time ops (integers only)                                                                             */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+/* requant_dyn of v[0..n) to ACT_LEVELS by its largest magnitude, the engine's closing step of every op: zeros at
+ * Scale::ZERO when that is 0, else codes at from_ratio(gmax, ACT_LEVELS) * c. */
+static void close_dyn(const int64_t* v, size_t n, kt_scale c, rd_t* y) {
+    int64_t gmax = 0;
+    for (size_t i = 0; i < n; i++) {
+        const int64_t a = abs_w(v[i]);
+        gmax = a > gmax ? a : gmax;
+    }
+    if (gmax == 0) {
+        memset(y->d, 0, n * sizeof(int32_t));
+        y->s = ZERO;
+        return;
+    }
+    for (size_t i = 0; i < n; i++) y->d[i] = kt_requant_dyn(v[i], ACT_LEVELS, gmax);
+    y->s = kt_scale_mul(ratio((u128)gmax, ACT_LEVELS), c);
+}
+
+/* RmsNorm::forward_int (layers.rs:392-434) over rows of dim. */
+void kt_rd_rmsnorm(const int32_t* x, size_t rows, size_t dim, kt_scale xs, const int32_t* g, kt_scale gs,
+                   kt_scale eps, int32_t* y, kt_scale* ys) {
+    const size_t n = rows * dim;
+    int64_t* p = (int64_t*)malloc(n * sizeof(int64_t) + 8);
+    kt_scale* c_rows = (kt_scale*)malloc(rows * sizeof(kt_scale) + 8);
+    for (size_t r = 0; r < rows; r++) {
+        const int32_t* xr = x + r * dim;
+        u128 ss = 0;
+        for (size_t i = 0; i < dim; i++) ss += (u128)((i128)xr[i] * (i128)xr[i]);
+        const kt_scale mean_sq = kt_scale_mul(kt_scale_mul(ratio(ss, dim), xs), xs);
+        const kt_scale denom = kt_scale_add(mean_sq, eps);
+        const kt_scale inv = denom.mant == 0 ? ZERO : kt_scale_rsqrt(denom);
+        c_rows[r] = kt_scale_mul(kt_scale_mul(xs, inv), gs);
+        for (size_t i = 0; i < dim; i++) p[r * dim + i] = (int64_t)xr[i] * (int64_t)g[i];
+    }
+    kt_scale cc = ZERO;
+    for (size_t r = 0; r < rows; r++) cc = fold_max(cc, c_rows[r]);
+    rd_t out = {y, n, ZERO};
+    if (cc.mant == 0) {
+        memset(y, 0, n * sizeof(int32_t));
+    } else {
+        const kt_scale cinv = kt_scale_recip(cc);
+        for (size_t r = 0; r < rows; r++) {
+            const kt_scale f = kt_scale_mul(c_rows[r], cinv);
+            for (size_t i = 0; i < dim; i++) p[r * dim + i] = kt_scale_apply(f, p[r * dim + i]);
+        }
+        close_dyn(p, n, cc, &out);
+    }
+    *ys = out.s;
+    free(p), free(c_rows);
+}
+
+/* add (layers.rs:121-136): both tensors to the larger scale, summed, requantized dynamically. */
+void kt_rd_add(const int32_t* a, kt_scale as, const int32_t* b, kt_scale bs, size_t n, int32_t* y, kt_scale* ys) {
+    const kt_scale common = kt_scale_ge(as, bs) ? as : bs;
+    rd_t out = {y, n, ZERO};
+    if (common.mant == 0) {
+        memset(y, 0, n * sizeof(int32_t));
+    } else {
+        const kt_scale cinv = kt_scale_recip(common), fa = kt_scale_mul(as, cinv), fb = kt_scale_mul(bs, cinv);
+        int64_t* sum = (int64_t*)malloc(n * sizeof(int64_t) + 8);
+        for (size_t i = 0; i < n; i++) sum[i] = wadd(kt_scale_apply(fa, a[i]), kt_scale_apply(fb, b[i]));
+        close_dyn(sum, n, common, &out);
+        free(sum);
+    }
+    *ys = out.s;
+}
+
+static void ql(const rd_ql* q, const rd_t* x, rd_t* y) {
+    int64_t xm, ym;
+    kt_quant_linear_forward(x->d, x->n / q->in, q->in, x->s, q->w, q->out, q->s, NULL, ZERO, 1, y->d, &y->s, &xm,
+                            &ym);
+}
+
+/* The SwiGLU activation between the gate/up and down products (SwiGluMlp::forward_int, layers.rs:615-637):
+ * h = silu_code(g) * u with the CodeLut's index, its clamp and its identity right tail, then requant_dyn at
+ * code_scale * u.scale. */
+void kt_rd_swiglu_act(const void* model, const int32_t* g, kt_scale gs, const int32_t* u, kt_scale us, size_t n,
+                      int32_t* h, kt_scale* hs) {
+    const rd_lut* L = &((const kt_refdec*)model)->silu;
+    const kt_scale id_factor = kt_scale_mul(gs, kt_scale_recip(L->code_scale));
+    int64_t* hv = (int64_t*)malloc(n * sizeof(int64_t) + 8);
+    for (size_t k = 0; k < n; k++) {
+        const int64_t gd = g[k], idx = lut_index(L, gd, gs);
+        const int64_t code = idx < 0 ? 0 : idx >= (int64_t)L->n ? kt_scale_apply(id_factor, gd) : lut_code_at(L, idx);
+        hv[k] = wmul(code, u[k]);
+    }
+    rd_t out = {h, n, ZERO};
+    close_dyn(hv, n, kt_scale_mul(L->code_scale, us), &out);
+    *hs = out.s;
+    free(hv);
+}
+
+/* Attention::rope_int (attention.rs:222-246): rotate_half pairs (j, j + hd/2) by the signed cos/sin Scales of
+ * position p. */
+static void rope(const kt_refdec* M, int32_t* v, size_t p) {
+    const size_t half = M->hd / 2;
+    for (size_t j = 0; j < half; j++) {
+        const size_t idx = p * half + j;
+        const int64_t cs = M->cos_sign[idx], ss = M->sin_sign[idx];
+        const kt_scale cm = M->cos_mag[idx], sm = M->sin_mag[idx];
+        const int64_t a = v[j], b = v[j + half];
+        v[j] = (int32_t)(cs * kt_scale_apply(cm, a) - ss * kt_scale_apply(sm, b));
+        v[j + half] = (int32_t)(cs * kt_scale_apply(cm, b) + ss * kt_scale_apply(sm, a));
+    }
+}
+
+/* The core of Attention::decode_step (attention.rs:358-458) after the q/k/v projections: RoPE at pos, append k and
+ * v with their scales, the integer-code softmax per head over every cached step at a common score scale, the
+ * heads brought to a common scale and requantized. Returns the concatenated head outputs (the wo input). */
+void kt_rd_attention_core(const void* model, void* cache, const int32_t* q, kt_scale qs, const int32_t* k,
+                          kt_scale ks, const int32_t* v, kt_scale vs, size_t pos, int32_t* o, kt_scale* os) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    rd_cache* C = (rd_cache*)cache;
+    const size_t hd = M->hd, nh = M->nh, nkv = M->nkv, group = nh / nkv, qstride = nh * hd, kstride = nkv * hd;
+    int32_t* qd = (int32_t*)malloc(qstride * sizeof(int32_t));
+    memcpy(qd, q, qstride * sizeof(int32_t));
+    for (size_t h = 0; h < nh; h++) rope(M, qd + h * hd, pos);
+    int32_t* kd = C->k + C->steps * kstride;
+    memcpy(kd, k, kstride * sizeof(int32_t));
+    for (size_t h = 0; h < nkv; h++) rope(M, kd + h * hd, pos);
+    memcpy(C->v + C->steps * kstride, v, kstride * sizeof(int32_t));
+    C->ks[C->steps] = ks;
+    C->vs[C->steps] = vs;
+    const size_t steps = ++C->steps;
+
+    kt_scale v_ref = ZERO;
+    for (size_t j = 0; j < steps; j++) v_ref = fold_max(v_ref, C->vs[j]);
+    kt_scale* vf = (kt_scale*)malloc(steps * sizeof(kt_scale));
+    if (v_ref.mant == 0) {
+        for (size_t j = 0; j < steps; j++) vf[j] = ZERO;
+    } else {
+        const kt_scale vinv = kt_scale_recip(v_ref);
+        for (size_t j = 0; j < steps; j++) vf[j] = kt_scale_mul(C->vs[j], vinv);
+    }
+    int64_t* head_out = (int64_t*)calloc(qstride, sizeof(int64_t));
+    kt_scale* scale_h = (kt_scale*)calloc(nh, sizeof(kt_scale));
+    int64_t *dots = (int64_t*)malloc(steps * 8), *score = (int64_t*)malloc(steps * 8), *ec = (int64_t*)malloc(steps * 8);
+    kt_scale* sj = (kt_scale*)malloc(steps * sizeof(kt_scale));
+    for (size_t h = 0; h < nh; h++) {
+        const size_t kv = h / group;
+        for (size_t j = 0; j < steps; j++) {
+            const int32_t* kr = C->k + j * kstride + kv * hd;
+            int64_t dot = 0;
+            for (size_t d = 0; d < hd; d++) dot = wadd(dot, wmul(qd[h * hd + d], kr[d]));
+            dots[j] = dot;
+            sj[j] = kt_scale_mul(kt_scale_mul(qs, C->ks[j]), M->inv_sqrt);
+        }
+        kt_scale s_ref = ZERO;
+        for (size_t j = 0; j < steps; j++) s_ref = fold_max(s_ref, sj[j]);
+        if (s_ref.mant == 0) continue;
+        const kt_scale sref_inv = kt_scale_recip(s_ref);
+        int64_t dmax = INT64_MIN;
+        for (size_t j = 0; j < steps; j++) {
+            score[j] = kt_scale_apply(kt_scale_mul(sj[j], sref_inv), dots[j]);
+            if (score[j] > dmax) dmax = score[j];
+        }
+        int64_t sumc = 0;
+        for (size_t j = 0; j < steps; j++) {
+            const int64_t idx = lut_index(&M->exp_code, score[j] - dmax, s_ref);
+            ec[j] = idx < 0 ? 0 : lut_code_at(&M->exp_code, idx);
+            sumc += ec[j];
+        }
+        if (sumc <= 0) continue;
+        for (size_t d = 0; d < hd; d++) {
+            int64_t acc = 0;
+            for (size_t j = 0; j < steps; j++)
+                acc = wadd(acc, wmul(ec[j], kt_scale_apply(vf[j], C->v[j * kstride + kv * hd + d])));
+            head_out[h * hd + d] = acc;
+        }
+        scale_h[h] = kt_scale_mul(v_ref, ratio(1, (u128)sumc));
+    }
+    kt_scale common = ZERO;
+    for (size_t h = 0; h < nh; h++) common = fold_max(common, scale_h[h]);
+    rd_t out = {o, qstride, ZERO};
+    if (common.mant == 0) {
+        memset(o, 0, qstride * sizeof(int32_t));
+    } else {
+        const kt_scale cinv = kt_scale_recip(common);
+        for (size_t h = 0; h < nh; h++) {
+            const kt_scale f = kt_scale_mul(scale_h[h], cinv);
+            for (size_t d = 0; d < hd; d++) head_out[h * hd + d] = kt_scale_apply(f, head_out[h * hd + d]);
+        }
+        close_dyn(head_out, qstride, common, &out);
+    }
+    *os = out.s;
+    free(qd), free(vf), free(head_out), free(scale_h), free(dots), free(score), free(ec), free(sj);
+}
+
+void* kt_rd_cache_new(const void* model) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    rd_cache* C = (rd_cache*)calloc(1, sizeof(rd_cache));
+    C->kstride = M->nkv * M->hd;
+    C->cap = M->max_seq;
+    C->k = (int32_t*)calloc(C->cap * C->kstride, sizeof(int32_t));
+    C->v = (int32_t*)calloc(C->cap * C->kstride, sizeof(int32_t));
+    C->ks = (kt_scale*)calloc(C->cap, sizeof(kt_scale));
+    C->vs = (kt_scale*)calloc(C->cap, sizeof(kt_scale));
+    return C;
+}
+void kt_rd_cache_free(void* cache) {
+    rd_cache* C = (rd_cache*)cache;
+    if (!C) return;
+    free(C->k), free(C->v), free(C->ks), free(C->vs), free(C);
+}
+
+/* DecoderModel::decode_step (model.rs:290-294, 338-353) of one token at position pos: embed, every block
+ * (input_norm -> attention decode step -> add; post_norm -> SwiGLU -> add), final norm, lm_head. caches: one per
+ * layer. logits: vocab codes, *ls their Scale. */
+void kt_rd_decode_step(const void* model, void** caches, int64_t token, size_t pos, int32_t* logits, kt_scale* ls) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    const size_t dim = M->dim, qd = M->nh * M->hd, kvd = M->nkv * M->hd, hid = M->hidden;
+    rd_t x = t_new(dim), h = t_new(dim), a = t_new(dim), q = t_new(qd), k = t_new(kvd), v = t_new(kvd);
+    rd_t cat = t_new(qd), g = t_new(hid), u = t_new(hid), hh = t_new(hid), m = t_new(dim), x2 = t_new(dim);
+    memcpy(x.d, M->emb + (size_t)token * dim, dim * sizeof(int32_t));
+    x.s = M->emb_scale;
+    for (size_t l = 0; l < M->layers; l++) {
+        const rd_layer* L = &M->L[l];
+        kt_rd_rmsnorm(x.d, 1, dim, x.s, L->in_norm.w, L->in_norm.s, L->in_norm.eps, h.d, &h.s);
+        ql(&L->wq, &h, &q);
+        ql(&L->wk, &h, &k);
+        ql(&L->wv, &h, &v);
+        kt_rd_attention_core(M, caches[l], q.d, q.s, k.d, k.s, v.d, v.s, pos, cat.d, &cat.s);
+        ql(&L->wo, &cat, &a);
+        kt_rd_add(x.d, x.s, a.d, a.s, dim, x2.d, &x2.s);
+        kt_rd_rmsnorm(x2.d, 1, dim, x2.s, L->post_norm.w, L->post_norm.s, L->post_norm.eps, h.d, &h.s);
+        ql(&L->gate, &h, &g);
+        ql(&L->up, &h, &u);
+        kt_rd_swiglu_act(M, g.d, g.s, u.d, u.s, hid, hh.d, &hh.s);
+        ql(&L->down, &hh, &m);
+        kt_rd_add(x2.d, x2.s, m.d, m.s, dim, x.d, &x.s);
+    }
+    kt_rd_rmsnorm(x.d, 1, dim, x.s, M->final_norm.w, M->final_norm.s, M->final_norm.eps, h.d, &h.s);
+    rd_t lg = {logits, M->vocab, ZERO};
+    ql(&M->lm_head, &h, &lg);
+    *ls = lg.s;
+    rd_t* all[] = {&x, &h, &a, &q, &k, &v, &cat, &g, &u, &hh, &m, &x2};
+    for (size_t i = 0; i < sizeof all / sizeof all[0]; i++) t_free(all[i]);
+}
+
+/* hash_step (generate.rs:58-64): the scale's mant (i64 LE) and shift (i32 LE), then every code (i32 LE). */
+static void hash_step(void* ctx, const int32_t* codes, size_t n, kt_scale s) {
+    kt_sha256_update(ctx, &s.mant, 8);
+    kt_sha256_update(ctx, &s.shift, 4);
+    kt_sha256_update(ctx, codes, n * sizeof(int32_t));
+}
+
+/* generate_greedy_by (generate.rs:82-111) with no stop ids, as repro::run drives it (repro.rs:60-84): the prompt
+ * position by position, then up to max_new greedy tokens (argmax_codes: the first maximum). tokens_out: max_new
+ * ids; run_hash: the Generation's logits_hash (every step that chose a token); pos_hashes (optional):
+ * P + max_new - 1 per-position logits_hash values (repro.rs:34-42), 32 bytes each. Returns 0, or -1 when the
+ * prompt is empty or the run needs more positions than the tables hold. */
+int kt_rd_generate(const void* model, const int32_t* prompt, size_t P, size_t max_new, int32_t* tokens_out,
+                   uint8_t run_hash[32], uint8_t* pos_hashes) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    if (P == 0 || P + (max_new ? max_new - 1 : 0) > M->max_seq) return -1;
+    void** caches = (void**)malloc(M->layers * sizeof(void*));
+    for (size_t l = 0; l < M->layers; l++) caches[l] = kt_rd_cache_new(M);
+    int32_t* logits = (int32_t*)malloc(M->vocab * sizeof(int32_t));
+    kt_scale ls = ZERO;
+    const size_t ctx_bytes = kt_sha256_ctx_size();
+    void* run = malloc(ctx_bytes);
+    void* one = malloc(ctx_bytes);
+    size_t npos = 0;
+#define STEP(tok, p)                                                          \
+    do {                                                                      \
+        kt_rd_decode_step(M, caches, (tok), (p), logits, &ls);                \
+        if (pos_hashes) {                                                     \
+            kt_sha256_init(one);                                              \
+            hash_step(one, logits, M->vocab, ls);                             \
+            kt_sha256_final(one, pos_hashes + 32 * npos);                     \
+        }                                                                     \
+        npos++;                                                               \
+    } while (0)
+    for (size_t p = 0; p < P; p++) STEP(prompt[p], p);
+    kt_sha256_init(run);
+    size_t pos = P, n = 0;
+    while (n < max_new) {
+        hash_step(run, logits, M->vocab, ls);
+        size_t best = 0;
+        for (size_t i = 1; i < M->vocab; i++)
+            if (logits[i] > logits[best]) best = i;
+        tokens_out[n++] = (int32_t)best;
+        if (n < max_new) {
+            STEP((int64_t)best, pos);
+            pos++;
+        }
+    }
+#undef STEP
+    kt_sha256_final(run, run_hash);
+    for (size_t l = 0; l < M->layers; l++) kt_rd_cache_free(caches[l]);
+    free(caches), free(logits), free(run), free(one);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* Accessors: the model's integers, for loading the same model on the device and for the table checks           */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+/* which: 0 wq, 1 wk, 2 wv, 3 wo, 4 gate, 5 up, 6 down, 7 lm_head (layer ignored). Copies out x in codes when
+ * codes is non-null; returns the scale and the shape. */
+kt_scale kt_rd_get_ql(const void* model, size_t layer, int which, int32_t* codes, size_t* out, size_t* in) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    const rd_ql* q = NULL;
+    if (which == 7) {
+        q = &M->lm_head;
+    } else {
+        const rd_layer* L = &M->L[layer];
+        const rd_ql* all[7] = {&L->wq, &L->wk, &L->wv, &L->wo, &L->gate, &L->up, &L->down};
+        q = all[which];
+    }
+    if (codes) memcpy(codes, q->w, q->out * q->in * sizeof(int32_t));
+    *out = q->out, *in = q->in;
+    return q->s;
+}
+/* which: 0 input_norm, 1 post_norm, 2 final_norm (layer ignored). */
+kt_scale kt_rd_get_norm(const void* model, size_t layer, int which, int32_t* codes, kt_scale* eps) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    const rd_norm* nm = which == 2 ? &M->final_norm : which == 0 ? &M->L[layer].in_norm : &M->L[layer].post_norm;
+    if (codes) memcpy(codes, nm->w, nm->dim * sizeof(int32_t));
+    *eps = nm->eps;
+    return nm->s;
+}
+kt_scale kt_rd_get_emb(const void* model, int32_t* codes) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    if (codes) memcpy(codes, M->emb, M->vocab * M->dim * sizeof(int32_t));
+    return M->emb_scale;
+}
+/* The run-time tables: which 0 exp, 1 silu -> codes (2^16 entries), inv_step scale, lo_index, code scale. */
+void kt_rd_get_lut(const void* model, int which, int64_t* codes, kt_scale* inv_step, int64_t* lo_index,
+                   kt_scale* code_scale) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    const rd_lut* L = which == 0 ? &M->exp_code : &M->silu;
+    if (codes) memcpy(codes, L->codes, L->n * sizeof(int64_t));
+    *inv_step = L->inv_step_scale, *lo_index = L->lo_index, *code_scale = L->code_scale;
+}
+/* RoPE tables: max_seq x hd/2 each of cos/sin magnitudes (mant, shift) and signs; and 1/sqrt(hd). */
+kt_scale kt_rd_get_rope(const void* model, int64_t* cos_mant, int32_t* cos_shift, int8_t* cos_sign,
+                        int64_t* sin_mant, int32_t* sin_shift, int8_t* sin_sign) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    const size_t n = M->max_seq * (M->hd / 2);
+    for (size_t i = 0; i < n; i++) {
+        cos_mant[i] = M->cos_mag[i].mant, cos_shift[i] = M->cos_mag[i].shift, cos_sign[i] = M->cos_sign[i];
+        sin_mant[i] = M->sin_mag[i].mant, sin_shift[i] = M->sin_mag[i].shift, sin_sign[i] = M->sin_sign[i];
+    }
+    return M->inv_sqrt;
+}

@@ -125,6 +125,21 @@ def _declare(L: C.CDLL) -> None:
         "kt_dec_generate": (C.c_int, [_P, _P, _SZ, _SZ, C.c_int, _P, _P, _SZ]),
         "kt_conv2d_i8w16": (None, [_P, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _SZ]),
         "kt_mlp_gelu": (C.c_int, [_P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ]),
+        "kt_rd_synthetic": (_P, [C.c_uint64, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_double, C.c_double, _SZ]),
+        "kt_rd_free": (None, [_P]),
+        "kt_rd_generate": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
+        "kt_rd_cache_new": (_P, [_P]),
+        "kt_rd_cache_free": (None, [_P]),
+        "kt_rd_decode_step": (None, [_P, _P, C.c_int64, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_rmsnorm": (None, [_P, _SZ, _SZ, Scale, _P, Scale, Scale, _P, C.POINTER(Scale)]),
+        "kt_rd_add": (None, [_P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_swiglu_act": (None, [_P, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_attention_core": (None, [_P, _P, _P, Scale, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_get_ql": (Scale, [_P, _SZ, C.c_int, _P, C.POINTER(_SZ), C.POINTER(_SZ)]),
+        "kt_rd_get_norm": (Scale, [_P, _SZ, C.c_int, _P, C.POINTER(Scale)]),
+        "kt_rd_get_emb": (Scale, [_P, _P]),
+        "kt_rd_get_lut": (None, [_P, C.c_int, _P, C.POINTER(Scale), C.POINTER(C.c_int64), C.POINTER(Scale)]),
+        "kt_rd_get_rope": (Scale, [_P, _P, _P, _P, _P, _P, _P]),
         "kt_moe_forward_token": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int,
                                         C.c_int, _P]),
     }
@@ -677,3 +692,139 @@ def dec_generate(shape: dict, arrays: dict, prompt, max_new: int, batched: bool 
     if r:
         raise ValueError("dec_generate: shape beyond the oracle's bounds")
     return toks, logits
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The reference decoder at its own semantics (kt_oracle_refdec.c): DecoderModel, RmsNorm, Attention::decode_step,
+# SwiGluMlp, add, generate_greedy_by and repro::run's hashes (crates/01-engine/kt-core/src/{model,layers,attention,
+# generate}.rs, crates/04-ingest/kt-convert/src/repro.rs)
+
+
+# repro::synthetic_model (repro.rs:260-300) and verify_repro --synthetic's input (verify_repro.rs:71-78)
+SYNTH_CFG = dict(dim=32, layers=2, nh=4, nkv=2, hd=8, hidden=64, vocab=64, eps=1e-6, theta=10000.0, max_seq=256)
+SYNTH_PROMPT = [3, 14, 15, 9, 26, 5, 35, 8, 9, 7, 9, 3]
+SYNTH_HASH = "8109ebad0a2883838a9d133351ce421f676e8d66dbcaffc5cde000272b748d03"  # REPRODUCE.md:17
+
+
+class RefModel:
+    """A DecoderModel built by the oracle from the seeded float weights of repro::synthetic_model's generator."""
+
+    def __init__(self, seed: int, cfg: dict = SYNTH_CFG):
+        self.cfg = dict(cfg)
+        c = self.cfg
+        self.ptr = lib().kt_rd_synthetic(seed, c["dim"], c["layers"], c["nh"], c["nkv"], c["hd"], c["hidden"],
+                                         c["vocab"], c["eps"], c["theta"], c["max_seq"])
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            lib().kt_rd_free(self.ptr)
+            self.ptr = None
+
+    def generate(self, prompt, max_new: int):
+        """(tokens, run logits_hash hex, per-position logits_hash hex list) of repro::run with no stop ids."""
+        p = _c(prompt, np.int32)
+        toks = np.zeros(max(max_new, 1), dtype=np.int32)
+        run = (C.c_uint8 * 32)()
+        npos = p.size + max(max_new - 1, 0)
+        ph = np.zeros(npos * 32, dtype=np.uint8)
+        if lib().kt_rd_generate(self.ptr, _ptr(p), p.size, max_new, _ptr(toks), run, _ptr(ph)):
+            raise ValueError("generate: empty prompt or past the position tables")
+        return toks[:max_new].tolist(), bytes(run).hex(), [bytes(ph[32 * i:32 * i + 32]).hex() for i in range(npos)]
+
+    def ql(self, layer: int, which: str):
+        """The (codes out x in, (mant, shift)) of a projection: wq wk wv wo gate up down, or lm_head."""
+        idx = {"wq": 0, "wk": 1, "wv": 2, "wo": 3, "gate": 4, "up": 5, "down": 6, "lm_head": 7}[which]
+        o, i = _SZ(), _SZ()
+        lib().kt_rd_get_ql(self.ptr, layer, idx, None, C.byref(o), C.byref(i))
+        codes = np.zeros(o.value * i.value, dtype=np.int32)
+        s = lib().kt_rd_get_ql(self.ptr, layer, idx, _ptr(codes), C.byref(o), C.byref(i))
+        return codes.reshape(o.value, i.value), (s.mant, s.shift)
+
+    def norm(self, layer: int, which: str):
+        """(gamma codes, (mant, shift), eps (mant, shift)) of in_norm / post_norm / final_norm."""
+        idx = {"in_norm": 0, "post_norm": 1, "final_norm": 2}[which]
+        codes = np.zeros(self.cfg["dim"], dtype=np.int32)
+        eps = Scale()
+        s = lib().kt_rd_get_norm(self.ptr, layer, idx, _ptr(codes), C.byref(eps))
+        return codes, (s.mant, s.shift), (eps.mant, eps.shift)
+
+    def emb(self):
+        codes = np.zeros(self.cfg["vocab"] * self.cfg["dim"], dtype=np.int32)
+        s = lib().kt_rd_get_emb(self.ptr, _ptr(codes))
+        return codes.reshape(self.cfg["vocab"], self.cfg["dim"]), (s.mant, s.shift)
+
+    def lut(self, which: str):
+        """(codes, inv_step (mant, shift), lo_index, code_scale (mant, shift)) of the exp or silu CodeLut."""
+        codes = np.zeros(1 << 16, dtype=np.int64)
+        inv, cs, lo = Scale(), Scale(), C.c_int64()
+        lib().kt_rd_get_lut(self.ptr, 0 if which == "exp" else 1, _ptr(codes), C.byref(inv), C.byref(lo),
+                            C.byref(cs))
+        return codes, (inv.mant, inv.shift), lo.value, (cs.mant, cs.shift)
+
+    def rope(self):
+        """(cos mant, cos shift, cos sign, sin mant, sin shift, sin sign), each max_seq x hd/2, and 1/sqrt(hd)."""
+        n = self.cfg["max_seq"] * (self.cfg["hd"] // 2)
+        a = [np.zeros(n, dtype=t) for t in (np.int64, np.int32, np.int8, np.int64, np.int32, np.int8)]
+        isq = lib().kt_rd_get_rope(self.ptr, *[_ptr(x) for x in a])
+        return a, (isq.mant, isq.shift)
+
+    def weights(self):
+        """The model as RefDecoder's constructor takes it: (emb, final_norm, lm_head, layers)."""
+        layers = []
+        for l in range(self.cfg["layers"]):
+            d = {n: self.norm(l, n)[:2] for n in ("in_norm", "post_norm")}
+            for n in ("wq", "wk", "wv", "wo", "gate", "up", "down"):
+                d[n] = self.ql(l, n)
+            layers.append(d)
+        return self.emb(), self.norm(0, "final_norm")[:2], self.ql(0, "lm_head"), layers
+
+
+class RefCache:
+    """One layer's LayerKv (attention.rs:251-265) in the oracle."""
+
+    def __init__(self, model: RefModel):
+        self.model = model
+        self.ptr = lib().kt_rd_cache_new(model.ptr)
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            lib().kt_rd_cache_free(self.ptr)
+            self.ptr = None
+
+
+def _sc(s) -> Scale:
+    return Scale(int(s[0]), int(s[1]))
+
+
+def rd_rmsnorm(x, rows: int, dim: int, xs, g, gs, eps):
+    """RmsNorm::forward_int (layers.rs:392-434): (codes, (mant, shift))."""
+    x, g = _c(x, np.int32), _c(g, np.int32)
+    y, ys = np.zeros(rows * dim, dtype=np.int32), Scale()
+    lib().kt_rd_rmsnorm(_ptr(x), rows, dim, _sc(xs), _ptr(g), _sc(gs), _sc(eps), _ptr(y), C.byref(ys))
+    return y, (ys.mant, ys.shift)
+
+
+def rd_add(a, as_, b, bs):
+    """add (layers.rs:121-136): (codes, (mant, shift))."""
+    a, b = _c(a, np.int32), _c(b, np.int32)
+    y, ys = np.zeros(a.size, dtype=np.int32), Scale()
+    lib().kt_rd_add(_ptr(a), _sc(as_), _ptr(b), _sc(bs), a.size, _ptr(y), C.byref(ys))
+    return y, (ys.mant, ys.shift)
+
+
+def rd_swiglu_act(model: RefModel, g, gs, u, us):
+    """SwiGluMlp::forward_int's activation with the model's SiLU CodeLut (layers.rs:615-637)."""
+    g, u = _c(g, np.int32), _c(u, np.int32)
+    h, hs = np.zeros(g.size, dtype=np.int32), Scale()
+    lib().kt_rd_swiglu_act(model.ptr, _ptr(g), _sc(gs), _ptr(u), _sc(us), g.size, _ptr(h), C.byref(hs))
+    return h, (hs.mant, hs.shift)
+
+
+def rd_attention_core(cache: RefCache, q, qs, k, ks, v, vs, pos: int):
+    """Attention::decode_step between its projections (attention.rs:358-458), appending to `cache`."""
+    q, k, v = _c(q, np.int32), _c(k, np.int32), _c(v, np.int32)
+    c = cache.model.cfg
+    o, os_ = np.zeros(c["nh"] * c["hd"], dtype=np.int32), Scale()
+    lib().kt_rd_attention_core(cache.model.ptr, cache.ptr, _ptr(q), _sc(qs), _ptr(k), _sc(ks), _ptr(v), _sc(vs), pos,
+                               _ptr(o), C.byref(os_))
+    return o, (os_.mant, os_.shift)

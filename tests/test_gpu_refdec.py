@@ -1,0 +1,211 @@
+"""The reference decoder at its own semantics on the GPU, through the C ABI, against the oracle
+(oracle/kt_oracle_refdec.c): every op on random inputs and scales (codes and Scale records bit for bit), the
+attention step over a growing cache, the reference's synthetic decoder reproducing verify_repro's golden
+8109ebad... at every position, and a Qwen2.5-shaped two-layer model against the oracle position by position."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def rec(torch, sc):
+    w = np.zeros(4, dtype=np.int64)
+    w[0] = sc[0]
+    w.view(np.int32)[2] = sc[1]
+    return torch.from_numpy(w).cuda()
+
+
+def rd(r):
+    w = r.cpu().numpy()
+    return int(w[0]), int(w.view(np.int32)[2])
+
+
+def dev_i32(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32).reshape(-1)).cuda()
+
+
+def rand_scale(rng):
+    return int(rng.integers(2**30, 2**31)), int(rng.integers(40, 62))
+
+
+@pytest.mark.parametrize("rows,dim,mag", [(1, 32, 2**28), (1, 896, 2**14), (1, 896, 2**28), (3, 200, 2**20),
+                                          (1, 5000, 2**27)])
+def test_ref_rmsnorm(torch_dev, rows, dim, mag):
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref_rmsnorm rows={rows} dim={dim} mag={mag}")
+    rng = np.random.default_rng(rows * 7 + dim)
+    x = rng.integers(-mag, mag, size=rows * dim).astype(np.int32)
+    g = rng.integers(-O.WLEVELS, O.WLEVELS + 1, size=dim).astype(np.int32)
+    if rows > 1:
+        x[dim:2 * dim] = 0  # a zero row among others
+    xs, gs, eps = rand_scale(rng), rand_scale(rng), B.ref_scale_from_f64(1e-6)
+    y, ys = torch.zeros(rows * dim, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_rmsnorm(dev_i32(torch, x), rec(torch, xs), rows, dim, dev_i32(torch, g), gs, eps, y, ys)
+    yo, so = O.rd_rmsnorm(x, rows, dim, xs, g, gs, eps)
+    assert np.array_equal(y.cpu().numpy(), yo) and rd(ys) == so
+    # a zero input scale gives zeros at Scale::ZERO
+    B.ref_rmsnorm(dev_i32(torch, x), rec(torch, (0, 0)), rows, dim, dev_i32(torch, g), gs, eps, y, ys)
+    assert not y.cpu().numpy().any() and rd(ys) == (0, 0)
+
+
+@pytest.mark.parametrize("n", [32, 896, 4864])
+def test_ref_add(torch_dev, n):
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref_add n={n}")
+    rng = np.random.default_rng(n)
+    for trial in range(4):
+        a = rng.integers(-(2**28), 2**28 + 1, size=n).astype(np.int32)
+        b = rng.integers(-(2**28), 2**28 + 1, size=n).astype(np.int32)
+        sa, sb = rand_scale(rng), rand_scale(rng)
+        if trial == 2:
+            sb = (0, 0)
+        if trial == 3:
+            b = -a
+            sb = sa  # cancels exactly: zeros at Scale::ZERO
+        yo, so = O.rd_add(a, sa, b, sb)
+        ad, ar = dev_i32(torch, a), rec(torch, sa)
+        B.ref_add(ad, ar, dev_i32(torch, b), rec(torch, sb), n, ad, ar)  # in place, as the residual add runs
+        assert np.array_equal(ad.cpu().numpy(), yo) and rd(ar) == so, trial
+
+
+@pytest.mark.parametrize("n,gshift", [(64, 53), (4864, 53), (4864, 60), (777, 48)])
+def test_ref_swiglu(torch_dev, n, gshift):
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref_swiglu n={n} gshift={gshift}")
+    model = O.RefModel(7)
+    rng = np.random.default_rng(n + gshift)
+    g = rng.integers(-(2**28), 2**28, size=n).astype(np.int32)
+    u = rng.integers(-(2**28), 2**28, size=n).astype(np.int32)
+    gs, us = (int(rng.integers(2**30, 2**31)), gshift), rand_scale(rng)
+    codes, lut = B.ref_codelut(B.LUT_SILU, -30.0, 30.0, 16, 20, True)
+    h, hs = torch.zeros(n, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_swiglu(dev_i32(torch, g), rec(torch, gs), dev_i32(torch, u), rec(torch, us), n,
+                 torch.from_numpy(codes).cuda(), lut, h, hs)
+    ho, so = O.rd_swiglu_act(model, g, gs, u, us)
+    assert np.array_equal(h.cpu().numpy(), ho) and rd(hs) == so
+
+
+def test_ref_embed_and_argmax(torch_dev):
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say("case: ref_embed / ref_argmax")
+    rng = np.random.default_rng(1)
+    vocab, dim = 50, 24
+    emb = rng.integers(-O.WLEVELS, O.WLEVELS + 1, size=vocab * dim).astype(np.int32)
+    ed = dev_i32(torch, emb)
+    y, ys = torch.zeros(dim, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    for t in (0, 17, 49, 50, -1):
+        B.ref_embed(ed, (1234567890, 50), dev_i32(torch, [t]), vocab, dim, y, ys)
+        if 0 <= t < vocab:
+            assert np.array_equal(y.cpu().numpy(), emb[t * dim:(t + 1) * dim]) and rd(ys) == (1234567890, 50)
+        else:
+            assert not y.cpu().numpy().any() and rd(ys) == (0, 0)
+    n = 151936
+    logits = rng.integers(-(2**28), 2**28, size=n).astype(np.int32)
+    logits[[5, 700, 150000]] = 2**28 + 7  # three equal maxima: the first wins
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    record = torch.zeros(2 * n, dtype=torch.int32, device="cuda")
+    rscale = torch.zeros(2 * 16, dtype=torch.uint8, device="cuda")
+    step = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ld = dev_i32(torch, logits)
+    for s in range(2):
+        B.ref_argmax(ld, n, rec(torch, (999, 9 + s)), tok, record, rscale, step)
+        assert int(tok.item()) == 5
+    assert int(step.item()) == 2
+    rs = rscale.cpu().numpy().view(B.SSCALE)
+    assert (rs["mant"] == 999).all() and rs["shift"].tolist() == [9, 10]
+    assert np.array_equal(record.cpu().numpy().reshape(2, n)[1], logits)
+
+
+@pytest.mark.parametrize("cfg", [dict(O.SYNTH_CFG, max_seq=48),
+                                 dict(dim=64, layers=1, nh=14, nkv=2, hd=64, hidden=64, vocab=8, eps=1e-6,
+                                      theta=1.0e6, max_seq=80)])
+def test_ref_attention_steps(torch_dev, cfg):
+    """Steps 0..max_seq-1 of Attention::decode_step's core on random q/k/v codes and scales (some steps with a zero k
+    or v scale), the device cache against the oracle's, output codes and scale at every step."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref_attention_steps nh={cfg['nh']} nkv={cfg['nkv']} hd={cfg['hd']} steps={cfg['max_seq']}")
+    model = O.RefModel(11, cfg)
+    cache = O.RefCache(model)
+    nh, nkv, hd, ms = cfg["nh"], cfg["nkv"], cfg["hd"], cfg["max_seq"]
+    qd, kvd = nh * hd, nkv * hd
+    cos_t, sin_t = B.ref_rope_tables(ms, hd, cfg["theta"])
+    cos_d, sin_d = (torch.from_numpy(t.view(np.uint8)).cuda() for t in (cos_t, sin_t))
+    exp_codes, exp_lut = B.ref_codelut(B.LUT_EXP, -30.0, 0.0, 16, 20, False)
+    exp_d = torch.from_numpy(exp_codes).cuda()
+    isq = B.ref_scale_from_f64(1.0 / np.sqrt(hd))
+    kc = torch.zeros(ms * kvd, dtype=torch.int32, device="cuda")
+    vc = torch.zeros(ms * kvd, dtype=torch.int32, device="cuda")
+    ks_d = torch.zeros(ms * 16, dtype=torch.uint8, device="cuda")
+    vs_d = torch.zeros(ms * 16, dtype=torch.uint8, device="cuda")
+    o, os_ = torch.zeros(qd, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    pos_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rng = np.random.default_rng(nh)
+    for p in range(ms):
+        q = rng.integers(-(2**28), 2**28, size=qd).astype(np.int32)
+        k = rng.integers(-(2**28), 2**28, size=kvd).astype(np.int32)
+        v = rng.integers(-(2**28), 2**28, size=kvd).astype(np.int32)
+        # scales spread over 2^6 so the softmax is neither flat nor one-hot
+        qs, ks, vs = (int(rng.integers(2**30, 2**31)), int(rng.integers(78, 84))), rand_scale(rng), rand_scale(rng)
+        if p % 7 == 3:
+            ks = (0, 0)
+        if p % 11 == 5:
+            vs = (0, 0)
+        pos_d.fill_(p)
+        B.ref_attention_step(dev_i32(torch, q), rec(torch, qs), dev_i32(torch, k), rec(torch, ks), dev_i32(torch, v),
+                             rec(torch, vs), pos_d, nh, nkv, hd, ms, kc, vc, ks_d, vs_d, cos_d, sin_d, isq, exp_d,
+                             exp_lut, o, os_)
+        oo, so = O.rd_attention_core(cache, q, qs, k, ks, v, vs, p)
+        got = o.cpu().numpy()
+        assert np.array_equal(got, oo), f"step {p}: {np.argwhere(got != oo)[:5].tolist()}"
+        assert rd(os_) == so, p
+
+
+def test_synthetic_decoder_reproduces_the_golden(torch_dev):
+    """verify_repro --synthetic on the device: RefDecoder over the seed-7 model gives logits_hash 8109ebad...
+    (REPRODUCE.md:17) and the oracle's hash at every position."""
+    from tritify_amd.refdecoder import RefDecoder
+
+    say("case: synthetic decoder seed 7, 12-token prompt, 32 greedy tokens")
+    model = O.RefModel(7)
+    toks_o, run_o, pos_o = model.generate(O.SYNTH_PROMPT, 32)
+    dec = RefDecoder(O.SYNTH_CFG, *model.weights())
+    toks, run, hashes = dec.generate_greedy(O.SYNTH_PROMPT, 32)
+    first = next((i for i, (a, b) in enumerate(zip(hashes, pos_o)) if a != b), None)
+    assert first is None, f"first differing position {first}"
+    assert toks == toks_o and run == run_o == O.SYNTH_HASH
+
+
+def test_qwen_shaped_decoder_against_the_oracle(torch_dev):
+    """Two layers of the Qwen2.5-0.5B shape (dim 896, 14 / 2 heads of 64, SwiGLU 4864, theta 1e6) with a short
+    vocabulary, seeded float weights quantized as the engine does: every position's logits hash equals the
+    oracle's."""
+    from tritify_amd.refdecoder import RefDecoder
+
+    cfg = dict(dim=896, layers=2, nh=14, nkv=2, hd=64, hidden=4864, vocab=512, eps=1e-6, theta=1.0e6, max_seq=64)
+    say("case: qwen-shaped reference decoder, 2 layers, 6-token prompt, 8 greedy tokens")
+    model = O.RefModel(5, cfg)
+    prompt = [1, 100, 200, 300, 400, 511]
+    toks_o, run_o, pos_o = model.generate(prompt, 8)
+    dec = RefDecoder(cfg, *model.weights())
+    toks, run, hashes = dec.generate_greedy(prompt, 8)
+    first = next((i for i, (a, b) in enumerate(zip(hashes, pos_o)) if a != b), None)
+    assert first is None, f"first differing position {first}"
+    assert toks == toks_o and run == run_o

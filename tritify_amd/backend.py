@@ -110,6 +110,16 @@ def _declare(L: C.CDLL) -> None:
                                      _SZ, _P, _P, _P]),
         "kt_hip_quant_linear_noalloc": (_I, [_I, _P, _I64, _I64, _P, _P, _I, _I64, _I64, C.c_int32, _P, _I64,
                                              C.c_int32, _P, _P, _P]),
+        "kt_hip_ref_scale_from_f64": (None, [C.c_double, C.POINTER(_I64), C.POINTER(C.c_int32)]),
+        "kt_hip_ref_codelut": (_I, [_I, C.c_double, C.c_double, _I, _I, _I, _P, _P]),
+        "kt_hip_ref_rope_tables": (_I, [_I64, _I64, C.c_double, _P, _P]),
+        "kt_hip_ref_embed": (_I, [_I, _P, _I64, C.c_int32, _P, _I64, _I64, _P, _P, _P]),
+        "kt_hip_ref_rmsnorm": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _P, _P]),
+        "kt_hip_ref_add": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P]),
+        "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_attention_step": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
+                                           _P, _P, _I64, C.c_int32, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P, _P, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
@@ -510,3 +520,85 @@ def gen_quant_rows_fast(seed: int, rows: int, cols: int) -> np.ndarray:
     out = np.empty(rows * cols, dtype=np.int32)
     lib().kt_hip_gen_quant_rows(seed & (2**64 - 1), rows, cols, out.ctypes.data)
     return out
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The reference decoder's layers at the reference's own semantics (crates/01-engine/kt-core/src/{layers,attention,
+# model,generate}.rs): i32 codes at the 2^28 level with one kt-int Scale per tensor, in 32-byte device records.
+# ---------------------------------------------------------------------------------------------------------------
+LUT_EXP, LUT_SILU = 0, 1
+REF_MAX_HEADS = 64
+
+
+class CodeLut(C.Structure):
+    """kt_hip_codelut: a CodeLut's run-time constants (kt-int/src/lib.rs:346-396)."""
+
+    _fields_ = [("inv_mant", C.c_int64), ("inv_shift", C.c_int32), ("n", C.c_int32), ("lo_index", C.c_int64),
+                ("code_mant", C.c_int64), ("code_shift", C.c_int32), ("right_identity", C.c_int32)]
+
+
+SSCALE = np.dtype([("mant", np.int64), ("shift", np.int32), ("sign", np.int32)])  # kt_hip_sscale
+
+
+def ref_scale_from_f64(x: float) -> tuple[int, int]:
+    """Scale::from_f64 (kt-int/src/lib.rs:215-222): (mant, shift) of a positive finite float, (0, 0) otherwise."""
+    m, s = C.c_int64(), C.c_int32()
+    lib().kt_hip_ref_scale_from_f64(float(x), C.byref(m), C.byref(s))
+    return int(m.value), int(s.value)
+
+
+def ref_codelut(kind: int, lo: float, hi: float, idx_bits: int, code_bits: int, right_identity: bool):
+    """CodeLut::build (kt-int/src/lib.rs:359-379) of exp (LUT_EXP) or SiLU (LUT_SILU): (codes i64, constants)."""
+    codes = np.zeros(1 << idx_bits, dtype=np.int64)
+    lut = CodeLut()
+    check(lib().kt_hip_ref_codelut(kind, lo, hi, idx_bits, code_bits, int(right_identity), codes.ctypes.data,
+                                   C.byref(lut)), "codelut")
+    return codes, lut
+
+
+def ref_rope_tables(max_seq: int, rot_dim: int, theta: float):
+    """The RoPE tables of Attention::new (attention.rs:64-90): (cos, sin) as max_seq x rot_dim/2 signed Scales."""
+    n = max_seq * (rot_dim // 2)
+    cos_t, sin_t = np.zeros(n, dtype=SSCALE), np.zeros(n, dtype=SSCALE)
+    check(lib().kt_hip_ref_rope_tables(max_seq, rot_dim, theta, cos_t.ctypes.data, sin_t.ctypes.data), "rope tables")
+    return cos_t, sin_t
+
+
+def ref_embed(emb_dev, e_scale, token_dev, vocab: int, dim: int, y_dev, ys_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_ref_embed(dev, _ptr(emb_dev), int(e_scale[0]), int(e_scale[1]), _ptr(token_dev), vocab, dim,
+                                 _ptr(y_dev), _ptr(ys_dev), _stream(stream)), "ref embed")
+
+
+def ref_rmsnorm(x_dev, xs_dev, rows: int, dim: int, g_dev, g_scale, eps_scale, y_dev, ys_dev, stream=None,
+                dev: int = 0) -> None:
+    check(lib().kt_hip_ref_rmsnorm(dev, _ptr(x_dev), _ptr(xs_dev), rows, dim, _ptr(g_dev), int(g_scale[0]),
+                                   int(g_scale[1]), int(eps_scale[0]), int(eps_scale[1]), _ptr(y_dev), _ptr(ys_dev),
+                                   _stream(stream)), "ref rmsnorm")
+
+
+def ref_add(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_ref_add(dev, _ptr(a_dev), _ptr(as_dev), _ptr(b_dev), _ptr(bs_dev), n, _ptr(y_dev),
+                               _ptr(ys_dev), _stream(stream)), "ref add")
+
+
+def ref_swiglu(g_dev, gs_dev, u_dev, us_dev, n: int, silu_codes_dev, silu: CodeLut, h_dev, hs_dev, stream=None,
+               dev: int = 0) -> None:
+    check(lib().kt_hip_ref_swiglu(dev, _ptr(g_dev), _ptr(gs_dev), _ptr(u_dev), _ptr(us_dev), n, _ptr(silu_codes_dev),
+                                  C.byref(silu), _ptr(h_dev), _ptr(hs_dev), _stream(stream)), "ref swiglu")
+
+
+def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh: int, nkv: int, hd: int,
+                       max_seq: int, kc_dev, vc_dev, kscale_dev, vscale_dev, cos_dev, sin_dev, inv_sqrt,
+                       exp_codes_dev, exp_lut: CodeLut, o_dev, os_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_ref_attention_step(dev, _ptr(q_dev), _ptr(qs_dev), _ptr(k_dev), _ptr(ks_dev), _ptr(v_dev),
+                                          _ptr(vs_dev), _ptr(pos_dev), nh, nkv, hd, max_seq, _ptr(kc_dev),
+                                          _ptr(vc_dev), _ptr(kscale_dev), _ptr(vscale_dev), _ptr(cos_dev),
+                                          _ptr(sin_dev), int(inv_sqrt[0]), int(inv_sqrt[1]), _ptr(exp_codes_dev),
+                                          C.byref(exp_lut), _ptr(o_dev), _ptr(os_dev), _stream(stream)),
+          "ref attention step")
+
+
+def ref_argmax(logits_dev, n: int, ls_dev, token_dev, record_dev=None, rscale_dev=None, step_dev=None, stream=None,
+               dev: int = 0) -> None:
+    check(lib().kt_hip_ref_argmax(dev, _ptr(logits_dev), n, _ptr(ls_dev), _ptr(token_dev), _ptr(record_dev),
+                                  _ptr(rscale_dev), _ptr(step_dev), _stream(stream)), "ref argmax")

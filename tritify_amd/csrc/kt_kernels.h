@@ -82,6 +82,21 @@ hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* 
 hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int F,
                                   const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift,
                                   int8_t* y, int ystride, hipStream_t s);
+struct RdAttn;
+size_t rd_attention_lds(int max_seq, int nh, int hd);
+hipError_t launch_rd_embed(const int32_t* emb, int64_t e_mant, int32_t e_shift, const int32_t* token, int vocab,
+                           int dim, int32_t* y, kt_hip_qscale* ys, hipStream_t s);
+hipError_t launch_rd_rmsnorm(const int32_t* x, int rows, int dim, const kt_hip_qscale* xs, const int32_t* g,
+                             int64_t g_mant, int32_t g_shift, int64_t e_mant, int32_t e_shift, int32_t* y,
+                             kt_hip_qscale* ys, hipStream_t s);
+hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_t* b, const kt_hip_qscale* bs, int n,
+                         int32_t* y, kt_hip_qscale* ys, hipStream_t s);
+hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
+                            int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h, kt_hip_qscale* hs,
+                            hipStream_t s);
+hipError_t launch_rd_attention_step(const RdAttn& a, hipStream_t s);
+hipError_t launch_rd_argmax(const int32_t* logits, int n, const kt_hip_qscale* ls, int32_t* token, int32_t* record,
+                            kt_hip_sscale* rscale, int32_t* step, hipStream_t s);
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s);
 
 }  // namespace kt

@@ -12,7 +12,8 @@
 //
 // No host synchronization: the maxima and the scales stay in the workspace, and the output scale is written to a
 // device record the next layer reads as its input scale. Integer arithmetic only, except a double-precision
-// quotient estimate in ql_requant and ql_quant that is corrected to the exact integer quotient before use.
+// quotient estimate in ql_requant and ql_quant that is corrected to the exact integer quotient before use (the
+// quotients are below 2^29, where the estimate is within one of the exact value).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -20,84 +21,17 @@
 #include <vector>
 
 #include "kt_kernels.h"
+#include "kt_scale_dev.h"
 #include "kt_w12_core.h"
 
 namespace kt {
 
 namespace {
 
-typedef unsigned __int128 u128;
-typedef __int128 i128;
-
 constexpr int64_t WLEVELS = 265720;       // (3^12 - 1) / 2, layers.rs:16
 constexpr int64_t ACT_LEVELS = 1LL << 28;  // layers.rs:18
 constexpr int QL_THREADS = 256;
 constexpr int64_t QL_FUSED_MAX = 8192;  // x of at most this many values: max |x| inside the quant pass
-
-struct Sc {
-    int64_t mant;
-    int32_t shift;
-};
-
-__device__ inline int bits_u128(u128 v) {
-    const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
-    return hi ? 128 - __clzll((long long)hi) : (lo ? 64 - __clzll((long long)lo) : 0);
-}
-
-// n / d for d > 0: native when both fit 64 bits, else restoring long division (used by one thread per call).
-__device__ u128 udiv128(u128 n, u128 d) {
-    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
-    u128 q = 0, r = 0;
-    for (int i = bits_u128(n) - 1; i >= 0; i--) {
-        r = (r << 1) | ((n >> i) & 1);
-        if (r >= d) r -= d, q |= (u128)1 << i;
-    }
-    return q;
-}
-
-// Scale::from_ratio (kt-int/src/lib.rs:191-212): a 31-bit-normalized mantissa of num / den, rounded.
-__device__ Sc from_ratio(u128 num, u128 den) {
-    if (num == 0) return Sc{0, 0};
-    while (bits_u128(num) > 64 || bits_u128(den) > 64) num >>= 1, den >>= 1;
-    if (den == 0) den = 1;
-    const int s = 31 - (bits_u128(num) - bits_u128(den));
-    u128 m;
-    if (s >= 0) {
-        m = udiv128((num << s) + den / 2, den);
-    } else {
-        const u128 dd = den << (-s);
-        m = udiv128(num + dd / 2, dd);
-    }
-    return Sc{(int64_t)m, s};
-}
-
-// Scale::mul (lib.rs:252-258)
-__device__ Sc sc_mul(Sc a, Sc b) {
-    if (a.mant == 0 || b.mant == 0) return Sc{0, 0};
-    Sc q = from_ratio((u128)(uint64_t)a.mant * (u128)(uint64_t)b.mant, 1);
-    q.shift += a.shift + b.shift;
-    return q;
-}
-
-// Scale::recip (lib.rs:275-280); a.mant > 0.
-__device__ Sc sc_recip(Sc a) {
-    const Sc r = from_ratio((u128)1 << 40, (u128)(uint64_t)a.mant);
-    return Sc{r.mant, r.shift - a.shift + 40};
-}
-
-// floor(n / d) for 0 <= n < 2^96, 0 < d < 2^63, with the quotient below 2^62: a double estimate (relative error
-// below 2^-50) corrected by the exact remainder.
-__device__ inline uint64_t udiv_est(u128 n, int64_t d) {
-    const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
-    double qd = dn / (double)d;
-    uint64_t q = qd <= 0.0 ? 0 : (qd >= 4.0e18 ? (uint64_t)4e18 : (uint64_t)qd);
-    i128 rem = (i128)n - (i128)q * (i128)d;
-#pragma unroll 1
-    for (int i = 0; i < 4 && rem < 0; i++) q--, rem += d;
-#pragma unroll 1
-    for (int i = 0; i < 4 && rem >= d; i++) q++, rem -= d;
-    return q;
-}
 
 // floor(n / d) for 0 <= n < 2^53 and 0 < d < 2^53 (both exact in a double): the correctly rounded double quotient is
 // the exact one or one above it at an integer boundary, which the remainder test corrects.
@@ -256,7 +190,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* _
         } else if (mode == 0 && ymax > 0) {
             const int64_t v = acc[i];
             const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
-            const uint64_t q = udiv_est(((u128)a << 28) + halfd, ymax);  // requant_dyn(v, 2^28, ymax)
+            const uint64_t q = udiv_small_q(((u128)a << 28) + halfd, ymax);  // requant_dyn(v, 2^28, ymax): q <= 2^28
             r = (int32_t)(v < 0 ? 0 - q : q);
         }
         y[i] = r;

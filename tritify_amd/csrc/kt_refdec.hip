@@ -1,0 +1,665 @@
+// The reference decoder's own layers on the device, at the reference's integer semantics: activations are i32 codes
+// at the 2^28 level with one kt-int Scale per tensor (a kt_hip_qscale record in device memory), every op closes
+// with requant_dyn to that level by its own largest magnitude, and scales compose with kt-int's integer Scale
+// arithmetic (kt_scale_dev.h). With kt_hip_quant_linear for every projection they run DecoderModel::decode_step
+// (crates/01-engine/kt-core/src/model.rs:290-294, 338-353) with no host round trip:
+//
+//   rd_embed           Embedding::lookup of a token read from device memory              (layers.rs:1127-1140)
+//   rd_rmsnorm         RmsNorm::forward_int                                                (layers.rs:392-434)
+//   rd_add             add, the residual add                                               (layers.rs:121-136)
+//   rd_swiglu          SwiGluMlp::forward_int between the gate/up and down products       (layers.rs:615-637)
+//   rd_attention_step  Attention::decode_step between the q/k/v and o products:           (attention.rs:358-458)
+//                      RoPE, the KV cache append with per-step scales, the integer-code
+//                      softmax at a common score scale, the heads brought to one scale
+//   rd_argmax          argmax_codes, the greedy choice, with an optional per-step record  (generate.rs:48-56)
+//
+// Each kernel is one CTA of 1024 threads (one token's tensors are at most a few thousand values); the Scale
+// arithmetic of a tensor runs in one thread, the per-element work in all of them. The offline tables
+// (CodeLut::build, the RoPE Scales, Scale::from_f64) are built on the host with the C library's f64 functions, as
+// the reference builds them with its platform's.
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "kt_kernels.h"
+#include "kt_scale_dev.h"
+
+namespace kt {
+
+namespace {
+
+constexpr int RD_THREADS = 1024;
+constexpr int RD_WAVES = RD_THREADS / 64;
+constexpr int RD_MAX_ROWS = 64;
+constexpr int64_t ACT_LEVELS = 1LL << 28;
+
+}  // namespace
+
+// The arguments of rd_attention_step_kernel (kt_hip_ref_attention_step).
+struct RdAttn {
+    const int32_t *q, *k, *v;
+    const kt_hip_qscale *qs, *ks, *vs;
+    const int32_t* pos;
+    int nh, nkv, hd, max_seq;
+    int32_t *kc, *vc;                  // [max_seq][nkv * hd]
+    kt_hip_sscale *kscale, *vscale;    // [max_seq]
+    const kt_hip_sscale *cos, *sin;    // [max_seq][hd / 2]
+    int64_t isq_mant;
+    int32_t isq_shift;
+    const int64_t* exp_codes;
+    kt_hip_codelut exp;
+    int32_t* o;
+    kt_hip_qscale* os;
+};
+
+namespace {
+
+__device__ inline Sc rec_sc(const kt_hip_qscale* r) { return Sc{r->mant, r->shift}; }
+__device__ inline void put_rec(kt_hip_qscale* r, Sc s) {
+    kt_hip_qscale o{};
+    o.mant = s.mant, o.shift = s.shift;
+    *r = o;
+}
+__device__ inline int64_t iabs(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64_t)v) : v; }
+__device__ inline int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+__device__ inline int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+
+// Block-wide reductions over the CTA's 1024 threads; every thread gets the result.
+__device__ int64_t block_max_i64(int64_t v, int64_t* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int64_t u = __shfl_xor(v, o, 64);
+        v = u > v ? u : v;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+    for (int w = 1; w < RD_WAVES; w++) v = red[w] > v ? red[w] : v;
+    __syncthreads();
+    return v;
+}
+__device__ int64_t block_sum_i64(int64_t v, int64_t* red) {  // wrapping
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = wadd(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+    for (int w = 1; w < RD_WAVES; w++) v = wadd(v, red[w]);
+    __syncthreads();
+    return v;
+}
+__device__ u128 block_sum_u128(u128 v, u128* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = RD_THREADS / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+        __syncthreads();
+    }
+    v = red[0];
+    __syncthreads();
+    return v;
+}
+
+// The engine's largest-scale fold (|a, b| if b.ge(a) { b } else { a } from Scale::ZERO, in sequence order) as a
+// parallel reduction: of equal values the one latest in the sequence wins, as in the fold. idx < 0: no element.
+struct ScIdx {
+    Sc s;
+    int idx;
+};
+__device__ inline ScIdx sc_pick(ScIdx a, ScIdx b) {
+    if (a.idx < 0) return b;
+    if (b.idx < 0) return a;
+    const bool ab = sc_ge(a.s, b.s), ba = sc_ge(b.s, a.s);
+    if (ab && ba) return a.idx > b.idx ? a : b;
+    return ba ? b : a;
+}
+__device__ ScIdx block_fold_max(ScIdx v, ScIdx* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = RD_THREADS / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = sc_pick(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    v = red[0];
+    __syncthreads();
+    return v;
+}
+
+// CodeLut::index / code_at (kt-int/src/lib.rs:382-395) with the call's factor m = scale * inv_step.
+__device__ inline int64_t lut_index(Sc m, int64_t data, int64_t lo_index) { return sc_apply(m, data) - lo_index; }
+__device__ inline int64_t lut_code(const int64_t* codes, int n, int64_t idx) {
+    return codes[idx < 0 ? 0 : (idx > n - 1 ? n - 1 : idx)];
+}
+
+}  // namespace
+
+// Embedding::lookup (layers.rs:1127-1140): y = the token's code row at the table's scale. A token outside
+// [0, vocab) gives zeros at Scale::ZERO (the reference panics there; a kernel must not read out of bounds).
+__global__ __launch_bounds__(RD_THREADS) void rd_embed_kernel(const int32_t* __restrict__ emb, int64_t e_mant,
+                                                              int32_t e_shift, const int32_t* __restrict__ token,
+                                                              int vocab, int dim, int32_t* __restrict__ y,
+                                                              kt_hip_qscale* __restrict__ ys) {
+    const int t = *token;
+    const bool ok = t >= 0 && t < vocab;
+    for (int i = threadIdx.x; i < dim; i += RD_THREADS) y[i] = ok ? emb[(size_t)t * dim + i] : 0;
+    if (threadIdx.x == 0) put_rec(ys, ok ? Sc{e_mant, e_shift} : Sc{0, 0});
+}
+
+// RmsNorm::forward_int (layers.rs:392-434) over `rows` rows of `dim`: per row the exact sum of squares, its
+// mean-square Scale plus eps, the integer inverse square root, the row factor c_r = xs * inv * gs; the products
+// x_i * g_i brought to the largest c_r and requantized by the largest magnitude.
+__global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* __restrict__ x, int rows, int dim,
+                                                                const kt_hip_qscale* __restrict__ xs_rec,
+                                                                const int32_t* __restrict__ g, int64_t g_mant,
+                                                                int32_t g_shift, int64_t e_mant, int32_t e_shift,
+                                                                int32_t* __restrict__ y,
+                                                                kt_hip_qscale* __restrict__ ys) {
+    __shared__ u128 red128[RD_THREADS];
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ Sc crow[RD_MAX_ROWS], frow[RD_MAX_ROWS];
+    __shared__ Sc cc_s;
+    const Sc xs = rec_sc(xs_rec), gs{g_mant, g_shift}, eps{e_mant, e_shift};
+    for (int r = 0; r < rows; r++) {
+        u128 ss = 0;
+        for (int i = threadIdx.x; i < dim; i += RD_THREADS) {
+            const int64_t v = x[(size_t)r * dim + i];
+            ss += (u128)(uint64_t)(v * v);
+        }
+        ss = block_sum_u128(ss, red128);
+        if (threadIdx.x == 0) {
+            const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xs), xs);
+            const Sc denom = sc_add(mean_sq, eps);
+            const Sc inv = denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom);
+            crow[r] = sc_mul(sc_mul(xs, inv), gs);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Sc cc{0, 0};
+        for (int r = 0; r < rows; r++) cc = sc_ge(crow[r], cc) ? crow[r] : cc;
+        if (cc.mant != 0) {
+            const Sc cinv = sc_recip(cc);
+            for (int r = 0; r < rows; r++) frow[r] = sc_mul(crow[r], cinv);
+        }
+        cc_s = cc;
+    }
+    __syncthreads();
+    const Sc cc = cc_s;
+    const int n = rows * dim;
+    int64_t m = 0;
+    if (cc.mant != 0)
+        for (int i = threadIdx.x; i < n; i += RD_THREADS) {
+            const int64_t v = sc_apply(frow[i / dim], (int64_t)x[i] * (int64_t)g[i % dim]);
+            m = iabs(v) > m ? iabs(v) : m;
+        }
+    const int64_t gmax = block_max_i64(m, red);
+    for (int i = threadIdx.x; i < n; i += RD_THREADS)
+        y[i] = gmax == 0 ? 0 : requant_dyn_dev(sc_apply(frow[i / dim], (int64_t)x[i] * (int64_t)g[i % dim]), gmax);
+    if (threadIdx.x == 0)
+        put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
+}
+
+// add (layers.rs:121-136): both to the larger scale, summed, requantized. y may alias a or b.
+__global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, const kt_hip_qscale* as_rec,
+                                                            const int32_t* b, const kt_hip_qscale* bs_rec, int n,
+                                                            int32_t* y, kt_hip_qscale* ys) {
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ Sc par[3];  // common, fa, fb
+    if (threadIdx.x == 0) {
+        const Sc as = rec_sc(as_rec), bs = rec_sc(bs_rec);
+        const Sc common = sc_ge(as, bs) ? as : bs;
+        par[0] = common;
+        if (common.mant != 0) {
+            const Sc cinv = sc_recip(common);
+            par[1] = sc_mul(as, cinv), par[2] = sc_mul(bs, cinv);
+        }
+    }
+    __syncthreads();
+    const Sc common = par[0], fa = par[1], fb = par[2];
+    int64_t m = 0;
+    if (common.mant != 0)
+        for (int i = threadIdx.x; i < n; i += RD_THREADS) {
+            const int64_t v = wadd(sc_apply(fa, a[i]), sc_apply(fb, b[i]));
+            m = iabs(v) > m ? iabs(v) : m;
+        }
+    const int64_t gmax = block_max_i64(m, red);  // every read of a, b, and their records, is done past here
+    for (int i = threadIdx.x; i < n; i += RD_THREADS)
+        y[i] = gmax == 0 ? 0 : requant_dyn_dev(wadd(sc_apply(fa, a[i]), sc_apply(fb, b[i])), gmax);
+    if (threadIdx.x == 0)
+        put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
+}
+
+// SwiGluMlp::forward_int's activation (layers.rs:615-637): h = silu_code(g) * u, the SiLU code from the CodeLut at
+// g's scale (0 below the table, the identity tail g * gs / code_scale above it), requantized at code_scale * us.
+__global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __restrict__ g,
+                                                               const kt_hip_qscale* __restrict__ gs_rec,
+                                                               const int32_t* __restrict__ u,
+                                                               const kt_hip_qscale* __restrict__ us_rec, int n,
+                                                               const int64_t* __restrict__ codes, kt_hip_codelut L,
+                                                               int32_t* __restrict__ h,
+                                                               kt_hip_qscale* __restrict__ hs) {
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ Sc par[3];  // index factor, identity factor, h scale
+    if (threadIdx.x == 0) {
+        const Sc gs = rec_sc(gs_rec), us = rec_sc(us_rec), cs{L.code_mant, L.code_shift};
+        par[0] = sc_mul(gs, Sc{L.inv_mant, L.inv_shift});
+        par[1] = sc_mul(gs, sc_recip(cs));
+        par[2] = sc_mul(cs, us);
+    }
+    __syncthreads();
+    const Sc mi = par[0], idf = par[1], hsc = par[2];
+    auto act = [&](int k) -> int64_t {
+        const int64_t gd = g[k], idx = lut_index(mi, gd, L.lo_index);
+        const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, gd) : lut_code(codes, L.n, idx));
+        return wmul(code, u[k]);
+    };
+    int64_t m = 0;
+    for (int k = threadIdx.x; k < n; k += RD_THREADS) m = iabs(act(k)) > m ? iabs(act(k)) : m;
+    const int64_t hmax = block_max_i64(m, red);
+    for (int k = threadIdx.x; k < n; k += RD_THREADS) h[k] = hmax == 0 ? 0 : requant_dyn_dev(act(k), hmax);
+    if (threadIdx.x == 0)
+        put_rec(hs, hmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)hmax, (u128)ACT_LEVELS), hsc));
+}
+
+// Attention::decode_step between its projections (attention.rs:358-458), at the position *pos:
+//  1. RoPE (rope_int, attention.rs:222-246) of every q head into LDS and every k head into the cache row pos; v
+//     into its cache row; this step's k and v scales into the per-step scale arrays;
+//  2. v_ref = the largest v scale over the steps 0..pos, vf_j = vs_j / v_ref; the score scales
+//     s_j = qs * ks_j * inv_sqrt, s_ref = the largest, f_j = s_j / s_ref;
+//  3. per head: score_j = f_j.apply(q . k_j), ec_j = exp_code(score_j - max score) at s_ref (0 below the table),
+//     sumc = sum ec_j, out_d = sum_j ec_j * vf_j.apply(v_jd), scale_h = v_ref / sumc;
+//  4. the heads brought to the largest scale_h and requantized: o and its record.
+// LDS: 40 bytes per position up to max_seq, 12 per q value, 8 per thread.
+__global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ ScIdx redsc[RD_THREADS];
+    __shared__ Sc par[4];  // v_ref, s_ref, lut factor, common
+    __shared__ Sc hsc[64];
+    const int tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv, group = nh / nkv;
+    const int kstride = nkv * hd, qstride = nh * hd;
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= a.max_seq) {  // outside the tables: zeros (the reference asserts here)
+        for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = 0;
+        if (tid == 0) put_rec(a.os, Sc{0, 0});
+        return;
+    }
+    const int steps = pos + 1;
+    Sc* F = reinterpret_cast<Sc*>(lds);  // score factors, per step
+    Sc* VF = F + a.max_seq;              // v factors, per step
+    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);  // scores, then exp codes, per step
+    int64_t* HO = S + a.max_seq;                                // head outputs, qstride
+    int64_t* PART = HO + qstride;                               // partial P.V sums, one per thread
+    int32_t* QD = reinterpret_cast<int32_t*>(PART + RD_THREADS);  // rotated q, qstride
+
+    // 1. RoPE and the cache append
+    auto rot = [&](const int32_t* src, int32_t* dst, int heads) {
+        for (int i = tid; i < heads * half; i += RD_THREADS) {
+            const int hh = i / half, j = i - hh * half;
+            const kt_hip_sscale c = a.cos[(size_t)pos * half + j], s = a.sin[(size_t)pos * half + j];
+            const int64_t av = src[hh * hd + j], bv = src[hh * hd + j + half];
+            const Sc cm{c.mant, c.shift}, sm{s.mant, s.shift};
+            dst[hh * hd + j] = (int32_t)(c.sign * sc_apply(cm, av) - s.sign * sc_apply(sm, bv));
+            dst[hh * hd + j + half] = (int32_t)(c.sign * sc_apply(cm, bv) + s.sign * sc_apply(sm, av));
+        }
+    };
+    rot(a.q, QD, nh);
+    rot(a.k, a.kc + (size_t)pos * kstride, nkv);
+    for (int i = tid; i < kstride; i += RD_THREADS) a.vc[(size_t)pos * kstride + i] = a.v[i];
+    const Sc qs = rec_sc(a.qs), isq{a.isq_mant, a.isq_shift};
+    if (tid == 0) {
+        a.kscale[pos] = kt_hip_sscale{a.ks->mant, a.ks->shift, 1};
+        a.vscale[pos] = kt_hip_sscale{a.vs->mant, a.vs->shift, 1};
+    }
+    __syncthreads();  // the cache row and both scales of this step are visible to the whole CTA past here
+
+    // 2. v_ref and s_ref
+    ScIdx bv{Sc{0, 0}, -1}, bs{Sc{0, 0}, -1};
+    for (int j = tid; j < steps; j += RD_THREADS) {
+        const Sc vj{a.vscale[j].mant, a.vscale[j].shift}, kj{a.kscale[j].mant, a.kscale[j].shift};
+        const Sc sj = sc_mul(sc_mul(qs, kj), isq);
+        F[j] = sj;
+        bv = sc_pick(bv, ScIdx{vj, j});
+        bs = sc_pick(bs, ScIdx{sj, j});
+    }
+    bv = block_fold_max(bv, redsc);
+    bs = block_fold_max(bs, redsc);
+    if (tid == 0) {
+        par[0] = bv.s, par[1] = bs.s;
+        par[2] = bs.s.mant ? sc_mul(bs.s, Sc{a.exp.inv_mant, a.exp.inv_shift}) : Sc{0, 0};
+    }
+    __syncthreads();
+    const Sc v_ref = par[0], s_ref = par[1], lm = par[2];
+    if (v_ref.mant != 0 || s_ref.mant != 0) {
+        __shared__ Sc inv2[2];
+        if (tid == 0) {
+            inv2[0] = v_ref.mant ? sc_recip(v_ref) : Sc{0, 0};
+            inv2[1] = s_ref.mant ? sc_recip(s_ref) : Sc{0, 0};
+        }
+        __syncthreads();
+        for (int j = tid; j < steps; j += RD_THREADS) {
+            VF[j] = v_ref.mant ? sc_mul(Sc{a.vscale[j].mant, a.vscale[j].shift}, inv2[0]) : Sc{0, 0};
+            if (s_ref.mant) F[j] = sc_mul(F[j], inv2[1]);
+        }
+    } else {
+        for (int j = tid; j < steps; j += RD_THREADS) VF[j] = Sc{0, 0};
+    }
+    __syncthreads();
+
+    // 3. the heads
+    const int chunks = RD_THREADS / hd, d = tid % hd, c = tid / hd;
+    for (int h = 0; h < nh; h++) {
+        const int kv = h / group;
+        if (s_ref.mant == 0) {  // every head skipped (the reference's `continue`)
+            for (int i = tid; i < hd; i += RD_THREADS) HO[h * hd + i] = 0;
+            if (tid == 0) hsc[h] = Sc{0, 0};
+            continue;
+        }
+        int64_t m = INT64_MIN;
+        for (int j = tid; j < steps; j += RD_THREADS) {
+            const int32_t* kr = a.kc + (size_t)j * kstride + kv * hd;
+            int64_t dot = 0;
+            for (int e = 0; e < hd; e++) dot = wadd(dot, wmul(QD[h * hd + e], kr[e]));
+            S[j] = sc_apply(F[j], dot);
+            m = S[j] > m ? S[j] : m;
+        }
+        const int64_t dmax = block_max_i64(m, red);
+        int64_t sum = 0;
+        for (int j = tid; j < steps; j += RD_THREADS) {
+            const int64_t idx = lut_index(lm, S[j] - dmax, a.exp.lo_index);
+            S[j] = idx < 0 ? 0 : lut_code(a.exp_codes, a.exp.n, idx);
+            sum += S[j];
+        }
+        const int64_t sumc = block_sum_i64(sum, red);  // also orders the S writes before the reads below
+        if (sumc <= 0) {
+            for (int i = tid; i < hd; i += RD_THREADS) HO[h * hd + i] = 0;
+            if (tid == 0) hsc[h] = Sc{0, 0};
+            continue;
+        }
+        int64_t acc = 0;
+        if (c < chunks)
+            for (int j = c; j < steps; j += chunks)
+                acc = wadd(acc, wmul(S[j], sc_apply(VF[j], a.vc[(size_t)j * kstride + kv * hd + d])));
+        PART[tid] = acc;
+        __syncthreads();
+        if (tid < hd) {
+            int64_t t = 0;
+            for (int cc = 0; cc < chunks; cc++) t = wadd(t, PART[cc * hd + tid]);
+            HO[h * hd + tid] = t;
+        }
+        if (tid == 0) hsc[h] = sc_mul(v_ref, from_ratio(1, (u128)(uint64_t)sumc));
+        __syncthreads();
+    }
+    __syncthreads();
+
+    // 4. one scale for the concatenated heads
+    if (tid == 0) {
+        Sc common{0, 0};
+        for (int h = 0; h < nh; h++) common = sc_ge(hsc[h], common) ? hsc[h] : common;
+        par[3] = common;
+        if (common.mant != 0) {
+            const Sc cinv = sc_recip(common);
+            for (int h = 0; h < nh; h++) hsc[h] = sc_mul(hsc[h], cinv);
+        }
+    }
+    __syncthreads();
+    const Sc common = par[3];
+    int64_t m = 0;
+    if (common.mant != 0)
+        for (int i = tid; i < qstride; i += RD_THREADS) {
+            HO[i] = sc_apply(hsc[i / hd], HO[i]);
+            m = iabs(HO[i]) > m ? iabs(HO[i]) : m;
+        }
+    const int64_t gmax = block_max_i64(m, red);
+    for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = gmax == 0 ? 0 : requant_dyn_dev(HO[i], gmax);
+    if (tid == 0)
+        put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
+}
+
+// argmax_codes (generate.rs:48-56): *token = the first index of the largest of n codes. With record non-null the
+// codes go to record + step * n and the scale to rscale[step], and *step advances (the per-step logits the
+// generation hash covers).
+__global__ __launch_bounds__(RD_THREADS) void rd_argmax_kernel(const int32_t* __restrict__ logits, int n,
+                                                               const kt_hip_qscale* __restrict__ ls,
+                                                               int32_t* __restrict__ token, int32_t* record,
+                                                               kt_hip_sscale* rscale, int32_t* step) {
+    __shared__ int64_t red[RD_WAVES];
+    // key: the value in the high word, the inverted index in the low word (the lower index wins a tie)
+    int64_t best = INT64_MIN;
+    for (int i = threadIdx.x; i < n; i += RD_THREADS) {
+        const int64_t key = (int64_t)logits[i] * 4294967296LL + (int64_t)(0x7FFFFFFF - i);
+        best = key > best ? key : best;
+    }
+    best = block_max_i64(best, red);
+    if (record) {
+        const int s = *step;
+        for (int i = threadIdx.x; i < n; i += RD_THREADS) record[(size_t)s * n + i] = logits[i];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            rscale[s] = kt_hip_sscale{ls->mant, ls->shift, 1};
+            *step = s + 1;
+        }
+    }
+    if (threadIdx.x == 0) *token = 0x7FFFFFFF - (int32_t)(uint32_t)(best & 0xFFFFFFFF);
+}
+
+size_t rd_attention_lds(int max_seq, int nh, int hd) {
+    return (size_t)max_seq * (2 * sizeof(Sc) + 8) + (size_t)nh * hd * (8 + 4) + RD_THREADS * 8;
+}
+
+hipError_t launch_rd_embed(const int32_t* emb, int64_t e_mant, int32_t e_shift, const int32_t* token, int vocab,
+                           int dim, int32_t* y, kt_hip_qscale* ys, hipStream_t s) {
+    rd_embed_kernel<<<1, RD_THREADS, 0, s>>>(emb, e_mant, e_shift, token, vocab, dim, y, ys);
+    return hipGetLastError();
+}
+hipError_t launch_rd_rmsnorm(const int32_t* x, int rows, int dim, const kt_hip_qscale* xs, const int32_t* g,
+                             int64_t g_mant, int32_t g_shift, int64_t e_mant, int32_t e_shift, int32_t* y,
+                             kt_hip_qscale* ys, hipStream_t s) {
+    if (rows < 1 || rows > RD_MAX_ROWS) return hipErrorInvalidValue;
+    rd_rmsnorm_kernel<<<1, RD_THREADS, 0, s>>>(x, rows, dim, xs, g, g_mant, g_shift, e_mant, e_shift, y, ys);
+    return hipGetLastError();
+}
+hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_t* b, const kt_hip_qscale* bs, int n,
+                         int32_t* y, kt_hip_qscale* ys, hipStream_t s) {
+    rd_add_kernel<<<1, RD_THREADS, 0, s>>>(a, as, b, bs, n, y, ys);
+    return hipGetLastError();
+}
+hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
+                            int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h, kt_hip_qscale* hs,
+                            hipStream_t s) {
+    rd_swiglu_kernel<<<1, RD_THREADS, 0, s>>>(g, gs, u, us, n, codes, *lut, h, hs);
+    return hipGetLastError();
+}
+hipError_t launch_rd_attention_step(const RdAttn& a, hipStream_t s) {
+    const size_t lds = rd_attention_lds(a.max_seq, a.nh, a.hd);
+    if (lds > KT_REF_ATTN_LDS) return hipErrorInvalidValue;
+    rd_attention_step_kernel<<<1, RD_THREADS, lds, s>>>(a);
+    return hipGetLastError();
+}
+hipError_t launch_rd_argmax(const int32_t* logits, int n, const kt_hip_qscale* ls, int32_t* token, int32_t* record,
+                            kt_hip_sscale* rscale, int32_t* step, hipStream_t s) {
+    rd_argmax_kernel<<<1, RD_THREADS, 0, s>>>(logits, n, ls, token, record, rscale, step);
+    return hipGetLastError();
+}
+
+}  // namespace kt
+
+
+// ---------------------------------------------------------------------------------------------------------------
+// C ABI (include/kt_hip.h): argument checks on the host, then one launch on `stream`.
+// ---------------------------------------------------------------------------------------------------------------
+#define RD_TRY(x)                               \
+    do {                                        \
+        const hipError_t e_ = (x);              \
+        if (e_ != hipSuccess) return (int)e_;   \
+    } while (0)
+
+static const int64_t RD_MAX_N = (int64_t)1 << 30;
+
+extern "C" int kt_hip_ref_embed(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_shift,
+                                const int32_t* token_dev, int64_t vocab, int64_t dim, int32_t* y_dev,
+                                kt_hip_qscale* ys_dev, void* stream) {
+    if (!emb_dev || !token_dev || !y_dev || !ys_dev || vocab < 1 || dim < 1 || vocab > INT32_MAX ||
+        vocab * dim > ((int64_t)1 << 40) || dim > RD_MAX_N || e_mant < 0)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_embed(emb_dev, e_mant, e_shift, token_dev, (int)vocab, (int)dim, y_dev, ys_dev,
+                                    (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_rmsnorm(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t rows,
+                                  int64_t dim, const int32_t* g_dev, int64_t g_mant, int32_t g_shift,
+                                  int64_t eps_mant, int32_t eps_shift, int32_t* y_dev, kt_hip_qscale* ys_dev,
+                                  void* stream) {
+    if (!x_dev || !xs_dev || !g_dev || !y_dev || !ys_dev || rows < 1 || dim < 1 || rows * dim > RD_MAX_N ||
+        g_mant < 0 || eps_mant < 0)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_rmsnorm(x_dev, (int)rows, (int)dim, xs_dev, g_dev, g_mant, g_shift, eps_mant, eps_shift,
+                                      y_dev, ys_dev, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
+                              const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev,
+                              void* stream) {
+    if (!a_dev || !as_dev || !b_dev || !bs_dev || !y_dev || !ys_dev || n < 1 || n > RD_MAX_N)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_add(a_dev, as_dev, b_dev, bs_dev, (int)n, y_dev, ys_dev, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
+                                 const kt_hip_qscale* us_dev, int64_t n, const int64_t* silu_codes_dev,
+                                 const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream) {
+    if (!g_dev || !gs_dev || !u_dev || !us_dev || !silu_codes_dev || !silu || !h_dev || !hs_dev || n < 1 ||
+        n > RD_MAX_N || silu->n < 1 || !silu->right_identity)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_swiglu(g_dev, gs_dev, u_dev, us_dev, (int)n, silu_codes_dev, silu, h_dev, hs_dev,
+                                     (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
+                                         const int32_t* k_dev, const kt_hip_qscale* ks_dev, const int32_t* v_dev,
+                                         const kt_hip_qscale* vs_dev, const int32_t* pos_dev, int64_t nh,
+                                         int64_t nkv, int64_t hd, int64_t max_seq, int32_t* kc_dev, int32_t* vc_dev,
+                                         kt_hip_sscale* kscale_dev, kt_hip_sscale* vscale_dev,
+                                         const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev,
+                                         int64_t isq_mant, int32_t isq_shift, const int64_t* exp_codes_dev,
+                                         const kt_hip_codelut* exp_lut, int32_t* o_dev, kt_hip_qscale* os_dev,
+                                         void* stream) {
+    if (!q_dev || !qs_dev || !k_dev || !ks_dev || !v_dev || !vs_dev || !pos_dev || !kc_dev || !vc_dev ||
+        !kscale_dev || !vscale_dev || !cos_dev || !sin_dev || !exp_codes_dev || !exp_lut || !o_dev || !os_dev)
+        return (int)hipErrorInvalidValue;
+    if (nh < 1 || nkv < 1 || nh % nkv || nh > KT_REF_MAX_HEADS || hd < 2 || (hd & 1) || hd > 1024 || max_seq < 1 ||
+        exp_lut->n < 1 || isq_mant < 0 || kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd) > KT_REF_ATTN_LDS)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    kt::RdAttn a{};
+    a.q = q_dev, a.k = k_dev, a.v = v_dev, a.qs = qs_dev, a.ks = ks_dev, a.vs = vs_dev, a.pos = pos_dev;
+    a.nh = (int)nh, a.nkv = (int)nkv, a.hd = (int)hd, a.max_seq = (int)max_seq;
+    a.kc = kc_dev, a.vc = vc_dev, a.kscale = kscale_dev, a.vscale = vscale_dev, a.cos = cos_dev, a.sin = sin_dev;
+    a.isq_mant = isq_mant, a.isq_shift = isq_shift, a.exp_codes = exp_codes_dev, a.exp = *exp_lut;
+    a.o = o_dev, a.os = os_dev;
+    return (int)kt::launch_rd_attention_step(a, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hip_qscale* ls_dev,
+                                 int32_t* token_dev, int32_t* record_dev, kt_hip_sscale* rscale_dev,
+                                 int32_t* step_dev, void* stream) {
+    if (!logits_dev || !ls_dev || !token_dev || n < 1 || n > INT32_MAX ||
+        (record_dev && (!rscale_dev || !step_dev)))
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_argmax(logits_dev, (int)n, ls_dev, token_dev, record_dev, rscale_dev, step_dev,
+                                     (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Offline tables (host, f64): Scale::from_f64, CodeLut::build, Attention::new's RoPE Scales. No float expression
+// here is contracted into a fused multiply-add, so each value is the one the reference's f64 arithmetic gives.
+// ---------------------------------------------------------------------------------------------------------------
+#pragma clang fp contract(off)
+
+// frexp (kt-int/src/lib.rs:46-60) by bit surgery; x > 0 finite.
+static double rd_frexp(double x, int* e) {
+    uint64_t bits;
+    memcpy(&bits, &x, 8);
+    const int ef = (int)((bits >> 52) & 0x7ff);
+    if (ef == 0) {
+        int e2;
+        const double m = rd_frexp(x * 9007199254740992.0, &e2);
+        *e = e2 - 53;
+        return m;
+    }
+    *e = ef - 1022;
+    const uint64_t mb = (bits & ~(0x7ffULL << 52)) | (1022ULL << 52);
+    double m;
+    memcpy(&m, &mb, 8);
+    return m;
+}
+
+extern "C" void kt_hip_ref_scale_from_f64(double x, int64_t* mant, int32_t* shift) {
+    *mant = 0, *shift = 0;
+    if (!(x > 0.0 && isfinite(x))) return;
+    int e;
+    const double m = rd_frexp(x, &e);
+    *mant = (int64_t)round(m * 2147483648.0);
+    *shift = 31 - e;
+}
+
+static double rd_lut_fn(int kind, double x) {
+    switch (kind) {
+        case KT_LUT_EXP:
+            return exp(x);
+        case KT_LUT_SILU:
+            return x / (1.0 + exp(-x));
+        default:
+            return 0.0;
+    }
+}
+
+extern "C" int kt_hip_ref_codelut(int kind, double lo, double hi, int idx_bits, int code_bits, int right_identity,
+                                  int64_t* codes, kt_hip_codelut* lut) {
+    if ((kind != KT_LUT_EXP && kind != KT_LUT_SILU) || idx_bits < 1 || idx_bits > 24 || code_bits < 0 ||
+        code_bits > 52 || !(hi > lo) || !lut)
+        return (int)hipErrorInvalidValue;
+    const int64_t n = (int64_t)1 << idx_bits;
+    const double k = (double)(1ULL << code_bits);
+    if (codes)
+        for (int64_t i = 0; i < n; i++) {
+            const double x = lo + (hi - lo) * ((double)i / (double)(n - 1));
+            codes[i] = (int64_t)round(rd_lut_fn(kind, x) * k);
+        }
+    const double inv_step = (double)(n - 1) / (hi - lo);
+    kt_hip_codelut L{};
+    kt_hip_ref_scale_from_f64(inv_step, &L.inv_mant, &L.inv_shift);
+    L.n = (int32_t)n;
+    L.lo_index = (int64_t)round(lo * inv_step);
+    kt_hip_ref_scale_from_f64(1.0 / k, &L.code_mant, &L.code_shift);
+    L.right_identity = right_identity;
+    *lut = L;
+    return 0;
+}
+
+extern "C" int kt_hip_ref_rope_tables(int64_t max_seq, int64_t rot_dim, double theta, kt_hip_sscale* cos_tab,
+                                      kt_hip_sscale* sin_tab) {
+    if (max_seq < 1 || rot_dim < 2 || (rot_dim & 1) || !cos_tab || !sin_tab) return (int)hipErrorInvalidValue;
+    const int64_t half = rot_dim / 2;
+    for (int64_t p = 0; p < max_seq; p++)
+        for (int64_t j = 0; j < half; j++) {
+            const double inv_freq = pow(theta, -(2.0 * (double)j) / (double)rot_dim);
+            const double ang = (double)p * inv_freq;
+            const double c = cos(ang), s = sin(ang);
+            kt_hip_sscale& C = cos_tab[p * half + j];
+            kt_hip_sscale& S = sin_tab[p * half + j];
+            kt_hip_ref_scale_from_f64(fabs(c), &C.mant, &C.shift);
+            kt_hip_ref_scale_from_f64(fabs(s), &S.mant, &S.shift);
+            C.sign = c < 0.0 ? -1 : 1;
+            S.sign = s < 0.0 ? -1 : 1;
+        }
+    return 0;
+}
+#pragma clang fp contract(on)

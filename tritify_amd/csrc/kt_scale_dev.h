@@ -1,0 +1,148 @@
+// kt-int's integer Scale (crates/00-kernels/kt-int/src/lib.rs:175-340) on the device, for the reference-semantics
+// layers: a non-negative scale mant * 2^-shift with a ~31-bit mantissa, composed with 128-bit integer arithmetic.
+// Every function gives the integers of its kt-int counterpart; these run in one thread per tensor (or per cached
+// step), never per element, except sc_apply and requant_dyn_dev.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kt {
+
+typedef unsigned __int128 u128;
+typedef __int128 i128;
+
+struct Sc {
+    int64_t mant;
+    int32_t shift;
+};
+
+__device__ inline int bits_u128(u128 v) {
+    const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
+    return hi ? 128 - __clzll((long long)hi) : (lo ? 64 - __clzll((long long)lo) : 0);
+}
+
+// n / d for d > 0: native when both fit 64 bits, else restoring long division.
+__device__ inline u128 udiv128(u128 n, u128 d) {
+    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
+    u128 q = 0, r = 0;
+    for (int i = bits_u128(n) - 1; i >= 0; i--) {
+        r = (r << 1) | ((n >> i) & 1);
+        if (r >= d) r -= d, q |= (u128)1 << i;
+    }
+    return q;
+}
+
+// Scale::from_ratio (lib.rs:191-212): a 31-bit-normalized mantissa of num / den, rounded.
+__device__ inline Sc from_ratio(u128 num, u128 den) {
+    if (num == 0) return Sc{0, 0};
+    while (bits_u128(num) > 64 || bits_u128(den) > 64) num >>= 1, den >>= 1;
+    if (den == 0) den = 1;
+    const int s = 31 - (bits_u128(num) - bits_u128(den));
+    u128 m;
+    if (s >= 0) {
+        m = udiv128((num << s) + den / 2, den);
+    } else {
+        const u128 dd = den << (-s);
+        m = udiv128(num + dd / 2, dd);
+    }
+    return Sc{(int64_t)m, s};
+}
+
+// Scale::mul (lib.rs:252-258)
+__device__ inline Sc sc_mul(Sc a, Sc b) {
+    if (a.mant == 0 || b.mant == 0) return Sc{0, 0};
+    Sc q = from_ratio((u128)(uint64_t)a.mant * (u128)(uint64_t)b.mant, 1);
+    q.shift += a.shift + b.shift;
+    return q;
+}
+
+// Scale::recip (lib.rs:275-280); a.mant > 0.
+__device__ inline Sc sc_recip(Sc a) {
+    const Sc r = from_ratio((u128)1 << 40, (u128)(uint64_t)a.mant);
+    return Sc{r.mant, r.shift - a.shift + 40};
+}
+
+// Scale::ge (lib.rs:227-248): a >= o by value.
+__device__ inline bool sc_ge(Sc a, Sc o) {
+    if (a.mant == 0) return o.mant == 0;
+    if (o.mant == 0) return true;
+    const u128 ma = (u128)(uint64_t)a.mant, mb = (u128)(uint64_t)o.mant;
+    const int d = o.shift - a.shift;
+    if (d >= 0) {
+        if (d + bits_u128(ma) > 127) return true;
+        return (ma << d) >= mb;
+    }
+    const int e = -d;
+    if (e + bits_u128(mb) > 127) return false;
+    return ma >= (mb << e);
+}
+
+// Scale::add (lib.rs:285-303)
+__device__ inline Sc sc_add(Sc a, Sc o) {
+    if (a.mant == 0) return o;
+    if (o.mant == 0) return a;
+    const int s = a.shift > o.shift ? a.shift : o.shift;
+    const int da = s - a.shift, db = s - o.shift;
+    if (da >= 96) return a;
+    if (db >= 96) return o;
+    const u128 sum = ((u128)(uint64_t)a.mant << da) + ((u128)(uint64_t)o.mant << db);
+    const Sc fr = from_ratio(sum, 1);
+    return Sc{fr.mant, fr.shift + s};
+}
+
+// isqrt_u128 (lib.rs:327-340): floor(sqrt(n)) by Newton's method from above.
+__device__ inline u128 isqrt_u128(u128 n) {
+    if (n == 0) return 0;
+    u128 x = (u128)1 << ((bits_u128(n) + 1) / 2);
+    for (;;) {
+        const u128 y = (x + udiv128(n, x)) >> 1;
+        if (y >= x) return x;
+        x = y;
+    }
+}
+
+// Scale::rsqrt (lib.rs:307-318); a.mant > 0.
+__device__ inline Sc sc_rsqrt(Sc a) {
+    u128 m = (u128)(uint64_t)a.mant;
+    int s = a.shift;
+    if (s & 1) m <<= 1, s += 1;
+    const u128 r = isqrt_u128(m << 62);
+    return sc_recip(Sc{(int64_t)r, 31 + s / 2});
+}
+
+// Scale::apply (lib.rs:261-272): round(value * a) half away from zero, i128 product, wrapped to i64.
+__device__ inline int64_t sc_apply(Sc a, int64_t value) {
+    if (a.mant == 0) return 0;
+    const i128 prod = (i128)value * (i128)a.mant;
+    if (a.shift <= 0) return (int64_t)(prod << (-a.shift));
+    const i128 half = (i128)1 << (a.shift - 1);
+    return (int64_t)(prod >= 0 ? (prod + half) >> a.shift : -(((-prod) + half) >> a.shift));
+}
+
+// floor(n / d) for 0 < d < 2^63 when the quotient is below 2^40: the double estimate's absolute error is then below
+// 2^40 * 2^-50 (three roundings of relative size 2^-53 each), so one correction step each way suffices; two are
+// allowed.
+__device__ inline uint64_t udiv_small_q(u128 n, int64_t d) {
+    const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
+    const double qd = dn / (double)d;
+    uint64_t q = qd <= 0.0 ? 0 : (uint64_t)qd;
+    i128 rem = (i128)n - (i128)q * (i128)d;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        if (rem < 0) q--, rem += d;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        if (rem >= d) q++, rem -= d;
+    return q;
+}
+
+// requant_dyn(v, 2^28, den) (crates/01-engine/kt-core/src/layers.rs:33-39) for |v| <= den: the quotient is at most
+// 2^28, within udiv_small_q's range.
+__device__ inline int32_t requant_dyn_dev(int64_t v, int64_t den) {
+    const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
+    const uint64_t q = udiv_small_q(((u128)a << 28) + (u128)(uint64_t)(den / 2), den);
+    return (int32_t)(v < 0 ? 0 - q : q);
+}
+
+}  // namespace kt

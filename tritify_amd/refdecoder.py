@@ -1,0 +1,177 @@
+"""The reference's decoder at its own integer semantics on one MI355X: the host-side mirror of DecoderModel
+(crates/01-engine/kt-core/src/model.rs) with every op of a decode step on the device.
+
+The reference runs its decoder on 12-trit weight codes with per-tensor kt-int Scales; activations are i32 codes at
+the 2^28 level, quantized dynamically per tensor after every op. `RefDecoder` keeps those integers exactly:
+
+  embed                       kt_hip_ref_embed               Embedding::lookup          (layers.rs:1127-1140)
+  input_norm / post_norm      kt_hip_ref_rmsnorm             RmsNorm::forward_int        (layers.rs:392-434)
+  wq, wk, wv, wo, gate, up,   kt_hip_quant_linear            QuantLinear::forward_int    (layers.rs:275-328)
+    down, lm_head             (digit-plane MFMA product)
+  attention core              kt_hip_ref_attention_step      Attention::decode_step      (attention.rs:340-459)
+  SiLU * up                   kt_hip_ref_swiglu              SwiGluMlp::forward_int      (layers.rs:609-640)
+  residual adds               kt_hip_ref_add                 add                         (layers.rs:121-136)
+  greedy choice               kt_hip_ref_argmax              argmax_codes                (generate.rs:48-56)
+
+The weights come in as the engine builds them (codes and Scales, `QuantLinear::from_weights` and its siblings);
+the run-time tables (RoPE Scales, the exp and SiLU CodeLuts, 1/sqrt(head_dim)) are built here from the
+configuration, as `Attention::new` and `SwiGluMlp::new` build them. `generate_greedy` follows generate_greedy_by
+(generate.rs:82-111) and repro::run (crates/04-ingest/kt-convert/src/repro.rs:60-84): the prompt position by
+position, then greedy tokens; every position's logits are hashed with the scale first (logits_hash, repro.rs:34-42)
+and the run's hash covers every step that chose a token (hash_step, generate.rs:58-64).
+
+torch holds the device buffers; it computes nothing.
+"""
+from __future__ import annotations
+
+import hashlib
+import math
+
+import numpy as np
+
+from . import backend as B
+from .quant import QuantLinear
+
+QL_NAMES = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+
+
+def logits_hash_bytes(codes: np.ndarray, scale) -> bytes:
+    """The bytes one step adds to the generation hash: mant (i64 LE), shift (i32 LE), every code (i32 LE)."""
+    return (np.int64(scale[0]).tobytes() + np.int32(scale[1]).tobytes() +
+            np.ascontiguousarray(codes, dtype="<i4").tobytes())
+
+
+class RefDecoder:
+    """DecoderModel { emb, blocks, final_norm, lm_head } resident on device `dev`.
+
+    cfg: dim, layers, nh, nkv, hd, hidden, vocab, eps, theta, max_seq (DecoderConfig, model.rs:17-29).
+    emb, lm_head: (codes vocab x dim, (mant, shift)); final_norm: (codes dim, (mant, shift)); layers: one dict per
+    block with in_norm, post_norm (codes dim, scale) and wq, wk, wv, wo, gate, up, down (codes out x in, scale).
+    """
+
+    def __init__(self, cfg: dict, emb, final_norm, lm_head, layers, dev: int = 0):
+        import torch
+
+        self.torch = torch
+        self.dev = dev
+        self.device = torch.device("cuda", dev)
+        c = {k: cfg[k] for k in ("dim", "layers", "nh", "nkv", "hd", "hidden", "vocab", "max_seq")}
+        self.dim, self.nl, self.nh, self.nkv, self.hd = c["dim"], c["layers"], c["nh"], c["nkv"], c["hd"]
+        self.hidden, self.vocab, self.max_seq = c["hidden"], c["vocab"], c["max_seq"]
+        if self.nh % self.nkv or self.hd % 2 or self.nh > B.REF_MAX_HEADS or len(layers) != self.nl:
+            raise ValueError("RefDecoder: heads, head_dim or layer count out of range")
+        dt = lambda a, t: torch.from_numpy(np.ascontiguousarray(a, dtype=t).reshape(-1)).to(self.device)  # noqa
+        self.eps = B.ref_scale_from_f64(cfg["eps"])
+        self.emb = dt(emb[0], np.int32)
+        self.emb_scale = tuple(emb[1])
+        self.final_norm = (dt(final_norm[0], np.int32), tuple(final_norm[1]))
+        qd, kvd = self.nh * self.hd, self.nkv * self.hd
+        shapes = {"wq": (qd, self.dim), "wk": (kvd, self.dim), "wv": (kvd, self.dim), "wo": (self.dim, qd),
+                  "gate": (self.hidden, self.dim), "up": (self.hidden, self.dim), "down": (self.dim, self.hidden)}
+        self.blocks = []
+        for i, lw in enumerate(layers):
+            blk = {n: (dt(lw[n][0], np.int32), tuple(lw[n][1])) for n in ("in_norm", "post_norm")}
+            for n in QL_NAMES:
+                out, inp = shapes[n]
+                blk[n] = QuantLinear(f"{n}{i}", lw[n][0], out, inp, lw[n][1], dev=dev)
+            self.blocks.append(blk)
+        self.lm_head = QuantLinear("lm_head", lm_head[0], self.vocab, self.dim, lm_head[1], dev=dev)
+        # the run-time tables of Attention::new and SwiGluMlp::new
+        cos_t, sin_t = B.ref_rope_tables(self.max_seq, self.hd, float(cfg["theta"]))
+        self.cos = torch.from_numpy(cos_t.view(np.uint8)).to(self.device)
+        self.sin = torch.from_numpy(sin_t.view(np.uint8)).to(self.device)
+        self.inv_sqrt = B.ref_scale_from_f64(1.0 / math.sqrt(self.hd))
+        exp_codes, self.exp_lut = B.ref_codelut(B.LUT_EXP, -30.0, 0.0, 16, 20, False)
+        silu_codes, self.silu_lut = B.ref_codelut(B.LUT_SILU, -30.0, 30.0, 16, 20, True)
+        self.exp_codes, self.silu_codes = dt(exp_codes, np.int64), dt(silu_codes, np.int64)
+        # one token's buffers and records
+        z = lambda n: torch.zeros(n, dtype=torch.int32, device=self.device)  # noqa
+        rec = lambda: torch.zeros(4, dtype=torch.int64, device=self.device)  # noqa
+        self.buf = {n: z(sz) for n, sz in (("x", self.dim), ("h", self.dim), ("a", self.dim), ("m", self.dim),
+                                           ("q", qd), ("k", kvd), ("v", kvd), ("cat", qd), ("g", self.hidden),
+                                           ("u", self.hidden), ("hh", self.hidden), ("logits", self.vocab))}
+        self.rec = {n: rec() for n in self.buf}
+        self.token = z(1)
+        self.pos = z(1)
+        self.new_cache()
+
+    def new_cache(self) -> None:
+        """A fresh KV cache (DecoderModel::new_cache, model.rs:280-284): per layer k and v codes and per-step scales."""
+        torch = self.torch
+        kvd = self.nkv * self.hd
+        self.kc = [torch.zeros(self.max_seq * kvd, dtype=torch.int32, device=self.device) for _ in range(self.nl)]
+        self.vc = [torch.zeros(self.max_seq * kvd, dtype=torch.int32, device=self.device) for _ in range(self.nl)]
+        self.ks = [torch.zeros(self.max_seq * 16, dtype=torch.uint8, device=self.device) for _ in range(self.nl)]
+        self.vs = [torch.zeros(self.max_seq * 16, dtype=torch.uint8, device=self.device) for _ in range(self.nl)]
+
+    def _ql(self, ql: QuantLinear, x: str, y: str, stream) -> None:
+        ql.forward_int(self.buf[x], self.rec[x], 1, y_dev=self.buf[y], os_dev=self.rec[y], stream=stream)
+
+    def step_launches(self, stream=None) -> None:
+        """DecoderModel::decode_step (model.rs:290-294, 338-353) of the token at self.token, position self.pos (both
+        device int32): every launch on `stream`, no host synchronization; the logits land in buf["logits"] with
+        their scale in rec["logits"]."""
+        b, r, dv = self.buf, self.rec, self.dev
+        B.ref_embed(self.emb, self.emb_scale, self.token, self.vocab, self.dim, b["x"], r["x"], stream, dv)
+        for i, blk in enumerate(self.blocks):
+            g, gs = blk["in_norm"]
+            B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
+            for n, out in (("wq", "q"), ("wk", "k"), ("wv", "v")):
+                self._ql(blk[n], "h", out, stream)
+            B.ref_attention_step(b["q"], r["q"], b["k"], r["k"], b["v"], r["v"], self.pos, self.nh, self.nkv,
+                                 self.hd, self.max_seq, self.kc[i], self.vc[i], self.ks[i], self.vs[i], self.cos,
+                                 self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, b["cat"], r["cat"], stream,
+                                 dv)
+            self._ql(blk["wo"], "cat", "a", stream)
+            B.ref_add(b["x"], r["x"], b["a"], r["a"], self.dim, b["x"], r["x"], stream, dv)
+            g, gs = blk["post_norm"]
+            B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
+            self._ql(blk["gate"], "h", "g", stream)
+            self._ql(blk["up"], "h", "u", stream)
+            B.ref_swiglu(b["g"], r["g"], b["u"], r["u"], self.hidden, self.silu_codes, self.silu_lut, b["hh"],
+                         r["hh"], stream, dv)
+            self._ql(blk["down"], "hh", "m", stream)
+            B.ref_add(b["x"], r["x"], b["m"], r["m"], self.dim, b["x"], r["x"], stream, dv)
+        g, gs = self.final_norm
+        B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
+        self._ql(self.lm_head, "h", "logits", stream)
+
+    def decode_step(self, token: int, pos: int):
+        """The logits of `token` at `pos` against the cache: (codes, (mant, shift)) on the host."""
+        if not 0 <= pos < self.max_seq:
+            raise ValueError(f"position {pos} beyond the tables' {self.max_seq}")
+        if not 0 <= token < self.vocab:
+            raise ValueError(f"token {token} out of vocab {self.vocab}")
+        self.token.fill_(int(token))
+        self.pos.fill_(int(pos))
+        self.step_launches()
+        return self.read_logits()
+
+    def read_logits(self):
+        self.torch.cuda.synchronize(self.device)
+        w = self.rec["logits"].cpu().numpy()
+        return self.buf["logits"].cpu().numpy(), (int(w[0]), int(w.view(np.int32)[2]))
+
+    def generate_greedy(self, prompt, max_new: int, stop=()):
+        """generate_greedy_by as repro::run drives it: (tokens, run logits_hash hex, per-position hashes hex)."""
+        if len(prompt) == 0:
+            raise ValueError("generate: the prompt is empty")
+        self.new_cache()
+        hashes, run = [], hashlib.sha256()
+        logits = None
+        for pos, t in enumerate(prompt):
+            logits = self.decode_step(int(t), pos)
+            hashes.append(hashlib.sha256(logits_hash_bytes(*logits)).hexdigest())
+        tokens, pos = [], len(prompt)
+        while len(tokens) < max_new:
+            codes, scale = logits
+            run.update(logits_hash_bytes(codes, scale))
+            nxt = int(np.argmax(codes))  # the first maximum, as argmax_codes
+            if nxt in stop:
+                break
+            tokens.append(nxt)
+            if len(tokens) < max_new:
+                logits = self.decode_step(nxt, pos)
+                hashes.append(hashlib.sha256(logits_hash_bytes(*logits)).hexdigest())
+                pos += 1
+        return tokens, run.hexdigest(), hashes
