@@ -525,13 +525,55 @@ static inline int64_t shift_round(int64_t v, int s) {
     return v < 0 ? -q : q;
 }
 
-static void rmsnorm_rows(const int32_t* r, size_t rows, size_t d, int8_t* q) {
+/* The decoder's RMSNorm to int8 codes (this build's rule): rms = isqrt(floor(sum r^2 / d)),
+ * q = clamp(div_round(32 r, rms), +-127), 0 when rms = 0. */
+void kt_dec_rmsnorm_rows(const int32_t* r, size_t rows, size_t d, int8_t* q) {
     for (size_t t = 0; t < rows; t++) {
         const int32_t* x = r + t * d;
-        uint64_t ss = 0;
-        for (size_t i = 0; i < d; i++) ss += (uint64_t)((int64_t)x[i] * x[i]);
-        int64_t rms = (int64_t)kt_isqrt_u128(0, ss / d);
+        unsigned __int128 ss = 0; /* exact: d values of at most 2^62 */
+        for (size_t i = 0; i < d; i++) ss += (unsigned __int128)(uint64_t)((int64_t)x[i] * x[i]);
+        int64_t rms = (int64_t)kt_isqrt_u128(0, (uint64_t)(ss / d)); /* the mean of squares is at most 2^62 */
         for (size_t i = 0; i < d; i++) q[t * d + i] = rms == 0 ? 0 : (int8_t)clamp64(div_round(32 * (int64_t)x[i], rms), -127, 127);
+    }
+}
+
+/* Rotate-half RoPE of `heads` heads of hd int8 values in place at position p: pairs (i, i + hd/2) rotated by the
+ * int16 tables C = cos[p][i], S = sin[p][i] at 2^14: a' = clamp(sr(a C - b S, 14)), b' = clamp(sr(b C + a S, 14)). */
+void kt_dec_rope_row(int8_t* x, size_t heads, size_t hd, size_t p, const int16_t* cos_t, const int16_t* sin_t) {
+    const size_t hh = hd / 2;
+    for (size_t hv = 0; hv < heads; hv++) {
+        int8_t* y = x + hv * hd;
+        for (size_t i = 0; i < hh; i++) {
+            int64_t a = y[i], b = y[i + hh], C = cos_t[p * hh + i], S = sin_t[p * hh + i];
+            y[i] = (int8_t)clamp64(shift_round(a * C - b * S, 14), -127, 127);
+            y[i + hh] = (int8_t)clamp64(shift_round(b * C + a * S, 14), -127, 127);
+        }
+    }
+}
+
+/* One head's attention (this build's integer softmax) over positions 0..p of one kv head g of the caches kl / vl
+ * ([pos][nkv][hd] int8): s_j = q . k_j, m = max s_j, e_j = exp_tab[(m - s_j + 64) >> 7] (0 past 1024 entries),
+ * o = clamp(div_round(sum_j e_j v_j, sum_j e_j)). sc: scratch of p + 1 values. */
+void kt_dec_attend(const int8_t* q, const int8_t* kl, const int8_t* vl, size_t p, size_t nkv, size_t g, size_t hd,
+                   const int32_t* exp_tab, int64_t* sc, int8_t* o) {
+    int64_t m = INT64_MIN;
+    for (size_t j = 0; j <= p; j++) {
+        const int8_t* k = kl + (j * nkv + g) * hd;
+        int64_t s = 0;
+        for (size_t i = 0; i < hd; i++) s += (int64_t)q[i] * k[i];
+        sc[j] = s;
+        if (s > m) m = s;
+    }
+    int64_t den = 0;
+    for (size_t j = 0; j <= p; j++) {
+        int64_t idx = (m - sc[j] + 64) >> 7;
+        sc[j] = idx < 1024 ? exp_tab[idx] : 0;
+        den += sc[j];
+    }
+    for (size_t i = 0; i < hd; i++) {
+        int64_t acc = 0;
+        for (size_t j = 0; j <= p; j++) acc += sc[j] * vl[(j * nkv + g) * hd + i];
+        o[i] = (int8_t)clamp64(div_round(acc, den), -127, 127);
     }
 }
 
@@ -541,7 +583,7 @@ static void rmsnorm_rows(const int32_t* r, size_t rows, size_t d, int8_t* q) {
 void kt_dec_forward(const kt_dec_model* M, const int32_t* tokens, size_t T, size_t pos0, int8_t* kc, int8_t* vc,
                     int32_t* logits, size_t threads) {
     const size_t d = (size_t)M->d, ffn = (size_t)M->ffn, nh = (size_t)M->nh, nkv = (size_t)M->nkv, hd = (size_t)M->hd;
-    const size_t nq = (nh + 2 * nkv) * hd, hh = hd / 2, maxp = (size_t)M->max_pos, rep = nh / nkv;
+    const size_t nq = (nh + 2 * nkv) * hd, maxp = (size_t)M->max_pos, rep = nh / nkv;
     int32_t* r = (int32_t*)malloc(T * d * sizeof(int32_t));
     int8_t* xn = (int8_t*)malloc(T * (d > ffn ? ffn : d) * 2 + T * ffn);
     int8_t* qkv = (int8_t*)malloc(T * nq);
@@ -554,52 +596,23 @@ void kt_dec_forward(const kt_dec_model* M, const int32_t* tokens, size_t T, size
     for (size_t l = 0; l < (size_t)M->layers; l++) {
         int8_t* kl = kc + l * maxp * nkv * hd;
         int8_t* vl = vc + l * maxp * nkv * hd;
-        rmsnorm_rows(r, T, d, xn);
+        kt_dec_rmsnorm_rows(r, T, d, xn);
         gemm_run(xn, M->wqkv + l * nq * d, T, nq, d, M->qkv_mant + l * nq, M->qkv_shift + l * nq, NULL, qkv, NULL, 0,
                  threads);
         for (size_t t = 0; t < T; t++) {
             size_t p = pos0 + t;
             int8_t* row = qkv + t * nq;
-            for (size_t hv = 0; hv < nh + nkv; hv++) { /* q heads then k heads */
-                int8_t* x = row + hv * hd;
-                for (size_t i = 0; i < hh; i++) {
-                    int64_t a = x[i], b = x[i + hh], C = M->rope_cos[p * hh + i], S = M->rope_sin[p * hh + i];
-                    x[i] = (int8_t)clamp64(shift_round(a * C - b * S, 14), -127, 127);
-                    x[i + hh] = (int8_t)clamp64(shift_round(b * C + a * S, 14), -127, 127);
-                }
-            }
+            kt_dec_rope_row(row, nh + nkv, hd, p, M->rope_cos, M->rope_sin); /* q heads then k heads */
             memcpy(kl + p * nkv * hd, row + nh * hd, nkv * hd);
             memcpy(vl + p * nkv * hd, row + (nh + nkv) * hd, nkv * hd);
         }
-        for (size_t t = 0; t < T; t++) {
-            size_t p = pos0 + t;
-            for (size_t hq = 0; hq < nh; hq++) {
-                const int8_t* q = qkv + t * nq + hq * hd;
-                size_t g = hq / rep;
-                int64_t m = INT64_MIN;
-                for (size_t j = 0; j <= p; j++) {
-                    const int8_t* k = kl + (j * nkv + g) * hd;
-                    int64_t s = 0;
-                    for (size_t i = 0; i < hd; i++) s += (int64_t)q[i] * k[i];
-                    sc[j] = s;
-                    if (s > m) m = s;
-                }
-                int64_t den = 0;
-                for (size_t j = 0; j <= p; j++) {
-                    int64_t idx = (m - sc[j] + 64) >> 7;
-                    sc[j] = idx < 1024 ? M->exp_tab[idx] : 0;
-                    den += sc[j];
-                }
-                for (size_t i = 0; i < hd; i++) {
-                    int64_t acc = 0;
-                    for (size_t j = 0; j <= p; j++) acc += sc[j] * vl[(j * nkv + g) * hd + i];
-                    o[t * nh * hd + hq * hd + i] = (int8_t)clamp64(div_round(acc, den), -127, 127);
-                }
-            }
-        }
+        for (size_t t = 0; t < T; t++)
+            for (size_t hq = 0; hq < nh; hq++)
+                kt_dec_attend(qkv + t * nq + hq * hd, kl, vl, pos0 + t, nkv, hq / rep, hd, M->exp_tab, sc,
+                              o + t * nh * hd + hq * hd);
         gemm_run(o, M->wo + l * d * nh * hd, T, d, nh * hd, M->o_mant + l * d, M->o_shift + l * d, NULL, NULL, r, 1,
                  threads);
-        rmsnorm_rows(r, T, d, xn);
+        kt_dec_rmsnorm_rows(r, T, d, xn);
         gemm_run(xn, M->wgu + l * 2 * ffn * d, T, 2 * ffn, d, M->gu_mant + l * 2 * ffn, M->gu_shift + l * 2 * ffn,
                  NULL, gu, NULL, 0, threads);
         for (size_t t = 0; t < T; t++)
@@ -610,7 +623,7 @@ void kt_dec_forward(const kt_dec_model* M, const int32_t* tokens, size_t T, size
         gemm_run(h, M->wd + l * d * ffn, T, d, ffn, M->d_mant + l * d, M->d_shift + l * d, NULL, NULL, r, 1, threads);
     }
     if (logits) {
-        rmsnorm_rows(r + (T - 1) * d, 1, d, xn);
+        kt_dec_rmsnorm_rows(r + (T - 1) * d, 1, d, xn);
         gemm_run(xn, M->emb, 1, (size_t)M->vocab, d, M->lm_mant, M->lm_shift, NULL, NULL, logits, 0, threads);
     }
     free(r);

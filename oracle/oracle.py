@@ -123,6 +123,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_channel_scales_target_i16": (None, [_P, _SZ, _SZ, C.c_int64, C.c_int64, _P, _P]),
         "kt_argmax_i32": (C.c_int64, [_P, _SZ]),
         "kt_dec_generate": (C.c_int, [_P, _P, _SZ, _SZ, C.c_int, _P, _P, _SZ]),
+        "kt_dec_rmsnorm_rows": (None, [_P, _SZ, _SZ, _P]),
+        "kt_dec_rope_row": (None, [_P, _SZ, _SZ, _SZ, _P, _P]),
+        "kt_dec_attend": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P, _P]),
         "kt_conv2d_i8w16": (None, [_P, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _SZ]),
         "kt_mlp_gelu": (C.c_int, [_P, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ]),
         "kt_rd_synthetic": (_P, [C.c_uint64, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_double, C.c_double, _SZ]),
@@ -679,6 +682,31 @@ def dec_model(shape: dict, arrays: dict):
         keep[k] = a
         setattr(m, k, a.ctypes.data)
     return m, keep
+
+
+def dec_rmsnorm(r, rows: int, d: int) -> np.ndarray:
+    """The W12 decoder's RMSNorm to int8 codes (kt_dec_rmsnorm_rows)."""
+    r = _c(r, np.int32)
+    q = np.zeros(rows * d, dtype=np.int8)
+    lib().kt_dec_rmsnorm_rows(_ptr(r), rows, d, _ptr(q))
+    return q
+
+
+def dec_rope(x, heads: int, hd: int, p: int, cos_t, sin_t) -> np.ndarray:
+    """The W12 decoder's rotate-half RoPE of heads x hd int8 values at position p (kt_dec_rope_row)."""
+    x = _c(x, np.int8).copy()
+    cos_t, sin_t = _c(cos_t, np.int16), _c(sin_t, np.int16)
+    lib().kt_dec_rope_row(_ptr(x), heads, hd, p, _ptr(cos_t), _ptr(sin_t))
+    return x
+
+
+def dec_attend(q, kl, vl, p: int, nkv: int, g: int, hd: int, exp_tab) -> np.ndarray:
+    """One head of the W12 decoder's attention over positions 0..p of kv head g (kt_dec_attend)."""
+    q, kl, vl, exp_tab = _c(q, np.int8), _c(kl, np.int8), _c(vl, np.int8), _c(exp_tab, np.int32)
+    sc = np.zeros(p + 1, dtype=np.int64)
+    o = np.zeros(hd, dtype=np.int8)
+    lib().kt_dec_attend(_ptr(q), _ptr(kl), _ptr(vl), p, nkv, g, hd, _ptr(exp_tab), _ptr(sc), _ptr(o))
+    return o
 
 
 def dec_generate(shape: dict, arrays: dict, prompt, max_new: int, batched: bool = True, threads: int = 0):

@@ -148,12 +148,12 @@ def test_w12_swiglu_every_path(torch_dev, m):
 
 
 def rmsnorm_rows_py(r: np.ndarray, d: int) -> np.ndarray:
-    """The decoder's RMSNorm in Python integers (the rule of kt_oracle_layers.c's rmsnorm_rows)."""
+    """The decoder's RMSNorm in Python integers (the rule of kt_oracle_layers.c's kt_dec_rmsnorm_rows)."""
     import math
 
     out = np.zeros(r.shape, dtype=np.int8)
     for t, row in enumerate(r.astype(np.int64)):
-        ss = int(sum(int(v) * int(v) for v in row)) % 2**64
+        ss = int(sum(int(v) * int(v) for v in row))  # exact: the full-range row sums past 2^64
         rms = math.isqrt(ss // d)
         for i, v in enumerate(row):
             if rms:
@@ -177,7 +177,7 @@ def test_w12_norm_fused_products(torch_dev, m, d):
     if m > 1:
         r[1] = 0  # rms = 0: the row quantizes to zeros
     if m > 2:
-        r[2] = rng.integers(-(2**31) + 1, 2**31 - 1, size=d).astype(np.int32)  # sum of squares wraps u64
+        r[2] = rng.integers(-(2**31) + 1, 2**31 - 1, size=d).astype(np.int32)  # sum of squares past 2^64
     q = rmsnorm_rows_py(r, d)
     rd = torch.from_numpy(r.reshape(-1)).cuda()
     n = 200

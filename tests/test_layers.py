@@ -9,6 +9,8 @@ What pins what:
     on a tiny case both equal a pure-Python restatement with Python integers (requant of kt-int lib.rs:78-86);
   - the SiLU / sigmoid code tables satisfy the identities of the closed forms they come from.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -396,3 +398,88 @@ def test_decoder_generators_equal_the_product():
     m1, s1 = TA.channel_scales_fast(w.astype(np.int32), 50, 200, 16, 2048)
     m2, s2 = O.channel_scales_target(w, 50, 200, 16, 2048)
     assert np.array_equal(m1, m2) and np.array_equal(s1, s2)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# config 3: each rule of the W12 decoder oracle pinned by what the mathematics fixes (not by a second statement of
+# the same formula)
+
+
+def test_w12_rmsnorm_pins():
+    """A constant row normalizes to +-32 everywhere (rms = |c|); a zero row gives 0; one nonzero value c in a row
+    of d gives 32 sqrt(d) when c^2 / d is a perfect square (64 for d = 4), clamped to 127 from d = 16."""
+    for c in (1, -7, 2**15 - 1, -(2**20), 2**31 - 1):
+        q = O.dec_rmsnorm(np.full(896, c, dtype=np.int32), 1, 896)
+        assert (q == (32 if c > 0 else -32)).all()
+    assert not O.dec_rmsnorm(np.zeros((3, 64), dtype=np.int32), 3, 64).any()
+    q = O.dec_rmsnorm(np.array([100, 0, 0, 0], dtype=np.int32), 1, 4)
+    assert q.tolist() == [64, 0, 0, 0]
+    q = O.dec_rmsnorm(np.array([-400] + [0] * 15, dtype=np.int32), 1, 16)
+    assert q.tolist() == [-127] + [0] * 15
+    # the sum of squares is exact: 896 values of 2^31 - 1 sum past 2^64 and still give rms = 2^31 - 1 (a wrapping
+    # 64-bit sum would not)
+    big = np.full(896, 2**31 - 1, dtype=np.int32)
+    big[::2] = -(2**31 - 1)
+    q = O.dec_rmsnorm(big, 1, 896)
+    assert (q == np.where(big > 0, 32, -32)).all()
+
+
+def test_w12_rope_pins():
+    """RoPE at position 0 is the identity on every int8 pair (cos 0 = 1, sin 0 = 0 in the real table); a quarter
+    turn (C = 0, S = 2^14) maps (a, b) to (-b, a) and a half turn to (-a, -b), clamped to +-127; at every position of
+    the real table the rotation is the float rotation within its rounding."""
+    from tritify_amd import workloads as W
+
+    cos_t, sin_t = W.rope_tables(64, 64)
+    a, b = np.meshgrid(np.arange(-127, 128), np.arange(-127, 128))
+    pairs = np.stack([a.ravel(), b.ravel()], axis=1).astype(np.int8)  # (a, b) as one 2-wide head each
+    one = np.array([[16384]], dtype=np.int16), np.array([[0]], dtype=np.int16)
+    assert np.array_equal(O.dec_rope(pairs, len(pairs), 2, 0, cos_t[:, :1].copy(), sin_t[:, :1].copy()), pairs)
+    quarter = O.dec_rope(pairs, len(pairs), 2, 0, np.array([0], dtype=np.int16), np.array([16384], dtype=np.int16))
+    want = np.stack([np.clip(-pairs[:, 1].astype(int), -127, 127), pairs[:, 0]], axis=1)
+    assert np.array_equal(quarter.reshape(-1, 2), want)
+    half = O.dec_rope(pairs, len(pairs), 2, 0, np.array([-16384], dtype=np.int16), np.array([0], dtype=np.int16))
+    assert np.array_equal(half.reshape(-1, 2), np.clip(-pairs.astype(int), -127, 127))
+    assert one[0][0, 0] == cos_t[0, 0] and one[1][0, 0] == sin_t[0, 0]
+    rng = np.random.default_rng(2)
+    x = rng.integers(-90, 91, size=64).astype(np.int8)  # |rotated| < 128: no clamp
+    for p in (1, 7, 63):
+        y = O.dec_rope(x, 1, 64, p, cos_t, sin_t).astype(float)
+        th = 1.0e6 ** (-2.0 * np.arange(32) / 64) * p
+        xa, xb = x[:32].astype(float), x[32:].astype(float)
+        fa, fb = xa * np.cos(th) - xb * np.sin(th), xb * np.cos(th) + xa * np.sin(th)
+        tol = 0.5 + (np.abs(xa) + np.abs(xb)) / 32768 + 1e-9
+        assert (np.abs(y[:32] - fa) <= tol).all() and (np.abs(y[32:] - fb) <= tol).all(), p
+
+
+def test_w12_attention_pins():
+    """At position 0 a head returns v_0 exactly; equal scores give the rounded mean of the v rows; one score ahead of
+    every other by at least 1024 * 128 returns that row's v; the exp table starts at 2^15, falls monotonically and
+    reads round(2^15 / e) at 64."""
+    from tritify_amd import workloads as W
+
+    E = W.exp_table()
+    assert E[0] == 2**15 and E[64] == round(2**15 / math.e) and (np.diff(E) <= 0).all() and E[-1] >= 0
+    rng = np.random.default_rng(12)
+    hd, nkv = 64, 2
+    q = rng.integers(-127, 128, size=hd).astype(np.int8)
+    kl = rng.integers(-127, 128, size=(40, nkv, hd)).astype(np.int8)
+    vl = rng.integers(-127, 128, size=(40, nkv, hd)).astype(np.int8)
+    for g in range(nkv):
+        assert np.array_equal(O.dec_attend(q, kl, vl, 0, nkv, g, hd, E), vl[0, g])
+    flat_k = np.repeat(kl[:1], 40, axis=0)  # every key equal: every score equal
+    o = O.dec_attend(q, flat_k, vl, 39, nkv, 1, hd, E)
+    s = vl[:, 1].astype(np.int64).sum(axis=0)
+    want = np.sign(s) * ((2 * np.abs(s) + 40) // 80)  # round half away from zero of s / 40
+    assert np.array_equal(o, want.astype(np.int8))
+    qd = np.full(hd, 127, dtype=np.int8)
+    dom = np.full((40, nkv, hd), -127, dtype=np.int8)
+    dom[17] = 127  # q . k = 64 * 127^2 there and -64 * 127^2 elsewhere: a gap of 2 064 512 > 1024 * 128
+    assert np.array_equal(O.dec_attend(qd, dom, vl, 39, nkv, 0, hd, E), vl[17, 0])
+
+
+def test_greedy_takes_the_first_maximum():
+    """argmax_codes (generate.rs:48-56; the reference's own test cases, tests_generate.rs:46-50)."""
+    for v, want in (([3, 7, 7, 1], 1), ([-5, -2, -9], 1), ([4], 0), ([0, 0, 0], 0)):
+        a = np.array(v, dtype=np.int32)
+        assert O.lib().kt_argmax_i32(a.ctypes.data, a.size) == want

@@ -44,17 +44,21 @@ __global__ __launch_bounds__(256) void dec_embed_kernel(const int32_t* __restric
 // have stride qs (columns d .. qs - 1 are left alone).
 __global__ __launch_bounds__(256) void dec_rmsnorm_kernel(const int32_t* __restrict__ r, int d, int8_t* __restrict__ q,
                                                           int qs) {
-    __shared__ uint64_t sw[4];
+    __shared__ uint64_t sw[8];
     __shared__ int64_t s_rms;
     const int t = blockIdx.x, tid = threadIdx.x;
     const int32_t* x = r + (size_t)t * d;
-    uint64_t ss = 0;
-    for (int i = tid; i < d; i += 256) ss += (uint64_t)((int64_t)x[i] * x[i]);
+    uint64_t sh = 0, sl = 0;  // the exact sum of squares as sh * 2^16 + sl (sq_mean_floor)
+    for (int i = tid; i < d; i += 256) {
+        const uint64_t sq = (uint64_t)((int64_t)x[i] * x[i]);
+        sh += sq >> 16, sl += sq & 0xFFFF;
+    }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((tid & 63) == 0) sw[tid >> 6] = ss;
+    for (int o = 32; o >= 1; o >>= 1) sh += __shfl_xor(sh, o), sl += __shfl_xor(sl, o);
+    if ((tid & 63) == 0) sw[tid >> 6] = sh, sw[4 + (tid >> 6)] = sl;
     __syncthreads();
-    if (tid == 0) s_rms = (int64_t)isqrt_u64((sw[0] + sw[1] + sw[2] + sw[3]) / (uint64_t)d);
+    if (tid == 0)
+        s_rms = (int64_t)isqrt_u64(sq_mean_floor(sw[0] + sw[1] + sw[2] + sw[3], sw[4] + sw[5] + sw[6] + sw[7], (uint64_t)d));
     __syncthreads();
     const int64_t rms = s_rms;
     const uint64_t inv = rms_inv(rms);

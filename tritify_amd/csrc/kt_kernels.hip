@@ -677,7 +677,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
     __shared__ part_t sP[NW][OUTS];
     __shared__ int32_t sX[NW][MT * 16];
     extern __shared__ __attribute__((aligned(16))) int8_t sQ[];  // NORM: the normalized rows, M x kp
-    __shared__ uint64_t sNss[NORM ? NW * 16 : 1], sNrq[NORM ? 32 : 1];
+    __shared__ uint64_t sNss[NORM ? NW * 32 : 1], sNrq[NORM ? 32 : 1];
     int32_t pre[2];  // NORM: row 0 of the residual, loaded first
     if constexpr (NORM) norm_preload<64 * NW, 2>(reinterpret_cast<const int32_t*>(x), d, pre);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -845,7 +845,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
     __shared__ int32_t sX[NW][MT * 16];
     __shared__ int16_t sSilu[256];
     extern __shared__ __attribute__((aligned(16))) int8_t sQ[];  // NORM: the normalized rows, M x kp
-    __shared__ uint64_t sNss[NORM ? NW * 16 : 1], sNrq[NORM ? 32 : 1];
+    __shared__ uint64_t sNss[NORM ? NW * 32 : 1], sNrq[NORM ? 32 : 1];
     int32_t pre[2];  // NORM: row 0 of the residual, loaded first
     if constexpr (NORM) norm_preload<64 * NW, 2>(reinterpret_cast<const int32_t*>(x), d, pre);
     int32_t fa[2] = {0, 0}, fm[2] = {0, 0}, fs[2] = {0, 0};  // FOLD_O: the o sums and scales of the same values

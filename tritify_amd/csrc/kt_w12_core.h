@@ -200,6 +200,13 @@ __device__ __forceinline__ uint64_t isqrt_u64(uint64_t n) {
     return x;
 }
 
+// floor(S / d) of an exact sum of squares S = hi * 2^16 + lo kept as two wrapping-free parts: hi sums v^2 >> 16 and
+// lo sums v^2 & 0xFFFF over at most 2^18 values of |v| <= 2^31 (hi < 2^64, lo < 2^34). The quotient is at most 2^62.
+__device__ __forceinline__ uint64_t sq_mean_floor(uint64_t hi, uint64_t lo, uint64_t d) {
+    const uint64_t q1 = hi / d, r1 = hi - q1 * d;
+    return (q1 << 16) + ((r1 << 16) + lo) / d;
+}
+
 // The decoder's RMSNorm code of one residual value: clamp(div_round(32 x, rms), +-127), 0 when rms = 0 (div_round =
 // round half away from zero). div_round(a, rms) = floor((2|a| + rms) / dd) with a's sign, dd = 2 rms. inv =
 // floor((2^64 - 1) / dd) (rms_inv) makes the quotient one high multiply: below the clamp n = 2|a| + rms < 2^38, so
@@ -217,10 +224,10 @@ __device__ __forceinline__ int rms_q8(int32_t x, int64_t rms, uint64_t inv) {
 }
 
 // RMSNorm of rows 0 .. M-1 (M <= 16) of the int32 residual r (row stride d) into int8 rows q[m][0 .. kp) in LDS,
-// zero padded from d: rms = isqrt(floor(sum r^2 / d)) over the row (sum in wrapping u64), then rms_q8 per value. All
-// NT threads share every row; row 0's values tid + j NT (j < PRE) come preloaded in pre[] (norm_preload, issued
-// before anything else so their latency overlaps the caller's weight loads). s_ss (NT / 64 x 16) and s_rq (2 x 16)
-// are LDS scratch. Ends with a barrier.
+// zero padded from d: rms = isqrt(floor(sum r^2 / d)) over the row (the exact sum, sq_mean_floor), then rms_q8 per
+// value. All NT threads share every row; row 0's values tid + j NT (j < PRE) come preloaded in pre[] (norm_preload,
+// issued before anything else so their latency overlaps the caller's weight loads). s_ss (NT / 64 x 32) and s_rq
+// (2 x 16) are LDS scratch. Ends with a barrier.
 template <int NT, int PRE>
 __device__ __forceinline__ void norm_preload(const int32_t* __restrict__ r, int d, int32_t (&pre)[PRE]) {
 #pragma unroll
@@ -235,26 +242,30 @@ __device__ __forceinline__ void norm_rows_to_lds(const int32_t* __restrict__ r, 
                                                  uint64_t* s_ss, uint64_t* s_rq, const int32_t (&pre)[PRE]) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     for (int m = 0; m < M; m++) {
-        uint64_t ss = 0;
+        uint64_t sh = 0, sl = 0;
         int i = tid;
         if (m == 0) {
 #pragma unroll
-            for (int j = 0; j < PRE; j++, i += NT) ss += (uint64_t)((int64_t)pre[j] * pre[j]);  // zero past d
+            for (int j = 0; j < PRE; j++, i += NT) {  // zero past d
+                const uint64_t sq = (uint64_t)((int64_t)pre[j] * pre[j]);
+                sh += sq >> 16, sl += sq & 0xFFFF;
+            }
         }
         for (; i < d; i += NT) {
             const int64_t v = r[(size_t)m * d + i];
-            ss += (uint64_t)(v * v);
+            const uint64_t sq = (uint64_t)(v * v);
+            sh += sq >> 16, sl += sq & 0xFFFF;
         }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) s_ss[w * 16 + m] = ss;
+        for (int o = 32; o >= 1; o >>= 1) sh += __shfl_xor(sh, o), sl += __shfl_xor(sl, o);
+        if (lane == 0) s_ss[w * 32 + m] = sh, s_ss[w * 32 + 16 + m] = sl;
     }
     __syncthreads();
     if (tid < M) {
-        uint64_t ss = 0;
+        uint64_t sh = 0, sl = 0;
 #pragma unroll
-        for (int q2 = 0; q2 < NT / 64; q2++) ss += s_ss[q2 * 16 + tid];
-        const int64_t rms = (int64_t)isqrt_u64(ss / (uint64_t)d);
+        for (int q2 = 0; q2 < NT / 64; q2++) sh += s_ss[q2 * 32 + tid], sl += s_ss[q2 * 32 + 16 + tid];
+        const int64_t rms = (int64_t)isqrt_u64(sq_mean_floor(sh, sl, (uint64_t)d));
         s_rq[tid] = (uint64_t)rms;
         s_rq[16 + tid] = rms_inv(rms);
     }
