@@ -643,3 +643,362 @@ kt_scale kt_rd_get_rope(const void* model, int64_t* cos_mant, int32_t* cos_shift
     }
     return M->inv_sqrt;
 }
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* MoeMlp at the reference's semantics (crates/01-engine/kt-core/src/layers.rs:652-1020, router.rs:29-79)        */
+/* ------------------------------------------------------------------------------------------------------------ */
+typedef struct {
+    rd_ql gate, up, down;
+} rd_mlp;
+
+typedef struct {
+    size_t dim, E, top_k, hidden, shared_hidden;
+    int norm_topk, sigmoid, has_shared;
+    rd_ql router;
+    rd_mlp* experts;
+    rd_mlp shared;
+    rd_lut exp_code, sig, silu;
+    int64_t* bias; /* the sigmoid router's coded selection bias, round(b * 2^20) */
+} kt_refmoe;
+
+#define ROUTER_CODE_BITS 20
+
+enum { LUT_SIGMOID = 2 };
+
+static double lut_f2(int kind, double x) { return kind == LUT_SIGMOID ? 1.0 / (1.0 + exp(-x)) : lut_f(kind, x); }
+
+static void lut_build2(rd_lut* L, int kind, double lo, double hi, unsigned idx_bits, unsigned code_bits,
+                       int right_id) {
+    if (kind != LUT_SIGMOID) {
+        lut_build(L, kind, lo, hi, idx_bits, code_bits, right_id);
+        return;
+    }
+    const size_t n = (size_t)1 << idx_bits;
+    const double k = (double)(1ULL << code_bits);
+    L->codes = (int64_t*)malloc(n * sizeof(int64_t));
+    for (size_t i = 0; i < n; i++) {
+        const double x = lo + (hi - lo) * ((double)i / (double)(n - 1));
+        L->codes[i] = (int64_t)round(lut_f2(kind, x) * k);
+    }
+    const double inv_step = (double)(n - 1) / (hi - lo);
+    L->inv_step_scale = kt_scale_from_f64(inv_step);
+    L->lo_index = (int64_t)round(lo * inv_step);
+    L->n = n;
+    L->code_scale = kt_scale_from_f64(1.0 / k);
+    L->right_identity = right_id;
+}
+
+static float unif_f32(uint64_t* s) {
+    *s = *s * 6364136223846793005ULL + 1442695040888963407ULL;
+    return (float)((double)(*s >> 40) / (double)(1ULL << 24) * 2.0 - 1.0);
+}
+static void draw(uint64_t* s, float* buf, size_t n) {
+    for (size_t i = 0; i < n; i++) buf[i] = unif_f32(s);
+}
+/* tests_glm.rs:20-29: a SwiGluMlp drawing gate, up (hidden x dim) and down (dim x hidden) from the stream. */
+static void mlp_build(rd_mlp* m, uint64_t* s, size_t dim, size_t hidden, float* buf) {
+    draw(s, buf, hidden * dim);
+    ql_build(&m->gate, buf, hidden, dim);
+    draw(s, buf, hidden * dim);
+    ql_build(&m->up, buf, hidden, dim);
+    draw(s, buf, dim * hidden);
+    ql_build(&m->down, buf, dim, hidden);
+}
+
+/* The MoE of the reference's GLM tests (tests_glm.rs:31-43, 224-228), generalized: the stream from `seed` draws the
+ * router (E x dim) and then each expert's gate / up / down (hidden 24 there); norm_topk_prob as given; with
+ * sigmoid != 0 a sigmoid router whose bias is vecf(bias_seed, E) * 0.05 (as f32); with shared_hidden > 0 a shared
+ * expert drawn from the stream seed ^ 0xA5. The tables are MoeMlp::new's exp CodeLut, SigmoidScore::new's table
+ * (router.rs:38-49) and SwiGluMlp::new's SiLU. */
+void* kt_rm_synthetic(uint64_t seed, size_t dim, size_t E, size_t top_k, size_t hidden, int norm_topk, int sigmoid,
+                      uint64_t bias_seed, size_t shared_hidden) {
+    kt_refmoe* M = (kt_refmoe*)calloc(1, sizeof(kt_refmoe));
+    M->dim = dim, M->E = E, M->top_k = top_k, M->hidden = hidden, M->shared_hidden = shared_hidden;
+    M->norm_topk = norm_topk, M->sigmoid = sigmoid, M->has_shared = shared_hidden > 0;
+    size_t big = E * dim;
+    const size_t h2 = hidden > shared_hidden ? hidden : shared_hidden;
+    if (h2 * dim > big) big = h2 * dim;
+    float* buf = (float*)malloc(big * sizeof(float));
+    uint64_t s = seed;
+    draw(&s, buf, E * dim);
+    ql_build(&M->router, buf, E, dim);
+    M->experts = (rd_mlp*)calloc(E, sizeof(rd_mlp));
+    for (size_t e = 0; e < E; e++) mlp_build(&M->experts[e], &s, dim, hidden, buf);
+    if (M->has_shared) {
+        uint64_t s2 = seed ^ 0xA5;
+        mlp_build(&M->shared, &s2, dim, shared_hidden, buf);
+    }
+    M->bias = (int64_t*)calloc(E, sizeof(int64_t));
+    if (sigmoid) {
+        uint64_t sb = bias_seed;
+        const double k = (double)(1ULL << ROUTER_CODE_BITS);
+        for (size_t e = 0; e < E; e++) {
+            const float b = unif_f32(&sb) * 0.05f;
+            M->bias[e] = (int64_t)round((double)b * k);
+        }
+    }
+    lut_build2(&M->exp_code, LUT_EXP, -30.0, 0.0, 16, ROUTER_CODE_BITS, 0);
+    lut_build2(&M->sig, LUT_SIGMOID, -16.0, 16.0, 16, ROUTER_CODE_BITS, 0);
+    lut_build2(&M->silu, LUT_SILU, -30.0, 30.0, 16, 20, 1);
+    free(buf);
+    return M;
+}
+
+static void mlp_free(rd_mlp* m) { ql_free(&m->gate), ql_free(&m->up), ql_free(&m->down); }
+void kt_rm_free(void* p) {
+    kt_refmoe* M = (kt_refmoe*)p;
+    if (!M) return;
+    ql_free(&M->router);
+    for (size_t e = 0; e < M->E; e++) mlp_free(&M->experts[e]);
+    free(M->experts);
+    if (M->has_shared) mlp_free(&M->shared);
+    free(M->bias), free(M->exp_code.codes), free(M->sig.codes), free(M->silu.codes);
+    free(M);
+}
+
+/* SwiGluMlp::forward_int (layers.rs:609-640) on rows x dim codes at xs, with the SiLU table `silu`. */
+static void mlp_forward(const rd_mlp* m, const rd_lut* silu, const rd_t* x, rd_t* y) {
+    const size_t rows = x->n / m->gate.in, hid = m->gate.out;
+    rd_t g = t_new(rows * hid), u = t_new(rows * hid), h = t_new(rows * hid);
+    ql(&m->gate, x, &g);
+    ql(&m->up, x, &u);
+    const kt_scale id_factor = kt_scale_mul(g.s, kt_scale_recip(silu->code_scale));
+    int64_t* hv = (int64_t*)malloc(g.n * sizeof(int64_t) + 8);
+    for (size_t k = 0; k < g.n; k++) {
+        const int64_t gd = g.d[k], idx = lut_index(silu, gd, g.s);
+        const int64_t code = idx < 0 ? 0 : idx >= (int64_t)silu->n ? kt_scale_apply(id_factor, gd) : lut_code_at(silu, idx);
+        hv[k] = wmul(code, u.d[k]);
+    }
+    close_dyn(hv, g.n, kt_scale_mul(silu->code_scale, u.s), &h);
+    ql(&m->down, &h, y);
+    free(hv);
+    t_free(&g), t_free(&u), t_free(&h);
+}
+
+/* MoeMlp::topk (layers.rs:800-805): the k largest keys, descending, ties to the lower index. */
+static void topk_i64(const int64_t* keys, size_t n, size_t k, int32_t* out) {
+    char* used = (char*)calloc(n, 1);
+    for (size_t i = 0; i < k; i++) {
+        size_t best = n;
+        for (size_t j = 0; j < n; j++)
+            if (!used[j] && (best == n || keys[j] > keys[best])) best = j;
+        used[best] = 1;
+        out[i] = (int32_t)best;
+    }
+    free(used);
+}
+
+/* MoeMlp::route (layers.rs:826-851) / route_sigmoid (layers.rs:855-870 with router.rs:61-71) for one token row x
+ * (dim codes at xs): the router's logits (its QuantLinear), then the softmax numerators exp(l - lmax) from the exp
+ * CodeLut and top-k by logit code, or the sigmoid codes and top-k by code + coded bias. sel, ec: top_k each;
+ * returns sumc (the top-k codes' sum with norm_topk_prob, else all E codes' sum, or 2^20 for a raw sigmoid). The
+ * logits (E codes) and their scale are written when non-null. */
+int64_t kt_rm_route(const void* p, const int32_t* x, kt_scale xs, int32_t* sel, int64_t* ec, int32_t* logits_out,
+                    kt_scale* ls_out) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    const size_t E = M->E, K = M->top_k;
+    rd_t row = {(int32_t*)x, M->dim, xs}, lg = t_new(E);
+    ql(&M->router, &row, &lg);
+    if (logits_out) memcpy(logits_out, lg.d, E * sizeof(int32_t));
+    if (ls_out) *ls_out = lg.s;
+    int64_t* codes = (int64_t*)malloc(E * sizeof(int64_t));
+    int64_t* keys = (int64_t*)malloc(E * sizeof(int64_t));
+    int64_t sumc = 0;
+    if (M->sigmoid) {
+        for (size_t j = 0; j < E; j++) {
+            codes[j] = lut_code_at(&M->sig, lut_index(&M->sig, lg.d[j], lg.s));
+            keys[j] = codes[j] + M->bias[j];
+        }
+        topk_i64(keys, E, K, sel);
+        for (size_t i = 0; i < K; i++) ec[i] = codes[sel[i]];
+        if (M->norm_topk)
+            for (size_t i = 0; i < K; i++) sumc += ec[i];
+        else
+            sumc = (int64_t)1 << ROUTER_CODE_BITS;
+    } else {
+        int32_t lmax = INT32_MIN;
+        for (size_t j = 0; j < E; j++) lmax = lg.d[j] > lmax ? lg.d[j] : lmax;
+        int64_t all = 0;
+        for (size_t j = 0; j < E; j++) {
+            const int64_t idx = lut_index(&M->exp_code, (int64_t)lg.d[j] - lmax, lg.s);
+            codes[j] = idx < 0 ? 0 : lut_code_at(&M->exp_code, idx);
+            all += codes[j];
+            keys[j] = lg.d[j];
+        }
+        topk_i64(keys, E, K, sel);
+        for (size_t i = 0; i < K; i++) ec[i] = codes[sel[i]];
+        if (M->norm_topk)
+            for (size_t i = 0; i < K; i++) sumc += ec[i];
+        else
+            sumc = all;
+    }
+    free(codes), free(keys);
+    t_free(&lg);
+    return sumc;
+}
+
+/* MoeMlp::combine (layers.rs:893-923): the k expert outputs (out_dim codes each, scales ys) brought to their largest
+ * scale, summed with the numerators ec, requantized; the scale folds in 1/sumc. */
+void kt_rm_combine(const int32_t* ys, const kt_scale* ys_s, size_t k, size_t out_dim, const int64_t* ec,
+                   int64_t sumc, int32_t* out, kt_scale* os) {
+    rd_t o = {out, out_dim, ZERO};
+    if (sumc <= 0 || k == 0) {
+        memset(out, 0, out_dim * sizeof(int32_t));
+        *os = ZERO;
+        return;
+    }
+    kt_scale common = ZERO;
+    for (size_t i = 0; i < k; i++) common = fold_max(common, ys_s[i]);
+    if (common.mant == 0) {
+        memset(out, 0, out_dim * sizeof(int32_t));
+        *os = ZERO;
+        return;
+    }
+    const kt_scale cinv = kt_scale_recip(common);
+    int64_t* acc = (int64_t*)calloc(out_dim, sizeof(int64_t));
+    for (size_t i = 0; i < k; i++) {
+        const kt_scale f = kt_scale_mul(ys_s[i], cinv);
+        for (size_t d = 0; d < out_dim; d++) acc[d] = wadd(acc[d], wmul(ec[i], kt_scale_apply(f, ys[i * out_dim + d])));
+    }
+    close_dyn(acc, out_dim, common, &o);
+    *os = o.s.mant ? kt_scale_mul(o.s, ratio(1, (u128)sumc)) : ZERO;
+    free(acc);
+}
+
+/* merge_rows (layers.rs:873-891; forward_routed's inline copy, 1000-1015): per-row outputs brought to the largest
+ * row scale, requantized together. */
+void kt_rm_merge_rows(const int32_t* rows, const kt_scale* rs, size_t T, size_t dim, int32_t* out, kt_scale* os) {
+    kt_scale common = ZERO;
+    for (size_t t = 0; t < T; t++) common = fold_max(common, rs[t]);
+    rd_t o = {out, T * dim, ZERO};
+    if (common.mant == 0) {
+        memset(out, 0, T * dim * sizeof(int32_t));
+        *os = ZERO;
+        return;
+    }
+    const kt_scale cinv = kt_scale_recip(common);
+    int64_t* a = (int64_t*)malloc(T * dim * sizeof(int64_t) + 8);
+    for (size_t t = 0; t < T; t++) {
+        const kt_scale f = kt_scale_mul(rs[t], cinv);
+        for (size_t d = 0; d < dim; d++) a[t * dim + d] = kt_scale_apply(f, rows[t * dim + d]);
+    }
+    close_dyn(a, T * dim, common, &o);
+    *os = o.s;
+    free(a);
+}
+
+/* MoeMlp::forward_int (layers.rs:1031-1034): forward_routed (one token: forward_one_int; a sequence: token by token,
+ * merged) then add_shared (the shared expert over the whole input, added by `add`). x: T x dim codes at xs. */
+void kt_rm_forward(const void* p, const int32_t* x, size_t T, kt_scale xs, int32_t* out, kt_scale* os) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    const size_t dim = M->dim, K = M->top_k;
+    int32_t* rows = (int32_t*)malloc(T * dim * sizeof(int32_t));
+    kt_scale* rs = (kt_scale*)malloc(T * sizeof(kt_scale));
+    int32_t* ys = (int32_t*)malloc(K * dim * sizeof(int32_t));
+    kt_scale* ys_s = (kt_scale*)malloc(K * sizeof(kt_scale));
+    int32_t sel[64];
+    int64_t ec[64];
+    for (size_t t = 0; t < T; t++) {
+        const int64_t sumc = kt_rm_route(M, x + t * dim, xs, sel, ec, NULL, NULL);
+        if (sumc <= 0) {
+            memset(rows + t * dim, 0, dim * sizeof(int32_t));
+            rs[t] = ZERO;
+            continue;
+        }
+        rd_t row = {(int32_t*)x + t * dim, dim, xs};
+        for (size_t i = 0; i < K; i++) {
+            rd_t y = {ys + i * dim, dim, ZERO};
+            mlp_forward(&M->experts[sel[i]], &M->silu, &row, &y);
+            ys_s[i] = y.s;
+        }
+        kt_rm_combine(ys, ys_s, K, dim, ec, sumc, rows + t * dim, &rs[t]);
+    }
+    rd_t routed = t_new(T * dim);
+    if (T <= 1) {
+        memcpy(routed.d, rows, T * dim * sizeof(int32_t));
+        routed.s = T ? rs[0] : ZERO;
+    } else {
+        kt_rm_merge_rows(rows, rs, T, dim, routed.d, &routed.s);
+    }
+    if (M->has_shared) {
+        rd_t xin = {(int32_t*)x, T * dim, xs}, sh = t_new(T * dim);
+        mlp_forward(&M->shared, &M->silu, &xin, &sh);
+        kt_rd_add(routed.d, routed.s, sh.d, sh.s, T * dim, out, os);
+        t_free(&sh);
+    } else {
+        memcpy(out, routed.d, T * dim * sizeof(int32_t));
+        *os = routed.s;
+    }
+    t_free(&routed);
+    free(rows), free(rs), free(ys), free(ys_s);
+}
+
+/* SwiGluMlp::forward_int of one expert (e < E) or the shared expert (e == E) on rows x dim codes at xs. */
+void kt_rm_expert(const void* p, size_t e, const int32_t* x, size_t rows, kt_scale xs, int32_t* y, kt_scale* ys) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    rd_t xin = {(int32_t*)x, rows * M->dim, xs}, out = {y, rows * M->dim, ZERO};
+    mlp_forward(e < M->E ? &M->experts[e] : &M->shared, &M->silu, &xin, &out);
+    *ys = out.s;
+}
+
+/* Accessors for loading the same layer on the device. which: 0 router; for experts e (e == E: shared) 1 gate,
+ * 2 up, 3 down. */
+kt_scale kt_rm_get_ql(const void* p, size_t e, int which, int32_t* codes, size_t* out, size_t* in) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    const rd_ql* q;
+    if (which == 0) {
+        q = &M->router;
+    } else {
+        const rd_mlp* m = e < M->E ? &M->experts[e] : &M->shared;
+        q = which == 1 ? &m->gate : which == 2 ? &m->up : &m->down;
+    }
+    if (codes) memcpy(codes, q->w, q->out * q->in * sizeof(int32_t));
+    *out = q->out, *in = q->in;
+    return q->s;
+}
+/* The run-time tables: which 0 exp, 1 sigmoid, 2 silu (as kt_rd_get_lut); and the coded bias (E values). */
+void kt_rm_get_lut(const void* p, int which, int64_t* codes, kt_scale* inv_step, int64_t* lo_index,
+                   kt_scale* code_scale) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    const rd_lut* L = which == 0 ? &M->exp_code : which == 1 ? &M->sig : &M->silu;
+    if (codes) memcpy(codes, L->codes, L->n * sizeof(int64_t));
+    *inv_step = L->inv_step_scale, *lo_index = L->lo_index, *code_scale = L->code_scale;
+}
+void kt_rm_get_bias(const void* p, int64_t* bias) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    memcpy(bias, M->bias, M->E * sizeof(int64_t));
+}
+
+/* IntTensor::from_reals (tensor.rs:106-117) of the reference tests' probe (tests.rs:29-32): rows x cols reals
+ * uniform in [-1, 1) from the stream s, quantized to ACT_LEVELS by their largest magnitude. */
+kt_scale kt_rm_probe(uint64_t* s, size_t n, int32_t* out) {
+    double* real = (double*)malloc(n * sizeof(double) + 8);
+    double mx = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        real[i] = (double)unif_f32(s);
+        const double a = fabs(real[i]);
+        mx = a > mx ? a : mx;
+    }
+    kt_scale sc = ZERO;
+    if (mx == 0.0) {
+        memset(out, 0, n * sizeof(int32_t));
+    } else {
+        const double step = mx / (double)ACT_LEVELS, inv = (double)ACT_LEVELS / mx;
+        sc = kt_scale_from_f64(step);
+        for (size_t i = 0; i < n; i++) out[i] = (int32_t)round(real[i] * inv);
+    }
+    free(real);
+    return sc;
+}
+
+/* The sigmoid router's selection bias: set expert e's to round(b * 2^20) for the f32 value b (SigmoidScore::new,
+ * router.rs:38-49); the reference tests plant one (tests_glm.rs:183-200) or use all zeros. */
+void kt_rm_set_bias(void* p, size_t e, float b) {
+    kt_refmoe* M = (kt_refmoe*)p;
+    M->bias[e] = (int64_t)round((double)b * (double)(1ULL << ROUTER_CODE_BITS));
+}
+/* SigmoidScore::codes (router.rs:61-63): n logits codes at scale ls -> sigma codes. */
+void kt_rm_sigmoid_codes(const void* p, const int32_t* logits, size_t n, kt_scale ls, int64_t* out) {
+    const kt_refmoe* M = (const kt_refmoe*)p;
+    for (size_t j = 0; j < n; j++) out[j] = lut_code_at(&M->sig, lut_index(&M->sig, logits[j], ls));
+}

@@ -143,6 +143,19 @@ def _declare(L: C.CDLL) -> None:
         "kt_rd_get_emb": (Scale, [_P, _P]),
         "kt_rd_get_lut": (None, [_P, C.c_int, _P, C.POINTER(Scale), C.POINTER(C.c_int64), C.POINTER(Scale)]),
         "kt_rd_get_rope": (Scale, [_P, _P, _P, _P, _P, _P, _P]),
+        "kt_rm_synthetic": (_P, [C.c_uint64, _SZ, _SZ, _SZ, _SZ, C.c_int, C.c_int, C.c_uint64, _SZ]),
+        "kt_rm_free": (None, [_P]),
+        "kt_rm_route": (C.c_int64, [_P, _P, Scale, _P, _P, _P, C.POINTER(Scale)]),
+        "kt_rm_combine": (None, [_P, _P, _SZ, _SZ, _P, C.c_int64, _P, C.POINTER(Scale)]),
+        "kt_rm_merge_rows": (None, [_P, _P, _SZ, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rm_forward": (None, [_P, _P, _SZ, Scale, _P, C.POINTER(Scale)]),
+        "kt_rm_expert": (None, [_P, _SZ, _P, _SZ, Scale, _P, C.POINTER(Scale)]),
+        "kt_rm_get_ql": (Scale, [_P, _SZ, C.c_int, _P, C.POINTER(_SZ), C.POINTER(_SZ)]),
+        "kt_rm_get_lut": (None, [_P, C.c_int, _P, C.POINTER(Scale), C.POINTER(C.c_int64), C.POINTER(Scale)]),
+        "kt_rm_get_bias": (None, [_P, _P]),
+        "kt_rm_probe": (Scale, [C.POINTER(C.c_uint64), _SZ, _P]),
+        "kt_rm_set_bias": (None, [_P, _SZ, C.c_float]),
+        "kt_rm_sigmoid_codes": (None, [_P, _P, _SZ, Scale, _P]),
         "kt_moe_forward_token": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int,
                                         C.c_int, _P]),
     }
@@ -856,3 +869,110 @@ def rd_attention_core(cache: RefCache, q, qs, k, ks, v, vs, pos: int):
     lib().kt_rd_attention_core(cache.model.ptr, cache.ptr, _ptr(q), _sc(qs), _ptr(k), _sc(ks), _ptr(v), _sc(vs), pos,
                                _ptr(o), C.byref(os_))
     return o, (os_.mant, os_.shift)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# MoeMlp at the reference's semantics (kt_oracle_refdec.c: route / route_sigmoid, combine, merge_rows, the shared
+# expert; crates/01-engine/kt-core/src/layers.rs:652-1020, router.rs:29-79)
+
+
+class RefMoe:
+    """The reference tests' MoE (tests.rs:113-150, tests_glm.rs:31-43, 224-228) built by the oracle from the seeded
+    float weights: the stream from `seed` draws the router then each expert's gate / up / down. sigmoid: 0 softmax
+    router, 1 sigmoid router with bias vecf(bias_seed, E) * 0.05, 2 sigmoid router with a zero bias."""
+
+    def __init__(self, seed: int, dim: int, E: int, top_k: int, hidden: int, norm_topk: bool = False,
+                 sigmoid: int = 0, bias_seed: int = 0, shared_hidden: int = 0):
+        self.dim, self.E, self.top_k, self.hidden, self.shared_hidden = dim, E, top_k, hidden, shared_hidden
+        self.norm_topk, self.sigmoid = bool(norm_topk), sigmoid
+        self.ptr = lib().kt_rm_synthetic(seed, dim, E, top_k, hidden, int(norm_topk), int(sigmoid == 1), bias_seed,
+                                         shared_hidden)
+        if sigmoid == 2:  # a sigmoid router with zero bias: the coded bias is already 0 when sigmoid == 0
+            self.ptr2 = None
+            lib().kt_rm_free(self.ptr)
+            self.ptr = lib().kt_rm_synthetic(seed, dim, E, top_k, hidden, int(norm_topk), 1, bias_seed, shared_hidden)
+            for e in range(E):
+                lib().kt_rm_set_bias(self.ptr, e, 0.0)
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            lib().kt_rm_free(self.ptr)
+            self.ptr = None
+
+    def set_bias(self, e: int, b: float) -> None:
+        lib().kt_rm_set_bias(self.ptr, e, float(b))
+
+    def route(self, x_row, xs):
+        """(experts, ec, sumc, logits codes, logits scale) of MoeMlp::route for one token row."""
+        x = _c(x_row, np.int32)
+        sel, ec = np.zeros(self.top_k, np.int32), np.zeros(self.top_k, np.int64)
+        lg, ls = np.zeros(self.E, np.int32), Scale()
+        sumc = lib().kt_rm_route(self.ptr, _ptr(x), _sc(xs), _ptr(sel), _ptr(ec), _ptr(lg), C.byref(ls))
+        return sel.tolist(), ec, int(sumc), lg, (ls.mant, ls.shift)
+
+    def sigmoid_codes(self, logits, ls):
+        lg = _c(logits, np.int32)
+        out = np.zeros(lg.size, np.int64)
+        lib().kt_rm_sigmoid_codes(self.ptr, _ptr(lg), lg.size, _sc(ls), _ptr(out))
+        return out
+
+    def forward(self, x, T: int, xs):
+        """MoeMlp::forward_int of T rows: (codes T x dim, (mant, shift))."""
+        x = _c(x, np.int32)
+        out, os_ = np.zeros(T * self.dim, np.int32), Scale()
+        lib().kt_rm_forward(self.ptr, _ptr(x), T, _sc(xs), _ptr(out), C.byref(os_))
+        return out, (os_.mant, os_.shift)
+
+    def expert(self, e: int, x, rows: int, xs):
+        """SwiGluMlp::forward_int of expert e (e == E: the shared expert)."""
+        x = _c(x, np.int32)
+        y, ys = np.zeros(rows * self.dim, np.int32), Scale()
+        lib().kt_rm_expert(self.ptr, e, _ptr(x), rows, _sc(xs), _ptr(y), C.byref(ys))
+        return y, (ys.mant, ys.shift)
+
+    def ql(self, e: int, which: str):
+        """(codes out x in, (mant, shift)) of the router (which 'router') or expert e's gate / up / down."""
+        idx = {"router": 0, "gate": 1, "up": 2, "down": 3}[which]
+        o, i = _SZ(), _SZ()
+        lib().kt_rm_get_ql(self.ptr, e, idx, None, C.byref(o), C.byref(i))
+        codes = np.zeros(o.value * i.value, np.int32)
+        s = lib().kt_rm_get_ql(self.ptr, e, idx, _ptr(codes), C.byref(o), C.byref(i))
+        return codes.reshape(o.value, i.value), (s.mant, s.shift)
+
+    def lut(self, which: str):
+        codes = np.zeros(1 << 16, np.int64)
+        inv, cs, lo = Scale(), Scale(), C.c_int64()
+        lib().kt_rm_get_lut(self.ptr, {"exp": 0, "sigmoid": 1, "silu": 2}[which], _ptr(codes), C.byref(inv),
+                            C.byref(lo), C.byref(cs))
+        return codes, (inv.mant, inv.shift), lo.value, (cs.mant, cs.shift)
+
+    def bias(self) -> np.ndarray:
+        b = np.zeros(self.E, np.int64)
+        lib().kt_rm_get_bias(self.ptr, _ptr(b))
+        return b
+
+
+def rm_probe(s: int, n: int):
+    """IntTensor::from_reals of the reference tests' probe (tests.rs:29-32): (codes, scale, the advanced stream)."""
+    st = C.c_uint64(s)
+    out = np.zeros(n, np.int32)
+    sc = lib().kt_rm_probe(C.byref(st), n, _ptr(out))
+    return out, (sc.mant, sc.shift), st.value
+
+
+def rm_combine(ys, ys_s, out_dim: int, ec, sumc: int):
+    k = len(ys_s)
+    y = _c(ys, np.int32)
+    sarr = (Scale * k)(*[Scale(int(a), int(b)) for a, b in ys_s])
+    ec = _c(ec, np.int64)
+    out, os_ = np.zeros(out_dim, np.int32), Scale()
+    lib().kt_rm_combine(_ptr(y), sarr, k, out_dim, _ptr(ec), sumc, _ptr(out), C.byref(os_))
+    return out, (os_.mant, os_.shift)
+
+
+def rm_merge_rows(rows, rs, T: int, dim: int):
+    r = _c(rows, np.int32)
+    sarr = (Scale * T)(*[Scale(int(a), int(b)) for a, b in rs])
+    out, os_ = np.zeros(T * dim, np.int32), Scale()
+    lib().kt_rm_merge_rows(_ptr(r), sarr, T, dim, _ptr(out), C.byref(os_))
+    return out, (os_.mant, os_.shift)
