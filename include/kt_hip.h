@@ -145,6 +145,7 @@ typedef struct {
 } kt_hip_codelut;
 #define KT_LUT_EXP 0  /* exp(x): the softmax table of Attention::new and MoeMlp::new */
 #define KT_LUT_SILU 1 /* x / (1 + exp(-x)): SwiGluMlp::new's SiLU */
+#define KT_LUT_SIGMOID 2 /* 1 / (1 + exp(-x)): SigmoidScore::new's router score (router.rs:38-49) */
 #define KT_REF_MAX_HEADS 64
 #define KT_REF_ATTN_LDS 65536 /* the attention step's LDS: 40 B per cached position + 12 B per q value + 8 KB */
 
@@ -171,10 +172,11 @@ int kt_hip_ref_rmsnorm(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_de
 /* add (layers.rs:121-136), the residual add of n codes: y_dev may alias a_dev or b_dev, ys_dev as_dev or bs_dev. */
 int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
                    const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
-/* SwiGluMlp::forward_int's activation (layers.rs:615-637): h = requant_dyn(silu_code(g) * u) of n values, the SiLU
- * CodeLut (right_identity set) with its codes at silu_codes_dev. */
+/* SwiGluMlp::forward_int's activation (layers.rs:615-637): h = requant_dyn(silu_code(g) * u), the SiLU CodeLut
+ * (right_identity set) with its codes at silu_codes_dev, for `rows` tensors of n values each, row r with its own
+ * records gs_dev[r], us_dev[r], hs_dev[r] (rows = 1: one tensor; rows > 1: the per-token expert calls of a MoE). */
 int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
-                      const kt_hip_qscale* us_dev, int64_t n, const int64_t* silu_codes_dev,
+                      const kt_hip_qscale* us_dev, int64_t rows, int64_t n, const int64_t* silu_codes_dev,
                       const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream);
 /* Attention::decode_step between its projections (attention.rs:358-458) at the position pos_dev[0]: RoPE of the q
  * (nh x hd) and k (nkv x hd) codes by the tables cos_dev / sin_dev (max_seq x hd/2), the rotated k and the v codes
@@ -195,6 +197,51 @@ int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale
  * step_dev[0], which then advances (the per-step logits hash_step covers, generate.rs:58-64). */
 int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hip_qscale* ls_dev, int32_t* token_dev,
                       int32_t* record_dev, kt_hip_sscale* rscale_dev, int32_t* step_dev, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * The reference's MoeMlp at its own semantics (crates/01-engine/kt-core/src/layers.rs:652-1020, router.rs:29-79):
+ * every router and expert call is a QuantLinear of one token row; the rows are grouped by their weights only at the
+ * product, which is exact.
+ * ------------------------------------------------------------------------------------------------------------- */
+#define KT_REF_MOE_MAX_E 4096 /* experts a route call takes (their codes live in LDS) */
+#define KT_REF_MOE_MAX_K 32    /* top-k a route or combine call takes */
+/* QuantLinear::forward_int (layers.rs:275-328) applied to each of `rows` rows on its own, as the reference's per-token
+ * calls run it: output row r is forward_int of input row xidx_dev[r] of x_dev (x_rows x in_f; xidx_dev NULL: row
+ * r; an index outside [0, x_rows) reads as zeros) at the scale record xs_dev[xs_step * r] (xs_step 0: one record
+ * for every row, 1: one per row), quantized by its own max |x|, requantized by its own max |acc|, against the weights
+ * of the group g holding r (rows off[g] .. off[g + 1] - 1; off_host and off_dev the same groups + 1 offsets, on the
+ * host and on the device, off[0] = 0, off[groups] = rows): pw digit planes of out_f x in_f codes at w_planes_dev +
+ * g * w_group_bytes (kt_hip_pack_planes), Scale (w_mant_dev[g], w_shift_dev[g]). No bias. y_dev: rows x out_f codes,
+ * ys_dev: rows records. ws_dev: the caller's workspace of kt_hip_quant_linear_rows_workspace bytes. */
+size_t kt_hip_quant_linear_rows_workspace(int64_t rows, int64_t in_f, int64_t out_f);
+int kt_hip_quant_linear_rows(int dev, const int32_t* x_dev, const int32_t* xidx_dev, int64_t x_rows, int64_t rows,
+                             int64_t in_f, const kt_hip_qscale* xs_dev, int xs_step, int64_t groups,
+                             const int64_t* off_host, const int64_t* off_dev, const int8_t* w_planes_dev,
+                             size_t w_group_bytes, int pw, int64_t out_f, const int64_t* w_mant_dev,
+                             const int32_t* w_shift_dev, void* ws_dev, size_t ws_bytes, int32_t* y_dev,
+                             kt_hip_qscale* ys_dev, void* stream);
+/* MoeMlp::route / route_sigmoid (layers.rs:826-870; router.rs:61-71) of `tokens` rows of router logits (experts
+ * codes each, row t at the record ls_dev[t]): softmax (sigmoid 0): the numerators exp(l - lmax) from the exp CodeLut
+ * (codes_dev, lut; 0 below the table), top-k by logit code; sigmoid (sigmoid 1): the sigma codes from its CodeLut,
+ * top-k by code + bias_dev[e] (the coded selection bias, round(b * 2^20)). Ties go to the lower index. sel_dev /
+ * ec_dev: tokens x top_k experts and numerators in rank order; sumc_dev: the normalizer (norm_topk: the top-k sum;
+ * else softmax: the sum over every expert, sigmoid: 2^20). */
+int kt_hip_ref_moe_route(int dev, const int32_t* logits_dev, int64_t tokens, int64_t experts, int top_k,
+                         const kt_hip_qscale* ls_dev, int sigmoid, int norm_topk, const int64_t* codes_dev,
+                         const kt_hip_codelut* lut, const int64_t* bias_dev, int32_t* sel_dev, int64_t* ec_dev,
+                         int64_t* sumc_dev, void* stream);
+/* MoeMlp::combine (layers.rs:893-923) for each token: the top_k expert outputs at rows pos_dev[t * top_k + i] of
+ * y_dev (y_rows rows of dim codes, records ys_dev; a row index outside them contributes nothing) brought to their
+ * largest scale, summed with the numerators ec_dev, requantized, 1/sumc folded into the scale; zeros at Scale::ZERO
+ * when sumc <= 0. out_dev: tokens x dim codes, os_dev: tokens records. */
+int kt_hip_ref_moe_combine(int dev, const int32_t* y_dev, const kt_hip_qscale* ys_dev, int64_t y_rows, int64_t dim,
+                           const int32_t* pos_dev, const int64_t* ec_dev, const int64_t* sumc_dev, int64_t tokens,
+                           int top_k, int32_t* out_dev, kt_hip_qscale* os_dev, void* stream);
+/* merge_rows (layers.rs:873-891): tokens rows of dim codes, row t at the record rs_dev[t], brought to the largest row
+ * scale (of equal values the latest row's) and requantized as one tensor: out_dev and os_dev. */
+size_t kt_hip_ref_merge_rows_workspace(int64_t tokens);
+int kt_hip_ref_merge_rows(int dev, const int32_t* rows_dev, const kt_hip_qscale* rs_dev, int64_t tokens, int64_t dim,
+                          void* ws_dev, size_t ws_bytes, int32_t* out_dev, kt_hip_qscale* os_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Backend layer: one LinearBackend on one device (kt_cuda::open, lib.rs:252; TcLinear, backend.rs:77-192).

@@ -1,0 +1,154 @@
+"""The reference's MoeMlp at its own semantics on the GPU, through the C ABI, against the oracle's restatement
+(oracle/kt_oracle_refdec.c, pinned by the reference's own MoE tests in tests/test_refmoe.py): the row-wise grouped
+QuantLinear against per-row forward_int calls, route and combine per token, merge_rows, and whole layers -- the
+reference tests' softmax MoE (one token and a sequence), the GLM-like sigmoid MoE with its bias and shared expert,
+and a larger GLM-shaped layer -- codes and Scales bit for bit."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+WL = 265720
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def recs(torch, scales):
+    w = np.zeros((len(scales), 4), dtype=np.int64)
+    for i, (m, s) in enumerate(scales):
+        w[i, 0] = m
+        w[i].view(np.int32)[2] = s
+    return torch.from_numpy(w.reshape(-1)).cuda()
+
+
+def read_recs(t, n):
+    w = t.cpu().numpy().reshape(n, 4)
+    return [(int(r[0]), int(r.view(np.int32)[2])) for r in w]
+
+
+def i32(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32).reshape(-1)).cuda()
+
+
+def test_quant_linear_rows_grouped(torch_dev):
+    """Each output row is forward_int of its own input row (own xmax, own ymax) against its group's weights; rows
+    picked by index (one past the input reads as zeros), per-row input scales, an empty group, a zero row."""
+    torch = torch_dev
+    import tritify_amd as T
+    from tritify_amd import backend as B
+
+    say("case: quant_linear_rows G=4 rows=37 in=300 out=70")
+    rng = np.random.default_rng(5)
+    G, inp, out, x_rows = 4, 300, 70, 12
+    counts = [10, 0, 20, 7]
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    P = int(off[-1])
+    x = rng.integers(-(2**28), 2**28, size=(x_rows, inp)).astype(np.int32)
+    x[3] = 0
+    xidx = rng.integers(0, x_rows, size=P).astype(np.int32)
+    xidx[5] = x_rows  # outside x: a zero row
+    xs = [(int(rng.integers(2**30, 2**31)), int(rng.integers(50, 60))) for _ in range(P)]
+    ws = [(int(rng.integers(2**30, 2**31)), int(rng.integers(40, 50))) for _ in range(G)]
+    w = rng.integers(-WL, WL + 1, size=(G, out, inp)).astype(np.int32)
+    pw = 3
+    kp = T.kp(inp)
+    gbytes = pw * out * kp
+    planes = torch.empty(G * gbytes, dtype=torch.int8, device="cuda")
+    for g in range(G):
+        T.pack_planes(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
+    n = B.quant_linear_rows_workspace(P, inp, out)
+    wsb = torch.empty(n, dtype=torch.uint8, device="cuda")
+    y = torch.empty(P * out, dtype=torch.int32, device="cuda")
+    ys = torch.zeros(P * 4, dtype=torch.int64, device="cuda")
+    B.quant_linear_rows(i32(torch, x), i32(torch, xidx), x_rows, P, inp, recs(torch, xs), 1, off,
+                        torch.from_numpy(off).cuda(), planes, gbytes, pw, out,
+                        torch.from_numpy(np.array([a for a, _ in ws], np.int64)).cuda(),
+                        torch.from_numpy(np.array([b for _, b in ws], np.int32)).cuda(), wsb, n, y, ys)
+    got, got_s = y.cpu().numpy().reshape(P, out), read_recs(ys, P)
+    for r in range(P):
+        g = int(np.searchsorted(off, r, side="right") - 1)
+        xr = x[xidx[r]] if xidx[r] < x_rows else np.zeros(inp, np.int32)
+        yo, so, _, _ = O.quant_linear_forward(xr, 1, inp, xs[r], w[g].reshape(-1), out, ws[g])
+        assert np.array_equal(got[r], yo.reshape(-1)), r
+        assert got_s[r] == so, r
+
+
+def layer_from(m: O.RefMoe, dev_sigmoid: bool):
+    from tritify_amd.refmoe import RefMoeLayer
+
+    experts = [{n: m.ql(e, n) for n in ("gate", "up", "down")} for e in range(m.E)]
+    shared = {n: m.ql(m.E, n) for n in ("gate", "up", "down")} if m.shared_hidden else None
+    return RefMoeLayer(m.dim, m.ql(0, "router"), experts, m.top_k, m.norm_topk,
+                       m.bias() if dev_sigmoid else None, shared)
+
+
+@pytest.mark.parametrize("case", [
+    dict(seed=0x30E1, dim=64, E=8, k=2, hidden=96, norm=False, sig=0, bseed=0, shared=0, T=1),
+    dict(seed=0x30E1, dim=64, E=8, k=2, hidden=96, norm=False, sig=0, bseed=0, shared=0, T=5),
+    dict(seed=0x5C, dim=32, E=16, k=4, hidden=24, norm=True, sig=1, bseed=0x5C, shared=40, T=6),
+    dict(seed=0x91, dim=256, E=32, k=4, hidden=128, norm=True, sig=1, bseed=0x92, shared=192, T=40),
+    dict(seed=0x93, dim=128, E=16, k=2, hidden=64, norm=False, sig=1, bseed=0x94, shared=0, T=9),
+])
+def test_moe_layer_against_the_oracle(torch_dev, case):
+    torch = torch_dev
+    c = case
+    say(f"case: ref moe {c}")
+    m = O.RefMoe(c["seed"], c["dim"], c["E"], c["k"], c["hidden"], c["norm"], c["sig"], c["bseed"], c["shared"])
+    layer = layer_from(m, c["sig"] == 1)
+    x, xs, _ = O.rm_probe(c["seed"] + 1, c["T"] * c["dim"])
+    xd, xr = i32(torch, x), recs(torch, [xs])
+    # route, token by token
+    sel, ec, sumc, logits, ls = layer.route(xd, xr, c["T"])
+    sel, ec, sumc = sel.cpu().numpy().reshape(c["T"], c["k"]), ec.cpu().numpy().reshape(c["T"], c["k"]), \
+        sumc.cpu().numpy()
+    lg, lsr = logits.cpu().numpy().reshape(c["T"], c["E"]), read_recs(ls, c["T"])
+    for t in range(c["T"]):
+        so, eo, sumo, lo, lso = m.route(x[t * c["dim"]:(t + 1) * c["dim"]], xs)
+        assert np.array_equal(lg[t], lo) and lsr[t] == lso, f"logits of token {t}"
+        assert sel[t].tolist() == so and np.array_equal(ec[t], eo) and sumc[t] == sumo, f"route of token {t}"
+    out, orec = layer.forward(xd, xr, c["T"])
+    want, ws = m.forward(x, c["T"], xs)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, want), f"codes differ at {np.argwhere(got != want)[:5].tolist()}"
+    assert read_recs(orec, 1)[0] == ws
+
+
+def test_combine_and_merge_against_the_oracle(torch_dev):
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say("case: ref moe combine / merge_rows")
+    rng = np.random.default_rng(21)
+    T, K, dim = 7, 3, 50
+    P = T * K
+    y = rng.integers(-(2**28), 2**28 + 1, size=(P, dim)).astype(np.int32)
+    ys = [(int(rng.integers(2**30, 2**31)), int(rng.integers(55, 62))) for _ in range(P)]
+    ys[4] = (0, 0)
+    ys[7] = (ys[8][0] * 2 if ys[8][0] < 2**31 else ys[8][0], ys[8][1] + (1 if ys[8][0] < 2**31 else 0))  # equal values
+    pos = rng.permutation(P).astype(np.int32)
+    ec = rng.integers(0, 1 << 20, size=P).astype(np.int64)
+    sumc = np.array([int(ec[t * K:(t + 1) * K].sum()) for t in range(T)], np.int64)
+    sumc[2] = 0  # the zero path
+    out = torch.empty(T * dim, dtype=torch.int32, device="cuda")
+    os_ = torch.zeros(T * 4, dtype=torch.int64, device="cuda")
+    B.ref_moe_combine(i32(torch, y), recs(torch, ys), P, dim, i32(torch, pos), torch.from_numpy(ec).cuda(),
+                      torch.from_numpy(sumc).cuda(), T, K, out, os_)
+    got, got_s = out.cpu().numpy().reshape(T, dim), read_recs(os_, T)
+    for t in range(T):
+        rows = [pos[t * K + i] for i in range(K)]
+        wo, wso = O.rm_combine(y[rows].reshape(-1), [ys[r] for r in rows], dim, ec[t * K:(t + 1) * K], int(sumc[t]))
+        assert np.array_equal(got[t], wo) and got_s[t] == wso, t
+    rs = [ys[i] for i in range(T)]
+    n = B.ref_merge_rows_workspace(T)
+    wsb = torch.empty(n, dtype=torch.uint8, device="cuda")
+    mo = torch.empty(T * dim, dtype=torch.int32, device="cuda")
+    mrec = torch.zeros(4, dtype=torch.int64, device="cuda")
+    B.ref_merge_rows(i32(torch, y[:T]), recs(torch, rs), T, dim, wsb, n, mo, mrec)
+    wo, wso = O.rm_merge_rows(y[:T].reshape(-1), rs, T, dim)
+    assert np.array_equal(mo.cpu().numpy(), wo) and read_recs(mrec, 1)[0] == wso

@@ -116,7 +116,14 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_embed": (_I, [_I, _P, _I64, C.c_int32, _P, _I64, _I64, _P, _P, _P]),
         "kt_hip_ref_rmsnorm": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _P, _P]),
         "kt_hip_ref_add": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P]),
-        "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_quant_linear_rows_workspace": (_SZ, [_I64, _I64, _I64]),
+        "kt_hip_quant_linear_rows": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _P, _P, _P, _SZ, _I, _I64, _P,
+                                          _P, _P, _SZ, _P, _P, _P]),
+        "kt_hip_ref_moe_route": (_I, [_I, _P, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_moe_combine": (_I, [_I, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I, _P, _P, _P]),
+        "kt_hip_ref_merge_rows_workspace": (_SZ, [_I64]),
+        "kt_hip_ref_merge_rows": (_I, [_I, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_attention_step": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
                                            _P, _P, _I64, C.c_int32, _P, _P, _P, _P, _P]),
         "kt_hip_ref_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P, _P, _P]),
@@ -526,7 +533,7 @@ def gen_quant_rows_fast(seed: int, rows: int, cols: int) -> np.ndarray:
 # The reference decoder's layers at the reference's own semantics (crates/01-engine/kt-core/src/{layers,attention,
 # model,generate}.rs): i32 codes at the 2^28 level with one kt-int Scale per tensor, in 32-byte device records.
 # ---------------------------------------------------------------------------------------------------------------
-LUT_EXP, LUT_SILU = 0, 1
+LUT_EXP, LUT_SILU, LUT_SIGMOID = 0, 1, 2
 REF_MAX_HEADS = 64
 
 
@@ -582,9 +589,11 @@ def ref_add(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, stream=None, de
 
 
 def ref_swiglu(g_dev, gs_dev, u_dev, us_dev, n: int, silu_codes_dev, silu: CodeLut, h_dev, hs_dev, stream=None,
-               dev: int = 0) -> None:
-    check(lib().kt_hip_ref_swiglu(dev, _ptr(g_dev), _ptr(gs_dev), _ptr(u_dev), _ptr(us_dev), n, _ptr(silu_codes_dev),
-                                  C.byref(silu), _ptr(h_dev), _ptr(hs_dev), _stream(stream)), "ref swiglu")
+               dev: int = 0, rows: int = 1) -> None:
+    """SwiGluMlp's activation of `rows` tensors of n values (row r with its own records at index r)."""
+    check(lib().kt_hip_ref_swiglu(dev, _ptr(g_dev), _ptr(gs_dev), _ptr(u_dev), _ptr(us_dev), rows, n,
+                                  _ptr(silu_codes_dev), C.byref(silu), _ptr(h_dev), _ptr(hs_dev), _stream(stream)),
+          "ref swiglu")
 
 
 def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh: int, nkv: int, hd: int,
@@ -602,3 +611,45 @@ def ref_argmax(logits_dev, n: int, ls_dev, token_dev, record_dev=None, rscale_de
                dev: int = 0) -> None:
     check(lib().kt_hip_ref_argmax(dev, _ptr(logits_dev), n, _ptr(ls_dev), _ptr(token_dev), _ptr(record_dev),
                                   _ptr(rscale_dev), _ptr(step_dev), _stream(stream)), "ref argmax")
+
+
+REF_MOE_MAX_K = 32
+
+
+def quant_linear_rows_workspace(rows: int, in_f: int, out_f: int) -> int:
+    return lib().kt_hip_quant_linear_rows_workspace(rows, in_f, out_f)
+
+
+def quant_linear_rows(x_dev, xidx_dev, x_rows: int, rows: int, in_f: int, xs_dev, xs_step: int, off_host, off_dev,
+                      w_planes_dev, w_group_bytes: int, pw: int, out_f: int, w_mant_dev, w_shift_dev, ws_dev,
+                      ws_bytes: int, y_dev, ys_dev, stream=None, dev: int = 0) -> None:
+    """QuantLinear::forward_int on each row on its own, rows grouped by weights (off: groups + 1 offsets)."""
+    off = np.ascontiguousarray(off_host, dtype=np.int64)
+    check(lib().kt_hip_quant_linear_rows(dev, _ptr(x_dev), _ptr(xidx_dev), x_rows, rows, in_f, _ptr(xs_dev), xs_step,
+                                         off.size - 1, off.ctypes.data, _ptr(off_dev), _ptr(w_planes_dev),
+                                         w_group_bytes, pw, out_f, _ptr(w_mant_dev), _ptr(w_shift_dev), _ptr(ws_dev),
+                                         ws_bytes, _ptr(y_dev), _ptr(ys_dev), _stream(stream)), "quant linear rows")
+
+
+def ref_moe_route(logits_dev, tokens: int, experts: int, top_k: int, ls_dev, sigmoid: bool, norm_topk: bool,
+                  codes_dev, lut: CodeLut, bias_dev, sel_dev, ec_dev, sumc_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_ref_moe_route(dev, _ptr(logits_dev), tokens, experts, top_k, _ptr(ls_dev), int(sigmoid),
+                                     int(norm_topk), _ptr(codes_dev), C.byref(lut), _ptr(bias_dev), _ptr(sel_dev),
+                                     _ptr(ec_dev), _ptr(sumc_dev), _stream(stream)), "ref moe route")
+
+
+def ref_moe_combine(y_dev, ys_dev, y_rows: int, dim: int, pos_dev, ec_dev, sumc_dev, tokens: int, top_k: int, out_dev,
+                    os_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_ref_moe_combine(dev, _ptr(y_dev), _ptr(ys_dev), y_rows, dim, _ptr(pos_dev), _ptr(ec_dev),
+                                       _ptr(sumc_dev), tokens, top_k, _ptr(out_dev), _ptr(os_dev), _stream(stream)),
+          "ref moe combine")
+
+
+def ref_merge_rows_workspace(tokens: int) -> int:
+    return lib().kt_hip_ref_merge_rows_workspace(tokens)
+
+
+def ref_merge_rows(rows_dev, rs_dev, tokens: int, dim: int, ws_dev, ws_bytes: int, out_dev, os_dev, stream=None,
+                   dev: int = 0) -> None:
+    check(lib().kt_hip_ref_merge_rows(dev, _ptr(rows_dev), _ptr(rs_dev), tokens, dim, _ptr(ws_dev), ws_bytes,
+                                      _ptr(out_dev), _ptr(os_dev), _stream(stream)), "ref merge rows")

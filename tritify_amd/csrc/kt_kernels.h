@@ -92,8 +92,23 @@ hipError_t launch_rd_rmsnorm(const int32_t* x, int rows, int dim, const kt_hip_q
 hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_t* b, const kt_hip_qscale* bs, int n,
                          int32_t* y, kt_hip_qscale* ys, hipStream_t s);
 hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
-                            int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h, kt_hip_qscale* hs,
-                            hipStream_t s);
+                            int rows, int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h,
+                            kt_hip_qscale* hs, hipStream_t s);
+size_t rq_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[3]);
+hipError_t launch_quant_linear_rows(const int32_t* x, const int32_t* xidx, int64_t x_rows, int64_t rows, int64_t in,
+                                    const kt_hip_qscale* xs, int xs_step, int groups, const int64_t* off_host,
+                                    const int64_t* off_dev, const int8_t* wb, size_t wgroup, int pw, int64_t out,
+                                    const int64_t* wm_dev, const int32_t* wsh_dev, int64_t flush_k, void* ws,
+                                    int32_t* y, kt_hip_qscale* ys, hipStream_t s);
+hipError_t launch_rm_route(const int32_t* logits, int T, int E, int top_k, const kt_hip_qscale* ls, int sigmoid,
+                           int norm_topk, const int64_t* codes, const kt_hip_codelut* lut, const int64_t* bias,
+                           int32_t* sel, int64_t* ec, int64_t* sumc, hipStream_t s);
+hipError_t launch_rm_combine(const int32_t* y, const kt_hip_qscale* ys, int y_rows, int dim, const int32_t* pos,
+                             const int64_t* ec, const int64_t* sumc, int T, int top_k, int32_t* out,
+                             kt_hip_qscale* os, hipStream_t s);
+size_t rm_merge_workspace_bytes(int64_t T);
+hipError_t launch_rm_merge_rows(const int32_t* rows, const kt_hip_qscale* rs, int T, int dim, void* ws, int32_t* out,
+                                kt_hip_qscale* os, hipStream_t s);
 hipError_t launch_rd_attention_step(const RdAttn& a, hipStream_t s);
 hipError_t launch_rd_argmax(const int32_t* logits, int n, const kt_hip_qscale* ls, int32_t* token, int32_t* record,
                             kt_hip_sscale* rscale, int32_t* step, hipStream_t s);

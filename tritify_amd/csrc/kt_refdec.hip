@@ -233,6 +233,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, co
 
 // SwiGluMlp::forward_int's activation (layers.rs:615-637): h = silu_code(g) * u, the SiLU code from the CodeLut at
 // g's scale (0 below the table, the identity tail g * gs / code_scale above it), requantized at code_scale * us.
+// One CTA per row: row r's n values with its own records gs_rec[r], us_rec[r], hs[r] (rows = 1: one tensor).
 __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __restrict__ g,
                                                                const kt_hip_qscale* __restrict__ gs_rec,
                                                                const int32_t* __restrict__ u,
@@ -241,6 +242,10 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
                                                                int32_t* __restrict__ h,
                                                                kt_hip_qscale* __restrict__ hs) {
     __shared__ int64_t red[RD_WAVES];
+    {
+        const int64_t r = blockIdx.x;
+        g += r * n, u += r * n, h += r * n, gs_rec += r, us_rec += r, hs += r;
+    }
     __shared__ Sc par[3];  // index factor, identity factor, h scale
     if (threadIdx.x == 0) {
         const Sc gs = rec_sc(gs_rec), us = rec_sc(us_rec), cs{L.code_mant, L.code_shift};
@@ -467,9 +472,9 @@ hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_
     return hipGetLastError();
 }
 hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
-                            int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h, kt_hip_qscale* hs,
-                            hipStream_t s) {
-    rd_swiglu_kernel<<<1, RD_THREADS, 0, s>>>(g, gs, u, us, n, codes, *lut, h, hs);
+                            int rows, int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h,
+                            kt_hip_qscale* hs, hipStream_t s) {
+    rd_swiglu_kernel<<<(unsigned)rows, RD_THREADS, 0, s>>>(g, gs, u, us, n, codes, *lut, h, hs);
     return hipGetLastError();
 }
 hipError_t launch_rd_attention_step(const RdAttn& a, hipStream_t s) {
@@ -531,14 +536,14 @@ extern "C" int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale
 }
 
 extern "C" int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
-                                 const kt_hip_qscale* us_dev, int64_t n, const int64_t* silu_codes_dev,
+                                 const kt_hip_qscale* us_dev, int64_t rows, int64_t n, const int64_t* silu_codes_dev,
                                  const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream) {
-    if (!g_dev || !gs_dev || !u_dev || !us_dev || !silu_codes_dev || !silu || !h_dev || !hs_dev || n < 1 ||
-        n > RD_MAX_N || silu->n < 1 || !silu->right_identity)
+    if (!g_dev || !gs_dev || !u_dev || !us_dev || !silu_codes_dev || !silu || !h_dev || !hs_dev || rows < 1 ||
+        rows > INT32_MAX || n < 1 || n > RD_MAX_N || silu->n < 1 || !silu->right_identity)
         return (int)hipErrorInvalidValue;
     RD_TRY(hipSetDevice(dev));
-    return (int)kt::launch_rd_swiglu(g_dev, gs_dev, u_dev, us_dev, (int)n, silu_codes_dev, silu, h_dev, hs_dev,
-                                     (hipStream_t)stream);
+    return (int)kt::launch_rd_swiglu(g_dev, gs_dev, u_dev, us_dev, (int)rows, (int)n, silu_codes_dev, silu, h_dev,
+                                     hs_dev, (hipStream_t)stream);
 }
 
 extern "C" int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
@@ -616,6 +621,8 @@ static double rd_lut_fn(int kind, double x) {
             return exp(x);
         case KT_LUT_SILU:
             return x / (1.0 + exp(-x));
+        case KT_LUT_SIGMOID:
+            return 1.0 / (1.0 + exp(-x));
         default:
             return 0.0;
     }
@@ -623,7 +630,7 @@ static double rd_lut_fn(int kind, double x) {
 
 extern "C" int kt_hip_ref_codelut(int kind, double lo, double hi, int idx_bits, int code_bits, int right_identity,
                                   int64_t* codes, kt_hip_codelut* lut) {
-    if ((kind != KT_LUT_EXP && kind != KT_LUT_SILU) || idx_bits < 1 || idx_bits > 24 || code_bits < 0 ||
+    if ((kind != KT_LUT_EXP && kind != KT_LUT_SILU && kind != KT_LUT_SIGMOID) || idx_bits < 1 || idx_bits > 24 || code_bits < 0 ||
         code_bits > 52 || !(hi > lo) || !lut)
         return (int)hipErrorInvalidValue;
     const int64_t n = (int64_t)1 << idx_bits;

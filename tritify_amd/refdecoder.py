@@ -129,7 +129,7 @@ class RefDecoder:
             self._ql(blk["gate"], "h", "g", stream)
             self._ql(blk["up"], "h", "u", stream)
             B.ref_swiglu(b["g"], r["g"], b["u"], r["u"], self.hidden, self.silu_codes, self.silu_lut, b["hh"],
-                         r["hh"], stream, dv)
+                         r["hh"], stream, dv)  # one tensor (rows = 1)
             self._ql(blk["down"], "hh", "m", stream)
             B.ref_add(b["x"], r["x"], b["m"], r["m"], self.dim, b["x"], r["x"], stream, dv)
         g, gs = self.final_norm
