@@ -146,6 +146,8 @@ typedef struct {
 #define KT_LUT_EXP 0  /* exp(x): the softmax table of Attention::new and MoeMlp::new */
 #define KT_LUT_SILU 1 /* x / (1 + exp(-x)): SwiGluMlp::new's SiLU */
 #define KT_LUT_SIGMOID 2 /* 1 / (1 + exp(-x)): SigmoidScore::new's router score (router.rs:38-49) */
+#define KT_LUT_GELU 3    /* 0.5 x (1 + erf(x / sqrt 2)), erf by A&S 7.1.26: build_gelu_lut (kt-model-vision/src/
+                            nonlin.rs:7-26) */
 #define KT_REF_MAX_HEADS 64
 #define KT_REF_ATTN_LDS 65536 /* the attention step's LDS: 40 B per cached position + 12 B per q value + 8 KB */
 
@@ -159,6 +161,12 @@ int kt_hip_ref_codelut(int kind, double lo, double hi, int idx_bits, int code_bi
                        int64_t* codes, kt_hip_codelut* lut);
 int kt_hip_ref_rope_tables(int64_t max_seq, int64_t rot_dim, double theta, kt_hip_sscale* cos_tab,
                            kt_hip_sscale* sin_tab);
+/* IntTensor::from_reals (crates/01-engine/kt-core/src/tensor.rs:106-117), the model's entry quantization (SAM's
+ * pixels, kt-model-vision/src/plugin.rs:38): codes round(v * levels / max |v|) (half away from zero) at
+ * Scale::from_f64(max / levels); all zeros give zeros at Scale::ZERO. Host only; non-finite values are an error
+ * (1 <= levels <= 2^30). */
+int kt_hip_ref_from_reals(const double* real, int64_t n, int64_t levels, int32_t* codes, int64_t* mant,
+                          int32_t* shift);
 
 /* Embedding::lookup (layers.rs:1127-1140): y (dim codes) and ys = the row of the token at token_dev[0] of the
  * vocab x dim code table at Scale (e_mant, e_shift); a token outside [0, vocab) gives zeros at Scale::ZERO. */
@@ -178,6 +186,26 @@ int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, c
 int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
                       const kt_hip_qscale* us_dev, int64_t rows, int64_t n, const int64_t* silu_codes_dev,
                       const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream);
+/* apply_gelu (crates/03-models/kt-model-vision/src/nonlin.rs:30-45) of n codes at xs_dev through the GELU CodeLut
+ * (KT_LUT_GELU over [-10, 10], 2^16 entries, 2^20 code scale, right_identity set; its codes at gelu_codes_dev): y_dev
+ * (may alias x_dev) at the table's code scale, written to ys_dev (which may not alias xs_dev). */
+int kt_hip_ref_gelu(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t n,
+                    const int64_t* gelu_codes_dev, const kt_hip_codelut* gelu, int32_t* y_dev, kt_hip_qscale* ys_dev,
+                    void* stream);
+/* Conv2d::forward_int (crates/01-engine/kt-core/src/conv.rs:68-130), SAM's PatchEmbed (kt-model-vision/src/
+ * hiera.rs:187-190): the image x_dev [ci][h][w] of i32 codes at xs_dev, quant_to by its whole-image max, the
+ * convolution against co x (ci kh kw) weight codes in the reference's [co][ci][kh][kw] order held as digit planes
+ * (kt_hip_pack_planes of that co x ci*kh*kw matrix, pw planes) at Scale (w_mant, w_shift), the optional i64 bias
+ * codes at (b_mant, b_shift) brought into the product's units, requant_dyn by the whole output's max. y_dev
+ * [co][oh][ow], oh = (h + 2 pad - kh) / stride + 1 (ow alike), and its record in os_dev; an all-zero image gives
+ * zeros at Scale::ZERO. The workspace holds kt_hip_ref_conv2d_workspace bytes (0: a shape out of range). */
+size_t kt_hip_ref_conv2d_workspace(int64_t ci, int64_t h, int64_t w, int64_t co, int64_t kh, int64_t kw,
+                                   int64_t stride, int64_t pad);
+int kt_hip_ref_conv2d(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t ci, int64_t h, int64_t w,
+                      const int8_t* w_planes_dev, int pw, int64_t co, int64_t kh, int64_t kw, int64_t stride,
+                      int64_t pad, int64_t w_mant, int32_t w_shift, const int64_t* bias_dev, int64_t b_mant,
+                      int32_t b_shift, void* ws_dev, size_t ws_bytes, int32_t* y_dev, kt_hip_qscale* os_dev,
+                      void* stream);
 /* Attention::decode_step between its projections (attention.rs:358-458) at the position pos_dev[0]: RoPE of the q
  * (nh x hd) and k (nkv x hd) codes by the tables cos_dev / sin_dev (max_seq x hd/2), the rotated k and the v codes
  * appended at row pos of kc_dev / vc_dev (max_seq x nkv hd) with their scales at kscale_dev / vscale_dev[pos], the

@@ -84,13 +84,14 @@ enum { LUT_EXP = 0, LUT_SILU = 1 };
 
 static double lut_f(int kind, double x) { return kind == LUT_EXP ? exp(x) : x / (1.0 + exp(-x)); }
 
-static void lut_build(rd_lut* L, int kind, double lo, double hi, unsigned idx_bits, unsigned code_bits, int right_id) {
+static void lut_build_f(rd_lut* L, double (*f)(double), double lo, double hi, unsigned idx_bits, unsigned code_bits,
+                        int right_id) {
     const size_t n = (size_t)1 << idx_bits;
     const double k = (double)(1ULL << code_bits);
     L->codes = (int64_t*)malloc(n * sizeof(int64_t));
     for (size_t i = 0; i < n; i++) {
         const double x = lo + (hi - lo) * ((double)i / (double)(n - 1));
-        L->codes[i] = (int64_t)round(lut_f(kind, x) * k);
+        L->codes[i] = (int64_t)round(f(x) * k);
     }
     const double inv_step = (double)(n - 1) / (hi - lo);
     L->inv_step_scale = kt_scale_from_f64(inv_step);
@@ -98,6 +99,12 @@ static void lut_build(rd_lut* L, int kind, double lo, double hi, unsigned idx_bi
     L->n = n;
     L->code_scale = kt_scale_from_f64(1.0 / k);
     L->right_identity = right_id;
+}
+
+static double f_exp(double x) { return lut_f(LUT_EXP, x); }
+static double f_silu(double x) { return lut_f(LUT_SILU, x); }
+static void lut_build(rd_lut* L, int kind, double lo, double hi, unsigned idx_bits, unsigned code_bits, int right_id) {
+    lut_build_f(L, kind == LUT_EXP ? f_exp : f_silu, lo, hi, idx_bits, code_bits, right_id);
 }
 
 /* CodeLut::index: round((data * scale - lo) * inv_step) with the build-time constants. */
@@ -667,25 +674,13 @@ enum { LUT_SIGMOID = 2 };
 
 static double lut_f2(int kind, double x) { return kind == LUT_SIGMOID ? 1.0 / (1.0 + exp(-x)) : lut_f(kind, x); }
 
+static double f_sigmoid(double x) { return lut_f2(LUT_SIGMOID, x); }
 static void lut_build2(rd_lut* L, int kind, double lo, double hi, unsigned idx_bits, unsigned code_bits,
                        int right_id) {
-    if (kind != LUT_SIGMOID) {
+    if (kind != LUT_SIGMOID)
         lut_build(L, kind, lo, hi, idx_bits, code_bits, right_id);
-        return;
-    }
-    const size_t n = (size_t)1 << idx_bits;
-    const double k = (double)(1ULL << code_bits);
-    L->codes = (int64_t*)malloc(n * sizeof(int64_t));
-    for (size_t i = 0; i < n; i++) {
-        const double x = lo + (hi - lo) * ((double)i / (double)(n - 1));
-        L->codes[i] = (int64_t)round(lut_f2(kind, x) * k);
-    }
-    const double inv_step = (double)(n - 1) / (hi - lo);
-    L->inv_step_scale = kt_scale_from_f64(inv_step);
-    L->lo_index = (int64_t)round(lo * inv_step);
-    L->n = n;
-    L->code_scale = kt_scale_from_f64(1.0 / k);
-    L->right_identity = right_id;
+    else
+        lut_build_f(L, f_sigmoid, lo, hi, idx_bits, code_bits, right_id);
 }
 
 static float unif_f32(uint64_t* s) {
@@ -1001,4 +996,157 @@ void kt_rm_set_bias(void* p, size_t e, float b) {
 void kt_rm_sigmoid_codes(const void* p, const int32_t* logits, size_t n, kt_scale ls, int64_t* out) {
     const kt_refmoe* M = (const kt_refmoe*)p;
     for (size_t j = 0; j < n; j++) out[j] = lut_code_at(&M->sig, lut_index(&M->sig, logits[j], ls));
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* The SAM 2.1 image path at the reference's semantics: Conv2d (crates/01-engine/kt-core/src/conv.rs:22-130),     */
+/* the pixel entry IntTensor::from_reals (tensor.rs:106-117), the GELU CodeLut and apply_gelu                      */
+/* (crates/03-models/kt-model-vision/src/nonlin.rs:7-47), FeedForward (hiera.rs:321-345)                           */
+/* ------------------------------------------------------------------------------------------------------------ */
+
+/* IntTensor::from_reals (tensor.rs:106-117): codes round(v * levels / max) at Scale::from_f64(max / levels). */
+kt_scale kt_rc_from_reals(const double* real, size_t n, int64_t levels, int32_t* out) {
+    double mx = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        const double a = fabs(real[i]);
+        mx = a > mx ? a : mx;
+    }
+    if (mx == 0.0) {
+        memset(out, 0, n * sizeof(int32_t));
+        return ZERO;
+    }
+    const double step = mx / (double)levels, inv = (double)levels / mx;
+    for (size_t i = 0; i < n; i++) out[i] = (int32_t)round(real[i] * inv);
+    return kt_scale_from_f64(step);
+}
+
+/* Conv2d::from_weights / QuantLinear::from_weights (conv.rs:25-47, layers.rs:212-232): b = 12 weight codes. */
+kt_scale kt_rc_quant_weights(const float* w, size_t n, int32_t* codes) { return quant_weights(w, n, codes); }
+
+/* Conv2d::with_bias / QuantLinear::with_bias (conv.rs:49-60, layers.rs:234-245): codes round(b / step), step =
+ * max |b| / ACT_LEVELS (no clamp), Scale::from_f64(step); a zero bias gives no bias (returns 0). */
+int kt_rc_quant_bias(const float* b, size_t n, int64_t* codes, kt_scale* bs) {
+    double mx = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        const double a = fabs((double)b[i]);
+        mx = a > mx ? a : mx;
+    }
+    if (!(mx > 0.0)) return 0;
+    const double step = mx / (double)ACT_LEVELS;
+    for (size_t i = 0; i < n; i++) codes[i] = (int64_t)round((double)b[i] / step);
+    *bs = kt_scale_from_f64(step);
+    return 1;
+}
+
+/* Conv2d::forward_int (conv.rs:68-130): x [ci][h][w] codes at xs, quant_to by its whole-tensor max, the direct
+ * convolution (accumulation order (ic, ky, kx), taps outside the image skipped) against w [co][ci][kh][kw] at ws, the
+ * bias in units of c, then requant_dyn by the whole output's max. out [co][oh][ow]. bias may be NULL. */
+void kt_rc_conv2d(const int32_t* x, kt_scale xs, size_t ci, size_t h, size_t w, const int32_t* wc, kt_scale ws,
+                  size_t co, size_t kh, size_t kw, size_t stride, size_t pad, const int64_t* bias, kt_scale bs,
+                  int32_t* out, kt_scale* os) {
+    const size_t oh = (h + 2 * pad - kh) / stride + 1, ow = (w + 2 * pad - kw) / stride + 1, n = co * oh * ow;
+    const size_t nx = ci * h * w;
+    int64_t xmax = 0;
+    for (size_t i = 0; i < nx; i++) {
+        const int64_t a = abs_w((int64_t)x[i]);
+        xmax = a > xmax ? a : xmax;
+    }
+    *os = ZERO;
+    if (xmax == 0) {
+        memset(out, 0, n * sizeof(int32_t));
+        return;
+    }
+    int32_t* qx = (int32_t*)malloc(nx * sizeof(int32_t));
+    for (size_t i = 0; i < nx; i++) { /* quant_to (layers.rs:23-31) */
+        const int64_t num = (int64_t)x[i] * WLEVELS, half = xmax / 2;
+        qx[i] = (int32_t)(num >= 0 ? (num + half) / xmax : -((-num + half) / xmax));
+    }
+    const kt_scale c = kt_scale_mul(kt_scale_mul(ratio((u128)xmax, WLEVELS), xs), ws);
+    if (c.mant == 0) {
+        memset(out, 0, n * sizeof(int32_t));
+        free(qx);
+        return;
+    }
+    kt_scale f = ZERO;
+    if (bias) f = kt_scale_mul(bs, kt_scale_recip(c));
+    int64_t* acc = (int64_t*)malloc(n * sizeof(int64_t));
+    for (size_t oc = 0; oc < co; oc++) {
+        const int64_t b = bias ? kt_scale_apply(f, bias[oc]) : 0;
+        for (size_t oy = 0; oy < oh; oy++)
+            for (size_t ox = 0; ox < ow; ox++) {
+                int64_t a = 0;
+                for (size_t ic = 0; ic < ci; ic++)
+                    for (size_t ky = 0; ky < kh; ky++) {
+                        const size_t iy = oy * stride + ky;
+                        if (iy < pad || iy - pad >= h) continue;
+                        for (size_t kx = 0; kx < kw; kx++) {
+                            const size_t ix = ox * stride + kx;
+                            if (ix < pad || ix - pad >= w) continue;
+                            a = wadd(a, wmul(qx[(ic * h + iy - pad) * w + ix - pad], wc[((oc * ci + ic) * kh + ky) * kw + kx]));
+                        }
+                    }
+                acc[(oc * oh + oy) * ow + ox] = wadd(a, b);
+            }
+    }
+    rd_t o = {out, n, ZERO};
+    close_dyn(acc, n, c, &o);
+    *os = o.s;
+    free(qx), free(acc);
+}
+
+/* nonlin.rs:7-21: erf by Abramowitz & Stegun 7.1.26, and the exact GELU 0.5 x (1 + erf(x / sqrt 2)). */
+static double as_erf(double x) {
+    const double sign = x < 0.0 ? -1.0 : 1.0;
+    x = fabs(x);
+    const double t = 1.0 / (1.0 + 0.3275911 * x);
+    const double y =
+        1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t - 0.284496736) * t + 0.254829592) * t *
+                  exp(-x * x);
+    return sign * y;
+}
+static double gelu_f64(double x) { return 0.5 * x * (1.0 + as_erf(x / 1.4142135623730951)); }
+
+static rd_lut* gelu_lut(void) {
+    static rd_lut L;
+    static int built = 0;
+    if (!built) {
+        lut_build_f(&L, gelu_f64, -10.0, 10.0, 16, 20, 1);
+        built = 1;
+    }
+    return &L;
+}
+
+/* build_gelu_lut (nonlin.rs:24-26): CodeLut(gelu, -10, 10, 2^16 entries, 20 code bits, identity right tail). */
+void kt_rc_gelu_table(int64_t* codes, kt_scale* inv_step, int64_t* lo_index, kt_scale* code_scale) {
+    const rd_lut* L = gelu_lut();
+    if (codes) memcpy(codes, L->codes, L->n * sizeof(int64_t));
+    *inv_step = L->inv_step_scale, *lo_index = L->lo_index, *code_scale = L->code_scale;
+}
+
+/* apply_gelu (nonlin.rs:30-45): each code -> the table's code (0 below it, the identity factor above), as i32, at
+ * the table's code scale (no requantization). */
+void kt_rc_apply_gelu(const int32_t* x, size_t n, kt_scale xs, int32_t* y, kt_scale* ys) {
+    const rd_lut* L = gelu_lut();
+    const kt_scale id_factor = kt_scale_mul(xs, kt_scale_recip(L->code_scale));
+    for (size_t i = 0; i < n; i++) {
+        const int64_t d = x[i], idx = lut_index(L, d, xs);
+        const int64_t code = idx < 0 ? 0 : idx >= (int64_t)L->n ? kt_scale_apply(id_factor, d) : lut_code_at(L, idx);
+        y[i] = (int32_t)code;
+    }
+    *ys = L->code_scale;
+}
+
+/* FeedForward::forward_int (hiera.rs:336-340): proj_in (+ bias) -> apply_gelu -> proj_out (+ bias). bi / bo may be
+ * NULL (no bias). */
+void kt_rc_feedforward(const int32_t* x, size_t rows, size_t dim, kt_scale xs, const int32_t* wi, kt_scale wis,
+                       const int64_t* bi, kt_scale bis, size_t hidden, const int32_t* wo, kt_scale wos,
+                       const int64_t* bo, kt_scale bos, int32_t* y, kt_scale* ys) {
+    int64_t xm, ym;
+    int32_t* h = (int32_t*)malloc(rows * hidden * sizeof(int32_t));
+    int32_t* g = (int32_t*)malloc(rows * hidden * sizeof(int32_t));
+    kt_scale hs, gs;
+    kt_quant_linear_forward(x, rows, dim, xs, wi, hidden, wis, bi, bis, 0, h, &hs, &xm, &ym);
+    kt_rc_apply_gelu(h, rows * hidden, hs, g, &gs);
+    kt_quant_linear_forward(g, rows, hidden, gs, wo, dim, wos, bo, bos, 0, y, ys, &xm, &ym);
+    free(h), free(g);
 }

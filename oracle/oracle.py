@@ -156,6 +156,15 @@ def _declare(L: C.CDLL) -> None:
         "kt_rm_probe": (Scale, [C.POINTER(C.c_uint64), _SZ, _P]),
         "kt_rm_set_bias": (None, [_P, _SZ, C.c_float]),
         "kt_rm_sigmoid_codes": (None, [_P, _P, _SZ, Scale, _P]),
+        "kt_rc_from_reals": (Scale, [_P, _SZ, C.c_int64, _P]),
+        "kt_rc_quant_weights": (Scale, [_P, _SZ, _P]),
+        "kt_rc_quant_bias": (C.c_int, [_P, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rc_conv2d": (None, [_P, Scale, _SZ, _SZ, _SZ, _P, Scale, _SZ, _SZ, _SZ, _SZ, _SZ, _P, Scale, _P,
+                                C.POINTER(Scale)]),
+        "kt_rc_gelu_table": (None, [_P, C.POINTER(Scale), C.POINTER(C.c_int64), C.POINTER(Scale)]),
+        "kt_rc_apply_gelu": (None, [_P, _SZ, Scale, _P, C.POINTER(Scale)]),
+        "kt_rc_feedforward": (None, [_P, _SZ, _SZ, Scale, _P, Scale, _P, Scale, _SZ, _P, Scale, _P, Scale, _P,
+                                     C.POINTER(Scale)]),
         "kt_moe_forward_token": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int,
                                         C.c_int, _P]),
     }
@@ -976,3 +985,84 @@ def rm_merge_rows(rows, rs, T: int, dim: int):
     out, os_ = np.zeros(T * dim, np.int32), Scale()
     lib().kt_rm_merge_rows(_ptr(r), sarr, T, dim, _ptr(out), C.byref(os_))
     return out, (os_.mant, os_.shift)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the SAM image path at the reference's semantics: Conv2d, the pixel entry, GELU, FeedForward
+
+
+def vecf(seed: int, n: int):
+    """The reference tests' float stream (conv.rs:471-477): ((lcg >> 40) / 2^24 * 2 - 1) as f32; (values, state)."""
+    s, out = seed, np.empty(n, np.float32)
+    for i in range(n):
+        s = (s * 6364136223846793005 + 1442695040888963407) % 2**64
+        out[i] = np.float32((s >> 40) / float(1 << 24) * 2.0 - 1.0)
+    return out, s
+
+
+def from_reals(real, levels: int = 1 << 28):
+    """IntTensor::from_reals (tensor.rs:106-117): (codes i32, (mant, shift))."""
+    r = np.ascontiguousarray(real, dtype=np.float64).reshape(-1)
+    out = np.empty(r.size, np.int32)
+    sc = lib().kt_rc_from_reals(_ptr(r), r.size, levels, _ptr(out))
+    return out, (sc.mant, sc.shift)
+
+
+def quant_weights(w):
+    """Conv2d::from_weights / QuantLinear::from_weights: (12-trit codes i32, (mant, shift))."""
+    f = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    out = np.empty(f.size, np.int32)
+    sc = lib().kt_rc_quant_weights(_ptr(f), f.size, _ptr(out))
+    return out, (sc.mant, sc.shift)
+
+
+def quant_bias(b):
+    """with_bias (conv.rs:49-60): (codes i64, (mant, shift)), or None for an all-zero bias."""
+    f = np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+    out, sc = np.empty(f.size, np.int64), Scale()
+    if not lib().kt_rc_quant_bias(_ptr(f), f.size, _ptr(out), C.byref(sc)):
+        return None
+    return out, (sc.mant, sc.shift)
+
+
+def ref_conv2d(x, xs, ci: int, h: int, w: int, wc, ws, co: int, kh: int, kw: int, stride: int, pad: int,
+               bias=None):
+    """Conv2d::forward_int (conv.rs:68-130): (codes co x oh x ow i32, (mant, shift)). bias: None or (codes, scale)."""
+    x, wc = _i32(x), _i32(wc)
+    assert x.size == ci * h * w and wc.size == co * ci * kh * kw
+    oh, ow = (h + 2 * pad - kh) // stride + 1, (w + 2 * pad - kw) // stride + 1
+    b = None if bias is None else np.ascontiguousarray(bias[0], dtype=np.int64)
+    bs = Scale(0, 0) if bias is None else Scale(*bias[1])
+    out, os_ = np.empty(co * oh * ow, np.int32), Scale()
+    lib().kt_rc_conv2d(_ptr(x), Scale(*xs), ci, h, w, _ptr(wc), Scale(*ws), co, kh, kw, stride, pad,
+                       0 if b is None else _ptr(b), bs, _ptr(out), C.byref(os_))
+    return out.reshape(co, oh, ow), (os_.mant, os_.shift)
+
+
+def gelu_table():
+    """build_gelu_lut (nonlin.rs:24-26): (codes i64[65536], inv_step scale, lo_index, code scale)."""
+    codes, inv, lo, cs = np.empty(1 << 16, np.int64), Scale(), C.c_int64(), Scale()
+    lib().kt_rc_gelu_table(_ptr(codes), C.byref(inv), C.byref(lo), C.byref(cs))
+    return codes, (inv.mant, inv.shift), lo.value, (cs.mant, cs.shift)
+
+
+def apply_gelu(x, xs):
+    """apply_gelu (nonlin.rs:30-45): (codes i32, the table's code scale)."""
+    x = _i32(x)
+    y, ys = np.empty(x.size, np.int32), Scale()
+    lib().kt_rc_apply_gelu(_ptr(x), x.size, Scale(*xs), _ptr(y), C.byref(ys))
+    return y, (ys.mant, ys.shift)
+
+
+def feedforward(x, rows: int, dim: int, xs, wi, wis, hidden: int, wo, wos, bi=None, bo=None):
+    """FeedForward::forward_int (hiera.rs:336-340): proj_in (+bias) -> apply_gelu -> proj_out (+bias).
+    wi hidden x dim, wo dim x hidden codes; bi / bo None or (codes, scale)."""
+    x, wi, wo = _i32(x), _i32(wi), _i32(wo)
+    bip = None if bi is None else np.ascontiguousarray(bi[0], dtype=np.int64)
+    bop = None if bo is None else np.ascontiguousarray(bo[0], dtype=np.int64)
+    y, ys = np.empty(rows * dim, np.int32), Scale()
+    lib().kt_rc_feedforward(_ptr(x), rows, dim, Scale(*xs), _ptr(wi), Scale(*wis),
+                            0 if bip is None else _ptr(bip), Scale(*(bi[1] if bi else (0, 0))), hidden, _ptr(wo),
+                            Scale(*wos), 0 if bop is None else _ptr(bop), Scale(*(bo[1] if bo else (0, 0))),
+                            _ptr(y), C.byref(ys))
+    return y.reshape(rows, dim), (ys.mant, ys.shift)

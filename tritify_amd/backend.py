@@ -117,6 +117,11 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_rmsnorm": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _P, _P]),
         "kt_hip_ref_add": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P]),
         "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_gelu": (_I, [_I, _P, _P, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_from_reals": (_I, [_P, _I64, _I64, _P, _P, _P]),
+        "kt_hip_ref_conv2d_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64]),
+        "kt_hip_ref_conv2d": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64,
+                                   C.c_int32, _P, _I64, C.c_int32, _P, _SZ, _P, _P, _P]),
         "kt_hip_quant_linear_rows_workspace": (_SZ, [_I64, _I64, _I64]),
         "kt_hip_quant_linear_rows": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _P, _P, _P, _SZ, _I, _I64, _P,
                                           _P, _P, _SZ, _P, _P, _P]),
@@ -533,7 +538,7 @@ def gen_quant_rows_fast(seed: int, rows: int, cols: int) -> np.ndarray:
 # The reference decoder's layers at the reference's own semantics (crates/01-engine/kt-core/src/{layers,attention,
 # model,generate}.rs): i32 codes at the 2^28 level with one kt-int Scale per tensor, in 32-byte device records.
 # ---------------------------------------------------------------------------------------------------------------
-LUT_EXP, LUT_SILU, LUT_SIGMOID = 0, 1, 2
+LUT_EXP, LUT_SILU, LUT_SIGMOID, LUT_GELU = 0, 1, 2, 3
 REF_MAX_HEADS = 64
 
 
@@ -555,7 +560,8 @@ def ref_scale_from_f64(x: float) -> tuple[int, int]:
 
 
 def ref_codelut(kind: int, lo: float, hi: float, idx_bits: int, code_bits: int, right_identity: bool):
-    """CodeLut::build (kt-int/src/lib.rs:359-379) of exp (LUT_EXP) or SiLU (LUT_SILU): (codes i64, constants)."""
+    """CodeLut::build (kt-int/src/lib.rs:359-379) of exp, SiLU, the router's sigmoid or SAM's GELU (LUT_*):
+    (codes i64, constants)."""
     codes = np.zeros(1 << idx_bits, dtype=np.int64)
     lut = CodeLut()
     check(lib().kt_hip_ref_codelut(kind, lo, hi, idx_bits, code_bits, int(right_identity), codes.ctypes.data,
@@ -594,6 +600,40 @@ def ref_swiglu(g_dev, gs_dev, u_dev, us_dev, n: int, silu_codes_dev, silu: CodeL
     check(lib().kt_hip_ref_swiglu(dev, _ptr(g_dev), _ptr(gs_dev), _ptr(u_dev), _ptr(us_dev), rows, n,
                                   _ptr(silu_codes_dev), C.byref(silu), _ptr(h_dev), _ptr(hs_dev), _stream(stream)),
           "ref swiglu")
+
+
+def ref_gelu(x_dev, xs_dev, n: int, gelu_codes_dev, gelu: CodeLut, y_dev, ys_dev, stream=None, dev: int = 0) -> None:
+    """apply_gelu (kt-model-vision/src/nonlin.rs:30-45) of n codes: y at the table's code scale."""
+    check(lib().kt_hip_ref_gelu(dev, _ptr(x_dev), _ptr(xs_dev), n, _ptr(gelu_codes_dev), C.byref(gelu), _ptr(y_dev),
+                                _ptr(ys_dev), _stream(stream)), "ref gelu")
+
+
+def ref_from_reals(real, levels: int = 1 << 28):
+    """IntTensor::from_reals (tensor.rs:106-117) on the host: (codes i32, (mant, shift))."""
+    r = np.ascontiguousarray(real, dtype=np.float64).reshape(-1)
+    codes = np.empty(r.size, dtype=np.int32)
+    m, s = C.c_int64(), C.c_int32()
+    check(lib().kt_hip_ref_from_reals(r.ctypes.data, r.size, levels, codes.ctypes.data, C.byref(m), C.byref(s)),
+          "from_reals")
+    return codes, (int(m.value), int(s.value))
+
+
+def ref_conv2d_workspace(ci: int, h: int, w: int, co: int, kh: int, kw: int, stride: int, pad: int) -> int:
+    n = lib().kt_hip_ref_conv2d_workspace(ci, h, w, co, kh, kw, stride, pad)
+    if n == 0:
+        raise ValueError("conv2d: shape out of range")
+    return n
+
+
+def ref_conv2d(x_dev, xs_dev, ci: int, h: int, w: int, w_planes_dev, pw: int, co: int, kh: int, kw: int, stride: int,
+               pad: int, w_scale, bias_dev, b_scale, ws_dev, ws_bytes: int, y_dev, os_dev, stream=None,
+               dev: int = 0) -> None:
+    """Conv2d::forward_int (conv.rs:68-130): y [co][oh][ow] codes and its record."""
+    bm, bsh = b_scale if b_scale is not None else (0, 0)
+    check(lib().kt_hip_ref_conv2d(dev, _ptr(x_dev), _ptr(xs_dev), ci, h, w, _ptr(w_planes_dev), pw, co, kh, kw,
+                                  stride, pad, int(w_scale[0]), int(w_scale[1]),
+                                  0 if bias_dev is None else _ptr(bias_dev), int(bm), int(bsh), _ptr(ws_dev), ws_bytes,
+                                  _ptr(y_dev), _ptr(os_dev), _stream(stream)), "ref conv2d")
 
 
 def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh: int, nkv: int, hd: int,

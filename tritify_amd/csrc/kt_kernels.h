@@ -74,6 +74,16 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
                                const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
                                const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
                                int32_t* y, kt_hip_qscale* os, hipStream_t s);
+// A Conv2d lowered onto QuantLinear: the image x [ci][h][w], kernel kh x kw, stride, zero padding, output oh x ow.
+struct ConvGeom {
+    int32_t ci, h, w, kh, kw, stride, pad, oh, ow;
+};
+// Conv2d::forward_int (conv.rs:68-130) as QuantLinear over the im2col rows (oh * ow rows of ci * kh * kw columns;
+// the workspace is ql_workspace_bytes of that shape) with the output stored [co][oh][ow].
+hipError_t launch_ref_conv2d(const int32_t* x, const ConvGeom& g, const kt_hip_qscale* xs, const int8_t* wb, int pw,
+                             int64_t co, int64_t w_mant, int32_t w_shift, const int64_t* bias, int64_t b_mant,
+                             int32_t b_shift, int64_t flush_k, void* ws, int32_t* y, kt_hip_qscale* os,
+                             hipStream_t s);
 // The device address of device `dev`'s QuantLinear scratch array (KT_QL_SCRATCH_BYTES), looked up once per device;
 // `dev` must be the current device.
 hipError_t ql_scratch(int dev, void** ptr);
@@ -94,6 +104,8 @@ hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_
 hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
                             int rows, int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h,
                             kt_hip_qscale* hs, hipStream_t s);
+hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, const int64_t* codes,
+                          const kt_hip_codelut* lut, int32_t* y, kt_hip_qscale* ys, hipStream_t s);
 size_t rq_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[3]);
 hipError_t launch_quant_linear_rows(const int32_t* x, const int32_t* xidx, int64_t x_rows, int64_t rows, int64_t in,
                                     const kt_hip_qscale* xs, int xs_step, int groups, const int64_t* off_host,

@@ -10,6 +10,10 @@
 //               and raises the call's max |acc| (layers.rs:304-321)
 //   ql_requant  y = requant_dyn(acc, ACT_LEVELS, ymax) and the output scale (layers.rs:33-39, 321-327)
 //
+// Conv2d::forward_int (conv.rs:68-130) runs the same passes over the image's im2col rows: max |x| over the whole
+// image, the patch gathered inside ql_quant (taps in the padding are zero, which the direct conv skips), the bias
+// and gmax in the GEMM epilogue, and ql_requant_conv storing the output channel-major through an LDS transpose.
+//
 // No host synchronization: the maxima and the scales stay in the workspace, and the output scale is written to a
 // device record the next layer reads as its input scale. Integer arithmetic only, except a double-precision
 // quotient estimate in ql_requant and ql_quant that is corrected to the exact integer quotient before use (the
@@ -76,10 +80,42 @@ __global__ __launch_bounds__(QL_THREADS) void ql_absmax_kernel(const int32_t* __
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
+// The column values of output row r from column c0 on, 4 of them: row r of x itself, or for a convolution the
+// im2col patch of output pixel r = oy * ow + ox, column c = (ic * kh + ky) * kw + kx (the weights' [co][ci][kh][kw]
+// order), zero for a tap in the padding or a column past `in`.
+template <bool CONV>
+__device__ inline void ql_fetch4(const int32_t* __restrict__ x, int64_t r, int64_t c0, int64_t in, const ConvGeom& g,
+                                 int32_t v[4]) {
+    if (!CONV) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) v[t] = c0 + t < in ? x[r * in + c0 + t] : 0;
+        return;
+    }
+    const int khw = g.kh * g.kw;
+    const int oy = (int)(r / g.ow), ox = (int)(r - (int64_t)oy * g.ow);
+    int ic = (int)(c0 / khw), rem = (int)(c0 - (int64_t)ic * khw);
+    int ky = rem / g.kw, kx = rem - ky * g.kw;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        int32_t val = 0;
+        if (c0 + t < in) {
+            const int iy = oy * g.stride + ky - g.pad, ix = ox * g.stride + kx - g.pad;
+            if (iy >= 0 && iy < g.h && ix >= 0 && ix < g.w) val = x[((int64_t)ic * g.h + iy) * g.w + ix];
+        }
+        v[t] = val;
+        if (++kx == g.kw) {
+            kx = 0;
+            if (++ky == g.kh) ky = 0, ic++;
+        }
+    }
+}
+
 // qx = quant_to(x, xmax) for 4 consecutive columns per thread, split into planes [3][rows][kp]; padding columns and
 // the xmax == 0 case give zero digits. |qx| <= WLEVELS < 127 * (1 + 256 + 65536), so 3 balanced digits hold it.
-__global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __restrict__ x, int64_t rows,
-                                                              int64_t in, int64_t kp,
+// xmax is taken over the nx values of x (the whole image for a convolution).
+template <bool CONV>
+__global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __restrict__ x, int64_t nx,
+                                                              int64_t rows, int64_t in, int64_t kp, ConvGeom geom,
                                                               const uint32_t* __restrict__ part, int nparts,
                                                               const kt_hip_qscale* __restrict__ xs, int64_t w_mant,
                                                               int32_t w_shift, int has_bias, int64_t b_mant,
@@ -97,7 +133,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
     if (nparts > 0) {
         for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
     } else {  // a short x (QL_FUSED_MAX values at most): every CTA takes max |x| itself, no ql_absmax pass
-        for (int64_t i = threadIdx.x; i < rows * in; i += QL_THREADS) {
+        for (int64_t i = threadIdx.x; i < nx; i += QL_THREADS) {
             const int32_t v = x[i];
             const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
             m = a > m ? a : m;
@@ -135,12 +171,13 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
         if (cq >= qpr) cq -= qpr, r++;
         const int64_t c0 = cq * 4;
         uint32_t word[3] = {0, 0, 0};
+        int32_t xv[4] = {0, 0, 0, 0};
+        if (live) ql_fetch4<CONV>(x, r, c0, in, geom, xv);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const int64_t c = c0 + t;
             int64_t v = 0;
-            if (live && c < in) {
-                const int64_t num = (int64_t)x[r * in + c] * WLEVELS;  // |num| < 2^49: exact in a double
+            if (xv[t] != 0) {
+                const int64_t num = (int64_t)xv[t] * WLEVELS;  // |num| < 2^49: exact in a double
                 const uint64_t a = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
                 const uint64_t qq = udiv_est53(a, xmax);  // a < 2^31 * WLEVELS + 2^30 < 2^53
                 v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
@@ -197,6 +234,48 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* _
     }
 }
 
+// Conv2d::forward_int's close (conv.rs:121-129): y = requant_dyn(acc, ACT_LEVELS, gmax) stored channel-major,
+// y[o * rows + r] for acc[r * out + o], through a 64 x 64 LDS tile so that both the acc reads and the y writes are
+// row-contiguous. An all-zero image (mode 1), c == 0 (mode 2) and gmax == 0 give zeros at Scale::ZERO.
+__global__ __launch_bounds__(QL_THREADS) void ql_requant_conv_kernel(const int64_t* __restrict__ acc, int64_t rows,
+                                                                     int64_t out, const QlState* __restrict__ st,
+                                                                     int32_t* __restrict__ y,
+                                                                     kt_hip_qscale* __restrict__ os) {
+    __shared__ int32_t tile[64][65];
+    int64_t ymax = 0;
+#pragma unroll
+    for (int i = 0; i < KT_QL_YSLOTS; i++) ymax = (int64_t)st->ymax[i].v > ymax ? (int64_t)st->ymax[i].v : ymax;
+    const bool live = st->mode == 0 && ymax > 0;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+        kt_hip_qscale o{};
+        o.xmax = st->xmax;
+        if (live) {
+            const Sc sc = sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{st->c_mant, st->c_shift});
+            o.mant = sc.mant, o.shift = sc.shift, o.ymax = ymax;
+        }
+        *os = o;
+    }
+    const u128 halfd = (u128)(uint64_t)(ymax / 2);
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * 64, o0 = (int64_t)blockIdx.y * 64;
+    for (int rr = ty; rr < 64; rr += QL_THREADS / 64) {
+        const int64_t r = r0 + rr, o = o0 + tx;
+        int32_t q32 = 0;
+        if (live && r < rows && o < out) {
+            const int64_t v = acc[r * out + o];
+            const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
+            const uint64_t q = udiv_small_q(((u128)a << 28) + halfd, ymax);
+            q32 = (int32_t)(v < 0 ? 0 - q : q);
+        }
+        tile[tx][rr] = q32;
+    }
+    __syncthreads();
+    for (int oo = ty; oo < 64; oo += QL_THREADS / 64) {
+        const int64_t o = o0 + oo, r = r0 + tx;
+        if (o < out && r < rows) y[o * rows + r] = tile[oo][tx];
+    }
+}
+
 size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]) {
     const size_t kp = (size_t)((in + 63) / 64 * 64);
     const size_t sizes[KT_QL_WS_PARTS] = {3 * (size_t)rows * kp, (size_t)rows * (size_t)out * 8, KT_QL_PARTS * 4,
@@ -237,10 +316,13 @@ static int grid_for(int64_t n, int64_t per_thread) {
     return (int)(g < 1 ? 1 : (g > KT_QL_PARTS ? KT_QL_PARTS : g));
 }
 
-hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
-                               const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
-                               const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
-                               int32_t* y, kt_hip_qscale* os, hipStream_t s) {
+// The four passes of QuantLinear::forward_int, or of Conv2d::forward_int when geom is non-null (the image x of
+// geom->ci x h x w values read as its im2col rows; the output channel-major, zeros at Scale::ZERO for an all-zero
+// image).
+static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, const ConvGeom* geom,
+                                 const kt_hip_qscale* xs, const int8_t* wb, int pw, int64_t out, int64_t w_mant,
+                                 int32_t w_shift, const int64_t* bias, int64_t b_mant, int32_t b_shift,
+                                 int64_t flush_k, void* ws, int32_t* y, kt_hip_qscale* os, hipStream_t s) {
     size_t off[KT_QL_WS_PARTS];
     ql_workspace_bytes(rows, in, out, off);
     char* base = (char*)ws;
@@ -250,17 +332,26 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
     uint32_t* tile_cnt = (uint32_t*)(base + off[3]);  // the split-k GEMM's per-tile arrival counters
     QlState* st = (QlState*)(base + off[4]);
     const int64_t kp = (in + 63) / 64 * 64, n = rows * out;
+    const int64_t nx = geom ? (int64_t)geom->ci * geom->h * geom->w : rows * in;
     // one k-chunk whose tiles leave CUs idle (the decode row, N = 896 at M = 512): split k across CTAs
     const int splits = kp <= flush_k ? plane_gemm_splits(3, pw, (int)rows, (int)out, 0, (int)kp) : 1;
     const int ntiles = splits > 1 ? (int)(((out + 63) / 64) * ((rows + 63) / 64)) : 0;
     if (ntiles * 4 > KT_QL_PARTS * 8) return hipErrorInvalidValue;  // cannot happen: a split grid has < 128 tiles
 
     // max |x| by its own pass, or inside every quant CTA when x is short (one launch fewer for a decode row)
-    const int gx = rows * in <= QL_FUSED_MAX ? 0 : grid_for(rows * in, 8);
-    if (gx > 0) ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, rows * in, part_x);
-    ql_quant_kernel<<<grid_for(rows * kp / 4, 1), QL_THREADS, 0, s>>>(
-        x, rows, in, kp, part_x, gx, xs, w_mant, w_shift, bias != nullptr, b_mant, b_shift, st, xa,
-        splits > 1 ? reinterpret_cast<uint64_t*>(acc) : nullptr, splits > 1 ? n : 0, tile_cnt, ntiles);
+    const int gx = nx <= QL_FUSED_MAX ? 0 : grid_for(nx, 8);
+    if (gx > 0) ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, nx, part_x);
+    uint64_t* zacc = splits > 1 ? reinterpret_cast<uint64_t*>(acc) : nullptr;
+    const int64_t nzacc = splits > 1 ? n : 0;
+    const int gq = grid_for(rows * kp / 4, 1);
+    if (geom)
+        ql_quant_kernel<true><<<gq, QL_THREADS, 0, s>>>(x, nx, rows, in, kp, *geom, part_x, gx, xs, w_mant, w_shift,
+                                                        bias != nullptr, b_mant, b_shift, st, xa, zacc, nzacc,
+                                                        tile_cnt, ntiles);
+    else
+        ql_quant_kernel<false><<<gq, QL_THREADS, 0, s>>>(x, nx, rows, in, kp, ConvGeom{}, part_x, gx, xs, w_mant,
+                                                         w_shift, bias != nullptr, b_mant, b_shift, st, xa, zacc,
+                                                         nzacc, tile_cnt, ntiles);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     for (int64_t k0 = 0; k0 < kp; k0 += flush_k) {
@@ -270,10 +361,31 @@ hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const
                               last ? bias : nullptr, last ? st : nullptr, splits, tile_cnt);
         if (e != hipSuccess) return e;
     }
+    if (geom) {
+        const dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((out + 63) / 64));
+        ql_requant_conv_kernel<<<grid, QL_THREADS, 0, s>>>(acc, rows, out, st, y, os);
+        return hipGetLastError();
+    }
     // one output per thread for short outputs (a decode row: its divisions then run side by side, not 8 in a row)
     ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 2), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift,
                                                                            y, os);
     return hipGetLastError();
+}
+
+hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
+                               const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
+                               const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
+                               int32_t* y, kt_hip_qscale* os, hipStream_t s) {
+    return launch_ql_impl(x, rows, in, nullptr, xs, wb, pw, out, w_mant, w_shift, bias, b_mant, b_shift, flush_k, ws,
+                          y, os, s);
+}
+
+hipError_t launch_ref_conv2d(const int32_t* x, const ConvGeom& g, const kt_hip_qscale* xs, const int8_t* wb, int pw,
+                             int64_t co, int64_t w_mant, int32_t w_shift, const int64_t* bias, int64_t b_mant,
+                             int32_t b_shift, int64_t flush_k, void* ws, int32_t* y, kt_hip_qscale* os,
+                             hipStream_t s) {
+    return launch_ql_impl(x, (int64_t)g.oh * g.ow, (int64_t)g.ci * g.kh * g.kw, &g, xs, wb, pw, co, w_mant, w_shift,
+                          bias, b_mant, b_shift, flush_k, ws, y, os, s);
 }
 
 }  // namespace kt

@@ -12,6 +12,8 @@
 //                      RoPE, the KV cache append with per-step scales, the integer-code
 //                      softmax at a common score scale, the heads brought to one scale
 //   rd_argmax          argmax_codes, the greedy choice, with an optional per-step record  (generate.rs:48-56)
+//   rd_gelu            apply_gelu, SAM's GELU by its CodeLut (many CTAs: a whole image's  (kt-model-vision/src/
+//                      tokens)                                                             nonlin.rs:30-45)
 //
 // Each kernel is one CTA of 1024 threads (one token's tensors are at most a few thousand values); the Scale
 // arithmetic of a tensor runs in one thread, the per-element work in all of them. The offline tables
@@ -268,6 +270,32 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
         put_rec(hs, hmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)hmax, (u128)ACT_LEVELS), hsc));
 }
 
+// apply_gelu (kt-model-vision/src/nonlin.rs:30-45): each code through the GELU CodeLut at x's scale (0 below the
+// table, the identity factor xs / code_scale above it), cast to i32, the output at the table's code scale with no
+// requantization. Grid-stride over n; each CTA forms the two factors from the record.
+__global__ __launch_bounds__(RD_THREADS) void rd_gelu_kernel(const int32_t* __restrict__ x,
+                                                             const kt_hip_qscale* __restrict__ xs_rec, int64_t n,
+                                                             const int64_t* __restrict__ codes, kt_hip_codelut L,
+                                                             int32_t* __restrict__ y,
+                                                             kt_hip_qscale* __restrict__ ys) {
+    __shared__ Sc par[2];  // index factor, identity factor
+    const Sc cs{L.code_mant, L.code_shift};
+    if (threadIdx.x == 0) {
+        const Sc xs = rec_sc(xs_rec);
+        par[0] = sc_mul(xs, Sc{L.inv_mant, L.inv_shift});
+        par[1] = sc_mul(xs, sc_recip(cs));
+    }
+    __syncthreads();
+    const Sc mi = par[0], idf = par[1];
+    const int64_t step = (int64_t)gridDim.x * RD_THREADS;
+    for (int64_t i = (int64_t)blockIdx.x * RD_THREADS + threadIdx.x; i < n; i += step) {
+        const int64_t d = x[i], idx = lut_index(mi, d, L.lo_index);
+        const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, d) : lut_code(codes, L.n, idx));
+        y[i] = (int32_t)code;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) put_rec(ys, cs);
+}
+
 // Attention::decode_step between its projections (attention.rs:358-458), at the position *pos:
 //  1. RoPE (rope_int, attention.rs:222-246) of every q head into LDS and every k head into the cache row pos; v
 //     into its cache row; this step's k and v scales into the per-step scale arrays;
@@ -477,6 +505,13 @@ hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int
     rd_swiglu_kernel<<<(unsigned)rows, RD_THREADS, 0, s>>>(g, gs, u, us, n, codes, *lut, h, hs);
     return hipGetLastError();
 }
+hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, const int64_t* codes,
+                          const kt_hip_codelut* lut, int32_t* y, kt_hip_qscale* ys, hipStream_t s) {
+    const int64_t per = (int64_t)RD_THREADS * 4;
+    const int64_t g = (n + per - 1) / per;
+    rd_gelu_kernel<<<(unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g)), RD_THREADS, 0, s>>>(x, xs, n, codes, *lut, y, ys);
+    return hipGetLastError();
+}
 hipError_t launch_rd_attention_step(const RdAttn& a, hipStream_t s) {
     const size_t lds = rd_attention_lds(a.max_seq, a.nh, a.hd);
     if (lds > KT_REF_ATTN_LDS) return hipErrorInvalidValue;
@@ -544,6 +579,48 @@ extern "C" int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qsc
     RD_TRY(hipSetDevice(dev));
     return (int)kt::launch_rd_swiglu(g_dev, gs_dev, u_dev, us_dev, (int)rows, (int)n, silu_codes_dev, silu, h_dev,
                                      hs_dev, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_gelu(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t n,
+                               const int64_t* gelu_codes_dev, const kt_hip_codelut* gelu, int32_t* y_dev,
+                               kt_hip_qscale* ys_dev, void* stream) {
+    if (!x_dev || !xs_dev || !gelu_codes_dev || !gelu || !y_dev || !ys_dev || n < 1 || gelu->n < 1 ||
+        !gelu->right_identity || (const void*)ys_dev == (const void*)xs_dev)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_gelu(x_dev, xs_dev, n, gelu_codes_dev, gelu, y_dev, ys_dev, (hipStream_t)stream);
+}
+
+extern "C" size_t kt_hip_ref_conv2d_workspace(int64_t ci, int64_t h, int64_t w, int64_t co, int64_t kh, int64_t kw,
+                                              int64_t stride, int64_t pad) {
+    if (ci < 1 || h < 1 || w < 1 || co < 1 || kh < 1 || kw < 1 || stride < 1 || pad < 0 || h + 2 * pad < kh ||
+        w + 2 * pad < kw)
+        return 0;
+    const int64_t oh = (h + 2 * pad - kh) / stride + 1, ow = (w + 2 * pad - kw) / stride + 1;
+    size_t off[KT_QL_WS_PARTS];
+    return kt::ql_workspace_bytes(oh * ow, ci * kh * kw, co, off);
+}
+
+extern "C" int kt_hip_ref_conv2d(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t ci, int64_t h,
+                                 int64_t w, const int8_t* w_planes_dev, int pw, int64_t co, int64_t kh, int64_t kw,
+                                 int64_t stride, int64_t pad, int64_t w_mant, int32_t w_shift,
+                                 const int64_t* bias_dev, int64_t b_mant, int32_t b_shift, void* ws_dev,
+                                 size_t ws_bytes, int32_t* y_dev, kt_hip_qscale* os_dev, void* stream) {
+    if (!x_dev || !xs_dev || !w_planes_dev || !ws_dev || !y_dev || !os_dev || (pw != 1 && pw != 3 && pw != 5) ||
+        w_mant < 0 || b_mant < 0)
+        return (int)hipErrorInvalidValue;
+    const size_t need = kt_hip_ref_conv2d_workspace(ci, h, w, co, kh, kw, stride, pad);
+    if (need == 0 || ws_bytes < need || ci * h * w >= ((int64_t)1 << 31) || kh >= 65536 || kw >= 65536 ||
+        stride >= 65536 || pad >= 65536)  // the gather's pixel arithmetic stays within int32
+        return (int)hipErrorInvalidValue;
+    const int64_t oh = (h + 2 * pad - kh) / stride + 1, ow = (w + 2 * pad - kw) / stride + 1;
+    const int64_t rows = oh * ow, kp = (ci * kh * kw + 63) / 64 * 64;
+    if (rows * kp >= ((int64_t)1 << 31) || rows * co >= ((int64_t)1 << 31)) return (int)hipErrorInvalidValue;
+    const kt::ConvGeom g{(int32_t)ci, (int32_t)h, (int32_t)w, (int32_t)kh, (int32_t)kw, (int32_t)stride,
+                         (int32_t)pad, (int32_t)oh, (int32_t)ow};
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_ref_conv2d(x_dev, g, xs_dev, w_planes_dev, pw, co, w_mant, w_shift, bias_dev, b_mant,
+                                      b_shift, kt_hip_flush_k(3, pw), ws_dev, y_dev, os_dev, (hipStream_t)stream);
 }
 
 extern "C" int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
@@ -615,6 +692,38 @@ extern "C" void kt_hip_ref_scale_from_f64(double x, int64_t* mant, int32_t* shif
     *shift = 31 - e;
 }
 
+extern "C" int kt_hip_ref_from_reals(const double* real, int64_t n, int64_t levels, int32_t* codes, int64_t* mant,
+                                     int32_t* shift) {
+    if (!real || !codes || !mant || !shift || n < 0 || levels < 1 || levels > ((int64_t)1 << 30))
+        return (int)hipErrorInvalidValue;
+    double mx = 0.0;
+    for (int64_t i = 0; i < n; i++) {
+        if (!isfinite(real[i])) return (int)hipErrorInvalidValue;
+        const double a = fabs(real[i]);
+        mx = a > mx ? a : mx;
+    }
+    *mant = 0, *shift = 0;
+    if (mx == 0.0) {
+        memset(codes, 0, (size_t)n * sizeof(int32_t));
+        return 0;
+    }
+    const double step = mx / (double)levels, inv = (double)levels / mx;
+    for (int64_t i = 0; i < n; i++) codes[i] = (int32_t)round(real[i] * inv);  // |value| <= levels
+    kt_hip_ref_scale_from_f64(step, mant, shift);
+    return 0;
+}
+
+// erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7) and the exact GELU 0.5 x (1 + erf(x / sqrt 2)), in the
+// reference's operation order (kt-model-vision/src/nonlin.rs:7-21).
+static double rd_erf_as(double x) {
+    const double sign = x < 0.0 ? -1.0 : 1.0;
+    x = fabs(x);
+    const double t = 1.0 / (1.0 + 0.3275911 * x);
+    const double p = (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t - 0.284496736) * t + 0.254829592);
+    return sign * (1.0 - p * t * exp(-x * x));
+}
+static double rd_gelu_f64(double x) { return 0.5 * x * (1.0 + rd_erf_as(x / 1.4142135623730951)); }
+
 static double rd_lut_fn(int kind, double x) {
     switch (kind) {
         case KT_LUT_EXP:
@@ -623,6 +732,8 @@ static double rd_lut_fn(int kind, double x) {
             return x / (1.0 + exp(-x));
         case KT_LUT_SIGMOID:
             return 1.0 / (1.0 + exp(-x));
+        case KT_LUT_GELU:
+            return rd_gelu_f64(x);
         default:
             return 0.0;
     }
@@ -630,7 +741,7 @@ static double rd_lut_fn(int kind, double x) {
 
 extern "C" int kt_hip_ref_codelut(int kind, double lo, double hi, int idx_bits, int code_bits, int right_identity,
                                   int64_t* codes, kt_hip_codelut* lut) {
-    if ((kind != KT_LUT_EXP && kind != KT_LUT_SILU && kind != KT_LUT_SIGMOID) || idx_bits < 1 || idx_bits > 24 || code_bits < 0 ||
+    if (kind < KT_LUT_EXP || kind > KT_LUT_GELU || idx_bits < 1 || idx_bits > 24 || code_bits < 0 ||
         code_bits > 52 || !(hi > lo) || !lut)
         return (int)hipErrorInvalidValue;
     const int64_t n = (int64_t)1 << idx_bits;
