@@ -305,6 +305,58 @@ uint64_t kt_hip_resident_bytes(const kt_hip_backend* b);
 uint64_t kt_hip_fallbacks(void);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * The cross-backend gates (crates/02-runtime/kt-runtime/src/gate.rs:1-140; runtime_probe, examples/runtime_probe.rs:
+ * 19-89): run the linear accumulate through every backend on one fixed corpus and require identical bytes. A gate
+ * backend is a name and a linear_weights function with its context: this library's backend (kt_hip_gate_backend),
+ * the engine's Portable (kt_hip_gate_portable, the gates' reference: the i64 dot of kt-core/src/backend.rs:66-160
+ * on the CPU; no HIP call ever hands work to it), a planted build's backend, or a caller's own.
+ * ------------------------------------------------------------------------------------------------------------- */
+#define KT_GATE_NAME_LEN 96
+#define KT_GATE_EINVAL 1     /* hipErrorInvalidValue */
+#define KT_GATE_DIVERGED (-1) /* a gate found a backend whose bytes differ */
+typedef struct {
+    const char* label;
+    uint64_t id; /* the weights' WeightId */
+    size_t rows, out, k;
+    const int32_t* x; /* rows x k */
+    const int32_t* w; /* out x k */
+} kt_gate_case;
+typedef int (*kt_gate_linear_fn)(void* ctx, const int32_t* x, uint64_t weight_id, const int32_t* w, size_t rows,
+                                 size_t out, size_t k, int64_t* y);
+typedef struct {
+    char name[KT_GATE_NAME_LEN];
+    kt_gate_linear_fn linear_weights;
+    void* ctx;
+} kt_gate_backend;
+/* GateReport (gate.rs:71-79): the backend's name, SHA-256 (hex) over every accumulator of every case in order
+ * (little-endian i64), the cases whose accumulators differ from the first backend's (bit c for case c), and the
+ * first error a call returned (its case counts as diverged). */
+typedef struct {
+    char backend[KT_GATE_NAME_LEN];
+    char hash[65];
+    uint64_t diverged;
+    int error;
+} kt_gate_report;
+/* corpus() (gate.rs:26-58): the fixed corpus, library-owned and the same bytes on every machine; returns the count. */
+size_t kt_hip_gate_corpus(const kt_gate_case** cases);
+/* The bound cases, outside the corpus: flush_case() (gate.rs:60-69), the reference digit backend's smallest k beyond
+ * one int32 flush, then this backend's own bound for 1-plane and 3-plane codes (one 256-deep chunk past
+ * kt_hip_flush_k, every digit -128). Each answer is +-k * code^2. Returns the count. */
+size_t kt_hip_gate_bound_cases(const kt_gate_case** cases);
+int kt_hip_gate_portable(kt_gate_backend* out);
+int kt_hip_gate_backend(kt_hip_backend* b, kt_gate_backend* out);
+/* Portable::linear (backend.rs:143-160) on the host: the gates' reference. */
+int kt_hip_portable_linear(const int32_t* x, const int32_t* w, size_t rows, size_t out, size_t k, int64_t* y);
+/* equality_gate (gate.rs:81-106): every backend over the cases (at most 64), the first as the reference; one report
+ * each. Returns 0 if all are byte-identical, KT_GATE_DIVERGED if any differs. */
+int kt_hip_equality_gate(const kt_gate_backend* backends, size_t n, const kt_gate_case* cases, size_t ncases,
+                         kt_gate_report* reports);
+/* residency_gate (gate.rs:108-140): the cases twice over (the second pass reuses every resident weight), then two
+ * weight matrices of one shape interleaved four times, each answer against Portable. 0 if it holds, else
+ * KT_GATE_DIVERGED with msg naming the first case that differs. */
+int kt_hip_residency_gate(const kt_gate_backend* b, const kt_gate_case* cases, size_t ncases, char* msg, size_t len);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * 12-bit-weight path (BASELINE workloads), device-resident operands. No counterpart in the reference: there the
  * weights are 12-trit codes on the digit path above. W12 digits: lo = (v & 255) - 128 (int8), hi = (v + 2048) >> 8
  * (4 bits), v = lo + 256 hi - 1920, stored fragment-tiled in blocks of 32 rows x 32 k (64 lanes x 16 lo bytes and

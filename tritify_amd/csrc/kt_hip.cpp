@@ -140,11 +140,18 @@ int kt_hip_device_count(int* n) {
     return (int)hipGetDeviceCount(n);
 }
 
+// The marketing name, or the gfx architecture where the runtime reports none (some hosts leave it empty).
+static std::string device_name(const hipDeviceProp_t& p) {
+    std::string n(p.name);
+    if (n.empty()) n = std::string(p.gcnArchName).substr(0, std::string(p.gcnArchName).find(':'));
+    return n.empty() ? std::string("device") : n;
+}
+
 int kt_hip_device_info(int dev, char* name, int len, int* major, int* minor, size_t* free_bytes) {
     hipDeviceProp_t p;
     KT_TRY(hipGetDeviceProperties(&p, dev));
     if (len > 0) {
-        strncpy(name, p.name, (size_t)len - 1);
+        strncpy(name, device_name(p).c_str(), (size_t)len - 1);
         name[len - 1] = 0;
     }
     *major = p.major;
@@ -270,7 +277,7 @@ static int open_impl(int dev, uint64_t budget, int plant, kt_hip_backend** out) 
     KT_TRY(hipMemGetInfo(&free_b, &total));
     kt_hip_backend* b = new kt_hip_backend();
     b->dev = dev;
-    b->devname = p.name;
+    b->devname = device_name(p);
     b->budget_given = budget != 0;
     b->budget = budget != 0 ? budget : (uint64_t)free_b / 5 * 4;  // kt-cuda/src/device.rs:147-149
     b->plant = plant;
