@@ -17,6 +17,10 @@ Also measured, each under "configs" (skip with --configs):
      N 112) and the stage-3 MLP (4096 tokens, 448 -> 1792 with the GELU table -> 448).
   ql the reference's own QuantLinear::forward_int on the device (dynamic per-tensor quantization around the digit
      GEMM) at the config-3 projection shapes, with the digit GEMM timed alone beside it.
+  lb the LinearBackend trait path (host buffers in, i64 out) on cuda_bench's shapes.
+  ref the reference's own integer semantics end to end: its DecoderModel at the Qwen2.5-0.5B shape (decode tokens/s
+     from one captured graph per position, every position's logits hash checked against the oracle, whose run is
+     the CPU baseline), and SAM's PatchEmbed Conv2d and a stage-3 FeedForward.
 
 Prints one JSON line on stdout (progress goes to stderr):
   value      logical effective TOPS = 2*M*N*K / time per step (one launch per step)
@@ -25,7 +29,7 @@ Prints one JSON line on stdout (progress goes to stderr):
   cpu_baseline  the reference's multithreaded CPU integer path (the oracle's restatement of linear_cpu, AVX-512
              variant when the host has it) on the same M = 2048 workload, timed on this host's cores
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,3,4,5,ql]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--configs 2,3,4,5,ql,lb,ref]
 """
 from __future__ import annotations
 
@@ -668,6 +672,172 @@ def bench_linear_backend(torch, args) -> dict:
 # ---------------------------------------------------------------------------------------------------------------
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# the reference's own integer semantics on the device (RefDecoder, RefConv2d, RefFeedForward)
+
+REF_QWEN = dict(dim=896, layers=24, nh=14, nkv=2, hd=64, hidden=4864, vocab=151936, eps=1e-6, theta=1.0e6, max_seq=64)
+WL = 265720
+
+
+def ref_decoder_weights(cfg: dict, seed: int):
+    """Qwen2.5-0.5B-shape codes and Scales from this build's generators: every weight and gamma code uniform in
+    +-WLEVELS at the Scale from_weights gives floats of peak 1 (1 / WLEVELS), the embedding alike."""
+    import tritify_amd as T
+    from tritify_amd import backend as B
+
+    sc = B.ref_scale_from_f64(1.0 / WL)
+    d, qd, kvd, h, V = cfg["dim"], cfg["nh"] * cfg["hd"], cfg["nkv"] * cfg["hd"], cfg["hidden"], cfg["vocab"]
+    state = [seed]
+
+    def codes(*shape):
+        state[0] += 1
+        return T.gen_uniform_fast(state[0], -WL, WL, int(np.prod(shape))).reshape(shape)
+
+    layers = []
+    for _ in range(cfg["layers"]):
+        layers.append({"in_norm": (codes(d), sc), "post_norm": (codes(d), sc), "wq": (codes(qd, d), sc),
+                       "wk": (codes(kvd, d), sc), "wv": (codes(kvd, d), sc), "wo": (codes(d, qd), sc),
+                       "gate": (codes(h, d), sc), "up": (codes(h, d), sc), "down": (codes(d, h), sc)})
+    return (codes(V, d), sc), (codes(d), sc), (codes(V, d), sc), layers
+
+
+def bench_ref_decoder(torch, args) -> dict:
+    """The reference's DecoderModel (model.rs:290-353) at its own semantics on the device, Qwen2.5-0.5B shape: a
+    4-token prompt then greedy decode, one captured HIP graph per position (decode step + argmax_codes, the
+    position advanced and the logits recorded on the device). Every recorded position's logits_hash is checked
+    against the oracle's restatement before the timing is reported; the oracle's run is the CPU baseline."""
+    from oracle import oracle as O
+    from tritify_amd.refdecoder import RefDecoder, logits_hash_bytes
+
+    cfg = REF_QWEN
+    prompt, n_dec = [9, 1000, 20000, 151935], 28
+    t0 = time.perf_counter()
+    w = ref_decoder_weights(cfg, 0x5EED)
+    dec = RefDecoder(cfg, *w)
+    log(f"bench: ref decoder: weights resident in {time.perf_counter() - t0:.1f}s")
+    dec.decode_step(prompt[0], 0)
+    g = dec.capture_greedy_step()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    best = None
+    for _ in range(3):
+        dec.new_cache()
+        dec.pos.zero_()
+        for t in prompt:
+            dec.token.fill_(t)
+            g.replay()
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        for _ in range(n_dec):
+            g.replay()
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / n_dec
+        best = ms if best is None else min(best, ms)
+    npos = len(prompt) + n_dec
+    got = [hashlib.sha256(logits_hash_bytes(*dec.recorded(p))).hexdigest() for p in range(npos)]
+    del dec, g
+    torch.cuda.empty_cache()
+    log(f"bench: ref decoder: checking {npos} positions against the oracle (CPU)")
+    model = O.RefModel.from_weights(cfg, *w)
+    del w
+    cores = cpu_threads()
+    O.set_max_threads(cores)
+    t0 = time.perf_counter()
+    _, _, want = model.generate(prompt, n_dec + 1)
+    cpu_s = time.perf_counter() - t0
+    if got != want:
+        first = next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
+        raise SystemExit(f"bench: ref decoder: position {first} differs from the CPU oracle")
+    wbytes = 3 * (cfg["layers"] * ((2 * cfg["nh"] + 2 * cfg["nkv"]) * cfg["hd"] * cfg["dim"] +
+                                   3 * cfg["hidden"] * cfg["dim"]) + cfg["vocab"] * cfg["dim"])
+    return {
+        "workload": "the reference's DecoderModel::decode_step at its own semantics (i32 codes at 2^28, 12-trit "
+                    "weights as 3 digit planes, per-tensor dynamic requant after every op, RmsNorm, RoPE Scales, "
+                    "exp and SiLU CodeLuts), Qwen2.5-0.5B shape (24 layers, dim 896, 14/2 heads, 4864, vocab "
+                    "151936), one HIP graph per position",
+        "bit_exact_positions": npos,
+        "decode_tokens_per_s": round(1e3 / best, 1),
+        "decode_us_per_token": round(best * 1e3, 1),
+        "weight_plane_gbs": round(wbytes / (best * 1e-3) / 1e9, 1),
+        "cpu_baseline": {
+            "value": round(npos / cpu_s, 2), "unit": "tokens/s", "cores": cores, "nproc": os.cpu_count(),
+            "kind": "port",
+            "sample": f"the oracle's restatement of the reference decoder (repro::run over {len(prompt)} prompt and "
+                      f"{n_dec} greedy positions, every QuantLinear through the threaded linear_cpu restatement), "
+                      f"{cpu_s * 1e3 / npos:.0f} ms/position"},
+    }
+
+
+def bench_ref_sam(torch, args) -> dict:
+    """SAM 2.1 Hiera-B+ at the reference's semantics: the PatchEmbed Conv2d (conv.rs:68-130) on a 1024 x 1024 image
+    entered by from_reals, and a stage-3 FeedForward (4096 tokens, 448 -> 1792 -> 448, GELU CodeLut), each checked
+    against the oracle before timing; the oracle's direct conv is the CPU baseline."""
+    import tritify_amd as T
+    from oracle import oracle as O
+    from tritify_amd import backend as B
+    from tritify_amd.refvision import RefConv2d, RefFeedForward
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0x5A)
+    real = rng.standard_normal(3 * 1024 * 1024) * 1.7
+    x, xs = B.ref_from_reals(real)
+    sc = B.ref_scale_from_f64(1.0 / WL)
+    wc = T.gen_uniform_fast(0xC0, -WL, WL, 112 * 3 * 49).reshape(112, 3, 7, 7)
+    bias = (T.gen_uniform_fast(0xC1, -(1 << 28), 1 << 28, 112).astype(np.int64), B.ref_scale_from_f64(1e-9))
+    conv = RefConv2d(wc, sc, 4, 3, bias)
+    xd = torch.from_numpy(x).to(dev)
+    xr = T.qscale_record(*xs)
+    y = torch.empty(112 * 256 * 256, dtype=torch.int32, device=dev)
+    yr = torch.zeros(4, dtype=torch.int64, device=dev)
+    conv.forward_int(xd, xr, 1024, 1024, y, yr)
+    t0 = time.perf_counter()
+    want, wso = O.ref_conv2d(x, xs, 3, 1024, 1024, wc.reshape(-1), sc, 112, 7, 7, 4, 3, bias)
+    cpu_conv_s = time.perf_counter() - t0
+    if not (np.array_equal(y.cpu().numpy(), want.reshape(-1)) and
+            tuple(T.read_qscale(yr)[k] for k in ("mant", "shift")) == wso):
+        raise SystemExit("bench: ref patch embed differs from the CPU oracle")
+    stream = torch.cuda.current_stream()
+    conv_ms, _ = time_launches(torch, lambda i: conv.forward_int(xd, xr, 1024, 1024, y, yr, stream=stream), 50, 10)
+    rows, dim, hid = 4096, 448, 1792
+    wi, wo = T.gen_uniform_fast(0xF1, -WL, WL, hid * dim), T.gen_uniform_fast(0xF2, -WL, WL, dim * hid)
+    bi = (T.gen_uniform_fast(0xF3, -(1 << 28), 1 << 28, hid).astype(np.int64), B.ref_scale_from_f64(1e-9))
+    bo = (T.gen_uniform_fast(0xF4, -(1 << 28), 1 << 28, dim).astype(np.int64), B.ref_scale_from_f64(1e-9))
+    ff = RefFeedForward(dim, hid, (wi, sc, bi), (wo, sc, bo))
+    fx = T.gen_uniform_fast(0xF5, -(1 << 28), 1 << 28, rows * dim)
+    fxs = B.ref_scale_from_f64(3.0 / (1 << 28))
+    fxd, fxr = torch.from_numpy(fx).to(dev), T.qscale_record(*fxs)
+    fy, fyr = ff.forward_int(fxd, fxr, rows)
+    fwant, fws = O.feedforward(fx, rows, dim, fxs, wi, sc, hid, wo, sc, bi, bo)
+    if not (np.array_equal(fy.cpu().numpy(), fwant.reshape(-1)) and
+            tuple(T.read_qscale(fyr)[k] for k in ("mant", "shift")) == fws):
+        raise SystemExit("bench: ref feedforward differs from the CPU oracle")
+    ff_ms, _ = time_launches(torch, lambda i: ff.forward_int(fxd, fxr, rows, stream=stream), 50, 10)
+    conv_ops, ff_ops = 2.0 * 65536 * 147 * 112, 2.0 * 2 * rows * dim * hid
+    return {
+        "workload": "SAM 2.1 Hiera-B+ at the reference's semantics: PatchEmbed Conv2d::forward_int (3 x 1024 x 1024 "
+                    "from_reals pixels, 112 channels, 7x7/4 pad 3: whole-image quant_to, im2col digit GEMM, bias, "
+                    "whole-output requant_dyn) and a stage-3 FeedForward (4096 x 448 -> 1792 GELU CodeLut -> 448)",
+        "bit_exact": True,
+        "patch_embed_us": round(conv_ms * 1e3, 1),
+        "patch_embed_effective_tops": round(conv_ops / (conv_ms * 1e-3) / 1e12, 2),
+        "feedforward_us": round(ff_ms * 1e3, 1),
+        "feedforward_effective_tops": round(ff_ops / (ff_ms * 1e-3) / 1e12, 2),
+        "cpu_baseline": {
+            "value": round(cpu_conv_s * 1e6, 0), "unit": "us per patch embed", "cores": 1, "nproc": os.cpu_count(),
+            "kind": "port", "sample": "the oracle's direct convolution (Conv2d::forward_int restated, one thread; "
+                                      "the reference splits the output channels over threads), one full image"},
+    }
+
+
+def bench_ref(torch, args) -> dict:
+    res = {"decoder": bench_ref_decoder(torch, args)}
+    torch.cuda.empty_cache()
+    res["sam"] = bench_ref_sam(torch, args)
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -677,9 +847,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--configs", type=str, default="2,3,4,5,ql,lb",
+    ap.add_argument("--configs", type=str, default="2,3,4,5,ql,lb,ref",
                     help="comma-separated configs to run (2 is the headline; ql = the reference's QuantLinear; "
-                         "lb = the LinearBackend trait path on cuda_bench's shapes)")
+                         "lb = the LinearBackend trait path on cuda_bench's shapes; ref = the reference-semantics "
+                         "decoder and SAM image path)")
     ap.add_argument("--ms", type=str, default="", help="comma-separated subset of config-2 M to run (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -721,6 +892,8 @@ def main() -> int:
         if c == "lb":
             extra["lb"] = bench_linear_backend(torch, args)
             torch.cuda.empty_cache()
+        if c == "ref":
+            extra["ref"] = bench_ref(torch, args)
 
     if headline is None:
         print(json.dumps({"sweep": sweep if "2" in configs else None, "configs": extra}), flush=True)

@@ -283,6 +283,49 @@ kt_refdec* kt_rd_synthetic(uint64_t seed, size_t dim, size_t layers, size_t nh, 
     return M;
 }
 
+/* A DecoderModel of the given shape whose codes and Scales the caller sets (kt_rd_set_*), with Attention::new's and
+ * SwiGluMlp::new's tables built here: the checker of a device model built from other inputs. */
+kt_refdec* kt_rd_new(size_t dim, size_t layers, size_t nh, size_t nkv, size_t hd, size_t hidden, size_t vocab,
+                     double eps, double theta, size_t max_seq) {
+    kt_refdec* M = (kt_refdec*)calloc(1, sizeof(kt_refdec));
+    M->dim = dim, M->layers = layers, M->nh = nh, M->nkv = nkv, M->hd = hd, M->hidden = hidden, M->vocab = vocab;
+    M->eps = eps, M->theta = theta, M->max_seq = max_seq;
+    M->L = (rd_layer*)calloc(layers, sizeof(rd_layer));
+    M->emb = (int32_t*)calloc(vocab * dim, sizeof(int32_t));
+    tables_build(M);
+    return M;
+}
+
+static rd_ql* ql_at(kt_refdec* M, size_t layer, int which) {
+    if (which == 7) return &M->lm_head;
+    rd_layer* L = &M->L[layer];
+    rd_ql* all[7] = {&L->wq, &L->wk, &L->wv, &L->wo, &L->gate, &L->up, &L->down};
+    return all[which];
+}
+
+/* Codes (out x in) and Scale of wq wk wv wo gate up down (0..6) of a layer, or the lm_head (7). */
+void kt_rd_set_ql(kt_refdec* M, size_t layer, int which, const int32_t* codes, size_t out, size_t in, kt_scale s) {
+    rd_ql* q = ql_at(M, layer, which);
+    free(q->w);
+    q->w = (int32_t*)malloc(out * in * sizeof(int32_t));
+    memcpy(q->w, codes, out * in * sizeof(int32_t));
+    q->out = out, q->in = in, q->s = s;
+}
+
+/* Gamma codes and Scale of in_norm (0) / post_norm (1) of a layer, or the final norm (2); eps from the model. */
+void kt_rd_set_norm(kt_refdec* M, size_t layer, int which, const int32_t* codes, kt_scale s) {
+    rd_norm* nm = which == 2 ? &M->final_norm : which == 0 ? &M->L[layer].in_norm : &M->L[layer].post_norm;
+    free(nm->w);
+    nm->w = (int32_t*)malloc(M->dim * sizeof(int32_t));
+    memcpy(nm->w, codes, M->dim * sizeof(int32_t));
+    nm->s = s, nm->eps = kt_scale_from_f64(M->eps), nm->dim = M->dim;
+}
+
+void kt_rd_set_emb(kt_refdec* M, const int32_t* codes, kt_scale s) {
+    memcpy(M->emb, codes, M->vocab * M->dim * sizeof(int32_t));
+    M->emb_scale = s;
+}
+
 static void ql_free(rd_ql* q) { free(q->w); }
 void kt_rd_free(kt_refdec* M) {
     if (!M) return;
@@ -373,7 +416,8 @@ void kt_rd_add(const int32_t* a, kt_scale as, const int32_t* b, kt_scale bs, siz
 
 static void ql(const rd_ql* q, const rd_t* x, rd_t* y) {
     int64_t xm, ym;
-    kt_quant_linear_forward(x->d, x->n / q->in, q->in, x->s, q->w, q->out, q->s, NULL, ZERO, 1, y->d, &y->s, &xm,
+    /* threads 0: linear_cpu's own plan_threads workers (backend.rs:89-94); any split gives the same integers */
+    kt_quant_linear_forward(x->d, x->n / q->in, q->in, x->s, q->w, q->out, q->s, NULL, ZERO, 0, y->d, &y->s, &xm,
                             &ym);
 }
 

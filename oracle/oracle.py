@@ -138,6 +138,10 @@ def _declare(L: C.CDLL) -> None:
         "kt_rd_add": (None, [_P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_swiglu_act": (None, [_P, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_attention_core": (None, [_P, _P, _P, Scale, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_new": (_P, [_SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_double, C.c_double, _SZ]),
+        "kt_rd_set_ql": (None, [_P, _SZ, C.c_int, _P, _SZ, _SZ, Scale]),
+        "kt_rd_set_norm": (None, [_P, _SZ, C.c_int, _P, Scale]),
+        "kt_rd_set_emb": (None, [_P, _P, Scale]),
         "kt_rd_get_ql": (Scale, [_P, _SZ, C.c_int, _P, C.POINTER(_SZ), C.POINTER(_SZ)]),
         "kt_rd_get_norm": (Scale, [_P, _SZ, C.c_int, _P, C.POINTER(Scale)]),
         "kt_rd_get_emb": (Scale, [_P, _P]),
@@ -764,6 +768,28 @@ class RefModel:
         c = self.cfg
         self.ptr = lib().kt_rd_synthetic(seed, c["dim"], c["layers"], c["nh"], c["nkv"], c["hd"], c["hidden"],
                                          c["vocab"], c["eps"], c["theta"], c["max_seq"])
+
+    @classmethod
+    def from_weights(cls, cfg: dict, emb, final_norm, lm_head, layers):
+        """The oracle's model of given codes and Scales, in RefDecoder's argument order."""
+        m = cls.__new__(cls)
+        m.cfg = dict(cfg)
+        c = m.cfg
+        m.ptr = lib().kt_rd_new(c["dim"], c["layers"], c["nh"], c["nkv"], c["hd"], c["hidden"], c["vocab"], c["eps"],
+                                c["theta"], c["max_seq"])
+        idx = {"wq": 0, "wk": 1, "wv": 2, "wo": 3, "gate": 4, "up": 5, "down": 6}
+        for l, lw in enumerate(layers):
+            for n, i in idx.items():
+                w = _c(lw[n][0], np.int32)
+                o, k = np.asarray(lw[n][0]).shape
+                lib().kt_rd_set_ql(m.ptr, l, i, _ptr(w), o, k, _sc(lw[n][1]))
+            for i, n in enumerate(("in_norm", "post_norm")):
+                lib().kt_rd_set_norm(m.ptr, l, i, _ptr(_c(lw[n][0], np.int32)), _sc(lw[n][1]))
+        lib().kt_rd_set_norm(m.ptr, 0, 2, _ptr(_c(final_norm[0], np.int32)), _sc(final_norm[1]))
+        lib().kt_rd_set_emb(m.ptr, _ptr(_c(emb[0], np.int32)), _sc(emb[1]))
+        w = _c(lm_head[0], np.int32)
+        lib().kt_rd_set_ql(m.ptr, 0, 7, _ptr(w), c["vocab"], c["dim"], _sc(lm_head[1]))
+        return m
 
     def __del__(self):
         if getattr(self, "ptr", None):

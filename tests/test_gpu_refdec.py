@@ -193,6 +193,38 @@ def test_synthetic_decoder_reproduces_the_golden(torch_dev):
     assert toks == toks_o and run == run_o == O.SYNTH_HASH
 
 
+def test_graph_replayed_greedy_steps_reproduce_the_golden(torch_dev):
+    """The same generation as replays of one captured greedy step (decode step + argmax_codes, the position advanced
+    and the logits recorded on the device): every recorded position's hash equals the oracle's and the run's hash is
+    8109ebad..."""
+    import hashlib
+
+    from tritify_amd.refdecoder import RefDecoder, logits_hash_bytes
+
+    say("case: synthetic decoder seed 7 as graph replays")
+    model = O.RefModel(7)
+    toks_o, run_o, pos_o = model.generate(O.SYNTH_PROMPT, 32)
+    dec = RefDecoder(O.SYNTH_CFG, *model.weights())
+    dec.decode_step(O.SYNTH_PROMPT[0], 0)  # workspaces exist before the capture
+    g = dec.capture_greedy_step()
+    dec.new_cache()
+    dec.pos.zero_()
+    for t in O.SYNTH_PROMPT:
+        dec.token.fill_(t)
+        g.replay()
+    for _ in range(31):
+        g.replay()
+    torch_dev.cuda.synchronize()
+    P = len(O.SYNTH_PROMPT)
+    rec = [dec.recorded(p) for p in range(P + 31)]
+    hashes = [hashlib.sha256(logits_hash_bytes(*r)).hexdigest() for r in rec]
+    assert hashes == pos_o
+    run = hashlib.sha256(b"".join(logits_hash_bytes(*r) for r in rec[P - 1:])).hexdigest()
+    assert run == run_o == O.SYNTH_HASH
+    assert [int(np.argmax(r[0])) for r in rec[P - 1:]] == toks_o
+    assert int(dec.pos.item()) == P + 31
+
+
 def test_qwen_shaped_decoder_against_the_oracle(torch_dev):
     """Two layers of the Qwen2.5-0.5B shape (dim 896, 14 / 2 heads of 64, SwiGLU 4864, theta 1e6) with a short
     vocabulary, seeded float weights quantized as the engine does: every position's logits hash equals the

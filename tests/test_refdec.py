@@ -157,3 +157,13 @@ def test_product_tables_equal_the_oracle(synth):
     half = c["hd"] // 2
     assert (pcos["mant"][:half] == 2**30).all() and (pcos["shift"][:half] == 30).all()
     assert (psin["mant"][:half] == 0).all()
+
+
+def test_the_oracle_model_from_given_codes_reproduces_the_golden():
+    """RefModel.from_weights (the checker of device models built from other inputs) over the seed-7 model's own
+    codes and Scales gives verify_repro's 8109ebad... and the same tokens."""
+    m = O.RefModel(7)
+    m2 = O.RefModel.from_weights(O.SYNTH_CFG, *m.weights())
+    toks, run, pos = m2.generate(O.SYNTH_PROMPT, 32)
+    assert run == O.SYNTH_HASH
+    assert (toks, pos) == m.generate(O.SYNTH_PROMPT, 32)[::2]

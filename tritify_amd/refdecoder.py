@@ -98,6 +98,10 @@ class RefDecoder:
     def new_cache(self) -> None:
         """A fresh KV cache (DecoderModel::new_cache, model.rs:280-284): per layer k and v codes and per-step scales."""
         torch = self.torch
+        if hasattr(self, "kc"):  # in place: a captured step keeps these buffers' addresses
+            for t in self.kc + self.vc + self.ks + self.vs:
+                t.zero_()
+            return
         kvd = self.nkv * self.hd
         self.kc = [torch.zeros(self.max_seq * kvd, dtype=torch.int32, device=self.device) for _ in range(self.nl)]
         self.vc = [torch.zeros(self.max_seq * kvd, dtype=torch.int32, device=self.device) for _ in range(self.nl)]
@@ -135,6 +139,34 @@ class RefDecoder:
         g, gs = self.final_norm
         B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
         self._ql(self.lm_head, "h", "logits", stream)
+
+    def capture_greedy_step(self):
+        """One position of greedy decoding as a HIP graph: decode_step of the token at self.token and position
+        self.pos, then argmax_codes into self.token, with the position's logits and scale recorded at
+        self.record[pos] and self.rscale[pos] and self.pos advanced -- so replays run a greedy generation with no host
+        work (a prompt position overwrites self.token before its replay). Call after one eager step (the launches'
+        workspaces exist)."""
+        torch = self.torch
+        if not hasattr(self, "record"):
+            self.record = torch.zeros(self.max_seq * self.vocab, dtype=torch.int32, device=self.device)
+            self.rscale = torch.zeros(self.max_seq * 16, dtype=torch.uint8, device=self.device)
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            g.capture_begin()
+            self.step_launches(stream=s)
+            B.ref_argmax(self.buf["logits"], self.vocab, self.rec["logits"], self.token, self.record, self.rscale,
+                         self.pos, s, self.dev)
+            g.capture_end()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        return g
+
+    def recorded(self, pos: int):
+        """The logits and scale a captured greedy step recorded at position `pos`: (codes, (mant, shift))."""
+        codes = self.record[pos * self.vocab:(pos + 1) * self.vocab].cpu().numpy()
+        w = self.rscale[pos * 16:(pos + 1) * 16].cpu().numpy()
+        return codes, (int(w.view(np.int64)[0]), int(w.view(np.int32)[2]))
 
     def decode_step(self, token: int, pos: int):
         """The logits of `token` at `pos` against the cache: (codes, (mant, shift)) on the host."""
