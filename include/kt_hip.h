@@ -149,7 +149,7 @@ typedef struct {
 #define KT_LUT_GELU 3    /* 0.5 x (1 + erf(x / sqrt 2)), erf by A&S 7.1.26: build_gelu_lut (kt-model-vision/src/
                             nonlin.rs:7-26) */
 #define KT_REF_MAX_HEADS 64
-#define KT_REF_ATTN_LDS 65536 /* the attention step's LDS: 40 B per cached position + 12 B per q value + 8 KB */
+#define KT_REF_ATTN_LDS 65536 /* the attention step's LDS: at least 40 B per cached position + 12 B per q value */
 
 /* Offline tables (host only, no GPU; f64 with the C library's exp/pow/cos/sin, as the reference's f64 methods use
  * its platform's): Scale::from_f64 (lib.rs:215-222); CodeLut::build (lib.rs:359-379) of `kind` over [lo, hi] at

@@ -93,7 +93,7 @@ hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* 
                                   const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift,
                                   int8_t* y, int ystride, hipStream_t s);
 struct RdAttn;
-size_t rd_attention_lds(int max_seq, int nh, int hd);
+size_t rd_attention_lds(int max_seq, int nh, int hd, int hb);
 hipError_t launch_rd_embed(const int32_t* emb, int64_t e_mant, int32_t e_shift, const int32_t* token, int vocab,
                            int dim, int32_t* y, kt_hip_qscale* ys, hipStream_t s);
 hipError_t launch_rd_rmsnorm(const int32_t* x, int rows, int dim, const kt_hip_qscale* xs, const int32_t* g,

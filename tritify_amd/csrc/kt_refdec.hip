@@ -45,6 +45,7 @@ struct RdAttn {
     const kt_hip_qscale *qs, *ks, *vs;
     const int32_t* pos;
     int nh, nkv, hd, max_seq;
+    int hb;                            // heads whose scores LDS holds at once
     int32_t *kc, *vc;                  // [max_seq][nkv * hd]
     kt_hip_sscale *kscale, *vscale;    // [max_seq]
     const kt_hip_sscale *cos, *sin;    // [max_seq][hd / 2]
@@ -322,10 +323,9 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     const int steps = pos + 1;
     Sc* F = reinterpret_cast<Sc*>(lds);  // score factors, per step
     Sc* VF = F + a.max_seq;              // v factors, per step
-    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);  // scores, then exp codes, per step
-    int64_t* HO = S + a.max_seq;                                // head outputs, qstride
-    int64_t* PART = HO + qstride;                               // partial P.V sums, one per thread
-    int32_t* QD = reinterpret_cast<int32_t*>(PART + RD_THREADS);  // rotated q, qstride
+    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);   // scores, then exp codes: [hb][max_seq]
+    int64_t* HO = S + (size_t)a.hb * a.max_seq;                  // head outputs, qstride
+    int32_t* QD = reinterpret_cast<int32_t*>(HO + qstride);     // rotated q, qstride
 
     // 1. RoPE and the cache append
     auto rot = [&](const int32_t* src, int32_t* dst, int heads) {
@@ -381,51 +381,64 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     }
     __syncthreads();
 
-    // 3. the heads
-    const int chunks = RD_THREADS / hd, d = tid % hd, c = tid / hd;
-    for (int h = 0; h < nh; h++) {
-        const int kv = h / group;
+    // 3. the heads, hb at a time: the scores by one wave per (head, cached row) with the lanes across head_dim, the
+    //    integer softmax by one wave per head, P.V by one thread per (head, dim). Sums wrap as i64 (any order gives
+    //    the reference's integers).
+    const int lane = tid & 63, wave = tid >> 6;
+    __shared__ int64_t hsum[KT_REF_MAX_HEADS];
+    for (int h0 = 0; h0 < nh; h0 += a.hb) {
+        const int hn = nh - h0 < a.hb ? nh - h0 : a.hb;
         if (s_ref.mant == 0) {  // every head skipped (the reference's `continue`)
-            for (int i = tid; i < hd; i += RD_THREADS) HO[h * hd + i] = 0;
-            if (tid == 0) hsc[h] = Sc{0, 0};
+            for (int i = tid; i < hn * hd; i += RD_THREADS) HO[h0 * hd + i] = 0;
+            if (tid < hn) hsc[h0 + tid] = Sc{0, 0};
             continue;
         }
-        int64_t m = INT64_MIN;
-        for (int j = tid; j < steps; j += RD_THREADS) {
+        for (int it = wave; it < hn * steps; it += RD_WAVES) {
+            const int h = it / steps, j = it - h * steps, kv = (h0 + h) / group;
             const int32_t* kr = a.kc + (size_t)j * kstride + kv * hd;
+            const int32_t* qh = QD + (h0 + h) * hd;
             int64_t dot = 0;
-            for (int e = 0; e < hd; e++) dot = wadd(dot, wmul(QD[h * hd + e], kr[e]));
-            S[j] = sc_apply(F[j], dot);
-            m = S[j] > m ? S[j] : m;
+            for (int e = lane; e < hd; e += 64) dot = wadd(dot, wmul(qh[e], kr[e]));
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) dot = wadd(dot, __shfl_xor(dot, o, 64));
+            if (lane == 0) S[(size_t)h * a.max_seq + j] = sc_apply(F[j], dot);
         }
-        const int64_t dmax = block_max_i64(m, red);
-        int64_t sum = 0;
-        for (int j = tid; j < steps; j += RD_THREADS) {
-            const int64_t idx = lut_index(lm, S[j] - dmax, a.exp.lo_index);
-            S[j] = idx < 0 ? 0 : lut_code(a.exp_codes, a.exp.n, idx);
-            sum += S[j];
-        }
-        const int64_t sumc = block_sum_i64(sum, red);  // also orders the S writes before the reads below
-        if (sumc <= 0) {
-            for (int i = tid; i < hd; i += RD_THREADS) HO[h * hd + i] = 0;
-            if (tid == 0) hsc[h] = Sc{0, 0};
-            continue;
-        }
-        int64_t acc = 0;
-        if (c < chunks)
-            for (int j = c; j < steps; j += chunks)
-                acc = wadd(acc, wmul(S[j], sc_apply(VF[j], a.vc[(size_t)j * kstride + kv * hd + d])));
-        PART[tid] = acc;
         __syncthreads();
-        if (tid < hd) {
-            int64_t t = 0;
-            for (int cc = 0; cc < chunks; cc++) t = wadd(t, PART[cc * hd + tid]);
-            HO[h * hd + tid] = t;
+        for (int h = wave; h < hn; h += RD_WAVES) {
+            int64_t* sh = S + (size_t)h * a.max_seq;
+            int64_t m = INT64_MIN;
+            for (int j = lane; j < steps; j += 64) m = sh[j] > m ? sh[j] : m;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const int64_t u = __shfl_xor(m, o, 64);
+                m = u > m ? u : m;
+            }
+            int64_t sum = 0;
+            for (int j = lane; j < steps; j += 64) {
+                const int64_t idx = lut_index(lm, (int64_t)((uint64_t)sh[j] - (uint64_t)m), a.exp.lo_index);
+                sh[j] = idx < 0 ? 0 : lut_code(a.exp_codes, a.exp.n, idx);
+                sum += sh[j];
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) sum = wadd(sum, __shfl_xor(sum, o, 64));
+            if (lane == 0) {
+                hsum[h] = sum;
+                hsc[h0 + h] = sum <= 0 ? Sc{0, 0} : sc_mul(v_ref, from_ratio(1, (u128)(uint64_t)sum));
+            }
         }
-        if (tid == 0) hsc[h] = sc_mul(v_ref, from_ratio(1, (u128)(uint64_t)sumc));
         __syncthreads();
+        for (int it = tid; it < hn * hd; it += RD_THREADS) {
+            const int h = it / hd, dd = it - h * hd, kv = (h0 + h) / group;
+            int64_t acc = 0;
+            if (hsum[h] > 0) {
+                const int64_t* sh = S + (size_t)h * a.max_seq;
+                const int32_t* vcol = a.vc + kv * hd + dd;
+                for (int j = 0; j < steps; j++) acc = wadd(acc, wmul(sh[j], sc_apply(VF[j], vcol[(size_t)j * kstride])));
+            }
+            HO[(h0 + h) * hd + dd] = acc;
+        }
+        __syncthreads();  // S and hsum are reused by the next batch
     }
-    __syncthreads();
 
     // 4. one scale for the concatenated heads
     if (tid == 0) {
@@ -478,8 +491,16 @@ __global__ __launch_bounds__(RD_THREADS) void rd_argmax_kernel(const int32_t* __
     if (threadIdx.x == 0) *token = 0x7FFFFFFF - (int32_t)(uint32_t)(best & 0xFFFFFFFF);
 }
 
-size_t rd_attention_lds(int max_seq, int nh, int hd) {
-    return (size_t)max_seq * (2 * sizeof(Sc) + 8) + (size_t)nh * hd * (8 + 4) + RD_THREADS * 8;
+// The attention step's LDS with hb heads' scores held at once: the per-step factors, hb score rows, the head
+// outputs and the rotated q. hb = 1 is the least it runs with.
+size_t rd_attention_lds(int max_seq, int nh, int hd, int hb) {
+    return (size_t)max_seq * (2 * sizeof(Sc) + 8 * (size_t)hb) + (size_t)nh * hd * (8 + 4);
+}
+static int rd_attention_hb(int max_seq, int nh, int hd) {
+    const size_t base = rd_attention_lds(max_seq, nh, hd, 0);
+    if (base >= KT_REF_ATTN_LDS) return 0;
+    const size_t hb = (KT_REF_ATTN_LDS - base) / (8 * (size_t)max_seq);
+    return (int)(hb < (size_t)nh ? hb : (size_t)nh);
 }
 
 hipError_t launch_rd_embed(const int32_t* emb, int64_t e_mant, int32_t e_shift, const int32_t* token, int vocab,
@@ -512,10 +533,11 @@ hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, 
     rd_gelu_kernel<<<(unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g)), RD_THREADS, 0, s>>>(x, xs, n, codes, *lut, y, ys);
     return hipGetLastError();
 }
-hipError_t launch_rd_attention_step(const RdAttn& a, hipStream_t s) {
-    const size_t lds = rd_attention_lds(a.max_seq, a.nh, a.hd);
-    if (lds > KT_REF_ATTN_LDS) return hipErrorInvalidValue;
-    rd_attention_step_kernel<<<1, RD_THREADS, lds, s>>>(a);
+hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
+    RdAttn a = a_in;
+    a.hb = rd_attention_hb(a.max_seq, a.nh, a.hd);
+    if (a.hb < 1) return hipErrorInvalidValue;
+    rd_attention_step_kernel<<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
     return hipGetLastError();
 }
 hipError_t launch_rd_argmax(const int32_t* logits, int n, const kt_hip_qscale* ls, int32_t* token, int32_t* record,
@@ -636,7 +658,7 @@ extern "C" int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt
         !kscale_dev || !vscale_dev || !cos_dev || !sin_dev || !exp_codes_dev || !exp_lut || !o_dev || !os_dev)
         return (int)hipErrorInvalidValue;
     if (nh < 1 || nkv < 1 || nh % nkv || nh > KT_REF_MAX_HEADS || hd < 2 || (hd & 1) || hd > 1024 || max_seq < 1 ||
-        exp_lut->n < 1 || isq_mant < 0 || kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd) > KT_REF_ATTN_LDS)
+        exp_lut->n < 1 || isq_mant < 0 || kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd, 1) > KT_REF_ATTN_LDS)
         return (int)hipErrorInvalidValue;
     RD_TRY(hipSetDevice(dev));
     kt::RdAttn a{};

@@ -22,9 +22,24 @@ __device__ inline int bits_u128(u128 v) {
     return hi ? 128 - __clzll((long long)hi) : (lo ? 64 - __clzll((long long)lo) : 0);
 }
 
-// n / d for d > 0: native when both fit 64 bits, else restoring long division.
+// floor(n / d) for d > 0, exact for every input:
+//  - both below 2^64: the 64-bit division;
+//  - d below 2^64 and the quotient below 2^49 (bits(n) - bits(d) < 49; every quotient of from_ratio, whose mantissa
+//    is below 2^33, and of isqrt's Newton steps): a double-precision estimate, whose relative error is at most
+//    5 * 2^-53 (the conversions of n's two halves and of d, their sum, the quotient), so at most 5/16 absolute,
+//    corrected against the exact i128 remainder (n < 2^113 here, so the remainder fits);
+//  - otherwise restoring long division.
 __device__ inline u128 udiv128(u128 n, u128 d) {
     if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
+    if ((d >> 64) == 0 && bits_u128(n) - bits_u128(d) < 49) {
+        const uint64_t d64 = (uint64_t)d;
+        const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
+        uint64_t q = (uint64_t)(dn / (double)d64);
+        i128 rem = (i128)n - (i128)q * (i128)d64;
+        while (rem < 0) q--, rem += (i128)d64;
+        while (rem >= (i128)d64) q++, rem -= (i128)d64;
+        return (u128)q;
+    }
     u128 q = 0, r = 0;
     for (int i = bits_u128(n) - 1; i >= 0; i--) {
         r = (r << 1) | ((n >> i) & 1);
