@@ -537,13 +537,15 @@ def bench_config3(torch, args) -> dict:
                                  "3 rotating weight copies"},
     }
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline_decoder(cfg, layers, emb, cos, sin, prompt, g3["h_shift"])
+        res["cpu_baseline"] = ref_decoder_cpu_baseline()
+        res["cpu_this_build_rules"] = cpu_baseline_decoder(cfg, layers, emb, cos, sin, prompt, g3["h_shift"])
     return res
 
 
 def cpu_baseline_decoder(cfg, layers, emb, cos, sin, prompt, h_shift) -> dict:
-    """The oracle's restatement of the reference decoder loop (generate_greedy_by, generate.rs:82-111) on a bounded
-    sample: a 32-token prompt and 4 greedy decode steps, on this host's cores."""
+    """This build's W12 int8 decoder on the CPU (the oracle's restatement of it, in the reference's decoder loop,
+    generate_greedy_by, generate.rs:82-111) on a bounded sample: a 32-token prompt and 4 greedy decode steps, on this
+    host's cores. Reported beside the reference's own decoder, which is config 3's CPU baseline."""
     from oracle import oracle as O
     from tritify_amd import workloads as W
 
@@ -701,16 +703,46 @@ def ref_decoder_weights(cfg: dict, seed: int):
     return (codes(V, d), sc), (codes(d), sc), (codes(V, d), sc), layers
 
 
+REF_PROMPT, REF_NDEC = [9, 1000, 20000, 151935], 28
+_ref_cpu: dict = {}
+
+
+def ref_decoder_oracle() -> tuple:
+    """The oracle's restatement of the reference decoder over REF_QWEN (the weights of ref_decoder_weights): every
+    position's logits hash of repro::run over REF_PROMPT and REF_NDEC greedy steps, the seconds it took, the
+    threads. Run once per bench and shared by config 3's CPU baseline and the ref entry's check."""
+    if not _ref_cpu:
+        from oracle import oracle as O
+
+        log("bench: the reference decoder on the CPU (the oracle), Qwen2.5-0.5B shape")
+        model = O.RefModel.from_weights(REF_QWEN, *ref_decoder_weights(REF_QWEN, 0x5EED))
+        cores = cpu_threads()
+        O.set_max_threads(cores)
+        t0 = time.perf_counter()
+        _, _, want = model.generate(REF_PROMPT, REF_NDEC + 1)
+        _ref_cpu.update(hashes=want, seconds=time.perf_counter() - t0, cores=cores)
+    return _ref_cpu["hashes"], _ref_cpu["seconds"], _ref_cpu["cores"]
+
+
+def ref_decoder_cpu_baseline() -> dict:
+    hashes, secs, cores = ref_decoder_oracle()
+    npos = len(hashes)
+    return {"value": round(npos / secs, 2), "unit": "tokens/s", "cores": cores, "nproc": os.cpu_count(),
+            "kind": "port",
+            "sample": f"the reference's own decoder at the Qwen2.5-0.5B shape (the oracle's restatement: repro::run "
+                      f"over {len(REF_PROMPT)} prompt and {REF_NDEC} greedy positions, 12-trit weights, every "
+                      f"QuantLinear through the threaded linear_cpu restatement), {secs * 1e3 / npos:.0f} ms/position"}
+
+
 def bench_ref_decoder(torch, args) -> dict:
     """The reference's DecoderModel (model.rs:290-353) at its own semantics on the device, Qwen2.5-0.5B shape: a
     4-token prompt then greedy decode, one captured HIP graph per position (decode step + argmax_codes, the
     position advanced and the logits recorded on the device). Every recorded position's logits_hash is checked
     against the oracle's restatement before the timing is reported; the oracle's run is the CPU baseline."""
-    from oracle import oracle as O
     from tritify_amd.refdecoder import RefDecoder, logits_hash_bytes
 
     cfg = REF_QWEN
-    prompt, n_dec = [9, 1000, 20000, 151935], 28
+    prompt, n_dec = REF_PROMPT, REF_NDEC
     t0 = time.perf_counter()
     w = ref_decoder_weights(cfg, 0x5EED)
     dec = RefDecoder(cfg, *w)
@@ -736,16 +768,10 @@ def bench_ref_decoder(torch, args) -> dict:
         best = ms if best is None else min(best, ms)
     npos = len(prompt) + n_dec
     got = [hashlib.sha256(logits_hash_bytes(*dec.recorded(p))).hexdigest() for p in range(npos)]
-    del dec, g
+    del dec, g, w
     torch.cuda.empty_cache()
     log(f"bench: ref decoder: checking {npos} positions against the oracle (CPU)")
-    model = O.RefModel.from_weights(cfg, *w)
-    del w
-    cores = cpu_threads()
-    O.set_max_threads(cores)
-    t0 = time.perf_counter()
-    _, _, want = model.generate(prompt, n_dec + 1)
-    cpu_s = time.perf_counter() - t0
+    want, _, _ = ref_decoder_oracle()
     if got != want:
         first = next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
         raise SystemExit(f"bench: ref decoder: position {first} differs from the CPU oracle")
@@ -760,12 +786,7 @@ def bench_ref_decoder(torch, args) -> dict:
         "decode_tokens_per_s": round(1e3 / best, 1),
         "decode_us_per_token": round(best * 1e3, 1),
         "weight_plane_gbs": round(wbytes / (best * 1e-3) / 1e9, 1),
-        "cpu_baseline": {
-            "value": round(npos / cpu_s, 2), "unit": "tokens/s", "cores": cores, "nproc": os.cpu_count(),
-            "kind": "port",
-            "sample": f"the oracle's restatement of the reference decoder (repro::run over {len(prompt)} prompt and "
-                      f"{n_dec} greedy positions, every QuantLinear through the threaded linear_cpu restatement), "
-                      f"{cpu_s * 1e3 / npos:.0f} ms/position"},
+        "cpu_baseline": ref_decoder_cpu_baseline(),
     }
 
 
