@@ -486,3 +486,48 @@ def test_config2_full_size_against_fixtures(torch_dev):
         torch.cuda.synchronize()
         assert O.sha256_hex(acc.cpu().numpy()) == want["acc_i64_sha256"], m
         assert O.sha256_hex(q.cpu().numpy()) == want["out_i8_sha256"], m
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 2048, 512), (161, 250, 448), (520, 4010, 200)])
+def test_w12_small_tile_variants_every_output(torch_dev, m, n, k):
+    """The dense W12 products on the smaller CTA tiles chosen when 128 x 128 tiles leave CUs idle: 512 x 2048 x 512
+    lands on the 64 x 64 variant (tiles_h = 128, tiles_q = 256), the ragged 161 x 250 x 448 on 32 x 64, the ragged
+    520 x 4010 x 200 on 64 x 128 (tiles_h = 288); each for i64, i32, int8, the saturating residual add (from residuals
+    at both int32 limits) and the int8 code table."""
+    torch = torch_dev
+    T = tb()
+    rng = np.random.default_rng(m + n + k)
+    x = rng.integers(-128, 128, size=m * k).astype(np.int32)
+    w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
+    mant, shift = O.channel_scales(w, n, k, 40)
+    mant[::7] = 2**31 - 1  # some channels far past int8 / int32 after the requant
+    lo, nib = _w12_device(torch, w, n, k)
+    xd = _x_device(torch, x, m, k)
+    md, sd = torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda()
+    acc = O.portable(x, w, m, n, k)
+    for out_kind in (0, 1, 2, 3):
+        say(f"case: w12 small-tile {m}x{n}x{k} out_kind={out_kind}")
+        dt = {0: torch.int64, 1: torch.int32, 2: torch.int8, 3: torch.int32}[out_kind]
+        prev = rng.integers(-(2**31), 2**31, size=m * n, dtype=np.int64).astype(np.int32)
+        prev[::5] = 2**31 - 1
+        prev[1::5] = -(2**31)
+        y = torch.from_numpy(prev.copy()).cuda() if out_kind == 3 else torch.empty(m * n, dtype=dt, device="cuda")
+        T.w12_linear(xd, lo, nib, m, n, k, y, out_kind, md, sd)
+        torch.cuda.synchronize()
+        if out_kind == 0:
+            want = acc
+        elif out_kind == 1:
+            want = O.requant_channels(acc, m, n, mant, shift, -(2**31), 2**31 - 1)
+        elif out_kind == 2:
+            want = O.requant_channels(acc, m, n, mant, shift, -127, 127).astype(np.int8)
+        else:
+            q = O.requant_channels(acc, m, n, mant, shift, -(2**31), 2**31 - 1).astype(np.int64)
+            want = np.clip(prev.astype(np.int64) + q, -(2**31), 2**31 - 1).astype(np.int32)
+        assert np.array_equal(y.cpu().numpy(), want), out_kind
+    say(f"case: w12 small-tile {m}x{n}x{k} lut")
+    lut = rng.integers(-128, 128, size=255).astype(np.int8)
+    y = torch.empty(m * n, dtype=torch.int8, device="cuda")
+    T.w12_linear_lut(xd, lo, nib, m, n, k, y, md, sd, torch.from_numpy(lut).cuda())
+    torch.cuda.synchronize()
+    q8 = O.requant_channels(acc, m, n, mant, shift, -127, 127).astype(np.int64)
+    assert np.array_equal(y.cpu().numpy(), lut[q8 + 127])

@@ -238,18 +238,22 @@ def test_decoder_long_context_step(torch_dev, fuse):
     assert np.array_equal(logits.reshape(-1), wl) and np.array_equal(toks, wt)
 
 
-def test_fold_o_entry_points_saturate(torch_dev):
+@pytest.mark.parametrize("ffn", [192, 1500, 4864])
+def test_fold_o_entry_points_saturate(torch_dev, ffn):
     """The decode step's o-projection fold through the C ABI against the unfused integers: kt_hip_w12_linear_add_o
     adds the requantized o sums into the residual and then its own requantized product, each addition saturating
     (residual entries at the int32 limits, o sums at both signs), and clears the accumulator; twice in a row on
-    one accumulator. (The gate/up side of the fold is covered by the decoder runs against the oracle.)"""
+    one accumulator, the second call's sums added on the device to what the first call left (so the cleared state
+    is what the next step starts from). ffn 192, 1500 and 4864 reach the kernel's three builds (8 waves x 2 pairs,
+    x 4 pairs, 16 waves x 5 pairs). (The gate/up side of the fold is covered by the decoder runs against the
+    oracle.)"""
     import tritify_amd as T
 
     torch = torch_dev
     lib, P = T.lib(), T.backend._ptr
     s = torch.cuda.current_stream().cuda_stream
-    d, ffn = 128, 192
-    rng = np.random.default_rng(77)
+    d = 128
+    rng = np.random.default_rng(77 + ffn)
     w_dn = rng.integers(-2048, 2048, size=d * ffn).astype(np.int32)
     dm, dsh = O.channel_scales(w_dn, d, ffn, 40)
     om = rng.integers(1 << 29, 1 << 30, size=d).astype(np.int32)
@@ -271,7 +275,10 @@ def test_fold_o_entry_points_saturate(torch_dev):
         dot = O.linear_threads(h.astype(np.int32), w_dn, 1, d, ffn, 1, O.lib().kt_cpu_auto_variant())
         want = np.clip(ro + O.requant_channels(dot, 1, d, dm, dsh, -(2**31), 2**31 - 1), -(2**31), 2**31 - 1)
         say(f"case: fold-o down d={d} ffn={ffn} call {call}")
-        acc_d.copy_(dev(acc))
+        if call == 0:
+            acc_d.copy_(dev(acc))
+        else:  # onto what the first call left: equal to acc only if that is zero everywhere
+            acc_d.add_(dev(acc))
         r_d = dev(r)
         h_d = torch.zeros(T.kp(ffn), dtype=torch.int8, device="cuda")
         h_d[:ffn] = dev(h)

@@ -215,14 +215,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_
                         atomicAdd(reinterpret_cast<unsigned long long*>(y + (size_t)m * N + n), (unsigned long long)v);
                 }
             }
-        // Every partial went to y as a device-scope atomic, performed where all CTAs' atomics are: once a wave's
-        // vector-memory count drains they are done, and the barrier then orders them before the tile's arrival
-        // (no cache write-back is needed, there are no plain stores to publish). The last CTA reads the sums
-        // with device-scope loads.
+        // The hand-off in the memory model. The partial sums are agent-scope atomic read-modify-writes; each wave
+        // releases them at workgroup scope (its own atomics performed) before the barrier, which orders them before
+        // thread 0's arrival on the tile's counter, an agent-scope acquire-release. The CTA that completes the
+        // count has acquired every other CTA's sums there; the barrier after it carries that to all its waves,
+        // which read the sums with agent-scope atomic loads.
         __shared__ int s_last;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __syncthreads();
-        if (tid == 0) s_last = atomicAdd(&tile_cnt[blockIdx.x], 1u) == gridDim.y - 1;
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(&tile_cnt[blockIdx.x], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+                     gridDim.y - 1;
         __syncthreads();
         if (!s_last) return;  // uniform
     }
