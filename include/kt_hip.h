@@ -172,7 +172,25 @@ int kt_hip_ref_from_reals(const double* real, int64_t n, int64_t levels, int32_t
  * vocab x dim code table at Scale (e_mant, e_shift); a token outside [0, vocab) gives zeros at Scale::ZERO. */
 int kt_hip_ref_embed(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_shift, const int32_t* token_dev,
                      int64_t vocab, int64_t dim, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
-/* RmsNorm::forward_int (layers.rs:392-434) of rows (<= 64) x dim codes at xs: gamma codes g_dev at (g_mant,
+/* Embedding::lookup_seq (layers.rs:1138-1145): y (T x dim codes) = the rows of the T tokens at tokens_dev, at the
+ * table's Scale; a token outside [0, vocab) gives a zero row (the reference panics). */
+int kt_hip_ref_embed_seq(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_shift, const int32_t* tokens_dev,
+                         int64_t T, int64_t vocab, int64_t dim, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+/* Attention::forward_int between its projections over a whole sequence (attention.rs:467-598), the prefill of
+ * DecoderModel's batched forward: q (T x nh hd), k and v (T x nkv hd) codes at one Scale each; row i rotated at
+ * position i (the RoPE tables of kt_hip_ref_rope_tables, T <= max_seq); per head and row the causal integer-code
+ * softmax at the one score scale q.scale * k.scale * (isq_mant, isq_shift) with the exp CodeLut; per (row, head)
+ * the scale v.scale / sumc; all brought to their largest (the engine's fold over the [row][head] order) and
+ * requantized: o_dev (T x nh hd) and os_dev. hd <= 256, T <= 8192; the workspace holds
+ * kt_hip_ref_attention_prefill_workspace bytes (0: out of range). */
+size_t kt_hip_ref_attention_prefill_workspace(int64_t T, int64_t nh, int64_t nkv, int64_t hd);
+int kt_hip_ref_attention_prefill(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev, const int32_t* k_dev,
+                                 const kt_hip_qscale* ks_dev, const int32_t* v_dev, const kt_hip_qscale* vs_dev,
+                                 int64_t T, int64_t nh, int64_t nkv, int64_t hd, int64_t max_seq,
+                                 const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev, int64_t isq_mant,
+                                 int32_t isq_shift, const int64_t* exp_codes_dev, const kt_hip_codelut* exp_lut,
+                                 void* ws_dev, size_t ws_bytes, int32_t* o_dev, kt_hip_qscale* os_dev, void* stream);
+/* RmsNorm::forward_int (layers.rs:392-434) of rows (<= 1024) x dim codes at xs: gamma codes g_dev at (g_mant,
  * g_shift), eps as the Scale (eps_mant, eps_shift). */
 int kt_hip_ref_rmsnorm(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t rows, int64_t dim,
                        const int32_t* g_dev, int64_t g_mant, int32_t g_shift, int64_t eps_mant, int32_t eps_shift,

@@ -587,6 +587,124 @@ void kt_rd_decode_step(const void* model, void** caches, int64_t token, size_t p
     for (size_t i = 0; i < sizeof all / sizeof all[0]; i++) t_free(all[i]);
 }
 
+/* Attention::forward_int between its projections over a whole sequence (attention.rs:467-598): rows i = 0..T-1 of
+ * q (nh heads) and k (nkv heads) rotated at position i; per head and row the causal scores j <= i (exact i64 dots)
+ * at the one score scale q.scale * k.scale * inv_sqrt, the exp-CodeLut numerators of (dot - max), their sum and
+ * the sum of numerator * v over the rows (v at its one scale); per (row, head) the scale v.scale / sumc; their
+ * largest (the engine's fold over the [row][head] order), every output brought to it, then requant_dyn. q: T x
+ * nh*hd, k and v: T x nkv*hd codes; o: T x nh*hd. Sums wrap as the reference's release build does. */
+void kt_rd_attention_prefill(const void* model, size_t T, const int32_t* q, kt_scale qs, const int32_t* k,
+                             kt_scale ks, const int32_t* v, kt_scale vs, int32_t* o, kt_scale* os) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    const size_t hd = M->hd, nh = M->nh, nkv = M->nkv, group = nh / nkv, qs_ = nh * hd, ks_ = nkv * hd;
+    const kt_scale s_score = kt_scale_mul(kt_scale_mul(qs, ks), M->inv_sqrt);
+    int32_t* qd = (int32_t*)malloc(T * qs_ * sizeof(int32_t) + 4);
+    int32_t* kd = (int32_t*)malloc(T * ks_ * sizeof(int32_t) + 4);
+    memcpy(qd, q, T * qs_ * sizeof(int32_t));
+    memcpy(kd, k, T * ks_ * sizeof(int32_t));
+    for (size_t i = 0; i < T; i++) {
+        for (size_t h = 0; h < nh; h++) rope(M, qd + i * qs_ + h * hd, i);
+        for (size_t h = 0; h < nkv; h++) rope(M, kd + i * ks_ + h * hd, i);
+    }
+    int64_t* head_out = (int64_t*)calloc(nh * T * hd + 1, sizeof(int64_t));
+    int64_t* head_sum = (int64_t*)calloc(nh * T + 1, sizeof(int64_t));
+    int64_t* dots = (int64_t*)malloc((T + 1) * sizeof(int64_t));
+    int64_t* ec = (int64_t*)malloc((T + 1) * sizeof(int64_t));
+    for (size_t h = 0; h < nh; h++) {
+        const size_t kv = h / group;
+        for (size_t i = 0; i < T; i++) {
+            int64_t dmax = INT64_MIN;
+            for (size_t j = 0; j <= i; j++) {
+                int64_t dot = 0;
+                for (size_t d = 0; d < hd; d++) dot = wadd(dot, wmul(qd[i * qs_ + h * hd + d], kd[j * ks_ + kv * hd + d]));
+                dots[j] = dot;
+                dmax = dot > dmax ? dot : dmax;
+            }
+            int64_t sumc = 0;
+            for (size_t j = 0; j <= i; j++) {
+                const int64_t idx = lut_index(&M->exp_code, wadd(dots[j], 0 - (uint64_t)dmax), s_score);
+                ec[j] = idx < 0 ? 0 : lut_code_at(&M->exp_code, idx);
+                sumc += ec[j];
+            }
+            if (sumc > 0) {
+                for (size_t d = 0; d < hd; d++) {
+                    int64_t acc = 0;
+                    for (size_t j = 0; j <= i; j++) acc = wadd(acc, wmul(ec[j], v[j * ks_ + kv * hd + d]));
+                    head_out[(h * T + i) * hd + d] = acc;
+                }
+                head_sum[h * T + i] = sumc;
+            }
+        }
+    }
+    kt_scale* sc = (kt_scale*)malloc((T * nh + 1) * sizeof(kt_scale));
+    kt_scale common = ZERO;
+    for (size_t i = 0; i < T; i++)
+        for (size_t h = 0; h < nh; h++) {
+            const int64_t sumc = head_sum[h * T + i];
+            sc[i * nh + h] = sumc > 0 ? kt_scale_mul(vs, ratio(1, (u128)sumc)) : ZERO;
+            common = fold_max(common, sc[i * nh + h]);
+        }
+    const size_t n = T * qs_;
+    if (common.mant == 0) {
+        memset(o, 0, n * sizeof(int32_t));
+        *os = ZERO;
+    } else {
+        const kt_scale cinv = kt_scale_recip(common);
+        int64_t* vv = (int64_t*)malloc((n + 1) * sizeof(int64_t));
+        for (size_t i = 0; i < T; i++)
+            for (size_t h = 0; h < nh; h++) {
+                const kt_scale f = kt_scale_mul(sc[i * nh + h], cinv);
+                for (size_t d = 0; d < hd; d++)
+                    vv[i * qs_ + h * hd + d] = kt_scale_apply(f, head_out[(h * T + i) * hd + d]);
+            }
+        rd_t out = {o, n, ZERO};
+        close_dyn(vv, n, common, &out);
+        *os = out.s;
+        free(vv);
+    }
+    free(qd), free(kd), free(head_out), free(head_sum), free(dots), free(ec), free(sc);
+}
+
+/* CausalLM::forward_int of DecoderModel (model.rs:361-367 = embed_int, blocks_int, head_int; model.rs:168-189):
+ * the T tokens' embedding rows as one tensor, per block input_norm -> Attention::forward_int -> add, post_norm ->
+ * SwiGluMlp::forward_int -> add, every op over the whole T-row tensor (one dynamic quantization per tensor), then
+ * the final norm and the lm_head: logits T x vocab at *ls. T must not exceed max_seq (the reference asserts). */
+int kt_rd_forward(const void* model, const int32_t* tokens, size_t T, int32_t* logits, kt_scale* ls) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    if (T == 0 || T > M->max_seq) return -1;
+    for (size_t i = 0; i < T; i++)
+        if (tokens[i] < 0 || (size_t)tokens[i] >= M->vocab) return -1;
+    const size_t dim = M->dim, qd = M->nh * M->hd, kvd = M->nkv * M->hd, hid = M->hidden;
+    rd_t x = t_new(T * dim), h = t_new(T * dim), a = t_new(T * dim), q = t_new(T * qd), k = t_new(T * kvd);
+    rd_t v = t_new(T * kvd), cat = t_new(T * qd), g = t_new(T * hid), u = t_new(T * hid), hh = t_new(T * hid);
+    rd_t m = t_new(T * dim), x2 = t_new(T * dim);
+    for (size_t i = 0; i < T; i++) memcpy(x.d + i * dim, M->emb + (size_t)tokens[i] * dim, dim * sizeof(int32_t));
+    x.s = M->emb_scale;
+    for (size_t l = 0; l < M->layers; l++) {
+        const rd_layer* L = &M->L[l];
+        kt_rd_rmsnorm(x.d, T, dim, x.s, L->in_norm.w, L->in_norm.s, L->in_norm.eps, h.d, &h.s);
+        ql(&L->wq, &h, &q);
+        ql(&L->wk, &h, &k);
+        ql(&L->wv, &h, &v);
+        kt_rd_attention_prefill(M, T, q.d, q.s, k.d, k.s, v.d, v.s, cat.d, &cat.s);
+        ql(&L->wo, &cat, &a);
+        kt_rd_add(x.d, x.s, a.d, a.s, T * dim, x2.d, &x2.s);
+        kt_rd_rmsnorm(x2.d, T, dim, x2.s, L->post_norm.w, L->post_norm.s, L->post_norm.eps, h.d, &h.s);
+        ql(&L->gate, &h, &g);
+        ql(&L->up, &h, &u);
+        kt_rd_swiglu_act(M, g.d, g.s, u.d, u.s, T * hid, hh.d, &hh.s);
+        ql(&L->down, &hh, &m);
+        kt_rd_add(x2.d, x2.s, m.d, m.s, T * dim, x.d, &x.s);
+    }
+    kt_rd_rmsnorm(x.d, T, dim, x.s, M->final_norm.w, M->final_norm.s, M->final_norm.eps, h.d, &h.s);
+    rd_t lg = {logits, T * M->vocab, ZERO};
+    ql(&M->lm_head, &h, &lg);
+    *ls = lg.s;
+    rd_t* all[] = {&x, &h, &a, &q, &k, &v, &cat, &g, &u, &hh, &m, &x2};
+    for (size_t i = 0; i < sizeof all / sizeof all[0]; i++) t_free(all[i]);
+    return 0;
+}
+
 /* hash_step (generate.rs:58-64): the scale's mant (i64 LE) and shift (i32 LE), then every code (i32 LE). */
 static void hash_step(void* ctx, const int32_t* codes, size_t n, kt_scale s) {
     kt_sha256_update(ctx, &s.mant, 8);

@@ -138,6 +138,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_rd_add": (None, [_P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_swiglu_act": (None, [_P, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_attention_core": (None, [_P, _P, _P, Scale, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_attention_prefill": (None, [_P, _SZ, _P, Scale, _P, Scale, _P, Scale, _P, C.POINTER(Scale)]),
+        "kt_rd_forward": (C.c_int, [_P, _P, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_new": (_P, [_SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_double, C.c_double, _SZ]),
         "kt_rd_set_ql": (None, [_P, _SZ, C.c_int, _P, _SZ, _SZ, Scale]),
         "kt_rd_set_norm": (None, [_P, _SZ, C.c_int, _P, Scale]),
@@ -806,6 +808,23 @@ class RefModel:
         if lib().kt_rd_generate(self.ptr, _ptr(p), p.size, max_new, _ptr(toks), run, _ptr(ph)):
             raise ValueError("generate: empty prompt or past the position tables")
         return toks[:max_new].tolist(), bytes(run).hex(), [bytes(ph[32 * i:32 * i + 32]).hex() for i in range(npos)]
+
+    def forward(self, tokens):
+        """CausalLM::forward_int (model.rs:361-367): the T tokens as one sequence, every op over the whole T-row
+        tensor: (logits T x vocab, (mant, shift))."""
+        t = _c(tokens, np.int32)
+        logits, ls = np.zeros(t.size * self.cfg["vocab"], dtype=np.int32), Scale()
+        if lib().kt_rd_forward(self.ptr, _ptr(t), t.size, _ptr(logits), C.byref(ls)):
+            raise ValueError("forward: empty, past max_seq or a token outside the vocabulary")
+        return logits.reshape(t.size, self.cfg["vocab"]), (ls.mant, ls.shift)
+
+    def attention_prefill(self, T: int, q, qs, k, ks, v, vs):
+        """Attention::forward_int between its projections over T rows (attention.rs:486-598): (o codes, scale)."""
+        q, k, v = _c(q, np.int32), _c(k, np.int32), _c(v, np.int32)
+        o, os_ = np.zeros(T * self.cfg["nh"] * self.cfg["hd"], dtype=np.int32), Scale()
+        lib().kt_rd_attention_prefill(self.ptr, T, _ptr(q), _sc(qs), _ptr(k), _sc(ks), _ptr(v), _sc(vs), _ptr(o),
+                                      C.byref(os_))
+        return o, (os_.mant, os_.shift)
 
     def ql(self, layer: int, which: str):
         """The (codes out x in, (mant, shift)) of a projection: wq wk wv wo gate up down, or lm_head."""

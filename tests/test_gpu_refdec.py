@@ -241,3 +241,80 @@ def test_qwen_shaped_decoder_against_the_oracle(torch_dev):
     first = next((i for i, (a, b) in enumerate(zip(hashes, pos_o)) if a != b), None)
     assert first is None, f"first differing position {first}"
     assert toks == toks_o and run == run_o
+
+
+@pytest.mark.parametrize("rows,dim", [(65, 896), (300, 64), (1024, 96)])
+def test_ref_rmsnorm_many_rows(torch_dev, rows, dim):
+    """RMSNorm over a sequence (the batched forward's norms): every row's factor, their largest, one requant."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref_rmsnorm rows={rows} dim={dim}")
+    rng = np.random.default_rng(rows + dim)
+    x = rng.integers(-(2**28), 2**28, size=rows * dim).astype(np.int32)
+    x[dim:2 * dim] = 0
+    x[5 * dim:6 * dim] = x[:dim]  # a row equal to row 0: equal factors, the later one is kept
+    g = rng.integers(-O.WLEVELS, O.WLEVELS + 1, size=dim).astype(np.int32)
+    xs, gs, eps = rand_scale(rng), rand_scale(rng), B.ref_scale_from_f64(1e-6)
+    y, ys = torch.zeros(rows * dim, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_rmsnorm(dev_i32(torch, x), rec(torch, xs), rows, dim, dev_i32(torch, g), gs, eps, y, ys)
+    yo, so = O.rd_rmsnorm(x, rows, dim, xs, g, gs, eps)
+    assert np.array_equal(y.cpu().numpy(), yo) and rd(ys) == so
+
+
+@pytest.mark.parametrize("nh,nkv,hd,T,max_seq", [(4, 2, 8, 5, 16), (14, 2, 64, 1, 64), (14, 2, 64, 37, 64),
+                                                 (14, 2, 64, 64, 64), (8, 8, 32, 200, 256)])
+def test_ref_attention_prefill_against_the_oracle(torch_dev, nh, nkv, hd, T, max_seq):
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref attention prefill nh={nh} nkv={nkv} hd={hd} T={T}")
+    cfg = dict(dim=nh * hd, layers=1, nh=nh, nkv=nkv, hd=hd, hidden=8, vocab=2, eps=1e-6, theta=10000.0,
+               max_seq=max_seq)
+    m = O.RefModel(3, cfg)
+    rng = np.random.default_rng(T + nh)
+    q = rng.integers(-(2**28), 2**28, size=T * nh * hd).astype(np.int32)
+    k = rng.integers(-(2**28), 2**28, size=T * nkv * hd).astype(np.int32)
+    v = rng.integers(-(2**28), 2**28, size=T * nkv * hd).astype(np.int32)
+    # score scales spread so the softmax is neither flat nor one-hot
+    qs, ks, vs = (int(rng.integers(2**30, 2**31)), 81), rand_scale(rng), rand_scale(rng)
+    o_want, os_want = m.attention_prefill(T, q, qs, k, ks, v, vs)
+    cos_t, sin_t = B.ref_rope_tables(max_seq, hd, 10000.0)
+    exp_codes, exp_lut = B.ref_codelut(B.LUT_EXP, -30.0, 0.0, 16, 20, False)
+    n = B.ref_attention_prefill_workspace(T, nh, nkv, hd)
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    o, os_ = torch.zeros(T * nh * hd, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_attention_prefill(dev_i32(torch, q), rec(torch, qs), dev_i32(torch, k), rec(torch, ks), dev_i32(torch, v),
+                            rec(torch, vs), T, nh, nkv, hd, max_seq,
+                            torch.from_numpy(cos_t.view(np.uint8)).cuda(),
+                            torch.from_numpy(sin_t.view(np.uint8)).cuda(), B.ref_scale_from_f64(1.0 / np.sqrt(hd)),
+                            torch.from_numpy(exp_codes).cuda(), exp_lut, ws, n, o, os_)
+    got = o.cpu().numpy()
+    assert np.array_equal(got, o_want), f"codes differ at {np.argwhere(got != o_want)[:5].tolist()}"
+    assert rd(os_) == os_want
+
+
+@pytest.mark.parametrize("case", ["synthetic", "d00d", "qwen2"])
+def test_ref_forward_against_the_oracle(torch_dev, case):
+    """CausalLM::forward_int of whole sequences on the device against the oracle's restatement: the seed-7
+    synthetic model over verify_repro's 12-token prompt, the reference test's 0xD00D model over [5, 6, 7, 8], a
+    Qwen2.5-shaped 2-layer model over 20 tokens -- logits codes and scale bit for bit."""
+    from tritify_amd.refdecoder import RefDecoder
+
+    if case == "synthetic":
+        cfg, seed, toks = O.SYNTH_CFG, 7, O.SYNTH_PROMPT
+    elif case == "d00d":
+        cfg = dict(dim=16, layers=2, nh=4, nkv=2, hd=4, hidden=32, vocab=20, eps=1e-6, theta=10000.0, max_seq=8)
+        seed, toks = 0xD00D, [5, 6, 7, 8]
+    else:
+        cfg = dict(dim=896, layers=2, nh=14, nkv=2, hd=64, hidden=4864, vocab=512, eps=1e-6, theta=1.0e6,
+                   max_seq=64)
+        seed, toks = 5, [1, 100, 200, 300, 400, 511, 7, 9, 11, 13, 17, 19, 23, 29, 31, 37, 41, 43, 47, 53]
+    say(f"case: ref forward {case} T={len(toks)}")
+    m = O.RefModel(seed, cfg)
+    want, ws_ = m.forward(toks)
+    dec = RefDecoder(cfg, *m.weights())
+    y, yr = dec.forward(toks)
+    got = y.cpu().numpy().reshape(want.shape)
+    assert np.array_equal(got, want), f"codes differ at {np.argwhere(got != want)[:5].tolist()}"
+    assert rd(yr) == ws_

@@ -167,3 +167,135 @@ def test_the_oracle_model_from_given_codes_reproduces_the_golden():
     toks, run, pos = m2.generate(O.SYNTH_PROMPT, 32)
     assert run == O.SYNTH_HASH
     assert (toks, pos) == m.generate(O.SYNTH_PROMPT, 32)[::2]
+
+
+# ---- the batched forward (CausalLM::forward_int: embed_int, blocks_int, head_int over a whole sequence) ----------
+
+
+def test_a_one_token_forward_is_the_decode_step_at_position_zero():
+    """Over one token the whole-sequence forward and decode_step at position 0 are the same integers (the
+    attention's one cached step has the sequence's score and v scales); decode_step is pinned by 8109ebad..."""
+    import hashlib
+
+    for seed, cfg in ((7, O.SYNTH_CFG), (5, dict(dim=64, layers=2, nh=4, nkv=2, hd=16, hidden=96, vocab=40,
+                                                 eps=1e-6, theta=1.0e6, max_seq=16))):
+        m = O.RefModel(seed, cfg)
+        for t in (0, 3, cfg["vocab"] - 1):
+            lg, ls = m.forward([t])
+            h = hashlib.sha256(np.int64(ls[0]).tobytes() + np.int32(ls[1]).tobytes() + lg.astype("<i4").tobytes())
+            assert h.hexdigest() == m.generate([t], 1)[2][0], (seed, t)
+
+
+def _dq(codes, sc):
+    return np.asarray(codes, np.float64) * (sc[0] * 2.0 ** -sc[1])
+
+
+def _lin_ref(x, w):
+    """QuantLinear::forward_ref (layers.rs:330-349): f64 dot with the dequantized weights, to f32."""
+    return (np.asarray(x, np.float64) @ _dq(*w).T).astype(np.float32)
+
+
+def _rope_ref(v, p, hd, theta):
+    half = hd // 2
+    j = np.arange(half)
+    ang = p * theta ** (-(2.0 * j) / hd)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = v[:half].copy(), v[half:].copy()
+    v[:half], v[half:] = a * c - b * s, b * c + a * s
+
+
+def _attention_ref(x, wq, wk, wv, wo, nh, nkv, hd, theta):
+    """Attention::forward_ref (attention.rs:603-663): float q / k / v, RoPE, causal softmax, o."""
+    seq = x.shape[0]
+    q = _lin_ref(x, wq).astype(np.float64).reshape(seq, nh, hd)
+    k = _lin_ref(x, wk).astype(np.float64).reshape(seq, nkv, hd)
+    v = _lin_ref(x, wv).astype(np.float64).reshape(seq, nkv, hd)
+    for i in range(seq):
+        for h in range(nh):
+            _rope_ref(q[i, h], i, hd, theta)
+        for h in range(nkv):
+            _rope_ref(k[i, h], i, hd, theta)
+    out = np.zeros((seq, nh * hd), np.float32)
+    for h in range(nh):
+        kv = h // (nh // nkv)
+        for i in range(seq):
+            sc = np.array([q[i, h] @ k[j, kv] for j in range(i + 1)]) / np.sqrt(hd)
+            e = np.exp(sc - sc.max())
+            out[i, h * hd:(h + 1) * hd] = ((e / e.sum()) @ v[:i + 1, kv]).astype(np.float32)
+    return _lin_ref(out, wo)
+
+
+def test_attention_gqa_causal_tracks_float():
+    """attention_gqa_causal_tracks_float_and_is_deterministic (tests.rs:184-198): seed 0x4242, dim 32, 4 / 2 heads
+    of 8, 5 rows, max_seq 16, theta 1e4; the integer attention within 3% of its float twin's peak."""
+    dim, nh, nkv, hd, seq = 32, 4, 2, 8, 5
+    qd, kvd = nh * hd, nkv * hd
+    s = 0x4242
+    ws = {}
+    for name, n in (("wq", qd * dim), ("wk", kvd * dim), ("wv", kvd * dim), ("wo", dim * qd)):
+        f, s = O.vecf(s, n)
+        ws[name] = O.quant_weights(f)
+    xf, s = O.vecf(s, seq * dim)
+    x, xs = O.from_reals(xf.astype(np.float64))
+    m = O.RefModel.from_weights(dict(dim=dim, layers=1, nh=nh, nkv=nkv, hd=hd, hidden=8, vocab=2, eps=1e-6,
+                                     theta=10000.0, max_seq=16),
+                                (np.zeros((2, dim), np.int32), (0, 0)), (np.zeros(dim, np.int32), (0, 0)),
+                                (np.zeros((2, dim), np.int32), (0, 0)), [])
+    shapes = {"wq": qd, "wk": kvd, "wv": kvd}
+    proj = {n: O.quant_linear_forward(x, seq, dim, xs, ws[n][0], shapes[n], ws[n][1])[:2] for n in shapes}
+    runs = []
+    for _ in range(2):
+        o, os_ = m.attention_prefill(seq, proj["wq"][0], proj["wq"][1], proj["wk"][0], proj["wk"][1],
+                                     proj["wv"][0], proj["wv"][1])
+        y, ys, _, _ = O.quant_linear_forward(o, seq, qd, os_, ws["wo"][0], dim, ws["wo"][1])
+        runs.append((y.copy(), ys))
+    assert np.array_equal(runs[0][0], runs[1][0]) and runs[0][1] == runs[1][1], "not deterministic"
+    w = {n: (ws[n][0].reshape(-1, dim if n != "wo" else qd), ws[n][1]) for n in ws}
+    r = _attention_ref(_dq(x, xs).astype(np.float32).reshape(seq, dim), w["wq"], w["wk"], w["wv"], w["wo"], nh,
+                       nkv, hd, 10000.0)
+    got = _dq(runs[0][0], runs[0][1]).reshape(seq, dim)
+    assert np.abs(got - r.astype(np.float64)).max() <= 3e-2 * np.abs(r).max()
+
+
+def test_full_decoder_forward_tracks_float():
+    """full_decoder_forward_tracks_float_and_is_deterministic (tests.rs:262-323): seed 0xD00D, dim 16, 2 layers,
+    4 / 2 heads of 4, hidden 32, vocab 20, max_seq 8, tokens [5, 6, 7, 8]: logits within 10% of the float twin's
+    peak and the same argmax at every position."""
+    cfg = dict(dim=16, layers=2, nh=4, nkv=2, hd=4, hidden=32, vocab=20, eps=1e-6, theta=10000.0, max_seq=8)
+    m = O.RefModel(0xD00D, cfg)
+    toks = [5, 6, 7, 8]
+    lg, ls = m.forward(toks)
+    lg2, ls2 = m.forward(toks)
+    assert np.array_equal(lg, lg2) and ls == ls2
+    # the float twin (model.rs:369-384) over the same quantized weights; the norms' own float gammas
+    d, qd, kvd, hid, voc = 16, 16, 8, 32, 20
+    s = 0xD00D
+    gam = []
+    for _ in range(2):
+        g_in, s = O.vecf(s, d)
+        for n in (qd * d, kvd * d, kvd * d, d * qd):
+            _, s = O.vecf(s, n)
+        g_post, s = O.vecf(s, d)
+        for n in (hid * d, hid * d, d * hid):
+            _, s = O.vecf(s, n)
+        gam.append((g_in.astype(np.float64), g_post.astype(np.float64)))
+    _, s = O.vecf(s, voc * d)
+    g_fin, s = O.vecf(s, d)
+
+    def rms(x, g):
+        ms = (x.astype(np.float64) ** 2).mean(axis=1, keepdims=True)
+        return (x.astype(np.float64) / np.sqrt(ms + 1e-6) * g).astype(np.float32)
+
+    emb = m.emb()
+    x = _dq(emb[0][toks], emb[1]).astype(np.float32)
+    for l in range(2):
+        a = _attention_ref(rms(x, gam[l][0]), m.ql(l, "wq"), m.ql(l, "wk"), m.ql(l, "wv"), m.ql(l, "wo"), 4, 2, 4,
+                           10000.0)
+        x = (x + a).astype(np.float32)
+        h = rms(x, gam[l][1])
+        g, u = _lin_ref(h, m.ql(l, "gate")).astype(np.float64), _lin_ref(h, m.ql(l, "up")).astype(np.float64)
+        x = (x + _lin_ref((g / (1.0 + np.exp(-g)) * u).astype(np.float32), m.ql(l, "down"))).astype(np.float32)
+    lr = _lin_ref(rms(x, g_fin.astype(np.float64)), m.ql(0, "lm_head")).astype(np.float64)
+    li = _dq(lg, ls)
+    assert np.abs(li - lr).max() <= 0.1 * np.abs(lr).max()
+    assert (np.argmax(li, axis=1) == np.argmax(lr, axis=1)).all()

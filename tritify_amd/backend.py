@@ -117,6 +117,10 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_rmsnorm": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _P, _P]),
         "kt_hip_ref_add": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P]),
         "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_embed_seq": (_I, [_I, _P, _I64, C.c_int32, _P, _I64, _I64, _I64, _P, _P, _P]),
+        "kt_hip_ref_attention_prefill_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+        "kt_hip_ref_attention_prefill": (_I, [_I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
+                                              C.c_int32, _P, _P, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_gelu": (_I, [_I, _P, _P, _I64, _P, _P, _P, _P, _P]),
         "kt_hip_ref_from_reals": (_I, [_P, _I64, _I64, _P, _P, _P]),
         "kt_hip_ref_conv2d_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64]),
@@ -634,6 +638,31 @@ def ref_conv2d(x_dev, xs_dev, ci: int, h: int, w: int, w_planes_dev, pw: int, co
                                   stride, pad, int(w_scale[0]), int(w_scale[1]),
                                   0 if bias_dev is None else _ptr(bias_dev), int(bm), int(bsh), _ptr(ws_dev), ws_bytes,
                                   _ptr(y_dev), _ptr(os_dev), _stream(stream)), "ref conv2d")
+
+
+def ref_embed_seq(emb_dev, e_scale, tokens_dev, T: int, vocab: int, dim: int, y_dev, ys_dev, stream=None,
+                  dev: int = 0) -> None:
+    """Embedding::lookup_seq (layers.rs:1138-1145) of T tokens in device memory."""
+    check(lib().kt_hip_ref_embed_seq(dev, _ptr(emb_dev), int(e_scale[0]), int(e_scale[1]), _ptr(tokens_dev), T, vocab,
+                                     dim, _ptr(y_dev), _ptr(ys_dev), _stream(stream)), "ref embed seq")
+
+
+def ref_attention_prefill_workspace(T: int, nh: int, nkv: int, hd: int) -> int:
+    n = lib().kt_hip_ref_attention_prefill_workspace(T, nh, nkv, hd)
+    if n == 0:
+        raise ValueError("attention prefill: shape out of range")
+    return n
+
+
+def ref_attention_prefill(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, T: int, nh: int, nkv: int, hd: int,
+                          max_seq: int, cos_dev, sin_dev, inv_sqrt, exp_codes_dev, exp_lut: CodeLut, ws_dev,
+                          ws_bytes: int, o_dev, os_dev, stream=None, dev: int = 0) -> None:
+    """Attention::forward_int between its projections over T rows (attention.rs:467-598)."""
+    check(lib().kt_hip_ref_attention_prefill(dev, _ptr(q_dev), _ptr(qs_dev), _ptr(k_dev), _ptr(ks_dev), _ptr(v_dev),
+                                             _ptr(vs_dev), T, nh, nkv, hd, max_seq, _ptr(cos_dev), _ptr(sin_dev),
+                                             int(inv_sqrt[0]), int(inv_sqrt[1]), _ptr(exp_codes_dev),
+                                             C.byref(exp_lut), _ptr(ws_dev), ws_bytes, _ptr(o_dev), _ptr(os_dev),
+                                             _stream(stream)), "ref attention prefill")
 
 
 def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh: int, nkv: int, hd: int,

@@ -34,7 +34,7 @@ namespace {
 
 constexpr int RD_THREADS = 1024;
 constexpr int RD_WAVES = RD_THREADS / 64;
-constexpr int RD_MAX_ROWS = 64;
+constexpr int RD_MAX_ROWS = 1024;  // RMSNorm rows in one call (one factor per thread)
 constexpr int64_t ACT_LEVELS = 1LL << 28;
 
 }  // namespace
@@ -54,6 +54,26 @@ struct RdAttn {
     const int64_t* exp_codes;
     kt_hip_codelut exp;
     int32_t* o;
+    kt_hip_qscale* os;
+};
+
+// Attention::forward_int over a sequence (prefill): the inputs, the tables and the workspace parts.
+struct RdPrefill {
+    const int32_t *q, *k, *v;          // T x nh*hd, T x nkv*hd, T x nkv*hd
+    const kt_hip_qscale *qs, *ks, *vs;
+    int T, nh, nkv, hd;
+    const kt_hip_sscale *cos, *sin;    // [max_seq][hd / 2]
+    int64_t isq_mant;
+    int32_t isq_shift;
+    const int64_t* exp_codes;
+    kt_hip_codelut exp;
+    int32_t *qd, *kd;                  // rotated q and k
+    int64_t* hout;                     // [nh][T][hd]: the sums of numerator * v, then the outputs at the common scale
+    int64_t* hsum;                     // [nh][T]: the numerators' sums
+    Sc* fac;                           // [T][nh]: each (row, head)'s scale over the common one
+    uint64_t* gmax;                    // the largest |output| at the common scale
+    Sc* common;
+    int32_t* o;                        // T x nh*hd
     kt_hip_qscale* os;
 };
 
@@ -90,6 +110,30 @@ __device__ int64_t block_sum_i64(int64_t v, int64_t* red) {  // wrapping
     __syncthreads();
     v = red[0];
     for (int w = 1; w < RD_WAVES; w++) v = wadd(v, red[w]);
+    __syncthreads();
+    return v;
+}
+// The same reductions for CTAs of 256 threads (4 waves).
+__device__ int64_t block_max_4w(int64_t v, int64_t* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int64_t u = __shfl_xor(v, o, 64);
+        v = u > v ? u : v;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+    for (int w = 1; w < 4; w++) v = red[w] > v ? red[w] : v;
+    __syncthreads();
+    return v;
+}
+__device__ int64_t block_sum_4w(int64_t v, int64_t* red) {  // wrapping
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = wadd(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+    for (int w = 1; w < 4; w++) v = wadd(v, red[w]);
     __syncthreads();
     return v;
 }
@@ -159,19 +203,27 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
                                                                 int32_t g_shift, int64_t e_mant, int32_t e_shift,
                                                                 int32_t* __restrict__ y,
                                                                 kt_hip_qscale* __restrict__ ys) {
-    __shared__ u128 red128[RD_THREADS];
     __shared__ int64_t red[RD_WAVES];
     __shared__ Sc crow[RD_MAX_ROWS], frow[RD_MAX_ROWS];
-    __shared__ Sc cc_s;
+    __shared__ ScIdx redsc[RD_THREADS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const Sc xs = rec_sc(xs_rec), gs{g_mant, g_shift}, eps{e_mant, e_shift};
-    for (int r = 0; r < rows; r++) {
-        u128 ss = 0;
-        for (int i = threadIdx.x; i < dim; i += RD_THREADS) {
+    // each row's exact sum of squares by one wave, its factor c_r = xs * rsqrt(mean_sq + eps) * gs by that wave's
+    // first lane (the rows' Scale arithmetic runs side by side)
+    for (int r = wave; r < rows; r += RD_WAVES) {
+        uint64_t hi = 0, lo = 0;  // the u128 sum as two words: squares below 2^62, at most 2^26 of them per lane
+        for (int i = lane; i < dim; i += 64) {
             const int64_t v = x[(size_t)r * dim + i];
-            ss += (u128)(uint64_t)(v * v);
+            const uint64_t sq = (uint64_t)(v * v), t = lo + sq;
+            hi += t < lo, lo = t;
         }
-        ss = block_sum_u128(ss, red128);
-        if (threadIdx.x == 0) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t ohi = __shfl_xor(hi, o, 64), olo = __shfl_xor(lo, o, 64), t = lo + olo;
+            hi += ohi + (t < lo), lo = t;
+        }
+        if (lane == 0) {
+            const u128 ss = ((u128)hi << 64) | lo;
             const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xs), xs);
             const Sc denom = sc_add(mean_sq, eps);
             const Sc inv = denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom);
@@ -179,17 +231,15 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        Sc cc{0, 0};
-        for (int r = 0; r < rows; r++) cc = sc_ge(crow[r], cc) ? crow[r] : cc;
-        if (cc.mant != 0) {
-            const Sc cinv = sc_recip(cc);
-            for (int r = 0; r < rows; r++) frow[r] = sc_mul(crow[r], cinv);
-        }
-        cc_s = cc;
+    // the largest row factor by the engine's fold (of equal values the latest row's), then each row's share of it
+    ScIdx best{Sc{0, 0}, -1};
+    for (int r = threadIdx.x; r < rows; r += RD_THREADS) best = sc_pick(best, ScIdx{crow[r], r});
+    const Sc cc = block_fold_max(best, redsc).s;
+    if (cc.mant != 0) {
+        const Sc cinv = sc_recip(cc);  // every thread: one Scale reciprocal, no extra barrier
+        for (int r = threadIdx.x; r < rows; r += RD_THREADS) frow[r] = sc_mul(crow[r], cinv);
     }
     __syncthreads();
-    const Sc cc = cc_s;
     const int n = rows * dim;
     int64_t m = 0;
     if (cc.mant != 0)
@@ -464,6 +514,138 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
 }
 
+// Embedding::lookup_seq (layers.rs:1138-1145): the code rows of T tokens at the table's scale (a token outside the
+// vocabulary gives a zero row; the reference panics there).
+__global__ __launch_bounds__(256) void rd_embed_seq_kernel(const int32_t* __restrict__ emb, int64_t e_mant,
+                                                           int32_t e_shift, const int32_t* __restrict__ tokens,
+                                                           int T, int vocab, int dim, int32_t* __restrict__ y,
+                                                           kt_hip_qscale* __restrict__ ys) {
+    const int64_t n = (int64_t)T * dim;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int t = tokens[i / dim];
+        y[i] = t >= 0 && t < vocab ? emb[(int64_t)t * dim + i % dim] : 0;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) put_rec(ys, Sc{e_mant, e_shift});
+}
+
+// Attention::forward_int (attention.rs:467-598) in five launches:
+//  rp_rope    q and k of row i rotated at position i (rope_int, attention.rs:208-229)
+//  rp_head    one CTA per (head, row i): the causal dots j <= i (exact, wrapping i64) at the one score scale
+//             q.scale * k.scale * inv_sqrt, the exp-CodeLut numerators of (dot - max), their sum, the sums of
+//             numerator * v over the rows
+//  rp_common  one CTA: each (row, head)'s scale v.scale / sumc, the largest by the engine's fold over the
+//             [row][head] order, every scale over it
+//  rp_apply   the outputs brought to the common scale, their largest magnitude
+//  rp_out     requant_dyn, and the output's scale
+__global__ __launch_bounds__(256) void rp_rope_kernel(RdPrefill a) {
+    const int i = blockIdx.x, half = a.hd / 2, qw = a.nh * a.hd, kw = a.nkv * a.hd;
+    for (int e = threadIdx.x; e < (a.nh + a.nkv) * half; e += 256) {
+        const bool isk = e >= a.nh * half;
+        const int hh = (isk ? e - a.nh * half : e) / half, j = (isk ? e - a.nh * half : e) % half;
+        const int32_t* src = isk ? a.k + (size_t)i * kw : a.q + (size_t)i * qw;
+        int32_t* dst = isk ? a.kd + (size_t)i * kw : a.qd + (size_t)i * qw;
+        const kt_hip_sscale c = a.cos[(size_t)i * half + j], sn = a.sin[(size_t)i * half + j];
+        const int64_t av = src[hh * a.hd + j], bv = src[hh * a.hd + j + half];
+        const Sc cm{c.mant, c.shift}, sm{sn.mant, sn.shift};
+        dst[hh * a.hd + j] = (int32_t)(c.sign * sc_apply(cm, av) - sn.sign * sc_apply(sm, bv));
+        dst[hh * a.hd + j + half] = (int32_t)(c.sign * sc_apply(cm, bv) + sn.sign * sc_apply(sm, av));
+    }
+}
+
+__global__ __launch_bounds__(256) void rp_head_kernel(RdPrefill a) {
+    extern __shared__ int64_t S[];  // T: the dots, then the numerators
+    __shared__ int64_t red[4];
+    __shared__ int64_t part[256];
+    __shared__ int32_t qrow[256];
+    __shared__ Sc lm_s;
+    const int h = blockIdx.x / a.T, i = blockIdx.x % a.T, hd = a.hd, kv = h / (a.nh / a.nkv);
+    const int kw = a.nkv * a.hd, tid = threadIdx.x;
+    for (int d = tid; d < hd; d += 256) qrow[d] = a.qd[(size_t)i * a.nh * hd + h * hd + d];
+    if (tid == 0) {
+        const Sc s_score = sc_mul(sc_mul(rec_sc(a.qs), rec_sc(a.ks)), Sc{a.isq_mant, a.isq_shift});
+        lm_s = sc_mul(s_score, Sc{a.exp.inv_mant, a.exp.inv_shift});
+    }
+    __syncthreads();
+    int64_t m = INT64_MIN;
+    for (int j = tid; j <= i; j += 256) {
+        const int32_t* kr = a.kd + (size_t)j * kw + kv * hd;
+        int64_t dot = 0;
+        for (int d = 0; d < hd; d++) dot = wadd(dot, wmul(qrow[d], kr[d]));
+        S[j] = dot;
+        m = dot > m ? dot : m;
+    }
+    const int64_t dmax = block_max_4w(m, red);
+    const Sc lm = lm_s;
+    int64_t sum = 0;
+    for (int j = tid; j <= i; j += 256) {
+        const int64_t idx = lut_index(lm, (int64_t)((uint64_t)S[j] - (uint64_t)dmax), a.exp.lo_index);
+        S[j] = idx < 0 ? 0 : lut_code(a.exp_codes, a.exp.n, idx);
+        sum += S[j];
+    }
+    const int64_t sumc = block_sum_4w(sum, red);  // also orders the numerator writes before the reads below
+    const int groups = 256 / hd, gq = tid / hd, d = tid - gq * hd;
+    int64_t acc = 0;
+    if (sumc > 0 && gq < groups)
+        for (int j = gq; j <= i; j += groups) acc = wadd(acc, wmul(S[j], a.v[(size_t)j * kw + kv * hd + d]));
+    part[tid] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        int64_t t = 0;
+        for (int q = 0; q < groups; q++) t = wadd(t, part[q * hd + tid]);
+        a.hout[((size_t)h * a.T + i) * hd + tid] = sumc > 0 ? t : 0;
+    }
+    if (tid == 0) a.hsum[(size_t)h * a.T + i] = sumc > 0 ? sumc : 0;
+}
+
+__global__ __launch_bounds__(RD_THREADS) void rp_common_kernel(RdPrefill a) {
+    __shared__ ScIdx redsc[RD_THREADS];
+    const int n = a.T * a.nh;
+    const Sc vs = rec_sc(a.vs);
+    ScIdx best{Sc{0, 0}, -1};
+    for (int e = threadIdx.x; e < n; e += RD_THREADS) {
+        const int i = e / a.nh, h = e - i * a.nh;
+        const int64_t sumc = a.hsum[(size_t)h * a.T + i];
+        const Sc sc = sumc > 0 ? sc_mul(vs, from_ratio(1, (u128)(uint64_t)sumc)) : Sc{0, 0};
+        a.fac[e] = sc;
+        best = sc_pick(best, ScIdx{sc, e});
+    }
+    const Sc common = block_fold_max(best, redsc).s;  // its barriers order the fac writes before the reads
+    if (common.mant != 0) {
+        const Sc cinv = sc_recip(common);
+        for (int e = threadIdx.x; e < n; e += RD_THREADS) a.fac[e] = sc_mul(a.fac[e], cinv);
+    }
+    if (threadIdx.x == 0) *a.common = common, *a.gmax = 0;
+}
+
+__global__ __launch_bounds__(256) void rp_apply_kernel(RdPrefill a) {
+    __shared__ int64_t red[4];
+    const int64_t n = (int64_t)a.T * a.nh * a.hd;
+    const bool live = a.common->mant != 0;
+    int64_t m = 0;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; live && e < n; e += (int64_t)gridDim.x * 256) {
+        const int64_t hi = e / a.hd, h = hi / a.T, i = hi - h * a.T;  // e indexes hout[h][i][d]
+        const int64_t v = sc_apply(a.fac[i * a.nh + h], a.hout[e]);
+        a.hout[e] = v;
+        m = iabs(v) > m ? iabs(v) : m;
+    }
+    m = block_max_4w(m, red);
+    if (threadIdx.x == 0 && m > 0) atomicMax(reinterpret_cast<unsigned long long*>(a.gmax), (unsigned long long)m);
+}
+
+__global__ __launch_bounds__(256) void rp_out_kernel(RdPrefill a) {
+    const int64_t gmax = (int64_t)*a.gmax;
+    const Sc common = *a.common;
+    const bool live = common.mant != 0 && gmax > 0;
+    const int qw = a.nh * a.hd;
+    const int64_t n = (int64_t)a.T * qw;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+        const int64_t i = e / qw, r = e - i * qw, h = r / a.hd, d = r - h * a.hd;  // e indexes o[i][h][d]
+        a.o[e] = live ? requant_dyn_dev(a.hout[((size_t)h * a.T + i) * a.hd + d], gmax) : 0;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        put_rec(a.os, live ? sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common) : Sc{0, 0});
+}
+
 // argmax_codes (generate.rs:48-56): *token = the first index of the largest of n codes. With record non-null the
 // codes go to record + step * n and the scale to rscale[step], and *step advances (the per-step logits the
 // generation hash covers).
@@ -540,6 +722,44 @@ hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
     rd_attention_step_kernel<<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
     return hipGetLastError();
 }
+hipError_t launch_rd_embed_seq(const int32_t* emb, int64_t e_mant, int32_t e_shift, const int32_t* tokens, int T,
+                               int vocab, int dim, int32_t* y, kt_hip_qscale* ys, hipStream_t s) {
+    const int64_t g = ((int64_t)T * dim + 255) / 256;
+    rd_embed_seq_kernel<<<(unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g)), 256, 0, s>>>(emb, e_mant, e_shift, tokens,
+                                                                                     T, vocab, dim, y, ys);
+    return hipGetLastError();
+}
+
+// The prefill attention's workspace: rotated q and k, the head sums, the numerators' sums, the factors, gmax and
+// the common scale, each part 256-byte aligned.
+size_t rd_prefill_workspace(int64_t T, int64_t nh, int64_t nkv, int64_t hd, size_t off[7]) {
+    const size_t sizes[7] = {(size_t)(T * nh * hd * 4), (size_t)(T * nkv * hd * 4), (size_t)(nh * T * hd * 8),
+                             (size_t)(nh * T * 8), (size_t)(T * nh) * sizeof(Sc), 8, sizeof(Sc)};
+    size_t at = 0;
+    for (int i = 0; i < 7; i++) {
+        off[i] = at;
+        at += (sizes[i] + 255) / 256 * 256;
+    }
+    return at;
+}
+
+hipError_t launch_rd_attention_prefill(RdPrefill a, void* ws, hipStream_t s) {
+    size_t off[7];
+    rd_prefill_workspace(a.T, a.nh, a.nkv, a.hd, off);
+    char* b = (char*)ws;
+    a.qd = (int32_t*)(b + off[0]), a.kd = (int32_t*)(b + off[1]), a.hout = (int64_t*)(b + off[2]);
+    a.hsum = (int64_t*)(b + off[3]), a.fac = (Sc*)(b + off[4]), a.gmax = (uint64_t*)(b + off[5]);
+    a.common = (Sc*)(b + off[6]);
+    rp_rope_kernel<<<(unsigned)a.T, 256, 0, s>>>(a);
+    rp_head_kernel<<<(unsigned)(a.T * a.nh), 256, (size_t)a.T * 8, s>>>(a);
+    rp_common_kernel<<<1, RD_THREADS, 0, s>>>(a);
+    const int64_t n = (int64_t)a.T * a.nh * a.hd, g = (n + 255) / 256;
+    const unsigned grid = (unsigned)(g < 1 ? 1 : (g > 2048 ? 2048 : g));
+    rp_apply_kernel<<<grid, 256, 0, s>>>(a);
+    rp_out_kernel<<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_rd_argmax(const int32_t* logits, int n, const kt_hip_qscale* ls, int32_t* token, int32_t* record,
                             kt_hip_sscale* rscale, int32_t* step, hipStream_t s) {
     rd_argmax_kernel<<<1, RD_THREADS, 0, s>>>(logits, n, ls, token, record, rscale, step);
@@ -569,6 +789,45 @@ extern "C" int kt_hip_ref_embed(int dev, const int32_t* emb_dev, int64_t e_mant,
     RD_TRY(hipSetDevice(dev));
     return (int)kt::launch_rd_embed(emb_dev, e_mant, e_shift, token_dev, (int)vocab, (int)dim, y_dev, ys_dev,
                                     (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_embed_seq(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_shift,
+                                    const int32_t* tokens_dev, int64_t T, int64_t vocab, int64_t dim, int32_t* y_dev,
+                                    kt_hip_qscale* ys_dev, void* stream) {
+    if (!emb_dev || !tokens_dev || !y_dev || !ys_dev || T < 1 || vocab < 1 || dim < 1 || vocab > INT32_MAX ||
+        T > INT32_MAX || dim > INT32_MAX || T * dim > RD_MAX_N || e_mant < 0)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_embed_seq(emb_dev, e_mant, e_shift, tokens_dev, (int)T, (int)vocab, (int)dim, y_dev,
+                                        ys_dev, (hipStream_t)stream);
+}
+
+extern "C" size_t kt_hip_ref_attention_prefill_workspace(int64_t T, int64_t nh, int64_t nkv, int64_t hd) {
+    if (T < 1 || nh < 1 || nkv < 1 || hd < 2 || T > 8192 || nh > KT_REF_MAX_HEADS || hd > 256) return 0;
+    size_t off[7];
+    return kt::rd_prefill_workspace(T, nh, nkv, hd, off);
+}
+
+extern "C" int kt_hip_ref_attention_prefill(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
+                                            const int32_t* k_dev, const kt_hip_qscale* ks_dev, const int32_t* v_dev,
+                                            const kt_hip_qscale* vs_dev, int64_t T, int64_t nh, int64_t nkv,
+                                            int64_t hd, int64_t max_seq, const kt_hip_sscale* cos_dev,
+                                            const kt_hip_sscale* sin_dev, int64_t isq_mant, int32_t isq_shift,
+                                            const int64_t* exp_codes_dev, const kt_hip_codelut* exp_lut,
+                                            void* ws_dev, size_t ws_bytes, int32_t* o_dev, kt_hip_qscale* os_dev,
+                                            void* stream) {
+    const size_t need = kt_hip_ref_attention_prefill_workspace(T, nh, nkv, hd);
+    if (!q_dev || !qs_dev || !k_dev || !ks_dev || !v_dev || !vs_dev || !cos_dev || !sin_dev || !exp_codes_dev ||
+        !exp_lut || !ws_dev || !o_dev || !os_dev || need == 0 || ws_bytes < need || T > max_seq || nh % nkv ||
+        (hd & 1) || exp_lut->n < 1 || isq_mant < 0)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    kt::RdPrefill a{};
+    a.q = q_dev, a.k = k_dev, a.v = v_dev, a.qs = qs_dev, a.ks = ks_dev, a.vs = vs_dev;
+    a.T = (int)T, a.nh = (int)nh, a.nkv = (int)nkv, a.hd = (int)hd, a.cos = cos_dev, a.sin = sin_dev;
+    a.isq_mant = isq_mant, a.isq_shift = isq_shift, a.exp_codes = exp_codes_dev, a.exp = *exp_lut;
+    a.o = o_dev, a.os = os_dev;
+    return (int)kt::launch_rd_attention_prefill(a, ws_dev, (hipStream_t)stream);
 }
 
 extern "C" int kt_hip_ref_rmsnorm(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t rows,

@@ -12,6 +12,9 @@ the 2^28 level, quantized dynamically per tensor after every op. `RefDecoder` ke
   SiLU * up                   kt_hip_ref_swiglu              SwiGluMlp::forward_int      (layers.rs:609-640)
   residual adds               kt_hip_ref_add                 add                         (layers.rs:121-136)
   greedy choice               kt_hip_ref_argmax              argmax_codes                (generate.rs:48-56)
+  sequence forward            kt_hip_ref_embed_seq,          CausalLM::forward_int       (model.rs:361-367,
+    (prefill)                 kt_hip_ref_attention_prefill,  Attention::forward_int       168-189; attention.rs:
+                              the ops above over T rows                                   467-598)
 
 The weights come in as the engine builds them (codes and Scales, `QuantLinear::from_weights` and its siblings);
 the run-time tables (RoPE Scales, the exp and SiLU CodeLuts, 1/sqrt(head_dim)) are built here from the
@@ -167,6 +170,49 @@ class RefDecoder:
         codes = self.record[pos * self.vocab:(pos + 1) * self.vocab].cpu().numpy()
         w = self.rscale[pos * 16:(pos + 1) * 16].cpu().numpy()
         return codes, (int(w.view(np.int64)[0]), int(w.view(np.int32)[2]))
+
+    def forward(self, tokens, stream=None):
+        """CausalLM::forward_int (model.rs:361-367 = embed_int, blocks_int, head_int): the T tokens as one sequence,
+        every op over the whole T-row tensor (one dynamic quantization per tensor, the prefill attention at one
+        score scale): (logits T x vocab codes, their record), device tensors. Independent of the KV cache."""
+        torch = self.torch
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        T = int(toks.size)
+        if not 1 <= T <= self.max_seq:
+            raise ValueError(f"forward: {T} tokens, max_seq {self.max_seq}")
+        if toks.min() < 0 or toks.max() >= self.vocab:
+            raise ValueError("forward: a token outside the vocabulary")
+        d, dv = self.device, self.dev
+        z = lambda n: torch.empty(n, dtype=torch.int32, device=d)  # noqa: E731
+        rec = lambda: torch.zeros(4, dtype=torch.int64, device=d)  # noqa: E731
+        qd, kvd = self.nh * self.hd, self.nkv * self.hd
+        x, xr, h, hr = z(T * self.dim), rec(), z(T * self.dim), rec()
+        t_dev = torch.from_numpy(toks).to(d)
+        B.ref_embed_seq(self.emb, self.emb_scale, t_dev, T, self.vocab, self.dim, x, xr, stream, dv)
+        nws = B.ref_attention_prefill_workspace(T, self.nh, self.nkv, self.hd)
+        ws = torch.empty(nws, dtype=torch.uint8, device=d)
+        cat, cr, a, ar, hh, hhr = z(T * qd), rec(), z(T * self.dim), rec(), z(T * self.hidden), rec()
+        for blk in self.blocks:
+            g, gs = blk["in_norm"]
+            B.ref_rmsnorm(x, xr, T, self.dim, g, gs, self.eps, h, hr, stream, dv)
+            q, qr = blk["wq"].forward_int(h, hr, T, stream=stream)
+            k, kr = blk["wk"].forward_int(h, hr, T, stream=stream)
+            v, vr = blk["wv"].forward_int(h, hr, T, stream=stream)
+            B.ref_attention_prefill(q, qr, k, kr, v, vr, T, self.nh, self.nkv, self.hd, self.max_seq, self.cos,
+                                    self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, ws, nws, cat, cr, stream,
+                                    dv)
+            blk["wo"].forward_int(cat, cr, T, y_dev=a, os_dev=ar, stream=stream)
+            B.ref_add(x, xr, a, ar, T * self.dim, x, xr, stream, dv)
+            g, gs = blk["post_norm"]
+            B.ref_rmsnorm(x, xr, T, self.dim, g, gs, self.eps, h, hr, stream, dv)
+            gt, gtr = blk["gate"].forward_int(h, hr, T, stream=stream)
+            up, upr = blk["up"].forward_int(h, hr, T, stream=stream)
+            B.ref_swiglu(gt, gtr, up, upr, T * self.hidden, self.silu_codes, self.silu_lut, hh, hhr, stream, dv)
+            m, mr = blk["down"].forward_int(hh, hhr, T, stream=stream)
+            B.ref_add(x, xr, m, mr, T * self.dim, x, xr, stream, dv)
+        g, gs = self.final_norm
+        B.ref_rmsnorm(x, xr, T, self.dim, g, gs, self.eps, h, hr, stream, dv)
+        return self.lm_head.forward_int(h, hr, T, stream=stream)
 
     def decode_step(self, token: int, pos: int):
         """The logits of `token` at `pos` against the cache: (codes, (mant, shift)) on the host."""
