@@ -724,6 +724,24 @@ def ref_decoder_oracle() -> tuple:
     return _ref_cpu["hashes"], _ref_cpu["seconds"], _ref_cpu["cores"]
 
 
+REF_PREFILL_T = 64
+
+
+def ref_forward_oracle() -> tuple:
+    """The oracle's CausalLM::forward_int over REF_PREFILL_T tokens of REF_QWEN: (logits, scale, seconds, threads)."""
+    if "fwd" not in _ref_cpu:
+        from oracle import oracle as O
+
+        model = O.RefModel.from_weights(REF_QWEN, *ref_decoder_weights(REF_QWEN, 0x5EED))
+        cores = cpu_threads()
+        O.set_max_threads(cores)
+        toks = [(7919 * i + 11) % REF_QWEN["vocab"] for i in range(REF_PREFILL_T)]
+        t0 = time.perf_counter()
+        lg, ls = model.forward(toks)
+        _ref_cpu["fwd"] = (toks, lg, ls, time.perf_counter() - t0, cores)
+    return _ref_cpu["fwd"]
+
+
 def ref_decoder_cpu_baseline() -> dict:
     hashes, secs, cores = ref_decoder_oracle()
     npos = len(hashes)
@@ -777,6 +795,17 @@ def bench_ref_decoder(torch, args) -> dict:
         raise SystemExit(f"bench: ref decoder: position {first} differs from the CPU oracle")
     wbytes = 3 * (cfg["layers"] * ((2 * cfg["nh"] + 2 * cfg["nkv"]) * cfg["hd"] * cfg["dim"] +
                                    3 * cfg["hidden"] * cfg["dim"]) + cfg["vocab"] * cfg["dim"])
+    # the batched forward (prefill) of REF_PREFILL_T tokens, checked against the oracle's, then timed
+    toks, lg_want, ls_want, cpu_fwd_s, cores = ref_forward_oracle()
+    dec = RefDecoder(cfg, *ref_decoder_weights(cfg, 0x5EED))
+    y, yr = dec.forward(toks)
+    ok = np.array_equal(y.cpu().numpy().reshape(lg_want.shape), lg_want)
+    w_ = yr.cpu().numpy()
+    if not (ok and (int(w_[0]), int(w_.view(np.int32)[2])) == ls_want):
+        raise SystemExit("bench: ref forward differs from the CPU oracle")
+    fwd_ms, _ = time_launches(torch, lambda i: dec.forward(toks, stream=stream), 5, 2)
+    del dec, y
+    torch.cuda.empty_cache()
     return {
         "workload": "the reference's DecoderModel::decode_step at its own semantics (i32 codes at 2^28, 12-trit "
                     "weights as 3 digit planes, per-tensor dynamic requant after every op, RmsNorm, RoPE Scales, "
@@ -787,6 +816,15 @@ def bench_ref_decoder(torch, args) -> dict:
         "decode_us_per_token": round(best * 1e3, 1),
         "weight_plane_gbs": round(wbytes / (best * 1e-3) / 1e9, 1),
         "cpu_baseline": ref_decoder_cpu_baseline(),
+        "forward": {
+            "what": f"CausalLM::forward_int over {REF_PREFILL_T} tokens (the batched prefill: every op over the "
+                    f"{REF_PREFILL_T}-row tensors, the prefill attention at one score scale), logits bit-exact",
+            "ms": round(fwd_ms, 3), "tokens_per_s": round(REF_PREFILL_T / (fwd_ms * 1e-3), 1),
+            "cpu_baseline": {"value": round(REF_PREFILL_T / cpu_fwd_s, 1), "unit": "tokens/s", "cores": cores,
+                             "nproc": os.cpu_count(), "kind": "port",
+                             "sample": f"the oracle's forward of the same {REF_PREFILL_T} tokens, "
+                                       f"{cpu_fwd_s * 1e3:.0f} ms"},
+        },
     }
 
 
