@@ -176,6 +176,22 @@ int kt_hip_ref_embed(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_
  * table's Scale; a token outside [0, vocab) gives a zero row (the reference panics). */
 int kt_hip_ref_embed_seq(int dev, const int32_t* emb_dev, int64_t e_mant, int32_t e_shift, const int32_t* tokens_dev,
                          int64_t T, int64_t vocab, int64_t dim, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+/* RmsNorm::forward_int, add and SwiGluMlp's activation (as kt_hip_ref_rmsnorm / _add / _swiglu with rows = 1: the
+ * same integers) over whole-sequence tensors on many CTAs, for the batched forward's T-row tensors: one CTA forms the
+ * tensor's Scales (and RMSNorm's row factors, any number of rows) into the workspace, a grid pass takes the largest
+ * magnitude, a grid pass requantizes. The workspace holds kt_hip_ref_seq_workspace(rows) bytes (rows = 1 for add
+ * and SwiGLU); add's y_dev / ys_dev may alias a / as or b / bs. */
+size_t kt_hip_ref_seq_workspace(int64_t rows);
+int kt_hip_ref_rmsnorm_seq(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t rows, int64_t dim,
+                           const int32_t* g_dev, int64_t g_mant, int32_t g_shift, int64_t eps_mant, int32_t eps_shift,
+                           void* ws_dev, size_t ws_bytes, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+int kt_hip_ref_add_seq(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
+                       const kt_hip_qscale* bs_dev, int64_t n, void* ws_dev, size_t ws_bytes, int32_t* y_dev,
+                       kt_hip_qscale* ys_dev, void* stream);
+int kt_hip_ref_swiglu_seq(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
+                          const kt_hip_qscale* us_dev, int64_t n, const int64_t* silu_codes_dev,
+                          const kt_hip_codelut* silu, void* ws_dev, size_t ws_bytes, int32_t* h_dev,
+                          kt_hip_qscale* hs_dev, void* stream);
 /* Attention::forward_int between its projections over a whole sequence (attention.rs:467-598), the prefill of
  * DecoderModel's batched forward: q (T x nh hd), k and v (T x nkv hd) codes at one Scale each; row i rotated at
  * position i (the RoPE tables of kt_hip_ref_rope_tables, T <= max_seq); per head and row the causal integer-code

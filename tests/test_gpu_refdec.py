@@ -318,3 +318,39 @@ def test_ref_forward_against_the_oracle(torch_dev, case):
     got = y.cpu().numpy().reshape(want.shape)
     assert np.array_equal(got, want), f"codes differ at {np.argwhere(got != want)[:5].tolist()}"
     assert rd(yr) == ws_
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 896), (64, 896), (300, 64), (2048, 40)])
+def test_ref_seq_ops_equal_the_one_cta_ops_and_the_oracle(torch_dev, rows, dim):
+    """The many-CTA RMSNorm, add (in place) and SwiGLU give the integers of the one-CTA kernels and the oracle."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref seq ops rows={rows} dim={dim}")
+    rng = np.random.default_rng(rows * 3 + dim)
+    n = rows * dim
+    x = rng.integers(-(2**28), 2**28, size=n).astype(np.int32)
+    x[:dim] = 0
+    g = rng.integers(-O.WLEVELS, O.WLEVELS + 1, size=dim).astype(np.int32)
+    xs, gs, eps = rand_scale(rng), rand_scale(rng), B.ref_scale_from_f64(1e-6)
+    nws = B.ref_seq_workspace(rows)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    y, ys = torch.zeros(n, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_rmsnorm_seq(dev_i32(torch, x), rec(torch, xs), rows, dim, dev_i32(torch, g), gs, eps, ws, nws, y, ys)
+    yo, so = O.rd_rmsnorm(x, rows, dim, xs, g, gs, eps)
+    assert np.array_equal(y.cpu().numpy(), yo) and rd(ys) == so
+    b = rng.integers(-(2**28), 2**28, size=n).astype(np.int32)
+    sb = rand_scale(rng)
+    ad, ar = dev_i32(torch, x), rec(torch, xs)
+    B.ref_add_seq(ad, ar, dev_i32(torch, b), rec(torch, sb), n, ws, nws, ad, ar)
+    wo, wso = O.rd_add(x, xs, b, sb)
+    assert np.array_equal(ad.cpu().numpy(), wo) and rd(ar) == wso
+    model = O.RefModel(7)
+    codes, lut = B.ref_codelut(B.LUT_SILU, -30.0, 30.0, 16, 20, True)
+    us = rand_scale(rng)
+    gsw = (int(rng.integers(2**30, 2**31)), 55)
+    h, hs = torch.zeros(n, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_swiglu_seq(dev_i32(torch, x), rec(torch, gsw), dev_i32(torch, b), rec(torch, us), n,
+                     torch.from_numpy(codes).cuda(), lut, ws, nws, h, hs)
+    ho, hso = O.rd_swiglu_act(model, x, gsw, b, us)
+    assert np.array_equal(h.cpu().numpy(), ho) and rd(hs) == hso

@@ -117,6 +117,11 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_rmsnorm": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _P, _P]),
         "kt_hip_ref_add": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P]),
         "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_seq_workspace": (_SZ, [_I64]),
+        "kt_hip_ref_rmsnorm_seq": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _SZ, _P, _P,
+                                        _P]),
+        "kt_hip_ref_add_seq": (_I, [_I, _P, _P, _P, _P, _I64, _P, _SZ, _P, _P, _P]),
+        "kt_hip_ref_swiglu_seq": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_embed_seq": (_I, [_I, _P, _I64, C.c_int32, _P, _I64, _I64, _I64, _P, _P, _P]),
         "kt_hip_ref_attention_prefill_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
         "kt_hip_ref_attention_prefill": (_I, [_I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
@@ -638,6 +643,31 @@ def ref_conv2d(x_dev, xs_dev, ci: int, h: int, w: int, w_planes_dev, pw: int, co
                                   stride, pad, int(w_scale[0]), int(w_scale[1]),
                                   0 if bias_dev is None else _ptr(bias_dev), int(bm), int(bsh), _ptr(ws_dev), ws_bytes,
                                   _ptr(y_dev), _ptr(os_dev), _stream(stream)), "ref conv2d")
+
+
+def ref_seq_workspace(rows: int) -> int:
+    return lib().kt_hip_ref_seq_workspace(rows)
+
+
+def ref_rmsnorm_seq(x_dev, xs_dev, rows: int, dim: int, g_dev, g_scale, eps, ws_dev, ws_bytes: int, y_dev, ys_dev,
+                    stream=None, dev: int = 0) -> None:
+    """RmsNorm::forward_int of a whole-sequence tensor on many CTAs (the integers of ref_rmsnorm)."""
+    check(lib().kt_hip_ref_rmsnorm_seq(dev, _ptr(x_dev), _ptr(xs_dev), rows, dim, _ptr(g_dev), int(g_scale[0]),
+                                       int(g_scale[1]), int(eps[0]), int(eps[1]), _ptr(ws_dev), ws_bytes,
+                                       _ptr(y_dev), _ptr(ys_dev), _stream(stream)), "ref rmsnorm seq")
+
+
+def ref_add_seq(a_dev, as_dev, b_dev, bs_dev, n: int, ws_dev, ws_bytes: int, y_dev, ys_dev, stream=None,
+                dev: int = 0) -> None:
+    check(lib().kt_hip_ref_add_seq(dev, _ptr(a_dev), _ptr(as_dev), _ptr(b_dev), _ptr(bs_dev), n, _ptr(ws_dev),
+                                   ws_bytes, _ptr(y_dev), _ptr(ys_dev), _stream(stream)), "ref add seq")
+
+
+def ref_swiglu_seq(g_dev, gs_dev, u_dev, us_dev, n: int, silu_codes_dev, silu: CodeLut, ws_dev, ws_bytes: int, h_dev,
+                   hs_dev, stream=None, dev: int = 0) -> None:
+    check(lib().kt_hip_ref_swiglu_seq(dev, _ptr(g_dev), _ptr(gs_dev), _ptr(u_dev), _ptr(us_dev), n,
+                                      _ptr(silu_codes_dev), C.byref(silu), _ptr(ws_dev), ws_bytes, _ptr(h_dev),
+                                      _ptr(hs_dev), _stream(stream)), "ref swiglu seq")
 
 
 def ref_embed_seq(emb_dev, e_scale, tokens_dev, T: int, vocab: int, dim: int, y_dev, ys_dev, stream=None,

@@ -514,6 +514,120 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
 }
 
+// The same ops over whole-sequence tensors on many CTAs (the batched forward's T-row tensors): one CTA forms the
+// tensor's Scales (and an RMSNorm's row factors) into the workspace and zeroes its max slot, a grid pass takes the
+// largest magnitude, a grid pass requantizes and writes the record. Integers identical to the one-CTA kernels.
+struct RdSeqWs {
+    Sc par[4];      // add: common, fa, fb; SwiGLU: index factor, identity factor, h scale; RMSNorm: cc
+    uint64_t gmax;  // the largest magnitude
+    Sc frow[1];     // RMSNorm: each row's factor over cc (rows of them)
+};
+enum { RS_ADD = 0, RS_SWIGLU = 1, RS_NORM = 2 };
+struct RdSeq {
+    int op;
+    const int32_t *a, *b;  // add: a, b; SwiGLU: g, u; RMSNorm: x, gamma
+    const kt_hip_qscale *as, *bs;
+    int64_t n;             // values (rows * dim for RMSNorm)
+    int rows, dim;
+    int64_t g_mant, e_mant;
+    int32_t g_shift, e_shift;
+    const int64_t* codes;
+    kt_hip_codelut lut;
+    RdSeqWs* ws;
+    int32_t* y;
+    kt_hip_qscale* ys;
+};
+
+__device__ inline int64_t rs_value(const RdSeq& q, const RdSeqWs* w, int64_t i) {
+    if (q.op == RS_ADD) return wadd(sc_apply(w->par[1], q.a[i]), sc_apply(w->par[2], q.b[i]));
+    if (q.op == RS_SWIGLU) {
+        const int64_t gd = q.a[i], idx = lut_index(w->par[0], gd, q.lut.lo_index);
+        const int64_t code = idx < 0 ? 0 : (idx >= q.lut.n ? sc_apply(w->par[1], gd) : lut_code(q.codes, q.lut.n, idx));
+        return wmul(code, q.b[i]);
+    }
+    return sc_apply(w->frow[i / q.dim], (int64_t)q.a[i] * (int64_t)q.b[i % q.dim]);
+}
+// whether the values are live (a zero common scale gives zeros)
+__device__ inline bool rs_live(const RdSeq& q, const RdSeqWs* w) { return q.op == RS_SWIGLU || w->par[0].mant != 0; }
+
+__global__ __launch_bounds__(RD_THREADS) void rs_prep_kernel(RdSeq q) {
+    __shared__ ScIdx redsc[RD_THREADS];
+    RdSeqWs* w = q.ws;
+    if (q.op == RS_NORM) {  // as rd_rmsnorm_kernel, the row factors in the workspace
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const Sc xs = rec_sc(q.as), gs{q.g_mant, q.g_shift}, eps{q.e_mant, q.e_shift};
+        for (int r = wave; r < q.rows; r += RD_WAVES) {
+            uint64_t hi = 0, lo = 0;
+            for (int i = lane; i < q.dim; i += 64) {
+                const int64_t v = q.a[(size_t)r * q.dim + i];
+                const uint64_t sq = (uint64_t)(v * v), t = lo + sq;
+                hi += t < lo, lo = t;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const uint64_t ohi = __shfl_xor(hi, o, 64), olo = __shfl_xor(lo, o, 64), t = lo + olo;
+                hi += ohi + (t < lo), lo = t;
+            }
+            if (lane == 0) {
+                const Sc mean_sq = sc_mul(sc_mul(from_ratio(((u128)hi << 64) | lo, (u128)q.dim), xs), xs);
+                const Sc denom = sc_add(mean_sq, eps);
+                w->frow[r] = sc_mul(sc_mul(xs, denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom)), gs);
+            }
+        }
+        __syncthreads();  // the CTA's own global writes are visible to it past the barrier
+        ScIdx best{Sc{0, 0}, -1};
+        for (int r = threadIdx.x; r < q.rows; r += RD_THREADS) best = sc_pick(best, ScIdx{w->frow[r], r});
+        const Sc cc = block_fold_max(best, redsc).s;
+        if (cc.mant != 0) {
+            const Sc cinv = sc_recip(cc);
+            for (int r = threadIdx.x; r < q.rows; r += RD_THREADS) w->frow[r] = sc_mul(w->frow[r], cinv);
+        }
+        if (threadIdx.x == 0) w->par[0] = cc, w->gmax = 0;
+        return;
+    }
+    if (threadIdx.x == 0) {
+        const Sc as = rec_sc(q.as), bs = rec_sc(q.bs);
+        if (q.op == RS_ADD) {
+            const Sc common = sc_ge(as, bs) ? as : bs;
+            w->par[0] = common, w->par[1] = w->par[2] = Sc{0, 0};
+            if (common.mant != 0) {
+                const Sc cinv = sc_recip(common);
+                w->par[1] = sc_mul(as, cinv), w->par[2] = sc_mul(bs, cinv);
+            }
+        } else {  // SwiGLU: as is g's record, bs u's
+            const Sc cs{q.lut.code_mant, q.lut.code_shift};
+            w->par[0] = sc_mul(as, Sc{q.lut.inv_mant, q.lut.inv_shift});
+            w->par[1] = sc_mul(as, sc_recip(cs));
+            w->par[2] = sc_mul(cs, bs);
+        }
+        w->gmax = 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void rs_max_kernel(RdSeq q) {
+    __shared__ int64_t red[4];
+    const RdSeqWs* w = q.ws;
+    int64_t m = 0;
+    if (rs_live(q, w))
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < q.n; i += (int64_t)gridDim.x * 256) {
+            const int64_t v = iabs(rs_value(q, w, i));
+            m = v > m ? v : m;
+        }
+    m = block_max_4w(m, red);
+    if (threadIdx.x == 0 && m > 0) atomicMax(reinterpret_cast<unsigned long long*>(&q.ws->gmax), (unsigned long long)m);
+}
+
+__global__ __launch_bounds__(256) void rs_out_kernel(RdSeq q) {
+    const RdSeqWs* w = q.ws;
+    const int64_t gmax = (int64_t)w->gmax;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < q.n; i += (int64_t)gridDim.x * 256)
+        q.y[i] = gmax == 0 ? 0 : requant_dyn_dev(rs_value(q, w, i), gmax);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const Sc sc = q.op == RS_SWIGLU ? w->par[2] : w->par[0];  // the tensor's scale before the requant
+        put_rec(q.ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), sc));
+    }
+}
+
 // Embedding::lookup_seq (layers.rs:1138-1145): the code rows of T tokens at the table's scale (a token outside the
 // vocabulary gives a zero row; the reference panics there).
 __global__ __launch_bounds__(256) void rd_embed_seq_kernel(const int32_t* __restrict__ emb, int64_t e_mant,
@@ -722,6 +836,17 @@ hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
     rd_attention_step_kernel<<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
     return hipGetLastError();
 }
+size_t rd_seq_workspace(int64_t rows) { return (sizeof(RdSeqWs) + (size_t)(rows > 1 ? rows - 1 : 0) * sizeof(Sc) + 255) / 256 * 256; }
+
+hipError_t launch_rd_seq(const RdSeq& q, hipStream_t s) {
+    rs_prep_kernel<<<1, RD_THREADS, 0, s>>>(q);
+    const int64_t g = (q.n + 255) / 256;
+    const unsigned grid = (unsigned)(g < 1 ? 1 : (g > 2048 ? 2048 : g));
+    rs_max_kernel<<<grid, 256, 0, s>>>(q);
+    rs_out_kernel<<<grid, 256, 0, s>>>(q);
+    return hipGetLastError();
+}
+
 hipError_t launch_rd_embed_seq(const int32_t* emb, int64_t e_mant, int32_t e_shift, const int32_t* tokens, int T,
                                int vocab, int dim, int32_t* y, kt_hip_qscale* ys, hipStream_t s) {
     const int64_t g = ((int64_t)T * dim + 255) / 256;
@@ -800,6 +925,53 @@ extern "C" int kt_hip_ref_embed_seq(int dev, const int32_t* emb_dev, int64_t e_m
     RD_TRY(hipSetDevice(dev));
     return (int)kt::launch_rd_embed_seq(emb_dev, e_mant, e_shift, tokens_dev, (int)T, (int)vocab, (int)dim, y_dev,
                                         ys_dev, (hipStream_t)stream);
+}
+
+extern "C" size_t kt_hip_ref_seq_workspace(int64_t rows) {
+    return rows < 1 || rows > INT32_MAX ? 0 : kt::rd_seq_workspace(rows);
+}
+
+static int rd_seq_call(int dev, const kt::RdSeq& q, size_t ws_bytes, void* stream) {
+    if (!q.a || !q.b || !q.as || !q.y || !q.ys || !q.ws || q.n < 1 || q.n > RD_MAX_N ||
+        ws_bytes < kt::rd_seq_workspace(q.rows))
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_seq(q, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_add_seq(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
+                                  const kt_hip_qscale* bs_dev, int64_t n, void* ws_dev, size_t ws_bytes,
+                                  int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream) {
+    kt::RdSeq q{};
+    q.op = kt::RS_ADD, q.a = a_dev, q.b = b_dev, q.as = as_dev, q.bs = bs_dev, q.n = n, q.rows = 1, q.dim = 1;
+    q.ws = (kt::RdSeqWs*)ws_dev, q.y = y_dev, q.ys = ys_dev;
+    if (!bs_dev) return (int)hipErrorInvalidValue;
+    return rd_seq_call(dev, q, ws_bytes, stream);
+}
+
+extern "C" int kt_hip_ref_swiglu_seq(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
+                                     const kt_hip_qscale* us_dev, int64_t n, const int64_t* silu_codes_dev,
+                                     const kt_hip_codelut* silu, void* ws_dev, size_t ws_bytes, int32_t* h_dev,
+                                     kt_hip_qscale* hs_dev, void* stream) {
+    if (!silu || !silu_codes_dev || !us_dev || silu->n < 1 || !silu->right_identity) return (int)hipErrorInvalidValue;
+    kt::RdSeq q{};
+    q.op = kt::RS_SWIGLU, q.a = g_dev, q.b = u_dev, q.as = gs_dev, q.bs = us_dev, q.n = n, q.rows = 1, q.dim = 1;
+    q.codes = silu_codes_dev, q.lut = *silu, q.ws = (kt::RdSeqWs*)ws_dev, q.y = h_dev, q.ys = hs_dev;
+    return rd_seq_call(dev, q, ws_bytes, stream);
+}
+
+extern "C" int kt_hip_ref_rmsnorm_seq(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev, int64_t rows,
+                                      int64_t dim, const int32_t* g_dev, int64_t g_mant, int32_t g_shift,
+                                      int64_t eps_mant, int32_t eps_shift, void* ws_dev, size_t ws_bytes,
+                                      int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream) {
+    if (rows < 1 || dim < 1 || rows > INT32_MAX || dim > INT32_MAX || rows * dim > RD_MAX_N || g_mant < 0 ||
+        eps_mant < 0)
+        return (int)hipErrorInvalidValue;
+    kt::RdSeq q{};
+    q.op = kt::RS_NORM, q.a = x_dev, q.b = g_dev, q.as = xs_dev, q.n = rows * dim, q.rows = (int)rows;
+    q.dim = (int)dim, q.g_mant = g_mant, q.g_shift = g_shift, q.e_mant = eps_mant, q.e_shift = eps_shift;
+    q.ws = (kt::RdSeqWs*)ws_dev, q.y = y_dev, q.ys = ys_dev;
+    return rd_seq_call(dev, q, ws_bytes, stream);
 }
 
 extern "C" size_t kt_hip_ref_attention_prefill_workspace(int64_t T, int64_t nh, int64_t nkv, int64_t hd) {

@@ -14,7 +14,7 @@ the 2^28 level, quantized dynamically per tensor after every op. `RefDecoder` ke
   greedy choice               kt_hip_ref_argmax              argmax_codes                (generate.rs:48-56)
   sequence forward            kt_hip_ref_embed_seq,          CausalLM::forward_int       (model.rs:361-367,
     (prefill)                 kt_hip_ref_attention_prefill,  Attention::forward_int       168-189; attention.rs:
-                              the ops above over T rows                                   467-598)
+                              kt_hip_ref_*_seq (many CTAs)                                467-598)
 
 The weights come in as the engine builds them (codes and Scales, `QuantLinear::from_weights` and its siblings);
 the run-time tables (RoPE Scales, the exp and SiLU CodeLuts, 1/sqrt(head_dim)) are built here from the
@@ -191,10 +191,14 @@ class RefDecoder:
         B.ref_embed_seq(self.emb, self.emb_scale, t_dev, T, self.vocab, self.dim, x, xr, stream, dv)
         nws = B.ref_attention_prefill_workspace(T, self.nh, self.nkv, self.hd)
         ws = torch.empty(nws, dtype=torch.uint8, device=d)
+        nsq = B.ref_seq_workspace(T)  # the many-CTA norm / add / SwiGLU over the T-row tensors
+        wsq = torch.empty(nsq, dtype=torch.uint8, device=d)
+        norm = lambda x_, xr_, g_, y_, yr_: B.ref_rmsnorm_seq(x_, xr_, T, self.dim, g_[0], g_[1], self.eps, wsq, nsq,  # noqa: E731
+                                                                 y_, yr_, stream, dv)
+        add = lambda y_, yr_, b_, br_: B.ref_add_seq(y_, yr_, b_, br_, T * self.dim, wsq, nsq, y_, yr_, stream, dv)  # noqa: E731
         cat, cr, a, ar, hh, hhr = z(T * qd), rec(), z(T * self.dim), rec(), z(T * self.hidden), rec()
         for blk in self.blocks:
-            g, gs = blk["in_norm"]
-            B.ref_rmsnorm(x, xr, T, self.dim, g, gs, self.eps, h, hr, stream, dv)
+            norm(x, xr, blk["in_norm"], h, hr)
             q, qr = blk["wq"].forward_int(h, hr, T, stream=stream)
             k, kr = blk["wk"].forward_int(h, hr, T, stream=stream)
             v, vr = blk["wv"].forward_int(h, hr, T, stream=stream)
@@ -202,16 +206,15 @@ class RefDecoder:
                                     self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, ws, nws, cat, cr, stream,
                                     dv)
             blk["wo"].forward_int(cat, cr, T, y_dev=a, os_dev=ar, stream=stream)
-            B.ref_add(x, xr, a, ar, T * self.dim, x, xr, stream, dv)
-            g, gs = blk["post_norm"]
-            B.ref_rmsnorm(x, xr, T, self.dim, g, gs, self.eps, h, hr, stream, dv)
+            add(x, xr, a, ar)
+            norm(x, xr, blk["post_norm"], h, hr)
             gt, gtr = blk["gate"].forward_int(h, hr, T, stream=stream)
             up, upr = blk["up"].forward_int(h, hr, T, stream=stream)
-            B.ref_swiglu(gt, gtr, up, upr, T * self.hidden, self.silu_codes, self.silu_lut, hh, hhr, stream, dv)
+            B.ref_swiglu_seq(gt, gtr, up, upr, T * self.hidden, self.silu_codes, self.silu_lut, wsq, nsq, hh, hhr,
+                             stream, dv)
             m, mr = blk["down"].forward_int(hh, hhr, T, stream=stream)
-            B.ref_add(x, xr, m, mr, T * self.dim, x, xr, stream, dv)
-        g, gs = self.final_norm
-        B.ref_rmsnorm(x, xr, T, self.dim, g, gs, self.eps, h, hr, stream, dv)
+            add(x, xr, m, mr)
+        norm(x, xr, self.final_norm, h, hr)
         return self.lm_head.forward_int(h, hr, T, stream=stream)
 
     def decode_step(self, token: int, pos: int):

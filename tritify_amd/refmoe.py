@@ -14,7 +14,8 @@ groups only the exact integer products:
   experts down             kt_hip_quant_linear_rows (E groups; per-row input scales)
   combine                  kt_hip_ref_moe_combine   (per token: common scale, ec-weighted sum, 1/sumc)
   merge_rows               kt_hip_ref_merge_rows    (a sequence: the tokens at one scale)
-  shared expert + add      kt_hip_quant_linear, kt_hip_ref_swiglu, kt_hip_ref_add (the whole tensor)
+  shared expert + add      kt_hip_quant_linear, kt_hip_ref_swiglu_seq, kt_hip_ref_add_seq (the whole tensor, many
+                           CTAs)
 
 torch holds the device buffers; it computes nothing.
 """
@@ -154,10 +155,12 @@ class RefMoeLayer:
         su, sus = self.shared["up"].forward_int(x_dev, xs_rec, T, stream=stream)
         sh = torch.empty(T * self.shared_hidden, dtype=torch.int32, device=self.device)
         shs = torch.zeros(4, dtype=torch.int64, device=self.device)
-        B.ref_swiglu(sg, sgs, su, sus, T * self.shared_hidden, self.silu_codes, self.silu_lut, sh, shs, stream,
-                     self.dev)
+        nsq = B.ref_seq_workspace(1)  # whole-tensor SwiGLU and add on many CTAs
+        wsq = torch.empty(nsq, dtype=torch.uint8, device=self.device)
+        B.ref_swiglu_seq(sg, sgs, su, sus, T * self.shared_hidden, self.silu_codes, self.silu_lut, wsq, nsq, sh, shs,
+                         stream, self.dev)
         sd, sds = self.shared["down"].forward_int(sh, shs, T, stream=stream)
         out = torch.empty(T * dim, dtype=torch.int32, device=self.device)
         orec = torch.zeros(4, dtype=torch.int64, device=self.device)
-        B.ref_add(routed, rrec, sd, sds, T * dim, out, orec, stream, self.dev)
+        B.ref_add_seq(routed, rrec, sd, sds, T * dim, wsq, nsq, out, orec, stream, self.dev)
         return out, orec
