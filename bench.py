@@ -375,10 +375,10 @@ def bench_config5(torch, args) -> dict:
     lut = W.sam_entry_table(g5["entry_scale"])
     assert sha(img) == g5["img_sha256"] and sha(lut) == g5["entry_sha256"]
     k = C * KH * KW
-    lo_b, nib_b = T.w12_bytes(CO, k)
+    lo_b, hi_b = T.sam_patch_bytes(CO, C, KH, KW)
     lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
-    nib = torch.empty(nib_b, dtype=torch.uint8, device="cuda")
-    T.w12_upload(w, CO, k, lo, nib)
+    hi = torch.empty(hi_b, dtype=torch.int8, device="cuda")
+    T.sam_patch_upload(w, CO, C, KH, KW, lo, hi)
     OH, OW = (H + 2 * P - KH) // S + 1, (Wd + 2 * P - KW) // S + 1
     out = torch.empty(CO * OH * OW, dtype=torch.int8, device="cuda")
     imgd, lutd = torch.from_numpy(img).cuda(), torch.from_numpy(lut).cuda()
@@ -386,7 +386,7 @@ def bench_config5(torch, args) -> dict:
     stream = torch.cuda.current_stream()
 
     def patch(i):
-        T.sam_patch_embed(imgd, lutd, C, H, Wd, lo, nib, CO, KH, KW, S, P, bd, md, sd, out, stream=stream)
+        T.sam_patch_embed(imgd, lutd, C, H, Wd, lo, hi, CO, KH, KW, S, P, bd, md, sd, out, stream=stream)
 
     patch(0)
     torch.cuda.synchronize()

@@ -537,15 +537,28 @@ int kt_hip_moe_forward(int dev, const int8_t* x_dev, const int32_t* logits_dev, 
  * uses it, crates/03-models/kt-model-vision/src/hiera.rs:165-190) as an im2col-fused W12 GEMM. img_dev holds the
  * u8 pixels [ci][h][w]; each pixel p of channel c enters as the int8 code lut_dev[c * 256 + p] (the entry
  * quantization of the normalized image, plugin.rs:38); taps outside the image contribute nothing. The weights are
- * the W12 planes (kt_hip_w12_upload / kt_hip_w12_pack) of the co x (ci * kh * kw) code matrix, k ordered
- * (ic, ky, kx) as the reference's accumulation. out_dev [co][oh][ow] int8 receives
+ * the co x (ci * kh * kw) code matrix, k ordered (ic, ky, kx) as the reference's accumulation, packed by
+ * kt_hip_sam_patch_pack / kt_hip_sam_patch_upload. out_dev [co][oh][ow] int8 receives
  * clamp(requant(acc + bias[c], mant[c], shift[c]), +-127) (bias_dev may be NULL; |bias| < 2^30).
- * oh = (h + 2 pad - kh) / stride + 1, likewise ow. Limits: ci <= 4, ci * kh * kw <= 256,
- * ci * kh * (127 stride + kw) <= 16384. Asynchronous on `stream`. */
+ * oh = (h + 2 pad - kh) / stride + 1, likewise ow. Limits: ci <= 4, kw <= 16, ci * kh * kwp <= 256 (kwp = kw
+ * rounded up to 4), and the staged image rows of 128 output positions fit 40.5 KiB: nc * rows * (stride * 127 / 4
+ * + kwp / 4) dwords plus bank padding, nc = 4 / gcd(stride, 4), rows = ci * kh * kwp rounded up to 64, divided by
+ * kwp (7 x 7 stride 4 over 3 channels: 13.5 KiB). Asynchronous on `stream`. */
 int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_dev, int64_t ci, int64_t h, int64_t w,
-                           const int8_t* lo_dev, const uint8_t* nib_dev, int64_t co, int64_t kh, int64_t kw,
+                           const int8_t* lo_dev, const int8_t* hi_dev, int64_t co, int64_t kh, int64_t kw,
                            int64_t stride, int64_t pad, const int32_t* bias_dev, const int32_t* mant_dev,
                            const int32_t* shift_dev, int8_t* out_dev, void* stream);
+/* Bytes of each of the two patch-embed weight planes for co x (ci * kh * kw) codes: co rounded up to 32 times
+ * ci * kh * kwp rounded up to 64; both 0 when the shape has no layout (kw > 16, ci > 4). */
+void kt_hip_sam_patch_bytes(int64_t co, int64_t ci, int64_t kh, int64_t kw, size_t* lo_bytes, size_t* hi_bytes);
+/* Pack co x (ci * kh * kw) codes in [-2048, 2047] (device, the reference's [c_out][c_in][kh][kw] order) into the
+ * patch-embed planes (device): int8 digits with code = lo + 256 hi (hi in [-8, 8]), each kernel row's taps padded
+ * to kwp with zero codes, in the W12 fragment tiling. Codes outside the range give wrong planes. */
+int kt_hip_sam_patch_pack(int dev, const int32_t* codes_dev, int64_t co, int64_t ci, int64_t kh, int64_t kw,
+                          int8_t* lo_dev, int8_t* hi_dev, void* stream);
+/* Check host codes (hipErrorInvalidValue if any is outside [-2048, 2047]), upload and pack them. */
+int kt_hip_sam_patch_upload(int dev, const int32_t* codes, int64_t co, int64_t ci, int64_t kh, int64_t kw,
+                            int8_t* lo_dev, int8_t* hi_dev);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Decoder of config 3 (Qwen2.5-0.5B shape): the operations between the W12 GEMMs, device-resident operands. They

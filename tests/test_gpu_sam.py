@@ -37,16 +37,15 @@ def run_conv(torch, C, H, W, CO, KH, KW, S, P, seeds=(61, 62, 63), bias=True):
     say(f"case: patch embed C={C} H={H} W={W} CO={CO} k={KH}x{KW} s={S} p={P}")
     img, w, b, mant, shift = W_.sam_patch_inputs(C, H, W, CO, KH, KW, *seeds)
     lut = np.concatenate([W_.sam_entry_table()] * 2)[:C]  # C <= 4 channels of entry codes
-    k = C * KH * KW
-    lo_b, nib_b = TA.w12_bytes(CO, k)
+    lo_b, hi_b = TA.sam_patch_bytes(CO, C, KH, KW)
     lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
-    nib = torch.empty(nib_b, dtype=torch.uint8, device="cuda")
-    TA.w12_upload(w, CO, k, lo, nib)
+    hi = torch.empty(hi_b, dtype=torch.int8, device="cuda")
+    TA.sam_patch_upload(w, CO, C, KH, KW, lo, hi)
     OH, OW = (H + 2 * P - KH) // S + 1, (W + 2 * P - KW) // S + 1
     out = torch.full((CO * OH * OW,), 77, dtype=torch.int8, device="cuda")
     bd = torch.from_numpy(b).cuda() if bias else None
     TA.sam_patch_embed(torch.from_numpy(img).cuda(), torch.from_numpy(np.ascontiguousarray(lut)).cuda(), C, H, W, lo,
-                       nib, CO, KH, KW, S, P, bd, torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda(), out)
+                       hi, CO, KH, KW, S, P, bd, torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda(), out)
     torch.cuda.synchronize()
     q = O.sam_entry(img, C, H * W, lut)
     want, _ = O.conv2d(q, C, H, W, w.astype(np.int16), CO, KH, KW, S, P, b if bias else None, mant, shift)
@@ -65,9 +64,33 @@ def test_patch_embed_ragged_segments_and_channel_tiles(torch_dev):
 
 
 def test_patch_embed_other_kernels(torch_dev):
-    """A 3x3 stride-1 conv over 4 channels (k = 36, one k tile) and a 5x5 stride-2 conv without bias (k = 75)."""
+    """A 3x3 stride-1 conv over 4 channels (k = 36, one k tile; four phase copies of each staged row) and a 5x5
+    stride-2 conv without bias (k = 75; two copies)."""
     run_conv(torch_dev, 4, 20, 260, 24, 3, 3, 1, 1, seeds=(67, 68, 69))
     run_conv(torch_dev, 2, 31, 45, 8, 5, 5, 2, 0, seeds=(70, 71, 72), bias=False)
+
+
+def test_patch_embed_wide_and_strided_kernels(torch_dev):
+    """A 9x9 stride-3 conv (taps padded to 12: three dwords per kernel row, four copies; k = 162 over 2 channels,
+    byte loads since w % 4 != 0) and a ViT-style 16x16 stride-16 patchify (one dword-aligned copy, k = 256)."""
+    run_conv(torch_dev, 2, 40, 66, 20, 9, 9, 3, 4, seeds=(73, 74, 75))
+    run_conv(torch_dev, 1, 64, 320, 36, 16, 16, 16, 0, seeds=(76, 77, 78))
+
+
+def test_patch_weight_layout_rejects_wide_kernels(torch_dev):
+    """kw > 16 and ci * kh * kwp > 256 have no patch-embed layout; the entry rejects them before any launch."""
+    import tritify_amd as TA
+
+    with pytest.raises(ValueError):
+        TA.sam_patch_bytes(8, 3, 3, 17)
+    lo = torch_dev.zeros(1 << 16, dtype=torch_dev.int8, device="cuda")
+    hi = torch_dev.zeros(1 << 16, dtype=torch_dev.int8, device="cuda")
+    out = torch_dev.zeros(64, dtype=torch_dev.int8, device="cuda")
+    img = torch_dev.zeros(3 * 32 * 32, dtype=torch_dev.uint8, device="cuda")
+    lut = torch_dev.zeros(3 * 256, dtype=torch_dev.int8, device="cuda")
+    sc = torch_dev.zeros(8, dtype=torch_dev.int32, device="cuda")
+    with pytest.raises(RuntimeError):  # 3 * 9 * 12 = 324 > 256
+        TA.sam_patch_embed(img, lut, 3, 32, 32, lo, hi, 8, 9, 9, 4, 0, None, sc, sc, out)
 
 
 def run_mlp(torch, tokens, dim, hidden, seeds=(81, 82, 83)):
@@ -118,15 +141,14 @@ def test_sam_full_config5(torch_dev):
                                                  g5["bias_sigma"])
     lut = W_.sam_entry_table(g5["entry_scale"])
     assert sha(img) == g5["img_sha256"] and sha(lut) == g5["entry_sha256"] and sha(W_.gelu_table()) == g5["gelu_sha256"]
-    k = g5["C"] * g5["KH"] * g5["KW"]
-    lo_b, nib_b = TA.w12_bytes(g5["CO"], k)
+    lo_b, hi_b = TA.sam_patch_bytes(g5["CO"], g5["C"], g5["KH"], g5["KW"])
     lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
-    nib = torch.empty(nib_b, dtype=torch.uint8, device="cuda")
-    TA.w12_upload(w, g5["CO"], k, lo, nib)
+    hi = torch.empty(hi_b, dtype=torch.int8, device="cuda")
+    TA.sam_patch_upload(w, g5["CO"], g5["C"], g5["KH"], g5["KW"], lo, hi)
     OH = (g5["H"] + 2 * g5["P"] - g5["KH"]) // g5["S"] + 1
     OW = (g5["W"] + 2 * g5["P"] - g5["KW"]) // g5["S"] + 1
     out = torch.empty(g5["CO"] * OH * OW, dtype=torch.int8, device="cuda")
-    TA.sam_patch_embed(torch.from_numpy(img).cuda(), torch.from_numpy(lut).cuda(), g5["C"], g5["H"], g5["W"], lo, nib,
+    TA.sam_patch_embed(torch.from_numpy(img).cuda(), torch.from_numpy(lut).cuda(), g5["C"], g5["H"], g5["W"], lo, hi,
                        g5["CO"], g5["KH"], g5["KW"], g5["S"], g5["P"], torch.from_numpy(b).cuda(),
                        torch.from_numpy(mant).cuda(), torch.from_numpy(shift).cuda(), out)
     torch.cuda.synchronize()

@@ -91,6 +91,9 @@ def _declare(L: C.CDLL) -> None:
                                     _I, _I, _P, _P, _P]),
         "kt_hip_sam_patch_embed": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P,
                                         _P, _P, _P]),
+        "kt_hip_sam_patch_bytes": (None, [_I64, _I64, _I64, _I64, C.POINTER(_SZ), C.POINTER(_SZ)]),
+        "kt_hip_sam_patch_pack": (_I, [_I, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+        "kt_hip_sam_patch_upload": (_I, [_I, _P, _I64, _I64, _I64, _I64, _P, _P]),
         "kt_hip_dec_embed": (_I, [_I, _P, _I64, _P, _I64, _P, _P]),
         "kt_hip_dec_rmsnorm": (_I, [_I, _P, _I64, _I64, _P, _I64, _P]),
         "kt_hip_dec_rope_kv": (_I, [_I, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
@@ -496,11 +499,37 @@ def moe_forward(x_dev, logits_dev, tokens: int, hidden: int, ffn: int, experts: 
 # SAM image path (config 5)
 
 
-def sam_patch_embed(img_dev, lut_dev, ci: int, h: int, w: int, lo_dev, nib_dev, co: int, kh: int, kw: int,
+def sam_patch_bytes(co: int, ci: int, kh: int, kw: int) -> tuple[int, int]:
+    """Bytes of the two patch-embed weight planes (int8 lo and hi digits, co·ci·kh·kwp codes, kwp = kw rounded up
+    to 4, in the W12 fragment tiling)."""
+    lo, hi = C.c_size_t(), C.c_size_t()
+    lib().kt_hip_sam_patch_bytes(co, ci, kh, kw, C.byref(lo), C.byref(hi))
+    if lo.value == 0 and co > 0:
+        raise ValueError(f"no patch-embed weight layout for ci={ci} kh={kh} kw={kw}")
+    return lo.value, hi.value
+
+
+def sam_patch_pack(codes_dev, co: int, ci: int, kh: int, kw: int, lo_dev, hi_dev, stream=None, dev: int = 0) -> None:
+    """Pack co x (ci·kh·kw) codes (i32, device, [c_out][c_in][kh][kw]) into the patch-embed planes."""
+    check(lib().kt_hip_sam_patch_pack(dev, _ptr(codes_dev), co, ci, kh, kw, _ptr(lo_dev), _ptr(hi_dev),
+                                      _stream(stream)), "sam patch pack")
+
+
+def sam_patch_upload(codes, co: int, ci: int, kh: int, kw: int, lo_dev, hi_dev, dev: int = 0) -> None:
+    """Check host codes against [-2048, 2047], upload and pack them into the patch-embed planes (synchronous)."""
+    c = _i32(codes)
+    if c.size != co * ci * kh * kw:
+        raise ValueError("codes are not co·ci·kh·kw")
+    check(lib().kt_hip_sam_patch_upload(dev, c.ctypes.data, co, ci, kh, kw, _ptr(lo_dev), _ptr(hi_dev)),
+          "sam patch upload")
+
+
+def sam_patch_embed(img_dev, lut_dev, ci: int, h: int, w: int, lo_dev, hi_dev, co: int, kh: int, kw: int,
                     stride: int, pad: int, bias_dev, mant_dev, shift_dev, out_dev, stream=None, dev: int = 0) -> None:
-    """The im2col-fused patch-embed conv: u8 pixels -> entry codes -> W12 GEMM -> +bias -> int8 [co][oh][ow]."""
+    """The im2col-fused patch-embed conv: u8 pixels -> entry codes -> W12 GEMM -> +bias -> int8 [co][oh][ow]; the
+    weights are the planes of sam_patch_pack / sam_patch_upload."""
     check(
-        lib().kt_hip_sam_patch_embed(dev, _ptr(img_dev), _ptr(lut_dev), ci, h, w, _ptr(lo_dev), _ptr(nib_dev), co, kh,
+        lib().kt_hip_sam_patch_embed(dev, _ptr(img_dev), _ptr(lut_dev), ci, h, w, _ptr(lo_dev), _ptr(hi_dev), co, kh,
                                      kw, stride, pad, _ptr(bias_dev), _ptr(mant_dev), _ptr(shift_dev), _ptr(out_dev),
                                      _stream(stream)),
         "sam patch embed",

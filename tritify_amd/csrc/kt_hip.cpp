@@ -691,8 +691,51 @@ int kt_hip_moe_forward(int dev, const int8_t* x_dev, const int32_t* logits_dev, 
 // SAM image path (config 5)
 // ----------------------------------------------------------------------------------------------------------------
 
+// The tap-padded k of a patch-embed weight matrix, 0 for shapes the patch embed does not take.
+static int64_t sam_patch_kp(int64_t ci, int64_t kh, int64_t kw) {
+    const int kwp = kt::conv_patch_kwp(kw);
+    if (ci < 1 || ci > 4 || kh < 1 || kh > 256 || kwp == 0) return 0;
+    return ci * kh * kwp;
+}
+
+void kt_hip_sam_patch_bytes(int64_t co, int64_t ci, int64_t kh, int64_t kw, size_t* lo_bytes, size_t* hi_bytes) {
+    const int64_t k = sam_patch_kp(ci, kh, kw);
+    if (co < 0 || k == 0) {
+        *lo_bytes = *hi_bytes = 0;
+        return;
+    }
+    *lo_bytes = *hi_bytes = (size_t)((co + 31) / 32 * 32) * (size_t)kp_of(k);
+}
+
+int kt_hip_sam_patch_pack(int dev, const int32_t* codes_dev, int64_t co, int64_t ci, int64_t kh, int64_t kw,
+                          int8_t* lo_dev, int8_t* hi_dev, void* stream) {
+    if (co < 0 || co > INT_MAX / 2 || sam_patch_kp(ci, kh, kw) == 0) return (int)hipErrorInvalidValue;
+    if (co == 0) return 0;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_conv_pack(codes_dev, (int)co, (int)ci, (int)kh, (int)kw, lo_dev, hi_dev,
+                                     (hipStream_t)stream);
+}
+
+int kt_hip_sam_patch_upload(int dev, const int32_t* codes, int64_t co, int64_t ci, int64_t kh, int64_t kw,
+                            int8_t* lo_dev, int8_t* hi_dev) {
+    if (co < 0 || co > INT_MAX / 2 || sam_patch_kp(ci, kh, kw) == 0) return (int)hipErrorInvalidValue;
+    const size_t cnt = (size_t)co * (size_t)(ci * kh * kw);
+    for (size_t i = 0; i < cnt; i++)
+        if (codes[i] < -2048 || codes[i] > 2047) return (int)hipErrorInvalidValue;
+    if (cnt == 0) return 0;
+    KT_TRY(hipSetDevice(dev));
+    void* tmp = nullptr;
+    KT_TRY(hipMalloc(&tmp, cnt * sizeof(int32_t)));
+    hipError_t e = hipMemcpy(tmp, codes, cnt * sizeof(int32_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = kt::launch_conv_pack((const int32_t*)tmp, (int)co, (int)ci, (int)kh, (int)kw, lo_dev, hi_dev, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    hipError_t f = hipFree(tmp);
+    return (int)(e != hipSuccess ? e : f);
+}
+
 int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_dev, int64_t ci, int64_t h, int64_t w,
-                           const int8_t* lo_dev, const uint8_t* nib_dev, int64_t co, int64_t kh, int64_t kw,
+                           const int8_t* lo_dev, const int8_t* hi_dev, int64_t co, int64_t kh, int64_t kw,
                            int64_t stride, int64_t pad, const int32_t* bias_dev, const int32_t* mant_dev,
                            const int32_t* shift_dev, int8_t* out_dev, void* stream) {
     if (ci < 1 || ci > 4 || h < 1 || w < 1 || h > INT_MAX || w > INT_MAX || co < 1 || co > INT_MAX || kh < 1 ||
@@ -701,7 +744,7 @@ int kt_hip_sam_patch_embed(int dev, const uint8_t* img_dev, const int8_t* lut_de
         return (int)hipErrorInvalidValue;
     KT_TRY(hipSetDevice(dev));
     return (int)kt::launch_conv_patch(img_dev, lut_dev, (int)ci, (int)h, (int)w, (int)kh, (int)kw, (int)stride,
-                                      (int)pad, lo_dev, nib_dev, (int)co, bias_dev, mant_dev, shift_dev, out_dev,
+                                      (int)pad, lo_dev, hi_dev, (int)co, bias_dev, mant_dev, shift_dev, out_dev,
                                       (hipStream_t)stream);
 }
 

@@ -35,8 +35,14 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
 hipError_t launch_moe_combine(const int8_t* d, const int32_t* off, const int32_t* sel, const int32_t* cw,
                               const int32_t* pos, int T, int H, int E, int top_k, int out_shift, int8_t* out,
                               hipStream_t s);
+// The tap-padded width of a patch-embed kernel row (the weights' k order is (ic, ky, kx < kwp)); 0 if kw > 16.
+inline int conv_patch_kwp(int64_t kw) { return kw >= 1 && kw <= 16 ? (int)((kw + 3) & ~3) : 0; }
+// Patch-embed weights: co x (ci * kh * kw) codes -> two int8 digit planes (lo, hi; code = lo + 256 hi), each
+// co rounded up to 32 by k = ci * kh * kwp rounded up to 64 bytes, in the W12 fragment tiling.
+hipError_t launch_conv_pack(const int32_t* codes, int co, int ci, int kh, int kw, int8_t* lo, int8_t* hi,
+                            hipStream_t s);
 hipError_t launch_conv_patch(const uint8_t* img, const int8_t* lut, int CI, int H, int W, int KH, int KW, int S, int P,
-                             const int8_t* wlo, const uint8_t* wnib, int CO, const int32_t* bias, const int32_t* mant,
+                             const int8_t* wlo, const int8_t* whi, int CO, const int32_t* bias, const int32_t* mant,
                              const int32_t* shift, int8_t* out, hipStream_t s);
 hipError_t launch_dec_embed(const int32_t* tokens, int T, const int16_t* emb, int d, int32_t* r, hipStream_t s);
 hipError_t launch_dec_rmsnorm(const int32_t* r, int T, int d, int8_t* q, int qs, hipStream_t s);
