@@ -262,6 +262,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         for (int r = 0; r < 16; r++) acc0[i][r] = cb;
         acc1[i] = v16i{};
     }
+    // The first half of the waves issues its MFMAs first, so its epilogue (VALU) overlaps the other half's MFMAs.
+    if (rh == 0) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
 #pragma unroll
@@ -284,6 +286,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         }
         if (kb + BW < KB) load_b(kb + BW);
     }
+    if (rh == 0) __builtin_amdgcn_s_setprio(0);
 
     {
         const int c = ct * 32 + j;
@@ -294,15 +297,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         q.bias = (uint64_t)(uint32_t)k8.x | (uint64_t)(uint32_t)k8.y << 32;
         const uint32_t sat = (uint32_t)k4.y;
         const double ms = __longlong_as_double((long long)((uint64_t)(uint32_t)k8.z | (uint64_t)(uint32_t)k8.w << 32));
-        // requant(v) = round(v * mant / 2^shift) half away from zero, clamped to +-127, is odd in mant: with
-        // ms = |mant| 2^-shift and shift <= 46 it is computed in double and the column's sign applied to the packed
-        // bytes. Unless the result saturates, |v * mant| < 127.5 * 2^shift < 2^53, so v * ms + copysign(0.5, v) is
-        // exact and truncation rounds it; a saturating value stays at or beyond +-127.5 after rounding (rounding is
-        // monotone), so the clamp holds it at +-127.
+        // requant(v) = round(v * mant / 2^shift) half away from zero, clamped to +-127, is odd in v and in mant:
+        // with ms = |mant| 2^-shift and shift <= 46 it is sign(v) sign(mant) min(floor(|v| ms + 0.5), 127) in
+        // double, the column's sign applied to the packed bytes. Unless the result saturates,
+        // |v| |mant| < 127.5 * 2^shift < 2^53, so |v| ms + 0.5 is exact and truncation floors it; a saturating value
+        // stays at or beyond 127.5 after rounding (rounding is monotone), so the clamp holds it at 127.
         auto rq_fp = [&](int v) {
-            const uint32_t hs = ((uint32_t)v & 0x80000000u) | 0x3FE00000u;  // +-0.5 with the sign of v
-            const double y = fma((double)v, ms, __hiloint2double((int)hs, 0));
-            return (int)fmin(fmax(y, -127.0), 127.0);
+            const int m = (int)fmin(fma(fabs((double)v), ms, 0.5), 127.0);  // round(|v| ms) half up, <= 127
+            return v < 0 ? -m : m;
         };
         // four int8 lanes negated at once (|b| <= 127: no byte borrows from its neighbour)
         auto neg4 = [](uint32_t x) { return (0x80808080u - (x & 0x7F7F7F7Fu)) ^ (~x & 0x80808080u); };
