@@ -181,6 +181,32 @@ __device__ __forceinline__ int32_t col_requant(int v, const ColQ& q) {
     return neg ? (int32_t)(0u - (uint32_t)m) : (int32_t)m;
 }
 
+// The int8 requant of one output channel with a double-precision path. requant(v) = round(v mant / 2^shift) half
+// away from zero, clamped to +-127, is odd in v and in mant, so it equals sign(v) sign(mant) min(floor(|v| ms + 0.5),
+// 127) with ms = |mant| 2^-shift (exact in double: a 31-bit integer scaled by a power of two in range). For
+// shift <= 46, unless the value saturates, |v mant| < 127.5 2^shift < 2^53, so |v| ms + 0.5 is exact and truncation
+// floors it; a saturating value rounds to 127.5 or more (rounding is monotone) and the clamp holds it at 127. Other
+// shifts take col_requant.
+struct ColQ8 {
+    ColQ q;
+    double ms;
+    bool fp;  // the double path is exact for this channel
+};
+
+__device__ __forceinline__ ColQ8 col_q8(int32_t mant, int32_t sh) {
+    ColQ8 c;
+    c.q = col_q(mant, sh);
+    c.fp = sh >= -512 && sh <= 46;
+    c.ms = c.fp ? ldexp(fabs((double)mant), -sh) : 0.0;
+    return c;
+}
+
+// col_requant<false>(v, c.q) for a channel with c.fp.
+__device__ __forceinline__ int32_t rq8_fp(int v, const ColQ8& c) {
+    const int m = (int)fmin(fma(fabs((double)v), c.ms, 0.5), 127.0);
+    return (v < 0) != c.q.neg ? -m : m;
+}
+
 // clamp(requant(v, 1, sh), -127, 127) for 1 <= sh <= 30 and |v| < 2^31: round half away from zero.
 __device__ __forceinline__ int32_t shift_rq8(int v, int sh) {
     const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
@@ -599,15 +625,26 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
     for (int j = 0; j < C::WTN; j++) {
         const int c = wave * 32 * C::WTN + j * 32 + (lane & 31), n = n0 + c;
         const int ch = n < N ? chan(n) : 0;
-        const ColQ q = col_q(n < N ? mant[ch] : 0, n < N ? shift[ch] : 1);
+        const ColQ8 q = col_q8(n < N ? mant[ch] : 0, n < N ? shift[ch] : 1);
+        if (__all(q.fp)) {  // every channel of the wave on the double path
 #pragma unroll
-        for (int i = 0; i < C::WTM; i++)
+            for (int i = 0; i < C::WTM; i++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
-                sO[rt * C::BN + c] = (int8_t)col_requant<false>(v, q);
-            }
+                for (int r = 0; r < 16; r++) {
+                    const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
+                    sO[rt * C::BN + c] = (int8_t)rq8_fp(v, q);
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::WTM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
+                    sO[rt * C::BN + c] = (int8_t)col_requant<false>(v, q.q);
+                }
+        }
     }
 }
 
