@@ -466,8 +466,10 @@ __device__ __forceinline__ void w12_gemm_epilogue(const v16i (&acc0)[C::WTM][C::
     const int wave = (tid >> 6) % WN, rw0 = ((tid >> 6) / WN) * 32 * WTM;
     const bool full = m0 + BM <= M && n0 + BN <= N;
     if constexpr (OUT == KT_OUT_I8 && SMALL) {
-        // requantize into an int8 tile in LDS (the A ring is no longer read), then store it with 16-byte writes
-        w12_requant_tile8<C>(acc0, acc1, sRow, mant, shift, n0, N, [](int n) { return n; }, smem);
+        // requantize (and map through the code table) into an int8 tile in LDS (the A ring is no longer read),
+        // then store it with 16-byte writes
+        if (lut) w12_requant_tile8<C, true>(acc0, acc1, sRow, mant, shift, n0, N, [](int n) { return n; }, smem, sLut);
+        else w12_requant_tile8<C, false>(acc0, acc1, sRow, mant, shift, n0, N, [](int n) { return n; }, smem);
         __syncthreads();
         constexpr int CH = BM * BN / 16;  // 16-byte chunks of the tile
 #pragma unroll
@@ -475,20 +477,9 @@ __device__ __forceinline__ void w12_gemm_epilogue(const v16i (&acc0)[C::WTM][C::
             const int idx = tid + NT * i;
             if (CH % NT != 0 && idx >= CH) break;
             const int rt = idx / (BN / 16), c = (idx % (BN / 16)) * 16, m = m0 + rt, n = n0 + c;
-            v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
+            const v4i v = *reinterpret_cast<const v4i*>(smem + rt * BN + c);
             // bytes are moved with shifts, never through the vector's address: an addressed vector becomes a
             // per-thread LDS slot whose indexing reads the dispatch packet, a long stall before the stores
-            if (lut) {
-#pragma unroll
-                for (int w4 = 0; w4 < 4; w4++) {
-                    const uint32_t xw = (uint32_t)v[w4];
-                    uint32_t yw = 0;
-#pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        yw |= (uint32_t)(uint8_t)sLut[(int)(int8_t)(xw >> (8 * t)) + 127] << (8 * t);
-                    v[w4] = (int)yw;
-                }
-            }
             int8_t* dst = reinterpret_cast<int8_t*>(y) + (size_t)m * N + n;
             if (full && (N & 15) == 0) {
                 *reinterpret_cast<v4i*>(dst) = v;

@@ -614,11 +614,12 @@ __device__ __forceinline__ void w12_row_sums(const int (&rsum)[C::AL], int* sRow
 // Requantize the CTA tile (SMALL domain: every dot fits int32) per output channel into an int8 tile sO[BM][BN] in
 // LDS. Channel n of the tile's column c is n0 + c; chan(n) maps it to the index of its (mant, shift) pair, and
 // columns at or past N get a zero scale.
-template <class C, class ChanFn>
+// LUT: sLut (LDS, 255 entries indexed by q + 127) maps each requantized code as it is written.
+template <class C, bool LUT = false, class ChanFn>
 __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::WTN],
                                                   const v16i (&acc1)[C::WTM][C::WTN], const int* sRow,
                                                   const int32_t* mant, const int32_t* shift, int n0, int N,
-                                                  ChanFn chan, int8_t* sO) {
+                                                  ChanFn chan, int8_t* sO, const int8_t* sLut = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
     const int wave = (tid >> 6) % C::WN, rw0 = ((tid >> 6) / C::WN) * 32 * C::WTM;
 #pragma unroll
@@ -626,14 +627,17 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
         const int c = wave * 32 * C::WTN + j * 32 + (lane & 31), n = n0 + c;
         const int ch = n < N ? chan(n) : 0;
         const ColQ8 q = col_q8(n < N ? mant[ch] : 0, n < N ? shift[ch] : 1);
+        auto put = [&](int rt, int code) {
+            if constexpr (LUT) sO[rt * C::BN + c] = sLut[code + 127];
+            else sO[rt * C::BN + c] = (int8_t)code;
+        };
         if (__all(q.fp)) {  // every channel of the wave on the double path
 #pragma unroll
             for (int i = 0; i < C::WTM; i++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
-                    sO[rt * C::BN + c] = (int8_t)rq8_fp(v, q);
+                    put(rt, rq8_fp(w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]), q));
                 }
         } else {
 #pragma unroll
@@ -641,8 +645,7 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
-                    sO[rt * C::BN + c] = (int8_t)col_requant<false>(v, q.q);
+                    put(rt, col_requant<false>(w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]), q.q));
                 }
         }
     }
