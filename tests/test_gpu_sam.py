@@ -77,6 +77,38 @@ def test_patch_embed_wide_and_strided_kernels(torch_dev):
     run_conv(torch_dev, 1, 64, 320, 36, 16, 16, 16, 0, seeds=(76, 77, 78))
 
 
+def test_patch_weights_device_pack_equals_upload(torch_dev):
+    """kt_hip_sam_patch_pack (device codes) writes the same two planes as kt_hip_sam_patch_upload (host codes): codes
+    at both ends of the range, tap widths padded by 1, 3 and 0, partial column blocks and k tiles."""
+    import tritify_amd as TA
+
+    torch = torch_dev
+    rng = np.random.default_rng(91)
+    for co, ci, kh, kw in [(40, 3, 7, 7), (20, 2, 9, 9), (8, 1, 16, 16), (33, 4, 3, 1)]:
+        say(f"case: patch weight planes co={co} ci={ci} k={kh}x{kw}")
+        w = rng.integers(-2048, 2048, size=co * ci * kh * kw).astype(np.int32)
+        w[:4] = [-2048, 2047, 0, -1]
+        lo_b, hi_b = TA.sam_patch_bytes(co, ci, kh, kw)
+        planes = []
+        for dev_pack in (False, True):
+            lo = torch.full((lo_b,), 55, dtype=torch.int8, device="cuda")
+            hi = torch.full((hi_b,), 55, dtype=torch.int8, device="cuda")
+            if dev_pack:
+                TA.sam_patch_pack(torch.from_numpy(w).cuda(), co, ci, kh, kw, lo, hi)
+            else:
+                TA.sam_patch_upload(w, co, ci, kh, kw, lo, hi)
+            torch.cuda.synchronize()
+            planes.append((lo.cpu().numpy(), hi.cpu().numpy()))
+        assert np.array_equal(planes[0][0], planes[1][0]) and np.array_equal(planes[0][1], planes[1][1])
+        # every code is lo + 256 hi with hi in [-8, 8]; the planes hold co * ci * kh * kw codes (the pad taps, rows
+        # and k are zero) and their sum of codes equals the weights'
+        lo8, hi8 = planes[0][0].astype(np.int64), planes[0][1].astype(np.int64)
+        assert hi8.min() >= -8 and hi8.max() <= 8
+        assert (lo8 + 256 * hi8).sum() == w.astype(np.int64).sum()
+    with pytest.raises(RuntimeError):  # a code out of range: refused before any upload
+        TA.sam_patch_upload(np.full(8 * 3 * 3 * 3, 2048, np.int32), 8, 3, 3, 3, lo, hi)
+
+
 def test_patch_weight_layout_rejects_wide_kernels(torch_dev):
     """kw > 16 and ci * kh * kwp > 256 have no patch-embed layout; the entry rejects them before any launch."""
     import tritify_amd as TA
