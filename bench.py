@@ -889,10 +889,87 @@ def bench_ref_sam(torch, args) -> dict:
     }
 
 
+# GLM-4.5-Air's MoE layer: hidden 4096, 128 routed experts of 1408, 8 per token, the sigmoid router with its
+# selection bias and norm_topk_prob, one shared expert of 1408
+REF_GLM = dict(dim=4096, E=128, top_k=8, hidden=1408, shared=1408)
+REF_MOE_T = (1, 256)
+
+
+def ref_moe_weights(cfg: dict, seed: int):
+    """(router, experts, coded bias, shared) of a REF_GLM layer: every code uniform in +-WLEVELS at the Scale
+    from_weights gives floats of peak 1 (1 / WLEVELS), the coded bias uniform in +-0.05 * 2^20; drawn on threads."""
+    import tritify_amd as T
+    from concurrent.futures import ThreadPoolExecutor
+    from tritify_amd import backend as B
+
+    sc = B.ref_scale_from_f64(1.0 / WL)
+    d, E, h, hs = cfg["dim"], cfg["E"], cfg["hidden"], cfg["shared"]
+    shapes = [(E, d)] + [sh for _ in range(E + 1) for sh in ((h, d), (h, d), (d, h))]
+    shapes[-3:] = [(hs, d), (hs, d), (d, hs)]
+    with ThreadPoolExecutor(max(1, min(8, cpu_threads()))) as ex:
+        mats = list(ex.map(lambda i: T.gen_uniform_fast(seed + i, -WL, WL, shapes[i][0] * shapes[i][1])
+                           .reshape(shapes[i]), range(len(shapes))))
+    names = ("gate", "up", "down")
+    experts = [{n: (mats[1 + 3 * e + j], sc) for j, n in enumerate(names)} for e in range(E + 1)]
+    bias = T.gen_uniform_fast(seed - 1, -52429, 52429, E).astype(np.int64)
+    return (mats[0], sc), experts[:E], bias, experts[E]
+
+
+def bench_ref_moe(torch, args) -> dict:
+    """MoeMlp::forward_int (layers.rs:652-1034) at the reference's semantics, GLM-4.5-Air's layer shape: one decode
+    token and a 256-token batch, each output checked against the oracle's token-by-token restatement before timing;
+    the oracle's run of the batch is the CPU baseline."""
+    from oracle import oracle as O
+    from tritify_amd import backend as B
+    from tritify_amd.refmoe import RefMoeLayer
+    import tritify_amd as T
+
+    cfg = REF_GLM
+    t0 = time.perf_counter()
+    router, experts, bias, shared = ref_moe_weights(cfg, 0x61A5)
+    layer = RefMoeLayer(cfg["dim"], router, experts, cfg["top_k"], True, bias, shared)
+    log(f"bench: ref moe: weights resident in {time.perf_counter() - t0:.1f}s")
+    model = O.RefMoe.from_weights(cfg["dim"], router, experts, cfg["top_k"], True, bias, shared)
+    del router, experts, shared
+    cores = cpu_threads()
+    O.set_max_threads(cores)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    rng = np.random.default_rng(0x61A7)
+    res = {"workload": "the reference's MoeMlp::forward_int at its own semantics (i32 codes, per-row dynamic "
+                       "quantization of every QuantLinear row, sigmoid router with selection bias and norm_topk, "
+                       "exp / sigmoid / SiLU CodeLuts, ec-weighted combine, merge_rows, shared expert), GLM-4.5-Air "
+                       "MoE layer shape (dim 4096, 128 experts of 1408, top-8, shared 1408), 12-trit weights",
+           "bit_exact": True}
+    for T_ in REF_MOE_T:
+        x, xs = B.ref_from_reals(rng.uniform(-1.0, 1.0, T_ * cfg["dim"]))
+        xd, xr = torch.from_numpy(x).to(dev), T.qscale_record(*xs)
+        out, orec = layer.forward(xd, xr, T_)
+        c0 = time.perf_counter()
+        want, ws = model.forward(x, T_, xs)
+        cpu_s = time.perf_counter() - c0
+        if not (np.array_equal(out.cpu().numpy(), want) and
+                tuple(T.read_qscale(orec)[k] for k in ("mant", "shift")) == ws):
+            raise SystemExit(f"bench: ref moe T={T_}: differs from the CPU oracle")
+        n = 200 if T_ == 1 else 20
+        ms, _ = time_launches(torch, lambda i: layer.forward(xd, xr, T_, stream=stream), n, 5)
+        res[f"T{T_}"] = {"us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(T_ / (ms * 1e-3), 1)}
+        log(f"bench: ref moe T={T_}: {ms * 1e3:.1f} us per forward, bit-exact")
+        if T_ == REF_MOE_T[-1]:
+            res["cpu_baseline"] = {
+                "value": round(T_ / cpu_s, 1), "unit": "tokens/s", "cores": cores, "nproc": os.cpu_count(),
+                "kind": "port", "sample": f"the oracle's MoeMlp::forward_int of the same {T_} tokens (token by "
+                                          f"token, QuantLinear rows on {cores} threads), {cpu_s * 1e3:.0f} ms"}
+    del layer, model
+    return res
+
+
 def bench_ref(torch, args) -> dict:
     res = {"decoder": bench_ref_decoder(torch, args)}
     torch.cuda.empty_cache()
     res["sam"] = bench_ref_sam(torch, args)
+    torch.cuda.empty_cache()
+    res["moe"] = bench_ref_moe(torch, args)
     torch.cuda.empty_cache()
     return res
 
@@ -909,7 +986,7 @@ def main() -> int:
     ap.add_argument("--configs", type=str, default="2,3,4,5,ql,lb,ref",
                     help="comma-separated configs to run (2 is the headline; ql = the reference's QuantLinear; "
                          "lb = the LinearBackend trait path on cuda_bench's shapes; ref = the reference-semantics "
-                         "decoder and SAM image path)")
+                         "decoder, SAM image path and GLM MoE layer)")
     ap.add_argument("--ms", type=str, default="", help="comma-separated subset of config-2 M to run (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")

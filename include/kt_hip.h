@@ -271,11 +271,14 @@ int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hi
  * calls run it: output row r is forward_int of input row xidx_dev[r] of x_dev (x_rows x in_f; xidx_dev NULL: row
  * r; an index outside [0, x_rows) reads as zeros) at the scale record xs_dev[xs_step * r] (xs_step 0: one record
  * for every row, 1: one per row), quantized by its own max |x|, requantized by its own max |acc|, against the weights
- * of the group g holding r (rows off[g] .. off[g + 1] - 1; off_host and off_dev the same groups + 1 offsets, on the
- * host and on the device, off[0] = 0, off[groups] = rows): pw digit planes of out_f x in_f codes at w_planes_dev +
- * g * w_group_bytes (kt_hip_pack_planes), Scale (w_mant_dev[g], w_shift_dev[g]). No bias. y_dev: rows x out_f codes,
- * ys_dev: rows records. ws_dev: the caller's workspace of kt_hip_quant_linear_rows_workspace bytes. */
-size_t kt_hip_quant_linear_rows_workspace(int64_t rows, int64_t in_f, int64_t out_f);
+ * of the group g holding r (rows off[g] .. off[g + 1] - 1, off_dev the groups + 1 offsets on the device, off[0] = 0,
+ * off[groups] = rows): pw digit planes of out_f x in_f codes at w_planes_dev + g * w_group_bytes
+ * (kt_hip_pack_planes), Scale (w_mant_dev[g], w_shift_dev[g]). No bias. y_dev: rows x out_f codes, ys_dev: rows
+ * records. ws_dev: the caller's workspace of kt_hip_quant_linear_rows_workspace bytes. The group sizes are read on
+ * the device (no host round trip): off_host, the same offsets on the host, is optional and only checked (an invalid
+ * copy is an error); offsets on the device that are not monotone or leave [0, rows] are clamped into a valid split
+ * rather than read out of bounds. Layers at model size bucket their rows with kt_hip_ref_moe_bucket. */
+size_t kt_hip_quant_linear_rows_workspace(int64_t rows, int64_t in_f, int64_t out_f, int64_t groups);
 int kt_hip_quant_linear_rows(int dev, const int32_t* x_dev, const int32_t* xidx_dev, int64_t x_rows, int64_t rows,
                              int64_t in_f, const kt_hip_qscale* xs_dev, int xs_step, int64_t groups,
                              const int64_t* off_host, const int64_t* off_dev, const int8_t* w_planes_dev,
@@ -292,6 +295,14 @@ int kt_hip_ref_moe_route(int dev, const int32_t* logits_dev, int64_t tokens, int
                          const kt_hip_qscale* ls_dev, int sigmoid, int norm_topk, const int64_t* codes_dev,
                          const kt_hip_codelut* lut, const int64_t* bias_dev, int32_t* sel_dev, int64_t* ec_dev,
                          int64_t* sumc_dev, void* stream);
+/* MoeMlp's bucket (layers.rs:928-937, forward_one_int's expert calls for every token) on the device: the tokens x
+ * top_k pairs of sel_dev (expert ids, as kt_hip_ref_moe_route writes them) grouped by expert for
+ * kt_hip_quant_linear_rows -- off_dev (experts + 1 offsets), xidx_dev (row -> token), pos_dev (pair t * top_k + i ->
+ * row, for kt_hip_ref_moe_combine). The order of the rows inside a group is not fixed (each row is computed on its
+ * own, so no result depends on it). A pair whose id is outside [0, experts) gets pos -1 and no row; the rows left
+ * over read as zeros (xidx -1). */
+int kt_hip_ref_moe_bucket(int dev, const int32_t* sel_dev, int64_t tokens, int top_k, int64_t experts,
+                          int64_t* off_dev, int32_t* xidx_dev, int32_t* pos_dev, void* stream);
 /* MoeMlp::combine (layers.rs:893-923) for each token: the top_k expert outputs at rows pos_dev[t * top_k + i] of
  * y_dev (y_rows rows of dim codes, records ys_dev; a row index outside them contributes nothing) brought to their
  * largest scale, summed with the numerators ec_dev, requantized, 1/sumc folded into the scale; zeros at Scale::ZERO

@@ -1154,6 +1154,48 @@ void kt_rm_set_bias(void* p, size_t e, float b) {
     kt_refmoe* M = (kt_refmoe*)p;
     M->bias[e] = (int64_t)round((double)b * (double)(1ULL << ROUTER_CODE_BITS));
 }
+/* The same MoeMlp with its QuantLinears given rather than drawn from seeded floats (MoeMlp::new over loaded
+ * weights, layers.rs:652-700): every matrix zero at scale zero until kt_rm_set_ql fills it, the selection bias zero
+ * until kt_rm_set_bias_code sets it, MoeMlp::new's and SigmoidScore::new's tables. For workloads at model size,
+ * where the seeded float draw of the reference tests would take minutes. */
+void* kt_rm_empty(size_t dim, size_t E, size_t top_k, size_t hidden, int norm_topk, int sigmoid,
+                  size_t shared_hidden) {
+    kt_refmoe* M = (kt_refmoe*)calloc(1, sizeof(kt_refmoe));
+    M->dim = dim, M->E = E, M->top_k = top_k, M->hidden = hidden, M->shared_hidden = shared_hidden;
+    M->norm_topk = norm_topk, M->sigmoid = sigmoid, M->has_shared = shared_hidden > 0;
+    const kt_scale z = ZERO;
+    M->router = (rd_ql){(int32_t*)calloc(E * dim, sizeof(int32_t)), z, E, dim};
+    M->experts = (rd_mlp*)calloc(E, sizeof(rd_mlp));
+    for (size_t e = 0; e <= E; e++) {
+        const size_t h = e < E ? hidden : shared_hidden;
+        if (e == E && !M->has_shared) break;
+        rd_mlp* m = e < E ? &M->experts[e] : &M->shared;
+        m->gate = (rd_ql){(int32_t*)calloc(h * dim, sizeof(int32_t)), z, h, dim};
+        m->up = (rd_ql){(int32_t*)calloc(h * dim, sizeof(int32_t)), z, h, dim};
+        m->down = (rd_ql){(int32_t*)calloc(dim * h, sizeof(int32_t)), z, dim, h};
+    }
+    M->bias = (int64_t*)calloc(E, sizeof(int64_t));
+    lut_build2(&M->exp_code, LUT_EXP, -30.0, 0.0, 16, ROUTER_CODE_BITS, 0);
+    lut_build2(&M->sig, LUT_SIGMOID, -16.0, 16.0, 16, ROUTER_CODE_BITS, 0);
+    lut_build2(&M->silu, LUT_SILU, -30.0, 30.0, 16, 20, 1);
+    return M;
+}
+/* Fill one QuantLinear (which as kt_rm_get_ql: 0 router; 1 gate, 2 up, 3 down of expert e, e == E the shared
+ * expert) with out x in codes at scale s. */
+void kt_rm_set_ql(void* p, size_t e, int which, const int32_t* codes, kt_scale s) {
+    kt_refmoe* M = (kt_refmoe*)p;
+    rd_ql* q;
+    if (which == 0) {
+        q = &M->router;
+    } else {
+        rd_mlp* m = e < M->E ? &M->experts[e] : &M->shared;
+        q = which == 1 ? &m->gate : which == 2 ? &m->up : &m->down;
+    }
+    memcpy(q->w, codes, q->out * q->in * sizeof(int32_t));
+    q->s = s;
+}
+/* The sigmoid router's coded selection bias of expert e, as SigmoidScore holds it (round(b * 2^20)). */
+void kt_rm_set_bias_code(void* p, size_t e, int64_t code) { ((kt_refmoe*)p)->bias[e] = code; }
 /* SigmoidScore::codes (router.rs:61-63): n logits codes at scale ls -> sigma codes. */
 void kt_rm_sigmoid_codes(const void* p, const int32_t* logits, size_t n, kt_scale ls, int64_t* out) {
     const kt_refmoe* M = (const kt_refmoe*)p;

@@ -161,6 +161,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_rm_get_bias": (None, [_P, _P]),
         "kt_rm_probe": (Scale, [C.POINTER(C.c_uint64), _SZ, _P]),
         "kt_rm_set_bias": (None, [_P, _SZ, C.c_float]),
+        "kt_rm_empty": (_P, [_SZ, _SZ, _SZ, _SZ, C.c_int, C.c_int, _SZ]),
+        "kt_rm_set_ql": (None, [_P, _SZ, C.c_int, _P, Scale]),
+        "kt_rm_set_bias_code": (None, [_P, _SZ, C.c_int64]),
         "kt_rm_sigmoid_codes": (None, [_P, _P, _SZ, Scale, _P]),
         "kt_rc_from_reals": (Scale, [_P, _SZ, C.c_int64, _P]),
         "kt_rc_quant_weights": (Scale, [_P, _SZ, _P]),
@@ -947,6 +950,36 @@ class RefMoe:
             self.ptr = lib().kt_rm_synthetic(seed, dim, E, top_k, hidden, int(norm_topk), 1, bias_seed, shared_hidden)
             for e in range(E):
                 lib().kt_rm_set_bias(self.ptr, e, 0.0)
+
+    @classmethod
+    def from_weights(cls, dim: int, router, experts, top_k: int, norm_topk: bool, bias_codes=None, shared=None):
+        """The same MoeMlp over given QuantLinears (kt_rm_empty / kt_rm_set_ql): router (codes E x dim, (mant,
+        shift)); experts one dict per expert of gate, up, down; bias_codes None for the softmax router, else the
+        sigmoid router's E coded biases; shared None or a dict like an expert's."""
+        m = cls.__new__(cls)
+        E = len(experts)
+        hidden = int(np.asarray(experts[0]["gate"][0]).shape[0])
+        sh = int(np.asarray(shared["gate"][0]).shape[0]) if shared is not None else 0
+        m.dim, m.E, m.top_k, m.hidden, m.shared_hidden = dim, E, top_k, hidden, sh
+        m.norm_topk, m.sigmoid = bool(norm_topk), (0 if bias_codes is None else 1)
+        m.ptr = lib().kt_rm_empty(dim, E, top_k, hidden, int(norm_topk), m.sigmoid, sh)
+        idx = {"gate": 1, "up": 2, "down": 3}
+
+        def put(e, which, q):
+            codes = _c(np.asarray(q[0]).reshape(-1), np.int32)
+            lib().kt_rm_set_ql(m.ptr, e, which, _ptr(codes), _sc(q[1]))
+
+        put(0, 0, router)
+        for e, ex in enumerate(experts):
+            for n, w in idx.items():
+                put(e, w, ex[n])
+        if shared is not None:
+            for n, w in idx.items():
+                put(E, w, shared[n])
+        if bias_codes is not None:
+            for e, c in enumerate(np.asarray(bias_codes, np.int64)):
+                lib().kt_rm_set_bias_code(m.ptr, e, int(c))
+        return m
 
     def __del__(self):
         if getattr(self, "ptr", None):

@@ -62,7 +62,7 @@ def test_quant_linear_rows_grouped(torch_dev):
     planes = torch.empty(G * gbytes, dtype=torch.int8, device="cuda")
     for g in range(G):
         T.pack_planes(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
-    n = B.quant_linear_rows_workspace(P, inp, out)
+    n = B.quant_linear_rows_workspace(P, inp, out, G)
     wsb = torch.empty(n, dtype=torch.uint8, device="cuda")
     y = torch.empty(P * out, dtype=torch.int32, device="cuda")
     ys = torch.zeros(P * 4, dtype=torch.int64, device="cuda")
@@ -77,6 +77,110 @@ def test_quant_linear_rows_grouped(torch_dev):
         yo, so, _, _ = O.quant_linear_forward(xr, 1, inp, xs[r], w[g].reshape(-1), out, ws[g])
         assert np.array_equal(got[r], yo.reshape(-1)), r
         assert got_s[r] == so, r
+
+
+def rows_ql_case(torch, rng, counts, inp, out, pw, wmax, x_rows=9, off_dev_override=None, host_off=True):
+    """quant_linear_rows over groups of the given row counts against per-row oracle forward_int calls; returns
+    (got codes, got records, want codes, want records)."""
+    import tritify_amd as T
+    from tritify_amd import backend as B
+
+    G = len(counts)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    P = int(off[-1])
+    x = rng.integers(-(2**28), 2**28, size=(x_rows, inp)).astype(np.int32)
+    xidx = rng.integers(0, x_rows, size=P).astype(np.int32)
+    xs = [(int(rng.integers(2**30, 2**31)), int(rng.integers(50, 60))) for _ in range(P)]
+    ws = [(int(rng.integers(2**30, 2**31)), int(rng.integers(40, 50))) for _ in range(G)]
+    w = rng.integers(-wmax, wmax + 1, size=(G, out, inp)).astype(np.int32)
+    kp = T.kp(inp)
+    gbytes = pw * out * kp
+    planes = torch.empty(G * gbytes, dtype=torch.int8, device="cuda")
+    for g in range(G):
+        T.pack_planes(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
+    n = B.quant_linear_rows_workspace(P, inp, out, G)
+    wsb = torch.empty(n, dtype=torch.uint8, device="cuda")
+    y = torch.empty(P * out, dtype=torch.int32, device="cuda")
+    ys = torch.empty(P * 4, dtype=torch.int64, device="cuda")
+    off_dev = torch.from_numpy(off if off_dev_override is None else off_dev_override).cuda()
+    B.quant_linear_rows(i32(torch, x), i32(torch, xidx), x_rows, P, inp, recs(torch, xs), 1,
+                        off if host_off else None, off_dev, planes, gbytes, pw, out,
+                        torch.from_numpy(np.array([a for a, _ in ws], np.int64)).cuda(),
+                        torch.from_numpy(np.array([b for _, b in ws], np.int32)).cuda(), wsb, n, y, ys, groups=G)
+    got, got_s = y.cpu().numpy().reshape(P, out), read_recs(ys, P)
+    want, want_s = np.zeros((P, out), np.int32), []
+    for r in range(P):
+        g = int(np.searchsorted(off, r, side="right") - 1)
+        yo, so, _, _ = O.quant_linear_forward(x[xidx[r]], 1, inp, xs[r], w[g].reshape(-1), out, ws[g])
+        want[r] = yo.reshape(-1)
+        want_s.append(so)
+    return got, got_s, want, want_s
+
+
+@pytest.mark.parametrize("pw,wmax", [(1, 127), (3, WL), (5, 2**30)])
+def test_quant_linear_rows_every_group_size(torch_dev, pw, wmax):
+    """Groups of every size the grouped products treat apart -- empty, 1 row (the one-row skinny list), 2-4 rows
+    (the few-row list), 5-32 rows (one MFMA tile), several tiles with a ragged last one -- over 1, 3 and 5 weight
+    planes, offsets on the device only: each row bit-exact against its own forward_int."""
+    counts = [0, 1, 2, 3, 4, 5, 31, 0, 32, 33, 70, 1]
+    say(f"case: quant_linear_rows every group size pw={pw}")
+    got, got_s, want, want_s = rows_ql_case(torch_dev, np.random.default_rng(pw), counts, 200, 150, pw, wmax,
+                                            host_off=False)
+    assert np.array_equal(got, want), f"rows differ: {np.unique(np.argwhere(got != want)[:, 0]).tolist()[:10]}"
+    assert got_s == want_s
+
+
+def test_quant_linear_rows_long_k_and_wide_out(torch_dev):
+    """K = 2100 (33 k-steps, kp padded) and 300 outputs (three 128-column tiles, the last ragged), groups of 1, 3, 9
+    and 40 rows."""
+    say("case: quant_linear_rows in=2100 out=300")
+    got, got_s, want, want_s = rows_ql_case(torch_dev, np.random.default_rng(11), [1, 3, 9, 40], 2100, 300, 3, WL)
+    assert np.array_equal(got, want) and got_s == want_s
+
+
+def test_quant_linear_rows_clamps_device_offsets(torch_dev):
+    """Offsets on the device that fall back or overshoot are taken as their running maximum clamped to [0, rows]
+    (a valid split, no access outside the buffers): the rows then follow that split's groups."""
+    torch = torch_dev
+    say("case: quant_linear_rows clamped offsets")
+    counts = [4, 6, 3, 7]  # the split the clamped offsets describe
+    bad = np.array([0, 4, 2, 10, 99], np.int64)  # falls back at 2, overshoots rows (20) at the end
+    # running max clamped: [0, 4, 4, 10, 20] -> groups of 4, 0, 6, 10 rows; the wanted rows use that split
+    got, got_s, _, _ = rows_ql_case(torch, np.random.default_rng(3), counts, 96, 40, 3, WL, off_dev_override=bad,
+                                    host_off=False)
+    want, want_s, _, _ = rows_ql_case(torch, np.random.default_rng(3), counts, 96, 40, 3, WL,
+                                      off_dev_override=np.array([0, 4, 4, 10, 20], np.int64), host_off=False)
+    assert np.array_equal(got, want) and got_s == want_s
+
+
+def test_bucket_groups_the_pairs_by_expert(torch_dev):
+    """kt_hip_ref_moe_bucket: the offsets are the experts' pair counts summed; every pair's row lies in its expert's
+    group and points back at its token; the rows are a permutation; an id outside [0, E) gets no row."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    rng = np.random.default_rng(21)
+    for T_, K, E in ((1, 8, 128), (37, 4, 16), (300, 8, 128), (5, 2, 3000)):
+        say(f"case: bucket T={T_} k={K} E={E}")
+        sel = np.stack([rng.choice(E, K, replace=False) for _ in range(T_)]).astype(np.int32).reshape(-1)
+        P = T_ * K
+        off = torch.empty(E + 1, dtype=torch.int64, device="cuda")
+        xidx = torch.empty(P, dtype=torch.int32, device="cuda")
+        pos = torch.empty(P, dtype=torch.int32, device="cuda")
+        B.ref_moe_bucket(i32(torch, sel), T_, K, E, off, xidx, pos)
+        o, xi, po = off.cpu().numpy(), xidx.cpu().numpy(), pos.cpu().numpy()
+        assert np.array_equal(o, np.concatenate([[0], np.cumsum(np.bincount(sel, minlength=E))]))
+        assert np.array_equal(np.sort(po), np.arange(P))
+        for p in range(P):
+            assert o[sel[p]] <= po[p] < o[sel[p] + 1] and xi[po[p]] == p // K
+    sel = np.array([0, 5, 1, -1, 2, 9], np.int32)  # E = 3: ids 5, -1, 9 get no row
+    off = torch.empty(4, dtype=torch.int64, device="cuda")
+    xidx = torch.empty(6, dtype=torch.int32, device="cuda")
+    pos = torch.empty(6, dtype=torch.int32, device="cuda")
+    B.ref_moe_bucket(i32(torch, sel), 3, 2, 3, off, xidx, pos)
+    o, xi, po = off.cpu().numpy(), xidx.cpu().numpy(), pos.cpu().numpy()
+    assert o.tolist() == [0, 1, 2, 3] and po[1] == po[3] == po[5] == -1 and (xi[3:] == -1).all()
+    assert [xi[po[p]] for p in (0, 2, 4)] == [0, 1, 2]
 
 
 def layer_from(m: O.RefMoe, dev_sigmoid: bool):

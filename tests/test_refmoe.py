@@ -184,3 +184,27 @@ def test_combine_and_merge_closed_forms():
     assert not out.reshape(3, 40)[1].any()
     for t in (0, 2):
         assert np.abs(got[t] - dq(rows[t], rs[t])).max() <= os_[0] * 2.0 ** -os_[1]
+
+
+@pytest.mark.parametrize("sig", [0, 1])
+def test_a_layer_built_from_given_weights_equals_the_seeded_one(sig):
+    """RefMoe.from_weights (kt_rm_empty / kt_rm_set_ql / kt_rm_set_bias_code) over the QuantLinears and coded bias of
+    a seeded layer routes and forwards exactly as that layer does, shared expert included; a layer built from the
+    same weights with one expert's scale changed does not."""
+    m = O.RefMoe(0x5C, 32, 16, 4, 24, True, sig, 0x5C, 40)
+    experts = [{n: m.ql(e, n) for n in ("gate", "up", "down")} for e in range(16)]
+    shared = {n: m.ql(16, n) for n in ("gate", "up", "down")}
+    g = O.RefMoe.from_weights(32, m.ql(0, "router"), experts, 4, True, m.bias() if sig else None, shared)
+    x, xs, _ = O.rm_probe(0x5E, 7 * 32)
+    for t in range(7):
+        (gs_, ge, gc, gl, gls), (ms_, me, mc, ml, mls) = g.route(x[t * 32:(t + 1) * 32], xs), \
+            m.route(x[t * 32:(t + 1) * 32], xs)
+        assert gs_ == ms_ and np.array_equal(ge, me) and gc == mc and np.array_equal(gl, ml) and gls == mls
+    want, ws = m.forward(x, 7, xs)
+    got, gs = g.forward(x, 7, xs)
+    assert np.array_equal(got, want) and gs == ws
+    sel = m.route(x[:32], xs)[0]
+    codes, (mant, shift) = experts[sel[0]]["down"]
+    experts[sel[0]]["down"] = (codes, (mant, shift + 1))
+    h = O.RefMoe.from_weights(32, m.ql(0, "router"), experts, 4, True, m.bias() if sig else None, shared)
+    assert not np.array_equal(h.forward(x, 7, xs)[0], want)

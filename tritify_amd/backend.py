@@ -134,11 +134,12 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_conv2d_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64]),
         "kt_hip_ref_conv2d": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64,
                                    C.c_int32, _P, _I64, C.c_int32, _P, _SZ, _P, _P, _P]),
-        "kt_hip_quant_linear_rows_workspace": (_SZ, [_I64, _I64, _I64]),
+        "kt_hip_quant_linear_rows_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
         "kt_hip_quant_linear_rows": (_I, [_I, _P, _P, _I64, _I64, _I64, _P, _I, _I64, _P, _P, _P, _SZ, _I, _I64, _P,
                                           _P, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_moe_route": (_I, [_I, _P, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
         "kt_hip_ref_moe_combine": (_I, [_I, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I, _P, _P, _P]),
+        "kt_hip_ref_moe_bucket": (_I, [_I, _P, _I64, _I, _I64, _P, _P, _P, _P]),
         "kt_hip_ref_merge_rows_workspace": (_SZ, [_I64]),
         "kt_hip_ref_merge_rows": (_I, [_I, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_attention_step": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
@@ -744,19 +745,34 @@ def ref_argmax(logits_dev, n: int, ls_dev, token_dev, record_dev=None, rscale_de
 REF_MOE_MAX_K = 32
 
 
-def quant_linear_rows_workspace(rows: int, in_f: int, out_f: int) -> int:
-    return lib().kt_hip_quant_linear_rows_workspace(rows, in_f, out_f)
+def quant_linear_rows_workspace(rows: int, in_f: int, out_f: int, groups: int) -> int:
+    return lib().kt_hip_quant_linear_rows_workspace(rows, in_f, out_f, groups)
 
 
 def quant_linear_rows(x_dev, xidx_dev, x_rows: int, rows: int, in_f: int, xs_dev, xs_step: int, off_host, off_dev,
                       w_planes_dev, w_group_bytes: int, pw: int, out_f: int, w_mant_dev, w_shift_dev, ws_dev,
-                      ws_bytes: int, y_dev, ys_dev, stream=None, dev: int = 0) -> None:
-    """QuantLinear::forward_int on each row on its own, rows grouped by weights (off: groups + 1 offsets)."""
-    off = np.ascontiguousarray(off_host, dtype=np.int64)
+                      ws_bytes: int, y_dev, ys_dev, stream=None, dev: int = 0, groups: int | None = None) -> None:
+    """QuantLinear::forward_int on each row on its own, rows grouped by weights (off_dev: groups + 1 offsets on the
+    device; off_host: None, or the same offsets on the host, checked; groups is then taken from them)."""
+    if off_host is not None:
+        off = np.ascontiguousarray(off_host, dtype=np.int64)
+        groups, off_ptr = off.size - 1, off.ctypes.data
+    else:
+        off, off_ptr = None, None
+        if groups is None:
+            raise ValueError("quant_linear_rows: groups is needed without off_host")
     check(lib().kt_hip_quant_linear_rows(dev, _ptr(x_dev), _ptr(xidx_dev), x_rows, rows, in_f, _ptr(xs_dev), xs_step,
-                                         off.size - 1, off.ctypes.data, _ptr(off_dev), _ptr(w_planes_dev),
-                                         w_group_bytes, pw, out_f, _ptr(w_mant_dev), _ptr(w_shift_dev), _ptr(ws_dev),
-                                         ws_bytes, _ptr(y_dev), _ptr(ys_dev), _stream(stream)), "quant linear rows")
+                                         groups, off_ptr, _ptr(off_dev), _ptr(w_planes_dev), w_group_bytes, pw, out_f,
+                                         _ptr(w_mant_dev), _ptr(w_shift_dev), _ptr(ws_dev), ws_bytes, _ptr(y_dev),
+                                         _ptr(ys_dev), _stream(stream)), "quant linear rows")
+
+
+def ref_moe_bucket(sel_dev, tokens: int, top_k: int, experts: int, off_dev, xidx_dev, pos_dev, stream=None,
+                   dev: int = 0) -> None:
+    """MoeMlp's bucket on the device: sel (tokens x top_k expert ids) -> off (experts + 1), xidx (row -> token), pos
+    (pair -> row)."""
+    check(lib().kt_hip_ref_moe_bucket(dev, _ptr(sel_dev), tokens, top_k, experts, _ptr(off_dev), _ptr(xidx_dev),
+                                      _ptr(pos_dev), _stream(stream)), "ref moe bucket")
 
 
 def ref_moe_route(logits_dev, tokens: int, experts: int, top_k: int, ls_dev, sigmoid: bool, norm_topk: bool,

@@ -112,12 +112,14 @@ hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int
                             kt_hip_qscale* hs, hipStream_t s);
 hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, const int64_t* codes,
                           const kt_hip_codelut* lut, int32_t* y, kt_hip_qscale* ys, hipStream_t s);
-size_t rq_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[3]);
+size_t rq_workspace_bytes(int64_t rows, int64_t in, int64_t out, int64_t groups, size_t off[5]);
 hipError_t launch_quant_linear_rows(const int32_t* x, const int32_t* xidx, int64_t x_rows, int64_t rows, int64_t in,
-                                    const kt_hip_qscale* xs, int xs_step, int groups, const int64_t* off_host,
-                                    const int64_t* off_dev, const int8_t* wb, size_t wgroup, int pw, int64_t out,
-                                    const int64_t* wm_dev, const int32_t* wsh_dev, int64_t flush_k, void* ws,
-                                    int32_t* y, kt_hip_qscale* ys, hipStream_t s);
+                                    const kt_hip_qscale* xs, int xs_step, int groups, const int64_t* off_dev,
+                                    const int8_t* wb, size_t wgroup, int pw, int64_t out, const int64_t* wm_dev,
+                                    const int32_t* wsh_dev, int64_t flush_k, void* ws, int32_t* y, kt_hip_qscale* ys,
+                                    hipStream_t s);
+hipError_t launch_rm_bucket(const int32_t* sel, int P, int top_k, int E, int64_t* off, int32_t* xidx, int32_t* pos,
+                            hipStream_t s);
 hipError_t launch_rm_route(const int32_t* logits, int T, int E, int top_k, const kt_hip_qscale* ls, int sigmoid,
                            int norm_topk, const int64_t* codes, const kt_hip_codelut* lut, const int64_t* bias,
                            int32_t* sel, int64_t* ec, int64_t* sumc, hipStream_t s);

@@ -8,7 +8,7 @@ groups only the exact integer products:
 
   router                   kt_hip_quant_linear_rows (one group: every token row quantized on its own)
   route / route_sigmoid    kt_hip_ref_moe_route     (exp or sigmoid CodeLut numerators, top-k, sumc)
-  bucket                   on the host: the (token, expert) rows ordered by expert, as one group per expert
+  bucket                   kt_hip_ref_moe_bucket    (the (token, expert) rows ordered by expert, on the device)
   experts gate / up        kt_hip_quant_linear_rows (E groups; x rows by index)
   SiLU * up                kt_hip_ref_swiglu        (one row per (token, expert))
   experts down             kt_hip_quant_linear_rows (E groups; per-row input scales)
@@ -16,6 +16,9 @@ groups only the exact integer products:
   merge_rows               kt_hip_ref_merge_rows    (a sequence: the tokens at one scale)
   shared expert + add      kt_hip_quant_linear, kt_hip_ref_swiglu_seq, kt_hip_ref_add_seq (the whole tensor, many
                            CTAs)
+
+Nothing waits on the host: the group sizes stay on the device (the grouped products plan their tiles there), so a
+forward is one stream of launches.
 
 torch holds the device buffers; it computes nothing.
 """
@@ -69,6 +72,7 @@ class RefMoeLayer:
                 for n in ("gate", "up", "down")}
             self.shared_hidden = sh_hidden
         self._i32 = i32
+        self._route_off = {}  # T -> the router's one-group offsets [0, T] on the device
 
     def _pack_groups(self, mats):
         """Digit planes of each (codes out x in, scale) in one buffer (all at the largest plane count), with the
@@ -88,23 +92,24 @@ class RefMoeLayer:
         torch.cuda.synchronize(self.device)
         return {"planes": planes, "gbytes": gbytes, "pw": pw, "out": out, "in": inp, "mant": mant, "shift": shift}
 
-    def _rows_ql(self, w, x, xidx, x_rows: int, rows: int, xs, xs_step: int, off, off_dev, stream):
+    def _rows_ql(self, w, x, xidx, x_rows: int, rows: int, xs, xs_step: int, off_dev, groups: int, stream):
         torch = self.torch
-        n = B.quant_linear_rows_workspace(rows, w["in"], w["out"])
+        n = B.quant_linear_rows_workspace(rows, w["in"], w["out"], groups)
         ws = torch.empty(n, dtype=torch.uint8, device=self.device)
         y = torch.empty(rows * w["out"], dtype=torch.int32, device=self.device)
-        ys = torch.zeros(rows * 4, dtype=torch.int64, device=self.device)
-        B.quant_linear_rows(x, xidx, x_rows, rows, w["in"], xs, xs_step, off, off_dev, w["planes"], w["gbytes"],
-                            w["pw"], w["out"], w["mant"], w["shift"], ws, n, y, ys, stream=stream, dev=self.dev)
+        ys = torch.empty(rows * 4, dtype=torch.int64, device=self.device)  # every row's record is written
+        B.quant_linear_rows(x, xidx, x_rows, rows, w["in"], xs, xs_step, None, off_dev, w["planes"], w["gbytes"],
+                            w["pw"], w["out"], w["mant"], w["shift"], ws, n, y, ys, stream=stream, dev=self.dev,
+                            groups=groups)
         return y, ys
 
     def route(self, x_dev, xs_rec, T: int, stream=None):
         """MoeMlp::route of every token row: (sel T x k int32, ec T x k int64, sumc T int64, logits, logit records),
         device tensors."""
         torch = self.torch
-        off = np.array([0, T], np.int64)
-        logits, ls = self._rows_ql(self.router, x_dev, None, T, T, xs_rec, 0, off,
-                                   torch.from_numpy(off).to(self.device), stream)
+        if T not in self._route_off:
+            self._route_off[T] = torch.tensor([0, T], dtype=torch.int64, device=self.device)
+        logits, ls = self._rows_ql(self.router, x_dev, None, T, T, xs_rec, 0, self._route_off[T], 1, stream)
         sel = torch.empty(T * self.top_k, dtype=torch.int32, device=self.device)
         ec = torch.empty(T * self.top_k, dtype=torch.int64, device=self.device)
         sumc = torch.empty(T, dtype=torch.int64, device=self.device)
@@ -112,32 +117,31 @@ class RefMoeLayer:
                         self.route_lut, self.bias, sel, ec, sumc, stream=stream, dev=self.dev)
         return sel, ec, sumc, logits, ls
 
+    def bucket(self, sel, T: int, stream=None):
+        """The (token, expert) rows grouped by expert, on the device: (off E + 1 int64, xidx P int32 row -> token,
+        pos P int32 pair -> row)."""
+        torch = self.torch
+        P = T * self.top_k
+        off = torch.empty(self.E + 1, dtype=torch.int64, device=self.device)
+        xidx = torch.empty(P, dtype=torch.int32, device=self.device)
+        pos = torch.empty(P, dtype=torch.int32, device=self.device)
+        B.ref_moe_bucket(sel, T, self.top_k, self.E, off, xidx, pos, stream=stream, dev=self.dev)
+        return off, xidx, pos
+
     def forward(self, x_dev, xs_rec, T: int, stream=None):
         """MoeMlp::forward_int (layers.rs:1031-1034) of T token rows (x_dev: T x dim i32 codes at the record
-        xs_rec): (out T x dim codes, its record), device tensors. Synchronizes once, to bucket the routed rows."""
+        xs_rec): (out T x dim codes, its record), device tensors. Asynchronous on `stream`."""
         torch = self.torch
         dim, K, E = self.dim, self.top_k, self.E
         sel, ec, sumc, _, _ = self.route(x_dev, xs_rec, T, stream)
-        torch.cuda.synchronize(self.device)
-        s = sel.cpu().numpy().reshape(T, K)
-        # bucket: the (token, expert) rows in expert order, tokens ascending within an expert
-        order = sorted(((int(s[t, i]), t, i) for t in range(T) for i in range(K)))
         P = T * K
-        xidx = np.empty(P, np.int32)
-        pos = np.empty(P, np.int32)
-        counts = np.zeros(E, np.int64)
-        for r, (e, t, i) in enumerate(order):
-            xidx[r], pos[t * K + i] = t, r
-            counts[e] += 1
-        off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
-        off_d = torch.from_numpy(off).to(self.device)
-        xidx_d, pos_d = self._i32(xidx), self._i32(pos)
-        g, gs = self._rows_ql(self.w["gate"], x_dev, xidx_d, T, P, xs_rec, 0, off, off_d, stream)
-        u, us = self._rows_ql(self.w["up"], x_dev, xidx_d, T, P, xs_rec, 0, off, off_d, stream)
+        off_d, xidx_d, pos_d = self.bucket(sel, T, stream)
+        g, gs = self._rows_ql(self.w["gate"], x_dev, xidx_d, T, P, xs_rec, 0, off_d, E, stream)
+        u, us = self._rows_ql(self.w["up"], x_dev, xidx_d, T, P, xs_rec, 0, off_d, E, stream)
         h = torch.empty(P * self.hidden, dtype=torch.int32, device=self.device)
         hs = torch.zeros(P * 4, dtype=torch.int64, device=self.device)
         B.ref_swiglu(g, gs, u, us, self.hidden, self.silu_codes, self.silu_lut, h, hs, stream, self.dev, rows=P)
-        y, ys = self._rows_ql(self.w["down"], h, None, P, P, hs, 1, off, off_d, stream)
+        y, ys = self._rows_ql(self.w["down"], h, None, P, P, hs, 1, off_d, E, stream)
         rows = torch.empty(T * dim, dtype=torch.int32, device=self.device)
         rs = torch.zeros(T * 4, dtype=torch.int64, device=self.device)
         B.ref_moe_combine(y, ys, P, dim, pos_d, ec, sumc, T, K, rows, rs, stream=stream, dev=self.dev)
