@@ -897,7 +897,10 @@ REF_MOE_T = (1, 256)
 
 def ref_moe_weights(cfg: dict, seed: int):
     """(router, experts, coded bias, shared) of a REF_GLM layer: every code uniform in +-WLEVELS at the Scale
-    from_weights gives floats of peak 1 (1 / WLEVELS), the coded bias uniform in +-0.05 * 2^20; drawn on threads."""
+    from_weights gives floats of peak 1 (1 / WLEVELS), the router's of peak 0.1 (its logits then spread with a
+    standard deviation near 2, so the sigmoid does not saturate and the tokens spread over about 122 of the 128
+    experts; at peak 1 most scores tie at the top code and the bias alone picks the same few experts), the coded
+    bias uniform in +-0.05 * 2^20; drawn on threads."""
     import tritify_amd as T
     from concurrent.futures import ThreadPoolExecutor
     from tritify_amd import backend as B
@@ -912,7 +915,7 @@ def ref_moe_weights(cfg: dict, seed: int):
     names = ("gate", "up", "down")
     experts = [{n: (mats[1 + 3 * e + j], sc) for j, n in enumerate(names)} for e in range(E + 1)]
     bias = T.gen_uniform_fast(seed - 1, -52429, 52429, E).astype(np.int64)
-    return (mats[0], sc), experts[:E], bias, experts[E]
+    return (mats[0], B.ref_scale_from_f64(0.1 / WL)), experts[:E], bias, experts[E]
 
 
 def bench_ref_moe(torch, args) -> dict:
@@ -945,6 +948,8 @@ def bench_ref_moe(torch, args) -> dict:
         x, xs = B.ref_from_reals(rng.uniform(-1.0, 1.0, T_ * cfg["dim"]))
         xd, xr = torch.from_numpy(x).to(dev), T.qscale_record(*xs)
         out, orec = layer.forward(xd, xr, T_)
+        off = layer.bucket(layer.route(xd, xr, T_)[0], T_)[0].cpu().numpy()
+        cnt = np.diff(off)
         c0 = time.perf_counter()
         want, ws = model.forward(x, T_, xs)
         cpu_s = time.perf_counter() - c0
@@ -953,8 +958,20 @@ def bench_ref_moe(torch, args) -> dict:
             raise SystemExit(f"bench: ref moe T={T_}: differs from the CPU oracle")
         n = 200 if T_ == 1 else 20
         ms, _ = time_launches(torch, lambda i: layer.forward(xd, xr, T_, stream=stream), n, 5)
-        res[f"T{T_}"] = {"us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(T_ / (ms * 1e-3), 1)}
-        log(f"bench: ref moe T={T_}: {ms * 1e3:.1f} us per forward, bit-exact")
+        # the same forward as one HIP graph (no host work between its launches), its output checked too
+        g, gout, grec = layer.capture(xd, xr, T_)
+        g.replay()
+        torch.cuda.synchronize()
+        if not (np.array_equal(gout.cpu().numpy(), want) and
+                tuple(T.read_qscale(grec)[k] for k in ("mant", "shift")) == ws):
+            raise SystemExit(f"bench: ref moe T={T_}: the graph replay differs from the CPU oracle")
+        gms, _ = time_launches(torch, lambda i: g.replay(), n, 5)
+        del g, gout, grec
+        res[f"T{T_}"] = {"us_per_forward": round(ms * 1e3, 1), "tokens_per_s": round(T_ / (ms * 1e-3), 1),
+                         "graph_us_per_forward": round(gms * 1e3, 1),
+                         "graph_tokens_per_s": round(T_ / (gms * 1e-3), 1),
+                         "experts_used": int((cnt > 0).sum()), "max_rows_per_expert": int(cnt.max())}
+        log(f"bench: ref moe T={T_}: {ms * 1e3:.1f} us per forward ({gms * 1e3:.1f} us as a graph), bit-exact")
         if T_ == REF_MOE_T[-1]:
             res["cpu_baseline"] = {
                 "value": round(T_ / cpu_s, 1), "unit": "tokens/s", "cores": cores, "nproc": os.cpu_count(),

@@ -272,13 +272,22 @@ int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hi
  * r; an index outside [0, x_rows) reads as zeros) at the scale record xs_dev[xs_step * r] (xs_step 0: one record
  * for every row, 1: one per row), quantized by its own max |x|, requantized by its own max |acc|, against the weights
  * of the group g holding r (rows off[g] .. off[g + 1] - 1, off_dev the groups + 1 offsets on the device, off[0] = 0,
- * off[groups] = rows): pw digit planes of out_f x in_f codes at w_planes_dev + g * w_group_bytes
- * (kt_hip_pack_planes), Scale (w_mant_dev[g], w_shift_dev[g]). No bias. y_dev: rows x out_f codes, ys_dev: rows
+ * off[groups] = rows): pw digit planes of out_f x in_f codes at w_planes_dev + g * w_group_bytes, in the tiled
+ * layout of kt_hip_pack_planes_tiled (w_group_bytes at least kt_hip_pack_planes_tiled_bytes), Scale
+ * (w_mant_dev[g], w_shift_dev[g]). No bias. y_dev: rows x out_f codes, ys_dev: rows
  * records. ws_dev: the caller's workspace of kt_hip_quant_linear_rows_workspace bytes. The group sizes are read on
  * the device (no host round trip): off_host, the same offsets on the host, is optional and only checked (an invalid
  * copy is an error); offsets on the device that are not monotone or leave [0, rows] are clamped into a valid split
  * rather than read out of bounds. Layers at model size bucket their rows with kt_hip_ref_moe_bucket. */
 size_t kt_hip_quant_linear_rows_workspace(int64_t rows, int64_t in_f, int64_t out_f, int64_t groups);
+/* The weight layout of kt_hip_quant_linear_rows: the pw balanced base-256 digit planes of rows x k codes (the digits
+ * of kt_hip_pack_planes) stored by tile -- for each block of 128 rows, k in steps of 64 bytes, each step the planes'
+ * 128 x 64-byte blocks with the 16-byte chunks of row r permuted by (r / 4) % 4 (the order the product's LDS reads
+ * want) -- so that one output block's run of k is contiguous memory. Rows past `rows` and k past `k` are zero.
+ * kt_hip_pack_planes_tiled_bytes: the size (0 for an invalid shape). */
+size_t kt_hip_pack_planes_tiled_bytes(int64_t rows, int64_t k, int planes);
+int kt_hip_pack_planes_tiled(int dev, const int32_t* codes_dev, int64_t rows, int64_t k, int planes,
+                             int8_t* planes_dev, void* stream);
 int kt_hip_quant_linear_rows(int dev, const int32_t* x_dev, const int32_t* xidx_dev, int64_t x_rows, int64_t rows,
                              int64_t in_f, const kt_hip_qscale* xs_dev, int xs_step, int64_t groups,
                              const int64_t* off_host, const int64_t* off_dev, const int8_t* w_planes_dev,

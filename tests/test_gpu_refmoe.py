@@ -57,11 +57,10 @@ def test_quant_linear_rows_grouped(torch_dev):
     ws = [(int(rng.integers(2**30, 2**31)), int(rng.integers(40, 50))) for _ in range(G)]
     w = rng.integers(-WL, WL + 1, size=(G, out, inp)).astype(np.int32)
     pw = 3
-    kp = T.kp(inp)
-    gbytes = pw * out * kp
+    gbytes = B.pack_planes_tiled_bytes(out, inp, pw)
     planes = torch.empty(G * gbytes, dtype=torch.int8, device="cuda")
     for g in range(G):
-        T.pack_planes(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
+        B.pack_planes_tiled(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
     n = B.quant_linear_rows_workspace(P, inp, out, G)
     wsb = torch.empty(n, dtype=torch.uint8, device="cuda")
     y = torch.empty(P * out, dtype=torch.int32, device="cuda")
@@ -93,11 +92,10 @@ def rows_ql_case(torch, rng, counts, inp, out, pw, wmax, x_rows=9, off_dev_overr
     xs = [(int(rng.integers(2**30, 2**31)), int(rng.integers(50, 60))) for _ in range(P)]
     ws = [(int(rng.integers(2**30, 2**31)), int(rng.integers(40, 50))) for _ in range(G)]
     w = rng.integers(-wmax, wmax + 1, size=(G, out, inp)).astype(np.int32)
-    kp = T.kp(inp)
-    gbytes = pw * out * kp
+    gbytes = B.pack_planes_tiled_bytes(out, inp, pw)
     planes = torch.empty(G * gbytes, dtype=torch.int8, device="cuda")
     for g in range(G):
-        T.pack_planes(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
+        B.pack_planes_tiled(i32(torch, w[g]), out, inp, pw, planes[g * gbytes:])
     n = B.quant_linear_rows_workspace(P, inp, out, G)
     wsb = torch.empty(n, dtype=torch.uint8, device="cuda")
     y = torch.empty(P * out, dtype=torch.int32, device="cuda")
@@ -151,6 +149,36 @@ def test_quant_linear_rows_clamps_device_offsets(torch_dev):
     want, want_s, _, _ = rows_ql_case(torch, np.random.default_rng(3), counts, 96, 40, 3, WL,
                                       off_dev_override=np.array([0, 4, 4, 10, 20], np.int64), host_off=False)
     assert np.array_equal(got, want) and got_s == want_s
+
+
+@pytest.mark.parametrize("rows,k,pw", [(128, 64, 3), (200, 150, 1), (300, 1000, 5)])
+def test_tiled_planes_are_the_row_major_digits_rearranged(torch_dev, rows, k, pw):
+    """kt_hip_pack_planes_tiled holds kt_hip_pack_planes' digits: byte t of chunk position s of row r in plane q of
+    k-step kt of row block nb is digit q of code (128 nb + r, 64 kt + 16 (s ^ (r / 4) % 4) + t); rows and k past the
+    matrix are zero."""
+    torch = torch_dev
+    import tritify_amd as T
+    from tritify_amd import backend as B
+
+    rng = np.random.default_rng(rows + k)
+    lim = {1: 127, 3: WL, 5: 2**30}[pw]
+    w = rng.integers(-lim, lim + 1, size=(rows, k)).astype(np.int32)
+    kp = T.kp(k)
+    flat = torch.empty(pw * rows * kp, dtype=torch.int8, device="cuda")
+    T.pack_planes(i32(torch, w), rows, k, pw, flat)
+    tiled = torch.empty(B.pack_planes_tiled_bytes(rows, k, pw), dtype=torch.int8, device="cuda")
+    B.pack_planes_tiled(i32(torch, w), rows, k, pw, tiled)
+    rm = flat.cpu().numpy().reshape(pw, rows, kp)
+    nblk = (rows + 127) // 128
+    pad = np.zeros((pw, nblk * 128, kp), np.int8)
+    pad[:, :rows] = rm
+    # [q][nb][r][kt][c][t] -> [nb][kt][q][r][slot][t] with slot = c ^ swz(r)
+    v = pad.reshape(pw, nblk, 128, kp // 64, 4, 16)
+    swz = (np.arange(128) >> 2) & 3
+    slots = np.arange(4)[None, :] ^ swz[:, None]  # (r, slot) -> the chunk stored there
+    gathered = np.take_along_axis(v, slots[None, None, :, None, :, None], axis=4)
+    want = gathered.transpose(1, 3, 0, 2, 4, 5).reshape(-1)
+    assert np.array_equal(tiled.cpu().numpy(), want)
 
 
 def test_bucket_groups_the_pairs_by_expert(torch_dev):
@@ -221,6 +249,32 @@ def test_moe_layer_against_the_oracle(torch_dev, case):
     got = out.cpu().numpy()
     assert np.array_equal(got, want), f"codes differ at {np.argwhere(got != want)[:5].tolist()}"
     assert read_recs(orec, 1)[0] == ws
+
+
+def test_moe_layer_graph_replays_equal_eager(torch_dev):
+    """The whole layer captured as one HIP graph (no host round trip in forward): three replays, each after eager
+    work of the program's own on the same buffers and a synchronization, over two inputs, every replay bit-exact
+    against the eager forward and the oracle."""
+    torch = torch_dev
+    say("case: ref moe graph replays")
+    m = O.RefMoe(0x91, 256, 32, 4, 128, True, 1, 0x92, 192)
+    layer = layer_from(m, True)
+    T_ = 40
+    x0, xs0, _ = O.rm_probe(0x95, T_ * 256)
+    x1, xs1, _ = O.rm_probe(0x96, T_ * 256)
+    xd, xr = i32(torch, x0), recs(torch, [xs0])
+    layer.forward(xd, xr, T_)
+    g, gout, grec = layer.capture(xd, xr, T_)
+    for rep, (x, xs) in enumerate(((x1, xs1), (x0, xs0), (x1, xs1))):
+        xd.copy_(i32(torch, x))
+        xr.copy_(recs(torch, [xs]))
+        eager, erec = layer.forward(xd, xr, T_)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want, ws = m.forward(x, T_, xs)
+        assert np.array_equal(gout.cpu().numpy(), eager.cpu().numpy()), f"replay {rep} differs from eager"
+        assert np.array_equal(gout.cpu().numpy(), want) and read_recs(grec, 1)[0] == ws, f"replay {rep}"
 
 
 def test_combine_and_merge_against_the_oracle(torch_dev):

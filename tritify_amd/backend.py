@@ -140,6 +140,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_moe_route": (_I, [_I, _P, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
         "kt_hip_ref_moe_combine": (_I, [_I, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I, _P, _P, _P]),
         "kt_hip_ref_moe_bucket": (_I, [_I, _P, _I64, _I, _I64, _P, _P, _P, _P]),
+        "kt_hip_pack_planes_tiled_bytes": (_SZ, [_I64, _I64, _I]),
+        "kt_hip_pack_planes_tiled": (_I, [_I, _P, _I64, _I64, _I, _P, _P]),
         "kt_hip_ref_merge_rows_workspace": (_SZ, [_I64]),
         "kt_hip_ref_merge_rows": (_I, [_I, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_attention_step": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
@@ -765,6 +767,19 @@ def quant_linear_rows(x_dev, xidx_dev, x_rows: int, rows: int, in_f: int, xs_dev
                                          groups, off_ptr, _ptr(off_dev), _ptr(w_planes_dev), w_group_bytes, pw, out_f,
                                          _ptr(w_mant_dev), _ptr(w_shift_dev), _ptr(ws_dev), ws_bytes, _ptr(y_dev),
                                          _ptr(ys_dev), _stream(stream)), "quant linear rows")
+
+
+def pack_planes_tiled_bytes(rows: int, k: int, planes: int) -> int:
+    n = lib().kt_hip_pack_planes_tiled_bytes(rows, k, planes)
+    if n == 0:
+        raise ValueError("pack_planes_tiled: no layout for this shape")
+    return n
+
+
+def pack_planes_tiled(codes_dev, rows: int, k: int, planes: int, planes_dev, stream=None, dev: int = 0) -> None:
+    """The digit planes of rows x k codes in quant_linear_rows' tiled weight layout."""
+    check(lib().kt_hip_pack_planes_tiled(dev, _ptr(codes_dev), rows, k, planes, _ptr(planes_dev), _stream(stream)),
+          "pack planes tiled")
 
 
 def ref_moe_bucket(sel_dev, tokens: int, top_k: int, experts: int, off_dev, xidx_dev, pos_dev, stream=None,

@@ -85,28 +85,61 @@ __device__ inline int group_of(const int64_t* off, int groups, int64_t r) {
 
 }  // namespace
 
-// Row r: xmax of its input row, quant_to into 3 balanced base-256 planes laid out per group ([3][count_g][kp] at
-// off[g] * 3 * kp), and its record: c = from_ratio(xmax, WLEVELS) * xs * ws_g (QuantLinear::forward_int steps 1-4).
-__global__ __launch_bounds__(RQ_THREADS) void rq_quant_kernel(const int32_t* __restrict__ x,
-                                                              const int32_t* __restrict__ xidx, int64_t x_rows,
-                                                              int64_t in,
-                                                              int64_t kp, const kt_hip_qscale* __restrict__ xs,
-                                                              int xs_step, int groups, const int64_t* __restrict__ off,
-                                                              const int64_t* __restrict__ wm,
-                                                              const int32_t* __restrict__ wsh, RqState* __restrict__ st,
-                                                              int8_t* __restrict__ xa) {
-    __shared__ uint32_t red[RQ_THREADS / 64];
+// The per-row passes run one CTA of RQ_ROW_THREADS per row, each thread holding up to RQ_VPT of the row's values in
+// registers between the row's maximum and its use (one load per value, all of a thread's loads in flight together);
+// rows longer than RQ_ROW_THREADS * RQ_VPT take a second load per value.
+constexpr int RQ_ROW_THREADS = 1024, RQ_VPT = 8;
+// The grouped product's tiles: 32 rows x 128 output columns, k in steps of 64 bytes.
+constexpr int RQ_BM = 32, RQ_BN = 128, RQ_BK = 64;
+
+// The activation planes by tile: row j of group g sits in tile tb[g] + j / 32 at row j % 32; a tile is nkt
+// k-steps of [3 planes][32 rows x 64 bytes], each 32 x 64 block in the MFMA reads' swizzled LDS layout (chunk c of row
+// rr at rr * 64 + 16 (c ^ swz(rr))), so a k-step of a tile is 6 KB of contiguous bytes that DMA copies as they are.
+__device__ __forceinline__ int64_t rq_a_off(int64_t ti, int64_t nkt, int p, int rr, int64_t c) {
+    const int64_t kt = c >> 6, cc = (c >> 4) & 3;
+    return ((ti * nkt + kt) * 3 + p) * (RQ_BM * RQ_BK) + rr * 64 + ((cc ^ ((rr >> 2) & 3)) << 4) + (c & 15);
+}
+
+// Row r: xmax of its input row, quant_to into 3 balanced base-256 planes (tiled as rq_a_off), and its record:
+// c = from_ratio(xmax, WLEVELS) * xs * ws_g (QuantLinear::forward_int steps 1-4).
+__global__ __launch_bounds__(RQ_ROW_THREADS) void rq_quant_kernel(const int32_t* __restrict__ x,
+                                                                  const int32_t* __restrict__ xidx, int64_t x_rows,
+                                                                  int64_t in, int64_t kp,
+                                                                  const kt_hip_qscale* __restrict__ xs, int xs_step,
+                                                                  int groups, const int64_t* __restrict__ off,
+                                                                  const int32_t* __restrict__ tb, int64_t cap,
+                                                                  const int64_t* __restrict__ wm,
+                                                                  const int32_t* __restrict__ wsh,
+                                                                  RqState* __restrict__ st, int8_t* __restrict__ xa) {
+    __shared__ uint32_t red[RQ_ROW_THREADS / 64];
     const int64_t r = blockIdx.x;
     const int g = group_of(off, groups, r);
-    const int64_t cnt = off[g + 1] - off[g], j = r - off[g];
+    const int64_t j = r - off[g], ti = tb[g] + j / RQ_BM, nkt = kp / RQ_BK;
+    const int rr = (int)(j % RQ_BM);
     const int64_t xr = xidx ? (int64_t)xidx[r] : r;
     const bool inside = xr >= 0 && xr < x_rows;  // an index past x reads as a zero row (no access)
     const int32_t* src = x + (inside ? xr : 0) * in;
+    const bool held = in <= (int64_t)RQ_ROW_THREADS * RQ_VPT;
+    int32_t v[RQ_VPT];
     uint32_t m = 0;
-    for (int64_t i = threadIdx.x; inside && i < in; i += RQ_THREADS) {
-        const int32_t v = src[i];
-        const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
-        m = a > m ? a : m;
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ_VPT; i++) {  // branch-free: a slot past the row loads its last value, then drops it
+            const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
+            const int32_t t = src[c < in ? c : in - 1];
+            v[i] = inside && c < in ? t : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < RQ_VPT; i++) {
+            const uint32_t a = v[i] < 0 ? 0u - (uint32_t)v[i] : (uint32_t)v[i];
+            m = a > m ? a : m;
+        }
+    } else {
+        for (int64_t i = threadIdx.x; inside && i < in; i += RQ_ROW_THREADS) {
+            const int32_t t = src[i];
+            const uint32_t a = t < 0 ? 0u - (uint32_t)t : (uint32_t)t;
+            m = a > m ? a : m;
+        }
     }
     m = block_max_t(m, red);
     if (threadIdx.x == 0) {
@@ -122,39 +155,95 @@ __global__ __launch_bounds__(RQ_THREADS) void rq_quant_kernel(const int32_t* __r
         st[r] = s;
     }
     const int64_t xmax = (int64_t)m, half = xmax / 2;
-    int8_t* base = xa + off[g] * 3 * kp;
-    for (int64_t c = threadIdx.x; c < kp; c += RQ_THREADS) {
-        int64_t v = 0;
+    const bool tiled = ti < cap;  // always, by the table's capacity; a guard for the writes below
+    auto put = [&](int64_t c, int32_t xv) {  // quant_to (layers.rs:23-31) of one value, its 3 digits
+        if (!tiled) return;
+        int64_t q = 0;
         if (m != 0 && c < in) {
-            const int64_t num = (int64_t)src[c] * WLEVELS;  // quant_to (layers.rs:23-31)
+            const int64_t num = (int64_t)xv * WLEVELS;
             // (|num| + half) / xmax: |num| < 2^50 and the quotient at most WLEVELS, within udiv_small_q's range
-            const uint64_t q = udiv_small_q((u128)(uint64_t)(num < 0 ? -num : num) + (u128)(uint64_t)half, xmax);
-            v = num >= 0 ? (int64_t)q : -(int64_t)q;
+            const uint64_t u = udiv_small_q((u128)(uint64_t)(num < 0 ? -num : num) + (u128)(uint64_t)half, xmax);
+            q = num >= 0 ? (int64_t)u : -(int64_t)u;
         }
 #pragma unroll
         for (int p = 0; p < 3; p++) {
-            const int64_t d = ((v + 128) & 255) - 128;
-            base[(p * cnt + j) * kp + c] = (int8_t)d;
-            v = (v - d) >> 8;
+            const int64_t d = ((q + 128) & 255) - 128;
+            xa[rq_a_off(ti, nkt, p, rr, c)] = (int8_t)d;
+            q = (q - d) >> 8;
         }
+    };
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ_VPT; i++) {
+            const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
+            if (c < kp) put(c, v[i]);
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < kp; c += RQ_ROW_THREADS) put(c, inside && c < in ? src[c] : 0);
     }
 }
 
 // Row r: ymax = max |acc|, y = requant_dyn(acc, ACT_LEVELS, ymax), the scale from_ratio(ymax, ACT_LEVELS) * c
 // (QuantLinear::forward_int steps 8-10); zeros at Scale::ZERO for a zero input, a zero c or ymax = 0.
-__global__ __launch_bounds__(RQ_THREADS) void rq_requant_kernel(const int64_t* __restrict__ acc, int64_t out,
-                                                                const RqState* __restrict__ st,
-                                                                int32_t* __restrict__ y,
-                                                                kt_hip_qscale* __restrict__ ys) {
-    __shared__ int64_t red[RQ_THREADS / 64];
+// acc holds `splits` slices of rows x out partial sums (runs of k); the row's product is their sum modulo 2^64.
+__global__ __launch_bounds__(RQ_ROW_THREADS) void rq_requant_kernel(const int64_t* __restrict__ acc, int64_t rows,
+                                                                    int64_t out, int splits,
+                                                                    const RqState* __restrict__ st,
+                                                                    int32_t* __restrict__ y,
+                                                                    kt_hip_qscale* __restrict__ ys) {
+    __shared__ int64_t red[RQ_ROW_THREADS / 64];
     const int64_t r = blockIdx.x;
     const RqState s = st[r];
     const int64_t* a = acc + r * out;
+    const int64_t slice = rows * out;
+    auto sum = [&](int64_t c) {
+        uint64_t t = 0;
+        for (int q = 0; q < splits; q++) t += (uint64_t)a[q * slice + c];
+        return (int64_t)t;
+    };
+    const bool held = out <= (int64_t)RQ_ROW_THREADS * RQ_VPT;
+    int64_t v[RQ_VPT];
     int64_t m = 0;
-    if (s.mode == 0)
-        for (int64_t i = threadIdx.x; i < out; i += RQ_THREADS) m = iabs(a[i]) > m ? iabs(a[i]) : m;
+    if (held) {  // the slices 4 at a time, all of a thread's loads of them in flight together (branch-free)
+#pragma unroll
+        for (int i = 0; i < RQ_VPT; i++) v[i] = 0;
+        for (int q0 = 0; q0 < splits; q0 += 4) {
+            int64_t t[4][RQ_VPT];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int64_t qq = q0 + u < splits ? q0 + u : splits - 1;
+#pragma unroll
+                for (int i = 0; i < RQ_VPT; i++) {
+                    const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
+                    t[u][i] = a[qq * slice + (c < out ? c : out - 1)];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int i = 0; i < RQ_VPT; i++)
+                    v[i] = (int64_t)((uint64_t)v[i] + (q0 + u < splits ? (uint64_t)t[u][i] : 0));
+        }
+#pragma unroll
+        for (int i = 0; i < RQ_VPT; i++)
+            if (threadIdx.x + (int64_t)RQ_ROW_THREADS * i >= out) v[i] = 0;
+        if (s.mode == 0)
+#pragma unroll
+            for (int i = 0; i < RQ_VPT; i++) m = iabs(v[i]) > m ? iabs(v[i]) : m;
+    } else if (s.mode == 0) {
+        for (int64_t i = threadIdx.x; i < out; i += RQ_ROW_THREADS) m = iabs(sum(i)) > m ? iabs(sum(i)) : m;
+    }
     const int64_t ymax = block_max_t(m, red);
-    for (int64_t i = threadIdx.x; i < out; i += RQ_THREADS) y[r * out + i] = ymax ? requant_dyn_dev(a[i], ymax) : 0;
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RQ_VPT; i++) {
+            const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
+            if (c < out) y[r * out + c] = ymax ? requant_dyn_dev(v[i], ymax) : 0;
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < out; i += RQ_ROW_THREADS)
+            y[r * out + i] = ymax ? requant_dyn_dev(sum(i), ymax) : 0;
+    }
     if (threadIdx.x == 0) {
         kt_hip_qscale o{};
         o.xmax = s.xmax;
@@ -173,18 +262,22 @@ __global__ __launch_bounds__(RQ_THREADS) void rq_requant_kernel(const int64_t* _
 // [pw][N][kp]. acc row r = the i64 sum over the planes, sum_{p,q} 256^(p+q) x_p . w_q, modulo 2^64 (the int32
 // plane-group partials stay exact within the host's flush bound, as in the ungrouped product).
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int RQ_SK_CPW = 2;   // skinny: output columns per wave
-constexpr int RQ_SK_Y = 16;    // skinny: CTAs along the entry list (each strides it)
-constexpr int RQ_BM = 32, RQ_BN = 128;
+// The tile table's capacity: the 32-row tiles of the non-empty groups number sum ceil(c / 32) < rows / 32 + (the
+// non-empty groups) <= rows / 32 + min(groups, rows).
+int64_t rq_tile_cap(int64_t rows, int64_t groups) { return (groups < rows ? groups : rows) + rows / 32 + 1; }
 
-struct RqCaps {
-    int64_t one, few, tiles;  // table capacities: groups of 1 row, of 2-4 rows, 32-row tiles of larger groups
-};
-RqCaps rq_caps(int64_t rows, int64_t groups) {
-    const auto mn = [](int64_t a, int64_t b) { return a < b ? a : b; };
-    // each kind's entries are bounded by the rows they cover: n1 <= rows, 2 n4 <= rows, and the tiles of the groups
-    // of >= 5 rows number sum ceil(c / 32) < rows / 32 + (those groups) <= rows / 32 + rows / 5
-    return RqCaps{mn(groups, rows), mn(groups, rows / 2), mn(groups, rows / 5) + rows / 32 + 1};
+// The k split of the grouped product: S runs of k-tiles, each within the int32 flush bound of the plane-group sums
+// (flush_k bytes), enough CTAs for the chip when the tiles are few (decode: a handful of one-row groups), each run at
+// least 8 k-tiles long so the DMA ring fills; every run non-empty. The partial products land in S slices of acc.
+int rq_splits(int64_t rows, int64_t groups, int64_t out, int64_t kp, int64_t flush_k) {
+    const int64_t nkt = kp / RQ_BK, ftiles = flush_k / RQ_BK;
+    const int64_t smin = (nkt + ftiles - 1) / ftiles;
+    const int64_t ctas = ((out + RQ_BN - 1) / RQ_BN) * rq_tile_cap(rows, groups);
+    int64_t S = (1024 + ctas - 1) / ctas;
+    const int64_t smax = nkt / 8 > smin ? nkt / 8 : smin;
+    S = S < smin ? smin : (S > smax ? smax : S);
+    const int64_t per = (nkt + S - 1) / S;
+    return (int)((nkt + per - 1) / per);
 }
 
 template <typename T, typename Op>
@@ -211,230 +304,172 @@ __device__ T block_incl_scan(T v, T* sh, Op op, T& total) {
     return have ? op(pre, v) : v;
 }
 
-// The tables (one CTA of 1024 threads): off_s, then the group ids of the groups of exactly 1 row (e1) and of 2-4
-// rows (e4), and (group, first row) of every 32-row tile of the larger groups (em); hdr = {n1, n4, nm}.
+// The tile table (one CTA of 1024 threads): off_s, then (group, first row) of every 32-row tile of the non-empty
+// groups in group order, tb[g] = the index of group g's first tile; hdr[0] = their number. 1024 groups a pass: off_s of the pass's 1024 upper ends by a
+// running-maximum scan (kept in LDS with the lower end carried in), then a scan of the tile counts.
 __global__ __launch_bounds__(1024) void rq_plan_kernel(const int64_t* __restrict__ off, int G, int64_t rows,
-                                                       int64_t* __restrict__ off_s, int32_t* __restrict__ hdr,
-                                                       int32_t* __restrict__ e1, int64_t cap1,
-                                                       int32_t* __restrict__ e4, int64_t cap4, int2* __restrict__ em,
+                                                       int64_t* __restrict__ off_s, int32_t* __restrict__ tb,
+                                                       int32_t* __restrict__ hdr, int2* __restrict__ em,
                                                        int64_t capm) {
     __shared__ int64_t sh[16];
+    __shared__ int64_t s_o[1025];
     const auto mx = [](int64_t a, int64_t b) { return a > b ? a : b; };
     const auto add = [](int64_t a, int64_t b) { return a + b; };
-    int64_t carry = 0;
-    for (int base = 0; base <= G; base += 1024) {  // off_s[g] = clamp(max(off[0..g]), 0, rows); ends 0 and rows
-        const int g = base + (int)threadIdx.x;
-        int64_t v = g <= G ? off[g] : 0;
+    const int tid = threadIdx.x;
+    int64_t carry = 0, cm = 0;
+    if (tid == 0) off_s[0] = 0;
+    for (int base = 0; base < G; base += 1024) {  // groups base .. base + 1023: offsets base + 1 .. base + 1024
+        const int idx = base + 1 + tid;
+        int64_t v = idx <= G ? off[idx] : rows;
         v = v < 0 ? 0 : (v > rows ? rows : v);
+        if (idx >= G) v = rows;
         int64_t tot;
         v = mx(block_incl_scan(v, sh, mx, tot), carry);
+        if (idx <= G) off_s[idx] = v;
+        s_o[tid + 1] = v;
+        if (tid == 0) s_o[0] = carry;
         carry = mx(carry, tot);
-        if (g == 0) v = 0;
-        if (g == G) v = rows;
-        if (g <= G) off_s[g] = v;
-    }
-    __syncthreads();  // off_s is read back by other threads of this CTA
-    int64_t c1 = 0, c4 = 0, cm = 0;
-    for (int base = 0; base < G; base += 1024) {
-        const int g = base + (int)threadIdx.x;
-        const int64_t cnt = g < G ? off_s[g + 1] - off_s[g] : 0;
-        const int64_t a1 = cnt == 1, a4 = cnt >= 2 && cnt <= 4, am = cnt >= 5 ? (cnt + RQ_BM - 1) / RQ_BM : 0;
-        int64_t t1, t4, tm;
-        const int64_t p1 = block_incl_scan(a1, sh, add, t1) - a1 + c1;
-        const int64_t p4 = block_incl_scan(a4, sh, add, t4) - a4 + c4;
-        const int64_t pm = block_incl_scan(am, sh, add, tm) - am + cm;
-        if (a1 && p1 < cap1) e1[p1] = g;
-        if (a4 && p4 < cap4) e4[p4] = g;
+        __syncthreads();
+        const int g = base + tid;
+        const int64_t cnt = g < G ? s_o[tid + 1] - s_o[tid] : 0;
+        const int64_t am = (cnt + RQ_BM - 1) / RQ_BM;
+        int64_t ptot;
+        const int64_t pm = block_incl_scan(am, sh, add, ptot) - am + cm;
+        if (g < G) tb[g] = (int32_t)(pm < capm ? pm : capm);  // the group's first tile
         for (int64_t t = 0; t < am; t++)
             if (pm + t < capm) em[pm + t] = int2{g, (int)(t * RQ_BM)};
-        c1 += t1, c4 += t4, cm += tm;
+        cm += ptot;
     }
-    if (threadIdx.x == 0) {
-        hdr[0] = (int32_t)(c1 < cap1 ? c1 : cap1);
-        hdr[1] = (int32_t)(c4 < cap4 ? c4 : cap4);
-        hdr[2] = (int32_t)(cm < capm ? cm : capm);
-    }
+    if (tid == 0) hdr[0] = (int32_t)(cm < capm ? cm : capm);
 }
 
-// Groups of at most MM rows: a wave per RQ_SK_CPW output columns, its lanes striding k[k0, k1) in 16-byte chunks
-// of every plane row (1 KB per load instruction), int32 plane-group sums per lane with sdot4, a butterfly across the
-// wave. The CTAs along y stride the entry list (list[0 .. *count)).
-template <int PW, int MM>
-__global__ __launch_bounds__(256) void rq_skinny_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
-                                                        size_t wgroup, int64_t* __restrict__ acc, int N, int kp,
-                                                        int k0, int k1, int accumulate,
-                                                        const int64_t* __restrict__ off_s,
-                                                        const int32_t* __restrict__ list,
-                                                        const int32_t* __restrict__ count) {
-    constexpr int PX = 3, NG = PX + PW - 1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nb = ((int)blockIdx.x * 4 + wave) * RQ_SK_CPW;  // the wave's first column
-    const int nch = (k1 - k0) / 16, n_ent = *count;
-    for (int e = blockIdx.y; e < n_ent; e += gridDim.y) {
-        const int g = list[e];
-        const int64_t base = off_s[g];
-        const int M = (int)(off_s[g + 1] - base);  // 1 .. MM by the plan
-        const int8_t* xg = xa + base * 3 * kp;
-        const int8_t* wg = wb + (size_t)g * wgroup;
-        const size_t xplane = (size_t)M * kp, wplane = (size_t)N * kp;
-        int a[RQ_SK_CPW][MM][NG];
-#pragma unroll
-        for (int c = 0; c < RQ_SK_CPW; c++)
-#pragma unroll
-            for (int m = 0; m < MM; m++)
-#pragma unroll
-                for (int q = 0; q < NG; q++) a[c][m][q] = 0;
-        for (int qc = lane; qc < nch; qc += 64) {
-            const size_t ko = (size_t)k0 + 16 * (size_t)qc;
-            v4i xv[PX][MM], wv[RQ_SK_CPW][PW];
-#pragma unroll
-            for (int i = 0; i < PX; i++)
-#pragma unroll
-                for (int m = 0; m < MM; m++)
-                    xv[i][m] = m < M ? gload16(xg + i * xplane + (size_t)m * kp + ko) : v4i{};
-#pragma unroll
-            for (int c = 0; c < RQ_SK_CPW; c++)
-#pragma unroll
-                for (int j = 0; j < PW; j++)
-                    wv[c][j] = nb + c < N ? gload16(wg + j * wplane + (size_t)(nb + c) * kp + ko) : v4i{};
-#pragma unroll
-            for (int c = 0; c < RQ_SK_CPW; c++)
-#pragma unroll
-                for (int m = 0; m < MM; m++)
-#pragma unroll
-                    for (int i = 0; i < PX; i++)
-#pragma unroll
-                        for (int j = 0; j < PW; j++) {
-                            int d = a[c][m][i + j];
-#pragma unroll
-                            for (int u = 0; u < 4; u++) d = __builtin_amdgcn_sdot4(xv[i][m][u], wv[c][j][u], d, false);
-                            a[c][m][i + j] = d;
-                        }
+// The weight planes by tile (kt_hip_pack_planes_tiled): for each 128-row block of the outputs, nkt k-steps of
+// [PW planes][128 rows x 64 bytes], each 128 x 64 block in the swizzled LDS layout; rows past the matrix are zero. A
+// CTA's run of k-steps is then one contiguous stretch of memory.
+__global__ void rq_pack_tiled_kernel(const int32_t* __restrict__ codes, int64_t rows, int64_t k, int64_t kp, int pw,
+                                     int8_t* __restrict__ out) {
+    // one thread per 16-byte chunk of the output: (n-block, k-step, plane, row, chunk position)
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nkt = kp / RQ_BK, nblk = (rows + RQ_BN - 1) / RQ_BN;
+    if (idx >= nblk * nkt * pw * RQ_BN * 4) return;
+    const int slot = (int)(idx & 3), r = (int)((idx >> 2) % RQ_BN);
+    const int64_t rest = (idx >> 2) / RQ_BN;
+    const int q = (int)(rest % pw);
+    const int64_t kt = (rest / pw) % nkt, nb = (rest / pw) / nkt;
+    const int c = slot ^ ((r >> 2) & 3);  // the chunk stored at this position
+    const int64_t n = nb * RQ_BN + r, k0 = kt * RQ_BK + 16 * c;
+    uint32_t wd[4] = {0, 0, 0, 0};
+    for (int t = 0; t < 16; t++) {
+        int64_t v = n < rows && k0 + t < k ? codes[n * k + k0 + t] : 0;
+        int64_t d = 0;
+        for (int i = 0; i <= q; i++) {  // digit q of the balanced base-256 expansion (as kt_hip_pack_planes)
+            d = ((v + 128) & 255) - 128;
+            v = (v - d) >> 8;
         }
-#pragma unroll
-        for (int c = 0; c < RQ_SK_CPW; c++)
-#pragma unroll
-            for (int m = 0; m < MM; m++)
-#pragma unroll
-                for (int q = 0; q < NG; q++)
-#pragma unroll
-                    for (int o = 32; o >= 1; o >>= 1) a[c][m][q] += __shfl_xor(a[c][m][q], o);
-        if (lane == 0) {
-#pragma unroll
-            for (int c = 0; c < RQ_SK_CPW; c++) {
-                const int n = nb + c;
-                if (n >= N) continue;
-#pragma unroll
-                for (int m = 0; m < MM; m++) {
-                    if (m >= M) continue;
-                    uint64_t v = 0;
-#pragma unroll
-                    for (int q = 0; q < NG; q++) v += (uint64_t)(int64_t)a[c][m][q] << (8 * q);
-                    int64_t* p = acc + (base + m) * N + n;
-                    *p = (int64_t)(accumulate ? (uint64_t)*p + v : v);
-                }
-            }
-        }
+        wd[t >> 2] |= ((uint32_t)d & 255u) << (8 * (t & 3));
     }
+    *reinterpret_cast<v4i*>(out + idx * 16) = v4i{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
 }
 
-// 32-row tiles of the larger groups: a CTA of 4 waves takes one tile (list[e] = (group, first row)) against RQ_BN
-// output columns, each wave 32 x 32 with 32x32x32 int8 MFMAs per plane pair; k in 64-byte steps through
-// double-buffered LDS (swizzled 16-byte chunks), the next step's loads in flight during the MFMAs. The CTAs are
-// numbered so that each XCD (block b -> XCD b % 8) gets a contiguous run of (column tile, entry) work, the tiles of
-// one group's rows next to each other, sharing the group's weight columns in that XCD's L2.
+// The grouped product: a CTA of 4 waves takes one 32-row tile (list[e] = (group, first row)) against RQ_BN output
+// columns and one run of k-steps, each wave 32 x 32 with 32x32x32 int8 MFMAs per plane pair. Every operand byte
+// arrives by LDS DMA (buffer_load ... lds, 1 KB per instruction, lane l's 16 bytes at 16 l) into a ring of NS stages,
+// NS - 1 k-steps in flight beyond the one being multiplied; both operands are stored tiled in the LDS image, so a
+// k-step of the tile (6 KB) and of the weight block (PW x 8 KB) are contiguous and copy as they are. Each wave moves
+// 2 + 2 PW pieces a step (A has 6: waves 2 and 3 send their second into a dump area), so one vmcnt target serves
+// every wave. Tile rows past the group hold stale bytes: they only reach outputs that are not stored. The CTAs are
+// numbered so that each XCD (block b -> XCD b % 8) gets a contiguous run of work.
+// acc slice `split`: rows x N i64 partial sums of this run of k-steps.
 template <int PW>
-__global__ __launch_bounds__(256) void rq_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
-                                                      size_t wgroup, int64_t* __restrict__ acc, int N, int kp, int k0,
-                                                      int k1, int accumulate, const int64_t* __restrict__ off_s,
-                                                      const int2* __restrict__ list, const int32_t* __restrict__ count,
-                                                      int cap) {
-    constexpr int PX = 3, BK = 64, CPR = BK / 16, NG = PX + PW - 1;
-    constexpr int AC = PX * RQ_BM * CPR, BC = PW * RQ_BN * CPR;  // 16-byte chunks per k step
-    constexpr int AL = (AC + 255) / 256, BL = BC / 256;
-    static_assert(BC % 256 == 0, "B chunks per thread");
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][PX][RQ_BM * BK];
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][PW][RQ_BN * BK];
+struct RqRing {
+    static constexpr int NS = PW == 5 ? 3 : 4;
+    static constexpr int A_BYTES = 3 * RQ_BM * RQ_BK, B_BYTES = PW * RQ_BN * RQ_BK, STAGE = A_BYTES + B_BYTES;
+    static constexpr int DUMP = NS * STAGE, LDS = DUMP + 1024;
+    static constexpr int DPW = 2 + 2 * PW;  // DMA instructions per wave and k-step
+    static_assert(DPW * (NS - 2) <= 63, "vmcnt holds the DMAs of NS - 2 later steps");
+};
 
+template <int PW>
+__global__ __launch_bounds__(256) void rq_gemm_kernel(const int8_t* __restrict__ xa, int64_t rows, int64_t kp_,
+                                                      const int8_t* __restrict__ wb, size_t wgroup,
+                                                      int64_t* __restrict__ acc, int N,
+                                                      const int64_t* __restrict__ off_s,
+                                                      const int2* __restrict__ list, const int32_t* __restrict__ count,
+                                                      int cap, int ntile, int per) {
+    using R = RqRing<PW>;
+    constexpr int NS = R::NS;
+    extern __shared__ __attribute__((aligned(16))) int8_t ring[];
+    const int nkt = (int)(kp_ / RQ_BK);
     const int nbk = (int)gridDim.x, b = (int)blockIdx.x, xcd = b & 7, q8 = nbk >> 3, r8 = nbk & 7;
     const int w = xcd * q8 + (xcd < r8 ? xcd : r8) + (b >> 3);
-    const int nt = w / cap, e = w - nt * cap;
+    const int e = w % cap, rest = w / cap, nt = rest % ntile, split = rest / ntile;
     if (e >= *count) return;  // uniform: past the table
     const int2 ent = list[e];
     const int g = ent.x, m0 = ent.y;
     const int64_t base = off_s[g];
     const int M = (int)(off_s[g + 1] - base);
     const int n0 = nt * RQ_BN;
-    const int8_t* xg = xa + base * 3 * kp;
-    const int8_t* wg = wb + (size_t)g * wgroup;
-    const size_t xplane = (size_t)M * kp, wplane = (size_t)N * kp;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kt0 = split * per;
+    const int nk = nkt - kt0 < per ? nkt - kt0 : per;  // >= 1 by the host's choice of the split
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    v16i c[NG];
+    // this tile's k-steps (e is its index in the tiled activations) and this block's weight k-steps
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(xa + (int64_t)e * nkt * R::A_BYTES, (uint32_t)(nkt * R::A_BYTES));
+    const __amdgpu_buffer_rsrc_t rB =
+        make_rsrc(wb + (size_t)g * wgroup + (size_t)nt * nkt * R::B_BYTES, (uint32_t)(nkt * R::B_BYTES));
+    const uint32_t lo = 16u * (uint32_t)lane;
+    const int pa1 = wv + 4;  // this wave's A pieces: wv and wv + 4 (pieces 6, 7 re-read piece 0 into the dump)
+    auto issue = [&](int st, int kt) {
+        const int kk = kt0 + (kt < nk ? kt : nk - 1);  // past the run: a re-read into a stage nobody reads
+        const uint32_t ka = (uint32_t)kk * R::A_BYTES, kb = (uint32_t)kk * R::B_BYTES;
+        int8_t* sp = ring + st * R::STAGE;
+        dma16(rA, sp + 1024 * wv, lo + 1024u * (uint32_t)wv, ka);
+        dma16(rA, pa1 < 6 ? sp + 1024 * pa1 : ring + R::DUMP, lo + (pa1 < 6 ? 1024u * (uint32_t)pa1 : 0u), ka);
 #pragma unroll
-    for (int q = 0; q < NG; q++) c[q] = v16i{};
-    v4i ra[AL], rb[BL];
-    auto gload_tile = [&](int k) {
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            const int idx = tid + 256 * i, p = idx / (RQ_BM * CPR), rem = idx % (RQ_BM * CPR);
-            const int r = rem / CPR, ch = rem % CPR, gr = m0 + r;
-            ra[i] = idx < AC && gr < M ? gload16(xg + p * xplane + (size_t)gr * kp + k + 16 * ch) : v4i{};
-        }
-#pragma unroll
-        for (int i = 0; i < BL; i++) {
-            const int idx = tid + 256 * i, p = idx / (RQ_BN * CPR), rem = idx % (RQ_BN * CPR);
-            const int r = rem / CPR, ch = rem % CPR, gn = n0 + r;
-            rb[i] = gn < N ? gload16(wg + p * wplane + (size_t)gn * kp + k + 16 * ch) : v4i{};
-        }
+        for (int t = 0; t < 2 * PW; t++)
+            dma16(rB, sp + R::A_BYTES + 1024 * (wv + 4 * t), lo + 1024u * (uint32_t)(wv + 4 * t), kb);
     };
-    auto lstore_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            const int idx = tid + 256 * i, p = idx / (RQ_BM * CPR), rem = idx % (RQ_BM * CPR);
-            if (idx < AC) lds_write16(sA[buf][p], lds_off<CPR>(rem / CPR, rem % CPR), ra[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < BL; i++) {
-            const int idx = tid + 256 * i, p = idx / (RQ_BN * CPR), rem = idx % (RQ_BN * CPR);
-            lds_write16(sB[buf][p], lds_off<CPR>(rem / CPR, rem % CPR), rb[i]);
-        }
+    auto wait_step = [&]() {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(R::DPW * (NS - 2)) : "memory");
     };
 
-    const int nk = (k1 - k0) / BK;
-    gload_tile(k0);
-    lstore_tile(0);
-    __syncthreads();
+    v16i c[3 + PW - 1];
+#pragma unroll
+    for (int q = 0; q < 3 + PW - 1; q++) c[q] = v16i{};
+#pragma unroll
+    for (int t = 0; t < NS - 1; t++) issue(t, t);
     for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload_tile(k0 + (kt + 1) * BK);
+        wait_step();  // step kt has landed for every wave; every wave is done reading step kt - 1
+        issue((kt + NS - 1) % NS, kt + NS - 1);
+        const int8_t* sp = ring + (kt % NS) * R::STAGE;
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
+        for (int ks = 0; ks < RQ_BK / 32; ks++) {
             const int chunk = 2 * ks + (lane >> 5);
-            v4i av[PX], bv[PW];
+            v4i av[3], bv[PW];
 #pragma unroll
-            for (int p = 0; p < PX; p++) av[p] = lds_read16(sA[cur][p], lds_off<CPR>(lane & 31, chunk));
+            for (int p = 0; p < 3; p++) av[p] = lds_read16(sp + p * (RQ_BM * RQ_BK), lds_off<4>(lane & 31, chunk));
 #pragma unroll
-            for (int p = 0; p < PW; p++) bv[p] = lds_read16(sB[cur][p], lds_off<CPR>(32 * wave + (lane & 31), chunk));
+            for (int q = 0; q < PW; q++)
+                bv[q] = lds_read16(sp + R::A_BYTES + q * (RQ_BN * RQ_BK), lds_off<4>(32 * wv + (lane & 31), chunk));
 #pragma unroll
-            for (int i = 0; i < PX; i++)
+            for (int i = 0; i < 3; i++)
 #pragma unroll
                 for (int j = 0; j < PW; j++) c[i + j] = mfma32(av[i], bv[j], c[i + j]);
         }
-        if (kt + 1 < nk) lstore_tile(cur ^ 1);
-        __syncthreads();
     }
-    const int n = n0 + 32 * wave + (lane & 31);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA may land after the CTA ends
+    const int n = n0 + 32 * wv + (lane & 31);
     if (n >= N) return;
+    int64_t* slice = acc + (int64_t)split * rows * N;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int m = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m >= M) continue;
         uint64_t v = 0;
 #pragma unroll
-        for (int q = 0; q < NG; q++) v += (uint64_t)(int64_t)c[q][r] << (8 * q);
-        int64_t* p = acc + (base + m) * N + n;
-        *p = (int64_t)(accumulate ? (uint64_t)*p + v : v);
+        for (int q = 0; q < 3 + PW - 1; q++) v += (uint64_t)(int64_t)c[q][r] << (8 * q);
+        slice[(base + m) * N + n] = (int64_t)v;
     }
 }
 
@@ -550,11 +585,13 @@ __device__ __forceinline__ int64_t sc_apply_i32(Sc a, bool fast, int32_t v) {
     return (v < 0) != (a.mant < 0) ? (int64_t)(0 - q) : (int64_t)q;
 }
 
-constexpr int RM_COMBINE_THREADS = 1024;
+constexpr int RM_COMBINE_THREADS = 1024, RM_VPT = 4, RM_KB = 4;
 
 // MoeMlp::combine for token t (one CTA of 1024 threads): its k expert outputs (rows pos[t, i] of y with records ys)
 // brought to their largest scale, summed with the numerators ec, requantized, 1/sumc folded into the scale; zeros
-// when sumc <= 0. Each element's sum is formed twice (for the maximum, then for the output), not stored.
+// when sumc <= 0. Up to RM_VPT sums per thread stay in registers between the maximum and the requant, and the
+// expert rows are read RM_KB at a time (all those loads in flight together, branch-free); longer rows form each sum
+// twice.
 __global__ __launch_bounds__(RM_COMBINE_THREADS) void rm_combine_kernel(const int32_t* __restrict__ y,
                                                                        const kt_hip_qscale* __restrict__ ys,
                                                                        int y_rows, int dim,
@@ -593,22 +630,52 @@ __global__ __launch_bounds__(RM_COMBINE_THREADS) void rm_combine_kernel(const in
     __syncthreads();
     const Sc common = s_common;
     const bool live = sc_ > 0 && common.mant != 0;
-    auto value = [&](int d) -> int64_t {
-        int64_t acc = 0;
-        for (int i = 0; i < top_k; i++)
-            if (s_row[i] >= 0 && f[i].mant != 0)
-                acc = wadd(acc, wmul(s_ec[i], sc_apply_i32(f[i], s_fast[i], y[(int64_t)s_row[i] * dim + d])));
-        return acc;
+    // the sums of the RM_VPT elements d0 + RM_COMBINE_THREADS * j (j < RM_VPT, d < dim), rows read RM_KB at a time
+    auto sums = [&](int d0, int64_t (&acc)[RM_VPT]) {
+#pragma unroll
+        for (int j = 0; j < RM_VPT; j++) acc[j] = 0;
+        for (int i0 = 0; i0 < top_k; i0 += RM_KB) {
+            int32_t yv[RM_KB][RM_VPT];
+#pragma unroll
+            for (int ii = 0; ii < RM_KB; ii++) {
+                const int i = i0 + ii;
+                const int64_t rw = i < top_k && s_row[i] >= 0 ? s_row[i] : 0;  // row 0 stands in; dropped below
+#pragma unroll
+                for (int j = 0; j < RM_VPT; j++) {
+                    const int d = d0 + RM_COMBINE_THREADS * j;
+                    yv[ii][j] = y[rw * dim + (d < dim ? d : dim - 1)];
+                }
+            }
+#pragma unroll
+            for (int ii = 0; ii < RM_KB; ii++) {
+                const int i = i0 + ii;
+                if (i >= top_k || s_row[i] < 0 || f[i].mant == 0) continue;  // uniform
+#pragma unroll
+                for (int j = 0; j < RM_VPT; j++)
+                    acc[j] = wadd(acc[j], wmul(s_ec[i], sc_apply_i32(f[i], s_fast[i], yv[ii][j])));
+            }
+        }
     };
+    const int span = RM_COMBINE_THREADS * RM_VPT;
+    int64_t hv[RM_VPT];
     int64_t m = 0;
     if (live)
-        for (int d = threadIdx.x; d < dim; d += RM_COMBINE_THREADS) {
-            const int64_t a = iabs(value(d));
-            m = a > m ? a : m;
+        for (int d0 = threadIdx.x; d0 < dim; d0 += span) {
+            sums(d0, hv);
+#pragma unroll
+            for (int j = 0; j < RM_VPT; j++)
+                if (d0 + RM_COMBINE_THREADS * j < dim) m = iabs(hv[j]) > m ? iabs(hv[j]) : m;
         }
     const int64_t gmax = block_max_t(m, red);
-    for (int d = threadIdx.x; d < dim; d += RM_COMBINE_THREADS)
-        out[(int64_t)t * dim + d] = gmax ? requant_dyn_dev(value(d), gmax) : 0;
+    const bool held = dim <= span;  // hv still holds this thread's sums
+    for (int d0 = threadIdx.x; d0 < dim; d0 += span) {
+        if (gmax && !held) sums(d0, hv);
+#pragma unroll
+        for (int j = 0; j < RM_VPT; j++) {
+            const int d = d0 + RM_COMBINE_THREADS * j;
+            if (d < dim) out[(int64_t)t * dim + d] = gmax ? requant_dyn_dev(hv[j], gmax) : 0;
+        }
+    }
     if (threadIdx.x == 0) {
         Sc s{0, 0};
         if (gmax)
@@ -693,12 +760,15 @@ __global__ __launch_bounds__(RQ_THREADS) void rm_merge_out_kernel(const int32_t*
         put_rec(os, gmax ? sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), *common) : Sc{0, 0});
 }
 
-// The workspace: activation planes, the i64 products, the row records, the sanitized offsets, the tables.
+// The workspace: the tiled activation planes, the i64 partial products (one slice per k run), the row records, the
+// sanitized offsets with each group's first tile, the tile table.
 size_t rq_workspace_bytes(int64_t rows, int64_t in, int64_t out, int64_t groups, size_t off[5]) {
-    const size_t kp = (size_t)((in + 63) / 64 * 64);
-    const RqCaps c = rq_caps(rows, groups);
-    const size_t sizes[5] = {3 * (size_t)rows * kp, (size_t)rows * (size_t)out * 8, (size_t)rows * sizeof(RqState),
-                             (size_t)(groups + 1) * 8, 16 + 8 * (size_t)c.tiles + 4 * (size_t)(c.one + c.few)};
+    const int64_t kp = (in + 63) / 64 * 64;
+    const int S = rq_splits(rows, groups, out, kp, kt_hip_flush_k(3, 3));  // the smallest flush bound: most runs
+    const size_t cap = (size_t)rq_tile_cap(rows, groups);
+    const size_t sizes[5] = {cap * RQ_BM * 3 * (size_t)kp, (size_t)S * (size_t)rows * (size_t)out * 8,
+                             (size_t)rows * sizeof(RqState), (size_t)(groups + 1) * 8 + (size_t)groups * 4,
+                             16 + 8 * cap};
     size_t at = 0;
     for (int i = 0; i < 5; i++) {
         off[i] = at;
@@ -708,19 +778,18 @@ size_t rq_workspace_bytes(int64_t rows, int64_t in, int64_t out, int64_t groups,
 }
 
 template <int PW>
-static void rq_products(const int8_t* xa, const int8_t* wb, size_t wgroup, int64_t* acc, int N, int kp, int k0, int k1,
-                        int accumulate, const int64_t* off_s, const int32_t* hdr, const int32_t* e1, const int32_t* e4,
-                        const int2* em, const RqCaps& c, hipStream_t s) {
-    const unsigned gx = (unsigned)((N + 4 * RQ_SK_CPW - 1) / (4 * RQ_SK_CPW));
-    if (c.one > 0)
-        rq_skinny_kernel<PW, 1><<<dim3(gx, (unsigned)(c.one < RQ_SK_Y ? c.one : RQ_SK_Y)), 256, 0, s>>>(
-            xa, wb, wgroup, acc, N, kp, k0, k1, accumulate, off_s, e1, hdr);
-    if (c.few > 0)
-        rq_skinny_kernel<PW, 4><<<dim3(gx, (unsigned)(c.few < RQ_SK_Y ? c.few : RQ_SK_Y)), 256, 0, s>>>(
-            xa, wb, wgroup, acc, N, kp, k0, k1, accumulate, off_s, e4, hdr + 1);
-    const int64_t nt = (N + RQ_BN - 1) / RQ_BN;
-    rq_gemm_kernel<PW><<<(unsigned)(nt * c.tiles), 256, 0, s>>>(xa, wb, wgroup, acc, N, kp, k0, k1, accumulate,
-                                                                 off_s, em, hdr + 2, (int)c.tiles);
+static hipError_t rq_product(const int8_t* xa, int64_t rows, int64_t kp, const int8_t* wb, size_t wgroup,
+                             int64_t* acc, int64_t N, const int64_t* off_s, const int2* em, const int32_t* hdr,
+                             int64_t cap, int S, hipStream_t s) {
+    using R = RqRing<PW>;
+    int dev = 0, mx = 0;  // the ring must fit one CTA's LDS (160 KB on gfx950)
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || R::LDS > mx)
+        return hipErrorInvalidConfiguration;
+    const int64_t ntile = (N + RQ_BN - 1) / RQ_BN, nkt = kp / RQ_BK, per = (nkt + S - 1) / S;
+    rq_gemm_kernel<PW><<<(unsigned)(ntile * cap * S), 256, R::LDS, s>>>(xa, rows, kp, wb, wgroup, acc, (int)N, off_s,
+                                                                       em, hdr, (int)cap, (int)ntile, (int)per);
+    return hipGetLastError();
 }
 
 hipError_t launch_quant_linear_rows(const int32_t* x, const int32_t* xidx, int64_t x_rows, int64_t rows, int64_t in,
@@ -730,34 +799,36 @@ hipError_t launch_quant_linear_rows(const int32_t* x, const int32_t* xidx, int64
                                     hipStream_t s) {
     size_t off[5];
     rq_workspace_bytes(rows, in, out, groups, off);
-    const RqCaps c = rq_caps(rows, groups);
+    const int64_t cap = rq_tile_cap(rows, groups), kp = (in + 63) / 64 * 64;
+    const int S = rq_splits(rows, groups, out, kp, flush_k);
     char* base = (char*)ws;
     int8_t* xa = (int8_t*)(base + off[0]);
     int64_t* acc = (int64_t*)(base + off[1]);
     RqState* st = (RqState*)(base + off[2]);
     int64_t* off_s = (int64_t*)(base + off[3]);
+    int32_t* tb = (int32_t*)(off_s + groups + 1);
     int32_t* hdr = (int32_t*)(base + off[4]);
     int2* em = (int2*)(hdr + 4);
-    int32_t* e1 = (int32_t*)(em + c.tiles);
-    int32_t* e4 = e1 + c.one;
-    const int64_t kp = (in + 63) / 64 * 64;
-    rq_plan_kernel<<<1, 1024, 0, s>>>(off_dev, groups, rows, off_s, hdr, e1, c.one, e4, c.few, em, c.tiles);
-    rq_quant_kernel<<<(unsigned)rows, RQ_THREADS, 0, s>>>(x, xidx, x_rows, in, kp, xs, xs_step, groups, off_s,
-                                                          wm_dev, wsh_dev, st, xa);
-    for (int64_t k0 = 0; k0 < kp; k0 += flush_k) {
-        const int64_t k1 = kp - k0 < flush_k ? kp : k0 + flush_k;
-        const int acc_in = k0 > 0;
-        if (pw == 1)
-            rq_products<1>(xa, wb, wgroup, acc, (int)out, (int)kp, (int)k0, (int)k1, acc_in, off_s, hdr, e1, e4, em,
-                           c, s);
-        else if (pw == 3)
-            rq_products<3>(xa, wb, wgroup, acc, (int)out, (int)kp, (int)k0, (int)k1, acc_in, off_s, hdr, e1, e4, em,
-                           c, s);
-        else
-            rq_products<5>(xa, wb, wgroup, acc, (int)out, (int)kp, (int)k0, (int)k1, acc_in, off_s, hdr, e1, e4, em,
-                           c, s);
-    }
-    rq_requant_kernel<<<(unsigned)rows, RQ_THREADS, 0, s>>>(acc, out, st, y, ys);
+    rq_plan_kernel<<<1, 1024, 0, s>>>(off_dev, groups, rows, off_s, tb, hdr, em, cap);
+    rq_quant_kernel<<<(unsigned)rows, RQ_ROW_THREADS, 0, s>>>(x, xidx, x_rows, in, kp, xs, xs_step, groups, off_s,
+                                                              tb, cap, wm_dev, wsh_dev, st, xa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = pw == 1   ? rq_product<1>(xa, rows, kp, wb, wgroup, acc, out, off_s, em, hdr, cap, S, s)
+        : pw == 3 ? rq_product<3>(xa, rows, kp, wb, wgroup, acc, out, off_s, em, hdr, cap, S, s)
+                  : rq_product<5>(xa, rows, kp, wb, wgroup, acc, out, off_s, em, hdr, cap, S, s);
+    if (e != hipSuccess) return e;
+    rq_requant_kernel<<<(unsigned)rows, RQ_ROW_THREADS, 0, s>>>(acc, rows, out, S, st, y, ys);
+    return hipGetLastError();
+}
+
+size_t rq_tiled_bytes(int64_t rows, int64_t k, int p) {
+    return (size_t)((rows + RQ_BN - 1) / RQ_BN) * RQ_BN * (size_t)((k + 63) / 64 * 64) * (size_t)p;
+}
+
+hipError_t launch_rq_pack_tiled(const int32_t* codes, int64_t rows, int64_t k, int p, int8_t* out, hipStream_t s) {
+    const int64_t chunks = (int64_t)(rq_tiled_bytes(rows, k, p) / 16);
+    rq_pack_tiled_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, s>>>(codes, rows, k, (k + 63) / 64 * 64, p, out);
     return hipGetLastError();
 }
 
@@ -835,12 +906,30 @@ extern "C" int kt_hip_quant_linear_rows(int dev, const int32_t* x_dev, const int
             if (off_host[g + 1] < off_host[g]) return (int)hipErrorInvalidValue;
     }
     if (ws_bytes < kt_hip_quant_linear_rows_workspace(rows, in_f, out_f, groups)) return (int)hipErrorInvalidValue;
-    const kt::RqCaps c = kt::rq_caps(rows, groups);
-    if (((out_f + kt::RQ_BN - 1) / kt::RQ_BN) * c.tiles > INT32_MAX) return (int)hipErrorInvalidValue;
+    // the grouped product addresses one tile's and one weight block's k-steps with 32-bit offsets
+    if (w_group_bytes < kt::rq_tiled_bytes(out_f, in_f, pw) || (int64_t)pw * kt::RQ_BN * kp >= ((int64_t)1 << 32))
+        return (int)hipErrorInvalidValue;
+    const int64_t S = kt::rq_splits(rows, groups, out_f, kp, kt_hip_flush_k(3, pw));
+    if (((out_f + kt::RQ_BN - 1) / kt::RQ_BN) * kt::rq_tile_cap(rows, groups) * S > INT32_MAX)
+        return (int)hipErrorInvalidValue;
     RM_TRY(hipSetDevice(dev));
     return (int)kt::launch_quant_linear_rows(x_dev, xidx_dev, x_rows, rows, in_f, xs_dev, xs_step, (int)groups,
                                              off_dev, w_planes_dev, w_group_bytes, pw, out_f, w_mant_dev, w_shift_dev,
                                              kt_hip_flush_k(3, pw), ws_dev, y_dev, ys_dev, (hipStream_t)stream);
+}
+
+extern "C" size_t kt_hip_pack_planes_tiled_bytes(int64_t rows, int64_t k, int planes) {
+    if (rows < 1 || k < 1 || (planes != 1 && planes != 3 && planes != 5)) return 0;
+    return kt::rq_tiled_bytes(rows, k, planes);
+}
+
+extern "C" int kt_hip_pack_planes_tiled(int dev, const int32_t* codes_dev, int64_t rows, int64_t k, int planes,
+                                        int8_t* planes_dev, void* stream) {
+    if (!codes_dev || !planes_dev || rows < 1 || k < 1 || (planes != 1 && planes != 3 && planes != 5) ||
+        rows > INT32_MAX || k > INT32_MAX || kt::rq_tiled_bytes(rows, k, planes) / 16 > (size_t)UINT32_MAX * 256)
+        return (int)hipErrorInvalidValue;
+    RM_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rq_pack_tiled(codes_dev, rows, k, planes, planes_dev, (hipStream_t)stream);
 }
 
 extern "C" int kt_hip_ref_moe_bucket(int dev, const int32_t* sel_dev, int64_t tokens, int top_k, int64_t experts,

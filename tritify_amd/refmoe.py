@@ -75,18 +75,17 @@ class RefMoeLayer:
         self._route_off = {}  # T -> the router's one-group offsets [0, T] on the device
 
     def _pack_groups(self, mats):
-        """Digit planes of each (codes out x in, scale) in one buffer (all at the largest plane count), with the
-        per-group Scales on the device."""
+        """Digit planes of each (codes out x in, scale) in one buffer (all at the largest plane count, in the grouped
+        product's tiled layout), with the per-group Scales on the device."""
         torch = self.torch
         codes = [np.ascontiguousarray(m[0], dtype=np.int32) for m in mats]
         out, inp = codes[0].shape
         pw = max(B.planes_for(c) for c in codes)
-        kp = B.kp(inp)
-        gbytes = pw * out * kp
+        gbytes = B.pack_planes_tiled_bytes(out, inp, pw)
         planes = torch.empty(len(codes) * gbytes, dtype=torch.int8, device=self.device)
         for g, c in enumerate(codes):
-            B.pack_planes(torch.from_numpy(c.reshape(-1)).to(self.device), out, inp, pw, planes[g * gbytes:],
-                          dev=self.dev)
+            B.pack_planes_tiled(torch.from_numpy(c.reshape(-1)).to(self.device), out, inp, pw, planes[g * gbytes:],
+                                dev=self.dev)
         mant = torch.from_numpy(np.array([int(m[1][0]) for m in mats], np.int64)).to(self.device)
         shift = torch.from_numpy(np.array([int(m[1][1]) for m in mats], np.int32)).to(self.device)
         torch.cuda.synchronize(self.device)
@@ -127,6 +126,21 @@ class RefMoeLayer:
         pos = torch.empty(P, dtype=torch.int32, device=self.device)
         B.ref_moe_bucket(sel, T, self.top_k, self.E, off, xidx, pos, stream=stream, dev=self.dev)
         return off, xidx, pos
+
+    def capture(self, x_dev, xs_rec, T: int):
+        """forward of T rows of the buffers x_dev / xs_rec as one HIP graph: (graph, out, out record); each replay
+        recomputes from what the buffers then hold, into the same out buffers. Call after one eager forward of T rows
+        (its small device constants exist then)."""
+        torch = self.torch
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            g.capture_begin()
+            out, orec = self.forward(x_dev, xs_rec, T, stream=s)
+            g.capture_end()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        return g, out, orec
 
     def forward(self, x_dev, xs_rec, T: int, stream=None):
         """MoeMlp::forward_int (layers.rs:1031-1034) of T token rows (x_dev: T x dim i32 codes at the record
