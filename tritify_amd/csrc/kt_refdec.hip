@@ -313,10 +313,42 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
         const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, gd) : lut_code(codes, L.n, idx));
         return wmul(code, u[k]);
     };
+    // up to RD_VPT values per thread formed once and held in registers (each pass's loads issued together, the
+    // table reads after them); longer rows form each value twice
+    constexpr int RD_VPT = 8;
+    int64_t hv[RD_VPT];
     int64_t m = 0;
-    for (int k = threadIdx.x; k < n; k += RD_THREADS) m = iabs(act(k)) > m ? iabs(act(k)) : m;
+    const bool held = n <= RD_THREADS * RD_VPT;
+    if (held) {
+        int64_t gd[RD_VPT], ud[RD_VPT];
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            const int k = threadIdx.x + RD_THREADS * i, kk = k < n ? k : n - 1;
+            gd[i] = g[kk], ud[i] = u[kk];
+        }
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            const int64_t idx = lut_index(mi, gd[i], L.lo_index);
+            const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, gd[i]) : lut_code(codes, L.n, idx));
+            hv[i] = threadIdx.x + RD_THREADS * i < n ? wmul(code, ud[i]) : 0;
+            m = iabs(hv[i]) > m ? iabs(hv[i]) : m;
+        }
+    } else {
+        for (int k = threadIdx.x; k < n; k += RD_THREADS) {
+            const int64_t a = iabs(act(k));
+            m = a > m ? a : m;
+        }
+    }
     const int64_t hmax = block_max_i64(m, red);
-    for (int k = threadIdx.x; k < n; k += RD_THREADS) h[k] = hmax == 0 ? 0 : requant_dyn_dev(act(k), hmax);
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            const int k = threadIdx.x + RD_THREADS * i;
+            if (k < n) h[k] = hmax == 0 ? 0 : requant_dyn_dev(hv[i], hmax);
+        }
+    } else {
+        for (int k = threadIdx.x; k < n; k += RD_THREADS) h[k] = hmax == 0 ? 0 : requant_dyn_dev(act(k), hmax);
+    }
     if (threadIdx.x == 0)
         put_rec(hs, hmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)hmax, (u128)ACT_LEVELS), hsc));
 }

@@ -207,23 +207,27 @@ __global__ __launch_bounds__(RQ_ROW_THREADS) void rq_requant_kernel(const int64_
     if (held) {  // the slices 4 at a time, all of a thread's loads of them in flight together (branch-free)
 #pragma unroll
         for (int i = 0; i < RQ_VPT; i++) v[i] = 0;
-        for (int q0 = 0; q0 < splits; q0 += 4) {
+        int q0 = 0;
+        for (; q0 + 4 <= splits; q0 += 4) {
             int64_t t[4][RQ_VPT];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int64_t qq = q0 + u < splits ? q0 + u : splits - 1;
-#pragma unroll
-                for (int i = 0; i < RQ_VPT; i++) {
-                    const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
-                    t[u][i] = a[qq * slice + (c < out ? c : out - 1)];
-                }
-            }
 #pragma unroll
             for (int u = 0; u < 4; u++)
 #pragma unroll
-                for (int i = 0; i < RQ_VPT; i++)
-                    v[i] = (int64_t)((uint64_t)v[i] + (q0 + u < splits ? (uint64_t)t[u][i] : 0));
+                for (int i = 0; i < RQ_VPT; i++) {
+                    const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
+                    t[u][i] = a[(q0 + u) * slice + (c < out ? c : out - 1)];
+                }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int i = 0; i < RQ_VPT; i++) v[i] = (int64_t)((uint64_t)v[i] + (uint64_t)t[u][i]);
         }
+        for (; q0 < splits; q0++)
+#pragma unroll
+            for (int i = 0; i < RQ_VPT; i++) {
+                const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
+                v[i] = (int64_t)((uint64_t)v[i] + (uint64_t)a[q0 * slice + (c < out ? c : out - 1)]);
+            }
 #pragma unroll
         for (int i = 0; i < RQ_VPT; i++)
             if (threadIdx.x + (int64_t)RQ_ROW_THREADS * i >= out) v[i] = 0;
@@ -526,7 +530,6 @@ __global__ __launch_bounds__(RQ_THREADS) void rm_route_kernel(const int32_t* __r
     extern __shared__ int64_t s_code[];  // E codes
     __shared__ int64_t red[RQ_THREADS / 64];
     __shared__ Sc s_mult;
-    __shared__ int32_t s_pick;
     const int t = blockIdx.x;
     const int32_t* lg = logits + (int64_t)t * E;
     int32_t lmax = INT32_MIN;
@@ -546,30 +549,35 @@ __global__ __launch_bounds__(RQ_THREADS) void rm_route_kernel(const int32_t* __r
         part += c;
     }
     const int64_t all = block_sum_i64(part, red);
-    // top-k: k rounds of the largest key among the unpicked (ties to the lower index)
+    // top-k: k rounds of the largest key among the unpicked (ties to the lower index). Each thread's keys (experts
+    // tid + RQ_THREADS i) are formed once and held in registers; a picked expert's key drops to the minimum.
+    // The key sits in the high bits and the inverted index below: the largest packed value is the largest key at
+    // the lowest index (keys are below 2^40 in magnitude: codes, biases and logits are).
+    constexpr int KPT = KT_REF_MOE_MAX_E / RQ_THREADS;
+    int64_t kreg[KPT];
+#pragma unroll
+    for (int q = 0; q < KPT; q++) {
+        const int j = threadIdx.x + RQ_THREADS * q;
+        kreg[q] = INT64_MIN;
+        if (j < E) kreg[q] = (sigmoid ? s_code[j] + bias[j] : (int64_t)lg[j]) * 1048576 + (int64_t)(1048575 - j);
+    }
     int64_t tsum = 0;
     for (int i = 0; i < top_k; i++) {
         int64_t best = INT64_MIN;
-        for (int j = threadIdx.x; j < E; j += RQ_THREADS) {
-            bool used = false;
-            for (int q = 0; q < i; q++) used |= sel[(int64_t)t * top_k + q] == j;
-            if (used) continue;
-            const int64_t key = sigmoid ? s_code[j] + bias[j] : (int64_t)lg[j];
-            // key in the high bits, the inverted index below: the largest packed value is the largest key at the
-            // lowest index (keys are below 2^40 in magnitude: codes, biases and logits are)
-            const int64_t packed = key * 1048576 + (int64_t)(1048575 - j);
-            best = packed > best ? packed : best;
-        }
+#pragma unroll
+        for (int q = 0; q < KPT; q++) best = kreg[q] > best ? kreg[q] : best;
         best = block_max_t(best, red);
+        const int j = 1048575 - (int)(((best % 1048576) + 1048576) % 1048576);
         if (threadIdx.x == 0) {
-            const int j = 1048575 - (int)(((best % 1048576) + 1048576) % 1048576);
-            s_pick = j;
             sel[(int64_t)t * top_k + i] = j;
             ec[(int64_t)t * top_k + i] = s_code[j];
         }
-        __syncthreads();
-        tsum += s_code[s_pick];
-        __syncthreads();
+        if ((j % RQ_THREADS) == (int)threadIdx.x) {
+#pragma unroll
+            for (int q = 0; q < KPT; q++)
+                if (q == j / RQ_THREADS) kreg[q] = INT64_MIN;
+        }
+        tsum += s_code[j];
     }
     if (threadIdx.x == 0) sumc[t] = norm_topk ? tsum : (sigmoid ? (int64_t)1 << 20 : all);
 }
@@ -605,23 +613,26 @@ __global__ __launch_bounds__(RM_COMBINE_THREADS) void rm_combine_kernel(const in
     __shared__ int32_t s_row[KT_REF_MOE_MAX_K];
     __shared__ int64_t s_ec[KT_REF_MOE_MAX_K];
     __shared__ bool s_fast[KT_REF_MOE_MAX_K];
+    __shared__ Sc s_rec[KT_REF_MOE_MAX_K];
     const int t = blockIdx.x;
     const int64_t sc_ = sumc[t];
+    if (threadIdx.x < top_k) {  // the k rows, numerators and records, fetched in parallel
+        const int i = threadIdx.x;
+        const int32_t rw = pos[(int64_t)t * top_k + i];
+        s_row[i] = rw >= 0 && rw < y_rows ? rw : -1;  // a row outside y contributes nothing (no access)
+        s_ec[i] = ec[(int64_t)t * top_k + i];
+        s_rec[i] = s_row[i] >= 0 ? rec_sc(ys + rw) : Sc{0, 0};
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
         Sc common{0, 0};
-        for (int i = 0; i < top_k; i++) {
-            const int32_t rw = pos[(int64_t)t * top_k + i];
-            s_row[i] = rw >= 0 && rw < y_rows ? rw : -1;  // a row outside y contributes nothing (no access)
-            s_ec[i] = ec[(int64_t)t * top_k + i];
-            const Sc s = s_row[i] >= 0 ? rec_sc(ys + rw) : Sc{0, 0};
-            common = sc_ge(s, common) ? s : common;
-        }
+        for (int i = 0; i < top_k; i++) common = sc_ge(s_rec[i], common) ? s_rec[i] : common;
         s_common = common;
         for (int i = 0; i < top_k; i++) f[i] = Sc{0, 0}, s_fast[i] = true;
         if (common.mant != 0) {
             const Sc cinv = sc_recip(common);
             for (int i = 0; i < top_k; i++) {
-                f[i] = s_row[i] >= 0 ? sc_mul(rec_sc(ys + s_row[i]), cinv) : Sc{0, 0};
+                f[i] = s_row[i] >= 0 ? sc_mul(s_rec[i], cinv) : Sc{0, 0};
                 const int64_t m = f[i].mant;
                 s_fast[i] = m > -((int64_t)1 << 32) && m < ((int64_t)1 << 32) && f[i].shift >= 0 && f[i].shift <= 63;
             }

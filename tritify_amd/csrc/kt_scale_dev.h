@@ -23,6 +23,7 @@ __device__ inline int bits_u128(u128 v) {
 }
 
 // floor(n / d) for d > 0, exact for every input:
+//  - d a power of two below 2^64: a shift;
 //  - both below 2^64: the 64-bit division;
 //  - d below 2^64 and the quotient below 2^49 (bits(n) - bits(d) < 49; every quotient of from_ratio, whose mantissa
 //    is below 2^33, and of isqrt's Newton steps): a double-precision estimate, whose relative error is at most
@@ -30,6 +31,10 @@ __device__ inline int bits_u128(u128 v) {
 //    corrected against the exact i128 remainder (n < 2^113 here, so the remainder fits);
 //  - otherwise restoring long division.
 __device__ inline u128 udiv128(u128 n, u128 d) {
+    // from_ratio's normalizations divide by powers of two (Scale::mul by 1, a negative shift by 2^-s): a shift, where
+    // the general 64-bit division is a long instruction sequence
+    if ((d >> 64) == 0 && (uint64_t)d != 0 && ((uint64_t)d & ((uint64_t)d - 1)) == 0)
+        return n >> __builtin_ctzll((uint64_t)d);
     if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
     if ((d >> 64) == 0 && bits_u128(n) - bits_u128(d) < 49) {
         const uint64_t d64 = (uint64_t)d;

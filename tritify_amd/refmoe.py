@@ -153,15 +153,15 @@ class RefMoeLayer:
         g, gs = self._rows_ql(self.w["gate"], x_dev, xidx_d, T, P, xs_rec, 0, off_d, E, stream)
         u, us = self._rows_ql(self.w["up"], x_dev, xidx_d, T, P, xs_rec, 0, off_d, E, stream)
         h = torch.empty(P * self.hidden, dtype=torch.int32, device=self.device)
-        hs = torch.zeros(P * 4, dtype=torch.int64, device=self.device)
+        hs = torch.empty(P * 4, dtype=torch.int64, device=self.device)  # (every record below is written whole)
         B.ref_swiglu(g, gs, u, us, self.hidden, self.silu_codes, self.silu_lut, h, hs, stream, self.dev, rows=P)
         y, ys = self._rows_ql(self.w["down"], h, None, P, P, hs, 1, off_d, E, stream)
         rows = torch.empty(T * dim, dtype=torch.int32, device=self.device)
-        rs = torch.zeros(T * 4, dtype=torch.int64, device=self.device)
+        rs = torch.empty(T * 4, dtype=torch.int64, device=self.device)
         B.ref_moe_combine(y, ys, P, dim, pos_d, ec, sumc, T, K, rows, rs, stream=stream, dev=self.dev)
         if T > 1:
             routed = torch.empty(T * dim, dtype=torch.int32, device=self.device)
-            rrec = torch.zeros(4, dtype=torch.int64, device=self.device)
+            rrec = torch.empty(4, dtype=torch.int64, device=self.device)
             n = B.ref_merge_rows_workspace(T)
             ws = torch.empty(n, dtype=torch.uint8, device=self.device)
             B.ref_merge_rows(rows, rs, T, dim, ws, n, routed, rrec, stream=stream, dev=self.dev)
@@ -169,16 +169,17 @@ class RefMoeLayer:
             routed, rrec = rows, rs
         if self.shared is None:
             return routed, rrec
-        sg, sgs = self.shared["gate"].forward_int(x_dev, xs_rec, T, stream=stream)
-        su, sus = self.shared["up"].forward_int(x_dev, xs_rec, T, stream=stream)
+        rec = lambda: torch.empty(4, dtype=torch.int64, device=self.device)  # noqa: E731
+        sg, sgs = self.shared["gate"].forward_int(x_dev, xs_rec, T, os_dev=rec(), stream=stream)
+        su, sus = self.shared["up"].forward_int(x_dev, xs_rec, T, os_dev=rec(), stream=stream)
         sh = torch.empty(T * self.shared_hidden, dtype=torch.int32, device=self.device)
-        shs = torch.zeros(4, dtype=torch.int64, device=self.device)
+        shs = rec()
         nsq = B.ref_seq_workspace(1)  # whole-tensor SwiGLU and add on many CTAs
         wsq = torch.empty(nsq, dtype=torch.uint8, device=self.device)
         B.ref_swiglu_seq(sg, sgs, su, sus, T * self.shared_hidden, self.silu_codes, self.silu_lut, wsq, nsq, sh, shs,
                          stream, self.dev)
-        sd, sds = self.shared["down"].forward_int(sh, shs, T, stream=stream)
+        sd, sds = self.shared["down"].forward_int(sh, shs, T, os_dev=rec(), stream=stream)
         out = torch.empty(T * dim, dtype=torch.int32, device=self.device)
-        orec = torch.zeros(4, dtype=torch.int64, device=self.device)
+        orec = rec()
         B.ref_add_seq(routed, rrec, sd, sds, T * dim, wsq, nsq, out, orec, stream, self.dev)
         return out, orec
