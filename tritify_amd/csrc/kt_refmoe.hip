@@ -587,8 +587,9 @@ __global__ __launch_bounds__(RQ_THREADS) void rm_route_kernel(const int32_t* __r
 // (half away from zero) as sc_apply; other Scales go through it.
 __device__ __forceinline__ int64_t sc_apply_i32(Sc a, bool fast, int32_t v) {
     if (!fast) return sc_apply(a, v);
-    const uint64_t m = (uint64_t)(a.mant < 0 ? -a.mant : a.mant), x = v < 0 ? 0u - (uint64_t)(int64_t)v : (uint64_t)v;
-    const uint64_t p = x * m;
+    // |mant| < 2^32 and |v| <= 2^31: one 32 x 32 -> 64-bit product (the integer multiplies run at quarter rate)
+    const uint32_t m = (uint32_t)(a.mant < 0 ? -a.mant : a.mant), x = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
+    const uint64_t p = (uint64_t)x * (uint64_t)m;
     const uint64_t q = a.shift == 0 ? p : (p + ((uint64_t)1 << (a.shift - 1))) >> a.shift;
     return (v < 0) != (a.mant < 0) ? (int64_t)(0 - q) : (int64_t)q;
 }
@@ -624,19 +625,19 @@ __global__ __launch_bounds__(RM_COMBINE_THREADS) void rm_combine_kernel(const in
         s_rec[i] = s_row[i] >= 0 ? rec_sc(ys + rw) : Sc{0, 0};
     }
     __syncthreads();
+    __shared__ Sc s_cinv;
     if (threadIdx.x == 0) {
         Sc common{0, 0};
         for (int i = 0; i < top_k; i++) common = sc_ge(s_rec[i], common) ? s_rec[i] : common;
         s_common = common;
-        for (int i = 0; i < top_k; i++) f[i] = Sc{0, 0}, s_fast[i] = true;
-        if (common.mant != 0) {
-            const Sc cinv = sc_recip(common);
-            for (int i = 0; i < top_k; i++) {
-                f[i] = s_row[i] >= 0 ? sc_mul(s_rec[i], cinv) : Sc{0, 0};
-                const int64_t m = f[i].mant;
-                s_fast[i] = m > -((int64_t)1 << 32) && m < ((int64_t)1 << 32) && f[i].shift >= 0 && f[i].shift <= 63;
-            }
-        }
+        if (common.mant != 0) s_cinv = sc_recip(common);
+    }
+    __syncthreads();
+    if (threadIdx.x < top_k) {  // each row's factor to the common scale, k threads at once
+        const int i = threadIdx.x;
+        f[i] = s_common.mant != 0 && s_row[i] >= 0 ? sc_mul(s_rec[i], s_cinv) : Sc{0, 0};
+        const int64_t m = f[i].mant;
+        s_fast[i] = m > -((int64_t)1 << 32) && m < ((int64_t)1 << 32) && f[i].shift >= 0 && f[i].shift <= 63;
     }
     __syncthreads();
     const Sc common = s_common;
