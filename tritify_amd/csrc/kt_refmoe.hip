@@ -161,8 +161,12 @@ __global__ __launch_bounds__(RQ_ROW_THREADS) void rq_quant_kernel(const int32_t*
         int64_t q = 0;
         if (m != 0 && c < in) {
             const int64_t num = (int64_t)xv * WLEVELS;
-            // (|num| + half) / xmax: |num| < 2^50 and the quotient at most WLEVELS, within udiv_small_q's range
-            const uint64_t u = udiv_small_q((u128)(uint64_t)(num < 0 ? -num : num) + (u128)(uint64_t)half, xmax);
+            // (|num| + half) / xmax: the numerator is below 2^51 and exact as a double, xmax below 2^32, so the
+            // correctly rounded double quotient is within 2^-33 of the true one, which is at least 1 / xmax from
+            // the next integer above it: its truncation is the floor (the check below is a guard)
+            const uint64_t nn = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
+            uint64_t u = (uint64_t)((double)nn / (double)xmax);
+            if (u * (uint64_t)xmax > nn) u--;
             q = num >= 0 ? (int64_t)u : -(int64_t)u;
         }
 #pragma unroll
