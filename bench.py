@@ -1003,7 +1003,7 @@ def main() -> int:
     ap.add_argument("--configs", type=str, default="2,3,4,5,ql,lb,ref",
                     help="comma-separated configs to run (2 is the headline; ql = the reference's QuantLinear; "
                          "lb = the LinearBackend trait path on cuda_bench's shapes; ref = the reference-semantics "
-                         "decoder, SAM image path and GLM MoE layer; refmoe = that MoE layer alone)")
+                         "decoder, SAM image path and GLM MoE layer; refdec / refmoe = that decoder / MoE layer alone)")
     ap.add_argument("--ms", type=str, default="", help="comma-separated subset of config-2 M to run (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 10 times (scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -1047,6 +1047,9 @@ def main() -> int:
             torch.cuda.empty_cache()
         if c == "ref":
             extra["ref"] = bench_ref(torch, args)
+        if c == "refdec":  # the reference decoder alone (profiling runs)
+            extra["refdec"] = bench_ref_decoder(torch, args)
+            torch.cuda.empty_cache()
         if c == "refmoe":  # the reference MoE layer alone (profiling runs)
             extra["refmoe"] = bench_ref_moe(torch, args)
             torch.cuda.empty_cache()

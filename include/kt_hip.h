@@ -104,6 +104,23 @@ int kt_hip_quant_linear(int dev, const int32_t* x_dev, int64_t rows, int64_t in_
                         const int8_t* w_planes_dev, int pw, int64_t out_f, int64_t w_mant, int32_t w_shift,
                         const int64_t* bias_dev, int64_t b_mant, int32_t b_shift, void* ws_dev, size_t ws_bytes,
                         int32_t* y_dev, kt_hip_qscale* os_dev, void* stream);
+/* Several QuantLinear::forward_int calls on the same x (the reference's projections of one tensor, layers.rs:275-328
+ * called once each: q / k / v, gate / up), their outputs computed together: one quantization of x, one digit GEMM over
+ * the weights side by side, each call's own bias, output maximum, requant_dyn and record. nseg calls of seg_out[g]
+ * output columns; w_planes_dev: the pw digit planes of the calls' weight codes stacked by rows (kt_hip_pack_planes of
+ * the (sum seg_out) x in_f matrix); w_mant / w_shift, has_bias / b_mant / b_shift: host arrays, one entry per call;
+ * bias_dev: NULL or the stacked bias codes (zeros where a call has none); y_devs: a host array of nseg device
+ * pointers (rows x seg_out[g] codes each); os_dev: nseg records. Each call's codes and record equal
+ * kt_hip_quant_linear's. Every boundary between calls must be a multiple of kt_hip_quant_linear_multi_align(rows,
+ * sum seg_out, pw) (else hipErrorInvalidValue: make the calls one at a time). ws_dev: kt_hip_quant_linear_workspace
+ * of (rows, in_f, sum seg_out) bytes. No counterpart in the reference's API: it replaces nseg calls. */
+#define KT_QL_MAX_SEGMENTS 4
+int kt_hip_quant_linear_multi(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f, const kt_hip_qscale* xs_dev,
+                              int nseg, const int64_t* seg_out, const int8_t* w_planes_dev, int pw,
+                              const int64_t* w_mant, const int32_t* w_shift, const int64_t* bias_dev,
+                              const int* has_bias, const int64_t* b_mant, const int32_t* b_shift, void* ws_dev,
+                              size_t ws_bytes, int32_t* const* y_devs, kt_hip_qscale* os_dev, void* stream);
+int64_t kt_hip_quant_linear_multi_align(int64_t rows, int64_t out_f, int pw);
 /* kt_hip_quant_linear with no workspace argument and no allocation of any kind: the workspace lives in a
  * library-owned device array of KT_QL_SCRATCH_BYTES on each GPU (held until the process ends), so the call can run
  * where hipMalloc cannot (code under HIP graph capture, tight serving loops, hosts that forbid allocation). No

@@ -159,3 +159,72 @@ def test_chain_and_graph_replay(torch_dev):
         g.replay()
         torch.cuda.synchronize()
         check(x)
+
+
+def group_case(torch, rng, rows, inp, outs, lims, biases, zero_x=False, w_zero_scale=()):
+    """A QuantLinearGroup against each member's own QuantLinear and the oracle: codes and records."""
+    import tritify_amd as TA
+
+    say(f"case: quant_linear group rows={rows} in={inp} outs={outs} biases={biases}")
+    x = np.zeros(rows * inp, np.int32) if zero_x else rng.integers(-(2**27), 2**27, size=rows * inp).astype(np.int32)
+    xs = (1509949440, 58)
+    members = []
+    for g, (o, lim, hb) in enumerate(zip(outs, lims, biases)):
+        w = rng.integers(-lim, lim + 1, size=o * inp, dtype=np.int64).astype(np.int32).reshape(o, inp)
+        ws = (0, 0) if g in w_zero_scale else (int(rng.integers(2**30, 2**31)), int(rng.integers(40, 50)))
+        b = (rng.integers(-(2**28), 2**28, size=o).astype(np.int64), (int(rng.integers(2**30, 2**31)), 57)) \
+            if hb else None
+        members.append((f"m{g}", w, ws, b))
+    grp = TA.QuantLinearGroup("grp", members, inp)
+    xd = torch.from_numpy(x).cuda()
+    xr = TA.qscale_record(*xs)
+    res = grp.forward_int(xd, xr, rows)
+    torch.cuda.synchronize()
+    for (name, w, ws, b), (y, rec) in zip(members, res):
+        yo, so, xmax, ymax = O.quant_linear_forward(x, rows, inp, xs, w.reshape(-1), w.shape[0], ws,
+                                                    bias=None if b is None else b[0],
+                                                    bs=(0, 0) if b is None else b[1])
+        got = y.cpu().numpy().reshape(rows, w.shape[0])
+        assert np.array_equal(got, yo.reshape(rows, -1)), f"{name}: codes differ"
+        r = TA.read_qscale(rec)
+        assert (r["mant"], r["shift"]) == so and r["xmax"] == xmax and r["ymax"] == ymax, f"{name}: record"
+    return grp
+
+
+@pytest.mark.parametrize("rows", [1, 3, 64, 512])
+def test_group_equals_separate_calls(torch_dev, rows):
+    """q / k / v- and gate / up-shaped groups (decode rows on the skinny product, prefill rows on MFMA tiles, a
+    split-k shape), biases on some members: every member's codes, Scale and maxima equal its own call's."""
+    rng = np.random.default_rng(rows)
+    group_case(torch_dev, rng, rows, 896, (896, 128, 128), (WLEVELS,) * 3, (True, False, True))
+    group_case(torch_dev, rng, rows, 896, (1024, 1024), (WLEVELS, WLEVELS), (False, False))
+
+
+def test_group_plane_counts_and_zero_paths(torch_dev):
+    """Members of 1, 3 and 5 weight planes (the group packs at the largest), an all-zero x (bias codes or zeros),
+    a member at a zero weight scale."""
+    rng = np.random.default_rng(3)
+    grp = group_case(torch_dev, rng, 2, 200, (128, 256, 128), (127, WLEVELS, 2**31 - 1), (True, False, False))
+    assert grp.pw == 5
+    group_case(torch_dev, rng, 2, 200, (128, 128), (WLEVELS, WLEVELS), (True, False), zero_x=True)
+    group_case(torch_dev, rng, 5, 200, (256, 128), (WLEVELS, WLEVELS), (True, True), w_zero_scale=(1,))
+
+
+def test_group_rejects_misaligned_boundaries(torch_dev):
+    """A boundary that is not a multiple of the digit GEMM's column block is refused (the host then makes the calls
+    one at a time), by the class and by the C entry."""
+    torch = torch_dev
+    import tritify_amd as TA
+    from tritify_amd import backend as B
+
+    assert not TA.QuantLinearGroup.fits((100, 28)) and TA.QuantLinearGroup.fits((128, 28))
+    w = np.ones((136, 64), np.int32)
+    planes = torch.zeros(3 * 136 * 64, dtype=torch.int8, device="cuda")
+    n, _ = B.quant_linear_workspace(1, 64, 136)
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    ys = [torch.empty(100, dtype=torch.int32, device="cuda"), torch.empty(36, dtype=torch.int32, device="cuda")]
+    with pytest.raises(Exception):
+        B.quant_linear_multi(torch.zeros(64, dtype=torch.int32, device="cuda"), 1, 64, TA.qscale_record(1 << 30, 30),
+                             [100, 36], planes, 3, [(1 << 30, 40)] * 2, None, [None, None], ws, n, ys,
+                             torch.empty(8, dtype=torch.int64, device="cuda"))
+    del w

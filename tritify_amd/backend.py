@@ -140,6 +140,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_moe_route": (_I, [_I, _P, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
         "kt_hip_ref_moe_combine": (_I, [_I, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I, _P, _P, _P]),
         "kt_hip_ref_moe_bucket": (_I, [_I, _P, _I64, _I, _I64, _P, _P, _P, _P]),
+        "kt_hip_quant_linear_multi": (_I, [_I, _P, _I64, _I64, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P,
+                                            _SZ, _P, _P, _P]),
+        "kt_hip_quant_linear_multi_align": (_I64, [_I64, _I64, _I]),
         "kt_hip_pack_planes_tiled_bytes": (_SZ, [_I64, _I64, _I]),
         "kt_hip_pack_planes_tiled": (_I, [_I, _P, _I64, _I64, _I, _P, _P]),
         "kt_hip_ref_merge_rows_workspace": (_SZ, [_I64]),
@@ -391,6 +394,27 @@ def quant_linear(x_dev, rows: int, in_f: int, xs_dev, w_planes_dev, pw: int, out
                                   ws_bytes, _ptr(y_dev), _ptr(os_dev), _stream(stream)),
         "quant linear",
     )
+
+
+def quant_linear_multi_align(rows: int, out_f: int, pw: int) -> int:
+    """The multiple of which every boundary between the calls of quant_linear_multi must be."""
+    return lib().kt_hip_quant_linear_multi_align(rows, out_f, pw)
+
+
+def quant_linear_multi(x_dev, rows: int, in_f: int, xs_dev, seg_out, w_planes_dev, pw: int, w_scales, bias_dev,
+                       b_scales, ws_dev, ws_bytes: int, y_devs, os_dev, stream=None, dev: int = 0) -> None:
+    """Several QuantLinear::forward_int calls on one x, computed together (their weights stacked by rows in
+    w_planes_dev): y_devs[g] and record os_dev[g] equal call g's own. b_scales[g]: None where call g has no bias
+    (bias_dev: None, or the stacked bias codes with zeros there)."""
+    n = len(seg_out)
+    arr = lambda t, v: (t * n)(*v)  # noqa: E731
+    hb = [0 if (bias_dev is None or b is None) else 1 for b in b_scales]
+    check(lib().kt_hip_quant_linear_multi(
+        dev, _ptr(x_dev), rows, in_f, _ptr(xs_dev), n, arr(C.c_int64, [int(v) for v in seg_out]), _ptr(w_planes_dev),
+        pw, arr(C.c_int64, [int(w[0]) for w in w_scales]), arr(C.c_int32, [int(w[1]) for w in w_scales]),
+        _ptr(bias_dev), arr(C.c_int, hb), arr(C.c_int64, [int(b[0]) if b else 0 for b in b_scales]),
+        arr(C.c_int32, [int(b[1]) if b else 0 for b in b_scales]), _ptr(ws_dev), ws_bytes,
+        arr(C.c_void_p, [_ptr(y) for y in y_devs]), _ptr(os_dev), _stream(stream)), "quant linear multi")
 
 
 def quant_linear_noalloc(x_dev, rows: int, in_f: int, xs_dev, w_planes_dev, pw: int, out_f: int, w_scale,

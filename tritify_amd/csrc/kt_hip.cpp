@@ -242,6 +242,41 @@ int kt_hip_quant_linear(int dev, const int32_t* x_dev, int64_t rows, int64_t in_
                                         (hipStream_t)stream);
 }
 
+int kt_hip_quant_linear_multi(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f, const kt_hip_qscale* xs_dev,
+                              int nseg, const int64_t* seg_out, const int8_t* w_planes_dev, int pw,
+                              const int64_t* w_mant, const int32_t* w_shift, const int64_t* bias_dev,
+                              const int* has_bias, const int64_t* b_mant, const int32_t* b_shift, void* ws_dev,
+                              size_t ws_bytes, int32_t* const* y_devs, kt_hip_qscale* os_dev, void* stream) {
+    if (nseg < 1 || nseg > KT_QL_MAX_SEGMENTS || !seg_out || !w_mant || !w_shift || !y_devs || rows < 1 ||
+        in_f < 1 || (pw != 1 && pw != 3 && pw != 5) || (bias_dev && (!has_bias || !b_mant || !b_shift)))
+        return (int)hipErrorInvalidValue;
+    int64_t out_f = 0;
+    for (int g = 0; g < nseg; g++) {
+        if (seg_out[g] < 1 || w_mant[g] < 0 || (bias_dev && has_bias[g] && b_mant[g] < 0) || !y_devs[g])
+            return (int)hipErrorInvalidValue;
+        out_f += seg_out[g];
+    }
+    const int64_t kp = kp_of(in_f);
+    if (rows * kp >= ((int64_t)1 << 31) || rows * out_f >= ((int64_t)1 << 31) || kp > INT_MAX)
+        return (int)hipErrorInvalidValue;
+    if (!x_dev || !xs_dev || !w_planes_dev || !ws_dev || !os_dev ||
+        ws_bytes < kt_hip_quant_linear_workspace(rows, in_f, out_f, nullptr))
+        return (int)hipErrorInvalidValue;
+    // every CTA of the digit GEMM covers columns of one call: each boundary a multiple of its CTA's columns
+    const int64_t cols = kt::plane_gemm_cta_cols(3, pw, (int)rows, (int)out_f);
+    for (int64_t g = 0, at = 0; g + 1 < nseg; g++)
+        if ((at += seg_out[g]) % cols) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_quant_linear_multi(x_dev, rows, in_f, xs_dev, w_planes_dev, pw, nseg, seg_out, w_mant,
+                                              w_shift, bias_dev, has_bias, b_mant, b_shift, flush_of(3, pw), ws_dev,
+                                              y_devs, os_dev, (hipStream_t)stream);
+}
+
+int64_t kt_hip_quant_linear_multi_align(int64_t rows, int64_t out_f, int pw) {
+    if (rows < 1 || out_f < 1 || rows > INT_MAX || out_f > INT_MAX || (pw != 1 && pw != 3 && pw != 5)) return 0;
+    return kt::plane_gemm_cta_cols(3, pw, (int)rows, (int)out_f);
+}
+
 int kt_hip_quant_linear_noalloc(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f,
                                 const kt_hip_qscale* xs_dev, const int8_t* w_planes_dev, int pw, int64_t out_f,
                                 int64_t w_mant, int32_t w_shift, const int64_t* bias_dev, int64_t b_mant,

@@ -13,10 +13,14 @@ hipError_t launch_pack_planes(const int32_t* codes, int64_t rows, int64_t k, int
 hipError_t launch_w12_pack(const int32_t* codes, int64_t n, int64_t k, int64_t ilv, int8_t* lo, uint8_t* nib,
                            hipStream_t s);
 struct QlState;
+struct QlSeg;
+// ql: one state, or (seg non-null) seg->n states, one per output segment (each CTA's columns in one segment).
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
                              int k0, int k1, int accumulate, int drop_top, hipStream_t s,
                              const int64_t* ql_bias = nullptr, QlState* ql = nullptr, int splits = 1,
-                             unsigned* tile_cnt = nullptr);
+                             unsigned* tile_cnt = nullptr, const QlSeg* seg = nullptr);
+// The output columns each CTA of launch_plane_gemm covers (segment boundaries must be multiples of it).
+int plane_gemm_cta_cols(int px, int pw, int M, int N);
 // How many runs of k the digit-plane GEMM of [k0, k1) splits into (1 unless its tiles leave CUs idle); a split
 // launch needs y zeroed, one zeroed counter per tile (the grid's tiles: at most 128) and accumulate = 0.
 int plane_gemm_splits(int px, int pw, int M, int N, int k0, int k1);
@@ -76,6 +80,14 @@ hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* n
                              const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift, int8_t* y,
                              int ystride, hipStream_t s);
 size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]);
+// Several QuantLinear calls on one x (seg_out[g] output columns each, weights side by side in wb): one x pass, one
+// digit GEMM, each call's own requantization into y[g] with record os[g].
+hipError_t launch_quant_linear_multi(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
+                                     const int8_t* wb, int pw, int nseg, const int64_t* seg_out,
+                                     const int64_t* w_mant, const int32_t* w_shift, const int64_t* bias,
+                                     const int* has_bias, const int64_t* b_mant, const int32_t* b_shift,
+                                     int64_t flush_k, void* ws, int32_t* const* y, kt_hip_qscale* os,
+                                     hipStream_t s);
 hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
                                const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
                                const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,

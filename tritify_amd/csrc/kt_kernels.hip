@@ -92,8 +92,8 @@ template <int PX, int PW, int WTM, int WTN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_waves<PX, PW, WTM, WTN>(), 2))) void plane_gemm_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
                                                          int64_t* __restrict__ y, int M, int N, int kp, int k0,
                                                          int k1, int accumulate, int drop_top,
-                                                         const int64_t* __restrict__ ql_bias, QlState* ql,
-                                                         unsigned* __restrict__ tile_cnt) {
+                                                         const int64_t* __restrict__ ql_bias, QlState* ql_all,
+                                                         unsigned* __restrict__ tile_cnt, QlSeg seg) {
     constexpr int BK = 64, CPR = BK / 16;
     constexpr int BM = 64 * WTM, BN = 64 * WTN;
     constexpr int NG = PX + PW - 1;
@@ -106,6 +106,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_
     const int wm = wave >> 1, wn = wave & 1;
     const int tiles_n = (N + BN - 1) / BN;
     const int m0 = (blockIdx.x / tiles_n) * BM, n0 = (blockIdx.x % tiles_n) * BN;
+    QlState* ql = ql_all ? ql_all + ql_seg_of(seg, n0) : nullptr;  // this tile's call
     const size_t xplane = (size_t)M * kp, wplane = (size_t)N * kp;
 
     v16i acc[NG][WTM][WTN];
@@ -295,10 +296,12 @@ template <int PX, int PW, int MM>
 __global__ __launch_bounds__(256) void plane_skinny_kernel(const int8_t* __restrict__ xa, const int8_t* __restrict__ wb,
                                                            int64_t* __restrict__ y, int M, int N, int kp, int k0,
                                                            int k1, int accumulate, int drop_top,
-                                                           const int64_t* __restrict__ ql_bias, QlState* ql) {
+                                                           const int64_t* __restrict__ ql_bias, QlState* ql_all,
+                                                           QlSeg seg) {
     constexpr int NG = PX + PW - 1;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = ((int)blockIdx.x * 4 + wave) * PS_CPW;  // the wave's first column
+    QlState* ql = ql_all ? ql_all + ql_seg_of(seg, (int)blockIdx.x * 4 * PS_CPW) : nullptr;  // this CTA's call
     const size_t xplane = (size_t)M * kp, wplane = (size_t)N * kp;
     const int nch = (k1 - k0) / 16;
     int acc[PS_CPW][MM][NG];
@@ -1025,20 +1028,27 @@ int plane_gemm_splits(int px, int pw, int M, int N, int k0, int k1) {
     return (nk + per - 1) / per;  // every run of k-tiles is non-empty
 }
 
+int plane_gemm_cta_cols(int px, int pw, int M, int N) {
+    if (M <= KT_PLANE_SKINNY_M) return 4 * PS_CPW;
+    int wtm, wtn;
+    plane_gemm_shape(px, pw, M, N, wtm, wtn);
+    return 64 * wtn;
+}
+
 template <int PX, int PW>
 static hipError_t plane_gemm_px_pw(const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp, int k0,
                                    int k1, int accumulate, int drop_top, const int64_t* ql_bias, QlState* ql,
-                                   int splits, unsigned* cnt, hipStream_t s) {
+                                   int splits, unsigned* cnt, const QlSeg& seg, hipStream_t s) {
     if (M <= KT_PLANE_SKINNY_M) {
         if (splits != 1) return hipErrorInvalidValue;
         const dim3 grid((unsigned)ceil_div(N, 4 * PS_CPW));
         if (M == 1)
             plane_skinny_kernel<PX, PW, 1><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
-                                                                     drop_top, ql_bias, ql);
+                                                                     drop_top, ql_bias, ql, seg);
         else
             plane_skinny_kernel<PX, PW, KT_PLANE_SKINNY_M><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1,
                                                                                      accumulate, drop_top, ql_bias,
-                                                                                     ql);
+                                                                                     ql, seg);
         return hipGetLastError();
     }
     int wtm, wtn;
@@ -1047,16 +1057,19 @@ static hipError_t plane_gemm_px_pw(const int8_t* xa, const int8_t* wb, int64_t* 
     constexpr int NG = PX + PW - 1, WTM = NG <= 2 ? 2 : 1;
     if (wtn == 1)
         plane_gemm_kernel<PX, PW, WTM, 1><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
-                                                                     drop_top, ql_bias, ql, cnt);
+                                                                     drop_top, ql_bias, ql, cnt, seg);
     else if constexpr (NG <= 5)
         plane_gemm_kernel<PX, PW, WTM, 2><<<grid, dim3(256), 0, s>>>(xa, wb, y, M, N, kp, k0, k1, accumulate,
-                                                                     drop_top, ql_bias, ql, cnt);
+                                                                     drop_top, ql_bias, ql, cnt, seg);
     return hipGetLastError();
 }
 
 hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb, int64_t* y, int M, int N, int kp,
                              int k0, int k1, int accumulate, int drop_top, hipStream_t s, const int64_t* ql_bias,
-                             QlState* ql, int splits, unsigned* tile_cnt) {
+                             QlState* ql, int splits, unsigned* tile_cnt, const QlSeg* seg) {
+    const QlSeg one{1, {0, N, N, N, N}};
+    const QlSeg& sg = seg ? *seg : one;
+    if (sg.n < 1 || sg.n > KT_QL_MAX_SEG) return hipErrorInvalidValue;
     if (M <= 0 || N <= 0 || k1 <= k0) return hipSuccess;
     if ((k0 % 64) || (k1 % 64) || k1 > kp || ceil_div(M, 64) * ceil_div(N, 64) > INT32_MAX) return hipErrorInvalidValue;
     if (splits != 1 && (splits != plane_gemm_splits(px, pw, M, N, k0, k1) || !tile_cnt || accumulate))
@@ -1064,7 +1077,7 @@ hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb,
 #define KT_CASE(a, b) \
     if (px == a && pw == b)                                                                                  \
         return plane_gemm_px_pw<a, b>(xa, wb, y, M, N, kp, k0, k1, accumulate, drop_top, ql_bias, ql, splits, \
-                                      tile_cnt, s);
+                                      tile_cnt, sg, s);
     KT_CASE(1, 1) KT_CASE(1, 3) KT_CASE(1, 5) KT_CASE(3, 1) KT_CASE(3, 3) KT_CASE(3, 5) KT_CASE(5, 1) KT_CASE(5, 3)
     KT_CASE(5, 5)
 #undef KT_CASE

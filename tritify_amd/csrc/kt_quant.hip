@@ -113,13 +113,24 @@ __device__ inline void ql_fetch4(const int32_t* __restrict__ x, int64_t r, int64
 // qx = quant_to(x, xmax) for 4 consecutive columns per thread, split into planes [3][rows][kp]; padding columns and
 // the xmax == 0 case give zero digits. |qx| <= WLEVELS < 127 * (1 + 256 + 65536), so 3 balanced digits hold it.
 // xmax is taken over the nx values of x (the whole image for a convolution).
+// The weight and bias Scales of each output segment of a call (QlSeg; one segment for a single QuantLinear).
+struct QlScales {
+    int64_t w_mant[KT_QL_MAX_SEG], b_mant[KT_QL_MAX_SEG];
+    int32_t w_shift[KT_QL_MAX_SEG], b_shift[KT_QL_MAX_SEG];
+    int has_bias[KT_QL_MAX_SEG];
+};
+// Each segment's output codes and record.
+struct QlOut {
+    int32_t* y[KT_QL_MAX_SEG];
+    kt_hip_qscale* os[KT_QL_MAX_SEG];
+};
+
 template <bool CONV>
 __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __restrict__ x, int64_t nx,
                                                               int64_t rows, int64_t in, int64_t kp, ConvGeom geom,
                                                               const uint32_t* __restrict__ part, int nparts,
-                                                              const kt_hip_qscale* __restrict__ xs, int64_t w_mant,
-                                                              int32_t w_shift, int has_bias, int64_t b_mant,
-                                                              int32_t b_shift, QlState* __restrict__ st,
+                                                              const kt_hip_qscale* __restrict__ xs, QlSeg seg,
+                                                              QlScales sc, QlState* __restrict__ st,
                                                               int8_t* __restrict__ xa, uint64_t* __restrict__ zacc,
                                                               int64_t nzacc, uint32_t* __restrict__ zcnt,
                                                               int nzcnt) {
@@ -140,25 +151,28 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
         }
     }
     m = block_max(m, red);
-    if (blockIdx.x == 0 && threadIdx.x < KT_QL_YSLOTS) st->ymax[threadIdx.x].v = 0;
-    if (blockIdx.x == 0 && threadIdx.x == 0) {  // the call's record, for the GEMM epilogue and ql_requant
+    if (blockIdx.x == 0 && threadIdx.x < KT_QL_YSLOTS * seg.n)
+        st[threadIdx.x / KT_QL_YSLOTS].ymax[threadIdx.x % KT_QL_YSLOTS].v = 0;
+    if (blockIdx.x == 0 && (int)threadIdx.x < seg.n) {  // each segment's record, for the GEMM epilogue and ql_requant
+        const int g = threadIdx.x;
         QlState s{};
         s.xmax = (int64_t)m;
         if (m == 0) {
             s.mode = 1;
         } else {
             const Sc c = sc_mul(sc_mul(from_ratio((u128)m, (u128)WLEVELS), Sc{xs->mant, xs->shift}),
-                                Sc{w_mant, w_shift});
+                                Sc{sc.w_mant[g], sc.w_shift[g]});
             s.c_mant = c.mant, s.c_shift = c.shift;
             if (c.mant == 0) {
                 s.mode = 2;
-            } else if (has_bias) {
-                const Sc f = sc_mul(Sc{b_mant, b_shift}, sc_recip(c));
+            } else if (sc.has_bias[g]) {
+                const Sc f = sc_mul(Sc{sc.b_mant[g], sc.b_shift[g]}, sc_recip(c));
                 s.f_mant = f.mant, s.f_shift = f.shift;
             }
         }
-        st->xmax = s.xmax, st->c_mant = s.c_mant, st->f_mant = s.f_mant;
-        st->c_shift = s.c_shift, st->f_shift = s.f_shift, st->mode = s.mode;
+        QlState* q = st + g;
+        q->xmax = s.xmax, q->c_mant = s.c_mant, q->f_mant = s.f_mant;
+        q->c_shift = s.c_shift, q->f_shift = s.f_shift, q->mode = s.mode;
     }
     const int64_t quads = rows * (kp / 4);
     const int64_t xmax = (int64_t)m, half = xmax / 2;
@@ -197,40 +211,51 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
 
 __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* __restrict__ acc, int64_t n,
                                                                 int64_t out, const int64_t* __restrict__ bias,
-                                                                const QlState* __restrict__ st,
-                                                                int64_t b_mant, int32_t b_shift,
-                                                                int32_t* __restrict__ y,
-                                                                kt_hip_qscale* __restrict__ os) {
-    int64_t ymax = 0;
+                                                                const QlState* __restrict__ st, QlSeg seg,
+                                                                QlScales sc, QlOut yo) {
+    __shared__ int64_t s_ymax[KT_QL_MAX_SEG];
+    __shared__ int32_t s_mode[KT_QL_MAX_SEG];
+    if ((int)threadIdx.x < seg.n) {  // each segment's output maximum, mode and (CTA 0) record
+        const int g = threadIdx.x;
+        const QlState* q = st + g;
+        int64_t ymax = 0;
 #pragma unroll
-    for (int i = 0; i < KT_QL_YSLOTS; i++) ymax = (int64_t)st->ymax[i].v > ymax ? (int64_t)st->ymax[i].v : ymax;
-    const int mode = st->mode;
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        kt_hip_qscale o{};
-        o.xmax = st->xmax;
-        if (mode == 1) {
-            if (bias) o.mant = b_mant, o.shift = b_shift;
-        } else if (mode == 0 && ymax > 0) {
-            const Sc s = sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{st->c_mant, st->c_shift});
-            o.mant = s.mant, o.shift = s.shift, o.ymax = ymax;
+        for (int i = 0; i < KT_QL_YSLOTS; i++) ymax = (int64_t)q->ymax[i].v > ymax ? (int64_t)q->ymax[i].v : ymax;
+        const int mode = q->mode;
+        s_ymax[g] = ymax, s_mode[g] = mode;
+        if (blockIdx.x == 0) {
+            kt_hip_qscale o{};
+            o.xmax = q->xmax;
+            if (mode == 1) {
+                if (sc.has_bias[g]) o.mant = sc.b_mant[g], o.shift = sc.b_shift[g];
+            } else if (mode == 0 && ymax > 0) {
+                const Sc s2 = sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{q->c_mant, q->c_shift});
+                o.mant = s2.mant, o.shift = s2.shift, o.ymax = ymax;
+            }
+            *yo.os[g] = o;
         }
-        *os = o;
     }
-    const u128 halfd = (u128)(uint64_t)(ymax / 2);
+    __syncthreads();
     const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x, step = (int64_t)gridDim.x * QL_THREADS;
-    const int64_t dstep = step % out;
-    int64_t o = i0 % out;  // i % out, advanced incrementally
-    for (int64_t i = i0; i < n; i += step, o = o + dstep >= out ? o + dstep - out : o + dstep) {
-        int32_t r = 0;
+    const int64_t dstep = step % out, rstep = step / out;
+    int64_t o = i0 % out, r = i0 / out;  // (row, column) of i, advanced incrementally
+    for (int64_t i = i0; i < n; i += step, r += rstep, o += dstep) {
+        if (o >= out) o -= out, r++;
+        const int g = ql_seg_of(seg, (int)o);
+        const int64_t ymax = s_ymax[g];
+        const int mode = s_mode[g];
+        int32_t v32 = 0;
         if (mode == 1) {
-            r = bias ? (int32_t)bias[o] : 0;
+            v32 = sc.has_bias[g] && bias ? (int32_t)bias[o] : 0;
         } else if (mode == 0 && ymax > 0) {
             const int64_t v = acc[i];
             const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
-            const uint64_t q = udiv_small_q(((u128)a << 28) + halfd, ymax);  // requant_dyn(v, 2^28, ymax): q <= 2^28
-            r = (int32_t)(v < 0 ? 0 - q : q);
+            // requant_dyn(v, 2^28, ymax): q <= 2^28
+            const uint64_t q = udiv_small_q(((u128)a << 28) + (u128)(uint64_t)(ymax / 2), ymax);
+            v32 = (int32_t)(v < 0 ? 0 - q : q);
         }
-        y[i] = r;
+        const int64_t w = seg.col0[g + 1] - seg.col0[g];
+        yo.y[g][r * w + (o - seg.col0[g])] = v32;
     }
 }
 
@@ -279,7 +304,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_conv_kernel(const int64
 size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]) {
     const size_t kp = (size_t)((in + 63) / 64 * 64);
     const size_t sizes[KT_QL_WS_PARTS] = {3 * (size_t)rows * kp, (size_t)rows * (size_t)out * 8, KT_QL_PARTS * 4,
-                                          KT_QL_PARTS * 8, sizeof(QlState)};
+                                          KT_QL_PARTS * 8, KT_QL_MAX_SEG * sizeof(QlState)};
     size_t at = 0;
     for (int i = 0; i < KT_QL_WS_PARTS; i++) {
         off[i] = at;
@@ -318,11 +343,13 @@ static int grid_for(int64_t n, int64_t per_thread) {
 
 // The four passes of QuantLinear::forward_int, or of Conv2d::forward_int when geom is non-null (the image x of
 // geom->ci x h x w values read as its im2col rows; the output channel-major, zeros at Scale::ZERO for an all-zero
-// image).
+// image). seg splits the out columns into the outputs of several calls on the same x (their own weight and bias
+// Scales in sc, their own maximum, requantization and record): the x pass is shared and the digit GEMM runs once
+// over the side-by-side weights.
 static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, const ConvGeom* geom,
-                                 const kt_hip_qscale* xs, const int8_t* wb, int pw, int64_t out, int64_t w_mant,
-                                 int32_t w_shift, const int64_t* bias, int64_t b_mant, int32_t b_shift,
-                                 int64_t flush_k, void* ws, int32_t* y, kt_hip_qscale* os, hipStream_t s) {
+                                 const kt_hip_qscale* xs, const int8_t* wb, int pw, int64_t out, const QlSeg& seg,
+                                 const QlScales& sc, const int64_t* bias, int64_t flush_k, void* ws, const QlOut& yo,
+                                 hipStream_t s) {
     size_t off[KT_QL_WS_PARTS];
     ql_workspace_bytes(rows, in, out, off);
     char* base = (char*)ws;
@@ -345,47 +372,82 @@ static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, con
     const int64_t nzacc = splits > 1 ? n : 0;
     const int gq = grid_for(rows * kp / 4, 1);
     if (geom)
-        ql_quant_kernel<true><<<gq, QL_THREADS, 0, s>>>(x, nx, rows, in, kp, *geom, part_x, gx, xs, w_mant, w_shift,
-                                                        bias != nullptr, b_mant, b_shift, st, xa, zacc, nzacc,
-                                                        tile_cnt, ntiles);
+        ql_quant_kernel<true><<<gq, QL_THREADS, 0, s>>>(x, nx, rows, in, kp, *geom, part_x, gx, xs, seg, sc, st, xa,
+                                                        zacc, nzacc, tile_cnt, ntiles);
     else
-        ql_quant_kernel<false><<<gq, QL_THREADS, 0, s>>>(x, nx, rows, in, kp, ConvGeom{}, part_x, gx, xs, w_mant,
-                                                         w_shift, bias != nullptr, b_mant, b_shift, st, xa, zacc,
-                                                         nzacc, tile_cnt, ntiles);
+        ql_quant_kernel<false><<<gq, QL_THREADS, 0, s>>>(x, nx, rows, in, kp, ConvGeom{}, part_x, gx, xs, seg, sc, st,
+                                                         xa, zacc, nzacc, tile_cnt, ntiles);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     for (int64_t k0 = 0; k0 < kp; k0 += flush_k) {
         const int64_t k1 = kp - k0 < flush_k ? kp : k0 + flush_k;
         const bool last = k1 == kp;
         e = launch_plane_gemm(3, pw, xa, wb, acc, (int)rows, (int)out, (int)kp, (int)k0, (int)k1, k0 > 0, 0, s,
-                              last ? bias : nullptr, last ? st : nullptr, splits, tile_cnt);
+                              last ? bias : nullptr, last ? st : nullptr, splits, tile_cnt, &seg);
         if (e != hipSuccess) return e;
     }
     if (geom) {
         const dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((out + 63) / 64));
-        ql_requant_conv_kernel<<<grid, QL_THREADS, 0, s>>>(acc, rows, out, st, y, os);
+        ql_requant_conv_kernel<<<grid, QL_THREADS, 0, s>>>(acc, rows, out, st, yo.y[0], yo.os[0]);
         return hipGetLastError();
     }
     // one output per thread for short outputs (a decode row: its divisions then run side by side, not 8 in a row)
-    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 2), QL_THREADS, 0, s>>>(acc, n, out, bias, st, b_mant, b_shift,
-                                                                           y, os);
+    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 2), QL_THREADS, 0, s>>>(acc, n, out, bias, st, seg, sc, yo);
     return hipGetLastError();
+}
+
+static void ql_one(int64_t out, int64_t w_mant, int32_t w_shift, const int64_t* bias, int64_t b_mant,
+                   int32_t b_shift, int32_t* y, kt_hip_qscale* os, QlSeg& seg, QlScales& sc, QlOut& yo) {
+    seg = QlSeg{1, {0, (int)out, (int)out, (int)out, (int)out}};
+    sc = QlScales{};
+    sc.w_mant[0] = w_mant, sc.w_shift[0] = w_shift, sc.has_bias[0] = bias != nullptr;
+    sc.b_mant[0] = b_mant, sc.b_shift[0] = b_shift;
+    yo = QlOut{};
+    yo.y[0] = y, yo.os[0] = os;
 }
 
 hipError_t launch_quant_linear(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
                                const int8_t* wb, int pw, int64_t out, int64_t w_mant, int32_t w_shift,
                                const int64_t* bias, int64_t b_mant, int32_t b_shift, int64_t flush_k, void* ws,
                                int32_t* y, kt_hip_qscale* os, hipStream_t s) {
-    return launch_ql_impl(x, rows, in, nullptr, xs, wb, pw, out, w_mant, w_shift, bias, b_mant, b_shift, flush_k, ws,
-                          y, os, s);
+    QlSeg seg;
+    QlScales sc;
+    QlOut yo;
+    ql_one(out, w_mant, w_shift, bias, b_mant, b_shift, y, os, seg, sc, yo);
+    return launch_ql_impl(x, rows, in, nullptr, xs, wb, pw, out, seg, sc, bias, flush_k, ws, yo, s);
+}
+
+hipError_t launch_quant_linear_multi(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,
+                                     const int8_t* wb, int pw, int nseg, const int64_t* seg_out,
+                                     const int64_t* w_mant, const int32_t* w_shift, const int64_t* bias,
+                                     const int* has_bias, const int64_t* b_mant, const int32_t* b_shift,
+                                     int64_t flush_k, void* ws, int32_t* const* y, kt_hip_qscale* os,
+                                     hipStream_t s) {
+    QlSeg seg{nseg, {0, 0, 0, 0, 0}};
+    QlScales sc{};
+    QlOut yo{};
+    int64_t at = 0;
+    for (int g = 0; g < nseg; g++) {
+        seg.col0[g] = (int)at;
+        at += seg_out[g];
+        sc.w_mant[g] = w_mant[g], sc.w_shift[g] = w_shift[g], sc.has_bias[g] = bias && has_bias[g];
+        sc.b_mant[g] = sc.has_bias[g] ? b_mant[g] : 0, sc.b_shift[g] = sc.has_bias[g] ? b_shift[g] : 0;
+        yo.y[g] = y[g], yo.os[g] = os + g;
+    }
+    for (int g = nseg; g <= KT_QL_MAX_SEG; g++) seg.col0[g] = (int)at;
+    return launch_ql_impl(x, rows, in, nullptr, xs, wb, pw, at, seg, sc, bias, flush_k, ws, yo, s);
 }
 
 hipError_t launch_ref_conv2d(const int32_t* x, const ConvGeom& g, const kt_hip_qscale* xs, const int8_t* wb, int pw,
                              int64_t co, int64_t w_mant, int32_t w_shift, const int64_t* bias, int64_t b_mant,
                              int32_t b_shift, int64_t flush_k, void* ws, int32_t* y, kt_hip_qscale* os,
                              hipStream_t s) {
-    return launch_ql_impl(x, (int64_t)g.oh * g.ow, (int64_t)g.ci * g.kh * g.kw, &g, xs, wb, pw, co, w_mant, w_shift,
-                          bias, b_mant, b_shift, flush_k, ws, y, os, s);
+    QlSeg seg;
+    QlScales sc;
+    QlOut yo;
+    ql_one(co, w_mant, w_shift, bias, b_mant, b_shift, y, os, seg, sc, yo);
+    return launch_ql_impl(x, (int64_t)g.oh * g.ow, (int64_t)g.ci * g.kh * g.kw, &g, xs, wb, pw, co, seg, sc, bias,
+                          flush_k, ws, yo, s);
 }
 
 }  // namespace kt

@@ -208,6 +208,61 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
     __shared__ ScIdx redsc[RD_THREADS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const Sc xs = rec_sc(xs_rec), gs{g_mant, g_shift}, eps{e_mant, e_shift};
+    constexpr int RD_NV = 8;
+    if (rows == 1 && dim <= RD_THREADS * RD_NV) {
+        // one row (the decode step): its values and gammas loaded once by every thread, all in flight together, the
+        // sum of squares reduced across the CTA; the same integers as the general path below
+        int32_t xv[RD_NV], gv[RD_NV];
+#pragma unroll
+        for (int k = 0; k < RD_NV; k++) {
+            const int i = threadIdx.x + RD_THREADS * k, ic = i < dim ? i : dim - 1;
+            xv[k] = x[ic], gv[k] = g[ic];
+        }
+        uint64_t hi = 0, lo = 0;
+#pragma unroll
+        for (int k = 0; k < RD_NV; k++) {
+            if ((int)threadIdx.x + RD_THREADS * k >= dim) xv[k] = 0;
+            const int64_t v = xv[k];
+            const uint64_t sq = (uint64_t)(v * v), t = lo + sq;
+            hi += t < lo, lo = t;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t ohi = __shfl_xor(hi, o, 64), olo = __shfl_xor(lo, o, 64), t = lo + olo;
+            hi += ohi + (t < lo), lo = t;
+        }
+        __shared__ uint64_t sq2[RD_WAVES][2];
+        if (lane == 0) sq2[wave][0] = hi, sq2[wave][1] = lo;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            u128 ss = 0;
+            for (int w = 0; w < RD_WAVES; w++) ss += ((u128)sq2[w][0] << 64) | sq2[w][1];
+            const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xs), xs);
+            const Sc denom = sc_add(mean_sq, eps);
+            const Sc inv = denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom);
+            const Sc c0 = sc_mul(sc_mul(xs, inv), gs);
+            crow[0] = c0;  // the largest of one row's factors is that factor
+            frow[0] = c0.mant != 0 ? sc_mul(c0, sc_recip(c0)) : Sc{0, 0};
+        }
+        __syncthreads();
+        const Sc cc = crow[0], f0 = frow[0];
+        int64_t hv[RD_NV];
+        int64_t m = 0;
+#pragma unroll
+        for (int k = 0; k < RD_NV; k++) {
+            hv[k] = cc.mant != 0 ? sc_apply(f0, (int64_t)xv[k] * (int64_t)gv[k]) : 0;
+            m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
+        }
+        const int64_t gmax = block_max_i64(m, red);
+#pragma unroll
+        for (int k = 0; k < RD_NV; k++) {
+            const int i = threadIdx.x + RD_THREADS * k;
+            if (i < dim) y[i] = gmax == 0 ? 0 : requant_dyn_dev(hv[k], gmax);
+        }
+        if (threadIdx.x == 0)
+            put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
+        return;
+    }
     // each row's exact sum of squares by one wave, its factor c_r = xs * rsqrt(mean_sq + eps) * gs by that wave's
     // first lane (the rows' Scale arithmetic runs side by side)
     for (int r = wave; r < rows; r += RD_WAVES) {
@@ -475,15 +530,39 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
             if (tid < hn) hsc[h0 + tid] = Sc{0, 0};
             continue;
         }
-        for (int it = wave; it < hn * steps; it += RD_WAVES) {
-            const int h = it / steps, j = it - h * steps, kv = (h0 + h) / group;
-            const int32_t* kr = a.kc + (size_t)j * kstride + kv * hd;
-            const int32_t* qh = QD + (h0 + h) * hd;
-            int64_t dot = 0;
-            for (int e = lane; e < hd; e += 64) dot = wadd(dot, wmul(qh[e], kr[e]));
+        // RD_SU items per wave at a time, every cached k row of them loaded before the first product (an item past
+        // the end re-reads the last one and is dropped)
+        constexpr int RD_SU = 8;
+        const int items = hn * steps;
+        for (int it0 = wave; it0 < items; it0 += RD_WAVES * RD_SU) {
+            int64_t dot[RD_SU];
+            int hh[RD_SU], jj[RD_SU];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) dot = wadd(dot, __shfl_xor(dot, o, 64));
-            if (lane == 0) S[(size_t)h * a.max_seq + j] = sc_apply(F[j], dot);
+            for (int u = 0; u < RD_SU; u++) {
+                const int it = it0 + u * RD_WAVES, itc = it < items ? it : items - 1;
+                hh[u] = itc / steps, jj[u] = itc - hh[u] * steps, dot[u] = 0;
+            }
+            for (int e = lane; e < hd; e += 64) {
+                int32_t kk[RD_SU];
+#pragma unroll
+                for (int u = 0; u < RD_SU; u++)
+                    kk[u] = a.kc[(size_t)jj[u] * kstride + ((h0 + hh[u]) / group) * hd + e];
+#pragma unroll
+                for (int u = 0; u < RD_SU; u++) dot[u] = wadd(dot[u], wmul(QD[(h0 + hh[u]) * hd + e], kk[u]));
+            }
+#pragma unroll
+            for (int u = 0; u < RD_SU; u++) {
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) dot[u] = wadd(dot[u], __shfl_xor(dot[u], o, 64));
+            }
+            if (lane < RD_SU) {  // lane u stores item u (every lane holds every item's full sum)
+                int64_t d = dot[0];
+#pragma unroll
+                for (int u = 1; u < RD_SU; u++) d = lane == u ? dot[u] : d;
+                const int it = it0 + lane * RD_WAVES;
+                const int h = it / steps, j = it - h * steps;
+                if (it < items) S[(size_t)h * a.max_seq + j] = sc_apply(F[j], d);
+            }
         }
         __syncthreads();
         for (int h = wave; h < hn; h += RD_WAVES) {
@@ -515,7 +594,20 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
             if (hsum[h] > 0) {
                 const int64_t* sh = S + (size_t)h * a.max_seq;
                 const int32_t* vcol = a.vc + kv * hd + dd;
-                for (int j = 0; j < steps; j++) acc = wadd(acc, wmul(sh[j], sc_apply(VF[j], vcol[(size_t)j * kstride])));
+                // RD_PU cached v values loaded before their products (a step past the end re-reads the last one
+                // and is dropped)
+                constexpr int RD_PU = 8;
+                for (int j0 = 0; j0 < steps; j0 += RD_PU) {
+                    int32_t vv[RD_PU];
+#pragma unroll
+                    for (int u = 0; u < RD_PU; u++) {
+                        const int j = j0 + u < steps ? j0 + u : steps - 1;
+                        vv[u] = vcol[(size_t)j * kstride];
+                    }
+#pragma unroll
+                    for (int u = 0; u < RD_PU; u++)
+                        if (j0 + u < steps) acc = wadd(acc, wmul(sh[j0 + u], sc_apply32(VF[j0 + u], vv[u])));
+                }
             }
             HO[(h0 + h) * hd + dd] = acc;
         }
@@ -523,15 +615,15 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     }
 
     // 4. one scale for the concatenated heads
+    __shared__ Sc s_cinv;
     if (tid == 0) {
         Sc common{0, 0};
         for (int h = 0; h < nh; h++) common = sc_ge(hsc[h], common) ? hsc[h] : common;
         par[3] = common;
-        if (common.mant != 0) {
-            const Sc cinv = sc_recip(common);
-            for (int h = 0; h < nh; h++) hsc[h] = sc_mul(hsc[h], cinv);
-        }
+        if (common.mant != 0) s_cinv = sc_recip(common);
     }
+    __syncthreads();
+    if (tid < nh && par[3].mant != 0) hsc[tid] = sc_mul(hsc[tid], s_cinv);  // the heads' factors side by side
     __syncthreads();
     const Sc common = par[3];
     int64_t m = 0;

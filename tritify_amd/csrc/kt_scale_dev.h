@@ -140,6 +140,20 @@ __device__ inline int64_t sc_apply(Sc a, int64_t value) {
     return (int64_t)(prod >= 0 ? (prod + half) >> a.shift : -(((-prod) + half) >> a.shift));
 }
 
+// Scale::apply of an int32 code with 64-bit arithmetic where that is exact: |mant| < 2^32 and 0 <= shift <= 63 keep
+// |v * mant| below 2^63 and its sum with the rounding addend 2^(shift - 1) below 2^64 (unsigned); other Scales go
+// through the i128 sc_apply. The same rounding, half away from zero.
+__device__ inline int64_t sc_apply32(Sc a, int32_t v) {
+    if (a.mant > -((int64_t)1 << 32) && a.mant < ((int64_t)1 << 32) && a.shift >= 0 && a.shift <= 63) {
+        const uint64_t m = (uint64_t)(uint32_t)(a.mant < 0 ? -a.mant : a.mant);
+        const uint64_t x = (uint64_t)(uint32_t)(v < 0 ? 0u - (uint32_t)v : (uint32_t)v);
+        const uint64_t p = x * m;
+        const uint64_t q = a.shift == 0 ? p : (p + ((uint64_t)1 << (a.shift - 1))) >> a.shift;
+        return (v < 0) != (a.mant < 0) ? (int64_t)(0 - q) : (int64_t)q;
+    }
+    return sc_apply(a, v);
+}
+
 // floor(n / d) for 0 < d < 2^63 when the quotient is below 2^40: the double estimate's absolute error is then below
 // 2^40 * 2^-50 (three roundings of relative size 2^-53 each), so one correction step each way suffices; two are
 // allowed.

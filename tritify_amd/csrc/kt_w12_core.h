@@ -328,6 +328,21 @@ struct QlState {
     QlYSlot ymax[KT_QL_YSLOTS];  // max |acc + bias| over the output, in slots (above)
 };
 
+// Several QuantLinear calls on one input with their outputs side by side (the projections of one tensor): segment s
+// holds the output columns col0[s] .. col0[s + 1] - 1 and has its own state at ql + s. Every CTA of the digit GEMM
+// lies within one segment (the host checks that each boundary is a multiple of the CTA's columns). n = 1: one call.
+#define KT_QL_MAX_SEG KT_QL_MAX_SEGMENTS
+struct QlSeg {
+    int n;
+    int col0[KT_QL_MAX_SEG + 1];
+};
+__device__ __forceinline__ int ql_seg_of(const QlSeg& g, int col) {
+    int s = 0;
+#pragma unroll
+    for (int i = 1; i < KT_QL_MAX_SEG; i++) s += (i < g.n && col >= g.col0[i]) ? 1 : 0;
+    return s;
+}
+
 // Raise the call's output maximum from CTA b (b > 0 only).
 __device__ __forceinline__ void ql_raise_ymax(QlState* ql, int64_t b) {
     atomicMax(&ql->ymax[blockIdx.x % KT_QL_YSLOTS].v, (unsigned long long)b);

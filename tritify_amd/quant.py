@@ -104,3 +104,76 @@ class QuantLinear:
         xd = torch.from_numpy(x.reshape(-1)).to(self.device)
         y, os_ = self.forward_int(xd, qscale_record(x_scale[0], x_scale[1], self.dev), rows)
         return y.cpu().numpy().reshape(rows, self.out_features), read_qscale(os_)
+
+
+class QuantLinearGroup:
+    """Several QuantLinears that read the same input (a tensor's projections: q / k / v, gate / up), each
+    QuantLinear::forward_int called once by the reference (layers.rs:275-328), computed by one device call: one
+    quantization of x, one digit GEMM over the members' weights stacked by rows, each member's own bias, output
+    maximum, requant and record -- codes and records equal to its own QuantLinear's.
+
+    members: (name, w_codes out x in, w_scale, bias or None) each, with one in_features. The boundaries between the
+    members must be multiples of ALIGN (the widest column block of the digit GEMM, so any row count works):
+    QuantLinearGroup.fits tells.
+    """
+
+    ALIGN = 128
+
+    @staticmethod
+    def fits(outs) -> bool:
+        at = 0
+        for o in list(outs)[:-1]:
+            at += int(o)
+            if at % QuantLinearGroup.ALIGN:
+                return False
+        return 1 <= len(list(outs)) <= 4
+
+    def __init__(self, name: str, members, in_features: int, dev: int = 0):
+        import torch
+
+        self.torch = torch
+        self.name = name
+        self.in_features = int(in_features)
+        self.outs = [int(np.asarray(m[1]).shape[0]) for m in members]
+        if not QuantLinearGroup.fits(self.outs):
+            raise ValueError(f"{name}: member boundaries not multiples of {QuantLinearGroup.ALIGN}")
+        self.out_features = sum(self.outs)
+        self.dev = dev
+        self.device = torch.device("cuda", dev)
+        codes = np.concatenate([np.ascontiguousarray(m[1], dtype=np.int32).reshape(o, self.in_features)
+                                for m, o in zip(members, self.outs)])
+        self.pw = B.planes_for(codes)
+        kp = B.kp(self.in_features)
+        cdev = torch.from_numpy(codes).to(self.device)
+        self.w_planes = torch.empty(self.pw * self.out_features * kp, dtype=torch.int8, device=self.device)
+        B.pack_planes(cdev, self.out_features, self.in_features, self.pw, self.w_planes, dev=dev)
+        torch.cuda.synchronize(self.device)
+        del cdev
+        self.w_scales = [(int(m[2][0]), int(m[2][1])) for m in members]
+        self.b_scales = [None if m[3] is None else (int(m[3][1][0]), int(m[3][1][1])) for m in members]
+        if any(b is not None for b in self.b_scales):
+            b = np.concatenate([np.zeros(o, np.int64) if m[3] is None else np.asarray(m[3][0], np.int64)
+                                for m, o in zip(members, self.outs)])
+            self.bias = torch.from_numpy(b).to(self.device)
+        else:
+            self.bias = None
+        self._ws: dict[int, tuple] = {}
+
+    def workspace(self, rows: int):
+        if rows not in self._ws:
+            n, _ = B.quant_linear_workspace(rows, self.in_features, self.out_features)
+            self._ws[rows] = (self.torch.empty(n, dtype=self.torch.uint8, device=self.device), n)
+        return self._ws[rows]
+
+    def forward_int(self, x_dev, xs_dev, rows: int, y_devs=None, os_dev=None, stream=None):
+        """Each member's (y rows x out i32 codes, its record): y_devs / os_dev given (os_dev: one record per member,
+        consecutive) or allocated. Asynchronous on `stream`."""
+        torch = self.torch
+        if y_devs is None:
+            y_devs = [torch.empty(rows * o, dtype=torch.int32, device=self.device) for o in self.outs]
+        if os_dev is None:
+            os_dev = torch.empty(4 * len(self.outs), dtype=torch.int64, device=self.device)
+        ws, n = self.workspace(rows)
+        B.quant_linear_multi(x_dev, rows, self.in_features, xs_dev, self.outs, self.w_planes, self.pw, self.w_scales,
+                             self.bias, self.b_scales, ws, n, y_devs, os_dev, stream=stream, dev=self.dev)
+        return [(y, os_dev[4 * g:4 * g + 4]) for g, y in enumerate(y_devs)]

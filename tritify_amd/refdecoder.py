@@ -33,7 +33,7 @@ import math
 import numpy as np
 
 from . import backend as B
-from .quant import QuantLinear
+from .quant import QuantLinear, QuantLinearGroup
 
 QL_NAMES = ("wq", "wk", "wv", "wo", "gate", "up", "down")
 
@@ -71,12 +71,22 @@ class RefDecoder:
         qd, kvd = self.nh * self.hd, self.nkv * self.hd
         shapes = {"wq": (qd, self.dim), "wk": (kvd, self.dim), "wv": (kvd, self.dim), "wo": (self.dim, qd),
                   "gate": (self.hidden, self.dim), "up": (self.hidden, self.dim), "down": (self.dim, self.hidden)}
+        # q / k / v and gate / up each read one tensor: where their output boundaries allow, each trio / pair is one
+        # QuantLinearGroup (one device call, the same integers as the separate QuantLinears)
+        self.grouped = QuantLinearGroup.fits((qd, kvd, kvd)) and QuantLinearGroup.fits((self.hidden, self.hidden))
         self.blocks = []
         for i, lw in enumerate(layers):
             blk = {n: (dt(lw[n][0], np.int32), tuple(lw[n][1])) for n in ("in_norm", "post_norm")}
             for n in QL_NAMES:
+                if self.grouped and n in ("wq", "wk", "wv", "gate", "up"):
+                    continue
                 out, inp = shapes[n]
                 blk[n] = QuantLinear(f"{n}{i}", lw[n][0], out, inp, lw[n][1], dev=dev)
+            if self.grouped:
+                blk["qkv"] = QuantLinearGroup(f"qkv{i}", [(n, lw[n][0], lw[n][1], None) for n in ("wq", "wk", "wv")],
+                                              self.dim, dev=dev)
+                blk["gu"] = QuantLinearGroup(f"gu{i}", [(n, lw[n][0], lw[n][1], None) for n in ("gate", "up")],
+                                             self.dim, dev=dev)
             self.blocks.append(blk)
         self.lm_head = QuantLinear("lm_head", lm_head[0], self.vocab, self.dim, lm_head[1], dev=dev)
         # the run-time tables of Attention::new and SwiGluMlp::new
@@ -94,6 +104,11 @@ class RefDecoder:
                                            ("q", qd), ("k", kvd), ("v", kvd), ("cat", qd), ("g", self.hidden),
                                            ("u", self.hidden), ("hh", self.hidden), ("logits", self.vocab))}
         self.rec = {n: rec() for n in self.buf}
+        # a group writes its members' records side by side: q / k / v and g / u as views of one buffer each
+        qkv_rec, gu_rec = torch.zeros(12, dtype=torch.int64, device=self.device), torch.zeros(8, dtype=torch.int64,
+                                                                                                device=self.device)
+        self.rec.update(q=qkv_rec[0:4], k=qkv_rec[4:8], v=qkv_rec[8:12], g=gu_rec[0:4], u=gu_rec[4:8])
+        self._rec_qkv, self._rec_gu = qkv_rec, gu_rec
         self.token = z(1)
         self.pos = z(1)
         self.new_cache()
@@ -123,8 +138,12 @@ class RefDecoder:
         for i, blk in enumerate(self.blocks):
             g, gs = blk["in_norm"]
             B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
-            for n, out in (("wq", "q"), ("wk", "k"), ("wv", "v")):
-                self._ql(blk[n], "h", out, stream)
+            if self.grouped:
+                blk["qkv"].forward_int(b["h"], r["h"], 1, y_devs=[b["q"], b["k"], b["v"]], os_dev=self._rec_qkv,
+                                       stream=stream)
+            else:
+                for n, out in (("wq", "q"), ("wk", "k"), ("wv", "v")):
+                    self._ql(blk[n], "h", out, stream)
             B.ref_attention_step(b["q"], r["q"], b["k"], r["k"], b["v"], r["v"], self.pos, self.nh, self.nkv,
                                  self.hd, self.max_seq, self.kc[i], self.vc[i], self.ks[i], self.vs[i], self.cos,
                                  self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, b["cat"], r["cat"], stream,
@@ -133,8 +152,11 @@ class RefDecoder:
             B.ref_add(b["x"], r["x"], b["a"], r["a"], self.dim, b["x"], r["x"], stream, dv)
             g, gs = blk["post_norm"]
             B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
-            self._ql(blk["gate"], "h", "g", stream)
-            self._ql(blk["up"], "h", "u", stream)
+            if self.grouped:
+                blk["gu"].forward_int(b["h"], r["h"], 1, y_devs=[b["g"], b["u"]], os_dev=self._rec_gu, stream=stream)
+            else:
+                self._ql(blk["gate"], "h", "g", stream)
+                self._ql(blk["up"], "h", "u", stream)
             B.ref_swiglu(b["g"], r["g"], b["u"], r["u"], self.hidden, self.silu_codes, self.silu_lut, b["hh"],
                          r["hh"], stream, dv)  # one tensor (rows = 1)
             self._ql(blk["down"], "hh", "m", stream)
@@ -199,17 +221,23 @@ class RefDecoder:
         cat, cr, a, ar, hh, hhr = z(T * qd), rec(), z(T * self.dim), rec(), z(T * self.hidden), rec()
         for blk in self.blocks:
             norm(x, xr, blk["in_norm"], h, hr)
-            q, qr = blk["wq"].forward_int(h, hr, T, stream=stream)
-            k, kr = blk["wk"].forward_int(h, hr, T, stream=stream)
-            v, vr = blk["wv"].forward_int(h, hr, T, stream=stream)
+            if self.grouped:
+                (q, qr), (k, kr), (v, vr) = blk["qkv"].forward_int(h, hr, T, stream=stream)
+            else:
+                q, qr = blk["wq"].forward_int(h, hr, T, stream=stream)
+                k, kr = blk["wk"].forward_int(h, hr, T, stream=stream)
+                v, vr = blk["wv"].forward_int(h, hr, T, stream=stream)
             B.ref_attention_prefill(q, qr, k, kr, v, vr, T, self.nh, self.nkv, self.hd, self.max_seq, self.cos,
                                     self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, ws, nws, cat, cr, stream,
                                     dv)
             blk["wo"].forward_int(cat, cr, T, y_dev=a, os_dev=ar, stream=stream)
             add(x, xr, a, ar)
             norm(x, xr, blk["post_norm"], h, hr)
-            gt, gtr = blk["gate"].forward_int(h, hr, T, stream=stream)
-            up, upr = blk["up"].forward_int(h, hr, T, stream=stream)
+            if self.grouped:
+                (gt, gtr), (up, upr) = blk["gu"].forward_int(h, hr, T, stream=stream)
+            else:
+                gt, gtr = blk["gate"].forward_int(h, hr, T, stream=stream)
+                up, upr = blk["up"].forward_int(h, hr, T, stream=stream)
             B.ref_swiglu_seq(gt, gtr, up, upr, T * self.hidden, self.silu_codes, self.silu_lut, wsq, nsq, hh, hhr,
                              stream, dv)
             m, mr = blk["down"].forward_int(hh, hhr, T, stream=stream)
