@@ -226,6 +226,7 @@ def layer_from(m: O.RefMoe, dev_sigmoid: bool):
     dict(seed=0x5C, dim=32, E=16, k=4, hidden=24, norm=True, sig=1, bseed=0x5C, shared=40, T=6),
     dict(seed=0x91, dim=256, E=32, k=4, hidden=128, norm=True, sig=1, bseed=0x92, shared=192, T=40),
     dict(seed=0x93, dim=128, E=16, k=2, hidden=64, norm=False, sig=1, bseed=0x94, shared=0, T=9),
+    dict(seed=0x97, dim=128, E=16, k=4, hidden=64, norm=True, sig=1, bseed=0x98, shared=256, T=7),  # grouped gate/up
 ])
 def test_moe_layer_against_the_oracle(torch_dev, case):
     torch = torch_dev

@@ -14,7 +14,7 @@ groups only the exact integer products:
   experts down             kt_hip_quant_linear_rows (E groups; per-row input scales)
   combine                  kt_hip_ref_moe_combine   (per token: common scale, ec-weighted sum, 1/sumc)
   merge_rows               kt_hip_ref_merge_rows    (a sequence: the tokens at one scale)
-  shared expert + add      kt_hip_quant_linear, kt_hip_ref_swiglu_seq, kt_hip_ref_add_seq (the whole tensor, many
+  shared expert + add      kt_hip_quant_linear(_multi), kt_hip_ref_swiglu_seq, kt_hip_ref_add_seq (the whole tensor, many
                            CTAs)
 
 Nothing waits on the host: the group sizes stay on the device (the grouped products plan their tiles there), so a
@@ -27,7 +27,7 @@ from __future__ import annotations
 import numpy as np
 
 from . import backend as B
-from .quant import QuantLinear
+from .quant import QuantLinear, QuantLinearGroup
 
 
 class RefMoeLayer:
@@ -67,10 +67,16 @@ class RefMoeLayer:
         self.shared = None
         if shared is not None:
             sh_hidden = int(np.asarray(shared["gate"][0]).shape[0])
+            self.shared_hidden = sh_hidden
+            # gate and up read the same x: one QuantLinearGroup where their boundary allows
+            self.shared_grouped = QuantLinearGroup.fits((sh_hidden, sh_hidden))
+            names = ("down",) if self.shared_grouped else ("gate", "up", "down")
             self.shared = {n: QuantLinear(f"shared.{n}", shared[n][0], *(
                 (sh_hidden, self.dim) if n != "down" else (self.dim, sh_hidden)), shared[n][1], dev=dev)
-                for n in ("gate", "up", "down")}
-            self.shared_hidden = sh_hidden
+                for n in names}
+            if self.shared_grouped:
+                self.shared["gu"] = QuantLinearGroup("shared.gu", [(n, shared[n][0], shared[n][1], None)
+                                                                   for n in ("gate", "up")], self.dim, dev=dev)
         self._i32 = i32
         self._route_off = {}  # T -> the router's one-group offsets [0, T] on the device
 
@@ -170,8 +176,11 @@ class RefMoeLayer:
         if self.shared is None:
             return routed, rrec
         rec = lambda: torch.empty(4, dtype=torch.int64, device=self.device)  # noqa: E731
-        sg, sgs = self.shared["gate"].forward_int(x_dev, xs_rec, T, os_dev=rec(), stream=stream)
-        su, sus = self.shared["up"].forward_int(x_dev, xs_rec, T, os_dev=rec(), stream=stream)
+        if self.shared_grouped:
+            (sg, sgs), (su, sus) = self.shared["gu"].forward_int(x_dev, xs_rec, T, stream=stream)
+        else:
+            sg, sgs = self.shared["gate"].forward_int(x_dev, xs_rec, T, os_dev=rec(), stream=stream)
+            su, sus = self.shared["up"].forward_int(x_dev, xs_rec, T, os_dev=rec(), stream=stream)
         sh = torch.empty(T * self.shared_hidden, dtype=torch.int32, device=self.device)
         shs = rec()
         nsq = B.ref_seq_workspace(1)  # whole-tensor SwiGLU and add on many CTAs
