@@ -530,10 +530,34 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
             if (tid < hn) hsc[h0 + tid] = Sc{0, 0};
             continue;
         }
+        const int items = hn * steps;
+        // (16-byte loads: rows of a multiple of 32 values, q and the cache at 16-byte aligned addresses)
+        const bool vec = hd % 32 == 0 && (((size_t)((const char*)QD - (const char*)lds)) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.kc) & 15) == 0;
+        if (vec) {
+            // one thread per (head, cached row): the whole dot from 16-byte loads, 32 values of k in flight at a time
+            for (int it = tid; it < items; it += RD_THREADS) {
+                const int h = it / steps, j = it - h * steps, kv = (h0 + h) / group;
+                const int4* kr = reinterpret_cast<const int4*>(a.kc + (size_t)j * kstride + kv * hd);
+                const int4* qh = reinterpret_cast<const int4*>(QD + (h0 + h) * hd);
+                int64_t dot = 0;
+                for (int e4 = 0; e4 < hd / 4; e4 += 8) {
+                    int4 kk[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) kk[u] = kr[e4 + u];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const int4 qq = qh[e4 + u];
+                        dot = wadd(dot, (int64_t)qq.x * kk[u].x + (int64_t)qq.y * kk[u].y);  // each below 2^63
+                        dot = wadd(dot, (int64_t)qq.z * kk[u].z + (int64_t)qq.w * kk[u].w);
+                    }
+                }
+                S[(size_t)h * a.max_seq + j] = sc_apply(F[j], dot);
+            }
+        } else {
         // RD_SU items per wave at a time, every cached k row of them loaded before the first product (an item past
         // the end re-reads the last one and is dropped)
         constexpr int RD_SU = 8;
-        const int items = hn * steps;
         for (int it0 = wave; it0 < items; it0 += RD_WAVES * RD_SU) {
             int64_t dot[RD_SU];
             int hh[RD_SU], jj[RD_SU];
@@ -563,6 +587,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
                 const int h = it / steps, j = it - h * steps;
                 if (it < items) S[(size_t)h * a.max_seq + j] = sc_apply(F[j], d);
             }
+        }
         }
         __syncthreads();
         for (int h = wave; h < hn; h += RD_WAVES) {
