@@ -162,7 +162,25 @@ __device__ inline ScIdx sc_pick(ScIdx a, ScIdx b) {
     if (ab && ba) return a.idx > b.idx ? a : b;
     return ba ? b : a;
 }
-__device__ ScIdx block_fold_max(ScIdx v, ScIdx* red) {
+// n: how many leading threads hold items (the rest hold idx -1). sc_pick orders (value, index) totally, so any
+// reduction order gives the fold's result: up to 64 items by a butterfly in wave 0, more by a tree in LDS.
+__device__ ScIdx block_fold_max(ScIdx v, ScIdx* red, int n) {
+    if (n <= 64) {
+        if (threadIdx.x < 64) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                ScIdx u;
+                u.s.mant = __shfl_xor(v.s.mant, o, 64), u.s.shift = __shfl_xor(v.s.shift, o, 64);
+                u.idx = __shfl_xor(v.idx, o, 64);
+                v = sc_pick(v, u);
+            }
+            if (threadIdx.x == 0) red[0] = v;
+        }
+        __syncthreads();
+        v = red[0];
+        __syncthreads();
+        return v;
+    }
     red[threadIdx.x] = v;
     __syncthreads();
     for (int s = RD_THREADS / 2; s > 0; s >>= 1) {
@@ -289,7 +307,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
     // the largest row factor by the engine's fold (of equal values the latest row's), then each row's share of it
     ScIdx best{Sc{0, 0}, -1};
     for (int r = threadIdx.x; r < rows; r += RD_THREADS) best = sc_pick(best, ScIdx{crow[r], r});
-    const Sc cc = block_fold_max(best, redsc).s;
+    const Sc cc = block_fold_max(best, redsc, rows).s;
     if (cc.mant != 0) {
         const Sc cinv = sc_recip(cc);  // every thread: one Scale reciprocal, no extra barrier
         for (int r = threadIdx.x; r < rows; r += RD_THREADS) frow[r] = sc_mul(crow[r], cinv);
@@ -469,10 +487,10 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         for (int i = tid; i < heads * half; i += RD_THREADS) {
             const int hh = i / half, j = i - hh * half;
             const kt_hip_sscale c = a.cos[(size_t)pos * half + j], s = a.sin[(size_t)pos * half + j];
-            const int64_t av = src[hh * hd + j], bv = src[hh * hd + j + half];
+            const int32_t av = src[hh * hd + j], bv = src[hh * hd + j + half];
             const Sc cm{c.mant, c.shift}, sm{s.mant, s.shift};
-            dst[hh * hd + j] = (int32_t)(c.sign * sc_apply(cm, av) - s.sign * sc_apply(sm, bv));
-            dst[hh * hd + j + half] = (int32_t)(c.sign * sc_apply(cm, bv) + s.sign * sc_apply(sm, av));
+            dst[hh * hd + j] = (int32_t)(c.sign * sc_apply32(cm, av) - s.sign * sc_apply32(sm, bv));
+            dst[hh * hd + j + half] = (int32_t)(c.sign * sc_apply32(cm, bv) + s.sign * sc_apply32(sm, av));
         }
     };
     rot(a.q, QD, nh);
@@ -494,8 +512,8 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         bv = sc_pick(bv, ScIdx{vj, j});
         bs = sc_pick(bs, ScIdx{sj, j});
     }
-    bv = block_fold_max(bv, redsc);
-    bs = block_fold_max(bs, redsc);
+    bv = block_fold_max(bv, redsc, steps);
+    bs = block_fold_max(bs, redsc, steps);
     if (tid == 0) {
         par[0] = bv.s, par[1] = bs.s;
         par[2] = bs.s.mant ? sc_mul(bs.s, Sc{a.exp.inv_mant, a.exp.inv_shift}) : Sc{0, 0};
@@ -504,10 +522,8 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     const Sc v_ref = par[0], s_ref = par[1], lm = par[2];
     if (v_ref.mant != 0 || s_ref.mant != 0) {
         __shared__ Sc inv2[2];
-        if (tid == 0) {
-            inv2[0] = v_ref.mant ? sc_recip(v_ref) : Sc{0, 0};
-            inv2[1] = s_ref.mant ? sc_recip(s_ref) : Sc{0, 0};
-        }
+        if (tid == 0) inv2[0] = v_ref.mant ? sc_recip(v_ref) : Sc{0, 0};  // the two reciprocals in two waves
+        if (tid == 64) inv2[1] = s_ref.mant ? sc_recip(s_ref) : Sc{0, 0};
         __syncthreads();
         for (int j = tid; j < steps; j += RD_THREADS) {
             VF[j] = v_ref.mant ? sc_mul(Sc{a.vscale[j].mant, a.vscale[j].shift}, inv2[0]) : Sc{0, 0};
@@ -639,24 +655,17 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         __syncthreads();  // S and hsum are reused by the next batch
     }
 
-    // 4. one scale for the concatenated heads
-    __shared__ Sc s_cinv;
-    if (tid == 0) {
-        Sc common{0, 0};
-        for (int h = 0; h < nh; h++) common = sc_ge(hsc[h], common) ? hsc[h] : common;
-        par[3] = common;
-        if (common.mant != 0) s_cinv = sc_recip(common);
-    }
-    __syncthreads();
-    if (tid < nh && par[3].mant != 0) hsc[tid] = sc_mul(hsc[tid], s_cinv);  // the heads' factors side by side
-    __syncthreads();
-    const Sc common = par[3];
+    // 4. one scale for the concatenated heads: the heads' largest by the engine's fold, then every thread its own
+    //    reciprocal and its elements' head factors (no serial step)
+    const Sc common = block_fold_max(tid < nh ? ScIdx{hsc[tid], tid} : ScIdx{Sc{0, 0}, -1}, redsc, nh).s;
     int64_t m = 0;
-    if (common.mant != 0)
+    if (common.mant != 0) {
+        const Sc cinv = sc_recip(common);
         for (int i = tid; i < qstride; i += RD_THREADS) {
-            HO[i] = sc_apply(hsc[i / hd], HO[i]);
+            HO[i] = sc_apply(sc_mul(hsc[i / hd], cinv), HO[i]);
             m = iabs(HO[i]) > m ? iabs(HO[i]) : m;
         }
+    }
     const int64_t gmax = block_max_i64(m, red);
     for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = gmax == 0 ? 0 : requant_dyn_dev(HO[i], gmax);
     if (tid == 0)
@@ -726,7 +735,7 @@ __global__ __launch_bounds__(RD_THREADS) void rs_prep_kernel(RdSeq q) {
         __syncthreads();  // the CTA's own global writes are visible to it past the barrier
         ScIdx best{Sc{0, 0}, -1};
         for (int r = threadIdx.x; r < q.rows; r += RD_THREADS) best = sc_pick(best, ScIdx{w->frow[r], r});
-        const Sc cc = block_fold_max(best, redsc).s;
+        const Sc cc = block_fold_max(best, redsc, q.rows).s;
         if (cc.mant != 0) {
             const Sc cinv = sc_recip(cc);
             for (int r = threadIdx.x; r < q.rows; r += RD_THREADS) w->frow[r] = sc_mul(w->frow[r], cinv);
@@ -872,7 +881,7 @@ __global__ __launch_bounds__(RD_THREADS) void rp_common_kernel(RdPrefill a) {
         a.fac[e] = sc;
         best = sc_pick(best, ScIdx{sc, e});
     }
-    const Sc common = block_fold_max(best, redsc).s;  // its barriers order the fac writes before the reads
+    const Sc common = block_fold_max(best, redsc, n).s;  // its barriers order the fac writes before the reads
     if (common.mant != 0) {
         const Sc cinv = sc_recip(common);
         for (int e = threadIdx.x; e < n; e += RD_THREADS) a.fac[e] = sc_mul(a.fac[e], cinv);
