@@ -103,16 +103,6 @@ __device__ int64_t block_max_i64(int64_t v, int64_t* red) {
     __syncthreads();
     return v;
 }
-__device__ int64_t block_sum_i64(int64_t v, int64_t* red) {  // wrapping
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = wadd(v, __shfl_xor(v, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    v = red[0];
-    for (int w = 1; w < RD_WAVES; w++) v = wadd(v, red[w]);
-    __syncthreads();
-    return v;
-}
 // The same reductions for CTAs of 256 threads (4 waves).
 __device__ int64_t block_max_4w(int64_t v, int64_t* red) {
 #pragma unroll
@@ -134,17 +124,6 @@ __device__ int64_t block_sum_4w(int64_t v, int64_t* red) {  // wrapping
     __syncthreads();
     v = red[0];
     for (int w = 1; w < 4; w++) v = wadd(v, red[w]);
-    __syncthreads();
-    return v;
-}
-__device__ u128 block_sum_u128(u128 v, u128* red) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int s = RD_THREADS / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-        __syncthreads();
-    }
-    v = red[0];
     __syncthreads();
     return v;
 }
@@ -194,6 +173,8 @@ __device__ ScIdx block_fold_max(ScIdx v, ScIdx* red, int n) {
 
 // CodeLut::index / code_at (kt-int/src/lib.rs:382-395) with the call's factor m = scale * inv_step.
 __device__ inline int64_t lut_index(Sc m, int64_t data, int64_t lo_index) { return sc_apply(m, data) - lo_index; }
+// the same for an i32 code, in 64-bit arithmetic where sc_apply32 allows
+__device__ inline int64_t lut_index32(Sc m, int32_t data, int64_t lo_index) { return sc_apply32(m, data) - lo_index; }
 __device__ inline int64_t lut_code(const int64_t* codes, int n, int64_t idx) {
     return codes[idx < 0 ? 0 : (idx > n - 1 ? n - 1 : idx)];
 }
@@ -267,8 +248,9 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
         int64_t hv[RD_NV];
         int64_t m = 0;
 #pragma unroll
-        for (int k = 0; k < RD_NV; k++) {
-            hv[k] = cc.mant != 0 ? sc_apply(f0, (int64_t)xv[k] * (int64_t)gv[k]) : 0;
+        for (int k = 0; k < RD_NV; k++) {  // values past dim stay 0 (whole waves skip the 128-bit products)
+            hv[k] = 0;
+            if (cc.mant != 0 && (int)threadIdx.x + RD_THREADS * k < dim) hv[k] = sc_apply(f0, (int64_t)xv[k] * (int64_t)gv[k]);
             m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
         }
         const int64_t gmax = block_max_i64(m, red);
@@ -333,6 +315,18 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, co
                                                             int32_t* y, kt_hip_qscale* ys) {
     __shared__ int64_t red[RD_WAVES];
     __shared__ Sc par[3];  // common, fa, fb
+    // up to RD_AV values per thread held in registers, their loads issued before the Scale work of thread 0 so that
+    // the two overlap; longer tensors read a and b twice
+    constexpr int RD_AV = 4;
+    const bool held = n <= RD_THREADS * RD_AV;
+    int32_t av[RD_AV], bv[RD_AV];
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < RD_AV; k++) {
+            const int i = threadIdx.x + RD_THREADS * k, ic = i < n ? i : n - 1;
+            av[k] = a[ic], bv[k] = b[ic];
+        }
+    }
     if (threadIdx.x == 0) {
         const Sc as = rec_sc(as_rec), bs = rec_sc(bs_rec);
         const Sc common = sc_ge(as, bs) ? as : bs;
@@ -344,15 +338,32 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, co
     }
     __syncthreads();
     const Sc common = par[0], fa = par[1], fb = par[2];
-    int64_t m = 0;
-    if (common.mant != 0)
+    int64_t m = 0, hv[RD_AV];
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < RD_AV; k++) {  // values past n stay 0 (whole waves skip them)
+            hv[k] = 0;
+            if (common.mant != 0 && (int)threadIdx.x + RD_THREADS * k < n)
+                hv[k] = wadd(sc_apply32(fa, av[k]), sc_apply32(fb, bv[k]));
+            m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
+        }
+    } else if (common.mant != 0) {
         for (int i = threadIdx.x; i < n; i += RD_THREADS) {
-            const int64_t v = wadd(sc_apply(fa, a[i]), sc_apply(fb, b[i]));
+            const int64_t v = wadd(sc_apply32(fa, a[i]), sc_apply32(fb, b[i]));
             m = iabs(v) > m ? iabs(v) : m;
         }
+    }
     const int64_t gmax = block_max_i64(m, red);  // every read of a, b, and their records, is done past here
-    for (int i = threadIdx.x; i < n; i += RD_THREADS)
-        y[i] = gmax == 0 ? 0 : requant_dyn_dev(wadd(sc_apply(fa, a[i]), sc_apply(fb, b[i])), gmax);
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < RD_AV; k++) {
+            const int i = threadIdx.x + RD_THREADS * k;
+            if (i < n) y[i] = gmax == 0 ? 0 : requant_dyn_dev(hv[k], gmax);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += RD_THREADS)
+            y[i] = gmax == 0 ? 0 : requant_dyn_dev(wadd(sc_apply32(fa, a[i]), sc_apply32(fb, b[i])), gmax);
+    }
     if (threadIdx.x == 0)
         put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
 }
@@ -372,6 +383,18 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
         const int64_t r = blockIdx.x;
         g += r * n, u += r * n, h += r * n, gs_rec += r, us_rec += r, hs += r;
     }
+    // up to RD_VPT values per thread formed once and held in registers, their loads issued before thread 0's Scale
+    // work so that the two overlap (the table reads follow the factors); longer rows form each value twice
+    constexpr int RD_VPT = 8;
+    const bool held = n <= RD_THREADS * RD_VPT;
+    int32_t gd[RD_VPT], ud[RD_VPT];
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            const int k = threadIdx.x + RD_THREADS * i, kk = k < n ? k : n - 1;
+            gd[i] = g[kk], ud[i] = u[kk];
+        }
+    }
     __shared__ Sc par[3];  // index factor, identity factor, h scale
     if (threadIdx.x == 0) {
         const Sc gs = rec_sc(gs_rec), us = rec_sc(us_rec), cs{L.code_mant, L.code_shift};
@@ -382,28 +405,22 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
     __syncthreads();
     const Sc mi = par[0], idf = par[1], hsc = par[2];
     auto act = [&](int k) -> int64_t {
-        const int64_t gd = g[k], idx = lut_index(mi, gd, L.lo_index);
-        const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, gd) : lut_code(codes, L.n, idx));
+        const int32_t gk = g[k];
+        const int64_t idx = lut_index32(mi, gk, L.lo_index);
+        const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply32(idf, gk) : lut_code(codes, L.n, idx));
         return wmul(code, u[k]);
     };
-    // up to RD_VPT values per thread formed once and held in registers (each pass's loads issued together, the
-    // table reads after them); longer rows form each value twice
-    constexpr int RD_VPT = 8;
     int64_t hv[RD_VPT];
     int64_t m = 0;
-    const bool held = n <= RD_THREADS * RD_VPT;
     if (held) {
-        int64_t gd[RD_VPT], ud[RD_VPT];
 #pragma unroll
-        for (int i = 0; i < RD_VPT; i++) {
-            const int k = threadIdx.x + RD_THREADS * i, kk = k < n ? k : n - 1;
-            gd[i] = g[kk], ud[i] = u[kk];
-        }
-#pragma unroll
-        for (int i = 0; i < RD_VPT; i++) {
-            const int64_t idx = lut_index(mi, gd[i], L.lo_index);
-            const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, gd[i]) : lut_code(codes, L.n, idx));
-            hv[i] = threadIdx.x + RD_THREADS * i < n ? wmul(code, ud[i]) : 0;
+        for (int i = 0; i < RD_VPT; i++) {  // values past n stay 0 (whole waves skip them)
+            hv[i] = 0;
+            if ((int)threadIdx.x + RD_THREADS * i < n) {
+                const int64_t idx = lut_index32(mi, gd[i], L.lo_index);
+                const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply32(idf, gd[i]) : lut_code(codes, L.n, idx));
+                hv[i] = wmul(code, ud[i]);
+            }
             m = iabs(hv[i]) > m ? iabs(hv[i]) : m;
         }
     } else {
@@ -445,8 +462,9 @@ __global__ __launch_bounds__(RD_THREADS) void rd_gelu_kernel(const int32_t* __re
     const Sc mi = par[0], idf = par[1];
     const int64_t step = (int64_t)gridDim.x * RD_THREADS;
     for (int64_t i = (int64_t)blockIdx.x * RD_THREADS + threadIdx.x; i < n; i += step) {
-        const int64_t d = x[i], idx = lut_index(mi, d, L.lo_index);
-        const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply(idf, d) : lut_code(codes, L.n, idx));
+        const int32_t d = x[i];
+        const int64_t idx = lut_index32(mi, d, L.lo_index);
+        const int64_t code = idx < 0 ? 0 : (idx >= L.n ? sc_apply32(idf, d) : lut_code(codes, L.n, idx));
         y[i] = (int32_t)code;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) put_rec(ys, cs);
@@ -697,10 +715,11 @@ struct RdSeq {
 };
 
 __device__ inline int64_t rs_value(const RdSeq& q, const RdSeqWs* w, int64_t i) {
-    if (q.op == RS_ADD) return wadd(sc_apply(w->par[1], q.a[i]), sc_apply(w->par[2], q.b[i]));
+    if (q.op == RS_ADD) return wadd(sc_apply32(w->par[1], q.a[i]), sc_apply32(w->par[2], q.b[i]));
     if (q.op == RS_SWIGLU) {
-        const int64_t gd = q.a[i], idx = lut_index(w->par[0], gd, q.lut.lo_index);
-        const int64_t code = idx < 0 ? 0 : (idx >= q.lut.n ? sc_apply(w->par[1], gd) : lut_code(q.codes, q.lut.n, idx));
+        const int32_t gd = q.a[i];
+        const int64_t idx = lut_index32(w->par[0], gd, q.lut.lo_index);
+        const int64_t code = idx < 0 ? 0 : (idx >= q.lut.n ? sc_apply32(w->par[1], gd) : lut_code(q.codes, q.lut.n, idx));
         return wmul(code, q.b[i]);
     }
     return sc_apply(w->frow[i / q.dim], (int64_t)q.a[i] * (int64_t)q.b[i % q.dim]);
@@ -817,10 +836,10 @@ __global__ __launch_bounds__(256) void rp_rope_kernel(RdPrefill a) {
         const int32_t* src = isk ? a.k + (size_t)i * kw : a.q + (size_t)i * qw;
         int32_t* dst = isk ? a.kd + (size_t)i * kw : a.qd + (size_t)i * qw;
         const kt_hip_sscale c = a.cos[(size_t)i * half + j], sn = a.sin[(size_t)i * half + j];
-        const int64_t av = src[hh * a.hd + j], bv = src[hh * a.hd + j + half];
+        const int32_t av = src[hh * a.hd + j], bv = src[hh * a.hd + j + half];
         const Sc cm{c.mant, c.shift}, sm{sn.mant, sn.shift};
-        dst[hh * a.hd + j] = (int32_t)(c.sign * sc_apply(cm, av) - sn.sign * sc_apply(sm, bv));
-        dst[hh * a.hd + j + half] = (int32_t)(c.sign * sc_apply(cm, bv) + sn.sign * sc_apply(sm, av));
+        dst[hh * a.hd + j] = (int32_t)(c.sign * sc_apply32(cm, av) - sn.sign * sc_apply32(sm, bv));
+        dst[hh * a.hd + j + half] = (int32_t)(c.sign * sc_apply32(cm, bv) + sn.sign * sc_apply32(sm, av));
     }
 }
 

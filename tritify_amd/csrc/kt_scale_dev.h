@@ -2,10 +2,20 @@
 // layers: a non-negative scale mant * 2^-shift with a ~31-bit mantissa, composed with 128-bit integer arithmetic.
 // Every function gives the integers of its kt-int counterpart; these run in one thread per tensor (or per cached
 // step), never per element, except sc_apply and requant_dyn_dev.
+//
+// The same source compiles as host C++ (g++, no HIP headers) so that the exactness of every arithmetic path can be
+// checked on the CPU against the restatement of kt-int and against Python's integers.
 #pragma once
 
-#include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+#define KT_SC_FN __host__ __device__ inline
+#else
+#include <math.h>
+#define KT_SC_FN inline
+#endif
 
 namespace kt {
 
@@ -17,25 +27,24 @@ struct Sc {
     int32_t shift;
 };
 
-__device__ inline int bits_u128(u128 v) {
+KT_SC_FN int bits_u128(u128 v) {
     const uint64_t hi = (uint64_t)(v >> 64), lo = (uint64_t)v;
-    return hi ? 128 - __clzll((long long)hi) : (lo ? 64 - __clzll((long long)lo) : 0);
+    return hi ? 128 - __builtin_clzll(hi) : (lo ? 64 - __builtin_clzll(lo) : 0);
 }
 
 // floor(n / d) for d > 0, exact for every input:
 //  - d a power of two below 2^64: a shift;
-//  - both below 2^64: the 64-bit division;
 //  - d below 2^64 and the quotient below 2^49 (bits(n) - bits(d) < 49; every quotient of from_ratio, whose mantissa
 //    is below 2^33, and of isqrt's Newton steps): a double-precision estimate, whose relative error is at most
 //    5 * 2^-53 (the conversions of n's two halves and of d, their sum, the quotient), so at most 5/16 absolute,
-//    corrected against the exact i128 remainder (n < 2^113 here, so the remainder fits);
+//    corrected against the exact i128 remainder (n < 2^113 here, so the remainder fits). On the GPU this is a
+//    few dozen instructions, where a 64-bit integer division is a long software sequence;
+//  - both below 2^64: the 64-bit division;
 //  - otherwise restoring long division.
-__device__ inline u128 udiv128(u128 n, u128 d) {
-    // from_ratio's normalizations divide by powers of two (Scale::mul by 1, a negative shift by 2^-s): a shift, where
-    // the general 64-bit division is a long instruction sequence
+KT_SC_FN u128 udiv128(u128 n, u128 d) {
+    // from_ratio's normalizations divide by powers of two (Scale::mul by 1, a negative shift by 2^-s): a shift
     if ((d >> 64) == 0 && (uint64_t)d != 0 && ((uint64_t)d & ((uint64_t)d - 1)) == 0)
         return n >> __builtin_ctzll((uint64_t)d);
-    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
     if ((d >> 64) == 0 && bits_u128(n) - bits_u128(d) < 49) {
         const uint64_t d64 = (uint64_t)d;
         const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
@@ -45,6 +54,7 @@ __device__ inline u128 udiv128(u128 n, u128 d) {
         while (rem >= (i128)d64) q++, rem -= (i128)d64;
         return (u128)q;
     }
+    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
     u128 q = 0, r = 0;
     for (int i = bits_u128(n) - 1; i >= 0; i--) {
         r = (r << 1) | ((n >> i) & 1);
@@ -54,9 +64,12 @@ __device__ inline u128 udiv128(u128 n, u128 d) {
 }
 
 // Scale::from_ratio (lib.rs:191-212): a 31-bit-normalized mantissa of num / den, rounded.
-__device__ inline Sc from_ratio(u128 num, u128 den) {
+KT_SC_FN Sc from_ratio(u128 num, u128 den) {
     if (num == 0) return Sc{0, 0};
-    while (bits_u128(num) > 64 || bits_u128(den) > 64) num >>= 1, den >>= 1;
+    {  // the reference halves both until each fits 64 bits: that many halvings as one shift
+        const int bn = bits_u128(num), bd = bits_u128(den), k = (bn > bd ? bn : bd) - 64;
+        if (k > 0) num >>= k, den >>= k;
+    }
     if (den == 0) den = 1;
     const int s = 31 - (bits_u128(num) - bits_u128(den));
     u128 m;
@@ -70,7 +83,7 @@ __device__ inline Sc from_ratio(u128 num, u128 den) {
 }
 
 // Scale::mul (lib.rs:252-258)
-__device__ inline Sc sc_mul(Sc a, Sc b) {
+KT_SC_FN Sc sc_mul(Sc a, Sc b) {
     if (a.mant == 0 || b.mant == 0) return Sc{0, 0};
     Sc q = from_ratio((u128)(uint64_t)a.mant * (u128)(uint64_t)b.mant, 1);
     q.shift += a.shift + b.shift;
@@ -78,13 +91,13 @@ __device__ inline Sc sc_mul(Sc a, Sc b) {
 }
 
 // Scale::recip (lib.rs:275-280); a.mant > 0.
-__device__ inline Sc sc_recip(Sc a) {
+KT_SC_FN Sc sc_recip(Sc a) {
     const Sc r = from_ratio((u128)1 << 40, (u128)(uint64_t)a.mant);
     return Sc{r.mant, r.shift - a.shift + 40};
 }
 
 // Scale::ge (lib.rs:227-248): a >= o by value.
-__device__ inline bool sc_ge(Sc a, Sc o) {
+KT_SC_FN bool sc_ge(Sc a, Sc o) {
     if (a.mant == 0) return o.mant == 0;
     if (o.mant == 0) return true;
     const u128 ma = (u128)(uint64_t)a.mant, mb = (u128)(uint64_t)o.mant;
@@ -99,7 +112,7 @@ __device__ inline bool sc_ge(Sc a, Sc o) {
 }
 
 // Scale::add (lib.rs:285-303)
-__device__ inline Sc sc_add(Sc a, Sc o) {
+KT_SC_FN Sc sc_add(Sc a, Sc o) {
     if (a.mant == 0) return o;
     if (o.mant == 0) return a;
     const int s = a.shift > o.shift ? a.shift : o.shift;
@@ -111,9 +124,20 @@ __device__ inline Sc sc_add(Sc a, Sc o) {
     return Sc{fr.mant, fr.shift + s};
 }
 
-// isqrt_u128 (lib.rs:327-340): floor(sqrt(n)) by Newton's method from above.
-__device__ inline u128 isqrt_u128(u128 n) {
+// isqrt_u128 (lib.rs:327-340): floor(sqrt(n)), which the reference's Newton iteration from above (start
+// 2^ceil(bits/2) >= sqrt(n), stop when a step no longer decreases) arrives at. Below 2^104 the same integer comes
+// from the double-precision root corrected to the exact floor: the estimate is within 2 of sqrt(n) there (the
+// conversion and the root each add a relative error of at most 2^-53 to a value below 2^52), and the two loops move
+// it to the r with r^2 <= n < (r + 1)^2, which is unique. Larger n take the Newton iteration itself.
+KT_SC_FN u128 isqrt_u128(u128 n) {
     if (n == 0) return 0;
+    if (bits_u128(n) <= 104) {
+        const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
+        uint64_t r = (uint64_t)sqrt(dn);
+        while ((u128)r * r > n) r--;
+        while ((u128)(r + 1) * (r + 1) <= n) r++;
+        return (u128)r;
+    }
     u128 x = (u128)1 << ((bits_u128(n) + 1) / 2);
     for (;;) {
         const u128 y = (x + udiv128(n, x)) >> 1;
@@ -123,7 +147,7 @@ __device__ inline u128 isqrt_u128(u128 n) {
 }
 
 // Scale::rsqrt (lib.rs:307-318); a.mant > 0.
-__device__ inline Sc sc_rsqrt(Sc a) {
+KT_SC_FN Sc sc_rsqrt(Sc a) {
     u128 m = (u128)(uint64_t)a.mant;
     int s = a.shift;
     if (s & 1) m <<= 1, s += 1;
@@ -132,7 +156,7 @@ __device__ inline Sc sc_rsqrt(Sc a) {
 }
 
 // Scale::apply (lib.rs:261-272): round(value * a) half away from zero, i128 product, wrapped to i64.
-__device__ inline int64_t sc_apply(Sc a, int64_t value) {
+KT_SC_FN int64_t sc_apply(Sc a, int64_t value) {
     if (a.mant == 0) return 0;
     const i128 prod = (i128)value * (i128)a.mant;
     if (a.shift <= 0) return (int64_t)(prod << (-a.shift));
@@ -143,7 +167,7 @@ __device__ inline int64_t sc_apply(Sc a, int64_t value) {
 // Scale::apply of an int32 code with 64-bit arithmetic where that is exact: |mant| < 2^32 and 0 <= shift <= 63 keep
 // |v * mant| below 2^63 and its sum with the rounding addend 2^(shift - 1) below 2^64 (unsigned); other Scales go
 // through the i128 sc_apply. The same rounding, half away from zero.
-__device__ inline int64_t sc_apply32(Sc a, int32_t v) {
+KT_SC_FN int64_t sc_apply32(Sc a, int32_t v) {
     if (a.mant > -((int64_t)1 << 32) && a.mant < ((int64_t)1 << 32) && a.shift >= 0 && a.shift <= 63) {
         const uint64_t m = (uint64_t)(uint32_t)(a.mant < 0 ? -a.mant : a.mant);
         const uint64_t x = (uint64_t)(uint32_t)(v < 0 ? 0u - (uint32_t)v : (uint32_t)v);
@@ -157,7 +181,7 @@ __device__ inline int64_t sc_apply32(Sc a, int32_t v) {
 // floor(n / d) for 0 < d < 2^63 when the quotient is below 2^40: the double estimate's absolute error is then below
 // 2^40 * 2^-50 (three roundings of relative size 2^-53 each), so one correction step each way suffices; two are
 // allowed.
-__device__ inline uint64_t udiv_small_q(u128 n, int64_t d) {
+KT_SC_FN uint64_t udiv_small_q(u128 n, int64_t d) {
     const double dn = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 + (double)(uint64_t)n;
     const double qd = dn / (double)d;
     uint64_t q = qd <= 0.0 ? 0 : (uint64_t)qd;
@@ -173,7 +197,7 @@ __device__ inline uint64_t udiv_small_q(u128 n, int64_t d) {
 
 // requant_dyn(v, 2^28, den) (crates/01-engine/kt-core/src/layers.rs:33-39) for |v| <= den: the quotient is at most
 // 2^28, within udiv_small_q's range.
-__device__ inline int32_t requant_dyn_dev(int64_t v, int64_t den) {
+KT_SC_FN int32_t requant_dyn_dev(int64_t v, int64_t den) {
     const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
     const uint64_t q = udiv_small_q(((u128)a << 28) + (u128)(uint64_t)(den / 2), den);
     return (int32_t)(v < 0 ? 0 - q : q);
