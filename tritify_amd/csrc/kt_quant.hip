@@ -125,6 +125,74 @@ struct QlOut {
     kt_hip_qscale* os[KT_QL_MAX_SEG];
 };
 
+// A segment's Scale products for max |x| = m (layers.rs:279-303): c = from_ratio(m, WLEVELS) * xs * ws, the bias
+// factor f = bs * c^-1, and the mode (0: normal; 1: m == 0, the output is the bias codes or zeros; 2: c == 0, zeros).
+struct QlHead {
+    int64_t xmax;
+    Sc c, f;
+    int mode;
+};
+__device__ inline QlHead ql_head(uint32_t m, const kt_hip_qscale* xs, const QlScales& sc, int g) {
+    QlHead h{(int64_t)m, Sc{0, 0}, Sc{0, 0}, 0};
+    if (m == 0) {
+        h.mode = 1;
+        return h;
+    }
+    h.c = sc_mul(sc_mul(from_ratio((u128)m, (u128)WLEVELS), Sc{xs->mant, xs->shift}), Sc{sc.w_mant[g], sc.w_shift[g]});
+    if (h.c.mant == 0) h.mode = 2;
+    else if (sc.has_bias[g]) h.f = sc_mul(Sc{sc.b_mant[g], sc.b_shift[g]}, sc_recip(h.c));
+    return h;
+}
+
+// The three balanced base-256 digits of quant_to(x, xmax) for 4 columns (layers.rs:23-31), as one byte of each
+// plane word: |num| = |x| * WLEVELS < 2^49 is exact in a double, the quotient is corrected to the exact one.
+__device__ inline void ql_digits4(const int32_t xv[4], int64_t xmax, uint32_t word[3]) {
+    const int64_t half = xmax / 2;
+    word[0] = word[1] = word[2] = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        int64_t v = 0;
+        if (xv[t] != 0) {
+            const int64_t num = (int64_t)xv[t] * WLEVELS;
+            const uint64_t a = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
+            const uint64_t qq = udiv_est53(a, xmax);  // a < 2^31 * WLEVELS + 2^30 < 2^53
+            v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
+        }
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const int64_t d = ((v + 128) & 255) - 128;
+            word[p] |= ((uint32_t)d & 255u) << (8 * t);
+            v = (v - d) >> 8;
+        }
+    }
+}
+
+// ql_digits4 with the quotient from a multiplication by rinv = 1 / xmax (a double): for a < 2^53 and xmax < 2^32
+// the estimate of a / xmax (below 2^19 here) is off by less than 2^-30, so at most one step from the exact floor,
+// which the two integer tests restore. The same digits as ql_digits4.
+__device__ inline void ql_digits4r(const int32_t xv[4], uint32_t xmax, double rinv, uint32_t word[3]) {
+    const uint64_t half = xmax / 2;
+    word[0] = word[1] = word[2] = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        int64_t v = 0;
+        if (xv[t] != 0) {
+            const int64_t num = (int64_t)xv[t] * WLEVELS;
+            const uint64_t a = (uint64_t)(num < 0 ? -num : num) + half;
+            uint64_t qq = (uint64_t)((double)a * rinv);
+            if (qq * xmax > a) qq--;
+            else if ((qq + 1) * xmax <= a) qq++;
+            v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
+        }
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const int64_t d = ((v + 128) & 255) - 128;
+            word[p] |= ((uint32_t)d & 255u) << (8 * t);
+            v = (v - d) >> 8;
+        }
+    }
+}
+
 template <bool CONV>
 __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __restrict__ x, int64_t nx,
                                                               int64_t rows, int64_t in, int64_t kp, ConvGeom geom,
@@ -154,28 +222,13 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
     if (blockIdx.x == 0 && threadIdx.x < KT_QL_YSLOTS * seg.n)
         st[threadIdx.x / KT_QL_YSLOTS].ymax[threadIdx.x % KT_QL_YSLOTS].v = 0;
     if (blockIdx.x == 0 && (int)threadIdx.x < seg.n) {  // each segment's record, for the GEMM epilogue and ql_requant
-        const int g = threadIdx.x;
-        QlState s{};
-        s.xmax = (int64_t)m;
-        if (m == 0) {
-            s.mode = 1;
-        } else {
-            const Sc c = sc_mul(sc_mul(from_ratio((u128)m, (u128)WLEVELS), Sc{xs->mant, xs->shift}),
-                                Sc{sc.w_mant[g], sc.w_shift[g]});
-            s.c_mant = c.mant, s.c_shift = c.shift;
-            if (c.mant == 0) {
-                s.mode = 2;
-            } else if (sc.has_bias[g]) {
-                const Sc f = sc_mul(Sc{sc.b_mant[g], sc.b_shift[g]}, sc_recip(c));
-                s.f_mant = f.mant, s.f_shift = f.shift;
-            }
-        }
-        QlState* q = st + g;
-        q->xmax = s.xmax, q->c_mant = s.c_mant, q->f_mant = s.f_mant;
-        q->c_shift = s.c_shift, q->f_shift = s.f_shift, q->mode = s.mode;
+        const QlHead h = ql_head(m, xs, sc, threadIdx.x);
+        QlState* q = st + threadIdx.x;
+        q->xmax = h.xmax, q->c_mant = h.c.mant, q->f_mant = h.f.mant;
+        q->c_shift = h.c.shift, q->f_shift = h.f.shift, q->mode = h.mode;
     }
     const int64_t quads = rows * (kp / 4);
-    const int64_t xmax = (int64_t)m, half = xmax / 2;
+    const int64_t xmax = (int64_t)m;
     const bool live = m != 0;
     const size_t plane = (size_t)rows * (size_t)kp;
     const int64_t qpr = kp / 4, q0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x;
@@ -186,22 +239,9 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
         const int64_t c0 = cq * 4;
         uint32_t word[3] = {0, 0, 0};
         int32_t xv[4] = {0, 0, 0, 0};
-        if (live) ql_fetch4<CONV>(x, r, c0, in, geom, xv);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            int64_t v = 0;
-            if (xv[t] != 0) {
-                const int64_t num = (int64_t)xv[t] * WLEVELS;  // |num| < 2^49: exact in a double
-                const uint64_t a = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
-                const uint64_t qq = udiv_est53(a, xmax);  // a < 2^31 * WLEVELS + 2^30 < 2^53
-                v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
-            }
-#pragma unroll
-            for (int p = 0; p < 3; p++) {
-                const int64_t d = ((v + 128) & 255) - 128;
-                word[p] |= ((uint32_t)d & 255u) << (8 * t);
-                v = (v - d) >> 8;
-            }
+        if (live) {
+            ql_fetch4<CONV>(x, r, c0, in, geom, xv);
+            ql_digits4(xv, xmax, word);
         }
         const size_t at = (size_t)r * (size_t)kp + (size_t)c0;
 #pragma unroll
@@ -209,49 +249,243 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
     }
 }
 
+
+// One row (the decode step): the quant pass and the digit product in one launch. Every CTA takes max |x| over the
+// row and forms the row's three digit planes in LDS itself (a few thousand values, read from L2 by each CTA) while
+// its first weight chunks are in flight, then runs the product of plane_skinny_kernel over its 8 output columns
+// (4 waves x 2 columns, the lanes striding k in 16-byte chunks, int32 plane-group sums by sdot4, a butterfly across
+// the wave). The CTA's largest |result| goes to its own slot part[blockIdx.x] (overwritten on every call, so no
+// pass has to clear it); ql_requant_kernel takes each segment's maximum over its CTAs' slots. CTA 0 writes each
+// segment's state for ql_requant_kernel. A CTA whose segment has a bias forms the bias factor itself. Requires
+// kp <= QS_MAX_KP and a single k-chunk (kp within the flush bound).
+constexpr int QS_MAX_KP = 8192;
+constexpr int64_t QS_FUSED_KP = 1024, QS_FUSED_OUT = 4096;  // where launch_ql_impl takes this path
+constexpr int QS_THREADS = 256, QS_WAVES = QS_THREADS / 64;
+constexpr int QS_CPW = 2;  // output columns per wave
+constexpr int QS_COLS = QS_WAVES * QS_CPW;
+
+template <int PW>
+__global__ __launch_bounds__(QS_THREADS) void ql_skinny_kernel(const int32_t* __restrict__ x, int in, int kp,
+                                                               const kt_hip_qscale* __restrict__ xs,
+                                                               const int8_t* __restrict__ wb, int64_t* __restrict__ y,
+                                                               int N, const int64_t* __restrict__ bias, QlSeg seg,
+                                                               QlScales sc, QlState* __restrict__ st,
+                                                               int64_t* __restrict__ part) {
+    constexpr int NG = 3 + PW - 1, QPT = QS_MAX_KP / 4 / QS_THREADS;
+    __shared__ __attribute__((aligned(16))) int8_t xq[3 * QS_MAX_KP];
+    __shared__ uint32_t red[QS_WAVES];
+    __shared__ int64_t s_max[QS_WAVES];
+    __shared__ int64_t s_f[2];  // the bias factor of this CTA's segment (mant, shift), when it has a bias
+    __shared__ int s_badd;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = ((int)blockIdx.x * QS_WAVES + wave) * QS_CPW;  // the wave's first column
+    const int g = ql_seg_of(seg, (int)blockIdx.x * QS_COLS);
+    const size_t wplane = (size_t)N * kp;
+    const int nch = kp / 16;
+
+    v4i wn[QS_CPW][PW];  // the weights of the wave's next chunk
+    auto wload = [&](int q) {
+#pragma unroll
+        for (int c = 0; c < QS_CPW; c++)
+#pragma unroll
+            for (int j = 0; j < PW; j++)
+                wn[c][j] = q < nch && nb + c < N
+                               ? *reinterpret_cast<const v4i*>(wb + j * wplane + (size_t)(nb + c) * kp + 16 * (size_t)q)
+                               : v4i{};
+    };
+    wload(lane);  // in flight while the row is quantized
+
+    // the row, 4 columns per quad, QPT quads per thread held in registers; max |x| over the CTA
+    int32_t xv[QPT][4];
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int c0 = 4 * (tid + QS_THREADS * k);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            xv[k][t] = c0 + t < in ? x[c0 + t] : 0;
+            const uint32_t a = xv[k][t] < 0 ? 0u - (uint32_t)xv[k][t] : (uint32_t)xv[k][t];
+            m = a > m ? a : m;
+        }
+    }
+    m = block_max(m, red);
+    const double rinv = m != 0 ? 1.0 / (double)m : 0.0;
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int c0 = 4 * (tid + QS_THREADS * k);
+        if (c0 < kp) {
+            uint32_t word[3] = {0, 0, 0};
+            if (m != 0) ql_digits4r(xv[k], m, rinv, word);
+#pragma unroll
+            for (int p = 0; p < 3; p++) *reinterpret_cast<uint32_t*>(xq + p * kp + c0) = word[p];
+        }
+    }
+    if (blockIdx.x == 0 && tid < seg.n) {  // each segment's state, for ql_requant_kernel
+        const QlHead h = ql_head(m, xs, sc, tid);
+        QlState* q = st + tid;
+        q->xmax = h.xmax, q->c_mant = h.c.mant, q->f_mant = h.f.mant;
+        q->c_shift = h.c.shift, q->f_shift = h.f.shift, q->mode = h.mode;
+    }
+    if (tid == 0) {
+        int badd = 0;
+        if (bias && sc.has_bias[g]) {
+            const QlHead h = ql_head(m, xs, sc, g);
+            badd = h.mode == 0;
+            s_f[0] = h.f.mant, s_f[1] = h.f.shift;
+        }
+        s_badd = badd;
+    }
+    __syncthreads();
+
+    int acc[QS_CPW][NG];
+#pragma unroll
+    for (int c = 0; c < QS_CPW; c++)
+#pragma unroll
+        for (int i = 0; i < NG; i++) acc[c][i] = 0;
+    for (int q = lane; q < nch; q += 64) {
+        v4i wv[QS_CPW][PW];
+#pragma unroll
+        for (int c = 0; c < QS_CPW; c++)
+#pragma unroll
+            for (int j = 0; j < PW; j++) wv[c][j] = wn[c][j];
+        wload(q + 64);
+        v4i xd[3];
+#pragma unroll
+        for (int i = 0; i < 3; i++) xd[i] = *reinterpret_cast<const v4i*>(xq + i * kp + 16 * q);
+#pragma unroll
+        for (int c = 0; c < QS_CPW; c++)
+#pragma unroll
+            for (int i = 0; i < 3; i++)
+#pragma unroll
+                for (int j = 0; j < PW; j++) {
+                    int d = acc[c][i + j];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) d = __builtin_amdgcn_sdot4(xd[i][e], wv[c][j][e], d, false);
+                    acc[c][i + j] = d;
+                }
+    }
+#pragma unroll
+    for (int c = 0; c < QS_CPW; c++)
+#pragma unroll
+        for (int i = 0; i < NG; i++)
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) acc[c][i] += __shfl_xor(acc[c][i], o);
+    int64_t lmax = 0;
+    if (lane == 0) {
+        const bool badd = s_badd != 0;
+#pragma unroll
+        for (int c = 0; c < QS_CPW; c++) {
+            const int n = nb + c;
+            if (n >= N) continue;
+            uint64_t f = badd ? (uint64_t)scale_apply(s_f[0], (int32_t)s_f[1], bias[n]) : 0;
+#pragma unroll
+            for (int i = 0; i < NG; i++) f += (uint64_t)(int64_t)acc[c][i] << (8 * i);  // NG <= 7: 8 i < 64
+            y[n] = (int64_t)f;
+            const int64_t a = (int64_t)f < 0 ? (int64_t)(0 - f) : (int64_t)f;  // i64::abs, wrapping
+            lmax = a > lmax ? a : lmax;
+        }
+        s_max[wave] = lmax;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int64_t b = s_max[0];
+        for (int w = 1; w < QS_WAVES; w++) b = s_max[w] > b ? s_max[w] : b;
+        part[blockIdx.x] = b > 0 ? b : 0;
+    }
+}
+
+// y = requant_dyn(acc, ACT_LEVELS, ymax) per segment (layers.rs:33-39, 321-327). The grid's last CTA only writes
+// each segment's record (its Scale products run beside the other CTAs' divisions); the others requantize. Each
+// thread's first accumulator and the segments' states are read before the maximum is known. The maximum comes from
+// the state's slots, or with `part` from the one-row product's maximum per CTA of QS_COLS columns.
 __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* __restrict__ acc, int64_t n,
                                                                 int64_t out, const int64_t* __restrict__ bias,
                                                                 const QlState* __restrict__ st, QlSeg seg,
-                                                                QlScales sc, QlOut yo) {
+                                                                QlScales sc, QlOut yo,
+                                                                const int64_t* __restrict__ part, int nparts) {
     __shared__ int64_t s_ymax[KT_QL_MAX_SEG];
     __shared__ int32_t s_mode[KT_QL_MAX_SEG];
-    if ((int)threadIdx.x < seg.n) {  // each segment's output maximum, mode and (CTA 0) record
-        const int g = threadIdx.x;
-        const QlState* q = st + g;
-        int64_t ymax = 0;
+    __shared__ unsigned long long s_pmax[KT_QL_MAX_SEG];
+    const bool rec_cta = blockIdx.x == gridDim.x - 1;
+    const int tid = threadIdx.x;
+    const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + tid, step = (int64_t)(gridDim.x - 1) * QL_THREADS;
+    const int64_t a_first = !rec_cta && i0 < n ? acc[i0] : 0;
+    int mode = 0;
+    int64_t xmax = 0, c_mant = 0;
+    int32_t c_shift = 0;
+    if (tid < seg.n) {
+        const QlState* q = st + tid;
+        mode = q->mode, xmax = q->xmax, c_mant = q->c_mant, c_shift = q->c_shift;
+    }
+    int64_t ymax = 0;
+    if (part) {  // each segment's maximum over its CTAs' slots
+        if (tid < KT_QL_MAX_SEG) s_pmax[tid] = 0;
+        __syncthreads();
+        unsigned long long pm[KT_QL_MAX_SEG] = {};
+        for (int c0 = tid; c0 < nparts; c0 += 4 * QL_THREADS) {  // 4 loads in flight per thread
+            unsigned long long v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int c = c0 + u * QL_THREADS;
+                v[u] = c < nparts ? (unsigned long long)part[c] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int g = ql_seg_of(seg, (c0 + u * QL_THREADS) * QS_COLS);
+#pragma unroll
+                for (int i = 0; i < KT_QL_MAX_SEG; i++)
+                    if (i == g) pm[i] = v[u] > pm[i] ? v[u] : pm[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < KT_QL_MAX_SEG; i++) {
+            if (i >= seg.n) break;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const unsigned long long u = __shfl_xor(pm[i], o);
+                pm[i] = u > pm[i] ? u : pm[i];
+            }
+            if ((tid & 63) == 0 && pm[i] != 0) atomicMax(&s_pmax[i], pm[i]);
+        }
+        __syncthreads();
+        if (tid < seg.n) ymax = (int64_t)s_pmax[tid];
+    } else if (tid < seg.n) {
+        const QlState* q = st + tid;
 #pragma unroll
         for (int i = 0; i < KT_QL_YSLOTS; i++) ymax = (int64_t)q->ymax[i].v > ymax ? (int64_t)q->ymax[i].v : ymax;
-        const int mode = q->mode;
-        s_ymax[g] = ymax, s_mode[g] = mode;
-        if (blockIdx.x == 0) {
+    }
+    if (rec_cta) {  // each segment's record
+        if (tid < seg.n) {
+            const int g = tid;
             kt_hip_qscale o{};
-            o.xmax = q->xmax;
+            o.xmax = xmax;
             if (mode == 1) {
                 if (sc.has_bias[g]) o.mant = sc.b_mant[g], o.shift = sc.b_shift[g];
             } else if (mode == 0 && ymax > 0) {
-                const Sc s2 = sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{q->c_mant, q->c_shift});
+                const Sc s2 = sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{c_mant, c_shift});
                 o.mant = s2.mant, o.shift = s2.shift, o.ymax = ymax;
             }
             *yo.os[g] = o;
         }
+        return;
     }
+    if (tid < seg.n) s_ymax[tid] = ymax, s_mode[tid] = mode;
     __syncthreads();
-    const int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x, step = (int64_t)gridDim.x * QL_THREADS;
     const int64_t dstep = step % out, rstep = step / out;
     int64_t o = i0 % out, r = i0 / out;  // (row, column) of i, advanced incrementally
     for (int64_t i = i0; i < n; i += step, r += rstep, o += dstep) {
         if (o >= out) o -= out, r++;
         const int g = ql_seg_of(seg, (int)o);
-        const int64_t ymax = s_ymax[g];
-        const int mode = s_mode[g];
+        const int64_t ym = s_ymax[g];
+        const int md = s_mode[g];
         int32_t v32 = 0;
-        if (mode == 1) {
+        if (md == 1) {
             v32 = sc.has_bias[g] && bias ? (int32_t)bias[o] : 0;
-        } else if (mode == 0 && ymax > 0) {
-            const int64_t v = acc[i];
+        } else if (md == 0 && ym > 0) {
+            const int64_t v = i == i0 ? a_first : acc[i];
             const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
             // requant_dyn(v, 2^28, ymax): q <= 2^28
-            const uint64_t q = udiv_small_q(((u128)a << 28) + (u128)(uint64_t)(ymax / 2), ymax);
+            const uint64_t q = udiv_small_q(((u128)a << 28) + (u128)(uint64_t)(ym / 2), ym);
             v32 = (int32_t)(v < 0 ? 0 - q : q);
         }
         const int64_t w = seg.col0[g + 1] - seg.col0[g];
@@ -303,8 +537,11 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_conv_kernel(const int64
 
 size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]) {
     const size_t kp = (size_t)((in + 63) / 64 * 64);
-    const size_t sizes[KT_QL_WS_PARTS] = {3 * (size_t)rows * kp, (size_t)rows * (size_t)out * 8, KT_QL_PARTS * 4,
-                                          KT_QL_PARTS * 8, KT_QL_MAX_SEG * sizeof(QlState)};
+    // part 2: the partial maxima of |x|, or for one row the product's maximum per CTA of QS_COLS columns
+    const size_t pmax = rows == 1 ? (size_t)((out + QS_COLS - 1) / QS_COLS) * 8 : 0;
+    const size_t sizes[KT_QL_WS_PARTS] = {3 * (size_t)rows * kp, (size_t)rows * (size_t)out * 8,
+                                          pmax > KT_QL_PARTS * 4 ? pmax : KT_QL_PARTS * 4, KT_QL_PARTS * 8,
+                                          KT_QL_MAX_SEG * sizeof(QlState)};
     size_t at = 0;
     for (int i = 0; i < KT_QL_WS_PARTS; i++) {
         off[i] = at;
@@ -365,6 +602,28 @@ static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, con
     const int ntiles = splits > 1 ? (int)(((out + 63) / 64) * ((rows + 63) / 64)) : 0;
     if (ntiles * 4 > KT_QL_PARTS * 8) return hipErrorInvalidValue;  // cannot happen: a split grid has < 128 tiles
 
+    // one row within one k-chunk (the decode step): the quant pass inside the product, then the requant pass
+    // (a short row: each CTA quantizes it again, so a long one, or a grid of many CTAs, keeps the quant pass)
+    bool seg_ok = true;  // every CTA of QS_COLS columns within one segment
+    for (int g = 1; g < seg.n; g++) seg_ok = seg_ok && seg.col0[g] % QS_COLS == 0;
+    if (!geom && rows == 1 && kp <= QS_FUSED_KP && out <= QS_FUSED_OUT && kp <= flush_k && seg_ok &&
+        (pw == 1 || pw == 3 || pw == 5)) {
+        const int ctas = (int)((out + QS_COLS - 1) / QS_COLS);
+        int64_t* pm = reinterpret_cast<int64_t*>(base + off[2]);
+        if (pw == 1)
+            ql_skinny_kernel<1><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, seg, sc,
+                                                            st, pm);
+        else if (pw == 3)
+            ql_skinny_kernel<3><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, seg, sc,
+                                                            st, pm);
+        else
+            ql_skinny_kernel<5><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, seg, sc,
+                                                            st, pm);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        ql_requant_kernel<<<grid_for(n, 1) + 1, QL_THREADS, 0, s>>>(acc, n, out, bias, st, seg, sc, yo, pm, ctas);
+        return hipGetLastError();
+    }
     // max |x| by its own pass, or inside every quant CTA when x is short (one launch fewer for a decode row)
     const int gx = nx <= QL_FUSED_MAX ? 0 : grid_for(nx, 8);
     if (gx > 0) ql_absmax_kernel<<<gx, QL_THREADS, 0, s>>>(x, nx, part_x);
@@ -392,7 +651,8 @@ static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, con
         return hipGetLastError();
     }
     // one output per thread for short outputs (a decode row: its divisions then run side by side, not 8 in a row)
-    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 2), QL_THREADS, 0, s>>>(acc, n, out, bias, st, seg, sc, yo);
+    ql_requant_kernel<<<grid_for(n, n <= 65536 ? 1 : 2) + 1, QL_THREADS, 0, s>>>(acc, n, out, bias, st, seg, sc, yo,
+                                                                                 nullptr, 0);
     return hipGetLastError();
 }
 
