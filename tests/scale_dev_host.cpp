@@ -33,3 +33,5 @@ int64_t sd_apply32(int64_t am, int32_t as, int32_t v) { return kt::sc_apply32(Sc
 int32_t sd_requant_dyn(int64_t v, int64_t den) { return kt::requant_dyn_dev(v, den); }
 uint64_t sd_udiv_small_q(uint64_t nh, uint64_t nl, int64_t d) { return kt::udiv_small_q(join(nh, nl), d); }
 }
+
+extern "C" int32_t sd_rq_apply(int64_t den, int64_t v) { return kt::rq_apply(kt::rq_den(den), v); }

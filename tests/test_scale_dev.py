@@ -45,6 +45,7 @@ def sd(tmp_path_factory):
         ("sd_apply32", i64, [i64, i32, i32]),
         ("sd_requant_dyn", i32, [i64, i64]),
         ("sd_udiv_small_q", u, [u, u, i64]),
+        ("sd_rq_apply", i32, [i64, i64]),
     ):
         f = getattr(L, name)
         f.restype, f.argtypes = res, args
@@ -162,3 +163,27 @@ def test_requant_dyn_and_small_quotients(sd):
         n = rand_bits(rng, min(127, d.bit_length() + int(rng.integers(0, 41))))
         if n // d < 2**40:
             assert sd.sd_udiv_small_q(n >> 64, n & U64, d) == n // d, (n, d)
+
+
+def test_requant_by_reciprocal_equals_requant_dyn(sd):
+    """rq_apply: the per-tensor requant without a division per value, on both sides of its 2^62 bound, at the
+    rounding boundaries (|v| * 2^28 + den / 2 an exact multiple of den, and one below) and at |v| = den."""
+    rng = np.random.default_rng(16)
+    cases = [(1, 1), (1, -1), (1, 0), (2, 1), (3, 1), (3, 2), (2**62 - 1, 2**62 - 1), (2**62, 2**62 - 5),
+             (2**63 - 1, -(2**63 - 1)), (2**63 - 1, 2**62), (5, 7)]
+    for _ in range(6000):
+        den = rand_bits(rng, int(rng.integers(1, 64)))
+        v = int(rng.integers(-den, den + 1)) if den < 2**62 else rand_bits(rng, int(rng.integers(0, den.bit_length())))
+        cases.append((den, v))
+        # for odd den, the |v| with |v| * 2^28 + den / 2 an exact multiple of den, and its neighbours: the quotient
+        # sits on a rounding boundary, where an estimate can land on either side
+        if den % 2 == 1 and den > 2:
+            a = (-(den // 2) * pow(2**28, -1, den)) % den
+            for aa in (a - 1, a, a + 1):
+                if 0 <= aa <= den:
+                    cases += [(den, aa), (den, -aa)]
+        cases.append((den, den))
+        cases.append((den, -den))
+    for den, v in cases:
+        want = O.requant_dyn(v, 2**28, den) if abs(v) <= den else sd.sd_requant_dyn(v, den)
+        assert sd.sd_rq_apply(den, v) == want, (den, v)

@@ -404,6 +404,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* _
                                                                 QlScales sc, QlOut yo,
                                                                 const int64_t* __restrict__ part, int nparts) {
     __shared__ int64_t s_ymax[KT_QL_MAX_SEG];
+    __shared__ double s_rinv[KT_QL_MAX_SEG];
     __shared__ int32_t s_mode[KT_QL_MAX_SEG];
     __shared__ unsigned long long s_pmax[KT_QL_MAX_SEG];
     const bool rec_cta = blockIdx.x == gridDim.x - 1;
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* _
         }
         return;
     }
-    if (tid < seg.n) s_ymax[tid] = ymax, s_mode[tid] = mode;
+    if (tid < seg.n) s_ymax[tid] = ymax, s_mode[tid] = mode, s_rinv[tid] = rq_den(ymax).rinv;
     __syncthreads();
     const int64_t dstep = step % out, rstep = step / out;
     int64_t o = i0 % out, r = i0 / out;  // (row, column) of i, advanced incrementally
@@ -481,12 +482,8 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_kernel(const int64_t* _
         int32_t v32 = 0;
         if (md == 1) {
             v32 = sc.has_bias[g] && bias ? (int32_t)bias[o] : 0;
-        } else if (md == 0 && ym > 0) {
-            const int64_t v = i == i0 ? a_first : acc[i];
-            const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
-            // requant_dyn(v, 2^28, ymax): q <= 2^28
-            const uint64_t q = udiv_small_q(((u128)a << 28) + (u128)(uint64_t)(ym / 2), ym);
-            v32 = (int32_t)(v < 0 ? 0 - q : q);
+        } else if (md == 0 && ym > 0) {  // requant_dyn(v, 2^28, ymax)
+            v32 = rq_apply(RqDen{ym, (uint64_t)(ym / 2), s_rinv[g]}, i == i0 ? a_first : acc[i]);
         }
         const int64_t w = seg.col0[g + 1] - seg.col0[g];
         yo.y[g][r * w + (o - seg.col0[g])] = v32;
@@ -514,17 +511,14 @@ __global__ __launch_bounds__(QL_THREADS) void ql_requant_conv_kernel(const int64
         }
         *os = o;
     }
-    const u128 halfd = (u128)(uint64_t)(ymax / 2);
+    const RqDen rd = rq_den(ymax);
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const int64_t r0 = (int64_t)blockIdx.x * 64, o0 = (int64_t)blockIdx.y * 64;
     for (int rr = ty; rr < 64; rr += QL_THREADS / 64) {
         const int64_t r = r0 + rr, o = o0 + tx;
         int32_t q32 = 0;
         if (live && r < rows && o < out) {
-            const int64_t v = acc[r * out + o];
-            const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
-            const uint64_t q = udiv_small_q(((u128)a << 28) + halfd, ymax);
-            q32 = (int32_t)(v < 0 ? 0 - q : q);
+            q32 = rq_apply(rd, acc[r * out + o]);
         }
         tile[tx][rr] = q32;
     }

@@ -254,10 +254,11 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
             m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
         }
         const int64_t gmax = block_max_i64(m, red);
+        const RqDen rd_gmax = rq_den(gmax);
 #pragma unroll
         for (int k = 0; k < RD_NV; k++) {
             const int i = threadIdx.x + RD_THREADS * k;
-            if (i < dim) y[i] = gmax == 0 ? 0 : requant_dyn_dev(hv[k], gmax);
+            if (i < dim) y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
         }
         if (threadIdx.x == 0)
             put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
@@ -303,8 +304,9 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
             m = iabs(v) > m ? iabs(v) : m;
         }
     const int64_t gmax = block_max_i64(m, red);
+    const RqDen rd_gmax = rq_den(gmax);
     for (int i = threadIdx.x; i < n; i += RD_THREADS)
-        y[i] = gmax == 0 ? 0 : requant_dyn_dev(sc_apply(frow[i / dim], (int64_t)x[i] * (int64_t)g[i % dim]), gmax);
+        y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, sc_apply(frow[i / dim], (int64_t)x[i] * (int64_t)g[i % dim]));
     if (threadIdx.x == 0)
         put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
 }
@@ -354,15 +356,16 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, co
         }
     }
     const int64_t gmax = block_max_i64(m, red);  // every read of a, b, and their records, is done past here
+    const RqDen rd_gmax = rq_den(gmax);
     if (held) {
 #pragma unroll
         for (int k = 0; k < RD_AV; k++) {
             const int i = threadIdx.x + RD_THREADS * k;
-            if (i < n) y[i] = gmax == 0 ? 0 : requant_dyn_dev(hv[k], gmax);
+            if (i < n) y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
         }
     } else {
         for (int i = threadIdx.x; i < n; i += RD_THREADS)
-            y[i] = gmax == 0 ? 0 : requant_dyn_dev(wadd(sc_apply32(fa, a[i]), sc_apply32(fb, b[i])), gmax);
+            y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, wadd(sc_apply32(fa, a[i]), sc_apply32(fb, b[i])));
     }
     if (threadIdx.x == 0)
         put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
@@ -430,14 +433,15 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
         }
     }
     const int64_t hmax = block_max_i64(m, red);
+    const RqDen rd_hmax = rq_den(hmax);
     if (held) {
 #pragma unroll
         for (int i = 0; i < RD_VPT; i++) {
             const int k = threadIdx.x + RD_THREADS * i;
-            if (k < n) h[k] = hmax == 0 ? 0 : requant_dyn_dev(hv[i], hmax);
+            if (k < n) h[k] = hmax == 0 ? 0 : rq_apply(rd_hmax, hv[i]);
         }
     } else {
-        for (int k = threadIdx.x; k < n; k += RD_THREADS) h[k] = hmax == 0 ? 0 : requant_dyn_dev(act(k), hmax);
+        for (int k = threadIdx.x; k < n; k += RD_THREADS) h[k] = hmax == 0 ? 0 : rq_apply(rd_hmax, act(k));
     }
     if (threadIdx.x == 0)
         put_rec(hs, hmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)hmax, (u128)ACT_LEVELS), hsc));
@@ -685,7 +689,8 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         }
     }
     const int64_t gmax = block_max_i64(m, red);
-    for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = gmax == 0 ? 0 : requant_dyn_dev(HO[i], gmax);
+    const RqDen rd_gmax = rq_den(gmax);
+    for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, HO[i]);
     if (tid == 0)
         put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
 }
@@ -797,8 +802,9 @@ __global__ __launch_bounds__(256) void rs_max_kernel(RdSeq q) {
 __global__ __launch_bounds__(256) void rs_out_kernel(RdSeq q) {
     const RdSeqWs* w = q.ws;
     const int64_t gmax = (int64_t)w->gmax;
+    const RqDen rd_gmax = rq_den(gmax);
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < q.n; i += (int64_t)gridDim.x * 256)
-        q.y[i] = gmax == 0 ? 0 : requant_dyn_dev(rs_value(q, w, i), gmax);
+        q.y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, rs_value(q, w, i));
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         const Sc sc = q.op == RS_SWIGLU ? w->par[2] : w->par[0];  // the tensor's scale before the requant
         put_rec(q.ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), sc));
@@ -925,13 +931,14 @@ __global__ __launch_bounds__(256) void rp_apply_kernel(RdPrefill a) {
 
 __global__ __launch_bounds__(256) void rp_out_kernel(RdPrefill a) {
     const int64_t gmax = (int64_t)*a.gmax;
+    const RqDen rd_gmax = rq_den(gmax);
     const Sc common = *a.common;
     const bool live = common.mant != 0 && gmax > 0;
     const int qw = a.nh * a.hd;
     const int64_t n = (int64_t)a.T * qw;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
         const int64_t i = e / qw, r = e - i * qw, h = r / a.hd, d = r - h * a.hd;  // e indexes o[i][h][d]
-        a.o[e] = live ? requant_dyn_dev(a.hout[((size_t)h * a.T + i) * a.hd + d], gmax) : 0;
+        a.o[e] = live ? rq_apply(rd_gmax, a.hout[((size_t)h * a.T + i) * a.hd + d]) : 0;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0)
         put_rec(a.os, live ? sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common) : Sc{0, 0});

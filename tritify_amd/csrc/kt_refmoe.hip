@@ -242,15 +242,16 @@ __global__ __launch_bounds__(RQ_ROW_THREADS) void rq_requant_kernel(const int64_
         for (int64_t i = threadIdx.x; i < out; i += RQ_ROW_THREADS) m = iabs(sum(i)) > m ? iabs(sum(i)) : m;
     }
     const int64_t ymax = block_max_t(m, red);
+    const RqDen rd_ymax = rq_den(ymax);
     if (held) {
 #pragma unroll
         for (int i = 0; i < RQ_VPT; i++) {
             const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
-            if (c < out) y[r * out + c] = ymax ? requant_dyn_dev(v[i], ymax) : 0;
+            if (c < out) y[r * out + c] = ymax ? rq_apply(rd_ymax, v[i]) : 0;
         }
     } else {
         for (int64_t i = threadIdx.x; i < out; i += RQ_ROW_THREADS)
-            y[r * out + i] = ymax ? requant_dyn_dev(sum(i), ymax) : 0;
+            y[r * out + i] = ymax ? rq_apply(rd_ymax, sum(i)) : 0;
     }
     if (threadIdx.x == 0) {
         kt_hip_qscale o{};
@@ -683,13 +684,14 @@ __global__ __launch_bounds__(RM_COMBINE_THREADS) void rm_combine_kernel(const in
                 if (d0 + RM_COMBINE_THREADS * j < dim) m = iabs(hv[j]) > m ? iabs(hv[j]) : m;
         }
     const int64_t gmax = block_max_t(m, red);
+    const RqDen rd_gmax = rq_den(gmax);
     const bool held = dim <= span;  // hv still holds this thread's sums
     for (int d0 = threadIdx.x; d0 < dim; d0 += span) {
         if (gmax && !held) sums(d0, hv);
 #pragma unroll
         for (int j = 0; j < RM_VPT; j++) {
             const int d = d0 + RM_COMBINE_THREADS * j;
-            if (d < dim) out[(int64_t)t * dim + d] = gmax ? requant_dyn_dev(hv[j], gmax) : 0;
+            if (d < dim) out[(int64_t)t * dim + d] = gmax ? rq_apply(rd_gmax, hv[j]) : 0;
         }
     }
     if (threadIdx.x == 0) {
@@ -770,8 +772,9 @@ __global__ __launch_bounds__(RQ_THREADS) void rm_merge_out_kernel(const int32_t*
                                                                   int32_t* __restrict__ out,
                                                                   kt_hip_qscale* __restrict__ os) {
     const int64_t gmax = (int64_t)*gmax_slot;
+    const RqDen rd_gmax = rq_den(gmax);
     for (int64_t i = (int64_t)blockIdx.x * RQ_THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * RQ_THREADS)
-        out[i] = gmax ? requant_dyn_dev(sc_apply(fac[i / dim], rows[i]), gmax) : 0;
+        out[i] = gmax ? rq_apply(rd_gmax, sc_apply(fac[i / dim], rows[i])) : 0;
     if (blockIdx.x == 0 && threadIdx.x == 0)
         put_rec(os, gmax ? sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), *common) : Sc{0, 0});
 }
