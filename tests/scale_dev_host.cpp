@@ -35,3 +35,4 @@ uint64_t sd_udiv_small_q(uint64_t nh, uint64_t nl, int64_t d) { return kt::udiv_
 }
 
 extern "C" int32_t sd_rq_apply(int64_t den, int64_t v) { return kt::rq_apply(kt::rq_den(den), v); }
+extern "C" uint64_t sd_udiv64_small(uint64_t n, uint64_t d) { return kt::udiv64_small(n, d); }

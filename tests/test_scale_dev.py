@@ -46,6 +46,7 @@ def sd(tmp_path_factory):
         ("sd_requant_dyn", i32, [i64, i64]),
         ("sd_udiv_small_q", u, [u, u, i64]),
         ("sd_rq_apply", i32, [i64, i64]),
+        ("sd_udiv64_small", u, [u, u]),
     ):
         f = getattr(L, name)
         f.restype, f.argtypes = res, args
@@ -137,6 +138,46 @@ def test_scale_ops_equal_the_oracle(sd):
         for f, g in ((sd.sd_recip, O.scale_recip), (sd.sd_rsqrt, O.scale_rsqrt)):
             w = g(a)
             assert scale_out(f, am, ash) == (w.mant, w.shift), (f, am, ash)
+
+
+def test_udiv64_small_at_exact_multiples(sd):
+    """udiv64_small (d < 2^32, quotient < 2^40) on exact multiples k * d and their neighbours, where a rounded
+    double quotient can land just below an integer or just above it."""
+    rng = np.random.default_rng(18)
+    cases = []
+    for _ in range(20000):
+        d = rand_bits(rng, int(rng.integers(1, 33)))
+        k = rand_bits(rng, int(rng.integers(1, 41)))
+        n = k * d
+        cases += [(n + e, d) for e in (-1, 0, 1, d - 1) if 0 <= n + e < 2**64]
+    for n, d in cases:
+        assert sd.sd_udiv64_small(n, d) == n // d, (n, d)
+
+
+def test_from_ratio_64_bit_paths_equal_the_oracle(sd):
+    """from_ratio's 64-bit paths: den == 1 (Scale::mul and Scale::add; every bit length of num, the halves of a
+    rounding at its boundary) and num < 2^62 with den < 2^32 (Scale::recip, the requant scales), either side of
+    their bounds."""
+    rng = np.random.default_rng(17)
+    cases = []
+    for bn in range(1, 129):
+        for _ in range(12):
+            cases.append((rand_bits(rng, bn), 1))
+        k = max(bn - 32, 1)  # a value whose dropped bits are exactly one half, and one either side
+        h = (rand_bits(rng, bn) >> k << k) | (1 << (k - 1))
+        cases += [(h, 1), (h - 1, 1), (h + 1, 1)]
+    for _ in range(4000):
+        cases.append((rand_bits(rng, int(rng.integers(1, 66))), rand_bits(rng, int(rng.integers(1, 35)))))
+    for num, den in cases:
+        if num >= 2**128:
+            continue
+        want = O.from_ratio(num, den)
+        assert scale_out(sd.sd_from_ratio, num >> 64, num & U64, den >> 64, den & U64) == (want.mant, want.shift), \
+            (num, den)
+    for _ in range(3000):
+        (am, ash), (bm, bsh) = rand_scale(rng, (1, 33)), rand_scale(rng, (1, 33))
+        w = O.scale_mul(O.Scale(am, ash), O.Scale(bm, bsh))
+        assert scale_out(sd.sd_mul, am, ash, bm, bsh) == (w.mant, w.shift)
 
 
 def test_applies_equal_the_oracle(sd):

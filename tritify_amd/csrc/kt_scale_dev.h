@@ -63,9 +63,35 @@ KT_SC_FN u128 udiv128(u128 n, u128 d) {
     return q;
 }
 
+// floor(n / d) for d < 2^32 and a quotient below 2^40: the double quotient is within 2^-12 of the exact one (the
+// conversion of n and the division each add a relative error of at most 2^-53), so the floor is at most one away,
+// and the remainder, in (-2^33, 2^33), is exact in 64-bit wrapping arithmetic.
+KT_SC_FN uint64_t udiv64_small(uint64_t n, uint64_t d) {
+    uint64_t q = (uint64_t)((double)n / (double)d);
+    const int64_t rem = (int64_t)(n - q * d);
+    if (rem < 0) q--;
+    else if (rem >= (int64_t)d) q++;
+    return q;
+}
+
 // Scale::from_ratio (lib.rs:191-212): a 31-bit-normalized mantissa of num / den, rounded.
 KT_SC_FN Sc from_ratio(u128 num, u128 den) {
     if (num == 0) return Sc{0, 0};
+    // the same integers in 64-bit arithmetic where the operands allow (no halving applies below 2^64):
+    if (den == 1 && (num >> 64) == 0) {  // Scale::mul and Scale::add: a division by a power of two
+        const uint64_t n = (uint64_t)num;
+        const int s = 32 - (64 - __builtin_clzll(n));  // 31 - (bits(n) - bits(1))
+        if (s >= 0) return Sc{(int64_t)(n << s), s};
+        const int k = -s;  // floor((n + 2^(k-1)) / 2^k), without the sum's overflow
+        return Sc{(int64_t)((n >> k) + ((n >> (k - 1)) & 1)), s};
+    }
+    if ((num >> 62) == 0 && den != 0 && (den >> 32) == 0) {  // num < 2^62, den < 2^32: quotients below 2^33
+        const uint64_t n = (uint64_t)num, d = (uint64_t)den;
+        const int s = 31 - ((64 - __builtin_clzll(n)) - (64 - __builtin_clzll(d)));
+        if (s >= 0) return Sc{(int64_t)udiv64_small((n << s) + d / 2, d), s};  // n << s has 31 + bits(d) bits
+        const uint64_t dd = d << (-s);                                          // bits(n) - 31 bits
+        return Sc{(int64_t)udiv64_small(n + dd / 2, dd), s};
+    }
     {  // the reference halves both until each fits 64 bits: that many halvings as one shift
         const int bn = bits_u128(num), bd = bits_u128(den), k = (bn > bd ? bn : bd) - 64;
         if (k > 0) num >>= k, den >>= k;
@@ -85,7 +111,8 @@ KT_SC_FN Sc from_ratio(u128 num, u128 den) {
 // Scale::mul (lib.rs:252-258)
 KT_SC_FN Sc sc_mul(Sc a, Sc b) {
     if (a.mant == 0 || b.mant == 0) return Sc{0, 0};
-    Sc q = from_ratio((u128)(uint64_t)a.mant * (u128)(uint64_t)b.mant, 1);
+    const uint64_t am = (uint64_t)a.mant, bm = (uint64_t)b.mant;
+    Sc q = from_ratio((am >> 32) == 0 && (bm >> 32) == 0 ? (u128)(am * bm) : (u128)am * (u128)bm, 1);
     q.shift += a.shift + b.shift;
     return q;
 }
