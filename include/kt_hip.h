@@ -231,6 +231,15 @@ int kt_hip_ref_rmsnorm(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_de
 /* add (layers.rs:121-136), the residual add of n codes: y_dev may alias a_dev or b_dev, ys_dev as_dev or bs_dev. */
 int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
                    const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev, void* stream);
+/* add (layers.rs:121-136) and then RmsNorm::forward_int (layers.rs:392-434) of the sum, for one row of n <= 4096
+ * codes: DecoderModel::decode_step's residual add followed by the next norm (model.rs:338-353), as one launch. y / ys
+ * are kt_hip_ref_add's outputs (y_dev may alias a_dev or b_dev, ys_dev as_dev or bs_dev), h / hs kt_hip_ref_rmsnorm's
+ * of y with gamma g at (g_mant, g_shift) and eps (eps_mant, eps_shift): the same integers as the two calls in
+ * sequence. h_dev must not alias a_dev, b_dev or y_dev, nor hs_dev ys_dev. */
+int kt_hip_ref_add_rmsnorm(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const int32_t* b_dev,
+                           const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev,
+                           const int32_t* g_dev, int64_t g_mant, int32_t g_shift, int64_t eps_mant, int32_t eps_shift,
+                           int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream);
 /* SwiGluMlp::forward_int's activation (layers.rs:615-637): h = requant_dyn(silu_code(g) * u), the SiLU CodeLut
  * (right_identity set) with its codes at silu_codes_dev, for `rows` tensors of n values each, row r with its own
  * records gs_dev[r], us_dev[r], hs_dev[r] (rows = 1: one tensor; rows > 1: the per-token expert calls of a MoE). */

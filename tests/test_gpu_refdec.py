@@ -80,6 +80,39 @@ def test_ref_add(torch_dev, n):
         assert np.array_equal(ad.cpu().numpy(), yo) and rd(ar) == so, trial
 
 
+@pytest.mark.parametrize("n", [1, 32, 896, 4096])
+def test_ref_add_rmsnorm(torch_dev, n):
+    """The residual add and the next norm in one launch: the oracle's add, then its RmsNorm of the sum (in place
+    on a, as the decode step runs it), including a zero branch scale and an exact cancellation."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say(f"case: ref_add_rmsnorm n={n}")
+    rng = np.random.default_rng(n + 11)
+    g = rng.integers(-O.WLEVELS, O.WLEVELS + 1, size=n).astype(np.int32)
+    gs, eps = rand_scale(rng), B.ref_scale_from_f64(1e-6)
+    gd = dev_i32(torch, g)
+    for trial in range(4):
+        a = rng.integers(-(2**28), 2**28 + 1, size=n).astype(np.int32)
+        b = rng.integers(-(2**28), 2**28 + 1, size=n).astype(np.int32)
+        sa, sb = rand_scale(rng), rand_scale(rng)
+        if trial == 2:
+            sb = (0, 0)
+        if trial == 3:
+            b, sb = -a, sa  # cancels exactly: zeros at Scale::ZERO, then a zero norm
+        yo, so = O.rd_add(a, sa, b, sb)
+        ho, hso = O.rd_rmsnorm(yo, 1, n, so, g, gs, eps)
+        ad, ar = dev_i32(torch, a), rec(torch, sa)
+        h, hs = torch.zeros(n, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+        B.ref_add_rmsnorm(ad, ar, dev_i32(torch, b), rec(torch, sb), n, ad, ar, gd, gs, eps, h, hs)
+        assert np.array_equal(ad.cpu().numpy(), yo) and rd(ar) == so, trial
+        assert np.array_equal(h.cpu().numpy(), ho) and rd(hs) == hso, trial
+    with pytest.raises(B.HipError):  # a row past the one-CTA bound, and h over y, are refused
+        B.ref_add_rmsnorm(ad, ar, ad, ar, B.REF_ADD_NORM_MAX + 1, ad, ar, gd, gs, eps, h, hs)
+    with pytest.raises(B.HipError):
+        B.ref_add_rmsnorm(ad, ar, ad, ar, n, h, ar, gd, gs, eps, h, hs)
+
+
 @pytest.mark.parametrize("n,gshift", [(64, 53), (4864, 53), (4864, 60), (777, 48)])
 def test_ref_swiglu(torch_dev, n, gshift):
     torch = torch_dev

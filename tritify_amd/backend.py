@@ -119,6 +119,8 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_embed": (_I, [_I, _P, _I64, C.c_int32, _P, _I64, _I64, _P, _P, _P]),
         "kt_hip_ref_rmsnorm": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _P, _P]),
         "kt_hip_ref_add": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P]),
+        "kt_hip_ref_add_rmsnorm": (_I, [_I, _P, _P, _P, _P, _I64, _P, _P, _P, _I64, C.c_int32, _I64, C.c_int32, _P,
+                                        _P, _P]),
         "kt_hip_ref_swiglu": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
         "kt_hip_ref_seq_workspace": (_SZ, [_I64]),
         "kt_hip_ref_rmsnorm_seq": (_I, [_I, _P, _P, _I64, _I64, _P, _I64, C.c_int32, _I64, C.c_int32, _P, _SZ, _P, _P,
@@ -657,6 +659,18 @@ def ref_rmsnorm(x_dev, xs_dev, rows: int, dim: int, g_dev, g_scale, eps_scale, y
 def ref_add(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, stream=None, dev: int = 0) -> None:
     check(lib().kt_hip_ref_add(dev, _ptr(a_dev), _ptr(as_dev), _ptr(b_dev), _ptr(bs_dev), n, _ptr(y_dev),
                                _ptr(ys_dev), _stream(stream)), "ref add")
+
+
+REF_ADD_NORM_MAX = 4096  # kt_hip_ref_add_rmsnorm's longest row
+
+
+def ref_add_rmsnorm(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, g_dev, g_scale, eps_scale, h_dev, hs_dev,
+                    stream=None, dev: int = 0) -> None:
+    """add then RmsNorm of the sum in one launch (n <= REF_ADD_NORM_MAX): y = add(a, b), h = rmsnorm(y)."""
+    check(lib().kt_hip_ref_add_rmsnorm(dev, _ptr(a_dev), _ptr(as_dev), _ptr(b_dev), _ptr(bs_dev), n, _ptr(y_dev),
+                                       _ptr(ys_dev), _ptr(g_dev), int(g_scale[0]), int(g_scale[1]),
+                                       int(eps_scale[0]), int(eps_scale[1]), _ptr(h_dev), _ptr(hs_dev),
+                                       _stream(stream)), "ref add + rmsnorm")
 
 
 def ref_swiglu(g_dev, gs_dev, u_dev, us_dev, n: int, silu_codes_dev, silu: CodeLut, h_dev, hs_dev, stream=None,

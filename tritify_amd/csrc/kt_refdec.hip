@@ -193,6 +193,63 @@ __global__ __launch_bounds__(RD_THREADS) void rd_embed_kernel(const int32_t* __r
     if (threadIdx.x == 0) put_rec(ys, ok ? Sc{e_mant, e_shift} : Sc{0, 0});
 }
 
+// RmsNorm::forward_int of one row held in registers (NV values per thread, value i = threadIdx.x + RD_THREADS * k,
+// dim <= RD_THREADS * NV; gv the gammas likewise): the exact sum of squares reduced across the CTA, the row factor
+// c = xs * rsqrt(mean_sq + eps) * gs by thread 0 (only thread 0 reads xs), the products brought to c and
+// requantized by their largest magnitude. The same integers as rd_rmsnorm_kernel's general path for one row.
+template <int NV>
+__device__ void rd_norm_row(int32_t (&xv)[NV], const int32_t (&gv)[NV], int dim, Sc xs, Sc gs, Sc eps,
+                            int32_t* __restrict__ y, kt_hip_qscale* __restrict__ ys, int64_t* red) {
+    __shared__ uint64_t sq2[RD_WAVES][2];
+    __shared__ Sc cf[2];  // c and its factor over itself
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint64_t hi = 0, lo = 0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        if ((int)threadIdx.x + RD_THREADS * k >= dim) xv[k] = 0;
+        const int64_t v = xv[k];
+        const uint64_t sq = (uint64_t)(v * v), t = lo + sq;
+        hi += t < lo, lo = t;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t ohi = __shfl_xor(hi, o, 64), olo = __shfl_xor(lo, o, 64), t = lo + olo;
+        hi += ohi + (t < lo), lo = t;
+    }
+    if (lane == 0) sq2[wave][0] = hi, sq2[wave][1] = lo;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        u128 ss = 0;
+        for (int w = 0; w < RD_WAVES; w++) ss += ((u128)sq2[w][0] << 64) | sq2[w][1];
+        const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xs), xs);
+        const Sc denom = sc_add(mean_sq, eps);
+        const Sc inv = denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom);
+        const Sc c0 = sc_mul(sc_mul(xs, inv), gs);
+        cf[0] = c0;  // the largest of one row's factors is that factor
+        cf[1] = c0.mant != 0 ? sc_mul(c0, sc_recip(c0)) : Sc{0, 0};
+    }
+    __syncthreads();
+    const Sc cc = cf[0], f0 = cf[1];
+    int64_t hv[NV];
+    int64_t m = 0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {  // values past dim stay 0 (whole waves skip the 128-bit products)
+        hv[k] = 0;
+        if (cc.mant != 0 && (int)threadIdx.x + RD_THREADS * k < dim)
+            hv[k] = sc_apply(f0, (int64_t)xv[k] * (int64_t)gv[k]);
+        m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
+    }
+    const int64_t gmax = block_max_i64(m, red);
+    const RqDen rd_gmax = rq_den(gmax);
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        const int i = threadIdx.x + RD_THREADS * k;
+        if (i < dim) y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
+    }
+    if (threadIdx.x == 0)
+        put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
+}
+
 // RmsNorm::forward_int (layers.rs:392-434) over `rows` rows of `dim`: per row the exact sum of squares, its
 // mean-square Scale plus eps, the integer inverse square root, the row factor c_r = xs * inv * gs; the products
 // x_i * g_i brought to the largest c_r and requantized by the largest magnitude.
@@ -209,59 +266,14 @@ __global__ __launch_bounds__(RD_THREADS) void rd_rmsnorm_kernel(const int32_t* _
     const Sc xs = rec_sc(xs_rec), gs{g_mant, g_shift}, eps{e_mant, e_shift};
     constexpr int RD_NV = 8;
     if (rows == 1 && dim <= RD_THREADS * RD_NV) {
-        // one row (the decode step): its values and gammas loaded once by every thread, all in flight together, the
-        // sum of squares reduced across the CTA; the same integers as the general path below
+        // one row (the decode step): its values and gammas loaded once by every thread, all in flight together
         int32_t xv[RD_NV], gv[RD_NV];
 #pragma unroll
         for (int k = 0; k < RD_NV; k++) {
             const int i = threadIdx.x + RD_THREADS * k, ic = i < dim ? i : dim - 1;
             xv[k] = x[ic], gv[k] = g[ic];
         }
-        uint64_t hi = 0, lo = 0;
-#pragma unroll
-        for (int k = 0; k < RD_NV; k++) {
-            if ((int)threadIdx.x + RD_THREADS * k >= dim) xv[k] = 0;
-            const int64_t v = xv[k];
-            const uint64_t sq = (uint64_t)(v * v), t = lo + sq;
-            hi += t < lo, lo = t;
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const uint64_t ohi = __shfl_xor(hi, o, 64), olo = __shfl_xor(lo, o, 64), t = lo + olo;
-            hi += ohi + (t < lo), lo = t;
-        }
-        __shared__ uint64_t sq2[RD_WAVES][2];
-        if (lane == 0) sq2[wave][0] = hi, sq2[wave][1] = lo;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            u128 ss = 0;
-            for (int w = 0; w < RD_WAVES; w++) ss += ((u128)sq2[w][0] << 64) | sq2[w][1];
-            const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xs), xs);
-            const Sc denom = sc_add(mean_sq, eps);
-            const Sc inv = denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom);
-            const Sc c0 = sc_mul(sc_mul(xs, inv), gs);
-            crow[0] = c0;  // the largest of one row's factors is that factor
-            frow[0] = c0.mant != 0 ? sc_mul(c0, sc_recip(c0)) : Sc{0, 0};
-        }
-        __syncthreads();
-        const Sc cc = crow[0], f0 = frow[0];
-        int64_t hv[RD_NV];
-        int64_t m = 0;
-#pragma unroll
-        for (int k = 0; k < RD_NV; k++) {  // values past dim stay 0 (whole waves skip the 128-bit products)
-            hv[k] = 0;
-            if (cc.mant != 0 && (int)threadIdx.x + RD_THREADS * k < dim) hv[k] = sc_apply(f0, (int64_t)xv[k] * (int64_t)gv[k]);
-            m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
-        }
-        const int64_t gmax = block_max_i64(m, red);
-        const RqDen rd_gmax = rq_den(gmax);
-#pragma unroll
-        for (int k = 0; k < RD_NV; k++) {
-            const int i = threadIdx.x + RD_THREADS * k;
-            if (i < dim) y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
-        }
-        if (threadIdx.x == 0)
-            put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
+        rd_norm_row<RD_NV>(xv, gv, dim, xs, gs, eps, y, ys, red);
         return;
     }
     // each row's exact sum of squares by one wave, its factor c_r = xs * rsqrt(mean_sq + eps) * gs by that wave's
@@ -369,6 +381,63 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, co
     }
     if (threadIdx.x == 0)
         put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
+}
+
+// add (layers.rs:121-136) and then RmsNorm::forward_int (layers.rs:392-434) of the sum, for one row of
+// n <= RD_THREADS * RD_AN values: the decode step's residual add followed by the next norm (model.rs:338-353), one
+// launch where the two kernels took two. y = add(a, b) with its record ys (y may alias a or b), then h = the norm of
+// y from the codes still in registers and the Scale thread 0 formed for ys. The same integers as rd_add_kernel and
+// rd_rmsnorm_kernel in sequence.
+constexpr int RD_AN = 4;
+__global__ __launch_bounds__(RD_THREADS) void rd_add_norm_kernel(const int32_t* a, const kt_hip_qscale* as_rec,
+                                                                 const int32_t* b, const kt_hip_qscale* bs_rec, int n,
+                                                                 int32_t* y, kt_hip_qscale* ys,
+                                                                 const int32_t* __restrict__ g, int64_t g_mant,
+                                                                 int32_t g_shift, int64_t e_mant, int32_t e_shift,
+                                                                 int32_t* __restrict__ h,
+                                                                 kt_hip_qscale* __restrict__ hs) {
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ Sc par[3];  // common, fa, fb
+    int32_t av[RD_AN], bv[RD_AN], gv[RD_AN];
+#pragma unroll
+    for (int k = 0; k < RD_AN; k++) {
+        const int i = threadIdx.x + RD_THREADS * k, ic = i < n ? i : n - 1;
+        av[k] = a[ic], bv[k] = b[ic], gv[k] = g[ic];
+    }
+    if (threadIdx.x == 0) {
+        const Sc as = rec_sc(as_rec), bs = rec_sc(bs_rec);
+        const Sc common = sc_ge(as, bs) ? as : bs;
+        par[0] = common;
+        if (common.mant != 0) {
+            const Sc cinv = sc_recip(common);
+            par[1] = sc_mul(as, cinv), par[2] = sc_mul(bs, cinv);
+        }
+    }
+    __syncthreads();
+    const Sc common = par[0], fa = par[1], fb = par[2];
+    int64_t m = 0, hv[RD_AN];
+#pragma unroll
+    for (int k = 0; k < RD_AN; k++) {
+        hv[k] = 0;
+        if (common.mant != 0 && (int)threadIdx.x + RD_THREADS * k < n)
+            hv[k] = wadd(sc_apply32(fa, av[k]), sc_apply32(fb, bv[k]));
+        m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
+    }
+    const int64_t gmax = block_max_i64(m, red);  // every read of a and b is done past here
+    const RqDen rd_gmax = rq_den(gmax);
+    int32_t yv[RD_AN];
+#pragma unroll
+    for (int k = 0; k < RD_AN; k++) {
+        const int i = threadIdx.x + RD_THREADS * k;
+        yv[k] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
+        if (i < n) y[i] = yv[k];
+    }
+    Sc xs{0, 0};  // the sum's Scale: thread 0 writes the record and carries it into the norm
+    if (threadIdx.x == 0) {
+        xs = gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common);
+        put_rec(ys, xs);
+    }
+    rd_norm_row<RD_AN>(yv, gv, n, xs, Sc{g_mant, g_shift}, Sc{e_mant, e_shift}, h, hs, red);
 }
 
 // SwiGluMlp::forward_int's activation (layers.rs:615-637): h = silu_code(g) * u, the SiLU code from the CodeLut at
@@ -1000,6 +1069,12 @@ hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_
     rd_add_kernel<<<1, RD_THREADS, 0, s>>>(a, as, b, bs, n, y, ys);
     return hipGetLastError();
 }
+hipError_t launch_rd_add_norm(const int32_t* a, const kt_hip_qscale* as, const int32_t* b, const kt_hip_qscale* bs,
+                              int n, int32_t* y, kt_hip_qscale* ys, const int32_t* g, int64_t g_mant, int32_t g_shift,
+                              int64_t e_mant, int32_t e_shift, int32_t* h, kt_hip_qscale* hs, hipStream_t s) {
+    rd_add_norm_kernel<<<1, RD_THREADS, 0, s>>>(a, as, b, bs, n, y, ys, g, g_mant, g_shift, e_mant, e_shift, h, hs);
+    return hipGetLastError();
+}
 hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
                             int rows, int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h,
                             kt_hip_qscale* hs, hipStream_t s) {
@@ -1205,6 +1280,20 @@ extern "C" int kt_hip_ref_add(int dev, const int32_t* a_dev, const kt_hip_qscale
         return (int)hipErrorInvalidValue;
     RD_TRY(hipSetDevice(dev));
     return (int)kt::launch_rd_add(a_dev, as_dev, b_dev, bs_dev, (int)n, y_dev, ys_dev, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_add_rmsnorm(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev,
+                                      const int32_t* b_dev, const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev,
+                                      kt_hip_qscale* ys_dev, const int32_t* g_dev, int64_t g_mant, int32_t g_shift,
+                                      int64_t eps_mant, int32_t eps_shift, int32_t* h_dev, kt_hip_qscale* hs_dev,
+                                      void* stream) {
+    if (!a_dev || !as_dev || !b_dev || !bs_dev || !y_dev || !ys_dev || !g_dev || !h_dev || !hs_dev || n < 1 ||
+        n > (int64_t)kt::RD_THREADS * kt::RD_AN || g_mant < 0 || eps_mant < 0 || h_dev == y_dev || h_dev == a_dev ||
+        h_dev == b_dev || (void*)hs_dev == (void*)ys_dev)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    return (int)kt::launch_rd_add_norm(a_dev, as_dev, b_dev, bs_dev, (int)n, y_dev, ys_dev, g_dev, g_mant, g_shift,
+                                       eps_mant, eps_shift, h_dev, hs_dev, (hipStream_t)stream);
 }
 
 extern "C" int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,

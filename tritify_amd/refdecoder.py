@@ -10,7 +10,8 @@ the 2^28 level, quantized dynamically per tensor after every op. `RefDecoder` ke
     down, lm_head             (digit-plane MFMA product)
   attention core              kt_hip_ref_attention_step      Attention::decode_step      (attention.rs:340-459)
   SiLU * up                   kt_hip_ref_swiglu              SwiGluMlp::forward_int      (layers.rs:609-640)
-  residual adds               kt_hip_ref_add                 add                         (layers.rs:121-136)
+  residual adds               kt_hip_ref_add_rmsnorm         add, then the next RmsNorm  (layers.rs:121-136,
+                              (one launch; kt_hip_ref_add)                               392-434)
   greedy choice               kt_hip_ref_argmax              argmax_codes                (generate.rs:48-56)
   sequence forward            kt_hip_ref_embed_seq,          CausalLM::forward_int       (model.rs:361-367,
     (prefill)                 kt_hip_ref_attention_prefill,  Attention::forward_int       168-189; attention.rs:
@@ -134,10 +135,22 @@ class RefDecoder:
         device int32): every launch on `stream`, no host synchronization; the logits land in buf["logits"] with
         their scale in rec["logits"]."""
         b, r, dv = self.buf, self.rec, self.dev
+        # a residual add and the norm after it are one launch where the row allows (the same integers)
+        fuse = self.dim <= B.REF_ADD_NORM_MAX
+
+        def add_norm(branch, norm):
+            g_, gs_ = norm
+            if fuse:
+                B.ref_add_rmsnorm(b["x"], r["x"], b[branch], r[branch], self.dim, b["x"], r["x"], g_, gs_, self.eps,
+                                  b["h"], r["h"], stream, dv)
+            else:
+                B.ref_add(b["x"], r["x"], b[branch], r[branch], self.dim, b["x"], r["x"], stream, dv)
+                B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g_, gs_, self.eps, b["h"], r["h"], stream, dv)
+
         B.ref_embed(self.emb, self.emb_scale, self.token, self.vocab, self.dim, b["x"], r["x"], stream, dv)
+        g, gs = self.blocks[0]["in_norm"] if self.blocks else self.final_norm
+        B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
         for i, blk in enumerate(self.blocks):
-            g, gs = blk["in_norm"]
-            B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
             if self.grouped:
                 blk["qkv"].forward_int(b["h"], r["h"], 1, y_devs=[b["q"], b["k"], b["v"]], os_dev=self._rec_qkv,
                                        stream=stream)
@@ -149,9 +162,7 @@ class RefDecoder:
                                  self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, b["cat"], r["cat"], stream,
                                  dv)
             self._ql(blk["wo"], "cat", "a", stream)
-            B.ref_add(b["x"], r["x"], b["a"], r["a"], self.dim, b["x"], r["x"], stream, dv)
-            g, gs = blk["post_norm"]
-            B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
+            add_norm("a", blk["post_norm"])
             if self.grouped:
                 blk["gu"].forward_int(b["h"], r["h"], 1, y_devs=[b["g"], b["u"]], os_dev=self._rec_gu, stream=stream)
             else:
@@ -160,9 +171,8 @@ class RefDecoder:
             B.ref_swiglu(b["g"], r["g"], b["u"], r["u"], self.hidden, self.silu_codes, self.silu_lut, b["hh"],
                          r["hh"], stream, dv)  # one tensor (rows = 1)
             self._ql(blk["down"], "hh", "m", stream)
-            B.ref_add(b["x"], r["x"], b["m"], r["m"], self.dim, b["x"], r["x"], stream, dv)
-        g, gs = self.final_norm
-        B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
+            # the next block's input norm, or the final norm after the last block
+            add_norm("m", self.blocks[i + 1]["in_norm"] if i + 1 < len(self.blocks) else self.final_norm)
         self._ql(self.lm_head, "h", "logits", stream)
 
     def capture_greedy_step(self):
