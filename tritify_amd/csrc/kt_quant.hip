@@ -71,10 +71,16 @@ __global__ __launch_bounds__(QL_THREADS) void ql_absmax_kernel(const int32_t* __
                                                                uint32_t* __restrict__ part) {
     __shared__ uint32_t red[QL_THREADS / 64];
     uint32_t m = 0;
-    for (int64_t i = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * QL_THREADS) {
-        const int32_t v = x[i];
-        const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
-        m = a > m ? a : m;
+    const int64_t step = (int64_t)gridDim.x * QL_THREADS;
+    for (int64_t i0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x; i0 < n; i0 += 4 * step) {  // 4 loads in flight
+        int32_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = i0 + u * step < n ? x[i0 + u * step] : 0;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t a = v[u] < 0 ? 0u - (uint32_t)v[u] : (uint32_t)v[u];
+            m = a > m ? a : m;
+        }
     }
     m = block_max(m, red);
     if (threadIdx.x == 0) part[blockIdx.x] = m;
@@ -212,10 +218,15 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
     if (nparts > 0) {
         for (int i = threadIdx.x; i < nparts; i += QL_THREADS) m = part[i] > m ? part[i] : m;
     } else {  // a short x (QL_FUSED_MAX values at most): every CTA takes max |x| itself, no ql_absmax pass
-        for (int64_t i = threadIdx.x; i < nx; i += QL_THREADS) {
-            const int32_t v = x[i];
-            const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
-            m = a > m ? a : m;
+        for (int64_t i0 = threadIdx.x; i0 < nx; i0 += 8 * QL_THREADS) {  // 8 loads in flight per thread
+            int32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = i0 + u * QL_THREADS < nx ? x[i0 + u * QL_THREADS] : 0;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t a = v[u] < 0 ? 0u - (uint32_t)v[u] : (uint32_t)v[u];
+                m = a > m ? a : m;
+            }
         }
     }
     m = block_max(m, red);
