@@ -85,7 +85,9 @@ typedef struct {
     int64_t xmax;
     int64_t ymax;
 } kt_hip_qscale;
-#define KT_QL_WS_PARTS 5 /* workspace parts: x planes, i64 accumulators, |x| maxima, split-k tile counters, state */
+/* workspace parts: x planes, i64 accumulators, partial maxima (of |x|, or for one row of the product per 8 output
+ * columns), split-k tile counters, state */
+#define KT_QL_WS_PARTS 5
 #define KT_QL_PARTS 1024 /* partial maxima per reduction */
 /* Workspace bytes of kt_hip_quant_linear for rows x in_f -> out_f (parts at *off, 256-byte aligned). */
 size_t kt_hip_quant_linear_workspace(int64_t rows, int64_t in_f, int64_t out_f, size_t off[KT_QL_WS_PARTS]);
