@@ -262,15 +262,17 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
 
 
 // One row (the decode step): the quant pass and the digit product in one launch. Every CTA takes max |x| over the
-// row and forms the row's three digit planes in LDS itself (a few thousand values, read from L2 by each CTA) while
+// row and forms the row's three digit planes in LDS itself (at most QS_MAX_KP values, read from L2 by each CTA) while
 // its first weight chunks are in flight, then runs the product of plane_skinny_kernel over its 8 output columns
 // (4 waves x 2 columns, the lanes striding k in 16-byte chunks, int32 plane-group sums by sdot4, a butterfly across
 // the wave). The CTA's largest |result| goes to its own slot part[blockIdx.x] (overwritten on every call, so no
 // pass has to clear it); ql_requant_kernel takes each segment's maximum over its CTAs' slots. CTA 0 writes each
 // segment's state for ql_requant_kernel. A CTA whose segment has a bias forms the bias factor itself. Requires
-// kp <= QS_MAX_KP and a single k-chunk (kp within the flush bound).
-constexpr int QS_MAX_KP = 8192;
-constexpr int64_t QS_FUSED_KP = 1024, QS_FUSED_OUT = 4096;  // where launch_ql_impl takes this path
+// kp <= QS_MAX_KP and a single k-chunk (kp within the flush bound). launch_ql_impl takes this path for outputs of at
+// most QS_FUSED_OUT columns: a longer row, or a wider output's many CTAs, re-quantizing the row in every CTA cost
+// more than the launch of the quant pass (measured on the 4864-value down row and the 9728-column gate / up group).
+constexpr int QS_MAX_KP = 1024;
+constexpr int64_t QS_FUSED_OUT = 4096;
 constexpr int QS_THREADS = 256, QS_WAVES = QS_THREADS / 64;
 constexpr int QS_CPW = 2;  // output columns per wave
 constexpr int QS_COLS = QS_WAVES * QS_CPW;
@@ -611,7 +613,7 @@ static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, con
     // (a short row: each CTA quantizes it again, so a long one, or a grid of many CTAs, keeps the quant pass)
     bool seg_ok = true;  // every CTA of QS_COLS columns within one segment
     for (int g = 1; g < seg.n; g++) seg_ok = seg_ok && seg.col0[g] % QS_COLS == 0;
-    if (!geom && rows == 1 && kp <= QS_FUSED_KP && out <= QS_FUSED_OUT && kp <= flush_k && seg_ok &&
+    if (!geom && rows == 1 && kp <= QS_MAX_KP && out <= QS_FUSED_OUT && kp <= flush_k && seg_ok &&
         (pw == 1 || pw == 3 || pw == 5)) {
         const int ctas = (int)((out + QS_COLS - 1) / QS_COLS);
         int64_t* pm = reinterpret_cast<int64_t*>(base + off[2]);
