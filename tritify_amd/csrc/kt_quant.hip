@@ -269,10 +269,10 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
 // pass has to clear it); ql_requant_kernel takes each segment's maximum over its CTAs' slots. CTA 0 writes each
 // segment's state for ql_requant_kernel. A CTA whose segment has a bias forms the bias factor itself. Requires
 // kp <= QS_MAX_KP and a single k-chunk (kp within the flush bound). launch_ql_impl takes this path for outputs of at
-// most QS_FUSED_OUT columns: a longer row, or a wider output's many CTAs, re-quantizing the row in every CTA cost
-// more than the launch of the quant pass (measured on the 4864-value down row and the 9728-column gate / up group).
+// most QS_FUSED_OUT columns: for a longer row (the 4864-value down row in 112 CTAs) re-quantizing it in every CTA
+// cost more than the quant pass's launch; the 9728-column gate / up group (1216 CTAs) comes out even.
 constexpr int QS_MAX_KP = 1024;
-constexpr int64_t QS_FUSED_OUT = 4096;
+constexpr int64_t QS_FUSED_OUT = 16384;
 constexpr int QS_THREADS = 256, QS_WAVES = QS_THREADS / 64;
 constexpr int QS_CPW = 2;  // output columns per wave
 constexpr int QS_COLS = QS_WAVES * QS_CPW;
