@@ -37,14 +37,6 @@ constexpr int64_t ACT_LEVELS = 1LL << 28;  // layers.rs:18
 constexpr int QL_THREADS = 256;
 constexpr int64_t QL_FUSED_MAX = 8192;  // x of at most this many values: max |x| inside the quant pass
 
-// floor(n / d) for 0 <= n < 2^53 and 0 < d < 2^53 (both exact in a double): the correctly rounded double quotient is
-// the exact one or one above it at an integer boundary, which the remainder test corrects.
-__device__ inline uint64_t udiv_est53(uint64_t n, int64_t d) {
-    uint64_t q = (uint64_t)((double)n / (double)d);
-    if (q * (uint64_t)d > n) q--;
-    return q;
-}
-
 template <typename T>
 __device__ inline T block_max(T v, T* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -151,31 +143,9 @@ __device__ inline QlHead ql_head(uint32_t m, const kt_hip_qscale* xs, const QlSc
 }
 
 // The three balanced base-256 digits of quant_to(x, xmax) for 4 columns (layers.rs:23-31), as one byte of each
-// plane word: |num| = |x| * WLEVELS < 2^49 is exact in a double, the quotient is corrected to the exact one.
-__device__ inline void ql_digits4(const int32_t xv[4], int64_t xmax, uint32_t word[3]) {
-    const int64_t half = xmax / 2;
-    word[0] = word[1] = word[2] = 0;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        int64_t v = 0;
-        if (xv[t] != 0) {
-            const int64_t num = (int64_t)xv[t] * WLEVELS;
-            const uint64_t a = (uint64_t)(num < 0 ? -num : num) + (uint64_t)half;
-            const uint64_t qq = udiv_est53(a, xmax);  // a < 2^31 * WLEVELS + 2^30 < 2^53
-            v = num >= 0 ? (int64_t)qq : -(int64_t)qq;
-        }
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const int64_t d = ((v + 128) & 255) - 128;
-            word[p] |= ((uint32_t)d & 255u) << (8 * t);
-            v = (v - d) >> 8;
-        }
-    }
-}
-
-// ql_digits4 with the quotient from a multiplication by rinv = 1 / xmax (a double): for a < 2^53 and xmax < 2^32
-// the estimate of a / xmax (below 2^19 here) is off by less than 2^-30, so at most one step from the exact floor,
-// which the two integer tests restore. The same digits as ql_digits4.
+// plane word. |x| <= xmax, so the quotient (|x| * WLEVELS + xmax / 2) / xmax is below 2^19; it is estimated as a
+// product with rinv = 1 / xmax in double precision (relative error below 2^-51, so off by less than 2^-30 and at
+// most one step from the exact floor) and the two integer tests restore the exact quotient.
 __device__ inline void ql_digits4r(const int32_t xv[4], uint32_t xmax, double rinv, uint32_t word[3]) {
     const uint64_t half = xmax / 2;
     word[0] = word[1] = word[2] = 0;
@@ -239,8 +209,8 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
         q->c_shift = h.c.shift, q->f_shift = h.f.shift, q->mode = h.mode;
     }
     const int64_t quads = rows * (kp / 4);
-    const int64_t xmax = (int64_t)m;
     const bool live = m != 0;
+    const double rinv = live ? 1.0 / (double)m : 0.0;
     const size_t plane = (size_t)rows * (size_t)kp;
     const int64_t qpr = kp / 4, q0 = (int64_t)blockIdx.x * QL_THREADS + threadIdx.x;
     const int64_t step = (int64_t)gridDim.x * QL_THREADS, dr = step / qpr, dq = step - dr * qpr;
@@ -252,7 +222,7 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
         int32_t xv[4] = {0, 0, 0, 0};
         if (live) {
             ql_fetch4<CONV>(x, r, c0, in, geom, xv);
-            ql_digits4(xv, xmax, word);
+            ql_digits4r(xv, m, rinv, word);
         }
         const size_t at = (size_t)r * (size_t)kp + (size_t)c0;
 #pragma unroll
