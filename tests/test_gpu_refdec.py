@@ -167,10 +167,16 @@ def test_ref_embed_and_argmax(torch_dev):
 
 @pytest.mark.parametrize("cfg", [dict(O.SYNTH_CFG, max_seq=48),
                                  dict(dim=64, layers=1, nh=14, nkv=2, hd=64, hidden=64, vocab=8, eps=1e-6,
-                                      theta=1.0e6, max_seq=80)])
+                                      theta=1.0e6, max_seq=80),
+                                 dict(dim=64, layers=1, nh=12, nkv=1, hd=32, hidden=64, vocab=8, eps=1e-6,
+                                      theta=1.0e6, max_seq=40),
+                                 dict(dim=64, layers=1, nh=14, nkv=2, hd=128, hidden=64, vocab=8, eps=1e-6,
+                                      theta=1.0e6, max_seq=512)])
 def test_ref_attention_steps(torch_dev, cfg):
     """Steps 0..max_seq-1 of Attention::decode_step's core on random q/k/v codes and scales (some steps with a zero k
-    or v scale), the device cache against the oracle's, output codes and scale at every step."""
+    or v scale), the device cache against the oracle's, output codes and scale at every step. The configurations
+    reach both P.V layouts: by kv head (groups of up to 8 q heads; at max_seq 512 with head_dim 128 the heads' scores
+    fit 5 at a time, so batches split the groups) and by (head, dim) for a 12-head group."""
     torch = torch_dev
     from tritify_amd import backend as B
 

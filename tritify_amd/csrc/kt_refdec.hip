@@ -35,6 +35,7 @@ namespace {
 constexpr int RD_THREADS = 1024;
 constexpr int RD_WAVES = RD_THREADS / 64;
 constexpr int RD_MAX_ROWS = 1024;  // RMSNorm rows in one call (one factor per thread)
+constexpr int RD_PV_GROUP = 8;     // P.V by kv head for groups of up to this many q heads
 constexpr int64_t ACT_LEVELS = 1LL << 28;
 
 }  // namespace
@@ -720,28 +721,75 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
             }
         }
         __syncthreads();
-        for (int it = tid; it < hn * hd; it += RD_THREADS) {
-            const int h = it / hd, dd = it - h * hd, kv = (h0 + h) / group;
-            int64_t acc = 0;
-            if (hsum[h] > 0) {
-                const int64_t* sh = S + (size_t)h * a.max_seq;
-                const int32_t* vcol = a.vc + kv * hd + dd;
-                // RD_PU cached v values loaded before their products (a step past the end re-reads the last one
-                // and is dropped)
-                constexpr int RD_PU = 8;
-                for (int j0 = 0; j0 < steps; j0 += RD_PU) {
-                    int32_t vv[RD_PU];
+        if (group <= RD_PV_GROUP) {
+            // P.V by kv head: v_jd scaled once for the heads that share it (vf_j.apply(v_jd) is the same for every
+            // head of a group), each wave one (kv head, slice of the steps) with its lanes across head_dim, the
+            // heads' products summed into HO by LDS atomics (wrapping i64 sums: any order gives the same integers)
+            for (int i = tid; i < hn * hd; i += RD_THREADS) HO[h0 * hd + i] = 0;
+            __syncthreads();
+            const int kv0 = h0 / group, nkvb = (h0 + hn - 1) / group - kv0 + 1;
+            const int jp = RD_WAVES / nkvb > 1 ? RD_WAVES / nkvb : 1, tasks = nkvb * jp;
+            for (int t = wave; t < tasks; t += RD_WAVES) {
+                const int kv = kv0 + t / jp, js = t - (t / jp) * jp;
+                const int hs = kv * group > h0 ? kv * group : h0;
+                const int he = (kv + 1) * group < h0 + hn ? (kv + 1) * group : h0 + hn;  // heads [hs, he)
+                for (int dd = lane; dd < hd; dd += 64) {
+                    int64_t acc[RD_PV_GROUP];
 #pragma unroll
-                    for (int u = 0; u < RD_PU; u++) {
-                        const int j = j0 + u < steps ? j0 + u : steps - 1;
-                        vv[u] = vcol[(size_t)j * kstride];
+                    for (int g = 0; g < RD_PV_GROUP; g++) acc[g] = 0;
+                    const int32_t* vcol = a.vc + kv * hd + dd;
+                    constexpr int RD_PU = 4;  // cached v values loaded before their products
+                    for (int j0 = js; j0 < steps; j0 += RD_PU * jp) {
+                        int32_t vv[RD_PU];
+#pragma unroll
+                        for (int u = 0; u < RD_PU; u++) {
+                            const int j = j0 + u * jp < steps ? j0 + u * jp : steps - 1;
+                            vv[u] = vcol[(size_t)j * kstride];
+                        }
+#pragma unroll
+                        for (int u = 0; u < RD_PU; u++) {
+                            const int j = j0 + u * jp;
+                            if (j >= steps) break;
+                            const int64_t sv = sc_apply32(VF[j], vv[u]);
+#pragma unroll
+                            for (int g = 0; g < RD_PV_GROUP; g++)
+                                if (hs + g < he) acc[g] = wadd(acc[g], wmul(S[(size_t)(hs + g - h0) * a.max_seq + j], sv));
+                        }
                     }
 #pragma unroll
-                    for (int u = 0; u < RD_PU; u++)
-                        if (j0 + u < steps) acc = wadd(acc, wmul(sh[j0 + u], sc_apply32(VF[j0 + u], vv[u])));
+                    for (int g = 0; g < RD_PV_GROUP; g++)
+                        if (hs + g < he && acc[g] != 0)
+                            atomicAdd(reinterpret_cast<unsigned long long*>(&HO[(hs + g) * hd + dd]),
+                                      (unsigned long long)acc[g]);
                 }
             }
-            HO[(h0 + h) * hd + dd] = acc;
+            __syncthreads();
+            for (int i = tid; i < hn * hd; i += RD_THREADS)  // a head with no numerators: zeros
+                if (hsum[i / hd] <= 0) HO[h0 * hd + i] = 0;
+        } else {
+            for (int it = tid; it < hn * hd; it += RD_THREADS) {
+                const int h = it / hd, dd = it - h * hd, kv = (h0 + h) / group;
+                int64_t acc = 0;
+                if (hsum[h] > 0) {
+                    const int64_t* sh = S + (size_t)h * a.max_seq;
+                    const int32_t* vcol = a.vc + kv * hd + dd;
+                    // RD_PU cached v values loaded before their products (a step past the end re-reads the last one
+                    // and is dropped)
+                    constexpr int RD_PU = 8;
+                    for (int j0 = 0; j0 < steps; j0 += RD_PU) {
+                        int32_t vv[RD_PU];
+#pragma unroll
+                        for (int u = 0; u < RD_PU; u++) {
+                            const int j = j0 + u < steps ? j0 + u : steps - 1;
+                            vv[u] = vcol[(size_t)j * kstride];
+                        }
+#pragma unroll
+                        for (int u = 0; u < RD_PU; u++)
+                            if (j0 + u < steps) acc = wadd(acc, wmul(sh[j0 + u], sc_apply32(VF[j0 + u], vv[u])));
+                    }
+                }
+                HO[(h0 + h) * hd + dd] = acc;
+            }
         }
         __syncthreads();  // S and hsum are reused by the next batch
     }
