@@ -163,6 +163,17 @@ def test_ref_embed_and_argmax(torch_dev):
     rs = rscale.cpu().numpy().view(B.SSCALE)
     assert (rs["mant"] == 999).all() and rs["shift"].tolist() == [9, 10]
     assert np.array_equal(record.cpu().numpy().reshape(2, n)[1], logits)
+    # ties inside one 16-byte group and in its neighbour; a length that is not a multiple of 4 (the scalar path),
+    # with and without the record; a maximum at the last code
+    for n2, at, want in ((4096, [9, 8, 4000], 8), (1001, [1000], 1000), (1001, [3, 2, 999], 2)):
+        lg = rng.integers(-(2**30), 2**30, size=n2).astype(np.int32)
+        lg[at] = 2**31 - 1
+        ld2 = dev_i32(torch, lg)
+        B.ref_argmax(ld2, n2, rec(torch, (1, 1)), tok, None, None, None)
+        assert int(tok.item()) == want, (n2, at)
+        rec2, st2 = torch.zeros(n2, dtype=torch.int32, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda")
+        B.ref_argmax(ld2, n2, rec(torch, (1, 1)), tok, rec2, torch.zeros(16, dtype=torch.uint8, device="cuda"), st2)
+        assert int(tok.item()) == want and np.array_equal(rec2.cpu().numpy(), lg) and int(st2.item()) == 1
 
 
 @pytest.mark.parametrize("cfg", [dict(O.SYNTH_CFG, max_seq=48),

@@ -1070,22 +1070,48 @@ __global__ __launch_bounds__(RD_THREADS) void rd_argmax_kernel(const int32_t* __
                                                                kt_hip_sscale* rscale, int32_t* step) {
     __shared__ int64_t red[RD_WAVES];
     // key: the value in the high word, the inverted index in the low word (the lower index wins a tie)
+    auto key = [](int32_t v, int i) { return (int64_t)v * 4294967296LL + (int64_t)(0x7FFFFFFF - i); };
     int64_t best = INT64_MIN;
-    for (int i = threadIdx.x; i < n; i += RD_THREADS) {
-        const int64_t key = (int64_t)logits[i] * 4294967296LL + (int64_t)(0x7FFFFFFF - i);
-        best = key > best ? key : best;
+    const int s = record ? *step : 0;
+    int32_t* rec = record ? record + (size_t)s * n : nullptr;
+    // one pass over the codes, 16-byte loads (and stores into the record) where n and the addresses allow, several in
+    // flight per thread
+    const bool vec = n % 4 == 0 && ((uintptr_t)logits & 15) == 0 && (!rec || ((uintptr_t)rec & 15) == 0);
+    if (vec) {
+        const int n4 = n / 4;
+        const int4* l4 = reinterpret_cast<const int4*>(logits);
+        constexpr int U = 4;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += U * RD_THREADS) {
+            int4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) v[u] = i0 + u * RD_THREADS < n4 ? l4[i0 + u * RD_THREADS] : int4{0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * RD_THREADS;
+                if (i >= n4) break;
+                if (rec) reinterpret_cast<int4*>(rec)[i] = v[u];
+                const int64_t k0 = key(v[u].x, 4 * i), k1 = key(v[u].y, 4 * i + 1);
+                const int64_t k2 = key(v[u].z, 4 * i + 2), k3 = key(v[u].w, 4 * i + 3);
+                const int64_t a = k0 > k1 ? k0 : k1, b = k2 > k3 ? k2 : k3, c = a > b ? a : b;
+                best = c > best ? c : best;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += RD_THREADS) {
+            const int32_t v = logits[i];
+            if (rec) rec[i] = v;
+            const int64_t k = key(v, i);
+            best = k > best ? k : best;
+        }
     }
-    best = block_max_i64(best, red);
-    if (record) {
-        const int s = *step;
-        for (int i = threadIdx.x; i < n; i += RD_THREADS) record[(size_t)s * n + i] = logits[i];
-        __syncthreads();
-        if (threadIdx.x == 0) {
+    best = block_max_i64(best, red);  // every thread has read *step past here
+    if (threadIdx.x == 0) {
+        if (record) {
             rscale[s] = kt_hip_sscale{ls->mant, ls->shift, 1};
             *step = s + 1;
         }
+        *token = 0x7FFFFFFF - (int32_t)(uint32_t)(best & 0xFFFFFFFF);
     }
-    if (threadIdx.x == 0) *token = 0x7FFFFFFF - (int32_t)(uint32_t)(best & 0xFFFFFFFF);
 }
 
 // The attention step's LDS with hb heads' scores held at once: the per-step factors, hb score rows, the head
