@@ -208,7 +208,8 @@ __global__ __launch_bounds__(RQ_ROW_THREADS) void rq_requant_kernel(const int64_
     const bool held = out <= (int64_t)RQ_ROW_THREADS * RQ_VPT;
     int64_t v[RQ_VPT];
     int64_t m = 0;
-    if (held) {  // the slices 4 at a time, all of a thread's loads of them in flight together (branch-free)
+    if (held) {  // the slices 4 at a time, all of a thread's loads of them in flight together; a column block
+                 // past the row (the same for the whole CTA) is skipped
 #pragma unroll
         for (int i = 0; i < RQ_VPT; i++) v[i] = 0;
         int q0 = 0;
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(RQ_ROW_THREADS) void rq_requant_kernel(const int64_
 #pragma unroll
                 for (int i = 0; i < RQ_VPT; i++) {
                     const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
-                    t[u][i] = a[(q0 + u) * slice + (c < out ? c : out - 1)];
+                    t[u][i] = (int64_t)RQ_ROW_THREADS * i < out ? a[(q0 + u) * slice + (c < out ? c : out - 1)] : 0;
                 }
 #pragma unroll
             for (int u = 0; u < 4; u++)
@@ -230,7 +231,8 @@ __global__ __launch_bounds__(RQ_ROW_THREADS) void rq_requant_kernel(const int64_
 #pragma unroll
             for (int i = 0; i < RQ_VPT; i++) {
                 const int64_t c = threadIdx.x + (int64_t)RQ_ROW_THREADS * i;
-                v[i] = (int64_t)((uint64_t)v[i] + (uint64_t)a[q0 * slice + (c < out ? c : out - 1)]);
+                if ((int64_t)RQ_ROW_THREADS * i < out)
+                    v[i] = (int64_t)((uint64_t)v[i] + (uint64_t)a[q0 * slice + (c < out ? c : out - 1)]);
             }
 #pragma unroll
         for (int i = 0; i < RQ_VPT; i++)
