@@ -12,9 +12,11 @@
 #ifdef __HIPCC__
 #include <hip/hip_runtime.h>
 #define KT_SC_FN __host__ __device__ inline
+#define KT_SC_COLD __host__ __device__ inline __attribute__((noinline))
 #else
 #include <math.h>
 #define KT_SC_FN inline
+#define KT_SC_COLD inline __attribute__((noinline))
 #endif
 
 namespace kt {
@@ -41,6 +43,17 @@ KT_SC_FN int bits_u128(u128 v) {
 //    few dozen instructions, where a 64-bit integer division is a long software sequence;
 //  - both below 2^64: the 64-bit division;
 //  - otherwise restoring long division.
+// The last two are rare in the layers' Scale chains and long in code: they stay out of line (udiv128_rest), so the
+// inlined copies at every call site are short (one-token kernels fetch their straight-line code cold each launch).
+KT_SC_COLD u128 udiv128_rest(u128 n, u128 d) {
+    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
+    u128 q = 0, r = 0;
+    for (int i = bits_u128(n) - 1; i >= 0; i--) {
+        r = (r << 1) | ((n >> i) & 1);
+        if (r >= d) r -= d, q |= (u128)1 << i;
+    }
+    return q;
+}
 KT_SC_FN u128 udiv128(u128 n, u128 d) {
     // from_ratio's normalizations divide by powers of two (Scale::mul by 1, a negative shift by 2^-s): a shift
     if ((d >> 64) == 0 && (uint64_t)d != 0 && ((uint64_t)d & ((uint64_t)d - 1)) == 0)
@@ -54,13 +67,7 @@ KT_SC_FN u128 udiv128(u128 n, u128 d) {
         while (rem >= (i128)d64) q++, rem -= (i128)d64;
         return (u128)q;
     }
-    if ((n >> 64) == 0 && (d >> 64) == 0) return (u128)((uint64_t)n / (uint64_t)d);
-    u128 q = 0, r = 0;
-    for (int i = bits_u128(n) - 1; i >= 0; i--) {
-        r = (r << 1) | ((n >> i) & 1);
-        if (r >= d) r -= d, q |= (u128)1 << i;
-    }
-    return q;
+    return udiv128_rest(n, d);
 }
 
 // floor(n / d) for d < 2^32 and a quotient below 2^40: the double quotient is within 2^-12 of the exact one (the
@@ -156,6 +163,14 @@ KT_SC_FN Sc sc_add(Sc a, Sc o) {
 // from the double-precision root corrected to the exact floor: the estimate is within 2 of sqrt(n) there (the
 // conversion and the root each add a relative error of at most 2^-53 to a value below 2^52), and the two loops move
 // it to the r with r^2 <= n < (r + 1)^2, which is unique. Larger n take the Newton iteration itself.
+KT_SC_COLD u128 isqrt_newton(u128 n) {  // n >= 2^104: the reference's iteration itself
+    u128 x = (u128)1 << ((bits_u128(n) + 1) / 2);
+    for (;;) {
+        const u128 y = (x + udiv128(n, x)) >> 1;
+        if (y >= x) return x;
+        x = y;
+    }
+}
 KT_SC_FN u128 isqrt_u128(u128 n) {
     if (n == 0) return 0;
     if (bits_u128(n) <= 104) {
@@ -165,12 +180,7 @@ KT_SC_FN u128 isqrt_u128(u128 n) {
         while ((u128)(r + 1) * (r + 1) <= n) r++;
         return (u128)r;
     }
-    u128 x = (u128)1 << ((bits_u128(n) + 1) / 2);
-    for (;;) {
-        const u128 y = (x + udiv128(n, x)) >> 1;
-        if (y >= x) return x;
-        x = y;
-    }
+    return isqrt_newton(n);
 }
 
 // Scale::rsqrt (lib.rs:307-318); a.mant > 0.
@@ -194,6 +204,7 @@ KT_SC_FN int64_t sc_apply(Sc a, int64_t value) {
 // Scale::apply of an int32 code with 64-bit arithmetic where that is exact: |mant| < 2^32 and 0 <= shift <= 63 keep
 // |v * mant| below 2^63 and its sum with the rounding addend 2^(shift - 1) below 2^64 (unsigned); other Scales go
 // through the i128 sc_apply. The same rounding, half away from zero.
+KT_SC_COLD int64_t sc_apply_wide(Sc a, int64_t v) { return sc_apply(a, v); }
 KT_SC_FN int64_t sc_apply32(Sc a, int32_t v) {
     if (a.mant > -((int64_t)1 << 32) && a.mant < ((int64_t)1 << 32) && a.shift >= 0 && a.shift <= 63) {
         const uint64_t m = (uint64_t)(uint32_t)(a.mant < 0 ? -a.mant : a.mant);
@@ -202,7 +213,7 @@ KT_SC_FN int64_t sc_apply32(Sc a, int32_t v) {
         const uint64_t q = a.shift == 0 ? p : (p + ((uint64_t)1 << (a.shift - 1))) >> a.shift;
         return (v < 0) != (a.mant < 0) ? (int64_t)(0 - q) : (int64_t)q;
     }
-    return sc_apply(a, v);
+    return sc_apply_wide(a, v);  // a Scale outside the 64-bit range: rare, out of line
 }
 
 // floor(n / d) for 0 < d < 2^63 when the quotient is below 2^40: the double estimate's absolute error is then below
@@ -242,9 +253,10 @@ struct RqDen {
 KT_SC_FN RqDen rq_den(int64_t den) {
     return RqDen{den, (uint64_t)(den / 2), den > 0 ? 268435456.0 / (double)den : 0.0};
 }
+KT_SC_COLD int32_t requant_dyn_cold(int64_t v, int64_t den) { return requant_dyn_dev(v, den); }
 KT_SC_FN int32_t rq_apply(const RqDen& r, int64_t v) {
     const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
-    if (r.den <= 0 || r.den >= ((int64_t)1 << 62) || a > (uint64_t)r.den) return requant_dyn_dev(v, r.den);
+    if (r.den <= 0 || r.den >= ((int64_t)1 << 62) || a > (uint64_t)r.den) return requant_dyn_cold(v, r.den);
     uint64_t q = (uint64_t)((double)a * r.rinv + 0.5);
     const int64_t rem = (int64_t)((a << 28) + r.half - q * (uint64_t)r.den);
     if (rem < 0) q--;
