@@ -140,6 +140,25 @@ def test_scale_ops_equal_the_oracle(sd):
             assert scale_out(f, am, ash) == (w.mant, w.shift), (f, am, ash)
 
 
+def test_scale_ge_at_its_64_bit_bounds(sd):
+    """Scale::ge's 64-bit comparison (mantissas below 2^33, shifts within 30) against the oracle at and beyond its
+    bounds, including equal values written with different shifts."""
+    rng = np.random.default_rng(19)
+    cases = []
+    for d in (-32, -31, -30, -29, -1, 0, 1, 29, 30, 31, 32):
+        for ma, mb in ((2**33 - 1, 2**33 - 1), (2**33, 2**32), (1, 2**32), (2**32 + 1, 2**32)):
+            cases.append((ma, 40, mb, 40 + d))
+        for _ in range(40):
+            ma = rand_bits(rng, int(rng.integers(1, 35)))
+            cases.append((ma, 50, ma << max(d, 0) >> max(-d, 0) or 1, 50 + d))  # near-equal values
+            cases.append((ma, 50, rand_bits(rng, int(rng.integers(1, 35))), 50 + d))
+    for am, ash, bm, bsh in cases:
+        if bm >= 2**62:  # mantissas are non-negative i64 values
+            continue
+        assert bool(sd.sd_ge(am, ash, bm, bsh)) == O.scale_ge(O.Scale(am, ash), O.Scale(bm, bsh)), (am, ash, bm, bsh)
+        assert bool(sd.sd_ge(bm, bsh, am, ash)) == O.scale_ge(O.Scale(bm, bsh), O.Scale(am, ash)), (am, ash, bm, bsh)
+
+
 def test_udiv64_small_at_exact_multiples(sd):
     """udiv64_small (d < 2^32, quotient < 2^40) on exact multiples k * d and their neighbours, where a rounded
     double quotient can land just below an integer or just above it."""

@@ -134,8 +134,13 @@ KT_SC_FN Sc sc_recip(Sc a) {
 KT_SC_FN bool sc_ge(Sc a, Sc o) {
     if (a.mant == 0) return o.mant == 0;
     if (o.mant == 0) return true;
-    const u128 ma = (u128)(uint64_t)a.mant, mb = (u128)(uint64_t)o.mant;
     const int d = o.shift - a.shift;
+    {  // mantissas below 2^33 and shifts within 30 of each other: the same comparison in 64 bits
+        const uint64_t ua = (uint64_t)a.mant, ub = (uint64_t)o.mant;
+        if ((ua >> 33) == 0 && (ub >> 33) == 0 && d <= 30 && d >= -30)
+            return d >= 0 ? (ua << d) >= ub : ua >= (ub << -d);
+    }
+    const u128 ma = (u128)(uint64_t)a.mant, mb = (u128)(uint64_t)o.mant;
     if (d >= 0) {
         if (d + bits_u128(ma) > 127) return true;
         return (ma << d) >= mb;
