@@ -232,30 +232,31 @@ __global__ __launch_bounds__(QL_THREADS) void ql_quant_kernel(const int32_t* __r
 
 
 // One row (the decode step): the quant pass and the digit product in one launch. Every CTA takes max |x| over the
-// row and forms the row's three digit planes in LDS itself (at most QS_MAX_KP values, read from L2 by each CTA) while
+// row and forms the row's three digit planes in LDS itself (at most MAXKP values, read from L2 by each CTA) while
 // its first weight chunks are in flight, then runs the product of plane_skinny_kernel over its 8 output columns
 // (4 waves x 2 columns, the lanes striding k in 16-byte chunks, int32 plane-group sums by sdot4, a butterfly across
 // the wave). The CTA's largest |result| goes to its own slot part[blockIdx.x] (overwritten on every call, so no
 // pass has to clear it); ql_requant_kernel takes each segment's maximum over its CTAs' slots. CTA 0 writes each
 // segment's state for ql_requant_kernel. A CTA whose segment has a bias forms the bias factor itself. Requires
-// kp <= QS_MAX_KP and a single k-chunk (kp within the flush bound). launch_ql_impl takes this path for outputs of at
-// most QS_FUSED_OUT columns: for a longer row (the 4864-value down row in 112 CTAs) re-quantizing it in every CTA
-// cost more than the quant pass's launch; the 9728-column gate / up group (1216 CTAs) comes out even.
-constexpr int QS_MAX_KP = 1024;
+// kp <= MAXKP and a single k-chunk (kp within the flush bound). launch_ql_impl takes this path for outputs of at
+// most QS_FUSED_OUT columns: rows up to QS_MAX_KP values, and for 3 weight planes rows up to QS_LONG_KP values in an
+// instantiation with the larger LDS image (the 4864-value down row: 13.6 us against 8.8 + 9.0 for the quant pass and
+// the product; the small instantiation keeps the short rows' registers and LDS low).
+constexpr int QS_MAX_KP = 1024, QS_LONG_KP = 8192;
 constexpr int64_t QS_FUSED_OUT = 16384;
 constexpr int QS_THREADS = 256, QS_WAVES = QS_THREADS / 64;
 constexpr int QS_CPW = 2;  // output columns per wave
 constexpr int QS_COLS = QS_WAVES * QS_CPW;
 
-template <int PW>
+template <int PW, int MAXKP>
 __global__ __launch_bounds__(QS_THREADS) void ql_skinny_kernel(const int32_t* __restrict__ x, int in, int kp,
                                                                const kt_hip_qscale* __restrict__ xs,
                                                                const int8_t* __restrict__ wb, int64_t* __restrict__ y,
                                                                int N, const int64_t* __restrict__ bias, QlSeg seg,
                                                                QlScales sc, QlState* __restrict__ st,
                                                                int64_t* __restrict__ part) {
-    constexpr int NG = 3 + PW - 1, QPT = QS_MAX_KP / 4 / QS_THREADS;
-    __shared__ __attribute__((aligned(16))) int8_t xq[3 * QS_MAX_KP];
+    constexpr int NG = 3 + PW - 1, QPT = MAXKP / 4 / QS_THREADS;
+    __shared__ __attribute__((aligned(16))) int8_t xq[3 * MAXKP];
     __shared__ uint32_t red[QS_WAVES];
     __shared__ int64_t s_max[QS_WAVES];
     __shared__ int64_t s_f[2];  // the bias factor of this CTA's segment (mant, shift), when it has a bias
@@ -580,22 +581,20 @@ static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, con
     if (ntiles * 4 > KT_QL_PARTS * 8) return hipErrorInvalidValue;  // cannot happen: a split grid has < 128 tiles
 
     // one row within one k-chunk (the decode step): the quant pass inside the product, then the requant pass
-    // (a short row: each CTA quantizes it again, so a long one, or a grid of many CTAs, keeps the quant pass)
     bool seg_ok = true;  // every CTA of QS_COLS columns within one segment
     for (int g = 1; g < seg.n; g++) seg_ok = seg_ok && seg.col0[g] % QS_COLS == 0;
-    if (!geom && rows == 1 && kp <= QS_MAX_KP && out <= QS_FUSED_OUT && kp <= flush_k && seg_ok &&
+    const bool long_row = kp > QS_MAX_KP && kp <= QS_LONG_KP && pw == 3;
+    if (!geom && rows == 1 && (kp <= QS_MAX_KP || long_row) && out <= QS_FUSED_OUT && kp <= flush_k && seg_ok &&
         (pw == 1 || pw == 3 || pw == 5)) {
         const int ctas = (int)((out + QS_COLS - 1) / QS_COLS);
         int64_t* pm = reinterpret_cast<int64_t*>(base + off[2]);
-        if (pw == 1)
-            ql_skinny_kernel<1><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, seg, sc,
-                                                            st, pm);
-        else if (pw == 3)
-            ql_skinny_kernel<3><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, seg, sc,
-                                                            st, pm);
-        else
-            ql_skinny_kernel<5><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, seg, sc,
-                                                            st, pm);
+#define KT_QS(P, K) ql_skinny_kernel<P, K><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, \
+                                                                      seg, sc, st, pm)
+        if (long_row) KT_QS(3, QS_LONG_KP);
+        else if (pw == 1) KT_QS(1, QS_MAX_KP);
+        else if (pw == 3) KT_QS(3, QS_MAX_KP);
+        else KT_QS(5, QS_MAX_KP);
+#undef KT_QS
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         ql_requant_kernel<<<grid_for(n, 1) + 1, QL_THREADS, 0, s>>>(acc, n, out, bias, st, seg, sc, yo, pm, ctas);
