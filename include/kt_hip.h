@@ -129,7 +129,10 @@ int64_t kt_hip_quant_linear_multi_align(int64_t rows, int64_t out_f, int pw);
  * counterpart in the reference; it is for those callers that cannot allocate. Same integers, arguments and
  * requirements as kt_hip_quant_linear, plus kt_hip_quant_linear_workspace(rows, in_f, out_f) <=
  * KT_QL_SCRATCH_BYTES (else hipErrorInvalidValue before any device work). Every call on one GPU shares that GPU's
- * array: calls that overlap on one GPU (two streams, two threads) race and must be ordered by the caller. */
+ * array: calls that overlap on one GPU (two streams, two threads) race and must be ordered by the caller. The first
+ * call on a GPU looks up its array's address (a runtime call outside any stream), so it must run eagerly: a first
+ * call whose stream is being captured returns hipErrorStreamCaptureUnsupported and does nothing; every later call,
+ * any shape, may be captured. */
 #define KT_QL_SCRATCH_BYTES ((size_t)32 << 20)
 int kt_hip_quant_linear_noalloc(int dev, const int32_t* x_dev, int64_t rows, int64_t in_f,
                                 const kt_hip_qscale* xs_dev, const int8_t* w_planes_dev, int pw, int64_t out_f,
@@ -169,6 +172,7 @@ typedef struct {
                             nonlin.rs:7-26) */
 #define KT_REF_MAX_HEADS 64
 #define KT_REF_ATTN_LDS 65536 /* the attention step's LDS: at least 40 B per cached position + 12 B per q value */
+#define KT_REF_ATTN_MAX_SEQ 65536 /* the longest cache the attention step takes (with a workspace) */
 
 /* Offline tables (host only, no GPU; f64 with the C library's exp/pow/cos/sin, as the reference's f64 methods use
  * its platform's): Scale::from_f64 (lib.rs:215-222); CodeLut::build (lib.rs:359-379) of `kind` over [lo, hi] at
@@ -274,7 +278,8 @@ int kt_hip_ref_conv2d(int dev, const int32_t* x_dev, const kt_hip_qscale* xs_dev
  * integer-code softmax over rows 0..pos at a common score scale (1/sqrt(hd) as (isq_mant, isq_shift); the exp
  * CodeLut), and the heads brought to one scale: o_dev (nh hd codes) and os_dev, the o projection's input. Rows
  * 0..pos-1 are those of earlier calls. A position outside [0, max_seq) gives zeros. nh <= KT_REF_MAX_HEADS, nh a
- * multiple of nkv, hd even, LDS (KT_REF_ATTN_LDS) bounds max_seq. */
+ * multiple of nkv, hd even; without a workspace LDS (KT_REF_ATTN_LDS) bounds max_seq (about 1,369 positions at
+ * nh = 14, hd = 64): kt_hip_ref_attention_step_ws takes longer caches. */
 int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev, const int32_t* k_dev,
                               const kt_hip_qscale* ks_dev, const int32_t* v_dev, const kt_hip_qscale* vs_dev,
                               const int32_t* pos_dev, int64_t nh, int64_t nkv, int64_t hd, int64_t max_seq,
@@ -282,11 +287,29 @@ int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale
                               const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev, int64_t isq_mant,
                               int32_t isq_shift, const int64_t* exp_codes_dev, const kt_hip_codelut* exp_lut,
                               int32_t* o_dev, kt_hip_qscale* os_dev, void* stream);
+/* kt_hip_ref_attention_step for caches longer than its LDS holds (the reference's MAX_SEQ_CAP = 4096,
+ * crates/03-models/kt-model-decoder/src/lib.rs:46, and beyond, up to KT_REF_ATTN_MAX_SEQ): the per-step score and v
+ * factors and every head's scores go to ws_dev, a caller buffer of at least
+ * kt_hip_ref_attention_step_workspace(max_seq, nh, hd) bytes, 16-byte aligned (unused, and may be null, while
+ * max_seq fits the LDS path). Same integers and arguments otherwise. Calls that share ws_dev must be ordered. */
+size_t kt_hip_ref_attention_step_workspace(int64_t max_seq, int64_t nh, int64_t hd);
+int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev, const int32_t* k_dev,
+                                 const kt_hip_qscale* ks_dev, const int32_t* v_dev, const kt_hip_qscale* vs_dev,
+                                 const int32_t* pos_dev, int64_t nh, int64_t nkv, int64_t hd, int64_t max_seq,
+                                 int32_t* kc_dev, int32_t* vc_dev, kt_hip_sscale* kscale_dev,
+                                 kt_hip_sscale* vscale_dev, const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev,
+                                 int64_t isq_mant, int32_t isq_shift, const int64_t* exp_codes_dev,
+                                 const kt_hip_codelut* exp_lut, int32_t* o_dev, kt_hip_qscale* os_dev, void* ws_dev,
+                                 size_t ws_bytes, void* stream);
 /* argmax_codes (generate.rs:48-56): token_dev[0] = the first index of the largest of n codes. With record_dev
  * non-null the codes are copied to record_dev + step * n and (mant, shift) of ls_dev to rscale_dev[step], step =
- * step_dev[0], which then advances (the per-step logits hash_step covers, generate.rs:58-64). */
+ * step_dev[0], which then advances (the per-step logits hash_step covers, generate.rs:58-64). record_dev holds
+ * record_rows rows of n codes and rscale_dev record_rows entries: a step outside [0, record_rows) writes neither and
+ * leaves step_dev unchanged (the token is still chosen), so replays of a captured step past the last row are
+ * harmless. record_rows is ignored without a record. */
 int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hip_qscale* ls_dev, int32_t* token_dev,
-                      int32_t* record_dev, kt_hip_sscale* rscale_dev, int32_t* step_dev, void* stream);
+                      int32_t* record_dev, kt_hip_sscale* rscale_dev, int32_t* step_dev, int64_t record_rows,
+                      void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * The reference's MoeMlp at its own semantics (crates/01-engine/kt-core/src/layers.rs:652-1020, router.rs:29-79):

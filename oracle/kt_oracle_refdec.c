@@ -454,6 +454,22 @@ static void rope(const kt_refdec* M, int32_t* v, size_t p) {
     }
 }
 
+/* The cache append of Attention::decode_step (attention.rs:366-384): k rotated at pos, k and v and their scales
+ * pushed. */
+void kt_rd_attention_append(const void* model, void* cache, const int32_t* k, kt_scale ks, const int32_t* v,
+                            kt_scale vs, size_t pos) {
+    const kt_refdec* M = (const kt_refdec*)model;
+    rd_cache* C = (rd_cache*)cache;
+    const size_t hd = M->hd, kstride = M->nkv * hd;
+    int32_t* kd = C->k + C->steps * kstride;
+    memcpy(kd, k, kstride * sizeof(int32_t));
+    for (size_t h = 0; h < M->nkv; h++) rope(M, kd + h * hd, pos);
+    memcpy(C->v + C->steps * kstride, v, kstride * sizeof(int32_t));
+    C->ks[C->steps] = ks;
+    C->vs[C->steps] = vs;
+    C->steps++;
+}
+
 /* The core of Attention::decode_step (attention.rs:358-458) after the q/k/v projections: RoPE at pos, append k and
  * v with their scales, the integer-code softmax per head over every cached step at a common score scale, the
  * heads brought to a common scale and requantized. Returns the concatenated head outputs (the wo input). */
@@ -465,13 +481,8 @@ void kt_rd_attention_core(const void* model, void* cache, const int32_t* q, kt_s
     int32_t* qd = (int32_t*)malloc(qstride * sizeof(int32_t));
     memcpy(qd, q, qstride * sizeof(int32_t));
     for (size_t h = 0; h < nh; h++) rope(M, qd + h * hd, pos);
-    int32_t* kd = C->k + C->steps * kstride;
-    memcpy(kd, k, kstride * sizeof(int32_t));
-    for (size_t h = 0; h < nkv; h++) rope(M, kd + h * hd, pos);
-    memcpy(C->v + C->steps * kstride, v, kstride * sizeof(int32_t));
-    C->ks[C->steps] = ks;
-    C->vs[C->steps] = vs;
-    const size_t steps = ++C->steps;
+    kt_rd_attention_append(model, cache, k, ks, v, vs, pos);
+    const size_t steps = C->steps;
 
     kt_scale v_ref = ZERO;
     for (size_t j = 0; j < steps; j++) v_ref = fold_max(v_ref, C->vs[j]);

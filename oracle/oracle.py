@@ -138,6 +138,7 @@ def _declare(L: C.CDLL) -> None:
         "kt_rd_add": (None, [_P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_swiglu_act": (None, [_P, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_attention_core": (None, [_P, _P, _P, Scale, _P, Scale, _P, Scale, _SZ, _P, C.POINTER(Scale)]),
+        "kt_rd_attention_append": (None, [_P, _P, _P, Scale, _P, Scale, _SZ]),
         "kt_rd_attention_prefill": (None, [_P, _SZ, _P, Scale, _P, Scale, _P, Scale, _P, C.POINTER(Scale)]),
         "kt_rd_forward": (C.c_int, [_P, _P, _SZ, _P, C.POINTER(Scale)]),
         "kt_rd_new": (_P, [_SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_double, C.c_double, _SZ]),
@@ -926,6 +927,12 @@ def rd_attention_core(cache: RefCache, q, qs, k, ks, v, vs, pos: int):
     lib().kt_rd_attention_core(cache.model.ptr, cache.ptr, _ptr(q), _sc(qs), _ptr(k), _sc(ks), _ptr(v), _sc(vs), pos,
                                _ptr(o), C.byref(os_))
     return o, (os_.mant, os_.shift)
+
+
+def rd_attention_append(cache: RefCache, k, ks, v, vs, pos: int) -> None:
+    """Only the cache append of Attention::decode_step (attention.rs:366-384): k rotated at pos, k, v, their scales."""
+    k, v = _c(k, np.int32), _c(v, np.int32)
+    lib().kt_rd_attention_append(cache.model.ptr, cache.ptr, _ptr(k), _sc(ks), _ptr(v), _sc(vs), pos)
 
 
 # ---------------------------------------------------------------------------------------------------------------

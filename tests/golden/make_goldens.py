@@ -2,7 +2,8 @@
 (oracle/kt_oracle.c, the restated reference CPU path). The GPU tests compare the device results with these fixtures
 at full size, where recomputing the CPU answer inside a test would take too long.
 
-Run from the repository root:  python tests/golden/make_goldens.py [config1 config2 config3 config4 config5]
+Run from the repository root:  python tests/golden/make_goldens.py [config1 config2 config3 config4 config5
+config3_ref]  (config3_ref, the reference-semantics decoder over config 3's 640 positions, only when named)
 """
 import json
 import os
@@ -168,6 +169,8 @@ def main() -> None:
         g["config4"] = config4()
     if "config5" in want:
         g["config5"] = config5()
+    if "config3_ref" in want:
+        g["config3_ref"] = config3_ref()
     json.dump(g, open(OUT, "w"), indent=1, sort_keys=True)
     print(f"wrote {OUT} in {time.time() - t0:.1f}s")
 
@@ -195,6 +198,27 @@ def config2() -> dict:
         }
         print(f"config2 M={m}: {time.time() - t:.1f}s", flush=True)
     return c2
+
+
+def config3_ref() -> dict:
+    """Config 3 at the reference's own semantics: the oracle's restatement of DecoderModel (kt_oracle_refdec.c) at
+    the Qwen2.5-0.5B shape over the weights of tritify_amd.workloads.ref_decoder_weights, repro::run of a 512-token
+    prompt (every prompt token through decode_step, generate.rs:82-93) and 128 greedy steps: the logits_hash of
+    each of the 640 positions, the run's hash and the chosen tokens. Not in the default set (minutes of CPU)."""
+    from tritify_amd import workloads as W
+
+    cfg, rc = W.REF_QWEN, W.REF_C3
+    t = time.time()
+    model = O.RefModel.from_weights(cfg, *W.ref_decoder_weights(cfg, rc["w_seed"]))
+    prompt = W.ref_c3_prompt(cfg)
+    print(f"config3_ref: model built in {time.time() - t:.1f}s", flush=True)
+    O.set_max_threads(0)
+    t = time.time()
+    toks, run, pos = model.generate(prompt, rc["decode"] + 1)
+    print(f"config3_ref: {len(pos)} positions in {time.time() - t:.1f}s", flush=True)
+    return {"cfg": cfg, "w_seed": rc["w_seed"], "prompt_seed": rc["prompt_seed"], "prompt": len(prompt),
+            "decode": rc["decode"], "prompt_sha256": O.sha256_hex(np.asarray(prompt, dtype=np.int32)),
+            "tokens": toks, "run_sha256": run, "position_sha256": pos}
 
 
 if __name__ == "__main__":

@@ -176,6 +176,38 @@ def test_ref_embed_and_argmax(torch_dev):
         assert int(tok.item()) == want and np.array_equal(rec2.cpu().numpy(), lg) and int(st2.item()) == 1
 
 
+def test_ref_argmax_record_stops_at_its_last_row(torch_dev):
+    """A step at or past the record's rows (replays of a captured greedy step beyond max_seq) or below zero records
+    nothing and does not advance: the guard rows after the record stay untouched."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    say("case: ref_argmax record capacity")
+    rng = np.random.default_rng(5)
+    n, cap, guard = 1000, 3, 2
+    lg = rng.integers(-(2**30), 2**30, size=n).astype(np.int32)
+    lg[417] = 2**31 - 1
+    ld = dev_i32(torch, lg)
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    record = torch.full(((cap + guard) * n,), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+    rscale = torch.full(((cap + guard) * 16,), 0xA5, dtype=torch.uint8, device="cuda")
+    step = torch.tensor([cap - 1], dtype=torch.int32, device="cuda")
+    for _ in range(cap + 2):
+        B.ref_argmax(ld, n, rec(torch, (7, 3)), tok, record, rscale, step, record_rows=cap)
+        assert int(tok.item()) == 417
+    assert int(step.item()) == cap
+    r = record.cpu().numpy().reshape(cap + guard, n)
+    assert np.array_equal(r[cap - 1], lg) and (r[cap:] == 0x5A5A5A5A).all() and (r[:cap - 1] == 0x5A5A5A5A).all()
+    rs = rscale.cpu().numpy().reshape(cap + guard, 16)
+    assert (rs[cap:] == 0xA5).all() and (rs[:cap - 1] == 0xA5).all()
+    step.fill_(-1)
+    B.ref_argmax(ld, n, rec(torch, (7, 3)), tok, record, rscale, step, record_rows=cap)
+    assert int(step.item()) == -1 and int(tok.item()) == 417
+    assert (record.cpu().numpy().reshape(cap + guard, n)[:cap - 1] == 0x5A5A5A5A).all()
+    with pytest.raises(RuntimeError):
+        B.ref_argmax(ld, n, rec(torch, (7, 3)), tok, record, rscale, step, record_rows=0)
+
+
 @pytest.mark.parametrize("cfg", [dict(O.SYNTH_CFG, max_seq=48),
                                  dict(dim=64, layers=1, nh=14, nkv=2, hd=64, hidden=64, vocab=8, eps=1e-6,
                                       theta=1.0e6, max_seq=80),
@@ -226,6 +258,71 @@ def test_ref_attention_steps(torch_dev, cfg):
         got = o.cpu().numpy()
         assert np.array_equal(got, oo), f"step {p}: {np.argwhere(got != oo)[:5].tolist()}"
         assert rd(os_) == so, p
+
+
+@pytest.mark.parametrize("max_seq", [1369, 4096])
+def test_ref_attention_steps_long_cache(torch_dev, max_seq):
+    """Attention::decode_step's core at the Qwen2.5-0.5B heads (14 / 2 of 64) over every position of a long cache:
+    1369 positions, the most the LDS path holds (one head's scores at a time), and 4096, the reference's MAX_SEQ_CAP
+    (crates/03-models/kt-model-decoder/src/lib.rs:46), on the workspace path. The device runs every step; the oracle
+    checks the output codes and scale at spread positions (the first steps, every 97th, around 1369 and the last)
+    and only appends to its cache in between."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    nh, nkv, hd = 14, 2, 64
+    say(f"case: ref_attention_steps long cache max_seq={max_seq}")
+    cfg = dict(dim=64, layers=1, nh=nh, nkv=nkv, hd=hd, hidden=64, vocab=8, eps=1e-6, theta=1.0e6, max_seq=max_seq)
+    assert B.ref_attention_step_fits_lds(max_seq, nh, hd) == (max_seq <= 1369)
+    model = O.RefModel(11, cfg)
+    cache = O.RefCache(model)
+    qd, kvd, ms = nh * hd, nkv * hd, max_seq
+    cos_t, sin_t = B.ref_rope_tables(ms, hd, cfg["theta"])
+    cos_d, sin_d = (torch.from_numpy(t.view(np.uint8)).cuda() for t in (cos_t, sin_t))
+    exp_codes, exp_lut = B.ref_codelut(B.LUT_EXP, -30.0, 0.0, 16, 20, False)
+    exp_d = torch.from_numpy(exp_codes).cuda()
+    isq = B.ref_scale_from_f64(1.0 / np.sqrt(hd))
+    kc = torch.zeros(ms * kvd, dtype=torch.int32, device="cuda")
+    vc = torch.zeros(ms * kvd, dtype=torch.int32, device="cuda")
+    ks_d = torch.zeros(ms * 16, dtype=torch.uint8, device="cuda")
+    vs_d = torch.zeros(ms * 16, dtype=torch.uint8, device="cuda")
+    o, os_ = torch.zeros(qd, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    pos_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = None
+    if not B.ref_attention_step_fits_lds(ms, nh, hd):
+        ws = torch.empty(B.ref_attention_step_workspace(ms, nh, hd), dtype=torch.uint8, device="cuda")
+    check = set(range(8)) | set(range(0, ms, 97)) | {1367, 1368, 1369, 1370} | set(range(ms - 3, ms))
+    rng = np.random.default_rng(4096 + ms)
+    qb = rng.integers(-(2**28), 2**28, size=(ms, qd)).astype(np.int32)
+    kb = rng.integers(-(2**28), 2**28, size=(ms, kvd)).astype(np.int32)
+    vb = rng.integers(-(2**28), 2**28, size=(ms, kvd)).astype(np.int32)
+    qdv, kdv, vdv = (torch.from_numpy(a).cuda() for a in (qb, kb, vb))
+    scl = [((int(rng.integers(2**30, 2**31)), int(rng.integers(78, 84))), rand_scale(rng), rand_scale(rng))
+           for _ in range(ms)]
+    srec = torch.from_numpy(np.array([[m, sh] for t in scl for (m, sh) in t], dtype=np.int64)).cuda()
+    recs = torch.zeros((ms * 3, 4), dtype=torch.int64, device="cuda")
+    recs[:, 0] = srec[:, 0]
+    recs[:, 1] = srec[:, 1]  # the shift in the low word of the second int64 (little endian)
+    checked = 0
+    for p in range(ms):
+        (qs, ks, vs) = scl[p]
+        pos_d.fill_(p)
+        B.ref_attention_step(qdv[p], recs[3 * p], kdv[p], recs[3 * p + 1], vdv[p], recs[3 * p + 2], pos_d, nh, nkv,
+                             hd, ms, kc, vc, ks_d, vs_d, cos_d, sin_d, isq, exp_d, exp_lut, o, os_, ws_dev=ws)
+        if p in check:
+            oo, so = O.rd_attention_core(cache, qb[p], qs, kb[p], ks, vb[p], vs, p)
+            got = o.cpu().numpy()
+            assert np.array_equal(got, oo), f"step {p}: {np.argwhere(got != oo)[:5].tolist()}"
+            assert rd(os_) == so, p
+            checked += 1
+        else:
+            O.rd_attention_append(cache, kb[p], ks, vb[p], vs, p)
+    assert checked == len([c for c in check if c < ms])
+    # the workspace path refuses to run without its workspace
+    if ws is not None:
+        with pytest.raises(RuntimeError):
+            B.ref_attention_step(qdv[0], recs[0], kdv[0], recs[1], vdv[0], recs[2], pos_d, nh, nkv, hd, ms, kc, vc,
+                                 ks_d, vs_d, cos_d, sin_d, isq, exp_d, exp_lut, o, os_)
 
 
 def test_synthetic_decoder_reproduces_the_golden(torch_dev):
@@ -291,6 +388,67 @@ def test_qwen_shaped_decoder_against_the_oracle(torch_dev):
     first = next((i for i, (a, b) in enumerate(zip(hashes, pos_o)) if a != b), None)
     assert first is None, f"first differing position {first}"
     assert toks == toks_o and run == run_o
+
+
+_C3_WEIGHTS: dict = {}
+
+
+def _c3_weights():
+    """Config 3's reference-decoder weights (generated once per session: 494 M codes)."""
+    from tritify_amd import workloads as W
+
+    if not _C3_WEIGHTS:
+        _C3_WEIGHTS["w"] = W.ref_decoder_weights(W.REF_QWEN, W.REF_C3["w_seed"])
+    return _C3_WEIGHTS["w"]
+
+
+@pytest.mark.parametrize("max_seq", [640, 4096])
+def test_config3_at_the_reference_semantics_full_size(torch_dev, max_seq):
+    """Config 3's workload at the reference's own semantics on the device: the Qwen2.5-0.5B-shape DecoderModel
+    (24 layers, vocab 151936), a 512-token prompt through decode_step and 128 greedy steps as replays of one
+    captured greedy step. Every one of the 640 positions' logits hash, the run's hash and the chosen tokens equal the
+    committed fixture (the oracle's repro::run, tests/golden/make_goldens.py config3_ref). With max_seq 4096 (the
+    reference's MAX_SEQ_CAP) the attention step runs on its workspace path at every position; with 640 on LDS."""
+    import hashlib
+    import json
+    import os
+
+    from tritify_amd import workloads as W
+    from tritify_amd.refdecoder import RefDecoder, logits_hash_bytes
+
+    torch = torch_dev
+    fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "goldens.json")))["config3_ref"]
+    cfg = dict(W.REF_QWEN, max_seq=max_seq)
+    assert fx["cfg"] == W.REF_QWEN
+    prompt = W.ref_c3_prompt(cfg)
+    assert hashlib.sha256(np.asarray(prompt, dtype=np.int32).tobytes()).hexdigest() == fx["prompt_sha256"]
+    say(f"case: config 3 at the reference semantics, 512 + 128 positions, max_seq {max_seq}")
+    dec = RefDecoder(cfg, *_c3_weights())
+    assert (dec.attn_ws is None) == (max_seq == 640)
+    dec.decode_step(prompt[0], 0)
+    g = dec.capture_greedy_step()
+    dec.new_cache()
+    dec.pos.zero_()
+    for t in prompt:
+        dec.token.fill_(t)
+        g.replay()
+    for _ in range(W.REF_C3["decode"]):
+        g.replay()
+    torch.cuda.synchronize()
+    P, npos = len(prompt), len(prompt) + W.REF_C3["decode"]
+    rec = [dec.recorded(p) for p in range(npos)]
+    hashes = [hashlib.sha256(logits_hash_bytes(*r)).hexdigest() for r in rec]
+    first = next((i for i, (a, b) in enumerate(zip(hashes, fx["position_sha256"])) if a != b), None)
+    assert first is None, f"first differing position {first}"
+    assert len(hashes) == len(fx["position_sha256"]) == 640
+    run = hashlib.sha256(b"".join(logits_hash_bytes(*r) for r in rec[P - 1:])).hexdigest()
+    assert run == fx["run_sha256"]
+    assert [int(np.argmax(r[0])) for r in rec[P - 1:]] == fx["tokens"]
+    assert int(dec.pos.item()) == npos
+    del dec, g, rec
+    torch.cuda.empty_cache()
+    if max_seq == 4096:
+        _C3_WEIGHTS.clear()
 
 
 @pytest.mark.parametrize("rows,dim", [(65, 896), (300, 64), (1024, 96)])

@@ -299,3 +299,119 @@ def test_full_decoder_forward_tracks_float():
     li = _dq(lg, ls)
     assert np.abs(li - lr).max() <= 0.1 * np.abs(lr).max()
     assert (np.argmax(li, axis=1) == np.argmax(lr, axis=1)).all()
+
+
+# Exact cases of the batched forward (CausalLM::forward_int, Attention::forward_int over a sequence). The v scale is
+# a power of two (2^31, s) = 2^(31 - s), so every Scale product, reciprocal and ratio of the attention's close is
+# exact (kt-int/src/lib.rs:191-300) and the outputs follow from integer arithmetic: requant_dyn(v, 2^28, g) is
+# round(v 2^28 / g) half away from zero.
+
+def _rha(n, d):
+    q = (2 * abs(n) + d) // (2 * d)
+    return q if n >= 0 else -q
+
+
+def _sval(sc):
+    from fractions import Fraction
+
+    return Fraction(sc[0]) / Fraction(2) ** sc[1]
+
+
+PREFILL_CFG = dict(dim=16, layers=1, nh=4, nkv=2, hd=8, hidden=16, vocab=8, eps=1e-6, theta=1.0e6, max_seq=16)
+
+
+def test_prefill_attention_one_hot_returns_the_attended_v_row_in_every_row():
+    """Only k_0 is nonzero and every q row meets it with a score far past the exp table's -30 cutoff: every row's
+    softmax is one-hot on step 0 (attention.rs:506-530), every row and head returns v_0 of its kv head; with v's
+    largest |code| 2^28 the output codes are v_0 exactly and the scale is v's (2^20 / 2^20 cancels)."""
+    m = O.RefModel(3, PREFILL_CFG)
+    T, nh, nkv, hd = 9, 4, 2, 8
+    rng = np.random.default_rng(31)
+    q = np.zeros((T, nh, hd), np.int64)
+    k = np.zeros((T, nkv, hd), np.int64)
+    v = rng.integers(-(2**28), 2**28, size=(T, nkv, hd))
+    k[0] = 2**20
+    q[:] = 2**20  # rotated by position i, q_i . k_0 = 2^41 sum_j cos(i theta_j) > 2^42 for i < 9 (hd 8): at q and
+    v[0, 0, 0] = 2**28  # k scales of 1 that is far past 30 real units ahead of the zero scores of steps 1..i
+    qs, ks, vs = (1 << 31, 31), (1 << 31, 31), (1 << 31, 44)
+    o, os_ = m.attention_prefill(T, q.astype(np.int32).ravel(), qs, k.astype(np.int32).ravel(), ks,
+                                 v.astype(np.int32).ravel(), vs)
+    o = o.reshape(T, nh, hd)
+    for i in range(T):
+        for h in range(nh):
+            assert np.array_equal(o[i, h], v[0, h // 2]), (i, h)
+    assert _sval(os_) == _sval(vs)
+
+
+def test_prefill_attention_two_rows_uniform_softmax_is_exact():
+    """k = 0: every score is 0, every numerator exp(0) = 2^20; row 0 returns v_0, row 1 the mean (v_0 + v_1) / 2
+    (sumc 2^21: the scale v / 2^21 brought to the common v / 2^20 by an exact 1/2, attention.rs:560-590). A code of
+    2^29 in row 0 sets the requant's divisor: out = round(2^20 v_0 / 2^21) and round(2^19 (v_0 + v_1) / 2^21),
+    half away from zero, with values of both signs on the halves."""
+    m = O.RefModel(3, PREFILL_CFG)
+    T, nh, nkv, hd = 2, 4, 2, 8
+    rng = np.random.default_rng(32)
+    q = rng.integers(-(2**28), 2**28, size=(T, nh, hd))
+    k = np.zeros((T, nkv, hd), np.int64)
+    v = rng.integers(-(2**27), 2**27, size=(T, nkv, hd))
+    v[0, 0, 0], v[1, 0, 0] = 2**29, 0
+    # row 0 halves 1, -1 (v_0 / 2); row 1's sums 2, -2, 6, -6 land on halves of the quarter 2^19 s / 2^21
+    v[0, 1, :4], v[1, 1, :4] = [1, -1, 2, -2], [1, -1, 4, -4]
+    vs = (1 << 31, 50)
+    o, os_ = m.attention_prefill(T, q.astype(np.int32).ravel(), (1 << 30, 40), k.astype(np.int32).ravel(),
+                                 (1 << 30, 40), v.astype(np.int32).ravel(), vs)
+    o = o.reshape(T, nh, hd)
+    vv0 = [[2**20 * int(v[0, h // 2, d]) for d in range(hd)] for h in range(nh)]
+    vv1 = [[(2**20 * (int(v[0, h // 2, d]) + int(v[1, h // 2, d]))) // 2 for d in range(hd)] for h in range(nh)]
+    g = max(abs(x) for r in vv0 + vv1 for x in r)
+    assert g == 2**49
+    for h in range(nh):
+        assert o[0, h].tolist() == [_rha(x * 2**28, g) for x in vv0[h]]
+        assert o[1, h].tolist() == [_rha(x * 2**28, g) for x in vv1[h]]
+    assert o[0, 2, :4].tolist() == [1, -1, 1, -1] and o[1, 2, :4].tolist() == [1, -1, 2, -2]
+    from fractions import Fraction
+
+    assert _sval(os_) == Fraction(g, 2**28) * _sval(vs) / 2**20
+
+
+def test_batched_forward_is_the_composition_of_its_pinned_ops():
+    """CausalLM::forward_int over T tokens (model.rs:361-367: embed_int, blocks_int, head_int; each block x + attn
+    (input_norm(x)), then + ffn(post_norm(x)), model.rs:175-183; SwiGluMlp layers.rs:609-640) composed here from the
+    oracle's separately pinned ops -- the Embedding rows at the embedding's scale, RmsNorm over T rows,
+    QuantLinear over T rows, the prefill attention core, add, the SwiGLU activation over the T x hidden tensor --
+    equals the oracle's batched forward, logits and scale, bit for bit, at T = 1, 2, 5 and 11."""
+    cfg = dict(dim=32, layers=2, nh=4, nkv=2, hd=8, hidden=48, vocab=37, eps=1e-6, theta=1.0e6, max_seq=16)
+    m = O.RefModel(0xC0FFEE, cfg)
+    emb, es = m.emb()
+    dim, hid, qd, kvd = cfg["dim"], cfg["hidden"], cfg["nh"] * cfg["hd"], cfg["nkv"] * cfg["hd"]
+
+    def ql(x, xs, rows, which, layer=0):
+        w, ws = m.ql(layer, which)
+        y, ys, _, _ = O.quant_linear_forward(x, rows, w.shape[1], xs, w, w.shape[0], ws)
+        return y.ravel(), ys
+
+    def norm(x, xs, rows, layer, which):
+        g, gs, eps = m.norm(layer, which)
+        return O.rd_rmsnorm(x, rows, dim, xs, g, gs, eps)
+
+    for T in (1, 2, 5, 11):
+        toks = [(7 * i + 3) % cfg["vocab"] for i in range(T)]
+        x, xs = emb[toks].ravel().astype(np.int32), es
+        for l in range(cfg["layers"]):
+            h, hs = norm(x, xs, T, l, "in_norm")
+            q, qs = ql(h, hs, T, "wq", l)
+            k, ks = ql(h, hs, T, "wk", l)
+            v, vs = ql(h, hs, T, "wv", l)
+            o, os_ = m.attention_prefill(T, q, qs, k, ks, v, vs)
+            a, as_ = ql(o, os_, T, "wo", l)
+            x, xs = O.rd_add(x, xs, a, as_)
+            h, hs = norm(x, xs, T, l, "post_norm")
+            g, gs = ql(h, hs, T, "gate", l)
+            u, us = ql(h, hs, T, "up", l)
+            hh, hhs = O.rd_swiglu_act(m, g, gs, u, us)
+            d, ds = ql(hh, hhs, T, "down", l)
+            x, xs = O.rd_add(x, xs, d, ds)
+        h, hs = norm(x, xs, T, 0, "final_norm")
+        lg, ls = ql(h, hs, T, "lm_head")
+        want, wls = m.forward(toks)
+        assert np.array_equal(lg.reshape(T, cfg["vocab"]), want) and ls == wls, T

@@ -186,6 +186,158 @@ def test_combine_and_merge_closed_forms():
         assert np.abs(got[t] - dq(rows[t], rs[t])).max() <= os_[0] * 2.0 ** -os_[1]
 
 
+# Exact cases. A Scale (2^31, s) is the power of two 2^(31 - s); products, reciprocals and from_ratio of powers of
+# two are exact in kt-int (crates/00-kernels/kt-int/src/lib.rs:191-300), so with such scales every factor combine
+# and merge_rows form is exact and their outputs follow from integer arithmetic alone: f.apply(v) for f = 2^-e is
+# round(v / 2^e) half away from zero, requant_dyn(v, 2^28, g) is round(v 2^28 / g) half away from zero. The inputs
+# put values on exact halves, where a truncating, flooring or half-even rounding gives another answer.
+
+
+def p2(s):
+    return (1 << 31, s)
+
+
+def rha(n, d):
+    """round(n / d) half away from zero, Python integers, d > 0."""
+    q = (2 * abs(n) + d) // (2 * d)
+    return q if n >= 0 else -q
+
+
+def sval(sc):
+    from fractions import Fraction
+
+    return Fraction(sc[0]) / Fraction(2) ** sc[1]
+
+
+def test_combine_of_one_expert_with_its_own_numerator_returns_its_codes():
+    """ec = sumc = 2^19, the expert's largest |code| 2^28, its scale a power of two: the codes come back unchanged
+    and the scale equals the expert's (layers.rs:893-923)."""
+    rng = np.random.default_rng(21)
+    y = rng.integers(-(2**28), 2**28, size=57).astype(np.int32)
+    y[13] = -(2**28)
+    out, os_ = O.rm_combine(y, [p2(44)], 57, [2**19], 2**19)
+    assert np.array_equal(out, y)
+    assert sval(os_) == sval(p2(44))
+
+
+def test_combine_rounds_half_away_from_zero_at_both_steps():
+    """Two experts at 2^-9 and 2^-10 (the second brought to the first's scale: round(v / 2) on odd codes, exact
+    halves of both signs), ec = [1, 1], sumc = 2, and one sum of exactly 2^29 so requant_dyn halves every sum:
+    out = round(round(y1 / 2) + y0) / 2), all half away from zero; the output scale is the common scale."""
+    rng = np.random.default_rng(22)
+    n = 64
+    y0 = rng.integers(-(2**26), 2**26, size=n).astype(np.int64)
+    y1 = (rng.integers(-(2**26), 2**26, size=n) | 1).astype(np.int64)  # odd: y1 / 2 on a half
+    y0[0], y1[0] = 2**29, 0
+    y0[1:9] = [1, -1, 2, -2, 0, 0, 5, -5]
+    y1[1:9] = [1, -1, 1, -1, 3, -3, -1, 1]
+    ys = np.concatenate([y0, y1]).astype(np.int32)
+    out, os_ = O.rm_combine(ys, [p2(40), p2(41)], n, [1, 1], 2)
+    acc = [int(a) + rha(int(b), 2) for a, b in zip(y0, y1)]
+    assert max(abs(a) for a in acc) == 2**29
+    want = [rha(a * 2**28, 2**29) for a in acc]
+    assert out.tolist() == want
+    # the planted halves: 1 + round(1/2) = 2 -> 1; -1 + round(-1/2) = -2 -> -1; 2 + 1 = 3 -> 2 (half away);
+    # -2 - 1 = -3 -> -2; round(3/2) = 2 -> 1; round(-3/2) = -2 -> -1; 5 - 1 = 4 -> 2; -5 + 1 = -4 -> -2
+    assert out[1:9].tolist() == [1, -1, 2, -2, 1, -1, 2, -2]
+    assert sval(os_) == sval(p2(40))
+
+
+def test_combine_weighted_sum_is_exact_at_power_of_two_numerators():
+    """ec = [2^19, 2^19], sumc = 2^20, experts at 2^-9 and 2^-10, one sum exactly 2^47: every code is
+    y0 + round(y1 / 2) with nothing lost, and the scale is 2^-9 (2^47 / 2^28) / 2^20."""
+    rng = np.random.default_rng(23)
+    n = 50
+    y0 = rng.integers(-(2**27) + 1, 2**27, size=n).astype(np.int64)
+    y1 = rng.integers(-(2**27), 2**27, size=n).astype(np.int64)
+    y0[0], y1[0] = 2**28, 0
+    out, os_ = O.rm_combine(np.concatenate([y0, y1]).astype(np.int32), [p2(40), p2(41)], n, [2**19, 2**19], 2**20)
+    assert out.tolist() == [int(a) + rha(int(b), 2) for a, b in zip(y0, y1)]
+    from fractions import Fraction
+
+    assert sval(os_) == sval(p2(40)) * Fraction(2**47, 2**28) / 2**20
+
+
+def test_merge_rows_at_one_scale_is_requant_dyn_of_the_concatenation():
+    """Rows that share one power-of-two scale merge as requant_dyn of their concatenation by its largest |code|
+    (layers.rs:866-891); the scale is that maximum over 2^28 times the rows' scale."""
+    rng = np.random.default_rng(24)
+    T, d = 5, 33
+    rows = rng.integers(-(2**30), 2**30, size=T * d).astype(np.int32)
+    out, os_ = O.rm_merge_rows(rows, [p2(47)] * T, T, d)
+    g = int(np.abs(rows.astype(np.int64)).max())
+    assert out.tolist() == [rha(int(v) * 2**28, g) for v in rows]
+    from fractions import Fraction
+
+    assert sval(os_) == Fraction(g, 2**28) * sval(p2(47))
+
+
+def test_merge_rows_brings_rows_to_the_largest_scale_with_exact_halves():
+    """Rows at 2^-9, 2^-11 and zero: the second brought to the first by round(v / 4) (v = 2 mod 4: exact halves),
+    the third all zeros; one code of exactly 2^29 makes requant_dyn halve every value: round(a / 2), half away from
+    zero throughout."""
+    rng = np.random.default_rng(25)
+    d = 40
+    r0 = rng.integers(-(2**27), 2**27, size=d).astype(np.int64)
+    r1 = (rng.integers(-(2**26), 2**26, size=d) * 4 + 2).astype(np.int64)
+    r1[1::2] = -r1[1::2]
+    r2 = rng.integers(-(2**30), 2**30, size=d).astype(np.int64)
+    r0[0] = 2**29
+    r0[1:5], r1[1:5] = [1, -1, 3, -3], [2, -2, 6, -6]
+    rows = np.concatenate([r0, r1, r2]).astype(np.int32)
+    out, os_ = O.rm_merge_rows(rows, [p2(40), p2(42), (0, 0)], 3, d)
+    a = [int(v) for v in r0] + [rha(int(v), 4) for v in r1] + [0] * d
+    assert max(abs(x) for x in a) == 2**29
+    assert out.tolist() == [rha(x * 2**28, 2**29) for x in a]
+    # 1 -> round(1/2) = 1; -1 -> -1; 3 -> 2; -3 -> -2; round(2/4) = 1 -> 1; -1 -> -1; round(6/4) = 2 -> 1; -> -1
+    assert out[1:5].tolist() == [1, -1, 2, -2] and out[d + 1:d + 5].tolist() == [1, -1, 1, -1]
+    assert not out[2 * d:].any()
+    assert sval(os_) == 2 * sval(p2(40))
+
+
+def test_softmax_route_exact_identities():
+    """MoeMlp::route (layers.rs:826-851): the selected experts are the top-k logits with ties to the lower index;
+    the strongest one's numerator is exp(0) = 2^20 exactly (the table's last entry); numerators fall with the logit;
+    normalized over the top k, sumc is their sum; normalized over all E, sumc is the sum of every expert's numerator,
+    which a top-E route of the same layer lists."""
+    for norm in (False, True):
+        m = O.RefMoe(0x30E1, 64, 8, 2, 96, norm)
+        full = O.RefMoe(0x30E1, 64, 8, 8, 96, norm)
+        x, xs, _ = O.rm_probe(0x30E4, 9 * 64)
+        for t in range(9):
+            row = x[t * 64:(t + 1) * 64]
+            sel, ec, sumc, lg, ls = m.route(row, xs)
+            fsel, fec, fsumc, flg, _ = full.route(row, xs)
+            assert np.array_equal(lg, flg)
+            assert sel == topk_ref(lg.astype(np.int64), 2) and fsel == topk_ref(lg.astype(np.int64), 8)
+            assert ec[0] == 1 << 20 and fec[0] == 1 << 20
+            assert all(fec[i] >= fec[i + 1] for i in range(7))
+            assert np.array_equal(ec, fec[:2])
+            assert sumc == (int(ec.sum()) if norm else int(fec.sum()))
+            assert fsumc == int(fec.sum())
+
+
+def test_sigmoid_route_exact_identities():
+    """route_sigmoid (router.rs:29-79): the score of a zero logit at any scale is the table entry at index 32768 (
+    = -round(-16 * 65535 / 32)), round(2^20 sigma(-16 + 32 * 32768 / 65535)) by math.exp; the choice is the
+    top-k of score plus coded bias with ties to the lower index; the numerators are the chosen scores and sumc their
+    sum (norm_topk_prob) or 2^20."""
+    import math
+
+    m = O.RefMoe(0x53, 32, 16, 4, 24, True, 1, 0x55)
+    for sc in ((1 << 30, 30), (1234567890, 45), (1 << 31, 80)):
+        c = m.sigmoid_codes(np.zeros(4, np.int32), sc)
+        xg = -16.0 + 32.0 * 32768 / 65535
+        assert (c == round((1 << 20) / (1.0 + math.exp(-xg)))).all()
+    bias = m.bias()
+    x, xs, _ = O.rm_probe(0x58, 6 * 32)
+    for t in range(6):
+        sel, ec, sumc, lg, ls = m.route(x[t * 32:(t + 1) * 32], xs)
+        codes = m.sigmoid_codes(lg, ls)
+        assert sel == topk_ref((codes + bias).astype(np.int64), 4)
+        assert ec.tolist() == [int(codes[e]) for e in sel] and sumc == int(ec.sum())
+
+
 @pytest.mark.parametrize("sig", [0, 1])
 def test_a_layer_built_from_given_weights_equals_the_seeded_one(sig):
     """RefMoe.from_weights (kt_rm_empty / kt_rm_set_ql / kt_rm_set_bias_code) over the QuantLinears and coded bias of

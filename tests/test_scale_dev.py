@@ -245,5 +245,29 @@ def test_requant_by_reciprocal_equals_requant_dyn(sd):
         cases.append((den, den))
         cases.append((den, -den))
     for den, v in cases:
-        want = O.requant_dyn(v, 2**28, den) if abs(v) <= den else sd.sd_requant_dyn(v, den)
+        assert sd.sd_rq_apply(den, v) == O.requant_dyn(v, 2**28, den), (den, v)
+
+
+def test_requant_outside_the_fast_range_is_the_references(sd):
+    """rq_apply's cold path (|v| > den, den < 0, den >= 2^62) is layers.rs:33-39's i128 arithmetic, wrap to i32
+    included: quotients far past 2^40, negative denominators (truncating division and half = den / 2 toward zero)
+    and extreme v, against the oracle and against Python's integers."""
+    rng = np.random.default_rng(17)
+
+    def ref(v, den):  # layers.rs:33-39 with Python integers: truncating division, `as i32`
+        prod, half = v * 2**28, (abs(den) // 2) * (1 if den > 0 else -1)
+        t = lambda a, b: (abs(a) // abs(b)) * (1 if (a < 0) == (b < 0) else -1)
+        r = t(prod + half, den) if prod >= 0 else -t(-prod + half, den)
+        return (r + 2**31) % 2**32 - 2**31
+
+    cases = [(1, 2**63 - 1), (1, -(2**63)), (3, -(2**63)), (-1, 5), (-3, 7), (-3, -7), (-(2**63), 2**63 - 1),
+             (-(2**63) + 1, -(2**62)), (7, 2**40), (2**62, 2**63 - 1), (2**63 - 1, -(2**63)), (-2, 1), (-2, -1)]
+    for _ in range(4000):
+        den = rand_bits(rng, int(rng.integers(1, 64))) * (1 if rng.integers(0, 2) else -1)
+        v = rand_bits(rng, int(rng.integers(0, 64))) * (1 if rng.integers(0, 2) else -1)
+        v = max(min(v, 2**63 - 1), -(2**63))
+        cases.append((den, v))
+    for den, v in cases:
+        want = O.requant_dyn(v, 2**28, den)
+        assert want == ref(v, den), (den, v)
         assert sd.sd_rq_apply(den, v) == want, (den, v)

@@ -61,6 +61,57 @@ def test_noalloc_equals_the_workspace_entry_on_calls_in_a_row(torch_dev):
         del ql
 
 
+def test_noalloc_captured_in_a_graph_and_replayed(torch_dev):
+    """After one eager call on the GPU (the array's address is looked up there), the call captures into a HIP graph;
+    replays with new inputs equal the oracle, for a shape whose digit GEMM splits k across CTAs and for a decode row,
+    with eager work on the same scratch between the replays."""
+    torch = torch_dev
+    import tritify_amd as TA
+    from tritify_amd import backend as B
+    from tritify_amd.quant import qscale_record, read_qscale
+
+    rng = np.random.default_rng(77)
+    xs, wsc = (1509949440, 58), (1657624235, 49)
+    for rows, inp, out in ((512, 896, 896), (1, 896, 4864)):
+        say(f"case: quant_linear_noalloc graph rows={rows} in={inp} out={out}")
+        x, w, _ = _case(rng, rows, inp, out, False)
+        ql = TA.QuantLinear("g", w, out, inp, wsc, None)
+        xd = torch.from_numpy(x).cuda()
+        xr = qscale_record(*xs)
+        y = torch.zeros(rows * out, dtype=torch.int32, device="cuda")
+        osr = torch.zeros(4, dtype=torch.int64, device="cuda")
+        B.quant_linear_noalloc(xd, rows, inp, xr, ql.w_planes, ql.pw, out, ql.w_scale, None, None, y, osr)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            B.quant_linear_noalloc(xd, rows, inp, xr, ql.w_planes, ql.pw, out, ql.w_scale, None, None, y, osr,
+                                   stream=s)
+        torch.cuda.synchronize()
+        other = _case(rng, 3, 130, 65, False)
+        for rep in range(3):
+            x = rng.integers(-(2 ** (22 + 2 * rep)), 2 ** (22 + 2 * rep), size=rows * inp).astype(np.int32)
+            xd.copy_(torch.from_numpy(x))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            yo, so, xmax, ymax = O.quant_linear_forward(x, rows, inp, xs, w, out, wsc)
+            assert np.array_equal(y.cpu().numpy().reshape(rows, out), yo), (rows, rep)
+            r = read_qscale(osr)
+            assert (r["mant"], r["shift"]) == so and r["xmax"] == xmax and r["ymax"] == ymax
+            # an eager call of another shape between the replays overwrites the scratch
+            ox, ow, _ = other
+            q2 = TA.QuantLinear("o", ow, 65, 130, wsc, None)
+            y2 = torch.zeros(3 * 65, dtype=torch.int32, device="cuda")
+            B.quant_linear_noalloc(torch.from_numpy(ox).cuda(), 3, 130, xr, q2.w_planes, q2.pw, 65, q2.w_scale, None,
+                                   None, y2, torch.zeros(4, dtype=torch.int64, device="cuda"))
+            torch.cuda.synchronize()
+            assert np.array_equal(y2.cpu().numpy().reshape(3, 65), O.quant_linear_forward(ox, 3, 130, xs, ow, 65,
+                                                                                          wsc)[0])
+        del g, ql
+
+
 def test_noalloc_refuses_a_workspace_past_the_scratch(torch_dev):
     torch = torch_dev
     from tritify_amd import backend as B

@@ -151,7 +151,10 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_ref_merge_rows": (_I, [_I, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P]),
         "kt_hip_ref_attention_step": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
                                            _P, _P, _I64, C.c_int32, _P, _P, _P, _P, _P]),
-        "kt_hip_ref_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_attention_step_ws": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
+                                              _P, _P, _P, _I64, C.c_int32, _P, _P, _P, _P, _P, _SZ, _P]),
+        "kt_hip_ref_attention_step_workspace": (_SZ, [_I64, _I64, _I64]),
+        "kt_hip_ref_argmax": (_I, [_I, _P, _I64, _P, _P, _P, _P, _P, _I64, _P]),
         "kt_hip_gen_w12": (None, [_U64, _SZ, _P]),
         "kt_hip_gen_gauss": (None, [_U64, _I64, _I64, _SZ, _P]),
         "kt_hip_gen_uniform": (None, [_U64, _I64, _I64, _SZ, _P]),
@@ -765,21 +768,44 @@ def ref_attention_prefill(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, T: int, n
                                              _stream(stream)), "ref attention prefill")
 
 
+def ref_attention_step_workspace(max_seq: int, nh: int, hd: int) -> int:
+    """Bytes of the global workspace the attention step takes for caches past its LDS (kt_hip_ref_attention_step_ws)."""
+    return lib().kt_hip_ref_attention_step_workspace(max_seq, nh, hd)
+
+
+def ref_attention_step_fits_lds(max_seq: int, nh: int, hd: int) -> bool:
+    """Whether the attention step holds a cache of max_seq positions in LDS alone (no workspace needed)."""
+    return max_seq * (32 + 8) + nh * hd * 12 <= REF_ATTN_LDS
+
+
+REF_ATTN_LDS = 65536  # KT_REF_ATTN_LDS
+
+
 def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh: int, nkv: int, hd: int,
                        max_seq: int, kc_dev, vc_dev, kscale_dev, vscale_dev, cos_dev, sin_dev, inv_sqrt,
-                       exp_codes_dev, exp_lut: CodeLut, o_dev, os_dev, stream=None, dev: int = 0) -> None:
-    check(lib().kt_hip_ref_attention_step(dev, _ptr(q_dev), _ptr(qs_dev), _ptr(k_dev), _ptr(ks_dev), _ptr(v_dev),
-                                          _ptr(vs_dev), _ptr(pos_dev), nh, nkv, hd, max_seq, _ptr(kc_dev),
-                                          _ptr(vc_dev), _ptr(kscale_dev), _ptr(vscale_dev), _ptr(cos_dev),
-                                          _ptr(sin_dev), int(inv_sqrt[0]), int(inv_sqrt[1]), _ptr(exp_codes_dev),
-                                          C.byref(exp_lut), _ptr(o_dev), _ptr(os_dev), _stream(stream)),
+                       exp_codes_dev, exp_lut: CodeLut, o_dev, os_dev, stream=None, dev: int = 0, ws_dev=None) -> None:
+    """Attention::decode_step's core at position pos_dev[0]; ws_dev (ref_attention_step_workspace bytes) is needed
+    only when the cache does not fit the LDS path."""
+    ws_bytes = 0 if ws_dev is None else ws_dev.numel() * ws_dev.element_size()
+    check(lib().kt_hip_ref_attention_step_ws(dev, _ptr(q_dev), _ptr(qs_dev), _ptr(k_dev), _ptr(ks_dev),
+                                             _ptr(v_dev), _ptr(vs_dev), _ptr(pos_dev), nh, nkv, hd, max_seq,
+                                             _ptr(kc_dev), _ptr(vc_dev), _ptr(kscale_dev), _ptr(vscale_dev),
+                                             _ptr(cos_dev), _ptr(sin_dev), int(inv_sqrt[0]), int(inv_sqrt[1]),
+                                             _ptr(exp_codes_dev), C.byref(exp_lut), _ptr(o_dev), _ptr(os_dev),
+                                             _ptr(ws_dev), ws_bytes, _stream(stream)),
           "ref attention step")
 
 
 def ref_argmax(logits_dev, n: int, ls_dev, token_dev, record_dev=None, rscale_dev=None, step_dev=None, stream=None,
-               dev: int = 0) -> None:
+               dev: int = 0, record_rows: int = None) -> None:
+    """argmax_codes into token_dev; with a record, the codes and scale go to row step_dev[0] of record_dev /
+    rscale_dev while that row exists (record_rows, by default as many rows of n codes as record_dev holds and as
+    many 16-byte entries as rscale_dev holds), and the step advances; past the last row nothing is recorded."""
+    if record_dev is not None and record_rows is None:
+        record_rows = min(record_dev.numel() // n, rscale_dev.numel() * rscale_dev.element_size() // 16)
     check(lib().kt_hip_ref_argmax(dev, _ptr(logits_dev), n, _ptr(ls_dev), _ptr(token_dev), _ptr(record_dev),
-                                  _ptr(rscale_dev), _ptr(step_dev), _stream(stream)), "ref argmax")
+                                  _ptr(rscale_dev), _ptr(step_dev), int(record_rows or 0), _stream(stream)),
+          "ref argmax")
 
 
 REF_MOE_MAX_K = 32

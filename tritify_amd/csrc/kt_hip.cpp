@@ -291,7 +291,7 @@ int kt_hip_quant_linear_noalloc(int dev, const int32_t* x_dev, int64_t rows, int
     if (need == 0 || need > KT_QL_SCRATCH_BYTES) return (int)hipErrorInvalidValue;
     KT_TRY(hipSetDevice(dev));
     void* ws = nullptr;
-    KT_TRY(kt::ql_scratch(dev, &ws));
+    KT_TRY(kt::ql_scratch(dev, &ws, (hipStream_t)stream));
     return (int)kt::launch_quant_linear(x_dev, rows, in_f, xs_dev, w_planes_dev, pw, out_f, w_mant, w_shift, bias_dev,
                                         b_mant, b_shift, flush_of(3, pw), ws, y_dev, os_dev, (hipStream_t)stream);
 }

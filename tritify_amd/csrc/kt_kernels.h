@@ -104,7 +104,7 @@ hipError_t launch_ref_conv2d(const int32_t* x, const ConvGeom& g, const kt_hip_q
                              hipStream_t s);
 // The device address of device `dev`'s QuantLinear scratch array (KT_QL_SCRATCH_BYTES), looked up once per device;
 // `dev` must be the current device.
-hipError_t ql_scratch(int dev, void** ptr);
+hipError_t ql_scratch(int dev, void** ptr, hipStream_t s);
 hipError_t launch_w12_linear_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int N,
                                   const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s);
 hipError_t launch_w12_swiglu_norm(const int32_t* r, int M, int d, const int8_t* lo, const uint8_t* nib, int F,

@@ -533,7 +533,9 @@ size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_Q
 // it uses the address ql_scratch looked up for the current device.
 static __device__ __align__(256) uint8_t scratch[KT_QL_SCRATCH_BYTES];
 
-hipError_t ql_scratch(int dev, void** ptr) {
+// The lookup is a runtime call outside any stream; a first call whose stream is being captured into a graph is
+// refused (hipErrorStreamCaptureUnsupported) rather than making it there: one eager call per device comes first.
+hipError_t ql_scratch(int dev, void** ptr, hipStream_t s) {
     static std::mutex mu;
     static std::vector<void*> addr;  // per device, filled on the device's first call
     *ptr = nullptr;
@@ -541,6 +543,10 @@ hipError_t ql_scratch(int dev, void** ptr) {
     std::lock_guard<std::mutex> g(mu);
     if ((size_t)dev >= addr.size()) addr.resize((size_t)dev + 1, nullptr);
     if (!addr[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        const hipError_t ce = hipStreamIsCapturing(s, &cs);
+        if (ce != hipSuccess) return ce;
+        if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;

@@ -46,7 +46,6 @@ struct RdAttn {
     const kt_hip_qscale *qs, *ks, *vs;
     const int32_t* pos;
     int nh, nkv, hd, max_seq;
-    int hb;                            // heads whose scores LDS holds at once
     int32_t *kc, *vc;                  // [max_seq][nkv * hd]
     kt_hip_sscale *kscale, *vscale;    // [max_seq]
     const kt_hip_sscale *cos, *sin;    // [max_seq][hd / 2]
@@ -56,6 +55,8 @@ struct RdAttn {
     kt_hip_codelut exp;
     int32_t* o;
     kt_hip_qscale* os;
+    unsigned char* ws;                 // global-memory per-step arrays for steps past the LDS path, or null
+    int hb;                            // LDS path: heads whose scores LDS holds at once
 };
 
 // Attention::forward_int over a sequence (prefill): the inputs, the tables and the workspace parts.
@@ -552,27 +553,36 @@ __global__ __launch_bounds__(RD_THREADS) void rd_gelu_kernel(const int32_t* __re
 //  3. per head: score_j = f_j.apply(q . k_j), ec_j = exp_code(score_j - max score) at s_ref (0 below the table),
 //     sumc = sum ec_j, out_d = sum_j ec_j * vf_j.apply(v_jd), scale_h = v_ref / sumc;
 //  4. the heads brought to the largest scale_h and requantized: o and its record.
-// LDS: 40 bytes per position up to max_seq, 12 per q value, 8 per thread.
-__global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    __shared__ int64_t red[RD_WAVES];
-    __shared__ ScIdx redsc[RD_THREADS];
-    __shared__ Sc par[4];  // v_ref, s_ref, lut factor, common
-    __shared__ Sc hsc[64];
+// The per-step arrays: score and v factors (32 B per cached position) and hb heads' scores (8 B per position each).
+// LDS path (GWS = false): rows of max_seq positions in LDS, the head outputs and the rotated q (12 B per q value)
+// after them, hb heads at a time. Workspace path (GWS = true, caches longer than LDS holds): rows of this step's
+// pos + 1 positions in the caller's global workspace a.ws, every head at once; LDS keeps the head outputs and q.
+struct RdAttnShared {
+    int64_t red[RD_WAVES];
+    ScIdx redsc[RD_THREADS];
+    Sc par[4];  // v_ref, s_ref, lut factor, common
+    Sc hsc[64];
+    Sc inv2[2];
+    int64_t hsum[KT_REF_MAX_HEADS];
+};
+
+template <bool GWS>
+__device__ __forceinline__ void rd_attention_core(const RdAttn& a, unsigned char* lds, RdAttnShared& sh_,
+                                                  int pos, int hb) {
+    int64_t* red = sh_.red;
+    ScIdx* redsc = sh_.redsc;
+    Sc* par = sh_.par;
+    Sc* hsc = sh_.hsc;
     const int tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv, group = nh / nkv;
     const int kstride = nkv * hd, qstride = nh * hd;
-    const int pos = *a.pos;
-    if (pos < 0 || pos >= a.max_seq) {  // outside the tables: zeros (the reference asserts here)
-        for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = 0;
-        if (tid == 0) put_rec(a.os, Sc{0, 0});
-        return;
-    }
-    const int steps = pos + 1;
-    Sc* F = reinterpret_cast<Sc*>(lds);  // score factors, per step
-    Sc* VF = F + a.max_seq;              // v factors, per step
-    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);   // scores, then exp codes: [hb][max_seq]
-    int64_t* HO = S + (size_t)a.hb * a.max_seq;                  // head outputs, qstride
-    int32_t* QD = reinterpret_cast<int32_t*>(HO + qstride);     // rotated q, qstride
+    const int steps = pos + 1, rows = GWS ? steps : a.max_seq;  // rows: the per-step arrays' length
+    unsigned char* arr = GWS ? a.ws : lds;
+    Sc* F = reinterpret_cast<Sc*>(arr);  // score factors, per step
+    Sc* VF = F + rows;                   // v factors, per step
+    int64_t* S = reinterpret_cast<int64_t*>(VF + rows);   // scores, then exp codes: [hb][rows]
+    // head outputs (qstride) and the rotated q (qstride) always in LDS: after the arrays, or from its start
+    int64_t* HO = GWS ? reinterpret_cast<int64_t*>(lds) : S + (size_t)hb * rows;
+    int32_t* QD = reinterpret_cast<int32_t*>(HO + qstride);
 
     // 1. RoPE and the cache append
     auto rot = [&](const int32_t* src, int32_t* dst, int heads) {
@@ -613,7 +623,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     __syncthreads();
     const Sc v_ref = par[0], s_ref = par[1], lm = par[2];
     if (v_ref.mant != 0 || s_ref.mant != 0) {
-        __shared__ Sc inv2[2];
+        Sc* inv2 = sh_.inv2;
         if (tid == 0) inv2[0] = v_ref.mant ? sc_recip(v_ref) : Sc{0, 0};  // the two reciprocals in two waves
         if (tid == 64) inv2[1] = s_ref.mant ? sc_recip(s_ref) : Sc{0, 0};
         __syncthreads();
@@ -630,9 +640,9 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     //    integer softmax by one wave per head, P.V by one thread per (head, dim). Sums wrap as i64 (any order gives
     //    the reference's integers).
     const int lane = tid & 63, wave = tid >> 6;
-    __shared__ int64_t hsum[KT_REF_MAX_HEADS];
-    for (int h0 = 0; h0 < nh; h0 += a.hb) {
-        const int hn = nh - h0 < a.hb ? nh - h0 : a.hb;
+    int64_t* hsum = sh_.hsum;
+    for (int h0 = 0; h0 < nh; h0 += hb) {
+        const int hn = nh - h0 < hb ? nh - h0 : hb;
         if (s_ref.mant == 0) {  // every head skipped (the reference's `continue`)
             for (int i = tid; i < hn * hd; i += RD_THREADS) HO[h0 * hd + i] = 0;
             if (tid < hn) hsc[h0 + tid] = Sc{0, 0};
@@ -660,7 +670,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
                         dot = wadd(dot, (int64_t)qq.z * kk[u].z + (int64_t)qq.w * kk[u].w);
                     }
                 }
-                S[(size_t)h * a.max_seq + j] = sc_apply(F[j], dot);
+                S[(size_t)h * rows + j] = sc_apply(F[j], dot);
             }
         } else {
         // RD_SU items per wave at a time, every cached k row of them loaded before the first product (an item past
@@ -693,13 +703,13 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
                 for (int u = 1; u < RD_SU; u++) d = lane == u ? dot[u] : d;
                 const int it = it0 + lane * RD_WAVES;
                 const int h = it / steps, j = it - h * steps;
-                if (it < items) S[(size_t)h * a.max_seq + j] = sc_apply(F[j], d);
+                if (it < items) S[(size_t)h * rows + j] = sc_apply(F[j], d);
             }
         }
         }
         __syncthreads();
         for (int h = wave; h < hn; h += RD_WAVES) {
-            int64_t* sh = S + (size_t)h * a.max_seq;
+            int64_t* sh = S + (size_t)h * rows;
             int64_t m = INT64_MIN;
             for (int j = lane; j < steps; j += 64) m = sh[j] > m ? sh[j] : m;
 #pragma unroll
@@ -753,7 +763,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
                             const int64_t sv = sc_apply32(VF[j], vv[u]);
 #pragma unroll
                             for (int g = 0; g < RD_PV_GROUP; g++)
-                                if (hs + g < he) acc[g] = wadd(acc[g], wmul(S[(size_t)(hs + g - h0) * a.max_seq + j], sv));
+                                if (hs + g < he) acc[g] = wadd(acc[g], wmul(S[(size_t)(hs + g - h0) * rows + j], sv));
                         }
                     }
 #pragma unroll
@@ -771,7 +781,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
                 const int h = it / hd, dd = it - h * hd, kv = (h0 + h) / group;
                 int64_t acc = 0;
                 if (hsum[h] > 0) {
-                    const int64_t* sh = S + (size_t)h * a.max_seq;
+                    const int64_t* sh = S + (size_t)h * rows;
                     const int32_t* vcol = a.vc + kv * hd + dd;
                     // RD_PU cached v values loaded before their products (a step past the end re-reads the last one
                     // and is dropped)
@@ -810,6 +820,25 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, HO[i]);
     if (tid == 0)
         put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
+}
+
+// GWS = false: every array in LDS, sized for max_seq positions with hb >= 1 heads' scores at a time (a.lds_bytes);
+// GWS = true (a cache longer than that LDS holds): the per-step arrays in a.ws, every head's scores at once.
+template <bool GWS>
+__global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ RdAttnShared sh_;
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= a.max_seq) {  // outside the tables: zeros (the reference asserts here)
+        for (int i = threadIdx.x; i < a.nh * a.hd; i += RD_THREADS) a.o[i] = 0;
+        if (threadIdx.x == 0) put_rec(a.os, Sc{0, 0});
+        return;
+    }
+    if constexpr (GWS) {
+        rd_attention_core<true>(a, lds, sh_, pos, a.nh);
+    } else {
+        rd_attention_core<false>(a, lds, sh_, pos, a.hb);
+    }
 }
 
 // The same ops over whole-sequence tensors on many CTAs (the batched forward's T-row tensors): one CTA forms the
@@ -1063,17 +1092,19 @@ __global__ __launch_bounds__(256) void rp_out_kernel(RdPrefill a) {
 
 // argmax_codes (generate.rs:48-56): *token = the first index of the largest of n codes. With record non-null the
 // codes go to record + step * n and the scale to rscale[step], and *step advances (the per-step logits the
-// generation hash covers).
+// generation hash covers) -- only while step lies in [0, cap), the rows record and rscale hold; any other step
+// records nothing and stays where it is (the token is still chosen).
 __global__ __launch_bounds__(RD_THREADS) void rd_argmax_kernel(const int32_t* __restrict__ logits, int n,
                                                                const kt_hip_qscale* __restrict__ ls,
                                                                int32_t* __restrict__ token, int32_t* record,
-                                                               kt_hip_sscale* rscale, int32_t* step) {
+                                                               kt_hip_sscale* rscale, int32_t* step, int cap) {
     __shared__ int64_t red[RD_WAVES];
     // key: the value in the high word, the inverted index in the low word (the lower index wins a tie)
     auto key = [](int32_t v, int i) { return (int64_t)v * 4294967296LL + (int64_t)(0x7FFFFFFF - i); };
     int64_t best = INT64_MIN;
     const int s = record ? *step : 0;
-    int32_t* rec = record ? record + (size_t)s * n : nullptr;
+    const bool keep = record && s >= 0 && s < cap;
+    int32_t* rec = keep ? record + (size_t)s * n : nullptr;
     // one pass over the codes, 16-byte loads (and stores into the record) where n and the addresses allow, several in
     // flight per thread
     const bool vec = n % 4 == 0 && ((uintptr_t)logits & 15) == 0 && (!rec || ((uintptr_t)rec & 15) == 0);
@@ -1106,7 +1137,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_argmax_kernel(const int32_t* __
     }
     best = block_max_i64(best, red);  // every thread has read *step past here
     if (threadIdx.x == 0) {
-        if (record) {
+        if (keep) {
             rscale[s] = kt_hip_sscale{ls->mant, ls->shift, 1};
             *step = s + 1;
         }
@@ -1119,10 +1150,24 @@ __global__ __launch_bounds__(RD_THREADS) void rd_argmax_kernel(const int32_t* __
 size_t rd_attention_lds(int max_seq, int nh, int hd, int hb) {
     return (size_t)max_seq * (2 * sizeof(Sc) + 8 * (size_t)hb) + (size_t)nh * hd * (8 + 4);
 }
-static int rd_attention_hb(int max_seq, int nh, int hd) {
+// The dynamic LDS the attention step may take on the current device: KT_REF_ATTN_LDS, less what the device's
+// per-block limit leaves after the kernel's static LDS.
+static size_t rd_attention_budget(bool gws) {
+    int dev = 0, mx = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return 0;
+    hipFuncAttributes fa{};
+    const void* fn = gws ? reinterpret_cast<const void*>(&rd_attention_step_kernel<true>)
+                         : reinterpret_cast<const void*>(&rd_attention_step_kernel<false>);
+    if (hipFuncGetAttributes(&fa, fn) != hipSuccess || fa.sharedSizeBytes >= (size_t)mx) return 0;
+    const size_t room = (size_t)mx - fa.sharedSizeBytes;
+    return room < KT_REF_ATTN_LDS ? room : KT_REF_ATTN_LDS;
+}
+static int rd_attention_hb(int max_seq, int nh, int hd, size_t budget) {
     const size_t base = rd_attention_lds(max_seq, nh, hd, 0);
-    if (base >= KT_REF_ATTN_LDS) return 0;
-    const size_t hb = (KT_REF_ATTN_LDS - base) / (8 * (size_t)max_seq);
+    if (base >= budget) return 0;
+    const size_t hb = (budget - base) / (8 * (size_t)max_seq);
     return (int)(hb < (size_t)nh ? hb : (size_t)nh);
 }
 
@@ -1162,11 +1207,21 @@ hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, 
     rd_gelu_kernel<<<(unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g)), RD_THREADS, 0, s>>>(x, xs, n, codes, *lut, y, ys);
     return hipGetLastError();
 }
+// The LDS kernel while one head's scores at max_seq positions fit the budget (dynamic LDS for as many heads as fit,
+// at most all); past that the workspace kernel, a.ws holding kt_hip_ref_attention_step_workspace bytes (the entry
+// point checks).
 hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
     RdAttn a = a_in;
-    a.hb = rd_attention_hb(a.max_seq, a.nh, a.hd);
-    if (a.hb < 1) return hipErrorInvalidValue;
-    rd_attention_step_kernel<<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
+    const size_t budget = rd_attention_budget(false);
+    a.hb = rd_attention_hb(a.max_seq, a.nh, a.hd, budget);
+    if (a.hb >= 1) {
+        rd_attention_step_kernel<false><<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
+        return hipGetLastError();
+    }
+    const size_t lds = (size_t)a.nh * a.hd * (8 + 4);  // the head outputs and the rotated q
+    if (!a.ws || lds > rd_attention_budget(true)) return hipErrorInvalidValue;
+    a.hb = a.nh;
+    rd_attention_step_kernel<true><<<1, RD_THREADS, lds, s>>>(a);
     return hipGetLastError();
 }
 size_t rd_seq_workspace(int64_t rows) { return (sizeof(RdSeqWs) + (size_t)(rows > 1 ? rows - 1 : 0) * sizeof(Sc) + 255) / 256 * 256; }
@@ -1219,8 +1274,8 @@ hipError_t launch_rd_attention_prefill(RdPrefill a, void* ws, hipStream_t s) {
 }
 
 hipError_t launch_rd_argmax(const int32_t* logits, int n, const kt_hip_qscale* ls, int32_t* token, int32_t* record,
-                            kt_hip_sscale* rscale, int32_t* step, hipStream_t s) {
-    rd_argmax_kernel<<<1, RD_THREADS, 0, s>>>(logits, n, ls, token, record, rscale, step);
+                            kt_hip_sscale* rscale, int32_t* step, int cap, hipStream_t s) {
+    rd_argmax_kernel<<<1, RD_THREADS, 0, s>>>(logits, n, ls, token, record, rscale, step, cap);
     return hipGetLastError();
 }
 
@@ -1423,6 +1478,41 @@ extern "C" int kt_hip_ref_conv2d(int dev, const int32_t* x_dev, const kt_hip_qsc
                                       b_shift, kt_hip_flush_k(3, pw), ws_dev, y_dev, os_dev, (hipStream_t)stream);
 }
 
+extern "C" size_t kt_hip_ref_attention_step_workspace(int64_t max_seq, int64_t nh, int64_t hd) {
+    if (nh < 1 || nh > KT_REF_MAX_HEADS || hd < 2 || hd > 1024 || max_seq < 1 || max_seq > KT_REF_ATTN_MAX_SEQ)
+        return 0;
+    return (size_t)max_seq * (2 * sizeof(kt::Sc) + 8 * (size_t)nh);
+}
+
+extern "C" int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
+                                            const int32_t* k_dev, const kt_hip_qscale* ks_dev, const int32_t* v_dev,
+                                            const kt_hip_qscale* vs_dev, const int32_t* pos_dev, int64_t nh,
+                                            int64_t nkv, int64_t hd, int64_t max_seq, int32_t* kc_dev,
+                                            int32_t* vc_dev, kt_hip_sscale* kscale_dev, kt_hip_sscale* vscale_dev,
+                                            const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev,
+                                            int64_t isq_mant, int32_t isq_shift, const int64_t* exp_codes_dev,
+                                            const kt_hip_codelut* exp_lut, int32_t* o_dev, kt_hip_qscale* os_dev,
+                                            void* ws_dev, size_t ws_bytes, void* stream) {
+    if (!q_dev || !qs_dev || !k_dev || !ks_dev || !v_dev || !vs_dev || !pos_dev || !kc_dev || !vc_dev ||
+        !kscale_dev || !vscale_dev || !cos_dev || !sin_dev || !exp_codes_dev || !exp_lut || !o_dev || !os_dev)
+        return (int)hipErrorInvalidValue;
+    if (nh < 1 || nkv < 1 || nh % nkv || nh > KT_REF_MAX_HEADS || hd < 2 || (hd & 1) || hd > 1024 || max_seq < 1 ||
+        max_seq > KT_REF_ATTN_MAX_SEQ || exp_lut->n < 1 || isq_mant < 0)
+        return (int)hipErrorInvalidValue;
+    const bool fits = kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd, 1) <= KT_REF_ATTN_LDS;
+    if (!fits && (!ws_dev || (reinterpret_cast<uintptr_t>(ws_dev) & 15) ||
+                  ws_bytes < kt_hip_ref_attention_step_workspace(max_seq, nh, hd)))
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    kt::RdAttn a{};
+    a.q = q_dev, a.k = k_dev, a.v = v_dev, a.qs = qs_dev, a.ks = ks_dev, a.vs = vs_dev, a.pos = pos_dev;
+    a.nh = (int)nh, a.nkv = (int)nkv, a.hd = (int)hd, a.max_seq = (int)max_seq;
+    a.kc = kc_dev, a.vc = vc_dev, a.kscale = kscale_dev, a.vscale = vscale_dev, a.cos = cos_dev, a.sin = sin_dev;
+    a.isq_mant = isq_mant, a.isq_shift = isq_shift, a.exp_codes = exp_codes_dev, a.exp = *exp_lut;
+    a.o = o_dev, a.os = os_dev, a.ws = (unsigned char*)ws_dev;
+    return (int)kt::launch_rd_attention_step(a, (hipStream_t)stream);
+}
+
 extern "C" int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
                                          const int32_t* k_dev, const kt_hip_qscale* ks_dev, const int32_t* v_dev,
                                          const kt_hip_qscale* vs_dev, const int32_t* pos_dev, int64_t nh,
@@ -1432,31 +1522,20 @@ extern "C" int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt
                                          int64_t isq_mant, int32_t isq_shift, const int64_t* exp_codes_dev,
                                          const kt_hip_codelut* exp_lut, int32_t* o_dev, kt_hip_qscale* os_dev,
                                          void* stream) {
-    if (!q_dev || !qs_dev || !k_dev || !ks_dev || !v_dev || !vs_dev || !pos_dev || !kc_dev || !vc_dev ||
-        !kscale_dev || !vscale_dev || !cos_dev || !sin_dev || !exp_codes_dev || !exp_lut || !o_dev || !os_dev)
-        return (int)hipErrorInvalidValue;
-    if (nh < 1 || nkv < 1 || nh % nkv || nh > KT_REF_MAX_HEADS || hd < 2 || (hd & 1) || hd > 1024 || max_seq < 1 ||
-        exp_lut->n < 1 || isq_mant < 0 || kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd, 1) > KT_REF_ATTN_LDS)
-        return (int)hipErrorInvalidValue;
-    RD_TRY(hipSetDevice(dev));
-    kt::RdAttn a{};
-    a.q = q_dev, a.k = k_dev, a.v = v_dev, a.qs = qs_dev, a.ks = ks_dev, a.vs = vs_dev, a.pos = pos_dev;
-    a.nh = (int)nh, a.nkv = (int)nkv, a.hd = (int)hd, a.max_seq = (int)max_seq;
-    a.kc = kc_dev, a.vc = vc_dev, a.kscale = kscale_dev, a.vscale = vscale_dev, a.cos = cos_dev, a.sin = sin_dev;
-    a.isq_mant = isq_mant, a.isq_shift = isq_shift, a.exp_codes = exp_codes_dev, a.exp = *exp_lut;
-    a.o = o_dev, a.os = os_dev;
-    return (int)kt::launch_rd_attention_step(a, (hipStream_t)stream);
+    return kt_hip_ref_attention_step_ws(dev, q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh, nkv, hd,
+                                        max_seq, kc_dev, vc_dev, kscale_dev, vscale_dev, cos_dev, sin_dev, isq_mant,
+                                        isq_shift, exp_codes_dev, exp_lut, o_dev, os_dev, nullptr, 0, stream);
 }
 
 extern "C" int kt_hip_ref_argmax(int dev, const int32_t* logits_dev, int64_t n, const kt_hip_qscale* ls_dev,
                                  int32_t* token_dev, int32_t* record_dev, kt_hip_sscale* rscale_dev,
-                                 int32_t* step_dev, void* stream) {
+                                 int32_t* step_dev, int64_t record_rows, void* stream) {
     if (!logits_dev || !ls_dev || !token_dev || n < 1 || n > INT32_MAX ||
-        (record_dev && (!rscale_dev || !step_dev)))
+        (record_dev && (!rscale_dev || !step_dev || record_rows < 1 || record_rows > INT32_MAX)))
         return (int)hipErrorInvalidValue;
     RD_TRY(hipSetDevice(dev));
     return (int)kt::launch_rd_argmax(logits_dev, (int)n, ls_dev, token_dev, record_dev, rscale_dev, step_dev,
-                                     (hipStream_t)stream);
+                                     record_dev ? (int)record_rows : 0, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -249,7 +249,8 @@ KT_SC_FN int32_t requant_dyn_dev(int64_t v, int64_t den) {
 // requant_dyn(v, 2^28, den) for many v over one den, without a division per value: q = floor((|v| 2^28 + den / 2)
 // / den) estimated as |v| * (2^28 / den) + 1/2 in double precision (relative error below 2^-51 on a value at most
 // 2^28, so within one of q) and corrected by the exact remainder. For den < 2^62 and |v| <= den that remainder lies
-// in (-2^62, 2^63), so its 64-bit wrapping value is exact. Other inputs take requant_dyn_dev.
+// in (-2^62, 2^63), so its 64-bit wrapping value is exact. Every other input (|v| > den, den <= 0, den >= 2^62)
+// takes requant_dyn_cold, the reference's own i128 arithmetic.
 struct RqDen {
     int64_t den;
     uint64_t half;
@@ -258,7 +259,20 @@ struct RqDen {
 KT_SC_FN RqDen rq_den(int64_t den) {
     return RqDen{den, (uint64_t)(den / 2), den > 0 ? 268435456.0 / (double)den : 0.0};
 }
-KT_SC_COLD int32_t requant_dyn_cold(int64_t v, int64_t den) { return requant_dyn_dev(v, den); }
+// requant_dyn(v, 2^28, den) for any v and den != 0 exactly as layers.rs:33-39 computes it: the i128 product, half =
+// den / 2 truncated, the truncating i128 quotient (signs from the numerator and den), the result wrapped to i32. The
+// reference's division by a zero den panics; 0 is returned for it.
+KT_SC_COLD int32_t requant_dyn_cold(int64_t v, int64_t den) {
+    if (den == 0) return 0;
+    const i128 prod = (i128)v * ((i128)1 << 28), half = (i128)(den / 2);
+    const i128 num = prod >= 0 ? prod + half : -prod + half;  // |num| < 2^92
+    const u128 un = num < 0 ? (u128)(-num) : (u128)num;
+    const u128 ud = den < 0 ? (u128)(0 - (uint64_t)den) : (u128)(uint64_t)den;
+    const u128 uq = udiv128(un, ud);
+    const i128 q = ((num < 0) != (den < 0)) ? -(i128)uq : (i128)uq;  // num / den, truncated
+    const i128 r = prod >= 0 ? q : -q;
+    return (int32_t)(uint32_t)(uint64_t)(u128)r;
+}
 KT_SC_FN int32_t rq_apply(const RqDen& r, int64_t v) {
     const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
     if (r.den <= 0 || r.den >= ((int64_t)1 << 62) || a > (uint64_t)r.den) return requant_dyn_cold(v, r.den);

@@ -507,6 +507,11 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
 // A fragment of row tile w % 4, read once more by each wave. Ends with every DMA landed, sRow[256] written and a barrier: the ring is free.
 // ------------------------------------------------------------------------------------------------------------------
 constexpr int KT_DMA_STAGE = 28672, KT_DMA_LO = 16384, KT_DMA_NIB = 24576;
+// BAL (the balanced two-plane weights, W12B): the hi plane is a full int8 fragment like lo, 1 KB per (column block,
+// k32 half), at KT_DMA_HI; a stage is 32 KB.
+constexpr int KT_DMA_STAGE_BAL = 32768, KT_DMA_HI = 24576;
+template <bool BAL>
+constexpr int dma_stage_bytes() { return BAL ? KT_DMA_STAGE_BAL : KT_DMA_STAGE; }
 #ifndef KT_DMA_NS
 #define KT_DMA_NS 4  // ring stages of the DMA-fed kernels
 #endif
@@ -527,11 +532,14 @@ __device__ __forceinline__ uint32_t dma_a_chunk(int lane) { return 16u * ((lane 
 
 // va0 / va1: the byte offsets in rA of this lane's two A pieces at k = 0 (rows dma_a_row(w, lane, 0 / 1), chunk
 // dma_a_chunk(lane)); an offset past the descriptor reads zeros (rows past the tile's rows).
-template <int NS>
+// BAL: rN is the hi plane of the balanced split (v = lo + 256 hi, no offset): each wave moves its hi fragment with one
+// 16-byte DMA like lo (4 DMAs per k-tile, not 5), the MFMA takes it as read, and there are no row sums (sRow is 0).
+template <int NS, bool BAL = false>
 __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA, const __amdgpu_buffer_rsrc_t rL,
                                                  const __amdgpu_buffer_rsrc_t rN, uint32_t va0, uint32_t va1, int kp,
                                                  int8_t* ring, v16i (&acc0)[4][1], v16i (&acc1)[4][1], int* sRow) {
-    static_assert(NS >= 2 && 5 * (NS - 2) <= 63, "vmcnt holds the DMAs of NS - 2 later tiles");
+    constexpr int ND = BAL ? 4 : 5, STAGE = dma_stage_bytes<BAL>();  // DMAs per wave and k-tile
+    static_assert(NS >= 2 && ND * (NS - 2) <= 63, "vmcnt holds the DMAs of NS - 2 later tiles");
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = w & 3, rw0 = 128 * (w >> 2);
@@ -540,43 +548,51 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
     const int cbw = w >> 1, ksw = w & 1;  // the fragment this wave moves
     const uint32_t vl = (uint32_t)(cbw * KB) * 1024u + 16 * lane, vn = (uint32_t)(cbw * KB) * 512u + 4 * lane;
 
-    // 5 DMAs per wave and k-tile on every wave, so one vmcnt target serves all (a wave-dependent count would put
+    // ND DMAs per wave and k-tile on every wave, so one vmcnt target serves all (a wave-dependent count would put
     // branches in the loop, which keep the scheduler from moving MFMAs across the barrier)
     auto issue = [&](int st, int kt) {
         const uint32_t kl = (uint32_t)(kt < nk ? kt : nk - 1);
-        int8_t* s = ring + st * KT_DMA_STAGE;
+        int8_t* s = ring + st * STAGE;
         dma16(rA, s + 2048 * w, va0, kl * 64);
         dma16(rA, s + 2048 * w + 1024, va1, kl * 64);
         dma16(rL, s + KT_DMA_LO + 1024 * w, vl, (2 * kl + ksw) * 1024u);
-        dma4(rN, s + KT_DMA_NIB + 512 * w, vn, (2 * kl + ksw) * 512u);
-        dma4(rN, s + KT_DMA_NIB + 512 * w + 256, vn + 256, (2 * kl + ksw) * 512u);
+        if constexpr (BAL) {
+            dma16(rN, s + KT_DMA_HI + 1024 * w, vl, (2 * kl + ksw) * 1024u);
+        } else {
+            dma4(rN, s + KT_DMA_NIB + 512 * w, vn, (2 * kl + ksw) * 512u);
+            dma4(rN, s + KT_DMA_NIB + 512 * w + 256, vn + 256, (2 * kl + ksw) * 512u);
+        }
     };
     // the wave's DMAs of a tile have landed once at most those of the NS - 2 later tiles are outstanding
     auto wait_tile = [&]() {
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(5 * (NS - 2)) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(ND * (NS - 2)) : "memory");
     };
 
-    struct Frag {  // one k32 half of a k-tile: the wave's 4 A fragments, its row-sum fragment and its B fragment
-        v4i a[4], ar, b0;
+    struct Frag {  // one k32 half of a k-tile: the wave's 4 A fragments, its row-sum fragment and its B fragments
+        v4i a[4], ar, b0, b1;
         v2i bn;
     };
     auto load = [&](const int8_t* s, int ks, Frag& f) {
 #pragma unroll
         for (int i = 0; i < 4; i++) f.a[i] = lds_read16(s, lds_off<4>(rw0 + 32 * i + (lane & 31), 2 * ks + half));
-        // row tile wn once more: a wave-uniform select among f.a would compile to branches
-        f.ar = lds_read16(s, lds_off<4>(rw0 + 32 * wn + (lane & 31), 2 * ks + half));
         f.b0 = lds_read16(s + KT_DMA_LO + 1024 * (2 * wn + ks), 16 * lane);
-        f.bn = *reinterpret_cast<const v2i*>(s + KT_DMA_NIB + 512 * (2 * wn + ks) + 8 * lane);
+        if constexpr (BAL) {
+            f.b1 = lds_read16(s + KT_DMA_HI + 1024 * (2 * wn + ks), 16 * lane);
+        } else {
+            // row tile wn once more: a wave-uniform select among f.a would compile to branches
+            f.ar = lds_read16(s, lds_off<4>(rw0 + 32 * wn + (lane & 31), 2 * ks + half));
+            f.bn = *reinterpret_cast<const v2i*>(s + KT_DMA_NIB + 512 * (2 * wn + ks) + 8 * lane);
+        }
     };
     int rsum = 0;
     auto mma = [&](const Frag& f) {
-        const v4i b1 = unpack_hi(f.bn);
+        const v4i b1 = BAL ? f.b1 : unpack_hi(f.bn);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             acc0[i][0] = mfma32(f.a[i], f.b0, acc0[i][0]);
             acc1[i][0] = mfma32(f.a[i], b1, acc1[i][0]);
         }
-        rsum += sum4(f.ar);
+        if constexpr (!BAL) rsum += sum4(f.ar);
     };
 
 #pragma unroll
@@ -597,7 +613,7 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
         // reads of tile kt are done (lgkmcnt), so after the barrier its stage takes tile kt + NS
         wait_tile();
         issue(kt % NS, kt + NS);
-        const int8_t* sn = ring + ((kt + 1) % NS) * KT_DMA_STAGE;
+        const int8_t* sn = ring + ((kt + 1) % NS) * STAGE;
         load(sn, 0, f0);
         __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs they hide under
         mma(f1);
@@ -607,7 +623,7 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
     // the re-reads past the end still target the ring
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     rsum += __shfl_xor(rsum, 32);
-    if (lane < 32) sRow[rw0 + 32 * wn + lane] = rsum;
+    if (lane < 32) sRow[rw0 + 32 * wn + lane] = BAL ? 0 : rsum;  // BAL: no offset term to correct
     __syncthreads();
 }
 

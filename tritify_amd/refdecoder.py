@@ -112,6 +112,14 @@ class RefDecoder:
         self._rec_qkv, self._rec_gu = qkv_rec, gu_rec
         self.token = z(1)
         self.pos = z(1)
+        # caches past the attention step's LDS keep its per-step arrays in one workspace the layers share (their
+        # steps run in order on one stream)
+        self.attn_ws = None
+        if not B.ref_attention_step_fits_lds(self.max_seq, self.nh, self.hd):
+            n = B.ref_attention_step_workspace(self.max_seq, self.nh, self.hd)
+            if n == 0:
+                raise ValueError(f"max_seq {self.max_seq} beyond the attention step's limit")
+            self.attn_ws = torch.empty((n + 15) // 16 * 16, dtype=torch.uint8, device=self.device)
         self.new_cache()
 
     def new_cache(self) -> None:
@@ -160,7 +168,7 @@ class RefDecoder:
             B.ref_attention_step(b["q"], r["q"], b["k"], r["k"], b["v"], r["v"], self.pos, self.nh, self.nkv,
                                  self.hd, self.max_seq, self.kc[i], self.vc[i], self.ks[i], self.vs[i], self.cos,
                                  self.sin, self.inv_sqrt, self.exp_codes, self.exp_lut, b["cat"], r["cat"], stream,
-                                 dv)
+                                 dv, ws_dev=self.attn_ws)
             self._ql(blk["wo"], "cat", "a", stream)
             add_norm("a", blk["post_norm"])
             if self.grouped:
@@ -192,7 +200,7 @@ class RefDecoder:
             g.capture_begin()
             self.step_launches(stream=s)
             B.ref_argmax(self.buf["logits"], self.vocab, self.rec["logits"], self.token, self.record, self.rscale,
-                         self.pos, s, self.dev)
+                         self.pos, s, self.dev, record_rows=self.max_seq)
             g.capture_end()
         torch.cuda.current_stream(self.device).wait_stream(s)
         return g

@@ -306,3 +306,41 @@ def decoder_prompt(seed: int, n: int, vocab: int) -> np.ndarray:
     from . import backend as B
 
     return B.gen_uniform_fast(seed, 0, vocab - 1, n)
+
+
+# The reference decoder at its own semantics (tritify_amd/refdecoder.py) at the Qwen2.5-0.5B shape: 12-trit weight
+# codes, config 3's run (a 512-token prompt fed through decode_step, generate.rs:82-93, then 128 greedy steps:
+# 640 positions).
+WLEVELS = 265720
+REF_QWEN = dict(dim=896, layers=24, nh=14, nkv=2, hd=64, hidden=4864, vocab=151936, eps=1e-6, theta=1.0e6,
+                max_seq=640)
+REF_C3 = dict(w_seed=0x5EED, prompt_seed=3001, prompt=512, decode=128)
+
+
+def ref_decoder_weights(cfg: dict, seed: int):
+    """Codes and Scales of a reference decoder of shape cfg, as RefDecoder's constructor takes them: every weight,
+    gamma and embedding code uniform in +-WLEVELS at Scale(1 / WLEVELS) (floats of peak 1), from the LCG seeded
+    seed + 1, seed + 2, ... in the order embedding-free layers first: per layer in_norm, post_norm, wq, wk, wv, wo,
+    gate, up, down; then the embedding, the final norm and the lm_head."""
+    from . import backend as B
+
+    sc = B.ref_scale_from_f64(1.0 / WLEVELS)
+    d, qd, kvd, h, V = cfg["dim"], cfg["nh"] * cfg["hd"], cfg["nkv"] * cfg["hd"], cfg["hidden"], cfg["vocab"]
+    state = [seed]
+
+    def codes(*shape):
+        state[0] += 1
+        return B.gen_uniform_fast(state[0], -WLEVELS, WLEVELS, int(np.prod(shape))).reshape(shape)
+
+    layers = []
+    for _ in range(cfg["layers"]):
+        layers.append({"in_norm": (codes(d), sc), "post_norm": (codes(d), sc), "wq": (codes(qd, d), sc),
+                       "wk": (codes(kvd, d), sc), "wv": (codes(kvd, d), sc), "wo": (codes(d, qd), sc),
+                       "gate": (codes(h, d), sc), "up": (codes(h, d), sc), "down": (codes(d, h), sc)})
+    return (codes(V, d), sc), (codes(d), sc), (codes(V, d), sc), layers
+
+
+def ref_c3_prompt(cfg: dict = REF_QWEN) -> list:
+    """Config 3's 512 prompt token ids (uniform over the vocabulary) for the reference-semantics decoder."""
+    return decoder_prompt(REF_C3["prompt_seed"], REF_C3["prompt"], cfg["vocab"]).astype(int).tolist()
+
