@@ -2,10 +2,11 @@
 """Benchmark of the MI355X exact-integer GEMM backend on the BASELINE workloads, one GPU.
 
 Headline (`value`): config 2, the exact 12-bit GEMM at M = 2048, N = K = 4096 -- int8 activations (round(N(0,40))
-clipped to +-127) against 12-bit weight codes (packed W12, 1.5 bytes per weight), int32 accumulation per digit plane,
-exact recombination, then the per-channel integer requant (int32 multiplier + shift) to int8 outputs. A step is one
-launch. Inputs are resident in HBM before the timed region; the weights rotate over 12 copies (> 256 MB) so no
-launch finds them in the Infinity Cache. Every configuration's result is checked byte for byte against the fixture
+clipped to +-127) against 12-bit weight codes (as BASELINE describes them, two int8 digit planes: the balanced
+W12B split, lo in [-128, 127] and hi in [-8, 8], 2 bytes per weight; the packed 1.5-byte W12 planes are timed
+beside it), int32 accumulation per digit plane, exact recombination, then the per-channel integer requant (int32
+multiplier + shift) to int8 outputs. A step is one launch. Inputs are resident in HBM before the timed region; the
+weights rotate over 12 copies (> 256 MB) so no launch finds them in the Infinity Cache. Every configuration's result is checked byte for byte against the fixture
 hashes the CPU oracle produced (tests/golden/goldens.json) before anything is timed.
 
 Also measured, each under "configs" (skip with --configs):
@@ -24,7 +25,8 @@ Also measured, each under "configs" (skip with --configs):
 
 Prints one JSON line on stdout (progress goes to stderr):
   value      logical effective TOPS = 2*M*N*K / time per step (one launch per step)
-  roofline   the dominant kernel (w12_gemm at M = 2048) against the dense int8 MFMA peak (5.0 POPS)
+  roofline   the dominant kernel (w12_gemm_dma on the W12B planes at M = 2048) against the dense int8 MFMA peak
+             (5.0 POPS)
   sweep      config 2, M in {1, 16, 128, 2048}: per-launch time, effective TOPS, algorithmic GB/s, roofline fractions
   cpu_baseline  the reference's multithreaded CPU integer path (the oracle's restatement of linear_cpu, AVX-512
              variant when the host has it) on the same M = 2048 workload, timed on this host's cores
@@ -141,10 +143,20 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
     T.w12_upload(w, N, K, lo0, nib0)
     los = [lo0] + [lo0.clone() for _ in range(ROTATE - 1)]
     nibs = [nib0] + [nib0.clone() for _ in range(ROTATE - 1)]
+    # the MFMA-bound M = 2048 product on the balanced two-plane weights (W12B: no nibble unpack, no row sums)
+    nb = T.w12b_bytes(N, K)
+    blo0 = torch.empty(nb, dtype=torch.int8, device=dev)
+    bhi0 = torch.empty(nb, dtype=torch.int8, device=dev)
+    T.w12b_pack(torch.from_numpy(w).to(dev), N, K, blo0, bhi0)
+    blos = [blo0] + [blo0.clone() for _ in range(ROTATE - 1)]
+    bhis = [bhi0] + [bhi0.clone() for _ in range(ROTATE - 1)]
     xd = torch.from_numpy(W.pad_k(x, MH, K)).to(dev)
     md, sd = torch.from_numpy(mant).to(dev), torch.from_numpy(shift).to(dev)
     stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
+
+    def big(m):  # the products timed on the W12B planes
+        return m > 128
 
     # every M's result is checked first; the timings then run back to back with no host work between them, the
     # headline M last, so the GPU is busy (and its clocks up) when the headline's own warmup starts
@@ -153,13 +165,19 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
         want = g2["outputs"][str(m)]
         y8 = torch.empty(m * N, dtype=torch.int8, device=dev)
         acc = torch.empty(m * N, dtype=torch.int64, device=dev)
-        T.w12_linear(xd, lo0, nib0, m, N, K, acc, T.OUT_I64, stream=stream)
-        T.w12_linear(xd, lo0, nib0, m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
-        torch.cuda.synchronize()
-        exact = sha(acc.cpu().numpy()) == want["acc_i64_sha256"] and sha(y8.cpu().numpy()) == want["out_i8_sha256"]
-        if not exact:
-            raise SystemExit(f"bench: config 2 M={m}: the GPU result differs from the CPU fixture")
-        log(f"bench: config 2 M={m}: bit-exact vs the CPU fixture")
+        for planes in (("w12",) + (("w12b",) if big(m) else ())):
+            acc.zero_(), y8.zero_()
+            if planes == "w12":
+                T.w12_linear(xd, lo0, nib0, m, N, K, acc, T.OUT_I64, stream=stream)
+                T.w12_linear(xd, lo0, nib0, m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+            else:
+                T.w12b_linear(xd, blo0, bhi0, m, N, K, acc, T.OUT_I64, stream=stream)
+                T.w12b_linear(xd, blo0, bhi0, m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+            torch.cuda.synchronize()
+            exact = sha(acc.cpu().numpy()) == want["acc_i64_sha256"] and sha(y8.cpu().numpy()) == want["out_i8_sha256"]
+            if not exact:
+                raise SystemExit(f"bench: config 2 M={m} ({planes}): the GPU result differs from the CPU fixture")
+            log(f"bench: config 2 M={m} ({planes}): bit-exact vs the CPU fixture")
         del acc
         outs[m] = y8
 
@@ -171,7 +189,10 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
 
         def launch(i, m=m, y8=y8):
             j = i % ROTATE
-            T.w12_linear(xd, los[j], nibs[j], m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+            if big(m):
+                T.w12b_linear(xd, blos[j], bhis[j], m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+            else:
+                T.w12_linear(xd, los[j], nibs[j], m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
 
         n_launch = args.steps if m == MH else max(args.steps, 1000)
         warm = args.warmup if m == MH else max(args.warmup, 100)
@@ -179,7 +200,8 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
         ms, wall = time_launches(torch, launch, n_launch, warm)
         us = ms * 1e3
         ops = 2.0 * m * N * K
-        bytes_alg = 1.5 * N * K + m * K + m * N * 1  # packed weights + int8 activations + int8 outputs
+        # weights as stored (1.5 B per weight packed W12; 2 B as the two W12B planes) + int8 activations + int8 out
+        bytes_alg = (2.0 if big(m) else 1.5) * N * K + m * K + m * N * 1
         tops = ops / (us * 1e-6) / 1e12
         gbs = bytes_alg / (us * 1e-6) / 1e9
         sweep[str(m)] = {
@@ -190,7 +212,7 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
             "alg_gbs": round(gbs, 1),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "bit_exact": True,
-            "kernel": "w12_skinny" if m <= 128 else "w12_gemm",
+            "kernel": "w12_skinny" if m <= 128 else "w12_gemm_dma on the W12B planes",
             "launches": n_launch, "warmup_launches": warm,
         }
         if m == MH:
@@ -200,7 +222,16 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
             sweep[str(m)]["settled_us_per_launch"] = round(ms_s * 1e3, 3)
             sweep[str(m)]["settled_effective_tops"] = round(ops / (ms_s * 1e-3) / 1e12, 2)
             sweep[str(m)]["settled_launches"] = "1000 after 500 warmup launches, right after the headline timing"
-    del los, nibs
+
+            # the same product on the packed W12 planes (1.5 B per weight), for comparison
+            def launch_w12(i, m=m, y8=y8):
+                j = i % ROTATE
+                T.w12_linear(xd, los[j], nibs[j], m, N, K, y8, T.OUT_I8, md, sd, stream=stream)
+
+            ms_p, _ = time_launches(torch, launch_w12, 1000, 500)
+            sweep[str(m)]["w12_planes_us_per_launch"] = round(ms_p * 1e3, 3)
+            sweep[str(m)]["w12_planes_effective_tops"] = round(ops / (ms_p * 1e-3) / 1e12, 2)
+    del los, nibs, blos, bhis
     return sweep, headline, x, w
 
 
@@ -1084,7 +1115,7 @@ def main() -> int:
         "data": "synthetic (LCG integer samplers; inputs and outputs hash-checked against the CPU oracle fixtures)",
         "config": {
             "workload": "config 2: exact 12-bit GEMM, int8 x 12-bit codes -> i64 -> per-channel requant -> int8",
-            "M": MH, "N": N, "K": K, "weights": "W12 packed, 1.5 B/weight, 12 rotating copies",
+            "M": MH, "N": N, "K": K, "weights": "two balanced int8 digit planes (W12B), 2 B/weight, 12 rotating copies",
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -1096,7 +1127,8 @@ def main() -> int:
             "traffic": traffic,
             "traffic_source": "the committed rocprofv3 FETCH_SIZE + WRITE_SIZE figure of this kernel "
                               "(profiles/w12_gemm_m2048_traffic.json, copy-calibrated), not measured in this run",
-            "kernel": "w12_gemm_dma_kernel (logical ops 2*M*N*K per launch; the 2 digit planes execute twice that)",
+            "kernel": "w12_gemm_dma_kernel<I8, SMALL, BAL> on the W12B planes (logical ops 2*M*N*K per launch; the 2 "
+                      "digit planes execute twice that)",
         },
         "sweep": sweep,
         "configs": extra,

@@ -490,6 +490,20 @@ int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
                       int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
                       void* y_dev, void* stream);
 
+/* The same 12-bit weights as two balanced int8 digit planes (W12B), for the MFMA-bound products whose m gives every CU
+ * a 256 x 128 tile (config 2 at m = 2048): hi = (v + 128) >> 8 in [-8, 8], lo = v - 256 hi in [-128, 127], so
+ * v = lo + 256 hi with no offset term and the product needs no row sums of x and no nibble unpacking. Each plane is
+ * fragment-tiled as the W12 lo plane (kt_hip_w12b_bytes: round_up(n, 32) * kp bytes each, 2 bytes per weight
+ * together). kt_hip_w12b_linear: the same integers and out_kind semantics as kt_hip_w12_linear for every m and n
+ * (always the DMA-fed 256 x 128 GEMM), k <= KT_W12_GEMM_MAX_K, m * kp and round_up(n, 32) * kp below 2^32. No
+ * counterpart in the reference. */
+void kt_hip_w12b_bytes(int64_t n, int64_t k, size_t* plane_bytes);
+int kt_hip_w12b_pack(int dev, const int32_t* codes_dev, int64_t n, int64_t k, int8_t* lo_dev, int8_t* hi_dev,
+                     void* stream);
+int kt_hip_w12b_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const int8_t* hi_dev, int64_t m,
+                       int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
+                       void* y_dev, void* stream);
+
 /* As kt_hip_w12_linear with out_kind KT_OUT_I8, then each int8 output q replaced by lut_dev[q + 127] (255 int8
  * entries, device): an activation-code table applied in the epilogue (the GELU of config 5's FeedForward,
  * crates/03-models/kt-model-vision/src/hiera.rs:336-340 with nonlin.rs:30-47, as an int8 code table).

@@ -77,6 +77,9 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_w12_pack": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
         "kt_hip_w12_upload": (_I, [_I, _P, _I64, _I64, _P, _P]),
         "kt_hip_w12_linear": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
+        "kt_hip_w12b_bytes": (None, [_I64, _I64, C.POINTER(_SZ)]),
+        "kt_hip_w12b_pack": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
+        "kt_hip_w12b_linear": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
         "kt_hip_probe_mfma": (_I, [_I, _P, _P, _P, _P, _P]),
         "kt_hip_w12_linear_lut": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
         "kt_hip_w12_pack_gate_up": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
@@ -339,6 +342,29 @@ def w12_linear(x_dev, lo_dev, nib_dev, m: int, n: int, k: int, y_dev, out_kind: 
         lib().kt_hip_w12_linear(dev, _ptr(x_dev), _ptr(lo_dev), _ptr(nib_dev), m, n, k, _ptr(mant_dev),
                                 _ptr(shift_dev), out_kind, _ptr(y_dev), _stream(stream)),
         "w12 linear",
+    )
+
+
+def w12b_bytes(n: int, k: int) -> int:
+    """Bytes of each of the two balanced W12B planes (lo, hi) of an n x k weight matrix."""
+    b = C.c_size_t()
+    lib().kt_hip_w12b_bytes(n, k, C.byref(b))
+    return b.value
+
+
+def w12b_pack(codes_dev, n: int, k: int, lo_dev, hi_dev, stream=None, dev: int = 0) -> None:
+    """Pack n x k codes in [-2048, 2047] (i32, device) into the balanced planes: hi = (v + 128) >> 8, lo = v - 256 hi."""
+    check(lib().kt_hip_w12b_pack(dev, _ptr(codes_dev), n, k, _ptr(lo_dev), _ptr(hi_dev), _stream(stream)),
+          "w12b pack")
+
+
+def w12b_linear(x_dev, lo_dev, hi_dev, m: int, n: int, k: int, y_dev, out_kind: int = OUT_I64, mant_dev=None,
+                shift_dev=None, stream=None, dev: int = 0) -> None:
+    """w12_linear's integers over the balanced W12B planes (the DMA-fed 256 x 128 GEMM). Asynchronous."""
+    check(
+        lib().kt_hip_w12b_linear(dev, _ptr(x_dev), _ptr(lo_dev), _ptr(hi_dev), m, n, k, _ptr(mant_dev),
+                                 _ptr(shift_dev), out_kind, _ptr(y_dev), _stream(stream)),
+        "w12b linear",
     )
 
 

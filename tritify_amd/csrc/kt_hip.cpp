@@ -549,6 +549,33 @@ int kt_hip_w12_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const 
                                       y_dev, (hipStream_t)stream);
 }
 
+void kt_hip_w12b_bytes(int64_t n, int64_t k, size_t* plane_bytes) {
+    *plane_bytes = (size_t)((n + 31) / 32 * 32) * (size_t)kp_of(k);
+}
+
+int kt_hip_w12b_pack(int dev, const int32_t* codes_dev, int64_t n, int64_t k, int8_t* lo_dev, int8_t* hi_dev,
+                     void* stream) {
+    if (n < 0 || k < 0) return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12b_pack(codes_dev, n, k, lo_dev, hi_dev, (hipStream_t)stream);
+}
+
+int kt_hip_w12b_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const int8_t* hi_dev, int64_t m,
+                       int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
+                       void* y_dev, void* stream) {
+    if (m < 0 || n < 0 || k < 1) return (int)hipErrorInvalidValue;
+    if (m == 0 || n == 0) return 0;
+    const int64_t kp = kp_of(k);
+    if (m > INT_MAX || n > INT_MAX || kp > KT_W12_GEMM_MAX_K) return (int)hipErrorInvalidValue;
+    if (m * kp > (int64_t)UINT32_MAX || (n + 31) / 32 * 32 * kp > (int64_t)UINT32_MAX) return (int)hipErrorInvalidValue;
+    if (out_kind != KT_OUT_I64 && (mant_dev == nullptr || shift_dev == nullptr)) return (int)hipErrorInvalidValue;
+    if (out_kind != KT_OUT_I64 && out_kind != KT_OUT_I32 && out_kind != KT_OUT_I8 && out_kind != KT_OUT_I32_ADD)
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_w12b_linear(x_dev, lo_dev, hi_dev, (int)m, (int)n, (int)kp, mant_dev, shift_dev, out_kind,
+                                       y_dev, (hipStream_t)stream);
+}
+
 int kt_hip_w12_linear_lut(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                           int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
                           const int8_t* lut_dev, int8_t* y_dev, void* stream) {

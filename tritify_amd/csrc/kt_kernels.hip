@@ -72,6 +72,32 @@ __global__ void w12_pack_kernel(const int32_t* __restrict__ codes, int64_t n, in
     *reinterpret_cast<v2i*>(nib + idx * 8) = v2i{(int)nw[0], (int)nw[1]};
 }
 
+// i32 codes [n][k] in [-2048, 2047] -> the balanced W12B planes: hi = (v + 128) >> 8 in [-8, 8], lo = v - 256 hi in
+// [-128, 127] (v = lo + 256 hi exactly), each plane fragment-tiled as W12's lo plane (np * kp bytes). One thread per
+// fragment lane: 16 lo bytes and 16 hi bytes; padding rows and k are 0 in both.
+__global__ void w12b_pack_kernel(const int32_t* __restrict__ codes, int64_t n, int64_t k, int64_t kp,
+                                 int8_t* __restrict__ lo, int8_t* __restrict__ hi) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // fragment-lane index
+    const int64_t KB = kp / 32, total = (n + 31) / 32 * KB * 64;
+    if (idx >= total) return;
+    const int64_t frag = idx >> 6, l = idx & 63, nb = frag / KB, kb = frag - nb * KB;
+    const int64_t r = nb * 32 + (l & 31), c0 = kb * 32 + 16 * (l >> 5);
+    uint32_t lw[4] = {0, 0, 0, 0}, hw[4] = {0, 0, 0, 0};
+    for (int t = 0; t < 16; t++) {
+        const int64_t c = c0 + t;
+        uint32_t lb = 0, hb = 0;
+        if (r < n && c < k) {
+            const int32_t v = codes[r * k + c], h = (v + 128) >> 8;
+            lb = (uint32_t)(v - 256 * h) & 255;
+            hb = (uint32_t)h & 255;
+        }
+        lw[t >> 2] |= lb << (8 * (t & 3));
+        hw[t >> 2] |= hb << (8 * (t & 3));
+    }
+    *reinterpret_cast<v4i*>(lo + idx * 16) = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+    *reinterpret_cast<v4i*>(hi + idx * 16) = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // Digit-plane GEMM (LinearBackend path). CTA = 4 waves in 2x2; each wave WTM x WTN tiles of 32x32; BK = 64.
 // Processes k in [k0, k1) (multiples of 64) and writes y = result (first chunk) or y += result.
@@ -591,7 +617,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WA
 #ifndef KT_W12_DMA
 #define KT_W12_DMA 1
 #endif
-template <int OUT, bool SMALL>
+// BAL: the weights are the balanced W12B planes (wnib is the hi plane, int8, laid out as lo).
+template <int OUT, bool SMALL, bool BAL = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void w12_gemm_dma_kernel(
     const int8_t* __restrict__ x, const int8_t* __restrict__ wlo, const uint8_t* __restrict__ wnib,
     void* __restrict__ y, int M, int N, int kp, const int32_t* __restrict__ mant, const int32_t* __restrict__ shift,
@@ -599,6 +626,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     typedef W12Tile<2, 4, 1, 2, 4> C;  // 256 x 128, 8 waves (the tile's NSLOT is not used by this mainloop)
     static_assert(C::BM == 256 && C::BN == 128 && C::NT == 512, "the DMA mainloop's tile");
     static_assert(KT_DMA_NS * KT_DMA_STAGE >= C::BM * C::BN, "the int8 output tile fits the ring");
+    constexpr uint32_t HB = BAL ? 1024 : 512;  // bytes of the hi plane per k32 block of a column block
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
     __shared__ int sRow[C::BM];
     __shared__ int8_t sLut[256];
@@ -613,11 +641,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(x + (size_t)m0 * kp, rows_a * (uint32_t)kp);
     const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < 4 ? (N - n0 + 31) / 32 : 4;
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
-    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb0 * KB * HB, (uint32_t)ncb * KB * HB);
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const uint32_t va0 = (uint32_t)dma_a_row(w, lane, 0) * (uint32_t)kp + dma_a_chunk(lane);
     v16i acc0[4][1], acc1[4][1];
-    w12_mainloop_dma<KT_DMA_NS>(rA, rL, rN, va0, va0 + 16u * (uint32_t)kp, kp, ring, acc0, acc1, sRow);
+    w12_mainloop_dma<KT_DMA_NS, BAL>(rA, rL, rN, va0, va0 + 16u * (uint32_t)kp, kp, ring, acc0, acc1, sRow);
     w12_gemm_epilogue<C, OUT, SMALL>(acc0, acc1, sRow, ring, sLut, y, M, N, m0, n0, mant, shift, lut);
 }
 
@@ -631,7 +659,7 @@ static bool dma_lds_ok() {
              hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
              hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&w12_gemm_dma_kernel<KT_OUT_I8, true>)) ==
                  hipSuccess &&
-             fa.sharedSizeBytes + (size_t)KT_DMA_NS * KT_DMA_STAGE <= (size_t)mx;
+             fa.sharedSizeBytes + (size_t)KT_DMA_NS * KT_DMA_STAGE_BAL <= (size_t)mx;
     }
     return ok == 1;
 }
@@ -1168,6 +1196,45 @@ hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* n
         case KT_OUT_I32: return w12_linear_out<KT_OUT_I32>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         case KT_OUT_I32_ADD: return w12_linear_out<KT_OUT_I32_ADD>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
         case KT_OUT_I8: return w12_linear_out<KT_OUT_I8>(x, lo, nib, M, N, kp, mant, shift, lut, y, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_w12b_pack(const int32_t* codes, int64_t n, int64_t k, int8_t* lo, int8_t* hi, hipStream_t s) {
+    const int64_t kp = ceil_div(k, 64) * 64, total = ceil_div(n, 32) * (kp / 32) * 64;
+    if (total == 0) return hipSuccess;
+    w12b_pack_kernel<<<dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s>>>(codes, n, k, kp, lo, hi);
+    return hipGetLastError();
+}
+
+// The balanced-plane product: always the DMA-fed 256 x 128 kernel (built for m that gives every CU a tile; any m
+// and n are correct: rows and columns past them read as zero and are not stored).
+template <int OUT>
+static hipError_t w12b_linear_out(const int8_t* x, const int8_t* lo, const int8_t* hi, int M, int N, int kp,
+                                  const int32_t* mant, const int32_t* shift, void* y, hipStream_t s) {
+    if (!dma_lds_ok()) return hipErrorInvalidConfiguration;
+    const int64_t tiles_d = ceil_div(N, 128) * ceil_div(M, 256);
+    if (tiles_d > INT32_MAX) return hipErrorInvalidValue;
+    const size_t lds = (size_t)KT_DMA_NS * KT_DMA_STAGE_BAL;
+    const uint8_t* h = reinterpret_cast<const uint8_t*>(hi);
+    if (kp <= KT_SMALL_KP)
+        w12_gemm_dma_kernel<OUT, true, true><<<dim3((unsigned)tiles_d), dim3(512), lds, s>>>(x, lo, h, y, M, N, kp,
+                                                                                          mant, shift, nullptr);
+    else
+        w12_gemm_dma_kernel<OUT, false, true><<<dim3((unsigned)tiles_d), dim3(512), lds, s>>>(x, lo, h, y, M, N, kp,
+                                                                                           mant, shift, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_w12b_linear(const int8_t* x, const int8_t* lo, const int8_t* hi, int M, int N, int kp,
+                              const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (kp <= 0 || (kp % 64)) return hipErrorInvalidValue;
+    switch (out_kind) {
+        case KT_OUT_I64: return w12b_linear_out<KT_OUT_I64>(x, lo, hi, M, N, kp, mant, shift, y, s);
+        case KT_OUT_I32: return w12b_linear_out<KT_OUT_I32>(x, lo, hi, M, N, kp, mant, shift, y, s);
+        case KT_OUT_I32_ADD: return w12b_linear_out<KT_OUT_I32_ADD>(x, lo, hi, M, N, kp, mant, shift, y, s);
+        case KT_OUT_I8: return w12b_linear_out<KT_OUT_I8>(x, lo, hi, M, N, kp, mant, shift, y, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -605,18 +605,25 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
     load(ring, 0, f0);
     load(ring, 1, f1);
     // Ping-pong: the first half of tile kt's MFMAs covers the barrier that publishes tile kt + 1, the second half
-    // covers the LDS reads of tile kt + 1's first half, and those of its second half run under the next step's
+    // covers the LDS reads of tile kt + 1's first half and the DMAs of tile kt + NS (one DMA after every two MFMAs:
+    // issued all at once after the barrier, the eight waves' DMAs queue up at the CU's memory path and hold back
+    // the MFMAs behind them; 1.7% faster measured), and the reads of its second half run under the next step's
     // first MFMAs. Reads in the last step fetch a stage nobody consumes.
     for (int kt = 0; kt < nk; kt++) {
         mma(f0);
         // tile kt + 1 has landed once at most the DMAs of tiles kt + 2 .. kt + NS - 1 are outstanding; every wave's
         // reads of tile kt are done (lgkmcnt), so after the barrier its stage takes tile kt + NS
         wait_tile();
-        issue(kt % NS, kt + NS);
         const int8_t* sn = ring + ((kt + 1) % NS) * STAGE;
         load(sn, 0, f0);
         __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs they hide under
+        issue(kt % NS, kt + NS);
         mma(f1);
+#pragma unroll
+        for (int q = 0; q < ND; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one vector-memory read (a DMA)
+        }
         __builtin_amdgcn_sched_barrier(0);
         load(sn, 1, f1);
     }
