@@ -730,7 +730,7 @@ def ref_decoder_oracle() -> tuple:
     """The oracle's restatement of the reference decoder (the weights of config 3's reference-semantics run) over
     REF_PROMPT and REF_NDEC greedy steps: every position's logits hash, the seconds it took, the threads. The CPU
     baseline's bounded sample (32 positions)."""
-    if not _ref_cpu:
+    if "hashes" not in _ref_cpu:
         from oracle import oracle as O
 
         log("bench: the reference decoder on the CPU (the oracle), Qwen2.5-0.5B shape, 32 positions")

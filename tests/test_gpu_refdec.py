@@ -215,15 +215,18 @@ def test_ref_argmax_record_stops_at_its_last_row(torch_dev):
                                       theta=1.0e6, max_seq=40),
                                  dict(dim=64, layers=1, nh=14, nkv=2, hd=128, hidden=64, vocab=8, eps=1e-6,
                                       theta=1.0e6, max_seq=512)])
-def test_ref_attention_steps(torch_dev, cfg):
+@pytest.mark.parametrize("heads", [False, True])
+def test_ref_attention_steps(torch_dev, cfg, heads):
     """Steps 0..max_seq-1 of Attention::decode_step's core on random q/k/v codes and scales (some steps with a zero k
     or v scale), the device cache against the oracle's, output codes and scale at every step. The configurations
-    reach both P.V layouts: by kv head (groups of up to 8 q heads; at max_seq 512 with head_dim 128 the heads' scores
-    fit 5 at a time, so batches split the groups) and by (head, dim) for a 12-head group."""
+    reach both P.V layouts of the one-CTA kernel: by kv head (groups of up to 8 q heads; at max_seq 512 with head_dim
+    128 the heads' scores fit 5 at a time, so batches split the groups) and by (head, dim) for a 12-head group.
+    heads: the same steps on the one-CTA-per-head kernels (a workspace given), head_dim 8 to 128."""
     torch = torch_dev
     from tritify_amd import backend as B
 
-    say(f"case: ref_attention_steps nh={cfg['nh']} nkv={cfg['nkv']} hd={cfg['hd']} steps={cfg['max_seq']}")
+    say(f"case: ref_attention_steps nh={cfg['nh']} nkv={cfg['nkv']} hd={cfg['hd']} steps={cfg['max_seq']} "
+        f"heads={heads}")
     model = O.RefModel(11, cfg)
     cache = O.RefCache(model)
     nh, nkv, hd, ms = cfg["nh"], cfg["nkv"], cfg["hd"], cfg["max_seq"]
@@ -239,6 +242,8 @@ def test_ref_attention_steps(torch_dev, cfg):
     vs_d = torch.zeros(ms * 16, dtype=torch.uint8, device="cuda")
     o, os_ = torch.zeros(qd, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
     pos_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = torch.full((B.ref_attention_step_workspace(ms, nh, hd),), 0x77, dtype=torch.uint8, device="cuda") \
+        if heads else None
     rng = np.random.default_rng(nh)
     for p in range(ms):
         q = rng.integers(-(2**28), 2**28, size=qd).astype(np.int32)
@@ -253,25 +258,26 @@ def test_ref_attention_steps(torch_dev, cfg):
         pos_d.fill_(p)
         B.ref_attention_step(dev_i32(torch, q), rec(torch, qs), dev_i32(torch, k), rec(torch, ks), dev_i32(torch, v),
                              rec(torch, vs), pos_d, nh, nkv, hd, ms, kc, vc, ks_d, vs_d, cos_d, sin_d, isq, exp_d,
-                             exp_lut, o, os_)
+                             exp_lut, o, os_, ws_dev=ws)
         oo, so = O.rd_attention_core(cache, q, qs, k, ks, v, vs, p)
         got = o.cpu().numpy()
         assert np.array_equal(got, oo), f"step {p}: {np.argwhere(got != oo)[:5].tolist()}"
         assert rd(os_) == so, p
 
 
-@pytest.mark.parametrize("max_seq", [1369, 4096])
-def test_ref_attention_steps_long_cache(torch_dev, max_seq):
+@pytest.mark.parametrize("max_seq,heads", [(1369, False), (1369, True), (4096, True)])
+def test_ref_attention_steps_long_cache(torch_dev, max_seq, heads):
     """Attention::decode_step's core at the Qwen2.5-0.5B heads (14 / 2 of 64) over every position of a long cache:
-    1369 positions, the most the LDS path holds (one head's scores at a time), and 4096, the reference's MAX_SEQ_CAP
-    (crates/03-models/kt-model-decoder/src/lib.rs:46), on the workspace path. The device runs every step; the oracle
+    1369 positions, the most the one-CTA kernel's LDS holds (one head's scores at a time), and on the one-CTA-per-head
+    kernels 1369 and 4096, the reference's MAX_SEQ_CAP (crates/03-models/kt-model-decoder/src/lib.rs:46). The device
+    runs every step; the oracle
     checks the output codes and scale at spread positions (the first steps, every 97th, around 1369 and the last)
     and only appends to its cache in between."""
     torch = torch_dev
     from tritify_amd import backend as B
 
     nh, nkv, hd = 14, 2, 64
-    say(f"case: ref_attention_steps long cache max_seq={max_seq}")
+    say(f"case: ref_attention_steps long cache max_seq={max_seq} heads={heads}")
     cfg = dict(dim=64, layers=1, nh=nh, nkv=nkv, hd=hd, hidden=64, vocab=8, eps=1e-6, theta=1.0e6, max_seq=max_seq)
     assert B.ref_attention_step_fits_lds(max_seq, nh, hd) == (max_seq <= 1369)
     model = O.RefModel(11, cfg)
@@ -288,9 +294,7 @@ def test_ref_attention_steps_long_cache(torch_dev, max_seq):
     vs_d = torch.zeros(ms * 16, dtype=torch.uint8, device="cuda")
     o, os_ = torch.zeros(qd, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
     pos_d = torch.zeros(1, dtype=torch.int32, device="cuda")
-    ws = None
-    if not B.ref_attention_step_fits_lds(ms, nh, hd):
-        ws = torch.empty(B.ref_attention_step_workspace(ms, nh, hd), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(B.ref_attention_step_workspace(ms, nh, hd), dtype=torch.uint8, device="cuda") if heads else None
     check = set(range(8)) | set(range(0, ms, 97)) | {1367, 1368, 1369, 1370} | set(range(ms - 3, ms))
     rng = np.random.default_rng(4096 + ms)
     qb = rng.integers(-(2**28), 2**28, size=(ms, qd)).astype(np.int32)
@@ -318,8 +322,8 @@ def test_ref_attention_steps_long_cache(torch_dev, max_seq):
         else:
             O.rd_attention_append(cache, kb[p], ks, vb[p], vs, p)
     assert checked == len([c for c in check if c < ms])
-    # the workspace path refuses to run without its workspace
-    if ws is not None:
+    # a cache past the one-CTA kernel's LDS is refused without a workspace
+    if max_seq > 1369:
         with pytest.raises(RuntimeError):
             B.ref_attention_step(qdv[0], recs[0], kdv[0], recs[1], vdv[0], recs[2], pos_d, nh, nkv, hd, ms, kc, vc,
                                  ks_d, vs_d, cos_d, sin_d, isq, exp_d, exp_lut, o, os_)
@@ -402,13 +406,14 @@ def _c3_weights():
     return _C3_WEIGHTS["w"]
 
 
-@pytest.mark.parametrize("max_seq", [640, 4096])
-def test_config3_at_the_reference_semantics_full_size(torch_dev, max_seq):
+@pytest.mark.parametrize("max_seq,heads", [(640, False), (640, True), (4096, True)])
+def test_config3_at_the_reference_semantics_full_size(torch_dev, max_seq, heads):
     """Config 3's workload at the reference's own semantics on the device: the Qwen2.5-0.5B-shape DecoderModel
     (24 layers, vocab 151936), a 512-token prompt through decode_step and 128 greedy steps as replays of one
     captured greedy step. Every one of the 640 positions' logits hash, the run's hash and the chosen tokens equal the
-    committed fixture (the oracle's repro::run, tests/golden/make_goldens.py config3_ref). With max_seq 4096 (the
-    reference's MAX_SEQ_CAP) the attention step runs on its workspace path at every position; with 640 on LDS."""
+    committed fixture (the oracle's repro::run, tests/golden/make_goldens.py config3_ref): on the one-CTA attention
+    step (max_seq 640 in its LDS) and on the one-CTA-per-head step at max_seq 640 and 4096 (the reference's
+    MAX_SEQ_CAP)."""
     import hashlib
     import json
     import os
@@ -418,13 +423,13 @@ def test_config3_at_the_reference_semantics_full_size(torch_dev, max_seq):
 
     torch = torch_dev
     fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "goldens.json")))["config3_ref"]
-    cfg = dict(W.REF_QWEN, max_seq=max_seq)
+    cfg = dict(W.REF_QWEN, max_seq=max_seq, attn_heads=heads)
     assert fx["cfg"] == W.REF_QWEN
-    prompt = W.ref_c3_prompt(cfg)
+    prompt = W.ref_c3_prompt(W.REF_QWEN)
     assert hashlib.sha256(np.asarray(prompt, dtype=np.int32).tobytes()).hexdigest() == fx["prompt_sha256"]
-    say(f"case: config 3 at the reference semantics, 512 + 128 positions, max_seq {max_seq}")
+    say(f"case: config 3 at the reference semantics, 512 + 128 positions, max_seq {max_seq} heads={heads}")
     dec = RefDecoder(cfg, *_c3_weights())
-    assert (dec.attn_ws is None) == (max_seq == 640)
+    assert (dec.attn_ws is None) == (not heads)
     dec.decode_step(prompt[0], 0)
     g = dec.capture_greedy_step()
     dec.new_cache()

@@ -55,8 +55,8 @@ struct RdAttn {
     kt_hip_codelut exp;
     int32_t* o;
     kt_hip_qscale* os;
-    unsigned char* ws;                 // global-memory per-step arrays for steps past the LDS path, or null
-    int hb;                            // LDS path: heads whose scores LDS holds at once
+    unsigned char* ws;                 // the heads kernels' workspace (rd_heads_layout), or null: the one-CTA kernel
+    int hb;                            // the one-CTA kernel: heads whose scores LDS holds at once
 };
 
 // Attention::forward_int over a sequence (prefill): the inputs, the tables and the workspace parts.
@@ -553,10 +553,8 @@ __global__ __launch_bounds__(RD_THREADS) void rd_gelu_kernel(const int32_t* __re
 //  3. per head: score_j = f_j.apply(q . k_j), ec_j = exp_code(score_j - max score) at s_ref (0 below the table),
 //     sumc = sum ec_j, out_d = sum_j ec_j * vf_j.apply(v_jd), scale_h = v_ref / sumc;
 //  4. the heads brought to the largest scale_h and requantized: o and its record.
-// The per-step arrays: score and v factors (32 B per cached position) and hb heads' scores (8 B per position each).
-// LDS path (GWS = false): rows of max_seq positions in LDS, the head outputs and the rotated q (12 B per q value)
-// after them, hb heads at a time. Workspace path (GWS = true, caches longer than LDS holds): rows of this step's
-// pos + 1 positions in the caller's global workspace a.ws, every head at once; LDS keeps the head outputs and q.
+// LDS: the per-step arrays (score and v factors, 32 B per cached position; hb heads' scores, 8 B per position each)
+// for max_seq positions, then the head outputs and the rotated q (12 B per q value).
 struct RdAttnShared {
     int64_t red[RD_WAVES];
     ScIdx redsc[RD_THREADS];
@@ -566,7 +564,6 @@ struct RdAttnShared {
     int64_t hsum[KT_REF_MAX_HEADS];
 };
 
-template <bool GWS>
 __device__ __forceinline__ void rd_attention_core(const RdAttn& a, unsigned char* lds, RdAttnShared& sh_,
                                                   int pos, int hb) {
     int64_t* red = sh_.red;
@@ -575,14 +572,12 @@ __device__ __forceinline__ void rd_attention_core(const RdAttn& a, unsigned char
     Sc* hsc = sh_.hsc;
     const int tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv, group = nh / nkv;
     const int kstride = nkv * hd, qstride = nh * hd;
-    const int steps = pos + 1, rows = GWS ? steps : a.max_seq;  // rows: the per-step arrays' length
-    unsigned char* arr = GWS ? a.ws : lds;
-    Sc* F = reinterpret_cast<Sc*>(arr);  // score factors, per step
+    const int steps = pos + 1, rows = a.max_seq;  // rows: the per-step arrays' length
+    Sc* F = reinterpret_cast<Sc*>(lds);  // score factors, per step
     Sc* VF = F + rows;                   // v factors, per step
     int64_t* S = reinterpret_cast<int64_t*>(VF + rows);   // scores, then exp codes: [hb][rows]
-    // head outputs (qstride) and the rotated q (qstride) always in LDS: after the arrays, or from its start
-    int64_t* HO = GWS ? reinterpret_cast<int64_t*>(lds) : S + (size_t)hb * rows;
-    int32_t* QD = reinterpret_cast<int32_t*>(HO + qstride);
+    int64_t* HO = S + (size_t)hb * rows;                  // head outputs, qstride
+    int32_t* QD = reinterpret_cast<int32_t*>(HO + qstride);  // rotated q, qstride
 
     // 1. RoPE and the cache append
     auto rot = [&](const int32_t* src, int32_t* dst, int heads) {
@@ -822,9 +817,7 @@ __device__ __forceinline__ void rd_attention_core(const RdAttn& a, unsigned char
         put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
 }
 
-// GWS = false: every array in LDS, sized for max_seq positions with hb >= 1 heads' scores at a time (a.lds_bytes);
-// GWS = true (a cache longer than that LDS holds): the per-step arrays in a.ws, every head's scores at once.
-template <bool GWS>
+// One CTA for every head: hb heads' scores at a time in LDS (a.hb >= 1).
 __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ RdAttnShared sh_;
@@ -834,11 +827,216 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
         if (threadIdx.x == 0) put_rec(a.os, Sc{0, 0});
         return;
     }
-    if constexpr (GWS) {
-        rd_attention_core<true>(a, lds, sh_, pos, a.nh);
-    } else {
-        rd_attention_core<false>(a, lds, sh_, pos, a.hb);
+    rd_attention_core(a, lds, sh_, pos, a.hb);
+}
+
+// Attention::decode_step between its projections with one CTA per q head, for caches of any length up to max_seq
+// (kt_hip_ref_attention_step_ws): the cache reads, the per-step Scale work and P.V spread over nh CUs instead of one.
+// rd_attention_heads_kernel (CTA h): RoPE of q_h and of this step's k (the first CTA of each kv group appends the
+// step's k and v rows to the cache, CTA 0 the step's scales; row pos is taken from the inputs by every CTA, so no
+// CTA reads what another writes in the same launch); every step's score factor f_j = s_j / s_ref and v factor
+// vf_j = vs_j / v_ref (the same integers in every CTA); its head's scores, integer softmax and P.V; the head's output
+// codes and scale v_ref / sumc into the workspace. rd_attention_combine_kernel (one CTA, the next launch): the heads
+// at their largest scale, requantized -- step 4 of the one-CTA kernel.
+struct RdHeadsLayout {
+    size_t ho, hsc, arr, arr_stride;  // byte offsets: head outputs, head scales, per-head step arrays (and stride)
+};
+__host__ __device__ inline size_t rd_round256(size_t v) { return (v + 255) / 256 * 256; }
+__host__ __device__ inline RdHeadsLayout rd_heads_layout(int max_seq, int nh, int hd) {
+    RdHeadsLayout L;
+    L.ho = 0;
+    L.hsc = rd_round256((size_t)nh * hd * sizeof(int64_t));
+    L.arr = L.hsc + rd_round256((size_t)nh * sizeof(Sc));
+    L.arr_stride = rd_round256((size_t)max_seq * (2 * sizeof(Sc) + sizeof(int64_t)));
+    return L;
+}
+
+constexpr int RD_PV_U = 4;  // cached v values loaded before their products in the heads kernel's P.V
+
+__global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a, RdHeadsLayout L) {
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ ScIdx redsc[RD_THREADS];
+    __shared__ Sc par[4];  // v_ref, s_ref, lut factor, 1 / v_ref
+    __shared__ Sc sinv_s;
+    __shared__ int64_t PV[RD_THREADS];
+    extern __shared__ __align__(16) int32_t qk[];  // the rotated q_h (hd), then this step's rotated k (hd)
+    const int h = blockIdx.x, tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv;
+    const int group = nh / nkv, kv = h / group, kstride = nkv * hd;
+    const int pos = *a.pos;
+    unsigned char* ws = a.ws;
+    int64_t* HO = reinterpret_cast<int64_t*>(ws + L.ho);
+    Sc* HSC = reinterpret_cast<Sc*>(ws + L.hsc);
+    if (pos < 0 || pos >= a.max_seq) {  // outside the tables: the combine writes zeros
+        for (int d = tid; d < hd; d += RD_THREADS) HO[(size_t)h * hd + d] = 0;
+        if (tid == 0) HSC[h] = Sc{0, 0};
+        return;
     }
+    const int steps = pos + 1;
+    Sc* F = reinterpret_cast<Sc*>(ws + L.arr + (size_t)h * L.arr_stride);  // score factors, per step
+    Sc* VF = F + a.max_seq;                                                 // v factors, per step
+    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);                // scores, then exp codes
+    int32_t* QD = qk;
+    int32_t* KP = qk + hd;
+
+    // 1. RoPE (attention.rs:222-246) of q_h and of this step's k of kv head `kv`; the cache append
+    for (int j = tid; j < half; j += RD_THREADS) {
+        const kt_hip_sscale c = a.cos[(size_t)pos * half + j], sn = a.sin[(size_t)pos * half + j];
+        const Sc cm{c.mant, c.shift}, sm{sn.mant, sn.shift};
+        const int32_t qa = a.q[h * hd + j], qb = a.q[h * hd + j + half];
+        QD[j] = (int32_t)(c.sign * sc_apply32(cm, qa) - sn.sign * sc_apply32(sm, qb));
+        QD[j + half] = (int32_t)(c.sign * sc_apply32(cm, qb) + sn.sign * sc_apply32(sm, qa));
+        const int32_t ka = a.k[kv * hd + j], kb = a.k[kv * hd + j + half];
+        KP[j] = (int32_t)(c.sign * sc_apply32(cm, ka) - sn.sign * sc_apply32(sm, kb));
+        KP[j + half] = (int32_t)(c.sign * sc_apply32(cm, kb) + sn.sign * sc_apply32(sm, ka));
+    }
+    __syncthreads();
+    if (h == kv * group)
+        for (int i = tid; i < hd; i += RD_THREADS) {
+            a.kc[(size_t)pos * kstride + kv * hd + i] = KP[i];
+            a.vc[(size_t)pos * kstride + kv * hd + i] = a.v[kv * hd + i];
+        }
+    if (h == 0 && tid == 0) {
+        a.kscale[pos] = kt_hip_sscale{a.ks->mant, a.ks->shift, 1};
+        a.vscale[pos] = kt_hip_sscale{a.vs->mant, a.vs->shift, 1};
+    }
+
+    // 2. every step's score scale s_j = qs * ks_j * inv_sqrt and v scale; their largest (the engine's fold)
+    const Sc qs = rec_sc(a.qs), isq{a.isq_mant, a.isq_shift}, ksp = rec_sc(a.ks), vsp = rec_sc(a.vs);
+    ScIdx bv{Sc{0, 0}, -1}, bs{Sc{0, 0}, -1};
+    for (int j = tid; j < steps; j += RD_THREADS) {
+        const Sc kj = j == pos ? ksp : Sc{a.kscale[j].mant, a.kscale[j].shift};
+        const Sc vj = j == pos ? vsp : Sc{a.vscale[j].mant, a.vscale[j].shift};
+        const Sc sj = sc_mul(sc_mul(qs, kj), isq);
+        F[j] = sj;
+        VF[j] = vj;
+        bv = sc_pick(bv, ScIdx{vj, j});
+        bs = sc_pick(bs, ScIdx{sj, j});
+    }
+    bv = block_fold_max(bv, redsc, steps);
+    bs = block_fold_max(bs, redsc, steps);
+    if (tid == 0) {
+        par[0] = bv.s, par[1] = bs.s;
+        par[2] = bs.s.mant ? sc_mul(bs.s, Sc{a.exp.inv_mant, a.exp.inv_shift}) : Sc{0, 0};
+        par[3] = bv.s.mant ? sc_recip(bv.s) : Sc{0, 0};  // the two reciprocals in two waves
+    }
+    if (tid == 64) sinv_s = bs.s.mant ? sc_recip(bs.s) : Sc{0, 0};
+    __syncthreads();
+    const Sc v_ref = par[0], s_ref = par[1], lm = par[2], vinv = par[3], sinv = sinv_s;
+    if (s_ref.mant == 0) {  // the head is skipped (the reference's `continue`): zeros at Scale::ZERO
+        for (int d = tid; d < hd; d += RD_THREADS) HO[(size_t)h * hd + d] = 0;
+        if (tid == 0) HSC[h] = Sc{0, 0};
+        return;
+    }
+
+    // 3. scores: one thread per cached step, the whole dot (16-byte loads of the cache row where it allows)
+    const bool vec = hd % 4 == 0 && (reinterpret_cast<uintptr_t>(a.kc) & 15) == 0 && ((size_t)kstride * 4) % 16 == 0;
+    int64_t m = INT64_MIN;
+    for (int j = tid; j < steps; j += RD_THREADS) {
+        VF[j] = v_ref.mant ? sc_mul(VF[j], vinv) : Sc{0, 0};
+        int64_t dot = 0;
+        if (j == pos) {
+            for (int d = 0; d < hd; d++) dot = wadd(dot, (int64_t)QD[d] * KP[d]);
+        } else if (vec) {
+            const int4* kr = reinterpret_cast<const int4*>(a.kc + (size_t)j * kstride + kv * hd);
+            for (int e4 = 0; e4 < hd / 4; e4 += 4) {
+                int4 kk[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) kk[u] = e4 + u < hd / 4 ? kr[e4 + u] : int4{0, 0, 0, 0};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (e4 + u >= hd / 4) break;
+                    const int d = 4 * (e4 + u);
+                    dot = wadd(dot, (int64_t)QD[d] * kk[u].x + (int64_t)QD[d + 1] * kk[u].y);  // each below 2^63
+                    dot = wadd(dot, (int64_t)QD[d + 2] * kk[u].z + (int64_t)QD[d + 3] * kk[u].w);
+                }
+            }
+        } else {
+            const int32_t* kr = a.kc + (size_t)j * kstride + kv * hd;
+            for (int d = 0; d < hd; d++) dot = wadd(dot, (int64_t)QD[d] * kr[d]);
+        }
+        const int64_t sc = sc_apply(sc_mul(F[j], sinv), dot);
+        S[j] = sc;
+        m = sc > m ? sc : m;
+    }
+    const int64_t dmax = block_max_i64(m, red);
+
+    // 4. the integer-code softmax numerators and their sum
+    int64_t sum = 0;
+    for (int j = tid; j < steps; j += RD_THREADS) {
+        const int64_t idx = lut_index(lm, (int64_t)((uint64_t)S[j] - (uint64_t)dmax), a.exp.lo_index);
+        const int64_t ec = idx < 0 ? 0 : lut_code(a.exp_codes, a.exp.n, idx);
+        S[j] = ec;
+        sum += ec;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = sum;
+    __syncthreads();
+    int64_t sumc = 0;
+    for (int w = 0; w < RD_WAVES; w++) sumc += red[w];
+    if (sumc <= 0) {
+        for (int d = tid; d < hd; d += RD_THREADS) HO[(size_t)h * hd + d] = 0;
+        if (tid == 0) HSC[h] = Sc{0, 0};
+        return;
+    }
+
+    // 5. P.V: thread js * hd + d (hd <= RD_THREADS) sums the steps j = js (mod slices) of column d (wrapping i64:
+    //    any order gives the reference's integers); the slices then add up in LDS
+    const int slices = RD_THREADS / hd, d = tid % hd, js = tid / hd;
+    int64_t acc = 0;
+    if (js < slices) {
+        const int32_t* vcol = a.vc + kv * hd + d;
+        for (int j0 = js; j0 < steps; j0 += RD_PV_U * slices) {
+            int32_t vv[RD_PV_U];
+#pragma unroll
+            for (int u = 0; u < RD_PV_U; u++) {
+                const int j = j0 + u * slices;
+                vv[u] = j >= steps ? 0 : (j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride]);
+            }
+#pragma unroll
+            for (int u = 0; u < RD_PV_U; u++) {
+                const int j = j0 + u * slices;
+                if (j < steps) acc = wadd(acc, wmul(S[j], sc_apply32(VF[j], vv[u])));
+            }
+        }
+    }
+    PV[tid] = acc;
+    __syncthreads();
+    for (int dd = tid; dd < hd; dd += RD_THREADS) {
+        int64_t t = 0;
+        for (int q = 0; q < slices; q++) t = wadd(t, PV[q * hd + dd]);
+        HO[(size_t)h * hd + dd] = t;
+    }
+    if (tid == 0) HSC[h] = sc_mul(v_ref, from_ratio(1, (u128)(uint64_t)sumc));
+}
+
+// Step 4 of Attention::decode_step over the heads kernel's outputs: the heads' largest scale by the engine's fold,
+// each head brought to it, requant_dyn of the concatenation, the record.
+__global__ __launch_bounds__(RD_THREADS) void rd_attention_combine_kernel(RdAttn a, RdHeadsLayout L) {
+    __shared__ int64_t red[RD_WAVES];
+    __shared__ ScIdx redsc[RD_THREADS];
+    const int tid = threadIdx.x, hd = a.hd, nh = a.nh, qstride = nh * hd;
+    const int64_t* HO = reinterpret_cast<const int64_t*>(a.ws + L.ho);
+    const Sc* HSC = reinterpret_cast<const Sc*>(a.ws + L.hsc);
+    const Sc common = block_fold_max(tid < nh ? ScIdx{HSC[tid], tid} : ScIdx{Sc{0, 0}, -1}, redsc, nh).s;
+    int64_t m = 0;
+    if (common.mant != 0) {
+        const Sc cinv = sc_recip(common);
+        for (int i = tid; i < qstride; i += RD_THREADS) {
+            const int64_t v = sc_apply(sc_mul(HSC[i / hd], cinv), HO[i]);
+            m = iabs(v) > m ? iabs(v) : m;
+        }
+    }
+    const int64_t gmax = block_max_i64(m, red);
+    const RqDen rd_gmax = rq_den(gmax);
+    if (gmax == 0) {
+        for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = 0;
+    } else {
+        const Sc cinv = sc_recip(common);
+        for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = rq_apply(rd_gmax, sc_apply(sc_mul(HSC[i / hd], cinv), HO[i]));
+    }
+    if (tid == 0)
+        put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
 }
 
 // The same ops over whole-sequence tensors on many CTAs (the batched forward's T-row tensors): one CTA forms the
@@ -1152,15 +1350,15 @@ size_t rd_attention_lds(int max_seq, int nh, int hd, int hb) {
 }
 // The dynamic LDS the attention step may take on the current device: KT_REF_ATTN_LDS, less what the device's
 // per-block limit leaves after the kernel's static LDS.
-static size_t rd_attention_budget(bool gws) {
+static size_t rd_attention_budget() {
     int dev = 0, mx = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
         return 0;
     hipFuncAttributes fa{};
-    const void* fn = gws ? reinterpret_cast<const void*>(&rd_attention_step_kernel<true>)
-                         : reinterpret_cast<const void*>(&rd_attention_step_kernel<false>);
-    if (hipFuncGetAttributes(&fa, fn) != hipSuccess || fa.sharedSizeBytes >= (size_t)mx) return 0;
+    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&rd_attention_step_kernel)) != hipSuccess ||
+        fa.sharedSizeBytes >= (size_t)mx)
+        return 0;
     const size_t room = (size_t)mx - fa.sharedSizeBytes;
     return room < KT_REF_ATTN_LDS ? room : KT_REF_ATTN_LDS;
 }
@@ -1207,21 +1405,20 @@ hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, 
     rd_gelu_kernel<<<(unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g)), RD_THREADS, 0, s>>>(x, xs, n, codes, *lut, y, ys);
     return hipGetLastError();
 }
-// The LDS kernel while one head's scores at max_seq positions fit the budget (dynamic LDS for as many heads as fit,
-// at most all); past that the workspace kernel, a.ws holding kt_hip_ref_attention_step_workspace bytes (the entry
-// point checks).
+// With a workspace: the heads kernel (one CTA per q head) and the combine. Without: the one-CTA kernel, its LDS
+// holding at least one head's scores at max_seq positions (the entry point checks which applies).
 hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
     RdAttn a = a_in;
-    const size_t budget = rd_attention_budget(false);
-    a.hb = rd_attention_hb(a.max_seq, a.nh, a.hd, budget);
-    if (a.hb >= 1) {
-        rd_attention_step_kernel<false><<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
+    if (a.ws) {
+        const RdHeadsLayout L = rd_heads_layout(a.max_seq, a.nh, a.hd);
+        rd_attention_heads_kernel<<<(unsigned)a.nh, RD_THREADS, (size_t)2 * a.hd * sizeof(int32_t), s>>>(a, L);
+        rd_attention_combine_kernel<<<1, RD_THREADS, 0, s>>>(a, L);
         return hipGetLastError();
     }
-    const size_t lds = (size_t)a.nh * a.hd * (8 + 4);  // the head outputs and the rotated q
-    if (!a.ws || lds > rd_attention_budget(true)) return hipErrorInvalidValue;
-    a.hb = a.nh;
-    rd_attention_step_kernel<true><<<1, RD_THREADS, lds, s>>>(a);
+    const size_t budget = rd_attention_budget();
+    a.hb = rd_attention_hb(a.max_seq, a.nh, a.hd, budget);
+    if (a.hb < 1) return hipErrorInvalidValue;
+    rd_attention_step_kernel<<<1, RD_THREADS, rd_attention_lds(a.max_seq, a.nh, a.hd, a.hb), s>>>(a);
     return hipGetLastError();
 }
 size_t rd_seq_workspace(int64_t rows) { return (sizeof(RdSeqWs) + (size_t)(rows > 1 ? rows - 1 : 0) * sizeof(Sc) + 255) / 256 * 256; }
@@ -1481,7 +1678,8 @@ extern "C" int kt_hip_ref_conv2d(int dev, const int32_t* x_dev, const kt_hip_qsc
 extern "C" size_t kt_hip_ref_attention_step_workspace(int64_t max_seq, int64_t nh, int64_t hd) {
     if (nh < 1 || nh > KT_REF_MAX_HEADS || hd < 2 || hd > 1024 || max_seq < 1 || max_seq > KT_REF_ATTN_MAX_SEQ)
         return 0;
-    return (size_t)max_seq * (2 * sizeof(kt::Sc) + 8 * (size_t)nh);
+    const kt::RdHeadsLayout L = kt::rd_heads_layout((int)max_seq, (int)nh, (int)hd);
+    return L.arr + (size_t)nh * L.arr_stride;
 }
 
 extern "C" int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,
@@ -1499,9 +1697,9 @@ extern "C" int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const
     if (nh < 1 || nkv < 1 || nh % nkv || nh > KT_REF_MAX_HEADS || hd < 2 || (hd & 1) || hd > 1024 || max_seq < 1 ||
         max_seq > KT_REF_ATTN_MAX_SEQ || exp_lut->n < 1 || isq_mant < 0)
         return (int)hipErrorInvalidValue;
-    const bool fits = kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd, 1) <= KT_REF_ATTN_LDS;
-    if (!fits && (!ws_dev || (reinterpret_cast<uintptr_t>(ws_dev) & 15) ||
-                  ws_bytes < kt_hip_ref_attention_step_workspace(max_seq, nh, hd)))
+    if (ws_dev ? ((reinterpret_cast<uintptr_t>(ws_dev) & 15) ||
+                  ws_bytes < kt_hip_ref_attention_step_workspace(max_seq, nh, hd))
+               : kt::rd_attention_lds((int)max_seq, (int)nh, (int)hd, 1) > KT_REF_ATTN_LDS)
         return (int)hipErrorInvalidValue;
     RD_TRY(hipSetDevice(dev));
     kt::RdAttn a{};

@@ -112,10 +112,10 @@ class RefDecoder:
         self._rec_qkv, self._rec_gu = qkv_rec, gu_rec
         self.token = z(1)
         self.pos = z(1)
-        # caches past the attention step's LDS keep its per-step arrays in one workspace the layers share (their
-        # steps run in order on one stream)
+        # the attention step on one CTA per head, its workspace shared by the layers (their steps run in order on
+        # one stream); attn_heads=False keeps the one-CTA step where its LDS holds max_seq
         self.attn_ws = None
-        if not B.ref_attention_step_fits_lds(self.max_seq, self.nh, self.hd):
+        if cfg.get("attn_heads", True) or not B.ref_attention_step_fits_lds(self.max_seq, self.nh, self.hd):
             n = B.ref_attention_step_workspace(self.max_seq, self.nh, self.hd)
             if n == 0:
                 raise ValueError(f"max_seq {self.max_seq} beyond the attention step's limit")
