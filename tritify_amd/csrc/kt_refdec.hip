@@ -851,8 +851,13 @@ __host__ __device__ inline RdHeadsLayout rd_heads_layout(int max_seq, int nh, in
     return L;
 }
 
-constexpr int RD_PV_U = 4;  // cached v values loaded before their products in the heads kernel's P.V
+constexpr int RD_PV_U = 8;  // cached v values (and their steps' numerators and factors) loaded before the products
+// The heads kernel's dynamic LDS when its per-step arrays stay in LDS (max_seq up to about 2,400 at head_dim 64; the
+// static part is about 33 KB).
+constexpr size_t RD_HEADS_LDS = 96 * 1024;
 
+// GA: the per-step arrays in the workspace (caches longer than LDS holds), else in LDS after q and k.
+template <bool GA>
 __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a, RdHeadsLayout L) {
     __shared__ int64_t red[RD_WAVES];
     __shared__ ScIdx redsc[RD_THREADS];
@@ -872,11 +877,13 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         return;
     }
     const int steps = pos + 1;
-    Sc* F = reinterpret_cast<Sc*>(ws + L.arr + (size_t)h * L.arr_stride);  // score factors, per step
-    Sc* VF = F + a.max_seq;                                                 // v factors, per step
-    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);                // scores, then exp codes
     int32_t* QD = qk;
     int32_t* KP = qk + hd;
+    unsigned char* arr = GA ? ws + L.arr + (size_t)h * L.arr_stride
+                            : reinterpret_cast<unsigned char*>(qk) + (size_t)rd_round256(2 * (size_t)hd * 4);
+    Sc* F = reinterpret_cast<Sc*>(arr);                        // score factors, per step
+    Sc* VF = F + a.max_seq;                                    // v factors, per step
+    int64_t* S = reinterpret_cast<int64_t*>(VF + a.max_seq);   // scores, then exp codes
 
     // 1. RoPE (attention.rs:222-246) of q_h and of this step's k of kv head `kv`; the cache append
     for (int j = tid; j < half; j += RD_THREADS) {
@@ -937,13 +944,14 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         if (j == pos) {
             for (int d = 0; d < hd; d++) dot = wadd(dot, (int64_t)QD[d] * KP[d]);
         } else if (vec) {
+            // 8 x 16 bytes of the cache row in flight at a time
             const int4* kr = reinterpret_cast<const int4*>(a.kc + (size_t)j * kstride + kv * hd);
-            for (int e4 = 0; e4 < hd / 4; e4 += 4) {
-                int4 kk[4];
+            for (int e4 = 0; e4 < hd / 4; e4 += 8) {
+                int4 kk[8];
 #pragma unroll
-                for (int u = 0; u < 4; u++) kk[u] = e4 + u < hd / 4 ? kr[e4 + u] : int4{0, 0, 0, 0};
+                for (int u = 0; u < 8; u++) kk[u] = e4 + u < hd / 4 ? kr[e4 + u] : int4{0, 0, 0, 0};
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
+                for (int u = 0; u < 8; u++) {
                     if (e4 + u >= hd / 4) break;
                     const int d = 4 * (e4 + u);
                     dot = wadd(dot, (int64_t)QD[d] * kk[u].x + (int64_t)QD[d + 1] * kk[u].y);  // each below 2^63
@@ -988,16 +996,18 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         const int32_t* vcol = a.vc + kv * hd + d;
         for (int j0 = js; j0 < steps; j0 += RD_PV_U * slices) {
             int32_t vv[RD_PV_U];
+            int64_t ec[RD_PV_U];
+            Sc vf[RD_PV_U];
 #pragma unroll
-            for (int u = 0; u < RD_PV_U; u++) {
-                const int j = j0 + u * slices;
-                vv[u] = j >= steps ? 0 : (j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride]);
+            for (int u = 0; u < RD_PV_U; u++) {  // a step past the end reads the last one and adds nothing
+                const int j = j0 + u * slices < steps ? j0 + u * slices : steps - 1;
+                vv[u] = j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride];
+                ec[u] = S[j];
+                vf[u] = VF[j];
             }
 #pragma unroll
-            for (int u = 0; u < RD_PV_U; u++) {
-                const int j = j0 + u * slices;
-                if (j < steps) acc = wadd(acc, wmul(S[j], sc_apply32(VF[j], vv[u])));
-            }
+            for (int u = 0; u < RD_PV_U; u++)
+                if (j0 + u * slices < steps) acc = wadd(acc, wmul(ec[u], sc_apply32(vf[u], vv[u])));
         }
     }
     PV[tid] = acc;
@@ -1411,7 +1421,11 @@ hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
     RdAttn a = a_in;
     if (a.ws) {
         const RdHeadsLayout L = rd_heads_layout(a.max_seq, a.nh, a.hd);
-        rd_attention_heads_kernel<<<(unsigned)a.nh, RD_THREADS, (size_t)2 * a.hd * sizeof(int32_t), s>>>(a, L);
+        const size_t qk = rd_round256((size_t)2 * a.hd * sizeof(int32_t)), lds = qk + L.arr_stride;
+        if (lds <= RD_HEADS_LDS)
+            rd_attention_heads_kernel<false><<<(unsigned)a.nh, RD_THREADS, lds, s>>>(a, L);
+        else
+            rd_attention_heads_kernel<true><<<(unsigned)a.nh, RD_THREADS, qk, s>>>(a, L);
         rd_attention_combine_kernel<<<1, RD_THREADS, 0, s>>>(a, L);
         return hipGetLastError();
     }
