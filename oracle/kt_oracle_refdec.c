@@ -27,6 +27,7 @@
  * Built with -ffp-contract=off: no float expression is contracted into a fused multiply-add.
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -1256,6 +1257,39 @@ int kt_rc_quant_bias(const float* b, size_t n, int64_t* codes, kt_scale* bs) {
 /* Conv2d::forward_int (conv.rs:68-130): x [ci][h][w] codes at xs, quant_to by its whole-tensor max, the direct
  * convolution (accumulation order (ic, ky, kx), taps outside the image skipped) against w [co][ci][kh][kw] at ws, the
  * bias in units of c, then requant_dyn by the whole output's max. out [co][oh][ow]. bias may be NULL. */
+/* One block of output channels [oc0, oc1) of the direct convolution (conv.rs:91-120), accumulation order
+ * (ic, ky, kx); the bias in units of c added last. */
+typedef struct {
+    const int32_t *qx, *wc;
+    const int64_t* bias;
+    kt_scale f;
+    size_t ci, h, w, kh, kw, stride, pad, oh, ow, oc0, oc1;
+    int64_t* acc;
+} rc_block;
+static void* rc_conv_block(void* p) {
+    const rc_block* B = (const rc_block*)p;
+    for (size_t oc = B->oc0; oc < B->oc1; oc++) {
+        const int64_t b = B->bias ? kt_scale_apply(B->f, B->bias[oc]) : 0;
+        for (size_t oy = 0; oy < B->oh; oy++)
+            for (size_t ox = 0; ox < B->ow; ox++) {
+                int64_t a = 0;
+                for (size_t ic = 0; ic < B->ci; ic++)
+                    for (size_t ky = 0; ky < B->kh; ky++) {
+                        const size_t iy = oy * B->stride + ky;
+                        if (iy < B->pad || iy - B->pad >= B->h) continue;
+                        for (size_t kx = 0; kx < B->kw; kx++) {
+                            const size_t ix = ox * B->stride + kx;
+                            if (ix < B->pad || ix - B->pad >= B->w) continue;
+                            a = wadd(a, wmul(B->qx[(ic * B->h + iy - B->pad) * B->w + ix - B->pad],
+                                             B->wc[((oc * B->ci + ic) * B->kh + ky) * B->kw + kx]));
+                        }
+                    }
+                B->acc[(oc * B->oh + oy) * B->ow + ox] = wadd(a, b);
+            }
+    }
+    return NULL;
+}
+
 void kt_rc_conv2d(const int32_t* x, kt_scale xs, size_t ci, size_t h, size_t w, const int32_t* wc, kt_scale ws,
                   size_t co, size_t kh, size_t kw, size_t stride, size_t pad, const int64_t* bias, kt_scale bs,
                   int32_t* out, kt_scale* os) {
@@ -1285,24 +1319,22 @@ void kt_rc_conv2d(const int32_t* x, kt_scale xs, size_t ci, size_t h, size_t w, 
     kt_scale f = ZERO;
     if (bias) f = kt_scale_mul(bs, kt_scale_recip(c));
     int64_t* acc = (int64_t*)malloc(n * sizeof(int64_t));
-    for (size_t oc = 0; oc < co; oc++) {
-        const int64_t b = bias ? kt_scale_apply(f, bias[oc]) : 0;
-        for (size_t oy = 0; oy < oh; oy++)
-            for (size_t ox = 0; ox < ow; ox++) {
-                int64_t a = 0;
-                for (size_t ic = 0; ic < ci; ic++)
-                    for (size_t ky = 0; ky < kh; ky++) {
-                        const size_t iy = oy * stride + ky;
-                        if (iy < pad || iy - pad >= h) continue;
-                        for (size_t kx = 0; kx < kw; kx++) {
-                            const size_t ix = ox * stride + kx;
-                            if (ix < pad || ix - pad >= w) continue;
-                            a = wadd(a, wmul(qx[(ic * h + iy - pad) * w + ix - pad], wc[((oc * ci + ic) * kh + ky) * kw + kx]));
-                        }
-                    }
-                acc[(oc * oh + oy) * ow + ox] = wadd(a, b);
-            }
+    /* par_blocks (layers.rs:88-115): the output channels in contiguous blocks, one per worker, when the work is at
+     * least 2^20 MAC; the calling thread takes the first block. Disjoint writes: the same integers for any split. */
+    const size_t work = n * ci * kh * kw;
+    size_t nt = work >= ((size_t)1 << 20) ? kt_resolve_threads(co) : 1;
+    nt = nt < 1 ? 1 : (nt > co ? co : nt);
+    const size_t chunk = (co + nt - 1) / nt, nb = (co + chunk - 1) / chunk;
+    rc_block* blk = (rc_block*)calloc(nb ? nb : 1, sizeof(rc_block));
+    pthread_t* th = (pthread_t*)calloc(nb ? nb : 1, sizeof(pthread_t));
+    for (size_t i = 0; i < nb; i++) {
+        const size_t a0 = i * chunk, a1 = a0 + chunk < co ? a0 + chunk : co;
+        blk[i] = (rc_block){qx, wc, bias, f, ci, h, w, kh, kw, stride, pad, oh, ow, a0, a1, acc};
     }
+    for (size_t i = 1; i < nb; i++) pthread_create(&th[i], NULL, rc_conv_block, &blk[i]);
+    if (nb) rc_conv_block(&blk[0]);
+    for (size_t i = 1; i < nb; i++) pthread_join(th[i], NULL);
+    free(blk), free(th);
     rd_t o = {out, n, ZERO};
     close_dyn(acc, n, c, &o);
     *os = o.s;

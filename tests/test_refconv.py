@@ -204,3 +204,21 @@ def test_product_host_builders_equal_the_oracle():
     assert np.array_equal(codes, oc)
     assert (lut.inv_mant, lut.inv_shift) == inv and lut.lo_index == lo and (lut.code_mant, lut.code_shift) == cs
     assert lut.n == 1 << 16 and lut.right_identity == 1
+
+
+def test_conv_is_the_same_for_any_thread_count():
+    """par_blocks (layers.rs:88-115) splits Conv2d::forward_int's output channels over workers: 1, 2, 3 and 8
+    threads give the same codes and scale (the partition property of tests_partition.rs:43-58, for the conv)."""
+    rng = np.random.default_rng(91)
+    ci, h, w, co, k = 3, 64, 80, 13, 5
+    x = rng.integers(-(2**28), 2**28, size=ci * h * w).astype(np.int32)
+    wc = rng.integers(-O.WLEVELS, O.WLEVELS + 1, size=co * ci * k * k).astype(np.int32)
+    bias = (rng.integers(-(2**40), 2**40, size=co).astype(np.int64), (1 << 30, 70))
+    runs = []
+    for t in (1, 2, 3, 8):
+        O.set_max_threads(t)
+        runs.append(O.ref_conv2d(x, (1 << 30, 40), ci, h, w, wc, (1 << 30, 50), co, k, k, 2, 2, bias))
+    O.set_max_threads(0)
+    for y, s in runs[1:]:
+        assert np.array_equal(y, runs[0][0]) and s == runs[0][1]
+
