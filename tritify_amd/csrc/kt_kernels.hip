@@ -847,6 +847,151 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// W12 skinny GEMM for 64 < M <= 128 with x staged through LDS. Every CTA (half a column block, as above) reads all of
+// x; loaded straight into the MFMA operand lanes, each load instruction touches 16 rows x 64 bytes, half of every
+// 128-byte cache line it requests, and the x requests, not the bytes, set the time (the same bytes read as 8 rows x
+// 128 bytes per instruction ran 17.0 against 21.7 us at N = K = 4096). Here x arrives by LDS DMA in stages of 256 k:
+// each DMA instruction moves 4 rows x 256 contiguous bytes (8 whole lines), lane L landing at row L / 16, 16-byte
+// chunk position L % 16 of the stage and fetching chunk (L % 16) ^ (row % 16) (the XOR swizzle that makes the
+// fragment reads below conflict-free). A ring of SK_NS stages keeps SK_NS - 1 in flight. Wave w takes pair w % 4 of
+// the stage's four k64 pairs and the row tiles 4 (w / 4) .. +3: its A fragments come from LDS, its weight fragments
+// straight from memory as in the skinny kernel. The waves' partial sums then meet in the ring's LDS.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int SK_NS = 4, SK_STAGE = 128 * 256;  // ring stages; bytes of one stage (128 rows x 256 k)
+
+template <int OUT>
+__global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __restrict__ x,
+                                                             const int8_t* __restrict__ wlo,
+                                                             const uint8_t* __restrict__ wnib, void* __restrict__ y,
+                                                             int M, int N, int kp, const int32_t* __restrict__ mant,
+                                                             const int32_t* __restrict__ shift,
+                                                             const int8_t* __restrict__ lut) {
+    constexpr int NT = 512, MT = 8, OUTS = MT * 256;  // 128 rows x 16 columns
+    static_assert(SK_NS * SK_STAGE >= 8 * OUTS * 4, "the waves' partials fit the ring");
+    extern __shared__ __attribute__((aligned(16))) int8_t ring[];
+    __shared__ int32_t sX[8][MT * 16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cb = blockIdx.x >> 1, hb = blockIdx.x & 1, n0 = cb * 32 + 16 * hb;
+    const int KB = kp / 32, np = KB / 2, nst = (np + 3) / 4;  // k32 blocks, k64 pairs, stages of 4 pairs
+
+    const int oc = tid & 15, on = n0 + oc;
+    const int32_t om = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? mant[on] : 0;
+    const int32_t os = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? shift[on] : 0;
+
+    const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
+    const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb * KB * 512, (uint32_t)KB * 512);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)M * (uint32_t)kp);
+    const int c = lane & 15, g = lane >> 4, kbq = g >> 1, h = g & 1;
+    const int slot = 16 * hb + c + 32 * h;
+    const uint32_t oL = 16 * slot + 1024 * kbq, oN = 8 * slot + 512 * kbq;
+    const int pp = w & 3, th = w >> 2;  // the wave's pair within a stage; its half of the row tiles
+
+    // DMA lanes: instruction i (0..3) of wave w moves rows 16 w + 4 i + lane / 16, chunk position lane % 16
+    uint32_t vX[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * w + 4 * i + (lane >> 4), q = (lane & 15) ^ (r & 15);
+        vX[i] = r < M ? (uint32_t)r * (uint32_t)kp + 16u * q : KT_OOB;  // rows past M read as zero
+    }
+    // The CTAs walk the stages in rotated order, CTA b from stage b % nst: all of them read the same x, and in
+    // lockstep their requests would meet at the same L2 channels (the k order does not change the integer sums).
+    const int rot = (int)(blockIdx.x % (unsigned)nst);
+    auto phys = [&](int st) {
+        const int sc = st < nst ? st : nst - 1;
+        return sc + rot < nst ? sc + rot : sc + rot - nst;
+    };
+    // one stage's 4 DMAs and this wave's weight fragments (6 loads, in this order on every wave); a stage past the
+    // end re-reads the last one (inside every buffer), and chunks past kp read as zero
+    v4i L[SK_NS];
+    v2i D[SK_NS];
+    auto issue = [&](auto S, int st) {
+        constexpr int sl = decltype(S)::value;
+        const int sc = phys(st);
+        int8_t* sbuf = ring + sl * SK_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t k0 = 256u * (uint32_t)sc;
+            const int q = (lane & 15) ^ ((16 * w + 4 * i + (lane >> 4)) & 15);
+            const uint32_t v = k0 + 16u * q < (uint32_t)kp ? vX[i] : KT_OOB;
+            dma16(rX, sbuf + 4096 * w + 1024 * i, v, v == KT_OOB ? 0u : k0);
+        }
+        const int p = 4 * sc + pp, pl = p < np ? p : np - 1;
+        L[sl] = bload16(rL, oL, (uint32_t)pl * 2048u);
+        D[sl] = bload8(rN, oN, (uint32_t)pl * 1024u);
+    };
+
+    v4i acc0[4], acc1[4];
+    int sx[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc0[t] = acc1[t] = v4i{}, sx[t] = 0;
+
+    static_for<0, SK_NS - 1>([&](auto S) { issue(S, decltype(S)::value); });
+    int st = 0;
+    do {
+        static_for<0, SK_NS>([&](auto S) {
+            constexpr int sl = decltype(S)::value;
+            const int s = st + sl;
+            if (s < nst) {
+                // stage s has landed once the 6 loads of each of the SK_NS - 2 later stages are all that remain
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(6 * (SK_NS - 2)) : "memory");
+                // every wave is past stage s - 1: its buffer takes stage s + SK_NS - 1
+                issue(slot_t<(sl + SK_NS - 1) % SK_NS>{}, s + SK_NS - 1);
+                const int8_t* sb = ring + sl * SK_STAGE;
+                const int mask = 4 * phys(s) + pp < np ? -1 : 0;  // a pair past the end adds nothing (nor to the row sums)
+                const v4i hi = unpack_hi(D[sl]);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int R = 64 * th + 16 * t + c, q = 4 * pp + g;
+                    const v4i a = *reinterpret_cast<const v4i*>(sb + R * 256 + ((q ^ (R & 15)) << 4)) & mask;
+                    sx[t] += sum4(a);
+                    acc0[t] = mfma16(a, L[sl], acc0[t]);
+                    acc1[t] = mfma16(a, hi, acc1[t]);
+                }
+            }
+        });
+        st += SK_NS;
+    } while (st < nst);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is free (re-reads past the end landed)
+
+    // the wave's partials (rows of its half) and row sums into LDS (the ring)
+    int32_t* sP = reinterpret_cast<int32_t*>(ring);  // [8][OUTS]
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            sP[w * OUTS + ((4 * th + t) * 16 + 4 * g + r) * 16 + c] =
+                (int32_t)((uint32_t)acc0[t][r] + ((uint32_t)acc1[t][r] << 8));
+        int sv = sx[t];
+        sv += __shfl_xor(sv, 16);
+        sv += __shfl_xor(sv, 32);
+        if (lane < 16) sX[w][(4 * th + t) * 16 + lane] = sv;
+    }
+    __syncthreads();
+    const ColQ cq = col_q(om, os);
+#pragma unroll
+    for (int o = tid; o < OUTS; o += NT) {
+        const int m = o >> 4, half = m >> 6;  // output (m, oc); the waves 4 half .. 4 half + 3 hold its sums
+        uint32_t v = 0, rs = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) v += (uint32_t)sP[(4 * half + q) * OUTS + o], rs += (uint32_t)sX[4 * half + q][m];
+        const int vi = (int)(v - 1920u * rs);
+        if (m < M && on < N) {
+            const size_t idx = (size_t)m * N + on;
+            if constexpr (OUT == KT_OUT_I64) reinterpret_cast<int64_t*>(y)[idx] = vi;
+            else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
+            else if constexpr (OUT == KT_OUT_I32_ADD) {
+                int32_t* py = reinterpret_cast<int32_t*>(y) + idx;
+                *py = sat_add32(*py, col_requant<true>(vi, cq));
+            } else {
+                const int qv = col_requant<false>(vi, cq);
+                reinterpret_cast<int8_t*>(y)[idx] = lut ? lut[qv + 127] : (int8_t)qv;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // W12 skinny SwiGLU (M <= 16 * MT): the skinny kernel over a gate/up matrix packed with the 32-row interleave. A CTA
 // owns 16 hidden units u0 .. u0 + 15: half hb of gate block 2j and the same half of up block 2j + 1 (adjacent in
 // memory), both streamed in one pass over k. Epilogue: g, u = int8 requant per channel (gate channel u, up channel
@@ -1112,6 +1257,21 @@ hipError_t launch_plane_gemm(int px, int pw, const int8_t* xa, const int8_t* wb,
     return hipErrorInvalidValue;
 }
 
+// Whether the device gives one CTA the LDS-staged skinny kernel's ring; queried once per process.
+static bool skinny_lds_ok() {
+    static int ok = -1;
+    if (ok < 0) {
+        hipFuncAttributes fa;
+        int dev = 0, mx = 0;
+        ok = hipGetDevice(&dev) == hipSuccess &&
+             hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+             hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&w12_skinny_lds_kernel<KT_OUT_I8>)) ==
+                 hipSuccess &&
+             fa.sharedSizeBytes + (size_t)SK_NS * SK_STAGE <= (size_t)mx;
+    }
+    return ok == 1;
+}
+
 template <int OUT>
 static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,
                                  const int32_t* mant, const int32_t* shift, const int8_t* lut, void* y, hipStream_t s) {
@@ -1137,8 +1297,14 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
         if (kp <= 1024) {  // short k at M <= 16: 8 waves x 2 pairs cover kp in one batch with fewer clamped re-reads
             KT_SKINNY(1, 8, 2)
         }
-        // 65-128 rows: 8 waves x 2 pairs (21.8 us at M = 128, N = K = 4096, against 22.4 for 4 waves x 4 pairs, 25.3
-        // for 4 x 8 and 31.0 for 8 x 4)
+        // 65-128 rows with int32 dots: x staged through LDS (w12_skinny_lds_kernel)
+        if (M > 64 && kp <= KT_SMALL_KP && skinny_lds_ok()) {
+            w12_skinny_lds_kernel<OUT><<<grid, dim3(512), (size_t)SK_NS * SK_STAGE, s>>>(x, lo, nib, y, M, N, kp, mant,
+                                                                                    shift, lut);
+            return hipGetLastError();
+        }
+        // otherwise 65-128 rows: 8 waves x 2 pairs (21.8 us at M = 128, N = K = 4096, against 22.4 for 4 waves x 4
+        // pairs, 25.3 for 4 x 8 and 31.0 for 8 x 4)
         KT_SKINNY(1, 8, 4) KT_SKINNY(2, 8, 4) KT_SKINNY(4, 8, 2) KT_SKINNY(8, 8, 2)
 #undef KT_SKINNY
     }
