@@ -263,7 +263,7 @@ def test_w12_linear_against_the_oracle(torch_dev, out_kind):
     rng = np.random.default_rng(10 + out_kind)
     for m, n, k in [(1, 1, 1), (1, 5, 7), (2, 33, 100), (3, 64, 64), (4, 130, 1000), (5, 17, 4096), (8, 256, 2048),
                     (9, 70, 129), (16, 4096, 512), (17, 65, 64), (33, 200, 300), (64, 64, 4096), (65, 129, 640),
-                    (100, 96, 2000), (128, 512, 1024), (129, 100, 256), (130, 300, 96), (300, 257, 448)]:
+                    (100, 96, 2000), (96, 1000, 4096), (128, 512, 1024), (129, 100, 256), (130, 300, 96), (300, 257, 448)]:
         x = rng.integers(-128, 128, size=m * k).astype(np.int32)
         w = rng.integers(-2048, 2048, size=n * k).astype(np.int32)
         mant, shift = O.channel_scales(w, n, k, 40)

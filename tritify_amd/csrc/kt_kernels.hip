@@ -847,17 +847,19 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// W12 skinny GEMM for 64 < M <= 128 with x staged through LDS. Every CTA (half a column block, as above) reads all of
-// x; loaded straight into the MFMA operand lanes, each load instruction touches 16 rows x 64 bytes, half of every
-// 128-byte cache line it requests, and the x requests, not the bytes, set the time (the same bytes read as 8 rows x
-// 128 bytes per instruction ran 17.0 against 21.7 us at N = K = 4096). Here x arrives by LDS DMA in stages of 256 k:
-// each DMA instruction moves 4 rows x 256 contiguous bytes (8 whole lines), lane L landing at row L / 16, 16-byte
-// chunk position L % 16 of the stage and fetching chunk (L % 16) ^ (row % 16) (the XOR swizzle that makes the
-// fragment reads below conflict-free). A ring of SK_NS stages keeps SK_NS - 1 in flight. Wave w takes pair w % 4 of
-// the stage's four k64 pairs and the row tiles 4 (w / 4) .. +3: its A fragments come from LDS, its weight fragments
-// straight from memory as in the skinny kernel. The waves' partial sums then meet in the ring's LDS.
+// W12 skinny GEMM for 64 < M <= 128 with x staged through LDS. Loaded straight into the MFMA operand lanes (the skinny
+// kernel above), each x load instruction touches 16 rows x 64 bytes, half of every 128-byte line it requests, and
+// every one of the N / 16 CTAs reads all of x: at N = K = 4096, 128 MB of x requests for 25 MB of weights, and the
+// requests, not the bytes, set the time (the same bytes read as 8 rows x 128 bytes per instruction ran 17.0 against
+// 21.7 us). Here a CTA owns 64 rows x one 32-column block (CTAs 8 apart, on one XCD, share the block's weights:
+// rows 0-63 and 64-127), so x is read N / 32 times, and x arrives by LDS DMA in stages of 256 k: each DMA instruction
+// moves 4 rows x 256 contiguous bytes (8 whole lines), lane L landing at row L / 16, 16-byte chunk position L % 16 of
+// the stage, fetching chunk (L % 16) ^ (row % 16) (the swizzle that keeps the fragment reads conflict-free). A ring
+// of SK_NS stages keeps SK_NS - 1 in flight. Wave w takes pair w % 4 of a stage's four k64 pairs and column half
+// w / 4, all 4 row tiles: its A fragments from LDS, its weight fragments straight from memory as in the skinny kernel.
+// The waves' partial sums then meet in the ring's LDS.
 // ------------------------------------------------------------------------------------------------------------------
-constexpr int SK_NS = 4, SK_STAGE = 128 * 256;  // ring stages; bytes of one stage (128 rows x 256 k)
+constexpr int SK_NS = 8, SK_STAGE = 64 * 256;  // ring stages; bytes of one stage (64 rows x 256 k)
 
 template <int OUT>
 __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __restrict__ x,
@@ -866,55 +868,48 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
                                                              int M, int N, int kp, const int32_t* __restrict__ mant,
                                                              const int32_t* __restrict__ shift,
                                                              const int8_t* __restrict__ lut) {
-    constexpr int NT = 512, MT = 8, OUTS = MT * 256;  // 128 rows x 16 columns
-    static_assert(SK_NS * SK_STAGE >= 8 * OUTS * 4, "the waves' partials fit the ring");
+    constexpr int NT = 512, OUTS = 64 * 32;  // 64 rows x 32 columns
+    static_assert(SK_NS * SK_STAGE >= 8 * 64 * 16 * 4, "the waves' partials fit the ring");
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
-    __shared__ int32_t sX[8][MT * 16];
+    __shared__ int32_t sX[4][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int cb = blockIdx.x >> 1, hb = blockIdx.x & 1, n0 = cb * 32 + 16 * hb;
+    const int b = blockIdx.x, rh = (b >> 3) & 1, cb = (b & 7) | ((b >> 4) << 3);
+    const int m0 = 64 * rh, n0 = 32 * cb;
+    if (n0 >= N) return;  // past the last column block: the whole CTA idles
     const int KB = kp / 32, np = KB / 2, nst = (np + 3) / 4;  // k32 blocks, k64 pairs, stages of 4 pairs
-
-    const int oc = tid & 15, on = n0 + oc;
-    const int32_t om = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? mant[on] : 0;
-    const int32_t os = (OUT != KT_OUT_I64 && tid < OUTS && on < N) ? shift[on] : 0;
+    const int Mr = M - m0 < 64 ? M - m0 : 64;                  // rows of this CTA (>= 1: M > 64)
 
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
     const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb * KB * 512, (uint32_t)KB * 512);
-    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x, (uint32_t)M * (uint32_t)kp);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x + (size_t)m0 * kp, (uint32_t)Mr * (uint32_t)kp);
     const int c = lane & 15, g = lane >> 4, kbq = g >> 1, h = g & 1;
-    const int slot = 16 * hb + c + 32 * h;
+    const int pp = w & 3, ch = w >> 2;  // the wave's pair within a stage; its column half
+    const int slot = 16 * ch + c + 32 * h;
     const uint32_t oL = 16 * slot + 1024 * kbq, oN = 8 * slot + 512 * kbq;
-    const int pp = w & 3, th = w >> 2;  // the wave's pair within a stage; its half of the row tiles
 
-    // DMA lanes: instruction i (0..3) of wave w moves rows 16 w + 4 i + lane / 16, chunk position lane % 16
-    uint32_t vX[4];
+    // DMA lanes: instruction i (0, 1) of wave w moves rows 8 w + 4 i + lane / 16, chunk position lane % 16
+    uint32_t vX[2];
+    int qX[2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 16 * w + 4 * i + (lane >> 4), q = (lane & 15) ^ (r & 15);
-        vX[i] = r < M ? (uint32_t)r * (uint32_t)kp + 16u * q : KT_OOB;  // rows past M read as zero
+    for (int i = 0; i < 2; i++) {
+        const int r = 8 * w + 4 * i + (lane >> 4);
+        qX[i] = (lane & 15) ^ (r & 15);
+        vX[i] = r < Mr ? (uint32_t)r * (uint32_t)kp + 16u * qX[i] : KT_OOB;  // rows past M read as zero
     }
-    // The CTAs walk the stages in rotated order, CTA b from stage b % nst: all of them read the same x, and in
-    // lockstep their requests would meet at the same L2 channels (the k order does not change the integer sums).
-    const int rot = (int)(blockIdx.x % (unsigned)nst);
-    auto phys = [&](int st) {
-        const int sc = st < nst ? st : nst - 1;
-        return sc + rot < nst ? sc + rot : sc + rot - nst;
-    };
-    // one stage's 4 DMAs and this wave's weight fragments (6 loads, in this order on every wave); a stage past the
+    // one stage's 2 DMAs and this wave's weight fragments (4 loads, in this order on every wave); a stage past the
     // end re-reads the last one (inside every buffer), and chunks past kp read as zero
     v4i L[SK_NS];
     v2i D[SK_NS];
     auto issue = [&](auto S, int st) {
         constexpr int sl = decltype(S)::value;
-        const int sc = phys(st);
+        const int sc = st < nst ? st : nst - 1;
         int8_t* sbuf = ring + sl * SK_STAGE;
+        const uint32_t k0 = 256u * (uint32_t)sc;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t k0 = 256u * (uint32_t)sc;
-            const int q = (lane & 15) ^ ((16 * w + 4 * i + (lane >> 4)) & 15);
-            const uint32_t v = k0 + 16u * q < (uint32_t)kp ? vX[i] : KT_OOB;
-            dma16(rX, sbuf + 4096 * w + 1024 * i, v, v == KT_OOB ? 0u : k0);
+        for (int i = 0; i < 2; i++) {
+            const uint32_t v = k0 + 16u * qX[i] < (uint32_t)kp ? vX[i] : KT_OOB;
+            dma16(rX, sbuf + 2048 * w + 1024 * i, v, v == KT_OOB ? 0u : k0);
         }
         const int p = 4 * sc + pp, pl = p < np ? p : np - 1;
         L[sl] = bload16(rL, oL, (uint32_t)pl * 2048u);
@@ -933,16 +928,16 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
             constexpr int sl = decltype(S)::value;
             const int s = st + sl;
             if (s < nst) {
-                // stage s has landed once the 6 loads of each of the SK_NS - 2 later stages are all that remain
-                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(6 * (SK_NS - 2)) : "memory");
+                // stage s has landed once the 4 loads of each of the SK_NS - 2 later stages are all that remain
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * (SK_NS - 2)) : "memory");
                 // every wave is past stage s - 1: its buffer takes stage s + SK_NS - 1
                 issue(slot_t<(sl + SK_NS - 1) % SK_NS>{}, s + SK_NS - 1);
                 const int8_t* sb = ring + sl * SK_STAGE;
-                const int mask = 4 * phys(s) + pp < np ? -1 : 0;  // a pair past the end adds nothing (nor to the row sums)
+                const int mask = 4 * s + pp < np ? -1 : 0;  // a pair past the end adds nothing (nor to the row sums)
                 const v4i hi = unpack_hi(D[sl]);
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    const int R = 64 * th + 16 * t + c, q = 4 * pp + g;
+                    const int R = 16 * t + c, q = 4 * pp + g;
                     const v4i a = *reinterpret_cast<const v4i*>(sb + R * 256 + ((q ^ (R & 15)) << 4)) & mask;
                     sx[t] += sum4(a);
                     acc0[t] = mfma16(a, L[sl], acc0[t]);
@@ -954,30 +949,32 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
     } while (st < nst);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is free (re-reads past the end landed)
 
-    // the wave's partials (rows of its half) and row sums into LDS (the ring)
-    int32_t* sP = reinterpret_cast<int32_t*>(ring);  // [8][OUTS]
+    // the wave's partials (64 rows x its 16 columns) and, from the first column half, the row sums, into LDS
+    int32_t* sP = reinterpret_cast<int32_t*>(ring);  // [8 waves][64 rows][16 columns]
 #pragma unroll
     for (int t = 0; t < 4; t++) {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            sP[w * OUTS + ((4 * th + t) * 16 + 4 * g + r) * 16 + c] =
-                (int32_t)((uint32_t)acc0[t][r] + ((uint32_t)acc1[t][r] << 8));
+            sP[(w * 64 + 16 * t + 4 * g + r) * 16 + c] = (int32_t)((uint32_t)acc0[t][r] + ((uint32_t)acc1[t][r] << 8));
         int sv = sx[t];
         sv += __shfl_xor(sv, 16);
         sv += __shfl_xor(sv, 32);
-        if (lane < 16) sX[w][(4 * th + t) * 16 + lane] = sv;
+        if (ch == 0 && lane < 16) sX[pp][16 * t + lane] = sv;
     }
     __syncthreads();
+    const int cc = tid & 31, on = n0 + cc;  // every output of this thread is in column on
+    const int32_t om = (OUT != KT_OUT_I64 && on < N) ? mant[on] : 0;
+    const int32_t os = (OUT != KT_OUT_I64 && on < N) ? shift[on] : 0;
     const ColQ cq = col_q(om, os);
 #pragma unroll
     for (int o = tid; o < OUTS; o += NT) {
-        const int m = o >> 4, half = m >> 6;  // output (m, oc); the waves 4 half .. 4 half + 3 hold its sums
+        const int m = o >> 5, hc = cc >> 4, c16 = cc & 15;  // output (m0 + m, on); waves 4 hc .. 4 hc + 3 hold it
         uint32_t v = 0, rs = 0;
 #pragma unroll
-        for (int q = 0; q < 4; q++) v += (uint32_t)sP[(4 * half + q) * OUTS + o], rs += (uint32_t)sX[4 * half + q][m];
+        for (int q = 0; q < 4; q++) v += (uint32_t)sP[((4 * hc + q) * 64 + m) * 16 + c16], rs += (uint32_t)sX[q][m];
         const int vi = (int)(v - 1920u * rs);
-        if (m < M && on < N) {
-            const size_t idx = (size_t)m * N + on;
+        if (m < Mr && on < N) {
+            const size_t idx = (size_t)(m0 + m) * N + on;
             if constexpr (OUT == KT_OUT_I64) reinterpret_cast<int64_t*>(y)[idx] = vi;
             else if constexpr (OUT == KT_OUT_I32) reinterpret_cast<int32_t*>(y)[idx] = col_requant<true>(vi, cq);
             else if constexpr (OUT == KT_OUT_I32_ADD) {
@@ -1299,8 +1296,11 @@ static hipError_t w12_linear_out(const int8_t* x, const int8_t* lo, const uint8_
         }
         // 65-128 rows with int32 dots: x staged through LDS (w12_skinny_lds_kernel)
         if (M > 64 && kp <= KT_SMALL_KP && skinny_lds_ok()) {
-            w12_skinny_lds_kernel<OUT><<<grid, dim3(512), (size_t)SK_NS * SK_STAGE, s>>>(x, lo, nib, y, M, N, kp, mant,
-                                                                                    shift, lut);
+            // CTA b: rows 64 ((b >> 3) & 1), column block (b & 7) | ((b >> 4) << 3): 16 * ceil(ncb / 8) CTAs, the
+            // ones past the last column block idle
+            const int64_t ncb = ceil_div(N, 32), grid_l = 16 * ceil_div(ncb, 8);
+            w12_skinny_lds_kernel<OUT><<<dim3((unsigned)grid_l), dim3(512), (size_t)SK_NS * SK_STAGE, s>>>(
+                x, lo, nib, y, M, N, kp, mant, shift, lut);
             return hipGetLastError();
         }
         // otherwise 65-128 rows: 8 waves x 2 pairs (21.8 us at M = 128, N = K = 4096, against 22.4 for 4 waves x 4
