@@ -850,16 +850,19 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
 // W12 skinny GEMM for 64 < M <= 128 with x staged through LDS. Loaded straight into the MFMA operand lanes (the skinny
 // kernel above), each x load instruction touches 16 rows x 64 bytes, half of every 128-byte line it requests, and
 // every one of the N / 16 CTAs reads all of x: at N = K = 4096, 128 MB of x requests for 25 MB of weights, and the
-// requests, not the bytes, set the time (the same bytes read as 8 rows x 128 bytes per instruction ran 17.0 against
-// 21.7 us). Here a CTA owns 64 rows x one 32-column block (CTAs 8 apart, on one XCD, share the block's weights:
-// rows 0-63 and 64-127), so x is read N / 32 times, and x arrives by LDS DMA in stages of 256 k: each DMA instruction
-// moves 4 rows x 256 contiguous bytes (8 whole lines), lane L landing at row L / 16, 16-byte chunk position L % 16 of
-// the stage, fetching chunk (L % 16) ^ (row % 16) (the swizzle that keeps the fragment reads conflict-free). A ring
-// of SK_NS stages keeps SK_NS - 1 in flight. Wave w takes pair w % 4 of a stage's four k64 pairs and column half
-// w / 4, all 4 row tiles: its A fragments from LDS, its weight fragments straight from memory as in the skinny kernel.
-// The waves' partial sums then meet in the ring's LDS.
+// requests, not the bytes, set the time. Here a CTA owns 64 rows x one 32-column block (CTAs 8 apart, on one XCD,
+// share the block's weights: rows 0-63 and 64-127), so x is read N / 32 times, and everything arrives by LDS DMA in
+// stages of 256 k (SK_STAGE bytes: x, then the block's lo and nib planes for those k, which are contiguous in the
+// packed layout). Each x DMA instruction moves 4 rows x 256 contiguous bytes (8 whole lines), lane L landing at row
+// L / 16, 16-byte chunk position L % 16 of the stage, fetching chunk (L % 16) ^ (row % 16) (the swizzle that keeps the
+// fragment reads conflict-free). Every wave issues the same SK_DMAS DMA instructions per stage and none writes a
+// register, so one s_waitcnt vmcnt per stage, in the instruction stream, is the only wait: a ring of SK_NS stages
+// keeps SK_NS - 1 in flight. Offsets past a buffer (rows past M, k past kp, stages past the end) read as zero, so
+// nothing needs masking. Wave w takes pair w % 4 of a stage's four k64 pairs and column half w / 4, all 4 row tiles,
+// and the row sums of tiles 2 (w / 4) and 2 (w / 4) + 1; the waves' partial sums then meet in the ring's LDS.
 // ------------------------------------------------------------------------------------------------------------------
-constexpr int SK_NS = 8, SK_STAGE = 64 * 256;  // ring stages; bytes of one stage (64 rows x 256 k)
+constexpr int SK_NS = 5, SK_X = 64 * 256, SK_LO = 32 * 256, SK_NIB = 32 * 128;  // ring stages; bytes per stage
+constexpr int SK_STAGE = SK_X + SK_LO + SK_NIB, SK_DMAS = 4;                     // 28 KB; DMAs per wave per stage
 
 template <int OUT>
 __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __restrict__ x,
@@ -877,8 +880,8 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
     const int b = blockIdx.x, rh = (b >> 3) & 1, cb = (b & 7) | ((b >> 4) << 3);
     const int m0 = 64 * rh, n0 = 32 * cb;
     if (n0 >= N) return;  // past the last column block: the whole CTA idles
-    const int KB = kp / 32, np = KB / 2, nst = (np + 3) / 4;  // k32 blocks, k64 pairs, stages of 4 pairs
-    const int Mr = M - m0 < 64 ? M - m0 : 64;                  // rows of this CTA (>= 1: M > 64)
+    const int KB = kp / 32, nst = (kp + 255) / 256;  // k32 blocks, stages
+    const int Mr = M - m0 < 64 ? M - m0 : 64;        // rows of this CTA (>= 1: M > 64)
 
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(wlo + (size_t)cb * KB * 1024, (uint32_t)KB * 1024);
     const __amdgpu_buffer_rsrc_t rN = make_rsrc(wnib + (size_t)cb * KB * 512, (uint32_t)KB * 512);
@@ -886,9 +889,10 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
     const int c = lane & 15, g = lane >> 4, kbq = g >> 1, h = g & 1;
     const int pp = w & 3, ch = w >> 2;  // the wave's pair within a stage; its column half
     const int slot = 16 * ch + c + 32 * h;
-    const uint32_t oL = 16 * slot + 1024 * kbq, oN = 8 * slot + 512 * kbq;
 
-    // DMA lanes: instruction i (0, 1) of wave w moves rows 8 w + 4 i + lane / 16, chunk position lane % 16
+    // DMA lanes. x: instruction i (0, 1) of wave w moves rows 8 w + 4 i + lane / 16, chunk position lane % 16; lo: wave
+    // w moves bytes 1024 w .. 1024 w + 1023 of the stage's 8 KB; nib: lanes 0-31 of wave w move bytes 512 w .. 512 w +
+    // 511 of its 4 KB. Every offset is a VGPR (the SGPR offset stays 0, uniform), so the range check sees all of it.
     uint32_t vX[2];
     int qX[2];
 #pragma unroll
@@ -897,29 +901,32 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
         qX[i] = (lane & 15) ^ (r & 15);
         vX[i] = r < Mr ? (uint32_t)r * (uint32_t)kp + 16u * qX[i] : KT_OOB;  // rows past M read as zero
     }
-    // one stage's 2 DMAs and this wave's weight fragments (4 loads, in this order on every wave); a stage past the
-    // end re-reads the last one (inside every buffer), and chunks past kp read as zero
-    v4i L[SK_NS];
-    v2i D[SK_NS];
+    const uint32_t vL = 1024u * w + 16u * lane, vN = 512u * w + 16u * (lane & 31);
     auto issue = [&](auto S, int st) {
         constexpr int sl = decltype(S)::value;
-        const int sc = st < nst ? st : nst - 1;
-        int8_t* sbuf = ring + sl * SK_STAGE;
-        const uint32_t k0 = 256u * (uint32_t)sc;
+        int8_t* sb = ring + sl * SK_STAGE;
+        const uint32_t k0 = 256u * (uint32_t)st;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const uint32_t v = k0 + 16u * qX[i] < (uint32_t)kp ? vX[i] : KT_OOB;
-            dma16(rX, sbuf + 2048 * w + 1024 * i, v, v == KT_OOB ? 0u : k0);
+            const uint32_t v = vX[i] != KT_OOB && k0 + 16u * qX[i] < (uint32_t)kp ? vX[i] + k0 : KT_OOB;
+            dma16(rX, sb + 2048 * w + 1024 * i, v, 0);
         }
-        const int p = 4 * sc + pp, pl = p < np ? p : np - 1;
-        L[sl] = bload16(rL, oL, (uint32_t)pl * 2048u);
-        D[sl] = bload8(rN, oN, (uint32_t)pl * 1024u);
+        dma16(rL, sb + SK_X + 1024 * w, vL + (uint32_t)SK_LO * st, 0);
+        if (lane < 32) dma16(rN, sb + SK_X + SK_LO + 512 * w, vN + (uint32_t)SK_NIB * st, 0);
     };
 
     v4i acc0[4], acc1[4];
-    int sx[4];
+    int sx0 = 0, sx1 = 0;
 #pragma unroll
-    for (int t = 0; t < 4; t++) acc0[t] = acc1[t] = v4i{}, sx[t] = 0;
+    for (int t = 0; t < 4; t++) acc0[t] = acc1[t] = v4i{};
+    // fragment offsets within a stage
+    int oA[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int R = 16 * t + c, q = 4 * pp + g;
+        oA[t] = R * 256 + ((q ^ (R & 15)) << 4);
+    }
+    const int oL = SK_X + 2048 * pp + 1024 * kbq + 16 * slot, oN = SK_X + SK_LO + 1024 * pp + 512 * kbq + 8 * slot;
 
     static_for<0, SK_NS - 1>([&](auto S) { issue(S, decltype(S)::value); });
     int st = 0;
@@ -928,38 +935,43 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
             constexpr int sl = decltype(S)::value;
             const int s = st + sl;
             if (s < nst) {
-                // stage s has landed once the 4 loads of each of the SK_NS - 2 later stages are all that remain
-                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * (SK_NS - 2)) : "memory");
+                // stage s has landed once the DMAs of the SK_NS - 2 later stages are all that remain
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(SK_DMAS * (SK_NS - 2)) : "memory");
                 // every wave is past stage s - 1: its buffer takes stage s + SK_NS - 1
                 issue(slot_t<(sl + SK_NS - 1) % SK_NS>{}, s + SK_NS - 1);
                 const int8_t* sb = ring + sl * SK_STAGE;
-                const int mask = 4 * s + pp < np ? -1 : 0;  // a pair past the end adds nothing (nor to the row sums)
-                const v4i hi = unpack_hi(D[sl]);
+                v4i a[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) a[t] = *reinterpret_cast<const v4i*>(sb + oA[t]);
+                const v4i lo = *reinterpret_cast<const v4i*>(sb + oL);
+                const v4i hi = unpack_hi(*reinterpret_cast<const v2i*>(sb + oN));
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    const int R = 16 * t + c, q = 4 * pp + g;
-                    const v4i a = *reinterpret_cast<const v4i*>(sb + R * 256 + ((q ^ (R & 15)) << 4)) & mask;
-                    sx[t] += sum4(a);
-                    acc0[t] = mfma16(a, L[sl], acc0[t]);
-                    acc1[t] = mfma16(a, hi, acc1[t]);
+                    acc0[t] = mfma16(a[t], lo, acc0[t]);
+                    acc1[t] = mfma16(a[t], hi, acc1[t]);
                 }
+                if (ch == 0) sx0 += sum4(a[0]), sx1 += sum4(a[1]);
+                else sx0 += sum4(a[2]), sx1 += sum4(a[3]);
             }
         });
         st += SK_NS;
     } while (st < nst);
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is free (re-reads past the end landed)
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the ring is free (stages past the end landed)
 
-    // the wave's partials (64 rows x its 16 columns) and, from the first column half, the row sums, into LDS
+    // the wave's partials (64 rows x its 16 columns) and its two tiles' row sums, into LDS
     int32_t* sP = reinterpret_cast<int32_t*>(ring);  // [8 waves][64 rows][16 columns]
 #pragma unroll
     for (int t = 0; t < 4; t++) {
 #pragma unroll
         for (int r = 0; r < 4; r++)
             sP[(w * 64 + 16 * t + 4 * g + r) * 16 + c] = (int32_t)((uint32_t)acc0[t][r] + ((uint32_t)acc1[t][r] << 8));
-        int sv = sx[t];
+    }
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        int sv = tt ? sx1 : sx0;
         sv += __shfl_xor(sv, 16);
         sv += __shfl_xor(sv, 32);
-        if (ch == 0 && lane < 16) sX[pp][16 * t + lane] = sv;
+        if (lane < 16) sX[pp][16 * (2 * ch + tt) + lane] = sv;
     }
     __syncthreads();
     const int cc = tid & 31, on = n0 + cc;  // every output of this thread is in column on
