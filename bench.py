@@ -215,6 +215,17 @@ def bench_config2(torch, args) -> tuple[dict, tuple, np.ndarray, np.ndarray]:
             "kernel": "w12_skinny" if m <= 128 else "w12_gemm_dma on the W12B planes",
             "launches": n_launch, "warmup_launches": warm,
         }
+        if m == 1:
+            # the read floor of the same bytes: kt_hip_stream_read (the GEMV's 16-byte load form, no compute) over
+            # each weight copy's two planes as one contiguous buffer, the same rotation and launch count
+            flat = [torch.cat([los[j], nibs[j].view(torch.int8)]) for j in range(ROTATE)]
+            xo = torch.empty(T.backend.STREAM_READ_CTAS, dtype=torch.int32, device=dev)
+            ms_r, _ = time_launches(torch, lambda i: T.backend.stream_read(flat[i % ROTATE], flat[0].numel(), xo,
+                                                                           stream=stream), n_launch, warm)
+            sweep[str(m)]["read_floor_us"] = round(ms_r * 1e3, 3)
+            sweep[str(m)]["read_floor"] = (f"kt_hip_stream_read of the {flat[0].numel() / 1e6:.1f} MB of one W12 "
+                                           f"weight copy (both planes), {ROTATE} copies rotated, timed as this GEMV")
+            del flat
         if m == MH:
             headline = (ms, wall, n_launch, warm, us, tops)
             # the same kernel once its clocks have settled under its own load (not the headline value)

@@ -506,6 +506,14 @@ int kt_hip_w12b_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const
                        int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev, int out_kind,
                        void* y_dev, void* stream);
 
+/* A pure read of bytes_n bytes (a multiple of 16, below 2^31) of src_dev with the W12 GEMV's load form (16-byte buffer
+ * loads, 4 per thread in flight, KT_STREAM_READ_CTAS CTAs over contiguous chunks); out_dev (KT_STREAM_READ_CTAS
+ * uint32, device) receives each chunk's XOR of 32-bit words. A measurement aid with no counterpart in the reference:
+ * the time memory takes to deliver a weight matrix's bytes to this load form with no compute, beside the GEMVs that
+ * stream the same bytes. */
+#define KT_STREAM_READ_CTAS 256
+int kt_hip_stream_read(int dev, const uint8_t* src_dev, int64_t bytes_n, uint32_t* out_dev, void* stream);
+
 /* As kt_hip_w12_linear with out_kind KT_OUT_I8, then each int8 output q replaced by lut_dev[q + 127] (255 int8
  * entries, device): an activation-code table applied in the epilogue (the GELU of config 5's FeedForward,
  * crates/03-models/kt-model-vision/src/hiera.rs:336-340 with nonlin.rs:30-47, as an int8 code table).

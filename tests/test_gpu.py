@@ -255,6 +255,27 @@ def test_w12_pack_matches_the_oracle_layout(torch_dev):
         _w12_device(torch, np.array([2048], np.int32), 1, 1)
 
 
+def test_stream_read_touches_every_byte(torch_dev):
+    """kt_hip_stream_read (the read-floor probe): the XOR of its per-chunk words is the XOR of every 32-bit word of
+    the buffer, for empty, one-load, ragged-chunk and config-2-sized buffers; a length that is not a multiple of 16
+    is refused."""
+    torch = torch_dev
+    T = tb()
+    rng = np.random.default_rng(3)
+    out = torch.empty(T.backend.STREAM_READ_CTAS, dtype=torch.int32, device="cuda")
+    for nbytes in (0, 16, 16 * 1001, 4096 * 4096 * 3 // 2):
+        buf = rng.integers(-(2**31), 2**31, size=max(nbytes // 4, 1), dtype=np.int64).astype(np.int32)[: nbytes // 4]
+        src = torch.from_numpy(buf.copy() if nbytes else np.zeros(4, np.int32)).cuda()
+        say(f"case: stream read {nbytes} bytes")
+        out.fill_(0x5A5A5A5A)
+        T.backend.stream_read(src, nbytes, out)
+        torch.cuda.synchronize()
+        want = np.bitwise_xor.reduce(buf.view(np.uint32)) if nbytes else np.uint32(0)
+        assert np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32)) == want, nbytes
+    with pytest.raises(T.HipError):
+        T.backend.stream_read(src, 24, out)
+
+
 @pytest.mark.parametrize("out_kind", [0, 1, 2])
 def test_w12_linear_against_the_oracle(torch_dev, out_kind):
     """GEMV (m <= 8) and MFMA GEMM (m > 8) for tails in m, n and k, every output kind."""

@@ -80,6 +80,7 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_w12b_bytes": (None, [_I64, _I64, C.POINTER(_SZ)]),
         "kt_hip_w12b_pack": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
         "kt_hip_w12b_linear": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I, _P, _P]),
+        "kt_hip_stream_read": (_I, [_I, _P, _I64, _P, _P]),
         "kt_hip_probe_mfma": (_I, [_I, _P, _P, _P, _P, _P]),
         "kt_hip_w12_linear_lut": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
         "kt_hip_w12_pack_gate_up": (_I, [_I, _P, _I64, _I64, _P, _P, _P]),
@@ -366,6 +367,15 @@ def w12b_linear(x_dev, lo_dev, hi_dev, m: int, n: int, k: int, y_dev, out_kind: 
                                  _ptr(shift_dev), out_kind, _ptr(y_dev), _stream(stream)),
         "w12b linear",
     )
+
+
+STREAM_READ_CTAS = 256  # KT_STREAM_READ_CTAS
+
+
+def stream_read(src_dev, nbytes: int, out_dev, stream=None, dev: int = 0) -> None:
+    """A pure read of nbytes (a multiple of 16) of src_dev with the GEMV's load form; out_dev (STREAM_READ_CTAS
+    uint32) receives each chunk's XOR of 32-bit words. A measurement aid. Asynchronous."""
+    check(lib().kt_hip_stream_read(dev, _ptr(src_dev), nbytes, _ptr(out_dev), _stream(stream)), "stream read")
 
 
 def digit_gemm(xa_dev, px: int, wb_dev, pw: int, y_dev, rows: int, out: int, k: int, flush: int = 0,

@@ -576,6 +576,14 @@ int kt_hip_w12b_linear(int dev, const int8_t* x_dev, const int8_t* lo_dev, const
                                        y_dev, (hipStream_t)stream);
 }
 
+int kt_hip_stream_read(int dev, const uint8_t* src_dev, int64_t bytes_n, uint32_t* out_dev, void* stream) {
+    if (bytes_n < 0 || bytes_n % 16 || bytes_n >= ((int64_t)1 << 31) || out_dev == nullptr ||
+        (bytes_n > 0 && src_dev == nullptr))
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_stream_read(src_dev, (uint32_t)bytes_n, out_dev, (hipStream_t)stream);
+}
+
 int kt_hip_w12_linear_lut(int dev, const int8_t* x_dev, const int8_t* lo_dev, const uint8_t* nib_dev, int64_t m,
                           int64_t n, int64_t k, const int32_t* mant_dev, const int32_t* shift_dev,
                           const int8_t* lut_dev, int8_t* y_dev, void* stream) {

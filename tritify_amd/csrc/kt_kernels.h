@@ -25,6 +25,7 @@ int plane_gemm_cta_cols(int px, int pw, int M, int N);
 // launch needs y zeroed, one zeroed counter per tile (the grid's tiles: at most 128) and accumulate = 0.
 int plane_gemm_splits(int px, int pw, int M, int N, int k0, int k1);
 hipError_t launch_w12b_pack(const int32_t* codes, int64_t n, int64_t k, int8_t* lo, int8_t* hi, hipStream_t s);
+hipError_t launch_stream_read(const uint8_t* src, uint32_t bytes, uint32_t* out, hipStream_t s);
 hipError_t launch_w12b_linear(const int8_t* x, const int8_t* lo, const int8_t* hi, int M, int N, int kp,
                               const int32_t* mant, const int32_t* shift, int out_kind, void* y, hipStream_t s);
 hipError_t launch_w12_linear(const int8_t* x, const int8_t* lo, const uint8_t* nib, int M, int N, int kp,

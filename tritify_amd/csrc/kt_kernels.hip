@@ -1536,6 +1536,44 @@ hipError_t launch_w12_linear_add_o(const int8_t* x, const int8_t* lo, const uint
     return hipGetLastError();
 }
 
+// A pure read of `bytes` (a multiple of 16) with the GEMV's load form: KT_STREAM_READ_CTAS CTAs of 512 threads, CTA b
+// over the b-th contiguous chunk (a multiple of 16 bytes), 16-byte buffer loads, 4 per thread in flight before any is
+// used; out[b] = the XOR of the chunk's 32-bit words (so no load can be dropped). A measurement of what the memory
+// delivers to this load form with no compute, beside the products that stream the same bytes. (Over 25 MB, a sweep of
+// 4-32 loads per thread, 256-1024 threads and 256-2048 CTAs found none faster than this shape by more than 1%.)
+__global__ __launch_bounds__(512) void stream_read_kernel(const uint8_t* __restrict__ src, uint32_t bytes,
+                                                          uint32_t chunk, uint32_t* __restrict__ out) {
+    __shared__ uint32_t red[8];
+    const uint32_t b = blockIdx.x, off = b * chunk;
+    const uint32_t len = off >= bytes ? 0u : (bytes - off < chunk ? bytes - off : chunk);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src + (len ? off : 0u), len);  // loads past len read as zero
+    v4i acc = {};
+    for (uint32_t o = 16u * threadIdx.x; o < len; o += 4u * 512u * 16u) {
+        v4i v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = bload16(r, o + (uint32_t)u * 512u * 16u, 0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u];
+    }
+    uint32_t x = (uint32_t)(acc.x ^ acc.y ^ acc.z ^ acc.w);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) x ^= (uint32_t)__shfl_xor((int)x, d);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) t ^= red[q];
+        out[b] = t;
+    }
+}
+
+hipError_t launch_stream_read(const uint8_t* src, uint32_t bytes, uint32_t* out, hipStream_t s) {
+    const uint32_t chunk = (uint32_t)ceil_div(ceil_div((int64_t)bytes, KT_STREAM_READ_CTAS), 16) * 16u;
+    stream_read_kernel<<<dim3(KT_STREAM_READ_CTAS), dim3(512), 0, s>>>(src, bytes, chunk ? chunk : 16u, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_mfma_probe(const int8_t* a, const int8_t* b, int32_t* c32, int32_t* c16, hipStream_t s) {
     mfma_probe_kernel<<<dim3(1), dim3(64), 0, s>>>(a, b, c32, c16);
     return hipGetLastError();
