@@ -507,6 +507,49 @@ def test_ref_attention_prefill_against_the_oracle(torch_dev, nh, nkv, hd, T, max
     assert rd(os_) == os_want
 
 
+def test_ref_attention_prefill_thirds_closed_form(torch_dev):
+    """The device prefill attention on the closed-form case of the oracle's pin (k = 0, v in {-1, 0, 1}, three
+    rows: row r averages r + 1 positions, row 2 brought to the common scale by the Scale nearest 1/3): out =
+    2^8 * (2^20 S_0, 2^19 S_1, rha(2^20 S_2, 3)), every unit of the per-row rounding visible."""
+    torch = torch_dev
+    from tritify_amd import backend as B
+
+    nh, nkv, hd, T, max_seq = 4, 2, 8, 3, 16
+    say(f"case: ref attention prefill thirds T={T}")
+    rng = np.random.default_rng(33)
+    q = rng.integers(-(2**28), 2**28, size=(T, nh, hd)).astype(np.int32)
+    k = np.zeros((T, nkv, hd), np.int32)
+    v = rng.integers(-1, 2, size=(T, nkv, hd)).astype(np.int32)
+    v[0, 0, 0] = 1
+    v[:, 1, :6] = [[1, 1, 1, -1, -1, -1], [1, 0, 1, -1, 0, -1], [0, 0, 1, 0, 0, -1]]
+    qs, ks, vs = (1 << 30, 40), (1 << 30, 40), (1 << 31, 50)
+    cos_t, sin_t = B.ref_rope_tables(max_seq, hd, 1.0e6)
+    exp_codes, exp_lut = B.ref_codelut(B.LUT_EXP, -30.0, 0.0, 16, 20, False)
+    n = B.ref_attention_prefill_workspace(T, nh, nkv, hd)
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    o, os_ = torch.zeros(T * nh * hd, dtype=torch.int32, device="cuda"), rec(torch, (0, 0))
+    B.ref_attention_prefill(dev_i32(torch, q.ravel()), rec(torch, qs), dev_i32(torch, k.ravel()), rec(torch, ks),
+                            dev_i32(torch, v.ravel()), rec(torch, vs), T, nh, nkv, hd, max_seq,
+                            torch.from_numpy(cos_t.view(np.uint8)).cuda(),
+                            torch.from_numpy(sin_t.view(np.uint8)).cuda(), B.ref_scale_from_f64(1.0 / np.sqrt(hd)),
+                            torch.from_numpy(exp_codes).cuda(), exp_lut, ws, n, o, os_)
+    got = o.cpu().numpy().reshape(T, nh, hd)
+
+    def rha(a, b):
+        r = (2 * abs(a) + b) // (2 * b)
+        return r if a >= 0 else -r
+
+    for h in range(nh):
+        for d in range(hd):
+            s0 = int(v[0, h // 2, d])
+            s1, s2 = s0 + int(v[1, h // 2, d]), s0 + int(v[1, h // 2, d]) + int(v[2, h // 2, d])
+            assert [int(got[r, h, d]) for r in range(3)] == [2**28 * s0, 2**27 * s1, 2**8 * rha(2**20 * s2, 3)], (h, d)
+    m = O.RefModel(3, dict(dim=nh * hd, layers=1, nh=nh, nkv=nkv, hd=hd, hidden=16, vocab=8, eps=1e-6, theta=1.0e6,
+                           max_seq=max_seq))
+    o_want, os_want = m.attention_prefill(T, q.ravel(), qs, k.ravel(), ks, v.ravel(), vs)
+    assert np.array_equal(got.ravel(), o_want) and rd(os_) == os_want
+
+
 @pytest.mark.parametrize("case", ["synthetic", "d00d", "qwen2"])
 def test_ref_forward_against_the_oracle(torch_dev, case):
     """CausalLM::forward_int of whole sequences on the device against the oracle's restatement: the seed-7

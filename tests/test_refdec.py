@@ -374,6 +374,38 @@ def test_prefill_attention_two_rows_uniform_softmax_is_exact():
     assert _sval(os_) == Fraction(g, 2**28) * _sval(vs) / 2**20
 
 
+def test_prefill_attention_thirds_round_half_away_per_row():
+    """k = 0 over three rows: row r averages its r + 1 positions (sumc = (r + 1) 2^20). Every row's sum is brought
+    to the common scale v / 2^20 by f = 1, 1/2 and, for row 2, the Scale nearest 1/3 (attention.rs:560-590); with
+    v in {-1, 0, 1} the products 2^20 S / 3 sit at a third or two thirds past an integer, far from any half, so
+    Scale::apply's round-half-away gives rha(2^20 S, 3) (a truncating apply, or one rounding the wrong way, differs
+    on every S = 2 mod 3). One code of 1 in row 0 makes the largest |value| 2^20, so requant_dyn multiplies by 2^8
+    exactly and no later rounding hides a unit of the per-row step."""
+    m = O.RefModel(3, PREFILL_CFG)
+    T, nh, nkv, hd = 3, 4, 2, 8
+    rng = np.random.default_rng(33)
+    q = rng.integers(-(2**28), 2**28, size=(T, nh, hd))
+    k = np.zeros((T, nkv, hd), np.int64)
+    v = rng.integers(-1, 2, size=(T, nkv, hd))
+    v[0, 0, 0] = 1
+    v[:, 1, :6] = [[1, 1, 1, -1, -1, -1], [1, 0, 1, -1, 0, -1], [0, 0, 1, 0, 0, -1]]  # S_2 = 2, 1, 3, -2, -1, -3
+    vs = (1 << 31, 50)
+    o, os_ = m.attention_prefill(T, q.astype(np.int32).ravel(), (1 << 30, 40), k.astype(np.int32).ravel(),
+                                 (1 << 30, 40), v.astype(np.int32).ravel(), vs)
+    o = o.reshape(T, nh, hd)
+    for h in range(nh):
+        g = h // 2
+        for d in range(hd):
+            s0 = int(v[0, g, d])
+            s1 = s0 + int(v[1, g, d])
+            s2 = s1 + int(v[2, g, d])
+            assert int(o[0, h, d]) == 2**8 * 2**20 * s0, (h, d)
+            assert int(o[1, h, d]) == 2**8 * 2**19 * s1, (h, d)
+            assert int(o[2, h, d]) == 2**8 * _rha(2**20 * s2, 3), (h, d, s2)
+    assert o[2, 2, :6].tolist() == [2**8 * x for x in (699051, 349525, 2**20, -699051, -349525, -(2**20))]
+    assert _sval(os_) == _sval(vs) / 2**28
+
+
 def test_batched_forward_is_the_composition_of_its_pinned_ops():
     """CausalLM::forward_int over T tokens (model.rs:361-367: embed_int, blocks_int, head_int; each block x + attn
     (input_norm(x)), then + ffn(post_norm(x)), model.rs:175-183; SwiGluMlp layers.rs:609-640) composed here from the
