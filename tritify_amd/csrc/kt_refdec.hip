@@ -143,34 +143,41 @@ __device__ inline ScIdx sc_pick(ScIdx a, ScIdx b) {
     if (ab && ba) return a.idx > b.idx ? a : b;
     return ba ? b : a;
 }
-// n: how many leading threads hold items (the rest hold idx -1). sc_pick orders (value, index) totally, so any
-// reduction order gives the fold's result: up to 64 items by a butterfly in wave 0, more by a tree in LDS.
+// n: how many leading threads hold items (the rest hold idx -1); every thread of the CTA calls it. The fold is by
+// value, then by index: each Scale is normalized exactly to m * 2^-e with m's top bit set (a zero Scale: the
+// smallest key), so comparing values (sc_ge) is comparing (e, m) as integers, and three block maxima -- the largest
+// e, the largest m at it, the largest index among equal values (the fold's later-wins rule) -- find sc_pick's total
+// order's maximum with no Scale arithmetic in the tree. The winner's own Scale is returned. Ends with a barrier.
 __device__ ScIdx block_fold_max(ScIdx v, ScIdx* red, int n) {
-    if (n <= 64) {
-        if (threadIdx.x < 64) {
+    (void)n;
+    int64_t* r64 = reinterpret_cast<int64_t*>(red);  // 3 x RD_WAVES maxima, then the winner at red[RD_THREADS - 1]
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const bool live = v.idx >= 0 && v.s.mant != 0;
+    const uint64_t a = (uint64_t)v.s.mant;
+    const int lz = live ? __builtin_clzll(a) : 0;
+    const int64_t e = live ? -(int64_t)v.s.shift - lz : INT64_MIN;
+    const uint64_t m = live ? a << lz : 0;
+    auto bmax = [&](uint64_t x, int slot, bool is_signed) -> uint64_t {  // a block maximum, signed or unsigned
+        auto gt = [&](uint64_t p, uint64_t q) { return is_signed ? (int64_t)p > (int64_t)q : p > q; };
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                ScIdx u;
-                u.s.mant = __shfl_xor(v.s.mant, o, 64), u.s.shift = __shfl_xor(v.s.shift, o, 64);
-                u.idx = __shfl_xor(v.idx, o, 64);
-                v = sc_pick(v, u);
-            }
-            if (threadIdx.x == 0) red[0] = v;
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t u = (uint64_t)__shfl_xor((long long)x, o, 64);
+            x = gt(u, x) ? u : x;
         }
+        if (lane == 0) r64[slot * RD_WAVES + w] = (int64_t)x;
         __syncthreads();
-        v = red[0];
-        __syncthreads();
-        return v;
-    }
-    red[threadIdx.x] = v;
+        uint64_t r = (uint64_t)r64[slot * RD_WAVES];
+        for (int q = 1; q < RD_WAVES; q++) r = gt((uint64_t)r64[slot * RD_WAVES + q], r) ? (uint64_t)r64[slot * RD_WAVES + q] : r;
+        return r;
+    };
+    const int64_t emax = (int64_t)bmax((uint64_t)e, 0, true);
+    const uint64_t mmax = bmax(e == emax ? m : 0, 1, false);
+    const int64_t imax = (int64_t)bmax((uint64_t)(int64_t)(e == emax && m == mmax && v.idx >= 0 ? v.idx : -1), 2, true);
+    if (imax >= 0 && v.idx == imax) red[RD_THREADS - 1] = v;
     __syncthreads();
-    for (int s = RD_THREADS / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = sc_pick(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    v = red[0];
+    const ScIdx r = imax >= 0 ? red[RD_THREADS - 1] : ScIdx{Sc{0, 0}, -1};
     __syncthreads();
-    return v;
+    return r;
 }
 
 // CodeLut::index / code_at (kt-int/src/lib.rs:382-395) with the call's factor m = scale * inv_step.
