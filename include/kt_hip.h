@@ -287,11 +287,12 @@ int kt_hip_ref_attention_step(int dev, const int32_t* q_dev, const kt_hip_qscale
                               const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev, int64_t isq_mant,
                               int32_t isq_shift, const int64_t* exp_codes_dev, const kt_hip_codelut* exp_lut,
                               int32_t* o_dev, kt_hip_qscale* os_dev, void* stream);
-/* kt_hip_ref_attention_step with a workspace: one CTA per q head (the cache reads, the per-step Scale work and P.V
- * spread over nh CUs; the heads then brought to one scale by a second launch), for caches of any length up to
+/* kt_hip_ref_attention_step with a workspace: several CTAs per q head (the cache reads and the per-step Scale work of
+ * the head in each, P.V split between them: up to 128 CTAs in all; the parts added and the heads brought to one scale
+ * by a second launch), for caches of any length up to
  * KT_REF_ATTN_MAX_SEQ (the reference's MAX_SEQ_CAP = 4096, crates/03-models/kt-model-decoder/src/lib.rs:46, and
  * beyond). ws_dev: a caller buffer of at least kt_hip_ref_attention_step_workspace(max_seq, nh, hd) bytes,
- * 16-byte aligned (per head: its output and scale, and 40 B per cached position). With ws_dev null this is
+ * 16-byte aligned (per head: its output parts and scale, and 40 B per cached position and CTA). With ws_dev null this is
  * kt_hip_ref_attention_step (one CTA, max_seq bounded by its LDS). The same integers either way. Calls that share
  * ws_dev must be ordered. */
 size_t kt_hip_ref_attention_step_workspace(int64_t max_seq, int64_t nh, int64_t hd);

@@ -805,7 +805,7 @@ def ref_attention_prefill(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, T: int, n
 
 
 def ref_attention_step_workspace(max_seq: int, nh: int, hd: int) -> int:
-    """Bytes of the workspace of the one-CTA-per-head attention step (kt_hip_ref_attention_step_ws)."""
+    """Bytes of the workspace of the several-CTAs-per-head attention step (kt_hip_ref_attention_step_ws)."""
     return lib().kt_hip_ref_attention_step_workspace(max_seq, nh, hd)
 
 
@@ -820,8 +820,8 @@ REF_ATTN_LDS = 65536  # KT_REF_ATTN_LDS
 def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh: int, nkv: int, hd: int,
                        max_seq: int, kc_dev, vc_dev, kscale_dev, vscale_dev, cos_dev, sin_dev, inv_sqrt,
                        exp_codes_dev, exp_lut: CodeLut, o_dev, os_dev, stream=None, dev: int = 0, ws_dev=None) -> None:
-    """Attention::decode_step's core at position pos_dev[0]: with ws_dev (ref_attention_step_workspace bytes) one CTA
-    per head, any max_seq; without, one CTA whose LDS bounds max_seq (ref_attention_step_fits_lds)."""
+    """Attention::decode_step's core at position pos_dev[0]: with ws_dev (ref_attention_step_workspace bytes) several
+    CTAs per head, any max_seq; without, one CTA whose LDS bounds max_seq (ref_attention_step_fits_lds)."""
     ws_bytes = 0 if ws_dev is None else ws_dev.numel() * ws_dev.element_size()
     check(lib().kt_hip_ref_attention_step_ws(dev, _ptr(q_dev), _ptr(qs_dev), _ptr(k_dev), _ptr(ks_dev),
                                              _ptr(v_dev), _ptr(vs_dev), _ptr(pos_dev), nh, nkv, hd, max_seq,

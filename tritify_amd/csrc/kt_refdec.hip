@@ -837,28 +837,35 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_step_kernel(RdAttn a)
     rd_attention_core(a, lds, sh_, pos, a.hb);
 }
 
-// Attention::decode_step between its projections with one CTA per q head, for caches of any length up to max_seq
-// (kt_hip_ref_attention_step_ws): the cache reads, the per-step Scale work and P.V spread over nh CUs instead of one.
-// rd_attention_heads_kernel (CTA h): RoPE of q_h and of this step's k (the first CTA of each kv group appends the
-// step's k and v rows to the cache, CTA 0 the step's scales; row pos is taken from the inputs by every CTA, so no
-// CTA reads what another writes in the same launch); every step's score factor f_j = s_j / s_ref and v factor
-// vf_j = vs_j / v_ref (the same integers in every CTA); its head's scores, integer softmax and P.V; the head's output
-// codes and scale v_ref / sumc into the workspace. rd_attention_combine_kernel (one CTA, the next launch): the heads
-// at their largest scale, requantized -- step 4 of the one-CTA kernel.
+// Attention::decode_step between its projections with L.parts CTAs per q head, for caches of any length up to
+// max_seq (kt_hip_ref_attention_step_ws): the cache reads, the per-step Scale work and P.V spread over nh * parts CUs
+// instead of one. rd_attention_heads_kernel (CTA h * parts + part): RoPE of q_h and of this step's k (part 0 of the
+// first head of each kv group appends the step's k and v rows to the cache, part 0 of head 0 the step's scales; row
+// pos is taken from the inputs by every CTA, so no CTA reads what another writes in the same launch); every step's
+// score factor f_j = s_j / s_ref and v factor vf_j = vs_j / v_ref, its head's scores, maximum and integer softmax
+// numerators (the same integers in every CTA of the head); P.V over its share of the steps (P.V's 64-bit products
+// are the step's largest cost, so they are what the parts divide); its part of the head's sums, and (part 0) the
+// head's scale v_ref / sumc, into the workspace. rd_attention_combine_kernel (one CTA, the next launch): each head's
+// parts added (wrapping, exact in any order), the heads at their largest scale, requantized -- step 4 of the one-CTA
+// kernel.
 struct RdHeadsLayout {
-    size_t ho, hsc, arr, arr_stride;  // byte offsets: head outputs, head scales, per-head step arrays (and stride)
+    size_t ho, hsc, arr, arr_stride;  // byte offsets: head output parts, head scales, per-CTA step arrays (and stride)
+    int parts;                        // CTAs per head: each sums P.V over its share of the steps
 };
 __host__ __device__ inline size_t rd_round256(size_t v) { return (v + 255) / 256 * 256; }
 __host__ __device__ inline RdHeadsLayout rd_heads_layout(int max_seq, int nh, int hd) {
     RdHeadsLayout L;
+    L.parts = 128 / nh < 1 ? 1 : (128 / nh > 8 ? 8 : 128 / nh);  // 8 CTAs per head at the Qwen shape (112 CTAs)
     L.ho = 0;
-    L.hsc = rd_round256((size_t)nh * hd * sizeof(int64_t));
+    L.hsc = rd_round256((size_t)nh * L.parts * hd * sizeof(int64_t));
     L.arr = L.hsc + rd_round256((size_t)nh * sizeof(Sc));
     L.arr_stride = rd_round256((size_t)max_seq * (2 * sizeof(Sc) + sizeof(int64_t)));
     return L;
 }
 
-constexpr int RD_PV_U = 8;  // cached v values (and their steps' numerators and factors) loaded before the products
+// cached v values (and their steps' numerators and factors) loaded before the products; RD_PV_W: the v values a lane
+// of the wave-uniform P.V path has in flight
+constexpr int RD_PV_U = 8, RD_PV_W = 16;
 // The heads kernel's dynamic LDS when its per-step arrays stay in LDS (max_seq up to about 2,400 at head_dim 64; the
 // static part is about 33 KB).
 constexpr size_t RD_HEADS_LDS = 96 * 1024;
@@ -872,21 +879,22 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     __shared__ Sc sinv_s;
     __shared__ int64_t PV[RD_THREADS];
     extern __shared__ __align__(16) int32_t qk[];  // the rotated q_h (hd), then this step's rotated k (hd)
-    const int h = blockIdx.x, tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv;
+    const int P = L.parts, h = (int)blockIdx.x / P, part = (int)blockIdx.x % P;
+    const int tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv;
     const int group = nh / nkv, kv = h / group, kstride = nkv * hd;
     const int pos = *a.pos;
     unsigned char* ws = a.ws;
     int64_t* HO = reinterpret_cast<int64_t*>(ws + L.ho);
     Sc* HSC = reinterpret_cast<Sc*>(ws + L.hsc);
     if (pos < 0 || pos >= a.max_seq) {  // outside the tables: the combine writes zeros
-        for (int d = tid; d < hd; d += RD_THREADS) HO[(size_t)h * hd + d] = 0;
-        if (tid == 0) HSC[h] = Sc{0, 0};
+        for (int d = tid; d < hd; d += RD_THREADS) HO[((size_t)h * P + part) * hd + d] = 0;
+        if (tid == 0 && part == 0) HSC[h] = Sc{0, 0};
         return;
     }
     const int steps = pos + 1;
     int32_t* QD = qk;
     int32_t* KP = qk + hd;
-    unsigned char* arr = GA ? ws + L.arr + (size_t)h * L.arr_stride
+    unsigned char* arr = GA ? ws + L.arr + ((size_t)h * P + part) * L.arr_stride
                             : reinterpret_cast<unsigned char*>(qk) + (size_t)rd_round256(2 * (size_t)hd * 4);
     Sc* F = reinterpret_cast<Sc*>(arr);                        // score factors, per step
     Sc* VF = F + a.max_seq;                                    // v factors, per step
@@ -904,12 +912,12 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         KP[j + half] = (int32_t)(c.sign * sc_apply32(cm, kb) + sn.sign * sc_apply32(sm, ka));
     }
     __syncthreads();
-    if (h == kv * group)
+    if (h == kv * group && part == 0)
         for (int i = tid; i < hd; i += RD_THREADS) {
             a.kc[(size_t)pos * kstride + kv * hd + i] = KP[i];
             a.vc[(size_t)pos * kstride + kv * hd + i] = a.v[kv * hd + i];
         }
-    if (h == 0 && tid == 0) {
+    if (h == 0 && part == 0 && tid == 0) {
         a.kscale[pos] = kt_hip_sscale{a.ks->mant, a.ks->shift, 1};
         a.vscale[pos] = kt_hip_sscale{a.vs->mant, a.vs->shift, 1};
     }
@@ -937,8 +945,8 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     __syncthreads();
     const Sc v_ref = par[0], s_ref = par[1], lm = par[2], vinv = par[3], sinv = sinv_s;
     if (s_ref.mant == 0) {  // the head is skipped (the reference's `continue`): zeros at Scale::ZERO
-        for (int d = tid; d < hd; d += RD_THREADS) HO[(size_t)h * hd + d] = 0;
-        if (tid == 0) HSC[h] = Sc{0, 0};
+        for (int d = tid; d < hd; d += RD_THREADS) HO[((size_t)h * P + part) * hd + d] = 0;
+        if (tid == 0 && part == 0) HSC[h] = Sc{0, 0};
         return;
     }
 
@@ -951,7 +959,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         if (j == pos) {
             for (int d = 0; d < hd; d++) dot = wadd(dot, (int64_t)QD[d] * KP[d]);
         } else if (vec) {
-            // 8 x 16 bytes of the cache row in flight at a time
+            // 8 x 16 bytes of the cache row in flight at a time (16 spill registers)
             const int4* kr = reinterpret_cast<const int4*>(a.kc + (size_t)j * kstride + kv * hd);
             for (int e4 = 0; e4 < hd / 4; e4 += 8) {
                 int4 kk[8];
@@ -990,8 +998,8 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     int64_t sumc = 0;
     for (int w = 0; w < RD_WAVES; w++) sumc += red[w];
     if (sumc <= 0) {
-        for (int d = tid; d < hd; d += RD_THREADS) HO[(size_t)h * hd + d] = 0;
-        if (tid == 0) HSC[h] = Sc{0, 0};
+        for (int d = tid; d < hd; d += RD_THREADS) HO[((size_t)h * P + part) * hd + d] = 0;
+        if (tid == 0 && part == 0) HSC[h] = Sc{0, 0};
         return;
     }
 
@@ -999,32 +1007,67 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     //    any order gives the reference's integers); the slices then add up in LDS
     const int slices = RD_THREADS / hd, d = tid % hd, js = tid / hd;
     int64_t acc = 0;
-    if (js < slices) {
+    if (hd % 64 == 0) {
+        // a wave is one slice: its step, numerator and v factor are the same on every lane, so they are read once
+        // into scalar registers and Scale::apply's branches and shift amounts are scalar
+        // The cached v rows come from HBM (the weight streams evicted them since the previous token): RD_PV_W of
+        // them in flight per lane at a time, so that a few dependent round trips, not one per RD_PV_U steps, pay
+        // for the whole column.
+        // slice jw of this CTA's share: the steps j = part * slices + jw (mod P * slices)
+        const int jw = __builtin_amdgcn_readfirstlane(js), ST = P * slices;
+        if (jw < slices) {
+            const int32_t* vcol = a.vc + kv * hd + d;
+            for (int j0 = part * slices + jw; j0 < steps; j0 += RD_PV_W * ST) {
+                int32_t vv[RD_PV_W];
+#pragma unroll
+                for (int u = 0; u < RD_PV_W; u++) {  // a step past the end reads the last one and adds nothing
+                    const int j = j0 + u * ST < steps ? j0 + u * ST : steps - 1;
+                    vv[u] = j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride];
+                }
+#pragma unroll
+                for (int u = 0; u < RD_PV_W; u++) {
+                    const int j = j0 + u * ST;
+                    if (j < steps) {  // uniform
+                        const int64_t e = S[j];
+                        const Sc f = VF[j];
+                        const int64_t ec = ((int64_t)__builtin_amdgcn_readfirstlane((int)((uint64_t)e >> 32)) << 32) |
+                                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)e);
+                        Sc vf;
+                        vf.mant = ((int64_t)__builtin_amdgcn_readfirstlane((int)((uint64_t)f.mant >> 32)) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)f.mant);
+                        vf.shift = __builtin_amdgcn_readfirstlane(f.shift);
+                        acc = wadd(acc, wmul(ec, sc_apply32(vf, vv[u])));
+                    }
+                }
+            }
+        }
+    } else if (js < slices) {
+        const int ST = P * slices;
         const int32_t* vcol = a.vc + kv * hd + d;
-        for (int j0 = js; j0 < steps; j0 += RD_PV_U * slices) {
+        for (int j0 = part * slices + js; j0 < steps; j0 += RD_PV_U * ST) {
             int32_t vv[RD_PV_U];
             int64_t ec[RD_PV_U];
             Sc vf[RD_PV_U];
 #pragma unroll
             for (int u = 0; u < RD_PV_U; u++) {  // a step past the end reads the last one and adds nothing
-                const int j = j0 + u * slices < steps ? j0 + u * slices : steps - 1;
+                const int j = j0 + u * ST < steps ? j0 + u * ST : steps - 1;
                 vv[u] = j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride];
                 ec[u] = S[j];
                 vf[u] = VF[j];
             }
 #pragma unroll
             for (int u = 0; u < RD_PV_U; u++)
-                if (j0 + u * slices < steps) acc = wadd(acc, wmul(ec[u], sc_apply32(vf[u], vv[u])));
+                if (j0 + u * ST < steps) acc = wadd(acc, wmul(ec[u], sc_apply32(vf[u], vv[u])));
         }
     }
     PV[tid] = acc;
     __syncthreads();
-    for (int dd = tid; dd < hd; dd += RD_THREADS) {
+    for (int dd = tid; dd < hd; dd += RD_THREADS) {  // this CTA's part of the head's sums (the combine adds the parts)
         int64_t t = 0;
         for (int q = 0; q < slices; q++) t = wadd(t, PV[q * hd + dd]);
-        HO[(size_t)h * hd + dd] = t;
+        HO[((size_t)h * P + part) * hd + dd] = t;
     }
-    if (tid == 0) HSC[h] = sc_mul(v_ref, from_ratio(1, (u128)(uint64_t)sumc));
+    if (tid == 0 && part == 0) HSC[h] = sc_mul(v_ref, from_ratio(1, (u128)(uint64_t)sumc));
 }
 
 // Step 4 of Attention::decode_step over the heads kernel's outputs: the heads' largest scale by the engine's fold,
@@ -1032,15 +1075,22 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
 __global__ __launch_bounds__(RD_THREADS) void rd_attention_combine_kernel(RdAttn a, RdHeadsLayout L) {
     __shared__ int64_t red[RD_WAVES];
     __shared__ ScIdx redsc[RD_THREADS];
-    const int tid = threadIdx.x, hd = a.hd, nh = a.nh, qstride = nh * hd;
-    const int64_t* HO = reinterpret_cast<const int64_t*>(a.ws + L.ho);
+    const int tid = threadIdx.x, hd = a.hd, nh = a.nh, qstride = nh * hd, P = L.parts;
+    const int64_t* HOP = reinterpret_cast<const int64_t*>(a.ws + L.ho);
     const Sc* HSC = reinterpret_cast<const Sc*>(a.ws + L.hsc);
+    // each head's sums: its CTAs' parts added (wrapping, in any order: the reference's integers)
+    auto ho = [&](int i) {
+        const int hh = i / hd, dd = i - hh * hd;
+        int64_t t = 0;
+        for (int q = 0; q < P; q++) t = wadd(t, HOP[((size_t)hh * P + q) * hd + dd]);
+        return t;
+    };
     const Sc common = block_fold_max(tid < nh ? ScIdx{HSC[tid], tid} : ScIdx{Sc{0, 0}, -1}, redsc, nh).s;
     int64_t m = 0;
     if (common.mant != 0) {
         const Sc cinv = sc_recip(common);
         for (int i = tid; i < qstride; i += RD_THREADS) {
-            const int64_t v = sc_apply(sc_mul(HSC[i / hd], cinv), HO[i]);
+            const int64_t v = sc_apply(sc_mul(HSC[i / hd], cinv), ho(i));
             m = iabs(v) > m ? iabs(v) : m;
         }
     }
@@ -1050,7 +1100,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_combine_kernel(RdAttn
         for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = 0;
     } else {
         const Sc cinv = sc_recip(common);
-        for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = rq_apply(rd_gmax, sc_apply(sc_mul(HSC[i / hd], cinv), HO[i]));
+        for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = rq_apply(rd_gmax, sc_apply(sc_mul(HSC[i / hd], cinv), ho(i)));
     }
     if (tid == 0)
         put_rec(a.os, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common));
@@ -1422,7 +1472,7 @@ hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, 
     rd_gelu_kernel<<<(unsigned)(g < 1 ? 1 : (g > 4096 ? 4096 : g)), RD_THREADS, 0, s>>>(x, xs, n, codes, *lut, y, ys);
     return hipGetLastError();
 }
-// With a workspace: the heads kernel (one CTA per q head) and the combine. Without: the one-CTA kernel, its LDS
+// With a workspace: the heads kernel (L.parts CTAs per q head) and the combine. Without: the one-CTA kernel, its LDS
 // holding at least one head's scores at max_seq positions (the entry point checks which applies).
 hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
     RdAttn a = a_in;
@@ -1430,9 +1480,9 @@ hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
         const RdHeadsLayout L = rd_heads_layout(a.max_seq, a.nh, a.hd);
         const size_t qk = rd_round256((size_t)2 * a.hd * sizeof(int32_t)), lds = qk + L.arr_stride;
         if (lds <= RD_HEADS_LDS)
-            rd_attention_heads_kernel<false><<<(unsigned)a.nh, RD_THREADS, lds, s>>>(a, L);
+            rd_attention_heads_kernel<false><<<(unsigned)(a.nh * L.parts), RD_THREADS, lds, s>>>(a, L);
         else
-            rd_attention_heads_kernel<true><<<(unsigned)a.nh, RD_THREADS, qk, s>>>(a, L);
+            rd_attention_heads_kernel<true><<<(unsigned)(a.nh * L.parts), RD_THREADS, qk, s>>>(a, L);
         rd_attention_combine_kernel<<<1, RD_THREADS, 0, s>>>(a, L);
         return hipGetLastError();
     }
@@ -1700,7 +1750,7 @@ extern "C" size_t kt_hip_ref_attention_step_workspace(int64_t max_seq, int64_t n
     if (nh < 1 || nh > KT_REF_MAX_HEADS || hd < 2 || hd > 1024 || max_seq < 1 || max_seq > KT_REF_ATTN_MAX_SEQ)
         return 0;
     const kt::RdHeadsLayout L = kt::rd_heads_layout((int)max_seq, (int)nh, (int)hd);
-    return L.arr + (size_t)nh * L.arr_stride;
+    return L.arr + (size_t)nh * L.parts * L.arr_stride;
 }
 
 extern "C" int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const kt_hip_qscale* qs_dev,

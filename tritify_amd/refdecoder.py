@@ -112,7 +112,7 @@ class RefDecoder:
         self._rec_qkv, self._rec_gu = qkv_rec, gu_rec
         self.token = z(1)
         self.pos = z(1)
-        # the attention step on one CTA per head, its workspace shared by the layers (their steps run in order on
+        # the attention step on several CTAs per head, its workspace shared by the layers (their steps run in order on
         # one stream); attn_heads=False keeps the one-CTA step where its LDS holds max_seq
         self.attn_ws = None
         if cfg.get("attn_heads", True) or not B.ref_attention_step_fits_lds(self.max_seq, self.nh, self.hd):
