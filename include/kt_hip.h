@@ -123,6 +123,30 @@ int kt_hip_quant_linear_multi(int dev, const int32_t* x_dev, int64_t rows, int64
                               const int* has_bias, const int64_t* b_mant, const int32_t* b_shift, void* ws_dev,
                               size_t ws_bytes, int32_t* const* y_devs, kt_hip_qscale* os_dev, void* stream);
 int64_t kt_hip_quant_linear_multi_align(int64_t rows, int64_t out_f, int pw);
+/* The decode row's QuantLinear calls up to their exact sums: kt_hip_quant_linear_multi at rows = 1 with no bias and
+ * no codes out -- the quantization of x and the digit product, one launch -- leaving each call's i64 sums and state
+ * (max |x|, c = from_ratio(xmax, WLEVELS) * xs * ws, the mode) in ws_dev for the op that reads the output next,
+ * which applies requant_dyn (layers.rs:33-39, 321-327) itself and forms the record (the kt_hip_ref_*_sums entry
+ * points): one launch fewer per projection, the same integers as kt_hip_quant_linear_multi followed by the plain
+ * entry point. ws_dev (kt_hip_quant_linear_workspace(1, in_f, sum seg_out) bytes) must not be reused before that op
+ * has run. Requires kt_hip_quant_linear_sums_ok(in_f, sum seg_out, pw) (the one-launch product takes the shape) and
+ * every boundary between calls a multiple of 8. No counterpart in the reference's API: it splits QuantLinear's
+ * forward_int at its requant. */
+int kt_hip_quant_linear_sums_ok(int64_t in_f, int64_t out_f, int pw);
+int kt_hip_quant_linear_multi_sums(int dev, const int32_t* x_dev, int64_t in_f, const kt_hip_qscale* xs_dev,
+                                   int nseg, const int64_t* seg_out, const int8_t* w_planes_dev, int pw,
+                                   const int64_t* w_mant, const int32_t* w_shift, void* ws_dev, size_t ws_bytes,
+                                   void* stream);
+/* One call's output of a kt_hip_quant_linear_multi_sums launch, as the op that reads it takes it: that launch's
+ * workspace and shape (in_f, out_f = sum seg_out), the call's index seg and its columns [col0, col0 + n), and where
+ * the reader writes the output's record (kt_hip_quant_linear's os_dev for that call), or NULL for none. */
+typedef struct {
+    const void* ws;
+    int64_t in_f, out_f, col0, n;
+    int32_t seg;
+    int32_t pad;
+    kt_hip_qscale* rec;
+} kt_hip_ql_sums;
 /* kt_hip_quant_linear with no workspace argument and no allocation of any kind: the workspace lives in a
  * library-owned device array of KT_QL_SCRATCH_BYTES on each GPU (held until the process ends), so the call can run
  * where hipMalloc cannot (code under HIP graph capture, tight serving loops, hosts that forbid allocation). No
@@ -246,12 +270,25 @@ int kt_hip_ref_add_rmsnorm(int dev, const int32_t* a_dev, const kt_hip_qscale* a
                            const kt_hip_qscale* bs_dev, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev,
                            const int32_t* g_dev, int64_t g_mant, int32_t g_shift, int64_t eps_mant, int32_t eps_shift,
                            int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream);
+/* kt_hip_ref_add_rmsnorm with b the output of a kt_hip_quant_linear_multi_sums call (b->n == n): its requant_dyn
+ * and record formed in the same launch, then the add and the norm -- the same integers as that QuantLinear call
+ * (kt_hip_quant_linear_multi) followed by kt_hip_ref_add_rmsnorm. y_dev may alias a_dev. */
+int kt_hip_ref_add_rmsnorm_sums(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev, const kt_hip_ql_sums* b,
+                                int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev, const int32_t* g_dev,
+                                int64_t g_mant, int32_t g_shift, int64_t eps_mant, int32_t eps_shift, int32_t* h_dev,
+                                kt_hip_qscale* hs_dev, void* stream);
 /* SwiGluMlp::forward_int's activation (layers.rs:615-637): h = requant_dyn(silu_code(g) * u), the SiLU CodeLut
  * (right_identity set) with its codes at silu_codes_dev, for `rows` tensors of n values each, row r with its own
  * records gs_dev[r], us_dev[r], hs_dev[r] (rows = 1: one tensor; rows > 1: the per-token expert calls of a MoE). */
 int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
                       const kt_hip_qscale* us_dev, int64_t rows, int64_t n, const int64_t* silu_codes_dev,
                       const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream);
+/* kt_hip_ref_swiglu of one tensor (rows = 1, n <= 8192) with g and u the outputs of kt_hip_quant_linear_multi_sums
+ * calls (g->n == u->n == n; the gate / up pair of one launch): their requant_dyn and records formed in the same
+ * launch -- the same integers as the QuantLinear calls followed by kt_hip_ref_swiglu. */
+int kt_hip_ref_swiglu_sums(int dev, const kt_hip_ql_sums* g, const kt_hip_ql_sums* u, int64_t n,
+                           const int64_t* silu_codes_dev, const kt_hip_codelut* silu, int32_t* h_dev,
+                           kt_hip_qscale* hs_dev, void* stream);
 /* apply_gelu (crates/03-models/kt-model-vision/src/nonlin.rs:30-45) of n codes at xs_dev through the GELU CodeLut
  * (KT_LUT_GELU over [-10, 10], 2^16 entries, 2^20 code scale, right_identity set; its codes at gelu_codes_dev): y_dev
  * (may alias x_dev) at the table's code scale, written to ys_dev (which may not alias xs_dev). */
@@ -304,6 +341,17 @@ int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const kt_hip_qsc
                                  int64_t isq_mant, int32_t isq_shift, const int64_t* exp_codes_dev,
                                  const kt_hip_codelut* exp_lut, int32_t* o_dev, kt_hip_qscale* os_dev, void* ws_dev,
                                  size_t ws_bytes, void* stream);
+/* kt_hip_ref_attention_step_ws (a workspace required) with q, k and v the outputs of kt_hip_quant_linear_multi_sums
+ * calls (q->n == nh hd, k->n == v->n == nkv hd; the q / k / v trio of one launch): every CTA forms the three
+ * outputs' maxima, Scales and the codes it reads itself (the first CTA writes the records) -- the same integers as
+ * the QuantLinear calls followed by kt_hip_ref_attention_step_ws. */
+int kt_hip_ref_attention_step_sums(int dev, const kt_hip_ql_sums* q, const kt_hip_ql_sums* k, const kt_hip_ql_sums* v,
+                                   const int32_t* pos_dev, int64_t nh, int64_t nkv, int64_t hd, int64_t max_seq,
+                                   int32_t* kc_dev, int32_t* vc_dev, kt_hip_sscale* kscale_dev,
+                                   kt_hip_sscale* vscale_dev, const kt_hip_sscale* cos_dev,
+                                   const kt_hip_sscale* sin_dev, int64_t isq_mant, int32_t isq_shift,
+                                   const int64_t* exp_codes_dev, const kt_hip_codelut* exp_lut, int32_t* o_dev,
+                                   kt_hip_qscale* os_dev, void* ws_dev, size_t ws_bytes, void* stream);
 /* argmax_codes (generate.rs:48-56): token_dev[0] = the first index of the largest of n codes. With record_dev
  * non-null the codes are copied to record_dev + step * n and (mant, shift) of ls_dev to rscale_dev[step], step =
  * step_dev[0], which then advances (the per-step logits hash_step covers, generate.rs:58-64). record_dev holds

@@ -48,6 +48,19 @@ def test_host_helpers_agree_with_the_oracle():
     assert B.fallbacks() == 0
 
 
+def test_which_decode_rows_stop_at_their_sums():
+    """kt_hip_quant_linear_sums_ok: the one-launch product takes rows of up to 1024 values (8192 with 3 weight
+    planes) and up to 16384 outputs; the Qwen2.5-0.5B decode projections all fit."""
+    from tritify_amd import backend as B
+
+    for inp, out in [(896, 1152), (896, 896), (896, 9728), (4864, 896)]:
+        assert B.quant_linear_sums_ok(inp, out, 3)
+    assert B.quant_linear_sums_ok(1024, 64, 5) and not B.quant_linear_sums_ok(1025, 64, 5)
+    assert not B.quant_linear_sums_ok(4864, 896, 5) and not B.quant_linear_sums_ok(8193, 64, 3)
+    assert B.quant_linear_sums_ok(896, 16384, 3) and not B.quant_linear_sums_ok(896, 16385, 3)
+    assert not B.quant_linear_sums_ok(896, 896, 2) and not B.quant_linear_sums_ok(0, 896, 3)
+
+
 def test_the_product_build_refuses_plants():
     """Planted defects exist only in the test build (kt-runtime/Cargo.toml `plants` feature)."""
     from tritify_amd import backend as B

@@ -149,6 +149,13 @@ def _declare(L: C.CDLL) -> None:
         "kt_hip_quant_linear_multi": (_I, [_I, _P, _I64, _I64, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P,
                                             _SZ, _P, _P, _P]),
         "kt_hip_quant_linear_multi_align": (_I64, [_I64, _I64, _I]),
+        "kt_hip_quant_linear_sums_ok": (_I, [_I64, _I64, _I]),
+        "kt_hip_quant_linear_multi_sums": (_I, [_I, _P, _I64, _P, _I, _P, _P, _I, _P, _P, _P, _SZ, _P]),
+        "kt_hip_ref_add_rmsnorm_sums": (_I, [_I, _P, _P, _P, _I64, _P, _P, _P, _I64, C.c_int32, _I64, C.c_int32, _P,
+                                             _P, _P]),
+        "kt_hip_ref_swiglu_sums": (_I, [_I, _P, _P, _I64, _P, _P, _P, _P, _P]),
+        "kt_hip_ref_attention_step_sums": (_I, [_I, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P,
+                                                _I64, C.c_int32, _P, _P, _P, _P, _P, _SZ, _P]),
         "kt_hip_pack_planes_tiled_bytes": (_SZ, [_I64, _I64, _I]),
         "kt_hip_pack_planes_tiled": (_I, [_I, _P, _I64, _I64, _I, _P, _P]),
         "kt_hip_ref_merge_rows_workspace": (_SZ, [_I64]),
@@ -458,6 +465,38 @@ def quant_linear_multi(x_dev, rows: int, in_f: int, xs_dev, seg_out, w_planes_de
         arr(C.c_void_p, [_ptr(y) for y in y_devs]), _ptr(os_dev), _stream(stream)), "quant linear multi")
 
 
+class QlSums(C.Structure):
+    """kt_hip_ql_sums: one call's output of a quant_linear_multi_sums launch (its exact sums and state in that launch's
+    workspace), as the op that reads it next takes it; rec: where that op writes the output's record, or 0."""
+    _fields_ = [("ws", _P), ("in_f", _I64), ("out_f", _I64), ("col0", _I64), ("n", _I64), ("seg", C.c_int32),
+                ("pad", C.c_int32), ("rec", _P)]
+
+
+def quant_linear_sums_ok(in_f: int, out_f: int, pw: int) -> bool:
+    """Whether a one-row QuantLinear of in_f -> out_f can stop at its sums (quant_linear_multi_sums)."""
+    return bool(lib().kt_hip_quant_linear_sums_ok(in_f, out_f, pw))
+
+
+def quant_linear_multi_sums(x_dev, in_f: int, xs_dev, seg_out, w_planes_dev, pw: int, w_scales, ws_dev,
+                            ws_bytes: int, recs=None, stream=None, dev: int = 0) -> list:
+    """quant_linear_multi of one row with no bias, stopped at the exact sums: the quantization and the digit product
+    in one launch, each call's sums and state left in ws_dev for the op that reads the output next (ref_*_sums),
+    which applies requant_dyn and writes the record (recs[g], or none). Returns one QlSums per call."""
+    n = len(seg_out)
+    arr = lambda t, v: (t * n)(*v)  # noqa: E731
+    check(lib().kt_hip_quant_linear_multi_sums(
+        dev, _ptr(x_dev), in_f, _ptr(xs_dev), n, arr(C.c_int64, [int(v) for v in seg_out]), _ptr(w_planes_dev), pw,
+        arr(C.c_int64, [int(w[0]) for w in w_scales]), arr(C.c_int32, [int(w[1]) for w in w_scales]), _ptr(ws_dev),
+        ws_bytes, _stream(stream)), "quant linear sums")
+    out, col0 = [], 0
+    for g, o in enumerate(seg_out):
+        r = recs[g] if recs is not None else None
+        out.append(QlSums(_ptr(ws_dev), in_f, sum(int(v) for v in seg_out), col0, int(o), g, 0,
+                          _ptr(r) if r is not None else 0))
+        col0 += int(o)
+    return out
+
+
 def quant_linear_noalloc(x_dev, rows: int, in_f: int, xs_dev, w_planes_dev, pw: int, out_f: int, w_scale,
                          bias_dev, b_scale, y_dev, os_dev, stream=None, dev: int = 0) -> None:
     """quant_linear with its workspace in the library's per-GPU scratch array: allocates nothing. Calls that overlap
@@ -701,6 +740,7 @@ def ref_add(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, stream=None, de
 
 
 REF_ADD_NORM_MAX = 4096  # kt_hip_ref_add_rmsnorm's longest row
+REF_SWIGLU_SUMS_MAX = 8192  # kt_hip_ref_swiglu_sums's longest tensor
 
 
 def ref_add_rmsnorm(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, g_dev, g_scale, eps_scale, h_dev, hs_dev,
@@ -710,6 +750,22 @@ def ref_add_rmsnorm(a_dev, as_dev, b_dev, bs_dev, n: int, y_dev, ys_dev, g_dev, 
                                        _ptr(ys_dev), _ptr(g_dev), int(g_scale[0]), int(g_scale[1]),
                                        int(eps_scale[0]), int(eps_scale[1]), _ptr(h_dev), _ptr(hs_dev),
                                        _stream(stream)), "ref add + rmsnorm")
+
+
+def ref_add_rmsnorm_sums(a_dev, as_dev, b: QlSums, n: int, y_dev, ys_dev, g_dev, g_scale, eps_scale, h_dev, hs_dev,
+                         stream=None, dev: int = 0) -> None:
+    """ref_add_rmsnorm with b a QuantLinear's sums (quant_linear_multi_sums): its requant_dyn in the same launch."""
+    check(lib().kt_hip_ref_add_rmsnorm_sums(dev, _ptr(a_dev), _ptr(as_dev), C.byref(b), n, _ptr(y_dev), _ptr(ys_dev),
+                                            _ptr(g_dev), int(g_scale[0]), int(g_scale[1]), int(eps_scale[0]),
+                                            int(eps_scale[1]), _ptr(h_dev), _ptr(hs_dev), _stream(stream)),
+          "ref add + rmsnorm (sums)")
+
+
+def ref_swiglu_sums(g: QlSums, u: QlSums, n: int, silu_codes_dev, silu: CodeLut, h_dev, hs_dev, stream=None,
+                    dev: int = 0) -> None:
+    """ref_swiglu of one tensor with g and u a gate / up product's sums: their requant_dyn in the same launch."""
+    check(lib().kt_hip_ref_swiglu_sums(dev, C.byref(g), C.byref(u), n, _ptr(silu_codes_dev), C.byref(silu),
+                                       _ptr(h_dev), _ptr(hs_dev), _stream(stream)), "ref swiglu (sums)")
 
 
 def ref_swiglu(g_dev, gs_dev, u_dev, us_dev, n: int, silu_codes_dev, silu: CodeLut, h_dev, hs_dev, stream=None,
@@ -830,6 +886,20 @@ def ref_attention_step(q_dev, qs_dev, k_dev, ks_dev, v_dev, vs_dev, pos_dev, nh:
                                              _ptr(exp_codes_dev), C.byref(exp_lut), _ptr(o_dev), _ptr(os_dev),
                                              _ptr(ws_dev), ws_bytes, _stream(stream)),
           "ref attention step")
+
+
+def ref_attention_step_sums(q: QlSums, k: QlSums, v: QlSums, pos_dev, nh: int, nkv: int, hd: int, max_seq: int,
+                            kc_dev, vc_dev, kscale_dev, vscale_dev, cos_dev, sin_dev, inv_sqrt, exp_codes_dev,
+                            exp_lut: CodeLut, o_dev, os_dev, ws_dev, stream=None, dev: int = 0) -> None:
+    """ref_attention_step with a workspace and q, k, v a q / k / v product's sums: every CTA applies their
+    requant_dyn itself."""
+    ws_bytes = ws_dev.numel() * ws_dev.element_size()
+    check(lib().kt_hip_ref_attention_step_sums(dev, C.byref(q), C.byref(k), C.byref(v), _ptr(pos_dev), nh, nkv, hd,
+                                               max_seq, _ptr(kc_dev), _ptr(vc_dev), _ptr(kscale_dev),
+                                               _ptr(vscale_dev), _ptr(cos_dev), _ptr(sin_dev), int(inv_sqrt[0]),
+                                               int(inv_sqrt[1]), _ptr(exp_codes_dev), C.byref(exp_lut), _ptr(o_dev),
+                                               _ptr(os_dev), _ptr(ws_dev), ws_bytes, _stream(stream)),
+          "ref attention step (sums)")
 
 
 def ref_argmax(logits_dev, n: int, ls_dev, token_dev, record_dev=None, rscale_dev=None, step_dev=None, stream=None,

@@ -272,6 +272,32 @@ int kt_hip_quant_linear_multi(int dev, const int32_t* x_dev, int64_t rows, int64
                                               y_devs, os_dev, (hipStream_t)stream);
 }
 
+int kt_hip_quant_linear_sums_ok(int64_t in_f, int64_t out_f, int pw) {
+    if (pw != 1 && pw != 3 && pw != 5) return 0;
+    return kt::ql_sums_ok(in_f, out_f, pw, flush_of(3, pw)) ? 1 : 0;
+}
+
+int kt_hip_quant_linear_multi_sums(int dev, const int32_t* x_dev, int64_t in_f, const kt_hip_qscale* xs_dev,
+                                   int nseg, const int64_t* seg_out, const int8_t* w_planes_dev, int pw,
+                                   const int64_t* w_mant, const int32_t* w_shift, void* ws_dev, size_t ws_bytes,
+                                   void* stream) {
+    if (nseg < 1 || nseg > KT_QL_MAX_SEGMENTS || !seg_out || !w_mant || !w_shift || in_f < 1 ||
+        (pw != 1 && pw != 3 && pw != 5))
+        return (int)hipErrorInvalidValue;
+    int64_t out_f = 0;
+    for (int g = 0; g < nseg; g++) {
+        if (seg_out[g] < 1 || w_mant[g] < 0 || (g + 1 < nseg && (out_f + seg_out[g]) % 8))
+            return (int)hipErrorInvalidValue;
+        out_f += seg_out[g];
+    }
+    if (!kt_hip_quant_linear_sums_ok(in_f, out_f, pw) || !x_dev || !xs_dev || !w_planes_dev || !ws_dev ||
+        ws_bytes < kt_hip_quant_linear_workspace(1, in_f, out_f, nullptr))
+        return (int)hipErrorInvalidValue;
+    KT_TRY(hipSetDevice(dev));
+    return (int)kt::launch_quant_linear_sums(x_dev, in_f, xs_dev, w_planes_dev, pw, nseg, seg_out, w_mant, w_shift,
+                                             flush_of(3, pw), ws_dev, (hipStream_t)stream);
+}
+
 int64_t kt_hip_quant_linear_multi_align(int64_t rows, int64_t out_f, int pw) {
     if (rows < 1 || out_f < 1 || rows > INT_MAX || out_f > INT_MAX || (pw != 1 && pw != 3 && pw != 5)) return 0;
     return kt::plane_gemm_cta_cols(3, pw, (int)rows, (int)out_f);

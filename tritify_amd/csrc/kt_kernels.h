@@ -84,6 +84,11 @@ hipError_t launch_w12_swiglu(const int8_t* x, const int8_t* lo, const uint8_t* n
                              const int32_t* mant, const int32_t* shift, const int16_t* silu, int h_shift, int8_t* y,
                              int ystride, hipStream_t s);
 size_t ql_workspace_bytes(int64_t rows, int64_t in, int64_t out, size_t off[KT_QL_WS_PARTS]);
+// The one-row product alone (kt_hip_quant_linear_multi_sums): no bias, the sums and states left in the workspace.
+bool ql_sums_ok(int64_t in, int64_t out, int pw, int64_t flush_k);
+hipError_t launch_quant_linear_sums(const int32_t* x, int64_t in, const kt_hip_qscale* xs, const int8_t* wb, int pw,
+                                    int nseg, const int64_t* seg_out, const int64_t* w_mant, const int32_t* w_shift,
+                                    int64_t flush_k, void* ws, hipStream_t s);
 // Several QuantLinear calls on one x (seg_out[g] output columns each, weights side by side in wb): one x pass, one
 // digit GEMM, each call's own requantization into y[g] with record os[g].
 hipError_t launch_quant_linear_multi(const int32_t* x, int64_t rows, int64_t in, const kt_hip_qscale* xs,

@@ -562,6 +562,44 @@ static int grid_for(int64_t n, int64_t per_thread) {
     return (int)(g < 1 ? 1 : (g > KT_QL_PARTS ? KT_QL_PARTS : g));
 }
 
+// Whether one row of in values -> out columns takes the one-launch product (ql_skinny_kernel): the row within one
+// k-chunk and the kernel's LDS image, at most QS_FUSED_OUT columns.
+bool ql_sums_ok(int64_t in, int64_t out, int pw, int64_t flush_k) {
+    const int64_t kp = (in + 63) / 64 * 64;
+    const bool long_row = kp > QS_MAX_KP && kp <= QS_LONG_KP && pw == 3;
+    return in >= 1 && out >= 1 && (kp <= QS_MAX_KP || long_row) && out <= QS_FUSED_OUT && kp <= flush_k &&
+           (pw == 1 || pw == 3 || pw == 5);
+}
+// every CTA of QS_COLS columns within one segment
+static bool ql_seg_cols_ok(const QlSeg& seg) {
+    bool ok = true;
+    for (int g = 1; g < seg.n; g++) ok = ok && seg.col0[g] % QS_COLS == 0;
+    return ok;
+}
+// The one-row product (ql_sums_ok): the sums at the workspace's part 1, each segment's state at part 4, each CTA's
+// largest |sum| at part 2.
+static hipError_t launch_ql_skinny(const int32_t* x, int64_t in, const kt_hip_qscale* xs, const int8_t* wb, int pw,
+                                   int64_t out, const QlSeg& seg, const QlScales& sc, const int64_t* bias, void* ws,
+                                   hipStream_t s) {
+    size_t off[KT_QL_WS_PARTS];
+    ql_workspace_bytes(1, in, out, off);
+    char* base = (char*)ws;
+    int64_t* acc = (int64_t*)(base + off[1]);
+    int64_t* pm = reinterpret_cast<int64_t*>(base + off[2]);
+    QlState* st = (QlState*)(base + off[4]);
+    const int64_t kp = (in + 63) / 64 * 64;
+    const bool long_row = kp > QS_MAX_KP && kp <= QS_LONG_KP && pw == 3;
+    const int ctas = (int)((out + QS_COLS - 1) / QS_COLS);
+#define KT_QS(P, K) ql_skinny_kernel<P, K><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, \
+                                                                      seg, sc, st, pm)
+    if (long_row) KT_QS(3, QS_LONG_KP);
+    else if (pw == 1) KT_QS(1, QS_MAX_KP);
+    else if (pw == 3) KT_QS(3, QS_MAX_KP);
+    else KT_QS(5, QS_MAX_KP);
+#undef KT_QS
+    return hipGetLastError();
+}
+
 // The four passes of QuantLinear::forward_int, or of Conv2d::forward_int when geom is non-null (the image x of
 // geom->ci x h x w values read as its im2col rows; the output channel-major, zeros at Scale::ZERO for an all-zero
 // image). seg splits the out columns into the outputs of several calls on the same x (their own weight and bias
@@ -587,22 +625,11 @@ static hipError_t launch_ql_impl(const int32_t* x, int64_t rows, int64_t in, con
     if (ntiles * 4 > KT_QL_PARTS * 8) return hipErrorInvalidValue;  // cannot happen: a split grid has < 128 tiles
 
     // one row within one k-chunk (the decode step): the quant pass inside the product, then the requant pass
-    bool seg_ok = true;  // every CTA of QS_COLS columns within one segment
-    for (int g = 1; g < seg.n; g++) seg_ok = seg_ok && seg.col0[g] % QS_COLS == 0;
-    const bool long_row = kp > QS_MAX_KP && kp <= QS_LONG_KP && pw == 3;
-    if (!geom && rows == 1 && (kp <= QS_MAX_KP || long_row) && out <= QS_FUSED_OUT && kp <= flush_k && seg_ok &&
-        (pw == 1 || pw == 3 || pw == 5)) {
+    if (!geom && rows == 1 && ql_sums_ok(in, out, pw, flush_k) && ql_seg_cols_ok(seg)) {
+        const hipError_t e = launch_ql_skinny(x, in, xs, wb, pw, out, seg, sc, bias, ws, s);
+        if (e != hipSuccess) return e;
         const int ctas = (int)((out + QS_COLS - 1) / QS_COLS);
         int64_t* pm = reinterpret_cast<int64_t*>(base + off[2]);
-#define KT_QS(P, K) ql_skinny_kernel<P, K><<<ctas, QS_THREADS, 0, s>>>(x, (int)in, (int)kp, xs, wb, acc, (int)out, bias, \
-                                                                      seg, sc, st, pm)
-        if (long_row) KT_QS(3, QS_LONG_KP);
-        else if (pw == 1) KT_QS(1, QS_MAX_KP);
-        else if (pw == 3) KT_QS(3, QS_MAX_KP);
-        else KT_QS(5, QS_MAX_KP);
-#undef KT_QS
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
         ql_requant_kernel<<<grid_for(n, 1) + 1, QL_THREADS, 0, s>>>(acc, n, out, bias, st, seg, sc, yo, pm, ctas);
         return hipGetLastError();
     }
@@ -678,6 +705,22 @@ hipError_t launch_quant_linear_multi(const int32_t* x, int64_t rows, int64_t in,
     }
     for (int g = nseg; g <= KT_QL_MAX_SEG; g++) seg.col0[g] = (int)at;
     return launch_ql_impl(x, rows, in, nullptr, xs, wb, pw, at, seg, sc, bias, flush_k, ws, yo, s);
+}
+
+hipError_t launch_quant_linear_sums(const int32_t* x, int64_t in, const kt_hip_qscale* xs, const int8_t* wb, int pw,
+                                    int nseg, const int64_t* seg_out, const int64_t* w_mant, const int32_t* w_shift,
+                                    int64_t flush_k, void* ws, hipStream_t s) {
+    QlSeg seg{nseg, {0, 0, 0, 0, 0}};
+    QlScales sc{};
+    int64_t at = 0;
+    for (int g = 0; g < nseg; g++) {
+        seg.col0[g] = (int)at;
+        at += seg_out[g];
+        sc.w_mant[g] = w_mant[g], sc.w_shift[g] = w_shift[g];
+    }
+    for (int g = nseg; g <= KT_QL_MAX_SEG; g++) seg.col0[g] = (int)at;
+    if (!ql_sums_ok(in, at, pw, flush_k) || !ql_seg_cols_ok(seg)) return hipErrorInvalidValue;
+    return launch_ql_skinny(x, in, xs, wb, pw, at, seg, sc, nullptr, ws, s);
 }
 
 hipError_t launch_ref_conv2d(const int32_t* x, const ConvGeom& g, const kt_hip_qscale* xs, const int8_t* wb, int pw,

@@ -27,6 +27,7 @@
 
 #include "kt_kernels.h"
 #include "kt_scale_dev.h"
+#include "kt_w12_core.h"
 
 namespace kt {
 
@@ -39,6 +40,17 @@ constexpr int RD_PV_GROUP = 8;     // P.V by kv head for groups of up to this ma
 constexpr int64_t ACT_LEVELS = 1LL << 28;
 
 }  // namespace
+
+// A QuantLinear output left as its exact sums by the one-row product (kt_hip_quant_linear_multi_sums), as the op
+// reading it next takes it: the output's sums, its call's state (max |x|, c, mode) and where its record goes (or
+// null). That op applies requant_dyn (layers.rs:33-39, 321-327) as ql_requant_kernel would: ymax = max |sum| over
+// the output (i64::abs, wrapping, as the product's own maximum); codes requant_dyn(sum, 2^28, ymax) when the mode is
+// 0 and ymax > 0, else zeros (x all zero, or c zero; the path carries no bias); the Scale from_ratio(ymax, 2^28) * c.
+struct RqSums {
+    const int64_t* acc;
+    const QlState* st;
+    kt_hip_qscale* rec;
+};
 
 // The arguments of rd_attention_step_kernel (kt_hip_ref_attention_step).
 struct RdAttn {
@@ -57,6 +69,8 @@ struct RdAttn {
     kt_hip_qscale* os;
     unsigned char* ws;                 // the heads kernels' workspace (rd_heads_layout), or null: the one-CTA kernel
     int hb;                            // the one-CTA kernel: heads whose scores LDS holds at once
+    int sums;                          // the heads kernels: q, k, v as the product's sums (qsum, ksum, vsum)
+    RqSums qsum, ksum, vsum;
 };
 
 // Attention::forward_int over a sequence (prefill): the inputs, the tables and the workspace parts.
@@ -128,6 +142,42 @@ __device__ int64_t block_sum_4w(int64_t v, int64_t* red) {  // wrapping
     for (int w = 1; w < 4; w++) v = wadd(v, red[w]);
     __syncthreads();
     return v;
+}
+
+// Block maxima of two or three values at once (one pair of barriers); red holds 3 x RD_WAVES values.
+template <int K>
+__device__ void block_max_k(int64_t (&v)[K], int64_t* red) {
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const int64_t u = __shfl_xor(v[k], o, 64);
+            v[k] = u > v[k] ? u : v[k];
+        }
+        if ((threadIdx.x & 63) == 0) red[k * RD_WAVES + (threadIdx.x >> 6)] = v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        v[k] = red[k * RD_WAVES];
+        for (int w = 1; w < RD_WAVES; w++) v[k] = red[k * RD_WAVES + w] > v[k] ? red[k * RD_WAVES + w] : v[k];
+    }
+    __syncthreads();
+}
+
+// requant_dyn of a sums output (RqSums): whether its codes are live, the Scale, the record as ql_requant_kernel
+// writes it.
+__device__ inline bool rqs_live(const QlState* st, int64_t ymax) { return st->mode == 0 && ymax > 0; }
+__device__ inline Sc rqs_scale(const QlState* st, int64_t ymax) {
+    return rqs_live(st, ymax) ? sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{st->c_mant, st->c_shift})
+                              : Sc{0, 0};
+}
+__device__ inline void rqs_record(const RqSums& r, int64_t ymax, Sc s) {
+    if (!r.rec) return;
+    kt_hip_qscale o{};
+    o.xmax = r.st->xmax;
+    if (rqs_live(r.st, ymax)) o.mant = s.mant, o.shift = s.shift, o.ymax = ymax;
+    *r.rec = o;
 }
 
 // The engine's largest-scale fold (|a, b| if b.ge(a) { b } else { a } from Scale::ZERO, in sequence order) as a
@@ -396,11 +446,13 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_kernel(const int32_t* a, co
 // n <= RD_THREADS * RD_AN values: the decode step's residual add followed by the next norm (model.rs:338-353), one
 // launch where the two kernels took two. y = add(a, b) with its record ys (y may alias a or b), then h = the norm of
 // y from the codes still in registers and the Scale thread 0 formed for ys. The same integers as rd_add_kernel and
-// rd_rmsnorm_kernel in sequence.
+// rd_rmsnorm_kernel in sequence. SUMS: b is a QuantLinear's sums (bsum), its requant_dyn and record formed here
+// first, as ql_requant_kernel would.
 constexpr int RD_AN = 4;
+template <bool SUMS>
 __global__ __launch_bounds__(RD_THREADS) void rd_add_norm_kernel(const int32_t* a, const kt_hip_qscale* as_rec,
-                                                                 const int32_t* b, const kt_hip_qscale* bs_rec, int n,
-                                                                 int32_t* y, kt_hip_qscale* ys,
+                                                                 const int32_t* b, const kt_hip_qscale* bs_rec,
+                                                                 RqSums bsum, int n, int32_t* y, kt_hip_qscale* ys,
                                                                  const int32_t* __restrict__ g, int64_t g_mant,
                                                                  int32_t g_shift, int64_t e_mant, int32_t e_shift,
                                                                  int32_t* __restrict__ h,
@@ -408,13 +460,33 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_norm_kernel(const int32_t* 
     __shared__ int64_t red[RD_WAVES];
     __shared__ Sc par[3];  // common, fa, fb
     int32_t av[RD_AN], bv[RD_AN], gv[RD_AN];
+    int64_t bacc[RD_AN];
 #pragma unroll
     for (int k = 0; k < RD_AN; k++) {
         const int i = threadIdx.x + RD_THREADS * k, ic = i < n ? i : n - 1;
-        av[k] = a[ic], bv[k] = b[ic], gv[k] = g[ic];
+        av[k] = a[ic], gv[k] = g[ic];
+        if constexpr (SUMS) bacc[k] = bsum.acc[ic];
+        else bv[k] = b[ic];
+    }
+    int64_t bmax = 0;
+    if constexpr (SUMS) {  // b's maximum (the values past n repeat value n - 1), codes and Scale
+#pragma unroll
+        for (int k = 0; k < RD_AN; k++) bmax = iabs(bacc[k]) > bmax ? iabs(bacc[k]) : bmax;
+        bmax = block_max_i64(bmax, red);
+        const bool live = rqs_live(bsum.st, bmax);
+        const RqDen d = rq_den(bmax);
+#pragma unroll
+        for (int k = 0; k < RD_AN; k++) bv[k] = live ? rq_apply(d, bacc[k]) : 0;
     }
     if (threadIdx.x == 0) {
-        const Sc as = rec_sc(as_rec), bs = rec_sc(bs_rec);
+        Sc bs;
+        if constexpr (SUMS) {
+            bs = rqs_scale(bsum.st, bmax);
+            rqs_record(bsum, bmax, bs);
+        } else {
+            bs = rec_sc(bs_rec);
+        }
+        const Sc as = rec_sc(as_rec);
         const Sc common = sc_ge(as, bs) ? as : bs;
         par[0] = common;
         if (common.mant != 0) {
@@ -452,24 +524,50 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_norm_kernel(const int32_t* 
 // SwiGluMlp::forward_int's activation (layers.rs:615-637): h = silu_code(g) * u, the SiLU code from the CodeLut at
 // g's scale (0 below the table, the identity tail g * gs / code_scale above it), requantized at code_scale * us.
 // One CTA per row: row r's n values with its own records gs_rec[r], us_rec[r], hs[r] (rows = 1: one tensor).
+// SUMS (one row, n <= RD_THREADS * RD_VPT): g and u are QuantLinear sums (gsum, usum), their requant_dyn and records
+// formed here first, as ql_requant_kernel would.
+template <bool SUMS>
 __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __restrict__ g,
                                                                const kt_hip_qscale* __restrict__ gs_rec,
                                                                const int32_t* __restrict__ u,
-                                                               const kt_hip_qscale* __restrict__ us_rec, int n,
-                                                               const int64_t* __restrict__ codes, kt_hip_codelut L,
-                                                               int32_t* __restrict__ h,
+                                                               const kt_hip_qscale* __restrict__ us_rec, RqSums gsum,
+                                                               RqSums usum, int n, const int64_t* __restrict__ codes,
+                                                               kt_hip_codelut L, int32_t* __restrict__ h,
                                                                kt_hip_qscale* __restrict__ hs) {
-    __shared__ int64_t red[RD_WAVES];
-    {
+    __shared__ int64_t red[3 * RD_WAVES];
+    if constexpr (!SUMS) {
         const int64_t r = blockIdx.x;
         g += r * n, u += r * n, h += r * n, gs_rec += r, us_rec += r, hs += r;
     }
     // up to RD_VPT values per thread formed once and held in registers, their loads issued before thread 0's Scale
     // work so that the two overlap (the table reads follow the factors); longer rows form each value twice
     constexpr int RD_VPT = 8;
-    const bool held = n <= RD_THREADS * RD_VPT;
+    const bool held = SUMS || n <= RD_THREADS * RD_VPT;
     int32_t gd[RD_VPT], ud[RD_VPT];
-    if (held) {
+    int64_t gmax = 0, umax = 0;
+    if constexpr (SUMS) {  // the sums, their maxima (the values past n repeat value n - 1), codes and Scales
+        int64_t ga[RD_VPT], ua[RD_VPT];
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            const int k = threadIdx.x + RD_THREADS * i, kk = k < n ? k : n - 1;
+            ga[i] = gsum.acc[kk], ua[i] = usum.acc[kk];
+        }
+        int64_t mx[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            mx[0] = iabs(ga[i]) > mx[0] ? iabs(ga[i]) : mx[0];
+            mx[1] = iabs(ua[i]) > mx[1] ? iabs(ua[i]) : mx[1];
+        }
+        block_max_k<2>(mx, red);
+        gmax = mx[0], umax = mx[1];
+        const bool lg = rqs_live(gsum.st, gmax), lu = rqs_live(usum.st, umax);
+        const RqDen dg = rq_den(gmax), du = rq_den(umax);
+#pragma unroll
+        for (int i = 0; i < RD_VPT; i++) {
+            gd[i] = lg ? rq_apply(dg, ga[i]) : 0;
+            ud[i] = lu ? rq_apply(du, ua[i]) : 0;
+        }
+    } else if (held) {
 #pragma unroll
         for (int i = 0; i < RD_VPT; i++) {
             const int k = threadIdx.x + RD_THREADS * i, kk = k < n ? k : n - 1;
@@ -477,10 +575,26 @@ __global__ __launch_bounds__(RD_THREADS) void rd_swiglu_kernel(const int32_t* __
         }
     }
     __shared__ Sc par[3];  // index factor, identity factor, h scale
-    if (threadIdx.x == 0) {
-        const Sc gs = rec_sc(gs_rec), us = rec_sc(us_rec), cs{L.code_mant, L.code_shift};
+    const Sc cs{L.code_mant, L.code_shift};
+    if (threadIdx.x == 0) {  // g's factors (and with SUMS its Scale and record first)
+        Sc gs;
+        if constexpr (SUMS) {
+            gs = rqs_scale(gsum.st, gmax);
+            rqs_record(gsum, gmax, gs);
+        } else {
+            gs = rec_sc(gs_rec);
+        }
         par[0] = sc_mul(gs, Sc{L.inv_mant, L.inv_shift});
         par[1] = sc_mul(gs, sc_recip(cs));
+    }
+    if (threadIdx.x == 64) {  // u's side, in another wave
+        Sc us;
+        if constexpr (SUMS) {
+            us = rqs_scale(usum.st, umax);
+            rqs_record(usum, umax, us);
+        } else {
+            us = rec_sc(us_rec);
+        }
         par[2] = sc_mul(cs, us);
     }
     __syncthreads();
@@ -870,10 +984,13 @@ constexpr int RD_PV_U = 8, RD_PV_W = 16;
 // static part is about 33 KB).
 constexpr size_t RD_HEADS_LDS = 96 * 1024;
 
-// GA: the per-step arrays in the workspace (caches longer than LDS holds), else in LDS after q and k.
-template <bool GA>
+// GA: the per-step arrays in the workspace (caches longer than LDS holds), else in LDS after q and k. SUMS: q, k and v
+// are the q / k / v product's sums (a.qsum, a.ksum, a.vsum): every CTA takes their maxima over the whole outputs,
+// forms their Scales and the codes it reads as ql_requant_kernel would (CTA 0 writes the records).
+template <bool GA, bool SUMS>
 __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a, RdHeadsLayout L) {
-    __shared__ int64_t red[RD_WAVES];
+    __shared__ int64_t red[3 * RD_WAVES];
+    __shared__ Sc qkv_s[3];
     __shared__ ScIdx redsc[RD_THREADS];
     __shared__ Sc par[4];  // v_ref, s_ref, lut factor, 1 / v_ref
     __shared__ Sc sinv_s;
@@ -883,6 +1000,41 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     const int tid = threadIdx.x, hd = a.hd, half = hd / 2, nh = a.nh, nkv = a.nkv;
     const int group = nh / nkv, kv = h / group, kstride = nkv * hd;
     const int pos = *a.pos;
+    // q, k and v: codes and Scales from the inputs, or requant_dyn of the sums
+    int64_t ymax[3] = {0, 0, 0};
+    if constexpr (SUMS) {
+        for (int i = tid; i < nh * hd; i += RD_THREADS) ymax[0] = iabs(a.qsum.acc[i]) > ymax[0] ? iabs(a.qsum.acc[i]) : ymax[0];
+        for (int i = tid; i < nkv * hd; i += RD_THREADS) {
+            ymax[1] = iabs(a.ksum.acc[i]) > ymax[1] ? iabs(a.ksum.acc[i]) : ymax[1];
+            ymax[2] = iabs(a.vsum.acc[i]) > ymax[2] ? iabs(a.vsum.acc[i]) : ymax[2];
+        }
+        block_max_k<3>(ymax, red);
+        if ((tid & 63) == 0 && tid < 192) {  // the three Scale chains in three waves
+            const RqSums& r = tid == 0 ? a.qsum : (tid == 64 ? a.ksum : a.vsum);
+            const int64_t ym = ymax[tid >> 6];
+            const Sc sc = rqs_scale(r.st, ym);
+            qkv_s[tid >> 6] = sc;
+            if (blockIdx.x == 0) rqs_record(r, ym, sc);
+        }
+        __syncthreads();
+    }
+    const bool lq = SUMS && rqs_live(a.qsum.st, ymax[0]), lk = SUMS && rqs_live(a.ksum.st, ymax[1]),
+               lv = SUMS && rqs_live(a.vsum.st, ymax[2]);
+    const RqDen dq = rq_den(ymax[0]), dk = rq_den(ymax[1]), dv = rq_den(ymax[2]);
+    auto qcode = [&](int i) -> int32_t {
+        if constexpr (SUMS) return lq ? rq_apply(dq, a.qsum.acc[i]) : 0;
+        else return a.q[i];
+    };
+    auto kcode = [&](int i) -> int32_t {
+        if constexpr (SUMS) return lk ? rq_apply(dk, a.ksum.acc[i]) : 0;
+        else return a.k[i];
+    };
+    auto vcode = [&](int i) -> int32_t {
+        if constexpr (SUMS) return lv ? rq_apply(dv, a.vsum.acc[i]) : 0;
+        else return a.v[i];
+    };
+    const Sc qs = SUMS ? qkv_s[0] : rec_sc(a.qs), ksp = SUMS ? qkv_s[1] : rec_sc(a.ks),
+             vsp = SUMS ? qkv_s[2] : rec_sc(a.vs);
     unsigned char* ws = a.ws;
     int64_t* HO = reinterpret_cast<int64_t*>(ws + L.ho);
     Sc* HSC = reinterpret_cast<Sc*>(ws + L.hsc);
@@ -904,10 +1056,10 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     for (int j = tid; j < half; j += RD_THREADS) {
         const kt_hip_sscale c = a.cos[(size_t)pos * half + j], sn = a.sin[(size_t)pos * half + j];
         const Sc cm{c.mant, c.shift}, sm{sn.mant, sn.shift};
-        const int32_t qa = a.q[h * hd + j], qb = a.q[h * hd + j + half];
+        const int32_t qa = qcode(h * hd + j), qb = qcode(h * hd + j + half);
         QD[j] = (int32_t)(c.sign * sc_apply32(cm, qa) - sn.sign * sc_apply32(sm, qb));
         QD[j + half] = (int32_t)(c.sign * sc_apply32(cm, qb) + sn.sign * sc_apply32(sm, qa));
-        const int32_t ka = a.k[kv * hd + j], kb = a.k[kv * hd + j + half];
+        const int32_t ka = kcode(kv * hd + j), kb = kcode(kv * hd + j + half);
         KP[j] = (int32_t)(c.sign * sc_apply32(cm, ka) - sn.sign * sc_apply32(sm, kb));
         KP[j + half] = (int32_t)(c.sign * sc_apply32(cm, kb) + sn.sign * sc_apply32(sm, ka));
     }
@@ -915,15 +1067,15 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     if (h == kv * group && part == 0)
         for (int i = tid; i < hd; i += RD_THREADS) {
             a.kc[(size_t)pos * kstride + kv * hd + i] = KP[i];
-            a.vc[(size_t)pos * kstride + kv * hd + i] = a.v[kv * hd + i];
+            a.vc[(size_t)pos * kstride + kv * hd + i] = vcode(kv * hd + i);
         }
     if (h == 0 && part == 0 && tid == 0) {
-        a.kscale[pos] = kt_hip_sscale{a.ks->mant, a.ks->shift, 1};
-        a.vscale[pos] = kt_hip_sscale{a.vs->mant, a.vs->shift, 1};
+        a.kscale[pos] = kt_hip_sscale{ksp.mant, ksp.shift, 1};
+        a.vscale[pos] = kt_hip_sscale{vsp.mant, vsp.shift, 1};
     }
 
     // 2. every step's score scale s_j = qs * ks_j * inv_sqrt and v scale; their largest (the engine's fold)
-    const Sc qs = rec_sc(a.qs), isq{a.isq_mant, a.isq_shift}, ksp = rec_sc(a.ks), vsp = rec_sc(a.vs);
+    const Sc isq{a.isq_mant, a.isq_shift};
     ScIdx bv{Sc{0, 0}, -1}, bs{Sc{0, 0}, -1};
     for (int j = tid; j < steps; j += RD_THREADS) {
         const Sc kj = j == pos ? ksp : Sc{a.kscale[j].mant, a.kscale[j].shift};
@@ -1006,6 +1158,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
     // 5. P.V: thread js * hd + d (hd <= RD_THREADS) sums the steps j = js (mod slices) of column d (wrapping i64:
     //    any order gives the reference's integers); the slices then add up in LDS
     const int slices = RD_THREADS / hd, d = tid % hd, js = tid / hd;
+    const int32_t vpos = vcode(kv * hd + d);  // this step's v (its cache row is written in this same launch)
     int64_t acc = 0;
     if (hd % 64 == 0) {
         // a wave is one slice: its step, numerator and v factor are the same on every lane, so they are read once
@@ -1022,7 +1175,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
 #pragma unroll
                 for (int u = 0; u < RD_PV_W; u++) {  // a step past the end reads the last one and adds nothing
                     const int j = j0 + u * ST < steps ? j0 + u * ST : steps - 1;
-                    vv[u] = j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride];
+                    vv[u] = j == pos ? vpos : vcol[(size_t)j * kstride];
                 }
 #pragma unroll
                 for (int u = 0; u < RD_PV_W; u++) {
@@ -1051,7 +1204,7 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
 #pragma unroll
             for (int u = 0; u < RD_PV_U; u++) {  // a step past the end reads the last one and adds nothing
                 const int j = j0 + u * ST < steps ? j0 + u * ST : steps - 1;
-                vv[u] = j == pos ? a.v[kv * hd + d] : vcol[(size_t)j * kstride];
+                vv[u] = j == pos ? vpos : vcol[(size_t)j * kstride];
                 ec[u] = S[j];
                 vf[u] = VF[j];
             }
@@ -1072,32 +1225,62 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
 
 // Step 4 of Attention::decode_step over the heads kernel's outputs: the heads' largest scale by the engine's fold,
 // each head brought to it, requant_dyn of the concatenation, the record.
+constexpr int RD_CB = 2;  // head-output values a combine thread holds (nh * hd up to 2048); longer rows recompute
 __global__ __launch_bounds__(RD_THREADS) void rd_attention_combine_kernel(RdAttn a, RdHeadsLayout L) {
     __shared__ int64_t red[RD_WAVES];
     __shared__ ScIdx redsc[RD_THREADS];
     const int tid = threadIdx.x, hd = a.hd, nh = a.nh, qstride = nh * hd, P = L.parts;
     const int64_t* HOP = reinterpret_cast<const int64_t*>(a.ws + L.ho);
     const Sc* HSC = reinterpret_cast<const Sc*>(a.ws + L.hsc);
-    // each head's sums: its CTAs' parts added (wrapping, in any order: the reference's integers)
+    // each head's sums: its CTAs' parts (at most 8) added, wrapping, in any order (the reference's integers); the
+    // parts' loads all issued before the adds
     auto ho = [&](int i) {
         const int hh = i / hd, dd = i - hh * hd;
-        int64_t t = 0;
-        for (int q = 0; q < P; q++) t = wadd(t, HOP[((size_t)hh * P + q) * hd + dd]);
-        return t;
+        const int64_t* p = HOP + (size_t)hh * P * hd + dd;
+        int64_t t[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) t[q] = q < P ? p[(size_t)q * hd] : 0;
+        int64_t s = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) s = wadd(s, t[q]);
+        return s;
     };
+    // the sums of the values a thread holds are read before the heads' fold, so the two overlap
+    const bool held = qstride <= RD_THREADS * RD_CB;
+    int64_t hv[RD_CB];
+#pragma unroll
+    for (int k = 0; k < RD_CB; k++) {
+        const int i = tid + RD_THREADS * k;
+        hv[k] = held && i < qstride ? ho(i) : 0;
+    }
     const Sc common = block_fold_max(tid < nh ? ScIdx{HSC[tid], tid} : ScIdx{Sc{0, 0}, -1}, redsc, nh).s;
     int64_t m = 0;
     if (common.mant != 0) {
         const Sc cinv = sc_recip(common);
-        for (int i = tid; i < qstride; i += RD_THREADS) {
-            const int64_t v = sc_apply(sc_mul(HSC[i / hd], cinv), ho(i));
-            m = iabs(v) > m ? iabs(v) : m;
+        if (held) {
+#pragma unroll
+            for (int k = 0; k < RD_CB; k++) {  // each value at the common scale, kept for the requant
+                const int i = tid + RD_THREADS * k;
+                if (i < qstride) hv[k] = sc_apply(sc_mul(HSC[i / hd], cinv), hv[k]);
+                m = iabs(hv[k]) > m ? iabs(hv[k]) : m;
+            }
+        } else {
+            for (int i = tid; i < qstride; i += RD_THREADS) {
+                const int64_t v = sc_apply(sc_mul(HSC[i / hd], cinv), ho(i));
+                m = iabs(v) > m ? iabs(v) : m;
+            }
         }
     }
     const int64_t gmax = block_max_i64(m, red);
     const RqDen rd_gmax = rq_den(gmax);
     if (gmax == 0) {
         for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = 0;
+    } else if (held) {
+#pragma unroll
+        for (int k = 0; k < RD_CB; k++) {
+            const int i = tid + RD_THREADS * k;
+            if (i < qstride) a.o[i] = rq_apply(rd_gmax, hv[k]);
+        }
     } else {
         const Sc cinv = sc_recip(common);
         for (int i = tid; i < qstride; i += RD_THREADS) a.o[i] = rq_apply(rd_gmax, sc_apply(sc_mul(HSC[i / hd], cinv), ho(i)));
@@ -1456,13 +1639,15 @@ hipError_t launch_rd_add(const int32_t* a, const kt_hip_qscale* as, const int32_
 hipError_t launch_rd_add_norm(const int32_t* a, const kt_hip_qscale* as, const int32_t* b, const kt_hip_qscale* bs,
                               int n, int32_t* y, kt_hip_qscale* ys, const int32_t* g, int64_t g_mant, int32_t g_shift,
                               int64_t e_mant, int32_t e_shift, int32_t* h, kt_hip_qscale* hs, hipStream_t s) {
-    rd_add_norm_kernel<<<1, RD_THREADS, 0, s>>>(a, as, b, bs, n, y, ys, g, g_mant, g_shift, e_mant, e_shift, h, hs);
+    rd_add_norm_kernel<false><<<1, RD_THREADS, 0, s>>>(a, as, b, bs, RqSums{}, n, y, ys, g, g_mant, g_shift, e_mant,
+                                                       e_shift, h, hs);
     return hipGetLastError();
 }
 hipError_t launch_rd_swiglu(const int32_t* g, const kt_hip_qscale* gs, const int32_t* u, const kt_hip_qscale* us,
                             int rows, int n, const int64_t* codes, const kt_hip_codelut* lut, int32_t* h,
                             kt_hip_qscale* hs, hipStream_t s) {
-    rd_swiglu_kernel<<<(unsigned)rows, RD_THREADS, 0, s>>>(g, gs, u, us, n, codes, *lut, h, hs);
+    rd_swiglu_kernel<false><<<(unsigned)rows, RD_THREADS, 0, s>>>(g, gs, u, us, RqSums{}, RqSums{}, n, codes, *lut, h,
+                                                                  hs);
     return hipGetLastError();
 }
 hipError_t launch_rd_gelu(const int32_t* x, const kt_hip_qscale* xs, int64_t n, const int64_t* codes,
@@ -1480,9 +1665,11 @@ hipError_t launch_rd_attention_step(const RdAttn& a_in, hipStream_t s) {
         const RdHeadsLayout L = rd_heads_layout(a.max_seq, a.nh, a.hd);
         const size_t qk = rd_round256((size_t)2 * a.hd * sizeof(int32_t)), lds = qk + L.arr_stride;
         if (lds <= RD_HEADS_LDS)
-            rd_attention_heads_kernel<false><<<(unsigned)(a.nh * L.parts), RD_THREADS, lds, s>>>(a, L);
+            a.sums ? rd_attention_heads_kernel<false, true><<<(unsigned)(a.nh * L.parts), RD_THREADS, lds, s>>>(a, L)
+                   : rd_attention_heads_kernel<false, false><<<(unsigned)(a.nh * L.parts), RD_THREADS, lds, s>>>(a, L);
         else
-            rd_attention_heads_kernel<true><<<(unsigned)(a.nh * L.parts), RD_THREADS, qk, s>>>(a, L);
+            a.sums ? rd_attention_heads_kernel<true, true><<<(unsigned)(a.nh * L.parts), RD_THREADS, qk, s>>>(a, L)
+                   : rd_attention_heads_kernel<true, false><<<(unsigned)(a.nh * L.parts), RD_THREADS, qk, s>>>(a, L);
         rd_attention_combine_kernel<<<1, RD_THREADS, 0, s>>>(a, L);
         return hipGetLastError();
     }
@@ -1693,6 +1880,52 @@ extern "C" int kt_hip_ref_add_rmsnorm(int dev, const int32_t* a_dev, const kt_hi
                                        eps_mant, eps_shift, h_dev, hs_dev, (hipStream_t)stream);
 }
 
+// The device view of one call's output of kt_hip_quant_linear_multi_sums (its workspace parts as ql_workspace_bytes
+// lays them out at one row); false for a malformed description or one of other than n values.
+static bool rq_sums_of(const kt_hip_ql_sums* d, int64_t n, kt::RqSums* r) {
+    if (!d || !d->ws || d->seg < 0 || d->seg >= KT_QL_MAX_SEGMENTS || d->in_f < 1 || d->out_f < 1 || d->col0 < 0 ||
+        d->n != n || d->col0 + d->n > d->out_f || (reinterpret_cast<uintptr_t>(d->ws) & 15))
+        return false;
+    size_t off[KT_QL_WS_PARTS];
+    kt::ql_workspace_bytes(1, d->in_f, d->out_f, off);
+    const char* base = static_cast<const char*>(d->ws);
+    r->acc = reinterpret_cast<const int64_t*>(base + off[1]) + d->col0;
+    r->st = reinterpret_cast<const kt::QlState*>(base + off[4]) + d->seg;
+    r->rec = d->rec;
+    return true;
+}
+
+extern "C" int kt_hip_ref_add_rmsnorm_sums(int dev, const int32_t* a_dev, const kt_hip_qscale* as_dev,
+                                           const kt_hip_ql_sums* b, int64_t n, int32_t* y_dev, kt_hip_qscale* ys_dev,
+                                           const int32_t* g_dev, int64_t g_mant, int32_t g_shift, int64_t eps_mant,
+                                           int32_t eps_shift, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream) {
+    kt::RqSums bs{};
+    if (!a_dev || !as_dev || !y_dev || !ys_dev || !g_dev || !h_dev || !hs_dev || n < 1 ||
+        n > (int64_t)kt::RD_THREADS * kt::RD_AN || g_mant < 0 || eps_mant < 0 || h_dev == y_dev || h_dev == a_dev ||
+        (void*)hs_dev == (void*)ys_dev || !rq_sums_of(b, n, &bs) || bs.rec == as_dev || bs.rec == ys_dev ||
+        bs.rec == hs_dev)
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    kt::rd_add_norm_kernel<true><<<1, kt::RD_THREADS, 0, (hipStream_t)stream>>>(
+        a_dev, as_dev, nullptr, nullptr, bs, (int)n, y_dev, ys_dev, g_dev, g_mant, g_shift, eps_mant, eps_shift, h_dev,
+        hs_dev);
+    return (int)hipGetLastError();
+}
+
+extern "C" int kt_hip_ref_swiglu_sums(int dev, const kt_hip_ql_sums* g, const kt_hip_ql_sums* u, int64_t n,
+                                      const int64_t* silu_codes_dev, const kt_hip_codelut* silu, int32_t* h_dev,
+                                      kt_hip_qscale* hs_dev, void* stream) {
+    kt::RqSums gs{}, us{};
+    if (!silu_codes_dev || !silu || !h_dev || !hs_dev || n < 1 || n > (int64_t)kt::RD_THREADS * 8 || silu->n < 1 ||
+        !silu->right_identity || !rq_sums_of(g, n, &gs) || !rq_sums_of(u, n, &us) || gs.rec == hs_dev ||
+        us.rec == hs_dev || (gs.rec && gs.rec == us.rec))
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    kt::rd_swiglu_kernel<true><<<1, kt::RD_THREADS, 0, (hipStream_t)stream>>>(
+        nullptr, nullptr, nullptr, nullptr, gs, us, (int)n, silu_codes_dev, *silu, h_dev, hs_dev);
+    return (int)hipGetLastError();
+}
+
 extern "C" int kt_hip_ref_swiglu(int dev, const int32_t* g_dev, const kt_hip_qscale* gs_dev, const int32_t* u_dev,
                                  const kt_hip_qscale* us_dev, int64_t rows, int64_t n, const int64_t* silu_codes_dev,
                                  const kt_hip_codelut* silu, int32_t* h_dev, kt_hip_qscale* hs_dev, void* stream) {
@@ -1775,6 +2008,33 @@ extern "C" int kt_hip_ref_attention_step_ws(int dev, const int32_t* q_dev, const
     RD_TRY(hipSetDevice(dev));
     kt::RdAttn a{};
     a.q = q_dev, a.k = k_dev, a.v = v_dev, a.qs = qs_dev, a.ks = ks_dev, a.vs = vs_dev, a.pos = pos_dev;
+    a.nh = (int)nh, a.nkv = (int)nkv, a.hd = (int)hd, a.max_seq = (int)max_seq;
+    a.kc = kc_dev, a.vc = vc_dev, a.kscale = kscale_dev, a.vscale = vscale_dev, a.cos = cos_dev, a.sin = sin_dev;
+    a.isq_mant = isq_mant, a.isq_shift = isq_shift, a.exp_codes = exp_codes_dev, a.exp = *exp_lut;
+    a.o = o_dev, a.os = os_dev, a.ws = (unsigned char*)ws_dev;
+    return (int)kt::launch_rd_attention_step(a, (hipStream_t)stream);
+}
+
+extern "C" int kt_hip_ref_attention_step_sums(int dev, const kt_hip_ql_sums* q, const kt_hip_ql_sums* k,
+                                              const kt_hip_ql_sums* v, const int32_t* pos_dev, int64_t nh,
+                                              int64_t nkv, int64_t hd, int64_t max_seq, int32_t* kc_dev,
+                                              int32_t* vc_dev, kt_hip_sscale* kscale_dev, kt_hip_sscale* vscale_dev,
+                                              const kt_hip_sscale* cos_dev, const kt_hip_sscale* sin_dev,
+                                              int64_t isq_mant, int32_t isq_shift, const int64_t* exp_codes_dev,
+                                              const kt_hip_codelut* exp_lut, int32_t* o_dev, kt_hip_qscale* os_dev,
+                                              void* ws_dev, size_t ws_bytes, void* stream) {
+    if (!pos_dev || !kc_dev || !vc_dev || !kscale_dev || !vscale_dev || !cos_dev || !sin_dev || !exp_codes_dev ||
+        !exp_lut || !o_dev || !os_dev || !ws_dev)
+        return (int)hipErrorInvalidValue;
+    if (nh < 1 || nkv < 1 || nh % nkv || nh > KT_REF_MAX_HEADS || hd < 2 || (hd & 1) || hd > 1024 || max_seq < 1 ||
+        max_seq > KT_REF_ATTN_MAX_SEQ || exp_lut->n < 1 || isq_mant < 0 ||
+        (reinterpret_cast<uintptr_t>(ws_dev) & 15) || ws_bytes < kt_hip_ref_attention_step_workspace(max_seq, nh, hd))
+        return (int)hipErrorInvalidValue;
+    kt::RdAttn a{};
+    if (!rq_sums_of(q, nh * hd, &a.qsum) || !rq_sums_of(k, nkv * hd, &a.ksum) || !rq_sums_of(v, nkv * hd, &a.vsum))
+        return (int)hipErrorInvalidValue;
+    RD_TRY(hipSetDevice(dev));
+    a.sums = 1, a.pos = pos_dev;
     a.nh = (int)nh, a.nkv = (int)nkv, a.hd = (int)hd, a.max_seq = (int)max_seq;
     a.kc = kc_dev, a.vc = vc_dev, a.kscale = kscale_dev, a.vscale = vscale_dev, a.cos = cos_dev, a.sin = sin_dev;
     a.isq_mant = isq_mant, a.isq_shift = isq_shift, a.exp_codes = exp_codes_dev, a.exp = *exp_lut;

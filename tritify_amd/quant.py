@@ -94,6 +94,18 @@ class QuantLinear:
                        self.w_scale, self.bias, self.b_scale, ws, n, y_dev, os_dev, stream=stream, dev=self.dev)
         return y_dev, os_dev
 
+    def sums_ok(self) -> bool:
+        """Whether a one-row forward can stop at its exact sums (forward_sums): no bias, the one-launch product."""
+        return self.bias is None and B.quant_linear_sums_ok(self.in_features, self.out_features, self.pw)
+
+    def forward_sums(self, x_dev, xs_dev, rec=None, stream=None):
+        """forward_int of one row stopped at its exact sums, left in this layer's one-row workspace: a B.QlSums for the
+        op that reads the output next (B.ref_*_sums), which applies requant_dyn and writes the record to `rec` (or
+        none). That op must run before this layer's next one-row call. Asynchronous on `stream`."""
+        ws, n = self.workspace(1)
+        return B.quant_linear_multi_sums(x_dev, self.in_features, xs_dev, [self.out_features], self.w_planes, self.pw,
+                                         [self.w_scale], ws, n, recs=[rec], stream=stream, dev=self.dev)[0]
+
     def forward_int_host(self, x_codes, x_scale):
         """forward_int on host codes at Scale x_scale = (mant, shift): (y codes, dict of the output scale)."""
         torch = self.torch
@@ -177,3 +189,17 @@ class QuantLinearGroup:
         B.quant_linear_multi(x_dev, rows, self.in_features, xs_dev, self.outs, self.w_planes, self.pw, self.w_scales,
                              self.bias, self.b_scales, ws, n, y_devs, os_dev, stream=stream, dev=self.dev)
         return [(y, os_dev[4 * g:4 * g + 4]) for g, y in enumerate(y_devs)]
+
+    def sums_ok(self) -> bool:
+        """Whether a one-row forward can stop at its members' exact sums (forward_sums)."""
+        return (self.bias is None and all(o % 8 == 0 for o in self.outs[:-1]) and
+                B.quant_linear_sums_ok(self.in_features, self.out_features, self.pw))
+
+    def forward_sums(self, x_dev, xs_dev, os_dev=None, stream=None):
+        """forward_int of one row stopped at the members' exact sums (QuantLinear.forward_sums for each member, one
+        launch): a B.QlSums per member; their readers write the records to os_dev (one per member, consecutive) or
+        none."""
+        ws, n = self.workspace(1)
+        recs = None if os_dev is None else [os_dev[4 * g:4 * g + 4] for g in range(len(self.outs))]
+        return B.quant_linear_multi_sums(x_dev, self.in_features, xs_dev, self.outs, self.w_planes, self.pw,
+                                         self.w_scales, ws, n, recs=recs, stream=stream, dev=self.dev)

@@ -120,6 +120,11 @@ class RefDecoder:
             if n == 0:
                 raise ValueError(f"max_seq {self.max_seq} beyond the attention step's limit")
             self.attn_ws = torch.empty((n + 15) // 16 * 16, dtype=torch.uint8, device=self.device)
+        # each projection stops at its exact sums and the op reading its output applies requant_dyn (four launches
+        # fewer per layer, the same integers); sums=False keeps the requant launches
+        self.sums = (cfg.get("sums", True) and self.grouped and self.attn_ws is not None and
+                     self.dim <= B.REF_ADD_NORM_MAX and self.hidden <= B.REF_SWIGLU_SUMS_MAX and
+                     all(blk[n].sums_ok() for blk in self.blocks for n in ("qkv", "wo", "gu", "down")))
         self.new_cache()
 
     def new_cache(self) -> None:
@@ -159,6 +164,9 @@ class RefDecoder:
         g, gs = self.blocks[0]["in_norm"] if self.blocks else self.final_norm
         B.ref_rmsnorm(b["x"], r["x"], 1, self.dim, g, gs, self.eps, b["h"], r["h"], stream, dv)
         for i, blk in enumerate(self.blocks):
+            if self.sums:
+                self._block_sums(i, blk, stream)
+                continue
             if self.grouped:
                 blk["qkv"].forward_int(b["h"], r["h"], 1, y_devs=[b["q"], b["k"], b["v"]], os_dev=self._rec_qkv,
                                        stream=stream)
@@ -182,6 +190,25 @@ class RefDecoder:
             # the next block's input norm, or the final norm after the last block
             add_norm("m", self.blocks[i + 1]["in_norm"] if i + 1 < len(self.blocks) else self.final_norm)
         self._ql(self.lm_head, "h", "logits", stream)
+
+    def _block_sums(self, i: int, blk, stream) -> None:
+        """One block of decode_step with each projection stopped at its sums and requantized by its reader: q / k / v
+        -> attention, o -> add + post norm, gate / up -> SwiGLU, down -> add + the next norm (9 launches)."""
+        b, r, dv = self.buf, self.rec, self.dev
+        q, k, v = blk["qkv"].forward_sums(b["h"], r["h"], os_dev=self._rec_qkv, stream=stream)
+        B.ref_attention_step_sums(q, k, v, self.pos, self.nh, self.nkv, self.hd, self.max_seq, self.kc[i], self.vc[i],
+                                  self.ks[i], self.vs[i], self.cos, self.sin, self.inv_sqrt, self.exp_codes,
+                                  self.exp_lut, b["cat"], r["cat"], self.attn_ws, stream, dv)
+        a = blk["wo"].forward_sums(b["cat"], r["cat"], rec=r["a"], stream=stream)
+        g_, gs_ = blk["post_norm"]
+        B.ref_add_rmsnorm_sums(b["x"], r["x"], a, self.dim, b["x"], r["x"], g_, gs_, self.eps, b["h"], r["h"], stream,
+                               dv)
+        gt, up = blk["gu"].forward_sums(b["h"], r["h"], os_dev=self._rec_gu, stream=stream)
+        B.ref_swiglu_sums(gt, up, self.hidden, self.silu_codes, self.silu_lut, b["hh"], r["hh"], stream, dv)
+        m = blk["down"].forward_sums(b["hh"], r["hh"], rec=r["m"], stream=stream)
+        g_, gs_ = self.blocks[i + 1]["in_norm"] if i + 1 < len(self.blocks) else self.final_norm
+        B.ref_add_rmsnorm_sums(b["x"], r["x"], m, self.dim, b["x"], r["x"], g_, gs_, self.eps, b["h"], r["h"], stream,
+                               dv)
 
     def capture_greedy_step(self):
         """One position of greedy decoding as a HIP graph: decode_step of the token at self.token and position
