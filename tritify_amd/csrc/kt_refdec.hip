@@ -105,17 +105,72 @@ __device__ inline int64_t iabs(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64
 __device__ inline int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
 __device__ inline int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
 
-// Block-wide reductions over the CTA's 1024 threads; every thread gets the result.
+// Wave reductions without LDS: DPP moves between the lanes of one 16-lane row (the xor-1 and xor-2 partners within
+// quads, then the 8- and 16-lane mirrors) pair every lane with lanes holding disjoint, equal-sized groups, so four
+// steps leave each row's reduction (maximum, wrapping sum, the fold's order) in all of its lanes; the four rows'
+// results (lanes 0, 16, 32, 48) are then read into scalars and combined there. Every lane must be active.
+template <int CTRL>
+__device__ inline uint64_t dpp64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ inline uint64_t lane64(uint64_t v, int l) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+__device__ inline int64_t max64(int64_t a, int64_t b) { return b > a ? b : a; }
+__device__ inline int64_t row_max_i64(int64_t v) {
+    v = max64(v, (int64_t)dpp64<DPP_XOR1>((uint64_t)v));
+    v = max64(v, (int64_t)dpp64<DPP_XOR2>((uint64_t)v));
+    v = max64(v, (int64_t)dpp64<DPP_HALF_MIRROR>((uint64_t)v));
+    return max64(v, (int64_t)dpp64<DPP_MIRROR>((uint64_t)v));
+}
+__device__ inline uint64_t row_sum_u64(uint64_t v) {  // wrapping
+    v += dpp64<DPP_XOR1>(v);
+    v += dpp64<DPP_XOR2>(v);
+    v += dpp64<DPP_HALF_MIRROR>(v);
+    return v + dpp64<DPP_MIRROR>(v);
+}
+// a u128 (hi, lo) summed over each row
+template <int CTRL>
+__device__ inline void add128_dpp(uint64_t& hi, uint64_t& lo) {
+    const uint64_t ohi = dpp64<CTRL>(hi), olo = dpp64<CTRL>(lo), t = lo + olo;
+    hi += ohi + (t < lo), lo = t;
+}
+__device__ inline void add128_row(uint64_t& hi, uint64_t& lo) {
+    add128_dpp<DPP_XOR1>(hi, lo);
+    add128_dpp<DPP_XOR2>(hi, lo);
+    add128_dpp<DPP_HALF_MIRROR>(hi, lo);
+    add128_dpp<DPP_MIRROR>(hi, lo);
+}
+__device__ inline int64_t wave_max_i64(int64_t v) {
+    v = row_max_i64(v);
+    return max64(max64((int64_t)lane64(v, 0), (int64_t)lane64(v, 16)),
+                 max64((int64_t)lane64(v, 32), (int64_t)lane64(v, 48)));
+}
+__device__ inline uint64_t wave_sum_u64(uint64_t v) {
+    v = row_sum_u64(v);
+    return lane64(v, 0) + lane64(v, 16) + lane64(v, 32) + lane64(v, 48);
+}
+// Block-wide reductions over the CTA's 1024 threads; every thread gets the result: each wave's result to LDS, one
+// barrier, the 16 of them reduced in row 0 of every wave.
 __device__ int64_t block_max_i64(int64_t v, int64_t* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const int64_t u = __shfl_xor(v, o, 64);
-        v = u > v ? u : v;
-    }
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    v = wave_max_i64(v);
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    v = red[0];
-    for (int w = 1; w < RD_WAVES; w++) v = red[w] > v ? red[w] : v;
+    v = (int64_t)lane64((uint64_t)row_max_i64(lane < RD_WAVES ? red[lane] : INT64_MIN), 0);
+    __syncthreads();
+    return v;
+}
+__device__ int64_t block_sum_i64(int64_t v, int64_t* red) {  // wrapping
+    v = (int64_t)wave_sum_u64((uint64_t)v);
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = (int64_t)lane64(row_sum_u64(lane < RD_WAVES ? (uint64_t)red[lane] : 0), 0);
     __syncthreads();
     return v;
 }
@@ -149,19 +204,14 @@ template <int K>
 __device__ void block_max_k(int64_t (&v)[K], int64_t* red) {
 #pragma unroll
     for (int k = 0; k < K; k++) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const int64_t u = __shfl_xor(v[k], o, 64);
-            v[k] = u > v[k] ? u : v[k];
-        }
+        v[k] = wave_max_i64(v[k]);
         if ((threadIdx.x & 63) == 0) red[k * RD_WAVES + (threadIdx.x >> 6)] = v[k];
     }
     __syncthreads();
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int k = 0; k < K; k++) {
-        v[k] = red[k * RD_WAVES];
-        for (int w = 1; w < RD_WAVES; w++) v[k] = red[k * RD_WAVES + w] > v[k] ? red[k * RD_WAVES + w] : v[k];
-    }
+    for (int k = 0; k < K; k++)
+        v[k] = (int64_t)lane64((uint64_t)row_max_i64(lane < RD_WAVES ? red[k * RD_WAVES + lane] : INT64_MIN), 0);
     __syncthreads();
 }
 
@@ -193,41 +243,89 @@ __device__ inline ScIdx sc_pick(ScIdx a, ScIdx b) {
     if (ab && ba) return a.idx > b.idx ? a : b;
     return ba ? b : a;
 }
-// n: how many leading threads hold items (the rest hold idx -1); every thread of the CTA calls it. The fold is by
-// value, then by index: each Scale is normalized exactly to m * 2^-e with m's top bit set (a zero Scale: the
-// smallest key), so comparing values (sc_ge) is comparing (e, m) as integers, and three block maxima -- the largest
-// e, the largest m at it, the largest index among equal values (the fold's later-wins rule) -- find sc_pick's total
-// order's maximum with no Scale arithmetic in the tree. The winner's own Scale is returned. Ends with a barrier.
-__device__ ScIdx block_fold_max(ScIdx v, ScIdx* red, int n) {
-    (void)n;
-    int64_t* r64 = reinterpret_cast<int64_t*>(red);  // 3 x RD_WAVES maxima, then the winner at red[RD_THREADS - 1]
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// The fold's total order as a key of three words per item: each Scale normalized exactly to m * 2^e with m's top bit
+// set (e = -shift - clz(mant) lies in [-2^31 - 63, 2^31], stored as e + 2^40 > 0), so comparing values (sc_ge) is
+// comparing (e, m) as integers, and the index breaks ties (the fold's later-wins rule). The third word holds the
+// index above the item's clz, which the order then ignores (indices are distinct) and from which the winner's own
+// (mant, shift) comes back exactly: mant = m >> clz, shift = -e - clz. A dead item (idx < 0 or a zero Scale) is the
+// key (0, 0, 0), below every live one.
+struct FoldKey {
+    uint64_t e, m, i;
+};
+__device__ inline FoldKey fold_key(const ScIdx& v) {
     const bool live = v.idx >= 0 && v.s.mant != 0;
     const uint64_t a = (uint64_t)v.s.mant;
     const int lz = live ? __builtin_clzll(a) : 0;
-    const int64_t e = live ? -(int64_t)v.s.shift - lz : INT64_MIN;
-    const uint64_t m = live ? a << lz : 0;
-    auto bmax = [&](uint64_t x, int slot, bool is_signed) -> uint64_t {  // a block maximum, signed or unsigned
-        auto gt = [&](uint64_t p, uint64_t q) { return is_signed ? (int64_t)p > (int64_t)q : p > q; };
+    return live ? FoldKey{(uint64_t)(-(int64_t)v.s.shift - lz + (1LL << 40)), a << lz,
+                          ((uint64_t)(uint32_t)v.idx << 6) | (uint64_t)lz}
+                : FoldKey{0, 0, 0};
+}
+__device__ inline ScIdx fold_item(const FoldKey& k) {
+    if (k.e == 0) return ScIdx{Sc{0, 0}, -1};
+    const int lz = (int)(k.i & 63);
+    return ScIdx{Sc{(int64_t)(k.m >> lz), (int32_t)(-((int64_t)k.e - (1LL << 40)) - lz)}, (int)(k.i >> 6)};
+}
+__device__ inline bool fold_gt(const FoldKey& x, const FoldKey& y) {
+    return x.e != y.e ? x.e > y.e : (x.m != y.m ? x.m > y.m : x.i > y.i);
+}
+template <int CTRL>
+__device__ inline void fold_dpp(FoldKey& k) {
+    const FoldKey u{dpp64<CTRL>(k.e), dpp64<CTRL>(k.m), dpp64<CTRL>(k.i)};
+    if (fold_gt(u, k)) k = u;
+}
+__device__ inline void fold_row(FoldKey& k) {
+    fold_dpp<DPP_XOR1>(k);
+    fold_dpp<DPP_XOR2>(k);
+    fold_dpp<DPP_HALF_MIRROR>(k);
+    fold_dpp<DPP_MIRROR>(k);
+}
+__device__ inline FoldKey fold_lane(const FoldKey& k, int l) { return FoldKey{lane64(k.e, l), lane64(k.m, l), lane64(k.i, l)}; }
+// The engine's fold over K sequences at once, one item per thread for each: the largest key of each wave by DPP
+// steps, one barrier, the 16 waves' keys folded in row 0 of every wave; the winners (their own Scales and indices)
+// are returned. Ends with a barrier. red: at least 3 K RD_WAVES words.
+template <int K>
+__device__ void block_fold_max_k(ScIdx (&v)[K], ScIdx* red) {
+    uint64_t* r64 = reinterpret_cast<uint64_t*>(red);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    FoldKey k[K];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const uint64_t u = (uint64_t)__shfl_xor((long long)x, o, 64);
-            x = gt(u, x) ? u : x;
+    for (int q = 0; q < K; q++) {
+        k[q] = fold_key(v[q]);
+        fold_row(k[q]);
+        FoldKey b = fold_lane(k[q], 0);
+#pragma unroll
+        for (int l = 16; l < 64; l += 16) {
+            const FoldKey c = fold_lane(k[q], l);
+            if (fold_gt(c, b)) b = c;
         }
-        if (lane == 0) r64[slot * RD_WAVES + w] = (int64_t)x;
-        __syncthreads();
-        uint64_t r = (uint64_t)r64[slot * RD_WAVES];
-        for (int q = 1; q < RD_WAVES; q++) r = gt((uint64_t)r64[slot * RD_WAVES + q], r) ? (uint64_t)r64[slot * RD_WAVES + q] : r;
-        return r;
-    };
-    const int64_t emax = (int64_t)bmax((uint64_t)e, 0, true);
-    const uint64_t mmax = bmax(e == emax ? m : 0, 1, false);
-    const int64_t imax = (int64_t)bmax((uint64_t)(int64_t)(e == emax && m == mmax && v.idx >= 0 ? v.idx : -1), 2, true);
-    if (imax >= 0 && v.idx == imax) red[RD_THREADS - 1] = v;
+        k[q] = b;
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int q = 0; q < K; q++) {
+            uint64_t* d = r64 + (q * RD_WAVES + w) * 3;
+            d[0] = k[q].e, d[1] = k[q].m, d[2] = k[q].i;
+        }
     __syncthreads();
-    const ScIdx r = imax >= 0 ? red[RD_THREADS - 1] : ScIdx{Sc{0, 0}, -1};
+#pragma unroll
+    for (int q = 0; q < K; q++) {
+        FoldKey b{0, 0, 0};
+        if (lane < RD_WAVES) {
+            const uint64_t* d = r64 + (q * RD_WAVES + lane) * 3;
+            b = FoldKey{d[0], d[1], d[2]};
+        }
+        fold_row(b);
+        v[q] = fold_item(fold_lane(b, 0));
+    }
     __syncthreads();
-    return r;
+}
+// n: how many leading threads hold items (the rest hold idx -1); every thread of the CTA calls it. Ends with a
+// barrier.
+__device__ ScIdx block_fold_max(ScIdx v, ScIdx* red, int n) {
+    (void)n;
+    ScIdx a[1] = {v};
+    block_fold_max_k<1>(a, red);
+    return a[0];
 }
 
 // CodeLut::index / code_at (kt-int/src/lib.rs:382-395) with the call's factor m = scale * inv_step.
@@ -270,10 +368,12 @@ __device__ void rd_norm_row(int32_t (&xv)[NV], const int32_t (&gv)[NV], int dim,
         const uint64_t sq = (uint64_t)(v * v), t = lo + sq;
         hi += t < lo, lo = t;
     }
+    add128_row(hi, lo);
+    {  // the four rows' sums
+        u128 w = 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t ohi = __shfl_xor(hi, o, 64), olo = __shfl_xor(lo, o, 64), t = lo + olo;
-        hi += ohi + (t < lo), lo = t;
+        for (int l = 0; l < 64; l += 16) w += ((u128)lane64(hi, l) << 64) | lane64(lo, l);
+        hi = (uint64_t)(w >> 64), lo = (uint64_t)w;
     }
     if (lane == 0) sq2[wave][0] = hi, sq2[wave][1] = lo;
     __syncthreads();
@@ -730,8 +830,11 @@ __device__ __forceinline__ void rd_attention_core(const RdAttn& a, unsigned char
         bv = sc_pick(bv, ScIdx{vj, j});
         bs = sc_pick(bs, ScIdx{sj, j});
     }
-    bv = block_fold_max(bv, redsc, steps);
-    bs = block_fold_max(bs, redsc, steps);
+    {
+        ScIdx two[2] = {bv, bs};
+        block_fold_max_k<2>(two, redsc);
+        bv = two[0], bs = two[1];
+    }
     if (tid == 0) {
         par[0] = bv.s, par[1] = bs.s;
         par[2] = bs.s.mant ? sc_mul(bs.s, Sc{a.exp.inv_mant, a.exp.inv_shift}) : Sc{0, 0};
@@ -1086,8 +1189,11 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         bv = sc_pick(bv, ScIdx{vj, j});
         bs = sc_pick(bs, ScIdx{sj, j});
     }
-    bv = block_fold_max(bv, redsc, steps);
-    bs = block_fold_max(bs, redsc, steps);
+    {
+        ScIdx two[2] = {bv, bs};
+        block_fold_max_k<2>(two, redsc);
+        bv = two[0], bs = two[1];
+    }
     if (tid == 0) {
         par[0] = bv.s, par[1] = bs.s;
         par[2] = bs.s.mant ? sc_mul(bs.s, Sc{a.exp.inv_mant, a.exp.inv_shift}) : Sc{0, 0};
@@ -1143,12 +1249,10 @@ __global__ __launch_bounds__(RD_THREADS) void rd_attention_heads_kernel(RdAttn a
         S[j] = ec;
         sum += ec;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    sum = (int64_t)wave_sum_u64((uint64_t)sum);
     if ((tid & 63) == 0) red[tid >> 6] = sum;
     __syncthreads();
-    int64_t sumc = 0;
-    for (int w = 0; w < RD_WAVES; w++) sumc += red[w];
+    const int64_t sumc = (int64_t)lane64(row_sum_u64((tid & 63) < RD_WAVES ? (uint64_t)red[tid & 63] : 0), 0);
     if (sumc <= 0) {
         for (int d = tid; d < hd; d += RD_THREADS) HO[((size_t)h * P + part) * hd + d] = 0;
         if (tid == 0 && part == 0) HSC[h] = Sc{0, 0};
