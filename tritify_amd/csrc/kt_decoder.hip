@@ -318,8 +318,11 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
         for (int q = 0; q < 4; q++) {
             const size_t blk = (size_t)(on / 32) * KB + 2 * h + (q >> 1);
             const int slot = on % 32 + 32 * (q & 1);
-            wl[q] = has_col ? *reinterpret_cast<const v4i*>(fo.lo + blk * 1024 + 16 * slot) : v4i{};
-            wn[q] = has_col ? *reinterpret_cast<const v2i*>(fo.nib + blk * 512 + 8 * slot) : v2i{};
+            // W_o, read once per launch: non-temporal, as the other weight streams
+            wl[q] = has_col ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(fo.lo + blk * 1024 + 16 * slot))
+                            : v4i{};
+            wn[q] = has_col ? __builtin_nontemporal_load(reinterpret_cast<const v2i*>(fo.nib + blk * 512 + 8 * slot))
+                            : v2i{};
         }
     }
     const v4i q4 = *reinterpret_cast<const v4i*>(s_q + 16 * kq);

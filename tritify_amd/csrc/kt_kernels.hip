@@ -349,7 +349,8 @@ __global__ __launch_bounds__(256) void plane_skinny_kernel(const int8_t* __restr
         for (int c = 0; c < PS_CPW; c++)
 #pragma unroll
             for (int j = 0; j < PW; j++)
-                wv[c][j] = nb + c < N ? *reinterpret_cast<const v4i*>(wb + j * wplane + (size_t)(nb + c) * kp + ko)
+                wv[c][j] = nb + c < N ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(
+                                            wb + j * wplane + (size_t)(nb + c) * kp + ko))  // read once: non-temporal
                                       : v4i{};
 #pragma unroll
         for (int c = 0; c < PS_CPW; c++)
@@ -753,8 +754,8 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
             // a pair past the end re-reads the last pair (its x is masked below): every load stays in the buffers
             const int p = w + NW * (U * b + u);
             const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
-            L[u] = bload16(rL, oL, pl * 2048u);
-            D[u] = bload8(rN, oN, pl * 1024u);
+            L[u] = bload16nt(rL, oL, pl * 2048u);  // the weights: read once per launch
+            D[u] = bload8nt(rN, oN, pl * 1024u);
             if constexpr (!NORM) {
 #pragma unroll
                 for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);
@@ -1072,10 +1073,10 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
         for (int u = 0; u < U; u++) {
             const int p = w + NW * (U * b + u);
             const uint32_t pl = (uint32_t)(p < np ? p : np - 1);
-            Lg[u] = bload16(rL, oL, pl * 2048u);
-            Dg[u] = bload8(rN, oN, pl * 1024u);
-            Lu[u] = bload16(rL, uL, pl * 2048u);
-            Du[u] = bload8(rN, uN, pl * 1024u);
+            Lg[u] = bload16nt(rL, oL, pl * 2048u);  // the weights: read once per launch
+            Dg[u] = bload8nt(rN, oN, pl * 1024u);
+            Lu[u] = bload16nt(rL, uL, pl * 2048u);
+            Du[u] = bload8nt(rN, uN, pl * 1024u);
             if constexpr (!NORM) {
 #pragma unroll
                 for (int t = 0; t < MT; t++) X[u][t] = bload16(rX, oX[t], pl * 64u);

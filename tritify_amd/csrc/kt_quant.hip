@@ -267,14 +267,17 @@ __global__ __launch_bounds__(QS_THREADS) void ql_skinny_kernel(const int32_t* __
     const size_t wplane = (size_t)N * kp;
     const int nch = kp / 16;
 
-    v4i wn[QS_CPW][PW];  // the weights of the wave's next chunk
+    // the weights of the wave's next chunk; non-temporal loads (read once per call), so the stream does not push the
+    // small tensors the next launches read (the sums, the records, the cache rows) out of the caches
+    v4i wn[QS_CPW][PW];
     auto wload = [&](int q) {
 #pragma unroll
         for (int c = 0; c < QS_CPW; c++)
 #pragma unroll
             for (int j = 0; j < PW; j++)
                 wn[c][j] = q < nch && nb + c < N
-                               ? *reinterpret_cast<const v4i*>(wb + j * wplane + (size_t)(nb + c) * kp + 16 * (size_t)q)
+                               ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(
+                                     wb + j * wplane + (size_t)(nb + c) * kp + 16 * (size_t)q))
                                : v4i{};
     };
     wload(lane);  // in flight while the row is quantized

@@ -75,6 +75,14 @@ __device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 __device__ __forceinline__ v2i bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
 }
+// The same loads non-temporal (cache policy nt): for weight streams a launch reads once, so that they do not push
+// the small tensors the next launches read out of the caches.
+__device__ __forceinline__ v4i bload16nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
+}
+__device__ __forceinline__ v2i bload8nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 2);
+}
 // An offset that is out of range for every buffer here (buffers are below 4 GB - 16 B).
 #define KT_OOB 0xFFFFFFF0u
 
