@@ -120,6 +120,12 @@ __device__ inline uint64_t lane64(uint64_t v, int l) {
            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
 }
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+// Lane 0's value as a wave-uniform one (scalar registers). The one-thread Scale chains run in all lanes of wave 0 on
+// such values, so their integer arithmetic is scalar and their branches are uniform, rather than per-lane code under
+// a one-lane exec mask.
+__device__ inline int64_t uni64(int64_t v) { return (int64_t)lane64((uint64_t)v, 0); }
+__device__ inline Sc uni(Sc s) { return Sc{uni64(s.mant), __builtin_amdgcn_readlane(s.shift, 0)}; }
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 __device__ inline int64_t max64(int64_t a, int64_t b) { return b > a ? b : a; }
 __device__ inline int64_t row_max_i64(int64_t v) {
     v = max64(v, (int64_t)dpp64<DPP_XOR1>((uint64_t)v));
@@ -221,6 +227,12 @@ __device__ inline bool rqs_live(const QlState* st, int64_t ymax) { return st->mo
 __device__ inline Sc rqs_scale(const QlState* st, int64_t ymax) {
     return rqs_live(st, ymax) ? sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), Sc{st->c_mant, st->c_shift})
                               : Sc{0, 0};
+}
+// rqs_scale with the state's fields read as wave-uniform values (wave 0's scalar chains)
+__device__ inline Sc rqs_scale_u(const QlState* st, int64_t ymax) {
+    const int mode = __builtin_amdgcn_readfirstlane(st->mode);
+    const Sc c = uni(Sc{st->c_mant, st->c_shift});
+    return mode == 0 && ymax > 0 ? sc_mul(from_ratio((u128)(uint64_t)ymax, (u128)ACT_LEVELS), c) : Sc{0, 0};
 }
 __device__ inline void rqs_record(const RqSums& r, int64_t ymax, Sc s) {
     if (!r.rec) return;
@@ -377,18 +389,23 @@ __device__ void rd_norm_row(int32_t (&xv)[NV], const int32_t (&gv)[NV], int dim,
     }
     if (lane == 0) sq2[wave][0] = hi, sq2[wave][1] = lo;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        u128 ss = 0;
-        for (int w = 0; w < RD_WAVES; w++) ss += ((u128)sq2[w][0] << 64) | sq2[w][1];
-        const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xs), xs);
+    const int wv = wave_id();
+    Sc cc{0, 0};  // wave 0: the row factor (uniform)
+    if (wv == 0) {  // the 16 waves' sums (lane q < 16 reads wave q's), then the row factor's chain on scalars
+        uint64_t h2 = lane < RD_WAVES ? sq2[lane][0] : 0, l2 = lane < RD_WAVES ? sq2[lane][1] : 0;
+        add128_row(h2, l2);
+        const u128 ss = ((u128)lane64(h2, 0) << 64) | lane64(l2, 0);
+        const Sc xu = uni(xs);
+        const Sc mean_sq = sc_mul(sc_mul(from_ratio(ss, (u128)dim), xu), xu);
         const Sc denom = sc_add(mean_sq, eps);
         const Sc inv = denom.mant == 0 ? Sc{0, 0} : sc_rsqrt(denom);
-        const Sc c0 = sc_mul(sc_mul(xs, inv), gs);
-        cf[0] = c0;  // the largest of one row's factors is that factor
-        cf[1] = c0.mant != 0 ? sc_mul(c0, sc_recip(c0)) : Sc{0, 0};
+        cc = sc_mul(sc_mul(xu, inv), gs);  // the largest of one row's factors is that factor
+        const Sc f = cc.mant != 0 ? sc_mul(cc, sc_recip(cc)) : Sc{0, 0};
+        if (lane == 0) cf[0] = cc, cf[1] = f;
     }
     __syncthreads();
-    const Sc cc = cf[0], f0 = cf[1];
+    const Sc f0 = cf[1];
+    if (wv != 0) cc = cf[0];
     int64_t hv[NV];
     int64_t m = 0;
 #pragma unroll
@@ -405,8 +422,10 @@ __device__ void rd_norm_row(int32_t (&xv)[NV], const int32_t (&gv)[NV], int dim,
         const int i = threadIdx.x + RD_THREADS * k;
         if (i < dim) y[i] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
     }
-    if (threadIdx.x == 0)
-        put_rec(ys, gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc));
+    if (wv == 0) {
+        const Sc r = gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), cc);
+        if (lane == 0) put_rec(ys, r);
+    }
 }
 
 // RmsNorm::forward_int (layers.rs:392-434) over `rows` rows of `dim`: per row the exact sum of squares, its
@@ -578,24 +597,28 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_norm_kernel(const int32_t* 
 #pragma unroll
         for (int k = 0; k < RD_AN; k++) bv[k] = live ? rq_apply(d, bacc[k]) : 0;
     }
-    if (threadIdx.x == 0) {
+    const int wv = wave_id(), lane = threadIdx.x & 63;
+    Sc common{0, 0};  // wave 0: the common Scale (uniform)
+    if (wv == 0) {  // the Scale chain on scalars
         Sc bs;
         if constexpr (SUMS) {
-            bs = rqs_scale(bsum.st, bmax);
-            rqs_record(bsum, bmax, bs);
+            bs = rqs_scale_u(bsum.st, bmax);
+            if (lane == 0) rqs_record(bsum, bmax, bs);
         } else {
-            bs = rec_sc(bs_rec);
+            bs = uni(rec_sc(bs_rec));
         }
-        const Sc as = rec_sc(as_rec);
-        const Sc common = sc_ge(as, bs) ? as : bs;
-        par[0] = common;
+        const Sc as = uni(rec_sc(as_rec));
+        common = sc_ge(as, bs) ? as : bs;
+        Sc fa{0, 0}, fb{0, 0};
         if (common.mant != 0) {
             const Sc cinv = sc_recip(common);
-            par[1] = sc_mul(as, cinv), par[2] = sc_mul(bs, cinv);
+            fa = sc_mul(as, cinv), fb = sc_mul(bs, cinv);
         }
+        if (lane == 0) par[0] = common, par[1] = fa, par[2] = fb;
     }
     __syncthreads();
-    const Sc common = par[0], fa = par[1], fb = par[2];
+    const Sc fa = par[1], fb = par[2];
+    if (wv != 0) common = par[0];
     int64_t m = 0, hv[RD_AN];
 #pragma unroll
     for (int k = 0; k < RD_AN; k++) {
@@ -613,10 +636,10 @@ __global__ __launch_bounds__(RD_THREADS) void rd_add_norm_kernel(const int32_t* 
         yv[k] = gmax == 0 ? 0 : rq_apply(rd_gmax, hv[k]);
         if (i < n) y[i] = yv[k];
     }
-    Sc xs{0, 0};  // the sum's Scale: thread 0 writes the record and carries it into the norm
-    if (threadIdx.x == 0) {
+    Sc xs{0, 0};  // the sum's Scale: wave 0 writes the record and carries it into the norm
+    if (wv == 0) {
         xs = gmax == 0 ? Sc{0, 0} : sc_mul(from_ratio((u128)(uint64_t)gmax, (u128)ACT_LEVELS), common);
-        put_rec(ys, xs);
+        if (lane == 0) put_rec(ys, xs);
     }
     rd_norm_row<RD_AN>(yv, gv, n, xs, Sc{g_mant, g_shift}, Sc{e_mant, e_shift}, h, hs, red);
 }
