@@ -24,6 +24,7 @@
 #include <mutex>
 #include <vector>
 
+#include "kt_dpp.h"
 #include "kt_kernels.h"
 #include "kt_scale_dev.h"
 #include "kt_w12_core.h"
@@ -295,7 +296,13 @@ __global__ __launch_bounds__(QS_THREADS) void ql_skinny_kernel(const int32_t* __
             m = a > m ? a : m;
         }
     }
-    m = block_max(m, red);
+    {  // max |x| over the CTA: each wave's by DPP, then the QS_WAVES of them
+        m = wave_max_u32(m);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < QS_WAVES; w++) m = red[w] > m ? red[w] : m;
+    }
     const double rinv = m != 0 ? 1.0 / (double)m : 0.0;
 #pragma unroll
     for (int k = 0; k < QPT; k++) {
@@ -354,9 +361,7 @@ __global__ __launch_bounds__(QS_THREADS) void ql_skinny_kernel(const int32_t* __
 #pragma unroll
     for (int c = 0; c < QS_CPW; c++)
 #pragma unroll
-        for (int i = 0; i < NG; i++)
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) acc[c][i] += __shfl_xor(acc[c][i], o);
+        for (int i = 0; i < NG; i++) acc[c][i] = wave_sum_i32(acc[c][i]);  // the wave's sums, in every lane
     int64_t lmax = 0;
     if (lane == 0) {
         const bool badd = s_badd != 0;

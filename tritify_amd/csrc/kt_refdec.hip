@@ -25,6 +25,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include "kt_dpp.h"
 #include "kt_kernels.h"
 #include "kt_scale_dev.h"
 #include "kt_w12_core.h"
@@ -105,61 +106,12 @@ __device__ inline int64_t iabs(int64_t v) { return v < 0 ? (int64_t)(0 - (uint64
 __device__ inline int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
 __device__ inline int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
 
-// Wave reductions without LDS: DPP moves between the lanes of one 16-lane row (the xor-1 and xor-2 partners within
-// quads, then the 8- and 16-lane mirrors) pair every lane with lanes holding disjoint, equal-sized groups, so four
-// steps leave each row's reduction (maximum, wrapping sum, the fold's order) in all of its lanes; the four rows'
-// results (lanes 0, 16, 32, 48) are then read into scalars and combined there. Every lane must be active.
-template <int CTRL>
-__device__ inline uint64_t dpp64(uint64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
-    return ((uint64_t)hi << 32) | lo;
-}
-__device__ inline uint64_t lane64(uint64_t v, int l) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-}
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
 // Lane 0's value as a wave-uniform one (scalar registers). The one-thread Scale chains run in all lanes of wave 0 on
 // such values, so their integer arithmetic is scalar and their branches are uniform, rather than per-lane code under
 // a one-lane exec mask.
 __device__ inline int64_t uni64(int64_t v) { return (int64_t)lane64((uint64_t)v, 0); }
 __device__ inline Sc uni(Sc s) { return Sc{uni64(s.mant), __builtin_amdgcn_readlane(s.shift, 0)}; }
 __device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
-__device__ inline int64_t max64(int64_t a, int64_t b) { return b > a ? b : a; }
-__device__ inline int64_t row_max_i64(int64_t v) {
-    v = max64(v, (int64_t)dpp64<DPP_XOR1>((uint64_t)v));
-    v = max64(v, (int64_t)dpp64<DPP_XOR2>((uint64_t)v));
-    v = max64(v, (int64_t)dpp64<DPP_HALF_MIRROR>((uint64_t)v));
-    return max64(v, (int64_t)dpp64<DPP_MIRROR>((uint64_t)v));
-}
-__device__ inline uint64_t row_sum_u64(uint64_t v) {  // wrapping
-    v += dpp64<DPP_XOR1>(v);
-    v += dpp64<DPP_XOR2>(v);
-    v += dpp64<DPP_HALF_MIRROR>(v);
-    return v + dpp64<DPP_MIRROR>(v);
-}
-// a u128 (hi, lo) summed over each row
-template <int CTRL>
-__device__ inline void add128_dpp(uint64_t& hi, uint64_t& lo) {
-    const uint64_t ohi = dpp64<CTRL>(hi), olo = dpp64<CTRL>(lo), t = lo + olo;
-    hi += ohi + (t < lo), lo = t;
-}
-__device__ inline void add128_row(uint64_t& hi, uint64_t& lo) {
-    add128_dpp<DPP_XOR1>(hi, lo);
-    add128_dpp<DPP_XOR2>(hi, lo);
-    add128_dpp<DPP_HALF_MIRROR>(hi, lo);
-    add128_dpp<DPP_MIRROR>(hi, lo);
-}
-__device__ inline int64_t wave_max_i64(int64_t v) {
-    v = row_max_i64(v);
-    return max64(max64((int64_t)lane64(v, 0), (int64_t)lane64(v, 16)),
-                 max64((int64_t)lane64(v, 32), (int64_t)lane64(v, 48)));
-}
-__device__ inline uint64_t wave_sum_u64(uint64_t v) {
-    v = row_sum_u64(v);
-    return lane64(v, 0) + lane64(v, 16) + lane64(v, 32) + lane64(v, 48);
-}
 // Block-wide reductions over the CTA's 1024 threads; every thread gets the result: each wave's result to LDS, one
 // barrier, the 16 of them reduced in row 0 of every wave.
 __device__ int64_t block_max_i64(int64_t v, int64_t* red) {
