@@ -13,6 +13,7 @@
 #include <limits.h>
 #include <stdint.h>
 
+#include "kt_dpp.h"
 #include "kt_kernels.h"
 #include "kt_w12_core.h"
 
@@ -337,8 +338,7 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
         sc = __builtin_amdgcn_sdot4(q4.y, k4.y, sc, false);
         sc = __builtin_amdgcn_sdot4(q4.z, k4.z, sc, false);
         sc = __builtin_amdgcn_sdot4(q4.w, k4.w, sc, false);
-        sc += __shfl_xor(sc, 1);
-        sc += __shfl_xor(sc, 2);
+        sc = add_xor2(add_xor1(sc));  // the quad's sum (DPP)
         if (j < L) {
             if (kq == 0) s_sc[j] = sc;
             mx = sc > mx ? sc : mx;
@@ -359,11 +359,7 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
             score(j, j < p ? *reinterpret_cast<const v4i*>(kg + (size_t)j * rstride + 16 * kq) : v4i{});
         }
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const int v = __shfl_xor(mx, d);
-        mx = v > mx ? v : mx;
-    }
+    mx = wave_max_i32(mx);
     if (lane == 0) s_red[0][w] = mx;
     __syncthreads();
     mx = s_red[0][0];
@@ -378,8 +374,7 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
         s_sc[j] = e;
         den += e;
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) den += __shfl_xor(den, d);
+    den = wave_sum_i32(den);
     if (lane == 0) s_red[1][w] = den;
     __syncthreads();
 
@@ -399,11 +394,7 @@ __global__ __launch_bounds__(ATT_NT) void dec_attention_step_kernel(const int8_t
             for (int b = 0; b < 4; b++) a[b] += __mul24(e, (int)(int8_t)(vv >> (8 * b)));  // |e v| < 2^23
         }
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            a[b] += __shfl_xor(a[b], 16);
-            a[b] += __shfl_xor(a[b], 32);
-            accd[b] += a[b];
-        }
+        for (int b = 0; b < 4; b++) accd[b] += add_xor32(add_xor16(a[b]));
     };
 #pragma unroll
     for (int c = 0; c < ATT_PRE; c++) {

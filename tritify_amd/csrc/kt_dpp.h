@@ -79,6 +79,29 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
               mx((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
 }
 
+__device__ inline int32_t wave_max_i32(int32_t v) {
+    auto mx = [](int32_t a, int32_t b) { return b > a ? b : a; };
+    v = mx(v, (int32_t)dpp32<DPP_XOR1>((uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_XOR2>((uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_HALF_MIRROR>((uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_MIRROR>((uint32_t)v));
+    return mx(mx(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+              mx(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+// x plus its value in lane l ^ 1, l ^ 2 (DPP), l ^ 16 and l ^ 32 (the lane-swap instructions: swapping the odd
+// 16-lane rows of one copy of x with the even rows of another, or the upper 32 lanes with the lower 32, leaves
+// every lane's partner in one of the two copies), wrapping: no LDS.
+__device__ inline int32_t add_xor1(int32_t x) { return x + (int32_t)dpp32<DPP_XOR1>((uint32_t)x); }
+__device__ inline int32_t add_xor2(int32_t x) { return x + (int32_t)dpp32<DPP_XOR2>((uint32_t)x); }
+__device__ inline int32_t add_xor16(int32_t x) {
+    const auto p = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    return (int32_t)(p[0] + p[1]);
+}
+__device__ inline int32_t add_xor32(int32_t x) {
+    const auto p = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return (int32_t)(p[0] + p[1]);
+}
+
 }  // namespace
 
 }  // namespace kt
