@@ -292,11 +292,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_
         }
     if (ql) {  // the CTA's largest |result| into the call's maximum
         __shared__ int64_t s_max[4];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const int64_t u = __shfl_xor(lmax, o);
-            lmax = u > lmax ? u : lmax;
-        }
+        lmax = wave_max_i64(lmax);
         if (lane == 0) s_max[wave] = lmax;
         __syncthreads();
         if (tid == 0) {
@@ -372,8 +368,7 @@ __global__ __launch_bounds__(256) void plane_skinny_kernel(const int8_t* __restr
         for (int m = 0; m < MM; m++)
 #pragma unroll
             for (int g = 0; g < NG; g++)
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) acc[c][m][g] += __shfl_xor(acc[c][m][g], o);
+                acc[c][m][g] = wave_sum_i32(acc[c][m][g]);
     const bool badd = ql && ql_bias && ql->mode == 0;
     int64_t lmax = 0;
     if (lane == 0) {
@@ -804,9 +799,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_kernel(const int8_t* __res
             else
                 sP[w][(t * 16 + 4 * g + r) * 16 + c] = (int64_t)acc0[t][r] + 256 * (int64_t)acc1[t][r];
         }
-        int s = sx[t];
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
+        const int s = add_xor32(add_xor16(sx[t]));
         if (lane < 16) sX[w][t * 16 + lane] = s;
     }
     __syncthreads();
@@ -970,9 +963,7 @@ __global__ __launch_bounds__(512) void w12_skinny_lds_kernel(const int8_t* __res
     }
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) {
-        int sv = tt ? sx1 : sx0;
-        sv += __shfl_xor(sv, 16);
-        sv += __shfl_xor(sv, 32);
+        const int sv = add_xor32(add_xor16(tt ? sx1 : sx0));
         if (lane < 16) sX[pp][16 * (2 * ch + tt) + lane] = sv;
     }
     __syncthreads();
@@ -1129,9 +1120,7 @@ __global__ __launch_bounds__(64 * NW) void w12_skinny_swiglu_kernel(
             sPg[w][o] = (int32_t)((uint32_t)ag0[t][r] + ((uint32_t)ag1[t][r] << 8));
             sPu[w][o] = (int32_t)((uint32_t)au0[t][r] + ((uint32_t)au1[t][r] << 8));
         }
-        int s = sx[t];
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
+        const int s = add_xor32(add_xor16(sx[t]));
         if (lane < 16) sX[w][t * 16 + lane] = s;
     }
     if (tid < 256) sSilu[tid] = silu_v;

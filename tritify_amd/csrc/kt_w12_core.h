@@ -25,6 +25,7 @@
 
 #include <type_traits>
 
+#include "kt_dpp.h"
 #include "kt_hip.h"
 
 namespace kt {
@@ -290,8 +291,7 @@ __device__ __forceinline__ void norm_rows_to_lds(const int32_t* __restrict__ r, 
             const uint64_t sq = (uint64_t)(v * v);
             sh += sq >> 16, sl += sq & 0xFFFF;
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) sh += __shfl_xor(sh, o), sl += __shfl_xor(sl, o);
+        sh = wave_sum_u64(sh), sl = wave_sum_u64(sl);  // DPP, no LDS
         if (lane == 0) s_ss[w * 32 + m] = sh, s_ss[w * 32 + 16 + m] = sl;
     }
     __syncthreads();
