@@ -199,6 +199,29 @@ def test_from_ratio_64_bit_paths_equal_the_oracle(sd):
         assert scale_out(sd.sd_mul, am, ash, bm, bsh) == (w.mant, w.shift)
 
 
+def test_from_ratio_general_path_equals_the_oracle(sd):
+    """from_ratio past its 64-bit paths: a numerator past 2^62 or a denominator past 2^32 (the sums of squares over
+    a row against its length, the fold's ratios), the halving of both past 64 bits, divisors of 60 to 64 bits, and
+    quotients at a rounding boundary."""
+    rng = np.random.default_rng(20)
+    cases = []
+    for _ in range(6000):
+        cases.append((rand_bits(rng, int(rng.integers(60, 129))), rand_bits(rng, int(rng.integers(1, 129)))))
+        cases.append((rand_bits(rng, int(rng.integers(1, 129))), rand_bits(rng, int(rng.integers(30, 66)))))
+        cases.append((rand_bits(rng, int(rng.integers(64, 129))), int(rng.integers(1, 5000))))
+    for bd in (60, 61, 62, 63, 64):
+        for _ in range(300):
+            d = rand_bits(rng, bd)
+            q = rand_bits(rng, 32)
+            cases += [(q * d + d // 2 + e, d) for e in (-1, 0, 1)]
+    for num, den in cases:
+        if num >= 2**128 or num <= 0 or den <= 0 or den >= 2**128:
+            continue
+        want = O.from_ratio(num, den)
+        assert scale_out(sd.sd_from_ratio, num >> 64, num & U64, den >> 64, den & U64) == (want.mant, want.shift), \
+            (num, den)
+
+
 def test_applies_equal_the_oracle(sd):
     rng = np.random.default_rng(14)
     for _ in range(4000):
