@@ -123,15 +123,6 @@ __device__ int64_t block_max_i64(int64_t v, int64_t* red) {
     __syncthreads();
     return v;
 }
-__device__ int64_t block_sum_i64(int64_t v, int64_t* red) {  // wrapping
-    v = (int64_t)wave_sum_u64((uint64_t)v);
-    const int lane = threadIdx.x & 63;
-    if (lane == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    v = (int64_t)lane64(row_sum_u64(lane < RD_WAVES ? (uint64_t)red[lane] : 0), 0);
-    __syncthreads();
-    return v;
-}
 // The same reductions for CTAs of 256 threads (4 waves).
 __device__ int64_t block_max_4w(int64_t v, int64_t* red) {
 #pragma unroll
