@@ -111,26 +111,29 @@ typedef W12Tile<1, 2, 1, 4> GTileH;
 // The epilogue of one grouped output tile (rows row0 .. row0 + rows - 1 of group g, columns n0 .. n0 + BN - 1): the
 // int8 requant (EPI_I8) or the SwiGLU of the tile's gate/up block pairs (EPI_SWIGLU), staged through `smem`
 // (BM x BN bytes, free once the mainloop is done).
-template <class C, int EPI>
+// XR (the 288-row DMA tile): xs holds the strip of rows 256 .. 287, requantized into the same staged tile.
+template <class C, int EPI, int XR = 0>
 __device__ __forceinline__ void grouped_epilogue(const v16i (&acc0)[C::WTM][1], const v16i (&acc1)[C::WTM][1],
                                                  const int* sRow, int g, int row0, int rows, int n0, const int* sOff,
                                                  int N, const int32_t* __restrict__ mant,
                                                  const int32_t* __restrict__ shift, const int16_t* sSilu,
-                                                 int h_shift, int8_t* __restrict__ y, int ystride, int8_t* smem) {
-    constexpr int NT = C::NT, BM = C::BM, BN = C::BN;
-    const int tid = threadIdx.x;
+                                                 int h_shift, int8_t* __restrict__ y, int ystride, int8_t* smem,
+                                                 const DmaStrip* xs = nullptr) {
+    constexpr int NT = C::NT, BM = C::BM + XR, BN = C::BN;
+    const int tid = tid_now();
     const int32_t* gm = mant + (size_t)g * N;
     const int32_t* gs = shift + (size_t)g * N;
     int8_t* yg = y + (size_t)(sOff[g] + row0) * ystride;
     if constexpr (EPI == KT_EPI_I8) {
         w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, [](int n) { return n; }, smem);
+        if constexpr (XR != 0) w12_requant_strip8<BN>(*xs, sRow, gm, gs, n0, N, [](int n) { return n; }, smem);
         __syncthreads();
         constexpr int CH = BM * BN / 16;
         const bool vec = n0 + BN <= N && (ystride & 15) == 0;
 #pragma unroll
-        for (int i = 0; i < CH / NT; i++) {
+        for (int i = 0; i < (CH + NT - 1) / NT; i++) {
             const int idx = tid + NT * i, r = idx / (BN / 16), c = (idx % (BN / 16)) * 16;
-            if (r >= rows) continue;
+            if (idx >= CH || r >= rows) continue;
             const v4i v = *reinterpret_cast<const v4i*>(smem + r * BN + c);
             int8_t* dst = yg + (size_t)r * ystride + n0 + c;
             if (vec) {
@@ -148,6 +151,7 @@ __device__ __forceinline__ void grouped_epilogue(const v16i (&acc0)[C::WTM][1], 
             return (blk & 1) * F + (blk >> 1) * 32 + (n & 31);
         };
         w12_requant_tile8<C>(acc0, acc1, sRow, gm, gs, n0, N, chan, smem);
+        if constexpr (XR != 0) w12_requant_strip8<BN>(*xs, sRow, gm, gs, n0, N, chan, smem);
         __syncthreads();
         // the tile's columns are gate/up block pairs: hidden units n0/2 .. n0/2 + units - 1
         const int units = (N - n0 < BN ? N - n0 : BN) / 2;
@@ -178,7 +182,7 @@ __device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, ui
                                              int8_t* smem, int* sRow) {
     constexpr int NT = C::NT, BM = C::BM, BN = C::BN, AL = C::AL, AC = C::AC;
     static_assert(C::RING >= BM * BN, "the int8 output tile reuses the A ring");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = tid_now(), lane = tid & 63, wave = tid >> 6;
     const int KB = kp / 32;
     uint32_t oa[AL];
 #pragma unroll
@@ -208,9 +212,10 @@ __device__ __forceinline__ void grouped_tile(const __amdgpu_buffer_rsrc_t rA, ui
 }
 
 // The 256 x 128 tile of the DMA-fed grouped kernel (w12_mainloop_dma, 8 waves): the lanes' A pieces are gathered
-// rows of group g, rows at or past `rows` read zero.
+// rows of group g, rows at or past `rows` read zero. XR: the 288-row tile (a group's last tile absorbing a tail of
+// up to 32 rows).
 typedef W12Tile<2, 4, 1, 2, 4> GTileD;
-template <int EPI>
+template <int EPI, int XR = 0>
 __device__ __forceinline__ void grouped_tile_dma(const __amdgpu_buffer_rsrc_t rA, uint32_t x_bytes,
                                                  const int32_t* __restrict__ list, int list_stride, int g, int row0,
                                                  int rows, int n0, const int* sOff, const int8_t* __restrict__ wlo,
@@ -219,7 +224,7 @@ __device__ __forceinline__ void grouped_tile_dma(const __amdgpu_buffer_rsrc_t rA
                                                  const int16_t* sSilu, int h_shift, int8_t* __restrict__ y,
                                                  int ystride, int8_t* ring, int* sRow) {
     constexpr int BN = GTileD::BN;
-    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = tid_now(), lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int KB = kp / 32;
     uint32_t va[2];
 #pragma unroll
@@ -232,15 +237,32 @@ __device__ __forceinline__ void grouped_tile_dma(const __amdgpu_buffer_rsrc_t rA
             va[j] = x_bytes;  // out of range whatever the k offset: reads zero
         }
     }
+    DmaStrip xs;
+    if constexpr (XR != 0) {
+        const int r = dma_x_row(w, lane);
+        if (r < rows) {
+            const int xr = list ? list[(size_t)g * list_stride + row0 + r] : sOff[g] + row0 + r;
+            xs.vx = (uint32_t)xr * (uint32_t)kp + dma_x_byte(w, lane);
+        } else {
+            xs.vx = x_bytes;
+        }
+    }
     const int cb0 = n0 / 32, ncb = (N - n0 + 31) / 32 < BN / 32 ? (N - n0 + 31) / 32 : BN / 32;
     const int8_t* gl = wlo + (size_t)g * glo;
     const uint8_t* gn = wnib + (size_t)g * (glo / 2);
     const __amdgpu_buffer_rsrc_t rL = make_rsrc(gl + (size_t)cb0 * KB * 1024, (uint32_t)ncb * KB * 1024);
     const __amdgpu_buffer_rsrc_t rN = make_rsrc(gn + (size_t)cb0 * KB * 512, (uint32_t)ncb * KB * 512);
     v16i acc0[4][1], acc1[4][1];
-    w12_mainloop_dma<KT_DMA_NS>(rA, rL, rN, va[0], va[1], kp, ring, acc0, acc1, sRow);
-    grouped_epilogue<GTileD, EPI>(acc0, acc1, sRow, g, row0, rows, n0, sOff, N, mant, shift, sSilu, h_shift, y,
-                                  ystride, ring);
+    w12_mainloop_dma<KT_DMA_NS, false, XR>(rA, rL, rN, va[0], va[1], kp, ring, acc0, acc1, sRow, &xs);
+    grouped_epilogue<GTileD, EPI, XR>(acc0, acc1, sRow, g, row0, rows, n0, sOff, N, mant, shift, sSilu, h_shift, y,
+                                      ystride, ring, &xs);
+}
+
+// Row tiles of a group of c rows on the DMA-fed kernel: 256-row tiles, the last absorbing a tail of up to 32 rows
+// (the 288-row tile) rather than taking a tile of its own that would stream the group's weights again.
+__device__ __forceinline__ int dma_row_tiles(int c) {
+    const int t = c & 255;
+    return c > 256 && t != 0 && t <= KT_DMA_XR ? c >> 8 : (c + 255) >> 8;
 }
 
 // The ragged grouped W12 GEMM on 256-row tiles fed by LDS DMA, for products with enough rows to give every CU a
@@ -259,9 +281,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     typedef W12Tile<2, 1, 1, 4, 4> GT64;
     static_assert(GT128::NT == 512 && GT64::NT == 512 && GT128::BN == 128 && GT64::BN == 128, "one tile space");
     static_assert(GT128::RING <= KT_DMA_NS * KT_DMA_STAGE, "the register tiles' A rings fit the DMA ring");
+    static_assert((256 + KT_DMA_XR) * 128 <= KT_DMA_NS * dma_stage_x<KT_DMA_XR>(), "the 288-row output tile fits");
     constexpr int NT = 512, BM = 256, BN = 128;
     extern __shared__ __attribute__((aligned(16))) int8_t ring[];
-    __shared__ int sRow[BM];
+    __shared__ int sRow[BM + KT_DMA_XR];
     __shared__ int sRpre[KT_MAX_GROUPS + 1], sOff[KT_MAX_GROUPS + 1];
     __shared__ int scr[16];
     __shared__ int16_t sSilu[256];
@@ -271,7 +294,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int g0 = 0; g0 < groups; g0 += NT) {
         const int g = g0 + tid, c = g < groups ? (count ? count[g] : rows_one) : 0;
         int er, eo, tr, to;
-        block_scan2<NT>((c + BM - 1) / BM, c, er, eo, tr, to, scr);
+        block_scan2<NT>(dma_row_tiles(c), c, er, eo, tr, to, scr);
         if (g < groups) sRpre[g] = carry_r + er, sOff[g] = carry_o + eo;
         carry_r += tr, carry_o += to;
     }
@@ -294,8 +317,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             else hi = mid - 1;
         }
         const int g = lo, row0 = (rt - sRpre[g]) * BM, cnt = sOff[g + 1] - sOff[g];
-        const int rows = cnt - row0 < BM ? cnt - row0 : BM;
-        if (rows > GT128::BM)  // uniform
+        // the group's last tile holds the rest (at most BM + KT_DMA_XR rows), the others BM
+        const int rows = rt == sRpre[g + 1] - 1 ? cnt - row0 : BM;
+        if (rows > BM)  // uniform: a tail of at most KT_DMA_XR rows on the 288-row tile
+            grouped_tile_dma<EPI, KT_DMA_XR>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N,
+                                             kp, mant, shift, sSilu, h_shift, y, ystride, ring, sRow);
+        else if (rows > GT128::BM)
             grouped_tile_dma<EPI>(rA, x_bytes, list, list_stride, g, row0, rows, n0, sOff, wlo, wnib, glo, N, kp, mant,
                                   shift, sSilu, h_shift, y, ystride, ring, sRow);
         else if (rows > GT64::BM)
@@ -441,7 +468,7 @@ static bool grouped_dma_lds_ok() {
              hipDeviceGetAttribute(&mx, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
              hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&w12_grouped_dma_kernel<KT_EPI_SWIGLU>)) ==
                  hipSuccess &&
-             fa.sharedSizeBytes + (size_t)KT_DMA_NS * KT_DMA_STAGE <= (size_t)mx;
+             fa.sharedSizeBytes + (size_t)KT_DMA_NS * dma_stage_x<KT_DMA_XR>() <= (size_t)mx;
     }
     return ok == 1;
 }
@@ -464,7 +491,7 @@ hipError_t launch_w12_grouped(const int8_t* x, size_t x_bytes, const int32_t* li
     if (epi != KT_EPI_I8 && epi != KT_EPI_SWIGLU) return hipErrorInvalidValue;
     // enough 256-row tiles (at full groups) to give every CU one: the DMA-fed kernel, one CTA per CU
     if (max_rows / 256 * tiles_n >= 256 && grouped_dma_lds_ok()) {
-        const size_t lds = (size_t)KT_DMA_NS * KT_DMA_STAGE;
+        const size_t lds = (size_t)KT_DMA_NS * dma_stage_x<KT_DMA_XR>();  // the 288-row tile's stages
         const int64_t ub2 = ((max_rows + 255) / 256 + groups) * tiles_n;
         const unsigned grid2 = (unsigned)(ub2 < 256 ? (ub2 + 7) / 8 * 8 : 256);
         if (epi == KT_EPI_I8)

@@ -93,6 +93,16 @@ __device__ __forceinline__ v4i unpack_hi(v2i d) {
     return v4i{d.x & m4, (d.x >> 4) & m4, d.y & m4, (d.y >> 4) & m4};
 }
 
+// The thread's index as a value the compiler cannot prove loop-invariant (an empty asm that may change it): the tile
+// code derives its per-lane offsets from it, so that a persistent kernel recomputes them for each tile (a few VALU
+// instructions) instead of hoisting them out of its tile loop and holding them, or spilling them to scratch memory,
+// across every mainloop (the grouped MoE kernel went from 77-153 spilled VGPRs to none).
+__device__ __forceinline__ int tid_now() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 __device__ __forceinline__ int sum4(v4i v) {
     const int ones = 0x01010101;
     int s = __builtin_amdgcn_sdot4(v.x, ones, 0, false);
@@ -275,7 +285,7 @@ __device__ __forceinline__ void norm_preload(const int32_t* __restrict__ r, int 
 template <int NT, int PRE>
 __device__ __forceinline__ void norm_rows_to_lds(const int32_t* __restrict__ r, int M, int d, int kp, int8_t* q,
                                                  uint64_t* s_ss, uint64_t* s_rq, const int32_t (&pre)[PRE]) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = tid_now(), lane = tid & 63, w = tid >> 6;
     for (int m = 0; m < M; m++) {
         uint64_t sh = 0, sl = 0;
         int i = tid;
@@ -414,7 +424,7 @@ __device__ __forceinline__ void w12_mainloop(const __amdgpu_buffer_rsrc_t rA, co
     constexpr int NT = C::NT, NSLOT = C::NSLOT, AL = C::AL, AC = C::AC, WTM = C::WTM, WTN = C::WTN;
     constexpr int CPR = C::CPR, BM = C::BM, BK = C::BK;
     int8_t(*sA)[BM * BK] = reinterpret_cast<int8_t(*)[BM * BK]>(smem);
-    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int tid = tid_now(), lane = tid & 63, half = lane >> 5;
     const int rw0 = ((tid >> 6) / C::WN) * 32 * WTM;  // the wave's first row in the tile
 
 #pragma unroll
@@ -520,6 +530,24 @@ constexpr int KT_DMA_STAGE = 28672, KT_DMA_LO = 16384, KT_DMA_NIB = 24576;
 constexpr int KT_DMA_STAGE_BAL = 32768, KT_DMA_HI = 24576;
 template <bool BAL>
 constexpr int dma_stage_bytes() { return BAL ? KT_DMA_STAGE_BAL : KT_DMA_STAGE; }
+// XR = 32 (W12 planes only): the stage's A part holds 32 more rows (256 .. 287), so the lo and nib parts move up by
+// 2 KB: A [0, 18432), lo [18432, 26624), nib [26624, 30720).
+constexpr int KT_DMA_XR = 32;
+template <int XR>
+constexpr int dma_lo_off() { return 64 * (256 + XR); }
+template <int XR>
+constexpr int dma_nib_off() { return dma_lo_off<XR>() + 8192; }
+template <int XR>
+constexpr int dma_stage_x() { return dma_nib_off<XR>() + 4096; }
+static_assert(dma_lo_off<0>() == KT_DMA_LO && dma_nib_off<0>() == KT_DMA_NIB && dma_stage_x<0>() == KT_DMA_STAGE,
+              "XR = 0 is the plain stage");
+
+// The strip of a 288-row tile (XR): rows 256 + 16 mh .. + 15 of M-half mh against the wave's 32 columns as two
+// 16 x 16 blocks (j = 0, 1), both planes; vx: this lane's A piece of the strip rows at k = 0 (see w12_mainloop_dma).
+struct DmaStrip {
+    uint32_t vx;
+    v4i acc0[2], acc1[2];
+};
 #ifndef KT_DMA_NS
 #define KT_DMA_NS 4  // ring stages of the DMA-fed kernels
 #endif
@@ -538,17 +566,34 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, int8_t* lds, uint
 __device__ __forceinline__ int dma_a_row(int w, int lane, int j) { return 32 * w + 16 * j + (lane >> 2); }
 __device__ __forceinline__ uint32_t dma_a_chunk(int lane) { return 16u * ((lane & 3) ^ ((lane >> 4) & 3)); }
 
+// The strip rows' A pieces (XR): wave w moves rows 256 + 4 w .. + 3 with one 4-byte DMA (lane l: row 256 + 4 w +
+// l / 16, byte 4 (l % 16) of its LDS row, i.e. chunk position (l % 16) / 4, dword l % 4); the swizzle of those rows is
+// (row >> 2) & 3 = w & 3. Returns the byte offset within a k-tile row of x that the lane fetches.
+__device__ __forceinline__ int dma_x_row(int w, int lane) { return 256 + 4 * w + (lane >> 4); }
+__device__ __forceinline__ uint32_t dma_x_byte(int w, int lane) {
+    return 16u * (((lane >> 2) & 3) ^ (w & 3)) + 4u * (lane & 3);
+}
+
 // va0 / va1: the byte offsets in rA of this lane's two A pieces at k = 0 (rows dma_a_row(w, lane, 0 / 1), chunk
 // dma_a_chunk(lane)); an offset past the descriptor reads zeros (rows past the tile's rows).
 // BAL: rN is the hi plane of the balanced split (v = lo + 256 hi, no offset): each wave moves its hi fragment with one
 // 16-byte DMA like lo (4 DMAs per k-tile, not 5), the MFMA takes it as read, and there are no row sums (sRow is 0).
-template <int NS, bool BAL = false>
+// XR (W12 planes): a 288-row tile. Each wave also moves its 4 strip rows (one more DMA per k-tile) and multiplies
+// the strip of its M-half (xs: 16 rows x its 32 columns, two 16x16x64 products per plane per k-tile, the operands
+// read from the stage in the 16x16x64 layout: A row 256 + 16 mh + l % 16, k chunk l / 16; B lane l' = 32 ((l / 16)
+// % 2) + 16 j + l % 16 of the (column block, k32 half l / 32) fragment); the waves of column block 0 write the strip
+// rows' sums to sRow[256 ..].
+template <int NS, bool BAL = false, int XR = 0>
 __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA, const __amdgpu_buffer_rsrc_t rL,
                                                  const __amdgpu_buffer_rsrc_t rN, uint32_t va0, uint32_t va1, int kp,
-                                                 int8_t* ring, v16i (&acc0)[4][1], v16i (&acc1)[4][1], int* sRow) {
-    constexpr int ND = BAL ? 4 : 5, STAGE = dma_stage_bytes<BAL>();  // DMAs per wave and k-tile
+                                                 int8_t* ring, v16i (&acc0)[4][1], v16i (&acc1)[4][1], int* sRow,
+                                                 DmaStrip* xs = nullptr) {
+    static_assert(XR == 0 || (XR == KT_DMA_XR && !BAL), "the strip is for the W12 planes");
+    constexpr int ND = (BAL ? 4 : 5) + (XR ? 1 : 0);  // DMAs per wave and k-tile
+    constexpr int STAGE = XR ? dma_stage_x<XR>() : dma_stage_bytes<BAL>();
+    constexpr int LO = XR ? dma_lo_off<XR>() : KT_DMA_LO, NIB = XR ? dma_nib_off<XR>() : KT_DMA_NIB;
     static_assert(NS >= 2 && ND * (NS - 2) <= 63, "vmcnt holds the DMAs of NS - 2 later tiles");
-    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int tid = tid_now(), lane = tid & 63, half = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = w & 3, rw0 = 128 * (w >> 2);
     const int nk = kp / 64, KB = kp / 32;
@@ -563,13 +608,14 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
         int8_t* s = ring + st * STAGE;
         dma16(rA, s + 2048 * w, va0, kl * 64);
         dma16(rA, s + 2048 * w + 1024, va1, kl * 64);
-        dma16(rL, s + KT_DMA_LO + 1024 * w, vl, (2 * kl + ksw) * 1024u);
+        dma16(rL, s + LO + 1024 * w, vl, (2 * kl + ksw) * 1024u);
         if constexpr (BAL) {
             dma16(rN, s + KT_DMA_HI + 1024 * w, vl, (2 * kl + ksw) * 1024u);
         } else {
-            dma4(rN, s + KT_DMA_NIB + 512 * w, vn, (2 * kl + ksw) * 512u);
-            dma4(rN, s + KT_DMA_NIB + 512 * w + 256, vn + 256, (2 * kl + ksw) * 512u);
+            dma4(rN, s + NIB + 512 * w, vn, (2 * kl + ksw) * 512u);
+            dma4(rN, s + NIB + 512 * w + 256, vn + 256, (2 * kl + ksw) * 512u);
         }
+        if constexpr (XR != 0) dma4(rA, s + 64 * (256 + 4 * w), xs->vx, kl * 64);
     };
     // the wave's DMAs of a tile have landed once at most those of the NS - 2 later tiles are outstanding
     auto wait_tile = [&]() {
@@ -580,19 +626,33 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
         v4i a[4], ar, b0, b1;
         v2i bn;
     };
+    // XR: the strip's operands of a whole k-tile, read with its second half
+    struct XFrag {
+        v4i a, b0[2];
+        v2i bn[2];
+    };
+    const int xrow = 256 + 16 * (w >> 2) + (lane & 15), xl = 32 * ((lane >> 4) & 1) + (lane & 15), xks = lane >> 5;
     auto load = [&](const int8_t* s, int ks, Frag& f) {
 #pragma unroll
         for (int i = 0; i < 4; i++) f.a[i] = lds_read16(s, lds_off<4>(rw0 + 32 * i + (lane & 31), 2 * ks + half));
-        f.b0 = lds_read16(s + KT_DMA_LO + 1024 * (2 * wn + ks), 16 * lane);
+        f.b0 = lds_read16(s + LO + 1024 * (2 * wn + ks), 16 * lane);
         if constexpr (BAL) {
             f.b1 = lds_read16(s + KT_DMA_HI + 1024 * (2 * wn + ks), 16 * lane);
         } else {
             // row tile wn once more: a wave-uniform select among f.a would compile to branches
             f.ar = lds_read16(s, lds_off<4>(rw0 + 32 * wn + (lane & 31), 2 * ks + half));
-            f.bn = *reinterpret_cast<const v2i*>(s + KT_DMA_NIB + 512 * (2 * wn + ks) + 8 * lane);
+            f.bn = *reinterpret_cast<const v2i*>(s + NIB + 512 * (2 * wn + ks) + 8 * lane);
         }
     };
-    int rsum = 0;
+    auto xload = [&](const int8_t* s, XFrag& x) {
+        x.a = lds_read16(s, lds_off<4>(xrow, lane >> 4));
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            x.b0[j] = lds_read16(s + LO + 1024 * (2 * wn + xks), 16 * (xl + 16 * j));
+            x.bn[j] = *reinterpret_cast<const v2i*>(s + NIB + 512 * (2 * wn + xks) + 8 * (xl + 16 * j));
+        }
+    };
+    int rsum = 0, xsum = 0;
     auto mma = [&](const Frag& f) {
         const v4i b1 = BAL ? f.b1 : unpack_hi(f.bn);
 #pragma unroll
@@ -602,16 +662,29 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
         }
         if constexpr (!BAL) rsum += sum4(f.ar);
     };
+    auto xmma = [&](const XFrag& x) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            xs->acc0[j] = mfma16(x.a, x.b0[j], xs->acc0[j]);
+            xs->acc1[j] = mfma16(x.a, unpack_hi(x.bn[j]), xs->acc1[j]);
+        }
+        xsum += sum4(x.a);
+    };
 
 #pragma unroll
     for (int i = 0; i < 4; i++) acc0[i][0] = acc1[i][0] = v16i{};
+    if constexpr (XR != 0)
+#pragma unroll
+        for (int j = 0; j < 2; j++) xs->acc0[j] = xs->acc1[j] = v4i{};
 #pragma unroll
     for (int t = 0; t < NS - 1; t++) issue(t, t);
     wait_tile();
     issue(NS - 1, NS - 1);
     Frag f0, f1;
+    XFrag xf;
     load(ring, 0, f0);
     load(ring, 1, f1);
+    if constexpr (XR != 0) xload(ring, xf);
     // Ping-pong: the first half of tile kt's MFMAs covers the barrier that publishes tile kt + 1, the second half
     // covers the LDS reads of tile kt + 1's first half and the DMAs of tile kt + NS (one DMA after every two MFMAs:
     // issued all at once after the barrier, the eight waves' DMAs queue up at the CU's memory path and hold back
@@ -627,6 +700,7 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
         __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs they hide under
         issue(kt % NS, kt + NS);
         mma(f1);
+        if constexpr (XR != 0) xmma(xf);
 #pragma unroll
         for (int q = 0; q < ND; q++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
@@ -634,18 +708,24 @@ __device__ __forceinline__ void w12_mainloop_dma(const __amdgpu_buffer_rsrc_t rA
         }
         __builtin_amdgcn_sched_barrier(0);
         load(sn, 1, f1);
+        if constexpr (XR != 0) xload(sn, xf);
     }
     // the re-reads past the end still target the ring
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     rsum += __shfl_xor(rsum, 32);
     if (lane < 32) sRow[rw0 + 32 * wn + lane] = BAL ? 0 : rsum;  // BAL: no offset term to correct
+    if constexpr (XR != 0) {  // the strip row's sum over the four k chunks (lanes l, l ^ 16, l ^ 32, l ^ 48)
+        xsum += __shfl_xor(xsum, 16);
+        xsum += __shfl_xor(xsum, 32);
+        if (wn == 0 && lane < 16) sRow[xrow] = xsum;
+    }
     __syncthreads();
 }
 
 // The CTA's row sums of x into sRow[BM] (the 4 threads of a row are consecutive lanes). Ends with a barrier.
 template <class C>
 __device__ __forceinline__ void w12_row_sums(const int (&rsum)[C::AL], int* sRow) {
-    const int tid = threadIdx.x;
+    const int tid = tid_now();
 #pragma unroll
     for (int i = 0; i < C::AL; i++) {
         const int idx = tid + C::NT * i;
@@ -666,7 +746,7 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
                                                   const v16i (&acc1)[C::WTM][C::WTN], const int* sRow,
                                                   const int32_t* mant, const int32_t* shift, int n0, int N,
                                                   ChanFn chan, int8_t* sO, const int8_t* sLut = nullptr) {
-    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int tid = tid_now(), lane = tid & 63, half = lane >> 5;
     const int wave = (tid >> 6) % C::WN, rw0 = ((tid >> 6) / C::WN) * 32 * C::WTM;
 #pragma unroll
     for (int j = 0; j < C::WTN; j++) {
@@ -697,11 +777,32 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
     }
 }
 
+// The strip of a 288-row DMA tile (DmaStrip) requantized into rows 256 .. 287 of the int8 tile sO[.][BN] as
+// w12_requant_tile8 does the rest: wave w (M-half w / 4, column block w % 4) holds rows 256 + 16 (w / 4) + 4 (l / 16)
+// + r of columns 32 (w % 4) + 16 j + l % 16.
+template <int BN, class ChanFn>
+__device__ __forceinline__ void w12_requant_strip8(const DmaStrip& xs, const int* sRow, const int32_t* mant,
+                                                   const int32_t* shift, int n0, int N, ChanFn chan, int8_t* sO) {
+    const int tid = tid_now(), lane = tid & 63, w = tid >> 6;
+    const int r0 = 256 + 16 * (w >> 2) + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int c = 32 * (w & 3) + 16 * j + (lane & 15), n = n0 + c;
+        const int ch = n < N ? chan(n) : 0;
+        const ColQ8 q = col_q8(n < N ? mant[ch] : 0, n < N ? shift[ch] : 1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int v = w12_value(xs.acc0[j][r], xs.acc1[j][r], -1920 * sRow[r0 + r]);
+            sO[(r0 + r) * BN + c] = (int8_t)(q.fp ? rq8_fp(v, q) : col_requant<false>(v, q.q));
+        }
+    }
+}
+
 // Block-wide exclusive prefix sums of two ints per thread (blockDim.x = NT, a multiple of 64); `tot` receives the
 // totals. Uses 2 * (NT / 64) ints of LDS at `scr` and ends with a barrier.
 template <int NT>
 __device__ __forceinline__ void block_scan2(int a, int b, int& ea, int& eb, int& ta, int& tb, int* scr) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = tid_now(), lane = tid & 63, w = tid >> 6;
     int ia = a, ib = b;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
