@@ -524,7 +524,7 @@ __device__ __forceinline__ void w12_gemm_epilogue(const v16i (&acc0)[C::WTM][C::
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3), m = m0 + rt;
-                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]);
+                    const int v = w12_value(acc0[i][j][r], acc1[i][j][r], w12_corr(sRow[rt]));
                     const int32_t o = col_requant<true>(v, q);
                     if (full || (m < M && n < N)) {
                         int32_t* p = reinterpret_cast<int32_t*>(y) + (size_t)m * N + n;

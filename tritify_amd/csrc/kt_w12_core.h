@@ -209,7 +209,8 @@ __device__ __forceinline__ int32_t col_requant(int v, const ColQ& q) {
 struct ColQ8 {
     ColQ q;
     double ms;
-    bool fp;  // the double path is exact for this channel
+    bool fp;          // the double path is exact for this channel
+    uint32_t negbit;  // 0x80000000 when the channel's scale is negative
 };
 
 __device__ __forceinline__ ColQ8 col_q8(int32_t mant, int32_t sh) {
@@ -217,14 +218,24 @@ __device__ __forceinline__ ColQ8 col_q8(int32_t mant, int32_t sh) {
     c.q = col_q(mant, sh);
     c.fp = sh >= -512 && sh <= 46;
     c.ms = c.fp ? ldexp(fabs((double)mant), -sh) : 0.0;
+    c.negbit = c.q.neg ? 0x80000000u : 0u;
     return c;
 }
 
-// col_requant<false>(v, c.q) for a channel with c.fp.
+// col_requant<false>(v, c.q) for a channel with c.fp: min(floor(|v| ms + 0.5), 127) with the sign of v times the
+// scale's. The sign goes onto the double's sign bit before the conversion: |d| >= 0.5 and the conversion truncates
+// toward zero, so (int)(-d) = -floor(d), the same integer as negating after it, in two bit operations instead of a
+// compare, a negation and a select.
 __device__ __forceinline__ int32_t rq8_fp(int v, const ColQ8& c) {
-    const int m = (int)fmin(fma(fabs((double)v), c.ms, 0.5), 127.0);
-    return (v < 0) != c.q.neg ? -m : m;
+    const double d = fmin(fma(fabs((double)v), c.ms, 0.5), 127.0);
+    const uint32_t sgn = ((uint32_t)v ^ c.negbit) & 0x80000000u;
+    const uint64_t b = (uint64_t)__double_as_longlong(d) | ((uint64_t)sgn << 32);
+    return (int)__longlong_as_double((long long)b);
 }
+
+// -1920 x (a row's sum of x), the W12 offset term of the int8-output epilogues, as one full-rate 24-bit multiply: those
+// products have kp <= KT_SMALL_KP, so |row sum| <= 128 kp < 2^23 and the product fits int32.
+__device__ __forceinline__ int w12_corr(int rowsum) { return __mul24(rowsum, -1920); }
 
 // clamp(requant(v, 1, sh), -127, 127) for 1 <= sh <= 30 and |v| < 2^31: round half away from zero.
 __device__ __forceinline__ int32_t shift_rq8(int v, int sh) {
@@ -763,7 +774,7 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    put(rt, rq8_fp(w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]), q));
+                    put(rt, rq8_fp(w12_value(acc0[i][j][r], acc1[i][j][r], w12_corr(sRow[rt])), q));
                 }
         } else {
 #pragma unroll
@@ -771,7 +782,7 @@ __device__ __forceinline__ void w12_requant_tile8(const v16i (&acc0)[C::WTM][C::
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int rt = rw0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    put(rt, col_requant<false>(w12_value(acc0[i][j][r], acc1[i][j][r], -1920 * sRow[rt]), q.q));
+                    put(rt, col_requant<false>(w12_value(acc0[i][j][r], acc1[i][j][r], w12_corr(sRow[rt])), q.q));
                 }
         }
     }
@@ -792,7 +803,7 @@ __device__ __forceinline__ void w12_requant_strip8(const DmaStrip& xs, const int
         const ColQ8 q = col_q8(n < N ? mant[ch] : 0, n < N ? shift[ch] : 1);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int v = w12_value(xs.acc0[j][r], xs.acc1[j][r], -1920 * sRow[r0 + r]);
+            const int v = w12_value(xs.acc0[j][r], xs.acc1[j][r], w12_corr(sRow[r0 + r]));
             sO[(r0 + r) * BN + c] = (int8_t)(q.fp ? rq8_fp(v, q) : col_requant<false>(v, q.q));
         }
     }
