@@ -158,12 +158,20 @@ __device__ __forceinline__ void grouped_epilogue(const v16i (&acc0)[C::WTM][1], 
         for (int task = tid; task < BM * (BN / 32); task += NT) {
             const int r = task / (BN / 32), q = task % (BN / 32);  // row, 16-unit chunk
             if (r >= rows || 16 * q >= units) continue;
+            // units 16 q .. 16 q + 15: 16 consecutive gate codes at gc0 (one 32-unit block holds them), their up codes
+            // 32 bytes on; every table read is issued before the first is used
+            const int gc0 = (q >> 1) * 64 + (q & 1) * 16;
+            const v4i gv = *reinterpret_cast<const v4i*>(smem + r * BN + gc0);
+            const v4i uv = *reinterpret_cast<const v4i*>(smem + r * BN + gc0 + 32);
+            int sl[16];
+#pragma unroll
+            for (int t2 = 0; t2 < 16; t2++)
+                sl[t2] = sSilu[(int)(int8_t)((uint32_t)gv[t2 >> 2] >> (8 * (t2 & 3))) + 127];
             v4i out = {0, 0, 0, 0};
 #pragma unroll
             for (int t2 = 0; t2 < 16; t2++) {
-                const int u = 16 * q + t2, gc = (u >> 5) * 64 + (u & 31);
-                const int gq = smem[r * BN + gc], uq = smem[r * BN + gc + 32];
-                const uint32_t hb = (uint32_t)(uint8_t)shift_rq8((int)sSilu[gq + 127] * uq, h_shift);
+                const int uq = (int)(int8_t)((uint32_t)uv[t2 >> 2] >> (8 * (t2 & 3)));
+                const uint32_t hb = (uint32_t)(uint8_t)shift_rq8(sl[t2] * uq, h_shift);
                 out[t2 >> 2] |= (int)(hb << (8 * (t2 & 3)));
             }
             *reinterpret_cast<v4i*>(yg + (size_t)r * ystride + n0 / 2 + 16 * q) = out;

@@ -238,11 +238,14 @@ __device__ __forceinline__ int32_t rq8_fp(int v, const ColQ8& c) {
 __device__ __forceinline__ int w12_corr(int rowsum) { return __mul24(rowsum, -1920); }
 
 // clamp(requant(v, 1, sh), -127, 127) for 1 <= sh <= 30 and |v| < 2^31: round half away from zero.
+// |v| + 2^(sh - 1) <= 2^31 + 2^29 stays below 2^32, so the sum and shift are 32-bit; the sign is applied as
+// (m ^ s) - s with s = v >> 31.
 __device__ __forceinline__ int32_t shift_rq8(int v, int sh) {
-    const uint32_t a = v < 0 ? 0u - (uint32_t)v : (uint32_t)v;
-    uint32_t m = (uint32_t)(((uint64_t)a + (1u << (sh - 1))) >> sh);
-    m = m > 127 ? 127 : m;
-    return v < 0 ? -(int32_t)m : (int32_t)m;
+    const int32_t s = v >> 31;
+    const uint32_t a = ((uint32_t)v ^ (uint32_t)s) - (uint32_t)s;
+    uint32_t m = (a + (1u << (sh - 1))) >> sh;
+    m = m > 127u ? 127u : m;
+    return ((int32_t)m ^ s) - s;
 }
 
 // The longest k for which every W12 dot fits int32: 8128 * 128 * 2048 < 2^31 <= 8192 * 128 * 2048.
