@@ -302,9 +302,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         // double, the column's sign applied to the packed bytes. Unless the result saturates,
         // |v| |mant| < 127.5 * 2^shift < 2^53, so |v| ms + 0.5 is exact and truncation floors it; a saturating value
         // stays at or beyond 127.5 after rounding (rounding is monotone), so the clamp holds it at 127.
-        auto rq_fp = [&](int v) {
-            const int m = (int)fmin(fma(fabs((double)v), ms, 0.5), 127.0);  // round(|v| ms) half up, <= 127
-            return v < 0 ? -m : m;
+        auto rq_fp = [&](int v) {  // round(|v| ms) half up, <= 127, with v's sign set on the double before the
+            // conversion (it truncates toward zero: (int)(-d) = -floor(d) for d >= 0.5)
+            const double d = fmin(fma(fabs((double)v), ms, 0.5), 127.0);
+            const uint64_t b = (uint64_t)__double_as_longlong(d) | ((uint64_t)((uint32_t)v & 0x80000000u) << 32);
+            return (int)__longlong_as_double((long long)b);
         };
         // four int8 lanes negated at once (|b| <= 127: no byte borrows from its neighbour)
         auto neg4 = [](uint32_t x) { return (0x80808080u - (x & 0x7F7F7F7Fu)) ^ (~x & 0x80808080u); };
