@@ -179,12 +179,12 @@ def test_grouped_linear_ragged_gather(torch_dev):
         at += c
 
 
-@pytest.mark.parametrize("k,gathered", [(100, True), (320, False)])
+@pytest.mark.parametrize("k,gathered", [(40, True), (100, True), (320, False)])
 def test_grouped_dma_tiles(torch_dev, k, gathered):
     """Enough rows for the DMA-fed grouped kernel (256-row tiles, one CTA per CU), int8 epilogue: groups of 0, 1, 64,
     65, 128, 129, 256, 257, 288, 289, 300, 520, 544 and 700 rows (every tail class: the 64- and 128-row register
     tiles, the DMA tile, and the 288-row DMA tile that absorbs a tail of 1-32 rows: 257, 288, 520, 544; 289 keeps a
-    33-row tail tile), n = 4000 (a partial last column tile), k of two and five 64-deep k-tiles; rows gathered
+    33-row tail tile), n = 4000 (a partial last column tile), k of one, two and five 64-deep k-tiles; rows gathered
     through a list with repeats, or read in place from offset ranges."""
     import tritify_amd as TA
     from tritify_amd import workloads as W
