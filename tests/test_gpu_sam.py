@@ -30,12 +30,14 @@ def sha(a) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
 
-def run_conv(torch, C, H, W, CO, KH, KW, S, P, seeds=(61, 62, 63), bias=True):
+def run_conv(torch, C, H, W, CO, KH, KW, S, P, seeds=(61, 62, 63), bias=True, scales=None):
     import tritify_amd as TA
     from tritify_amd import workloads as W_
 
     say(f"case: patch embed C={C} H={H} W={W} CO={CO} k={KH}x{KW} s={S} p={P}")
     img, w, b, mant, shift = W_.sam_patch_inputs(C, H, W, CO, KH, KW, *seeds)
+    if scales is not None:
+        mant, shift = scales(mant, shift)
     lut = np.concatenate([W_.sam_entry_table()] * 2)[:C]  # C <= 4 channels of entry codes
     lo_b, hi_b = TA.sam_patch_bytes(CO, C, KH, KW)
     lo = torch.empty(lo_b, dtype=torch.int8, device="cuda")
@@ -75,6 +77,28 @@ def test_patch_embed_wide_and_strided_kernels(torch_dev):
     byte loads since w % 4 != 0) and a ViT-style 16x16 stride-16 patchify (one dword-aligned copy, k = 256)."""
     run_conv(torch_dev, 2, 40, 66, 20, 9, 9, 3, 4, seeds=(73, 74, 75))
     run_conv(torch_dev, 1, 64, 320, 36, 16, 16, 16, 0, seeds=(76, 77, 78))
+
+
+def test_patch_embed_negative_and_edge_scales(torch_dev):
+    """The requant epilogue's sign and clamp: every other channel's multiplier negated (the double path with both
+    signs), then every pairing of edge multipliers and shifts, first those the double path takes (shift -200 .. 33,
+    saturating ones included), then all of them (waves whose channels mix the double and the integer path)."""
+    from test_oracle import EDGE_MANT, EDGE_SHIFT
+
+    def negate_odd(mant, shift):
+        mant = mant.copy()
+        mant[1::2] = -mant[1::2]
+        return mant, shift
+
+    def edges(shifts):
+        pairs = [(m, s) for m in EDGE_MANT for s in shifts]
+        return len(pairs), lambda mant, shift: (np.array([p[0] for p in pairs], np.int32),
+                                                np.array([p[1] for p in pairs], np.int32))
+
+    run_conv(torch_dev, 3, 70, 70, 40, 7, 7, 4, 3, seeds=(79, 80, 81), scales=negate_odd)
+    for shifts in ([s for s in EDGE_SHIFT if -512 <= s <= 46], EDGE_SHIFT):
+        co, f = edges(shifts)
+        run_conv(torch_dev, 3, 40, 64, co, 7, 7, 4, 3, seeds=(82, 83, 84), scales=f)
 
 
 def test_patch_weights_device_pack_equals_upload(torch_dev):

@@ -188,13 +188,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         for (int u = 0; u < 2; u++)
             if (tid + 512 * u < p.CI * 256) sLut[tid + 512 * u] = lv[u];
         if (tid < BN) {
-            const ColQ q = col_q(cm, cs);
-            // |mant| * 2^-shift as a double (exact: a 31-bit integer scaled by a power of two in range)
-            const bool fp = cs >= -512 && cs <= 46;
-            const double ms = fp ? ldexp(fabs((double)cm), -cs) : 0.0;
-            const uint64_t mb = (uint64_t)__double_as_longlong(ms);
+            const ColQ8 q8 = col_q8(cm, cs);
+            const ColQ& q = q8.q;
+            const uint64_t mb = (uint64_t)__double_as_longlong(q8.ms);
             *reinterpret_cast<v4i*>(sCol + 8 * tid) =
-                v4i{(int)q.mt, (int)rq8_threshold(q), cbias, (int)(q.shr | (q.neg ? 256u : 0u) | (fp ? 512u : 0u))};
+                v4i{(int)q.mt, (int)q8.hsb, cbias, (int)(q.shr | (q.neg ? 256u : 0u) | (q8.fp ? 512u : 0u))};
             *reinterpret_cast<v4i*>(sCol + 8 * tid + 4) =
                 v4i{(int)(uint32_t)q.bias, (int)(uint32_t)(q.bias >> 32), (int)(uint32_t)mb, (int)(uint32_t)(mb >> 32)};
         }
@@ -295,40 +293,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         ColQ q;
         q.mt = (uint32_t)k4.x, q.shr = (uint32_t)k4.w & 255u, q.neg = (k4.w >> 8) & 1;
         q.bias = (uint64_t)(uint32_t)k8.x | (uint64_t)(uint32_t)k8.y << 32;
-        const uint32_t sat = (uint32_t)k4.y;
+        const uint32_t hsb = (uint32_t)k4.y;
         const double ms = __longlong_as_double((long long)((uint64_t)(uint32_t)k8.z | (uint64_t)(uint32_t)k8.w << 32));
-        // requant(v) = round(v * mant / 2^shift) half away from zero, clamped to +-127, is odd in v and in mant:
-        // with ms = |mant| 2^-shift and shift <= 46 it is sign(v) sign(mant) min(floor(|v| ms + 0.5), 127) in
-        // double, the column's sign applied to the packed bytes. Unless the result saturates,
-        // |v| |mant| < 127.5 * 2^shift < 2^53, so |v| ms + 0.5 is exact and truncation floors it; a saturating value
-        // stays at or beyond 127.5 after rounding (rounding is monotone), so the clamp holds it at 127.
-        auto rq_fp = [&](int v) {  // round(|v| ms) half up, <= 127, with v's sign set on the double before the
-            // conversion (it truncates toward zero: (int)(-d) = -floor(d) for d >= 0.5)
-            const double d = fmin(fma(fabs((double)v), ms, 0.5), 127.0);
-            const uint64_t b = (uint64_t)__double_as_longlong(d) | ((uint64_t)((uint32_t)v & 0x80000000u) << 32);
-            return (int)__longlong_as_double((long long)b);
+        // four codes (each in [-127, 127]) into the bytes of one dword, three byte permutes
+        auto pack4 = [](const int (&y)[4]) {
+            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)y[1], (uint32_t)y[0], 0x0C0C0400u);
+            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)y[3], (uint32_t)y[2], 0x0C0C0400u);
+            return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         };
-        // four int8 lanes negated at once (|b| <= 127: no byte borrows from its neighbour)
-        auto neg4 = [](uint32_t x) { return (0x80808080u - (x & 0x7F7F7F7Fu)) ^ (~x & 0x80808080u); };
-        const bool all_fp = __all((k4.w >> 9) & 1), any_neg = __any(q.neg);
+        const bool all_fp = __all((k4.w >> 9) & 1);
+        // the clamp threshold of the integer path, needed only when a column of the wave is off the double path
+        const uint32_t sat = all_fp ? 0u : rq8_threshold(q);
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
                 const int m0 = (2 * rh + i) * 32 + 8 * g4 + 4 * h;
-                int v[4];
+                int v[4], y[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++)  // bias + s_lo + 256 s_hi, formed modulo 2^32 (the value fits int32)
                     v[e] = (int)((uint32_t)acc0[i][4 * g4 + e] + ((uint32_t)acc1[i][4 * g4 + e] << 8));
-                uint32_t packed = 0;
                 if (all_fp) {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) packed |= ((uint32_t)rq_fp(v[e]) & 255u) << (8 * e);
-                    if (any_neg && q.neg) packed = neg4(packed);
+                    for (int e = 0; e < 4; e++) y[e] = rq8_fp(v[e], ms, hsb);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) packed |= ((uint32_t)rq8((uint32_t)v[e], q, sat) & 255u) << (8 * e);
+                    for (int e = 0; e < 4; e++) y[e] = rq8((uint32_t)v[e], q, sat);
                 }
+                const uint32_t packed = pack4(y);
                 *reinterpret_cast<uint32_t*>(sO + c * SOP + m0) = packed;
             }
     }

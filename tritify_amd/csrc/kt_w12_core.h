@@ -208,30 +208,50 @@ __device__ __forceinline__ int32_t col_requant(int v, const ColQ& q) {
 // shifts take col_requant.
 struct ColQ8 {
     ColQ q;
-    double ms;
-    bool fp;          // the double path is exact for this channel
-    uint32_t negbit;  // 0x80000000 when the channel's scale is negative
+    double ms;     // mant x 2^-shift (exact when fp)
+    bool fp;       // the double path is exact for this channel
+    uint32_t hsb;  // high dword of 0.5 with the scale's sign: 0x3FE00000, or 0xBFE00000 for a negative scale
 };
 
 __device__ __forceinline__ ColQ8 col_q8(int32_t mant, int32_t sh) {
     ColQ8 c;
     c.q = col_q(mant, sh);
     c.fp = sh >= -512 && sh <= 46;
-    c.ms = c.fp ? ldexp(fabs((double)mant), -sh) : 0.0;
-    c.negbit = c.q.neg ? 0x80000000u : 0u;
+    c.ms = c.fp ? ldexp((double)mant, -sh) : 0.0;
+    c.hsb = 0x3FE00000u | (mant < 0 ? 0x80000000u : 0u);
     return c;
 }
 
-// col_requant<false>(v, c.q) for a channel with c.fp: min(floor(|v| ms + 0.5), 127) with the sign of v times the
-// scale's. The sign goes onto the double's sign bit before the conversion: |d| >= 0.5 and the conversion truncates
-// toward zero, so (int)(-d) = -floor(d), the same integer as negating after it, in two bit operations instead of a
-// compare, a negation and a select.
-__device__ __forceinline__ int32_t rq8_fp(int v, const ColQ8& c) {
-    const double d = fmin(fma(fabs((double)v), c.ms, 0.5), 127.0);
-    const uint32_t sgn = ((uint32_t)v ^ c.negbit) & 0x80000000u;
-    const uint64_t b = (uint64_t)__double_as_longlong(d) | ((uint64_t)sgn << 32);
-    return (int)__longlong_as_double((long long)b);
+// v_cvt_i32_f64: values beyond the int32 range convert to its nearest end (a C++ conversion of them is undefined).
+__device__ __forceinline__ int cvt_i32_sat(double d) {
+    int r;
+    asm("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(d));
+    return r;
 }
+
+// The double operand 0.5 sign(v) sign(scale), from the column's hsb: one bit operation on its high dword.
+__device__ __forceinline__ double rq8_half(int v, uint32_t hsb) {
+    return __longlong_as_double((long long)((uint64_t)(((uint32_t)v & 0x80000000u) ^ hsb) << 32));
+}
+
+// a * b + c in one rounding as the three-operand v_fma_f64: the compiler's two-operand v_fmac_f64 would copy the
+// addend first, since the addend's zero low dword is one register shared by every value of an epilogue
+__device__ __forceinline__ double fma3_f64(double a, double b, double c) {
+    double r;
+    asm("v_fma_f64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// col_requant<false>(v, q) for a channel with fp (ms = mant x 2^-shift, hsb its half's high dword): v ms +
+// 0.5 sign(v ms) truncated toward zero is sign(v ms) floor(|v ms| + 0.5), clamped to [-127, 127]. Unless the result
+// saturates, |v| |mant| < 127.5 * 2^shift < 2^53 (shift <= 46), so the fma is exact; a saturating value stays at or
+// beyond 127.5 in magnitude after rounding (rounding is monotone) and the clamp holds it at 127. |v ms| < 2^574, so
+// no value is infinite and the saturating conversion keeps the clamp's input ordered.
+__device__ __forceinline__ int32_t rq8_fp(int v, double ms, uint32_t hsb) {
+    const int y = cvt_i32_sat(fma3_f64((double)v, ms, rq8_half(v, hsb)));
+    return min(max(y, -127), 127);
+}
+__device__ __forceinline__ int32_t rq8_fp(int v, const ColQ8& c) { return rq8_fp(v, c.ms, c.hsb); }
 
 // -1920 x (a row's sum of x), the W12 offset term of the int8-output epilogues, as one full-rate 24-bit multiply: those
 // products have kp <= KT_SMALL_KP, so |row sum| <= 128 kp < 2^23 and the product fits int32.
