@@ -130,8 +130,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(plane_gemm_
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int tiles_n = (N + BN - 1) / BN;
-    const int m0 = (blockIdx.x / tiles_n) * BM, n0 = (blockIdx.x % tiles_n) * BN;
+    const int tiles_n = (N + BN - 1) / BN, tiles_m = (int)gridDim.x / tiles_n;  // gridDim.x = tiles_m * tiles_n
+    // Block b runs on XCD b % 8. XCD x takes a contiguous run of the tile numbers (a bijection for any tile count),
+    // numbered row tile fastest, so the row tiles of one column tile read its weight planes through one L2.
+    const int nt = (int)gridDim.x, q8 = nt >> 3, r8 = nt & 7, xcd = (int)blockIdx.x & 7;
+    const int t = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + ((int)blockIdx.x >> 3);
+    const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
     QlState* ql = ql_all ? ql_all + ql_seg_of(seg, n0) : nullptr;  // this tile's call
     const size_t xplane = (size_t)M * kp, wplane = (size_t)N * kp;
 
