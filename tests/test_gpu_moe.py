@@ -131,6 +131,29 @@ def test_moe_one_token(torch_dev):
     run_and_compare(torch_dev, 1, 256, 128, 8, 2, seeds=(1100, 111, 112))
 
 
+@pytest.mark.parametrize("T,E,K", [(1, 4, 2), (4096, 64, 8), (5000, 64, 8), (300, 40, 12), (9000, 16, 16)])
+def test_moe_bucket_against_the_oracle(torch_dev, T, E, K):
+    """kt_hip_moe_bucket's lists (each group's tokens in increasing order), positions and counts equal the oracle's;
+    T past one 4096-token pass and ragged, top_k past the unrolled 8."""
+    from tritify_amd import backend as B
+
+    torch = torch_dev
+    rng = np.random.default_rng(T * 131 + E * 7 + K)
+    sel = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32).ravel()
+    lst, pos, count = O.moe_bucket(sel, T, E, K)
+    say(f"case: moe bucket T={T} E={E} top_k={K}")
+    d_lst = torch.full(((E + 1) * T,), -7, dtype=torch.int32, device="cuda")
+    d_pos = torch.full((T * K,), -7, dtype=torch.int32, device="cuda")
+    d_cnt = torch.full((E + 1,), -7, dtype=torch.int32, device="cuda")
+    B.moe_bucket(torch.from_numpy(sel).cuda(), T, E, K, d_lst, d_pos, d_cnt)
+    torch.cuda.synchronize()
+    got_cnt, got_lst = d_cnt.cpu().numpy(), d_lst.cpu().numpy()
+    assert np.array_equal(got_cnt, count)
+    for g in range(E + 1):
+        assert np.array_equal(got_lst[g * T:g * T + count[g]], lst[g * T:g * T + count[g]]), g
+    assert np.array_equal(d_pos.cpu().numpy(), pos)
+
+
 def test_grouped_linear_ragged_gather(torch_dev):
     """The grouped W12 GEMM alone, int8 epilogue: ragged counts (0, 1, one row tile + 2, two + 1, 64), rows gathered
     through a list with repeats, n not a multiple of the tile, k not a multiple of 64."""
@@ -249,7 +272,7 @@ def test_moe_layer_on_dma_tiles(torch_dev):
 
 
 def test_moe_full_config4(torch_dev):
-    """BASELINE config 4 at full size (4096 tokens, H 4096, 128 experts + shared, F 1408, top-8) against the
+    """benchmark config 4 at full size (4096 tokens, H 4096, 128 experts + shared, F 1408, top-8) against the
     fixture hashes of the oracle's expert-major evaluation."""
     from tritify_amd import workloads as W
 

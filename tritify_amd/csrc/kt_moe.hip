@@ -1,4 +1,4 @@
-// The MoE layer of BASELINE config 4 on gfx950: routing, bucketing, the ragged grouped W12 GEMM and the weighted
+// The MoE layer of benchmark config 4 on gfx950: routing, bucketing, the ragged grouped W12 GEMM and the weighted
 // combine. The reference runs a MoE layer token by token (MoeMlp::forward_routed / forward_one_int,
 // crates/01-engine/kt-core/src/layers.rs:928-936, 988-1020), each selected expert called with one row; here the
 // tokens are bucketed by expert and every expert's rows run as one ragged group of a single grouped GEMM launch.
@@ -72,31 +72,54 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t* __restric
 }
 
 // One CTA per group g <= E: list[g * T + j] = the j-th token (increasing) that chose g, pos[t * top_k + i] = j for
-// (t, its choice i == g), count[g] = the group size. Group E (the shared expert) is every token.
-__global__ __launch_bounds__(256) void moe_bucket_kernel(const int32_t* __restrict__ sel, int T, int E, int top_k,
-                                                         int32_t* __restrict__ list, int32_t* __restrict__ pos,
-                                                         int32_t* __restrict__ count) {
-    __shared__ int scr[8];
+// (t, its choice i == g), count[g] = the group size. Group E (the shared expert) is every token. A pass covers
+// 1024 x BK_TPT tokens, thread tid the BK_TPT consecutive tokens from BK_TPT * tid, so one block scan of the
+// threads' hit counts orders a pass's hits by token. MAXK >= top_k bounds the unrolled selection loads (0: a loop
+// over top_k).
+constexpr int BK_NT = 1024, BK_TPT = 4;
+template <int MAXK>
+__global__ __launch_bounds__(BK_NT) void moe_bucket_kernel(const int32_t* __restrict__ sel, int T, int E, int top_k,
+                                                           int32_t* __restrict__ list, int32_t* __restrict__ pos,
+                                                           int32_t* __restrict__ count) {
+    __shared__ int scr[2 * (BK_NT / 64)];
     const int g = blockIdx.x, tid = threadIdx.x;
     int32_t* lg = list + (size_t)g * T;
     if (g == E) {
-        for (int t = tid; t < T; t += 256) lg[t] = t;
+        for (int t = tid; t < T; t += BK_NT) lg[t] = t;
         if (tid == 0) count[E] = T;
         return;
     }
     int base = 0;
-    for (int t0 = 0; t0 < T; t0 += 256) {
-        const int t = t0 + tid;
-        int hit = -1;
-        if (t < T)
-            for (int i = 0; i < top_k; i++)
-                if (sel[(size_t)t * top_k + i] == g) hit = i;
-        int ex, ez, tot, tz;
-        block_scan2<256>(hit >= 0 ? 1 : 0, 0, ex, ez, tot, tz, scr);
-        if (hit >= 0) {
-            lg[base + ex] = t;
-            pos[(size_t)t * top_k + hit] = base + ex;
+    for (int t0 = 0; t0 < T; t0 += BK_NT * BK_TPT) {
+        const int tb = t0 + BK_TPT * tid;
+        int hit[BK_TPT], n = 0;
+#pragma unroll
+        for (int j = 0; j < BK_TPT; j++) {
+            const int t = tb + j;
+            hit[j] = -1;
+            if constexpr (MAXK > 0) {  // every load of the token's selections in flight before the first compare
+                int32_t v[MAXK];
+#pragma unroll
+                for (int i = 0; i < MAXK; i++) v[i] = t < T && i < top_k ? sel[(size_t)t * top_k + i] : -1;
+#pragma unroll
+                for (int i = 0; i < MAXK; i++)
+                    if (v[i] == g) hit[j] = i;
+            } else if (t < T) {
+                for (int i = 0; i < top_k; i++)
+                    if (sel[(size_t)t * top_k + i] == g) hit[j] = i;
+            }
+            n += hit[j] >= 0 ? 1 : 0;
         }
+        int ex, ez, tot, tz;
+        block_scan2<BK_NT>(n, 0, ex, ez, tot, tz, scr);
+        int p = base + ex;
+#pragma unroll
+        for (int j = 0; j < BK_TPT; j++)
+            if (hit[j] >= 0) {
+                lg[p] = tb + j;
+                pos[(size_t)(tb + j) * top_k + hit[j]] = p;
+                p++;
+            }
         base += tot;
     }
     if (tid == 0) count[g] = base;
@@ -462,7 +485,10 @@ hipError_t launch_moe_bucket(const int32_t* sel, int T, int E, int top_k, int32_
                              int32_t* count, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     if (E < 1 || E + 1 > KT_MAX_GROUPS || top_k < 1 || top_k > E) return hipErrorInvalidValue;
-    moe_bucket_kernel<<<dim3((unsigned)(E + 1)), dim3(256), 0, s>>>(sel, T, E, top_k, list, pos, count);
+    if (top_k <= 8)
+        moe_bucket_kernel<8><<<dim3((unsigned)(E + 1)), dim3(BK_NT), 0, s>>>(sel, T, E, top_k, list, pos, count);
+    else
+        moe_bucket_kernel<0><<<dim3((unsigned)(E + 1)), dim3(BK_NT), 0, s>>>(sel, T, E, top_k, list, pos, count);
     return hipGetLastError();
 }
 
