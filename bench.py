@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X exact-integer GEMM backend on the BASELINE workloads, one GPU.
+"""Benchmark of the MI355X exact-integer GEMM backend on the benchmark workloads, one GPU.
 
 Headline (`value`): config 2, the exact 12-bit GEMM at M = 2048, N = K = 4096 -- int8 activations (round(N(0,40))
-clipped to +-127) against 12-bit weight codes (as BASELINE describes them, two int8 digit planes: the balanced
+clipped to +-127) against 12-bit weight codes (as the benchmark describes them, two int8 digit planes: the balanced
 W12B split, lo in [-128, 127] and hi in [-8, 8], 2 bytes per weight; the packed 1.5-byte W12 planes are timed
 beside it), int32 accumulation per digit plane, exact recombination, then the per-channel integer requant (int32
 multiplier + shift) to int8 outputs. A step is one launch. Inputs are resident in HBM before the timed region; the
@@ -11,7 +11,7 @@ hashes the CPU oracle produced (tests/golden/goldens.json) before anything is ti
 
 Also measured, each under "configs" (skip with --configs):
   3  a Qwen2.5-0.5B-shape decoder: 512-token prefill, then 128 greedy decode steps replayed from one captured HIP
-     graph -- decode tokens/s (BASELINE's second metric), prefill tokens/s, the weight bandwidth of a decode step.
+     graph -- decode tokens/s (the benchmark's second metric), prefill tokens/s, the weight bandwidth of a decode step.
   4  one MoE layer, GLM-4.5-Air shape (4096 tokens, H 4096, 128 experts top-8 + 1 shared, F 1408): route, bucket,
      the ragged grouped W12 GEMMs (gate/up with the SwiGLU epilogue, down), combine; per-stage times.
   5  SAM 2.1 Hiera-B+ encoder GEMMs: the 1024 x 1024 x 3 patch embed as an im2col-fused W12 GEMM (M 65,536, K 147,

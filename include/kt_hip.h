@@ -513,7 +513,7 @@ int kt_hip_equality_gate(const kt_gate_backend* backends, size_t n, const kt_gat
 int kt_hip_residency_gate(const kt_gate_backend* b, const kt_gate_case* cases, size_t ncases, char* msg, size_t len);
 
 /* ---------------------------------------------------------------------------------------------------------------
- * 12-bit-weight path (BASELINE workloads), device-resident operands. No counterpart in the reference: there the
+ * 12-bit-weight path (benchmark workloads), device-resident operands. No counterpart in the reference: there the
  * weights are 12-trit codes on the digit path above. W12 digits: lo = (v & 255) - 128 (int8), hi = (v + 2048) >> 8
  * (4 bits), v = lo + 256 hi - 1920, stored fragment-tiled in blocks of 32 rows x 32 k (64 lanes x 16 lo bytes and
  * 64 lanes x 8 nib bytes per block, in MFMA operand order). Activations are int8, m x kp, zero padded in k.
@@ -782,7 +782,7 @@ int kt_hip_dec_embed_argmax(int dev, const uint64_t* part_dev, int64_t nparts, c
                             int32_t* r_dev, int32_t* token_dev, int32_t* step_dev, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------------
- * Synthetic workload generators (host only, no GPU): the BASELINE configs' integer samplers on the reference LCG
+ * Synthetic workload generators (host only, no GPU): the benchmark configs' integer samplers on the reference LCG
  * (apps/kt-demo/src/main.rs:19-22), multithreaded over the host cores. No counterpart in the reference.
  * ------------------------------------------------------------------------------------------------------------- */
 /* n codes uniform in [-2048, 2047]: ((s >> 33) % 4096) - 2048 on the stream seeded seed ^ 0x9E3779B97F4A7C15. */

@@ -351,7 +351,7 @@ void kt_gen_wlevels(uint64_t* state, size_t n, int32_t* out) {
     for (size_t i = 0; i < n; i++) out[i] = (int32_t)((lcg(state) >> 33) % (2 * (uint64_t)WLEVELS + 1)) - (int32_t)WLEVELS;
 }
 
-/* The BASELINE config-2 generators (this build's own definitions; integer only, no libm):
+/* The benchmark config-2 generators (this build's own definitions; integer only, no libm):
  *  - weights: uniform signed 12-bit codes in [-2048, 2047]: ((s >> 33) % 4096) - 2048 on a stream seeded
  *    seed ^ 0x9E3779B97F4A7C15 (the kt-demo convention, main.rs:24);
  *  - activations: round(N(0, sigma)) clipped to +-127, where N(0,1) is the Irwin-Hall sum of 12 uniforms
@@ -763,7 +763,7 @@ void kt_quant_linear_forward(const int32_t* x, size_t rows, size_t in, kt_scale 
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
-/* The 12-bit weight path (this build's own format, restated here as the checker)          */
+/* The 12-bit weight path (benchmark configs 2-5; this build's own format, restated here as the checker)          */
 /* ------------------------------------------------------------------------------------------------------------ */
 
 /* W12 layout (this build's 12-bit weight format) for an n x k matrix of codes v in [-2048, 2047]. Digits:

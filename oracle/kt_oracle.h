@@ -1,6 +1,6 @@
 /*
  * kt_oracle.h -- TEST INFRASTRUCTURE ONLY. Prototypes shared by the two halves of the CPU oracle:
- * kt_oracle.c (the reference's integer path) and kt_oracle_layers.c (the layers of BASELINE configs 3-5 around the
+ * kt_oracle.c (the reference's integer path) and kt_oracle_layers.c (the layers of benchmark configs 3-5 around the
  * 12-bit GEMM). Never part of the product.
  */
 #ifndef KT_ORACLE_H

@@ -1,9 +1,9 @@
 /*
- * kt_oracle_layers.c -- TEST INFRASTRUCTURE ONLY. CPU restatements of the layers that BASELINE configs 3-5 build
+ * kt_oracle_layers.c -- TEST INFRASTRUCTURE ONLY. CPU restatements of the layers that benchmark configs 3-5 build
  * around the 12-bit GEMM, used as the checker of the GPU path and as the timed CPU figure of those configs. Never
  * part of the product; only tests/, __graft_entry__.smoke() and bench.py's CPU legs load it (through oracle.py).
  *
- * The reference runs these layers in its 12-trit domain with per-tensor dynamic requant; the BASELINE configs ask
+ * The reference runs these layers in its 12-trit domain with per-tensor dynamic requant; the benchmark configs ask
  * for int8 activations, 12-bit weight codes and per-channel integer requant instead. The structure each function
  * follows is the reference's (file:line given per function); the int8 epilogues are this build's definitions,
  * written out in full in each function's comment so the GPU path and this file implement one stated rule.

@@ -1,4 +1,4 @@
-"""Writes tests/golden/goldens.json: input and output hashes of the BASELINE workloads, computed by the CPU oracle
+"""Writes tests/golden/goldens.json: input and output hashes of the benchmark workloads, computed by the CPU oracle
 (oracle/kt_oracle.c, the restated reference CPU path). The GPU tests compare the device results with these fixtures
 at full size, where recomputing the CPU answer inside a test would take too long.
 
@@ -18,15 +18,15 @@ from oracle import oracle as O  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "goldens.json")
 
-# BASELINE config 2 (this build's definitions; see oracle/kt_oracle.c kt_gen_w12 / kt_gen_act_gauss /
+# benchmark config 2 (this build's definitions; see oracle/kt_oracle.c kt_gen_w12 / kt_gen_act_gauss /
 # kt_channel_scales): N = K = 4096, M in {1, 16, 128, 2048} taking the first M rows of one 2048-row activation draw.
 C2 = {"w_seed": 2, "x_seed": 3, "sigma": 40, "N": 4096, "K": 4096, "Ms": [1, 16, 128, 2048]}
 
-# BASELINE config 4 (this build's integer MoE layer, include/kt_hip.h): GLM-4.5-Air shape.
+# benchmark config 4 (this build's integer MoE layer, include/kt_hip.h): GLM-4.5-Air shape.
 C4 = {"T": 4096, "H": 4096, "F": 1408, "E": 128, "top_k": 8, "x_seed": 41, "r_seed": 42, "w_seed": 4000,
       "sigma_x": 40, "sigma_r": 1024, "sigma_h": 16, "h_shift": 8, "out_shift": 13}
 
-# BASELINE config 5 (this build's integer definition of the SAM 2.1 Hiera-B+ encoder GEMMs, include/kt_hip.h).
+# benchmark config 5 (this build's integer definition of the SAM 2.1 Hiera-B+ encoder GEMMs, include/kt_hip.h).
 C5 = {"C": 3, "H": 1024, "W": 1024, "CO": 112, "KH": 7, "KW": 7, "S": 4, "P": 3, "tokens": 4096, "dim": 448,
       "hidden": 1792, "img_seed": 51, "pe_seed": 52, "bias_seed": 53, "x_seed": 54, "wi_seed": 55, "wo_seed": 56,
       "entry_scale": 48, "sigma_q": 61, "bias_sigma": 131072, "sigma_x": 40, "sigma_h": 24}
@@ -65,7 +65,7 @@ def config5() -> dict:
     return c
 
 
-# BASELINE config 3 (this build's integer decoder, include/kt_hip.h): Qwen2.5-0.5B shape.
+# benchmark config 3 (this build's integer decoder, include/kt_hip.h): Qwen2.5-0.5B shape.
 C3 = {"d": 896, "ffn": 4864, "nh": 14, "nkv": 2, "hd": 64, "layers": 24, "vocab": 151936, "prompt": 512,
       "max_new": 129, "w_seed": 3000, "prompt_seed": 3001, "h_shift": 8}
 

@@ -2,7 +2,7 @@
 
 Mirrors the reference's backend tests: crates/02-runtime/kt-runtime/src/tests_cuda.rs (the corpus hash, residency,
 the bound case, every planted defect caught), crates/02-runtime/kt-cuda/src/tests.rs (tails, extremes, bounds), and
-the BASELINE workloads (config 1 through the LinearBackend path; config 2 through the 12-bit-weight path) checked
+the benchmark workloads (config 1 through the LinearBackend path; config 2 through the 12-bit-weight path) checked
 byte for byte: against the oracle at sizes it computes in seconds, and against the committed fixture hashes at full
 size.
 """
@@ -170,7 +170,7 @@ def test_every_planted_defect_is_caught():
 
 
 def test_kt_demo_and_config1_hashes(hip_backend):
-    """apps/kt-demo (README.md:74) and BASELINE config 1 through the LinearBackend ABI."""
+    """apps/kt-demo (README.md:74) and benchmark config 1 through the LinearBackend ABI."""
     qx, qw = O.gen_demo(64, 768, 768, 42)
     assert O.sha256_hex(hip_backend.linear(qx, qw, 64, 768, 768)) == KT_DEMO_HASH
     g = GOLD["config1"]
@@ -484,7 +484,7 @@ def test_w12_dma_tile_kernel_past_int32(torch_dev):
 
 
 def test_config2_full_size_against_fixtures(torch_dev):
-    """BASELINE config 2 at its full shape (N = K = 4096, M in {1, 16, 128, 2048}): the i64 accumulators and the
+    """benchmark config 2 at its full shape (N = K = 4096, M in {1, 16, 128, 2048}): the i64 accumulators and the
     requantized int8 outputs hash to the fixtures the CPU oracle produced (tests/golden/goldens.json)."""
     torch = torch_dev
     T = tb()

@@ -5,7 +5,7 @@ The GPU path (tritify_amd.decoder: embed, RmsNorm, q/k/v W12 GEMM, RoPE + KV cac
 the residual, SwiGLU gate/up GEMM, down GEMM into the residual, lm_head, greedy argmax on the device) is compared
 with the oracle's decoder (kt_dec_generate, the reference's DecoderModel / generate_greedy_by loop,
 crates/01-engine/kt-core/src/model.rs:290-353, generate.rs:82-111): every step's logits and token byte for byte on
-a small model, eager and as a replayed HIP graph, and at the full BASELINE shape (512-token prefill, 128 greedy
+a small model, eager and as a replayed HIP graph, and at the full benchmark shape (512-token prefill, 128 greedy
 decode steps) against the fixture's logits hash.
 """
 import hashlib
@@ -87,7 +87,7 @@ def test_decoder_prompt_of_one_and_ragged_heads(torch_dev):
 
 
 def test_decoder_full_config3(torch_dev):
-    """Qwen2.5-0.5B shape, 512-token prefill, 128 greedy decode steps (129 hashed logit rows),
+    """benchmark config 3: Qwen2.5-0.5B shape, 512-token prefill, 128 greedy decode steps (129 hashed logit rows),
     decode steps replayed from one captured HIP graph."""
     from tritify_amd import workloads as W
 

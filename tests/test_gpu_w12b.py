@@ -131,7 +131,7 @@ def test_w12b_extremes(torch_dev):
 
 
 def test_w12b_config2_m2048_against_the_fixture(torch_dev):
-    """BASELINE config 2 at M = 2048 (N = K = 4096) on the balanced planes: the i64 accumulators and the int8
+    """benchmark config 2 at M = 2048 (N = K = 4096) on the balanced planes: the i64 accumulators and the int8
     outputs hash to the fixtures the CPU oracle produced, as the W12 path's do."""
     torch = torch_dev
     T = tb()

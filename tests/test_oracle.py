@@ -31,7 +31,7 @@ def test_kt_demo_default_hash():
 
 
 def test_config1_hashes():
-    """BASELINE config 1 (64x1024x1024, seed 42): the kt-demo generator at that shape, hashed over i64 and i32."""
+    """benchmark config 1 (64x1024x1024, seed 42): the kt-demo generator at that shape, hashed over i64 and i32."""
     g = GOLD["config1"]
     qx, qw = O.gen_demo(64, 1024, 1024, 42)
     assert O.sha256_hex(qx) == g["x_sha256"] and O.sha256_hex(qw) == g["w_sha256"]
@@ -467,7 +467,7 @@ def test_w12_recombination_equals_the_direct_sum():
 
 
 def test_config2_generators_match_fixtures():
-    """The BASELINE config-2 inputs (this build's integer-only samplers) are stable: hashes pinned in goldens.json."""
+    """The benchmark config-2 inputs (this build's integer-only samplers) are stable: hashes pinned in goldens.json."""
     g = GOLD["config2"]
     w = O.gen_w12(g["w_seed"], 4096 * 4096)
     assert O.sha256_hex(w) == g["w_sha256"]

@@ -11,7 +11,7 @@
 //    wrap and launches one kernel per chunk, each adding its i64 result into y.
 //    Layout of a planed operand: [plane][row][kp] int8, kp = k rounded up to 64, zero padded.
 //
-// 2. W12 (int8 activations x 12-bit weight codes in [-2048, 2047]), the format and the mainloop
+// 2. W12 (benchmark configs: int8 activations x 12-bit weight codes in [-2048, 2047]), the format and the mainloop
 //    of kt_w12_core.h: the dense GEMM for large M and the skinny GEMM for batch decode live here, the grouped (MoE)
 //    and im2col GEMMs in their own files.
 //

@@ -1,4 +1,4 @@
-// SAM 2.1's image path on gfx950: the patch-embed convolution as an im2col-fused W12 GEMM.
+// SAM 2.1's image path on gfx950 (benchmark config 5): the patch-embed convolution as an im2col-fused W12 GEMM.
 //
 // The reference runs Conv2d::forward_int as a direct loop over (ic, ky, kx) per output element on the CPU
 // (crates/01-engine/kt-core/src/conv.rs:68-130), output [c_out, OH, OW]. Here one CTA of 8 waves owns 128 consecutive

@@ -1,4 +1,4 @@
-// Host-side generators of the BASELINE workloads' synthetic inputs (integer-only, identical on every machine), for
+// Host-side generators of the benchmark workloads' synthetic inputs (integer-only, identical on every machine), for
 // the shapes where numpy is too slow: config 3's decoder weights, config 4's 129 experts and config 5's image. The
 // stream is the reference's LCG, s <- s * 6364136223846793005 + 1442695040888963407 mod 2^64, drawn as s >> 33
 // (apps/kt-demo/src/main.rs:19-22). tritify_amd/workloads.py holds the same definitions in numpy; the tests check

@@ -4,8 +4,8 @@ The stream is the reference's LCG, s <- s*6364136223846793005 + 1442695040888963
 (apps/kt-demo/src/main.rs:19-22), drawn as (s >> 33). It is evaluated here in numpy: a first block step by step,
 then the sequence doubles, each new half the affine map s -> A*s + C (mod 2^64) of the half before it.
 
-- gen_demo: the kt-demo generator (main.rs:23-28), BASELINE config 1.
-- gen_w12 / gen_act_gauss / channel_scales: BASELINE config 2 (this build's definitions): 12-bit weight codes
+- gen_demo: the kt-demo generator (main.rs:23-28), benchmark config 1.
+- gen_w12 / gen_act_gauss / channel_scales: benchmark config 2 (this build's definitions): 12-bit weight codes
   uniform in [-2048, 2047]; activations round(N(0, sigma)) clipped to +-127, N(0,1) drawn as an Irwin-Hall sum of
   12 16-bit uniforms; per-channel int32 requant scales mapping 4 standard deviations of a channel's accumulator to
   127 (crates/00-kernels/kt-int/src/lib.rs:191-212 for the fixed-point ratio).
